@@ -1,0 +1,673 @@
+/*
+ * oracle/orc_model.c -- plaintext fixed-point affinity forward and the
+ * two-party protocol over the whole model.  TEST INFRASTRUCTURE ONLY.
+ *
+ * Plaintext semantics follow reference/fixed_forward.py:
+ *   _wrap            :121-129  (signed reduction mod 2^bw)
+ *   _linear          :132-138  (wrap(tr(x W^T)) then wrap(+b))
+ *   _gcn_layer       :140-144  (transform first: wrap(tr(A_fx . wrap(tr(H W^T)))) + b)
+ *   _drug_path_fx    :147-162  (3x GCN + ReLU, sentinel max-pool, drug FCs)
+ *   _fusion_fx       :165-172  (concat [drug, protein], ReLU on all but last)
+ * with fixed_matmul = exact product, floor(./2^s) (reference/fixedpoint.py:61-77),
+ * and A_fx taken from the secure normalisation's closed form
+ * A[i,j]*floor(T[d_i]*T[d_j]/2^s) (gpu_mpc/secure_adj_norm.h:138-184,326-365)
+ * instead of to_fixed(A_hat) (fixed_forward.py:149), because the secure path
+ * computes exactly that.
+ *
+ * Weights are the weights.bin layout of gpu_mpc/deepdtagen_inference.cu:121-181:
+ * per layer W^T (in x out, row-major) then bias (out), int64 at scale s.
+ */
+#include <math.h>
+#include <stdlib.h>
+#include <string.h>
+#include "orc.h"
+
+typedef __int128 i128;
+typedef unsigned __int128 u128;
+
+static inline uint64_t rmask(int bw) { return bw >= 64 ? ~0ull : ((1ull << bw) - 1ull); }
+
+static orc_trace_fn g_trace = 0;
+void orc_set_trace(orc_trace_fn fn) { g_trace = fn; }
+static void trace(uint32_t g, size_t n, const uint64_t *v) {
+  if (g_trace) g_trace(g, n, v);
+}
+
+/* ---------------- dims / weights ---------------- */
+static int nlayers(const orc_dims *d) { return 5 + d->nfus; }
+static void layer_io(const orc_dims *d, int l, int *in, int *out) {
+  if (l < 3) {
+    *in = l == 0 ? d->feat : d->gcn[l - 1];
+    *out = d->gcn[l];
+  } else if (l < 5) {
+    *in = l == 3 ? d->gcn[2] : d->dfc[0];
+    *out = d->dfc[l - 3];
+  } else {
+    int k = l - 5;
+    *in = k == 0 ? d->dfc[1] + d->prot : d->fus[k - 1];
+    *out = d->fus[k];
+  }
+}
+static size_t layer_off(const orc_dims *d, int l) {
+  size_t o = 0;
+  for (int j = 0; j < l; j++) {
+    int in, out;
+    layer_io(d, j, &in, &out);
+    o += (size_t)in * out + (size_t)out;
+  }
+  return o;
+}
+size_t orc_weights_len(const orc_dims *d) { return layer_off(d, nlayers(d)); }
+
+void orc_invsqrt_table(int s, int nmax, uint64_t *table) {
+  for (int k = 0; k < 256; k++) table[k] = 0;
+  double q = ldexp(1.0, s);
+  for (int k = 1; k <= nmax && k < 256; k++) table[k] = (uint64_t)llround(q / sqrt((double)k));
+}
+
+/* ---------------- plaintext forward ---------------- */
+static const char *DOMAIN_MSG[] = {
+    "ok",
+    "pre-truncation product outside the signed ring",
+    "product + bias*2^s outside the signed ring",
+    "max-pool input >= 2^(bw-2) (sentinel headroom)",
+    "sample without a real atom",
+    "node degree outside the 8-bit LUT domain",
+    "adjacency or mask entry not 0/1",
+};
+const char *orc_domain_msg(int code) {
+  if (code < 0 || code > 6) return "unknown";
+  return DOMAIN_MSG[code];
+}
+
+typedef struct {
+  int bw, s;
+  int err;
+} fx;
+
+static int fits(const fx *f, i128 v) {
+  i128 h = (i128)1 << (f->bw - 1);
+  return v >= -h && v < h;
+}
+static int64_t wrapv(const fx *f, i128 v) {
+  if (f->bw >= 64) return (int64_t)v;
+  uint64_t m = (uint64_t)v & rmask(f->bw);
+  uint64_t half = 1ull << (f->bw - 1);
+  return m >= half ? (int64_t)m - (int64_t)(1ull << f->bw) : (int64_t)m;
+}
+static void seterr(fx *f, int code) {
+  if (!f->err) f->err = code;
+}
+/* exact  sum_k a[k*as] * b[k*bs]  as a 128-bit integer */
+static i128 dot(const int64_t *a, size_t as, const int64_t *b, size_t bs, size_t K) {
+  u128 acc = 0;
+  for (size_t k = 0; k < K; k++) acc += (u128)((i128)a[k * as] * (i128)b[k * bs]);
+  return (i128)acc;
+}
+/* y(MxN) = wrap(tr(X(MxK) . B(KxN))); optional bias check for the fused gate */
+static void fixed_mm(fx *f, const int64_t *X, const int64_t *Bm, size_t M, size_t K, size_t N,
+                     const int64_t *bias_check, int64_t *Y) {
+  for (size_t i = 0; i < M; i++)
+    for (size_t j = 0; j < N; j++) {
+      i128 P = dot(X + i * K, 1, Bm + j, N, K);
+      if (!fits(f, P)) seterr(f, 1);
+      if (bias_check && !fits(f, P + ((i128)bias_check[j] << f->s))) seterr(f, 2);
+      Y[i * N + j] = wrapv(f, P >> f->s);
+    }
+}
+
+void orc_adj_norm_plain(int s, int N, int B, const int64_t *A, int64_t *Ahat) {
+  uint64_t T[256];
+  orc_invsqrt_table(s, 138, T);
+  for (int b = 0; b < B; b++) {
+    const int64_t *a = A + (size_t)b * N * N;
+    int64_t *o = Ahat + (size_t)b * N * N;
+    int *deg = (int *)calloc((size_t)N, sizeof(int));
+    for (int i = 0; i < N; i++)
+      for (int j = 0; j < N; j++) deg[i] += (int)a[(size_t)i * N + j];
+    for (int i = 0; i < N; i++)
+      for (int j = 0; j < N; j++) {
+        uint64_t ti = deg[i] >= 0 && deg[i] < 256 ? T[deg[i]] : 0;
+        uint64_t tj = deg[j] >= 0 && deg[j] < 256 ? T[deg[j]] : 0;
+        o[(size_t)i * N + j] = a[(size_t)i * N + j] * (int64_t)((ti * tj) >> s);
+      }
+    free(deg);
+  }
+}
+
+static void adj_norm_tab(const orc_dims *d, const int64_t *a, int64_t *o, fx *f) {
+  const int N = d->n_nodes;
+  uint64_t T[256];
+  orc_invsqrt_table(d->s, d->lut_nmax, T);
+  int *deg = (int *)calloc((size_t)N, sizeof(int));
+  for (int i = 0; i < N; i++)
+    for (int j = 0; j < N; j++) {
+      int64_t v = a[(size_t)i * N + j];
+      if (v != 0 && v != 1) seterr(f, 6);
+      deg[i] += (int)v;
+    }
+  for (int i = 0; i < N; i++)
+    if (deg[i] < 0 || deg[i] > 255) seterr(f, 5);
+  for (int i = 0; i < N; i++)
+    for (int j = 0; j < N; j++) {
+      uint64_t ti = T[deg[i] & 255], tj = T[deg[j] & 255];
+      o[(size_t)i * N + j] = a[(size_t)i * N + j] * (int64_t)((ti * tj) >> d->s);
+    }
+  free(deg);
+}
+
+int orc_plain_forward(const orc_dims *d, int B, const int64_t *X, const int64_t *A,
+                      const int64_t *mask, const int64_t *prot, const int64_t *W,
+                      int64_t *out) {
+  const int N = d->n_nodes, bw = d->bw, s = d->s;
+  int err_all = 0;
+#pragma omp parallel for schedule(dynamic) num_threads(orc_get_threads())
+  for (int b = 0; b < B; b++) {
+    fx f = {bw, s, 0};
+    int maxw = d->feat;
+    for (int l = 0; l < nlayers(d); l++) {
+      int in, o;
+      layer_io(d, l, &in, &o);
+      if (o > maxw) maxw = o;
+      if (in > maxw) maxw = in;
+    }
+    int64_t *Af = (int64_t *)malloc(sizeof(int64_t) * (size_t)N * N);
+    int64_t *H = (int64_t *)malloc(sizeof(int64_t) * (size_t)N * maxw);
+    int64_t *XW = (int64_t *)malloc(sizeof(int64_t) * (size_t)N * maxw);
+    int64_t *Hn = (int64_t *)malloc(sizeof(int64_t) * (size_t)N * maxw);
+    adj_norm_tab(d, A + (size_t)b * N * N, Af, &f);
+    int fin = d->feat;
+    memcpy(H, X + (size_t)b * N * fin, sizeof(int64_t) * (size_t)N * fin);
+    for (int l = 0; l < 3; l++) {
+      int fo = d->gcn[l];
+      const int64_t *Wt = W + layer_off(d, l);
+      const int64_t *bias = Wt + (size_t)fin * fo;
+      fixed_mm(&f, H, Wt, (size_t)N, (size_t)fin, (size_t)fo, NULL, XW); /* XW */
+      fixed_mm(&f, Af, XW, (size_t)N, (size_t)N, (size_t)fo, bias, Hn);  /* A . XW */
+      for (int i = 0; i < N; i++)
+        for (int j = 0; j < fo; j++) {
+          int64_t v = wrapv(&f, (i128)Hn[(size_t)i * fo + j] + bias[j]);
+          H[(size_t)i * fo + j] = v > 0 ? v : 0;
+        }
+      fin = fo;
+    }
+    /* masked global max-pool, sentinel -2^(bw-2) */
+    const int C = d->gcn[2];
+    const int64_t sentinel = -(int64_t)(1ull << (bw - 2));
+    int64_t *pooled = (int64_t *)malloc(sizeof(int64_t) * (size_t)C);
+    int nreal = 0;
+    for (int i = 0; i < N; i++) {
+      int64_t mv = mask[(size_t)b * N + i];
+      if (mv != 0 && mv != 1) f.err = f.err ? f.err : 6;
+      nreal += mv != 0;
+    }
+    if (nreal == 0) seterr(&f, 4);
+    for (int c = 0; c < C; c++) {
+      int64_t best = sentinel;
+      for (int i = 0; i < N; i++) {
+        int64_t v = H[(size_t)i * C + c];
+        if (v >= (int64_t)(1ull << (bw - 2))) seterr(&f, 3);
+        int64_t mv = mask[(size_t)b * N + i] != 0 ? v : sentinel;
+        if (mv > best) best = mv;
+      }
+      pooled[c] = best;
+    }
+    /* drug FCs */
+    int64_t *h1 = (int64_t *)malloc(sizeof(int64_t) * (size_t)maxw);
+    int64_t *h2 = (int64_t *)malloc(sizeof(int64_t) * (size_t)maxw * 2);
+    {
+      const int64_t *Wt = W + layer_off(d, 3);
+      const int64_t *bias = Wt + (size_t)C * d->dfc[0];
+      fixed_mm(&f, pooled, Wt, 1, (size_t)C, (size_t)d->dfc[0], bias, h1);
+      for (int j = 0; j < d->dfc[0]; j++) {
+        int64_t v = wrapv(&f, (i128)h1[j] + bias[j]);
+        h1[j] = v > 0 ? v : 0;
+      }
+      Wt = W + layer_off(d, 4);
+      bias = Wt + (size_t)d->dfc[0] * d->dfc[1];
+      fixed_mm(&f, h1, Wt, 1, (size_t)d->dfc[0], (size_t)d->dfc[1], bias, h2);
+      for (int j = 0; j < d->dfc[1]; j++) h2[j] = wrapv(&f, (i128)h2[j] + bias[j]);
+    }
+    /* fusion: concat [drug, protein] (fixed_forward.py:166) */
+    int width = d->dfc[1] + d->prot;
+    for (int j = 0; j < d->prot; j++) h2[d->dfc[1] + j] = prot[(size_t)b * d->prot + j];
+    for (int k = 0; k < d->nfus; k++) {
+      const int64_t *Wt = W + layer_off(d, 5 + k);
+      int fo = d->fus[k];
+      const int64_t *bias = Wt + (size_t)width * fo;
+      fixed_mm(&f, h2, Wt, 1, (size_t)width, (size_t)fo, bias, h1);
+      for (int j = 0; j < fo; j++) {
+        int64_t v = wrapv(&f, (i128)h1[j] + bias[j]);
+        h2[j] = (k < d->nfus - 1 && v < 0) ? 0 : v;
+      }
+      width = fo;
+    }
+    out[b] = h2[0];
+    free(Af);
+    free(H);
+    free(XW);
+    free(Hn);
+    free(pooled);
+    free(h1);
+    free(h2);
+    if (f.err) {
+#pragma omp critical
+      {
+        if (!err_all) err_all = f.err;
+      }
+    }
+  }
+  return err_all;
+}
+
+/* ---------------- two-party model ---------------- */
+typedef struct {
+  size_t off;
+  uint32_t gate;
+} walker;
+
+static size_t pairs_of(int N) { return (size_t)N * (N + 1) / 2; }
+static size_t pidx(int N, int i, int j) { /* i <= j */
+  return (size_t)i * N - (size_t)i * (i - 1) / 2 + (size_t)(j - i);
+}
+
+/* pool tree: returns the number of levels, fills pairs per level */
+static int pool_levels(int N, int *pairs) {
+  int R = N, L = 0;
+  while (R > 1) {
+    pairs[L++] = R / 2;
+    R = R / 2 + (R & 1);
+  }
+  return L;
+}
+
+static void build_maps(int B, int N, uint32_t *oa, uint32_t *ob, uint32_t *wa, uint32_t *wb) {
+  size_t P = pairs_of(N);
+  for (int b = 0; b < B; b++) {
+    size_t q = (size_t)b * P;
+    for (int i = 0; i < N; i++)
+      for (int j = i; j < N; j++) {
+        oa[q] = (uint32_t)(b * N + i);
+        ob[q] = (uint32_t)(b * N + j);
+        q++;
+      }
+    for (int i = 0; i < N; i++)
+      for (int j = 0; j < N; j++) {
+        size_t e = ((size_t)b * N + i) * N + j;
+        wa[e] = (uint32_t)e;
+        wb[e] = (uint32_t)((size_t)b * P + (i <= j ? pidx(N, i, j) : pidx(N, j, i)));
+      }
+  }
+}
+
+size_t orc_model_key_bytes(const orc_dims *d, int B) {
+  const int bw = d->bw, s = d->s, N = d->n_nodes;
+  size_t o = 0, r1, r2, r3;
+  orc_dcf_layout D;
+  o = orc_reveal_layout(bw, (size_t)B * N * d->feat, o, &r1);
+  o = orc_reveal_layout(bw, (size_t)B * N * N, o, &r1);
+  o = orc_reveal_layout(bw, (size_t)B * N, o, &r1);
+  o = orc_reveal_layout(bw, (size_t)B * N, o, &r1);
+  o = orc_lut8_layout(bw, (size_t)B * N, o, &D, &r1, &r2, &r3);
+  size_t P = pairs_of(N);
+  o = orc_mul_layout(bw, (size_t)B * N, (size_t)B * N, (size_t)B * P, o, &r1, &r2, &r3);
+  o = orc_tr_layout_make(ORC_G_TRSLACK, bw, s, (size_t)B * P, o).end;
+  o = orc_mul_layout(bw, (size_t)B * N * N, (size_t)B * P, (size_t)B * N * N, o, &r1, &r2, &r3);
+  for (int l = 0; l < 3; l++) {
+    size_t E = (size_t)B * N * d->gcn[l];
+    o = orc_tr_layout_make(ORC_G_TR, bw, s, E, o).end;
+    o = orc_sxs_layout(bw, (size_t)B, (size_t)N, (size_t)N, (size_t)d->gcn[l], o, &r1, &r2, &r3);
+    o = orc_tr_layout_make(ORC_G_TRRELU, bw, s, E, o).end;
+  }
+  int pairs[32];
+  int L = pool_levels(N, pairs);
+  for (int l = 0; l < L; l++)
+    o = orc_tr_layout_make(ORC_G_RELU, bw, s, (size_t)B * pairs[l] * d->gcn[2], o).end;
+  o = orc_tr_layout_make(ORC_G_TRRELU, bw, s, (size_t)B * d->dfc[0], o).end;
+  o = orc_tr_layout_make(ORC_G_TR, bw, s, (size_t)B * d->dfc[1], o).end;
+  for (int k = 0; k < d->nfus - 1; k++)
+    o = orc_tr_layout_make(ORC_G_TRRELU, bw, s, (size_t)B * d->fus[k], o).end;
+  o = orc_reveal_layout(bw, (size_t)B * d->fus[d->nfus - 1], o, &r1);
+  return o;
+}
+
+/* y (rows x fo) = x (rows x fi) . Wt mod 2^bw, with Wt int64 */
+static void pub_gemm(int bw, size_t rows, int fi, int fo, const uint64_t *x, const int64_t *Wt,
+                     uint64_t *y) {
+  orc_ring_gemm(bw, 1, rows, (size_t)fi, (size_t)fo, x, (const uint64_t *)Wt, y, 0);
+}
+
+int orc_model_keygen(const orc_dims *d, int B, uint64_t seed, const int64_t *W, uint8_t *k0,
+                     uint8_t *k1) {
+  const int bw = d->bw, s = d->s, N = d->n_nodes;
+  const uint64_t M = rmask(bw);
+  size_t o = 0, r1, r2, r3;
+  uint32_t g = 1;
+  orc_dcf_layout D;
+  const size_t BN = (size_t)B * N, BNN = BN * N, P = pairs_of(N);
+  int maxw = d->feat;
+  for (int l = 0; l < nlayers(d); l++) {
+    int in, out;
+    layer_io(d, l, &in, &out);
+    if (out > maxw) maxw = out;
+    if (in > maxw) maxw = in;
+  }
+  uint64_t *rX = (uint64_t *)malloc(8 * BN * maxw);
+  uint64_t *rA = (uint64_t *)malloc(8 * BNN), *rm = (uint64_t *)malloc(8 * BN);
+  uint64_t *rd = (uint64_t *)malloc(8 * BN), *rinv = (uint64_t *)malloc(8 * BN);
+  uint64_t *rP = (uint64_t *)malloc(8 * B * P), *rW = (uint64_t *)malloc(8 * B * P);
+  uint64_t *rN = (uint64_t *)malloc(8 * BNN);
+  uint64_t *t1 = (uint64_t *)malloc(8 * BN * maxw), *t2 = (uint64_t *)malloc(8 * BN * maxw);
+  uint32_t *oa = (uint32_t *)malloc(4 * B * P), *ob = (uint32_t *)malloc(4 * B * P);
+  uint32_t *wa = (uint32_t *)malloc(4 * BNN), *wb = (uint32_t *)malloc(4 * BNN);
+  build_maps(B, N, oa, ob, wa, wb);
+
+  orc_reveal_keygen(seed, g++, bw, BN * d->feat, rX, k0, k1, o);
+  o = orc_reveal_layout(bw, BN * d->feat, o, &r1);
+  orc_reveal_keygen(seed, g++, bw, BNN, rA, k0, k1, o);
+  o = orc_reveal_layout(bw, BNN, o, &r1);
+  orc_reveal_keygen(seed, g++, bw, BN, rm, k0, k1, o);
+  o = orc_reveal_layout(bw, BN, o, &r1);
+  orc_reveal_keygen(seed, g++, bw, BN, rd, k0, k1, o);
+  o = orc_reveal_layout(bw, BN, o, &r1);
+  orc_lut8_keygen(seed, g++, bw, BN, rd, rinv, k0, k1, o);
+  o = orc_lut8_layout(bw, BN, o, &D, &r1, &r2, &r3);
+  orc_mul_keygen(seed, g++, bw, BN, BN, (size_t)B * P, oa, ob, rinv, rinv, rP, k0, k1, o);
+  o = orc_mul_layout(bw, BN, BN, (size_t)B * P, o, &r1, &r2, &r3);
+  orc_tr_keygen(seed, g++, ORC_G_TRSLACK, bw, s, (size_t)B * P, rP, rW, k0, k1, o);
+  o = orc_tr_layout_make(ORC_G_TRSLACK, bw, s, (size_t)B * P, o).end;
+  orc_mul_keygen(seed, g++, bw, BNN, (size_t)B * P, BNN, wa, wb, rA, rW, rN, k0, k1, o);
+  o = orc_mul_layout(bw, BNN, (size_t)B * P, BNN, o, &r1, &r2, &r3);
+
+  /* GCN stack: rX holds the running H mask */
+  int fin = d->feat;
+  for (int l = 0; l < 3; l++) {
+    int fo = d->gcn[l];
+    size_t E = BN * fo;
+    pub_gemm(bw, BN, fin, fo, rX, W + layer_off(d, l), t1); /* mask of H.Wt */
+    orc_tr_keygen(seed, g++, ORC_G_TR, bw, s, E, t1, t2, k0, k1, o);
+    o = orc_tr_layout_make(ORC_G_TR, bw, s, E, o).end;
+    orc_sxs_keygen(seed, g++, bw, (size_t)B, (size_t)N, (size_t)N, (size_t)fo, rN, t2, t1, k0, k1, o);
+    o = orc_sxs_layout(bw, (size_t)B, (size_t)N, (size_t)N, (size_t)fo, o, &r1, &r2, &r3);
+    orc_tr_keygen(seed, g++, ORC_G_TRRELU, bw, s, E, t1, rX, k0, k1, o);
+    o = orc_tr_layout_make(ORC_G_TRRELU, bw, s, E, o).end;
+    fin = fo;
+  }
+  /* pool: V = H3 + S*m - S, mask rH3 + S*rm */
+  const int C = d->gcn[2];
+  const uint64_t S = 1ull << (bw - 2);
+  for (size_t r = 0; r < BN; r++)
+    for (int c = 0; c < C; c++) rX[r * C + c] = (rX[r * C + c] + S * rm[r]) & M;
+  int pairs[32];
+  int L = pool_levels(N, pairs), R = N;
+  for (int l = 0; l < L; l++) {
+    int pr = pairs[l];
+    size_t E = (size_t)B * pr * C;
+    for (int b = 0; b < B; b++)
+      for (int j = 0; j < pr; j++)
+        for (int c = 0; c < C; c++)
+          t1[((size_t)b * pr + j) * C + c] =
+              (rX[((size_t)b * R + 2 * j + 1) * C + c] - rX[((size_t)b * R + 2 * j) * C + c]) & M;
+    orc_tr_keygen(seed, g++, ORC_G_RELU, bw, s, E, t1, t2, k0, k1, o);
+    o = orc_tr_layout_make(ORC_G_RELU, bw, s, E, o).end;
+    int Rn = pr + (R & 1);
+    for (int b = 0; b < B; b++) {
+      for (int j = 0; j < pr; j++)
+        for (int c = 0; c < C; c++)
+          t1[((size_t)b * Rn + j) * C + c] =
+              (rX[((size_t)b * R + 2 * j) * C + c] + t2[((size_t)b * pr + j) * C + c]) & M;
+      if (R & 1)
+        for (int c = 0; c < C; c++)
+          t1[((size_t)b * Rn + pr) * C + c] = rX[((size_t)b * R + R - 1) * C + c];
+    }
+    memcpy(rX, t1, 8 * (size_t)B * Rn * C);
+    R = Rn;
+  }
+  /* drug FCs on the pooled (B x C) mask in rX */
+  pub_gemm(bw, (size_t)B, C, d->dfc[0], rX, W + layer_off(d, 3), t1);
+  orc_tr_keygen(seed, g++, ORC_G_TRRELU, bw, s, (size_t)B * d->dfc[0], t1, t2, k0, k1, o);
+  o = orc_tr_layout_make(ORC_G_TRRELU, bw, s, (size_t)B * d->dfc[0], o).end;
+  pub_gemm(bw, (size_t)B, d->dfc[0], d->dfc[1], t2, W + layer_off(d, 4), t1);
+  orc_tr_keygen(seed, g++, ORC_G_TR, bw, s, (size_t)B * d->dfc[1], t1, t2, k0, k1, o);
+  o = orc_tr_layout_make(ORC_G_TR, bw, s, (size_t)B * d->dfc[1], o).end;
+  /* concat [drug (mask t2), protein (public, mask 0)] */
+  int width = d->dfc[1] + d->prot;
+  for (int b = 0; b < B; b++)
+    for (int j = 0; j < width; j++)
+      rX[(size_t)b * width + j] = j < d->dfc[1] ? t2[(size_t)b * d->dfc[1] + j] : 0;
+  for (int k = 0; k < d->nfus; k++) {
+    int fo = d->fus[k];
+    pub_gemm(bw, (size_t)B, width, fo, rX, W + layer_off(d, 5 + k), t1);
+    if (k < d->nfus - 1) {
+      orc_tr_keygen(seed, g++, ORC_G_TRRELU, bw, s, (size_t)B * fo, t1, rX, k0, k1, o);
+      o = orc_tr_layout_make(ORC_G_TRRELU, bw, s, (size_t)B * fo, o).end;
+    } else {
+      /* output mask given to both evaluators in the clear (ddg_orca_base.h:296-302,511-517) */
+      size_t orr;
+      orc_reveal_layout(bw, (size_t)B * fo, o, &orr);
+      for (size_t i = 0; i < (size_t)B * fo; i++) {
+        uint64_t v = t1[i] & M;
+        if (bw == 32) {
+          uint32_t x = (uint32_t)v;
+          memcpy(k0 + orr + 4 * i, &x, 4);
+          memcpy(k1 + orr + 4 * i, &x, 4);
+        } else {
+          memcpy(k0 + orr + 8 * i, &v, 8);
+          memcpy(k1 + orr + 8 * i, &v, 8);
+        }
+      }
+      o = orc_reveal_layout(bw, (size_t)B * fo, o, &r1);
+      g++;
+    }
+    width = fo;
+  }
+  free(rX);
+  free(rA);
+  free(rm);
+  free(rd);
+  free(rinv);
+  free(rP);
+  free(rW);
+  free(rN);
+  free(t1);
+  free(t2);
+  free(oa);
+  free(ob);
+  free(wa);
+  free(wb);
+  return 0;
+}
+
+int orc_model_eval(const orc_dims *d, int B, const int64_t *W, const uint8_t *k0,
+                   const uint8_t *k1, const uint64_t *x0, const uint64_t *x1,
+                   const uint64_t *a0, const uint64_t *a1, const uint64_t *m0,
+                   const uint64_t *m1, const int64_t *prot, int64_t *out, uint64_t *bytes) {
+  const int bw = d->bw, s = d->s, N = d->n_nodes;
+  const uint64_t M = rmask(bw);
+  size_t o = 0, r1, r2, r3;
+  uint32_t g = 1;
+  orc_dcf_layout D;
+  const size_t BN = (size_t)B * N, BNN = BN * N, P = pairs_of(N);
+  int maxw = d->feat;
+  for (int l = 0; l < nlayers(d); l++) {
+    int in, outw;
+    layer_io(d, l, &in, &outw);
+    if (outw > maxw) maxw = outw;
+    if (in > maxw) maxw = in;
+  }
+  uint64_t *H = (uint64_t *)malloc(8 * BN * maxw);
+  uint64_t *Ah = (uint64_t *)malloc(8 * BNN), *mh = (uint64_t *)malloc(8 * BN);
+  uint64_t *dh = (uint64_t *)malloc(8 * BN), *inv = (uint64_t *)malloc(8 * BN);
+  uint64_t *Ph = (uint64_t *)malloc(8 * B * P), *Wh = (uint64_t *)malloc(8 * B * P);
+  uint64_t *An = (uint64_t *)malloc(8 * BNN);
+  uint64_t *t1 = (uint64_t *)malloc(8 * BN * maxw), *t2 = (uint64_t *)malloc(8 * BN * maxw);
+  uint64_t *dg0 = (uint64_t *)calloc(BN, 8), *dg1 = (uint64_t *)calloc(BN, 8);
+  int64_t *be = (int64_t *)malloc(8 * BN * maxw);
+  uint32_t *oa = (uint32_t *)malloc(4 * B * P), *ob = (uint32_t *)malloc(4 * B * P);
+  uint32_t *wa = (uint32_t *)malloc(4 * BNN), *wb = (uint32_t *)malloc(4 * BNN);
+  uint64_t T[256];
+  build_maps(B, N, oa, ob, wa, wb);
+  orc_invsqrt_table(s, d->lut_nmax, T);
+  uint64_t by = 0;
+
+  orc_reveal_eval(bw, BN * d->feat, k0, k1, o, x0, x1, H, &by);
+  trace(g, BN * d->feat, H);
+  g++;
+  o = orc_reveal_layout(bw, BN * d->feat, o, &r1);
+  orc_reveal_eval(bw, BNN, k0, k1, o, a0, a1, Ah, &by);
+  trace(g++, BNN, Ah);
+  o = orc_reveal_layout(bw, BNN, o, &r1);
+  orc_reveal_eval(bw, BN, k0, k1, o, m0, m1, mh, &by);
+  trace(g++, BN, mh);
+  o = orc_reveal_layout(bw, BN, o, &r1);
+  for (size_t r = 0; r < BN; r++)
+    for (int j = 0; j < N; j++) {
+      dg0[r] += a0[r * N + j];
+      dg1[r] += a1[r * N + j];
+    }
+  for (size_t r = 0; r < BN; r++) {
+    dg0[r] &= M;
+    dg1[r] &= M;
+  }
+  orc_reveal_eval(bw, BN, k0, k1, o, dg0, dg1, dh, &by);
+  trace(g++, BN, dh);
+  o = orc_reveal_layout(bw, BN, o, &r1);
+  orc_lut8_eval(bw, BN, k0, k1, o, T, dh, inv, &by);
+  trace(g++, BN, inv);
+  o = orc_lut8_layout(bw, BN, o, &D, &r1, &r2, &r3);
+  orc_mul_eval(bw, BN, BN, (size_t)B * P, oa, ob, k0, k1, o, inv, inv, Ph, &by);
+  trace(g++, (size_t)B * P, Ph);
+  o = orc_mul_layout(bw, BN, BN, (size_t)B * P, o, &r1, &r2, &r3);
+  orc_tr_eval(ORC_G_TRSLACK, bw, s, (size_t)B * P, k0, k1, o, Ph, NULL, Wh, &by);
+  trace(g++, (size_t)B * P, Wh);
+  o = orc_tr_layout_make(ORC_G_TRSLACK, bw, s, (size_t)B * P, o).end;
+  orc_mul_eval(bw, BNN, (size_t)B * P, BNN, wa, wb, k0, k1, o, Ah, Wh, An, &by);
+  trace(g++, BNN, An);
+  o = orc_mul_layout(bw, BNN, (size_t)B * P, BNN, o, &r1, &r2, &r3);
+
+  int fin = d->feat;
+  for (int l = 0; l < 3; l++) {
+    int fo = d->gcn[l];
+    size_t E = BN * fo;
+    const int64_t *Wt = W + layer_off(d, l);
+    const int64_t *bias = Wt + (size_t)fin * fo;
+    pub_gemm(bw, BN, fin, fo, H, Wt, t1);
+    orc_tr_eval(ORC_G_TR, bw, s, E, k0, k1, o, t1, NULL, t2, &by);
+    trace(g++, E, t2);
+    o = orc_tr_layout_make(ORC_G_TR, bw, s, E, o).end;
+    orc_sxs_eval(bw, (size_t)B, (size_t)N, (size_t)N, (size_t)fo, k0, k1, o, An, t2, t1, &by);
+    trace(g++, E, t1);
+    o = orc_sxs_layout(bw, (size_t)B, (size_t)N, (size_t)N, (size_t)fo, o, &r1, &r2, &r3);
+    for (size_t e = 0; e < E; e++) be[e] = bias[e % fo];
+    orc_tr_eval(ORC_G_TRRELU, bw, s, E, k0, k1, o, t1, be, H, &by);
+    trace(g++, E, H);
+    o = orc_tr_layout_make(ORC_G_TRRELU, bw, s, E, o).end;
+    fin = fo;
+  }
+  const int C = d->gcn[2];
+  const uint64_t S = 1ull << (bw - 2);
+  for (size_t r = 0; r < BN; r++)
+    for (int c = 0; c < C; c++) H[r * C + c] = (H[r * C + c] + S * mh[r] - S) & M;
+  int pairs[32];
+  int L = pool_levels(N, pairs), R = N;
+  for (int l = 0; l < L; l++) {
+    int pr = pairs[l];
+    size_t E = (size_t)B * pr * C;
+    for (int b = 0; b < B; b++)
+      for (int j = 0; j < pr; j++)
+        for (int c = 0; c < C; c++)
+          t1[((size_t)b * pr + j) * C + c] =
+              (H[((size_t)b * R + 2 * j + 1) * C + c] - H[((size_t)b * R + 2 * j) * C + c]) & M;
+    orc_tr_eval(ORC_G_RELU, bw, s, E, k0, k1, o, t1, NULL, t2, &by);
+    trace(g++, E, t2);
+    o = orc_tr_layout_make(ORC_G_RELU, bw, s, E, o).end;
+    int Rn = pr + (R & 1);
+    for (int b = 0; b < B; b++) {
+      for (int j = 0; j < pr; j++)
+        for (int c = 0; c < C; c++)
+          t1[((size_t)b * Rn + j) * C + c] =
+              (H[((size_t)b * R + 2 * j) * C + c] + t2[((size_t)b * pr + j) * C + c]) & M;
+      if (R & 1)
+        for (int c = 0; c < C; c++)
+          t1[((size_t)b * Rn + pr) * C + c] = H[((size_t)b * R + R - 1) * C + c];
+    }
+    memcpy(H, t1, 8 * (size_t)B * Rn * C);
+    R = Rn;
+  }
+  {
+    const int64_t *Wt = W + layer_off(d, 3);
+    const int64_t *bias = Wt + (size_t)C * d->dfc[0];
+    pub_gemm(bw, (size_t)B, C, d->dfc[0], H, Wt, t1);
+    for (size_t e = 0; e < (size_t)B * d->dfc[0]; e++) be[e] = bias[e % d->dfc[0]];
+    orc_tr_eval(ORC_G_TRRELU, bw, s, (size_t)B * d->dfc[0], k0, k1, o, t1, be, t2, &by);
+    trace(g++, (size_t)B * d->dfc[0], t2);
+    o = orc_tr_layout_make(ORC_G_TRRELU, bw, s, (size_t)B * d->dfc[0], o).end;
+    Wt = W + layer_off(d, 4);
+    bias = Wt + (size_t)d->dfc[0] * d->dfc[1];
+    pub_gemm(bw, (size_t)B, d->dfc[0], d->dfc[1], t2, Wt, t1);
+    for (size_t e = 0; e < (size_t)B * d->dfc[1]; e++) be[e] = bias[e % d->dfc[1]];
+    orc_tr_eval(ORC_G_TR, bw, s, (size_t)B * d->dfc[1], k0, k1, o, t1, be, t2, &by);
+    trace(g++, (size_t)B * d->dfc[1], t2);
+    o = orc_tr_layout_make(ORC_G_TR, bw, s, (size_t)B * d->dfc[1], o).end;
+  }
+  int width = d->dfc[1] + d->prot;
+  for (int b = 0; b < B; b++)
+    for (int j = 0; j < width; j++)
+      H[(size_t)b * width + j] = j < d->dfc[1] ? t2[(size_t)b * d->dfc[1] + j]
+                                               : ((uint64_t)prot[(size_t)b * d->prot + j - d->dfc[1]] & M);
+  /* the protein embedding is revealed by its owner (deepdtagen.h:60-67): one
+   * message of B x prot ring elements each way */
+  by += 2ull * (size_t)B * d->prot * (uint64_t)(bw / 8);
+  for (int k = 0; k < d->nfus; k++) {
+    int fo = d->fus[k];
+    const int64_t *Wt = W + layer_off(d, 5 + k);
+    const int64_t *bias = Wt + (size_t)width * fo;
+    pub_gemm(bw, (size_t)B, width, fo, H, Wt, t1);
+    if (k < d->nfus - 1) {
+      for (size_t e = 0; e < (size_t)B * fo; e++) be[e] = bias[e % fo];
+      orc_tr_eval(ORC_G_TRRELU, bw, s, (size_t)B * fo, k0, k1, o, t1, be, H, &by);
+      trace(g++, (size_t)B * fo, H);
+      o = orc_tr_layout_make(ORC_G_TRRELU, bw, s, (size_t)B * fo, o).end;
+    } else {
+      size_t orr;
+      orc_reveal_layout(bw, (size_t)B * fo, o, &orr);
+      for (int b = 0; b < B; b++) {
+        uint64_t rz;
+        if (bw == 32) {
+          uint32_t x;
+          memcpy(&x, k0 + orr + 4 * (size_t)b * fo, 4);
+          rz = x;
+        } else {
+          memcpy(&rz, k0 + orr + 8 * (size_t)b * fo, 8);
+        }
+        uint64_t z = (t1[(size_t)b * fo] - rz) & M;
+        int64_t zs = bw == 32 ? (int64_t)(int32_t)(uint32_t)z : (int64_t)z;
+        int64_t y = (zs >> s) + bias[0];
+        if (bw == 32) y = (int64_t)(int32_t)(uint32_t)((uint64_t)y & M);
+        out[b] = y;
+      }
+      trace(g++, (size_t)B * fo, t1);
+      o = orc_reveal_layout(bw, (size_t)B * fo, o, &r1);
+    }
+    width = fo;
+  }
+  if (bytes) *bytes = by;
+  free(H);
+  free(Ah);
+  free(mh);
+  free(dh);
+  free(inv);
+  free(Ph);
+  free(Wh);
+  free(An);
+  free(t1);
+  free(t2);
+  free(dg0);
+  free(dg1);
+  free(be);
+  free(oa);
+  free(ob);
+  free(wa);
+  free(wb);
+  return 0;
+}
