@@ -1,0 +1,201 @@
+// aes_dev.h -- AES-128 encryption on CDNA4 with T-tables staged in LDS, and the
+// half-tree hashes / dealer PRF built on it.
+//
+// State: four little-endian 32-bit columns (c_j = byte 4j | byte 4j+1 << 8 | ...).
+// One round:  n_j = T0[b0(c_j)] ^ T1[b1(c_j+1)] ^ T2[b2(c_j+2)] ^ T3[b3(c_j+3)] ^ rk_j
+// with T0[x] = (2S[x], S[x], S[x], 3S[x]) as bytes 0..3 and T_k = rotl(T0, 8k).
+// The last round reads S[x] out of the byte of T_(r+3)%4 that holds it.
+//
+// LDS layout: NT tables (1 = T0 only, rotations computed; 4 = all four), each
+// entry replicated REP times and interleaved so that word address of entry e,
+// copy c is e*REP + c.  Lane l reads copy (l % REP), so with REP equal to the
+// number of LDS banks the 64 lanes of a wavefront never collide on a bank.
+#pragma once
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+
+#include "mpcx_core.h"
+
+namespace mpcx {
+
+struct T0Table {
+  uint32_t v[256];
+};
+
+constexpr uint8_t kSboxC[256] = {
+    0x63, 0x7c, 0x77, 0x7b, 0xf2, 0x6b, 0x6f, 0xc5, 0x30, 0x01, 0x67, 0x2b, 0xfe, 0xd7, 0xab, 0x76,
+    0xca, 0x82, 0xc9, 0x7d, 0xfa, 0x59, 0x47, 0xf0, 0xad, 0xd4, 0xa2, 0xaf, 0x9c, 0xa4, 0x72, 0xc0,
+    0xb7, 0xfd, 0x93, 0x26, 0x36, 0x3f, 0xf7, 0xcc, 0x34, 0xa5, 0xe5, 0xf1, 0x71, 0xd8, 0x31, 0x15,
+    0x04, 0xc7, 0x23, 0xc3, 0x18, 0x96, 0x05, 0x9a, 0x07, 0x12, 0x80, 0xe2, 0xeb, 0x27, 0xb2, 0x75,
+    0x09, 0x83, 0x2c, 0x1a, 0x1b, 0x6e, 0x5a, 0xa0, 0x52, 0x3b, 0xd6, 0xb3, 0x29, 0xe3, 0x2f, 0x84,
+    0x53, 0xd1, 0x00, 0xed, 0x20, 0xfc, 0xb1, 0x5b, 0x6a, 0xcb, 0xbe, 0x39, 0x4a, 0x4c, 0x58, 0xcf,
+    0xd0, 0xef, 0xaa, 0xfb, 0x43, 0x4d, 0x33, 0x85, 0x45, 0xf9, 0x02, 0x7f, 0x50, 0x3c, 0x9f, 0xa8,
+    0x51, 0xa3, 0x40, 0x8f, 0x92, 0x9d, 0x38, 0xf5, 0xbc, 0xb6, 0xda, 0x21, 0x10, 0xff, 0xf3, 0xd2,
+    0xcd, 0x0c, 0x13, 0xec, 0x5f, 0x97, 0x44, 0x17, 0xc4, 0xa7, 0x7e, 0x3d, 0x64, 0x5d, 0x19, 0x73,
+    0x60, 0x81, 0x4f, 0xdc, 0x22, 0x2a, 0x90, 0x88, 0x46, 0xee, 0xb8, 0x14, 0xde, 0x5e, 0x0b, 0xdb,
+    0xe0, 0x32, 0x3a, 0x0a, 0x49, 0x06, 0x24, 0x5c, 0xc2, 0xd3, 0xac, 0x62, 0x91, 0x95, 0xe4, 0x79,
+    0xe7, 0xc8, 0x37, 0x6d, 0x8d, 0xd5, 0x4e, 0xa9, 0x6c, 0x56, 0xf4, 0xea, 0x65, 0x7a, 0xae, 0x08,
+    0xba, 0x78, 0x25, 0x2e, 0x1c, 0xa6, 0xb4, 0xc6, 0xe8, 0xdd, 0x74, 0x1f, 0x4b, 0xbd, 0x8b, 0x8a,
+    0x70, 0x3e, 0xb5, 0x66, 0x48, 0x03, 0xf6, 0x0e, 0x61, 0x35, 0x57, 0xb9, 0x86, 0xc1, 0x1d, 0x9e,
+    0xe1, 0xf8, 0x98, 0x11, 0x69, 0xd9, 0x8e, 0x94, 0x9b, 0x1e, 0x87, 0xe9, 0xce, 0x55, 0x28, 0xdf,
+    0x8c, 0xa1, 0x89, 0x0d, 0xbf, 0xe6, 0x42, 0x68, 0x41, 0x99, 0x2d, 0x0f, 0xb0, 0x54, 0xbb, 0x16};
+
+constexpr uint8_t xtime_c(uint8_t a) { return uint8_t((a << 1) ^ ((a & 0x80) ? 0x1b : 0)); }
+constexpr T0Table make_t0() {
+  T0Table t{};
+  for (int x = 0; x < 256; x++) {
+    uint8_t s = kSboxC[x];
+    uint8_t s2 = xtime_c(s);
+    uint8_t s3 = uint8_t(s2 ^ s);
+    t.v[x] = uint32_t(s2) | (uint32_t(s) << 8) | (uint32_t(s) << 16) | (uint32_t(s3) << 24);
+  }
+  return t;
+}
+
+__device__ __constant__ const T0Table c_T0 = make_t0();
+
+// FIPS-197 5.2 key expansion, evaluated at compile time for the two fixed keys
+// so that every round-key word folds into an instruction literal.
+constexpr AesRK aes_expand_c(const uint8_t (&key)[16]) {
+  constexpr uint8_t rcon[10] = {0x01, 0x02, 0x04, 0x08, 0x10, 0x20, 0x40, 0x80, 0x1b, 0x36};
+  uint8_t b[176] = {};
+  for (int i = 0; i < 16; i++) b[i] = key[i];
+  for (int i = 4; i < 44; i++) {
+    uint8_t t[4] = {b[4 * (i - 1)], b[4 * (i - 1) + 1], b[4 * (i - 1) + 2], b[4 * (i - 1) + 3]};
+    if (i % 4 == 0) {
+      const uint8_t t0 = t[0];
+      t[0] = uint8_t(kSboxC[t[1]] ^ rcon[i / 4 - 1]);
+      t[1] = kSboxC[t[2]];
+      t[2] = kSboxC[t[3]];
+      t[3] = kSboxC[t0];
+    }
+    for (int j = 0; j < 4; j++) b[4 * i + j] = uint8_t(b[4 * (i - 4) + j] ^ t[j]);
+  }
+  AesRK rk{};
+  for (int j = 0; j < 44; j++)
+    rk.w[j] = uint32_t(b[4 * j]) | (uint32_t(b[4 * j + 1]) << 8) | (uint32_t(b[4 * j + 2]) << 16) |
+              (uint32_t(b[4 * j + 3]) << 24);
+  return rk;
+}
+constexpr uint8_t kKeyHc[16] = {'M', 'I', '3', '5', '5', 'X', '-', 'H', 'a', 'l', 'f', 'T', 'r', 'e', 'e', 'H'};
+constexpr uint8_t kKeyLc[16] = {'M', 'I', '3', '5', '5', 'X', '-', 'H', 'a', 'l', 'f', 'T', 'r', 'e', 'e', 'L'};
+__device__ __constant__ const AesRK c_rkH = aes_expand_c(kKeyHc);  // tree hash H
+__device__ __constant__ const AesRK c_rkL = aes_expand_c(kKeyLc);  // leaf hash HL
+
+__device__ __forceinline__ uint32_t rotl32(uint32_t v, int k) {
+  return k == 0 ? v : ((v << k) | (v >> (32 - k)));
+}
+
+template <int NT, int REP>
+struct AesLds {
+  static_assert(NT == 1 || NT == 4, "NT");
+  static_assert(REP >= 1 && REP <= 64 && (REP & (REP - 1)) == 0, "REP");
+  static constexpr int kWords = NT * 256 * REP;
+  static constexpr int kBytes = kWords * 4;
+  static constexpr int kLogRep = REP == 1 ? 0 : REP == 2 ? 1 : REP == 4 ? 2 : REP == 8 ? 3 : REP == 16 ? 4 : REP == 32 ? 5 : 6;
+
+  const char *base;
+  uint32_t laneoff;
+
+  // Fill the replicated tables; must be called by every thread of the block.
+  __device__ static void fill(uint32_t *lds) {
+    for (int w = threadIdx.x; w < kWords; w += blockDim.x) {
+      int e = w >> kLogRep;
+      int k = e >> 8, x = e & 255;
+      lds[w] = rotl32(c_T0.v[x], 8 * k);
+    }
+    __syncthreads();
+  }
+
+  __device__ AesLds(const uint32_t *lds) : base((const char *)lds) {
+    laneoff = (threadIdx.x & (REP - 1)) * 4u;
+  }
+
+  __device__ __forceinline__ uint32_t T(int k, uint32_t x) const {
+    if constexpr (NT == 4) {
+      return *(const uint32_t *)(base + k * (256 * REP * 4) + (x << (2 + kLogRep)) + laneoff);
+    } else {
+      uint32_t v = *(const uint32_t *)(base + (x << (2 + kLogRep)) + laneoff);
+      return rotl32(v, 8 * k);
+    }
+  }
+
+  __device__ __forceinline__ uint4 enc(uint4 in, const AesRK &rk) const {
+    uint32_t c0 = in.x ^ rk.w[0], c1 = in.y ^ rk.w[1], c2 = in.z ^ rk.w[2], c3 = in.w ^ rk.w[3];
+#pragma unroll
+    for (int r = 1; r < 10; r++) {
+      uint32_t n0 = T(0, c0 & 255u) ^ T(1, (c1 >> 8) & 255u) ^ T(2, (c2 >> 16) & 255u) ^ T(3, c3 >> 24) ^ rk.w[4 * r + 0];
+      uint32_t n1 = T(0, c1 & 255u) ^ T(1, (c2 >> 8) & 255u) ^ T(2, (c3 >> 16) & 255u) ^ T(3, c0 >> 24) ^ rk.w[4 * r + 1];
+      uint32_t n2 = T(0, c2 & 255u) ^ T(1, (c3 >> 8) & 255u) ^ T(2, (c0 >> 16) & 255u) ^ T(3, c1 >> 24) ^ rk.w[4 * r + 2];
+      uint32_t n3 = T(0, c3 & 255u) ^ T(1, (c0 >> 8) & 255u) ^ T(2, (c1 >> 16) & 255u) ^ T(3, c2 >> 24) ^ rk.w[4 * r + 3];
+      c0 = n0;
+      c1 = n1;
+      c2 = n2;
+      c3 = n3;
+    }
+    uint4 o;
+    o.x = ((T(3, c0 & 255u) & 0xffu) | (T(0, (c1 >> 8) & 255u) & 0xff00u) | (T(1, (c2 >> 16) & 255u) & 0xff0000u) |
+           (T(2, c3 >> 24) & 0xff000000u)) ^ rk.w[40];
+    o.y = ((T(3, c1 & 255u) & 0xffu) | (T(0, (c2 >> 8) & 255u) & 0xff00u) | (T(1, (c3 >> 16) & 255u) & 0xff0000u) |
+           (T(2, c0 >> 24) & 0xff000000u)) ^ rk.w[41];
+    o.z = ((T(3, c2 & 255u) & 0xffu) | (T(0, (c3 >> 8) & 255u) & 0xff00u) | (T(1, (c0 >> 16) & 255u) & 0xff0000u) |
+           (T(2, c1 >> 24) & 0xff000000u)) ^ rk.w[42];
+    o.w = ((T(3, c3 & 255u) & 0xffu) | (T(0, (c0 >> 8) & 255u) & 0xff00u) | (T(1, (c1 >> 16) & 255u) & 0xff0000u) |
+           (T(2, c2 >> 24) & 0xff000000u)) ^ rk.w[43];
+    return o;
+  }
+
+  // H(s) = AES_k(sigma(s)) ^ sigma(s), sigma(xL||xR) = (xL^xR)||xL, xR = words 0,1.
+  __device__ __forceinline__ uint4 hash(uint4 s, const AesRK &rk) const {
+    uint4 x;
+    x.x = s.z;
+    x.y = s.w;
+    x.z = s.z ^ s.x;
+    x.w = s.w ^ s.y;
+    uint4 y = enc(x, rk);
+    y.x ^= x.x;
+    y.y ^= x.y;
+    y.z ^= x.z;
+    y.w ^= x.w;
+    return y;
+  }
+
+  // Dealer PRF block AES_kd(idx_lo, idx_hi, field, gate).
+  __device__ __forceinline__ uint4 prf(const AesRK &kd, uint32_t gate, uint32_t field, uint64_t idx) const {
+    uint4 b;
+    b.x = uint32_t(idx);
+    b.y = uint32_t(idx >> 32);
+    b.z = field;
+    b.w = gate;
+    return enc(b, kd);
+  }
+};
+
+__device__ __forceinline__ uint4 xor4(uint4 a, uint4 b) {
+  return make_uint4(a.x ^ b.x, a.y ^ b.y, a.z ^ b.z, a.w ^ b.w);
+}
+__device__ __forceinline__ uint4 and4(uint4 a, uint32_t m) {
+  return make_uint4(a.x & m, a.y & m, a.z & m, a.w & m);
+}
+
+// parity of the bits of b at positions > pos, pos in [0, 127]
+__device__ __forceinline__ uint32_t parity_above(uint4 b, uint32_t pos) {
+  uint32_t acc = 0;
+  const uint32_t w[4] = {b.x, b.y, b.z, b.w};
+#pragma unroll
+  for (int k = 0; k < 4; k++) {
+    uint32_t lo = 32u * k;
+    uint32_t m;
+    if (pos < lo)
+      m = 0xffffffffu;
+    else if (pos >= lo + 31)
+      m = 0u;
+    else
+      m = 0xffffffffu << (pos - lo + 1);
+    acc ^= w[k] & m;
+  }
+  return __popc(acc) & 1u;
+}
+
+}  // namespace mpcx

@@ -1,0 +1,650 @@
+// capi.hip -- extern "C" entry points of libmpcx (declared in include/mpcx.h).
+#include <hip/hip_runtime.h>
+
+#include <cstdio>
+#include <cstring>
+#include <string>
+
+#include "../../include/mpcx.h"
+#include "kernels.h"
+#include "model.h"
+#include "mpcx_core.h"
+
+// ---------------------------------------------------------------------------
+// AES-128 key schedule (FIPS-197 5.2) and the fixed keys
+// ---------------------------------------------------------------------------
+namespace mpcx {
+
+const uint8_t kSbox[256] = {
+    0x63, 0x7c, 0x77, 0x7b, 0xf2, 0x6b, 0x6f, 0xc5, 0x30, 0x01, 0x67, 0x2b, 0xfe, 0xd7, 0xab, 0x76,
+    0xca, 0x82, 0xc9, 0x7d, 0xfa, 0x59, 0x47, 0xf0, 0xad, 0xd4, 0xa2, 0xaf, 0x9c, 0xa4, 0x72, 0xc0,
+    0xb7, 0xfd, 0x93, 0x26, 0x36, 0x3f, 0xf7, 0xcc, 0x34, 0xa5, 0xe5, 0xf1, 0x71, 0xd8, 0x31, 0x15,
+    0x04, 0xc7, 0x23, 0xc3, 0x18, 0x96, 0x05, 0x9a, 0x07, 0x12, 0x80, 0xe2, 0xeb, 0x27, 0xb2, 0x75,
+    0x09, 0x83, 0x2c, 0x1a, 0x1b, 0x6e, 0x5a, 0xa0, 0x52, 0x3b, 0xd6, 0xb3, 0x29, 0xe3, 0x2f, 0x84,
+    0x53, 0xd1, 0x00, 0xed, 0x20, 0xfc, 0xb1, 0x5b, 0x6a, 0xcb, 0xbe, 0x39, 0x4a, 0x4c, 0x58, 0xcf,
+    0xd0, 0xef, 0xaa, 0xfb, 0x43, 0x4d, 0x33, 0x85, 0x45, 0xf9, 0x02, 0x7f, 0x50, 0x3c, 0x9f, 0xa8,
+    0x51, 0xa3, 0x40, 0x8f, 0x92, 0x9d, 0x38, 0xf5, 0xbc, 0xb6, 0xda, 0x21, 0x10, 0xff, 0xf3, 0xd2,
+    0xcd, 0x0c, 0x13, 0xec, 0x5f, 0x97, 0x44, 0x17, 0xc4, 0xa7, 0x7e, 0x3d, 0x64, 0x5d, 0x19, 0x73,
+    0x60, 0x81, 0x4f, 0xdc, 0x22, 0x2a, 0x90, 0x88, 0x46, 0xee, 0xb8, 0x14, 0xde, 0x5e, 0x0b, 0xdb,
+    0xe0, 0x32, 0x3a, 0x0a, 0x49, 0x06, 0x24, 0x5c, 0xc2, 0xd3, 0xac, 0x62, 0x91, 0x95, 0xe4, 0x79,
+    0xe7, 0xc8, 0x37, 0x6d, 0x8d, 0xd5, 0x4e, 0xa9, 0x6c, 0x56, 0xf4, 0xea, 0x65, 0x7a, 0xae, 0x08,
+    0xba, 0x78, 0x25, 0x2e, 0x1c, 0xa6, 0xb4, 0xc6, 0xe8, 0xdd, 0x74, 0x1f, 0x4b, 0xbd, 0x8b, 0x8a,
+    0x70, 0x3e, 0xb5, 0x66, 0x48, 0x03, 0xf6, 0x0e, 0x61, 0x35, 0x57, 0xb9, 0x86, 0xc1, 0x1d, 0x9e,
+    0xe1, 0xf8, 0x98, 0x11, 0x69, 0xd9, 0x8e, 0x94, 0x9b, 0x1e, 0x87, 0xe9, 0xce, 0x55, 0x28, 0xdf,
+    0x8c, 0xa1, 0x89, 0x0d, 0xbf, 0xe6, 0x42, 0x68, 0x41, 0x99, 0x2d, 0x0f, 0xb0, 0x54, 0xbb, 0x16};
+
+const uint8_t kKeyH[16] = {'M', 'I', '3', '5', '5', 'X', '-', 'H', 'a', 'l', 'f', 'T', 'r', 'e', 'e', 'H'};
+const uint8_t kKeyL[16] = {'M', 'I', '3', '5', '5', 'X', '-', 'H', 'a', 'l', 'f', 'T', 'r', 'e', 'e', 'L'};
+
+AesRK aes_expand(const uint8_t key[16]) {
+  static const uint8_t rcon[10] = {0x01, 0x02, 0x04, 0x08, 0x10, 0x20, 0x40, 0x80, 0x1b, 0x36};
+  uint8_t b[176];
+  std::memcpy(b, key, 16);
+  for (int i = 4; i < 44; i++) {
+    uint8_t t[4];
+    std::memcpy(t, b + 4 * (i - 1), 4);
+    if (i % 4 == 0) {
+      const uint8_t t0 = t[0];
+      t[0] = uint8_t(kSbox[t[1]] ^ rcon[i / 4 - 1]);
+      t[1] = kSbox[t[2]];
+      t[2] = kSbox[t[3]];
+      t[3] = kSbox[t0];
+    }
+    for (int j = 0; j < 4; j++) b[4 * i + j] = uint8_t(b[4 * (i - 4) + j] ^ t[j]);
+  }
+  AesRK rk;
+  for (int j = 0; j < 44; j++)
+    rk.w[j] = uint32_t(b[4 * j]) | (uint32_t(b[4 * j + 1]) << 8) | (uint32_t(b[4 * j + 2]) << 16) |
+              (uint32_t(b[4 * j + 3]) << 24);
+  return rk;
+}
+
+AesRK dealer_key(uint64_t seed) {
+  uint8_t k[16];
+  const uint64_t a = seed, b = seed ^ 0x9E3779B97F4A7C15ull;
+  for (int i = 0; i < 8; i++) {
+    k[i] = uint8_t(a >> (8 * i));
+    k[8 + i] = uint8_t(b >> (8 * i));
+  }
+  return aes_expand(k);
+}
+
+}  // namespace mpcx
+
+using namespace mpcx;
+
+struct mpcx_ctx {
+  int bw = 32, s = 12, device = 0;
+  hipStream_t own = nullptr;
+  Launch L;
+  Counters counters;
+  std::string err;
+};
+
+struct mpcx_model {
+  mpcx_ctx *ctx = nullptr;
+  ModelBase *impl = nullptr;
+};
+
+static mpcx_status fail(mpcx_ctx *c, mpcx_status st, const std::string &msg) {
+  if (c) c->err = msg;
+  return st;
+}
+static mpcx_status hip_status(mpcx_ctx *c, hipError_t e, const char *what) {
+  if (e == hipSuccess) return MPCX_OK;
+  std::string m = std::string(what) + ": " + hipGetErrorString(e);
+  if (e == hipErrorOutOfMemory) return fail(c, MPCX_ENOMEM, m);
+  if (e == hipErrorInvalidValue) return fail(c, MPCX_EINVAL, m);
+  return fail(c, MPCX_EHIP, m);
+}
+#define CHECK_CTX(c)                  \
+  do {                                \
+    if (!(c)) return MPCX_EINVAL;     \
+  } while (0)
+#define HIPC(c, x, what)                                   \
+  do {                                                     \
+    hipError_t e_ = (x);                                   \
+    if (e_ != hipSuccess) return hip_status(c, e_, what);  \
+  } while (0)
+
+// All entry points below were declared extern "C" in mpcx.h and keep C linkage.
+
+mpcx_status mpcx_create(int bw, int scale, int device, mpcx_ctx **out) {
+  if (!out || (bw != 32 && bw != 64) || scale < 1 || scale > bw / 2 - 2) return MPCX_EINVAL;
+  int ndev = 0;
+  if (hipGetDeviceCount(&ndev) != hipSuccess || ndev == 0) return MPCX_EHIP;
+  if (device < 0 || device >= ndev) return MPCX_EINVAL;
+  if (hipSetDevice(device) != hipSuccess) return MPCX_EHIP;
+  auto *c = new mpcx_ctx();
+  c->bw = bw;
+  c->s = scale;
+  c->device = device;
+  hipDeviceProp_t prop;
+  if (hipGetDeviceProperties(&prop, device) == hipSuccess) c->L.num_cu = prop.multiProcessorCount;
+  if (hipStreamCreateWithFlags(&c->own, hipStreamNonBlocking) != hipSuccess) {
+    delete c;
+    return MPCX_EHIP;
+  }
+  c->L.stream = c->own;
+  if (const char *v = std::getenv("MPCX_AES_VARIANT")) c->L.aes_variant = std::atoi(v);
+  if (const char *v = std::getenv("MPCX_AES_BLOCK")) c->L.aes_block = std::atoi(v);
+  *out = c;
+  return MPCX_OK;
+}
+
+void mpcx_destroy(mpcx_ctx *c) {
+  if (!c) return;
+  if (c->own) {
+    (void)hipStreamSynchronize(c->own);
+    (void)hipStreamDestroy(c->own);
+  }
+  delete c;
+}
+
+const char *mpcx_last_error(const mpcx_ctx *c) { return c ? c->err.c_str() : "null context"; }
+
+mpcx_status mpcx_set_stream(mpcx_ctx *c, void *s) {
+  CHECK_CTX(c);
+  c->L.stream = s ? static_cast<hipStream_t>(s) : c->own;
+  return MPCX_OK;
+}
+
+mpcx_status mpcx_synchronize(mpcx_ctx *c) {
+  CHECK_CTX(c);
+  HIPC(c, hipStreamSynchronize(c->L.stream), "hipStreamSynchronize");
+  return MPCX_OK;
+}
+
+int mpcx_aes_variant_count(void) {
+  int n;
+  aes_variants(&n);
+  return n;
+}
+const char *mpcx_aes_variant_name(int i) {
+  int n;
+  const AesVariant *v = aes_variants(&n);
+  return (i >= 0 && i < n) ? v[i].name : "";
+}
+mpcx_status mpcx_set_aes_variant(mpcx_ctx *c, int variant, int block) {
+  CHECK_CTX(c);
+  if (variant < 0 || variant >= mpcx_aes_variant_count()) return fail(c, MPCX_EINVAL, "bad AES variant");
+  if (block != 0 && (block < 64 || block > 1024 || (block % 64) != 0))
+    return fail(c, MPCX_EINVAL, "block must be a multiple of 64 in [64, 1024]");
+  c->L.aes_variant = variant;
+  c->L.aes_block = block;
+  return MPCX_OK;
+}
+
+uint64_t mpcx_bytes_exchanged(const mpcx_ctx *c) { return c ? c->counters.bytes : 0; }
+uint64_t mpcx_rounds(const mpcx_ctx *c) { return c ? c->counters.rounds : 0; }
+void mpcx_reset_counters(mpcx_ctx *c) {
+  if (c) c->counters = Counters();
+}
+
+// ---------------- PRG ----------------
+mpcx_status mpcx_prg_hash(mpcx_ctx *c, int leaf, size_t n, const void *in, void *out) {
+  CHECK_CTX(c);
+  if (!in || !out) return fail(c, MPCX_EINVAL, "null pointer");
+  HIPC(c, launch_hash(c->L, leaf, n, static_cast<const uint4 *>(in), static_cast<uint4 *>(out)), "prg_hash");
+  return MPCX_OK;
+}
+mpcx_status mpcx_prf(mpcx_ctx *c, uint64_t seed, uint32_t gate, uint32_t field, size_t n, void *out) {
+  CHECK_CTX(c);
+  if (!out) return fail(c, MPCX_EINVAL, "null pointer");
+  HIPC(c, launch_prf(c->L, seed, gate, field, n, static_cast<uint4 *>(out)), "prf");
+  return MPCX_OK;
+}
+
+// ---------------- DCF ----------------
+size_t mpcx_dcf_key_bytes(int bin, size_t n) { return dcf_layout(bin, n, 0, true).end; }
+
+mpcx_status mpcx_dcf_keygen(mpcx_ctx *c, int bin, size_t n, const uint64_t *alpha, const uint8_t *rbit,
+                            uint64_t seed, uint32_t gate, void *k0, void *k1) {
+  CHECK_CTX(c);
+  if (bin < 1 || bin > 64 || !alpha || !k0 || !k1) return fail(c, MPCX_EINVAL, "dcf_keygen: bad argument");
+  HIPC(c,
+       launch_dcf_keygen(c->L, seed, gate, F_DCFA, bin, n, alpha, rbit, static_cast<uint8_t *>(k0),
+                         static_cast<uint8_t *>(k1), 0),
+       "dcf_keygen");
+  return MPCX_OK;
+}
+
+mpcx_status mpcx_dcf_eval(mpcx_ctx *c, int party, int bin, size_t n, const void *key, const uint64_t *x,
+                          uint64_t *out) {
+  CHECK_CTX(c);
+  if (bin < 1 || bin > 64 || (party != 0 && party != 1) || !key || !x || !out)
+    return fail(c, MPCX_EINVAL, "dcf_eval: bad argument");
+  HIPC(c, launch_dcf_eval(c->L, party, bin, n, static_cast<const uint8_t *>(key), 0, x, out), "dcf_eval");
+  return MPCX_OK;
+}
+
+// ---------------- workspace for standalone gate evaluation ----------------
+namespace {
+struct Scratch {
+  void *p = nullptr;
+  size_t n = 0;
+  ~Scratch() {
+    if (p) (void)hipFree(p);
+  }
+};
+hipError_t scratch_alloc(Scratch &s, size_t bytes) {
+  return hipMalloc(&s.p, bytes ? bytes : 1);
+}
+bool valid_kind(int k) { return k == MPCX_TR || k == MPCX_TRRELU || k == MPCX_RELU || k == MPCX_TRSLACK; }
+}  // namespace
+
+size_t mpcx_tr_key_bytes(mpcx_ctx *c, int kind, size_t n) {
+  if (!c || !valid_kind(kind)) return 0;
+  return tr_layout(kind, c->bw, c->s, n, 0).end;
+}
+
+template <typename T>
+static mpcx_status tr_keygen_t(mpcx_ctx *c, int kind, size_t n, const void *in, void *out, uint64_t seed,
+                               uint32_t gate, void *k0, void *k1) {
+  TrLayout lay = tr_layout(kind, c->bw, c->s, n, 0);
+  HIPC(c,
+       launch_tr_keygen<T>(c->L, lay, seed, gate, static_cast<const T *>(in), static_cast<T *>(out),
+                           static_cast<uint8_t *>(k0), static_cast<uint8_t *>(k1)),
+       "tr_keygen");
+  return MPCX_OK;
+}
+
+mpcx_status mpcx_tr_keygen(mpcx_ctx *c, int kind, size_t n, const void *in, void *out, uint64_t seed, uint32_t gate,
+                           void *k0, void *k1) {
+  CHECK_CTX(c);
+  if (!valid_kind(kind) || !in || !out || !k0 || !k1) return fail(c, MPCX_EINVAL, "tr_keygen: bad argument");
+  return c->bw == 32 ? tr_keygen_t<uint32_t>(c, kind, n, in, out, seed, gate, k0, k1)
+                     : tr_keygen_t<uint64_t>(c, kind, n, in, out, seed, gate, k0, k1);
+}
+
+template <typename T>
+static mpcx_status tr_eval_t(mpcx_ctx *c, int kind, size_t n, const void *k0, const void *k1, const void *x,
+                             const void *bias, int ncol, void *y) {
+  TrLayout lay = tr_layout(kind, c->bw, c->s, n, 0);
+  const size_t wb = ((n + 63) / 64) * 8;
+  Scratch s;
+  HIPC(c, scratch_alloc(s, 4 * wb + 2 * n * sizeof(T)), "hipMalloc");
+  uint64_t *b = static_cast<uint64_t *>(s.p);
+  const size_t ww = wb / 8;
+  T *m0 = reinterpret_cast<T *>(b + 4 * ww);
+  T *m1 = m0 + n;
+  const uint8_t *K0 = static_cast<const uint8_t *>(k0), *K1 = static_cast<const uint8_t *>(k1);
+  const T *X = static_cast<const T *>(x), *Bi = static_cast<const T *>(bias);
+  HIPC(c, launch_tr_phase1<T>(c->L, lay, K0, K1, X, Bi, ncol, b, b + ww, b + 2 * ww, b + 3 * ww), "tr_phase1");
+  c->counters.bitplanes(n, int(lay.use_a) + int(lay.use_b));
+  HIPC(c, launch_tr_phase2<T>(c->L, lay, K0, K1, X, Bi, ncol, b, b + ww, b + 2 * ww, b + 3 * ww, m0, m1),
+       "tr_phase2");
+  c->counters.msg(n, c->bw);
+  HIPC(c, launch_reconstruct<T>(c->L, n, m0, m1, static_cast<T *>(y)), "reconstruct");
+  HIPC(c, hipStreamSynchronize(c->L.stream), "sync");
+  return MPCX_OK;
+}
+
+mpcx_status mpcx_tr_eval(mpcx_ctx *c, int kind, size_t n, const void *k0, const void *k1, const void *x,
+                         const void *bias, int ncol, void *y) {
+  CHECK_CTX(c);
+  if (!valid_kind(kind) || !k0 || !k1 || !x || !y || (bias && ncol < 1))
+    return fail(c, MPCX_EINVAL, "tr_eval: bad argument");
+  return c->bw == 32 ? tr_eval_t<uint32_t>(c, kind, n, k0, k1, x, bias, ncol, y)
+                     : tr_eval_t<uint64_t>(c, kind, n, k0, k1, x, bias, ncol, y);
+}
+
+// ---------------- MUL ----------------
+size_t mpcx_mul_key_bytes(mpcx_ctx *c, size_t nx, size_t ny, size_t nz) {
+  return c ? mul_layout(c->bw, nx, ny, nz, 0).end : 0;
+}
+template <typename T>
+static mpcx_status mul_keygen_t(mpcx_ctx *c, size_t nx, size_t ny, size_t nz, const uint32_t *ia, const uint32_t *ib,
+                                const void *rx, const void *ry, void *rz, uint64_t seed, uint32_t gate, void *k0,
+                                void *k1) {
+  MulLayout lay = mul_layout(c->bw, nx, ny, nz, 0);
+  HIPC(c,
+       launch_mul_keygen<T>(c->L, lay, seed, gate, ia, ib, static_cast<const T *>(rx), static_cast<const T *>(ry),
+                            static_cast<T *>(rz), static_cast<uint8_t *>(k0), static_cast<uint8_t *>(k1)),
+       "mul_keygen");
+  return MPCX_OK;
+}
+mpcx_status mpcx_mul_keygen(mpcx_ctx *c, size_t nx, size_t ny, size_t nz, const uint32_t *ia, const uint32_t *ib,
+                            const void *rx, const void *ry, void *rz, uint64_t seed, uint32_t gate, void *k0,
+                            void *k1) {
+  CHECK_CTX(c);
+  if (!ia || !ib || !rx || !ry || !rz || !k0 || !k1) return fail(c, MPCX_EINVAL, "mul_keygen: null pointer");
+  return c->bw == 32 ? mul_keygen_t<uint32_t>(c, nx, ny, nz, ia, ib, rx, ry, rz, seed, gate, k0, k1)
+                     : mul_keygen_t<uint64_t>(c, nx, ny, nz, ia, ib, rx, ry, rz, seed, gate, k0, k1);
+}
+template <typename T>
+static mpcx_status mul_eval_t(mpcx_ctx *c, size_t nx, size_t ny, size_t nz, const uint32_t *ia, const uint32_t *ib,
+                              const void *k0, const void *k1, const void *x, const void *y, void *z) {
+  MulLayout lay = mul_layout(c->bw, nx, ny, nz, 0);
+  Scratch s;
+  HIPC(c, scratch_alloc(s, 2 * nz * sizeof(T)), "hipMalloc");
+  T *m0 = static_cast<T *>(s.p), *m1 = m0 + nz;
+  HIPC(c,
+       launch_mul_eval<T>(c->L, lay, static_cast<const uint8_t *>(k0), static_cast<const uint8_t *>(k1), ia, ib,
+                          static_cast<const T *>(x), static_cast<const T *>(y), m0, m1),
+       "mul_eval");
+  c->counters.msg(nz, c->bw);
+  HIPC(c, launch_reconstruct<T>(c->L, nz, m0, m1, static_cast<T *>(z)), "reconstruct");
+  HIPC(c, hipStreamSynchronize(c->L.stream), "sync");
+  return MPCX_OK;
+}
+mpcx_status mpcx_mul_eval(mpcx_ctx *c, size_t nx, size_t ny, size_t nz, const uint32_t *ia, const uint32_t *ib,
+                          const void *k0, const void *k1, const void *x, const void *y, void *z) {
+  CHECK_CTX(c);
+  if (!ia || !ib || !k0 || !k1 || !x || !y || !z) return fail(c, MPCX_EINVAL, "mul_eval: null pointer");
+  return c->bw == 32 ? mul_eval_t<uint32_t>(c, nx, ny, nz, ia, ib, k0, k1, x, y, z)
+                     : mul_eval_t<uint64_t>(c, nx, ny, nz, ia, ib, k0, k1, x, y, z);
+}
+
+// ---------------- LUT8 ----------------
+size_t mpcx_lut8_key_bytes(mpcx_ctx *c, size_t n) { return c ? lut8_layout(c->bw, n, 0).end : 0; }
+template <typename T>
+static mpcx_status lut_keygen_t(mpcx_ctx *c, size_t n, const void *in, void *out, uint64_t seed, uint32_t gate,
+                                void *k0, void *k1) {
+  Lut8Layout lay = lut8_layout(c->bw, n, 0);
+  HIPC(c,
+       launch_lut8_keygen<T>(c->L, lay, seed, gate, static_cast<const T *>(in), static_cast<T *>(out),
+                             static_cast<uint8_t *>(k0), static_cast<uint8_t *>(k1)),
+       "lut8_keygen");
+  return MPCX_OK;
+}
+mpcx_status mpcx_lut8_keygen(mpcx_ctx *c, size_t n, const void *in, void *out, uint64_t seed, uint32_t gate, void *k0,
+                             void *k1) {
+  CHECK_CTX(c);
+  if (!in || !out || !k0 || !k1) return fail(c, MPCX_EINVAL, "lut8_keygen: null pointer");
+  return c->bw == 32 ? lut_keygen_t<uint32_t>(c, n, in, out, seed, gate, k0, k1)
+                     : lut_keygen_t<uint64_t>(c, n, in, out, seed, gate, k0, k1);
+}
+template <typename T>
+static mpcx_status lut_eval_t(mpcx_ctx *c, size_t n, const void *k0, const void *k1, const void *table, const void *x,
+                              void *y) {
+  Lut8Layout lay = lut8_layout(c->bw, n, 0);
+  Scratch s;
+  HIPC(c, scratch_alloc(s, 3 * n * sizeof(T)), "hipMalloc");
+  T *m0 = static_cast<T *>(s.p), *m1 = m0 + n, *vh = m1 + n;
+  const uint8_t *K0 = static_cast<const uint8_t *>(k0), *K1 = static_cast<const uint8_t *>(k1);
+  HIPC(c,
+       launch_lut8_phase1<T>(c->L, lay, K0, K1, static_cast<const T *>(table), static_cast<const T *>(x), m0, m1),
+       "lut8_phase1");
+  c->counters.msg(n, c->bw);
+  HIPC(c, launch_reconstruct<T>(c->L, n, m0, m1, vh), "reconstruct");
+  HIPC(c, launch_lut8_phase2<T>(c->L, lay, K0, K1, vh, m0, m1), "lut8_phase2");
+  c->counters.msg(n, c->bw);
+  HIPC(c, launch_reconstruct<T>(c->L, n, m0, m1, static_cast<T *>(y)), "reconstruct");
+  HIPC(c, hipStreamSynchronize(c->L.stream), "sync");
+  return MPCX_OK;
+}
+mpcx_status mpcx_lut8_eval(mpcx_ctx *c, size_t n, const void *k0, const void *k1, const void *table, const void *x,
+                           void *y) {
+  CHECK_CTX(c);
+  if (!k0 || !k1 || !table || !x || !y) return fail(c, MPCX_EINVAL, "lut8_eval: null pointer");
+  return c->bw == 32 ? lut_eval_t<uint32_t>(c, n, k0, k1, table, x, y)
+                     : lut_eval_t<uint64_t>(c, n, k0, k1, table, x, y);
+}
+
+// ---------------- SxS ----------------
+size_t mpcx_sxs_key_bytes(mpcx_ctx *c, int nb, int M, int K, int N) {
+  return c ? sxs_layout(c->bw, nb, M, K, N, 0).end : 0;
+}
+template <typename T>
+static mpcx_status sxs_keygen_t(mpcx_ctx *c, int nb, int M, int K, int N, const void *ra, const void *rb, void *rc,
+                                uint64_t seed, uint32_t gate, void *k0v, void *k1v) {
+  SxsLayout lay = sxs_layout(c->bw, nb, M, K, N, 0);
+  uint8_t *k0 = static_cast<uint8_t *>(k0v), *k1 = static_cast<uint8_t *>(k1v);
+  const size_t nc = size_t(nb) * M * N;
+  T *RA0 = reinterpret_cast<T *>(k0 + lay.off_ra), *RA1 = reinterpret_cast<T *>(k1 + lay.off_ra);
+  T *RB0 = reinterpret_cast<T *>(k0 + lay.off_rb), *RB1 = reinterpret_cast<T *>(k1 + lay.off_rb);
+  HIPC(c, launch_split<T>(c->L, seed, gate, F_SPLIT + 0, size_t(nb) * M * K, static_cast<const T *>(ra), RA0, RA1,
+                          nullptr),
+       "split");
+  HIPC(c, launch_split<T>(c->L, seed, gate, F_SPLIT + 1, size_t(nb) * K * N, static_cast<const T *>(rb), RB0, RB1,
+                          nullptr),
+       "split");
+  HIPC(c, launch_prf_ring<T>(c->L, seed, gate, F_ROUT, nc, static_cast<T *>(rc)), "prf");
+  Scratch s;
+  HIPC(c, scratch_alloc(s, nc * sizeof(T)), "hipMalloc");
+  T *g = static_cast<T *>(s.p);
+  GemmArgs<T> a;
+  a.M = M;
+  a.K = K;
+  a.N = N;
+  a.batch = nb;
+  a.sA = size_t(M) * K;
+  a.sB = size_t(K) * N;
+  a.sC = size_t(M) * N;
+  a.A1 = static_cast<const T *>(ra);
+  a.B1 = static_cast<const T *>(rb);
+  a.Cin = static_cast<const T *>(rc);
+  a.C = g;
+  HIPC(c, launch_gemm<T>(c->L, a), "gemm");
+  a.A1 = RA0;
+  a.B1 = RB0;
+  a.Cin = g;
+  a.sign = -1;
+  HIPC(c, launch_gemm<T>(c->L, a), "gemm");
+  HIPC(c, launch_split<T>(c->L, seed, gate, F_SPLIT + 2, nc, g, reinterpret_cast<T *>(k0 + lay.off_c),
+                          reinterpret_cast<T *>(k1 + lay.off_c), nullptr),
+       "split");
+  HIPC(c, hipStreamSynchronize(c->L.stream), "sync");
+  return MPCX_OK;
+}
+mpcx_status mpcx_sxs_keygen(mpcx_ctx *c, int nb, int M, int K, int N, const void *ra, const void *rb, void *rc,
+                            uint64_t seed, uint32_t gate, void *k0, void *k1) {
+  CHECK_CTX(c);
+  if (nb < 1 || M < 1 || K < 1 || N < 1 || !ra || !rb || !rc || !k0 || !k1)
+    return fail(c, MPCX_EINVAL, "sxs_keygen: bad argument");
+  return c->bw == 32 ? sxs_keygen_t<uint32_t>(c, nb, M, K, N, ra, rb, rc, seed, gate, k0, k1)
+                     : sxs_keygen_t<uint64_t>(c, nb, M, K, N, ra, rb, rc, seed, gate, k0, k1);
+}
+template <typename T>
+static mpcx_status sxs_eval_t(mpcx_ctx *c, int nb, int M, int K, int N, const void *k0v, const void *k1v,
+                              const void *a, const void *b, void *out) {
+  SxsLayout lay = sxs_layout(c->bw, nb, M, K, N, 0);
+  const uint8_t *k0 = static_cast<const uint8_t *>(k0v), *k1 = static_cast<const uint8_t *>(k1v);
+  const size_t nc = size_t(nb) * M * N;
+  Scratch s;
+  HIPC(c, scratch_alloc(s, 2 * nc * sizeof(T)), "hipMalloc");
+  T *m0 = static_cast<T *>(s.p), *m1 = m0 + nc;
+  GemmArgs<T> g;
+  g.M = M;
+  g.K = K;
+  g.N = N;
+  g.batch = nb;
+  g.sA = size_t(M) * K;
+  g.sB = size_t(K) * N;
+  g.sC = size_t(M) * N;
+  g.A1 = static_cast<const T *>(a);
+  g.A2 = reinterpret_cast<const T *>(k0 + lay.off_ra);
+  g.B1 = static_cast<const T *>(b);
+  g.B2 = reinterpret_cast<const T *>(k0 + lay.off_rb);
+  g.Cin = reinterpret_cast<const T *>(k0 + lay.off_c);
+  g.C = m0;
+  HIPC(c, launch_gemm<T>(c->L, g), "gemm");
+  GemmArgs<T> h = g;
+  h.A2 = nullptr;
+  h.B2 = nullptr;
+  h.B1 = reinterpret_cast<const T *>(k1 + lay.off_rb);
+  h.Cin = reinterpret_cast<const T *>(k1 + lay.off_c);
+  h.C = m1;
+  h.sign = -1;
+  HIPC(c, launch_gemm<T>(c->L, h), "gemm");
+  h.A1 = reinterpret_cast<const T *>(k1 + lay.off_ra);
+  h.B1 = static_cast<const T *>(b);
+  h.Cin = m1;
+  HIPC(c, launch_gemm<T>(c->L, h), "gemm");
+  c->counters.msg(nc, c->bw);
+  HIPC(c, launch_reconstruct<T>(c->L, nc, m0, m1, static_cast<T *>(out)), "reconstruct");
+  HIPC(c, hipStreamSynchronize(c->L.stream), "sync");
+  return MPCX_OK;
+}
+mpcx_status mpcx_sxs_eval(mpcx_ctx *c, int nb, int M, int K, int N, const void *k0, const void *k1, const void *a,
+                          const void *b, void *out) {
+  CHECK_CTX(c);
+  if (nb < 1 || M < 1 || K < 1 || N < 1 || !k0 || !k1 || !a || !b || !out)
+    return fail(c, MPCX_EINVAL, "sxs_eval: bad argument");
+  return c->bw == 32 ? sxs_eval_t<uint32_t>(c, nb, M, K, N, k0, k1, a, b, out)
+                     : sxs_eval_t<uint64_t>(c, nb, M, K, N, k0, k1, a, b, out);
+}
+
+template <typename T>
+static mpcx_status gemm_t(mpcx_ctx *c, int M, int K, int N, const void *a, const void *b, void *out) {
+  GemmArgs<T> g;
+  g.M = M;
+  g.K = K;
+  g.N = N;
+  g.A1 = static_cast<const T *>(a);
+  g.B1 = static_cast<const T *>(b);
+  g.C = static_cast<T *>(out);
+  HIPC(c, launch_gemm<T>(c->L, g), "gemm");
+  return MPCX_OK;
+}
+mpcx_status mpcx_ring_gemm(mpcx_ctx *c, int M, int K, int N, const void *a, const void *b, void *out) {
+  CHECK_CTX(c);
+  if (M < 1 || K < 1 || N < 1 || !a || !b || !out) return fail(c, MPCX_EINVAL, "ring_gemm: bad argument");
+  return c->bw == 32 ? gemm_t<uint32_t>(c, M, K, N, a, b, out) : gemm_t<uint64_t>(c, M, K, N, a, b, out);
+}
+
+// ---------------- reveal ----------------
+size_t mpcx_reveal_key_bytes(mpcx_ctx *c, size_t n) { return c ? reveal_layout(c->bw, n, 0).end : 0; }
+template <typename T>
+static mpcx_status reveal_keygen_t(mpcx_ctx *c, size_t n, void *mask, uint64_t seed, uint32_t gate, void *k0,
+                                   void *k1) {
+  RevealLayout lay = reveal_layout(c->bw, n, 0);
+  HIPC(c,
+       launch_reveal_keygen<T>(c->L, lay, seed, gate, static_cast<T *>(mask), static_cast<uint8_t *>(k0),
+                               static_cast<uint8_t *>(k1)),
+       "reveal_keygen");
+  return MPCX_OK;
+}
+mpcx_status mpcx_reveal_keygen(mpcx_ctx *c, size_t n, void *mask, uint64_t seed, uint32_t gate, void *k0, void *k1) {
+  CHECK_CTX(c);
+  if (!mask || !k0 || !k1) return fail(c, MPCX_EINVAL, "reveal_keygen: null pointer");
+  return c->bw == 32 ? reveal_keygen_t<uint32_t>(c, n, mask, seed, gate, k0, k1)
+                     : reveal_keygen_t<uint64_t>(c, n, mask, seed, gate, k0, k1);
+}
+template <typename T>
+static mpcx_status reveal_eval_t(mpcx_ctx *c, size_t n, const void *k0, const void *k1, const void *v0,
+                                 const void *v1, void *out) {
+  RevealLayout lay = reveal_layout(c->bw, n, 0);
+  Scratch s;
+  HIPC(c, scratch_alloc(s, 2 * n * sizeof(T)), "hipMalloc");
+  T *m0 = static_cast<T *>(s.p), *m1 = m0 + n;
+  HIPC(c,
+       launch_reveal_eval<T>(c->L, lay, static_cast<const uint8_t *>(k0), static_cast<const uint8_t *>(k1),
+                             static_cast<const T *>(v0), static_cast<const T *>(v1), 0, m0, m1),
+       "reveal_eval");
+  c->counters.msg(n, c->bw);
+  HIPC(c, launch_reconstruct<T>(c->L, n, m0, m1, static_cast<T *>(out)), "reconstruct");
+  HIPC(c, hipStreamSynchronize(c->L.stream), "sync");
+  return MPCX_OK;
+}
+mpcx_status mpcx_reveal_eval(mpcx_ctx *c, size_t n, const void *k0, const void *k1, const void *v0, const void *v1,
+                             void *out) {
+  CHECK_CTX(c);
+  if (!k0 || !k1 || !v0 || !v1 || !out) return fail(c, MPCX_EINVAL, "reveal_eval: null pointer");
+  return c->bw == 32 ? reveal_eval_t<uint32_t>(c, n, k0, k1, v0, v1, out)
+                     : reveal_eval_t<uint64_t>(c, n, k0, k1, v0, v1, out);
+}
+
+// ---------------- model ----------------
+mpcx_status mpcx_model_create(mpcx_ctx *c, const mpcx_model_dims *dims, const int64_t *W, size_t nW,
+                              mpcx_model **out) {
+  CHECK_CTX(c);
+  if (!dims || !W || !out) return fail(c, MPCX_EINVAL, "model_create: null pointer");
+  ModelDims d;
+  d.n_nodes = dims->n_nodes;
+  d.feat = dims->feat;
+  for (int i = 0; i < 3; i++) d.gcn[i] = dims->gcn[i];
+  for (int i = 0; i < 2; i++) d.dfc[i] = dims->dfc[i];
+  d.prot = dims->prot;
+  d.nfus = dims->nfus;
+  for (int i = 0; i < 4; i++) d.fus[i] = dims->fus[i];
+  d.lut_nmax = dims->lut_nmax;
+  std::string err;
+  ModelBase *impl = make_model(c->bw, c->s, d, W, nW, c->L, &err);
+  if (!impl) return fail(c, MPCX_EINVAL, "model_create: " + err);
+  auto *m = new mpcx_model();
+  m->ctx = c;
+  m->impl = impl;
+  *out = m;
+  return MPCX_OK;
+}
+
+void mpcx_model_destroy(mpcx_model *m) {
+  if (!m) return;
+  delete m->impl;
+  delete m;
+}
+
+size_t mpcx_model_key_bytes(const mpcx_model *m, int B) { return (m && B > 0) ? m->impl->key_bytes(B) : 0; }
+
+mpcx_status mpcx_model_keygen(mpcx_model *m, int B, uint64_t seed) {
+  if (!m) return MPCX_EINVAL;
+  if (B < 1) return fail(m->ctx, MPCX_EINVAL, "B must be >= 1");
+  HIPC(m->ctx, m->impl->keygen(B, seed), "model_keygen");
+  return MPCX_OK;
+}
+
+mpcx_status mpcx_model_import_keys(mpcx_model *m, int B, const void *k0, const void *k1, size_t bytes) {
+  if (!m || !k0 || !k1) return MPCX_EINVAL;
+  if (bytes != m->impl->key_bytes(B)) return fail(m->ctx, MPCX_EINVAL, "key size mismatch");
+  HIPC(m->ctx, m->impl->import_keys(B, k0, k1, bytes), "model_import_keys");
+  return MPCX_OK;
+}
+
+mpcx_status mpcx_model_export_keys(mpcx_model *m, int party, void *dst, size_t bytes) {
+  if (!m || !dst || (party != 0 && party != 1)) return MPCX_EINVAL;
+  HIPC(m->ctx, m->impl->export_keys(party, dst, bytes), "model_export_keys");
+  return MPCX_OK;
+}
+
+mpcx_status mpcx_model_set_inputs(mpcx_model *m, int B, const void *x0, const void *x1, const void *a0, const void *a1,
+                                  const void *m0, const void *m1, const int64_t *prot) {
+  if (!m || !x0 || !x1 || !a0 || !a1 || !m0 || !m1 || !prot) return MPCX_EINVAL;
+  if (B < 1) return fail(m->ctx, MPCX_EINVAL, "B must be >= 1");
+  HIPC(m->ctx, m->impl->set_inputs(B, x0, x1, a0, a1, m0, m1, prot), "model_set_inputs");
+  return MPCX_OK;
+}
+
+mpcx_status mpcx_model_forward(mpcx_model *m, int B) {
+  if (!m) return MPCX_EINVAL;
+  m->impl->counters = Counters();
+  hipError_t e = m->impl->forward(B);
+  if (e == hipErrorInvalidValue) return fail(m->ctx, MPCX_ESTATE, "forward: keys or inputs not set for this B");
+  HIPC(m->ctx, e, "model_forward");
+  m->ctx->counters.bytes += m->impl->counters.bytes;
+  m->ctx->counters.rounds += m->impl->counters.rounds;
+  return MPCX_OK;
+}
+
+mpcx_status mpcx_model_output(mpcx_model *m, int B, int64_t *out) {
+  if (!m || !out) return MPCX_EINVAL;
+  HIPC(m->ctx, m->impl->output(out, B), "model_output");
+  return MPCX_OK;
+}
+
+mpcx_status mpcx_model_profile(mpcx_model *m, int enable) {
+  if (!m) return MPCX_EINVAL;
+  m->impl->timer.reset();
+  m->impl->timer.on = enable != 0;
+  return MPCX_OK;
+}
+
+mpcx_status mpcx_model_profile_read(mpcx_model *m, int *launches, double *ms, double *elements, double *aes) {
+  if (!m) return MPCX_EINVAL;
+  auto &t = m->impl->timer;
+  HIPC(m->ctx, hipStreamSynchronize(m->ctx->L.stream), "sync");
+  double tot = 0, el = 0, ae = 0;
+  for (size_t k = 0; k + 1 < t.ev.size(); k += 2) {
+    float f = 0;
+    HIPC(m->ctx, hipEventElapsedTime(&f, t.ev[k], t.ev[k + 1]), "hipEventElapsedTime");
+    tot += f;
+    el += 2.0 * double(t.elems[k / 2]);
+    ae += 2.0 * double(t.elems[k / 2]) * double(t.levels[k / 2]);
+  }
+  if (launches) *launches = int(t.ev.size() / 2);
+  if (ms) *ms = tot;
+  if (elements) *elements = el;
+  if (aes) *aes = ae;
+  return MPCX_OK;
+}

@@ -1,0 +1,94 @@
+// dcf_dev.h -- device-side half-tree DPF/DCF walks (evaluation and dealer).
+//
+// Evaluation of the comparison [x < alpha] (m-bit x): walk the DPF tree of the
+// point alpha along the bits of x, MSB first.  At every level where the bit of x
+// is 0 the right sibling's control bit is XORed into the output: the two parties'
+// control bits differ exactly on the path of alpha, so the XOR of both outputs is
+// 1 iff the path of alpha leaves the path of x to the right, i.e. x < alpha.  The
+// 128-bit leaf holds the last 7 levels as a one-hot block, and the bits above
+// the low 7 bits of x are folded in with a parity.  This is the DPF-based DCF the
+// reference builds on (gpu_mpc/dpf_dcf_adapter.h:1-12, gpu_mpc/ddg_orca.h:11-12).
+//
+// The tree is the half-tree one (Guo et al., EUROCRYPT 2023): one fixed-key AES
+// call per level,  sL = H(s) ^ t*CW,  sR = sL ^ s,  t = lsb(s).
+#pragma once
+#include "aes_dev.h"
+
+namespace mpcx {
+
+template <class A>
+__device__ __forceinline__ uint32_t dcf_eval_walk(const A &aes, uint4 s,
+                                                  int m, int L, const uint4 *__restrict__ cw, size_t stride,
+                                                  uint4 leaf, uint64_t x) {
+  uint32_t t = s.x & 1u, out = 0;
+  uint4 cnext = L > 0 ? cw[0] : make_uint4(0, 0, 0, 0);
+  for (int l = 0; l < L; l++) {
+    const uint4 c = cnext;
+    if (l + 1 < L) cnext = cw[size_t(l + 1) * stride];
+    const uint32_t bit = uint32_t(x >> (m - 1 - l)) & 1u;
+    const uint4 h = aes.hash(s, c_rkH);
+    const uint4 sl = xor4(h, and4(c, 0u - t));
+    const uint32_t tl = sl.x & 1u;
+    out ^= (bit ^ 1u) & (tl ^ t);
+    s = xor4(sl, and4(s, 0u - bit));
+    t = tl ^ (t & bit);
+  }
+  const uint4 lb = xor4(aes.hash(s, c_rkL), and4(leaf, 0u - t));
+  const uint32_t pos = m >= 7 ? uint32_t(x & 127u) : uint32_t(x);
+  return out ^ parity_above(lb, pos);
+}
+
+struct DcfGenOut {
+  uint4 s0;      // party 0's final on-path seed
+  uint32_t t0;   // party 0's final on-path control bit
+  uint4 leafcw;  // leaf correction word
+};
+
+// Dealer walk for one element.  Writes the root seeds, level correction words
+// (level-major, stride N) and the leaf correction word of both parties.
+template <class A>
+__device__ __forceinline__ DcfGenOut dcf_gen_walk(const A &aes, const AesRK &kd, uint32_t gate, uint32_t fb, int m, int L,
+                                                  uint64_t alpha, size_t i, size_t N, uint8_t *k0,
+                                                  uint8_t *k1, size_t off_root, size_t off_cw,
+                                                  size_t off_leaf) {
+  uint4 s0 = aes.prf(kd, gate, fb + 0, i);
+  s0.x &= ~1u;
+  uint4 D = aes.prf(kd, gate, fb + 1, i);
+  D.x |= 1u;
+  uint4 s1 = xor4(s0, D);
+  reinterpret_cast<uint4 *>(k0 + off_root)[i] = s0;
+  reinterpret_cast<uint4 *>(k1 + off_root)[i] = s1;
+  uint32_t t0 = 0, t1 = 1;
+  uint4 *c0 = reinterpret_cast<uint4 *>(k0 + off_cw) + i;
+  uint4 *c1 = reinterpret_cast<uint4 *>(k1 + off_cw) + i;
+  for (int l = 0; l < L; l++) {
+    const uint32_t a = uint32_t(alpha >> (m - 1 - l)) & 1u;
+    const uint4 h0 = aes.hash(s0, c_rkH);
+    const uint4 h1 = aes.hash(s1, c_rkH);
+    const uint4 cw = xor4(xor4(h0, h1), and4(D, a - 1u));  // a ? 0 : D
+    c0[size_t(l) * N] = cw;
+    c1[size_t(l) * N] = cw;
+    const uint4 sl0 = xor4(h0, and4(cw, 0u - t0));
+    const uint4 sl1 = xor4(h1, and4(cw, 0u - t1));
+    s0 = xor4(sl0, and4(s0, 0u - a));
+    s1 = xor4(sl1, and4(s1, 0u - a));
+    t0 = s0.x & 1u;
+    t1 = s1.x & 1u;
+  }
+  const uint32_t pos = m >= 7 ? uint32_t(alpha & 127u) : uint32_t(alpha);
+  uint4 lcw = xor4(aes.hash(s0, c_rkL), aes.hash(s1, c_rkL));
+  const uint32_t bitv = 1u << (pos & 31u);
+  lcw.x ^= (pos >> 5) == 0 ? bitv : 0u;
+  lcw.y ^= (pos >> 5) == 1 ? bitv : 0u;
+  lcw.z ^= (pos >> 5) == 2 ? bitv : 0u;
+  lcw.w ^= (pos >> 5) == 3 ? bitv : 0u;
+  reinterpret_cast<uint4 *>(k0 + off_leaf)[i] = lcw;
+  reinterpret_cast<uint4 *>(k1 + off_leaf)[i] = lcw;
+  DcfGenOut o;
+  o.s0 = s0;
+  o.t0 = t0;
+  o.leafcw = lcw;
+  return o;
+}
+
+}  // namespace mpcx

@@ -1,0 +1,140 @@
+// kernels.h -- host-side launchers of the libmpcx HIP kernels.
+//
+// Every launcher enqueues on the given stream and returns the launch status.
+// Two-party kernels take both parties' key blocks: blockIdx.y selects the party
+// and a party's threads read only that party's key planes; exchanged messages
+// are written to per-party device buffers and read back by the peer's kernels
+// (the online exchange through device memory).
+#pragma once
+#include <hip/hip_runtime.h>
+
+#include <cstddef>
+#include <cstdint>
+
+#include "mpcx_core.h"
+
+namespace mpcx {
+
+struct Launch {
+  hipStream_t stream = nullptr;
+  int num_cu = 256;
+  int aes_variant = 0;  // LDS T-table layout, see aes_variants()
+  int aes_block = 0;    // threads per block for AES kernels (0 = variant default)
+};
+
+struct AesVariant {
+  int nt, rep, block;
+  const char *name;
+};
+const AesVariant *aes_variants(int *count);
+
+// ---------------- PRG ----------------
+hipError_t launch_hash(const Launch &L, int leaf, size_t n, const uint4 *in, uint4 *out);
+hipError_t launch_prf(const Launch &L, uint64_t seed, uint32_t gate, uint32_t field, size_t n, uint4 *out);
+
+// ---------------- standalone DCF ----------------
+hipError_t launch_dcf_keygen(const Launch &L, uint64_t seed, uint32_t gate, uint32_t fbase, int m, size_t n,
+                             const uint64_t *alpha, const uint8_t *rbit, uint8_t *k0, uint8_t *k1, size_t base);
+hipError_t launch_dcf_eval(const Launch &L, int party, int m, size_t n, const uint8_t *key, size_t base,
+                           const uint64_t *x, uint64_t *out_bits);
+
+// ---------------- truncation / ReLU family ----------------
+template <typename T>
+struct TrPlan {
+  TrLayout lay;
+  const uint8_t *key[2];
+};
+
+template <typename T>
+hipError_t launch_tr_keygen(const Launch &L, const TrLayout &lay, uint64_t seed, uint32_t gate, const T *in_mask,
+                            T *out_mask, uint8_t *k0, uint8_t *k1);
+// phase 1: DCF evaluation, writes bit messages bits_a[p], bits_b[p] (zwords(N) u32 each)
+template <typename T>
+hipError_t launch_tr_phase1(const Launch &L, const TrLayout &lay, const uint8_t *k0, const uint8_t *k1,
+                            const T *xhat, const T *bias, int bias_ncol, uint64_t *bits_a0, uint64_t *bits_a1,
+                            uint64_t *bits_b0, uint64_t *bits_b1);
+// phase 2: output shares after the bit exchange, writes msg0/msg1 (N each)
+template <typename T>
+hipError_t launch_tr_phase2(const Launch &L, const TrLayout &lay, const uint8_t *k0, const uint8_t *k1,
+                            const T *xhat, const T *bias, int bias_ncol, const uint64_t *bits_a0,
+                            const uint64_t *bits_a1, const uint64_t *bits_b0, const uint64_t *bits_b1, T *msg0,
+                            T *msg1);
+
+// out = m0 + m1 (reconstruction of a revealed value from both parties' messages)
+template <typename T>
+hipError_t launch_reconstruct(const Launch &L, size_t n, const T *m0, const T *m1, T *out);
+
+// ---------------- reveal ----------------
+template <typename T>
+hipError_t launch_reveal_keygen(const Launch &L, const RevealLayout &lay, uint64_t seed, uint32_t gate, T *mask,
+                                uint8_t *k0, uint8_t *k1);
+// msg_p = v_p + R_p ; if rowlen > 0, v_p[i] is the row sum of a_p (degree shares)
+template <typename T>
+hipError_t launch_reveal_eval(const Launch &L, const RevealLayout &lay, const uint8_t *k0, const uint8_t *k1,
+                              const T *v0, const T *v1, int rowlen, T *msg0, T *msg1);
+
+// ---------------- Beaver product ----------------
+template <typename T>
+hipError_t launch_mul_keygen(const Launch &L, const MulLayout &lay, uint64_t seed, uint32_t gate,
+                             const uint32_t *ia, const uint32_t *ib, const T *rx, const T *ry, T *rz,
+                             uint8_t *k0, uint8_t *k1);
+template <typename T>
+hipError_t launch_mul_eval(const Launch &L, const MulLayout &lay, const uint8_t *k0, const uint8_t *k1,
+                           const uint32_t *ia, const uint32_t *ib, const T *xhat, const T *yhat, T *msg0,
+                           T *msg1);
+
+// ---------------- LUT8 ----------------
+template <typename T>
+hipError_t launch_lut8_keygen(const Launch &L, const Lut8Layout &lay, uint64_t seed, uint32_t gate,
+                              const T *in_mask, T *out_mask, uint8_t *k0, uint8_t *k1);
+template <typename T>
+hipError_t launch_lut8_phase1(const Launch &L, const Lut8Layout &lay, const uint8_t *k0, const uint8_t *k1,
+                              const T *table, const T *xhat, T *msg0, T *msg1);
+template <typename T>
+hipError_t launch_lut8_phase2(const Launch &L, const Lut8Layout &lay, const uint8_t *k0, const uint8_t *k1,
+                              const T *vhat, T *msg0, T *msg1);
+
+// ---------------- ring GEMM ----------------
+// C[b] = Cin[b] + sign * (A1[b] - A2[b]) (B1[b] - B2[b]) mod 2^bw.
+// Any of A2, B2, Cin may be null.  Batch strides in elements (0 = shared).
+template <typename T>
+struct GemmArgs {
+  int M = 0, N = 0, K = 0, batch = 1;
+  const T *A1 = nullptr, *A2 = nullptr, *B1 = nullptr, *B2 = nullptr, *Cin = nullptr;
+  T *C = nullptr;
+  size_t sA = 0, sB = 0, sC = 0;
+  int sign = 1;
+};
+template <typename T>
+hipError_t launch_gemm(const Launch &L, const GemmArgs<T> &g);
+
+// ---------------- SxS keys ----------------
+template <typename T>
+hipError_t launch_split(const Launch &L, uint64_t seed, uint32_t gate, uint32_t field, size_t n, const T *v,
+                        T *p0, T *p1, T *share0_copy);
+template <typename T>
+hipError_t launch_prf_ring(const Launch &L, uint64_t seed, uint32_t gate, uint32_t field, size_t n, T *out);
+
+// ---------------- elementwise ----------------
+template <typename T>
+hipError_t launch_axpby(const Launch &L, size_t n, T a, const T *x, T b, const T *y, T c, T *out);
+// pool prep: V[r*C+c] = H[r*C+c] + S*m[r] + off
+template <typename T>
+hipError_t launch_pool_prep(const Launch &L, size_t rows, int C, const T *H, const T *m, T S, T off, T *V);
+// D[(b*pr+j)*C+c] = V[(b*R+2j+1)*C+c] - V[(b*R+2j)*C+c]
+template <typename T>
+hipError_t launch_pool_diff(const Launch &L, int B, int R, int C, const T *V, T *D);
+// Vn[(b*Rn+j)*C+c] = V[(b*R+2j)*C+c] + y0[..] (+ y1[..]); carry the odd row
+template <typename T>
+hipError_t launch_pool_combine(const Launch &L, int B, int R, int C, const T *V, const T *y0, const T *y1, T *Vn);
+// concat rows: out[b*(w1+w2)+j] = j<w1 ? a[b*w1+j] : (bzero ? 0 : b[b*w2+j-w1])
+template <typename T>
+hipError_t launch_concat(const Launch &L, int B, int w1, int w2, const T *a, const T *b, T *out);
+// output: out[b] = wrap((signed(zhat[b]-rz[b]) >> s) + bias)
+template <typename T>
+hipError_t launch_output(const Launch &L, int B, int bw, int s, const T *zhat, const T *rz, int64_t bias,
+                         int64_t *out);
+template <typename T>
+hipError_t launch_rowsum(const Launch &L, size_t rows, int len, const T *a, T *out);
+
+}  // namespace mpcx

@@ -1,0 +1,1093 @@
+// kernels.hip -- HIP kernels of the secure-inference online path for gfx950.
+//
+// Reference interfaces these kernels stand behind (EzPC GPU-MPC, called from the
+// reference's backend; signatures reconstructed from the call sites):
+//   DCF eval / keygen ........ gpuDcf / gpuKeyGenDCF    (gpu_mpc/dpf_dcf_adapter.h:266,372)
+//   ReLU ..................... gpuRelu / gpuGenReluKey   (gpu_mpc/ddg_orca.h:103-104,233)
+//   exact truncation ......... gpuTruncate / genGPUTruncateKey (gpu_mpc/ddg_orca.h:116-118,240)
+//   Beaver product ........... gpuMul / gpuKeygenMul    (gpu_mpc/secure_adj_norm.h:611-651,326-365)
+//   8-bit DPF LUT ............ gpuDpfLUT / gpuKeyGenLUT (gpu_mpc/secure_adj_norm.h:510-520,270-279)
+//   ring GEMM ................ gpuMatmul / gpuKeygenMatmul (gpu_mpc/ddg_orca_base.h:170-271,394-469)
+//   reveal ................... reconstructInPlace       (gpu_mpc/utils/gpu_comms.h:290-302)
+// The algebra of every gate is derived in DESIGN.md ("Gate algebra").
+#include <hip/hip_runtime.h>
+
+#include <type_traits>
+
+#include "dcf_dev.h"
+#include "kernels.h"
+
+namespace mpcx {
+
+// ---------------------------------------------------------------------------
+// AES LDS variants
+// ---------------------------------------------------------------------------
+static const AesVariant kVariants[] = {
+    {4, 32, 1024, "t4_rep32_b1024"}, {4, 16, 512, "t4_rep16_b512"}, {1, 32, 512, "t1_rep32_b512"},
+    {4, 1, 256, "t4_rep1_b256"},     {4, 8, 256, "t4_rep8_b256"},   {1, 64, 1024, "t1_rep64_b1024"},
+    {4, 32, 512, "t4_rep32_b512"},   {1, 16, 256, "t1_rep16_b256"},
+};
+const AesVariant *aes_variants(int *count) {
+  *count = int(sizeof(kVariants) / sizeof(kVariants[0]));
+  return kVariants;
+}
+
+template <int NT, int REP>
+struct V {
+  static constexpr int nt = NT, rep = REP;
+};
+
+template <class Fn>
+static hipError_t with_variant(const Launch &L, Fn &&fn) {
+  switch (L.aes_variant) {
+    case 0: return fn(V<4, 32>{});
+    case 1: return fn(V<4, 16>{});
+    case 2: return fn(V<1, 32>{});
+    case 3: return fn(V<4, 1>{});
+    case 4: return fn(V<4, 8>{});
+    case 5: return fn(V<1, 64>{});
+    case 6: return fn(V<4, 32>{});
+    case 7: return fn(V<1, 16>{});
+    default: return hipErrorInvalidValue;
+  }
+}
+static int variant_block(const Launch &L) {
+  if (L.aes_block > 0) return L.aes_block;
+  int n;
+  const AesVariant *v = aes_variants(&n);
+  return (L.aes_variant >= 0 && L.aes_variant < n) ? v[L.aes_variant].block : 256;
+}
+
+template <typename K>
+static int grid_for(K kernel, int block, size_t n, int num_cu) {
+  int occ = 0;
+  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ, kernel, block, 0) != hipSuccess || occ < 1) occ = 1;
+  size_t need = (n + block - 1) / block;
+  size_t cap = size_t(occ) * size_t(num_cu);
+  size_t g = need < cap ? need : cap;
+  return int(g < 1 ? 1 : g);
+}
+
+
+__device__ __forceinline__ uint32_t lane_id() { return threadIdx.x & 63u; }
+
+template <typename T>
+__device__ __forceinline__ T ring_of(uint4 b) {
+  if constexpr (sizeof(T) == 4)
+    return T(b.x);
+  else
+    return T(uint64_t(b.x) | (uint64_t(b.y) << 32));
+}
+
+__device__ __forceinline__ uint32_t get_bit(const uint64_t *plane, size_t i) {
+  return uint32_t(plane[i >> 6] >> (i & 63)) & 1u;
+}
+
+// ---------------------------------------------------------------------------
+// PRG probes
+// ---------------------------------------------------------------------------
+template <int NT, int REP>
+__global__ void k_hash(int leaf, size_t n, const uint4 *in, uint4 *out) {
+  __shared__ uint32_t lds[AesLds<NT, REP>::kWords];
+  AesLds<NT, REP>::fill(lds);
+  AesLds<NT, REP> aes(lds);
+  for (size_t i = size_t(blockIdx.x) * blockDim.x + threadIdx.x; i < n; i += size_t(gridDim.x) * blockDim.x)
+    out[i] = leaf ? aes.hash(in[i], c_rkL) : aes.hash(in[i], c_rkH);
+}
+
+hipError_t launch_hash(const Launch &L, int leaf, size_t n, const uint4 *in, uint4 *out) {
+  return with_variant(L, [&](auto v) {
+    constexpr int NT = decltype(v)::nt, REP = decltype(v)::rep;
+    int block = variant_block(L);
+    int grid = grid_for(k_hash<NT, REP>, block, n, L.num_cu);
+    hipLaunchKernelGGL((k_hash<NT, REP>), dim3(grid), dim3(block), 0, L.stream, leaf, n, in, out);
+    return hipGetLastError();
+  });
+}
+
+template <int NT, int REP>
+__global__ void k_prf(AesRK kd, uint32_t gate, uint32_t field, size_t n, uint4 *out) {
+  __shared__ uint32_t lds[AesLds<NT, REP>::kWords];
+  AesLds<NT, REP>::fill(lds);
+  AesLds<NT, REP> aes(lds);
+  for (size_t i = size_t(blockIdx.x) * blockDim.x + threadIdx.x; i < n; i += size_t(gridDim.x) * blockDim.x)
+    out[i] = aes.prf(kd, gate, field, i);
+}
+
+hipError_t launch_prf(const Launch &L, uint64_t seed, uint32_t gate, uint32_t field, size_t n, uint4 *out) {
+  const AesRK kd = dealer_key(seed);
+  return with_variant(L, [&](auto v) {
+    constexpr int NT = decltype(v)::nt, REP = decltype(v)::rep;
+    int block = variant_block(L);
+    int grid = grid_for(k_prf<NT, REP>, block, n, L.num_cu);
+    hipLaunchKernelGGL((k_prf<NT, REP>), dim3(grid), dim3(block), 0, L.stream, kd, gate, field, n, out);
+    return hipGetLastError();
+  });
+}
+
+// ---------------------------------------------------------------------------
+// standalone DCF (gpuKeyGenDCF / gpuDcf)
+// ---------------------------------------------------------------------------
+struct DcfGenArgs {
+  AesRK kd;
+  uint32_t gate, fb;
+  int m, L;
+  size_t n;
+  const uint64_t *alpha;
+  const uint8_t *rbit;
+  uint8_t *k0, *k1;
+  size_t off_root, off_cw, off_leaf, off_z;
+};
+
+template <int NT, int REP>
+__global__ void k_dcf_keygen(DcfGenArgs a) {
+  __shared__ uint32_t lds[AesLds<NT, REP>::kWords];
+  AesLds<NT, REP>::fill(lds);
+  AesLds<NT, REP> aes(lds);
+  const size_t stride = size_t(gridDim.x) * blockDim.x;
+  for (size_t base = size_t(blockIdx.x) * blockDim.x + (threadIdx.x & ~63u); base < a.n; base += stride) {
+    const size_t i = base + lane_id();
+    uint32_t z0 = 0, z1 = 0;
+    if (i < a.n) {
+      dcf_gen_walk(aes, a.kd, a.gate, a.fb, a.m, a.L, a.alpha[i], i, a.n, a.k0, a.k1, a.off_root,
+                   a.off_cw, a.off_leaf);
+      z0 = aes.prf(a.kd, a.gate, a.fb + 2, i).x & 1u;
+      z1 = z0 ^ (a.rbit ? (a.rbit[i] & 1u) : 0u);
+    }
+    const uint64_t w0 = __ballot(z0), w1 = __ballot(z1);
+    if (lane_id() == 0) {
+      reinterpret_cast<uint64_t *>(a.k0 + a.off_z)[base >> 6] = w0;
+      reinterpret_cast<uint64_t *>(a.k1 + a.off_z)[base >> 6] = w1;
+    }
+  }
+}
+
+hipError_t launch_dcf_keygen(const Launch &L, uint64_t seed, uint32_t gate, uint32_t fbase, int m, size_t n,
+                             const uint64_t *alpha, const uint8_t *rbit, uint8_t *k0, uint8_t *k1, size_t base) {
+  DcfLayout lay = dcf_layout(m, n, base, true);
+  DcfGenArgs a;
+  a.kd = dealer_key(seed);
+  a.gate = gate;
+  a.fb = fbase;
+  a.m = m;
+  a.L = lay.L;
+  a.n = n;
+  a.alpha = alpha;
+  a.rbit = rbit;
+  a.k0 = k0;
+  a.k1 = k1;
+  a.off_root = lay.off_root;
+  a.off_cw = lay.off_cw;
+  a.off_leaf = lay.off_leaf;
+  a.off_z = lay.off_z;
+  return with_variant(L, [&](auto v) {
+    constexpr int NT = decltype(v)::nt, REP = decltype(v)::rep;
+    int block = variant_block(L);
+    int grid = grid_for(k_dcf_keygen<NT, REP>, block, n, L.num_cu);
+    hipLaunchKernelGGL((k_dcf_keygen<NT, REP>), dim3(grid), dim3(block), 0, L.stream, a);
+    return hipGetLastError();
+  });
+}
+
+struct DcfEvalArgs {
+  int m, L;
+  size_t n;
+  const uint8_t *key;
+  size_t off_root, off_cw, off_leaf, off_z;
+  const uint64_t *x;
+  uint64_t *out;
+};
+
+template <int NT, int REP>
+__global__ void k_dcf_eval(DcfEvalArgs a) {
+  __shared__ uint32_t lds[AesLds<NT, REP>::kWords];
+  AesLds<NT, REP>::fill(lds);
+  AesLds<NT, REP> aes(lds);
+  const size_t stride = size_t(gridDim.x) * blockDim.x;
+  const uint4 *root = reinterpret_cast<const uint4 *>(a.key + a.off_root);
+  const uint4 *cw = reinterpret_cast<const uint4 *>(a.key + a.off_cw);
+  const uint4 *leaf = reinterpret_cast<const uint4 *>(a.key + a.off_leaf);
+  const uint64_t *zp = reinterpret_cast<const uint64_t *>(a.key + a.off_z);
+  for (size_t base = size_t(blockIdx.x) * blockDim.x + (threadIdx.x & ~63u); base < a.n; base += stride) {
+    const size_t i = base + lane_id();
+    uint32_t b = 0;
+    if (i < a.n) {
+      b = dcf_eval_walk(aes, root[i], a.m, a.L, cw + i, a.n, leaf[i], a.x[i]);
+      b ^= get_bit(zp, i);
+    }
+    const uint64_t w = __ballot(b);
+    if (lane_id() == 0) a.out[base >> 6] = w;
+  }
+}
+
+hipError_t launch_dcf_eval(const Launch &L, int party, int m, size_t n, const uint8_t *key, size_t base,
+                           const uint64_t *x, uint64_t *out_bits) {
+  (void)party;
+  DcfLayout lay = dcf_layout(m, n, base, true);
+  DcfEvalArgs a;
+  a.m = m;
+  a.L = lay.L;
+  a.n = n;
+  a.key = key;
+  a.off_root = lay.off_root;
+  a.off_cw = lay.off_cw;
+  a.off_leaf = lay.off_leaf;
+  a.off_z = lay.off_z;
+  a.x = x;
+  a.out = out_bits;
+  return with_variant(L, [&](auto v) {
+    constexpr int NT = decltype(v)::nt, REP = decltype(v)::rep;
+    int block = variant_block(L);
+    int grid = grid_for(k_dcf_eval<NT, REP>, block, n, L.num_cu);
+    hipLaunchKernelGGL((k_dcf_eval<NT, REP>), dim3(grid), dim3(block), 0, L.stream, a);
+    return hipGetLastError();
+  });
+}
+
+// ---------------------------------------------------------------------------
+// truncation / ReLU family
+// ---------------------------------------------------------------------------
+template <typename T>
+struct TrArgs {
+  AesRK kd;
+  int kind, n, s;
+  size_t N;
+  const uint8_t *k0, *k1;
+  uint8_t *w0, *w1;  // writable keys (keygen)
+  DcfLayout a, b;
+  size_t off_kappa, off_g;
+  int use_a, use_b;
+  const T *xhat;
+  const T *bias;
+  int bias_ncol;
+  uint64_t *ba[2], *bb[2];
+  const uint64_t *cba[2], *cbb[2];
+  T *msg[2];
+  const T *in_mask;
+  T *out_mask;
+  uint32_t gate;
+};
+
+template <typename T>
+__device__ __forceinline__ T tr_shifted_input(const TrArgs<T> &a, size_t i) {
+  T x = a.xhat[i];
+  if (a.kind != G_RELU && a.bias) x += T(a.bias[uint32_t(i % uint32_t(a.bias_ncol))]) << a.s;
+  return x + (T(1) << (a.n - 1));
+}
+
+template <typename T, int NT, int REP>
+__global__ void k_tr_phase1(TrArgs<T> a) {
+  __shared__ uint32_t lds[AesLds<NT, REP>::kWords];
+  AesLds<NT, REP>::fill(lds);
+  AesLds<NT, REP> aes(lds);
+  const int p = blockIdx.y;
+  const uint8_t *K = p ? a.k1 : a.k0;
+  const size_t stride = size_t(gridDim.x) * blockDim.x;
+  const T lowmask = (T(1) << (a.n - 1)) - T(1);
+  const T smask = (T(1) << a.s) - T(1);
+  for (size_t base = size_t(blockIdx.x) * blockDim.x + (threadIdx.x & ~63u); base < a.N; base += stride) {
+    const size_t i = base + lane_id();
+    uint32_t ra = 0, rb = 0;
+    if (i < a.N) {
+      const T xp = tr_shifted_input(a, i);
+      if (a.use_a) {
+        ra = dcf_eval_walk(aes, reinterpret_cast<const uint4 *>(K + a.a.off_root)[i], a.a.m, a.a.L,
+                           reinterpret_cast<const uint4 *>(K + a.a.off_cw) + i, a.N,
+                           reinterpret_cast<const uint4 *>(K + a.a.off_leaf)[i], uint64_t(xp & lowmask));
+        ra ^= get_bit(reinterpret_cast<const uint64_t *>(K + a.a.off_z), i);
+      }
+      if (a.use_b) {
+        rb = dcf_eval_walk(aes, reinterpret_cast<const uint4 *>(K + a.b.off_root)[i], a.b.m, a.b.L,
+                           reinterpret_cast<const uint4 *>(K + a.b.off_cw) + i, a.N,
+                           reinterpret_cast<const uint4 *>(K + a.b.off_leaf)[i], uint64_t(xp & smask));
+        rb ^= get_bit(reinterpret_cast<const uint64_t *>(K + a.b.off_z), i);
+      }
+    }
+    const uint64_t wa = __ballot(ra), wb = __ballot(rb);
+    if (lane_id() == 0) {
+      if (a.use_a) a.ba[p][base >> 6] = wa;
+      if (a.use_b) a.bb[p][base >> 6] = wb;
+    }
+  }
+}
+
+template <typename T>
+__global__ void k_tr_phase2(TrArgs<T> a) {
+  const int p = blockIdx.y;
+  const uint8_t *K = p ? a.k1 : a.k0;
+  const T *G = reinterpret_cast<const T *>(K + a.off_g);
+  const T *kap = reinterpret_cast<const T *>(K + a.off_kappa);
+  const T one0 = p == 0 ? T(1) : T(0);
+  for (size_t i = size_t(blockIdx.x) * blockDim.x + threadIdx.x; i < a.N; i += size_t(gridDim.x) * blockDim.x) {
+    const T xp = tr_shifted_input(a, i);
+    const uint32_t h = uint32_t(xp >> (a.n - 1)) & 1u;
+    const uint32_t bh = a.use_a ? (get_bit(a.cba[0], i) ^ get_bit(a.cba[1], i)) : 0u;
+    const uint32_t dh = a.use_b ? (get_bit(a.cbb[0], i) ^ get_bit(a.cbb[1], i)) : 0u;
+    const T A = (xp >> a.s) - (T(1) << (a.n - 1 - a.s));
+    T y;
+    if (a.kind == G_TR) {
+      const uint32_t c = h * 4 + bh * 2 + dh;
+      y = one0 * A + G[size_t(c) * a.N + i];
+    } else if (a.kind == G_TRRELU) {
+      const uint32_t c = h * 4 + bh * 2 + dh;
+      const uint32_t z = h ^ bh;
+      const T k = kap[i];
+      const T cp = z ? T(one0 - k) : k;
+      y = cp * A + G[size_t(c) * a.N + i];
+    } else if (a.kind == G_RELU) {
+      const uint32_t z = h ^ bh;
+      const T k = kap[i];
+      const T cp = z ? T(one0 - k) : k;
+      y = cp * a.xhat[i] + G[size_t(z) * a.N + i];
+    } else {  // G_TRSLACK
+      const uint32_t Hh = uint32_t(xp >> (a.n - 2)) & 3u;
+      const uint32_t c = Hh * 2 + dh;
+      y = one0 * A + G[size_t(c) * a.N + i];
+    }
+    a.msg[p][i] = y;
+  }
+}
+
+template <typename T, int NT, int REP>
+__global__ void k_tr_keygen(TrArgs<T> a) {
+  __shared__ uint32_t lds[AesLds<NT, REP>::kWords];
+  AesLds<NT, REP>::fill(lds);
+  AesLds<NT, REP> aes(lds);
+  const size_t stride = size_t(gridDim.x) * blockDim.x;
+  const int n = a.n, s = a.s;
+  const T lowmask = (T(1) << (n - 1)) - T(1);
+  const T smask = (T(1) << s) - T(1);
+  T *G0 = reinterpret_cast<T *>(a.w0 + a.off_g);
+  T *G1 = reinterpret_cast<T *>(a.w1 + a.off_g);
+  const int ncase = a.kind == G_RELU ? 2 : 8;
+  for (size_t base = size_t(blockIdx.x) * blockDim.x + (threadIdx.x & ~63u); base < a.N; base += stride) {
+    const size_t i = base + lane_id();
+    uint32_t za0 = 0, za1 = 0, zb0 = 0, zb1 = 0;
+    if (i < a.N) {
+      const T r = a.in_mask[i];
+      const uint32_t rho = uint32_t(r >> (n - 1)) & 1u;
+      const T R = r >> s;
+      const uint32_t rbi = aes.prf(a.kd, a.gate, F_DCFA + 3, i).x & 1u;
+      const uint32_t rdi = aes.prf(a.kd, a.gate, F_DCFB + 3, i).x & 1u;
+      const T rout = ring_of<T>(aes.prf(a.kd, a.gate, F_ROUT, i));
+      a.out_mask[i] = rout;
+      const uint32_t kappa = rho ^ rbi;
+      for (int c = 0; c < ncase; c++) {
+        T Gv;
+        if (a.kind == G_TR || a.kind == G_TRRELU) {
+          const uint32_t h = uint32_t(c) >> 2, bh = (uint32_t(c) >> 1) & 1u, dh = uint32_t(c) & 1u;
+          const uint32_t b = bh ^ rbi, d = dh ^ rdi;
+          const uint32_t w = h ? (rho & b) : (rho | b);
+          if (a.kind == G_TRRELU) {
+            const T cc = T(h ^ rho ^ b);
+            Gv = rout - cc * R - cc * T(d) + ((cc * T(w)) << (n - s));
+          } else {
+            Gv = rout - R - T(d) + (T(w) << (n - s));
+          }
+        } else if (a.kind == G_RELU) {
+          const T cc = T(uint32_t(c) ^ kappa);
+          Gv = rout - cc * r;
+        } else {
+          const uint32_t Hh = uint32_t(c) >> 1, dh = uint32_t(c) & 1u;
+          const uint32_t d = dh ^ rdi;
+          const uint32_t R2 = uint32_t(r >> (n - 2)) & 3u;
+          const uint32_t w = Hh < R2 ? 1u : 0u;
+          Gv = rout - R - T(d) + (T(w) << (n - s));
+        }
+        const T g0 = ring_of<T>(aes.prf(a.kd, a.gate, F_SPLIT + uint32_t(c), i));
+        G0[size_t(c) * a.N + i] = g0;
+        G1[size_t(c) * a.N + i] = Gv - g0;
+      }
+      if (a.kind == G_TRRELU || a.kind == G_RELU) {
+        const T q0 = ring_of<T>(aes.prf(a.kd, a.gate, F_SPLIT + 8, i));
+        reinterpret_cast<T *>(a.w0 + a.off_kappa)[i] = q0;
+        reinterpret_cast<T *>(a.w1 + a.off_kappa)[i] = T(kappa) - q0;
+      }
+      if (a.use_a) {
+        dcf_gen_walk(aes, a.kd, a.gate, F_DCFA, a.a.m, a.a.L, uint64_t(r & lowmask), i, a.N, a.w0,
+                     a.w1, a.a.off_root, a.a.off_cw, a.a.off_leaf);
+        za0 = aes.prf(a.kd, a.gate, F_DCFA + 2, i).x & 1u;
+        za1 = za0 ^ rbi;
+      }
+      if (a.use_b) {
+        dcf_gen_walk(aes, a.kd, a.gate, F_DCFB, a.b.m, a.b.L, uint64_t(r & smask), i, a.N, a.w0,
+                     a.w1, a.b.off_root, a.b.off_cw, a.b.off_leaf);
+        zb0 = aes.prf(a.kd, a.gate, F_DCFB + 2, i).x & 1u;
+        zb1 = zb0 ^ rdi;
+      }
+    }
+    const uint64_t wa0 = __ballot(za0), wa1 = __ballot(za1), wb0 = __ballot(zb0), wb1 = __ballot(zb1);
+    if (lane_id() == 0) {
+      if (a.use_a) {
+        reinterpret_cast<uint64_t *>(a.w0 + a.a.off_z)[base >> 6] = wa0;
+        reinterpret_cast<uint64_t *>(a.w1 + a.a.off_z)[base >> 6] = wa1;
+      }
+      if (a.use_b) {
+        reinterpret_cast<uint64_t *>(a.w0 + a.b.off_z)[base >> 6] = wb0;
+        reinterpret_cast<uint64_t *>(a.w1 + a.b.off_z)[base >> 6] = wb1;
+      }
+    }
+  }
+}
+
+template <typename T>
+static TrArgs<T> tr_args(const TrLayout &lay) {
+  TrArgs<T> a{};
+  a.kind = lay.kind;
+  a.n = lay.bw;
+  a.s = lay.s;
+  a.N = lay.N;
+  a.a = lay.a;
+  a.b = lay.b;
+  a.off_kappa = lay.off_kappa;
+  a.off_g = lay.off_g;
+  a.use_a = lay.use_a;
+  a.use_b = lay.use_b;
+  a.bias_ncol = 1;
+  return a;
+}
+
+template <typename T>
+hipError_t launch_tr_keygen(const Launch &L, const TrLayout &lay, uint64_t seed, uint32_t gate, const T *in_mask,
+                            T *out_mask, uint8_t *k0, uint8_t *k1) {
+  if (lay.bw != int(8 * sizeof(T))) return hipErrorInvalidValue;
+  TrArgs<T> a = tr_args<T>(lay);
+  a.kd = dealer_key(seed);
+  a.gate = gate;
+  a.w0 = k0;
+  a.w1 = k1;
+  a.in_mask = in_mask;
+  a.out_mask = out_mask;
+  return with_variant(L, [&](auto v) {
+    constexpr int NT = decltype(v)::nt, REP = decltype(v)::rep;
+    int block = variant_block(L);
+    int grid = grid_for(k_tr_keygen<T, NT, REP>, block, lay.N, L.num_cu);
+    hipLaunchKernelGGL((k_tr_keygen<T, NT, REP>), dim3(grid), dim3(block), 0, L.stream, a);
+    return hipGetLastError();
+  });
+}
+
+template <typename T>
+hipError_t launch_tr_phase1(const Launch &L, const TrLayout &lay, const uint8_t *k0, const uint8_t *k1,
+                            const T *xhat, const T *bias, int bias_ncol, uint64_t *bits_a0, uint64_t *bits_a1,
+                            uint64_t *bits_b0, uint64_t *bits_b1) {
+  if (lay.bw != int(8 * sizeof(T))) return hipErrorInvalidValue;
+  TrArgs<T> a = tr_args<T>(lay);
+  a.k0 = k0;
+  a.k1 = k1;
+  a.xhat = xhat;
+  a.bias = bias;
+  a.bias_ncol = bias_ncol > 0 ? bias_ncol : 1;
+  a.ba[0] = bits_a0;
+  a.ba[1] = bits_a1;
+  a.bb[0] = bits_b0;
+  a.bb[1] = bits_b1;
+  return with_variant(L, [&](auto v) {
+    constexpr int NT = decltype(v)::nt, REP = decltype(v)::rep;
+    int block = variant_block(L);
+    int grid = grid_for(k_tr_phase1<T, NT, REP>, block, lay.N, L.num_cu);
+    hipLaunchKernelGGL((k_tr_phase1<T, NT, REP>), dim3(grid, 2), dim3(block), 0, L.stream, a);
+    return hipGetLastError();
+  });
+}
+
+template <typename T>
+hipError_t launch_tr_phase2(const Launch &L, const TrLayout &lay, const uint8_t *k0, const uint8_t *k1,
+                            const T *xhat, const T *bias, int bias_ncol, const uint64_t *bits_a0,
+                            const uint64_t *bits_a1, const uint64_t *bits_b0, const uint64_t *bits_b1, T *msg0,
+                            T *msg1) {
+  if (lay.bw != int(8 * sizeof(T))) return hipErrorInvalidValue;
+  TrArgs<T> a = tr_args<T>(lay);
+  a.k0 = k0;
+  a.k1 = k1;
+  a.xhat = xhat;
+  a.bias = bias;
+  a.bias_ncol = bias_ncol > 0 ? bias_ncol : 1;
+  a.cba[0] = bits_a0;
+  a.cba[1] = bits_a1;
+  a.cbb[0] = bits_b0;
+  a.cbb[1] = bits_b1;
+  a.msg[0] = msg0;
+  a.msg[1] = msg1;
+  const int block = 256;
+  int grid = grid_for(k_tr_phase2<T>, block, lay.N, L.num_cu);
+  hipLaunchKernelGGL((k_tr_phase2<T>), dim3(grid, 2), dim3(block), 0, L.stream, a);
+  return hipGetLastError();
+}
+
+// ---------------------------------------------------------------------------
+// reconstruct / reveal
+// ---------------------------------------------------------------------------
+template <typename T>
+__global__ void k_reconstruct(size_t n, const T *m0, const T *m1, T *out) {
+  for (size_t i = size_t(blockIdx.x) * blockDim.x + threadIdx.x; i < n; i += size_t(gridDim.x) * blockDim.x)
+    out[i] = m0[i] + m1[i];
+}
+template <typename T>
+hipError_t launch_reconstruct(const Launch &L, size_t n, const T *m0, const T *m1, T *out) {
+  const int block = 256;
+  int grid = grid_for(k_reconstruct<T>, block, n, L.num_cu);
+  hipLaunchKernelGGL((k_reconstruct<T>), dim3(grid), dim3(block), 0, L.stream, n, m0, m1, out);
+  return hipGetLastError();
+}
+
+template <typename T, int NT, int REP>
+__global__ void k_split(AesRK kd, uint32_t gate, uint32_t field, size_t n, const T *v, T *p0, T *p1, T *copy0,
+                        T *mask_out) {
+  __shared__ uint32_t lds[AesLds<NT, REP>::kWords];
+  AesLds<NT, REP>::fill(lds);
+  AesLds<NT, REP> aes(lds);
+  for (size_t i = size_t(blockIdx.x) * blockDim.x + threadIdx.x; i < n; i += size_t(gridDim.x) * blockDim.x) {
+    T val;
+    if (v) {
+      val = v[i];
+    } else {  // fresh reveal mask
+      val = ring_of<T>(aes.prf(kd, gate, F_RIN, i));
+      mask_out[i] = val;
+    }
+    const T s0 = ring_of<T>(aes.prf(kd, gate, field, i));
+    p0[i] = s0;
+    p1[i] = val - s0;
+    if (copy0) copy0[i] = s0;
+  }
+}
+
+template <typename T>
+static hipError_t split_impl(const Launch &L, uint64_t seed, uint32_t gate, uint32_t field, size_t n, const T *v,
+                             T *p0, T *p1, T *copy0, T *mask_out) {
+  const AesRK kd = dealer_key(seed);
+  return with_variant(L, [&](auto vv) {
+    constexpr int NT = decltype(vv)::nt, REP = decltype(vv)::rep;
+    int block = variant_block(L);
+    int grid = grid_for(k_split<T, NT, REP>, block, n, L.num_cu);
+    hipLaunchKernelGGL((k_split<T, NT, REP>), dim3(grid), dim3(block), 0, L.stream, kd, gate, field, n, v, p0, p1,
+                       copy0, mask_out);
+    return hipGetLastError();
+  });
+}
+
+template <typename T>
+hipError_t launch_split(const Launch &L, uint64_t seed, uint32_t gate, uint32_t field, size_t n, const T *v, T *p0,
+                        T *p1, T *share0_copy) {
+  return split_impl<T>(L, seed, gate, field, n, v, p0, p1, share0_copy, nullptr);
+}
+
+template <typename T>
+hipError_t launch_reveal_keygen(const Launch &L, const RevealLayout &lay, uint64_t seed, uint32_t gate, T *mask,
+                                uint8_t *k0, uint8_t *k1) {
+  return split_impl<T>(L, seed, gate, F_SPLIT + 0, lay.N, nullptr, reinterpret_cast<T *>(k0 + lay.off_r),
+                       reinterpret_cast<T *>(k1 + lay.off_r), nullptr, mask);
+}
+
+template <typename T>
+__global__ void k_reveal_eval(size_t n, const T *R0, const T *R1, const T *v0, const T *v1, int rowlen, T *msg0,
+                              T *msg1) {
+  const int p = blockIdx.y;
+  const T *R = p ? R1 : R0;
+  const T *v = p ? v1 : v0;
+  T *msg = p ? msg1 : msg0;
+  for (size_t i = size_t(blockIdx.x) * blockDim.x + threadIdx.x; i < n; i += size_t(gridDim.x) * blockDim.x) {
+    T x;
+    if (rowlen > 0) {
+      x = 0;
+      const T *row = v + i * size_t(rowlen);
+      for (int j = 0; j < rowlen; j++) x += row[j];
+    } else {
+      x = v[i];
+    }
+    msg[i] = x + R[i];
+  }
+}
+
+template <typename T>
+hipError_t launch_reveal_eval(const Launch &L, const RevealLayout &lay, const uint8_t *k0, const uint8_t *k1,
+                              const T *v0, const T *v1, int rowlen, T *msg0, T *msg1) {
+  const int block = 256;
+  int grid = grid_for(k_reveal_eval<T>, block, lay.N, L.num_cu);
+  hipLaunchKernelGGL((k_reveal_eval<T>), dim3(grid, 2), dim3(block), 0, L.stream, lay.N,
+                     reinterpret_cast<const T *>(k0 + lay.off_r), reinterpret_cast<const T *>(k1 + lay.off_r), v0,
+                     v1, rowlen, msg0, msg1);
+  return hipGetLastError();
+}
+
+// ---------------------------------------------------------------------------
+// Beaver product
+// ---------------------------------------------------------------------------
+template <typename T, int NT, int REP>
+__global__ void k_mul_keygen_c(AesRK kd, uint32_t gate, size_t nz, const uint32_t *ia, const uint32_t *ib,
+                               const T *rx, const T *ry, T *rz, T *C0, T *C1) {
+  __shared__ uint32_t lds[AesLds<NT, REP>::kWords];
+  AesLds<NT, REP>::fill(lds);
+  AesLds<NT, REP> aes(lds);
+  for (size_t i = size_t(blockIdx.x) * blockDim.x + threadIdx.x; i < nz; i += size_t(gridDim.x) * blockDim.x) {
+    const T r = ring_of<T>(aes.prf(kd, gate, F_ROUT, i));
+    rz[i] = r;
+    const T C = rx[ia[i]] * ry[ib[i]] + r;
+    const T c0 = ring_of<T>(aes.prf(kd, gate, F_SPLIT + 2, i));
+    C0[i] = c0;
+    C1[i] = C - c0;
+  }
+}
+
+template <typename T>
+hipError_t launch_mul_keygen(const Launch &L, const MulLayout &lay, uint64_t seed, uint32_t gate,
+                             const uint32_t *ia, const uint32_t *ib, const T *rx, const T *ry, T *rz, uint8_t *k0,
+                             uint8_t *k1) {
+  hipError_t e = launch_split<T>(L, seed, gate, F_SPLIT + 0, lay.nx, rx, reinterpret_cast<T *>(k0 + lay.off_rx),
+                                 reinterpret_cast<T *>(k1 + lay.off_rx), nullptr);
+  if (e != hipSuccess) return e;
+  e = launch_split<T>(L, seed, gate, F_SPLIT + 1, lay.ny, ry, reinterpret_cast<T *>(k0 + lay.off_ry),
+                      reinterpret_cast<T *>(k1 + lay.off_ry), nullptr);
+  if (e != hipSuccess) return e;
+  const AesRK kd = dealer_key(seed);
+  return with_variant(L, [&](auto v) {
+    constexpr int NT = decltype(v)::nt, REP = decltype(v)::rep;
+    int block = variant_block(L);
+    int grid = grid_for(k_mul_keygen_c<T, NT, REP>, block, lay.nz, L.num_cu);
+    hipLaunchKernelGGL((k_mul_keygen_c<T, NT, REP>), dim3(grid), dim3(block), 0, L.stream, kd, gate, lay.nz, ia, ib,
+                       rx, ry, rz, reinterpret_cast<T *>(k0 + lay.off_c), reinterpret_cast<T *>(k1 + lay.off_c));
+    return hipGetLastError();
+  });
+}
+
+template <typename T>
+__global__ void k_mul_eval(size_t nz, const T *Rx0, const T *Rx1, const T *Ry0, const T *Ry1, const T *C0,
+                           const T *C1, const uint32_t *ia, const uint32_t *ib, const T *xhat, const T *yhat,
+                           T *msg0, T *msg1) {
+  const int p = blockIdx.y;
+  const T *Rx = p ? Rx1 : Rx0;
+  const T *Ry = p ? Ry1 : Ry0;
+  const T *Cc = p ? C1 : C0;
+  T *msg = p ? msg1 : msg0;
+  for (size_t i = size_t(blockIdx.x) * blockDim.x + threadIdx.x; i < nz; i += size_t(gridDim.x) * blockDim.x) {
+    const uint32_t a = ia[i], b = ib[i];
+    const T x = xhat[a], y = yhat[b];
+    T z = Cc[i] - x * Ry[b] - y * Rx[a];
+    if (p == 0) z += x * y;
+    msg[i] = z;
+  }
+}
+
+template <typename T>
+hipError_t launch_mul_eval(const Launch &L, const MulLayout &lay, const uint8_t *k0, const uint8_t *k1,
+                           const uint32_t *ia, const uint32_t *ib, const T *xhat, const T *yhat, T *msg0, T *msg1) {
+  const int block = 256;
+  int grid = grid_for(k_mul_eval<T>, block, lay.nz, L.num_cu);
+  hipLaunchKernelGGL((k_mul_eval<T>), dim3(grid, 2), dim3(block), 0, L.stream, lay.nz,
+                     reinterpret_cast<const T *>(k0 + lay.off_rx), reinterpret_cast<const T *>(k1 + lay.off_rx),
+                     reinterpret_cast<const T *>(k0 + lay.off_ry), reinterpret_cast<const T *>(k1 + lay.off_ry),
+                     reinterpret_cast<const T *>(k0 + lay.off_c), reinterpret_cast<const T *>(k1 + lay.off_c), ia, ib,
+                     xhat, yhat, msg0, msg1);
+  return hipGetLastError();
+}
+
+// ---------------------------------------------------------------------------
+// 8-bit DPF lookup table
+// ---------------------------------------------------------------------------
+template <typename T, int NT, int REP>
+__global__ void k_lut8_keygen(AesRK kd, uint32_t gate, Lut8Layout lay, const T *in_mask,
+                              T *out_mask, uint8_t *k0, uint8_t *k1) {
+  __shared__ uint32_t lds[AesLds<NT, REP>::kWords];
+  AesLds<NT, REP>::fill(lds);
+  AesLds<NT, REP> aes(lds);
+  const size_t N = lay.dpf.N;
+  for (size_t i = size_t(blockIdx.x) * blockDim.x + threadIdx.x; i < N; i += size_t(gridDim.x) * blockDim.x) {
+    const uint64_t alpha = uint64_t(in_mask[i]) & 255u;
+    const DcfGenOut g = dcf_gen_walk(aes, kd, gate, F_DCFA, 8, lay.dpf.L, alpha, i, N, k0, k1,
+                                     lay.dpf.off_root, lay.dpf.off_cw, lay.dpf.off_leaf);
+    const uint4 lb = xor4(aes.hash(g.s0, c_rkL), and4(g.leafcw, 0u - g.t0));
+    const uint32_t pos = uint32_t(alpha & 127u);
+    const uint32_t wsel = pos >> 5;
+    const uint32_t word = wsel == 0 ? lb.x : wsel == 1 ? lb.y : wsel == 2 ? lb.z : lb.w;
+    const uint32_t u0 = (word >> (pos & 31u)) & 1u;
+    const T sigma = u0 ? T(1) : T(0) - T(1);
+    const T rv = ring_of<T>(aes.prf(kd, gate, F_LUTV, i));
+    const T rout = ring_of<T>(aes.prf(kd, gate, F_ROUT, i));
+    out_mask[i] = rout;
+    const T C = rout - sigma * rv;
+    const T v0 = ring_of<T>(aes.prf(kd, gate, F_SPLIT + 0, i));
+    const T s0 = ring_of<T>(aes.prf(kd, gate, F_SPLIT + 1, i));
+    const T c0 = ring_of<T>(aes.prf(kd, gate, F_SPLIT + 2, i));
+    reinterpret_cast<T *>(k0 + lay.off_rv)[i] = v0;
+    reinterpret_cast<T *>(k1 + lay.off_rv)[i] = rv - v0;
+    reinterpret_cast<T *>(k0 + lay.off_sig)[i] = s0;
+    reinterpret_cast<T *>(k1 + lay.off_sig)[i] = sigma - s0;
+    reinterpret_cast<T *>(k0 + lay.off_c)[i] = c0;
+    reinterpret_cast<T *>(k1 + lay.off_c)[i] = C - c0;
+  }
+}
+
+template <typename T>
+hipError_t launch_lut8_keygen(const Launch &L, const Lut8Layout &lay, uint64_t seed, uint32_t gate,
+                              const T *in_mask, T *out_mask, uint8_t *k0, uint8_t *k1) {
+  const AesRK kd = dealer_key(seed);
+  return with_variant(L, [&](auto v) {
+    constexpr int NT = decltype(v)::nt, REP = decltype(v)::rep;
+    int block = variant_block(L);
+    int grid = grid_for(k_lut8_keygen<T, NT, REP>, block, lay.dpf.N, L.num_cu);
+    hipLaunchKernelGGL((k_lut8_keygen<T, NT, REP>), dim3(grid), dim3(block), 0, L.stream, kd, gate, lay,
+                       in_mask, out_mask, k0, k1);
+    return hipGetLastError();
+  });
+}
+
+// Phase 1: full-domain expansion of the 8-bit DPF (1 tree level + two 128-bit
+// leaves) and the signed inner product with the public table rotated by x^.
+template <typename T, int NT, int REP>
+__global__ void k_lut8_phase1(Lut8Layout lay, const uint8_t *k0, const uint8_t *k1,
+                              const T *table, const T *xhat, T *msg0, T *msg1) {
+  __shared__ uint32_t lds[AesLds<NT, REP>::kWords];
+  __shared__ T tab[256];
+  for (int k = threadIdx.x; k < 256; k += blockDim.x) tab[k] = table[k];
+  AesLds<NT, REP>::fill(lds);
+  AesLds<NT, REP> aes(lds);
+  const int p = blockIdx.y;
+  const uint8_t *K = p ? k1 : k0;
+  T *msg = p ? msg1 : msg0;
+  const size_t N = lay.dpf.N;
+  for (size_t i = size_t(blockIdx.x) * blockDim.x + threadIdx.x; i < N; i += size_t(gridDim.x) * blockDim.x) {
+    const uint4 s = reinterpret_cast<const uint4 *>(K + lay.dpf.off_root)[i];
+    const uint4 cw = reinterpret_cast<const uint4 *>(K + lay.dpf.off_cw)[i];
+    const uint4 leaf = reinterpret_cast<const uint4 *>(K + lay.dpf.off_leaf)[i];
+    const uint32_t t = s.x & 1u;
+    const uint4 sl = xor4(aes.hash(s, c_rkH), and4(cw, 0u - t));
+    const uint4 sr = xor4(sl, s);
+    const uint32_t tl = sl.x & 1u, tr = tl ^ t;
+    const uint4 L0 = xor4(aes.hash(sl, c_rkL), and4(leaf, 0u - tl));
+    const uint4 L1 = xor4(aes.hash(sr, c_rkL), and4(leaf, 0u - tr));
+    const uint32_t w[8] = {L0.x, L0.y, L0.z, L0.w, L1.x, L1.y, L1.z, L1.w};
+    const uint32_t xh = uint32_t(xhat[i]) & 255u;
+    T acc = 0;
+#pragma unroll
+    for (int q = 0; q < 8; q++) {
+      uint32_t bits = w[q];
+      while (bits) {
+        const int b = __ffs(bits) - 1;
+        bits &= bits - 1;
+        acc += tab[(xh - uint32_t(q * 32 + b)) & 255u];
+      }
+    }
+    if (p == 1) acc = T(0) - acc;
+    msg[i] = acc + reinterpret_cast<const T *>(K + lay.off_rv)[i];
+  }
+}
+
+template <typename T>
+hipError_t launch_lut8_phase1(const Launch &L, const Lut8Layout &lay, const uint8_t *k0, const uint8_t *k1,
+                              const T *table, const T *xhat, T *msg0, T *msg1) {
+  return with_variant(L, [&](auto v) {
+    constexpr int NT = decltype(v)::nt, REP = decltype(v)::rep;
+    int block = variant_block(L);
+    int grid = grid_for(k_lut8_phase1<T, NT, REP>, block, lay.dpf.N, L.num_cu);
+    hipLaunchKernelGGL((k_lut8_phase1<T, NT, REP>), dim3(grid, 2), dim3(block), 0, L.stream, lay, k0,
+                       k1, table, xhat, msg0, msg1);
+    return hipGetLastError();
+  });
+}
+
+template <typename T>
+__global__ void k_lut8_phase2(Lut8Layout lay, const uint8_t *k0, const uint8_t *k1, const T *vhat, T *msg0,
+                              T *msg1) {
+  const int p = blockIdx.y;
+  const uint8_t *K = p ? k1 : k0;
+  T *msg = p ? msg1 : msg0;
+  const size_t N = lay.dpf.N;
+  for (size_t i = size_t(blockIdx.x) * blockDim.x + threadIdx.x; i < N; i += size_t(gridDim.x) * blockDim.x)
+    msg[i] = vhat[i] * reinterpret_cast<const T *>(K + lay.off_sig)[i] + reinterpret_cast<const T *>(K + lay.off_c)[i];
+}
+
+template <typename T>
+hipError_t launch_lut8_phase2(const Launch &L, const Lut8Layout &lay, const uint8_t *k0, const uint8_t *k1,
+                              const T *vhat, T *msg0, T *msg1) {
+  const int block = 256;
+  int grid = grid_for(k_lut8_phase2<T>, block, lay.dpf.N, L.num_cu);
+  hipLaunchKernelGGL((k_lut8_phase2<T>), dim3(grid, 2), dim3(block), 0, L.stream, lay, k0, k1, vhat, msg0, msg1);
+  return hipGetLastError();
+}
+
+// ---------------------------------------------------------------------------
+// ring GEMM: 64x64 tile per 256-thread block, 4x4 outputs per thread,
+// K staged through LDS in slices of 16.  Integer multiply-add on the VALU
+// (v_mul_lo_u32 / v_mad_u64_u32); operand differences are applied on load.
+// ---------------------------------------------------------------------------
+template <typename T>
+__global__ __launch_bounds__(256) void k_gemm(GemmArgs<T> g) {
+  constexpr int BM = 64, BN = 64, BK = 16;
+  __shared__ T As[BK][BM + 1];
+  __shared__ T Bs[BK][BN + 1];
+  const int bz = blockIdx.z;
+  const T *A1 = g.A1 + size_t(bz) * g.sA;
+  const T *A2 = g.A2 ? g.A2 + size_t(bz) * g.sA : nullptr;
+  const T *B1 = g.B1 + size_t(bz) * g.sB;
+  const T *B2 = g.B2 ? g.B2 + size_t(bz) * g.sB : nullptr;
+  const int m0 = blockIdx.y * BM, n0 = blockIdx.x * BN;
+  const int tid = threadIdx.x;
+  const int tr = tid / 16, tc = tid % 16;  // 16 x 16 thread grid, 4 x 4 each
+  T acc[4][4];
+#pragma unroll
+  for (int i = 0; i < 4; i++)
+#pragma unroll
+    for (int j = 0; j < 4; j++) acc[i][j] = 0;
+  for (int k0 = 0; k0 < g.K; k0 += BK) {
+#pragma unroll
+    for (int r = 0; r < 4; r++) {
+      const int e = tid + r * 256;  // 0..1023
+      // A tile: 64 rows x 16 cols, row-major source
+      const int am = e / BK, ak = e % BK;
+      const int gm = m0 + am, gk = k0 + ak;
+      T av = 0;
+      if (gm < g.M && gk < g.K) {
+        const size_t idx = size_t(gm) * g.K + gk;
+        av = A1[idx];
+        if (A2) av -= A2[idx];
+      }
+      As[ak][am] = av;
+      // B tile: 16 rows x 64 cols
+      const int bk = e / BN, bn = e % BN;
+      const int gk2 = k0 + bk, gn = n0 + bn;
+      T bv = 0;
+      if (gk2 < g.K && gn < g.N) {
+        const size_t idx = size_t(gk2) * g.N + gn;
+        bv = B1[idx];
+        if (B2) bv -= B2[idx];
+      }
+      Bs[bk][bn] = bv;
+    }
+    __syncthreads();
+#pragma unroll
+    for (int kk = 0; kk < BK; kk++) {
+      T a[4], b[4];
+#pragma unroll
+      for (int i = 0; i < 4; i++) a[i] = As[kk][tr * 4 + i];
+#pragma unroll
+      for (int j = 0; j < 4; j++) b[j] = Bs[kk][tc * 4 + j];
+#pragma unroll
+      for (int i = 0; i < 4; i++)
+#pragma unroll
+        for (int j = 0; j < 4; j++) acc[i][j] += a[i] * b[j];
+    }
+    __syncthreads();
+  }
+  T *C = g.C + size_t(bz) * g.sC;
+  const T *Cin = g.Cin ? g.Cin + size_t(bz) * g.sC : nullptr;
+#pragma unroll
+  for (int i = 0; i < 4; i++) {
+    const int gm = m0 + tr * 4 + i;
+    if (gm >= g.M) continue;
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+      const int gn = n0 + tc * 4 + j;
+      if (gn >= g.N) continue;
+      const size_t idx = size_t(gm) * g.N + gn;
+      T v = g.sign < 0 ? T(T(0) - acc[i][j]) : acc[i][j];
+      if (Cin) v += Cin[idx];
+      C[idx] = v;
+    }
+  }
+}
+
+template <typename T>
+hipError_t launch_gemm(const Launch &L, const GemmArgs<T> &g) {
+  if (g.M <= 0 || g.N <= 0 || g.batch <= 0) return hipSuccess;
+  dim3 grid((g.N + 63) / 64, (g.M + 63) / 64, g.batch);
+  hipLaunchKernelGGL((k_gemm<T>), grid, dim3(256), 0, L.stream, g);
+  return hipGetLastError();
+}
+
+template <typename T, int NT, int REP>
+__global__ void k_prf_ring(AesRK kd, uint32_t gate, uint32_t field, size_t n, T *out) {
+  __shared__ uint32_t lds[AesLds<NT, REP>::kWords];
+  AesLds<NT, REP>::fill(lds);
+  AesLds<NT, REP> aes(lds);
+  for (size_t i = size_t(blockIdx.x) * blockDim.x + threadIdx.x; i < n; i += size_t(gridDim.x) * blockDim.x)
+    out[i] = ring_of<T>(aes.prf(kd, gate, field, i));
+}
+template <typename T>
+hipError_t launch_prf_ring(const Launch &L, uint64_t seed, uint32_t gate, uint32_t field, size_t n, T *out) {
+  const AesRK kd = dealer_key(seed);
+  return with_variant(L, [&](auto v) {
+    constexpr int NT = decltype(v)::nt, REP = decltype(v)::rep;
+    int block = variant_block(L);
+    int grid = grid_for(k_prf_ring<T, NT, REP>, block, n, L.num_cu);
+    hipLaunchKernelGGL((k_prf_ring<T, NT, REP>), dim3(grid), dim3(block), 0, L.stream, kd, gate, field, n, out);
+    return hipGetLastError();
+  });
+}
+
+// ---------------------------------------------------------------------------
+// elementwise helpers
+// ---------------------------------------------------------------------------
+template <typename T>
+__global__ void k_axpby(size_t n, T a, const T *x, T b, const T *y, T c, T *out) {
+  for (size_t i = size_t(blockIdx.x) * blockDim.x + threadIdx.x; i < n; i += size_t(gridDim.x) * blockDim.x) {
+    T v = c;
+    if (x) v += a * x[i];
+    if (y) v += b * y[i];
+    out[i] = v;
+  }
+}
+template <typename T>
+hipError_t launch_axpby(const Launch &L, size_t n, T a, const T *x, T b, const T *y, T c, T *out) {
+  const int block = 256;
+  int grid = grid_for(k_axpby<T>, block, n, L.num_cu);
+  hipLaunchKernelGGL((k_axpby<T>), dim3(grid), dim3(block), 0, L.stream, n, a, x, b, y, c, out);
+  return hipGetLastError();
+}
+
+template <typename T>
+__global__ void k_pool_prep(size_t rows, int C, const T *H, const T *m, T S, T off, T *V) {
+  const size_t n = rows * size_t(C);
+  for (size_t i = size_t(blockIdx.x) * blockDim.x + threadIdx.x; i < n; i += size_t(gridDim.x) * blockDim.x)
+    V[i] = H[i] + S * m[i / size_t(C)] + off;
+}
+template <typename T>
+hipError_t launch_pool_prep(const Launch &L, size_t rows, int C, const T *H, const T *m, T S, T off, T *V) {
+  const int block = 256;
+  int grid = grid_for(k_pool_prep<T>, block, rows * size_t(C), L.num_cu);
+  hipLaunchKernelGGL((k_pool_prep<T>), dim3(grid), dim3(block), 0, L.stream, rows, C, H, m, S, off, V);
+  return hipGetLastError();
+}
+
+template <typename T>
+__global__ void k_pool_diff(int B, int R, int C, const T *V, T *D) {
+  const int pr = R / 2;
+  const size_t n = size_t(B) * pr * C;
+  for (size_t i = size_t(blockIdx.x) * blockDim.x + threadIdx.x; i < n; i += size_t(gridDim.x) * blockDim.x) {
+    const size_t c = i % C, bj = i / C;
+    const size_t b = bj / pr, j = bj % pr;
+    const size_t e = (b * R + 2 * j) * C + c;
+    D[i] = V[e + C] - V[e];
+  }
+}
+template <typename T>
+hipError_t launch_pool_diff(const Launch &L, int B, int R, int C, const T *V, T *D) {
+  const int block = 256;
+  int grid = grid_for(k_pool_diff<T>, block, size_t(B) * (R / 2) * C, L.num_cu);
+  hipLaunchKernelGGL((k_pool_diff<T>), dim3(grid), dim3(block), 0, L.stream, B, R, C, V, D);
+  return hipGetLastError();
+}
+
+template <typename T>
+__global__ void k_pool_combine(int B, int R, int C, const T *V, const T *y0, const T *y1, T *Vn) {
+  const int pr = R / 2, Rn = pr + (R & 1);
+  const size_t n = size_t(B) * Rn * C;
+  for (size_t i = size_t(blockIdx.x) * blockDim.x + threadIdx.x; i < n; i += size_t(gridDim.x) * blockDim.x) {
+    const size_t c = i % C, bj = i / C;
+    const size_t b = bj / Rn, j = bj % Rn;
+    if (int(j) < pr) {
+      const size_t yi = (b * pr + j) * C + c;
+      T v = V[(b * R + 2 * j) * C + c] + y0[yi];
+      if (y1) v += y1[yi];
+      Vn[i] = v;
+    } else {
+      Vn[i] = V[(b * R + R - 1) * C + c];
+    }
+  }
+}
+template <typename T>
+hipError_t launch_pool_combine(const Launch &L, int B, int R, int C, const T *V, const T *y0, const T *y1, T *Vn) {
+  const int block = 256;
+  const int Rn = R / 2 + (R & 1);
+  int grid = grid_for(k_pool_combine<T>, block, size_t(B) * Rn * C, L.num_cu);
+  hipLaunchKernelGGL((k_pool_combine<T>), dim3(grid), dim3(block), 0, L.stream, B, R, C, V, y0, y1, Vn);
+  return hipGetLastError();
+}
+
+template <typename T>
+__global__ void k_concat(int B, int w1, int w2, const T *a, const T *b, T *out) {
+  const int w = w1 + w2;
+  const size_t n = size_t(B) * w;
+  for (size_t i = size_t(blockIdx.x) * blockDim.x + threadIdx.x; i < n; i += size_t(gridDim.x) * blockDim.x) {
+    const size_t r = i / w;
+    const int j = int(i % w);
+    out[i] = j < w1 ? a[r * w1 + j] : (b ? b[r * w2 + (j - w1)] : T(0));
+  }
+}
+template <typename T>
+hipError_t launch_concat(const Launch &L, int B, int w1, int w2, const T *a, const T *b, T *out) {
+  const int block = 256;
+  int grid = grid_for(k_concat<T>, block, size_t(B) * (w1 + w2), L.num_cu);
+  hipLaunchKernelGGL((k_concat<T>), dim3(grid), dim3(block), 0, L.stream, B, w1, w2, a, b, out);
+  return hipGetLastError();
+}
+
+template <typename T>
+__global__ void k_output(int B, int bw, int s, const T *zhat, const T *rz, int64_t bias, int64_t *out) {
+  const int b = blockIdx.x * blockDim.x + threadIdx.x;
+  if (b >= B) return;
+  const T z = zhat[b] - rz[b];
+  int64_t zs;
+  if constexpr (sizeof(T) == 4)
+    zs = int64_t(int32_t(z));
+  else
+    zs = int64_t(z);
+  int64_t y = (zs >> s) + bias;
+  if (bw == 32) y = int64_t(int32_t(uint32_t(uint64_t(y))));
+  out[b] = y;
+}
+template <typename T>
+hipError_t launch_output(const Launch &L, int B, int bw, int s, const T *zhat, const T *rz, int64_t bias,
+                         int64_t *out) {
+  hipLaunchKernelGGL((k_output<T>), dim3((B + 255) / 256), dim3(256), 0, L.stream, B, bw, s, zhat, rz, bias, out);
+  return hipGetLastError();
+}
+
+template <typename T>
+__global__ void k_rowsum(size_t rows, int len, const T *a, T *out) {
+  for (size_t r = size_t(blockIdx.x) * blockDim.x + threadIdx.x; r < rows; r += size_t(gridDim.x) * blockDim.x) {
+    T acc = 0;
+    for (int j = 0; j < len; j++) acc += a[r * len + j];
+    out[r] = acc;
+  }
+}
+template <typename T>
+hipError_t launch_rowsum(const Launch &L, size_t rows, int len, const T *a, T *out) {
+  const int block = 256;
+  int grid = grid_for(k_rowsum<T>, block, rows, L.num_cu);
+  hipLaunchKernelGGL((k_rowsum<T>), dim3(grid), dim3(block), 0, L.stream, rows, len, a, out);
+  return hipGetLastError();
+}
+
+// ---------------------------------------------------------------------------
+// explicit instantiations
+// ---------------------------------------------------------------------------
+#define INST(T)                                                                                                      \
+  template hipError_t launch_tr_keygen<T>(const Launch &, const TrLayout &, uint64_t, uint32_t, const T *, T *,      \
+                                          uint8_t *, uint8_t *);                                                     \
+  template hipError_t launch_tr_phase1<T>(const Launch &, const TrLayout &, const uint8_t *, const uint8_t *,        \
+                                          const T *, const T *, int, uint64_t *, uint64_t *, uint64_t *,             \
+                                          uint64_t *);                                                               \
+  template hipError_t launch_tr_phase2<T>(const Launch &, const TrLayout &, const uint8_t *, const uint8_t *,        \
+                                          const T *, const T *, int, const uint64_t *, const uint64_t *,             \
+                                          const uint64_t *, const uint64_t *, T *, T *);                             \
+  template hipError_t launch_reconstruct<T>(const Launch &, size_t, const T *, const T *, T *);                      \
+  template hipError_t launch_reveal_keygen<T>(const Launch &, const RevealLayout &, uint64_t, uint32_t, T *,         \
+                                              uint8_t *, uint8_t *);                                                 \
+  template hipError_t launch_reveal_eval<T>(const Launch &, const RevealLayout &, const uint8_t *, const uint8_t *,  \
+                                            const T *, const T *, int, T *, T *);                                    \
+  template hipError_t launch_mul_keygen<T>(const Launch &, const MulLayout &, uint64_t, uint32_t, const uint32_t *,  \
+                                           const uint32_t *, const T *, const T *, T *, uint8_t *, uint8_t *);       \
+  template hipError_t launch_mul_eval<T>(const Launch &, const MulLayout &, const uint8_t *, const uint8_t *,        \
+                                         const uint32_t *, const uint32_t *, const T *, const T *, T *, T *);        \
+  template hipError_t launch_lut8_keygen<T>(const Launch &, const Lut8Layout &, uint64_t, uint32_t, const T *, T *, \
+                                            uint8_t *, uint8_t *);                                                   \
+  template hipError_t launch_lut8_phase1<T>(const Launch &, const Lut8Layout &, const uint8_t *, const uint8_t *,    \
+                                            const T *, const T *, T *, T *);                                         \
+  template hipError_t launch_lut8_phase2<T>(const Launch &, const Lut8Layout &, const uint8_t *, const uint8_t *,    \
+                                            const T *, T *, T *);                                                    \
+  template hipError_t launch_gemm<T>(const Launch &, const GemmArgs<T> &);                                           \
+  template hipError_t launch_split<T>(const Launch &, uint64_t, uint32_t, uint32_t, size_t, const T *, T *, T *,     \
+                                      T *);                                                                          \
+  template hipError_t launch_prf_ring<T>(const Launch &, uint64_t, uint32_t, uint32_t, size_t, T *);                \
+  template hipError_t launch_axpby<T>(const Launch &, size_t, T, const T *, T, const T *, T, T *);                   \
+  template hipError_t launch_pool_prep<T>(const Launch &, size_t, int, const T *, const T *, T, T, T *);            \
+  template hipError_t launch_pool_diff<T>(const Launch &, int, int, int, const T *, T *);                            \
+  template hipError_t launch_pool_combine<T>(const Launch &, int, int, int, const T *, const T *, const T *, T *);   \
+  template hipError_t launch_concat<T>(const Launch &, int, int, int, const T *, const T *, T *);                    \
+  template hipError_t launch_output<T>(const Launch &, int, int, int, const T *, const T *, int64_t, int64_t *);     \
+  template hipError_t launch_rowsum<T>(const Launch &, size_t, int, const T *, T *);
+
+INST(uint32_t)
+INST(uint64_t)
+
+}  // namespace mpcx

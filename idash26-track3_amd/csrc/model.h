@@ -1,0 +1,78 @@
+// model.h -- the DeepDTAGen affinity branch as a sequence of two-party gates
+// (dealer keygen and online forward), both parties on one GPU.
+//
+// Mirrors DeepDTAGenAffinity<T>::_forward (gpu_mpc/deepdtagen.h:183-222) with
+// the op order of reference/fixed_forward.py:140-172:
+//   secure adjacency normalisation (secure_adj_norm.h:393-659)
+//   3 x GCN:  Z = H.W^T (public weights, no exchange) -> TR -> A_norm.(XW) (SxS)
+//             -> TRRELU(+bias)
+//   masked max-pool tree (masked_maxpool_layer.h:47-165), sentinel form
+//   drug FC (TRRELU), drug FC (TR), concat [drug, protein] (deepdtagen.h:45-101)
+//   fusion FCs (TRRELU ...), output layer unmasked with the clear output mask
+//   (ddg_orca_base.h:296-302) and truncated locally.
+#pragma once
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+#include <string>
+#include <vector>
+
+#include "kernels.h"
+#include "mpcx_core.h"
+
+namespace mpcx {
+
+struct ModelDims {
+  int n_nodes = 140, feat = 78;
+  int gcn[3] = {78, 156, 312};
+  int dfc[2] = {1024, 128};
+  int prot = 128;
+  int nfus = 3;
+  int fus[4] = {1024, 512, 1, 0};
+  int lut_nmax = 138;
+};
+
+struct Counters {
+  uint64_t bytes = 0;   // bytes exchanged, both directions
+  uint64_t rounds = 0;  // exchange rounds
+  void msg(size_t n_elems, int bw) {
+    bytes += 2ull * n_elems * uint64_t(bw / 8);
+    rounds++;
+  }
+  void bitplanes(size_t n, int planes) {
+    bytes += 2ull * uint64_t(planes) * (((n + 31) / 32) * 4);
+    rounds++;
+  }
+};
+
+// Per-kernel timing of the DCF-evaluation (phase-1) launches, HIP events on the
+// launch stream.
+struct Phase1Timer {
+  bool on = false;
+  std::vector<hipEvent_t> ev;  // start/stop pairs
+  std::vector<size_t> elems;   // elements per launch
+  std::vector<int> levels;     // AES calls per element per party
+  void reset();
+};
+
+class ModelBase {
+ public:
+  virtual ~ModelBase() = default;
+  virtual size_t key_bytes(int B) const = 0;
+  virtual hipError_t keygen(int B, uint64_t seed) = 0;
+  virtual hipError_t import_keys(int B, const void *k0, const void *k1, size_t bytes) = 0;
+  virtual hipError_t export_keys(int party, void *dst, size_t bytes) = 0;
+  virtual hipError_t set_inputs(int B, const void *x0, const void *x1, const void *a0, const void *a1,
+                                const void *m0, const void *m1, const int64_t *prot) = 0;
+  virtual hipError_t forward(int B) = 0;
+  virtual hipError_t output(int64_t *h_out, int B) = 0;
+  virtual uint8_t *arena(int party) = 0;
+  Counters counters;
+  Phase1Timer timer;
+  std::string err;
+};
+
+ModelBase *make_model(int bw, int s, const ModelDims &d, const int64_t *W, size_t nW, const Launch &L,
+                      std::string *err);
+
+}  // namespace mpcx

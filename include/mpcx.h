@@ -1,0 +1,209 @@
+/*
+ * mpcx.h -- C ABI of libmpcx, the MI355X (gfx950) implementation of the
+ * secure-inference online path of the DeepDTAGen affinity branch.
+ *
+ * Plain C: opaque handles, plain pointers and sizes, status codes, explicit
+ * HIP stream.  Both parties of the two-party protocol are evaluated in one
+ * process on one GPU; every protocol exchange goes through device memory and
+ * is counted (mpcx_bytes_exchanged).
+ *
+ * Each entry point names the reference interface it replaces (paths relative
+ * to the reference repository).  The reference's kernels live in EzPC GPU-MPC
+ * (not vendored); their signatures are those used at the cited call sites.
+ *
+ * Ring elements: uint32_t when bw == 32, uint64_t when bw == 64 ("T" below).
+ * Device pointers are marked d_, host pointers h_.
+ */
+#ifndef MPCX_H
+#define MPCX_H
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef int mpcx_status;
+#define MPCX_OK 0
+#define MPCX_EINVAL 1  /* bad argument (sizes, kinds, null pointers)        */
+#define MPCX_EHIP 2    /* a HIP call failed; see mpcx_last_error            */
+#define MPCX_ENOMEM 3  /* device allocation failed                          */
+#define MPCX_ESTATE 4  /* call out of order (e.g. forward before keygen)    */
+
+typedef struct mpcx_ctx mpcx_ctx;
+typedef struct mpcx_model mpcx_model;
+
+/* Gate kinds of the truncation / ReLU family. */
+#define MPCX_TR 1       /* exact floor(x/2^s) + bias  (TruncateType::TrFloor) */
+#define MPCX_TRRELU 2   /* ReLU(floor(x/2^s) + bias), fused                   */
+#define MPCX_RELU 3     /* ReLU(x)                                            */
+#define MPCX_TRSLACK 4  /* exact floor(x/2^s), requires |x| < 2^(bw-2)        */
+
+/* ---------------- context ----------------
+ * Replaces the evaluator/dealer constructors DDGOrcaBase(party, ip, bw, scale)
+ * and DDGOrcaBaseKeygen(party, bw, scale, keyFile)
+ * (gpu_mpc/ddg_orca_base.h:93-116, 338-355): one context serves both parties. */
+mpcx_status mpcx_create(int bw, int scale, int device, mpcx_ctx **out);
+void mpcx_destroy(mpcx_ctx *ctx);
+const char *mpcx_last_error(const mpcx_ctx *ctx);
+/* hipStream_t; NULL = the context's own stream */
+mpcx_status mpcx_set_stream(mpcx_ctx *ctx, void *hip_stream);
+mpcx_status mpcx_synchronize(mpcx_ctx *ctx);
+/* AES T-table LDS layout used by the DCF kernels (0 = default).  Returns the
+ * number of variants; name of variant i via mpcx_aes_variant_name. */
+int mpcx_aes_variant_count(void);
+const char *mpcx_aes_variant_name(int i);
+mpcx_status mpcx_set_aes_variant(mpcx_ctx *ctx, int variant, int block_threads);
+
+/* Exchange accounting, both directions summed (the reference's "Comm (B)",
+ * gpu_mpc/deepdtagen_inference.cu:556-558, and GpuPeer::bytesSent/Received,
+ * gpu_mpc/utils/gpu_comms.h:290-397). */
+uint64_t mpcx_bytes_exchanged(const mpcx_ctx *ctx);
+uint64_t mpcx_rounds(const mpcx_ctx *ctx);
+void mpcx_reset_counters(mpcx_ctx *ctx);
+
+/* ---------------- PRG ----------------
+ * Tree hash H(s) = AES_KH(sigma(s)) ^ sigma(s) (leaf = 0) or the leaf hash HL
+ * (leaf = 1) on n 128-bit blocks; replaces the AES context of GPU-MPC
+ * (AESGlobalContext / initAESContext, gpu_mpc/ddg_orca_base.h:50,95). */
+mpcx_status mpcx_prg_hash(mpcx_ctx *ctx, int leaf, size_t n, const void *d_in, void *d_out);
+/* Dealer PRF blocks AES_Kd(i, field, gate), i = 0..n-1 (randomGEOnGpu,
+ * randomAESBlockOnGpu in GPU-MPC). */
+mpcx_status mpcx_prf(mpcx_ctx *ctx, uint64_t seed, uint32_t gate, uint32_t field, size_t n, void *d_out);
+
+/* ---------------- DCF ----------------
+ * [x < alpha] over bin-bit inputs, XOR-shared output bits masked by rbit.
+ * Replaces gpuKeyGenDCF<T>(u8**, party, bin, N, T* d_rin, AESGlobalContext*)
+ * (gpu_mpc/dpf_dcf_adapter.h:372), readGPUDcfKey (:100) and
+ * gpuDcf<T,1,idPrologue,maskEpilogue>(key, party, d_in, g, s) (:266).
+ * alpha and x: n uint64_t each; rbit: n bytes or NULL; out: packed bits,
+ * bit i of 64-bit word i/64, (n+63)/64 words. */
+size_t mpcx_dcf_key_bytes(int bin, size_t n);
+mpcx_status mpcx_dcf_keygen(mpcx_ctx *ctx, int bin, size_t n, const uint64_t *d_alpha,
+                            const uint8_t *d_rbit, uint64_t seed, uint32_t gate, void *d_key0,
+                            void *d_key1);
+mpcx_status mpcx_dcf_eval(mpcx_ctx *ctx, int party, int bin, size_t n, const void *d_key,
+                          const uint64_t *d_x, uint64_t *d_out_bits);
+
+/* ---------------- truncation / ReLU ----------------
+ * Keygen replaces gpuGenReluKey<T,T,0,0,false>(kb, party, bin, bout, N,
+ * d_inMask, g) (gpu_mpc/ddg_orca.h:233) and genGPUTruncateKey<T,T>(kb, party,
+ * TrFloor, bin, bout, shift, N, d_inMask, g) (gpu_mpc/ddg_orca.h:240-241):
+ * takes the input mask, writes the output mask and both parties' keys.
+ * Eval replaces gpuRelu<T,T,0,0,false>(peer, party, key, d_in, g, s)
+ * (gpu_mpc/ddg_orca.h:103-104) and gpuTruncate<T,T>(bin, bout, TrFloor, k,
+ * shift, peer, party, N, d_in, g, s) (gpu_mpc/ddg_orca.h:116-118), for both
+ * parties at once: masked input in, masked output out.
+ * bias: ncol ring elements at scale s (element i uses bias[i % ncol]) or NULL;
+ * ignored by MPCX_RELU. */
+size_t mpcx_tr_key_bytes(mpcx_ctx *ctx, int kind, size_t n);
+mpcx_status mpcx_tr_keygen(mpcx_ctx *ctx, int kind, size_t n, const void *d_in_mask,
+                           void *d_out_mask, uint64_t seed, uint32_t gate, void *d_key0,
+                           void *d_key1);
+mpcx_status mpcx_tr_eval(mpcx_ctx *ctx, int kind, size_t n, const void *d_key0,
+                         const void *d_key1, const void *d_xhat, const void *d_bias, int ncol,
+                         void *d_yhat);
+
+/* ---------------- Beaver product ----------------
+ * z[i] = x[ia[i]] * y[ib[i]] on masked operands (index maps allow the
+ * broadcast/outer products of the adjacency normalisation).  Replaces
+ * gpuKeygenMul<T>(kb, party, bw, scale, N, d_maskA, d_maskB, None, g) and
+ * gpuMul<T>(peer, party, bw, scale, N, key, d_A, d_B, None, g, s)
+ * (gpu_mpc/secure_adj_norm.h:326-337, 611-624; gpu_mpc/ddg_orca.h:43-63). */
+size_t mpcx_mul_key_bytes(mpcx_ctx *ctx, size_t nx, size_t ny, size_t nz);
+mpcx_status mpcx_mul_keygen(mpcx_ctx *ctx, size_t nx, size_t ny, size_t nz, const uint32_t *d_ia,
+                            const uint32_t *d_ib, const void *d_rx, const void *d_ry, void *d_rz,
+                            uint64_t seed, uint32_t gate, void *d_key0, void *d_key1);
+mpcx_status mpcx_mul_eval(mpcx_ctx *ctx, size_t nx, size_t ny, size_t nz, const uint32_t *d_ia,
+                          const uint32_t *d_ib, const void *d_key0, const void *d_key1,
+                          const void *d_xhat, const void *d_yhat, void *d_zhat);
+
+/* ---------------- 8-bit DPF lookup table ----------------
+ * y = table[x] for secret x in [0, 256) (the D^-1/2 degree table).  Replaces
+ * gpuKeyGenLUT<T,T>(kb, party, 8, bw, N, d_inMask, g), readGPULUTKey and
+ * gpuDpfLUT<T,T>(key, peer, party, d_x, d_table, g, s, true)
+ * (gpu_mpc/secure_adj_norm.h:270-279, 498-520).  table: 256 ring elements. */
+size_t mpcx_lut8_key_bytes(mpcx_ctx *ctx, size_t n);
+mpcx_status mpcx_lut8_keygen(mpcx_ctx *ctx, size_t n, const void *d_in_mask, void *d_out_mask,
+                             uint64_t seed, uint32_t gate, void *d_key0, void *d_key1);
+mpcx_status mpcx_lut8_eval(mpcx_ctx *ctx, size_t n, const void *d_key0, const void *d_key1,
+                           const void *d_table, const void *d_xhat, void *d_yhat);
+
+/* ---------------- ring GEMMs ----------------
+ * Batched secret x secret product C_b = A_b (M x K) . B_b (K x N) on masked
+ * operands (Beaver).  Replaces the 3-argument DDGOrcaBase::matmul and its
+ * keygen mirror (gpu_mpc/ddg_orca_base.h:170-205, 394-410), i.e.
+ * gpuKeygenMatmul / gpuMatmul with wIsOnGpu = true and the per-sample loop of
+ * _MatMul (gpu_mpc/sytorch/layers/layers.h:67-93). */
+size_t mpcx_sxs_key_bytes(mpcx_ctx *ctx, int nb, int M, int K, int N);
+mpcx_status mpcx_sxs_keygen(mpcx_ctx *ctx, int nb, int M, int K, int N, const void *d_ra,
+                            const void *d_rb, void *d_rc, uint64_t seed, uint32_t gate,
+                            void *d_key0, void *d_key1);
+mpcx_status mpcx_sxs_eval(mpcx_ctx *ctx, int nb, int M, int K, int N, const void *d_key0,
+                          const void *d_key1, const void *d_ahat, const void *d_bhat,
+                          void *d_chat);
+/* Public ring GEMM C = A . B mod 2^bw (masked activations x public weights;
+ * the 4-argument DDGOrcaBase::matmul, gpu_mpc/ddg_orca_base.h:208-271, needs no
+ * key and no exchange when the output mask is r_A . W). */
+mpcx_status mpcx_ring_gemm(mpcx_ctx *ctx, int M, int K, int N, const void *d_a, const void *d_b,
+                           void *d_c);
+
+/* ---------------- reveal ----------------
+ * Additive shares v0, v1 -> masked public v + r (revealIfLeaf,
+ * gpu_mpc/ddg_orca_base.h:72-80; peer->reconstructInPlace,
+ * gpu_mpc/utils/gpu_comms.h:290-302). */
+size_t mpcx_reveal_key_bytes(mpcx_ctx *ctx, size_t n);
+mpcx_status mpcx_reveal_keygen(mpcx_ctx *ctx, size_t n, void *d_mask, uint64_t seed, uint32_t gate,
+                               void *d_key0, void *d_key1);
+mpcx_status mpcx_reveal_eval(mpcx_ctx *ctx, size_t n, const void *d_key0, const void *d_key1,
+                             const void *d_v0, const void *d_v1, void *d_vhat);
+
+/* ---------------- the model ----------------
+ * DeepDTAGenAffinity<T> (gpu_mpc/deepdtagen.h:110-223) with the driver's
+ * resident-key evaluation loop (gpu_mpc/deepdtagen_inference.cu:422-607).
+ * Weights: the weights.bin layout (deepdtagen_inference.cu:121-181): for each
+ * linear layer W^T (in x out, row-major) then bias (out), int64 at scale s. */
+typedef struct {
+  int n_nodes;  /* padded atoms per molecule (<= 255) */
+  int feat;     /* atom feature width */
+  int gcn[3];   /* GCN output widths */
+  int dfc[2];   /* drug FC widths */
+  int prot;     /* protein embedding width */
+  int nfus;     /* fusion layers (last has width 1) */
+  int fus[4];
+  int lut_nmax; /* largest degree with a D^-1/2 table entry */
+} mpcx_model_dims;
+
+mpcx_status mpcx_model_create(mpcx_ctx *ctx, const mpcx_model_dims *dims, const int64_t *h_weights,
+                              size_t n_weights, mpcx_model **out);
+void mpcx_model_destroy(mpcx_model *m);
+/* Key bytes per party for a batch of B molecules. */
+size_t mpcx_model_key_bytes(const mpcx_model *m, int B);
+/* Dealer on the GPU: generates both parties' keys into the resident key arena
+ * (initGPUKeyArena, patches/EzPC-GPU-MPC.track3.patch:632-661). */
+mpcx_status mpcx_model_keygen(mpcx_model *m, int B, uint64_t seed);
+/* Upload / download whole key arenas (host buffers of mpcx_model_key_bytes). */
+mpcx_status mpcx_model_import_keys(mpcx_model *m, int B, const void *h_key0, const void *h_key1,
+                                   size_t bytes);
+mpcx_status mpcx_model_export_keys(mpcx_model *m, int party, void *h_dst, size_t bytes);
+/* Both parties' input shares (host, ring elements): x (B,N,feat), adjacency
+ * (B,N,N) at scale 0 with self loops, atom mask (B,N); protein embedding
+ * (B,prot) int64 at scale s, public. */
+mpcx_status mpcx_model_set_inputs(mpcx_model *m, int B, const void *h_x0, const void *h_x1,
+                                  const void *h_a0, const void *h_a1, const void *h_m0,
+                                  const void *h_m1, const int64_t *h_prot);
+/* One online forward of both parties (enqueued on the context stream). */
+mpcx_status mpcx_model_forward(mpcx_model *m, int B);
+/* Reconstructed outputs (B int64 at scale s); synchronizes the stream. */
+mpcx_status mpcx_model_output(mpcx_model *m, int B, int64_t *h_out);
+/* DCF (phase-1) kernel timing with HIP events on the launch stream. */
+mpcx_status mpcx_model_profile(mpcx_model *m, int enable);
+/* After a synchronized forward: number of phase-1 launches, their summed time
+ * (ms), elements (both parties) and AES calls (both parties). */
+mpcx_status mpcx_model_profile_read(mpcx_model *m, int *launches, double *ms, double *elements,
+                                    double *aes_calls);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

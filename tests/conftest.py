@@ -1,0 +1,31 @@
+"""Shared test setup: module paths and the `gpu` marker.
+
+`-m "not gpu"` runs the oracle tests and host-side checks (no GPU needed);
+`-m gpu` runs the parity tests of the HIP path against the oracle.
+"""
+import os
+import sys
+
+import pytest
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+for p in (os.path.join(ROOT, "oracle"), os.path.join(ROOT, "idash26-track3_amd"), ROOT):
+    if p not in sys.path:
+        sys.path.insert(0, p)
+
+
+def pytest_configure(config):
+    config.addinivalue_line("markers", "gpu: needs an MI355X (runs the HIP path through libmpcx)")
+
+
+@pytest.fixture(scope="session")
+def orc():
+    import orc as _orc
+    _orc.lib()
+    return _orc
+
+
+@pytest.fixture(scope="session")
+def synth():
+    import synth as _synth
+    return _synth

@@ -1,0 +1,294 @@
+"""Parity of the HIP path (libmpcx through its C ABI) with the CPU oracle.
+
+For every primitive and gate: the GPU dealer must write byte-identical keys to
+the oracle's dealer, the GPU evaluation must reconstruct the same masked
+outputs as the oracle's evaluation, and the unmasked outputs must equal the
+plaintext function.  Integer work: bit-exact, no tolerance.
+"""
+import numpy as np
+import pytest
+
+pytestmark = pytest.mark.gpu
+
+S = 12
+
+
+@pytest.fixture(scope="module")
+def mp():
+    import mpcx
+    return mpcx
+
+
+@pytest.fixture(scope="module", params=[32, 64])
+def ctx(request, mp):
+    c = mp.Ctx(bw=request.param, scale=S)
+    yield c
+    c.close()
+
+
+def M(bw):
+    return np.uint64((1 << bw) - 1 if bw < 64 else 0xFFFFFFFFFFFFFFFF)
+
+
+def signed(v, bw):
+    v = np.asarray(v, np.uint64) & M(bw)
+    if bw == 64:
+        return v.view(np.int64)
+    v = v.astype(np.int64)
+    return np.where(v >= 1 << (bw - 1), v - (1 << bw), v)
+
+
+def rmask(rng, n, bw):
+    return rng.integers(0, np.iinfo(np.uint64).max, size=n, dtype=np.uint64, endpoint=True) & M(bw)
+
+
+def host(t):
+    import mpcx
+    return mpcx.from_dev(t, np.uint8)
+
+
+# ---------------------------------------------------------------------------
+def test_prg_hash_matches_oracle(mp, orc):
+    c = mp.Ctx(bw=32)
+    rng = np.random.default_rng(0)
+    blocks = rng.integers(0, 2**32, size=(4099, 4), dtype=np.uint64).astype(np.uint32)
+    for leaf in (False, True):
+        assert np.array_equal(c.prg_hash(blocks, leaf), orc.hash_blocks(blocks, leaf))
+    assert np.array_equal(c.prf(77, 5, 0x30, 1000), orc.prf_blocks(77, 5, 0x30, 1000))
+    c.close()
+
+
+@pytest.mark.parametrize("m", [5, 8, 12, 31, 63])
+def test_dcf_keys_and_eval(mp, orc, m):
+    c = mp.Ctx(bw=64 if m > 31 else 32)
+    rng = np.random.default_rng(m)
+    n = 3001
+    top = (1 << m) - 1
+    alpha = rng.integers(0, top, size=n, dtype=np.uint64, endpoint=True)
+    alpha[:4] = [0, top, 1, top - 1]
+    rb = rng.integers(0, 2, size=n).astype(np.uint8)
+    g0, g1 = c.dcf_keygen(m, alpha, rb, seed=31, gate=9)
+    o0, o1 = orc.dcf_keygen(31, 9, m, alpha, rbit=rb)
+    assert np.array_equal(host(g0)[:o0.size], o0) and np.array_equal(host(g1)[:o1.size], o1)
+    x = rng.integers(0, top, size=n, dtype=np.uint64, endpoint=True)
+    x[:8] = [0, top, alpha[2], alpha[3], alpha[4], alpha[4] - 1 if alpha[4] else 0, top, 0]
+    b = c.dcf_eval(0, m, g0, x) ^ c.dcf_eval(1, m, g1, x)
+    assert np.array_equal(b, (x < alpha).astype(np.uint8) ^ rb)
+    assert np.array_equal(c.dcf_eval(0, m, g0, x), orc.dcf_eval(0, m, o0, x))
+    c.close()
+
+
+def test_dcf_exhaustive_small_domain(mp):
+    c = mp.Ctx(bw=32)
+    m, N = 10, 1024
+    x = np.arange(N, dtype=np.uint64)
+    for alpha in (0, 1, 511, 512, 1023, 777):
+        g0, g1 = c.dcf_keygen(m, np.full(N, alpha, np.uint64), None, seed=alpha, gate=1)
+        b = c.dcf_eval(0, m, g0, x) ^ c.dcf_eval(1, m, g1, x)
+        assert np.array_equal(b, (x < alpha).astype(np.uint8)), alpha
+    c.close()
+
+
+def _tr_inputs(rng, kind, bw, n=4000):
+    h = 1 << (bw - 1)
+    q = 1 << (bw - 2)
+    edge = [-h, -h + 1, -1, 0, 1, h - 1, (1 << S) - 1, 1 << S, -(1 << S), -(1 << S) - 1]
+    if kind == 4:
+        x = np.concatenate([np.array([-q, -1, 0, 1, q - 1], np.int64), rng.integers(-q, q, size=n, dtype=np.int64)])
+        return x, None
+    x = np.concatenate([np.array(edge, np.int64), rng.integers(-(h // 4), h // 4, size=n // 2, dtype=np.int64),
+                        rng.integers(-8 << S, 8 << S, size=n // 2)])
+    bias = None
+    if kind in (1, 2):
+        bias = rng.integers(-(1 << 14), 1 << 14, size=37)
+        lim = h - (1 << (14 + S)) - 1
+        x = np.clip(x, -lim, lim)
+    return x, bias
+
+
+def _tr_expected(kind, x, bias):
+    if kind in (1, 2):
+        bb = np.resize(bias, x.size)
+        t = (x + (bb << S)) >> S
+        return t if kind == 1 else np.maximum(t, 0)
+    if kind == 3:
+        return np.maximum(x, 0)
+    return x >> S
+
+
+@pytest.mark.parametrize("kind", [1, 2, 3, 4])
+def test_tr_family_keys_and_eval(ctx, orc, kind):
+    bw = ctx.bw
+    rng = np.random.default_rng(kind * 100 + bw)
+    x, bias = _tr_inputs(rng, kind, bw)
+    rin = rmask(rng, x.size, bw)
+    g0, g1, grout = ctx.tr_keygen(kind, rin, seed=5, gate=17)
+    o0, o1, orout = orc.tr_keygen(5, 17, kind, bw, S, rin)
+    assert np.array_equal(grout.astype(np.uint64), orout)
+    assert np.array_equal(host(g0)[:o0.size], o0) and np.array_equal(host(g1)[:o1.size], o1)
+    xhat = (x.astype(np.uint64) + rin) & M(bw)
+    ctx.reset_counters()
+    y = ctx.tr_eval(kind, g0, g1, xhat, bias)
+    by = ctx.bytes_exchanged
+    be = None if bias is None else np.resize(bias, x.size)
+    oy, oby = orc.tr_eval(kind, bw, S, o0, o1, xhat, be)
+    assert np.array_equal(y.astype(np.uint64), oy)
+    assert by == oby
+    assert np.array_equal(signed(y.astype(np.uint64) - orout, bw), _tr_expected(kind, x, bias))
+
+
+def test_all_aes_variants_agree(mp, orc):
+    c = mp.Ctx(bw=32)
+    rng = np.random.default_rng(4)
+    x, bias = _tr_inputs(rng, 2, 32, n=3000)
+    rin = rmask(rng, x.size, 32)
+    o0, o1, orout = orc.tr_keygen(8, 2, 2, 32, S, rin)
+    k0, k1 = mp.to_dev(o0), mp.to_dev(o1)
+    xhat = (x.astype(np.uint64) + rin) & M(32)
+    want = _tr_expected(2, x, bias)
+    nvar = c.lib.mpcx_aes_variant_count()
+    for v in range(nvar):
+        c.set_aes_variant(v)
+        y = c.tr_eval(2, k0, k1, xhat, bias)
+        assert np.array_equal(signed(y.astype(np.uint64) - orout, 32), want), v
+    c.close()
+
+
+def test_mul_keys_and_eval(ctx, orc):
+    bw = ctx.bw
+    rng = np.random.default_rng(bw)
+    nx, ny, nz = 300, 200, 5000
+    lim = 1 << (14 if bw == 32 else 30)
+    xv = rng.integers(-lim, lim, size=nx)
+    yv = rng.integers(-lim, lim, size=ny)
+    ia = rng.integers(0, nx, size=nz).astype(np.uint32)
+    ib = rng.integers(0, ny, size=nz).astype(np.uint32)
+    rx, ry = rmask(rng, nx, bw), rmask(rng, ny, bw)
+    g0, g1, grz = ctx.mul_keygen(rx, ry, ia, ib, seed=2, gate=4)
+    o0, o1, orz = orc.mul_keygen(2, 4, bw, rx, ry, ia, ib)
+    assert np.array_equal(host(g0)[:o0.size], o0) and np.array_equal(host(g1)[:o1.size], o1)
+    xh = (xv.astype(np.uint64) + rx) & M(bw)
+    yh = (yv.astype(np.uint64) + ry) & M(bw)
+    z = ctx.mul_eval(g0, g1, xh, yh, ia, ib)
+    assert np.array_equal(signed(z.astype(np.uint64) - orz, bw), xv[ia] * yv[ib])
+
+
+def test_lut8_keys_and_eval(ctx, orc):
+    bw = ctx.bw
+    rng = np.random.default_rng(9)
+    table = orc.invsqrt_table(S, 138)
+    x = np.tile(np.arange(256, dtype=np.uint64), 4)
+    rin = rmask(rng, x.size, bw)
+    g0, g1, grout = ctx.lut8_keygen(rin, seed=4, gate=6)
+    o0, o1, orout = orc.lut8_keygen(4, 6, bw, rin)
+    assert np.array_equal(host(g0)[:o0.size], o0) and np.array_equal(host(g1)[:o1.size], o1)
+    y = ctx.lut8_eval(g0, g1, table, (x + rin) & M(bw))
+    assert np.array_equal((y.astype(np.uint64) - orout) & M(bw), table[x.astype(np.int64)])
+
+
+def test_sxs_keys_and_eval(ctx, orc):
+    bw = ctx.bw
+    rng = np.random.default_rng(12)
+    nb, Mm, K, N = 3, 70, 66, 37
+    A = rng.integers(-(1 << 10), 1 << 10, size=(nb, Mm, K))
+    B = rng.integers(-(1 << 10), 1 << 10, size=(nb, K, N))
+    ra, rb = rmask(rng, A.size, bw), rmask(rng, B.size, bw)
+    g0, g1, grc = ctx.sxs_keygen(nb, Mm, K, N, ra, rb, seed=3, gate=2)
+    o0, o1, orc_ = orc.sxs_keygen(3, 2, bw, nb, Mm, K, N, ra, rb)
+    assert np.array_equal(host(g0)[:o0.size], o0) and np.array_equal(host(g1)[:o1.size], o1)
+    ah = (A.ravel().astype(np.uint64) + ra) & M(bw)
+    bh = (B.ravel().astype(np.uint64) + rb) & M(bw)
+    c = ctx.sxs_eval(nb, Mm, K, N, g0, g1, ah, bh)
+    assert np.array_equal(signed(c.astype(np.uint64) - orc_, bw).reshape(nb, Mm, N), np.einsum("bmk,bkn->bmn", A, B))
+
+
+def test_ring_gemm(ctx, orc):
+    bw = ctx.bw
+    rng = np.random.default_rng(1)
+    A = rmask(rng, 130 * 77, bw).reshape(130, 77)
+    B = rmask(rng, 77 * 65, bw).reshape(77, 65)
+    assert np.array_equal(ctx.ring_gemm(A, B).astype(np.uint64), orc.ring_gemm(bw, A, B))
+
+
+def test_reveal_keys_and_eval(ctx, orc):
+    bw = ctx.bw
+    rng = np.random.default_rng(2)
+    n = 1001
+    g0, g1, gm = ctx.reveal_keygen(n, seed=1, gate=3)
+    o0, o1, om = orc.reveal_keygen(1, 3, bw, n)
+    assert np.array_equal(host(g0)[:o0.size], o0) and np.array_equal(gm.astype(np.uint64), om)
+    v = rng.integers(-1000, 1000, size=n)
+    v0 = rmask(rng, n, bw)
+    v1 = (v.astype(np.uint64) - v0) & M(bw)
+    vh = ctx.reveal_eval(g0, g1, v0, v1)
+    assert np.array_equal(signed(vh.astype(np.uint64) - om, bw), v)
+
+
+# ---------------------------------------------------------------------------
+def _od(orc, dims):
+    return orc.make_dims(bw=dims.bw, s=dims.s, n_nodes=dims.n_nodes, feat=dims.feat, gcn=dims.gcn, dfc=dims.dfc,
+                         prot=dims.prot, fus=dims.fus, lut_nmax=dims.lut_nmax)
+
+
+@pytest.mark.parametrize("bw", [32, 64])
+def test_model_keys_and_forward(mp, orc, synth, bw):
+    B = 2
+    wl = synth.workload(B, synth.Dims(bw=bw), seed=21)
+    d = _od(orc, wl.dims)
+    want, code = orc.plain_forward(d, wl.X, wl.A, wl.mask, wl.prot, wl.W)
+    assert code == 0
+    c = mp.Ctx(bw=bw)
+    m = mp.Model(c, wl.dims, wl.W)
+    assert m.key_bytes(B) == orc.model_key_bytes(d, B)
+    m.keygen(B, 777)
+    o0, o1 = orc.model_keygen(d, B, 777, wl.W)
+    assert np.array_equal(m.export_keys(0, B), o0)
+    assert np.array_equal(m.export_keys(1, B), o1)
+    x0, x1 = wl.shares["x"]
+    a0, a1 = wl.shares["a"]
+    m0, m1 = wl.shares["m"]
+    m.set_inputs(B, x0, x1, a0, a1, m0, m1, wl.prot)
+    c.reset_counters()
+    m.forward(B)
+    got = m.output(B)
+    assert np.array_equal(got, want)
+    _, oby = orc.model_eval(d, B, wl.W, o0, o1, x0, x1, a0, a1, m0, m1, wl.prot)
+    assert c.bytes_exchanged == oby
+    m.close()
+    c.close()
+
+
+def test_model_forward_on_oracle_keys_config0(mp, orc, synth):
+    """Config 0 shape (B=16, N=140, bw=32): keys from the oracle's dealer,
+    online phase on the GPU, outputs equal to the plaintext forward."""
+    B = 16
+    wl = synth.workload(B, synth.Dims(bw=32), seed=0)
+    d = _od(orc, wl.dims)
+    want, code = orc.plain_forward(d, wl.X, wl.A, wl.mask, wl.prot, wl.W)
+    assert code == 0
+    o0, o1 = orc.model_keygen(d, B, 4242, wl.W)
+    c = mp.Ctx(bw=32)
+    m = mp.Model(c, wl.dims, wl.W)
+    m.import_keys(B, o0, o1)
+    m.set_inputs(B, *wl.shares["x"], *wl.shares["a"], *wl.shares["m"], wl.prot)
+    m.forward(B)
+    assert np.array_equal(m.output(B), want)
+    # repeated forwards on the same resident keys are deterministic
+    m.forward(B)
+    assert np.array_equal(m.output(B), want)
+    m.close()
+    c.close()
+
+
+def test_relu_microbench_slice(mp):
+    """Config 1 shape at 2^20 elements: ReLU of uniform fixed-point values in
+    [-8, 8), reconstructed against max(x, 0)."""
+    c = mp.Ctx(bw=32)
+    rng = np.random.default_rng(1)
+    n = 1 << 20
+    x = rng.integers(-8 << S, 8 << S, size=n)
+    rin = rmask(rng, n, 32)
+    k0, k1, rout = c.tr_keygen(3, rin, seed=11, gate=1)
+    y = c.tr_eval(3, k0, k1, (x.astype(np.uint64) + rin) & M(32))
+    assert np.array_equal(signed(y.astype(np.uint64) - rout.astype(np.uint64), 32), np.maximum(x, 0))
+    c.close()

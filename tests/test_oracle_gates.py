@@ -1,0 +1,153 @@
+"""Pins the oracle's two-party gates against closed forms (CPU only).
+
+Each gate is keyed on a random input mask, evaluated by both parties on the
+masked input, reconstructed, unmasked, and compared with the plaintext
+function: signed floor(x/2^s) + bias (TrFloor, gpu_mpc/ddg_orca.h:112-123),
+max(x, 0) (ddg_orca.h:83-110), x*y (Beaver, secure_adj_norm.h:611-651),
+table[x] (DPF LUT, secure_adj_norm.h:495-520), A.B mod 2^bw
+(ddg_orca_base.h:170-205).  Boundary values of the signed ring are included.
+"""
+import numpy as np
+import pytest
+
+S = 12
+
+
+def mod(bw):
+    return (1 << bw) - 1
+
+
+def to_signed(v, bw):
+    v = np.asarray(v, np.uint64)
+    if bw == 64:
+        return v.view(np.int64)
+    v = (v & np.uint64(mod(bw))).astype(np.int64)
+    return np.where(v >= 1 << (bw - 1), v - (1 << bw), v)
+
+
+def ring(v, bw):
+    return np.asarray(v, np.int64).astype(np.uint64) & np.uint64(mod(bw) if bw < 64 else 0xFFFFFFFFFFFFFFFF)
+
+
+def mask_in(rng, n, bw):
+    return rng.integers(0, 2**63, size=n, dtype=np.uint64) * np.uint64(2) + rng.integers(0, 2, size=n,
+                                                                                       dtype=np.uint64) \
+        if bw == 64 else rng.integers(0, 1 << bw, size=n, dtype=np.uint64)
+
+
+def edge_values(bw, s):
+    h = 1 << (bw - 1)
+    return [-h, -h + 1, -1, 0, 1, h - 1, (1 << s) - 1, 1 << s, -(1 << s), -(1 << s) - 1, -(1 << s) + 1]
+
+
+@pytest.mark.parametrize("bw", [32, 64])
+@pytest.mark.parametrize("kind", [1, 2, 3])
+def test_tr_relu_family(orc, bw, kind):
+    rng = np.random.default_rng(bw * 10 + kind)
+    n = 3000
+    h = 1 << (bw - 1)
+    x = np.concatenate([np.array(edge_values(bw, S), np.int64),
+                        rng.integers(-(h // 4), h // 4, size=n, dtype=np.int64)])
+    x = np.concatenate([x, rng.integers(-5 << S, 5 << S, size=n)])
+    N = x.size
+    bias = rng.integers(-(1 << 14), 1 << 14, size=N) if kind in (1, 2) else None
+    if bias is not None:
+        # keep x + bias*2^s inside the signed ring (the bit-exact domain)
+        lim = h - (1 << (14 + S)) - 1
+        x = np.clip(x, -lim, lim)
+    rin = mask_in(rng, N, bw)
+    k0, k1, rout = orc.tr_keygen(5, 17, kind, bw, S, rin)
+    xhat = (ring(x, bw) + rin) & np.uint64(mod(bw) if bw < 64 else 0xFFFFFFFFFFFFFFFF)
+    y, by = orc.tr_eval(kind, bw, S, k0, k1, xhat, bias)
+    got = to_signed(y - rout, bw)
+    if kind == 1:
+        exp = (x + (bias << S)) >> S
+    elif kind == 2:
+        exp = np.maximum((x + (bias << S)) >> S, 0)
+    else:
+        exp = np.maximum(x, 0)
+    assert np.array_equal(got, exp)
+    nbits = 2 if kind in (1, 2) else 1
+    assert by == 2 * (nbits * ((N + 31) // 32) * 4 + N * bw // 8)
+
+
+@pytest.mark.parametrize("bw", [32, 64])
+def test_tr_slack(orc, bw):
+    rng = np.random.default_rng(bw)
+    q = 1 << (bw - 2)
+    x = np.concatenate([np.array([-q, -q + 1, -1, 0, 1, q - 1, (1 << S) - 1, -(1 << S)], np.int64),
+                        rng.integers(-q, q, size=4000, dtype=np.int64)])
+    rin = mask_in(rng, x.size, bw)
+    k0, k1, rout = orc.tr_keygen(9, 3, 4, bw, S, rin)
+    xhat = (ring(x, bw) + rin) & np.uint64(mod(bw) if bw < 64 else 0xFFFFFFFFFFFFFFFF)
+    y, _ = orc.tr_eval(4, bw, S, k0, k1, xhat)
+    assert np.array_equal(to_signed(y - rout, bw), x >> S)
+
+
+@pytest.mark.parametrize("bw", [32, 64])
+def test_mul_index_maps(orc, bw):
+    rng = np.random.default_rng(3)
+    nx, ny, nz = 50, 40, 500
+    lim = 1 << (14 if bw == 32 else 30)  # products stay inside the signed ring
+    xv = rng.integers(-lim, lim, size=nx)
+    yv = rng.integers(-lim, lim, size=ny)
+    ia = rng.integers(0, nx, size=nz).astype(np.uint32)
+    ib = rng.integers(0, ny, size=nz).astype(np.uint32)
+    rx, ry = mask_in(rng, nx, bw), mask_in(rng, ny, bw)
+    k0, k1, rz = orc.mul_keygen(2, 4, bw, rx, ry, ia, ib)
+    M = np.uint64(mod(bw) if bw < 64 else 0xFFFFFFFFFFFFFFFF)
+    z, _ = orc.mul_eval(bw, k0, k1, (ring(xv, bw) + rx) & M, (ring(yv, bw) + ry) & M, ia, ib)
+    assert np.array_equal(to_signed(z - rz, bw), xv[ia] * yv[ib])
+
+
+@pytest.mark.parametrize("bw", [32, 64])
+def test_lut8_all_inputs(orc, bw):
+    rng = np.random.default_rng(8)
+    table = orc.invsqrt_table(S, 138)
+    x = np.tile(np.arange(256, dtype=np.uint64), 3)
+    rin = mask_in(rng, x.size, bw)
+    k0, k1, rout = orc.lut8_keygen(4, 6, bw, rin)
+    M = np.uint64(mod(bw) if bw < 64 else 0xFFFFFFFFFFFFFFFF)
+    y, _ = orc.lut8_eval(bw, k0, k1, table, (x + rin) & M)
+    assert np.array_equal((y - rout) & M, table[x.astype(np.int64)])
+
+
+def test_invsqrt_table_values(orc):
+    # T[k] = llround(2^12/sqrt(k)), T[0] = 0 (secure_adj_norm.h:138-184)
+    t = orc.invsqrt_table(12, 138)
+    assert list(t[:7]) == [0, 4096, 2896, 2365, 2048, 1832, 1672]
+    assert t[138] == round(4096 / 138 ** 0.5) and t[139] == 0 and t[255] == 0
+
+
+@pytest.mark.parametrize("bw", [32, 64])
+def test_sxs_matches_matmul(orc, bw):
+    rng = np.random.default_rng(11)
+    nb, M_, K, N = 3, 7, 9, 5
+    A = rng.integers(-(1 << 12), 1 << 12, size=(nb, M_, K))
+    B = rng.integers(-(1 << 12), 1 << 12, size=(nb, K, N))
+    ra, rb = mask_in(rng, A.size, bw), mask_in(rng, B.size, bw)
+    k0, k1, rc = orc.sxs_keygen(3, 2, bw, nb, M_, K, N, ra, rb)
+    MM = np.uint64(mod(bw) if bw < 64 else 0xFFFFFFFFFFFFFFFF)
+    c, _ = orc.sxs_eval(bw, nb, M_, K, N, k0, k1, (ring(A, bw).ravel() + ra) & MM, (ring(B, bw).ravel() + rb) & MM)
+    assert np.array_equal(to_signed(c - rc, bw).reshape(nb, M_, N), np.einsum("bmk,bkn->bmn", A, B))
+
+
+def test_reveal(orc):
+    rng = np.random.default_rng(2)
+    bw = 32
+    v = rng.integers(-1000, 1000, size=100)
+    v0 = rng.integers(0, 1 << 32, size=100, dtype=np.uint64)
+    v1 = (ring(v, bw) - v0) & np.uint64(mod(bw))
+    k0, k1, m = orc.reveal_keygen(1, 1, bw, 100)
+    vh, by = orc.reveal_eval(bw, k0, k1, v0, v1)
+    assert np.array_equal(to_signed(vh - m, bw), v)
+    assert by == 2 * 100 * 4
+
+
+def test_gate_keys_deterministic_and_seed_dependent(orc):
+    rin = np.arange(100, dtype=np.uint64) * np.uint64(2654435761)
+    a0, a1, ra = orc.tr_keygen(1, 2, 2, 32, S, rin)
+    b0, b1, rb = orc.tr_keygen(1, 2, 2, 32, S, rin)
+    c0, _, rc = orc.tr_keygen(2, 2, 2, 32, S, rin)
+    assert np.array_equal(a0, b0) and np.array_equal(a1, b1) and np.array_equal(ra, rb)
+    assert not np.array_equal(a0, c0) and not np.array_equal(ra, rc)

@@ -1,0 +1,192 @@
+"""Pins the oracle's plaintext fixed-point forward and its two-party protocol
+(CPU only).
+
+- A_hat closed form: A[i,j]*floor(T[d_i]T[d_j]/2^12) with the hand-checkable
+  degree pairs of gpu_mpc/secure_adj_norm.h:138-184,326-365.
+- a 2-node model whose every intermediate is computed by hand below (floor
+  rounding of a negative product included), following the op order of
+  reference/fixed_forward.py:140-172;
+- node-permutation invariance and padding invariance (exact);
+- agreement with an independent float64 forward of the same network;
+- bw=32 and bw=64 agree when nothing wraps (microbench/test_ring32.py:167-176);
+- the two-party protocol reconstructs exactly the plaintext outputs.
+"""
+import numpy as np
+import pytest
+
+
+def test_adj_norm_degree_pairs(orc):
+    # graph with nodes of degree (incl. self loop) 1..5 connected as needed
+    cases = {(1, 1): 4096, (2, 2): 2047, (2, 3): 1672, (3, 3): 1365, (3, 5): 1057, (4, 4): 1024,
+             (5, 5): 819}
+    t = orc.invsqrt_table(12, 138)
+    for (da, db), want in cases.items():
+        assert (int(t[da]) * int(t[db])) >> 12 == want
+    # a path 0-1-2 with self loops: degrees 2,3,2
+    A = np.zeros((1, 4, 4), np.int64)
+    for i, j in ((0, 1), (1, 2)):
+        A[0, i, j] = A[0, j, i] = 1
+    for v in range(3):
+        A[0, v, v] = 1
+    Ah = orc.adj_norm_plain(A)[0]
+    assert Ah[0, 0] == 2047 and Ah[0, 1] == 1672 and Ah[1, 1] == 1365 and Ah[2, 1] == 1672
+    assert Ah[3].sum() == 0 and Ah[:, 3].sum() == 0 and Ah[0, 2] == 0
+
+
+def _tiny(orc):
+    d = orc.make_dims(bw=32, s=12, n_nodes=2, feat=1, gcn=(1, 1, 1), dfc=(1, 1), prot=1, fus=(1, 1))
+    W = np.array([
+        8192, 2048,      # gcn0: W=2.0, b=0.5
+        8192, 2048,      # gcn1
+        8192, 2048,      # gcn2
+        2048, -4096,     # dfc0: W=0.5, b=-1.0
+        -4096, 1024,     # dfc1: W=-1.0, b=0.25
+        4096, 4096, 0,   # fus0: W^T=[[1],[1]], b=0
+        -8193, 512,      # fus1: W=-2.000244, b=0.125
+    ], np.int64)
+    assert W.size == orc.weights_len(d)
+    X = np.array([[[4096], [0]]], np.int64)
+    A = np.array([[[1, 0], [0, 0]]], np.int64)
+    mask = np.array([[1, 0]], np.int64)
+    prot = np.array([[32768]], np.int64)
+    return d, W, X, A, mask, prot
+
+
+def test_hand_computed_two_node_model(orc):
+    """Real atom: H = 2.5, 5.5, 11.5 after the GCNs (A_fx[0,0] = 4096);
+    padding atom: H = ReLU(b) = 0.5 (masked out of the pool).
+    dfc0: floor(47104*2048/4096) - 4096 = 19456; dfc1: -19456 + 1024 = -18432;
+    fus0: floor((-18432 + 32768)*4096/4096) = 14336;
+    fus1: floor(14336*-8193/4096) = floor(-28675.5) = -28676, + 512 = -28164."""
+    d, W, X, A, mask, prot = _tiny(orc)
+    out, code = orc.plain_forward(d, X, A, mask, prot, W)
+    assert code == 0
+    assert out.tolist() == [-28164]
+
+
+def test_hand_computed_two_party(orc):
+    d, W, X, A, mask, prot = _tiny(orc)
+    k0, k1 = orc.model_keygen(d, 1, 99, W)
+    rng = np.random.default_rng(0)
+    shares = []
+    for v in (X, A, mask):
+        v0 = rng.integers(0, 1 << 32, size=v.size, dtype=np.uint64)
+        shares += [v0, (v.ravel().astype(np.uint64) - v0) & np.uint64(0xFFFFFFFF)]
+    out, _ = orc.model_eval(d, 1, W, k0, k1, *shares, prot)
+    assert out.tolist() == [-28164]
+
+
+def test_domain_violation_is_reported(orc):
+    d, W, X, A, mask, prot = _tiny(orc)
+    W = W.copy()
+    W[0] = 1 << 30  # XW product 4096 * 2^30 overflows the 32-bit ring
+    _, code = orc.plain_forward(d, X, A, mask, prot, W)
+    assert code == 1
+    assert "pre-truncation" in orc.domain_msg(code)
+
+
+def _wl(synth, B, bw=32, seed=0, n_nodes=140):
+    dims = synth.Dims(bw=bw, n_nodes=n_nodes)
+    return synth.workload(B, dims, seed=seed)
+
+
+def _od(orc, wl):
+    d = wl.dims
+    return orc.make_dims(bw=d.bw, s=d.s, n_nodes=d.n_nodes, feat=d.feat, gcn=d.gcn, dfc=d.dfc, prot=d.prot,
+                         fus=d.fus, lut_nmax=d.lut_nmax)
+
+
+def test_permutation_invariance(orc, synth):
+    wl = _wl(synth, 3, seed=4)
+    d = _od(orc, wl)
+    out, code = orc.plain_forward(d, wl.X, wl.A, wl.mask, wl.prot, wl.W)
+    assert code == 0
+    rng = np.random.default_rng(1)
+    X, A, M = wl.X.copy(), wl.A.copy(), wl.mask.copy()
+    for b in range(3):
+        p = rng.permutation(wl.dims.n_nodes)
+        X[b] = wl.X[b][p]
+        A[b] = wl.A[b][p][:, p]
+        M[b] = wl.mask[b][p]
+    out2, code2 = orc.plain_forward(d, X, A, M, wl.prot, wl.W)
+    assert code2 == 0 and np.array_equal(out, out2)
+
+
+def test_padding_invariance(orc, synth):
+    wl = _wl(synth, 2, seed=6)
+    d = _od(orc, wl)
+    out, _ = orc.plain_forward(d, wl.X, wl.A, wl.mask, wl.prot, wl.W)
+    n = 64  # every molecule has <= 60 real atoms
+    d2 = orc.make_dims(bw=32, n_nodes=n)
+    out2, code = orc.plain_forward(d2, wl.X[:, :n], wl.A[:, :n, :n], wl.mask[:, :n], wl.prot, wl.W)
+    assert code == 0 and np.array_equal(out, out2)
+
+
+def _float_forward(wl):
+    """Independent float64 forward of the same network (dequantised weights)."""
+    dims = wl.dims
+    s = float(1 << dims.s)
+    layers = []
+    o = 0
+    for fin, fout in dims.layers():
+        Wt = wl.W[o:o + fin * fout].reshape(fin, fout) / s
+        o += fin * fout
+        b = wl.W[o:o + fout] / s
+        o += fout
+        layers.append((Wt, b))
+    outs = []
+    for bi in range(wl.B):
+        A = wl.A[bi].astype(float)
+        deg = A.sum(1)
+        inv = np.where(deg > 0, 1.0 / np.sqrt(np.maximum(deg, 1)), 0.0)
+        Ah = inv[:, None] * A * inv[None, :]
+        H = wl.X[bi] / s
+        for l in range(3):
+            Wt, b = layers[l]
+            H = np.maximum(Ah @ (H @ Wt) + b, 0)
+        keep = wl.mask[bi] != 0
+        p = H[keep].max(0)
+        Wt, b = layers[3]
+        h = np.maximum(p @ Wt + b, 0)
+        Wt, b = layers[4]
+        h = np.concatenate([h @ Wt + b, wl.prot[bi] / s])
+        for k in range(len(dims.fus)):
+            Wt, b = layers[5 + k]
+            h = h @ Wt + b
+            if k < len(dims.fus) - 1:
+                h = np.maximum(h, 0)
+        outs.append(h[0])
+    return np.array(outs)
+
+
+def test_close_to_float_model(orc, synth):
+    wl = _wl(synth, 6, seed=2)
+    d = _od(orc, wl)
+    out, code = orc.plain_forward(d, wl.X, wl.A, wl.mask, wl.prot, wl.W)
+    assert code == 0
+    ref = _float_forward(wl)
+    fx = out / 4096.0
+    assert np.abs(fx - ref).max() < 0.05, (fx, ref)
+    assert np.ptp(ref) > 0.1  # outputs are not degenerate
+
+
+def test_bw32_equals_bw64_in_domain(orc, synth):
+    wl = _wl(synth, 3, seed=8)
+    o32, c32 = orc.plain_forward(_od(orc, wl), wl.X, wl.A, wl.mask, wl.prot, wl.W)
+    o64, c64 = orc.plain_forward(orc.make_dims(bw=64), wl.X, wl.A, wl.mask, wl.prot, wl.W)
+    assert c32 == 0 and c64 == 0 and np.array_equal(o32, o64)
+
+
+@pytest.mark.parametrize("bw", [32, 64])
+def test_two_party_matches_plaintext(orc, synth, bw):
+    wl = _wl(synth, 2, bw=bw, seed=10)
+    d = _od(orc, wl)
+    out, code = orc.plain_forward(d, wl.X, wl.A, wl.mask, wl.prot, wl.W)
+    assert code == 0
+    k0, k1 = orc.model_keygen(d, 2, 2024, wl.W)
+    x0, x1 = wl.shares["x"]
+    a0, a1 = wl.shares["a"]
+    m0, m1 = wl.shares["m"]
+    o2, by = orc.model_eval(d, 2, wl.W, k0, k1, x0, x1, a0, a1, m0, m1, wl.prot)
+    assert np.array_equal(o2, out)
+    assert by > 0
