@@ -9,7 +9,11 @@
 //   8-bit DPF LUT ............ gpuDpfLUT / gpuKeyGenLUT (gpu_mpc/secure_adj_norm.h:510-520,270-279)
 //   ring GEMM ................ gpuMatmul / gpuKeygenMatmul (gpu_mpc/ddg_orca_base.h:170-271,394-469)
 //   reveal ................... reconstructInPlace       (gpu_mpc/utils/gpu_comms.h:290-302)
-// The algebra of every gate is derived in DESIGN.md ("Gate algebra").
+// Gate algebra (masked-public x^ = x + r): the truncation family evaluates two DCFs on
+// x' = x^ + bias*2^s + 2^(n-1), c = [x' mod 2^(n-1) < r mod 2^(n-1)] and
+// d = [x' mod 2^s < r mod 2^s], then floor(u/2^s) = floor(x'/2^s) - floor(r/2^s) - d
+// + 2^(n-s)*w with the wrap w = msb(x') ? (msb(r) & c) : (msb(r) | c); the dealer
+// tabulates all but the public floor(x'/2^s) over the 8 public cases.
 #include <hip/hip_runtime.h>
 
 #include <type_traits>

@@ -2,7 +2,7 @@
 // (dealer keygen and online forward), both parties on one GPU.
 //
 // Mirrors DeepDTAGenAffinity<T>::_forward (gpu_mpc/deepdtagen.h:183-222) with
-// the op order of reference/fixed_forward.py:140-172:
+// the op order of reference/fixed_forward.py:63-95:
 //   secure adjacency normalisation (secure_adj_norm.h:393-659)
 //   3 x GCN:  Z = H.W^T (public weights, no exchange) -> TR -> A_norm.(XW) (SxS)
 //             -> TRRELU(+bias)

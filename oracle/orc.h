@@ -13,8 +13,8 @@
  *   - A_hat produced by the secure adjacency normalisation, i.e. the LUT
  *     closed form A[i,j]*floor(T[d_i]*T[d_j]/2^s), T[k]=llround(2^s/sqrt(k)),
  *     T[0]=0: gpu_mpc/secure_adj_norm.h:138-184 and :326-365;
- *   - the masked max-pool (sentinel -2^(bw-2)): fixed_forward.py:109-113,
- *     153-157;
+ *   - the masked max-pool (sentinel -2^(bw-2)): fixed_forward.py:33-36,
+ *     76-80;
  *   - AES-128 (FIPS-197), used by the FSS PRG; KAT vector of
  *     gpu_mpc/lss/lss_test.cpp:52-70;
  *   - the two-party online protocol itself (DCF/DPF keys, ReLU, truncation,
@@ -22,7 +22,9 @@
  *     implementation, so that keys, exchanged messages and reconstructed
  *     outputs can be compared byte for byte.
  *
- * Parity status of each function is listed in DESIGN.md at the repo root.
+ * Every function is checked by tests/ against closed forms, brute force or the
+ * known-answer vectors of tests/golden/ (FIPS-197, the reference's fixed-point
+ * test vectors and the D^-1/2 table values).
  *
  * Ring elements are carried in uint64_t and reduced mod 2^bw (bw = 32 or 64).
  */

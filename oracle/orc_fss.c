@@ -20,7 +20,12 @@
  *   LUT8                          -- secure_adj_norm.h:495-520
  *   SXS                           -- ddg_orca_base.h:170-205
  *   REVEAL                        -- ddg_orca_base.h:72-89
- * Derivations of every key coefficient are in DESIGN.md ("Gate algebra").
+ * Key coefficients: with x' = x^ + bias*2^s + 2^(n-1), h = msb(x'), rho = msb(r),
+ * c = [x' mod 2^(n-1) < r mod 2^(n-1)], d = [x' mod 2^s < r mod 2^s], the wrap of x' - r
+ * is w = h ? (rho & c) : (rho | c) and floor(u/2^s) = floor(x'/2^s) - floor(r/2^s) - d
+ * + 2^(n-s) w for u = x + bias*2^s + 2^(n-1); the dealer tabulates everything but the
+ * public floor(x'/2^s) over the 8 public cases (h, c^, d^).  The ReLU variants multiply by
+ * the sign bit h ^ rho ^ c = z ^ kappa (z public, kappa shared).
  */
 #include <stdlib.h>
 #include <string.h>

@@ -3,15 +3,15 @@
  * two-party protocol over the whole model.  TEST INFRASTRUCTURE ONLY.
  *
  * Plaintext semantics follow reference/fixed_forward.py:
- *   _wrap            :121-129  (signed reduction mod 2^bw)
- *   _linear          :132-138  (wrap(tr(x W^T)) then wrap(+b))
- *   _gcn_layer       :140-144  (transform first: wrap(tr(A_fx . wrap(tr(H W^T)))) + b)
- *   _drug_path_fx    :147-162  (3x GCN + ReLU, sentinel max-pool, drug FCs)
- *   _fusion_fx       :165-172  (concat [drug, protein], ReLU on all but last)
+ *   _wrap            :44-52  (signed reduction mod 2^bw)
+ *   _linear          :55-61  (wrap(tr(x W^T)) then wrap(+b))
+ *   _gcn_layer       :63-67  (transform first: wrap(tr(A_fx . wrap(tr(H W^T)))) + b)
+ *   _drug_path_fx    :70-85  (3x GCN + ReLU, sentinel max-pool, drug FCs)
+ *   _fusion_fx       :88-95  (concat [drug, protein], ReLU on all but last)
  * with fixed_matmul = exact product, floor(./2^s) (reference/fixedpoint.py:61-77),
  * and A_fx taken from the secure normalisation's closed form
  * A[i,j]*floor(T[d_i]*T[d_j]/2^s) (gpu_mpc/secure_adj_norm.h:138-184,326-365)
- * instead of to_fixed(A_hat) (fixed_forward.py:149), because the secure path
+ * instead of to_fixed(A_hat) (fixed_forward.py:72), because the secure path
  * computes exactly that.
  *
  * Weights are the weights.bin layout of gpu_mpc/deepdtagen_inference.cu:121-181:
@@ -228,7 +228,7 @@ int orc_plain_forward(const orc_dims *d, int B, const int64_t *X, const int64_t 
       fixed_mm(&f, h1, Wt, 1, (size_t)d->dfc[0], (size_t)d->dfc[1], bias, h2);
       for (int j = 0; j < d->dfc[1]; j++) h2[j] = wrapv(&f, (i128)h2[j] + bias[j]);
     }
-    /* fusion: concat [drug, protein] (fixed_forward.py:166) */
+    /* fusion: concat [drug, protein] (fixed_forward.py:89) */
     int width = d->dfc[1] + d->prot;
     for (int j = 0; j < d->prot; j++) h2[d->dfc[1] + j] = prot[(size_t)b * d->prot + j];
     for (int k = 0; k < d->nfus; k++) {

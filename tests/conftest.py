@@ -9,7 +9,8 @@ import sys
 import pytest
 
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
-for p in (os.path.join(ROOT, "oracle"), os.path.join(ROOT, "idash26-track3_amd"), ROOT):
+for p in (os.path.join(ROOT, "oracle"), os.path.join(ROOT, "idash26-track3_amd"), ROOT,
+          os.path.join(ROOT, "tests", "golden")):
     if p not in sys.path:
         sys.path.insert(0, p)
 

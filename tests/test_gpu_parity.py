@@ -292,3 +292,42 @@ def test_relu_microbench_slice(mp):
     y = c.tr_eval(3, k0, k1, (x.astype(np.uint64) + rin) & M(32))
     assert np.array_equal(signed(y.astype(np.uint64) - rout.astype(np.uint64), 32), np.maximum(x, 0))
     c.close()
+
+
+# ---------------------------------------------------------------------------
+# committed fixtures (tests/golden/)
+# ---------------------------------------------------------------------------
+@pytest.mark.parametrize("bw", [32, 64])
+def test_model_small_fixture(mp, synth, bw):
+    import os
+    from golden_dims import SMALL
+    f = np.load(os.path.join(os.path.dirname(__file__), "golden", "model_small.npz"))
+    dims = synth.Dims(bw=bw, **SMALL)
+    B = f["X"].shape[0]
+    sh = {k: synth.share(f[v], bw, 40 + i) for i, (k, v) in enumerate((("x", "X"), ("a", "A"), ("m", "mask")))}
+    c = mp.Ctx(bw=bw)
+    m = mp.Model(c, dims, f["W"])
+    m.keygen(B, 99)
+    m.set_inputs(B, *sh["x"], *sh["a"], *sh["m"], f["prot"])
+    m.forward(B)
+    assert np.array_equal(m.output(B), f[f"want_bw{bw}"])
+    m.close()
+    c.close()
+
+
+@pytest.mark.parametrize("bw", [32, 64])
+def test_model_default_fixture(mp, synth, bw):
+    import json
+    import os
+    with open(os.path.join(os.path.dirname(__file__), "golden", "model_default.json")) as fh:
+        rec = json.load(fh)
+    B = rec["B"]
+    wl = synth.workload(B, synth.Dims(bw=bw), seed=rec["seed"])
+    c = mp.Ctx(bw=bw)
+    m = mp.Model(c, wl.dims, wl.W)
+    m.keygen(B, 2024)
+    m.set_inputs(B, *wl.shares["x"], *wl.shares["a"], *wl.shares["m"], wl.prot)
+    m.forward(B)
+    assert m.output(B).tolist() == rec[f"want_bw{bw}"]
+    m.close()
+    c.close()

@@ -5,10 +5,10 @@
   degree pairs of gpu_mpc/secure_adj_norm.h:138-184,326-365.
 - a 2-node model whose every intermediate is computed by hand below (floor
   rounding of a negative product included), following the op order of
-  reference/fixed_forward.py:140-172;
+  reference/fixed_forward.py:63-95;
 - node-permutation invariance and padding invariance (exact);
 - agreement with an independent float64 forward of the same network;
-- bw=32 and bw=64 agree when nothing wraps (microbench/test_ring32.py:167-176);
+- bw=32 and bw=64 agree when nothing wraps (microbench/test_ring32.py:57-66);
 - the two-party protocol reconstructs exactly the plaintext outputs.
 """
 import numpy as np
