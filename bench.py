@@ -21,11 +21,17 @@ METRIC = "online secure samples/s (bw=32, B=64, 1 GPU); DCF evals/s; % roofline"
 # Peak integer VALU rate of MI355X: 256 CUs x 4 SIMD x 16 lanes x 2.4 GHz.
 VALU_PEAK_TOPS = 256 * 64 * 2.4e9 / 1e12
 HBM_PEAK_GBS = 8000.0
-# VALU instructions per AES call of the DCF walk, counted in the gfx950 ISA of
-# this build (hipcc --cuda-device-only -S of csrc/kernels.hip, the unrolled
-# level-loop block of k_tr_phase1<uint32_t,4,32>: 10 T-table rounds, sigma,
-# feed-forward and the level update).
-VALU_OPS_PER_AES = 534
+# VALU instructions per AES call of the DCF walk (one tree level: the unrolled
+# cipher, sigma, feed-forward and the level update), counted in the gfx950 ISA
+# of this build: hipcc --cuda-device-only -S csrc/kernels.hip, level-loop block
+# of k_tr_phase1<uint32_t, NT, REP> for each LDS table variant.
+# HBM bytes per k_tr_phase1 launch measured with rocprofv3 --pmc FETCH_SIZE and
+# WRITE_SIZE on this bench command (19 launches per forward, mean), each scaled by
+# the same counter's reading for a 1 GiB elementwise copy (FETCH_SIZE x 2.0,
+# WRITE_SIZE x 1.0); the summary is profiles/k_tr_phase1_affinity_bw32_B64.md.
+TRAFFIC_BYTES_PER_LAUNCH = {"perm64_b512": 689753000}
+VALU_OPS_PER_AES = {"perm64_b512": 402, "perm64_b1024": 402, "t4_rep32_b1024": 462, "t4_rep16_b512": 462,
+                    "t1_rep32_b512": 486}
 
 
 def log(msg):
@@ -97,7 +103,9 @@ def main():
     dcf_ms = prof["ms"]
     dcf_evals_per_s = prof["elements"] / (dcf_ms / 1e3) if dcf_ms > 0 else 0.0
     aes_per_s = prof["aes_calls"] / (dcf_ms / 1e3) if dcf_ms > 0 else 0.0
-    achieved_tops = aes_per_s * VALU_OPS_PER_AES / 1e12
+    variant = ctx.aes_variant_name()
+    key_gbs = prof["hbm_bytes"] / (dcf_ms / 1e3) / 1e9 if dcf_ms > 0 else 0.0
+    achieved_tops = aes_per_s * VALU_OPS_PER_AES.get(variant, float("nan")) / 1e12
     log(f"[bench] DCF phase-1: {prof['launches']} launches, {dcf_ms:.2f} ms/forward, "
         f"{dcf_evals_per_s / 1e9:.3f} G evals/s, {aes_per_s / 1e9:.2f} G AES/s")
 
@@ -125,7 +133,7 @@ def main():
         "rounds_per_step": rounds_per_fwd,
         "key_bytes_per_sample_per_party": round(key_bytes / B, 1),
         "roofline": {
-            "kernel": "k_tr_phase1 (DCF evaluation, AES-128 T-tables in LDS)",
+            "kernel": f"k_tr_phase1 (DCF evaluation, AES-128 T-tables in LDS, {variant})",
             "launches": prof["launches"],
             "avg_launch_us": round(1e3 * dcf_ms / max(prof["launches"], 1), 2),
             "bound": "valu",
@@ -133,7 +141,17 @@ def main():
             "peak": round(VALU_PEAK_TOPS, 2),
             "unit": "TOP/s",
             "frac": round(achieved_tops / VALU_PEAK_TOPS, 4),
-            "traffic": None,
+            "traffic": TRAFFIC_BYTES_PER_LAUNCH.get(variant),
+            "traffic_unit": "bytes per launch (mean over the forward's launches)",
+            "algorithmic_bytes_per_launch": round(prof["hbm_bytes"] / max(prof["launches"], 1)),
+        },
+        "roofline_hbm": {
+            "kernel": "k_tr_phase1 key stream",
+            "bound": "hbm",
+            "achieved": round(key_gbs, 1),
+            "peak": HBM_PEAK_GBS,
+            "unit": "GB/s",
+            "frac": round(key_gbs / HBM_PEAK_GBS, 4),
         },
     }
 

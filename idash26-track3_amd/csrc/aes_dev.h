@@ -87,9 +87,14 @@ __device__ __forceinline__ uint32_t rotl32(uint32_t v, int k) {
   return k == 0 ? v : ((v << k) | (v >> (32 - k)));
 }
 
+// a ^ b ^ c in one v_bitop3_b32 (truth table 0x96 = 0xf0 ^ 0xcc ^ 0xaa).
+__device__ __forceinline__ uint32_t xor3(uint32_t a, uint32_t b, uint32_t c) {
+  return __builtin_amdgcn_bitop3_b32(a, b, c, 0x96);
+}
+
 template <int NT, int REP>
-struct AesLds {
-  static_assert(NT == 1 || NT == 4, "NT");
+struct AesTab {
+  static_assert(NT == 1 || NT == 4, "NT");  // NT == 0: AesPerm
   static_assert(REP >= 1 && REP <= 64 && (REP & (REP - 1)) == 0, "REP");
   static constexpr int kWords = NT * 256 * REP;
   static constexpr int kBytes = kWords * 4;
@@ -108,7 +113,7 @@ struct AesLds {
     __syncthreads();
   }
 
-  __device__ AesLds(const uint32_t *lds) : base((const char *)lds) {
+  __device__ AesTab(const uint32_t *lds) : base((const char *)lds) {
     laneoff = (threadIdx.x & (REP - 1)) * 4u;
   }
 
@@ -125,10 +130,10 @@ struct AesLds {
     uint32_t c0 = in.x ^ rk.w[0], c1 = in.y ^ rk.w[1], c2 = in.z ^ rk.w[2], c3 = in.w ^ rk.w[3];
 #pragma unroll
     for (int r = 1; r < 10; r++) {
-      uint32_t n0 = T(0, c0 & 255u) ^ T(1, (c1 >> 8) & 255u) ^ T(2, (c2 >> 16) & 255u) ^ T(3, c3 >> 24) ^ rk.w[4 * r + 0];
-      uint32_t n1 = T(0, c1 & 255u) ^ T(1, (c2 >> 8) & 255u) ^ T(2, (c3 >> 16) & 255u) ^ T(3, c0 >> 24) ^ rk.w[4 * r + 1];
-      uint32_t n2 = T(0, c2 & 255u) ^ T(1, (c3 >> 8) & 255u) ^ T(2, (c0 >> 16) & 255u) ^ T(3, c1 >> 24) ^ rk.w[4 * r + 2];
-      uint32_t n3 = T(0, c3 & 255u) ^ T(1, (c0 >> 8) & 255u) ^ T(2, (c1 >> 16) & 255u) ^ T(3, c2 >> 24) ^ rk.w[4 * r + 3];
+      uint32_t n0 = xor3(xor3(T(0, c0 & 255u), T(1, (c1 >> 8) & 255u), T(2, (c2 >> 16) & 255u)), T(3, c3 >> 24), rk.w[4 * r + 0]);
+      uint32_t n1 = xor3(xor3(T(0, c1 & 255u), T(1, (c2 >> 8) & 255u), T(2, (c3 >> 16) & 255u)), T(3, c0 >> 24), rk.w[4 * r + 1]);
+      uint32_t n2 = xor3(xor3(T(0, c2 & 255u), T(1, (c3 >> 8) & 255u), T(2, (c0 >> 16) & 255u)), T(3, c1 >> 24), rk.w[4 * r + 2]);
+      uint32_t n3 = xor3(xor3(T(0, c3 & 255u), T(1, (c0 >> 8) & 255u), T(2, (c1 >> 16) & 255u)), T(3, c2 >> 24), rk.w[4 * r + 3]);
       c0 = n0;
       c1 = n1;
       c2 = n2;
@@ -171,6 +176,104 @@ struct AesLds {
     return enc(b, kd);
   }
 };
+
+// T0 alone, 64 copies per entry: entry x, copy j at byte address 256*x + 4*j.
+// Lane l reads copy l mod 64, so a wavefront never has two lanes on one bank, and the
+// byte address of "T0[byte k of c] for this lane" is one v_perm_b32:
+//   byte 0 = (lane*4) mod 256, byte 1 = byte k of c, bytes 2..3 = 0.
+// T1..T3 are rotations of T0 (v_alignbit_b32), three-input XORs are v_bitop3_b32,
+// and the last round gathers the S-box bytes (byte 1 of T0) with v_perm_b32.
+struct AesPerm {
+  static constexpr int kWords = 256 * 64;
+  static constexpr int kBytes = kWords * 4;
+
+  const char *base;
+  uint32_t lane4;
+
+  __device__ static void fill(uint32_t *lds) {
+    for (int w = threadIdx.x; w < kWords; w += blockDim.x) lds[w] = c_T0.v[w >> 6];
+    __syncthreads();
+  }
+
+  __device__ AesPerm(const uint32_t *lds) : base((const char *)lds) { lane4 = (threadIdx.x & 63u) * 4u; }
+
+  // T0[byte K of c]
+  template <int K>
+  __device__ __forceinline__ uint32_t L(uint32_t c) const {
+    const uint32_t addr = __builtin_amdgcn_perm(c, lane4, 0x0c0c0000u | ((4u + K) << 8));
+    return *(const uint32_t *)(base + addr);
+  }
+  // rotl(v, 8k) as a funnel shift
+  template <int K>
+  __device__ __forceinline__ static uint32_t rot(uint32_t v) {
+    return K == 0 ? v : __builtin_amdgcn_alignbit(v, v, 32 - 8 * K);
+  }
+  __device__ __forceinline__ uint32_t col(uint32_t a, uint32_t b, uint32_t c, uint32_t d, uint32_t k) const {
+    return xor3(xor3(L<0>(a), rot<1>(L<1>(b)), rot<2>(L<2>(c))), rot<3>(L<3>(d)), k);
+  }
+  // S[byte 0 of a] | S[byte 1 of b] << 8 | S[byte 2 of c] << 16 | S[byte 3 of d] << 24, ^ k
+  __device__ __forceinline__ uint32_t last(uint32_t a, uint32_t b, uint32_t c, uint32_t d, uint32_t k) const {
+    const uint32_t lo = __builtin_amdgcn_perm(L<1>(b), L<0>(a), 0x0c0c0501u);
+    const uint32_t hi = __builtin_amdgcn_perm(L<3>(d), L<2>(c), 0x0c0c0501u);
+    return ((hi << 16) | lo) ^ k;
+  }
+
+  __device__ __forceinline__ uint4 enc(uint4 in, const AesRK &rk) const {
+    uint32_t c0 = in.x ^ rk.w[0], c1 = in.y ^ rk.w[1], c2 = in.z ^ rk.w[2], c3 = in.w ^ rk.w[3];
+#pragma unroll
+    for (int r = 1; r < 10; r++) {
+      const uint32_t n0 = col(c0, c1, c2, c3, rk.w[4 * r + 0]);
+      const uint32_t n1 = col(c1, c2, c3, c0, rk.w[4 * r + 1]);
+      const uint32_t n2 = col(c2, c3, c0, c1, rk.w[4 * r + 2]);
+      const uint32_t n3 = col(c3, c0, c1, c2, rk.w[4 * r + 3]);
+      c0 = n0;
+      c1 = n1;
+      c2 = n2;
+      c3 = n3;
+    }
+    uint4 o;
+    o.x = last(c0, c1, c2, c3, rk.w[40]);
+    o.y = last(c1, c2, c3, c0, rk.w[41]);
+    o.z = last(c2, c3, c0, c1, rk.w[42]);
+    o.w = last(c3, c0, c1, c2, rk.w[43]);
+    return o;
+  }
+
+  __device__ __forceinline__ uint4 hash(uint4 s, const AesRK &rk) const {
+    uint4 x;
+    x.x = s.z;
+    x.y = s.w;
+    x.z = s.z ^ s.x;
+    x.w = s.w ^ s.y;
+    uint4 y = enc(x, rk);
+    y.x ^= x.x;
+    y.y ^= x.y;
+    y.z ^= x.z;
+    y.w ^= x.w;
+    return y;
+  }
+
+  __device__ __forceinline__ uint4 prf(const AesRK &kd, uint32_t gate, uint32_t field, uint64_t idx) const {
+    uint4 b;
+    b.x = uint32_t(idx);
+    b.y = uint32_t(idx >> 32);
+    b.z = field;
+    b.w = gate;
+    return enc(b, kd);
+  }
+};
+
+// NT = 0 selects the permute-addressed single table (REP must be 64).
+template <int NT, int REP>
+struct AesSel {
+  using type = AesTab<NT, REP>;
+};
+template <>
+struct AesSel<0, 64> {
+  using type = AesPerm;
+};
+template <int NT, int REP>
+using AesLds = typename AesSel<NT, REP>::type;
 
 __device__ __forceinline__ uint4 xor4(uint4 a, uint4 b) {
   return make_uint4(a.x ^ b.x, a.y ^ b.y, a.z ^ b.z, a.w ^ b.w);

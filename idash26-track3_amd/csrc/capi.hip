@@ -165,6 +165,8 @@ const char *mpcx_aes_variant_name(int i) {
   const AesVariant *v = aes_variants(&n);
   return (i >= 0 && i < n) ? v[i].name : "";
 }
+int mpcx_aes_variant(const mpcx_ctx *c) { return c ? c->L.aes_variant : -1; }
+
 mpcx_status mpcx_set_aes_variant(mpcx_ctx *c, int variant, int block) {
   CHECK_CTX(c);
   if (variant < 0 || variant >= mpcx_aes_variant_count()) return fail(c, MPCX_EINVAL, "bad AES variant");
@@ -630,21 +632,24 @@ mpcx_status mpcx_model_profile(mpcx_model *m, int enable) {
   return MPCX_OK;
 }
 
-mpcx_status mpcx_model_profile_read(mpcx_model *m, int *launches, double *ms, double *elements, double *aes) {
+mpcx_status mpcx_model_profile_read(mpcx_model *m, int *launches, double *ms, double *elements, double *aes,
+                                    double *hbm_bytes) {
   if (!m) return MPCX_EINVAL;
   auto &t = m->impl->timer;
   HIPC(m->ctx, hipStreamSynchronize(m->ctx->L.stream), "sync");
-  double tot = 0, el = 0, ae = 0;
+  double tot = 0, el = 0, ae = 0, by = 0;
   for (size_t k = 0; k + 1 < t.ev.size(); k += 2) {
     float f = 0;
     HIPC(m->ctx, hipEventElapsedTime(&f, t.ev[k], t.ev[k + 1]), "hipEventElapsedTime");
     tot += f;
     el += 2.0 * double(t.elems[k / 2]);
     ae += 2.0 * double(t.elems[k / 2]) * double(t.levels[k / 2]);
+    by += t.bytes[k / 2];
   }
   if (launches) *launches = int(t.ev.size() / 2);
   if (ms) *ms = tot;
   if (elements) *elements = el;
   if (aes) *aes = ae;
+  if (hbm_bytes) *hbm_bytes = by;
   return MPCX_OK;
 }

@@ -27,9 +27,8 @@ namespace mpcx {
 // AES LDS variants
 // ---------------------------------------------------------------------------
 static const AesVariant kVariants[] = {
-    {4, 32, 1024, "t4_rep32_b1024"}, {4, 16, 512, "t4_rep16_b512"}, {1, 32, 512, "t1_rep32_b512"},
-    {4, 1, 256, "t4_rep1_b256"},     {4, 8, 256, "t4_rep8_b256"},   {1, 64, 1024, "t1_rep64_b1024"},
-    {4, 32, 512, "t4_rep32_b512"},   {1, 16, 256, "t1_rep16_b256"},
+    {0, 64, 512, "perm64_b512"},   {0, 64, 1024, "perm64_b1024"}, {4, 32, 1024, "t4_rep32_b1024"},
+    {4, 16, 512, "t4_rep16_b512"}, {1, 32, 512, "t1_rep32_b512"},
 };
 const AesVariant *aes_variants(int *count) {
   *count = int(sizeof(kVariants) / sizeof(kVariants[0]));
@@ -44,14 +43,11 @@ struct V {
 template <class Fn>
 static hipError_t with_variant(const Launch &L, Fn &&fn) {
   switch (L.aes_variant) {
-    case 0: return fn(V<4, 32>{});
-    case 1: return fn(V<4, 16>{});
-    case 2: return fn(V<1, 32>{});
-    case 3: return fn(V<4, 1>{});
-    case 4: return fn(V<4, 8>{});
-    case 5: return fn(V<1, 64>{});
-    case 6: return fn(V<4, 32>{});
-    case 7: return fn(V<1, 16>{});
+    case 0: return fn(V<0, 64>{});
+    case 1: return fn(V<0, 64>{});
+    case 2: return fn(V<4, 32>{});
+    case 3: return fn(V<4, 16>{});
+    case 4: return fn(V<1, 32>{});
     default: return hipErrorInvalidValue;
   }
 }

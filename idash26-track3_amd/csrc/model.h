@@ -52,6 +52,7 @@ struct Phase1Timer {
   std::vector<hipEvent_t> ev;  // start/stop pairs
   std::vector<size_t> elems;   // elements per launch
   std::vector<int> levels;     // AES calls per element per party
+  std::vector<double> bytes;   // algorithmic HBM bytes per launch (both parties)
   void reset();
 };
 

@@ -18,6 +18,7 @@ void Phase1Timer::reset() {
   ev.clear();
   elems.clear();
   levels.clear();
+  bytes.clear();
 }
 
 #define TRY(x)                           \
@@ -436,6 +437,13 @@ class Model final : public ModelBase {
       timer.ev.push_back(e1);
       timer.elems.push_back(n);
       timer.levels.push_back((lay.use_a ? lay.a.L + 1 : 0) + (lay.use_b ? lay.b.L + 1 : 0));
+      // per element and party: the masked input, and for every DCF the root,
+      // correction words and leaf (16 B each), the output-mask bit read and the
+      // message bit written (the bias vector is ncol words, cache resident)
+      double per = double(sizeof(T));
+      if (lay.use_a) per += 16.0 * (lay.a.L + 2) + 0.125 + 0.125;
+      if (lay.use_b) per += 16.0 * (lay.b.L + 2) + 0.125 + 0.125;
+      timer.bytes.push_back(2.0 * per * double(n));
     }
     counters.bitplanes(n, int(lay.use_a) + int(lay.use_b));
     TRY(launch_tr_phase2<T>(L_, lay, K0, K1, x, bias, ncol, ba0_.p, ba1_.p, bb0_.p, bb1_.p, msg0_.p, msg1_.p));

@@ -31,6 +31,7 @@ _SIGS = {
     "mpcx_aes_variant_count": (C.c_int, []),
     "mpcx_aes_variant_name": (C.c_char_p, [C.c_int]),
     "mpcx_set_aes_variant": (C.c_int, [C.c_void_p, C.c_int, C.c_int]),
+    "mpcx_aes_variant": (C.c_int, [C.c_void_p]),
     "mpcx_bytes_exchanged": (C.c_uint64, [C.c_void_p]),
     "mpcx_rounds": (C.c_uint64, [C.c_void_p]),
     "mpcx_reset_counters": (None, [C.c_void_p]),
@@ -79,7 +80,7 @@ _SIGS = {
     "mpcx_model_forward": (C.c_int, [C.c_void_p, C.c_int]),
     "mpcx_model_output": (C.c_int, [C.c_void_p, C.c_int, C.c_void_p]),
     "mpcx_model_profile": (C.c_int, [C.c_void_p, C.c_int]),
-    "mpcx_model_profile_read": (C.c_int, [C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p]),
+    "mpcx_model_profile_read": (C.c_int, [C.c_void_p] + [C.c_void_p] * 5),
 }
 
 
@@ -174,6 +175,9 @@ class Ctx:
 
     def set_aes_variant(self, v, block=0):
         self.check(self.lib.mpcx_set_aes_variant(self.h, v, block), "set_aes_variant")
+
+    def aes_variant_name(self):
+        return self.lib.mpcx_aes_variant_name(self.lib.mpcx_aes_variant(self.h)).decode()
 
     @property
     def bytes_exchanged(self):
@@ -414,7 +418,8 @@ class Model:
 
     def profile_read(self):
         n = C.c_int()
-        ms, el, ae = C.c_double(), C.c_double(), C.c_double()
-        self.ctx.check(self.lib.mpcx_model_profile_read(self.h, C.byref(n), C.byref(ms), C.byref(el), C.byref(ae)),
-                       "profile_read")
-        return {"launches": n.value, "ms": ms.value, "elements": el.value, "aes_calls": ae.value}
+        ms, el, ae, by = C.c_double(), C.c_double(), C.c_double(), C.c_double()
+        self.ctx.check(self.lib.mpcx_model_profile_read(self.h, C.byref(n), C.byref(ms), C.byref(el), C.byref(ae),
+                                                        C.byref(by)), "profile_read")
+        return {"launches": n.value, "ms": ms.value, "elements": el.value, "aes_calls": ae.value,
+                "hbm_bytes": by.value}

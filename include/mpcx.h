@@ -54,6 +54,9 @@ mpcx_status mpcx_synchronize(mpcx_ctx *ctx);
 int mpcx_aes_variant_count(void);
 const char *mpcx_aes_variant_name(int i);
 mpcx_status mpcx_set_aes_variant(mpcx_ctx *ctx, int variant, int block_threads);
+/* Variant in use (set by mpcx_set_aes_variant or the MPCX_AES_VARIANT environment
+ * variable at mpcx_create). */
+int mpcx_aes_variant(const mpcx_ctx *ctx);
 
 /* Exchange accounting, both directions summed (the reference's "Comm (B)",
  * gpu_mpc/deepdtagen_inference.cu:556-558, and GpuPeer::bytesSent/Received,
@@ -199,9 +202,10 @@ mpcx_status mpcx_model_output(mpcx_model *m, int B, int64_t *h_out);
 /* DCF (phase-1) kernel timing with HIP events on the launch stream. */
 mpcx_status mpcx_model_profile(mpcx_model *m, int enable);
 /* After a synchronized forward: number of phase-1 launches, their summed time
- * (ms), elements (both parties) and AES calls (both parties). */
+ * (ms), elements (both parties), AES calls (both parties) and algorithmic HBM
+ * bytes (keys and inputs read, message bits written; both parties). */
 mpcx_status mpcx_model_profile_read(mpcx_model *m, int *launches, double *ms, double *elements,
-                                    double *aes_calls);
+                                    double *aes_calls, double *hbm_bytes);
 
 #ifdef __cplusplus
 }
