@@ -548,6 +548,44 @@ mpcx_status mpcx_reveal_eval(mpcx_ctx *c, size_t n, const void *k0, const void *
                      : reveal_eval_t<uint64_t>(c, n, k0, k1, v0, v1, out);
 }
 
+// ---------------- adjacency normalisation ----------------
+size_t mpcx_adjnorm_key_bytes(mpcx_ctx *c, int B, int N) {
+  return (c && B > 0 && N > 0) ? adjnorm_key_bytes(c->bw, c->s, B, N) : 0;
+}
+
+mpcx_status mpcx_adjnorm_keygen(mpcx_ctx *c, int B, int N, uint64_t seed, void *mask, void *k0, void *k1) {
+  CHECK_CTX(c);
+  if (B < 1 || N < 1 || N > 255 || !mask || !k0 || !k1) return fail(c, MPCX_EINVAL, "adjnorm_keygen: bad argument");
+  HIPC(c, adjnorm_keygen(c->bw, c->s, B, N, seed, c->L, mask, static_cast<uint8_t *>(k0), static_cast<uint8_t *>(k1)),
+       "adjnorm_keygen");
+  return MPCX_OK;
+}
+
+mpcx_status mpcx_adjnorm_eval(mpcx_ctx *c, int B, int N, int nmax, const void *k0, const void *k1, const void *a0,
+                              const void *a1, void *out) {
+  CHECK_CTX(c);
+  if (B < 1 || N < 1 || N > 255 || nmax < 0 || nmax > 255 || !k0 || !k1 || !a0 || !a1 || !out)
+    return fail(c, MPCX_EINVAL, "adjnorm_eval: bad argument");
+  HIPC(c,
+       adjnorm_eval(c->bw, c->s, B, N, nmax, c->L, static_cast<const uint8_t *>(k0), static_cast<const uint8_t *>(k1),
+                    a0, a1, out, &c->counters),
+       "adjnorm_eval");
+  return MPCX_OK;
+}
+
+// ---------------- pinned host memory ----------------
+mpcx_status mpcx_host_alloc(size_t bytes, void **out) {
+  if (!out || bytes == 0) return MPCX_EINVAL;
+  *out = nullptr;
+  hipError_t e = hipHostMalloc(out, bytes, hipHostMallocDefault);
+  if (e == hipErrorOutOfMemory || e == hipErrorMemoryAllocation) return MPCX_ENOMEM;
+  return e == hipSuccess ? MPCX_OK : MPCX_EHIP;
+}
+
+void mpcx_host_free(void *p) {
+  if (p) (void)hipHostFree(p);
+}
+
 // ---------------- model ----------------
 mpcx_status mpcx_model_create(mpcx_ctx *c, const mpcx_model_dims *dims, const int64_t *W, size_t nW,
                               mpcx_model **out) {
@@ -597,6 +635,30 @@ mpcx_status mpcx_model_import_keys(mpcx_model *m, int B, const void *k0, const v
 mpcx_status mpcx_model_export_keys(mpcx_model *m, int party, void *dst, size_t bytes) {
   if (!m || !dst || (party != 0 && party != 1)) return MPCX_EINVAL;
   HIPC(m->ctx, m->impl->export_keys(party, dst, bytes), "model_export_keys");
+  return MPCX_OK;
+}
+
+mpcx_status mpcx_model_release_arena(mpcx_model *m) {
+  if (!m) return MPCX_EINVAL;
+  HIPC(m->ctx, m->impl->release_arena(), "model_release_arena");
+  return MPCX_OK;
+}
+
+mpcx_status mpcx_model_attach_host_keys(mpcx_model *m, int B, const void *k0, const void *k1, size_t bytes,
+                                        size_t slot_bytes) {
+  if (!m || !k0 || !k1) return MPCX_EINVAL;
+  if (B < 1 || bytes != m->impl->key_bytes(B)) return fail(m->ctx, MPCX_EINVAL, "attach_host_keys: key size mismatch");
+  hipError_t e = m->impl->attach_host_keys(B, k0, k1, bytes, slot_bytes);
+  if (e == hipErrorInvalidValue)
+    return fail(m->ctx, MPCX_EINVAL, "attach_host_keys: slot_bytes smaller than the largest gate key");
+  HIPC(m->ctx, e, "model_attach_host_keys");
+  return MPCX_OK;
+}
+
+mpcx_status mpcx_model_stream_stats(const mpcx_model *m, int *chunks, uint64_t *bytes_h2d) {
+  if (!m) return MPCX_EINVAL;
+  if (chunks) *chunks = m->impl->stream_stats.chunks;
+  if (bytes_h2d) *bytes_h2d = m->impl->stream_stats.bytes_h2d;
   return MPCX_OK;
 }
 

@@ -3,6 +3,7 @@
 //
 // Mirrors DeepDTAGenAffinity<T>::_forward (gpu_mpc/deepdtagen.h:183-222) with
 // the op order of reference/fixed_forward.py:63-95:
+//   reveal X and the atom mask
 //   secure adjacency normalisation (secure_adj_norm.h:393-659)
 //   3 x GCN:  Z = H.W^T (public weights, no exchange) -> TR -> A_norm.(XW) (SxS)
 //             -> TRRELU(+bias)
@@ -10,11 +11,17 @@
 //   drug FC (TRRELU), drug FC (TR), concat [drug, protein] (deepdtagen.h:45-101)
 //   fusion FCs (TRRELU ...), output layer unmasked with the clear output mask
 //   (ddg_orca_base.h:296-302) and truncated locally.
+//
+// Keys are read either from a resident arena in HBM (initGPUKeyArena,
+// patches/EzPC-GPU-MPC.track3.patch:632-661) or streamed from pinned host
+// memory through two device slots on a copy stream (the chunked pipeline of
+// gpu_mpc/deepdtagen_inference.cu:608-859).
 #pragma once
 #include <hip/hip_runtime.h>
 
 #include <cstdint>
 #include <string>
+#include <utility>
 #include <vector>
 
 #include "kernels.h"
@@ -56,6 +63,12 @@ struct Phase1Timer {
   void reset();
 };
 
+// Streaming statistics of the last forward (host-key mode).
+struct StreamStats {
+  int chunks = 0;
+  uint64_t bytes_h2d = 0;  // key bytes copied host -> device, both parties
+};
+
 class ModelBase {
  public:
   virtual ~ModelBase() = default;
@@ -63,6 +76,12 @@ class ModelBase {
   virtual hipError_t keygen(int B, uint64_t seed) = 0;
   virtual hipError_t import_keys(int B, const void *k0, const void *k1, size_t bytes) = 0;
   virtual hipError_t export_keys(int party, void *dst, size_t bytes) = 0;
+  virtual hipError_t release_arena() = 0;
+  // Host-key (streaming) mode: keys of a batch of B in host memory (pinned for
+  // asynchronous copies), copied per chunk of consecutive gates into one of two
+  // device slots of slot_bytes per party while the previous chunk computes.
+  virtual hipError_t attach_host_keys(int B, const void *h_k0, const void *h_k1, size_t bytes,
+                                      size_t slot_bytes) = 0;
   virtual hipError_t set_inputs(int B, const void *x0, const void *x1, const void *a0, const void *a1,
                                 const void *m0, const void *m1, const int64_t *prot) = 0;
   virtual hipError_t forward(int B) = 0;
@@ -70,10 +89,21 @@ class ModelBase {
   virtual uint8_t *arena(int party) = 0;
   Counters counters;
   Phase1Timer timer;
+  StreamStats stream_stats;
   std::string err;
 };
 
 ModelBase *make_model(int bw, int s, const ModelDims &d, const int64_t *W, size_t nW, const Launch &L,
                       std::string *err);
+
+// ---------------- standalone secure adjacency normalisation ----------------
+// ddgSecureAdjNormKeygen / ddgSecureAdjNormEval (gpu_mpc/secure_adj_norm.h:203-374,
+// 393-659): A (B x N x N, 0/1 with self loops) as additive shares -> masked
+// A_norm = A (.) floor(T[d_i] T[d_j] / 2^s) + out_mask.
+size_t adjnorm_key_bytes(int bw, int s, int B, int N);
+hipError_t adjnorm_keygen(int bw, int s, int B, int N, uint64_t seed, const Launch &L, void *out_mask,
+                          uint8_t *k0, uint8_t *k1);
+hipError_t adjnorm_eval(int bw, int s, int B, int N, int nmax, const Launch &L, const uint8_t *k0,
+                        const uint8_t *k1, const void *a0, const void *a1, void *out_masked, Counters *ctr);
 
 }  // namespace mpcx

@@ -1,7 +1,9 @@
-// model.hip -- dealer (keygen) and online forward of the secure affinity model.
-// See model.h for the reference mapping.  The gate sequence, gate ids and key
-// arena offsets are a pure function of (dims, B): keygen and forward walk the
-// same sequence with a cursor, so the key arena needs no index.
+// model.hip -- dealer (keygen) and online forward of the secure affinity model,
+// and the standalone secure adjacency normalisation.  See model.h for the
+// reference mapping.  The gate sequence, gate ids and key offsets are a pure
+// function of (dims, B): keygen and forward walk the same sequence with a
+// cursor, so the key arena needs no index; plan() lists the gates' key ranges
+// and the forward checks every gate against it.
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
@@ -52,27 +54,413 @@ struct DevBuf {
   size_t n = 0;
   hipError_t alloc(size_t count) {
     if (count <= n) return hipSuccess;
-    if (p) (void)hipFree(p);
-    p = nullptr;
-    n = 0;
+    release();
     hipError_t e = hipMalloc((void **)&p, std::max<size_t>(count, 1) * sizeof(T));
     if (e == hipSuccess) n = count;
     return e;
   }
-  ~DevBuf() {
+  void release() {
     if (p) (void)hipFree(p);
+    p = nullptr;
+    n = 0;
+  }
+  ~DevBuf() { release(); }
+};
+
+// Both parties' key bytes at absolute offset `off` live at k[p] + (off - begin).
+struct KeyView {
+  const uint8_t *k[2] = {nullptr, nullptr};
+  size_t begin = 0;
+};
+
+// Supplies the key bytes [begin, end) of the next gate (resident arena or a
+// streamed slot) before the gate's kernels are enqueued.
+struct KeySource {
+  virtual hipError_t acquire(size_t begin, size_t end, KeyView *kv) = 0;
+  virtual ~KeySource() = default;
+};
+
+// Exchange buffers shared by the gates: both parties' messages and the four
+// packed bit planes of the DCF outputs.
+template <typename T>
+struct Workspace {
+  DevBuf<T> m0, m1;
+  DevBuf<uint64_t> bits;
+  size_t cap = 0, wpp = 0;
+  hipError_t ensure(size_t n) {
+    if (n <= cap) return hipSuccess;
+    TRY(m0.alloc(n));
+    TRY(m1.alloc(n));
+    wpp = (n + 63) / 64;
+    TRY(bits.alloc(4 * wpp));
+    cap = n;
+    return hipSuccess;
+  }
+  uint64_t *plane(int k) { return bits.p + size_t(k) * wpp; }
+};
+
+// ---------------------------------------------------------------------------
+// online evaluation of gates at a cursor
+// ---------------------------------------------------------------------------
+template <typename T>
+struct Runner {
+  const Launch &L;
+  int bw, s;
+  Workspace<T> &ws;
+  Counters &ctr;
+  Phase1Timer *timer;
+  KeySource &src;
+  KeyView kv;
+  Cursor c;
+
+  Runner(const Launch &L_, int bw_, int s_, Workspace<T> &ws_, Counters &ctr_, Phase1Timer *t, KeySource &src_)
+      : L(L_), bw(bw_), s(s_), ws(ws_), ctr(ctr_), timer(t), src(src_) {}
+
+  // Make the gate [c.off, end) available; returns the base of the gate
+  // relative to the key view.
+  hipError_t enter(size_t end, size_t *rel) {
+    TRY(src.acquire(c.off, end, &kv));
+    *rel = c.off - kv.begin;
+    return hipSuccess;
+  }
+  void leave(size_t end) {
+    c.off = end;
+    c.gate++;
+  }
+
+  hipError_t reveal(size_t n, const T *v0, const T *v1, int rowlen, T *out) {
+    const size_t end = reveal_layout(bw, n, c.off).end;
+    size_t b;
+    TRY(enter(end, &b));
+    RevealLayout lay = reveal_layout(bw, n, b);
+    TRY(launch_reveal_eval<T>(L, lay, kv.k[0], kv.k[1], v0, v1, rowlen, ws.m0.p, ws.m1.p));
+    ctr.msg(n, bw);
+    TRY(launch_reconstruct<T>(L, n, ws.m0.p, ws.m1.p, out));
+    leave(end);
+    return hipSuccess;
+  }
+
+  hipError_t tr(int kind, size_t n, const T *x, const T *bias, int ncol, T *out) {
+    const size_t end = tr_layout(kind, bw, s, n, c.off).end;
+    size_t b;
+    TRY(enter(end, &b));
+    TrLayout lay = tr_layout(kind, bw, s, n, b);
+    hipEvent_t e0 = nullptr, e1 = nullptr;
+    if (timer && timer->on) {
+      TRY(hipEventCreate(&e0));
+      TRY(hipEventCreate(&e1));
+      TRY(hipEventRecord(e0, L.stream));
+    }
+    TRY(launch_tr_phase1<T>(L, lay, kv.k[0], kv.k[1], x, bias, ncol, ws.plane(0), ws.plane(1), ws.plane(2),
+                            ws.plane(3)));
+    if (timer && timer->on) {
+      TRY(hipEventRecord(e1, L.stream));
+      timer->ev.push_back(e0);
+      timer->ev.push_back(e1);
+      timer->elems.push_back(n);
+      timer->levels.push_back((lay.use_a ? lay.a.L + 1 : 0) + (lay.use_b ? lay.b.L + 1 : 0));
+      // per element and party: the masked input, and for every DCF the root,
+      // correction words and leaf (16 B each), the output-mask bit read and the
+      // message bit written (the bias vector is ncol words, cache resident)
+      double per = double(sizeof(T));
+      if (lay.use_a) per += 16.0 * (lay.a.L + 2) + 0.125 + 0.125;
+      if (lay.use_b) per += 16.0 * (lay.b.L + 2) + 0.125 + 0.125;
+      timer->bytes.push_back(2.0 * per * double(n));
+    }
+    ctr.bitplanes(n, int(lay.use_a) + int(lay.use_b));
+    TRY(launch_tr_phase2<T>(L, lay, kv.k[0], kv.k[1], x, bias, ncol, ws.plane(0), ws.plane(1), ws.plane(2),
+                            ws.plane(3), ws.m0.p, ws.m1.p));
+    ctr.msg(n, bw);
+    TRY(launch_reconstruct<T>(L, n, ws.m0.p, ws.m1.p, out));
+    leave(end);
+    return hipSuccess;
+  }
+
+  hipError_t mul(size_t nx, size_t ny, size_t nz, const uint32_t *ia, const uint32_t *ib, const T *x, const T *y,
+                 T *out) {
+    const size_t end = mul_layout(bw, nx, ny, nz, c.off).end;
+    size_t b;
+    TRY(enter(end, &b));
+    MulLayout lay = mul_layout(bw, nx, ny, nz, b);
+    TRY(launch_mul_eval<T>(L, lay, kv.k[0], kv.k[1], ia, ib, x, y, ws.m0.p, ws.m1.p));
+    ctr.msg(nz, bw);
+    TRY(launch_reconstruct<T>(L, nz, ws.m0.p, ws.m1.p, out));
+    leave(end);
+    return hipSuccess;
+  }
+
+  // vh: n-element scratch for the revealed intermediate
+  hipError_t lut8(size_t n, const T *table, const T *x, T *vh, T *out) {
+    const size_t end = lut8_layout(bw, n, c.off).end;
+    size_t b;
+    TRY(enter(end, &b));
+    Lut8Layout lay = lut8_layout(bw, n, b);
+    TRY(launch_lut8_phase1<T>(L, lay, kv.k[0], kv.k[1], table, x, ws.m0.p, ws.m1.p));
+    ctr.msg(n, bw);
+    TRY(launch_reconstruct<T>(L, n, ws.m0.p, ws.m1.p, vh));
+    TRY(launch_lut8_phase2<T>(L, lay, kv.k[0], kv.k[1], vh, ws.m0.p, ws.m1.p));
+    ctr.msg(n, bw);
+    TRY(launch_reconstruct<T>(L, n, ws.m0.p, ws.m1.p, out));
+    leave(end);
+    return hipSuccess;
+  }
+
+  // batched C_b = A_b (M x K) . B_b (K x N), Beaver
+  hipError_t sxs(int nb, int M, int K, int N, const T *A, const T *Bm, T *out) {
+    const size_t end = sxs_layout(bw, nb, M, K, N, c.off).end;
+    size_t b;
+    TRY(enter(end, &b));
+    SxsLayout lay = sxs_layout(bw, nb, M, K, N, b);
+    const uint8_t *K0 = kv.k[0], *K1 = kv.k[1];
+    GemmArgs<T> g;
+    g.M = M;
+    g.K = K;
+    g.N = N;
+    g.batch = nb;
+    g.sA = size_t(M) * K;
+    g.sB = size_t(K) * N;
+    g.sC = size_t(M) * N;
+    // party 0: (A^ - RA0)(B^ - RB0) + C0
+    g.A1 = A;
+    g.A2 = reinterpret_cast<const T *>(K0 + lay.off_ra);
+    g.B1 = Bm;
+    g.B2 = reinterpret_cast<const T *>(K0 + lay.off_rb);
+    g.Cin = reinterpret_cast<const T *>(K0 + lay.off_c);
+    g.C = ws.m0.p;
+    TRY(launch_gemm<T>(L, g));
+    // party 1: C1 - A^ RB1 - RA1 B^
+    GemmArgs<T> h = g;
+    h.A2 = nullptr;
+    h.B2 = nullptr;
+    h.B1 = reinterpret_cast<const T *>(K1 + lay.off_rb);
+    h.Cin = reinterpret_cast<const T *>(K1 + lay.off_c);
+    h.C = ws.m1.p;
+    h.sign = -1;
+    TRY(launch_gemm<T>(L, h));
+    h.A1 = reinterpret_cast<const T *>(K1 + lay.off_ra);
+    h.B1 = Bm;
+    h.Cin = ws.m1.p;
+    TRY(launch_gemm<T>(L, h));
+    const size_t nc = size_t(nb) * M * N;
+    ctr.msg(nc, bw);
+    TRY(launch_reconstruct<T>(L, nc, ws.m0.p, ws.m1.p, out));
+    leave(end);
+    return hipSuccess;
+  }
+
+  // last layer: unmask with the clear output mask, floor shift, bias
+  hipError_t output(int B, size_t n, const T *z, int64_t bias, int64_t *out) {
+    const size_t end = reveal_layout(bw, n, c.off).end;
+    size_t b;
+    TRY(enter(end, &b));
+    RevealLayout lay = reveal_layout(bw, n, b);
+    TRY(launch_output<T>(L, B, bw, s, z, reinterpret_cast<const T *>(kv.k[0] + lay.off_r), bias, out));
+    leave(end);
+    return hipSuccess;
+  }
+};
+
+// ---------------------------------------------------------------------------
+// dealer: keys of gates at a cursor, written into resident arenas
+// ---------------------------------------------------------------------------
+template <typename T>
+struct Dealer {
+  const Launch &L;
+  int bw, s;
+  uint64_t seed;
+  uint8_t *K0, *K1;
+  Cursor c;
+
+  hipError_t reveal(size_t n, T *mask) {
+    RevealLayout lay = reveal_layout(bw, n, c.off);
+    TRY(launch_reveal_keygen<T>(L, lay, seed, c.gate, mask, K0, K1));
+    c.off = lay.end;
+    c.gate++;
+    return hipSuccess;
+  }
+  hipError_t tr(int kind, size_t n, const T *in, T *out) {
+    TrLayout lay = tr_layout(kind, bw, s, n, c.off);
+    TRY(launch_tr_keygen<T>(L, lay, seed, c.gate, in, out, K0, K1));
+    c.off = lay.end;
+    c.gate++;
+    return hipSuccess;
+  }
+  hipError_t mul(size_t nx, size_t ny, size_t nz, const uint32_t *ia, const uint32_t *ib, const T *rx, const T *ry,
+                 T *rz) {
+    MulLayout lay = mul_layout(bw, nx, ny, nz, c.off);
+    TRY(launch_mul_keygen<T>(L, lay, seed, c.gate, ia, ib, rx, ry, rz, K0, K1));
+    c.off = lay.end;
+    c.gate++;
+    return hipSuccess;
+  }
+  hipError_t lut8(size_t n, const T *in, T *out) {
+    Lut8Layout lay = lut8_layout(bw, n, c.off);
+    TRY(launch_lut8_keygen<T>(L, lay, seed, c.gate, in, out, K0, K1));
+    c.off = lay.end;
+    c.gate++;
+    return hipSuccess;
+  }
+  // SxS: C = rA.rB - RA0.RB0 + rC; tmp: nb*M*N scratch
+  hipError_t sxs(int nb, int M, int K, int N, const T *rA, const T *rB, T *rC, T *tmp) {
+    SxsLayout lay = sxs_layout(bw, nb, M, K, N, c.off);
+    T *RA0 = reinterpret_cast<T *>(K0 + lay.off_ra), *RA1 = reinterpret_cast<T *>(K1 + lay.off_ra);
+    T *RB0 = reinterpret_cast<T *>(K0 + lay.off_rb), *RB1 = reinterpret_cast<T *>(K1 + lay.off_rb);
+    const size_t na = size_t(nb) * M * K, nbb = size_t(nb) * K * N, nc = size_t(nb) * M * N;
+    TRY(launch_split<T>(L, seed, c.gate, F_SPLIT + 0, na, rA, RA0, RA1, nullptr));
+    TRY(launch_split<T>(L, seed, c.gate, F_SPLIT + 1, nbb, rB, RB0, RB1, nullptr));
+    TRY(launch_prf_ring<T>(L, seed, c.gate, F_ROUT, nc, rC));  // output mask
+    GemmArgs<T> g;
+    g.M = M;
+    g.K = K;
+    g.N = N;
+    g.batch = nb;
+    g.sA = size_t(M) * K;
+    g.sB = size_t(K) * N;
+    g.sC = size_t(M) * N;
+    g.A1 = rA;
+    g.B1 = rB;
+    g.Cin = rC;
+    g.C = tmp;
+    TRY(launch_gemm<T>(L, g));  // rA.rB + rC
+    g.A1 = RA0;
+    g.B1 = RB0;
+    g.Cin = tmp;
+    g.C = tmp;
+    g.sign = -1;
+    TRY(launch_gemm<T>(L, g));  // - RA0.RB0
+    TRY(launch_split<T>(L, seed, c.gate, F_SPLIT + 2, nc, tmp, reinterpret_cast<T *>(K0 + lay.off_c),
+                        reinterpret_cast<T *>(K1 + lay.off_c), nullptr));
+    c.off = lay.end;
+    c.gate++;
+    return hipSuccess;
+  }
+  // output mask in the clear for both evaluators
+  hipError_t output(size_t n, const T *mask) {
+    RevealLayout lay = reveal_layout(bw, n, c.off);
+    TRY(hipMemcpyAsync(K0 + lay.off_r, mask, n * sizeof(T), hipMemcpyDeviceToDevice, L.stream));
+    TRY(hipMemcpyAsync(K1 + lay.off_r, mask, n * sizeof(T), hipMemcpyDeviceToDevice, L.stream));
+    c.off = lay.end;
+    c.gate++;
+    return hipSuccess;
+  }
+};
+
+// ---------------------------------------------------------------------------
+// secure adjacency normalisation block (secure_adj_norm.h:203-374, 393-659):
+// reveal A; reveal the degrees (row sums of the A shares); LUT8 -> T[d];
+// MUL T[d_i] T[d_j] over the upper triangle; TRSLACK; MUL A (.) W.
+// ---------------------------------------------------------------------------
+template <typename T>
+struct AdjNorm {
+  int B = -1, N = -1, s = 0, nmax = 0;
+  DevBuf<uint32_t> oa, ob, wa, wb;  // index maps: outer product, A (.) W
+  DevBuf<T> table;                  // T[k] = llround(2^s / sqrt(k)), 1 <= k <= nmax
+  DevBuf<T> t0, t1, p0, p1;         // scratch: 2 x BN, 2 x BP
+
+  static size_t layout_end(int bw, int s, int B, int N, size_t o) {
+    const size_t BN = size_t(B) * N, BNN = BN * N, BP = size_t(B) * pairs_of(N);
+    o = reveal_layout(bw, BNN, o).end;
+    o = reveal_layout(bw, BN, o).end;
+    o = lut8_layout(bw, BN, o).end;
+    o = mul_layout(bw, BN, BN, BP, o).end;
+    o = tr_layout(G_TRSLACK, bw, s, BP, o).end;
+    o = mul_layout(bw, BNN, BP, BNN, o).end;
+    return o;
+  }
+
+  hipError_t prepare(int B_, int N_, int s_, int nmax_) {
+    if (B_ == B && N_ == N && s_ == s && nmax_ == nmax) return hipSuccess;
+    const size_t P = pairs_of(N_), BN = size_t(B_) * N_, BNN = BN * N_;
+    std::vector<uint32_t> hoa(B_ * P), hob(B_ * P), hwa(BNN), hwb(BNN);
+    for (int b = 0; b < B_; b++) {
+      size_t q = size_t(b) * P;
+      for (int i = 0; i < N_; i++)
+        for (int j = i; j < N_; j++) {
+          hoa[q] = uint32_t(b * N_ + i);
+          hob[q] = uint32_t(b * N_ + j);
+          q++;
+        }
+      for (int i = 0; i < N_; i++)
+        for (int j = 0; j < N_; j++) {
+          size_t e = (size_t(b) * N_ + i) * N_ + j;
+          hwa[e] = uint32_t(e);
+          hwb[e] = uint32_t(size_t(b) * P + (i <= j ? pidx(N_, i, j) : pidx(N_, j, i)));
+        }
+    }
+    TRY(oa.alloc(hoa.size()));
+    TRY(ob.alloc(hob.size()));
+    TRY(wa.alloc(hwa.size()));
+    TRY(wb.alloc(hwb.size()));
+    TRY(hipMemcpy(oa.p, hoa.data(), hoa.size() * 4, hipMemcpyHostToDevice));
+    TRY(hipMemcpy(ob.p, hob.data(), hob.size() * 4, hipMemcpyHostToDevice));
+    TRY(hipMemcpy(wa.p, hwa.data(), hwa.size() * 4, hipMemcpyHostToDevice));
+    TRY(hipMemcpy(wb.p, hwb.data(), hwb.size() * 4, hipMemcpyHostToDevice));
+    std::vector<T> tab(256, T(0));
+    const double q = std::ldexp(1.0, s_);
+    for (int k = 1; k <= nmax_ && k < 256; k++) tab[k] = T(std::llround(q / std::sqrt(double(k))));
+    TRY(table.alloc(256));
+    TRY(hipMemcpy(table.p, tab.data(), 256 * sizeof(T), hipMemcpyHostToDevice));
+    TRY(t0.alloc(BN));
+    TRY(t1.alloc(BN));
+    TRY(p0.alloc(size_t(B_) * P));
+    TRY(p1.alloc(size_t(B_) * P));
+    B = B_;
+    N = N_;
+    s = s_;
+    nmax = nmax_;
+    return hipSuccess;
+  }
+
+  // rA: mask of the revealed A (BNN); rN: mask of A_norm (BNN)
+  hipError_t keygen(Dealer<T> &d, T *rA, T *rN) {
+    const size_t BN = size_t(B) * N, BNN = BN * N, BP = size_t(B) * pairs_of(N);
+    TRY(d.reveal(BNN, rA));
+    TRY(d.reveal(BN, t0.p));                                // degree mask
+    TRY(d.lut8(BN, t0.p, t1.p));                            // mask of T[d]
+    TRY(d.mul(BN, BN, BP, oa.p, ob.p, t1.p, t1.p, p0.p));  // mask of the outer product
+    TRY(d.tr(G_TRSLACK, BP, p0.p, p1.p));                    // mask of W
+    TRY(d.mul(BNN, BP, BNN, wa.p, wb.p, rA, p1.p, rN));    // mask of A_norm
+    return hipSuccess;
+  }
+
+  // a0, a1: A shares (BNN); Ah: revealed A (BNN); An: masked A_norm (BNN)
+  hipError_t eval(Runner<T> &r, const T *a0, const T *a1, T *Ah, T *An) {
+    const size_t BN = size_t(B) * N, BNN = BN * N, BP = size_t(B) * pairs_of(N);
+    TRY(r.reveal(BNN, a0, a1, 0, Ah));
+    TRY(r.reveal(BN, a0, a1, N, t0.p));  // degree = row sums of the A shares
+    TRY(r.lut8(BN, table.p, t0.p, t1.p, t0.p));
+    TRY(r.mul(BN, BN, BP, oa.p, ob.p, t0.p, t0.p, p0.p));
+    TRY(r.tr(G_TRSLACK, BP, p0.p, nullptr, 1, p1.p));
+    TRY(r.mul(BNN, BP, BNN, wa.p, wb.p, Ah, p1.p, An));
+    return hipSuccess;
+  }
+};
+
+// Keys in one device allocation per party, addressed directly.
+struct ArenaSource final : KeySource {
+  const uint8_t *k[2] = {nullptr, nullptr};
+  size_t bytes = 0;
+  hipError_t acquire(size_t begin, size_t end, KeyView *kv) override {
+    if (end > bytes || begin > end) return hipErrorInvalidValue;
+    kv->k[0] = k[0];
+    kv->k[1] = k[1];
+    kv->begin = 0;
+    return hipSuccess;
   }
 };
 
 }  // namespace
 
+// ===========================================================================
+// the model
+// ===========================================================================
 template <typename T>
-class Model final : public ModelBase {
+class Model final : public ModelBase, KeySource {
  public:
   Model(int bw, int s, const ModelDims &d, const Launch &L) : bw_(bw), s_(s), d_(d), L_(L) {}
   ~Model() override {
-    for (int p = 0; p < 2; p++)
-      if (arena_[p]) (void)hipFree(arena_[p]);
+    free_arena();
+    free_stream();
     timer.reset();
   }
 
@@ -119,53 +507,69 @@ class Model final : public ModelBase {
       TRY(hipMemcpy(wt_[l].p, w.data(), w.size() * sizeof(T), hipMemcpyHostToDevice));
       TRY(hipMemcpy(bias_[l].p, b.data(), b.size() * sizeof(T), hipMemcpyHostToDevice));
     }
-    std::vector<T> tab(256, T(0));
-    const double q = std::ldexp(1.0, s_);
-    for (int k = 1; k <= d_.lut_nmax && k < 256; k++) tab[k] = T(std::llround(q / std::sqrt(double(k))));
-    TRY(table_.alloc(256));
-    TRY(hipMemcpy(table_.p, tab.data(), 256 * sizeof(T), hipMemcpyHostToDevice));
     return hipSuccess;
   }
 
-  // ---------------- plan sizes ----------------
-  size_t key_bytes(int B) const override {
+  // ---------------- gate plan ----------------
+  // Key range of every gate of a batch of B, in forward order.
+  std::vector<std::pair<size_t, size_t>> plan(int B) const {
     const int N = d_.n_nodes;
-    const size_t BN = size_t(B) * N, BNN = BN * N, P = pairs_of(N);
+    const size_t BN = size_t(B) * N;
+    std::vector<std::pair<size_t, size_t>> g;
     size_t o = 0;
-    o = reveal_layout(bw_, BN * d_.feat, o).end;
-    o = reveal_layout(bw_, BNN, o).end;
-    o = reveal_layout(bw_, BN, o).end;
-    o = reveal_layout(bw_, BN, o).end;
-    o = lut8_layout(bw_, BN, o).end;
-    o = mul_layout(bw_, BN, BN, size_t(B) * P, o).end;
-    o = tr_layout(G_TRSLACK, bw_, s_, size_t(B) * P, o).end;
-    o = mul_layout(bw_, BNN, size_t(B) * P, BNN, o).end;
+    auto push = [&](size_t end) {
+      g.emplace_back(o, end);
+      o = end;
+    };
+    push(reveal_layout(bw_, BN * d_.feat, o).end);
+    push(reveal_layout(bw_, BN, o).end);
+    {  // adjacency block: six gates
+      const size_t BNN = BN * N, BP = size_t(B) * pairs_of(N);
+      push(reveal_layout(bw_, BNN, o).end);
+      push(reveal_layout(bw_, BN, o).end);
+      push(lut8_layout(bw_, BN, o).end);
+      push(mul_layout(bw_, BN, BN, BP, o).end);
+      push(tr_layout(G_TRSLACK, bw_, s_, BP, o).end);
+      push(mul_layout(bw_, BNN, BP, BNN, o).end);
+    }
     for (int l = 0; l < 3; l++) {
       size_t E = BN * d_.gcn[l];
-      o = tr_layout(G_TR, bw_, s_, E, o).end;
-      o = sxs_layout(bw_, B, N, N, d_.gcn[l], o).end;
-      o = tr_layout(G_TRRELU, bw_, s_, E, o).end;
+      push(tr_layout(G_TR, bw_, s_, E, o).end);
+      push(sxs_layout(bw_, B, N, N, d_.gcn[l], o).end);
+      push(tr_layout(G_TRRELU, bw_, s_, E, o).end);
     }
     int pairs[32];
     int Lv = pool_levels(N, pairs);
-    for (int l = 0; l < Lv; l++) o = tr_layout(G_RELU, bw_, s_, size_t(B) * pairs[l] * d_.gcn[2], o).end;
-    o = tr_layout(G_TRRELU, bw_, s_, size_t(B) * d_.dfc[0], o).end;
-    o = tr_layout(G_TR, bw_, s_, size_t(B) * d_.dfc[1], o).end;
-    for (int k = 0; k < d_.nfus - 1; k++) o = tr_layout(G_TRRELU, bw_, s_, size_t(B) * d_.fus[k], o).end;
-    o = reveal_layout(bw_, size_t(B) * d_.fus[d_.nfus - 1], o).end;
-    return o;
+    for (int l = 0; l < Lv; l++) push(tr_layout(G_RELU, bw_, s_, size_t(B) * pairs[l] * d_.gcn[2], o).end);
+    push(tr_layout(G_TRRELU, bw_, s_, size_t(B) * d_.dfc[0], o).end);
+    push(tr_layout(G_TR, bw_, s_, size_t(B) * d_.dfc[1], o).end);
+    for (int k = 0; k < d_.nfus - 1; k++) push(tr_layout(G_TRRELU, bw_, s_, size_t(B) * d_.fus[k], o).end);
+    push(reveal_layout(bw_, size_t(B) * d_.fus[d_.nfus - 1], o).end);
+    return g;
   }
+
+  size_t key_bytes(int B) const override { return plan(B).back().second; }
 
   uint8_t *arena(int party) override { return arena_[party]; }
 
-  hipError_t ensure_arena(int B) {
-    size_t need = key_bytes(B);
-    if (need <= arena_bytes_) return hipSuccess;
+  void free_arena() {
     for (int p = 0; p < 2; p++) {
       if (arena_[p]) (void)hipFree(arena_[p]);
       arena_[p] = nullptr;
     }
     arena_bytes_ = 0;
+  }
+  hipError_t release_arena() override {
+    TRY(hipStreamSynchronize(L_.stream));
+    free_arena();
+    if (!streaming_) keyed_B_ = -1;
+    return hipSuccess;
+  }
+
+  hipError_t ensure_arena(int B) {
+    size_t need = key_bytes(B);
+    if (need <= arena_bytes_) return hipSuccess;
+    free_arena();
     for (int p = 0; p < 2; p++) TRY(hipMalloc((void **)&arena_[p], need));
     arena_bytes_ = need;
     return hipSuccess;
@@ -185,87 +589,37 @@ class Model final : public ModelBase {
   hipError_t ensure_work(int B) {
     if (B == work_B_) return hipSuccess;
     const int N = d_.n_nodes;
-    const size_t E = emax(B), BN = size_t(B) * N, BNN = BN * N, BP = size_t(B) * pairs_of(N);
-    for (auto *b : {&bA_, &bB_, &bC_, &msg0_, &msg1_}) TRY(b->alloc(E));
-    for (auto *b : {&ba0_, &ba1_, &bb0_, &bb1_}) TRY(b->alloc((E + 63) / 64));
+    const size_t E = emax(B), BN = size_t(B) * N, BNN = BN * N;
+    for (auto *b : {&bA_, &bB_, &bC_}) TRY(b->alloc(E));
+    TRY(ws_.ensure(E));
     TRY(Ah_.alloc(BNN));
     TRY(An_.alloc(BNN));
     TRY(mh_.alloc(BN));
-    TRY(dh_.alloc(BN));
-    TRY(inv_.alloc(BN));
-    TRY(vh_.alloc(BN));
-    TRY(Ph_.alloc(BP));
-    TRY(Wh_.alloc(BP));
     TRY(V0_.alloc(BN * d_.gcn[2]));
     TRY(V1_.alloc(BN * d_.gcn[2]));
     TRY(out_.alloc(B));
-    // index maps of the adjacency normalisation (outer product, A (.) W)
-    const size_t P = pairs_of(N);
-    std::vector<uint32_t> oa(B * P), ob(B * P), wa(BNN), wb(BNN);
-    for (int b = 0; b < B; b++) {
-      size_t q = size_t(b) * P;
-      for (int i = 0; i < N; i++)
-        for (int j = i; j < N; j++) {
-          oa[q] = uint32_t(b * N + i);
-          ob[q] = uint32_t(b * N + j);
-          q++;
-        }
-      for (int i = 0; i < N; i++)
-        for (int j = 0; j < N; j++) {
-          size_t e = (size_t(b) * N + i) * N + j;
-          wa[e] = uint32_t(e);
-          wb[e] = uint32_t(size_t(b) * P + (i <= j ? pidx(N, i, j) : pidx(N, j, i)));
-        }
-    }
-    TRY(oa_.alloc(oa.size()));
-    TRY(ob_.alloc(ob.size()));
-    TRY(wa_.alloc(wa.size()));
-    TRY(wb_.alloc(wb.size()));
-    TRY(hipMemcpy(oa_.p, oa.data(), oa.size() * 4, hipMemcpyHostToDevice));
-    TRY(hipMemcpy(ob_.p, ob.data(), ob.size() * 4, hipMemcpyHostToDevice));
-    TRY(hipMemcpy(wa_.p, wa.data(), wa.size() * 4, hipMemcpyHostToDevice));
-    TRY(hipMemcpy(wb_.p, wb.data(), wb.size() * 4, hipMemcpyHostToDevice));
+    TRY(adj_.prepare(B, N, s_, d_.lut_nmax));
     work_B_ = B;
     return hipSuccess;
   }
 
   // ---------------- dealer ----------------
   hipError_t keygen(int B, uint64_t seed) override {
+    if (streaming_) return hipErrorInvalidValue;
     TRY(ensure_arena(B));
     TRY(ensure_work(B));
-    const int N = d_.n_nodes, bw = bw_, s = s_;
-    const size_t BN = size_t(B) * N, BNN = BN * N, P = pairs_of(N), BP = size_t(B) * P;
+    const int N = d_.n_nodes, bw = bw_;
+    const size_t BN = size_t(B) * N, BNN = BN * N;
     const size_t E = emax(B);
-    uint8_t *K0 = arena_[0], *K1 = arena_[1];
-    DevBuf<T> rX, t1, t2, rA, rN, rm, rd, rinv, rP, rW, sa0, sb0, gt;
+    DevBuf<T> rX, t1, t2, rA, rN, rm, gt;
     TRY(rX.alloc(E));
     TRY(t1.alloc(E));
     TRY(t2.alloc(E));
     TRY(rA.alloc(BNN));
     TRY(rN.alloc(BNN));
     TRY(rm.alloc(BN));
-    TRY(rd.alloc(BN));
-    TRY(rinv.alloc(BN));
-    TRY(rP.alloc(BP));
-    TRY(rW.alloc(BP));
-    TRY(sa0.alloc(BNN));
-    TRY(sb0.alloc(E));
     TRY(gt.alloc(E));
-    Cursor c;
-    auto reveal = [&](size_t n, T *mask) -> hipError_t {
-      RevealLayout lay = reveal_layout(bw, n, c.off);
-      TRY(launch_reveal_keygen<T>(L_, lay, seed, c.gate, mask, K0, K1));
-      c.off = lay.end;
-      c.gate++;
-      return hipSuccess;
-    };
-    auto tr = [&](int kind, size_t n, const T *in, T *out) -> hipError_t {
-      TrLayout lay = tr_layout(kind, bw, s, n, c.off);
-      TRY(launch_tr_keygen<T>(L_, lay, seed, c.gate, in, out, K0, K1));
-      c.off = lay.end;
-      c.gate++;
-      return hipSuccess;
-    };
+    Dealer<T> d{L_, bw_, s_, seed, arena_[0], arena_[1], Cursor{}};
     auto pub_gemm = [&](const T *x, int l, size_t rows, T *y) -> hipError_t {
       int in, out;
       layer_io(l, &in, &out);
@@ -279,67 +633,17 @@ class Model final : public ModelBase {
       return launch_gemm<T>(L_, g);
     };
 
-    TRY(reveal(BN * d_.feat, rX.p));
-    TRY(reveal(BNN, rA.p));
-    TRY(reveal(BN, rm.p));
-    TRY(reveal(BN, rd.p));
-    {
-      Lut8Layout lay = lut8_layout(bw, BN, c.off);
-      TRY(launch_lut8_keygen<T>(L_, lay, seed, c.gate, rd.p, rinv.p, K0, K1));
-      c.off = lay.end;
-      c.gate++;
-    }
-    {
-      MulLayout lay = mul_layout(bw, BN, BN, BP, c.off);
-      TRY(launch_mul_keygen<T>(L_, lay, seed, c.gate, oa_.p, ob_.p, rinv.p, rinv.p, rP.p, K0, K1));
-      c.off = lay.end;
-      c.gate++;
-    }
-    TRY(tr(G_TRSLACK, BP, rP.p, rW.p));
-    {
-      MulLayout lay = mul_layout(bw, BNN, BP, BNN, c.off);
-      TRY(launch_mul_keygen<T>(L_, lay, seed, c.gate, wa_.p, wb_.p, rA.p, rW.p, rN.p, K0, K1));
-      c.off = lay.end;
-      c.gate++;
-    }
+    TRY(d.reveal(BN * d_.feat, rX.p));
+    TRY(d.reveal(BN, rm.p));
+    TRY(adj_.keygen(d, rA.p, rN.p));
     // GCN stack; rX holds the running activation mask
     for (int l = 0; l < 3; l++) {
       const int fo = d_.gcn[l];
       const size_t En = BN * fo;
       TRY(pub_gemm(rX.p, l, BN, t1.p));
-      TRY(tr(G_TR, En, t1.p, t2.p));
-      {  // SxS: C = rA.rB - RA0.RB0 + rC
-        SxsLayout lay = sxs_layout(bw, B, N, N, fo, c.off);
-        T *RA0 = reinterpret_cast<T *>(K0 + lay.off_ra), *RA1 = reinterpret_cast<T *>(K1 + lay.off_ra);
-        T *RB0 = reinterpret_cast<T *>(K0 + lay.off_rb), *RB1 = reinterpret_cast<T *>(K1 + lay.off_rb);
-        TRY(launch_split<T>(L_, seed, c.gate, F_SPLIT + 0, BNN, rN.p, RA0, RA1, nullptr));
-        TRY(launch_split<T>(L_, seed, c.gate, F_SPLIT + 1, En, t2.p, RB0, RB1, nullptr));
-        TRY(launch_prf_ring<T>(L_, seed, c.gate, F_ROUT, En, t1.p));  // rC (output mask)
-        GemmArgs<T> g;
-        g.M = N;
-        g.K = N;
-        g.N = fo;
-        g.batch = B;
-        g.sA = size_t(N) * N;
-        g.sB = size_t(N) * fo;
-        g.sC = size_t(N) * fo;
-        g.A1 = rN.p;
-        g.B1 = t2.p;
-        g.Cin = t1.p;
-        g.C = gt.p;
-        TRY(launch_gemm<T>(L_, g));  // rA.rB + rC
-        g.A1 = RA0;
-        g.B1 = RB0;
-        g.Cin = gt.p;
-        g.C = gt.p;
-        g.sign = -1;
-        TRY(launch_gemm<T>(L_, g));  // - RA0.RB0
-        TRY(launch_split<T>(L_, seed, c.gate, F_SPLIT + 2, En, gt.p, reinterpret_cast<T *>(K0 + lay.off_c),
-                            reinterpret_cast<T *>(K1 + lay.off_c), nullptr));
-        c.off = lay.end;
-        c.gate++;
-      }
-      TRY(tr(G_TRRELU, En, t1.p, rX.p));
+      TRY(d.tr(G_TR, En, t1.p, t2.p));
+      TRY(d.sxs(B, N, N, fo, rN.p, t2.p, t1.p, gt.p));
+      TRY(d.tr(G_TRRELU, En, t1.p, rX.p));
     }
     // pool
     const int C = d_.gcn[2];
@@ -353,38 +657,35 @@ class Model final : public ModelBase {
       const int pr = pairs[l];
       const size_t En = size_t(B) * pr * C;
       TRY(launch_pool_diff<T>(L_, B, R, C, cur, t1.p));
-      TRY(tr(G_RELU, En, t1.p, gt.p));
+      TRY(d.tr(G_RELU, En, t1.p, gt.p));
       TRY(launch_pool_combine<T>(L_, B, R, C, cur, gt.p, nullptr, nxt));
       std::swap(cur, nxt);
       R = pr + (R & 1);
     }
     // drug FCs
     TRY(pub_gemm(cur, 3, B, t1.p));
-    TRY(tr(G_TRRELU, size_t(B) * d_.dfc[0], t1.p, gt.p));
+    TRY(d.tr(G_TRRELU, size_t(B) * d_.dfc[0], t1.p, gt.p));
     TRY(pub_gemm(gt.p, 4, B, t1.p));
-    TRY(tr(G_TR, size_t(B) * d_.dfc[1], t1.p, gt.p));
+    TRY(d.tr(G_TR, size_t(B) * d_.dfc[1], t1.p, gt.p));
     TRY(launch_concat<T>(L_, B, d_.dfc[1], d_.prot, gt.p, nullptr, nxt));
     T *h = nxt, *h2 = cur;
     for (int k = 0; k < d_.nfus; k++) {
       TRY(pub_gemm(h, 5 + k, B, t1.p));
       if (k < d_.nfus - 1) {
-        TRY(tr(G_TRRELU, size_t(B) * d_.fus[k], t1.p, h2));
+        TRY(d.tr(G_TRRELU, size_t(B) * d_.fus[k], t1.p, h2));
         std::swap(h, h2);
       } else {
-        RevealLayout lay = reveal_layout(bw, size_t(B) * d_.fus[k], c.off);
-        TRY(hipMemcpyAsync(K0 + lay.off_r, t1.p, lay.N * sizeof(T), hipMemcpyDeviceToDevice, L_.stream));
-        TRY(hipMemcpyAsync(K1 + lay.off_r, t1.p, lay.N * sizeof(T), hipMemcpyDeviceToDevice, L_.stream));
-        c.off = lay.end;
-        c.gate++;
+        TRY(d.output(size_t(B) * d_.fus[k], t1.p));
       }
     }
+    if (d.c.off != key_bytes(B)) return hipErrorUnknown;  // plan and dealer disagree
     TRY(hipStreamSynchronize(L_.stream));
     keyed_B_ = B;
     return hipSuccess;
   }
 
   hipError_t import_keys(int B, const void *k0, const void *k1, size_t bytes) override {
-    if (bytes != key_bytes(B)) return hipErrorInvalidValue;
+    if (streaming_ || bytes != key_bytes(B)) return hipErrorInvalidValue;
     TRY(ensure_arena(B));
     TRY(hipMemcpy(arena_[0], k0, bytes, hipMemcpyHostToDevice));
     TRY(hipMemcpy(arena_[1], k1, bytes, hipMemcpyHostToDevice));
@@ -393,9 +694,94 @@ class Model final : public ModelBase {
   }
   hipError_t export_keys(int party, void *dst, size_t bytes) override {
     if (!arena_[party] || bytes > arena_bytes_) return hipErrorInvalidValue;
+    TRY(hipStreamSynchronize(L_.stream));
     return hipMemcpy(dst, arena_[party], bytes, hipMemcpyDeviceToHost);
   }
 
+  // ---------------- streaming ----------------
+  void free_stream() {
+    for (int k = 0; k < 2; k++) {
+      for (int p = 0; p < 2; p++) {
+        if (slot_[k][p]) (void)hipFree(slot_[k][p]);
+        slot_[k][p] = nullptr;
+      }
+      if (ready_[k]) (void)hipEventDestroy(ready_[k]);
+      if (free_[k]) (void)hipEventDestroy(free_[k]);
+      ready_[k] = free_[k] = nullptr;
+    }
+    if (cs_) (void)hipStreamDestroy(cs_);
+    cs_ = nullptr;
+    streaming_ = false;
+  }
+
+  hipError_t attach_host_keys(int B, const void *h0, const void *h1, size_t bytes, size_t slot_bytes) override {
+    if (!h0 || !h1 || bytes != key_bytes(B) || slot_bytes == 0) return hipErrorInvalidValue;
+    TRY(hipStreamSynchronize(L_.stream));
+    free_stream();
+    free_arena();  // the two slots replace the resident arena
+    gates_ = plan(B);
+    // chunks: maximal runs of consecutive gates that fit in one slot
+    chunks_.clear();
+    chunk_of_.assign(gates_.size(), 0);
+    for (size_t i = 0; i < gates_.size(); i++) {
+      const size_t gb = gates_[i].first, ge = gates_[i].second;
+      if (ge - gb > slot_bytes) return hipErrorInvalidValue;  // a gate larger than a slot
+      if (chunks_.empty() || ge - chunks_.back().first > slot_bytes) chunks_.emplace_back(gb, ge);
+      chunks_.back().second = ge;
+      chunk_of_[i] = int(chunks_.size()) - 1;
+    }
+    size_t need = 0;
+    for (auto &c : chunks_) need = std::max(need, c.second - c.first);
+    for (int k = 0; k < 2; k++) {
+      for (int p = 0; p < 2; p++) TRY(hipMalloc((void **)&slot_[k][p], need));
+      TRY(hipEventCreateWithFlags(&ready_[k], hipEventDisableTiming));
+      TRY(hipEventCreateWithFlags(&free_[k], hipEventDisableTiming));
+    }
+    TRY(hipStreamCreateWithFlags(&cs_, hipStreamNonBlocking));
+    host_[0] = static_cast<const uint8_t *>(h0);
+    host_[1] = static_cast<const uint8_t *>(h1);
+    streaming_ = true;
+    keyed_B_ = B;
+    return hipSuccess;
+  }
+
+  // copy chunk k into slot k % 2 once the slot's previous chunk has been consumed
+  hipError_t issue_copy(int k) {
+    const int sl = k & 1;
+    const size_t b = chunks_[k].first, len = chunks_[k].second - chunks_[k].first;
+    TRY(hipStreamWaitEvent(cs_, free_[sl], 0));
+    for (int p = 0; p < 2; p++) TRY(hipMemcpyAsync(slot_[sl][p], host_[p] + b, len, hipMemcpyHostToDevice, cs_));
+    TRY(hipEventRecord(ready_[sl], cs_));
+    stream_stats.bytes_h2d += 2 * len;
+    return hipSuccess;
+  }
+
+  hipError_t acquire(size_t begin, size_t end, KeyView *kv) override {
+    if (gi_ >= gates_.size() || gates_[gi_].first != begin || gates_[gi_].second != end)
+      return hipErrorUnknown;  // forward walked off the plan
+    const int k = chunk_of_[gi_++];
+    if (!streaming_) {
+      kv->k[0] = arena_[0];
+      kv->k[1] = arena_[1];
+      kv->begin = 0;
+      return hipSuccess;
+    }
+    if (k != cur_chunk_) {
+      if (k > 0) {  // chunk k-1's kernels are all enqueued: its slot takes chunk k+1
+        TRY(hipEventRecord(free_[(k - 1) & 1], L_.stream));
+        if (k + 1 < int(chunks_.size())) TRY(issue_copy(k + 1));
+      }
+      TRY(hipStreamWaitEvent(L_.stream, ready_[k & 1], 0));
+      kv->k[0] = slot_[k & 1][0];
+      kv->k[1] = slot_[k & 1][1];
+      kv->begin = chunks_[k].first;
+      cur_chunk_ = k;
+      stream_stats.chunks++;
+    }
+    return hipSuccess;
+  }
+
+  // ---------------- inputs ----------------
   hipError_t set_inputs(int B, const void *x0, const void *x1, const void *a0, const void *a1, const void *m0,
                         const void *m1, const int64_t *prot) override {
     const int N = d_.n_nodes;
@@ -407,6 +793,7 @@ class Model final : public ModelBase {
     TRY(m0_.alloc(BN));
     TRY(m1_.alloc(BN));
     TRY(prot_.alloc(size_t(B) * d_.prot));
+    TRY(hipStreamSynchronize(L_.stream));
     TRY(hipMemcpy(x0_.p, x0, nx * sizeof(T), hipMemcpyHostToDevice));
     TRY(hipMemcpy(x1_.p, x1, nx * sizeof(T), hipMemcpyHostToDevice));
     TRY(hipMemcpy(a0_.p, a0, na * sizeof(T), hipMemcpyHostToDevice));
@@ -421,56 +808,23 @@ class Model final : public ModelBase {
   }
 
   // ---------------- online ----------------
-  hipError_t tr_eval(Cursor &c, int kind, size_t n, const T *x, const T *bias, int ncol, T *out) {
-    TrLayout lay = tr_layout(kind, bw_, s_, n, c.off);
-    const uint8_t *K0 = arena_[0], *K1 = arena_[1];
-    hipEvent_t e0 = nullptr, e1 = nullptr;
-    if (timer.on) {
-      TRY(hipEventCreate(&e0));
-      TRY(hipEventCreate(&e1));
-      TRY(hipEventRecord(e0, L_.stream));
-    }
-    TRY(launch_tr_phase1<T>(L_, lay, K0, K1, x, bias, ncol, ba0_.p, ba1_.p, bb0_.p, bb1_.p));
-    if (timer.on) {
-      TRY(hipEventRecord(e1, L_.stream));
-      timer.ev.push_back(e0);
-      timer.ev.push_back(e1);
-      timer.elems.push_back(n);
-      timer.levels.push_back((lay.use_a ? lay.a.L + 1 : 0) + (lay.use_b ? lay.b.L + 1 : 0));
-      // per element and party: the masked input, and for every DCF the root,
-      // correction words and leaf (16 B each), the output-mask bit read and the
-      // message bit written (the bias vector is ncol words, cache resident)
-      double per = double(sizeof(T));
-      if (lay.use_a) per += 16.0 * (lay.a.L + 2) + 0.125 + 0.125;
-      if (lay.use_b) per += 16.0 * (lay.b.L + 2) + 0.125 + 0.125;
-      timer.bytes.push_back(2.0 * per * double(n));
-    }
-    counters.bitplanes(n, int(lay.use_a) + int(lay.use_b));
-    TRY(launch_tr_phase2<T>(L_, lay, K0, K1, x, bias, ncol, ba0_.p, ba1_.p, bb0_.p, bb1_.p, msg0_.p, msg1_.p));
-    counters.msg(n, bw_);
-    TRY(launch_reconstruct<T>(L_, n, msg0_.p, msg1_.p, out));
-    c.off = lay.end;
-    c.gate++;
-    return hipSuccess;
-  }
-
   hipError_t forward(int B) override {
     if (keyed_B_ != B || input_B_ != B) return hipErrorInvalidValue;
     TRY(ensure_work(B));
     const int N = d_.n_nodes, bw = bw_;
-    const size_t BN = size_t(B) * N, BNN = BN * N, P = pairs_of(N), BP = size_t(B) * P;
-    const uint8_t *K0 = arena_[0], *K1 = arena_[1];
-    T *m0 = msg0_.p, *m1 = msg1_.p;
-    Cursor c;
-    auto reveal = [&](size_t n, const T *v0, const T *v1, int rowlen, T *out) -> hipError_t {
-      RevealLayout lay = reveal_layout(bw, n, c.off);
-      TRY(launch_reveal_eval<T>(L_, lay, K0, K1, v0, v1, rowlen, m0, m1));
-      counters.msg(n, bw);
-      TRY(launch_reconstruct<T>(L_, n, m0, m1, out));
-      c.off = lay.end;
-      c.gate++;
-      return hipSuccess;
-    };
+    const size_t BN = size_t(B) * N;
+    if (!streaming_) {
+      gates_ = plan(B);
+      chunk_of_.assign(gates_.size(), 0);
+    }
+    gi_ = 0;
+    cur_chunk_ = -1;
+    stream_stats = StreamStats();
+    if (streaming_) {
+      TRY(issue_copy(0));
+      if (chunks_.size() > 1) TRY(issue_copy(1));
+    }
+    Runner<T> r(L_, bw_, s_, ws_, counters, &timer, *this);
     auto pub_gemm = [&](const T *x, int l, size_t rows, T *y) -> hipError_t {
       int in, out;
       layer_io(l, &in, &out);
@@ -485,80 +839,16 @@ class Model final : public ModelBase {
     };
     T *H = bA_.p, *Z = bB_.p, *XW = bC_.p;
 
-    TRY(reveal(BN * d_.feat, x0_.p, x1_.p, 0, H));
-    TRY(reveal(BNN, a0_.p, a1_.p, 0, Ah_.p));
-    TRY(reveal(BN, m0_.p, m1_.p, 0, mh_.p));
-    TRY(reveal(BN, a0_.p, a1_.p, N, dh_.p));  // degree = row sums of the A shares
-    {
-      Lut8Layout lay = lut8_layout(bw, BN, c.off);
-      TRY(launch_lut8_phase1<T>(L_, lay, K0, K1, table_.p, dh_.p, m0, m1));
-      counters.msg(BN, bw);
-      TRY(launch_reconstruct<T>(L_, BN, m0, m1, vh_.p));
-      TRY(launch_lut8_phase2<T>(L_, lay, K0, K1, vh_.p, m0, m1));
-      counters.msg(BN, bw);
-      TRY(launch_reconstruct<T>(L_, BN, m0, m1, inv_.p));
-      c.off = lay.end;
-      c.gate++;
-    }
-    {
-      MulLayout lay = mul_layout(bw, BN, BN, BP, c.off);
-      TRY(launch_mul_eval<T>(L_, lay, K0, K1, oa_.p, ob_.p, inv_.p, inv_.p, m0, m1));
-      counters.msg(BP, bw);
-      TRY(launch_reconstruct<T>(L_, BP, m0, m1, Ph_.p));
-      c.off = lay.end;
-      c.gate++;
-    }
-    TRY(tr_eval(c, G_TRSLACK, BP, Ph_.p, nullptr, 1, Wh_.p));
-    {
-      MulLayout lay = mul_layout(bw, BNN, BP, BNN, c.off);
-      TRY(launch_mul_eval<T>(L_, lay, K0, K1, wa_.p, wb_.p, Ah_.p, Wh_.p, m0, m1));
-      counters.msg(BNN, bw);
-      TRY(launch_reconstruct<T>(L_, BNN, m0, m1, An_.p));
-      c.off = lay.end;
-      c.gate++;
-    }
+    TRY(r.reveal(BN * d_.feat, x0_.p, x1_.p, 0, H));
+    TRY(r.reveal(BN, m0_.p, m1_.p, 0, mh_.p));
+    TRY(adj_.eval(r, a0_.p, a1_.p, Ah_.p, An_.p));
     for (int l = 0; l < 3; l++) {
       const int fo = d_.gcn[l];
       const size_t En = BN * fo;
       TRY(pub_gemm(H, l, BN, Z));
-      TRY(tr_eval(c, G_TR, En, Z, nullptr, 1, XW));
-      {
-        SxsLayout lay = sxs_layout(bw, B, N, N, fo, c.off);
-        GemmArgs<T> g;
-        g.M = N;
-        g.K = N;
-        g.N = fo;
-        g.batch = B;
-        g.sA = size_t(N) * N;
-        g.sB = size_t(N) * fo;
-        g.sC = size_t(N) * fo;
-        // party 0: (A^ - RA0)(B^ - RB0) + C0
-        g.A1 = An_.p;
-        g.A2 = reinterpret_cast<const T *>(K0 + lay.off_ra);
-        g.B1 = XW;
-        g.B2 = reinterpret_cast<const T *>(K0 + lay.off_rb);
-        g.Cin = reinterpret_cast<const T *>(K0 + lay.off_c);
-        g.C = m0;
-        TRY(launch_gemm<T>(L_, g));
-        // party 1: C1 - A^ RB1 - RA1 B^
-        GemmArgs<T> h = g;
-        h.A2 = nullptr;
-        h.B2 = nullptr;
-        h.B1 = reinterpret_cast<const T *>(K1 + lay.off_rb);
-        h.Cin = reinterpret_cast<const T *>(K1 + lay.off_c);
-        h.C = m1;
-        h.sign = -1;
-        TRY(launch_gemm<T>(L_, h));
-        h.A1 = reinterpret_cast<const T *>(K1 + lay.off_ra);
-        h.B1 = XW;
-        h.Cin = m1;
-        TRY(launch_gemm<T>(L_, h));
-        counters.msg(En, bw);
-        TRY(launch_reconstruct<T>(L_, En, m0, m1, Z));
-        c.off = lay.end;
-        c.gate++;
-      }
-      TRY(tr_eval(c, G_TRRELU, En, Z, bias_[l].p, fo, H));
+      TRY(r.tr(G_TR, En, Z, nullptr, 1, XW));
+      TRY(r.sxs(B, N, N, fo, An_.p, XW, Z));
+      TRY(r.tr(G_TRRELU, En, Z, bias_[l].p, fo, H));
     }
     // masked max-pool: V = H + S*m^ - S, then a tree of max(a,b) = a + ReLU(b-a)
     const int C = d_.gcn[2];
@@ -572,16 +862,16 @@ class Model final : public ModelBase {
       const int pr = pairs[l];
       const size_t En = size_t(B) * pr * C;
       TRY(launch_pool_diff<T>(L_, B, R, C, cur, Z));
-      TRY(tr_eval(c, G_RELU, En, Z, nullptr, 1, XW));
+      TRY(r.tr(G_RELU, En, Z, nullptr, 1, XW));
       TRY(launch_pool_combine<T>(L_, B, R, C, cur, XW, nullptr, nxt));
       std::swap(cur, nxt);
       R = pr + (R & 1);
     }
     // drug FCs
     TRY(pub_gemm(cur, 3, B, Z));
-    TRY(tr_eval(c, G_TRRELU, size_t(B) * d_.dfc[0], Z, bias_[3].p, d_.dfc[0], XW));
+    TRY(r.tr(G_TRRELU, size_t(B) * d_.dfc[0], Z, bias_[3].p, d_.dfc[0], XW));
     TRY(pub_gemm(XW, 4, B, Z));
-    TRY(tr_eval(c, G_TR, size_t(B) * d_.dfc[1], Z, bias_[4].p, d_.dfc[1], XW));
+    TRY(r.tr(G_TR, size_t(B) * d_.dfc[1], Z, bias_[4].p, d_.dfc[1], XW));
     // concat [drug, protein]; the protein embedding owner reveals it (one message)
     counters.msg(size_t(B) * d_.prot, bw);
     TRY(launch_concat<T>(L_, B, d_.dfc[1], d_.prot, XW, prot_.p, H));
@@ -589,16 +879,15 @@ class Model final : public ModelBase {
     for (int k = 0; k < d_.nfus; k++) {
       TRY(pub_gemm(h, 5 + k, B, Z));
       if (k < d_.nfus - 1) {
-        TRY(tr_eval(c, G_TRRELU, size_t(B) * d_.fus[k], Z, bias_[5 + k].p, d_.fus[k], h2));
+        TRY(r.tr(G_TRRELU, size_t(B) * d_.fus[k], Z, bias_[5 + k].p, d_.fus[k], h2));
         std::swap(h, h2);
       } else {
-        RevealLayout lay = reveal_layout(bw, size_t(B) * d_.fus[k], c.off);
-        TRY(launch_output<T>(L_, B, bw, s_, Z, reinterpret_cast<const T *>(K0 + lay.off_r), hbias_[5 + k][0],
-                             out_.p));
-        c.off = lay.end;
-        c.gate++;
+        TRY(r.output(B, size_t(B) * d_.fus[k], Z, hbias_[5 + k][0], out_.p));
       }
     }
+    if (gi_ != gates_.size()) return hipErrorUnknown;
+    if (streaming_)  // both slots are free once this forward's kernels have run
+      for (int k = 0; k < 2; k++) TRY(hipEventRecord(free_[k], L_.stream));
     return hipGetLastError();
   }
 
@@ -613,16 +902,42 @@ class Model final : public ModelBase {
   Launch L_;
   std::vector<DevBuf<T>> wt_, bias_;
   std::vector<std::vector<int64_t>> hbias_;
-  DevBuf<T> table_;
   uint8_t *arena_[2] = {nullptr, nullptr};
   size_t arena_bytes_ = 0;
   int keyed_B_ = -1, input_B_ = -1, work_B_ = -1;
   DevBuf<T> x0_, x1_, a0_, a1_, m0_, m1_, prot_;
-  DevBuf<T> bA_, bB_, bC_, msg0_, msg1_, Ah_, An_, mh_, dh_, inv_, vh_, Ph_, Wh_, V0_, V1_;
-  DevBuf<uint64_t> ba0_, ba1_, bb0_, bb1_;
-  DevBuf<uint32_t> oa_, ob_, wa_, wb_;
+  DevBuf<T> bA_, bB_, bC_, Ah_, An_, mh_, V0_, V1_;
   DevBuf<int64_t> out_;
+  Workspace<T> ws_;
+  AdjNorm<T> adj_;
+  // gate plan and streaming state
+  std::vector<std::pair<size_t, size_t>> gates_, chunks_;
+  std::vector<int> chunk_of_;
+  size_t gi_ = 0;
+  int cur_chunk_ = -1;
+  bool streaming_ = false;
+  const uint8_t *host_[2] = {nullptr, nullptr};
+  uint8_t *slot_[2][2] = {{nullptr, nullptr}, {nullptr, nullptr}};
+  hipEvent_t ready_[2] = {nullptr, nullptr}, free_[2] = {nullptr, nullptr};
+  hipStream_t cs_ = nullptr;
 };
+
+template <typename T>
+static ModelBase *make_model_t(int bw, int s, const ModelDims &d, const int64_t *W, size_t nW, const Launch &L,
+                               std::string *err) {
+  auto *mm = new Model<T>(bw, s, d, L);
+  if (nW != mm->weights_len()) {
+    *err = "weight blob length mismatch";
+    delete mm;
+    return nullptr;
+  }
+  if (mm->set_weights(W) != hipSuccess) {
+    *err = "weight upload failed";
+    delete mm;
+    return nullptr;
+  }
+  return mm;
+}
 
 ModelBase *make_model(int bw, int s, const ModelDims &d, const int64_t *W, size_t nW, const Launch &L,
                       std::string *err) {
@@ -634,37 +949,59 @@ ModelBase *make_model(int bw, int s, const ModelDims &d, const int64_t *W, size_
     *err = "n_nodes must be in [1, 255] (8-bit degree LUT domain)";
     return nullptr;
   }
-  ModelBase *m = nullptr;
-  if (bw == 32) {
-    auto *mm = new Model<uint32_t>(bw, s, d, L);
-    if (nW != mm->weights_len()) {
-      *err = "weight blob length mismatch";
-      delete mm;
-      return nullptr;
-    }
-    if (mm->set_weights(W) != hipSuccess) {
-      *err = "weight upload failed";
-      delete mm;
-      return nullptr;
-    }
-    m = mm;
-  } else if (bw == 64) {
-    auto *mm = new Model<uint64_t>(bw, s, d, L);
-    if (nW != mm->weights_len()) {
-      *err = "weight blob length mismatch";
-      delete mm;
-      return nullptr;
-    }
-    if (mm->set_weights(W) != hipSuccess) {
-      *err = "weight upload failed";
-      delete mm;
-      return nullptr;
-    }
-    m = mm;
-  } else {
-    *err = "bw must be 32 or 64";
-  }
-  return m;
+  if (bw == 32) return make_model_t<uint32_t>(bw, s, d, W, nW, L, err);
+  if (bw == 64) return make_model_t<uint64_t>(bw, s, d, W, nW, L, err);
+  *err = "bw must be 32 or 64";
+  return nullptr;
+}
+
+// ===========================================================================
+// standalone secure adjacency normalisation
+// ===========================================================================
+size_t adjnorm_key_bytes(int bw, int s, int B, int N) { return AdjNorm<uint32_t>::layout_end(bw, s, B, N, 0); }
+
+template <typename T>
+static hipError_t adjnorm_keygen_t(int bw, int s, int B, int N, uint64_t seed, const Launch &L, void *out_mask,
+                                   uint8_t *k0, uint8_t *k1) {
+  AdjNorm<T> adj;
+  TRY(adj.prepare(B, N, s, 0));
+  DevBuf<T> rA;
+  TRY(rA.alloc(size_t(B) * N * N));
+  Dealer<T> d{L, bw, s, seed, k0, k1, Cursor{}};
+  TRY(adj.keygen(d, rA.p, static_cast<T *>(out_mask)));
+  return hipStreamSynchronize(L.stream);
+}
+
+hipError_t adjnorm_keygen(int bw, int s, int B, int N, uint64_t seed, const Launch &L, void *out_mask, uint8_t *k0,
+                          uint8_t *k1) {
+  return bw == 32 ? adjnorm_keygen_t<uint32_t>(bw, s, B, N, seed, L, out_mask, k0, k1)
+                  : adjnorm_keygen_t<uint64_t>(bw, s, B, N, seed, L, out_mask, k0, k1);
+}
+
+template <typename T>
+static hipError_t adjnorm_eval_t(int bw, int s, int B, int N, int nmax, const Launch &L, const uint8_t *k0,
+                                 const uint8_t *k1, const void *a0, const void *a1, void *out, Counters *ctr) {
+  AdjNorm<T> adj;
+  TRY(adj.prepare(B, N, s, nmax));
+  const size_t BNN = size_t(B) * N * N;
+  DevBuf<T> Ah;
+  TRY(Ah.alloc(BNN));
+  Workspace<T> ws;
+  TRY(ws.ensure(std::max(BNN, size_t(B) * pairs_of(N))));
+  ArenaSource src;
+  src.k[0] = k0;
+  src.k[1] = k1;
+  src.bytes = AdjNorm<T>::layout_end(bw, s, B, N, 0);
+  Counters local;
+  Runner<T> r(L, bw, s, ws, ctr ? *ctr : local, nullptr, src);
+  TRY(adj.eval(r, static_cast<const T *>(a0), static_cast<const T *>(a1), Ah.p, static_cast<T *>(out)));
+  return hipStreamSynchronize(L.stream);
+}
+
+hipError_t adjnorm_eval(int bw, int s, int B, int N, int nmax, const Launch &L, const uint8_t *k0, const uint8_t *k1,
+                        const void *a0, const void *a1, void *out, Counters *ctr) {
+  return bw == 32 ? adjnorm_eval_t<uint32_t>(bw, s, B, N, nmax, L, k0, k1, a0, a1, out, ctr)
+                  : adjnorm_eval_t<uint64_t>(bw, s, B, N, nmax, L, k0, k1, a0, a1, out, ctr);
 }
 
 }  // namespace mpcx

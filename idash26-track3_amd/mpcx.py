@@ -80,6 +80,16 @@ _SIGS = {
     "mpcx_model_forward": (C.c_int, [C.c_void_p, C.c_int]),
     "mpcx_model_output": (C.c_int, [C.c_void_p, C.c_int, C.c_void_p]),
     "mpcx_model_profile": (C.c_int, [C.c_void_p, C.c_int]),
+    "mpcx_model_release_arena": (C.c_int, [C.c_void_p]),
+    "mpcx_model_attach_host_keys": (C.c_int, [C.c_void_p, C.c_int, C.c_void_p, C.c_void_p, C.c_size_t,
+                                              C.c_size_t]),
+    "mpcx_model_stream_stats": (C.c_int, [C.c_void_p, C.c_void_p, C.c_void_p]),
+    "mpcx_adjnorm_key_bytes": (C.c_size_t, [C.c_void_p, C.c_int, C.c_int]),
+    "mpcx_adjnorm_keygen": (C.c_int, [C.c_void_p, C.c_int, C.c_int, C.c_uint64, C.c_void_p, C.c_void_p,
+                                      C.c_void_p]),
+    "mpcx_adjnorm_eval": (C.c_int, [C.c_void_p, C.c_int, C.c_int, C.c_int] + [C.c_void_p] * 5),
+    "mpcx_host_alloc": (C.c_int, [C.c_size_t, C.c_void_p]),
+    "mpcx_host_free": (None, [C.c_void_p]),
     "mpcx_model_profile_read": (C.c_int, [C.c_void_p] + [C.c_void_p] * 5),
 }
 
@@ -338,6 +348,49 @@ class Ctx:
                    "reveal_eval")
         return from_dev(out, self.T, v0.size)
 
+    # ---------------- adjacency normalisation ----------------
+    def adjnorm_keygen(self, B, N, seed=1):
+        nb = self.lib.mpcx_adjnorm_key_bytes(self.h, B, N)
+        k0, k1 = empty_dev(nb), empty_dev(nb)
+        mask = empty_dev(B * N * N * np.dtype(self.T).itemsize)
+        self.check(self.lib.mpcx_adjnorm_keygen(self.h, B, N, seed, dptr(mask), dptr(k0), dptr(k1)), "adjnorm_keygen")
+        return k0, k1, mask
+
+    def adjnorm_eval(self, B, N, nmax, k0, k1, a0, a1, as_device=False):
+        """a0, a1: numpy shares or device tensors; returns masked A_norm."""
+        d0 = a0 if not isinstance(a0, np.ndarray) else to_dev(self.ring(a0))
+        d1 = a1 if not isinstance(a1, np.ndarray) else to_dev(self.ring(a1))
+        out = empty_dev(B * N * N * np.dtype(self.T).itemsize)
+        self.check(self.lib.mpcx_adjnorm_eval(self.h, B, N, nmax, dptr(k0), dptr(k1), dptr(d0), dptr(d1), dptr(out)),
+                   "adjnorm_eval")
+        return out if as_device else from_dev(out, self.T, B * N * N)
+
+
+class PinnedBuffer:
+    """Page-locked host memory from libmpcx (hipHostMalloc), viewed as uint8."""
+
+    def __init__(self, nbytes):
+        self.lib = load()
+        p = C.c_void_p()
+        st = self.lib.mpcx_host_alloc(int(nbytes), C.byref(p))
+        if st != 0:
+            raise MpcxError(f"mpcx_host_alloc({nbytes}) failed ({st})")
+        self.ptr = p
+        self.nbytes = int(nbytes)
+        self.array = np.ctypeslib.as_array((C.c_uint8 * self.nbytes).from_address(p.value))
+
+    def free(self):
+        if self.ptr:
+            self.array = None
+            self.lib.mpcx_host_free(self.ptr)
+            self.ptr = None
+
+    def __del__(self):
+        try:
+            self.free()
+        except Exception:
+            pass
+
 
 def model_dims(d):
     """synth.Dims -> ModelDims"""
@@ -391,12 +444,35 @@ class Model:
         self.ctx.check(self.lib.mpcx_model_import_keys(self.h, B, k0.ctypes.data_as(C.c_void_p),
                                                        k1.ctypes.data_as(C.c_void_p), k0.size), "import_keys")
 
-    def export_keys(self, party, B):
+    def export_keys(self, party, B, into=None):
+        """Copy party's resident key arena to host (a new array, or `into`: a
+        PinnedBuffer or uint8 array of key_bytes(B))."""
         n = self.key_bytes(B)
-        out = np.zeros(n, np.uint8)
-        self.ctx.check(self.lib.mpcx_model_export_keys(self.h, party, out.ctypes.data_as(C.c_void_p), n),
-                       "export_keys")
+        if into is None:
+            out = np.zeros(n, np.uint8)
+            ptr = out.ctypes.data_as(C.c_void_p)
+        else:
+            out = into
+            ptr = into.ptr if isinstance(into, PinnedBuffer) else into.ctypes.data_as(C.c_void_p)
+        self.ctx.check(self.lib.mpcx_model_export_keys(self.h, party, ptr, n), "export_keys")
         return out
+
+    def release_arena(self):
+        self.ctx.check(self.lib.mpcx_model_release_arena(self.h), "release_arena")
+
+    def attach_host_keys(self, B, k0, k1, slot_bytes):
+        """Stream keys from host buffers (PinnedBuffer for overlap) through two
+        device slots of slot_bytes per party."""
+        self._host_keys = (k0, k1)
+        p0 = k0.ptr if isinstance(k0, PinnedBuffer) else k0.ctypes.data_as(C.c_void_p)
+        p1 = k1.ptr if isinstance(k1, PinnedBuffer) else k1.ctypes.data_as(C.c_void_p)
+        self.ctx.check(self.lib.mpcx_model_attach_host_keys(self.h, B, p0, p1, self.key_bytes(B), int(slot_bytes)),
+                       "attach_host_keys")
+
+    def stream_stats(self):
+        ch, by = C.c_int(), C.c_uint64()
+        self.ctx.check(self.lib.mpcx_model_stream_stats(self.h, C.byref(ch), C.byref(by)), "stream_stats")
+        return {"chunks": ch.value, "bytes_h2d": by.value}
 
     def set_inputs(self, B, x0, x1, a0, a1, m0, m1, prot):
         arrs = [self.ctx.ring(v) for v in (x0, x1, a0, a1, m0, m1)]

@@ -161,6 +161,25 @@ mpcx_status mpcx_reveal_keygen(mpcx_ctx *ctx, size_t n, void *d_mask, uint64_t s
 mpcx_status mpcx_reveal_eval(mpcx_ctx *ctx, size_t n, const void *d_key0, const void *d_key1,
                              const void *d_v0, const void *d_v1, void *d_vhat);
 
+/* ---------------- secure adjacency normalisation ----------------
+ * A_norm = D^-1/2 (A) D^-1/2 on secret A, in the fixed-point form of the secure
+ * path: A[i,j] * floor(T[d_i] T[d_j] / 2^s), T[k] = llround(2^s / sqrt(k)) for
+ * 1 <= k <= nmax, T[0] = 0, d = row sums of A (self loops included).  Replaces
+ * ddgSecureAdjNormKeygen / ddgSecureAdjNormEval (gpu_mpc/secure_adj_norm.h:203-374,
+ * 393-659): reveal A, reveal the degrees, 8-bit DPF-LUT, Beaver outer product,
+ * one exact truncation, Beaver A (.) W.  a0, a1: both parties' shares of A
+ * (B x N x N ring elements, N <= 255); out: A_norm + out_mask. */
+size_t mpcx_adjnorm_key_bytes(mpcx_ctx *ctx, int B, int N);
+mpcx_status mpcx_adjnorm_keygen(mpcx_ctx *ctx, int B, int N, uint64_t seed, void *d_out_mask, void *d_key0,
+                                void *d_key1);
+mpcx_status mpcx_adjnorm_eval(mpcx_ctx *ctx, int B, int N, int nmax, const void *d_key0, const void *d_key1,
+                              const void *d_a0, const void *d_a1, void *d_out);
+
+/* ---------------- pinned host memory ----------------
+ * Page-locked host buffers for streamed key arenas (hipHostMalloc). */
+mpcx_status mpcx_host_alloc(size_t bytes, void **out);
+void mpcx_host_free(void *p);
+
 /* ---------------- the model ----------------
  * DeepDTAGenAffinity<T> (gpu_mpc/deepdtagen.h:110-223) with the driver's
  * resident-key evaluation loop (gpu_mpc/deepdtagen_inference.cu:422-607).
@@ -189,6 +208,22 @@ mpcx_status mpcx_model_keygen(mpcx_model *m, int B, uint64_t seed);
 mpcx_status mpcx_model_import_keys(mpcx_model *m, int B, const void *h_key0, const void *h_key1,
                                    size_t bytes);
 mpcx_status mpcx_model_export_keys(mpcx_model *m, int party, void *h_dst, size_t bytes);
+/* Frees the resident key arenas (e.g. after mpcx_model_export_keys). */
+mpcx_status mpcx_model_release_arena(mpcx_model *m);
+/* Streaming key arena for batches whose keys do not stay resident: both parties'
+ * keys (mpcx_model_key_bytes(m, B) bytes each, host memory, pinned for overlap)
+ * are copied per chunk of consecutive gates into one of two device slots of at
+ * most slot_bytes per party, on a copy stream, while the previous chunk
+ * computes.  Replaces the chunked key pipeline of
+ * gpu_mpc/deepdtagen_inference.cu:608-859 (pinned double-buffered slots, copy
+ * stream, ready/free events) and setGPUKeyArenaSlot
+ * (patches/EzPC-GPU-MPC.track3.patch:680-685).  The resident arena is freed;
+ * the host buffers must stay valid until the model is destroyed or keys are
+ * imported again.  MPCX_EINVAL if a single gate's key exceeds slot_bytes. */
+mpcx_status mpcx_model_attach_host_keys(mpcx_model *m, int B, const void *h_key0, const void *h_key1,
+                                        size_t bytes, size_t slot_bytes);
+/* Chunks and host-to-device key bytes (both parties) of the last forward. */
+mpcx_status mpcx_model_stream_stats(const mpcx_model *m, int *chunks, uint64_t *bytes_h2d);
 /* Both parties' input shares (host, ring elements): x (B,N,feat), adjacency
  * (B,N,N) at scale 0 with self loops, atom mask (B,N); protein embedding
  * (B,prot) int64 at scale s, public. */

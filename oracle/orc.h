@@ -222,6 +222,15 @@ int orc_model_eval(const orc_dims *d, int B, const int64_t *W, const uint8_t *k0
                    const uint64_t *a0, const uint64_t *a1, const uint64_t *m0,
                    const uint64_t *m1, const int64_t *prot, int64_t *out,
                    uint64_t *bytes);
+/* Standalone secure adjacency normalisation (gpu_mpc/secure_adj_norm.h:203-374,
+ * 393-659): A (B x N x N, 0/1 with self loops) as additive shares a0, a1 ->
+ * masked A_norm = A (.) floor(T[d_i] T[d_j] / 2^s) + out_mask. */
+size_t orc_adjnorm_key_bytes(int bw, int s, int B, int N);
+int orc_adjnorm_keygen(int bw, int s, int B, int N, uint64_t seed, uint64_t *out_mask, uint8_t *k0,
+                       uint8_t *k1);
+int orc_adjnorm_eval(int bw, int s, int B, int N, int nmax, const uint8_t *k0, const uint8_t *k1,
+                     const uint64_t *a0, const uint64_t *a1, uint64_t *out_masked, uint64_t *bytes);
+
 /* Optional trace of reconstructed masked values (for debugging parity):
  * when set, each gate's public output is copied to the callback. */
 typedef void (*orc_trace_fn)(uint32_t gate, size_t n, const uint64_t *vals);

@@ -100,6 +100,9 @@ def lib():
             "orc_model_key_bytes": (sz, [P, i]),
             "orc_model_keygen": (i, [P, i, u64, P, P, P]),
             "orc_model_eval": (i, [P, i, P, P, P, P, P, P, P, P, P, P, P, P]),
+            "orc_adjnorm_key_bytes": (sz, [i, i, i, i]),
+            "orc_adjnorm_keygen": (i, [i, i, i, i, u64, P, P, P]),
+            "orc_adjnorm_eval": (i, [i, i, i, i, i, P, P, P, P, P, P]),
             "orc_set_threads": (None, [i]),
             "orc_get_threads": (i, []),
         }
@@ -347,6 +350,23 @@ def model_eval(d, B, W, k0, k1, x0, x1, a0, a1, m0, m1, prot):
     by = np.zeros(1, np.uint64)
     lib().orc_model_eval(C.byref(d), B, ptr(W), ptr(k0), ptr(k1), *[ptr(v) for v in arrs], ptr(prot),
                          ptr(out), ptr(by))
+    return out, int(by[0])
+
+
+def adjnorm_keygen(bw, s, B, N, seed):
+    n = lib().orc_adjnorm_key_bytes(bw, s, B, N)
+    k0 = np.zeros(n, np.uint8)
+    k1 = np.zeros(n, np.uint8)
+    mask = np.zeros(B * N * N, np.uint64)
+    lib().orc_adjnorm_keygen(bw, s, B, N, seed, ptr(mask), ptr(k0), ptr(k1))
+    return k0, k1, mask
+
+
+def adjnorm_eval(bw, s, B, N, nmax, k0, k1, a0, a1):
+    a0, a1 = _u64(a0), _u64(a1)
+    out = np.zeros(B * N * N, np.uint64)
+    by = np.zeros(1, np.uint64)
+    lib().orc_adjnorm_eval(bw, s, B, N, nmax, ptr(k0), ptr(k1), ptr(a0), ptr(a1), ptr(out), ptr(by))
     return out, int(by[0])
 
 

@@ -300,19 +300,141 @@ static void build_maps(int B, int N, uint32_t *oa, uint32_t *ob, uint32_t *wa, u
   }
 }
 
+/* Secure adjacency normalisation block, shared by the model and the standalone
+ * entry points (gpu_mpc/secure_adj_norm.h:203-374 keygen, :393-659 eval):
+ *   reveal A; reveal the degrees (row sums of the A shares, :421-493);
+ *   LUT8 -> T[d] (:495-520); MUL T[d_i]*T[d_j] over the upper triangle;
+ *   TRSLACK (one truncation); MUL A (.) W  (:569-651). */
+static size_t adjnorm_layout(int bw, int s, int B, int N, size_t o) {
+  size_t r1, r2, r3;
+  orc_dcf_layout D;
+  const size_t BN = (size_t)B * N, BNN = BN * N, BP = (size_t)B * pairs_of(N);
+  o = orc_reveal_layout(bw, BNN, o, &r1);
+  o = orc_reveal_layout(bw, BN, o, &r1);
+  o = orc_lut8_layout(bw, BN, o, &D, &r1, &r2, &r3);
+  o = orc_mul_layout(bw, BN, BN, BP, o, &r1, &r2, &r3);
+  o = orc_tr_layout_make(ORC_G_TRSLACK, bw, s, BP, o).end;
+  o = orc_mul_layout(bw, BNN, BP, BNN, o, &r1, &r2, &r3);
+  return o;
+}
+
+/* rA (BNN): mask of the revealed A; rN (BNN): mask of A_norm. */
+static size_t adjnorm_keygen_blk(int bw, int s, int B, int N, uint64_t seed, uint32_t *g, size_t o,
+                                 uint64_t *rA, uint64_t *rN, uint8_t *k0, uint8_t *k1) {
+  size_t r1, r2, r3;
+  orc_dcf_layout D;
+  const size_t BN = (size_t)B * N, BNN = BN * N, BP = (size_t)B * pairs_of(N);
+  uint64_t *rd = (uint64_t *)malloc(8 * BN), *rinv = (uint64_t *)malloc(8 * BN);
+  uint64_t *rP = (uint64_t *)malloc(8 * BP), *rW = (uint64_t *)malloc(8 * BP);
+  uint32_t *oa = (uint32_t *)malloc(4 * BP), *ob = (uint32_t *)malloc(4 * BP);
+  uint32_t *wa = (uint32_t *)malloc(4 * BNN), *wb = (uint32_t *)malloc(4 * BNN);
+  build_maps(B, N, oa, ob, wa, wb);
+  orc_reveal_keygen(seed, (*g)++, bw, BNN, rA, k0, k1, o);
+  o = orc_reveal_layout(bw, BNN, o, &r1);
+  orc_reveal_keygen(seed, (*g)++, bw, BN, rd, k0, k1, o);
+  o = orc_reveal_layout(bw, BN, o, &r1);
+  orc_lut8_keygen(seed, (*g)++, bw, BN, rd, rinv, k0, k1, o);
+  o = orc_lut8_layout(bw, BN, o, &D, &r1, &r2, &r3);
+  orc_mul_keygen(seed, (*g)++, bw, BN, BN, BP, oa, ob, rinv, rinv, rP, k0, k1, o);
+  o = orc_mul_layout(bw, BN, BN, BP, o, &r1, &r2, &r3);
+  orc_tr_keygen(seed, (*g)++, ORC_G_TRSLACK, bw, s, BP, rP, rW, k0, k1, o);
+  o = orc_tr_layout_make(ORC_G_TRSLACK, bw, s, BP, o).end;
+  orc_mul_keygen(seed, (*g)++, bw, BNN, BP, BNN, wa, wb, rA, rW, rN, k0, k1, o);
+  o = orc_mul_layout(bw, BNN, BP, BNN, o, &r1, &r2, &r3);
+  free(rd);
+  free(rinv);
+  free(rP);
+  free(rW);
+  free(oa);
+  free(ob);
+  free(wa);
+  free(wb);
+  return o;
+}
+
+/* Ah (BNN): revealed A (A + rA); An (BNN): A_norm + rN. */
+static size_t adjnorm_eval_blk(int bw, int s, int B, int N, int nmax, uint32_t *g, size_t o,
+                               const uint8_t *k0, const uint8_t *k1, const uint64_t *a0,
+                               const uint64_t *a1, uint64_t *Ah, uint64_t *An, uint64_t *by) {
+  size_t r1, r2, r3;
+  orc_dcf_layout D;
+  const uint64_t M = rmask(bw);
+  const size_t BN = (size_t)B * N, BNN = BN * N, BP = (size_t)B * pairs_of(N);
+  uint64_t *dg0 = (uint64_t *)calloc(BN, 8), *dg1 = (uint64_t *)calloc(BN, 8);
+  uint64_t *dh = (uint64_t *)malloc(8 * BN), *inv = (uint64_t *)malloc(8 * BN);
+  uint64_t *Ph = (uint64_t *)malloc(8 * BP), *Wh = (uint64_t *)malloc(8 * BP);
+  uint32_t *oa = (uint32_t *)malloc(4 * BP), *ob = (uint32_t *)malloc(4 * BP);
+  uint32_t *wa = (uint32_t *)malloc(4 * BNN), *wb = (uint32_t *)malloc(4 * BNN);
+  uint64_t T[256];
+  build_maps(B, N, oa, ob, wa, wb);
+  orc_invsqrt_table(s, nmax, T);
+  orc_reveal_eval(bw, BNN, k0, k1, o, a0, a1, Ah, by);
+  trace((*g)++, BNN, Ah);
+  o = orc_reveal_layout(bw, BNN, o, &r1);
+  for (size_t r = 0; r < BN; r++) {
+    for (int j = 0; j < N; j++) {
+      dg0[r] += a0[r * N + j];
+      dg1[r] += a1[r * N + j];
+    }
+    dg0[r] &= M;
+    dg1[r] &= M;
+  }
+  orc_reveal_eval(bw, BN, k0, k1, o, dg0, dg1, dh, by);
+  trace((*g)++, BN, dh);
+  o = orc_reveal_layout(bw, BN, o, &r1);
+  orc_lut8_eval(bw, BN, k0, k1, o, T, dh, inv, by);
+  trace((*g)++, BN, inv);
+  o = orc_lut8_layout(bw, BN, o, &D, &r1, &r2, &r3);
+  orc_mul_eval(bw, BN, BN, BP, oa, ob, k0, k1, o, inv, inv, Ph, by);
+  trace((*g)++, BP, Ph);
+  o = orc_mul_layout(bw, BN, BN, BP, o, &r1, &r2, &r3);
+  orc_tr_eval(ORC_G_TRSLACK, bw, s, BP, k0, k1, o, Ph, NULL, Wh, by);
+  trace((*g)++, BP, Wh);
+  o = orc_tr_layout_make(ORC_G_TRSLACK, bw, s, BP, o).end;
+  orc_mul_eval(bw, BNN, BP, BNN, wa, wb, k0, k1, o, Ah, Wh, An, by);
+  trace((*g)++, BNN, An);
+  o = orc_mul_layout(bw, BNN, BP, BNN, o, &r1, &r2, &r3);
+  free(dg0);
+  free(dg1);
+  free(dh);
+  free(inv);
+  free(Ph);
+  free(Wh);
+  free(oa);
+  free(ob);
+  free(wa);
+  free(wb);
+  return o;
+}
+
+size_t orc_adjnorm_key_bytes(int bw, int s, int B, int N) { return adjnorm_layout(bw, s, B, N, 0); }
+
+int orc_adjnorm_keygen(int bw, int s, int B, int N, uint64_t seed, uint64_t *out_mask, uint8_t *k0,
+                       uint8_t *k1) {
+  uint32_t g = 1;
+  uint64_t *rA = (uint64_t *)malloc(8 * (size_t)B * N * N);
+  adjnorm_keygen_blk(bw, s, B, N, seed, &g, 0, rA, out_mask, k0, k1);
+  free(rA);
+  return 0;
+}
+
+int orc_adjnorm_eval(int bw, int s, int B, int N, int nmax, const uint8_t *k0, const uint8_t *k1,
+                     const uint64_t *a0, const uint64_t *a1, uint64_t *out_masked, uint64_t *bytes) {
+  uint32_t g = 1;
+  uint64_t by = 0;
+  uint64_t *Ah = (uint64_t *)malloc(8 * (size_t)B * N * N);
+  adjnorm_eval_blk(bw, s, B, N, nmax, &g, 0, k0, k1, a0, a1, Ah, out_masked, &by);
+  free(Ah);
+  if (bytes) *bytes = by;
+  return 0;
+}
+
 size_t orc_model_key_bytes(const orc_dims *d, int B) {
   const int bw = d->bw, s = d->s, N = d->n_nodes;
   size_t o = 0, r1, r2, r3;
-  orc_dcf_layout D;
   o = orc_reveal_layout(bw, (size_t)B * N * d->feat, o, &r1);
-  o = orc_reveal_layout(bw, (size_t)B * N * N, o, &r1);
   o = orc_reveal_layout(bw, (size_t)B * N, o, &r1);
-  o = orc_reveal_layout(bw, (size_t)B * N, o, &r1);
-  o = orc_lut8_layout(bw, (size_t)B * N, o, &D, &r1, &r2, &r3);
-  size_t P = pairs_of(N);
-  o = orc_mul_layout(bw, (size_t)B * N, (size_t)B * N, (size_t)B * P, o, &r1, &r2, &r3);
-  o = orc_tr_layout_make(ORC_G_TRSLACK, bw, s, (size_t)B * P, o).end;
-  o = orc_mul_layout(bw, (size_t)B * N * N, (size_t)B * P, (size_t)B * N * N, o, &r1, &r2, &r3);
+  o = adjnorm_layout(bw, s, B, N, o);
   for (int l = 0; l < 3; l++) {
     size_t E = (size_t)B * N * d->gcn[l];
     o = orc_tr_layout_make(ORC_G_TR, bw, s, E, o).end;
@@ -343,8 +465,7 @@ int orc_model_keygen(const orc_dims *d, int B, uint64_t seed, const int64_t *W, 
   const uint64_t M = rmask(bw);
   size_t o = 0, r1, r2, r3;
   uint32_t g = 1;
-  orc_dcf_layout D;
-  const size_t BN = (size_t)B * N, BNN = BN * N, P = pairs_of(N);
+  const size_t BN = (size_t)B * N, BNN = BN * N;
   int maxw = d->feat;
   for (int l = 0; l < nlayers(d); l++) {
     int in, out;
@@ -354,30 +475,14 @@ int orc_model_keygen(const orc_dims *d, int B, uint64_t seed, const int64_t *W, 
   }
   uint64_t *rX = (uint64_t *)malloc(8 * BN * maxw);
   uint64_t *rA = (uint64_t *)malloc(8 * BNN), *rm = (uint64_t *)malloc(8 * BN);
-  uint64_t *rd = (uint64_t *)malloc(8 * BN), *rinv = (uint64_t *)malloc(8 * BN);
-  uint64_t *rP = (uint64_t *)malloc(8 * B * P), *rW = (uint64_t *)malloc(8 * B * P);
   uint64_t *rN = (uint64_t *)malloc(8 * BNN);
   uint64_t *t1 = (uint64_t *)malloc(8 * BN * maxw), *t2 = (uint64_t *)malloc(8 * BN * maxw);
-  uint32_t *oa = (uint32_t *)malloc(4 * B * P), *ob = (uint32_t *)malloc(4 * B * P);
-  uint32_t *wa = (uint32_t *)malloc(4 * BNN), *wb = (uint32_t *)malloc(4 * BNN);
-  build_maps(B, N, oa, ob, wa, wb);
 
   orc_reveal_keygen(seed, g++, bw, BN * d->feat, rX, k0, k1, o);
   o = orc_reveal_layout(bw, BN * d->feat, o, &r1);
-  orc_reveal_keygen(seed, g++, bw, BNN, rA, k0, k1, o);
-  o = orc_reveal_layout(bw, BNN, o, &r1);
   orc_reveal_keygen(seed, g++, bw, BN, rm, k0, k1, o);
   o = orc_reveal_layout(bw, BN, o, &r1);
-  orc_reveal_keygen(seed, g++, bw, BN, rd, k0, k1, o);
-  o = orc_reveal_layout(bw, BN, o, &r1);
-  orc_lut8_keygen(seed, g++, bw, BN, rd, rinv, k0, k1, o);
-  o = orc_lut8_layout(bw, BN, o, &D, &r1, &r2, &r3);
-  orc_mul_keygen(seed, g++, bw, BN, BN, (size_t)B * P, oa, ob, rinv, rinv, rP, k0, k1, o);
-  o = orc_mul_layout(bw, BN, BN, (size_t)B * P, o, &r1, &r2, &r3);
-  orc_tr_keygen(seed, g++, ORC_G_TRSLACK, bw, s, (size_t)B * P, rP, rW, k0, k1, o);
-  o = orc_tr_layout_make(ORC_G_TRSLACK, bw, s, (size_t)B * P, o).end;
-  orc_mul_keygen(seed, g++, bw, BNN, (size_t)B * P, BNN, wa, wb, rA, rW, rN, k0, k1, o);
-  o = orc_mul_layout(bw, BNN, (size_t)B * P, BNN, o, &r1, &r2, &r3);
+  o = adjnorm_keygen_blk(bw, s, B, N, seed, &g, o, rA, rN, k0, k1);
 
   /* GCN stack: rX holds the running H mask */
   int fin = d->feat;
@@ -464,17 +569,9 @@ int orc_model_keygen(const orc_dims *d, int B, uint64_t seed, const int64_t *W, 
   free(rX);
   free(rA);
   free(rm);
-  free(rd);
-  free(rinv);
-  free(rP);
-  free(rW);
   free(rN);
   free(t1);
   free(t2);
-  free(oa);
-  free(ob);
-  free(wa);
-  free(wb);
   return 0;
 }
 
@@ -486,8 +583,7 @@ int orc_model_eval(const orc_dims *d, int B, const int64_t *W, const uint8_t *k0
   const uint64_t M = rmask(bw);
   size_t o = 0, r1, r2, r3;
   uint32_t g = 1;
-  orc_dcf_layout D;
-  const size_t BN = (size_t)B * N, BNN = BN * N, P = pairs_of(N);
+  const size_t BN = (size_t)B * N, BNN = BN * N;
   int maxw = d->feat;
   for (int l = 0; l < nlayers(d); l++) {
     int in, outw;
@@ -497,53 +593,18 @@ int orc_model_eval(const orc_dims *d, int B, const int64_t *W, const uint8_t *k0
   }
   uint64_t *H = (uint64_t *)malloc(8 * BN * maxw);
   uint64_t *Ah = (uint64_t *)malloc(8 * BNN), *mh = (uint64_t *)malloc(8 * BN);
-  uint64_t *dh = (uint64_t *)malloc(8 * BN), *inv = (uint64_t *)malloc(8 * BN);
-  uint64_t *Ph = (uint64_t *)malloc(8 * B * P), *Wh = (uint64_t *)malloc(8 * B * P);
   uint64_t *An = (uint64_t *)malloc(8 * BNN);
   uint64_t *t1 = (uint64_t *)malloc(8 * BN * maxw), *t2 = (uint64_t *)malloc(8 * BN * maxw);
-  uint64_t *dg0 = (uint64_t *)calloc(BN, 8), *dg1 = (uint64_t *)calloc(BN, 8);
   int64_t *be = (int64_t *)malloc(8 * BN * maxw);
-  uint32_t *oa = (uint32_t *)malloc(4 * B * P), *ob = (uint32_t *)malloc(4 * B * P);
-  uint32_t *wa = (uint32_t *)malloc(4 * BNN), *wb = (uint32_t *)malloc(4 * BNN);
-  uint64_t T[256];
-  build_maps(B, N, oa, ob, wa, wb);
-  orc_invsqrt_table(s, d->lut_nmax, T);
   uint64_t by = 0;
 
   orc_reveal_eval(bw, BN * d->feat, k0, k1, o, x0, x1, H, &by);
-  trace(g, BN * d->feat, H);
-  g++;
+  trace(g++, BN * d->feat, H);
   o = orc_reveal_layout(bw, BN * d->feat, o, &r1);
-  orc_reveal_eval(bw, BNN, k0, k1, o, a0, a1, Ah, &by);
-  trace(g++, BNN, Ah);
-  o = orc_reveal_layout(bw, BNN, o, &r1);
   orc_reveal_eval(bw, BN, k0, k1, o, m0, m1, mh, &by);
   trace(g++, BN, mh);
   o = orc_reveal_layout(bw, BN, o, &r1);
-  for (size_t r = 0; r < BN; r++)
-    for (int j = 0; j < N; j++) {
-      dg0[r] += a0[r * N + j];
-      dg1[r] += a1[r * N + j];
-    }
-  for (size_t r = 0; r < BN; r++) {
-    dg0[r] &= M;
-    dg1[r] &= M;
-  }
-  orc_reveal_eval(bw, BN, k0, k1, o, dg0, dg1, dh, &by);
-  trace(g++, BN, dh);
-  o = orc_reveal_layout(bw, BN, o, &r1);
-  orc_lut8_eval(bw, BN, k0, k1, o, T, dh, inv, &by);
-  trace(g++, BN, inv);
-  o = orc_lut8_layout(bw, BN, o, &D, &r1, &r2, &r3);
-  orc_mul_eval(bw, BN, BN, (size_t)B * P, oa, ob, k0, k1, o, inv, inv, Ph, &by);
-  trace(g++, (size_t)B * P, Ph);
-  o = orc_mul_layout(bw, BN, BN, (size_t)B * P, o, &r1, &r2, &r3);
-  orc_tr_eval(ORC_G_TRSLACK, bw, s, (size_t)B * P, k0, k1, o, Ph, NULL, Wh, &by);
-  trace(g++, (size_t)B * P, Wh);
-  o = orc_tr_layout_make(ORC_G_TRSLACK, bw, s, (size_t)B * P, o).end;
-  orc_mul_eval(bw, BNN, (size_t)B * P, BNN, wa, wb, k0, k1, o, Ah, Wh, An, &by);
-  trace(g++, BNN, An);
-  o = orc_mul_layout(bw, BNN, (size_t)B * P, BNN, o, &r1, &r2, &r3);
+  o = adjnorm_eval_blk(bw, s, B, N, d->lut_nmax, &g, o, k0, k1, a0, a1, Ah, An, &by);
 
   int fin = d->feat;
   for (int l = 0; l < 3; l++) {
@@ -655,19 +716,9 @@ int orc_model_eval(const orc_dims *d, int B, const int64_t *W, const uint8_t *k0
   free(H);
   free(Ah);
   free(mh);
-  free(dh);
-  free(inv);
-  free(Ph);
-  free(Wh);
   free(An);
   free(t1);
   free(t2);
-  free(dg0);
-  free(dg1);
   free(be);
-  free(oa);
-  free(ob);
-  free(wa);
-  free(wb);
   return 0;
 }

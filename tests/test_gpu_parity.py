@@ -331,3 +331,98 @@ def test_model_default_fixture(mp, synth, bw):
     assert m.output(B).tolist() == rec[f"want_bw{bw}"]
     m.close()
     c.close()
+
+
+# ---------------------------------------------------------------------------
+# standalone secure adjacency normalisation (config 2)
+# ---------------------------------------------------------------------------
+@pytest.mark.parametrize("bw", [32, 64])
+def test_adjnorm_keys_and_eval(mp, orc, synth, bw):
+    B, N = 3, 24
+    _, A, _ = synth.molecules(B, synth.Dims(bw=bw, n_nodes=N), seed=5, min_atoms=3, max_atoms=N)
+    a0, a1 = synth.share(A, bw, 77)
+    c = mp.Ctx(bw=bw)
+    g0, g1, gmask = c.adjnorm_keygen(B, N, seed=123)
+    o0, o1, omask = orc.adjnorm_keygen(bw, S, B, N, 123)
+    assert np.array_equal(host(g0)[:o0.size], o0) and np.array_equal(host(g1)[:o1.size], o1)
+    assert np.array_equal(mp.from_dev(gmask, c.T, B * N * N).astype(np.uint64), omask)
+    c.reset_counters()
+    got = c.adjnorm_eval(B, N, 138, g0, g1, a0, a1)
+    want, oby = orc.adjnorm_eval(bw, S, B, N, 138, o0, o1, a0, a1)
+    assert np.array_equal(got.astype(np.uint64), want)
+    assert c.bytes_exchanged == oby
+    c.close()
+
+
+def test_adjnorm_config2_full_size(mp, orc, synth):
+    """Config 2: B=1024 graphs of the config-0 distribution, N=140, Z_2^32.
+    Every unmasked entry equals A[i,j] * floor(T[d_i] T[d_j] / 2^12)."""
+    B, N, bw = 1024, 140, 32
+    _, A, _ = synth.molecules(B, synth.Dims(bw=bw), seed=2)
+    a0, a1 = synth.share(A, bw, 3)
+    c = mp.Ctx(bw=bw)
+    k0, k1, mask = c.adjnorm_keygen(B, N, seed=9)
+    out = c.adjnorm_eval(B, N, 138, k0, k1, a0, a1, as_device=True)
+    got = (mp.from_dev(out, np.uint32, B * N * N) - mp.from_dev(mask, np.uint32, B * N * N)).astype(np.int64)
+    want = orc.adj_norm_plain(A).reshape(-1)
+    assert np.array_equal(got, want)
+    c.close()
+
+
+# ---------------------------------------------------------------------------
+# streamed key arena (config 4 path)
+# ---------------------------------------------------------------------------
+@pytest.mark.parametrize("bw", [32, 64])
+def test_model_streamed_keys_match_resident(mp, orc, synth, bw):
+    """Keys exported to pinned host memory and streamed through two small
+    device slots give the same outputs as the resident arena, on two
+    consecutive forwards (slot events reused)."""
+    B = 3
+    wl = synth.workload(B, synth.Dims(bw=bw), seed=31)
+    d = _od(orc, wl.dims)
+    want, code = orc.plain_forward(d, wl.X, wl.A, wl.mask, wl.prot, wl.W)
+    assert code == 0
+    c = mp.Ctx(bw=bw)
+    m = mp.Model(c, wl.dims, wl.W)
+    m.keygen(B, 555)
+    nbytes = m.key_bytes(B)
+    h0, h1 = mp.PinnedBuffer(nbytes), mp.PinnedBuffer(nbytes)
+    m.export_keys(0, B, into=h0)
+    m.export_keys(1, B, into=h1)
+    m.release_arena()
+    # a slot smaller than one gate's key is refused; a quarter of the arena
+    # (the largest gate, GCN-3's TRRELU, is about a fifth) gives several chunks
+    with pytest.raises(mp.MpcxError):
+        m.attach_host_keys(B, h0, h1, slot_bytes=4096)
+    m.attach_host_keys(B, h0, h1, slot_bytes=nbytes // 4)
+    m.set_inputs(B, *wl.shares["x"], *wl.shares["a"], *wl.shares["m"], wl.prot)
+    for _ in range(2):
+        m.forward(B)
+        assert np.array_equal(m.output(B), want)
+        st = m.stream_stats()
+        assert st["chunks"] >= 4 and st["bytes_h2d"] == 2 * nbytes
+    # a second input batch on the same streamed keys
+    wl2 = synth.workload(B, synth.Dims(bw=bw), seed=32)
+    want2, code = orc.plain_forward(d, wl2.X, wl2.A, wl2.mask, wl2.prot, wl.W)
+    assert code == 0
+    m.set_inputs(B, *wl2.shares["x"], *wl2.shares["a"], *wl2.shares["m"], wl2.prot)
+    m.forward(B)
+    assert np.array_equal(m.output(B), want2)
+    m.close()
+    c.close()
+    h0.free()
+    h1.free()
+
+
+def test_relu_config1_full_size(mp):
+    """Config 1: 2^24 ReLUs over Z_2^32 of uniform fixed-point values in
+    [-8, 8), one 31-bit DCF key per element, against max(x, 0)."""
+    c = mp.Ctx(bw=32)
+    rng = np.random.default_rng(24)
+    n = 1 << 24
+    x = rng.integers(-8 << S, 8 << S, size=n)
+    rin = rmask(rng, n, 32)
+    k0, k1, rout = c.tr_keygen(3, rin, seed=12, gate=1)
+    y = c.tr_eval(3, k0, k1, (x.astype(np.uint64) + rin) & M(32))
+    assert np.array_equal(signed(y.astype(np.uint64) - rout.astype(np.uint64), 32), np.maximum(x, 0))
+    c.close()

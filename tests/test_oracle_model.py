@@ -190,3 +190,20 @@ def test_two_party_matches_plaintext(orc, synth, bw):
     o2, by = orc.model_eval(d, 2, wl.W, k0, k1, x0, x1, a0, a1, m0, m1, wl.prot)
     assert np.array_equal(o2, out)
     assert by > 0
+
+
+@pytest.mark.parametrize("bw", [32, 64])
+def test_adjnorm_two_party_matches_closed_form(orc, synth, bw):
+    """Standalone secure adjacency normalisation (the config-2 pipeline) on
+    shares of A reconstructs A (.) floor(T[d_i] T[d_j] / 2^12) exactly."""
+    B, N = 3, 24
+    _, A, _ = synth.molecules(B, synth.Dims(bw=bw, n_nodes=N), seed=5, min_atoms=3, max_atoms=N)
+    a0, a1 = synth.share(A, bw, 77)
+    k0, k1, rout = orc.adjnorm_keygen(bw, 12, B, N, 123)
+    got, by = orc.adjnorm_eval(bw, 12, B, N, 138, k0, k1, a0, a1)
+    mod = (1 << bw) - 1 if bw < 64 else 0xFFFFFFFFFFFFFFFF
+    val = (got - rout) & np.uint64(mod)
+    want = orc.adj_norm_plain(A).reshape(-1)
+    assert np.array_equal(val.astype(np.int64), want)
+    # five exchanges of ring elements + one of DCF bit planes
+    assert by > 0
