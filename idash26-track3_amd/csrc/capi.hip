@@ -644,14 +644,26 @@ mpcx_status mpcx_model_release_arena(mpcx_model *m) {
   return MPCX_OK;
 }
 
-mpcx_status mpcx_model_attach_host_keys(mpcx_model *m, int B, const void *k0, const void *k1, size_t bytes,
-                                        size_t slot_bytes) {
+mpcx_status mpcx_model_attach_host_keys(mpcx_model *m, int B, const void *k0, size_t bytes0, const void *k1,
+                                        size_t bytes1, size_t slot_bytes) {
   if (!m || !k0 || !k1) return MPCX_EINVAL;
-  if (B < 1 || bytes != m->impl->key_bytes(B)) return fail(m->ctx, MPCX_EINVAL, "attach_host_keys: key size mismatch");
-  hipError_t e = m->impl->attach_host_keys(B, k0, k1, bytes, slot_bytes);
+  if (B < 1 || bytes0 != m->impl->key_bytes(B) ||
+      (bytes1 != m->impl->key_bytes(B) && bytes1 != m->impl->unique_key_bytes(B, 1)))
+    return fail(m->ctx, MPCX_EINVAL, "attach_host_keys: key size mismatch");
+  hipError_t e = m->impl->attach_host_keys(B, k0, bytes0, k1, bytes1, slot_bytes);
   if (e == hipErrorInvalidValue)
     return fail(m->ctx, MPCX_EINVAL, "attach_host_keys: slot_bytes smaller than the largest gate key");
   HIPC(m->ctx, e, "model_attach_host_keys");
+  return MPCX_OK;
+}
+
+size_t mpcx_model_unique_key_bytes(const mpcx_model *m, int B, int party) {
+  return (m && B > 0 && (party == 0 || party == 1)) ? m->impl->unique_key_bytes(B, party) : 0;
+}
+
+mpcx_status mpcx_model_export_unique_keys(mpcx_model *m, int party, void *dst, size_t bytes) {
+  if (!m || !dst || (party != 0 && party != 1)) return MPCX_EINVAL;
+  HIPC(m->ctx, m->impl->export_unique_keys(party, dst, bytes), "model_export_unique_keys");
   return MPCX_OK;
 }
 

@@ -282,6 +282,10 @@ __global__ void k_tr_phase1(TrArgs<T> a) {
   AesLds<NT, REP> aes(lds);
   const int p = blockIdx.y;
   const uint8_t *K = p ? a.k1 : a.k0;
+  // The correction words and leaf words of a DCF key are the same for both
+  // parties (public to both); both parties read party 0's planes, so one copy
+  // serves the two evaluations (and a streamed arena moves it once).
+  const uint8_t *KC = a.k0;
   const size_t stride = size_t(gridDim.x) * blockDim.x;
   const T lowmask = (T(1) << (a.n - 1)) - T(1);
   const T smask = (T(1) << a.s) - T(1);
@@ -292,14 +296,14 @@ __global__ void k_tr_phase1(TrArgs<T> a) {
       const T xp = tr_shifted_input(a, i);
       if (a.use_a) {
         ra = dcf_eval_walk(aes, reinterpret_cast<const uint4 *>(K + a.a.off_root)[i], a.a.m, a.a.L,
-                           reinterpret_cast<const uint4 *>(K + a.a.off_cw) + i, a.N,
-                           reinterpret_cast<const uint4 *>(K + a.a.off_leaf)[i], uint64_t(xp & lowmask));
+                           reinterpret_cast<const uint4 *>(KC + a.a.off_cw) + i, a.N,
+                           reinterpret_cast<const uint4 *>(KC + a.a.off_leaf)[i], uint64_t(xp & lowmask));
         ra ^= get_bit(reinterpret_cast<const uint64_t *>(K + a.a.off_z), i);
       }
       if (a.use_b) {
         rb = dcf_eval_walk(aes, reinterpret_cast<const uint4 *>(K + a.b.off_root)[i], a.b.m, a.b.L,
-                           reinterpret_cast<const uint4 *>(K + a.b.off_cw) + i, a.N,
-                           reinterpret_cast<const uint4 *>(K + a.b.off_leaf)[i], uint64_t(xp & smask));
+                           reinterpret_cast<const uint4 *>(KC + a.b.off_cw) + i, a.N,
+                           reinterpret_cast<const uint4 *>(KC + a.b.off_leaf)[i], uint64_t(xp & smask));
         rb ^= get_bit(reinterpret_cast<const uint64_t *>(K + a.b.off_z), i);
       }
     }
@@ -747,8 +751,9 @@ __global__ void k_lut8_phase1(Lut8Layout lay, const uint8_t *k0, const uint8_t *
   const size_t N = lay.dpf.N;
   for (size_t i = size_t(blockIdx.x) * blockDim.x + threadIdx.x; i < N; i += size_t(gridDim.x) * blockDim.x) {
     const uint4 s = reinterpret_cast<const uint4 *>(K + lay.dpf.off_root)[i];
-    const uint4 cw = reinterpret_cast<const uint4 *>(K + lay.dpf.off_cw)[i];
-    const uint4 leaf = reinterpret_cast<const uint4 *>(K + lay.dpf.off_leaf)[i];
+    // correction and leaf words are common to both parties: read party 0's
+    const uint4 cw = reinterpret_cast<const uint4 *>(k0 + lay.dpf.off_cw)[i];
+    const uint4 leaf = reinterpret_cast<const uint4 *>(k0 + lay.dpf.off_leaf)[i];
     const uint32_t t = s.x & 1u;
     const uint4 sl = xor4(aes.hash(s, c_rkH), and4(cw, 0u - t));
     const uint4 sr = xor4(sl, s);

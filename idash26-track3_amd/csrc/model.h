@@ -77,10 +77,17 @@ class ModelBase {
   virtual hipError_t import_keys(int B, const void *k0, const void *k1, size_t bytes) = 0;
   virtual hipError_t export_keys(int party, void *dst, size_t bytes) = 0;
   virtual hipError_t release_arena() = 0;
+  // Bytes of party 1's key planes that party 0 does not hold identically
+  // (its "unique" part; party 0's unique part is its whole arena).
+  virtual size_t unique_key_bytes(int B, int party) const = 0;
+  // Party 1's unique planes, packed back to back in arena order.
+  virtual hipError_t export_unique_keys(int party, void *dst, size_t bytes) = 0;
   // Host-key (streaming) mode: keys of a batch of B in host memory (pinned for
   // asynchronous copies), copied per chunk of consecutive gates into one of two
   // device slots of slot_bytes per party while the previous chunk computes.
-  virtual hipError_t attach_host_keys(int B, const void *h_k0, const void *h_k1, size_t bytes,
+  // Party 0's whole arena; party 1's arena (bytes1 = key_bytes) or its packed
+  // unique planes (bytes1 = unique_key_bytes).
+  virtual hipError_t attach_host_keys(int B, const void *h_k0, size_t bytes0, const void *h_k1, size_t bytes1,
                                       size_t slot_bytes) = 0;
   virtual hipError_t set_inputs(int B, const void *x0, const void *x1, const void *a0, const void *a1,
                                 const void *m0, const void *m1, const int64_t *prot) = 0;

@@ -73,6 +73,20 @@ struct KeyView {
   size_t begin = 0;
 };
 
+// Key range of one gate and the sub-ranges that both parties hold identically
+// (DCF correction and leaf words, the clear output mask): a streamed arena
+// copies those once, from party 0's buffer.
+struct GateKey {
+  size_t begin = 0, end = 0;
+  int nsh = 0;
+  size_t sh[2][2] = {{0, 0}, {0, 0}};
+  void share(size_t b, size_t e) {
+    sh[nsh][0] = b;
+    sh[nsh][1] = e;
+    nsh++;
+  }
+};
+
 // Supplies the key bytes [begin, end) of the next gate (resident arena or a
 // streamed slot) before the gate's kernels are enqueued.
 struct KeySource {
@@ -512,14 +526,25 @@ class Model final : public ModelBase, KeySource {
 
   // ---------------- gate plan ----------------
   // Key range of every gate of a batch of B, in forward order.
-  std::vector<std::pair<size_t, size_t>> plan(int B) const {
+  std::vector<GateKey> plan(int B) const {
     const int N = d_.n_nodes;
     const size_t BN = size_t(B) * N;
-    std::vector<std::pair<size_t, size_t>> g;
+    std::vector<GateKey> g;
     size_t o = 0;
-    auto push = [&](size_t end) {
-      g.emplace_back(o, end);
+    auto push = [&](size_t end) -> GateKey & {
+      GateKey k;
+      k.begin = o;
+      k.end = end;
+      g.push_back(k);
       o = end;
+      return g.back();
+    };
+    auto dcf_shared = [](GateKey &k, const DcfLayout &d) { k.share(d.off_cw, d.off_leaf + d.N * 16); };
+    auto tr = [&](int kind, size_t n) {
+      TrLayout lay = tr_layout(kind, bw_, s_, n, o);
+      GateKey &k = push(lay.end);
+      if (lay.use_a) dcf_shared(k, lay.a);
+      if (lay.use_b) dcf_shared(k, lay.b);
     };
     push(reveal_layout(bw_, BN * d_.feat, o).end);
     push(reveal_layout(bw_, BN, o).end);
@@ -527,28 +552,32 @@ class Model final : public ModelBase, KeySource {
       const size_t BNN = BN * N, BP = size_t(B) * pairs_of(N);
       push(reveal_layout(bw_, BNN, o).end);
       push(reveal_layout(bw_, BN, o).end);
-      push(lut8_layout(bw_, BN, o).end);
+      Lut8Layout lut = lut8_layout(bw_, BN, o);
+      dcf_shared(push(lut.end), lut.dpf);
       push(mul_layout(bw_, BN, BN, BP, o).end);
-      push(tr_layout(G_TRSLACK, bw_, s_, BP, o).end);
+      tr(G_TRSLACK, BP);
       push(mul_layout(bw_, BNN, BP, BNN, o).end);
     }
     for (int l = 0; l < 3; l++) {
       size_t E = BN * d_.gcn[l];
-      push(tr_layout(G_TR, bw_, s_, E, o).end);
+      tr(G_TR, E);
       push(sxs_layout(bw_, B, N, N, d_.gcn[l], o).end);
-      push(tr_layout(G_TRRELU, bw_, s_, E, o).end);
+      tr(G_TRRELU, E);
     }
     int pairs[32];
     int Lv = pool_levels(N, pairs);
-    for (int l = 0; l < Lv; l++) push(tr_layout(G_RELU, bw_, s_, size_t(B) * pairs[l] * d_.gcn[2], o).end);
-    push(tr_layout(G_TRRELU, bw_, s_, size_t(B) * d_.dfc[0], o).end);
-    push(tr_layout(G_TR, bw_, s_, size_t(B) * d_.dfc[1], o).end);
-    for (int k = 0; k < d_.nfus - 1; k++) push(tr_layout(G_TRRELU, bw_, s_, size_t(B) * d_.fus[k], o).end);
-    push(reveal_layout(bw_, size_t(B) * d_.fus[d_.nfus - 1], o).end);
+    for (int l = 0; l < Lv; l++) tr(G_RELU, size_t(B) * pairs[l] * d_.gcn[2]);
+    tr(G_TRRELU, size_t(B) * d_.dfc[0]);
+    tr(G_TR, size_t(B) * d_.dfc[1]);
+    for (int k = 0; k < d_.nfus - 1; k++) tr(G_TRRELU, size_t(B) * d_.fus[k]);
+    {  // output: the clear output mask, the same for both parties
+      RevealLayout lay = reveal_layout(bw_, size_t(B) * d_.fus[d_.nfus - 1], o);
+      push(lay.end).share(lay.off_r, lay.end);
+    }
     return g;
   }
 
-  size_t key_bytes(int B) const override { return plan(B).back().second; }
+  size_t key_bytes(int B) const override { return plan(B).back().end; }
 
   uint8_t *arena(int party) override { return arena_[party]; }
 
@@ -699,6 +728,45 @@ class Model final : public ModelBase, KeySource {
   }
 
   // ---------------- streaming ----------------
+  // Party 1's key planes outside the shared sub-ranges, split at gate
+  // boundaries so that each run lies inside one gate (hence one chunk).
+  struct Run {
+    size_t b, e, src;
+  };
+  std::vector<Run> unique_runs(int B, bool packed) const {
+    std::vector<Run> r;
+    size_t acc = 0;
+    auto add = [&](size_t b, size_t e) {
+      if (e <= b) return;
+      r.push_back(Run{b, e, packed ? acc : b});
+      acc += e - b;
+    };
+    for (const GateKey &g : plan(B)) {
+      size_t cur = g.begin;
+      for (int j = 0; j < g.nsh; j++) {
+        add(cur, g.sh[j][0]);
+        cur = g.sh[j][1];
+      }
+      add(cur, g.end);
+    }
+    return r;
+  }
+  size_t unique_key_bytes(int B, int party) const override {
+    if (party == 0) return key_bytes(B);
+    size_t n = 0;
+    for (const Run &u : unique_runs(B, true)) n += u.e - u.b;
+    return n;
+  }
+  hipError_t export_unique_keys(int party, void *dst, size_t bytes) override {
+    if (party == 0) return export_keys(0, dst, bytes);
+    if (!arena_[1] || keyed_B_ < 1 || bytes != unique_key_bytes(keyed_B_, 1)) return hipErrorInvalidValue;
+    TRY(hipStreamSynchronize(L_.stream));
+    uint8_t *d = static_cast<uint8_t *>(dst);
+    for (const Run &u : unique_runs(keyed_B_, true))
+      TRY(hipMemcpy(d + u.src, arena_[1] + u.b, u.e - u.b, hipMemcpyDeviceToHost));
+    return hipSuccess;
+  }
+
   void free_stream() {
     for (int k = 0; k < 2; k++) {
       for (int p = 0; p < 2; p++) {
@@ -714,8 +782,17 @@ class Model final : public ModelBase, KeySource {
     streaming_ = false;
   }
 
-  hipError_t attach_host_keys(int B, const void *h0, const void *h1, size_t bytes, size_t slot_bytes) override {
-    if (!h0 || !h1 || bytes != key_bytes(B) || slot_bytes == 0) return hipErrorInvalidValue;
+  hipError_t attach_host_keys(int B, const void *h0, size_t bytes0, const void *h1, size_t bytes1,
+                              size_t slot_bytes) override {
+    const size_t full = key_bytes(B);
+    if (!h0 || !h1 || bytes0 != full || slot_bytes == 0) return hipErrorInvalidValue;
+    bool packed;
+    if (bytes1 == full)
+      packed = false;
+    else if (bytes1 == unique_key_bytes(B, 1))
+      packed = true;
+    else
+      return hipErrorInvalidValue;
     TRY(hipStreamSynchronize(L_.stream));
     free_stream();
     free_arena();  // the two slots replace the resident arena
@@ -724,7 +801,7 @@ class Model final : public ModelBase, KeySource {
     chunks_.clear();
     chunk_of_.assign(gates_.size(), 0);
     for (size_t i = 0; i < gates_.size(); i++) {
-      const size_t gb = gates_[i].first, ge = gates_[i].second;
+      const size_t gb = gates_[i].begin, ge = gates_[i].end;
       if (ge - gb > slot_bytes) return hipErrorInvalidValue;  // a gate larger than a slot
       if (chunks_.empty() || ge - chunks_.back().first > slot_bytes) chunks_.emplace_back(gb, ge);
       chunks_.back().second = ge;
@@ -740,24 +817,31 @@ class Model final : public ModelBase, KeySource {
     TRY(hipStreamCreateWithFlags(&cs_, hipStreamNonBlocking));
     host_[0] = static_cast<const uint8_t *>(h0);
     host_[1] = static_cast<const uint8_t *>(h1);
+    runs1_ = unique_runs(B, packed);
     streaming_ = true;
     keyed_B_ = B;
     return hipSuccess;
   }
 
-  // copy chunk k into slot k % 2 once the slot's previous chunk has been consumed
+  // copy chunk k into slot k % 2 once the slot's previous chunk has been consumed;
+  // party 1's copy skips the planes both parties share (read from party 0's)
   hipError_t issue_copy(int k) {
     const int sl = k & 1;
-    const size_t b = chunks_[k].first, len = chunks_[k].second - chunks_[k].first;
+    const size_t b = chunks_[k].first, e = chunks_[k].second;
     TRY(hipStreamWaitEvent(cs_, free_[sl], 0));
-    for (int p = 0; p < 2; p++) TRY(hipMemcpyAsync(slot_[sl][p], host_[p] + b, len, hipMemcpyHostToDevice, cs_));
+    TRY(hipMemcpyAsync(slot_[sl][0], host_[0] + b, e - b, hipMemcpyHostToDevice, cs_));
+    stream_stats.bytes_h2d += e - b;
+    for (const Run &u : runs1_) {
+      if (u.b < b || u.b >= e) continue;
+      TRY(hipMemcpyAsync(slot_[sl][1] + (u.b - b), host_[1] + u.src, u.e - u.b, hipMemcpyHostToDevice, cs_));
+      stream_stats.bytes_h2d += u.e - u.b;
+    }
     TRY(hipEventRecord(ready_[sl], cs_));
-    stream_stats.bytes_h2d += 2 * len;
     return hipSuccess;
   }
 
   hipError_t acquire(size_t begin, size_t end, KeyView *kv) override {
-    if (gi_ >= gates_.size() || gates_[gi_].first != begin || gates_[gi_].second != end)
+    if (gi_ >= gates_.size() || gates_[gi_].begin != begin || gates_[gi_].end != end)
       return hipErrorUnknown;  // forward walked off the plan
     const int k = chunk_of_[gi_++];
     if (!streaming_) {
@@ -911,12 +995,14 @@ class Model final : public ModelBase, KeySource {
   Workspace<T> ws_;
   AdjNorm<T> adj_;
   // gate plan and streaming state
-  std::vector<std::pair<size_t, size_t>> gates_, chunks_;
+  std::vector<GateKey> gates_;
+  std::vector<std::pair<size_t, size_t>> chunks_;
   std::vector<int> chunk_of_;
   size_t gi_ = 0;
   int cur_chunk_ = -1;
   bool streaming_ = false;
   const uint8_t *host_[2] = {nullptr, nullptr};
+  std::vector<Run> runs1_;
   uint8_t *slot_[2][2] = {{nullptr, nullptr}, {nullptr, nullptr}};
   hipEvent_t ready_[2] = {nullptr, nullptr}, free_[2] = {nullptr, nullptr};
   hipStream_t cs_ = nullptr;

@@ -81,8 +81,10 @@ _SIGS = {
     "mpcx_model_output": (C.c_int, [C.c_void_p, C.c_int, C.c_void_p]),
     "mpcx_model_profile": (C.c_int, [C.c_void_p, C.c_int]),
     "mpcx_model_release_arena": (C.c_int, [C.c_void_p]),
-    "mpcx_model_attach_host_keys": (C.c_int, [C.c_void_p, C.c_int, C.c_void_p, C.c_void_p, C.c_size_t,
-                                              C.c_size_t]),
+    "mpcx_model_attach_host_keys": (C.c_int, [C.c_void_p, C.c_int, C.c_void_p, C.c_size_t, C.c_void_p,
+                                              C.c_size_t, C.c_size_t]),
+    "mpcx_model_unique_key_bytes": (C.c_size_t, [C.c_void_p, C.c_int, C.c_int]),
+    "mpcx_model_export_unique_keys": (C.c_int, [C.c_void_p, C.c_int, C.c_void_p, C.c_size_t]),
     "mpcx_model_stream_stats": (C.c_int, [C.c_void_p, C.c_void_p, C.c_void_p]),
     "mpcx_adjnorm_key_bytes": (C.c_size_t, [C.c_void_p, C.c_int, C.c_int]),
     "mpcx_adjnorm_keygen": (C.c_int, [C.c_void_p, C.c_int, C.c_int, C.c_uint64, C.c_void_p, C.c_void_p,
@@ -460,13 +462,28 @@ class Model:
     def release_arena(self):
         self.ctx.check(self.lib.mpcx_model_release_arena(self.h), "release_arena")
 
+    def unique_key_bytes(self, B, party):
+        return int(self.lib.mpcx_model_unique_key_bytes(self.h, B, party))
+
+    def export_unique_keys(self, party, B, into=None):
+        """Party 1: its key planes that differ from party 0's, packed (party 0:
+        the whole arena)."""
+        n = self.unique_key_bytes(B, party)
+        out = np.zeros(n, np.uint8) if into is None else into
+        ptr = out.ptr if isinstance(out, PinnedBuffer) else out.ctypes.data_as(C.c_void_p)
+        self.ctx.check(self.lib.mpcx_model_export_unique_keys(self.h, party, ptr, n), "export_unique_keys")
+        return out
+
     def attach_host_keys(self, B, k0, k1, slot_bytes):
         """Stream keys from host buffers (PinnedBuffer for overlap) through two
-        device slots of slot_bytes per party."""
+        device slots of slot_bytes per party; k1 is party 1's whole arena or its
+        packed unique planes."""
         self._host_keys = (k0, k1)
         p0 = k0.ptr if isinstance(k0, PinnedBuffer) else k0.ctypes.data_as(C.c_void_p)
         p1 = k1.ptr if isinstance(k1, PinnedBuffer) else k1.ctypes.data_as(C.c_void_p)
-        self.ctx.check(self.lib.mpcx_model_attach_host_keys(self.h, B, p0, p1, self.key_bytes(B), int(slot_bytes)),
+        n0 = k0.nbytes
+        n1 = k1.nbytes
+        self.ctx.check(self.lib.mpcx_model_attach_host_keys(self.h, B, p0, n0, p1, n1, int(slot_bytes)),
                        "attach_host_keys")
 
     def stream_stats(self):

@@ -210,18 +210,27 @@ mpcx_status mpcx_model_import_keys(mpcx_model *m, int B, const void *h_key0, con
 mpcx_status mpcx_model_export_keys(mpcx_model *m, int party, void *h_dst, size_t bytes);
 /* Frees the resident key arenas (e.g. after mpcx_model_export_keys). */
 mpcx_status mpcx_model_release_arena(mpcx_model *m);
+/* The DCF correction and leaf words and the clear output mask are the same in
+ * both parties' keys; the evaluation reads them from party 0's copy.  Party 1's
+ * remaining ("unique") planes, packed back to back in arena order, are
+ * mpcx_model_unique_key_bytes(m, B, 1) bytes (about a tenth of its arena at
+ * bw=64); party 0's unique part is its whole arena. */
+size_t mpcx_model_unique_key_bytes(const mpcx_model *m, int B, int party);
+mpcx_status mpcx_model_export_unique_keys(mpcx_model *m, int party, void *h_dst, size_t bytes);
 /* Streaming key arena for batches whose keys do not stay resident: both parties'
- * keys (mpcx_model_key_bytes(m, B) bytes each, host memory, pinned for overlap)
- * are copied per chunk of consecutive gates into one of two device slots of at
- * most slot_bytes per party, on a copy stream, while the previous chunk
- * computes.  Replaces the chunked key pipeline of
- * gpu_mpc/deepdtagen_inference.cu:608-859 (pinned double-buffered slots, copy
- * stream, ready/free events) and setGPUKeyArenaSlot
+ * keys in host memory (pinned for overlap) are copied per chunk of consecutive
+ * gates into one of two device slots of at most slot_bytes per party, on a copy
+ * stream, while the previous chunk computes; party 1's shared planes are not
+ * copied.  h_key0: party 0's arena (bytes0 = mpcx_model_key_bytes); h_key1:
+ * party 1's arena (bytes1 = mpcx_model_key_bytes) or its packed unique planes
+ * (bytes1 = mpcx_model_unique_key_bytes(m, B, 1)).  Replaces the chunked key
+ * pipeline of gpu_mpc/deepdtagen_inference.cu:608-859 (pinned double-buffered
+ * slots, copy stream, ready/free events) and setGPUKeyArenaSlot
  * (patches/EzPC-GPU-MPC.track3.patch:680-685).  The resident arena is freed;
- * the host buffers must stay valid until the model is destroyed or keys are
- * imported again.  MPCX_EINVAL if a single gate's key exceeds slot_bytes. */
-mpcx_status mpcx_model_attach_host_keys(mpcx_model *m, int B, const void *h_key0, const void *h_key1,
-                                        size_t bytes, size_t slot_bytes);
+ * the host buffers must stay valid until the model is destroyed.  MPCX_EINVAL
+ * if a single gate's key exceeds slot_bytes. */
+mpcx_status mpcx_model_attach_host_keys(mpcx_model *m, int B, const void *h_key0, size_t bytes0,
+                                        const void *h_key1, size_t bytes1, size_t slot_bytes);
 /* Chunks and host-to-device key bytes (both parties) of the last forward. */
 mpcx_status mpcx_model_stream_stats(const mpcx_model *m, int *chunks, uint64_t *bytes_h2d);
 /* Both parties' input shares (host, ring elements): x (B,N,feat), adjacency
