@@ -104,6 +104,7 @@ struct GemmArgs {
   T *C = nullptr;
   size_t sA = 0, sB = 0, sC = 0;
   int sign = 1;
+  int ksplit = 1;  // set by launch_gemm: K slices accumulated with atomic adds
 };
 template <typename T>
 hipError_t launch_gemm(const Launch &L, const GemmArgs<T> &g);

@@ -16,6 +16,7 @@
 // tabulates all but the public floor(x'/2^s) over the 8 public cases.
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <type_traits>
 
 #include "dcf_dev.h"
@@ -814,13 +815,20 @@ hipError_t launch_lut8_phase2(const Launch &L, const Lut8Layout &lay, const uint
 // ring GEMM: 64x64 tile per 256-thread block, 4x4 outputs per thread,
 // K staged through LDS in slices of 16.  Integer multiply-add on the VALU
 // (v_mul_lo_u32 / v_mad_u64_u32); operand differences are applied on load.
+// Skinny products (the FC layers: M = batch) would leave most CUs idle, so K is
+// split across blocks (gridDim.z = batch * ksplit) and the partial sums are
+// added with atomics into C, which is first set to Cin (or 0): addition mod
+// 2^bw is associative and commutative, so the result does not depend on the
+// order in which the slices land.
 // ---------------------------------------------------------------------------
 template <typename T>
 __global__ __launch_bounds__(256) void k_gemm(GemmArgs<T> g) {
   constexpr int BM = 64, BN = 64, BK = 16;
   __shared__ T As[BK][BM + 1];
   __shared__ T Bs[BK][BN + 1];
-  const int bz = blockIdx.z;
+  const int bz = blockIdx.z / g.ksplit, kz = blockIdx.z % g.ksplit;
+  const int kchunk = ((g.K + g.ksplit - 1) / g.ksplit + BK - 1) / BK * BK;
+  const int kbeg = kz * kchunk, kend = min(g.K, kbeg + kchunk);
   const T *A1 = g.A1 + size_t(bz) * g.sA;
   const T *A2 = g.A2 ? g.A2 + size_t(bz) * g.sA : nullptr;
   const T *B1 = g.B1 + size_t(bz) * g.sB;
@@ -833,7 +841,7 @@ __global__ __launch_bounds__(256) void k_gemm(GemmArgs<T> g) {
   for (int i = 0; i < 4; i++)
 #pragma unroll
     for (int j = 0; j < 4; j++) acc[i][j] = 0;
-  for (int k0 = 0; k0 < g.K; k0 += BK) {
+  for (int k0 = kbeg; k0 < kend; k0 += BK) {
 #pragma unroll
     for (int r = 0; r < 4; r++) {
       const int e = tid + r * 256;  // 0..1023
@@ -841,7 +849,7 @@ __global__ __launch_bounds__(256) void k_gemm(GemmArgs<T> g) {
       const int am = e / BK, ak = e % BK;
       const int gm = m0 + am, gk = k0 + ak;
       T av = 0;
-      if (gm < g.M && gk < g.K) {
+      if (gm < g.M && gk < kend) {
         const size_t idx = size_t(gm) * g.K + gk;
         av = A1[idx];
         if (A2) av -= A2[idx];
@@ -851,7 +859,7 @@ __global__ __launch_bounds__(256) void k_gemm(GemmArgs<T> g) {
       const int bk = e / BN, bn = e % BN;
       const int gk2 = k0 + bk, gn = n0 + bn;
       T bv = 0;
-      if (gk2 < g.K && gn < g.N) {
+      if (gk2 < kend && gn < g.N) {
         const size_t idx = size_t(gk2) * g.N + gn;
         bv = B1[idx];
         if (B2) bv -= B2[idx];
@@ -884,17 +892,47 @@ __global__ __launch_bounds__(256) void k_gemm(GemmArgs<T> g) {
       const int gn = n0 + tc * 4 + j;
       if (gn >= g.N) continue;
       const size_t idx = size_t(gm) * g.N + gn;
-      T v = g.sign < 0 ? T(T(0) - acc[i][j]) : acc[i][j];
-      if (Cin) v += Cin[idx];
-      C[idx] = v;
+      const T v = g.sign < 0 ? T(T(0) - acc[i][j]) : acc[i][j];
+      if (g.ksplit > 1) {
+        if constexpr (sizeof(T) == 4)
+          atomicAdd(reinterpret_cast<unsigned int *>(&C[idx]), static_cast<unsigned int>(v));
+        else
+          atomicAdd(reinterpret_cast<unsigned long long *>(&C[idx]), static_cast<unsigned long long>(v));
+      } else {
+        C[idx] = Cin ? T(v + Cin[idx]) : v;
+      }
     }
   }
 }
 
+// C[b] = Cin[b] (or 0) before the split-K slices are added
 template <typename T>
-hipError_t launch_gemm(const Launch &L, const GemmArgs<T> &g) {
-  if (g.M <= 0 || g.N <= 0 || g.batch <= 0) return hipSuccess;
-  dim3 grid((g.N + 63) / 64, (g.M + 63) / 64, g.batch);
+__global__ void k_gemm_init(int M, int N, int batch, size_t sC, const T *Cin, T *C) {
+  const size_t per = size_t(M) * N, n = per * batch;
+  for (size_t i = size_t(blockIdx.x) * blockDim.x + threadIdx.x; i < n; i += size_t(gridDim.x) * blockDim.x) {
+    const size_t b = i / per, r = i % per;
+    C[b * sC + r] = Cin ? Cin[b * sC + r] : T(0);
+  }
+}
+
+template <typename T>
+hipError_t launch_gemm(const Launch &L, const GemmArgs<T> &g0) {
+  if (g0.M <= 0 || g0.N <= 0 || g0.batch <= 0) return hipSuccess;
+  GemmArgs<T> g = g0;
+  const int tiles = ((g.N + 63) / 64) * ((g.M + 63) / 64) * g.batch;
+  g.ksplit = 1;
+  if (tiles < L.num_cu && g.K >= 64) {
+    const int want = (2 * L.num_cu + tiles - 1) / tiles;
+    g.ksplit = std::max(1, std::min(want, g.K / 32));
+  }
+  if (g.ksplit > 1 && g.C != g.Cin) {
+    const int block = 256;
+    int grid = grid_for(k_gemm_init<T>, block, size_t(g.M) * g.N * g.batch, L.num_cu);
+    hipLaunchKernelGGL((k_gemm_init<T>), dim3(grid), dim3(block), 0, L.stream, g.M, g.N, g.batch, g.sC, g.Cin, g.C);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+  }
+  dim3 grid((g.N + 63) / 64, (g.M + 63) / 64, g.batch * g.ksplit);
   hipLaunchKernelGGL((k_gemm<T>), grid, dim3(256), 0, L.stream, g);
   return hipGetLastError();
 }

@@ -202,11 +202,15 @@ def test_sxs_keys_and_eval(ctx, orc):
     assert np.array_equal(signed(c.astype(np.uint64) - orc_, bw).reshape(nb, Mm, N), np.einsum("bmk,bkn->bmn", A, B))
 
 
-def test_ring_gemm(ctx, orc):
+@pytest.mark.parametrize("shape", [(130, 77, 65), (64, 1024, 128), (64, 512, 1), (3, 1000, 70), (64, 312, 1024)])
+def test_ring_gemm(ctx, orc, shape):
+    """Square-ish and skinny (FC-layer, split-K with atomic accumulation)
+    products mod 2^bw against the oracle's exact ring GEMM."""
     bw = ctx.bw
-    rng = np.random.default_rng(1)
-    A = rmask(rng, 130 * 77, bw).reshape(130, 77)
-    B = rmask(rng, 77 * 65, bw).reshape(77, 65)
+    M, K, N = shape
+    rng = np.random.default_rng(M * K + N)
+    A = rmask(rng, M * K, bw).reshape(M, K)
+    B = rmask(rng, K * N, bw).reshape(K, N)
     assert np.array_equal(ctx.ring_gemm(A, B).astype(np.uint64), orc.ring_gemm(bw, A, B))
 
 
