@@ -170,7 +170,7 @@ def main():
         import orc
         d = dims
         od = orc.make_dims(bw=d.bw, s=d.s, n_nodes=d.n_nodes, feat=d.feat, gcn=d.gcn, dfc=d.dfc, prot=d.prot,
-                           fus=d.fus, lut_nmax=d.lut_nmax)
+                           fus=d.fus, lut_nmax=d.lut_nmax, mask_scale=d.mask_scale)
         want, code = orc.plain_forward(od, wl.X, wl.A, wl.mask, wl.prot, wl.W)
         result["bit_exact"] = bool(code == 0 and np.array_equal(want, out))
         if not args.no_cpu:
@@ -248,7 +248,7 @@ def run_stream(args):
         import orc
         d = dims
         od = orc.make_dims(bw=d.bw, s=d.s, n_nodes=d.n_nodes, feat=d.feat, gcn=d.gcn, dfc=d.dfc, prot=d.prot,
-                           fus=d.fus, lut_nmax=d.lut_nmax)
+                           fus=d.fus, lut_nmax=d.lut_nmax, mask_scale=d.mask_scale)
         for wl in wls:
             y, code = orc.plain_forward(od, wl.X, wl.A, wl.mask, wl.prot, W)
             want.append(y if code == 0 else None)

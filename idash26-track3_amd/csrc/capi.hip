@@ -600,6 +600,7 @@ mpcx_status mpcx_model_create(mpcx_ctx *c, const mpcx_model_dims *dims, const in
   d.nfus = dims->nfus;
   for (int i = 0; i < 4; i++) d.fus[i] = dims->fus[i];
   d.lut_nmax = dims->lut_nmax;
+  d.mask_scale = dims->mask_scale;
   std::string err;
   ModelBase *impl = make_model(c->bw, c->s, d, W, nW, c->L, &err);
   if (!impl) return fail(c, MPCX_EINVAL, "model_create: " + err);

@@ -37,6 +37,7 @@ struct ModelDims {
   int nfus = 3;
   int fus[4] = {1024, 512, 1, 0};
   int lut_nmax = 138;
+  int mask_scale = 0;  // atom mask values are 0 or 2^mask_scale
 };
 
 struct Counters {

@@ -676,8 +676,8 @@ class Model final : public ModelBase, KeySource {
     }
     // pool
     const int C = d_.gcn[2];
-    const T S = T(1) << (bw - 2);
-    TRY(launch_pool_prep<T>(L_, BN, C, rX.p, rm.p, S, T(0), t2.p));  // rV in t2
+    const T Sm = T(1) << (bw - 2 - d_.mask_scale);
+    TRY(launch_pool_prep<T>(L_, BN, C, rX.p, rm.p, Sm, T(0), t2.p));  // rV in t2
     T *cur = t2.p, *nxt = rX.p;
     int pairs[32];
     const int Lv = pool_levels(N, pairs);
@@ -934,10 +934,11 @@ class Model final : public ModelBase, KeySource {
       TRY(r.sxs(B, N, N, fo, An_.p, XW, Z));
       TRY(r.tr(G_TRRELU, En, Z, bias_[l].p, fo, H));
     }
-    // masked max-pool: V = H + S*m^ - S, then a tree of max(a,b) = a + ReLU(b-a)
+    // masked max-pool: V = H + 2^(bw-2-ms) m^ - 2^(bw-2) (the sentinel -2^(bw-2) on
+    // padding rows for a mask of 0 or 2^ms), then a tree of max(a,b) = a + ReLU(b-a)
     const int C = d_.gcn[2];
-    const T S = T(1) << (bw - 2);
-    TRY(launch_pool_prep<T>(L_, BN, C, H, mh_.p, S, T(0) - S, V0_.p));
+    const T S = T(1) << (bw - 2), Sm = T(1) << (bw - 2 - d_.mask_scale);
+    TRY(launch_pool_prep<T>(L_, BN, C, H, mh_.p, Sm, T(0) - S, V0_.p));
     T *cur = V0_.p, *nxt = V1_.p;
     int pairs[32];
     const int Lv = pool_levels(N, pairs);
@@ -1033,6 +1034,10 @@ ModelBase *make_model(int bw, int s, const ModelDims &d, const int64_t *W, size_
   }
   if (d.n_nodes < 1 || d.n_nodes > 255) {
     *err = "n_nodes must be in [1, 255] (8-bit degree LUT domain)";
+    return nullptr;
+  }
+  if (d.mask_scale < 0 || d.mask_scale > bw - 2 - 1) {
+    *err = "mask_scale must be in [0, bw - 3]";
     return nullptr;
   }
   if (bw == 32) return make_model_t<uint32_t>(bw, s, d, W, nW, L, err);

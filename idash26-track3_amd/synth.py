@@ -36,6 +36,7 @@ class Dims:
     prot: int = 128
     fus: tuple = (1024, 512, 1)
     lut_nmax: int = 138
+    mask_scale: int = 0  # the atom mask is 0 or 2^mask_scale
 
     def layers(self):
         """(in, out) of every linear layer in weight-blob order."""

@@ -194,6 +194,8 @@ typedef struct {
   int nfus;     /* fusion layers (last has width 1) */
   int fus[4];
   int lut_nmax; /* largest degree with a D^-1/2 table entry */
+  int mask_scale; /* atom mask values are 0 or 2^mask_scale: 0, or s for the reference's
+                     mask files (reference/share_data.py:135-159 shares the mask at scale s) */
 } mpcx_model_dims;
 
 mpcx_status mpcx_model_create(mpcx_ctx *ctx, const mpcx_model_dims *dims, const int64_t *h_weights,

@@ -192,6 +192,7 @@ typedef struct {
   int nfus;       /* number of fusion layers (last has width 1) */
   int fus[4];     /* fusion widths */
   int lut_nmax;   /* largest degree with a table entry (mpc_config.py NMAX) */
+  int mask_scale; /* the atom mask is 0 or 2^mask_scale (0; s for the reference's files) */
 } orc_dims;
 
 /* Weights: for each linear layer in order gcn0..2, dfc0..1, fus0..nfus-1:

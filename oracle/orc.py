@@ -21,7 +21,8 @@ _lib = None
 class Dims(C.Structure):
     _fields_ = [("bw", C.c_int), ("s", C.c_int), ("n_nodes", C.c_int), ("feat", C.c_int),
                 ("gcn", C.c_int * 3), ("dfc", C.c_int * 2), ("prot", C.c_int),
-                ("nfus", C.c_int), ("fus", C.c_int * 4), ("lut_nmax", C.c_int)]
+                ("nfus", C.c_int), ("fus", C.c_int * 4), ("lut_nmax", C.c_int),
+                ("mask_scale", C.c_int)]
 
 
 class DcfLayout(C.Structure):
@@ -38,7 +39,7 @@ class TrLayout(C.Structure):
 
 
 def make_dims(bw=32, s=12, n_nodes=140, feat=78, gcn=(78, 156, 312), dfc=(1024, 128), prot=128,
-              fus=(1024, 512, 1), lut_nmax=138):
+              fus=(1024, 512, 1), lut_nmax=138, mask_scale=0):
     d = Dims()
     d.bw, d.s, d.n_nodes, d.feat = bw, s, n_nodes, feat
     for i, v in enumerate(gcn):
@@ -50,6 +51,7 @@ def make_dims(bw=32, s=12, n_nodes=140, feat=78, gcn=(78, 156, 312), dfc=(1024, 
     for i, v in enumerate(fus):
         d.fus[i] = v
     d.lut_nmax = lut_nmax
+    d.mask_scale = mask_scale
     return d
 
 

@@ -198,7 +198,7 @@ int orc_plain_forward(const orc_dims *d, int B, const int64_t *X, const int64_t 
     int nreal = 0;
     for (int i = 0; i < N; i++) {
       int64_t mv = mask[(size_t)b * N + i];
-      if (mv != 0 && mv != 1) f.err = f.err ? f.err : 6;
+      if (mv != 0 && mv != ((int64_t)1 << d->mask_scale)) f.err = f.err ? f.err : 6;
       nreal += mv != 0;
     }
     if (nreal == 0) seterr(&f, 4);
@@ -500,9 +500,11 @@ int orc_model_keygen(const orc_dims *d, int B, uint64_t seed, const int64_t *W, 
   }
   /* pool: V = H3 + S*m - S, mask rH3 + S*rm */
   const int C = d->gcn[2];
-  const uint64_t S = 1ull << (bw - 2);
+  /* V = H + 2^(bw-2-ms) m - 2^(bw-2): the sentinel -2^(bw-2) on padding rows for a
+   * mask of 0 or 2^ms (ms = mask_scale) */
+  const uint64_t Sm = 1ull << (bw - 2 - d->mask_scale);
   for (size_t r = 0; r < BN; r++)
-    for (int c = 0; c < C; c++) rX[r * C + c] = (rX[r * C + c] + S * rm[r]) & M;
+    for (int c = 0; c < C; c++) rX[r * C + c] = (rX[r * C + c] + Sm * rm[r]) & M;
   int pairs[32];
   int L = pool_levels(N, pairs), R = N;
   for (int l = 0; l < L; l++) {
@@ -626,9 +628,9 @@ int orc_model_eval(const orc_dims *d, int B, const int64_t *W, const uint8_t *k0
     fin = fo;
   }
   const int C = d->gcn[2];
-  const uint64_t S = 1ull << (bw - 2);
+  const uint64_t S = 1ull << (bw - 2), Sm = 1ull << (bw - 2 - d->mask_scale);
   for (size_t r = 0; r < BN; r++)
-    for (int c = 0; c < C; c++) H[r * C + c] = (H[r * C + c] + S * mh[r] - S) & M;
+    for (int c = 0; c < C; c++) H[r * C + c] = (H[r * C + c] + Sm * mh[r] - S) & M;
   int pairs[32];
   int L = pool_levels(N, pairs), R = N;
   for (int l = 0; l < L; l++) {

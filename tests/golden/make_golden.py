@@ -33,7 +33,7 @@ from golden_dims import SMALL  # noqa: E402
 
 def odims(d):
     return orc.make_dims(bw=d.bw, s=d.s, n_nodes=d.n_nodes, feat=d.feat, gcn=d.gcn, dfc=d.dfc, prot=d.prot,
-                         fus=d.fus, lut_nmax=d.lut_nmax)
+                         fus=d.fus, lut_nmax=d.lut_nmax, mask_scale=d.mask_scale)
 
 
 def workload_digest(wl):

@@ -77,7 +77,7 @@ def test_model_small_fixture(orc, synth):
     for bw in (32, 64):
         d = synth.Dims(bw=bw, **SMALL)
         od = orc.make_dims(bw=bw, s=12, n_nodes=d.n_nodes, feat=d.feat, gcn=d.gcn, dfc=d.dfc, prot=d.prot,
-                           fus=d.fus, lut_nmax=d.lut_nmax)
+                           fus=d.fus, lut_nmax=d.lut_nmax, mask_scale=d.mask_scale)
         y, code = orc.plain_forward(od, f["X"], f["A"], f["mask"], f["prot"], f["W"])
         assert code == 0
         assert np.array_equal(y, f[f"want_bw{bw}"])
@@ -94,7 +94,7 @@ def test_model_default_fixture(orc, synth):
         assert h.hexdigest() == rec["inputs_sha256"], "synthetic generator changed"
         d = wl.dims
         od = orc.make_dims(bw=bw, s=12, n_nodes=d.n_nodes, feat=d.feat, gcn=d.gcn, dfc=d.dfc, prot=d.prot,
-                           fus=d.fus, lut_nmax=d.lut_nmax)
+                           fus=d.fus, lut_nmax=d.lut_nmax, mask_scale=d.mask_scale)
         y, code = orc.plain_forward(od, wl.X, wl.A, wl.mask, wl.prot, wl.W)
         assert code == 0
         assert y.tolist() == rec[f"want_bw{bw}"]

@@ -231,7 +231,7 @@ def test_reveal_keys_and_eval(ctx, orc):
 # ---------------------------------------------------------------------------
 def _od(orc, dims):
     return orc.make_dims(bw=dims.bw, s=dims.s, n_nodes=dims.n_nodes, feat=dims.feat, gcn=dims.gcn, dfc=dims.dfc,
-                         prot=dims.prot, fus=dims.fus, lut_nmax=dims.lut_nmax)
+                         prot=dims.prot, fus=dims.fus, lut_nmax=dims.lut_nmax, mask_scale=dims.mask_scale)
 
 
 @pytest.mark.parametrize("bw", [32, 64])
@@ -444,4 +444,34 @@ def test_relu_config1_full_size(mp):
     k0, k1, rout = c.tr_keygen(3, rin, seed=12, gate=1)
     y = c.tr_eval(3, k0, k1, (x.astype(np.uint64) + rin) & M(32))
     assert np.array_equal(signed(y.astype(np.uint64) - rout.astype(np.uint64), 32), np.maximum(x, 0))
+    c.close()
+
+
+# ---------------------------------------------------------------------------
+# inputs from the reference's file formats
+# ---------------------------------------------------------------------------
+@pytest.mark.parametrize("bw", [32, 64])
+def test_model_on_reference_files(mp, orc, synth, tmp_path, bw):
+    """Shares, protein rows and weights written in the reference's layout
+    (mask pre-tiled at scale s) load into the model with mask_scale = s and
+    reconstruct the plaintext forward exactly."""
+    import formats
+    B = 3
+    wl = synth.workload(B, synth.Dims(bw=bw), seed=12)
+    bdir = str(tmp_path / "batch")
+    formats.write_batch(bdir, wl.X, wl.A, wl.mask, wl.prot, bw=bw, scale=12, pool_dim=312, seed=5)
+    wpath = str(tmp_path / "weights.bin")
+    formats.write_weights(wpath, wl.W, wl.dims.layers(), scale=12)
+    got = formats.read_batch(bdir)
+    blob, layers, _ = formats.read_weights(wpath)
+    dims = formats.dims_from_weights(layers, n_nodes=140, bw=bw, mask_scale=got["mask_scale"])
+    want, code = orc.plain_forward(_od(orc, synth.Dims(bw=bw)), wl.X, wl.A, wl.mask, wl.prot, wl.W)
+    assert code == 0
+    c = mp.Ctx(bw=bw)
+    m = mp.Model(c, dims, blob)
+    m.keygen(B, 8)
+    m.set_inputs(B, *got["x"], *got["a"], *got["m"], got["prot"])
+    m.forward(B)
+    assert np.array_equal(m.output(B), want)
+    m.close()
     c.close()

@@ -93,7 +93,7 @@ def _wl(synth, B, bw=32, seed=0, n_nodes=140):
 def _od(orc, wl):
     d = wl.dims
     return orc.make_dims(bw=d.bw, s=d.s, n_nodes=d.n_nodes, feat=d.feat, gcn=d.gcn, dfc=d.dfc, prot=d.prot,
-                         fus=d.fus, lut_nmax=d.lut_nmax)
+                         fus=d.fus, lut_nmax=d.lut_nmax, mask_scale=d.mask_scale)
 
 
 def test_permutation_invariance(orc, synth):
