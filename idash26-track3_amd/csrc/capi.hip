@@ -142,6 +142,8 @@ void mpcx_destroy(mpcx_ctx *c) {
 }
 
 const char *mpcx_last_error(const mpcx_ctx *c) { return c ? c->err.c_str() : "null context"; }
+int mpcx_bw(const mpcx_ctx *c) { return c ? c->bw : 0; }
+int mpcx_scale(const mpcx_ctx *c) { return c ? c->s : 0; }
 
 mpcx_status mpcx_set_stream(mpcx_ctx *c, void *s) {
   CHECK_CTX(c);
@@ -504,6 +506,27 @@ mpcx_status mpcx_ring_gemm(mpcx_ctx *c, int M, int K, int N, const void *a, cons
   CHECK_CTX(c);
   if (M < 1 || K < 1 || N < 1 || !a || !b || !out) return fail(c, MPCX_EINVAL, "ring_gemm: bad argument");
   return c->bw == 32 ? gemm_t<uint32_t>(c, M, K, N, a, b, out) : gemm_t<uint64_t>(c, M, K, N, a, b, out);
+}
+
+// ---------------- local linear maps ----------------
+mpcx_status mpcx_ring_lincomb(mpcx_ctx *c, size_t rows, size_t cols, uint64_t a, const void *x, uint64_t b,
+                              const void *y, const void *v, int shift, void *out) {
+  CHECK_CTX(c);
+  if (!out || cols == 0 || shift < 0 || shift >= c->bw) return fail(c, MPCX_EINVAL, "ring_lincomb: bad argument");
+  if (c->bw == 32) {
+    HIPC(c,
+         launch_lincomb<uint32_t>(c->L, rows, cols, uint32_t(a), static_cast<const uint32_t *>(x), uint32_t(b),
+                                  static_cast<const uint32_t *>(y), static_cast<const uint32_t *>(v), shift,
+                                  static_cast<uint32_t *>(out)),
+         "ring_lincomb");
+  } else {
+    HIPC(c,
+         launch_lincomb<uint64_t>(c->L, rows, cols, a, static_cast<const uint64_t *>(x), b,
+                                  static_cast<const uint64_t *>(y), static_cast<const uint64_t *>(v), shift,
+                                  static_cast<uint64_t *>(out)),
+         "ring_lincomb");
+  }
+  return MPCX_OK;
 }
 
 // ---------------- reveal ----------------

@@ -119,6 +119,10 @@ hipError_t launch_prf_ring(const Launch &L, uint64_t seed, uint32_t gate, uint32
 // ---------------- elementwise ----------------
 template <typename T>
 hipError_t launch_axpby(const Launch &L, size_t n, T a, const T *x, T b, const T *y, T c, T *out);
+// out[r*cols+c] = a*x + b*y + (v[c] << shift); x, y, v may be null
+template <typename T>
+hipError_t launch_lincomb(const Launch &L, size_t rows, size_t cols, T a, const T *x, T b, const T *y, const T *v,
+                          int shift, T *out);
 // pool prep: V[r*C+c] = H[r*C+c] + S*m[r] + off
 template <typename T>
 hipError_t launch_pool_prep(const Launch &L, size_t rows, int C, const T *H, const T *m, T S, T off, T *V);

@@ -978,6 +978,26 @@ hipError_t launch_axpby(const Launch &L, size_t n, T a, const T *x, T b, const T
 }
 
 template <typename T>
+__global__ void k_lincomb(size_t rows, size_t cols, T a, const T *x, T b, const T *y, const T *v, int shift, T *out) {
+  const size_t n = rows * cols;
+  for (size_t i = size_t(blockIdx.x) * blockDim.x + threadIdx.x; i < n; i += size_t(gridDim.x) * blockDim.x) {
+    T r = 0;
+    if (x) r += a * x[i];
+    if (y) r += b * y[i];
+    if (v) r += v[i % cols] << shift;
+    out[i] = r;
+  }
+}
+template <typename T>
+hipError_t launch_lincomb(const Launch &L, size_t rows, size_t cols, T a, const T *x, T b, const T *y, const T *v,
+                          int shift, T *out) {
+  const int block = 256;
+  int grid = grid_for(k_lincomb<T>, block, rows * cols, L.num_cu);
+  hipLaunchKernelGGL((k_lincomb<T>), dim3(grid), dim3(block), 0, L.stream, rows, cols, a, x, b, y, v, shift, out);
+  return hipGetLastError();
+}
+
+template <typename T>
 __global__ void k_pool_prep(size_t rows, int C, const T *H, const T *m, T S, T off, T *V) {
   const size_t n = rows * size_t(C);
   for (size_t i = size_t(blockIdx.x) * blockDim.x + threadIdx.x; i < n; i += size_t(gridDim.x) * blockDim.x)
@@ -1123,6 +1143,8 @@ hipError_t launch_rowsum(const Launch &L, size_t rows, int len, const T *a, T *o
                                       T *);                                                                          \
   template hipError_t launch_prf_ring<T>(const Launch &, uint64_t, uint32_t, uint32_t, size_t, T *);                \
   template hipError_t launch_axpby<T>(const Launch &, size_t, T, const T *, T, const T *, T, T *);                   \
+  template hipError_t launch_lincomb<T>(const Launch &, size_t, size_t, T, const T *, T, const T *, const T *, int,   \
+                                        T *);                                                                        \
   template hipError_t launch_pool_prep<T>(const Launch &, size_t, int, const T *, const T *, T, T, T *);            \
   template hipError_t launch_pool_diff<T>(const Launch &, int, int, int, const T *, T *);                            \
   template hipError_t launch_pool_combine<T>(const Launch &, int, int, int, const T *, const T *, const T *, T *);   \

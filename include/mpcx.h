@@ -46,6 +46,9 @@ typedef struct mpcx_model mpcx_model;
 mpcx_status mpcx_create(int bw, int scale, int device, mpcx_ctx **out);
 void mpcx_destroy(mpcx_ctx *ctx);
 const char *mpcx_last_error(const mpcx_ctx *ctx);
+/* Ring width and fixed-point scale of the context. */
+int mpcx_bw(const mpcx_ctx *ctx);
+int mpcx_scale(const mpcx_ctx *ctx);
 /* hipStream_t; NULL = the context's own stream */
 mpcx_status mpcx_set_stream(mpcx_ctx *ctx, void *hip_stream);
 mpcx_status mpcx_synchronize(mpcx_ctx *ctx);
@@ -150,6 +153,16 @@ mpcx_status mpcx_sxs_eval(mpcx_ctx *ctx, int nb, int M, int K, int N, const void
  * key and no exchange when the output mask is r_A . W). */
 mpcx_status mpcx_ring_gemm(mpcx_ctx *ctx, int M, int K, int N, const void *d_a, const void *d_b,
                            void *d_c);
+
+/* Local linear map on masked-public ring tensors (rows x cols, row-major):
+ * out = a*x + b*y + (v[col] << shift), x, y or v may be NULL.  Linear maps need no
+ * key and no exchange: the evaluators apply them to masked values and the dealer
+ * to the masks (with v = NULL, since a public addend has mask 0).  Replaces
+ * gpuLinearComb / gpuAdd behind the backend's add, sub and scalarmul
+ * (gpu_mpc/ddg_orca_base.h:304-314, gpu_mpc/ddg_orca.h:65-81) and the bias add of
+ * the 4-argument matmul (ddg_orca_base.h:208-271, bias at scale 2s). */
+mpcx_status mpcx_ring_lincomb(mpcx_ctx *ctx, size_t rows, size_t cols, uint64_t a, const void *d_x, uint64_t b,
+                              const void *d_y, const void *d_v, int shift, void *d_out);
 
 /* ---------------- reveal ----------------
  * Additive shares v0, v1 -> masked public v + r (revealIfLeaf,
