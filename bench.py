@@ -30,8 +30,7 @@ HBM_PEAK_GBS = 8000.0
 # the same counter's reading for a 1 GiB elementwise copy (FETCH_SIZE x 2.0,
 # WRITE_SIZE x 1.0); the summary is profiles/k_tr_phase1_affinity_bw32_B64.md.
 TRAFFIC_BYTES_PER_LAUNCH = {"perm64_b512": 689753000}
-VALU_OPS_PER_AES = {"perm64_b512": 402, "perm64_b1024": 402, "t4_rep32_b1024": 462, "t4_rep16_b512": 462,
-                    "t1_rep32_b512": 486}
+VALU_OPS_PER_AES = {"perm64_b512": 402, "perm64_b1024": 402, "t4_rep32_b1024": 462}
 
 
 def log(msg):

@@ -178,17 +178,21 @@ struct AesTab {
 };
 
 // T0 alone, 64 copies per entry: entry x, copy j at byte address 256*x + 4*j.
-// Lane l reads copy l mod 64, so a wavefront never has two lanes on one bank, and the
-// byte address of "T0[byte k of c] for this lane" is one v_perm_b32:
-//   byte 0 = (lane*4) mod 256, byte 1 = byte k of c, bytes 2..3 = 0.
-// T1..T3 are rotations of T0 (v_alignbit_b32), three-input XORs are v_bitop3_b32,
-// and the last round gathers the S-box bytes (byte 1 of T0) with v_perm_b32.
+// Lane l reads copy l mod 64, so a wavefront never has two lanes on one bank,
+// and the byte address of "T0[byte k of c]" for this lane is one v_perm_b32 of
+// (c, lane word): byte 0 = (lane*4) mod 256, byte 1 = byte k of c, bytes 2..3 = 0.
+// T1..T3 are rotations of T0 (v_alignbit_b32), three-input XORs are
+// v_bitop3_b32, and the last round gathers the S-box bytes (byte 1 of T0) with
+// v_perm_b32.  The hash folds sigma into the first AddRoundKey and the
+// feed-forward into the last one.  (Holding T1 as a second 64 KiB table saves
+// two rotations per column but leaves room for only one workgroup per CU; it
+// measured slower.)
 struct AesPerm {
   static constexpr int kWords = 256 * 64;
   static constexpr int kBytes = kWords * 4;
 
   const char *base;
-  uint32_t lane4;
+  uint32_t lane4;  // (lane * 4) mod 256
 
   __device__ static void fill(uint32_t *lds) {
     for (int w = threadIdx.x; w < kWords; w += blockDim.x) lds[w] = c_T0.v[w >> 6];
@@ -198,8 +202,9 @@ struct AesPerm {
   __device__ AesPerm(const uint32_t *lds) : base((const char *)lds) { lane4 = (threadIdx.x & 63u) * 4u; }
 
   // T0[byte K of c]
-  template <int K>
+  template <int t, int K>
   __device__ __forceinline__ uint32_t L(uint32_t c) const {
+    static_assert(t == 0, "one table");
     const uint32_t addr = __builtin_amdgcn_perm(c, lane4, 0x0c0c0000u | ((4u + K) << 8));
     return *(const uint32_t *)(base + addr);
   }
@@ -209,17 +214,18 @@ struct AesPerm {
     return K == 0 ? v : __builtin_amdgcn_alignbit(v, v, 32 - 8 * K);
   }
   __device__ __forceinline__ uint32_t col(uint32_t a, uint32_t b, uint32_t c, uint32_t d, uint32_t k) const {
-    return xor3(xor3(L<0>(a), rot<1>(L<1>(b)), rot<2>(L<2>(c))), rot<3>(L<3>(d)), k);
+    return xor3(xor3(L<0, 0>(a), rot<1>(L<0, 1>(b)), rot<2>(L<0, 2>(c))), rot<3>(L<0, 3>(d)), k);
   }
-  // S[byte 0 of a] | S[byte 1 of b] << 8 | S[byte 2 of c] << 16 | S[byte 3 of d] << 24, ^ k
-  __device__ __forceinline__ uint32_t last(uint32_t a, uint32_t b, uint32_t c, uint32_t d, uint32_t k) const {
-    const uint32_t lo = __builtin_amdgcn_perm(L<1>(b), L<0>(a), 0x0c0c0501u);
-    const uint32_t hi = __builtin_amdgcn_perm(L<3>(d), L<2>(c), 0x0c0c0501u);
-    return ((hi << 16) | lo) ^ k;
+  // S[byte 0 of a] | S[byte 1 of b] << 8 | S[byte 2 of c] << 16 | S[byte 3 of d] << 24
+  __device__ __forceinline__ uint32_t last(uint32_t a, uint32_t b, uint32_t c, uint32_t d) const {
+    const uint32_t lo = __builtin_amdgcn_perm(L<0, 1>(b), L<0, 0>(a), 0x0c0c0501u);
+    const uint32_t hi = __builtin_amdgcn_perm(L<0, 3>(d), L<0, 2>(c), 0x0c0c0501u);
+    return (hi << 16) | lo;
   }
 
-  __device__ __forceinline__ uint4 enc(uint4 in, const AesRK &rk) const {
-    uint32_t c0 = in.x ^ rk.w[0], c1 = in.y ^ rk.w[1], c2 = in.z ^ rk.w[2], c3 = in.w ^ rk.w[3];
+  // rounds 1..9 on the whitened state
+  __device__ __forceinline__ void rounds(uint32_t &c0, uint32_t &c1, uint32_t &c2, uint32_t &c3,
+                                         const AesRK &rk) const {
 #pragma unroll
     for (int r = 1; r < 10; r++) {
       const uint32_t n0 = col(c0, c1, c2, c3, rk.w[4 * r + 0]);
@@ -231,28 +237,33 @@ struct AesPerm {
       c2 = n2;
       c3 = n3;
     }
+  }
+
+  __device__ __forceinline__ uint4 enc(uint4 in, const AesRK &rk) const {
+    uint32_t c0 = in.x ^ rk.w[0], c1 = in.y ^ rk.w[1], c2 = in.z ^ rk.w[2], c3 = in.w ^ rk.w[3];
+    rounds(c0, c1, c2, c3, rk);
     uint4 o;
-    o.x = last(c0, c1, c2, c3, rk.w[40]);
-    o.y = last(c1, c2, c3, c0, rk.w[41]);
-    o.z = last(c2, c3, c0, c1, rk.w[42]);
-    o.w = last(c3, c0, c1, c2, rk.w[43]);
+    o.x = last(c0, c1, c2, c3) ^ rk.w[40];
+    o.y = last(c1, c2, c3, c0) ^ rk.w[41];
+    o.z = last(c2, c3, c0, c1) ^ rk.w[42];
+    o.w = last(c3, c0, c1, c2) ^ rk.w[43];
     return o;
   }
 
+  // H(s) = AES_k(sigma(s)) ^ sigma(s), sigma(xL||xR) = (xL^xR)||xL, xR = words 0,1
   __device__ __forceinline__ uint4 hash(uint4 s, const AesRK &rk) const {
-    uint4 x;
-    x.x = s.z;
-    x.y = s.w;
-    x.z = s.z ^ s.x;
-    x.w = s.w ^ s.y;
-    uint4 y = enc(x, rk);
-    y.x ^= x.x;
-    y.y ^= x.y;
-    y.z ^= x.z;
-    y.w ^= x.w;
-    return y;
+    uint32_t c0 = s.z ^ rk.w[0], c1 = s.w ^ rk.w[1];
+    uint32_t c2 = xor3(s.z, s.x, rk.w[2]), c3 = xor3(s.w, s.y, rk.w[3]);
+    rounds(c0, c1, c2, c3, rk);
+    uint4 o;
+    o.x = xor3(last(c0, c1, c2, c3), rk.w[40], s.z);
+    o.y = xor3(last(c1, c2, c3, c0), rk.w[41], s.w);
+    o.z = xor3(last(c2, c3, c0, c1), rk.w[42], s.z) ^ s.x;
+    o.w = xor3(last(c3, c0, c1, c2), rk.w[43], s.w) ^ s.y;
+    return o;
   }
 
+  // Dealer PRF block AES_kd(idx_lo, idx_hi, field, gate).
   __device__ __forceinline__ uint4 prf(const AesRK &kd, uint32_t gate, uint32_t field, uint64_t idx) const {
     uint4 b;
     b.x = uint32_t(idx);
@@ -275,6 +286,13 @@ struct AesSel<0, 64> {
 template <int NT, int REP>
 using AesLds = typename AesSel<NT, REP>::type;
 
+// a ^ (b & m) in one v_bitop3_b32 (truth table 0x78 = 0xf0 ^ (0xcc & 0xaa))
+__device__ __forceinline__ uint32_t xor_and(uint32_t a, uint32_t b, uint32_t m) {
+  return __builtin_amdgcn_bitop3_b32(a, b, m, 0x78);
+}
+__device__ __forceinline__ uint4 xor_and4(uint4 a, uint4 b, uint32_t m) {
+  return make_uint4(xor_and(a.x, b.x, m), xor_and(a.y, b.y, m), xor_and(a.z, b.z, m), xor_and(a.w, b.w, m));
+}
 __device__ __forceinline__ uint4 xor4(uint4 a, uint4 b) {
   return make_uint4(a.x ^ b.x, a.y ^ b.y, a.z ^ b.z, a.w ^ b.w);
 }

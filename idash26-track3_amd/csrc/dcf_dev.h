@@ -22,18 +22,23 @@ __device__ __forceinline__ uint32_t dcf_eval_walk(const A &aes, uint4 s,
                                                   uint4 leaf, uint64_t x) {
   uint32_t t = s.x & 1u, out = 0;
   uint4 cnext = L > 0 ? cw[0] : make_uint4(0, 0, 0, 0);
+  // the path bits of x, MSB first: levels consume x >> (m-1-l); for m <= 32 the
+  // walk stays in 32-bit registers
+  const bool wide = m > 32;
+  const uint32_t xlo = uint32_t(x);
   for (int l = 0; l < L; l++) {
     const uint4 c = cnext;
     if (l + 1 < L) cnext = cw[size_t(l + 1) * stride];
-    const uint32_t bit = uint32_t(x >> (m - 1 - l)) & 1u;
+    const int sh = m - 1 - l;
+    const uint32_t bit = wide ? uint32_t(x >> sh) & 1u : (xlo >> sh) & 1u;
     const uint4 h = aes.hash(s, c_rkH);
-    const uint4 sl = xor4(h, and4(c, 0u - t));
+    const uint4 sl = xor_and4(h, c, 0u - t);
     const uint32_t tl = sl.x & 1u;
     out ^= (bit ^ 1u) & (tl ^ t);
-    s = xor4(sl, and4(s, 0u - bit));
+    s = xor_and4(sl, s, 0u - bit);
     t = tl ^ (t & bit);
   }
-  const uint4 lb = xor4(aes.hash(s, c_rkL), and4(leaf, 0u - t));
+  const uint4 lb = xor_and4(aes.hash(s, c_rkL), leaf, 0u - t);
   const uint32_t pos = m >= 7 ? uint32_t(x & 127u) : uint32_t(x);
   return out ^ parity_above(lb, pos);
 }

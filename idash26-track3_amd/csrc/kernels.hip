@@ -28,8 +28,9 @@ namespace mpcx {
 // AES LDS variants
 // ---------------------------------------------------------------------------
 static const AesVariant kVariants[] = {
-    {0, 64, 512, "perm64_b512"},   {0, 64, 1024, "perm64_b1024"}, {4, 32, 1024, "t4_rep32_b1024"},
-    {4, 16, 512, "t4_rep16_b512"}, {1, 32, 512, "t1_rep32_b512"},
+    {0, 64, 512, "perm64_b512"},
+    {0, 64, 1024, "perm64_b1024"},
+    {4, 32, 1024, "t4_rep32_b1024"},
 };
 const AesVariant *aes_variants(int *count) {
   *count = int(sizeof(kVariants) / sizeof(kVariants[0]));
@@ -47,8 +48,6 @@ static hipError_t with_variant(const Launch &L, Fn &&fn) {
     case 0: return fn(V<0, 64>{});
     case 1: return fn(V<0, 64>{});
     case 2: return fn(V<4, 32>{});
-    case 3: return fn(V<4, 16>{});
-    case 4: return fn(V<1, 32>{});
     default: return hipErrorInvalidValue;
   }
 }
