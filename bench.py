@@ -26,10 +26,11 @@ HBM_PEAK_GBS = 8000.0
 # of this build: hipcc --cuda-device-only -S csrc/kernels.hip, level-loop block
 # of k_tr_phase1<uint32_t, NT, REP> for each LDS table variant.
 # HBM bytes per k_tr_phase1 launch measured with rocprofv3 --pmc FETCH_SIZE and
-# WRITE_SIZE on this bench command (19 launches per forward, mean), each scaled by
-# the same counter's reading for a 1 GiB elementwise copy (FETCH_SIZE x 2.0,
-# WRITE_SIZE x 1.0); the summary is profiles/k_tr_phase1_affinity_bw32_B64.md.
-TRAFFIC_BYTES_PER_LAUNCH = {"perm64_b512": 689753000}
+# WRITE_SIZE on this bench command (mean over the profiled forward's launches,
+# 19 per lane), each scaled by the same counter's reading for a 1 GiB elementwise
+# copy (FETCH_SIZE x 2.0, WRITE_SIZE x 1.0); keyed by (variant, B, bw, lanes).
+# The summary is profiles/k_tr_phase1_affinity_bw32_B64.md.
+TRAFFIC_BYTES_PER_LAUNCH = {("perm64_b512", 64, 32, 3): 229643024, ("perm64_b512", 64, 32, 1): 689753000}
 VALU_OPS_PER_AES = {"perm64_b512": 402, "perm64_b1024": 402, "t4_rep32_b1024": 462}
 
 
@@ -49,6 +50,11 @@ def main():
     ap.add_argument("--cpu-seconds", type=float, default=10.0, help="minimum timed CPU baseline work")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--aes-variant", type=int, default=-1)
+    ap.add_argument("--lanes", type=int, default=3, help="concurrent sub-batches, each on its own stream")
+    ap.add_argument("--workload", choices=("affinity", "relu", "adjnorm"), default="affinity",
+                    help="affinity: the secure forward (default); relu: secure ReLU over --n elements (bw=32); "
+                         "adjnorm: secure adjacency normalisation of B=1024 graphs (bw=32)")
+    ap.add_argument("--n", type=int, default=1 << 24, help="elements of the relu workload")
     ap.add_argument("--stream", action="store_true",
                     help="bw=64 streamed-key workload: micro-batches of --batch (default 256) over --total samples, "
                          "keys in pinned host memory copied through two device slots")
@@ -64,6 +70,10 @@ def main():
 
     if args.stream:
         return run_stream(args)
+    if args.workload == "relu":
+        return run_relu(args)
+    if args.workload == "adjnorm":
+        return run_adjnorm(args)
 
     import numpy as np
 
@@ -79,7 +89,7 @@ def main():
     ctx = mpcx.Ctx(bw=args.bw, scale=dims.s)
     if args.aes_variant >= 0:
         ctx.set_aes_variant(args.aes_variant)
-    model = mpcx.Model(ctx, dims, wl.W)
+    model = mpcx.Model(ctx, dims, wl.W, lanes=args.lanes)
     key_bytes = model.key_bytes(B)
     t0 = time.time()
     model.keygen(B, 0xC0FFEE + args.seed)
@@ -103,7 +113,8 @@ def main():
     value = B * args.steps / elapsed
     log(f"[bench] {args.steps} steps in {elapsed:.3f}s -> {ms_per_step:.2f} ms/step, {value:.1f} samples/s")
 
-    # one profiled forward: HIP events around every DCF-evaluation launch
+    # one profiled forward: HIP events around every DCF-evaluation launch, the
+    # lanes run one after another so that each launch is timed alone
     model.profile(True)
     model.forward(B)
     prof = model.profile_read()
@@ -114,6 +125,7 @@ def main():
     variant = ctx.aes_variant_name()
     key_gbs = prof["hbm_bytes"] / (dcf_ms / 1e3) / 1e9 if dcf_ms > 0 else 0.0
     achieved_tops = aes_per_s * VALU_OPS_PER_AES.get(variant, float("nan")) / 1e12
+    step_tops = prof["aes_calls"] * VALU_OPS_PER_AES.get(variant, float("nan")) / (ms_per_step / 1e3) / 1e12
     log(f"[bench] DCF phase-1: {prof['launches']} launches, {dcf_ms:.2f} ms/forward, "
         f"{dcf_evals_per_s / 1e9:.3f} G evals/s, {aes_per_s / 1e9:.2f} G AES/s")
 
@@ -132,8 +144,8 @@ def main():
         "data": "synthetic molecules (random trees + ring closures, 10-60 atoms), Kaiming-normal weights",
         "config": {"workload": f"two-party secure affinity forward, bw={args.bw} s=12, B={B} molecules x "
                                f"{dims.n_nodes} atoms, GCN 78-78-156-312, FC 312-1024-128, fusion 256-1024-512-1, "
-                               "FSS keys resident in HBM",
-                   "B": B, "n_nodes": dims.n_nodes, "bw": args.bw, "scale": dims.s},
+                               f"FSS keys resident in HBM, {args.lanes} concurrent sub-batches",
+                   "B": B, "n_nodes": dims.n_nodes, "bw": args.bw, "scale": dims.s, "lanes": args.lanes},
         "dcf_evals_per_s": round(dcf_evals_per_s, 1),
         "aes_blocks_per_s": round(aes_per_s, 1),
         "dcf_ms_per_step": round(dcf_ms, 3),
@@ -141,7 +153,8 @@ def main():
         "rounds_per_step": rounds_per_fwd,
         "key_bytes_per_sample_per_party": round(key_bytes / B, 1),
         "roofline": {
-            "kernel": f"k_tr_phase1 (DCF evaluation, AES-128 T-tables in LDS, {variant})",
+            "kernel": f"k_tr_phase1 (DCF evaluation, AES-128 T-tables in LDS, {variant}; the profiled "
+                      f"forward's launches, lanes one after another, traced as k_tr_phase1<..., 1>)",
             "launches": prof["launches"],
             "avg_launch_us": round(1e3 * dcf_ms / max(prof["launches"], 1), 2),
             "bound": "valu",
@@ -149,9 +162,19 @@ def main():
             "peak": round(VALU_PEAK_TOPS, 2),
             "unit": "TOP/s",
             "frac": round(achieved_tops / VALU_PEAK_TOPS, 4),
-            "traffic": TRAFFIC_BYTES_PER_LAUNCH.get(variant),
+            "traffic": TRAFFIC_BYTES_PER_LAUNCH.get((variant, B, args.bw, args.lanes)),
             "traffic_unit": "bytes per launch (mean over the forward's launches)",
             "algorithmic_bytes_per_launch": round(prof["hbm_bytes"] / max(prof["launches"], 1)),
+        },
+        # the same DCF VALU work over the whole timed step (lanes overlapping):
+        # a lower bound on the kernel's rate while it shares the GPU
+        "roofline_step": {
+            "kernel": "k_tr_phase1, all launches of a step",
+            "bound": "valu",
+            "achieved": round(step_tops, 3),
+            "peak": round(VALU_PEAK_TOPS, 2),
+            "unit": "TOP/s",
+            "frac": round(step_tops / VALU_PEAK_TOPS, 4),
         },
         "roofline_hbm": {
             "kernel": "k_tr_phase1 key stream",
@@ -305,6 +328,194 @@ def run_stream(args):
     ctx.close()
     h0.free()
     h1.free()
+
+
+def _oracle():
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import orc
+    return orc
+
+
+def run_relu(args):
+    """Secure ReLU over n elements of Z_2^32 (one 31-bit DCF per element and
+    party): values uniform in [-8, 8) at scale 12, masked with uniform input
+    masks; keys and masked inputs resident in HBM.  One step = one two-party
+    evaluation (DCF phase, bit exchange, output shares, reconstruction) of all n
+    elements; the reconstruction is checked against max(x, 0)."""
+    import ctypes as C
+
+    import numpy as np
+
+    import mpcx
+
+    n, bw, s = args.n, 32, 12
+    rng = np.random.default_rng(args.seed)
+    x = rng.integers(-8 << s, 8 << s, size=n)
+    rin = rng.integers(0, 1 << 32, size=n, dtype=np.uint64)
+    ctx = mpcx.Ctx(bw=bw, scale=s)
+    if args.aes_variant >= 0:
+        ctx.set_aes_variant(args.aes_variant)
+    k0, k1, rout = ctx.tr_keygen(mpcx.RELU, rin, seed=0xACE + args.seed, gate=1)
+    key_bytes = int(ctx.lib.mpcx_tr_key_bytes(ctx.h, mpcx.RELU, n))
+    dx = mpcx.to_dev(((x.astype(np.uint64) + rin) & 0xFFFFFFFF).astype(np.uint32))
+    out = mpcx.empty_dev(4 * n)
+
+    def step():
+        ctx.check(ctx.lib.mpcx_tr_eval(ctx.h, mpcx.RELU, n, mpcx.dptr(k0), mpcx.dptr(k1), mpcx.dptr(dx), None, 0,
+                                       mpcx.dptr(out)), "tr_eval")
+
+    for _ in range(args.warmup):
+        step()
+    ctx.sync()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        step()
+    ctx.sync()
+    elapsed = time.perf_counter() - t0
+    y = mpcx.from_dev(out, np.uint32, n)
+    got = ((y.astype(np.int64) - rout.astype(np.int64)) & 0xFFFFFFFF)
+    got = np.where(got >= 1 << 31, got - (1 << 32), got)
+    exact = bool(np.array_equal(got, np.maximum(x, 0)))
+    aes_per_elem = (bw - 1 - 7) + 1  # 31-bit DCF: levels above the 7-level leaf, plus the leaf
+    evals = 2.0 * n * args.steps
+    aes_s = evals * aes_per_elem / elapsed
+    tops = aes_s * VALU_OPS_PER_AES.get(ctx.aes_variant_name(), float("nan")) / 1e12
+    key_gbs = 2.0 * key_bytes * args.steps / elapsed / 1e9
+    result = {
+        "metric": "DCF evals/s (secure ReLU, Z_2^32, both parties' evaluations, 1 GPU)",
+        "value": round(evals / elapsed, 1),
+        "unit": "DCF evals/s",
+        "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+        "ms_per_step": round(1e3 * elapsed / args.steps, 3),
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "u32",
+        "data": "synthetic: x uniform fixed-point in [-8, 8) at scale 12, uniform masks",
+        "config": {"workload": f"secure ReLU microbench, {n} elements, bw=32, keys resident in HBM", "n": n},
+        "aes_blocks_per_s": round(aes_s, 1),
+        "key_bytes_per_element_per_party": round(key_bytes / n, 2),
+        "roofline": {"kernel": "RELU gate call (k_tr_phase1, k_tr_phase2, k_reconstruct)", "bound": "valu",
+                     "achieved": round(tops, 3), "peak": round(VALU_PEAK_TOPS, 2), "unit": "TOP/s",
+                     "frac": round(tops / VALU_PEAK_TOPS, 4)},
+        "roofline_hbm": {"kernel": "key stream", "bound": "hbm", "achieved": round(key_gbs, 1),
+                         "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(key_gbs / HBM_PEAK_GBS, 4)},
+        "bit_exact": exact,
+    }
+    log(f"[relu] {args.steps} x {n} elements in {elapsed:.3f}s: {evals / elapsed / 1e9:.3f} G DCF evals/s")
+    if not args.no_cpu:
+        try:
+            orc = _oracle()
+            m = 1 << 16
+            ok0, ok1, orout = orc.tr_keygen(7, 1, mpcx.RELU, bw, s, rin[:m])
+            xh = (x[:m].astype(np.uint64) + rin[:m]) & 0xFFFFFFFF
+            reps, ct = 0, 0.0
+            while ct < args.cpu_seconds or reps == 0:
+                t0 = time.perf_counter()
+                yc, _ = orc.tr_eval(mpcx.RELU, bw, s, ok0, ok1, xh)
+                ct += time.perf_counter() - t0
+                reps += 1
+            gc = (np.asarray(yc, np.int64) - np.asarray(orout, np.int64)) & 0xFFFFFFFF
+            gc = np.where(gc >= 1 << 31, gc - (1 << 32), gc)
+            result["cpu_baseline"] = {
+                "value": round(2.0 * m * reps / ct, 1), "unit": "DCF evals/s", "cores": orc.get_threads(),
+                "kind": "port",
+                "sample": f"{reps} x {m} elements of the same workload, both parties, oracle/ C with AES-NI + "
+                          f"OpenMP, {ct:.1f}s",
+                "bit_exact": bool(np.array_equal(gc, np.maximum(x[:m], 0))),
+            }
+        except Exception as e:  # the product number stands without the checker
+            log(f"[relu] oracle unavailable: {e}")
+    print(json.dumps(result), flush=True)
+    ctx.close()
+
+
+def run_adjnorm(args):
+    """Secure adjacency normalisation of B=1024 graphs (N=140, Z_2^32): reveal
+    A, degrees as row sums of the shares, D^-1/2 through the 8-bit DPF table,
+    the outer product T[d_i] T[d_j] (Beaver), one exact truncation, A (.) W
+    (Beaver).  Keys and shares resident in HBM; one step = one evaluation of all
+    B graphs; the unmasked output is checked against the plaintext formula."""
+    import numpy as np
+
+    import mpcx
+    import synth
+
+    B, N, bw, nmax = 1024, 140, 32, 138
+    _, A, _ = synth.molecules(B, synth.Dims(bw=bw), seed=args.seed + 2)
+    a0, a1 = synth.share(A, bw, args.seed + 3)
+    ctx = mpcx.Ctx(bw=bw)
+    if args.aes_variant >= 0:
+        ctx.set_aes_variant(args.aes_variant)
+    k0, k1, mask = ctx.adjnorm_keygen(B, N, seed=0xADD + args.seed)
+    d0, d1 = mpcx.to_dev(ctx.ring(a0)), mpcx.to_dev(ctx.ring(a1))
+    out = mpcx.empty_dev(B * N * N * 4)
+
+    def step():
+        ctx.check(ctx.lib.mpcx_adjnorm_eval(ctx.h, B, N, nmax, mpcx.dptr(k0), mpcx.dptr(k1), mpcx.dptr(d0),
+                                            mpcx.dptr(d1), mpcx.dptr(out)), "adjnorm_eval")
+
+    for _ in range(args.warmup):
+        step()
+    ctx.sync()
+    ctx.reset_counters()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        step()
+    ctx.sync()
+    elapsed = time.perf_counter() - t0
+    P = N * (N + 1) // 2
+    got = (mpcx.from_dev(out, np.uint32, B * N * N) - mpcx.from_dev(mask, np.uint32, B * N * N)).astype(np.int64)
+    exact = None
+    try:
+        orc = _oracle()
+        exact = bool(np.array_equal(got, orc.adj_norm_plain(A).reshape(-1)))
+    except Exception as e:
+        log(f"[adjnorm] oracle unavailable: {e}")
+    per = elapsed / args.steps
+    # AES calls per step: LUT8 (3 per degree and party), TRSLACK (12-bit DCF:
+    # 5 levels + leaf per pair and party)
+    aes = 2.0 * (3 * B * N + 6 * B * P)
+    tops = aes / per * VALU_OPS_PER_AES.get(ctx.aes_variant_name(), float("nan")) / 1e12
+    result = {
+        "metric": "adjacency-normalisation graphs/s (B=1024, N=140, Z_2^32, 1 GPU)",
+        "value": round(B / per, 1),
+        "unit": "graphs/s",
+        "n_gpus": 1, "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(1e3 * per, 3),
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "u32",
+        "data": "synthetic molecular graphs (random trees + ring closures, 10-60 atoms, self loops)",
+        "config": {"workload": f"secure adjacency normalisation, B={B} graphs x N={N}, bw=32 s=12, keys resident",
+                   "B": B, "N": N},
+        "lut_evals_per_s": round(B * N / per, 1),
+        "beaver_products_per_s": round(2 * B * N * N / per, 1),
+        "truncations_per_s": round(B * P / per, 1),
+        "bytes_exchanged_per_graph": round(ctx.bytes_exchanged / (args.steps * B), 1),
+        "roofline": {"kernel": "adjacency normalisation call (DCF/DPF AES work over the call)", "bound": "valu",
+                     "achieved": round(tops, 3), "peak": round(VALU_PEAK_TOPS, 2), "unit": "TOP/s",
+                     "frac": round(tops / VALU_PEAK_TOPS, 4)},
+        "bit_exact": exact,
+    }
+    log(f"[adjnorm] {args.steps} x {B} graphs in {elapsed:.3f}s: {B / per:.0f} graphs/s")
+    if not args.no_cpu:
+        try:
+            orc = _oracle()
+            Bs = 16
+            ok0, ok1, omask = orc.adjnorm_keygen(bw, 12, Bs, N, 5)
+            s0, s1 = a0[:Bs], a1[:Bs]
+            reps, ct = 0, 0.0
+            while ct < args.cpu_seconds or reps == 0:
+                t0 = time.perf_counter()
+                oc, _ = orc.adjnorm_eval(bw, 12, Bs, N, nmax, ok0, ok1, s0, s1)
+                ct += time.perf_counter() - t0
+                reps += 1
+            gc = (np.asarray(oc, np.uint64) - np.asarray(omask, np.uint64)) & 0xFFFFFFFF
+            result["cpu_baseline"] = {
+                "value": round(Bs * reps / ct, 2), "unit": "graphs/s", "cores": orc.get_threads(), "kind": "port",
+                "sample": f"{reps} x {Bs} graphs of the same workload, both parties, oracle/ C with AES-NI + "
+                          f"OpenMP, {ct:.1f}s",
+                "bit_exact": bool(np.array_equal(gc.astype(np.int64), orc.adj_norm_plain(A[:Bs]).reshape(-1))),
+            }
+        except Exception as e:  # the product number stands without the checker
+            log(f"[adjnorm] oracle unavailable: {e}")
+    print(json.dumps(result), flush=True)
+    ctx.close()
 
 
 if __name__ == "__main__":

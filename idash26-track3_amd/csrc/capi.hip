@@ -79,11 +79,17 @@ struct mpcx_ctx {
   Launch L;
   Counters counters;
   std::string err;
+  // Device workspace of the standalone gate evaluations, grown on demand and
+  // kept until the context is destroyed (every such call synchronizes its
+  // stream before returning, so the next call may reuse it).
+  void *scratch = nullptr;
+  size_t scratch_bytes = 0;
+  AdjNormCache *adj = nullptr;  // prepared state of mpcx_adjnorm_eval
 };
 
 struct mpcx_model {
   mpcx_ctx *ctx = nullptr;
-  ModelBase *impl = nullptr;
+  LaneSet *impl = nullptr;
 };
 
 static mpcx_status fail(mpcx_ctx *c, mpcx_status st, const std::string &msg) {
@@ -138,6 +144,8 @@ void mpcx_destroy(mpcx_ctx *c) {
     (void)hipStreamSynchronize(c->own);
     (void)hipStreamDestroy(c->own);
   }
+  if (c->scratch) (void)hipFree(c->scratch);
+  adjnorm_cache_free(c->adj);
   delete c;
 }
 
@@ -224,15 +232,21 @@ mpcx_status mpcx_dcf_eval(mpcx_ctx *c, int party, int bin, size_t n, const void 
 
 // ---------------- workspace for standalone gate evaluation ----------------
 namespace {
-struct Scratch {
-  void *p = nullptr;
-  size_t n = 0;
-  ~Scratch() {
-    if (p) (void)hipFree(p);
+hipError_t ctx_scratch(mpcx_ctx *c, size_t bytes, void **p) {
+  if (bytes > c->scratch_bytes) {
+    if (c->scratch) {
+      hipError_t e = hipDeviceSynchronize();
+      if (e != hipSuccess) return e;
+      (void)hipFree(c->scratch);
+      c->scratch = nullptr;
+      c->scratch_bytes = 0;
+    }
+    hipError_t e = hipMalloc(&c->scratch, bytes);
+    if (e != hipSuccess) return e;
+    c->scratch_bytes = bytes;
   }
-};
-hipError_t scratch_alloc(Scratch &s, size_t bytes) {
-  return hipMalloc(&s.p, bytes ? bytes : 1);
+  *p = c->scratch;
+  return hipSuccess;
 }
 bool valid_kind(int k) { return k == MPCX_TR || k == MPCX_TRRELU || k == MPCX_RELU || k == MPCX_TRSLACK; }
 }  // namespace
@@ -266,9 +280,9 @@ static mpcx_status tr_eval_t(mpcx_ctx *c, int kind, size_t n, const void *k0, co
                              const void *bias, int ncol, void *y) {
   TrLayout lay = tr_layout(kind, c->bw, c->s, n, 0);
   const size_t wb = ((n + 63) / 64) * 8;
-  Scratch s;
-  HIPC(c, scratch_alloc(s, 4 * wb + 2 * n * sizeof(T)), "hipMalloc");
-  uint64_t *b = static_cast<uint64_t *>(s.p);
+  void *sp = nullptr;
+  HIPC(c, ctx_scratch(c, 4 * wb + 2 * n * sizeof(T), &sp), "hipMalloc");
+  uint64_t *b = static_cast<uint64_t *>(sp);
   const size_t ww = wb / 8;
   T *m0 = reinterpret_cast<T *>(b + 4 * ww);
   T *m1 = m0 + n;
@@ -303,7 +317,8 @@ static mpcx_status mul_keygen_t(mpcx_ctx *c, size_t nx, size_t ny, size_t nz, co
                                 void *k1) {
   MulLayout lay = mul_layout(c->bw, nx, ny, nz, 0);
   HIPC(c,
-       launch_mul_keygen<T>(c->L, lay, seed, gate, ia, ib, static_cast<const T *>(rx), static_cast<const T *>(ry),
+       launch_mul_keygen<T>(c->L, lay, seed, gate, MulMap::explicit_maps(ia, ib), static_cast<const T *>(rx),
+                            static_cast<const T *>(ry),
                             static_cast<T *>(rz), static_cast<uint8_t *>(k0), static_cast<uint8_t *>(k1)),
        "mul_keygen");
   return MPCX_OK;
@@ -320,11 +335,12 @@ template <typename T>
 static mpcx_status mul_eval_t(mpcx_ctx *c, size_t nx, size_t ny, size_t nz, const uint32_t *ia, const uint32_t *ib,
                               const void *k0, const void *k1, const void *x, const void *y, void *z) {
   MulLayout lay = mul_layout(c->bw, nx, ny, nz, 0);
-  Scratch s;
-  HIPC(c, scratch_alloc(s, 2 * nz * sizeof(T)), "hipMalloc");
-  T *m0 = static_cast<T *>(s.p), *m1 = m0 + nz;
+  void *sp = nullptr;
+  HIPC(c, ctx_scratch(c, 2 * nz * sizeof(T), &sp), "hipMalloc");
+  T *m0 = static_cast<T *>(sp), *m1 = m0 + nz;
   HIPC(c,
-       launch_mul_eval<T>(c->L, lay, static_cast<const uint8_t *>(k0), static_cast<const uint8_t *>(k1), ia, ib,
+       launch_mul_eval<T>(c->L, lay, static_cast<const uint8_t *>(k0), static_cast<const uint8_t *>(k1),
+                          MulMap::explicit_maps(ia, ib),
                           static_cast<const T *>(x), static_cast<const T *>(y), m0, m1),
        "mul_eval");
   c->counters.msg(nz, c->bw);
@@ -363,9 +379,9 @@ template <typename T>
 static mpcx_status lut_eval_t(mpcx_ctx *c, size_t n, const void *k0, const void *k1, const void *table, const void *x,
                               void *y) {
   Lut8Layout lay = lut8_layout(c->bw, n, 0);
-  Scratch s;
-  HIPC(c, scratch_alloc(s, 3 * n * sizeof(T)), "hipMalloc");
-  T *m0 = static_cast<T *>(s.p), *m1 = m0 + n, *vh = m1 + n;
+  void *sp = nullptr;
+  HIPC(c, ctx_scratch(c, 3 * n * sizeof(T), &sp), "hipMalloc");
+  T *m0 = static_cast<T *>(sp), *m1 = m0 + n, *vh = m1 + n;
   const uint8_t *K0 = static_cast<const uint8_t *>(k0), *K1 = static_cast<const uint8_t *>(k1);
   HIPC(c,
        launch_lut8_phase1<T>(c->L, lay, K0, K1, static_cast<const T *>(table), static_cast<const T *>(x), m0, m1),
@@ -405,9 +421,9 @@ static mpcx_status sxs_keygen_t(mpcx_ctx *c, int nb, int M, int K, int N, const 
                           nullptr),
        "split");
   HIPC(c, launch_prf_ring<T>(c->L, seed, gate, F_ROUT, nc, static_cast<T *>(rc)), "prf");
-  Scratch s;
-  HIPC(c, scratch_alloc(s, nc * sizeof(T)), "hipMalloc");
-  T *g = static_cast<T *>(s.p);
+  void *sp = nullptr;
+  HIPC(c, ctx_scratch(c, nc * sizeof(T), &sp), "hipMalloc");
+  T *g = static_cast<T *>(sp);
   GemmArgs<T> a;
   a.M = M;
   a.K = K;
@@ -446,9 +462,9 @@ static mpcx_status sxs_eval_t(mpcx_ctx *c, int nb, int M, int K, int N, const vo
   SxsLayout lay = sxs_layout(c->bw, nb, M, K, N, 0);
   const uint8_t *k0 = static_cast<const uint8_t *>(k0v), *k1 = static_cast<const uint8_t *>(k1v);
   const size_t nc = size_t(nb) * M * N;
-  Scratch s;
-  HIPC(c, scratch_alloc(s, 2 * nc * sizeof(T)), "hipMalloc");
-  T *m0 = static_cast<T *>(s.p), *m1 = m0 + nc;
+  void *sp = nullptr;
+  HIPC(c, ctx_scratch(c, 2 * nc * sizeof(T), &sp), "hipMalloc");
+  T *m0 = static_cast<T *>(sp), *m1 = m0 + nc;
   GemmArgs<T> g;
   g.M = M;
   g.K = K;
@@ -551,9 +567,9 @@ template <typename T>
 static mpcx_status reveal_eval_t(mpcx_ctx *c, size_t n, const void *k0, const void *k1, const void *v0,
                                  const void *v1, void *out) {
   RevealLayout lay = reveal_layout(c->bw, n, 0);
-  Scratch s;
-  HIPC(c, scratch_alloc(s, 2 * n * sizeof(T)), "hipMalloc");
-  T *m0 = static_cast<T *>(s.p), *m1 = m0 + n;
+  void *sp = nullptr;
+  HIPC(c, ctx_scratch(c, 2 * n * sizeof(T), &sp), "hipMalloc");
+  T *m0 = static_cast<T *>(sp), *m1 = m0 + n;
   HIPC(c,
        launch_reveal_eval<T>(c->L, lay, static_cast<const uint8_t *>(k0), static_cast<const uint8_t *>(k1),
                              static_cast<const T *>(v0), static_cast<const T *>(v1), 0, m0, m1),
@@ -591,7 +607,7 @@ mpcx_status mpcx_adjnorm_eval(mpcx_ctx *c, int B, int N, int nmax, const void *k
     return fail(c, MPCX_EINVAL, "adjnorm_eval: bad argument");
   HIPC(c,
        adjnorm_eval(c->bw, c->s, B, N, nmax, c->L, static_cast<const uint8_t *>(k0), static_cast<const uint8_t *>(k1),
-                    a0, a1, out, &c->counters),
+                    a0, a1, out, &c->counters, &c->adj),
        "adjnorm_eval");
   return MPCX_OK;
 }
@@ -625,7 +641,7 @@ mpcx_status mpcx_model_create(mpcx_ctx *c, const mpcx_model_dims *dims, const in
   d.lut_nmax = dims->lut_nmax;
   d.mask_scale = dims->mask_scale;
   std::string err;
-  ModelBase *impl = make_model(c->bw, c->s, d, W, nW, c->L, &err);
+  LaneSet *impl = make_lane_set(c->bw, c->s, d, W, nW, c->L, &err);
   if (!impl) return fail(c, MPCX_EINVAL, "model_create: " + err);
   auto *m = new mpcx_model();
   m->ctx = c;
@@ -639,6 +655,18 @@ void mpcx_model_destroy(mpcx_model *m) {
   delete m->impl;
   delete m;
 }
+
+mpcx_status mpcx_model_set_lanes(mpcx_model *m, int lanes) {
+  if (!m) return MPCX_EINVAL;
+  if (lanes < 1 || lanes > 16) return fail(m->ctx, MPCX_EINVAL, "model_set_lanes: lanes must be in [1, 16]");
+  std::string err;
+  hipError_t e = m->impl->set_lanes(lanes, &err);
+  if (e == hipErrorInvalidValue) return fail(m->ctx, MPCX_EINVAL, "model_set_lanes: " + err);
+  HIPC(m->ctx, e, "model_set_lanes");
+  return MPCX_OK;
+}
+
+int mpcx_model_lanes(const mpcx_model *m) { return m ? m->impl->lanes() : 0; }
 
 size_t mpcx_model_key_bytes(const mpcx_model *m, int B) { return (m && B > 0) ? m->impl->key_bytes(B) : 0; }
 
@@ -708,7 +736,6 @@ mpcx_status mpcx_model_set_inputs(mpcx_model *m, int B, const void *x0, const vo
 
 mpcx_status mpcx_model_forward(mpcx_model *m, int B) {
   if (!m) return MPCX_EINVAL;
-  m->impl->counters = Counters();
   hipError_t e = m->impl->forward(B);
   if (e == hipErrorInvalidValue) return fail(m->ctx, MPCX_ESTATE, "forward: keys or inputs not set for this B");
   HIPC(m->ctx, e, "model_forward");
@@ -725,29 +752,13 @@ mpcx_status mpcx_model_output(mpcx_model *m, int B, int64_t *out) {
 
 mpcx_status mpcx_model_profile(mpcx_model *m, int enable) {
   if (!m) return MPCX_EINVAL;
-  m->impl->timer.reset();
-  m->impl->timer.on = enable != 0;
+  m->impl->profile(enable != 0);
   return MPCX_OK;
 }
 
 mpcx_status mpcx_model_profile_read(mpcx_model *m, int *launches, double *ms, double *elements, double *aes,
                                     double *hbm_bytes) {
   if (!m) return MPCX_EINVAL;
-  auto &t = m->impl->timer;
-  HIPC(m->ctx, hipStreamSynchronize(m->ctx->L.stream), "sync");
-  double tot = 0, el = 0, ae = 0, by = 0;
-  for (size_t k = 0; k + 1 < t.ev.size(); k += 2) {
-    float f = 0;
-    HIPC(m->ctx, hipEventElapsedTime(&f, t.ev[k], t.ev[k + 1]), "hipEventElapsedTime");
-    tot += f;
-    el += 2.0 * double(t.elems[k / 2]);
-    ae += 2.0 * double(t.elems[k / 2]) * double(t.levels[k / 2]);
-    by += t.bytes[k / 2];
-  }
-  if (launches) *launches = int(t.ev.size() / 2);
-  if (ms) *ms = tot;
-  if (elements) *elements = el;
-  if (aes) *aes = ae;
-  if (hbm_bytes) *hbm_bytes = by;
+  HIPC(m->ctx, m->impl->profile_read(launches, ms, elements, aes, hbm_bytes), "model_profile_read");
   return MPCX_OK;
 }

@@ -20,6 +20,9 @@ struct Launch {
   int num_cu = 256;
   int aes_variant = 0;  // LDS T-table layout, see aes_variants()
   int aes_block = 0;    // threads per block for AES kernels (0 = variant default)
+  // Launches of a profiled forward use a separately named instantiation of the
+  // DCF-evaluation kernel (same code), so kernel traces can tell them apart.
+  bool profiled = false;
 };
 
 struct AesVariant {
@@ -74,14 +77,37 @@ hipError_t launch_reveal_eval(const Launch &L, const RevealLayout &lay, const ui
                               const T *v0, const T *v1, int rowlen, T *msg0, T *msg1);
 
 // ---------------- Beaver product ----------------
+// Operand indices of z[k] = x[a(k)] * y[b(k)]: explicit index arrays, or one of
+// the two maps of the adjacency normalisation, computed on the fly (N nodes
+// per graph, P = N(N+1)/2 node pairs i <= j per graph, pair index
+// pidx(i, j) = i*N - i(i-1)/2 + j - i):
+//   OUTER_TRI     k = g*P + pidx(i, j)        -> a = g*N + i, b = g*N + j
+//   SYM_HADAMARD  k = (g*N + i)*N + j         -> a = k, b = g*P + pidx(min(i,j), max(i,j))
+struct MulMap {
+  enum Kind { EXPLICIT = 0, OUTER_TRI = 1, SYM_HADAMARD = 2 };
+  int kind = EXPLICIT;
+  const uint32_t *ia = nullptr, *ib = nullptr;
+  uint32_t N = 0;
+  static MulMap explicit_maps(const uint32_t *a, const uint32_t *b) {
+    MulMap m;
+    m.ia = a;
+    m.ib = b;
+    return m;
+  }
+  static MulMap of(int kind, int n) {
+    MulMap m;
+    m.kind = kind;
+    m.N = uint32_t(n);
+    return m;
+  }
+};
+
 template <typename T>
-hipError_t launch_mul_keygen(const Launch &L, const MulLayout &lay, uint64_t seed, uint32_t gate,
-                             const uint32_t *ia, const uint32_t *ib, const T *rx, const T *ry, T *rz,
-                             uint8_t *k0, uint8_t *k1);
+hipError_t launch_mul_keygen(const Launch &L, const MulLayout &lay, uint64_t seed, uint32_t gate, const MulMap &map,
+                             const T *rx, const T *ry, T *rz, uint8_t *k0, uint8_t *k1);
 template <typename T>
 hipError_t launch_mul_eval(const Launch &L, const MulLayout &lay, const uint8_t *k0, const uint8_t *k1,
-                           const uint32_t *ia, const uint32_t *ib, const T *xhat, const T *yhat, T *msg0,
-                           T *msg1);
+                           const MulMap &map, const T *xhat, const T *yhat, T *msg0, T *msg1);
 
 // ---------------- LUT8 ----------------
 template <typename T>

@@ -275,7 +275,9 @@ __device__ __forceinline__ T tr_shifted_input(const TrArgs<T> &a, size_t i) {
   return x + (T(1) << (a.n - 1));
 }
 
-template <typename T, int NT, int REP>
+// TAG = 1 marks the launches of a profiled forward (identical code, its own
+// name in kernel traces).
+template <typename T, int NT, int REP, int TAG>
 __global__ void k_tr_phase1(TrArgs<T> a) {
   __shared__ uint32_t lds[AesLds<NT, REP>::kWords];
   AesLds<NT, REP>::fill(lds);
@@ -489,8 +491,11 @@ hipError_t launch_tr_phase1(const Launch &L, const TrLayout &lay, const uint8_t 
   return with_variant(L, [&](auto v) {
     constexpr int NT = decltype(v)::nt, REP = decltype(v)::rep;
     int block = variant_block(L);
-    int grid = grid_for(k_tr_phase1<T, NT, REP>, block, lay.N, L.num_cu);
-    hipLaunchKernelGGL((k_tr_phase1<T, NT, REP>), dim3(grid, 2), dim3(block), 0, L.stream, a);
+    int grid = grid_for(k_tr_phase1<T, NT, REP, 0>, block, lay.N, L.num_cu);
+    if (L.profiled)
+      hipLaunchKernelGGL((k_tr_phase1<T, NT, REP, 1>), dim3(grid, 2), dim3(block), 0, L.stream, a);
+    else
+      hipLaunchKernelGGL((k_tr_phase1<T, NT, REP, 0>), dim3(grid, 2), dim3(block), 0, L.stream, a);
     return hipGetLastError();
   });
 }
@@ -603,10 +608,40 @@ __global__ void k_reveal_eval(size_t n, const T *R0, const T *R1, const T *v0, c
   }
 }
 
+// Row-sum reveal: one wavefront per row of rowlen contiguous elements, lanes
+// read the row coalesced and reduce across the wave (sums mod 2^bw do not
+// depend on the order).
+template <typename T>
+__global__ void k_reveal_rowsum(size_t n, const T *R0, const T *R1, const T *v0, const T *v1, int rowlen, T *msg0,
+                                T *msg1) {
+  const int p = blockIdx.y;
+  const T *R = p ? R1 : R0;
+  const T *v = p ? v1 : v0;
+  T *msg = p ? msg1 : msg0;
+  const int lane = int(threadIdx.x & 63u);
+  const size_t wave = (size_t(blockIdx.x) * blockDim.x + threadIdx.x) >> 6;
+  const size_t nwaves = (size_t(gridDim.x) * blockDim.x) >> 6;
+  for (size_t r = wave; r < n; r += nwaves) {  // uniform across the wave
+    const T *row = v + r * size_t(rowlen);
+    T x = 0;
+    for (int j = lane; j < rowlen; j += 64) x += row[j];
+    for (int o = 32; o > 0; o >>= 1) x += __shfl_xor(x, o, 64);
+    if (lane == 0) msg[r] = x + R[r];
+  }
+}
+
 template <typename T>
 hipError_t launch_reveal_eval(const Launch &L, const RevealLayout &lay, const uint8_t *k0, const uint8_t *k1,
                               const T *v0, const T *v1, int rowlen, T *msg0, T *msg1) {
   const int block = 256;
+  if (rowlen > 0) {  // one wave per row, no grid-stride: the rows' loads all in flight at once
+    const size_t blocks = (lay.N * 64 + block - 1) / block;
+    const int grid = int(blocks < size_t(1) << 30 ? (blocks < 1 ? 1 : blocks) : size_t(1) << 30);
+    hipLaunchKernelGGL((k_reveal_rowsum<T>), dim3(grid, 2), dim3(block), 0, L.stream, lay.N,
+                       reinterpret_cast<const T *>(k0 + lay.off_r), reinterpret_cast<const T *>(k1 + lay.off_r), v0,
+                       v1, rowlen, msg0, msg1);
+    return hipGetLastError();
+  }
   int grid = grid_for(k_reveal_eval<T>, block, lay.N, L.num_cu);
   hipLaunchKernelGGL((k_reveal_eval<T>), dim3(grid, 2), dim3(block), 0, L.stream, lay.N,
                      reinterpret_cast<const T *>(k0 + lay.off_r), reinterpret_cast<const T *>(k1 + lay.off_r), v0,
@@ -617,16 +652,49 @@ hipError_t launch_reveal_eval(const Launch &L, const RevealLayout &lay, const ui
 // ---------------------------------------------------------------------------
 // Beaver product
 // ---------------------------------------------------------------------------
+__device__ __forceinline__ uint32_t pair_row_start(uint32_t N, uint32_t i) { return i * N - (i * (i - 1)) / 2; }
+
+// Operands of product k (MulMap in kernels.h).  The pair row i of a pair index
+// r is the largest i with pair_row_start(i) <= r: a float estimate from the
+// quadratic, then exact integer corrections.
+__device__ __forceinline__ void mul_operands(const MulMap &m, size_t k, uint32_t *a, uint32_t *b) {
+  if (m.kind == MulMap::EXPLICIT) {
+    *a = m.ia[k];
+    *b = m.ib[k];
+    return;
+  }
+  const uint32_t N = m.N, P = N * (N + 1) / 2;
+  const uint32_t k32 = uint32_t(k);
+  if (m.kind == MulMap::OUTER_TRI) {
+    const uint32_t g = k32 / P, r = k32 - g * P;
+    const float q = float(2 * N + 1);
+    int ie = int((q - sqrtf(q * q - 8.0f * float(r))) * 0.5f);
+    uint32_t i = uint32_t(ie < 0 ? 0 : (ie > int(N) - 1 ? int(N) - 1 : ie));
+    while (i + 1 < N && pair_row_start(N, i + 1) <= r) i++;
+    while (i > 0 && pair_row_start(N, i) > r) i--;
+    const uint32_t j = i + (r - pair_row_start(N, i));
+    *a = g * N + i;
+    *b = g * N + j;
+  } else {  // SYM_HADAMARD
+    const uint32_t NN = N * N, g = k32 / NN, rem = k32 - g * NN;
+    const uint32_t i = rem / N, j = rem - i * N;
+    const uint32_t lo = i < j ? i : j, hi = i < j ? j : i;
+    *a = k32;
+    *b = g * P + pair_row_start(N, lo) + (hi - lo);
+  }
+}
 template <typename T, int NT, int REP>
-__global__ void k_mul_keygen_c(AesRK kd, uint32_t gate, size_t nz, const uint32_t *ia, const uint32_t *ib,
-                               const T *rx, const T *ry, T *rz, T *C0, T *C1) {
+__global__ void k_mul_keygen_c(AesRK kd, uint32_t gate, size_t nz, MulMap map, const T *rx, const T *ry, T *rz,
+                               T *C0, T *C1) {
   __shared__ uint32_t lds[AesLds<NT, REP>::kWords];
   AesLds<NT, REP>::fill(lds);
   AesLds<NT, REP> aes(lds);
   for (size_t i = size_t(blockIdx.x) * blockDim.x + threadIdx.x; i < nz; i += size_t(gridDim.x) * blockDim.x) {
     const T r = ring_of<T>(aes.prf(kd, gate, F_ROUT, i));
     rz[i] = r;
-    const T C = rx[ia[i]] * ry[ib[i]] + r;
+    uint32_t a, b;
+    mul_operands(map, i, &a, &b);
+    const T C = rx[a] * ry[b] + r;
     const T c0 = ring_of<T>(aes.prf(kd, gate, F_SPLIT + 2, i));
     C0[i] = c0;
     C1[i] = C - c0;
@@ -634,9 +702,8 @@ __global__ void k_mul_keygen_c(AesRK kd, uint32_t gate, size_t nz, const uint32_
 }
 
 template <typename T>
-hipError_t launch_mul_keygen(const Launch &L, const MulLayout &lay, uint64_t seed, uint32_t gate,
-                             const uint32_t *ia, const uint32_t *ib, const T *rx, const T *ry, T *rz, uint8_t *k0,
-                             uint8_t *k1) {
+hipError_t launch_mul_keygen(const Launch &L, const MulLayout &lay, uint64_t seed, uint32_t gate, const MulMap &map,
+                             const T *rx, const T *ry, T *rz, uint8_t *k0, uint8_t *k1) {
   hipError_t e = launch_split<T>(L, seed, gate, F_SPLIT + 0, lay.nx, rx, reinterpret_cast<T *>(k0 + lay.off_rx),
                                  reinterpret_cast<T *>(k1 + lay.off_rx), nullptr);
   if (e != hipSuccess) return e;
@@ -648,7 +715,7 @@ hipError_t launch_mul_keygen(const Launch &L, const MulLayout &lay, uint64_t see
     constexpr int NT = decltype(v)::nt, REP = decltype(v)::rep;
     int block = variant_block(L);
     int grid = grid_for(k_mul_keygen_c<T, NT, REP>, block, lay.nz, L.num_cu);
-    hipLaunchKernelGGL((k_mul_keygen_c<T, NT, REP>), dim3(grid), dim3(block), 0, L.stream, kd, gate, lay.nz, ia, ib,
+    hipLaunchKernelGGL((k_mul_keygen_c<T, NT, REP>), dim3(grid), dim3(block), 0, L.stream, kd, gate, lay.nz, map,
                        rx, ry, rz, reinterpret_cast<T *>(k0 + lay.off_c), reinterpret_cast<T *>(k1 + lay.off_c));
     return hipGetLastError();
   });
@@ -656,15 +723,15 @@ hipError_t launch_mul_keygen(const Launch &L, const MulLayout &lay, uint64_t see
 
 template <typename T>
 __global__ void k_mul_eval(size_t nz, const T *Rx0, const T *Rx1, const T *Ry0, const T *Ry1, const T *C0,
-                           const T *C1, const uint32_t *ia, const uint32_t *ib, const T *xhat, const T *yhat,
-                           T *msg0, T *msg1) {
+                           const T *C1, MulMap map, const T *xhat, const T *yhat, T *msg0, T *msg1) {
   const int p = blockIdx.y;
   const T *Rx = p ? Rx1 : Rx0;
   const T *Ry = p ? Ry1 : Ry0;
   const T *Cc = p ? C1 : C0;
   T *msg = p ? msg1 : msg0;
   for (size_t i = size_t(blockIdx.x) * blockDim.x + threadIdx.x; i < nz; i += size_t(gridDim.x) * blockDim.x) {
-    const uint32_t a = ia[i], b = ib[i];
+    uint32_t a, b;
+    mul_operands(map, i, &a, &b);
     const T x = xhat[a], y = yhat[b];
     T z = Cc[i] - x * Ry[b] - y * Rx[a];
     if (p == 0) z += x * y;
@@ -674,13 +741,13 @@ __global__ void k_mul_eval(size_t nz, const T *Rx0, const T *Rx1, const T *Ry0, 
 
 template <typename T>
 hipError_t launch_mul_eval(const Launch &L, const MulLayout &lay, const uint8_t *k0, const uint8_t *k1,
-                           const uint32_t *ia, const uint32_t *ib, const T *xhat, const T *yhat, T *msg0, T *msg1) {
+                           const MulMap &map, const T *xhat, const T *yhat, T *msg0, T *msg1) {
   const int block = 256;
   int grid = grid_for(k_mul_eval<T>, block, lay.nz, L.num_cu);
   hipLaunchKernelGGL((k_mul_eval<T>), dim3(grid, 2), dim3(block), 0, L.stream, lay.nz,
                      reinterpret_cast<const T *>(k0 + lay.off_rx), reinterpret_cast<const T *>(k1 + lay.off_rx),
                      reinterpret_cast<const T *>(k0 + lay.off_ry), reinterpret_cast<const T *>(k1 + lay.off_ry),
-                     reinterpret_cast<const T *>(k0 + lay.off_c), reinterpret_cast<const T *>(k1 + lay.off_c), ia, ib,
+                     reinterpret_cast<const T *>(k0 + lay.off_c), reinterpret_cast<const T *>(k1 + lay.off_c), map,
                      xhat, yhat, msg0, msg1);
   return hipGetLastError();
 }
@@ -1127,10 +1194,10 @@ hipError_t launch_rowsum(const Launch &L, size_t rows, int len, const T *a, T *o
                                               uint8_t *, uint8_t *);                                                 \
   template hipError_t launch_reveal_eval<T>(const Launch &, const RevealLayout &, const uint8_t *, const uint8_t *,  \
                                             const T *, const T *, int, T *, T *);                                    \
-  template hipError_t launch_mul_keygen<T>(const Launch &, const MulLayout &, uint64_t, uint32_t, const uint32_t *,  \
-                                           const uint32_t *, const T *, const T *, T *, uint8_t *, uint8_t *);       \
+  template hipError_t launch_mul_keygen<T>(const Launch &, const MulLayout &, uint64_t, uint32_t, const MulMap &,   \
+                                           const T *, const T *, T *, uint8_t *, uint8_t *);                         \
   template hipError_t launch_mul_eval<T>(const Launch &, const MulLayout &, const uint8_t *, const uint8_t *,        \
-                                         const uint32_t *, const uint32_t *, const T *, const T *, T *, T *);        \
+                                         const MulMap &, const T *, const T *, T *, T *);                            \
   template hipError_t launch_lut8_keygen<T>(const Launch &, const Lut8Layout &, uint64_t, uint32_t, const T *, T *, \
                                             uint8_t *, uint8_t *);                                                   \
   template hipError_t launch_lut8_phase1<T>(const Launch &, const Lut8Layout &, const uint8_t *, const uint8_t *,    \

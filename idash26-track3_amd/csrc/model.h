@@ -104,6 +104,66 @@ class ModelBase {
 ModelBase *make_model(int bw, int s, const ModelDims &d, const int64_t *W, size_t nW, const Launch &L,
                       std::string *err);
 
+// The model as the library exposes it: a batch of B split into `lanes`
+// sub-batches of consecutive samples (B/lanes, the first B%lanes one larger),
+// each a complete ModelBase on its own stream.  Lane 0 runs on the caller's
+// stream, which waits for the other lanes at the end of every forward; the
+// gates of one lane that leave the GPU partly idle (small latency-bound DCF
+// launches, GEMMs, the memory-bound exchange kernels) overlap another lane's
+// DCF evaluation.
+// The keys of a batch are the lanes' key sets back to back; lane i's key set is
+// the one-lane key set of its samples under the seed lane_seed(seed, i).
+class LaneSet {
+ public:
+  LaneSet(int bw, int s, const ModelDims &d, const int64_t *W, size_t nW, const Launch &L);
+  ~LaneSet();
+  hipError_t set_lanes(int n, std::string *err);  // drops keys and inputs
+  int lanes() const { return int(lane_.size()); }
+  static uint64_t lane_seed(uint64_t seed, int i) { return seed + uint64_t(i) * 0x9E3779B97F4A7C15ull; }
+
+  size_t key_bytes(int B) const;
+  size_t unique_key_bytes(int B, int party) const;
+  hipError_t keygen(int B, uint64_t seed);
+  hipError_t import_keys(int B, const void *k0, const void *k1, size_t bytes);
+  hipError_t export_keys(int party, void *dst, size_t bytes);
+  hipError_t export_unique_keys(int party, void *dst, size_t bytes);
+  hipError_t release_arena();
+  hipError_t attach_host_keys(int B, const void *h_k0, size_t bytes0, const void *h_k1, size_t bytes1,
+                              size_t slot_bytes);
+  hipError_t set_inputs(int B, const void *x0, const void *x1, const void *a0, const void *a1, const void *m0,
+                        const void *m1, const int64_t *prot);
+  hipError_t forward(int B);
+  hipError_t output(int64_t *h_out, int B);
+  // Per-launch timing of the DCF-evaluation kernels.  A profiled forward runs
+  // the lanes one after another, so every launch is timed alone.
+  void profile(bool on);
+  hipError_t profile_read(int *launches, double *ms, double *elements, double *aes, double *hbm_bytes);
+
+  Counters counters;         // last forward: bytes summed over lanes, rounds of one lane
+  StreamStats stream_stats;  // last forward, summed over lanes
+  std::string err;
+
+ private:
+  // samples of lane i for a batch of B (0 for lanes beyond B)
+  int lane_B(int B, int i) const;
+  int active(int B) const;
+  template <class Fn>
+  hipError_t each(int B, Fn &&fn);
+
+  int bw_, s_;
+  ModelDims d_;
+  std::vector<int64_t> W_;
+  Launch L_;
+  std::vector<ModelBase *> lane_;
+  std::vector<hipStream_t> st_;  // st_[i]: lane i's stream (st_[0] = the caller's)
+  std::vector<hipEvent_t> done_;
+  bool serial_ = false;
+  int keyed_B_ = -1;
+};
+
+LaneSet *make_lane_set(int bw, int s, const ModelDims &d, const int64_t *W, size_t nW, const Launch &L,
+                       std::string *err);
+
 // ---------------- standalone secure adjacency normalisation ----------------
 // ddgSecureAdjNormKeygen / ddgSecureAdjNormEval (gpu_mpc/secure_adj_norm.h:203-374,
 // 393-659): A (B x N x N, 0/1 with self loops) as additive shares -> masked
@@ -111,7 +171,12 @@ ModelBase *make_model(int bw, int s, const ModelDims &d, const int64_t *W, size_
 size_t adjnorm_key_bytes(int bw, int s, int B, int N);
 hipError_t adjnorm_keygen(int bw, int s, int B, int N, uint64_t seed, const Launch &L, void *out_mask,
                           uint8_t *k0, uint8_t *k1);
+// *cache keeps the index maps, D^-1/2 table and scratch of the last (bw, B, N,
+// nmax) between calls (created on first use; free with adjnorm_cache_free).
+struct AdjNormCache;
+void adjnorm_cache_free(AdjNormCache *cache);
 hipError_t adjnorm_eval(int bw, int s, int B, int N, int nmax, const Launch &L, const uint8_t *k0,
-                        const uint8_t *k1, const void *a0, const void *a1, void *out_masked, Counters *ctr);
+                        const uint8_t *k1, const void *a0, const void *a1, void *out_masked, Counters *ctr,
+                        AdjNormCache **cache);
 
 }  // namespace mpcx

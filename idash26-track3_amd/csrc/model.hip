@@ -37,7 +37,6 @@ struct Cursor {
 };
 
 inline size_t pairs_of(int N) { return size_t(N) * (N + 1) / 2; }
-inline size_t pidx(int N, int i, int j) { return size_t(i) * N - size_t(i) * (i - 1) / 2 + size_t(j - i); }
 
 int pool_levels(int N, int *pairs) {
   int R = N, L = 0;
@@ -160,12 +159,14 @@ struct Runner {
     TRY(enter(end, &b));
     TrLayout lay = tr_layout(kind, bw, s, n, b);
     hipEvent_t e0 = nullptr, e1 = nullptr;
+    Launch L1 = L;
     if (timer && timer->on) {
       TRY(hipEventCreate(&e0));
       TRY(hipEventCreate(&e1));
       TRY(hipEventRecord(e0, L.stream));
+      L1.profiled = true;
     }
-    TRY(launch_tr_phase1<T>(L, lay, kv.k[0], kv.k[1], x, bias, ncol, ws.plane(0), ws.plane(1), ws.plane(2),
+    TRY(launch_tr_phase1<T>(L1, lay, kv.k[0], kv.k[1], x, bias, ncol, ws.plane(0), ws.plane(1), ws.plane(2),
                             ws.plane(3)));
     if (timer && timer->on) {
       TRY(hipEventRecord(e1, L.stream));
@@ -190,13 +191,12 @@ struct Runner {
     return hipSuccess;
   }
 
-  hipError_t mul(size_t nx, size_t ny, size_t nz, const uint32_t *ia, const uint32_t *ib, const T *x, const T *y,
-                 T *out) {
+  hipError_t mul(size_t nx, size_t ny, size_t nz, const MulMap &map, const T *x, const T *y, T *out) {
     const size_t end = mul_layout(bw, nx, ny, nz, c.off).end;
     size_t b;
     TRY(enter(end, &b));
     MulLayout lay = mul_layout(bw, nx, ny, nz, b);
-    TRY(launch_mul_eval<T>(L, lay, kv.k[0], kv.k[1], ia, ib, x, y, ws.m0.p, ws.m1.p));
+    TRY(launch_mul_eval<T>(L, lay, kv.k[0], kv.k[1], map, x, y, ws.m0.p, ws.m1.p));
     ctr.msg(nz, bw);
     TRY(launch_reconstruct<T>(L, nz, ws.m0.p, ws.m1.p, out));
     leave(end);
@@ -299,10 +299,9 @@ struct Dealer {
     c.gate++;
     return hipSuccess;
   }
-  hipError_t mul(size_t nx, size_t ny, size_t nz, const uint32_t *ia, const uint32_t *ib, const T *rx, const T *ry,
-                 T *rz) {
+  hipError_t mul(size_t nx, size_t ny, size_t nz, const MulMap &map, const T *rx, const T *ry, T *rz) {
     MulLayout lay = mul_layout(bw, nx, ny, nz, c.off);
-    TRY(launch_mul_keygen<T>(L, lay, seed, c.gate, ia, ib, rx, ry, rz, K0, K1));
+    TRY(launch_mul_keygen<T>(L, lay, seed, c.gate, map, rx, ry, rz, K0, K1));
     c.off = lay.end;
     c.gate++;
     return hipSuccess;
@@ -367,7 +366,6 @@ struct Dealer {
 template <typename T>
 struct AdjNorm {
   int B = -1, N = -1, s = 0, nmax = 0;
-  DevBuf<uint32_t> oa, ob, wa, wb;  // index maps: outer product, A (.) W
   DevBuf<T> table;                  // T[k] = llround(2^s / sqrt(k)), 1 <= k <= nmax
   DevBuf<T> t0, t1, p0, p1;         // scratch: 2 x BN, 2 x BP
 
@@ -385,30 +383,8 @@ struct AdjNorm {
   hipError_t prepare(int B_, int N_, int s_, int nmax_) {
     if (B_ == B && N_ == N && s_ == s && nmax_ == nmax) return hipSuccess;
     const size_t P = pairs_of(N_), BN = size_t(B_) * N_, BNN = BN * N_;
-    std::vector<uint32_t> hoa(B_ * P), hob(B_ * P), hwa(BNN), hwb(BNN);
-    for (int b = 0; b < B_; b++) {
-      size_t q = size_t(b) * P;
-      for (int i = 0; i < N_; i++)
-        for (int j = i; j < N_; j++) {
-          hoa[q] = uint32_t(b * N_ + i);
-          hob[q] = uint32_t(b * N_ + j);
-          q++;
-        }
-      for (int i = 0; i < N_; i++)
-        for (int j = 0; j < N_; j++) {
-          size_t e = (size_t(b) * N_ + i) * N_ + j;
-          hwa[e] = uint32_t(e);
-          hwb[e] = uint32_t(size_t(b) * P + (i <= j ? pidx(N_, i, j) : pidx(N_, j, i)));
-        }
-    }
-    TRY(oa.alloc(hoa.size()));
-    TRY(ob.alloc(hob.size()));
-    TRY(wa.alloc(hwa.size()));
-    TRY(wb.alloc(hwb.size()));
-    TRY(hipMemcpy(oa.p, hoa.data(), hoa.size() * 4, hipMemcpyHostToDevice));
-    TRY(hipMemcpy(ob.p, hob.data(), hob.size() * 4, hipMemcpyHostToDevice));
-    TRY(hipMemcpy(wa.p, hwa.data(), hwa.size() * 4, hipMemcpyHostToDevice));
-    TRY(hipMemcpy(wb.p, hwb.data(), hwb.size() * 4, hipMemcpyHostToDevice));
+    // the Beaver products index their operands with 32-bit element indices
+    if (BNN >= (size_t(1) << 32)) return hipErrorInvalidValue;
     std::vector<T> tab(256, T(0));
     const double q = std::ldexp(1.0, s_);
     for (int k = 1; k <= nmax_ && k < 256; k++) tab[k] = T(std::llround(q / std::sqrt(double(k))));
@@ -431,9 +407,9 @@ struct AdjNorm {
     TRY(d.reveal(BNN, rA));
     TRY(d.reveal(BN, t0.p));                                // degree mask
     TRY(d.lut8(BN, t0.p, t1.p));                            // mask of T[d]
-    TRY(d.mul(BN, BN, BP, oa.p, ob.p, t1.p, t1.p, p0.p));  // mask of the outer product
+    TRY(d.mul(BN, BN, BP, MulMap::of(MulMap::OUTER_TRI, N), t1.p, t1.p, p0.p));  // mask of the outer product
     TRY(d.tr(G_TRSLACK, BP, p0.p, p1.p));                    // mask of W
-    TRY(d.mul(BNN, BP, BNN, wa.p, wb.p, rA, p1.p, rN));    // mask of A_norm
+    TRY(d.mul(BNN, BP, BNN, MulMap::of(MulMap::SYM_HADAMARD, N), rA, p1.p, rN));  // mask of A_norm
     return hipSuccess;
   }
 
@@ -443,9 +419,9 @@ struct AdjNorm {
     TRY(r.reveal(BNN, a0, a1, 0, Ah));
     TRY(r.reveal(BN, a0, a1, N, t0.p));  // degree = row sums of the A shares
     TRY(r.lut8(BN, table.p, t0.p, t1.p, t0.p));
-    TRY(r.mul(BN, BN, BP, oa.p, ob.p, t0.p, t0.p, p0.p));
+    TRY(r.mul(BN, BN, BP, MulMap::of(MulMap::OUTER_TRI, N), t0.p, t0.p, p0.p));
     TRY(r.tr(G_TRSLACK, BP, p0.p, nullptr, 1, p1.p));
-    TRY(r.mul(BNN, BP, BNN, wa.p, wb.p, Ah, p1.p, An));
+    TRY(r.mul(BNN, BP, BNN, MulMap::of(MulMap::SYM_HADAMARD, N), Ah, p1.p, An));
     return hipSuccess;
   }
 };
@@ -1047,6 +1023,242 @@ ModelBase *make_model(int bw, int s, const ModelDims &d, const int64_t *W, size_
 }
 
 // ===========================================================================
+// lanes: concurrent sub-batches
+// ===========================================================================
+LaneSet::LaneSet(int bw, int s, const ModelDims &d, const int64_t *W, size_t nW, const Launch &L)
+    : bw_(bw), s_(s), d_(d), W_(W, W + nW), L_(L) {}
+
+LaneSet::~LaneSet() {
+  for (size_t i = 0; i < lane_.size(); i++) {
+    if (i > 0 && st_[i]) (void)hipStreamSynchronize(st_[i]);
+    delete lane_[i];
+  }
+  for (size_t i = 1; i < st_.size(); i++)
+    if (st_[i]) (void)hipStreamDestroy(st_[i]);
+  for (auto e : done_)
+    if (e) (void)hipEventDestroy(e);
+}
+
+hipError_t LaneSet::set_lanes(int n, std::string *e) {
+  if (n < 1 || n > 16) {
+    *e = "lanes must be in [1, 16]";
+    return hipErrorInvalidValue;
+  }
+  if (L_.stream) TRY(hipStreamSynchronize(L_.stream));
+  for (size_t i = 0; i < lane_.size(); i++) {
+    if (i > 0) TRY(hipStreamSynchronize(st_[i]));
+    delete lane_[i];
+  }
+  lane_.clear();
+  for (size_t i = 1; i < st_.size(); i++) (void)hipStreamDestroy(st_[i]);
+  st_.clear();
+  for (auto ev : done_) (void)hipEventDestroy(ev);
+  done_.clear();
+  keyed_B_ = -1;
+  for (int i = 0; i < n; i++) {
+    Launch Li = L_;
+    if (i > 0) TRY(hipStreamCreateWithFlags(&Li.stream, hipStreamNonBlocking));
+    st_.push_back(Li.stream);
+    hipEvent_t ev;
+    TRY(hipEventCreateWithFlags(&ev, hipEventDisableTiming));
+    done_.push_back(ev);
+    ModelBase *m = make_model(bw_, s_, d_, W_.data(), W_.size(), Li, e);
+    if (!m) return hipErrorInvalidValue;
+    lane_.push_back(m);
+  }
+  return hipSuccess;
+}
+
+int LaneSet::lane_B(int B, int i) const {
+  const int n = lanes();
+  return B / n + (i < B % n ? 1 : 0);
+}
+int LaneSet::active(int B) const { return std::min(lanes(), std::max(B, 0)); }
+
+// fn(i, Bi, sample offset) for every lane with samples
+template <class Fn>
+hipError_t LaneSet::each(int B, Fn &&fn) {
+  int off = 0;
+  for (int i = 0; i < active(B); i++) {
+    const int Bi = lane_B(B, i);
+    TRY(fn(i, Bi, off));
+    off += Bi;
+  }
+  return hipSuccess;
+}
+
+size_t LaneSet::key_bytes(int B) const {
+  size_t n = 0;
+  for (int i = 0; i < active(B); i++) n += lane_[i]->key_bytes(lane_B(B, i));
+  return n;
+}
+size_t LaneSet::unique_key_bytes(int B, int party) const {
+  size_t n = 0;
+  for (int i = 0; i < active(B); i++) n += lane_[i]->unique_key_bytes(lane_B(B, i), party);
+  return n;
+}
+
+hipError_t LaneSet::keygen(int B, uint64_t seed) {
+  keyed_B_ = -1;
+  TRY(each(B, [&](int i, int Bi, int) { return lane_[i]->keygen(Bi, lane_seed(seed, i)); }));
+  keyed_B_ = B;
+  return hipSuccess;
+}
+
+hipError_t LaneSet::import_keys(int B, const void *k0, const void *k1, size_t bytes) {
+  if (bytes != key_bytes(B)) return hipErrorInvalidValue;
+  keyed_B_ = -1;
+  size_t o = 0;
+  TRY(each(B, [&](int i, int Bi, int) {
+    const size_t n = lane_[i]->key_bytes(Bi);
+    hipError_t r = lane_[i]->import_keys(Bi, static_cast<const uint8_t *>(k0) + o,
+                                         static_cast<const uint8_t *>(k1) + o, n);
+    o += n;
+    return r;
+  }));
+  keyed_B_ = B;
+  return hipSuccess;
+}
+
+hipError_t LaneSet::export_keys(int party, void *dst, size_t bytes) {
+  if (lanes() == 1) return lane_[0]->export_keys(party, dst, bytes);
+  if (keyed_B_ < 1 || bytes != key_bytes(keyed_B_)) return hipErrorInvalidValue;
+  size_t o = 0;
+  return each(keyed_B_, [&](int i, int Bi, int) {
+    const size_t n = lane_[i]->key_bytes(Bi);
+    hipError_t r = lane_[i]->export_keys(party, static_cast<uint8_t *>(dst) + o, n);
+    o += n;
+    return r;
+  });
+}
+
+hipError_t LaneSet::export_unique_keys(int party, void *dst, size_t bytes) {
+  if (keyed_B_ < 1 || bytes != unique_key_bytes(keyed_B_, party)) return hipErrorInvalidValue;
+  size_t o = 0;
+  return each(keyed_B_, [&](int i, int Bi, int) {
+    const size_t n = lane_[i]->unique_key_bytes(Bi, party);
+    hipError_t r = lane_[i]->export_unique_keys(party, static_cast<uint8_t *>(dst) + o, n);
+    o += n;
+    return r;
+  });
+}
+
+hipError_t LaneSet::release_arena() {
+  for (auto *m : lane_) TRY(m->release_arena());
+  return hipSuccess;
+}
+
+hipError_t LaneSet::attach_host_keys(int B, const void *h0, size_t bytes0, const void *h1, size_t bytes1,
+                                     size_t slot_bytes) {
+  if (bytes0 != key_bytes(B)) return hipErrorInvalidValue;
+  bool packed;
+  if (bytes1 == key_bytes(B))
+    packed = false;
+  else if (bytes1 == unique_key_bytes(B, 1))
+    packed = true;
+  else
+    return hipErrorInvalidValue;
+  keyed_B_ = -1;
+  size_t o0 = 0, o1 = 0;
+  TRY(each(B, [&](int i, int Bi, int) {
+    const size_t n0 = lane_[i]->key_bytes(Bi), n1 = packed ? lane_[i]->unique_key_bytes(Bi, 1) : n0;
+    hipError_t r = lane_[i]->attach_host_keys(Bi, static_cast<const uint8_t *>(h0) + o0, n0,
+                                              static_cast<const uint8_t *>(h1) + o1, n1, slot_bytes);
+    o0 += n0;
+    o1 += n1;
+    return r;
+  }));
+  keyed_B_ = B;
+  return hipSuccess;
+}
+
+hipError_t LaneSet::set_inputs(int B, const void *x0, const void *x1, const void *a0, const void *a1,
+                               const void *m0, const void *m1, const int64_t *prot) {
+  const size_t es = size_t(bw_ / 8), N = size_t(d_.n_nodes);
+  const size_t px = N * d_.feat * es, pa = N * N * es, pm = N * es;  // bytes per sample
+  auto at = [](const void *p, size_t o) { return static_cast<const uint8_t *>(p) + o; };
+  return each(B, [&](int i, int Bi, int off) {
+    const size_t o = size_t(off);
+    return lane_[i]->set_inputs(Bi, at(x0, o * px), at(x1, o * px), at(a0, o * pa), at(a1, o * pa), at(m0, o * pm),
+                                at(m1, o * pm), prot + o * d_.prot);
+  });
+}
+
+hipError_t LaneSet::forward(int B) {
+  const int n = active(B);
+  counters = Counters();
+  stream_stats = StreamStats();
+  for (int i = 0; i < n; i++) {
+    // Lanes past the first do not wait for the caller's stream: the forward
+    // reads only the model's own buffers (written by synchronous uploads), so a
+    // lane may start its next forward while the others finish this one; the
+    // join below makes the caller's stream wait for every lane.  A profiled
+    // forward runs lane i after lane i-1 so that launches do not overlap.
+    if (i > 0 && serial_) TRY(hipStreamWaitEvent(st_[i], done_[i - 1], 0));
+    lane_[i]->counters = Counters();
+    hipError_t r = lane_[i]->forward(lane_B(B, i));
+    if (r != hipSuccess) {
+      err = lane_[i]->err;
+      return r;
+    }
+    if (n > 1) TRY(hipEventRecord(done_[i], st_[i]));
+    counters.bytes += lane_[i]->counters.bytes;
+    counters.rounds = std::max(counters.rounds, lane_[i]->counters.rounds);
+    stream_stats.chunks += lane_[i]->stream_stats.chunks;
+    stream_stats.bytes_h2d += lane_[i]->stream_stats.bytes_h2d;
+  }
+  for (int i = 1; i < n; i++) TRY(hipStreamWaitEvent(st_[0], done_[i], 0));
+  return hipSuccess;
+}
+
+hipError_t LaneSet::output(int64_t *h_out, int B) {
+  return each(B, [&](int i, int Bi, int off) { return lane_[i]->output(h_out + off, Bi); });
+}
+
+void LaneSet::profile(bool on) {
+  for (auto *m : lane_) {
+    m->timer.reset();
+    m->timer.on = on;
+  }
+  serial_ = on;
+}
+
+hipError_t LaneSet::profile_read(int *launches, double *ms, double *elements, double *aes, double *hbm_bytes) {
+  double tot = 0, el = 0, ae = 0, by = 0;
+  int nl = 0;
+  for (size_t i = 0; i < lane_.size(); i++) {
+    TRY(hipStreamSynchronize(st_[i]));
+    const Phase1Timer &t = lane_[i]->timer;
+    for (size_t k = 0; k + 1 < t.ev.size(); k += 2) {
+      float f = 0;
+      TRY(hipEventElapsedTime(&f, t.ev[k], t.ev[k + 1]));
+      tot += f;
+      el += 2.0 * double(t.elems[k / 2]);
+      ae += 2.0 * double(t.elems[k / 2]) * double(t.levels[k / 2]);
+      by += t.bytes[k / 2];
+      nl++;
+    }
+  }
+  if (launches) *launches = nl;
+  if (ms) *ms = tot;
+  if (elements) *elements = el;
+  if (aes) *aes = ae;
+  if (hbm_bytes) *hbm_bytes = by;
+  return hipSuccess;
+}
+
+LaneSet *make_lane_set(int bw, int s, const ModelDims &d, const int64_t *W, size_t nW, const Launch &L,
+                       std::string *err) {
+  auto *ls = new LaneSet(bw, s, d, W, nW, L);
+  if (ls->set_lanes(1, err) != hipSuccess) {
+    if (err->empty()) *err = "model allocation failed";
+    delete ls;
+    return nullptr;
+  }
+  return ls;
+}
+
+// ===========================================================================
 // standalone secure adjacency normalisation
 // ===========================================================================
 size_t adjnorm_key_bytes(int bw, int s, int B, int N) { return AdjNorm<uint32_t>::layout_end(bw, s, B, N, 0); }
@@ -1069,30 +1281,55 @@ hipError_t adjnorm_keygen(int bw, int s, int B, int N, uint64_t seed, const Laun
                   : adjnorm_keygen_t<uint64_t>(bw, s, B, N, seed, L, out_mask, k0, k1);
 }
 
+struct AdjNormCache {
+  int bw = 0;
+  virtual ~AdjNormCache() = default;
+};
+
+void adjnorm_cache_free(AdjNormCache *cache) { delete cache; }
+
+namespace {
+template <typename T>
+struct AdjNormCacheT final : AdjNormCache {
+  AdjNorm<T> adj;
+  DevBuf<T> Ah;
+  Workspace<T> ws;
+};
+}  // namespace
+
 template <typename T>
 static hipError_t adjnorm_eval_t(int bw, int s, int B, int N, int nmax, const Launch &L, const uint8_t *k0,
-                                 const uint8_t *k1, const void *a0, const void *a1, void *out, Counters *ctr) {
-  AdjNorm<T> adj;
-  TRY(adj.prepare(B, N, s, nmax));
+                                 const uint8_t *k1, const void *a0, const void *a1, void *out, Counters *ctr,
+                                 AdjNormCache **cache) {
+  if (*cache && (*cache)->bw != bw) {
+    TRY(hipStreamSynchronize(L.stream));
+    delete *cache;
+    *cache = nullptr;
+  }
+  if (!*cache) {
+    auto *c = new AdjNormCacheT<T>();
+    c->bw = bw;
+    *cache = c;
+  }
+  auto *st = static_cast<AdjNormCacheT<T> *>(*cache);
+  TRY(st->adj.prepare(B, N, s, nmax));
   const size_t BNN = size_t(B) * N * N;
-  DevBuf<T> Ah;
-  TRY(Ah.alloc(BNN));
-  Workspace<T> ws;
-  TRY(ws.ensure(std::max(BNN, size_t(B) * pairs_of(N))));
+  TRY(st->Ah.alloc(BNN));
+  TRY(st->ws.ensure(std::max(BNN, size_t(B) * pairs_of(N))));
   ArenaSource src;
   src.k[0] = k0;
   src.k[1] = k1;
   src.bytes = AdjNorm<T>::layout_end(bw, s, B, N, 0);
   Counters local;
-  Runner<T> r(L, bw, s, ws, ctr ? *ctr : local, nullptr, src);
-  TRY(adj.eval(r, static_cast<const T *>(a0), static_cast<const T *>(a1), Ah.p, static_cast<T *>(out)));
+  Runner<T> r(L, bw, s, st->ws, ctr ? *ctr : local, nullptr, src);
+  TRY(st->adj.eval(r, static_cast<const T *>(a0), static_cast<const T *>(a1), st->Ah.p, static_cast<T *>(out)));
   return hipStreamSynchronize(L.stream);
 }
 
 hipError_t adjnorm_eval(int bw, int s, int B, int N, int nmax, const Launch &L, const uint8_t *k0, const uint8_t *k1,
-                        const void *a0, const void *a1, void *out, Counters *ctr) {
-  return bw == 32 ? adjnorm_eval_t<uint32_t>(bw, s, B, N, nmax, L, k0, k1, a0, a1, out, ctr)
-                  : adjnorm_eval_t<uint64_t>(bw, s, B, N, nmax, L, k0, k1, a0, a1, out, ctr);
+                        const void *a0, const void *a1, void *out, Counters *ctr, AdjNormCache **cache) {
+  return bw == 32 ? adjnorm_eval_t<uint32_t>(bw, s, B, N, nmax, L, k0, k1, a0, a1, out, ctr, cache)
+                  : adjnorm_eval_t<uint64_t>(bw, s, B, N, nmax, L, k0, k1, a0, a1, out, ctr, cache);
 }
 
 }  // namespace mpcx

@@ -73,6 +73,8 @@ _SIGS = {
                                    C.c_void_p]),
     "mpcx_model_create": (C.c_int, [C.c_void_p, C.c_void_p, C.c_void_p, C.c_size_t, C.c_void_p]),
     "mpcx_model_destroy": (None, [C.c_void_p]),
+    "mpcx_model_set_lanes": (C.c_int, [C.c_void_p, C.c_int]),
+    "mpcx_model_lanes": (C.c_int, [C.c_void_p]),
     "mpcx_model_key_bytes": (C.c_size_t, [C.c_void_p, C.c_int]),
     "mpcx_model_keygen": (C.c_int, [C.c_void_p, C.c_int, C.c_uint64]),
     "mpcx_model_import_keys": (C.c_int, [C.c_void_p, C.c_int, C.c_void_p, C.c_void_p, C.c_size_t]),
@@ -413,7 +415,7 @@ def model_dims(d):
 class Model:
     """The secure affinity model on one GPU (both parties)."""
 
-    def __init__(self, ctx: Ctx, dims, weights):
+    def __init__(self, ctx: Ctx, dims, weights, lanes=1):
         self.ctx = ctx
         self.lib = ctx.lib
         self.dims = dims
@@ -424,6 +426,30 @@ class Model:
         ctx.check(self.lib.mpcx_model_create(ctx.h, C.byref(self.md), w.ctypes.data_as(C.c_void_p), w.size,
                                              C.byref(h)), "model_create")
         self.h = h
+        if lanes != 1:
+            self.set_lanes(lanes)
+
+    def set_lanes(self, lanes):
+        """Concurrent sub-batches on their own streams (drops keys and inputs)."""
+        self.ctx.check(self.lib.mpcx_model_set_lanes(self.h, int(lanes)), "model_set_lanes")
+
+    @property
+    def lanes(self):
+        return int(self.lib.mpcx_model_lanes(self.h))
+
+    @staticmethod
+    def lane_split(B, lanes):
+        """[(sample offset, samples)] of each lane with samples."""
+        out, off = [], 0
+        for i in range(min(lanes, B)):
+            n = B // lanes + (1 if i < B % lanes else 0)
+            out.append((off, n))
+            off += n
+        return out
+
+    @staticmethod
+    def lane_seed(seed, i):
+        return (int(seed) + i * 0x9E3779B97F4A7C15) % (1 << 64)
 
     def close(self):
         if self.h:

@@ -214,6 +214,22 @@ typedef struct {
 mpcx_status mpcx_model_create(mpcx_ctx *ctx, const mpcx_model_dims *dims, const int64_t *h_weights,
                               size_t n_weights, mpcx_model **out);
 void mpcx_model_destroy(mpcx_model *m);
+/* Concurrent sub-batches: every batch of B is split into `lanes` (1..16)
+ * sub-batches of consecutive samples (B/lanes each, the first B%lanes one
+ * larger), each evaluated by its own copy of the gate sequence on its own
+ * stream; the context stream waits for every lane at the end of a forward.
+ * Lanes past the first do not wait for work enqueued on the context stream
+ * before the forward (the forward reads only the model's buffers, which
+ * mpcx_model_set_inputs fills synchronously).  The reference
+ * evaluates a batch as one gate sequence (DeepDTAGenAffinity<T>::_forward,
+ * gpu_mpc/deepdtagen.h:183-222); lanes let the gates of one sub-batch that
+ * leave the GPU partly idle overlap another's DCF evaluation.  Keys of a batch
+ * are the lanes' key sets back to back, lane i's being the one-lane key set
+ * of its samples under seed + i * 0x9E3779B97F4A7C15 (mod 2^64); with
+ * host-streamed keys each lane has its own two slots of slot_bytes.  Drops
+ * keys and inputs.  Default: 1 lane. */
+mpcx_status mpcx_model_set_lanes(mpcx_model *m, int lanes);
+int mpcx_model_lanes(const mpcx_model *m);
 /* Key bytes per party for a batch of B molecules. */
 size_t mpcx_model_key_bytes(const mpcx_model *m, int B);
 /* Dealer on the GPU: generates both parties' keys into the resident key arena
@@ -258,7 +274,9 @@ mpcx_status mpcx_model_set_inputs(mpcx_model *m, int B, const void *h_x0, const 
 mpcx_status mpcx_model_forward(mpcx_model *m, int B);
 /* Reconstructed outputs (B int64 at scale s); synchronizes the stream. */
 mpcx_status mpcx_model_output(mpcx_model *m, int B, int64_t *h_out);
-/* DCF (phase-1) kernel timing with HIP events on the launch stream. */
+/* DCF (phase-1) kernel timing with HIP events on the launch streams.  While
+ * enabled, forwards run their lanes one after another (each launch is timed
+ * alone) and launch the separately named k_tr_phase1<..., 1> instantiation. */
 mpcx_status mpcx_model_profile(mpcx_model *m, int enable);
 /* After a synchronized forward: number of phase-1 launches, their summed time
  * (ms), elements (both parties), AES calls (both parties) and algorithmic HBM

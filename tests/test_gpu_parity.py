@@ -262,6 +262,102 @@ def test_model_keys_and_forward(mp, orc, synth, bw):
     c.close()
 
 
+def _tr_gates(dims):
+    """DCF-evaluation launches of one forward: TRSLACK, 3 x (TR, TRRELU), the
+    pool levels, the two drug FCs and the hidden fusion layers."""
+    R, levels = dims.n_nodes, 0
+    while R > 1:
+        R, levels = R // 2 + (R & 1), levels + 1
+    return 1 + 6 + levels + 2 + len(dims.fus) - 1
+
+
+@pytest.mark.parametrize("bw,B,lanes", [(32, 5, 2), (64, 4, 3), (32, 2, 4)])
+def test_model_lanes_keys_and_forward(mp, orc, synth, bw, B, lanes):
+    """Concurrent sub-batches: the key arena is the lanes' one-lane key sets
+    back to back, each byte-identical to the oracle dealer's under its lane
+    seed; each lane's key set evaluates correctly in the oracle; the forward
+    gives the plaintext outputs and the lanes' summed exchange bytes; a profiled
+    forward (lanes one after another) gives the same outputs and times every
+    lane's DCF launches.  B=2 with 4 lanes leaves two lanes empty."""
+    wl = synth.workload(B, synth.Dims(bw=bw), seed=23)
+    d = _od(orc, wl.dims)
+    want, code = orc.plain_forward(d, wl.X, wl.A, wl.mask, wl.prot, wl.W)
+    assert code == 0
+    c = mp.Ctx(bw=bw)
+    m = mp.Model(c, wl.dims, wl.W, lanes=lanes)
+    assert m.lanes == lanes
+    split = mp.Model.lane_split(B, lanes)
+    assert len(split) == min(B, lanes) and sum(n for _, n in split) == B
+    assert m.key_bytes(B) == sum(orc.model_key_bytes(d, n) for _, n in split)
+    seed = 901
+    m.keygen(B, seed)
+    got = [m.export_keys(p, B) for p in (0, 1)]
+    x0, x1 = wl.shares["x"]
+    a0, a1 = wl.shares["a"]
+    m0, m1 = wl.shares["m"]
+    o, want_bytes = 0, 0
+    for i, (s0, n) in enumerate(split):
+        k0, k1 = orc.model_keygen(d, n, mp.Model.lane_seed(seed, i), wl.W)
+        assert np.array_equal(got[0][o:o + k0.size], k0)
+        assert np.array_equal(got[1][o:o + k1.size], k1)
+        o += k0.size
+        sl = slice(s0, s0 + n)
+        y, by = orc.model_eval(d, n, wl.W, k0, k1, x0[sl], x1[sl], a0[sl], a1[sl], m0[sl], m1[sl], wl.prot[sl])
+        assert np.array_equal(y, want[sl])
+        want_bytes += by
+    assert o == got[0].size
+    m.set_inputs(B, x0, x1, a0, a1, m0, m1, wl.prot)
+    c.reset_counters()
+    m.forward(B)
+    assert np.array_equal(m.output(B), want)
+    assert c.bytes_exchanged == want_bytes
+    m.profile(True)
+    m.forward(B)
+    prof = m.profile_read()
+    m.profile(False)
+    assert np.array_equal(m.output(B), want)
+    assert prof["launches"] == _tr_gates(wl.dims) * len(split) and prof["ms"] > 0
+    # lanes back to one: the keys are dropped, a fresh one-lane key set works
+    m.set_lanes(1)
+    with pytest.raises(mp.MpcxError):
+        m.forward(B)
+    m.keygen(B, seed)
+    m.set_inputs(B, x0, x1, a0, a1, m0, m1, wl.prot)
+    m.forward(B)
+    assert np.array_equal(m.output(B), want)
+    m.close()
+    c.close()
+
+
+def test_model_lanes_streamed_keys(mp, orc, synth):
+    """Two lanes on host-streamed keys (party 1 packed to its unique planes):
+    each lane streams its part of the host buffers through its own two slots."""
+    B, bw = 3, 64
+    wl = synth.workload(B, synth.Dims(bw=bw), seed=33)
+    d = _od(orc, wl.dims)
+    want, code = orc.plain_forward(d, wl.X, wl.A, wl.mask, wl.prot, wl.W)
+    assert code == 0
+    c = mp.Ctx(bw=bw)
+    m = mp.Model(c, wl.dims, wl.W, lanes=2)
+    m.keygen(B, 4321)
+    nbytes = m.key_bytes(B)
+    h0, hp = mp.PinnedBuffer(nbytes), mp.PinnedBuffer(m.unique_key_bytes(B, 1))
+    m.export_keys(0, B, into=h0)
+    m.export_unique_keys(1, B, into=hp)
+    m.release_arena()
+    m.attach_host_keys(B, h0, hp, slot_bytes=nbytes // 6)
+    m.set_inputs(B, *wl.shares["x"], *wl.shares["a"], *wl.shares["m"], wl.prot)
+    for _ in range(2):
+        m.forward(B)
+        assert np.array_equal(m.output(B), want)
+        st = m.stream_stats()
+        assert st["bytes_h2d"] == nbytes + hp.nbytes and st["chunks"] >= 4
+    m.close()
+    c.close()
+    h0.free()
+    hp.free()
+
+
 def test_model_forward_on_oracle_keys_config0(mp, orc, synth):
     """Config 0 shape (B=16, N=140, bw=32): keys from the oracle's dealer,
     online phase on the GPU, outputs equal to the plaintext forward."""
@@ -355,6 +451,14 @@ def test_adjnorm_keys_and_eval(mp, orc, synth, bw):
     want, oby = orc.adjnorm_eval(bw, S, B, N, 138, o0, o1, a0, a1)
     assert np.array_equal(got.astype(np.uint64), want)
     assert c.bytes_exchanged == oby
+    # the context keeps the prepared maps and scratch between calls: a smaller
+    # batch (re-prepared), then the first batch again, on the same context
+    g0s, g1s, gms = c.adjnorm_keygen(1, N, seed=124)
+    o0s, o1s, _ = orc.adjnorm_keygen(bw, S, 1, N, 124)
+    got1 = c.adjnorm_eval(1, N, 138, g0s, g1s, a0[:1], a1[:1])
+    want1, _ = orc.adjnorm_eval(bw, S, 1, N, 138, o0s, o1s, a0[:1], a1[:1])
+    assert np.array_equal(got1.astype(np.uint64), want1)
+    assert np.array_equal(c.adjnorm_eval(B, N, 138, g0, g1, a0, a1).astype(np.uint64), want)
     c.close()
 
 
