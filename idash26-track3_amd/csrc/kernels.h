@@ -23,6 +23,9 @@ struct Launch {
   // Launches of a profiled forward use a separately named instantiation of the
   // DCF-evaluation kernel (same code), so kernel traces can tell them apart.
   bool profiled = false;
+  // ring GEMM path over Z_2^32: 0 = int8 matrix cores (limb products), 1 = VALU
+  // (Z_2^64 always uses the VALU path)
+  int gemm = 0;
 };
 
 struct AesVariant {

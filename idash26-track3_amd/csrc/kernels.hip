@@ -634,9 +634,8 @@ template <typename T>
 hipError_t launch_reveal_eval(const Launch &L, const RevealLayout &lay, const uint8_t *k0, const uint8_t *k1,
                               const T *v0, const T *v1, int rowlen, T *msg0, T *msg1) {
   const int block = 256;
-  if (rowlen > 0) {  // one wave per row, no grid-stride: the rows' loads all in flight at once
-    const size_t blocks = (lay.N * 64 + block - 1) / block;
-    const int grid = int(blocks < size_t(1) << 30 ? (blocks < 1 ? 1 : blocks) : size_t(1) << 30);
+  if (rowlen > 0) {
+    int grid = grid_for(k_reveal_rowsum<T>, block, lay.N * 64, L.num_cu);
     hipLaunchKernelGGL((k_reveal_rowsum<T>), dim3(grid, 2), dim3(block), 0, L.stream, lay.N,
                        reinterpret_cast<const T *>(k0 + lay.off_r), reinterpret_cast<const T *>(k1 + lay.off_r), v0,
                        v1, rowlen, msg0, msg1);
@@ -739,10 +738,74 @@ __global__ void k_mul_eval(size_t nz, const T *Rx0, const T *Rx1, const T *Ry0, 
   }
 }
 
+// A (.) W with W symmetric, stored as its upper triangle (SYM_HADAMARD): one
+// workgroup per (graph, tile of TI rows, party).  The tile's W entries are
+// staged in LDS as a dense TI x N block so that every global read is a
+// contiguous run: row i of the triangle for columns j >= i, and for j < i the
+// run of entries (j, i0..i0+TI-1) of triangle row j.  The tile's outputs are
+// then consecutive elements of A_norm, read and written coalesced.
+template <typename T, int TI>
+__global__ void k_mul_eval_sym(uint32_t N, const T *Rx0, const T *Rx1, const T *Ry0, const T *Ry1, const T *C0,
+                               const T *C1, const T *xhat, const T *yhat, T *msg0, T *msg1) {
+  extern __shared__ unsigned char lds_raw[];
+  T *Wy = reinterpret_cast<T *>(lds_raw);
+  T *Wr = Wy + TI * N;
+  const int p = blockIdx.y;
+  const T *Rx = p ? Rx1 : Rx0;
+  const T *Ry = p ? Ry1 : Ry0;
+  const T *Cc = p ? C1 : C0;
+  T *msg = p ? msg1 : msg0;
+  const uint32_t tiles = (N + TI - 1) / TI, P = N * (N + 1) / 2;
+  const uint32_t g = blockIdx.x / tiles, i0 = (blockIdx.x - g * tiles) * TI;
+  const uint32_t ni = N - i0 < uint32_t(TI) ? N - i0 : uint32_t(TI);
+  const T *yg = yhat + size_t(g) * P, *rg = Ry + size_t(g) * P;
+  // columns j >= i: triangle row i
+  for (uint32_t ii = 0; ii < ni; ii++) {
+    const uint32_t i = i0 + ii, base = pair_row_start(N, i) - i;
+    for (uint32_t j = i + threadIdx.x; j < N; j += blockDim.x) {
+      Wy[ii * N + j] = yg[base + j];
+      Wr[ii * N + j] = rg[base + j];
+    }
+  }
+  // columns j < i: entry (j, i) of triangle row j, tile rows fastest
+  const uint32_t nj = i0 + ni - 1;
+  for (uint32_t t = threadIdx.x; t < nj * TI; t += blockDim.x) {
+    const uint32_t j = t / TI, ii = t - j * TI, i = i0 + ii;
+    if (ii < ni && j < i) {
+      const uint32_t q = pair_row_start(N, j) + (i - j);
+      Wy[ii * N + j] = yg[q];
+      Wr[ii * N + j] = rg[q];
+    }
+  }
+  __syncthreads();
+  const size_t kb = (size_t(g) * N + i0) * N;
+  for (uint32_t t = threadIdx.x; t < ni * N; t += blockDim.x) {
+    const size_t k = kb + t;
+    const T x = xhat[k], y = Wy[t];
+    T z = Cc[k] - x * Wr[t] - y * Rx[k];
+    if (p == 0) z += x * y;
+    msg[k] = z;
+  }
+}
+
 template <typename T>
 hipError_t launch_mul_eval(const Launch &L, const MulLayout &lay, const uint8_t *k0, const uint8_t *k1,
                            const MulMap &map, const T *xhat, const T *yhat, T *msg0, T *msg1) {
   const int block = 256;
+  if (map.kind == MulMap::SYM_HADAMARD) {
+    constexpr int TI = sizeof(T) == 4 ? 16 : 8;
+    const size_t N = map.N, NN = N * N, P = N * (N + 1) / 2;
+    if (N == 0 || lay.nz % NN != 0 || lay.nx != lay.nz || lay.ny != (lay.nz / NN) * P) return hipErrorInvalidValue;
+    const size_t tiles = (N + TI - 1) / TI, blocks = (lay.nz / NN) * tiles;
+    if (blocks >= (size_t(1) << 31)) return hipErrorInvalidValue;
+    const size_t lds = 2 * TI * N * sizeof(T);
+    hipLaunchKernelGGL((k_mul_eval_sym<T, TI>), dim3(unsigned(blocks), 2), dim3(block), lds, L.stream,
+                       uint32_t(N), reinterpret_cast<const T *>(k0 + lay.off_rx),
+                       reinterpret_cast<const T *>(k1 + lay.off_rx), reinterpret_cast<const T *>(k0 + lay.off_ry),
+                       reinterpret_cast<const T *>(k1 + lay.off_ry), reinterpret_cast<const T *>(k0 + lay.off_c),
+                       reinterpret_cast<const T *>(k1 + lay.off_c), xhat, yhat, msg0, msg1);
+    return hipGetLastError();
+  }
   int grid = grid_for(k_mul_eval<T>, block, lay.nz, L.num_cu);
   hipLaunchKernelGGL((k_mul_eval<T>), dim3(grid, 2), dim3(block), 0, L.stream, lay.nz,
                      reinterpret_cast<const T *>(k0 + lay.off_rx), reinterpret_cast<const T *>(k1 + lay.off_rx),
@@ -971,6 +1034,128 @@ __global__ __launch_bounds__(256) void k_gemm(GemmArgs<T> g) {
   }
 }
 
+// ---------------------------------------------------------------------------
+// ring GEMM over Z_2^32 on the int8 matrix cores (v_mfma_i32_16x16x64_i8).
+// Balanced base-256 digits: the bytes of y = (a + 0x80808080) ^ 0x80808080,
+// read as signed int8 d_0..d_3 in [-128, 127], satisfy a = sum_p d_p 2^(8p)
+// mod 2^32 (y - 0x80808080 = a, and byte ^ 0x80 read as int8 is byte - 128).
+// Hence a*b mod 2^32 = sum_{s<4} 2^(8s) sum_{p+q=s} a_p b_q.  One MFMA takes 16
+// operand words per row and column (4 digit bytes each); with the row words'
+// digits permuted to (a_s, a_{s-1}, .., a_0, 0, ..) it returns the shift-s sum
+// over those 16 words, so four MFMAs (s = 0..3) cover 16 k.  The int32
+// accumulators wrap, and only acc_s mod 2^(32-8s) enters the result.
+// Tile: 64 x 64 per 256-thread block; wave w owns rows 16w..16w+15 and the four
+// 16-column MFMA tiles; K staged through LDS in slices of 64 words (A as
+// [m][k], B transposed to [n][k], rows padded to 68 words).  Split-K and the
+// epilogue follow k_gemm.
+// ---------------------------------------------------------------------------
+typedef int v4i_t __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ uint32_t ring_digits(uint32_t a) { return (a + 0x80808080u) ^ 0x80808080u; }
+
+__global__ __launch_bounds__(256) void k_gemm_mfma(GemmArgs<uint32_t> g) {
+  constexpr int BM = 64, BN = 64, BK = 64, LD = BK + 4;
+  __shared__ __align__(16) uint32_t As[BM * LD];
+  __shared__ __align__(16) uint32_t Bt[BN * LD];
+  const int bz = blockIdx.z / g.ksplit, kz = blockIdx.z % g.ksplit;
+  const int kchunk = ((g.K + g.ksplit - 1) / g.ksplit + BK - 1) / BK * BK;
+  const int kbeg = kz * kchunk, kend = min(g.K, kbeg + kchunk);
+  const uint32_t *A1 = g.A1 + size_t(bz) * g.sA;
+  const uint32_t *A2 = g.A2 ? g.A2 + size_t(bz) * g.sA : nullptr;
+  const uint32_t *B1 = g.B1 + size_t(bz) * g.sB;
+  const uint32_t *B2 = g.B2 ? g.B2 + size_t(bz) * g.sB : nullptr;
+  const int m0 = blockIdx.y * BM, n0 = blockIdx.x * BN;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int li = lane & 15, lg = lane >> 4;
+  v4i_t acc[4][4];
+#pragma unroll
+  for (int t = 0; t < 4; t++)
+#pragma unroll
+    for (int q = 0; q < 4; q++) acc[t][q] = v4i_t{0, 0, 0, 0};
+  // Each thread stages 16 words of the A tile (row hi, column lo) and 16 of the
+  // B tile (row hi, column lo; stored at Bt[lo][hi]), hi = (tid >> 6) + 4r,
+  // lo = tid & 63.  The next slice's words are loaded into registers while the
+  // matrix cores work on the current one.
+  uint32_t ra[16], rb[16];
+  const int lo = tid & 63, hb = tid >> 6;
+  auto load = [&](int k0) {
+#pragma unroll
+    for (int r = 0; r < 16; r++) {
+      const int hi = hb + 4 * r;
+      const int gm = m0 + hi, gk = k0 + lo;
+      uint32_t v = 0;
+      if (gm < g.M && gk < kend) {
+        const size_t idx = size_t(gm) * g.K + gk;
+        v = A1[idx];
+        if (A2) v -= A2[idx];
+      }
+      ra[r] = v;
+    }
+#pragma unroll
+    for (int r = 0; r < 16; r++) {
+      const int hi = hb + 4 * r;
+      const int gk = k0 + hi, gn = n0 + lo;
+      uint32_t v = 0;
+      if (gk < kend && gn < g.N) {
+        const size_t idx = size_t(gk) * g.N + gn;
+        v = B1[idx];
+        if (B2) v -= B2[idx];
+      }
+      rb[r] = v;
+    }
+  };
+  if (kbeg < kend) load(kbeg);
+  for (int k0 = kbeg; k0 < kend; k0 += BK) {
+#pragma unroll
+    for (int r = 0; r < 16; r++) {
+      const int hi = hb + 4 * r;
+      As[hi * LD + lo] = ring_digits(ra[r]);
+      Bt[lo * LD + hi] = ring_digits(rb[r]);
+    }
+    __syncthreads();
+    if (k0 + BK < kend) load(k0 + BK);
+#pragma unroll
+    for (int kc = 0; kc < BK / 16; kc++) {
+      const uint4 a = *reinterpret_cast<const uint4 *>(&As[(wave * 16 + li) * LD + kc * 16 + lg * 4]);
+      v4i_t as[4];
+      // byte p of the shift-s word: digit s-p of the row word (0x0c selects a zero byte)
+      constexpr uint32_t sel[4] = {0x0c0c0c00u, 0x0c0c0001u, 0x0c000102u, 0x00010203u};
+#pragma unroll
+      for (int q = 0; q < 4; q++)
+        as[q] = v4i_t{int(__builtin_amdgcn_perm(0u, a.x, sel[q])), int(__builtin_amdgcn_perm(0u, a.y, sel[q])),
+                      int(__builtin_amdgcn_perm(0u, a.z, sel[q])), int(__builtin_amdgcn_perm(0u, a.w, sel[q]))};
+#pragma unroll
+      for (int t = 0; t < 4; t++) {
+        const uint4 b = *reinterpret_cast<const uint4 *>(&Bt[(t * 16 + li) * LD + kc * 16 + lg * 4]);
+        const v4i_t bv = v4i_t{int(b.x), int(b.y), int(b.z), int(b.w)};
+#pragma unroll
+        for (int q = 0; q < 4; q++) acc[t][q] = __builtin_amdgcn_mfma_i32_16x16x64_i8(as[q], bv, acc[t][q], 0, 0, 0);
+      }
+    }
+    __syncthreads();
+  }
+  uint32_t *C = g.C + size_t(bz) * g.sC;
+  const uint32_t *Cin = g.Cin ? g.Cin + size_t(bz) * g.sC : nullptr;
+#pragma unroll
+  for (int t = 0; t < 4; t++) {
+    const int gn = n0 + t * 16 + li;
+#pragma unroll
+    for (int r = 0; r < 4; r++) {
+      // accumulator register r of lane (li, lg): row 4*lg + r, column li of the tile
+      const int gm = m0 + wave * 16 + lg * 4 + r;
+      if (gm >= g.M || gn >= g.N) continue;
+      uint32_t v = uint32_t(acc[t][0][r]) + (uint32_t(acc[t][1][r]) << 8) + (uint32_t(acc[t][2][r]) << 16) +
+                   (uint32_t(acc[t][3][r]) << 24);
+      if (g.sign < 0) v = 0u - v;
+      const size_t idx = size_t(gm) * g.N + gn;
+      if (g.ksplit > 1)
+        atomicAdd(reinterpret_cast<unsigned int *>(&C[idx]), static_cast<unsigned int>(v));
+      else
+        C[idx] = Cin ? v + Cin[idx] : v;
+    }
+  }
+}
+
 // C[b] = Cin[b] (or 0) before the split-K slices are added
 template <typename T>
 __global__ void k_gemm_init(int M, int N, int batch, size_t sC, const T *Cin, T *C) {
@@ -985,11 +1170,13 @@ template <typename T>
 hipError_t launch_gemm(const Launch &L, const GemmArgs<T> &g0) {
   if (g0.M <= 0 || g0.N <= 0 || g0.batch <= 0) return hipSuccess;
   GemmArgs<T> g = g0;
+  constexpr bool kMfma = sizeof(T) == 4;
+  const bool mfma = kMfma && L.gemm == 0;
   const int tiles = ((g.N + 63) / 64) * ((g.M + 63) / 64) * g.batch;
   g.ksplit = 1;
   if (tiles < L.num_cu && g.K >= 64) {
     const int want = (2 * L.num_cu + tiles - 1) / tiles;
-    g.ksplit = std::max(1, std::min(want, g.K / 32));
+    g.ksplit = std::max(1, std::min(want, mfma ? (g.K + 63) / 64 : g.K / 32));
   }
   if (g.ksplit > 1 && g.C != g.Cin) {
     const int block = 256;
@@ -999,6 +1186,12 @@ hipError_t launch_gemm(const Launch &L, const GemmArgs<T> &g0) {
     if (e != hipSuccess) return e;
   }
   dim3 grid((g.N + 63) / 64, (g.M + 63) / 64, g.batch * g.ksplit);
+  if constexpr (kMfma) {
+    if (mfma) {
+      hipLaunchKernelGGL(k_gemm_mfma, grid, dim3(256), 0, L.stream, g);
+      return hipGetLastError();
+    }
+  }
   hipLaunchKernelGGL((k_gemm<T>), grid, dim3(256), 0, L.stream, g);
   return hipGetLastError();
 }

@@ -202,16 +202,34 @@ def test_sxs_keys_and_eval(ctx, orc):
     assert np.array_equal(signed(c.astype(np.uint64) - orc_, bw).reshape(nb, Mm, N), np.einsum("bmk,bkn->bmn", A, B))
 
 
-@pytest.mark.parametrize("shape", [(130, 77, 65), (64, 1024, 128), (64, 512, 1), (3, 1000, 70), (64, 312, 1024)])
+GEMM_SHAPES = [(130, 77, 65), (64, 1024, 128), (64, 512, 1), (3, 1000, 70), (64, 312, 1024), (1, 1, 1),
+               (17, 63, 5), (200, 64, 64), (140, 140, 312)]
+
+
+@pytest.mark.parametrize("shape", GEMM_SHAPES)
 def test_ring_gemm(ctx, orc, shape):
     """Square-ish and skinny (FC-layer, split-K with atomic accumulation)
-    products mod 2^bw against the oracle's exact ring GEMM."""
+    products mod 2^bw against the oracle's exact ring GEMM, uniform operands
+    (every balanced digit value occurs)."""
     bw = ctx.bw
     M, K, N = shape
     rng = np.random.default_rng(M * K + N)
     A = rmask(rng, M * K, bw).reshape(M, K)
     B = rmask(rng, K * N, bw).reshape(K, N)
     assert np.array_equal(ctx.ring_gemm(A, B).astype(np.uint64), orc.ring_gemm(bw, A, B))
+
+
+def test_ring_gemm_valu_path(mp, orc, monkeypatch):
+    """Z_2^32 products on the VALU path (MPCX_GEMM=valu; the default is the
+    int8 matrix-core path) agree with the oracle too."""
+    monkeypatch.setenv("MPCX_GEMM", "valu")
+    c = mp.Ctx(bw=32)
+    for M, K, N in [(130, 77, 65), (64, 512, 1), (140, 140, 312)]:
+        rng = np.random.default_rng(M + K + N)
+        A = rmask(rng, M * K, 32).reshape(M, K)
+        B = rmask(rng, K * N, 32).reshape(K, N)
+        assert np.array_equal(c.ring_gemm(A, B).astype(np.uint64), orc.ring_gemm(32, A, B))
+    c.close()
 
 
 def test_reveal_keys_and_eval(ctx, orc):
