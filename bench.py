@@ -21,6 +21,10 @@ METRIC = "online secure samples/s (bw=32, B=64, 1 GPU); DCF evals/s; % roofline"
 # Peak integer VALU rate of MI355X: 256 CUs x 4 SIMD x 16 lanes x 2.4 GHz.
 VALU_PEAK_TOPS = 256 * 64 * 2.4e9 / 1e12
 HBM_PEAK_GBS = 8000.0
+# Ring multiply-adds per second at the peak of each Z_2^32 GEMM path: the int8
+# matrix cores (5.0 POP/s dense = 2.5 P int8 MAC/s) spend 16 int8 MACs per ring
+# MAC (four digit bytes x four shift MFMAs); the VALU path 2 instructions.
+GEMM_PEAK_TMACS = {"mfma": 5.0e3 / 2 / 16, "valu": VALU_PEAK_TOPS / 2}
 # VALU instructions per AES call of the DCF walk (one tree level: the unrolled
 # cipher, sigma, feed-forward and the level update), counted in the gfx950 ISA
 # of this build: hipcc --cuda-device-only -S csrc/kernels.hip, level-loop block
@@ -30,7 +34,7 @@ HBM_PEAK_GBS = 8000.0
 # 19 per lane), each scaled by the same counter's reading for a 1 GiB elementwise
 # copy (FETCH_SIZE x 2.0, WRITE_SIZE x 1.0); keyed by (variant, B, bw, lanes).
 # The summary is profiles/k_tr_phase1_affinity_bw32_B64.md.
-TRAFFIC_BYTES_PER_LAUNCH = {("perm64_b512", 64, 32, 3): 229643024, ("perm64_b512", 64, 32, 1): 689753000}
+TRAFFIC_BYTES_PER_LAUNCH = {("perm64_b512", 64, 32, 3): 229638822, ("perm64_b512", 64, 32, 1): 689753000}
 VALU_OPS_PER_AES = {"perm64_b512": 402, "perm64_b1024": 402, "t4_rep32_b1024": 462}
 
 
@@ -126,6 +130,8 @@ def main():
     key_gbs = prof["hbm_bytes"] / (dcf_ms / 1e3) / 1e9 if dcf_ms > 0 else 0.0
     achieved_tops = aes_per_s * VALU_OPS_PER_AES.get(variant, float("nan")) / 1e12
     step_tops = prof["aes_calls"] * VALU_OPS_PER_AES.get(variant, float("nan")) / (ms_per_step / 1e3) / 1e12
+    gemm_path = "valu" if (args.bw == 64 or os.environ.get("MPCX_GEMM") == "valu") else "mfma"
+    gemm_tmacs = prof["gemm_macs"] / (prof["gemm_ms"] / 1e3) / 1e12 if prof["gemm_ms"] > 0 else 0.0
     log(f"[bench] DCF phase-1: {prof['launches']} launches, {dcf_ms:.2f} ms/forward, "
         f"{dcf_evals_per_s / 1e9:.3f} G evals/s, {aes_per_s / 1e9:.2f} G AES/s")
 
@@ -175,6 +181,17 @@ def main():
             "peak": round(VALU_PEAK_TOPS, 2),
             "unit": "TOP/s",
             "frac": round(step_tops / VALU_PEAK_TOPS, 4),
+        },
+        "roofline_gemm": {
+            "kernel": f"ring GEMMs ({gemm_path}: public-weight products and SxS Beaver products, "
+                      f"{prof['gemm_sections']} sections of the profiled forward)",
+            "bound": "mfma" if gemm_path == "mfma" else "valu",
+            "achieved": round(gemm_tmacs, 3),
+            "peak": round(GEMM_PEAK_TMACS[gemm_path], 2),
+            "unit": "T ring MAC/s",
+            "frac": round(gemm_tmacs / GEMM_PEAK_TMACS[gemm_path], 4),
+            "ms_per_step": round(prof["gemm_ms"], 3),
+            "ring_macs_per_step": prof["gemm_macs"],
         },
         "roofline_hbm": {
             "kernel": "k_tr_phase1 key stream",

@@ -763,3 +763,9 @@ mpcx_status mpcx_model_profile_read(mpcx_model *m, int *launches, double *ms, do
   HIPC(m->ctx, m->impl->profile_read(launches, ms, elements, aes, hbm_bytes), "model_profile_read");
   return MPCX_OK;
 }
+
+mpcx_status mpcx_model_profile_gemm(mpcx_model *m, int *sections, double *ms, double *ring_macs) {
+  if (!m) return MPCX_EINVAL;
+  HIPC(m->ctx, m->impl->profile_gemm(sections, ms, ring_macs), "model_profile_gemm");
+  return MPCX_OK;
+}

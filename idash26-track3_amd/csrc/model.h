@@ -61,6 +61,10 @@ struct Phase1Timer {
   std::vector<size_t> elems;   // elements per launch
   std::vector<int> levels;     // AES calls per element per party
   std::vector<double> bytes;   // algorithmic HBM bytes per launch (both parties)
+  // ring GEMMs: start/stop pairs around each GEMM (an SxS gate's three Beaver
+  // products as one pair) and the ring multiply-adds inside
+  std::vector<hipEvent_t> gev;
+  std::vector<double> gmacs;
   void reset();
 };
 
@@ -138,6 +142,7 @@ class LaneSet {
   // the lanes one after another, so every launch is timed alone.
   void profile(bool on);
   hipError_t profile_read(int *launches, double *ms, double *elements, double *aes, double *hbm_bytes);
+  hipError_t profile_gemm(int *launches, double *ms, double *macs);
 
   Counters counters;         // last forward: bytes summed over lanes, rounds of one lane
   StreamStats stream_stats;  // last forward, summed over lanes

@@ -17,11 +17,39 @@ namespace mpcx {
 
 void Phase1Timer::reset() {
   for (auto e : ev) (void)hipEventDestroy(e);
+  for (auto e : gev) (void)hipEventDestroy(e);
   ev.clear();
   elems.clear();
   levels.clear();
   bytes.clear();
+  gev.clear();
+  gmacs.clear();
 }
+
+namespace {
+// start/stop events around a ring-GEMM section when profiling
+struct GemmSpan {
+  Phase1Timer *t;
+  hipStream_t st;
+  hipEvent_t e1 = nullptr;
+  hipError_t begin(double macs) {
+    if (!t || !t->on) return hipSuccess;
+    hipEvent_t e0;
+    hipError_t r = hipEventCreate(&e0);
+    if (r == hipSuccess) r = hipEventCreate(&e1);
+    if (r == hipSuccess) r = hipEventRecord(e0, st);
+    if (r != hipSuccess) return r;
+    t->gev.push_back(e0);
+    t->gmacs.push_back(macs);
+    return hipSuccess;
+  }
+  hipError_t end() {
+    if (!e1) return hipSuccess;
+    t->gev.push_back(e1);
+    return hipEventRecord(e1, st);
+  }
+};
+}  // namespace
 
 #define TRY(x)                           \
   do {                                   \
@@ -226,6 +254,8 @@ struct Runner {
     TRY(enter(end, &b));
     SxsLayout lay = sxs_layout(bw, nb, M, K, N, b);
     const uint8_t *K0 = kv.k[0], *K1 = kv.k[1];
+    GemmSpan span{timer, L.stream};
+    TRY(span.begin(3.0 * nb * double(M) * K * N));
     GemmArgs<T> g;
     g.M = M;
     g.K = K;
@@ -255,6 +285,7 @@ struct Runner {
     h.B1 = Bm;
     h.Cin = ws.m1.p;
     TRY(launch_gemm<T>(L, h));
+    TRY(span.end());
     const size_t nc = size_t(nb) * M * N;
     ctr.msg(nc, bw);
     TRY(launch_reconstruct<T>(L, nc, ws.m0.p, ws.m1.p, out));
@@ -888,6 +919,8 @@ class Model final : public ModelBase, KeySource {
     auto pub_gemm = [&](const T *x, int l, size_t rows, T *y) -> hipError_t {
       int in, out;
       layer_io(l, &in, &out);
+      GemmSpan span{&timer, L_.stream};
+      TRY(span.begin(double(rows) * in * out));
       GemmArgs<T> g;
       g.M = int(rows);
       g.K = in;
@@ -895,7 +928,8 @@ class Model final : public ModelBase, KeySource {
       g.A1 = x;
       g.B1 = wt_[l].p;
       g.C = y;
-      return launch_gemm<T>(L_, g);
+      TRY(launch_gemm<T>(L_, g));
+      return span.end();
     };
     T *H = bA_.p, *Z = bB_.p, *XW = bC_.p;
 
@@ -1244,6 +1278,26 @@ hipError_t LaneSet::profile_read(int *launches, double *ms, double *elements, do
   if (elements) *elements = el;
   if (aes) *aes = ae;
   if (hbm_bytes) *hbm_bytes = by;
+  return hipSuccess;
+}
+
+hipError_t LaneSet::profile_gemm(int *launches, double *ms, double *macs) {
+  double tot = 0, mc = 0;
+  int nl = 0;
+  for (size_t i = 0; i < lane_.size(); i++) {
+    TRY(hipStreamSynchronize(st_[i]));
+    const Phase1Timer &t = lane_[i]->timer;
+    for (size_t k = 0; k + 1 < t.gev.size(); k += 2) {
+      float f = 0;
+      TRY(hipEventElapsedTime(&f, t.gev[k], t.gev[k + 1]));
+      tot += f;
+      mc += t.gmacs[k / 2];
+      nl++;
+    }
+  }
+  if (launches) *launches = nl;
+  if (ms) *ms = tot;
+  if (macs) *macs = mc;
   return hipSuccess;
 }
 

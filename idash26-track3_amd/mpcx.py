@@ -96,6 +96,7 @@ _SIGS = {
     "mpcx_host_alloc": (C.c_int, [C.c_size_t, C.c_void_p]),
     "mpcx_host_free": (None, [C.c_void_p]),
     "mpcx_model_profile_read": (C.c_int, [C.c_void_p] + [C.c_void_p] * 5),
+    "mpcx_model_profile_gemm": (C.c_int, [C.c_void_p] + [C.c_void_p] * 3),
 }
 
 
@@ -542,5 +543,8 @@ class Model:
         ms, el, ae, by = C.c_double(), C.c_double(), C.c_double(), C.c_double()
         self.ctx.check(self.lib.mpcx_model_profile_read(self.h, C.byref(n), C.byref(ms), C.byref(el), C.byref(ae),
                                                         C.byref(by)), "profile_read")
+        gn, gms, gmac = C.c_int(), C.c_double(), C.c_double()
+        self.ctx.check(self.lib.mpcx_model_profile_gemm(self.h, C.byref(gn), C.byref(gms), C.byref(gmac)),
+                       "profile_gemm")
         return {"launches": n.value, "ms": ms.value, "elements": el.value, "aes_calls": ae.value,
-                "hbm_bytes": by.value}
+                "hbm_bytes": by.value, "gemm_sections": gn.value, "gemm_ms": gms.value, "gemm_macs": gmac.value}

@@ -283,6 +283,11 @@ mpcx_status mpcx_model_profile(mpcx_model *m, int enable);
  * bytes (keys and inputs read, message bits written; both parties). */
 mpcx_status mpcx_model_profile_read(mpcx_model *m, int *launches, double *ms, double *elements,
                                     double *aes_calls, double *hbm_bytes);
+/* After a synchronized profiled forward: ring-GEMM sections (one per public-
+ * weight product, one per SxS gate's three Beaver products), their summed time
+ * (ms, HIP events on the launch streams) and the ring multiply-adds inside
+ * (the reference's gpuMatmul, gpu_mpc/ddg_orca_base.h:170-271). */
+mpcx_status mpcx_model_profile_gemm(mpcx_model *m, int *sections, double *ms, double *ring_macs);
 
 #ifdef __cplusplus
 }

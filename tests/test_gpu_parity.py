@@ -335,6 +335,23 @@ def test_model_lanes_keys_and_forward(mp, orc, synth, bw, B, lanes):
     m.profile(False)
     assert np.array_equal(m.output(B), want)
     assert prof["launches"] == _tr_gates(wl.dims) * len(split) and prof["ms"] > 0
+    # ring GEMM sections: per lane 3 public GCN products, 3 SxS gates, 2 drug FCs
+    # and the fusion layers, with their ring multiply-adds
+    dm = wl.dims
+    widths = [dm.feat] + list(dm.gcn)
+    fc = [(dm.gcn[2], dm.dfc[0]), (dm.dfc[0], dm.dfc[1])]
+    fin = dm.dfc[1] + dm.prot
+    for w in dm.fus:
+        fc.append((fin, w))
+        fin = w
+    macs = 0
+    for _, n in split:
+        rows = n * dm.n_nodes
+        macs += sum(rows * widths[l] * widths[l + 1] for l in range(3))
+        macs += sum(3 * n * dm.n_nodes * dm.n_nodes * f for f in dm.gcn)
+        macs += sum(n * a * b for a, b in fc)
+    assert prof["gemm_sections"] == (8 + len(dm.fus)) * len(split)
+    assert prof["gemm_macs"] == macs and prof["gemm_ms"] > 0
     # lanes back to one: the keys are dropped, a fresh one-lane key set works
     m.set_lanes(1)
     with pytest.raises(mp.MpcxError):
