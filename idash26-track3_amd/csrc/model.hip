@@ -624,6 +624,7 @@ class Model final : public ModelBase, KeySource {
 
   hipError_t ensure_work(int B) {
     if (B == work_B_) return hipSuccess;
+    TRY(hipStreamSynchronize(L_.stream));  // buffers may be reallocated under earlier work
     const int N = d_.n_nodes;
     const size_t E = emax(B), BN = size_t(B) * N, BNN = BN * N;
     for (auto *b : {&bA_, &bB_, &bC_}) TRY(b->alloc(E));
@@ -642,6 +643,7 @@ class Model final : public ModelBase, KeySource {
   // ---------------- dealer ----------------
   hipError_t keygen(int B, uint64_t seed) override {
     if (streaming_) return hipErrorInvalidValue;
+    TRY(hipStreamSynchronize(L_.stream));  // a running forward may still read the arena
     TRY(ensure_arena(B));
     TRY(ensure_work(B));
     const int N = d_.n_nodes, bw = bw_;
@@ -722,6 +724,7 @@ class Model final : public ModelBase, KeySource {
 
   hipError_t import_keys(int B, const void *k0, const void *k1, size_t bytes) override {
     if (streaming_ || bytes != key_bytes(B)) return hipErrorInvalidValue;
+    TRY(hipStreamSynchronize(L_.stream));  // a running forward may still read the arena
     TRY(ensure_arena(B));
     TRY(hipMemcpy(arena_[0], k0, bytes, hipMemcpyHostToDevice));
     TRY(hipMemcpy(arena_[1], k1, bytes, hipMemcpyHostToDevice));
