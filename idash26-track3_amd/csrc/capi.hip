@@ -710,6 +710,28 @@ mpcx_status mpcx_model_attach_host_keys(mpcx_model *m, int B, const void *k0, si
   return MPCX_OK;
 }
 
+mpcx_status mpcx_model_write_keys(mpcx_model *m, int party, int packed, const char *path, int append) {
+  if (!m || !path || (party != 0 && party != 1) || (packed && party != 1)) return MPCX_EINVAL;
+  hipError_t e = m->impl->write_keys(party, packed != 0, path, append != 0);
+  if (e == hipErrorInvalidValue) return fail(m->ctx, MPCX_ESTATE, "write_keys: no resident keys");
+  if (e == hipErrorFileNotFound) return fail(m->ctx, MPCX_EIO, std::string("write_keys: cannot write ") + path);
+  HIPC(m->ctx, e, "model_write_keys");
+  return MPCX_OK;
+}
+
+mpcx_status mpcx_model_attach_key_files(mpcx_model *m, int B, const char *path0, const char *path1,
+                                        size_t slot_bytes) {
+  if (!m || !path0 || !path1) return MPCX_EINVAL;
+  if (B < 1 || slot_bytes == 0) return fail(m->ctx, MPCX_EINVAL, "attach_key_files: bad argument");
+  hipError_t e = m->impl->attach_key_files(B, path0, path1, slot_bytes);
+  if (e == hipErrorFileNotFound)
+    return fail(m->ctx, MPCX_EIO, "attach_key_files: key files missing or not whole key sets of this batch");
+  if (e == hipErrorInvalidValue)
+    return fail(m->ctx, MPCX_EINVAL, "attach_key_files: slot_bytes smaller than the largest gate key");
+  HIPC(m->ctx, e, "model_attach_key_files");
+  return MPCX_OK;
+}
+
 size_t mpcx_model_unique_key_bytes(const mpcx_model *m, int B, int party) {
   return (m && B > 0 && (party == 0 || party == 1)) ? m->impl->unique_key_bytes(B, party) : 0;
 }
@@ -739,6 +761,7 @@ mpcx_status mpcx_model_forward(mpcx_model *m, int B) {
   if (!m) return MPCX_EINVAL;
   hipError_t e = m->impl->forward(B);
   if (e == hipErrorInvalidValue) return fail(m->ctx, MPCX_ESTATE, "forward: keys or inputs not set for this B");
+  if (e == hipErrorFileNotFound) return fail(m->ctx, MPCX_EIO, "forward: key file read failed");
   HIPC(m->ctx, e, "model_forward");
   m->ctx->counters.bytes += m->impl->counters.bytes;
   m->ctx->counters.rounds += m->impl->counters.rounds;

@@ -74,6 +74,13 @@ struct StreamStats {
   uint64_t bytes_h2d = 0;  // key bytes copied host -> device, both parties
 };
 
+// A stream of key sets in a file: set k of this lane's keys starts at
+// base + k * stride (stride = bytes of a whole batch's set, all lanes).
+struct KeyFile {
+  int fd = -1;
+  uint64_t base = 0, stride = 0, nsets = 0;
+};
+
 class ModelBase {
  public:
   virtual ~ModelBase() = default;
@@ -94,6 +101,12 @@ class ModelBase {
   // unique planes (bytes1 = unique_key_bytes).
   virtual hipError_t attach_host_keys(int B, const void *h_k0, size_t bytes0, const void *h_k1, size_t bytes1,
                                       size_t slot_bytes) = 0;
+  // File-backed keys: each forward reads the next key set (cycling) chunk by
+  // chunk through pinned staging buffers filled by an I/O thread.
+  virtual hipError_t attach_key_files(int B, const KeyFile &f0, const KeyFile &f1, bool packed1,
+                                      size_t slot_bytes) = 0;
+  // Appends the resident key set of one party (party 1: arena or packed unique planes) to fd.
+  virtual hipError_t write_keys(int party, bool packed, int fd) = 0;
   virtual hipError_t set_inputs(int B, const void *x0, const void *x1, const void *a0, const void *a1,
                                 const void *m0, const void *m1, const int64_t *prot) = 0;
   virtual hipError_t forward(int B) = 0;
@@ -134,6 +147,11 @@ class LaneSet {
   hipError_t release_arena();
   hipError_t attach_host_keys(int B, const void *h_k0, size_t bytes0, const void *h_k1, size_t bytes1,
                               size_t slot_bytes);
+  // Key files of whole-batch key sets back to back (party 0: key_bytes(B) per set;
+  // party 1: key_bytes(B) or unique_key_bytes(B, 1) per set).  Returns
+  // hipErrorFileNotFound for files that cannot be opened or do not hold whole sets.
+  hipError_t attach_key_files(int B, const char *path0, const char *path1, size_t slot_bytes);
+  hipError_t write_keys(int party, bool packed, const char *path, bool append);
   hipError_t set_inputs(int B, const void *x0, const void *x1, const void *a0, const void *a1, const void *m0,
                         const void *m1, const int64_t *prot);
   hipError_t forward(int B);
@@ -164,6 +182,8 @@ class LaneSet {
   std::vector<hipEvent_t> done_;
   bool serial_ = false;
   int keyed_B_ = -1;
+  int fd_[2] = {-1, -1};  // attached key files
+  void close_files();
 };
 
 LaneSet *make_lane_set(int bw, int s, const ModelDims &d, const int64_t *W, size_t nW, const Launch &L,

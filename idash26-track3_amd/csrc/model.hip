@@ -6,10 +6,16 @@
 // and the forward checks every gate against it.
 #include <hip/hip_runtime.h>
 
+#include <fcntl.h>
+#include <unistd.h>
+
 #include <algorithm>
 #include <cmath>
+#include <condition_variable>
 #include <cstring>
 #include <memory>
+#include <mutex>
+#include <thread>
 
 #include "model.h"
 
@@ -480,6 +486,8 @@ class Model final : public ModelBase, KeySource {
  public:
   Model(int bw, int s, const ModelDims &d, const Launch &L) : bw_(bw), s_(s), d_(d), L_(L) {}
   ~Model() override {
+    stop_io();
+    if (cs_) (void)hipStreamSynchronize(cs_);
     free_arena();
     free_stream();
     timer.reset();
@@ -789,21 +797,20 @@ class Model final : public ModelBase, KeySource {
     }
     if (cs_) (void)hipStreamDestroy(cs_);
     cs_ = nullptr;
+    for (int p = 0; p < 2; p++)
+      for (int k = 0; k < 2; k++) {
+        if (stg_[p][k]) (void)hipHostFree(stg_[p][k]);
+        stg_[p][k] = nullptr;
+      }
+    files_ = false;
     streaming_ = false;
   }
 
-  hipError_t attach_host_keys(int B, const void *h0, size_t bytes0, const void *h1, size_t bytes1,
-                              size_t slot_bytes) override {
-    const size_t full = key_bytes(B);
-    if (!h0 || !h1 || bytes0 != full || slot_bytes == 0) return hipErrorInvalidValue;
-    bool packed;
-    if (bytes1 == full)
-      packed = false;
-    else if (bytes1 == unique_key_bytes(B, 1))
-      packed = true;
-    else
-      return hipErrorInvalidValue;
+  // plan, chunks, device slots and events of the streamed arena
+  hipError_t setup_stream(int B, bool packed, size_t slot_bytes) {
+    stop_io();
     TRY(hipStreamSynchronize(L_.stream));
+    if (cs_) TRY(hipStreamSynchronize(cs_));
     free_stream();
     free_arena();  // the two slots replace the resident arena
     gates_ = plan(B);
@@ -817,20 +824,138 @@ class Model final : public ModelBase, KeySource {
       chunks_.back().second = ge;
       chunk_of_[i] = int(chunks_.size()) - 1;
     }
-    size_t need = 0;
-    for (auto &c : chunks_) need = std::max(need, c.second - c.first);
+    chunk_max_ = 0;
+    for (auto &c : chunks_) chunk_max_ = std::max(chunk_max_, c.second - c.first);
     for (int k = 0; k < 2; k++) {
-      for (int p = 0; p < 2; p++) TRY(hipMalloc((void **)&slot_[k][p], need));
+      for (int p = 0; p < 2; p++) TRY(hipMalloc((void **)&slot_[k][p], chunk_max_));
       TRY(hipEventCreateWithFlags(&ready_[k], hipEventDisableTiming));
       TRY(hipEventCreateWithFlags(&free_[k], hipEventDisableTiming));
     }
     TRY(hipStreamCreateWithFlags(&cs_, hipStreamNonBlocking));
+    runs1_ = unique_runs(B, packed);
+    return hipSuccess;
+  }
+
+  hipError_t attach_host_keys(int B, const void *h0, size_t bytes0, const void *h1, size_t bytes1,
+                              size_t slot_bytes) override {
+    const size_t full = key_bytes(B);
+    if (!h0 || !h1 || bytes0 != full || slot_bytes == 0) return hipErrorInvalidValue;
+    bool packed;
+    if (bytes1 == full)
+      packed = false;
+    else if (bytes1 == unique_key_bytes(B, 1))
+      packed = true;
+    else
+      return hipErrorInvalidValue;
+    TRY(setup_stream(B, packed, slot_bytes));
     host_[0] = static_cast<const uint8_t *>(h0);
     host_[1] = static_cast<const uint8_t *>(h1);
-    runs1_ = unique_runs(B, packed);
     streaming_ = true;
     keyed_B_ = B;
     return hipSuccess;
+  }
+
+  // ---------------- file-backed keys ----------------
+  // Key sets in two files, read chunk by chunk by an I/O thread into two pinned
+  // staging buffers per party, then copied into the device slots.
+  hipError_t attach_key_files(int B, const KeyFile &f0, const KeyFile &f1, bool packed1,
+                              size_t slot_bytes) override {
+    if (f0.fd < 0 || f1.fd < 0 || f0.nsets == 0 || slot_bytes == 0) return hipErrorInvalidValue;
+    TRY(setup_stream(B, packed1, slot_bytes));
+    for (int p = 0; p < 2; p++)
+      for (int k = 0; k < 2; k++) TRY(hipHostMalloc((void **)&stg_[p][k], chunk_max_, hipHostMallocDefault));
+    kf_[0] = f0;
+    kf_[1] = f1;
+    set_ = 0;
+    files_ = true;
+    streaming_ = true;
+    keyed_B_ = B;
+    return hipSuccess;
+  }
+
+  static bool pread_all(int fd, uint8_t *dst, size_t n, uint64_t off) {
+    while (n > 0) {
+      const ssize_t r = ::pread(fd, dst, n, off_t(off));
+      if (r <= 0) return false;
+      dst += r;
+      n -= size_t(r);
+      off += uint64_t(r);
+    }
+    return true;
+  }
+
+  // I/O thread of one forward over key set `set`: chunk k goes to staging k % 2
+  // once the copies of chunk k - 2 out of that buffer have completed.
+  void io_loop(uint64_t set) {
+    for (int k = 0; k < int(chunks_.size()); k++) {
+      const int sl = k & 1;
+      {
+        std::unique_lock<std::mutex> lk(mu_);
+        cv_.wait(lk, [&] { return abort_ || issued_ >= k - 2; });
+        if (abort_) return;
+      }
+      // the last copies out of this buffer (this forward's chunk k - 2, or the
+      // previous forward's) were recorded before ready_[sl]
+      hipError_t e = hipEventSynchronize(ready_[sl]);
+      const size_t b = chunks_[k].first, en = chunks_[k].second;
+      bool ok = e == hipSuccess &&
+                pread_all(kf_[0].fd, stg_[0][sl], en - b, kf_[0].base + set * kf_[0].stride + b);
+      for (const Run &u : runs1_) {
+        if (!ok) break;
+        if (u.b < b || u.b >= en) continue;
+        ok = pread_all(kf_[1].fd, stg_[1][sl] + (u.b - b), u.e - u.b, kf_[1].base + set * kf_[1].stride + u.src);
+      }
+      {
+        std::lock_guard<std::mutex> lk(mu_);
+        if (!ok) {
+          io_err_ = e != hipSuccess ? e : hipErrorFileNotFound;
+        } else {
+          loaded_ = k;
+        }
+      }
+      cv_.notify_all();
+      if (!ok) return;
+    }
+  }
+
+  void stop_io() {
+    if (!io_.joinable()) return;
+    {
+      std::lock_guard<std::mutex> lk(mu_);
+      abort_ = true;
+    }
+    cv_.notify_all();
+    io_.join();
+  }
+
+  // Appends this lane's key set (party 0's arena; party 1's arena or packed
+  // unique planes) to fd through a pinned bounce buffer.
+  hipError_t write_keys(int party, bool packed, int fd) override {
+    if (!arena_[party] || keyed_B_ < 1) return hipErrorInvalidValue;
+    TRY(hipStreamSynchronize(L_.stream));
+    std::vector<Run> runs;
+    if (party == 1 && packed)
+      runs = unique_runs(keyed_B_, true);
+    else
+      runs.push_back(Run{0, key_bytes(keyed_B_), 0});
+    constexpr size_t kBounce = size_t(64) << 20;
+    uint8_t *h = nullptr;
+    TRY(hipHostMalloc((void **)&h, kBounce, hipHostMallocDefault));
+    hipError_t err = hipSuccess;
+    for (const Run &u : runs) {
+      for (size_t o = u.b; o < u.e && err == hipSuccess; o += kBounce) {
+        const size_t n = std::min(kBounce, u.e - o);
+        err = hipMemcpy(h, arena_[party] + o, n, hipMemcpyDeviceToHost);
+        for (size_t w = 0; err == hipSuccess && w < n;) {
+          const ssize_t r = ::write(fd, h + w, n - w);
+          if (r <= 0) err = hipErrorFileNotFound;
+          else w += size_t(r);
+        }
+      }
+      if (err != hipSuccess) break;
+    }
+    (void)hipHostFree(h);
+    return err;
   }
 
   // copy chunk k into slot k % 2 once the slot's previous chunk has been consumed;
@@ -838,15 +963,29 @@ class Model final : public ModelBase, KeySource {
   hipError_t issue_copy(int k) {
     const int sl = k & 1;
     const size_t b = chunks_[k].first, e = chunks_[k].second;
+    if (files_) {  // wait for the I/O thread to stage chunk k
+      std::unique_lock<std::mutex> lk(mu_);
+      cv_.wait(lk, [&] { return loaded_ >= k || io_err_ != hipSuccess; });
+      if (io_err_ != hipSuccess) return io_err_;
+    }
+    const uint8_t *src0 = files_ ? stg_[0][sl] : host_[0] + b;
     TRY(hipStreamWaitEvent(cs_, free_[sl], 0));
-    TRY(hipMemcpyAsync(slot_[sl][0], host_[0] + b, e - b, hipMemcpyHostToDevice, cs_));
+    TRY(hipMemcpyAsync(slot_[sl][0], src0, e - b, hipMemcpyHostToDevice, cs_));
     stream_stats.bytes_h2d += e - b;
     for (const Run &u : runs1_) {
       if (u.b < b || u.b >= e) continue;
-      TRY(hipMemcpyAsync(slot_[sl][1] + (u.b - b), host_[1] + u.src, u.e - u.b, hipMemcpyHostToDevice, cs_));
+      const uint8_t *src1 = files_ ? stg_[1][sl] + (u.b - b) : host_[1] + u.src;
+      TRY(hipMemcpyAsync(slot_[sl][1] + (u.b - b), src1, u.e - u.b, hipMemcpyHostToDevice, cs_));
       stream_stats.bytes_h2d += u.e - u.b;
     }
     TRY(hipEventRecord(ready_[sl], cs_));
+    if (files_) {
+      {
+        std::lock_guard<std::mutex> lk(mu_);
+        issued_ = k;
+      }
+      cv_.notify_all();
+    }
     return hipSuccess;
   }
 
@@ -903,6 +1042,24 @@ class Model final : public ModelBase, KeySource {
 
   // ---------------- online ----------------
   hipError_t forward(int B) override {
+    if (!files_) return forward_body(B);
+    if (keyed_B_ != B || input_B_ != B) return hipErrorInvalidValue;
+    {
+      std::lock_guard<std::mutex> lk(mu_);
+      loaded_ = -1;
+      issued_ = -1;
+      abort_ = false;
+      io_err_ = hipSuccess;
+    }
+    const uint64_t set = set_;
+    io_ = std::thread([this, set] { io_loop(set); });
+    const hipError_t e = forward_body(B);
+    stop_io();
+    if (e == hipSuccess) set_ = (set_ + 1) % kf_[0].nsets;
+    return e;
+  }
+
+  hipError_t forward_body(int B) {
     if (keyed_B_ != B || input_B_ != B) return hipErrorInvalidValue;
     TRY(ensure_work(B));
     const int N = d_.n_nodes, bw = bw_;
@@ -1016,6 +1173,18 @@ class Model final : public ModelBase, KeySource {
   int cur_chunk_ = -1;
   bool streaming_ = false;
   const uint8_t *host_[2] = {nullptr, nullptr};
+  size_t chunk_max_ = 0;
+  // file-backed keys: files, pinned staging buffers [party][k % 2], I/O thread
+  bool files_ = false;
+  KeyFile kf_[2];
+  uint8_t *stg_[2][2] = {{nullptr, nullptr}, {nullptr, nullptr}};
+  uint64_t set_ = 0;
+  std::thread io_;
+  std::mutex mu_;
+  std::condition_variable cv_;
+  int loaded_ = -1, issued_ = -1;
+  bool abort_ = false;
+  hipError_t io_err_ = hipSuccess;
   std::vector<Run> runs1_;
   uint8_t *slot_[2][2] = {{nullptr, nullptr}, {nullptr, nullptr}};
   hipEvent_t ready_[2] = {nullptr, nullptr}, free_[2] = {nullptr, nullptr};
@@ -1070,6 +1239,7 @@ LaneSet::~LaneSet() {
     if (i > 0 && st_[i]) (void)hipStreamSynchronize(st_[i]);
     delete lane_[i];
   }
+  close_files();
   for (size_t i = 1; i < st_.size(); i++)
     if (st_[i]) (void)hipStreamDestroy(st_[i]);
   for (auto e : done_)
@@ -1087,6 +1257,7 @@ hipError_t LaneSet::set_lanes(int n, std::string *e) {
     delete lane_[i];
   }
   lane_.clear();
+  close_files();
   for (size_t i = 1; i < st_.size(); i++) (void)hipStreamDestroy(st_[i]);
   st_.clear();
   for (auto ev : done_) (void)hipEventDestroy(ev);
@@ -1207,6 +1378,67 @@ hipError_t LaneSet::attach_host_keys(int B, const void *h0, size_t bytes0, const
   }));
   keyed_B_ = B;
   return hipSuccess;
+}
+
+void LaneSet::close_files() {
+  for (int p = 0; p < 2; p++) {
+    if (fd_[p] >= 0) ::close(fd_[p]);
+    fd_[p] = -1;
+  }
+}
+
+hipError_t LaneSet::attach_key_files(int B, const char *path0, const char *path1, size_t slot_bytes) {
+  const size_t set0 = key_bytes(B), full1 = set0, packed1 = unique_key_bytes(B, 1);
+  if (!path0 || !path1 || set0 == 0 || slot_bytes == 0) return hipErrorInvalidValue;
+  int fd[2] = {::open(path0, O_RDONLY), ::open(path1, O_RDONLY)};
+  auto fail = [&](hipError_t e) {
+    for (int p = 0; p < 2; p++)
+      if (fd[p] >= 0) ::close(fd[p]);
+    return e;
+  };
+  if (fd[0] < 0 || fd[1] < 0) return fail(hipErrorFileNotFound);
+  const off_t size0 = ::lseek(fd[0], 0, SEEK_END), size1 = ::lseek(fd[1], 0, SEEK_END);
+  if (size0 <= 0 || size_t(size0) % set0 != 0) return fail(hipErrorFileNotFound);
+  const uint64_t nsets = uint64_t(size0) / set0;
+  bool packed;
+  if (uint64_t(size1) == nsets * full1)
+    packed = false;
+  else if (uint64_t(size1) == nsets * packed1)
+    packed = true;
+  else
+    return fail(hipErrorFileNotFound);
+  const uint64_t stride1 = packed ? packed1 : full1;
+  keyed_B_ = -1;
+  uint64_t o0 = 0, o1 = 0;
+  hipError_t e = each(B, [&](int i, int Bi, int) {
+    KeyFile f0, f1;
+    f0.fd = fd[0];
+    f0.base = o0;
+    f0.stride = set0;
+    f0.nsets = nsets;
+    f1.fd = fd[1];
+    f1.base = o1;
+    f1.stride = stride1;
+    f1.nsets = nsets;
+    o0 += lane_[i]->key_bytes(Bi);
+    o1 += packed ? lane_[i]->unique_key_bytes(Bi, 1) : lane_[i]->key_bytes(Bi);
+    return lane_[i]->attach_key_files(Bi, f0, f1, packed, slot_bytes);
+  });
+  if (e != hipSuccess) return fail(e);
+  close_files();  // the lanes no longer read earlier files
+  fd_[0] = fd[0];
+  fd_[1] = fd[1];
+  keyed_B_ = B;
+  return hipSuccess;
+}
+
+hipError_t LaneSet::write_keys(int party, bool packed, const char *path, bool append) {
+  if (!path || keyed_B_ < 1 || (packed && party != 1)) return hipErrorInvalidValue;
+  const int fd = ::open(path, O_WRONLY | O_CREAT | (append ? O_APPEND : O_TRUNC), 0644);
+  if (fd < 0) return hipErrorFileNotFound;
+  hipError_t e = each(keyed_B_, [&](int i, int, int) { return lane_[i]->write_keys(party, packed, fd); });
+  if (::close(fd) != 0 && e == hipSuccess) e = hipErrorFileNotFound;
+  return e;
 }
 
 hipError_t LaneSet::set_inputs(int B, const void *x0, const void *x1, const void *a0, const void *a1,

@@ -74,6 +74,8 @@ _SIGS = {
     "mpcx_model_create": (C.c_int, [C.c_void_p, C.c_void_p, C.c_void_p, C.c_size_t, C.c_void_p]),
     "mpcx_model_destroy": (None, [C.c_void_p]),
     "mpcx_model_set_lanes": (C.c_int, [C.c_void_p, C.c_int]),
+    "mpcx_model_write_keys": (C.c_int, [C.c_void_p, C.c_int, C.c_int, C.c_char_p, C.c_int]),
+    "mpcx_model_attach_key_files": (C.c_int, [C.c_void_p, C.c_int, C.c_char_p, C.c_char_p, C.c_size_t]),
     "mpcx_model_lanes": (C.c_int, [C.c_void_p]),
     "mpcx_model_key_bytes": (C.c_size_t, [C.c_void_p, C.c_int]),
     "mpcx_model_keygen": (C.c_int, [C.c_void_p, C.c_int, C.c_uint64]),
@@ -514,6 +516,18 @@ class Model:
         n1 = k1.nbytes
         self.ctx.check(self.lib.mpcx_model_attach_host_keys(self.h, B, p0, n0, p1, n1, int(slot_bytes)),
                        "attach_host_keys")
+
+    def write_keys(self, party, path, packed=False, append=False):
+        """Append (or write) the key set of the last keygen for one party to a
+        file: party 0's arena, party 1's arena or packed unique planes."""
+        self.ctx.check(self.lib.mpcx_model_write_keys(self.h, party, 1 if packed else 0, os.fsencode(path),
+                                                      1 if append else 0), "write_keys")
+
+    def attach_key_files(self, B, path0, path1, slot_bytes):
+        """Stream key sets from files (one set per forward, cycling) through pinned
+        staging buffers filled by an I/O thread and two device slots."""
+        self.ctx.check(self.lib.mpcx_model_attach_key_files(self.h, B, os.fsencode(path0), os.fsencode(path1),
+                                                            int(slot_bytes)), "attach_key_files")
 
     def stream_stats(self):
         ch, by = C.c_int(), C.c_uint64()

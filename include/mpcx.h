@@ -29,6 +29,7 @@ typedef int mpcx_status;
 #define MPCX_EHIP 2    /* a HIP call failed; see mpcx_last_error            */
 #define MPCX_ENOMEM 3  /* device allocation failed                          */
 #define MPCX_ESTATE 4  /* call out of order (e.g. forward before keygen)    */
+#define MPCX_EIO 5     /* a key file could not be opened, read or written  */
 
 typedef struct mpcx_ctx mpcx_ctx;
 typedef struct mpcx_model mpcx_model;
@@ -262,6 +263,25 @@ mpcx_status mpcx_model_export_unique_keys(mpcx_model *m, int party, void *h_dst,
  * if a single gate's key exceeds slot_bytes. */
 mpcx_status mpcx_model_attach_host_keys(mpcx_model *m, int B, const void *h_key0, size_t bytes0,
                                         const void *h_key1, size_t bytes1, size_t slot_bytes);
+/* Key files.  mpcx_model_write_keys appends the key set of the batch keyed
+ * last (mpcx_model_keygen / import) for one party to a file: party 0's arena,
+ * or party 1's arena (packed = 0) or packed unique planes (packed = 1); append
+ * = 0 truncates the file first.  Sets of successive keygens (fresh seeds)
+ * appended in order form a key file of whole-batch key sets.
+ * mpcx_model_attach_key_files streams such files: each forward reads the next
+ * key set (cycling), chunk by chunk: an I/O thread preads chunk k into one of
+ * two pinned staging buffers per party (chunk k - 2's copies out of it done),
+ * the copy stream moves it into a device slot of at most slot_bytes per party
+ * and lane, and the gates of the chunk wait for that copy.  Replaces the
+ * SSD -> pinned -> VRAM pipeline of gpu_mpc/deepdtagen_inference.cu:608-859
+ * (I/O thread, pread into pinned slots, evH2D / evFree handshake); the
+ * reference's chunks are whole micro-batch key sets, these are gate-aligned
+ * pieces of one, so a key set need not fit in memory twice.  Party 1's file
+ * holds arenas or packed unique planes, told apart by its size.  MPCX_EIO if a
+ * file is missing, does not hold whole key sets, or a read fails. */
+mpcx_status mpcx_model_write_keys(mpcx_model *m, int party, int packed, const char *path, int append);
+mpcx_status mpcx_model_attach_key_files(mpcx_model *m, int B, const char *path0, const char *path1,
+                                        size_t slot_bytes);
 /* Chunks and host-to-device key bytes (both parties) of the last forward. */
 mpcx_status mpcx_model_stream_stats(const mpcx_model *m, int *chunks, uint64_t *bytes_h2d);
 /* Both parties' input shares (host, ring elements): x (B,N,feat), adjacency

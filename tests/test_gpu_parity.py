@@ -572,6 +572,46 @@ def test_model_streamed_keys_match_resident(mp, orc, synth, bw):
         h.free()
 
 
+@pytest.mark.parametrize("bw,lanes,packed", [(64, 1, True), (32, 2, False)])
+def test_model_key_files(mp, orc, synth, tmp_path, bw, lanes, packed):
+    """File-backed keys: three key sets (fresh dealer seeds) appended to two
+    files, streamed chunk by chunk through the I/O thread's pinned staging
+    buffers; four forwards use sets 0, 1, 2, 0, each on its own inputs, and
+    give the plaintext outputs.  Files that do not hold whole key sets are
+    refused."""
+    B = 3
+    c = mp.Ctx(bw=bw)
+    wls = [synth.workload(B, synth.Dims(bw=bw), seed=40 + k) for k in range(4)]
+    W = wls[0].W
+    d = _od(orc, wls[0].dims)
+    m = mp.Model(c, wls[0].dims, W, lanes=lanes)
+    p0, p1 = tmp_path / "keys0.bin", tmp_path / "keys1.bin"
+    for k in range(3):
+        m.keygen(B, 1000 + k)
+        m.write_keys(0, p0, append=k > 0)
+        m.write_keys(1, p1, packed=packed, append=k > 0)
+    nbytes = m.key_bytes(B)
+    assert p0.stat().st_size == 3 * nbytes
+    assert p1.stat().st_size == 3 * (m.unique_key_bytes(B, 1) if packed else nbytes)
+    m.release_arena()
+    bad = tmp_path / "short.bin"
+    bad.write_bytes(p0.read_bytes()[: nbytes // 2])
+    with pytest.raises(mp.MpcxError):
+        m.attach_key_files(B, bad, p1, slot_bytes=nbytes // 4)
+    with pytest.raises(mp.MpcxError):
+        m.attach_key_files(B, tmp_path / "missing.bin", p1, slot_bytes=nbytes // 4)
+    m.attach_key_files(B, p0, p1, slot_bytes=nbytes // 4)
+    for wl in wls:
+        want, code = orc.plain_forward(d, wl.X, wl.A, wl.mask, wl.prot, W)
+        assert code == 0
+        m.set_inputs(B, *wl.shares["x"], *wl.shares["a"], *wl.shares["m"], wl.prot)
+        m.forward(B)
+        assert np.array_equal(m.output(B), want)
+        assert m.stream_stats()["chunks"] >= 4
+    m.close()
+    c.close()
+
+
 def test_relu_config1_full_size(mp):
     """Config 1: 2^24 ReLUs over Z_2^32 of uniform fixed-point values in
     [-8, 8), one 31-bit DCF key per element, against max(x, 0)."""
