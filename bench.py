@@ -65,6 +65,10 @@ def main():
     ap.add_argument("--total", type=int, default=8192, help="samples of the streamed workload")
     ap.add_argument("--slot-gb", type=float, default=16.0, help="device slot size per party (streamed workload)")
     ap.add_argument("--distinct", type=int, default=4, help="distinct input micro-batches cycled (streamed workload)")
+    ap.add_argument("--key-files", default=None,
+                    help="streamed workload from key files in this directory: --sets distinct dealer key sets are "
+                         "appended to two files and every micro-batch reads the next set (cycling)")
+    ap.add_argument("--sets", type=int, default=4, help="key sets in the key files")
     args = ap.parse_args()
 
     if args.gpus != 1:
@@ -266,20 +270,38 @@ def run_stream(args):
     ctx = mpcx.Ctx(bw=bw, scale=dims.s)
     model = mpcx.Model(ctx, dims, W)
     kb = model.key_bytes(B)
-    t0 = time.time()
-    model.keygen(B, 0xBEEF + args.seed)
-    log(f"[stream] dealer: {2 * kb / 1e9:.1f} GB of keys for B={B} in {time.time() - t0:.1f}s")
-    # party 0's whole arena and party 1's unique planes (the correction words
-    # both parties hold are stored once): what fits the host's pinned memory
-    t0 = time.time()
-    h0, h1 = mpcx.PinnedBuffer(kb), mpcx.PinnedBuffer(model.unique_key_bytes(B, 1))
-    log(f"[stream] pinned host buffers ({(h0.nbytes + h1.nbytes) / 1e9:.1f} GB) in {time.time() - t0:.1f}s")
-    t0 = time.time()
-    model.export_keys(0, B, into=h0)
-    model.export_unique_keys(1, B, into=h1)
-    model.release_arena()
-    log(f"[stream] keys exported to host in {time.time() - t0:.1f}s")
-    model.attach_host_keys(B, h0, h1, int(args.slot_gb * 2 ** 30))
+    ku = model.unique_key_bytes(B, 1)
+    h0 = h1 = None
+    if args.key_files:
+        # distinct dealer key sets in two files (party 0's arenas, party 1's
+        # packed unique planes); each micro-batch reads the next set from disk
+        os.makedirs(args.key_files, exist_ok=True)
+        f0, f1 = os.path.join(args.key_files, "keys_p0.bin"), os.path.join(args.key_files, "keys_p1.bin")
+        t0 = time.time()
+        for k in range(args.sets):
+            model.keygen(B, 0xBEEF + args.seed + k)
+            model.write_keys(0, f0, append=k > 0)
+            model.write_keys(1, f1, packed=True, append=k > 0)
+            log(f"[stream] key set {k + 1}/{args.sets} written ({(kb + ku) / 1e9:.1f} GB), {time.time() - t0:.1f}s")
+        model.release_arena()
+        model.attach_key_files(B, f0, f1, int(args.slot_gb * 2 ** 30))
+        host_key_bytes = kb + ku
+    else:
+        t0 = time.time()
+        model.keygen(B, 0xBEEF + args.seed)
+        log(f"[stream] dealer: {2 * kb / 1e9:.1f} GB of keys for B={B} in {time.time() - t0:.1f}s")
+        # party 0's whole arena and party 1's unique planes (the correction words
+        # both parties hold are stored once): what fits the host's pinned memory
+        t0 = time.time()
+        h0, h1 = mpcx.PinnedBuffer(kb), mpcx.PinnedBuffer(ku)
+        log(f"[stream] pinned host buffers ({(h0.nbytes + h1.nbytes) / 1e9:.1f} GB) in {time.time() - t0:.1f}s")
+        t0 = time.time()
+        model.export_keys(0, B, into=h0)
+        model.export_unique_keys(1, B, into=h1)
+        model.release_arena()
+        log(f"[stream] keys exported to host in {time.time() - t0:.1f}s")
+        model.attach_host_keys(B, h0, h1, int(args.slot_gb * 2 ** 30))
+        host_key_bytes = h0.nbytes + h1.nbytes
 
     want = []
     try:
@@ -317,7 +339,8 @@ def run_stream(args):
         exact = exact and (w is not None and bool(np.array_equal(out, w)))
     value = nmb * B / elapsed
     result = {
-        "metric": f"online secure samples/s (bw={bw}, B={B} micro-batches, keys streamed from pinned host memory, 1 GPU)",
+        "metric": f"online secure samples/s (bw={bw}, B={B} micro-batches, keys streamed from "
+                  + ("key files" if args.key_files else "pinned host memory") + ", 1 GPU)",
         "value": round(value, 2),
         "unit": "samples/s",
         "n_gpus": 1,
@@ -328,13 +351,17 @@ def run_stream(args):
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "u64" if bw == 64 else "u32",
-        "data": "synthetic molecules; one dealer key set (pinned host memory) re-streamed for every micro-batch with fresh inputs",
+        "data": ("synthetic molecules; " + (f"{args.sets} dealer key sets in key files read in turn by the micro-batches"
+                                            if args.key_files else
+                                            "one dealer key set (pinned host memory) re-streamed for every micro-batch")
+                 + ", fresh inputs per micro-batch"),
         "config": {"workload": f"two-party secure affinity forward, bw={bw} s=12, {nmb} micro-batches of B={B} "
-                               f"molecules x {dims.n_nodes} atoms, keys streamed through two {args.slot_gb:g} GiB "
-                               "device slots per party",
-                   "B": B, "total": nmb * B, "bw": bw},
+                               f"molecules x {dims.n_nodes} atoms, keys streamed "
+                               + ("from key files through pinned staging buffers and " if args.key_files else "")
+                               + f"through two {args.slot_gb:g} GiB device slots per party",
+                   "B": B, "total": nmb * B, "bw": bw, "key_source": "files" if args.key_files else "pinned"},
         "key_bytes_per_sample_per_party": round(kb / B, 1),
-        "host_key_bytes_per_step": h0.nbytes + h1.nbytes,
+        "host_key_bytes_per_step": host_key_bytes,
         "key_h2d_bytes_per_step": h2d // nmb,
         "key_h2d_GBps": round(h2d / elapsed / 1e9, 2),
         "bytes_exchanged_per_sample": round(ctx.bytes_exchanged / (nmb * B), 1),
@@ -343,8 +370,9 @@ def run_stream(args):
     print(json.dumps(result), flush=True)
     model.close()
     ctx.close()
-    h0.free()
-    h1.free()
+    for h in (h0, h1):
+        if h is not None:
+            h.free()
 
 
 def _oracle():

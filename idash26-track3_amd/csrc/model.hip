@@ -898,12 +898,35 @@ class Model final : public ModelBase, KeySource {
       // previous forward's) were recorded before ready_[sl]
       hipError_t e = hipEventSynchronize(ready_[sl]);
       const size_t b = chunks_[k].first, en = chunks_[k].second;
-      bool ok = e == hipSuccess &&
-                pread_all(kf_[0].fd, stg_[0][sl], en - b, kf_[0].base + set * kf_[0].stride + b);
-      for (const Run &u : runs1_) {
-        if (!ok) break;
-        if (u.b < b || u.b >= en) continue;
-        ok = pread_all(kf_[1].fd, stg_[1][sl] + (u.b - b), u.e - u.b, kf_[1].base + set * kf_[1].stride + u.src);
+      // the chunk's file ranges, cut into pieces of at most kPiece bytes and
+      // read by up to 16 threads (one page-cache reader moves ~19 GB/s, 16 ~41)
+      struct Piece {
+        int fd;
+        uint8_t *dst;
+        size_t n;
+        uint64_t off;
+      };
+      constexpr size_t kPiece = size_t(64) << 20;
+      const int kReaders = int(std::max(1u, std::min(16u, std::thread::hardware_concurrency())));
+      std::vector<Piece> pieces;
+      auto add = [&](int fd, uint8_t *dst, size_t n, uint64_t off) {
+        for (size_t o = 0; o < n; o += kPiece) pieces.push_back(Piece{fd, dst + o, std::min(kPiece, n - o), off + o});
+      };
+      add(kf_[0].fd, stg_[0][sl], en - b, kf_[0].base + set * kf_[0].stride + b);
+      for (const Run &u : runs1_)
+        if (u.b >= b && u.b < en)
+          add(kf_[1].fd, stg_[1][sl] + (u.b - b), u.e - u.b, kf_[1].base + set * kf_[1].stride + u.src);
+      bool ok = e == hipSuccess;
+      if (ok) {
+        std::vector<char> good(kReaders, 1);
+        std::vector<std::thread> rd;
+        for (int t = 0; t < kReaders; t++)
+          rd.emplace_back([&, t] {
+            for (size_t i = size_t(t); i < pieces.size(); i += kReaders)
+              if (!pread_all(pieces[i].fd, pieces[i].dst, pieces[i].n, pieces[i].off)) good[t] = 0;
+          });
+        for (auto &th : rd) th.join();
+        for (char g : good) ok = ok && g;
       }
       {
         std::lock_guard<std::mutex> lk(mu_);
