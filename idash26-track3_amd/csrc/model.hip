@@ -1241,6 +1241,14 @@ ModelBase *make_model(int bw, int s, const ModelDims &d, const int64_t *W, size_
     *err = "n_nodes must be in [1, 255] (8-bit degree LUT domain)";
     return nullptr;
   }
+  bool widths_ok = d.feat >= 1 && d.prot >= 0 && d.lut_nmax >= 0 && d.lut_nmax <= 255;
+  for (int i = 0; i < 3; i++) widths_ok = widths_ok && d.gcn[i] >= 1;
+  for (int i = 0; i < 2; i++) widths_ok = widths_ok && d.dfc[i] >= 1;
+  for (int i = 0; i < d.nfus; i++) widths_ok = widths_ok && d.fus[i] >= 1;
+  if (!widths_ok) {
+    *err = "layer widths must be >= 1 (protein width >= 0, lut_nmax in [0, 255])";
+    return nullptr;
+  }
   if (d.mask_scale < 0 || d.mask_scale > bw - 2 - 1) {
     *err = "mask_scale must be in [0, bw - 3]";
     return nullptr;
@@ -1489,7 +1497,8 @@ hipError_t LaneSet::forward(int B) {
     if (i > 0 && serial_) TRY(hipStreamWaitEvent(st_[i], done_[i - 1], 0));
     lane_[i]->counters = Counters();
     hipError_t r = lane_[i]->forward(lane_B(B, i));
-    if (r != hipSuccess) {
+    if (r != hipSuccess) {  // the caller's stream still waits for the lanes already enqueued
+      for (int j = 1; j < i; j++) (void)hipStreamWaitEvent(st_[0], done_[j], 0);
       err = lane_[i]->err;
       return r;
     }

@@ -50,7 +50,9 @@ const char *mpcx_last_error(const mpcx_ctx *ctx);
 /* Ring width and fixed-point scale of the context. */
 int mpcx_bw(const mpcx_ctx *ctx);
 int mpcx_scale(const mpcx_ctx *ctx);
-/* hipStream_t; NULL = the context's own stream */
+/* hipStream_t for the standalone gate calls; NULL = the context's own stream.
+ * A model keeps the stream (and AES variant and GEMM path) the context had at
+ * mpcx_model_create; mpcx_synchronize waits for the context's current stream. */
 mpcx_status mpcx_set_stream(mpcx_ctx *ctx, void *hip_stream);
 mpcx_status mpcx_synchronize(mpcx_ctx *ctx);
 /* AES T-table LDS layout used by the DCF kernels (0 = default).  Returns the

@@ -393,6 +393,28 @@ def test_model_lanes_streamed_keys(mp, orc, synth):
     hp.free()
 
 
+def test_model_create_rejects_bad_dims(mp, synth):
+    """Model creation checks its dimensions and the weight blob length, and
+    the forward refuses to run before keys and inputs are set."""
+    import dataclasses
+    c = mp.Ctx(bw=32)
+    good = synth.Dims(bw=32, n_nodes=8)
+    W = np.zeros(sum(i * o + o for i, o in good.layers()), np.int64)
+    m = mp.Model(c, good, W)
+    with pytest.raises(mp.MpcxError):
+        m.forward(2)
+    m.close()
+    for bad in (dict(n_nodes=256), dict(feat=0), dict(gcn=(8, 0, 8)), dict(fus=(16, 4)),
+                dict(mask_scale=30), dict(lut_nmax=300)):
+        d = dataclasses.replace(good, **bad)
+        Wd = np.zeros(sum(i * o + o for i, o in d.layers()), np.int64)
+        with pytest.raises(mp.MpcxError):
+            mp.Model(c, d, Wd)
+    with pytest.raises(mp.MpcxError):
+        mp.Model(c, good, W[:-1])
+    c.close()
+
+
 def test_model_forward_on_oracle_keys_config0(mp, orc, synth):
     """Config 0 shape (B=16, N=140, bw=32): keys from the oracle's dealer,
     online phase on the GPU, outputs equal to the plaintext forward."""
