@@ -641,6 +641,7 @@ mpcx_status mpcx_model_create(mpcx_ctx *c, const mpcx_model_dims *dims, const in
   for (int i = 0; i < 4; i++) d.fus[i] = dims->fus[i];
   d.lut_nmax = dims->lut_nmax;
   d.mask_scale = dims->mask_scale;
+  d.xw_slack = dims->xw_slack;
   std::string err;
   LaneSet *impl = make_lane_set(c->bw, c->s, d, W, nW, c->L, &err);
   if (!impl) return fail(c, MPCX_EINVAL, "model_create: " + err);

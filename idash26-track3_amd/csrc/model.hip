@@ -493,6 +493,9 @@ class Model final : public ModelBase, KeySource {
     timer.reset();
   }
 
+  // gate of the GCN products H.W^T: exact TR, or TRSLACK (exact for |x| < 2^(bw-2))
+  int xw_kind() const { return d_.xw_slack ? G_TRSLACK : G_TR; }
+
   // ---------------- weights ----------------
   int nlayers() const { return 5 + d_.nfus; }
   void layer_io(int l, int *in, int *out) const {
@@ -575,7 +578,7 @@ class Model final : public ModelBase, KeySource {
     }
     for (int l = 0; l < 3; l++) {
       size_t E = BN * d_.gcn[l];
-      tr(G_TR, E);
+      tr(xw_kind(), E);
       push(sxs_layout(bw_, B, N, N, d_.gcn[l], o).end);
       tr(G_TRRELU, E);
     }
@@ -687,7 +690,7 @@ class Model final : public ModelBase, KeySource {
       const int fo = d_.gcn[l];
       const size_t En = BN * fo;
       TRY(pub_gemm(rX.p, l, BN, t1.p));
-      TRY(d.tr(G_TR, En, t1.p, t2.p));
+      TRY(d.tr(xw_kind(), En, t1.p, t2.p));
       TRY(d.sxs(B, N, N, fo, rN.p, t2.p, t1.p, gt.p));
       TRY(d.tr(G_TRRELU, En, t1.p, rX.p));
     }
@@ -1123,7 +1126,7 @@ class Model final : public ModelBase, KeySource {
       const int fo = d_.gcn[l];
       const size_t En = BN * fo;
       TRY(pub_gemm(H, l, BN, Z));
-      TRY(r.tr(G_TR, En, Z, nullptr, 1, XW));
+      TRY(r.tr(xw_kind(), En, Z, nullptr, 1, XW));
       TRY(r.sxs(B, N, N, fo, An_.p, XW, Z));
       TRY(r.tr(G_TRRELU, En, Z, bias_[l].p, fo, H));
     }
@@ -1247,6 +1250,10 @@ ModelBase *make_model(int bw, int s, const ModelDims &d, const int64_t *W, size_
   for (int i = 0; i < d.nfus; i++) widths_ok = widths_ok && d.fus[i] >= 1;
   if (!widths_ok) {
     *err = "layer widths must be >= 1 (protein width >= 0, lut_nmax in [0, 255])";
+    return nullptr;
+  }
+  if (d.xw_slack != 0 && d.xw_slack != 1) {
+    *err = "xw_slack must be 0 or 1";
     return nullptr;
   }
   if (d.mask_scale < 0 || d.mask_scale > bw - 2 - 1) {

@@ -212,6 +212,12 @@ typedef struct {
   int lut_nmax; /* largest degree with a D^-1/2 table entry */
   int mask_scale; /* atom mask values are 0 or 2^mask_scale: 0, or s for the reference's
                      mask files (reference/share_data.py:135-159 shares the mask at scale s) */
+  int xw_slack;   /* 0: the GCN products H.W^T are truncated exactly over the signed ring
+                     (DDGOrca::truncateForward TrFloor, gpu_mpc/ddg_orca.h:112-123: two DCFs,
+                     31 AES per element and party at bw=32); 1: with the top-two-bit slack
+                     truncation (the reference's TrWithSlack, ddg_orca.h:50, 60), exact for
+                     |H.W^T| < 2^(bw-2), one 12-bit DCF (6 AES).  Outputs are bit-exact with
+                     the fixed-point forward while every H.W^T lies in that half ring. */
 } mpcx_model_dims;
 
 mpcx_status mpcx_model_create(mpcx_ctx *ctx, const mpcx_model_dims *dims, const int64_t *h_weights,

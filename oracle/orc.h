@@ -193,6 +193,8 @@ typedef struct {
   int fus[4];     /* fusion widths */
   int lut_nmax;   /* largest degree with a table entry (mpc_config.py NMAX) */
   int mask_scale; /* the atom mask is 0 or 2^mask_scale (0; s for the reference's files) */
+  int xw_slack;   /* 1: the GCN products H.W^T are truncated with TRSLACK, exact for
+                     |H.W^T| < 2^(bw-2) (half the signed ring); 0: exact TR over the ring */
 } orc_dims;
 
 /* Weights: for each linear layer in order gcn0..2, dfc0..1, fus0..nfus-1:

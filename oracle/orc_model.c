@@ -35,6 +35,8 @@ static void trace(uint32_t g, size_t n, const uint64_t *v) {
 
 /* ---------------- dims / weights ---------------- */
 static int nlayers(const orc_dims *d) { return 5 + d->nfus; }
+/* gate of the GCN products H.W^T: exact TR, or TRSLACK when d->xw_slack */
+static int xw_kind(const orc_dims *d) { return d->xw_slack ? ORC_G_TRSLACK : ORC_G_TR; }
 static void layer_io(const orc_dims *d, int l, int *in, int *out) {
   if (l < 3) {
     *in = l == 0 ? d->feat : d->gcn[l - 1];
@@ -74,9 +76,10 @@ static const char *DOMAIN_MSG[] = {
     "sample without a real atom",
     "node degree outside the 8-bit LUT domain",
     "adjacency or mask entry not 0/1",
+    "GCN product H.W^T outside the slack truncation's domain (|x| < 2^(bw-2))",
 };
 const char *orc_domain_msg(int code) {
-  if (code < 0 || code > 6) return "unknown";
+  if (code < 0 || code > 7) return "unknown";
   return DOMAIN_MSG[code];
 }
 
@@ -104,13 +107,15 @@ static i128 dot(const int64_t *a, size_t as, const int64_t *b, size_t bs, size_t
   for (size_t k = 0; k < K; k++) acc += (u128)((i128)a[k * as] * (i128)b[k * bs]);
   return (i128)acc;
 }
-/* y(MxN) = wrap(tr(X(MxK) . B(KxN))); optional bias check for the fused gate */
+/* y(MxN) = wrap(tr(X(MxK) . B(KxN))); optional bias check for the fused gate;
+ * slack: the product must also lie in [-2^(bw-2), 2^(bw-2)) (TRSLACK) */
 static void fixed_mm(fx *f, const int64_t *X, const int64_t *Bm, size_t M, size_t K, size_t N,
-                     const int64_t *bias_check, int64_t *Y) {
+                     const int64_t *bias_check, int slack, int64_t *Y) {
   for (size_t i = 0; i < M; i++)
     for (size_t j = 0; j < N; j++) {
       i128 P = dot(X + i * K, 1, Bm + j, N, K);
       if (!fits(f, P)) seterr(f, 1);
+      if (slack && !(P >= -((i128)1 << (f->bw - 2)) && P < ((i128)1 << (f->bw - 2)))) seterr(f, 7);
       if (bias_check && !fits(f, P + ((i128)bias_check[j] << f->s))) seterr(f, 2);
       Y[i * N + j] = wrapv(f, P >> f->s);
     }
@@ -182,8 +187,8 @@ int orc_plain_forward(const orc_dims *d, int B, const int64_t *X, const int64_t 
       int fo = d->gcn[l];
       const int64_t *Wt = W + layer_off(d, l);
       const int64_t *bias = Wt + (size_t)fin * fo;
-      fixed_mm(&f, H, Wt, (size_t)N, (size_t)fin, (size_t)fo, NULL, XW); /* XW */
-      fixed_mm(&f, Af, XW, (size_t)N, (size_t)N, (size_t)fo, bias, Hn);  /* A . XW */
+      fixed_mm(&f, H, Wt, (size_t)N, (size_t)fin, (size_t)fo, NULL, d->xw_slack, XW); /* XW */
+      fixed_mm(&f, Af, XW, (size_t)N, (size_t)N, (size_t)fo, bias, 0, Hn);  /* A . XW */
       for (int i = 0; i < N; i++)
         for (int j = 0; j < fo; j++) {
           int64_t v = wrapv(&f, (i128)Hn[(size_t)i * fo + j] + bias[j]);
@@ -218,14 +223,14 @@ int orc_plain_forward(const orc_dims *d, int B, const int64_t *X, const int64_t 
     {
       const int64_t *Wt = W + layer_off(d, 3);
       const int64_t *bias = Wt + (size_t)C * d->dfc[0];
-      fixed_mm(&f, pooled, Wt, 1, (size_t)C, (size_t)d->dfc[0], bias, h1);
+      fixed_mm(&f, pooled, Wt, 1, (size_t)C, (size_t)d->dfc[0], bias, 0, h1);
       for (int j = 0; j < d->dfc[0]; j++) {
         int64_t v = wrapv(&f, (i128)h1[j] + bias[j]);
         h1[j] = v > 0 ? v : 0;
       }
       Wt = W + layer_off(d, 4);
       bias = Wt + (size_t)d->dfc[0] * d->dfc[1];
-      fixed_mm(&f, h1, Wt, 1, (size_t)d->dfc[0], (size_t)d->dfc[1], bias, h2);
+      fixed_mm(&f, h1, Wt, 1, (size_t)d->dfc[0], (size_t)d->dfc[1], bias, 0, h2);
       for (int j = 0; j < d->dfc[1]; j++) h2[j] = wrapv(&f, (i128)h2[j] + bias[j]);
     }
     /* fusion: concat [drug, protein] (fixed_forward.py:89) */
@@ -235,7 +240,7 @@ int orc_plain_forward(const orc_dims *d, int B, const int64_t *X, const int64_t 
       const int64_t *Wt = W + layer_off(d, 5 + k);
       int fo = d->fus[k];
       const int64_t *bias = Wt + (size_t)width * fo;
-      fixed_mm(&f, h2, Wt, 1, (size_t)width, (size_t)fo, bias, h1);
+      fixed_mm(&f, h2, Wt, 1, (size_t)width, (size_t)fo, bias, 0, h1);
       for (int j = 0; j < fo; j++) {
         int64_t v = wrapv(&f, (i128)h1[j] + bias[j]);
         h2[j] = (k < d->nfus - 1 && v < 0) ? 0 : v;
@@ -437,7 +442,7 @@ size_t orc_model_key_bytes(const orc_dims *d, int B) {
   o = adjnorm_layout(bw, s, B, N, o);
   for (int l = 0; l < 3; l++) {
     size_t E = (size_t)B * N * d->gcn[l];
-    o = orc_tr_layout_make(ORC_G_TR, bw, s, E, o).end;
+    o = orc_tr_layout_make(xw_kind(d), bw, s, E, o).end;
     o = orc_sxs_layout(bw, (size_t)B, (size_t)N, (size_t)N, (size_t)d->gcn[l], o, &r1, &r2, &r3);
     o = orc_tr_layout_make(ORC_G_TRRELU, bw, s, E, o).end;
   }
@@ -490,8 +495,8 @@ int orc_model_keygen(const orc_dims *d, int B, uint64_t seed, const int64_t *W, 
     int fo = d->gcn[l];
     size_t E = BN * fo;
     pub_gemm(bw, BN, fin, fo, rX, W + layer_off(d, l), t1); /* mask of H.Wt */
-    orc_tr_keygen(seed, g++, ORC_G_TR, bw, s, E, t1, t2, k0, k1, o);
-    o = orc_tr_layout_make(ORC_G_TR, bw, s, E, o).end;
+    orc_tr_keygen(seed, g++, xw_kind(d), bw, s, E, t1, t2, k0, k1, o);
+    o = orc_tr_layout_make(xw_kind(d), bw, s, E, o).end;
     orc_sxs_keygen(seed, g++, bw, (size_t)B, (size_t)N, (size_t)N, (size_t)fo, rN, t2, t1, k0, k1, o);
     o = orc_sxs_layout(bw, (size_t)B, (size_t)N, (size_t)N, (size_t)fo, o, &r1, &r2, &r3);
     orc_tr_keygen(seed, g++, ORC_G_TRRELU, bw, s, E, t1, rX, k0, k1, o);
@@ -615,9 +620,9 @@ int orc_model_eval(const orc_dims *d, int B, const int64_t *W, const uint8_t *k0
     const int64_t *Wt = W + layer_off(d, l);
     const int64_t *bias = Wt + (size_t)fin * fo;
     pub_gemm(bw, BN, fin, fo, H, Wt, t1);
-    orc_tr_eval(ORC_G_TR, bw, s, E, k0, k1, o, t1, NULL, t2, &by);
+    orc_tr_eval(xw_kind(d), bw, s, E, k0, k1, o, t1, NULL, t2, &by);
     trace(g++, E, t2);
-    o = orc_tr_layout_make(ORC_G_TR, bw, s, E, o).end;
+    o = orc_tr_layout_make(xw_kind(d), bw, s, E, o).end;
     orc_sxs_eval(bw, (size_t)B, (size_t)N, (size_t)N, (size_t)fo, k0, k1, o, An, t2, t1, &by);
     trace(g++, E, t1);
     o = orc_sxs_layout(bw, (size_t)B, (size_t)N, (size_t)N, (size_t)fo, o, &r1, &r2, &r3);

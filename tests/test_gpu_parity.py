@@ -249,13 +249,16 @@ def test_reveal_keys_and_eval(ctx, orc):
 # ---------------------------------------------------------------------------
 def _od(orc, dims):
     return orc.make_dims(bw=dims.bw, s=dims.s, n_nodes=dims.n_nodes, feat=dims.feat, gcn=dims.gcn, dfc=dims.dfc,
-                         prot=dims.prot, fus=dims.fus, lut_nmax=dims.lut_nmax, mask_scale=dims.mask_scale)
+                         prot=dims.prot, fus=dims.fus, lut_nmax=dims.lut_nmax, mask_scale=dims.mask_scale,
+                         xw_slack=dims.xw_slack)
 
 
-@pytest.mark.parametrize("bw", [32, 64])
-def test_model_keys_and_forward(mp, orc, synth, bw):
+@pytest.mark.parametrize("bw,xw_slack", [(32, 0), (64, 0), (32, 1), (64, 1)])
+def test_model_keys_and_forward(mp, orc, synth, bw, xw_slack):
+    """GPU dealer keys byte-identical to the oracle's, forward bit-exact, same
+    exchange bytes; with exact and with slack truncation of the GCN products."""
     B = 2
-    wl = synth.workload(B, synth.Dims(bw=bw), seed=21)
+    wl = synth.workload(B, synth.Dims(bw=bw, xw_slack=xw_slack), seed=21)
     d = _od(orc, wl.dims)
     want, code = orc.plain_forward(d, wl.X, wl.A, wl.mask, wl.prot, wl.W)
     assert code == 0

@@ -85,15 +85,34 @@ def test_domain_violation_is_reported(orc):
     assert "pre-truncation" in orc.domain_msg(code)
 
 
-def _wl(synth, B, bw=32, seed=0, n_nodes=140):
-    dims = synth.Dims(bw=bw, n_nodes=n_nodes)
+def test_slack_domain_violation_is_reported(orc):
+    """With slack truncation of the GCN products the bit-exact domain of H.W^T
+    is |x| < 2^(bw-2): a product of 2^30 is outside it (code 7) but inside the
+    exact truncation's (the first violation, if any, comes later)."""
+    d, W, X, A, mask, prot = _tiny(orc)
+    W = W.copy()
+    W[0] = 1 << 18  # XW product 4096 * 2^18 = 2^30
+    d.xw_slack = 1
+    _, code = orc.plain_forward(d, X, A, mask, prot, W)
+    assert code == 7 and "slack" in orc.domain_msg(code)
+    d.xw_slack = 0
+    _, code = orc.plain_forward(d, X, A, mask, prot, W)
+    assert code != 7
+    W[0] = (1 << 18) - 1  # just inside the half ring
+    d.xw_slack = 1
+    _, code = orc.plain_forward(d, X, A, mask, prot, W)
+    assert code != 7
+
+
+def _wl(synth, B, bw=32, seed=0, n_nodes=140, xw_slack=0):
+    dims = synth.Dims(bw=bw, n_nodes=n_nodes, xw_slack=xw_slack)
     return synth.workload(B, dims, seed=seed)
 
 
 def _od(orc, wl):
     d = wl.dims
     return orc.make_dims(bw=d.bw, s=d.s, n_nodes=d.n_nodes, feat=d.feat, gcn=d.gcn, dfc=d.dfc, prot=d.prot,
-                         fus=d.fus, lut_nmax=d.lut_nmax, mask_scale=d.mask_scale)
+                         fus=d.fus, lut_nmax=d.lut_nmax, mask_scale=d.mask_scale, xw_slack=d.xw_slack)
 
 
 def test_permutation_invariance(orc, synth):
@@ -177,9 +196,11 @@ def test_bw32_equals_bw64_in_domain(orc, synth):
     assert c32 == 0 and c64 == 0 and np.array_equal(o32, o64)
 
 
-@pytest.mark.parametrize("bw", [32, 64])
-def test_two_party_matches_plaintext(orc, synth, bw):
-    wl = _wl(synth, 2, bw=bw, seed=10)
+@pytest.mark.parametrize("bw,xw_slack", [(32, 0), (64, 0), (32, 1), (64, 1)])
+def test_two_party_matches_plaintext(orc, synth, bw, xw_slack):
+    """Two-party evaluation reconstructs the plaintext forward, with exact and
+    with slack truncation of the GCN products (in the slack domain)."""
+    wl = _wl(synth, 2, bw=bw, seed=10, xw_slack=xw_slack)
     d = _od(orc, wl)
     out, code = orc.plain_forward(d, wl.X, wl.A, wl.mask, wl.prot, wl.W)
     assert code == 0
