@@ -3,6 +3,7 @@
 
 #include <cstdio>
 #include <cstring>
+#include <new>
 #include <string>
 
 #include "../../include/mpcx.h"
@@ -112,6 +113,27 @@ static mpcx_status hip_status(mpcx_ctx *c, hipError_t e, const char *what) {
     hipError_t e_ = (x);                                   \
     if (e_ != hipSuccess) return hip_status(c, e_, what);  \
   } while (0)
+
+// C++ exceptions (allocation failures of host-side plans and threads) must not
+// cross the C ABI: model calls run through these guards.
+template <class F>
+static hipError_t guard(F &&f) noexcept {
+  try {
+    return f();
+  } catch (const std::bad_alloc &) {
+    return hipErrorOutOfMemory;
+  } catch (...) {
+    return hipErrorUnknown;
+  }
+}
+template <class F>
+static size_t guard_size(F &&f) noexcept {
+  try {
+    return f();
+  } catch (...) {
+    return 0;
+  }
+}
 
 // All entry points below were declared extern "C" in mpcx.h and keep C linkage.
 
@@ -643,9 +665,18 @@ mpcx_status mpcx_model_create(mpcx_ctx *c, const mpcx_model_dims *dims, const in
   d.mask_scale = dims->mask_scale;
   d.xw_slack = dims->xw_slack;
   std::string err;
-  LaneSet *impl = make_lane_set(c->bw, c->s, d, W, nW, c->L, &err);
+  LaneSet *impl = nullptr;
+  try {
+    impl = make_lane_set(c->bw, c->s, d, W, nW, c->L, &err);
+  } catch (const std::bad_alloc &) {
+    return fail(c, MPCX_ENOMEM, "model_create: host allocation failed");
+  }
   if (!impl) return fail(c, MPCX_EINVAL, "model_create: " + err);
-  auto *m = new mpcx_model();
+  auto *m = new (std::nothrow) mpcx_model();
+  if (!m) {
+    delete impl;
+    return fail(c, MPCX_ENOMEM, "model_create: host allocation failed");
+  }
   m->ctx = c;
   m->impl = impl;
   *out = m;
@@ -662,7 +693,7 @@ mpcx_status mpcx_model_set_lanes(mpcx_model *m, int lanes) {
   if (!m) return MPCX_EINVAL;
   if (lanes < 1 || lanes > 16) return fail(m->ctx, MPCX_EINVAL, "model_set_lanes: lanes must be in [1, 16]");
   std::string err;
-  hipError_t e = m->impl->set_lanes(lanes, &err);
+  hipError_t e = guard([&] { return m->impl->set_lanes(lanes, &err); });
   if (e == hipErrorInvalidValue) return fail(m->ctx, MPCX_EINVAL, "model_set_lanes: " + err);
   HIPC(m->ctx, e, "model_set_lanes");
   return MPCX_OK;
@@ -670,41 +701,43 @@ mpcx_status mpcx_model_set_lanes(mpcx_model *m, int lanes) {
 
 int mpcx_model_lanes(const mpcx_model *m) { return m ? m->impl->lanes() : 0; }
 
-size_t mpcx_model_key_bytes(const mpcx_model *m, int B) { return (m && B > 0) ? m->impl->key_bytes(B) : 0; }
+size_t mpcx_model_key_bytes(const mpcx_model *m, int B) {
+  return (m && B > 0) ? guard_size([&] { return m->impl->key_bytes(B); }) : 0;
+}
 
 mpcx_status mpcx_model_keygen(mpcx_model *m, int B, uint64_t seed) {
   if (!m) return MPCX_EINVAL;
   if (B < 1) return fail(m->ctx, MPCX_EINVAL, "B must be >= 1");
-  HIPC(m->ctx, m->impl->keygen(B, seed), "model_keygen");
+  HIPC(m->ctx, guard([&] { return m->impl->keygen(B, seed); }), "model_keygen");
   return MPCX_OK;
 }
 
 mpcx_status mpcx_model_import_keys(mpcx_model *m, int B, const void *k0, const void *k1, size_t bytes) {
   if (!m || !k0 || !k1) return MPCX_EINVAL;
-  if (bytes != m->impl->key_bytes(B)) return fail(m->ctx, MPCX_EINVAL, "key size mismatch");
-  HIPC(m->ctx, m->impl->import_keys(B, k0, k1, bytes), "model_import_keys");
+  if (bytes != mpcx_model_key_bytes(m, B)) return fail(m->ctx, MPCX_EINVAL, "key size mismatch");
+  HIPC(m->ctx, guard([&] { return m->impl->import_keys(B, k0, k1, bytes); }), "model_import_keys");
   return MPCX_OK;
 }
 
 mpcx_status mpcx_model_export_keys(mpcx_model *m, int party, void *dst, size_t bytes) {
   if (!m || !dst || (party != 0 && party != 1)) return MPCX_EINVAL;
-  HIPC(m->ctx, m->impl->export_keys(party, dst, bytes), "model_export_keys");
+  HIPC(m->ctx, guard([&] { return m->impl->export_keys(party, dst, bytes); }), "model_export_keys");
   return MPCX_OK;
 }
 
 mpcx_status mpcx_model_release_arena(mpcx_model *m) {
   if (!m) return MPCX_EINVAL;
-  HIPC(m->ctx, m->impl->release_arena(), "model_release_arena");
+  HIPC(m->ctx, guard([&] { return m->impl->release_arena(); }), "model_release_arena");
   return MPCX_OK;
 }
 
 mpcx_status mpcx_model_attach_host_keys(mpcx_model *m, int B, const void *k0, size_t bytes0, const void *k1,
                                         size_t bytes1, size_t slot_bytes) {
   if (!m || !k0 || !k1) return MPCX_EINVAL;
-  if (B < 1 || bytes0 != m->impl->key_bytes(B) ||
-      (bytes1 != m->impl->key_bytes(B) && bytes1 != m->impl->unique_key_bytes(B, 1)))
+  if (B < 1 || bytes0 != mpcx_model_key_bytes(m, B) ||
+      (bytes1 != mpcx_model_key_bytes(m, B) && bytes1 != mpcx_model_unique_key_bytes(m, B, 1)))
     return fail(m->ctx, MPCX_EINVAL, "attach_host_keys: key size mismatch");
-  hipError_t e = m->impl->attach_host_keys(B, k0, bytes0, k1, bytes1, slot_bytes);
+  hipError_t e = guard([&] { return m->impl->attach_host_keys(B, k0, bytes0, k1, bytes1, slot_bytes); });
   if (e == hipErrorInvalidValue)
     return fail(m->ctx, MPCX_EINVAL, "attach_host_keys: slot_bytes smaller than the largest gate key");
   HIPC(m->ctx, e, "model_attach_host_keys");
@@ -713,7 +746,7 @@ mpcx_status mpcx_model_attach_host_keys(mpcx_model *m, int B, const void *k0, si
 
 mpcx_status mpcx_model_write_keys(mpcx_model *m, int party, int packed, const char *path, int append) {
   if (!m || !path || (party != 0 && party != 1) || (packed && party != 1)) return MPCX_EINVAL;
-  hipError_t e = m->impl->write_keys(party, packed != 0, path, append != 0);
+  hipError_t e = guard([&] { return m->impl->write_keys(party, packed != 0, path, append != 0); });
   if (e == hipErrorInvalidValue) return fail(m->ctx, MPCX_ESTATE, "write_keys: no resident keys");
   if (e == hipErrorFileNotFound) return fail(m->ctx, MPCX_EIO, std::string("write_keys: cannot write ") + path);
   HIPC(m->ctx, e, "model_write_keys");
@@ -724,7 +757,7 @@ mpcx_status mpcx_model_attach_key_files(mpcx_model *m, int B, const char *path0,
                                         size_t slot_bytes) {
   if (!m || !path0 || !path1) return MPCX_EINVAL;
   if (B < 1 || slot_bytes == 0) return fail(m->ctx, MPCX_EINVAL, "attach_key_files: bad argument");
-  hipError_t e = m->impl->attach_key_files(B, path0, path1, slot_bytes);
+  hipError_t e = guard([&] { return m->impl->attach_key_files(B, path0, path1, slot_bytes); });
   if (e == hipErrorFileNotFound)
     return fail(m->ctx, MPCX_EIO, "attach_key_files: key files missing or not whole key sets of this batch");
   if (e == hipErrorInvalidValue)
@@ -734,12 +767,13 @@ mpcx_status mpcx_model_attach_key_files(mpcx_model *m, int B, const char *path0,
 }
 
 size_t mpcx_model_unique_key_bytes(const mpcx_model *m, int B, int party) {
-  return (m && B > 0 && (party == 0 || party == 1)) ? m->impl->unique_key_bytes(B, party) : 0;
+  return (m && B > 0 && (party == 0 || party == 1)) ? guard_size([&] { return m->impl->unique_key_bytes(B, party); })
+                                                   : 0;
 }
 
 mpcx_status mpcx_model_export_unique_keys(mpcx_model *m, int party, void *dst, size_t bytes) {
   if (!m || !dst || (party != 0 && party != 1)) return MPCX_EINVAL;
-  HIPC(m->ctx, m->impl->export_unique_keys(party, dst, bytes), "model_export_unique_keys");
+  HIPC(m->ctx, guard([&] { return m->impl->export_unique_keys(party, dst, bytes); }), "model_export_unique_keys");
   return MPCX_OK;
 }
 
@@ -754,13 +788,13 @@ mpcx_status mpcx_model_set_inputs(mpcx_model *m, int B, const void *x0, const vo
                                   const void *m0, const void *m1, const int64_t *prot) {
   if (!m || !x0 || !x1 || !a0 || !a1 || !m0 || !m1 || !prot) return MPCX_EINVAL;
   if (B < 1) return fail(m->ctx, MPCX_EINVAL, "B must be >= 1");
-  HIPC(m->ctx, m->impl->set_inputs(B, x0, x1, a0, a1, m0, m1, prot), "model_set_inputs");
+  HIPC(m->ctx, guard([&] { return m->impl->set_inputs(B, x0, x1, a0, a1, m0, m1, prot); }), "model_set_inputs");
   return MPCX_OK;
 }
 
 mpcx_status mpcx_model_forward(mpcx_model *m, int B) {
   if (!m) return MPCX_EINVAL;
-  hipError_t e = m->impl->forward(B);
+  hipError_t e = guard([&] { return m->impl->forward(B); });
   if (e == hipErrorInvalidValue) return fail(m->ctx, MPCX_ESTATE, "forward: keys or inputs not set for this B");
   if (e == hipErrorFileNotFound) return fail(m->ctx, MPCX_EIO, "forward: key file read failed");
   HIPC(m->ctx, e, "model_forward");
@@ -771,7 +805,7 @@ mpcx_status mpcx_model_forward(mpcx_model *m, int B) {
 
 mpcx_status mpcx_model_output(mpcx_model *m, int B, int64_t *out) {
   if (!m || !out) return MPCX_EINVAL;
-  HIPC(m->ctx, m->impl->output(out, B), "model_output");
+  HIPC(m->ctx, guard([&] { return m->impl->output(out, B); }), "model_output");
   return MPCX_OK;
 }
 
@@ -784,12 +818,12 @@ mpcx_status mpcx_model_profile(mpcx_model *m, int enable) {
 mpcx_status mpcx_model_profile_read(mpcx_model *m, int *launches, double *ms, double *elements, double *aes,
                                     double *hbm_bytes) {
   if (!m) return MPCX_EINVAL;
-  HIPC(m->ctx, m->impl->profile_read(launches, ms, elements, aes, hbm_bytes), "model_profile_read");
+  HIPC(m->ctx, guard([&] { return m->impl->profile_read(launches, ms, elements, aes, hbm_bytes); }), "model_profile_read");
   return MPCX_OK;
 }
 
 mpcx_status mpcx_model_profile_gemm(mpcx_model *m, int *sections, double *ms, double *ring_macs) {
   if (!m) return MPCX_EINVAL;
-  HIPC(m->ctx, m->impl->profile_gemm(sections, ms, ring_macs), "model_profile_gemm");
+  HIPC(m->ctx, guard([&] { return m->impl->profile_gemm(sections, ms, ring_macs); }), "model_profile_gemm");
   return MPCX_OK;
 }

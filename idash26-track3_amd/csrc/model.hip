@@ -890,6 +890,17 @@ class Model final : public ModelBase, KeySource {
   // I/O thread of one forward over key set `set`: chunk k goes to staging k % 2
   // once the copies of chunk k - 2 out of that buffer have completed.
   void io_loop(uint64_t set) {
+    try {
+      io_chunks(set);
+    } catch (...) {  // allocation failure: report it to the waiting host thread
+      {
+        std::lock_guard<std::mutex> lk(mu_);
+        io_err_ = hipErrorOutOfMemory;
+      }
+      cv_.notify_all();
+    }
+  }
+  void io_chunks(uint64_t set) {
     for (int k = 0; k < int(chunks_.size()); k++) {
       const int sl = k & 1;
       {
@@ -923,11 +934,16 @@ class Model final : public ModelBase, KeySource {
       if (ok) {
         std::vector<char> good(kReaders, 1);
         std::vector<std::thread> rd;
-        for (int t = 0; t < kReaders; t++)
-          rd.emplace_back([&, t] {
-            for (size_t i = size_t(t); i < pieces.size(); i += kReaders)
-              if (!pread_all(pieces[i].fd, pieces[i].dst, pieces[i].n, pieces[i].off)) good[t] = 0;
-          });
+        try {
+          for (int t = 0; t < kReaders; t++)
+            rd.emplace_back([&, t] {
+              for (size_t i = size_t(t); i < pieces.size(); i += kReaders)
+                if (!pread_all(pieces[i].fd, pieces[i].dst, pieces[i].n, pieces[i].off)) good[t] = 0;
+            });
+        } catch (...) {  // joinable threads must not be destroyed
+          for (auto &th : rd) th.join();
+          throw;
+        }
         for (auto &th : rd) th.join();
         for (char g : good) ok = ok && g;
       }
@@ -1078,7 +1094,11 @@ class Model final : public ModelBase, KeySource {
       io_err_ = hipSuccess;
     }
     const uint64_t set = set_;
-    io_ = std::thread([this, set] { io_loop(set); });
+    try {
+      io_ = std::thread([this, set] { io_loop(set); });
+    } catch (...) {
+      return hipErrorOutOfMemory;
+    }
     const hipError_t e = forward_body(B);
     stop_io();
     if (e == hipSuccess) set_ = (set_ + 1) % kf_[0].nsets;
