@@ -272,7 +272,7 @@ def run_stream(args):
 
     B = args.batch if args.batch != 64 else 256
     bw = 64 if args.bw == 32 else args.bw
-    dims = synth.Dims(bw=bw)
+    dims = synth.Dims(bw=bw, xw_slack=int(args.xw_slack))
     nmb = max(1, args.total // B)
     wls = [synth.workload(B, dims, seed=args.seed + 100 * k) for k in range(args.distinct)]
     W = wls[0].W
@@ -369,7 +369,8 @@ def run_stream(args):
                                f"molecules x {dims.n_nodes} atoms, keys streamed "
                                + ("from key files through pinned staging buffers and " if args.key_files else "")
                                + f"through two {args.slot_gb:g} GiB device slots per party",
-                   "B": B, "total": nmb * B, "bw": bw, "key_source": "files" if args.key_files else "pinned"},
+                   "B": B, "total": nmb * B, "bw": bw, "key_source": "files" if args.key_files else "pinned",
+                   "xw_truncation": "slack" if args.xw_slack else "exact"},
         "key_bytes_per_sample_per_party": round(kb / B, 1),
         "host_key_bytes_per_step": host_key_bytes,
         "key_h2d_bytes_per_step": h2d // nmb,
