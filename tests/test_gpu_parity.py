@@ -522,6 +522,41 @@ def test_adjnorm_keys_and_eval(mp, orc, synth, bw):
     c.close()
 
 
+@pytest.mark.parametrize("bw", [32, 64])
+def test_adjnorm_max_nodes_and_degrees(mp, orc, bw):
+    """N = 255 (the 8-bit degree domain's limit): a star whose centre has degree
+    255 (past the table's 138 entries, so T = 0), an isolated atom (self loop
+    only, degree 1), a path, random edges, and padding; keys byte-identical,
+    every unmasked entry equal to the closed form."""
+    B, N = 2, 255
+    rng = np.random.default_rng(255)
+    A = np.zeros((B, N, N), np.int64)
+    A[0, 0, :] = 1
+    A[0, :, 0] = 1
+    np.fill_diagonal(A[0], 1)  # star: centre degree 255, leaves degree 2
+    n1 = 200
+    idx = np.arange(n1)
+    A[1, idx, idx] = 1
+    A[1, idx[1:100], idx[:99]] = 1  # a path over atoms 0..99
+    A[1, idx[:99], idx[1:100]] = 1
+    for _ in range(300):  # random extra edges among atoms 100..198 (atom 199 stays isolated)
+        i, j = rng.integers(100, n1 - 1, size=2)
+        A[1, i, j] = A[1, j, i] = 1
+    M = (1 << bw) - 1
+    a0 = rng.integers(0, 1 << 63, size=A.size, dtype=np.uint64) & np.uint64(M)
+    a1 = (A.reshape(-1).astype(np.uint64) - a0) & np.uint64(M)
+    c = mp.Ctx(bw=bw)
+    g0, g1, gmask = c.adjnorm_keygen(B, N, seed=31)
+    o0, o1, omask = orc.adjnorm_keygen(bw, S, B, N, 31)
+    assert np.array_equal(host(g0)[:o0.size], o0) and np.array_equal(host(g1)[:o1.size], o1)
+    out = c.adjnorm_eval(B, N, 138, g0, g1, a0, a1)
+    got = signed(out.astype(np.uint64) - omask, bw)
+    want = orc.adj_norm_plain(A).reshape(-1)
+    assert np.array_equal(got, want)
+    assert want.reshape(B, N, N)[0, 0].sum() == 0  # the degree-255 centre has T = 0
+    c.close()
+
+
 def test_adjnorm_config2_full_size(mp, orc, synth):
     """Config 2: B=1024 graphs of the config-0 distribution, N=140, Z_2^32.
     Every unmasked entry equals A[i,j] * floor(T[d_i] T[d_j] / 2^12)."""
