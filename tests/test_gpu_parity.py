@@ -418,6 +418,31 @@ def test_model_create_rejects_bad_dims(mp, synth):
     c.close()
 
 
+@pytest.mark.parametrize("bw,lanes", [(32, 1), (64, 2)])
+def test_model_extreme_molecule_sizes(mp, orc, synth, bw, lanes):
+    """A molecule of one atom (a single real row in the pool tree, all others
+    sentinels) next to one that fills all 140 rows (no padding)."""
+    dims = synth.Dims(bw=bw)
+    X1, A1, m1 = synth.molecules(1, dims, seed=3, min_atoms=1, max_atoms=1)
+    X2, A2, m2 = synth.molecules(1, dims, seed=4, min_atoms=140, max_atoms=140)
+    X, A, mask = np.concatenate([X1, X2]), np.concatenate([A1, A2]), np.concatenate([m1, m2])
+    assert mask[0].sum() == 1 and mask[1].sum() == 140
+    W = synth.weights(dims, seed=5)
+    prot = synth.protein(2, dims, seed=6)
+    d = _od(orc, dims)
+    want, code = orc.plain_forward(d, X, A, mask, prot, W)
+    assert code == 0
+    c = mp.Ctx(bw=bw)
+    m = mp.Model(c, dims, W, lanes=lanes)
+    m.keygen(2, 77)
+    sh = [synth.share(v, bw, 20 + k) for k, v in enumerate((X, A, mask))]
+    m.set_inputs(2, *sh[0], *sh[1], *sh[2], prot)
+    m.forward(2)
+    assert np.array_equal(m.output(2), want)
+    m.close()
+    c.close()
+
+
 def test_model_forward_on_oracle_keys_config0(mp, orc, synth):
     """Config 0 shape (B=16, N=140, bw=32): keys from the oracle's dealer,
     online phase on the GPU, outputs equal to the plaintext forward."""
