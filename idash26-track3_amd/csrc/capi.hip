@@ -157,6 +157,7 @@ mpcx_status mpcx_create(int bw, int scale, int device, mpcx_ctx **out) {
   if (const char *v = std::getenv("MPCX_AES_VARIANT")) c->L.aes_variant = std::atoi(v);
   if (const char *v = std::getenv("MPCX_AES_BLOCK")) c->L.aes_block = std::atoi(v);
   if (const char *v = std::getenv("MPCX_GEMM")) c->L.gemm = std::strcmp(v, "valu") == 0 ? 1 : 0;
+  if (const char *v = std::getenv("MPCX_GRAPH")) c->L.graph = std::atoi(v) != 0 ? 1 : 0;
   *out = c;
   return MPCX_OK;
 }

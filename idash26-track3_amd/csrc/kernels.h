@@ -26,6 +26,9 @@ struct Launch {
   // ring GEMM path over Z_2^32: 0 = int8 matrix cores (limb products), 1 = VALU
   // (Z_2^64 always uses the VALU path)
   int gemm = 0;
+  // model forwards with resident keys are captured once per batch size into a
+  // HIP graph and replayed (0 = enqueue every kernel each time)
+  int graph = 1;
 };
 
 struct AesVariant {

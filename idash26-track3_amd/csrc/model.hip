@@ -486,6 +486,7 @@ class Model final : public ModelBase, KeySource {
  public:
   Model(int bw, int s, const ModelDims &d, const Launch &L) : bw_(bw), s_(s), d_(d), L_(L) {}
   ~Model() override {
+    drop_graph();
     stop_io();
     if (cs_) (void)hipStreamSynchronize(cs_);
     free_arena();
@@ -600,6 +601,7 @@ class Model final : public ModelBase, KeySource {
   uint8_t *arena(int party) override { return arena_[party]; }
 
   void free_arena() {
+    drop_graph();
     for (int p = 0; p < 2; p++) {
       if (arena_[p]) (void)hipFree(arena_[p]);
       arena_[p] = nullptr;
@@ -636,6 +638,7 @@ class Model final : public ModelBase, KeySource {
   hipError_t ensure_work(int B) {
     if (B == work_B_) return hipSuccess;
     TRY(hipStreamSynchronize(L_.stream));  // buffers may be reallocated under earlier work
+    drop_graph();
     const int N = d_.n_nodes;
     const size_t E = emax(B), BN = size_t(B) * N, BNN = BN * N;
     for (auto *b : {&bA_, &bB_, &bC_}) TRY(b->alloc(E));
@@ -655,6 +658,7 @@ class Model final : public ModelBase, KeySource {
   hipError_t keygen(int B, uint64_t seed) override {
     if (streaming_) return hipErrorInvalidValue;
     TRY(hipStreamSynchronize(L_.stream));  // a running forward may still read the arena
+    drop_graph();
     TRY(ensure_arena(B));
     TRY(ensure_work(B));
     const int N = d_.n_nodes, bw = bw_;
@@ -736,6 +740,7 @@ class Model final : public ModelBase, KeySource {
   hipError_t import_keys(int B, const void *k0, const void *k1, size_t bytes) override {
     if (streaming_ || bytes != key_bytes(B)) return hipErrorInvalidValue;
     TRY(hipStreamSynchronize(L_.stream));  // a running forward may still read the arena
+    drop_graph();
     TRY(ensure_arena(B));
     TRY(hipMemcpy(arena_[0], k0, bytes, hipMemcpyHostToDevice));
     TRY(hipMemcpy(arena_[1], k1, bytes, hipMemcpyHostToDevice));
@@ -1061,6 +1066,8 @@ class Model final : public ModelBase, KeySource {
                         const void *m1, const int64_t *prot) override {
     const int N = d_.n_nodes;
     const size_t BN = size_t(B) * N, nx = BN * d_.feat, na = BN * N;
+    TRY(hipStreamSynchronize(L_.stream));  // earlier forwards read these buffers
+    if (B != input_B_) drop_graph();       // buffers may move
     TRY(x0_.alloc(nx));
     TRY(x1_.alloc(nx));
     TRY(a0_.alloc(na));
@@ -1068,7 +1075,6 @@ class Model final : public ModelBase, KeySource {
     TRY(m0_.alloc(BN));
     TRY(m1_.alloc(BN));
     TRY(prot_.alloc(size_t(B) * d_.prot));
-    TRY(hipStreamSynchronize(L_.stream));
     TRY(hipMemcpy(x0_.p, x0, nx * sizeof(T), hipMemcpyHostToDevice));
     TRY(hipMemcpy(x1_.p, x1, nx * sizeof(T), hipMemcpyHostToDevice));
     TRY(hipMemcpy(a0_.p, a0, na * sizeof(T), hipMemcpyHostToDevice));
@@ -1083,7 +1089,55 @@ class Model final : public ModelBase, KeySource {
   }
 
   // ---------------- online ----------------
+  // ---------------- graph capture ----------------
+  void drop_graph() {
+    if (gexec_) (void)hipGraphExecDestroy(gexec_);
+    if (graph_) (void)hipGraphDestroy(graph_);
+    gexec_ = nullptr;
+    graph_ = nullptr;
+    graph_B_ = -1;
+  }
+
+  // Resident keys: the forward's kernels are captured once per batch size and
+  // the graph is replayed (the buffers it reads are fixed until keys, inputs of
+  // another size or work buffers are reallocated, which drop it).  The host-side
+  // exchange counters of the captured forward are replayed with it.
+  hipError_t forward_graph(int B) {
+    if (keyed_B_ != B || input_B_ != B) return hipErrorInvalidValue;
+    TRY(ensure_work(B));  // may synchronize: outside the capture
+    if (graph_B_ != B) {
+      drop_graph();
+      const Counters before = counters;
+      counters = Counters();
+      TRY(hipStreamBeginCapture(L_.stream, hipStreamCaptureModeThreadLocal));
+      const hipError_t e = forward_body(B);
+      hipGraph_t g = nullptr;
+      const hipError_t e2 = hipStreamEndCapture(L_.stream, &g);
+      if (e != hipSuccess || e2 != hipSuccess) {
+        if (g) (void)hipGraphDestroy(g);
+        counters = before;
+        return e != hipSuccess ? e : e2;
+      }
+      const hipError_t e3 = hipGraphInstantiate(&gexec_, g, nullptr, nullptr, 0);
+      if (e3 != hipSuccess) {
+        (void)hipGraphDestroy(g);
+        gexec_ = nullptr;
+        counters = before;
+        return e3;
+      }
+      graph_ = g;
+      graph_B_ = B;
+      graph_ctr_ = counters;
+      counters = before;
+    }
+    TRY(hipGraphLaunch(gexec_, L_.stream));
+    counters.bytes += graph_ctr_.bytes;
+    counters.rounds += graph_ctr_.rounds;
+    return hipSuccess;
+  }
+
   hipError_t forward(int B) override {
+    if (!files_ && !streaming_ && !timer.on && L_.graph) return forward_graph(B);
     if (!files_) return forward_body(B);
     if (keyed_B_ != B || input_B_ != B) return hipErrorInvalidValue;
     {
@@ -1206,6 +1260,10 @@ class Model final : public ModelBase, KeySource {
   uint8_t *arena_[2] = {nullptr, nullptr};
   size_t arena_bytes_ = 0;
   int keyed_B_ = -1, input_B_ = -1, work_B_ = -1;
+  hipGraph_t graph_ = nullptr;
+  hipGraphExec_t gexec_ = nullptr;
+  int graph_B_ = -1;
+  Counters graph_ctr_;
   DevBuf<T> x0_, x1_, a0_, a1_, m0_, m1_, prot_;
   DevBuf<T> bA_, bB_, bC_, Ah_, An_, mh_, V0_, V1_;
   DevBuf<int64_t> out_;

@@ -443,6 +443,54 @@ def test_model_extreme_molecule_sizes(mp, orc, synth, bw, lanes):
     c.close()
 
 
+@pytest.mark.parametrize("lanes", [1, 2])
+def test_model_graph_replays(mp, orc, synth, monkeypatch, lanes):
+    """Resident-key forwards are captured into a HIP graph once per batch size
+    and replayed: four inputs in turn (with synchronised host work and eager
+    kernels of the same context between replays), a second batch size (fresh
+    keys, a new capture), then the first size again; every replay matches the
+    oracle and the eager path (MPCX_GRAPH=0) on the same keys, exchange bytes
+    included."""
+    dims = synth.Dims(bw=32)
+    W = synth.weights(dims, seed=9)
+    d = _od(orc, dims)
+
+    def batch(B, seed):
+        X, A, mask = synth.molecules(B, dims, seed=seed)
+        prot = synth.protein(B, dims, seed=seed + 1)
+        want, code = orc.plain_forward(d, X, A, mask, prot, W)
+        assert code == 0
+        sh = [synth.share(v, 32, seed + 2 + k) for k, v in enumerate((X, A, mask))]
+        return sh, prot, want
+
+    c = mp.Ctx(bw=32)
+    monkeypatch.setenv("MPCX_GRAPH", "0")
+    ce = mp.Ctx(bw=32)
+    m = mp.Model(c, dims, W, lanes=lanes)
+    me = mp.Model(ce, dims, W, lanes=lanes)
+    for B, seeds in ((3, (50, 60, 70, 80)), (5, (90,)), (3, (100,))):
+        m.keygen(B, 123 + B)
+        me.keygen(B, 123 + B)
+        for sd in seeds:
+            sh, prot, want = batch(B, sd)
+            for mm in (m, me):
+                mm.set_inputs(B, *sh[0], *sh[1], *sh[2], prot)
+            c.reset_counters()
+            ce.reset_counters()
+            m.forward(B)
+            me.forward(B)
+            got = m.output(B)
+            assert np.array_equal(got, want) and np.array_equal(me.output(B), want)
+            assert c.bytes_exchanged == ce.bytes_exchanged > 0
+            # eager work on the same context between replays
+            A = rmask(np.random.default_rng(sd), 64 * 64, 32).reshape(64, 64)
+            assert np.array_equal(c.ring_gemm(A, A).astype(np.uint64), orc.ring_gemm(32, A, A))
+    m.close()
+    me.close()
+    c.close()
+    ce.close()
+
+
 def test_model_forward_on_oracle_keys_config0(mp, orc, synth):
     """Config 0 shape (B=16, N=140, bw=32): keys from the oracle's dealer,
     online phase on the GPU, outputs equal to the plaintext forward."""
