@@ -787,3 +787,49 @@ def test_model_on_reference_files(mp, orc, synth, tmp_path, bw):
     assert np.array_equal(m.output(B), want)
     m.close()
     c.close()
+
+
+# ---------------------------------------------------------------------------
+# command-line driver over the C ABI (the reference's deepdtagen_inference role)
+# ---------------------------------------------------------------------------
+@pytest.mark.parametrize("bw", [32, 64])
+def test_driver_dealer_then_evaluator(mp, orc, synth, tmp_path, bw):
+    """mpcx_infer: the dealer run writes both parties' key files, the evaluator
+    run reads them with the reference-format batch and weights and prints one
+    AFFINITY line per molecule, equal to the fixed-point forward; the combined
+    run (role 2, two lanes) prints the same lines."""
+    import os
+    import re
+    import subprocess
+    import formats
+    exe = os.path.join(os.path.dirname(mp.__file__), "mpcx_infer")
+    assert os.path.exists(exe), "mpcx_infer not built"
+    B = 3
+    wl = synth.workload(B, synth.Dims(bw=bw), seed=14)
+    bdir, kdir = tmp_path / "batch", tmp_path / "keys"
+    kdir.mkdir()
+    formats.write_batch(str(bdir), wl.X, wl.A, wl.mask, wl.prot, bw=bw, scale=12, pool_dim=312, seed=6)
+    wpath = str(tmp_path / "weights.bin")
+    formats.write_weights(wpath, wl.W, wl.dims.layers(), scale=12)
+    want, code = orc.plain_forward(_od(orc, synth.Dims(bw=bw)), wl.X, wl.A, wl.mask, wl.prot, wl.W)
+    assert code == 0
+    lines = [f"AFFINITY[{j}]={v / 4096.0:.6f}" for j, v in enumerate(want)]
+    env = dict(os.environ, MPCX_WEIGHTS_BIN=wpath)
+
+    def run(role, extra_env=None):
+        r = subprocess.run([exe, str(bw), "12", str(role), str(kdir), str(bdir)], env=dict(env, **(extra_env or {})),
+                           capture_output=True, text=True, timeout=120)
+        assert r.returncode == 0, r.stderr
+        return r.stdout
+
+    run(0)
+    assert (kdir / f"DeepDTAGen_{bw}_12_party0").stat().st_size > 0
+    out = run(1)
+    assert re.findall(r"AFFINITY\[\d+\]=\S+", out) == lines
+    assert int(re.search(r"Comm \(B\)=(\d+)", out).group(1)) > 0
+    out2 = run(2, {"MPCX_LANES": "2"})
+    assert re.findall(r"AFFINITY\[\d+\]=\S+", out2) == lines
+    # a batch that does not match the key files is refused
+    bad = subprocess.run([exe, str(bw), "12", "1", str(kdir), str(bdir), "2"], env=env, capture_output=True,
+                         text=True, timeout=120)
+    assert bad.returncode != 0
