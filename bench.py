@@ -32,10 +32,10 @@ GEMM_PEAK_TMACS = {"mfma": 5.0e3 / 2 / 16, "valu": VALU_PEAK_TOPS / 2}
 # HBM bytes per k_tr_phase1 launch measured with rocprofv3 --pmc FETCH_SIZE and
 # WRITE_SIZE on this bench command (mean over the profiled forward's launches,
 # 19 per lane), each scaled by the same counter's reading for a 1 GiB elementwise
-# copy (FETCH_SIZE x 2.0, WRITE_SIZE x 1.0); keyed by (variant, B, bw, lanes, XW truncation).
+# copy (FETCH_SIZE x 2.0, WRITE_SIZE x 1.0); keyed by (variant, B, bw, lanes, slack).
 # The summary is profiles/k_tr_phase1_affinity_bw32_B64.md.
-TRAFFIC_BYTES_PER_LAUNCH = {("perm64_b512", 64, 32, 3, "exact"): 229638822,
-                            ("perm64_b512", 64, 32, 1, "exact"): 689753000}
+TRAFFIC_BYTES_PER_LAUNCH = {("perm64_b512", 64, 32, 3, 0): 229638822,
+                            ("perm64_b512", 64, 32, 1, 0): 689753000}
 VALU_OPS_PER_AES = {"perm64_b512": 402, "perm64_b1024": 402, "t4_rep32_b1024": 462}
 
 
@@ -56,9 +56,11 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--aes-variant", type=int, default=-1)
     ap.add_argument("--lanes", type=int, default=3, help="concurrent sub-batches, each on its own stream")
-    ap.add_argument("--xw-slack", action="store_true",
-                    help="truncate the GCN products H.W^T with the slack gate (exact for |H.W^T| < 2^(bw-2)) "
-                         "instead of the exact truncation over the whole signed ring")
+    ap.add_argument("--slack", type=int, default=0, choices=(0, 1, 2),
+                    help="slack truncations of the GCN (exact while the values lie in half the signed ring): "
+                         "0 none (exact truncation over the whole ring), 1 the products H.W^T, 2 also the "
+                         "aggregation A.XW + bias (then a small-domain ReLU)")
+    ap.add_argument("--xw-slack", action="store_true", help="same as --slack 1")
     ap.add_argument("--workload", choices=("affinity", "relu", "adjnorm"), default="affinity",
                     help="affinity: the secure forward (default); relu: secure ReLU over --n elements (bw=32); "
                          "adjnorm: secure adjacency normalisation of B=1024 graphs (bw=32)")
@@ -74,6 +76,8 @@ def main():
                          "appended to two files and every micro-batch reads the next set (cycling)")
     ap.add_argument("--sets", type=int, default=4, help="key sets in the key files")
     args = ap.parse_args()
+    if args.xw_slack:
+        args.slack = max(args.slack, 1)
 
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (every box here has one GPU); got --gpus {args.gpus}.",
@@ -93,7 +97,7 @@ def main():
     import synth
 
     B = args.batch
-    dims = synth.Dims(bw=args.bw, xw_slack=int(args.xw_slack))
+    dims = synth.Dims(bw=args.bw, slack=args.slack)
     t0 = time.time()
     wl = synth.workload(B, dims, seed=args.seed)
     log(f"[bench] workload B={B} bw={args.bw} generated in {time.time() - t0:.1f}s")
@@ -159,10 +163,11 @@ def main():
         "config": {"workload": f"two-party secure affinity forward, bw={args.bw} s=12, B={B} molecules x "
                                f"{dims.n_nodes} atoms, GCN 78-78-156-312, FC 312-1024-128, fusion 256-1024-512-1, "
                                f"FSS keys resident in HBM, {args.lanes} concurrent sub-batches"
-                               + (", GCN products truncated with the slack gate (|H.W^T| < 2^(bw-2))"
-                                  if args.xw_slack else ""),
+                               + ({1: ", GCN products H.W^T truncated with the slack gate",
+                                   2: ", GCN products and aggregations truncated with the slack gate"}
+                                  .get(args.slack, "")),
                    "B": B, "n_nodes": dims.n_nodes, "bw": args.bw, "scale": dims.s, "lanes": args.lanes,
-                   "xw_truncation": "slack" if args.xw_slack else "exact"},
+                   "slack": args.slack},
         "dcf_evals_per_s": round(dcf_evals_per_s, 1),
         "aes_blocks_per_s": round(aes_per_s, 1),
         "dcf_ms_per_step": round(dcf_ms, 3),
@@ -179,8 +184,7 @@ def main():
             "peak": round(VALU_PEAK_TOPS, 2),
             "unit": "TOP/s",
             "frac": round(achieved_tops / VALU_PEAK_TOPS, 4),
-            "traffic": TRAFFIC_BYTES_PER_LAUNCH.get((variant, B, args.bw, args.lanes,
-                                                     "slack" if args.xw_slack else "exact")),
+            "traffic": TRAFFIC_BYTES_PER_LAUNCH.get((variant, B, args.bw, args.lanes, args.slack)),
             "traffic_unit": "bytes per launch (mean over the forward's launches)",
             "algorithmic_bytes_per_launch": round(prof["hbm_bytes"] / max(prof["launches"], 1)),
         },
@@ -222,7 +226,7 @@ def main():
         d = dims
         od = orc.make_dims(bw=d.bw, s=d.s, n_nodes=d.n_nodes, feat=d.feat, gcn=d.gcn, dfc=d.dfc, prot=d.prot,
                            fus=d.fus, lut_nmax=d.lut_nmax, mask_scale=d.mask_scale,
-                           xw_slack=d.xw_slack)
+                           slack=d.slack)
         want, code = orc.plain_forward(od, wl.X, wl.A, wl.mask, wl.prot, wl.W)
         result["bit_exact"] = bool(code == 0 and np.array_equal(want, out))
         if not args.no_cpu:
@@ -272,7 +276,7 @@ def run_stream(args):
 
     B = args.batch if args.batch != 64 else 256
     bw = 64 if args.bw == 32 else args.bw
-    dims = synth.Dims(bw=bw, xw_slack=int(args.xw_slack))
+    dims = synth.Dims(bw=bw, slack=args.slack)
     nmb = max(1, args.total // B)
     wls = [synth.workload(B, dims, seed=args.seed + 100 * k) for k in range(args.distinct)]
     W = wls[0].W
@@ -319,7 +323,7 @@ def run_stream(args):
         d = dims
         od = orc.make_dims(bw=d.bw, s=d.s, n_nodes=d.n_nodes, feat=d.feat, gcn=d.gcn, dfc=d.dfc, prot=d.prot,
                            fus=d.fus, lut_nmax=d.lut_nmax, mask_scale=d.mask_scale,
-                           xw_slack=d.xw_slack)
+                           slack=d.slack)
         for wl in wls:
             y, code = orc.plain_forward(od, wl.X, wl.A, wl.mask, wl.prot, W)
             want.append(y if code == 0 else None)
@@ -370,7 +374,7 @@ def run_stream(args):
                                + ("from key files through pinned staging buffers and " if args.key_files else "")
                                + f"through two {args.slot_gb:g} GiB device slots per party",
                    "B": B, "total": nmb * B, "bw": bw, "key_source": "files" if args.key_files else "pinned",
-                   "xw_truncation": "slack" if args.xw_slack else "exact"},
+                   "slack": args.slack},
         "key_bytes_per_sample_per_party": round(kb / B, 1),
         "host_key_bytes_per_step": host_key_bytes,
         "key_h2d_bytes_per_step": h2d // nmb,

@@ -272,7 +272,9 @@ hipError_t ctx_scratch(mpcx_ctx *c, size_t bytes, void **p) {
   *p = c->scratch;
   return hipSuccess;
 }
-bool valid_kind(int k) { return k == MPCX_TR || k == MPCX_TRRELU || k == MPCX_RELU || k == MPCX_TRSLACK; }
+bool valid_kind(int k) {
+  return k == MPCX_TR || k == MPCX_TRRELU || k == MPCX_RELU || k == MPCX_TRSLACK || k == MPCX_RELUSLACK;
+}
 }  // namespace
 
 size_t mpcx_tr_key_bytes(mpcx_ctx *c, int kind, size_t n) {
@@ -664,7 +666,7 @@ mpcx_status mpcx_model_create(mpcx_ctx *c, const mpcx_model_dims *dims, const in
   for (int i = 0; i < 4; i++) d.fus[i] = dims->fus[i];
   d.lut_nmax = dims->lut_nmax;
   d.mask_scale = dims->mask_scale;
-  d.xw_slack = dims->xw_slack;
+  d.slack = dims->slack;
   std::string err;
   LaneSet *impl = nullptr;
   try {

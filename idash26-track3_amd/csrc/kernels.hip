@@ -251,6 +251,7 @@ template <typename T>
 struct TrArgs {
   AesRK kd;
   int kind, n, s;
+  int sb;  // sign bit of the shifted input (tr_sign_bit)
   size_t N;
   const uint8_t *k0, *k1;
   uint8_t *w0, *w1;  // writable keys (keygen)
@@ -268,11 +269,13 @@ struct TrArgs {
   uint32_t gate;
 };
 
+__device__ __forceinline__ bool relu_like(int kind) { return kind == G_RELU || kind == G_RELUSLACK; }
+
 template <typename T>
 __device__ __forceinline__ T tr_shifted_input(const TrArgs<T> &a, size_t i) {
   T x = a.xhat[i];
-  if (a.kind != G_RELU && a.bias) x += T(a.bias[uint32_t(i % uint32_t(a.bias_ncol))]) << a.s;
-  return x + (T(1) << (a.n - 1));
+  if (!relu_like(a.kind) && a.bias) x += T(a.bias[uint32_t(i % uint32_t(a.bias_ncol))]) << a.s;
+  return x + (T(1) << a.sb);
 }
 
 // TAG = 1 marks the launches of a profiled forward (identical code, its own
@@ -289,7 +292,7 @@ __global__ void k_tr_phase1(TrArgs<T> a) {
   // serves the two evaluations (and a streamed arena moves it once).
   const uint8_t *KC = a.k0;
   const size_t stride = size_t(gridDim.x) * blockDim.x;
-  const T lowmask = (T(1) << (a.n - 1)) - T(1);
+  const T lowmask = (T(1) << a.sb) - T(1);
   const T smask = (T(1) << a.s) - T(1);
   for (size_t base = size_t(blockIdx.x) * blockDim.x + (threadIdx.x & ~63u); base < a.N; base += stride) {
     const size_t i = base + lane_id();
@@ -326,7 +329,7 @@ __global__ void k_tr_phase2(TrArgs<T> a) {
   const T one0 = p == 0 ? T(1) : T(0);
   for (size_t i = size_t(blockIdx.x) * blockDim.x + threadIdx.x; i < a.N; i += size_t(gridDim.x) * blockDim.x) {
     const T xp = tr_shifted_input(a, i);
-    const uint32_t h = uint32_t(xp >> (a.n - 1)) & 1u;
+    const uint32_t h = uint32_t(xp >> a.sb) & 1u;
     const uint32_t bh = a.use_a ? (get_bit(a.cba[0], i) ^ get_bit(a.cba[1], i)) : 0u;
     const uint32_t dh = a.use_b ? (get_bit(a.cbb[0], i) ^ get_bit(a.cbb[1], i)) : 0u;
     const T A = (xp >> a.s) - (T(1) << (a.n - 1 - a.s));
@@ -340,7 +343,7 @@ __global__ void k_tr_phase2(TrArgs<T> a) {
       const T k = kap[i];
       const T cp = z ? T(one0 - k) : k;
       y = cp * A + G[size_t(c) * a.N + i];
-    } else if (a.kind == G_RELU) {
+    } else if (relu_like(a.kind)) {
       const uint32_t z = h ^ bh;
       const T k = kap[i];
       const T cp = z ? T(one0 - k) : k;
@@ -361,17 +364,17 @@ __global__ void k_tr_keygen(TrArgs<T> a) {
   AesLds<NT, REP> aes(lds);
   const size_t stride = size_t(gridDim.x) * blockDim.x;
   const int n = a.n, s = a.s;
-  const T lowmask = (T(1) << (n - 1)) - T(1);
+  const T lowmask = (T(1) << a.sb) - T(1);
   const T smask = (T(1) << s) - T(1);
   T *G0 = reinterpret_cast<T *>(a.w0 + a.off_g);
   T *G1 = reinterpret_cast<T *>(a.w1 + a.off_g);
-  const int ncase = a.kind == G_RELU ? 2 : 8;
+  const int ncase = relu_like(a.kind) ? 2 : 8;
   for (size_t base = size_t(blockIdx.x) * blockDim.x + (threadIdx.x & ~63u); base < a.N; base += stride) {
     const size_t i = base + lane_id();
     uint32_t za0 = 0, za1 = 0, zb0 = 0, zb1 = 0;
     if (i < a.N) {
       const T r = a.in_mask[i];
-      const uint32_t rho = uint32_t(r >> (n - 1)) & 1u;
+      const uint32_t rho = uint32_t(r >> a.sb) & 1u;
       const T R = r >> s;
       const uint32_t rbi = aes.prf(a.kd, a.gate, F_DCFA + 3, i).x & 1u;
       const uint32_t rdi = aes.prf(a.kd, a.gate, F_DCFB + 3, i).x & 1u;
@@ -390,7 +393,7 @@ __global__ void k_tr_keygen(TrArgs<T> a) {
           } else {
             Gv = rout - R - T(d) + (T(w) << (n - s));
           }
-        } else if (a.kind == G_RELU) {
+        } else if (relu_like(a.kind)) {
           const T cc = T(uint32_t(c) ^ kappa);
           Gv = rout - cc * r;
         } else {
@@ -404,7 +407,7 @@ __global__ void k_tr_keygen(TrArgs<T> a) {
         G0[size_t(c) * a.N + i] = g0;
         G1[size_t(c) * a.N + i] = Gv - g0;
       }
-      if (a.kind == G_TRRELU || a.kind == G_RELU) {
+      if (a.kind == G_TRRELU || relu_like(a.kind)) {
         const T q0 = ring_of<T>(aes.prf(a.kd, a.gate, F_SPLIT + 8, i));
         reinterpret_cast<T *>(a.w0 + a.off_kappa)[i] = q0;
         reinterpret_cast<T *>(a.w1 + a.off_kappa)[i] = T(kappa) - q0;
@@ -442,6 +445,7 @@ static TrArgs<T> tr_args(const TrLayout &lay) {
   a.kind = lay.kind;
   a.n = lay.bw;
   a.s = lay.s;
+  a.sb = tr_sign_bit(lay.kind, lay.bw, lay.s);
   a.N = lay.N;
   a.a = lay.a;
   a.b = lay.b;

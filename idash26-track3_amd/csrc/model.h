@@ -38,7 +38,7 @@ struct ModelDims {
   int fus[4] = {1024, 512, 1, 0};
   int lut_nmax = 138;
   int mask_scale = 0;  // atom mask values are 0 or 2^mask_scale
-  int xw_slack = 0;    // truncate the GCN products H.W^T with TRSLACK (|x| < 2^(bw-2))
+  int slack = 0;  // 0 exact; 1 H.W^T truncated with TRSLACK; 2 also A.XW + b: TRSLACK + RELUSLACK
 };
 
 struct Counters {

@@ -494,8 +494,12 @@ class Model final : public ModelBase, KeySource {
     timer.reset();
   }
 
-  // gate of the GCN products H.W^T: exact TR, or TRSLACK (exact for |x| < 2^(bw-2))
-  int xw_kind() const { return d_.xw_slack ? G_TRSLACK : G_TR; }
+  // gate of the GCN products H.W^T: exact TR, or (slack >= 1) TRSLACK, exact
+  // for |x| < 2^(bw-2)
+  int xw_kind() const { return d_.slack >= 1 ? G_TRSLACK : G_TR; }
+  // the GCN aggregation A.XW + bias, then ReLU: one TRRELU gate, or (slack >= 2)
+  // TRSLACK with the bias followed by RELUSLACK on the truncated value
+  bool agg_split() const { return d_.slack >= 2; }
 
   // ---------------- weights ----------------
   int nlayers() const { return 5 + d_.nfus; }
@@ -581,7 +585,12 @@ class Model final : public ModelBase, KeySource {
       size_t E = BN * d_.gcn[l];
       tr(xw_kind(), E);
       push(sxs_layout(bw_, B, N, N, d_.gcn[l], o).end);
-      tr(G_TRRELU, E);
+      if (agg_split()) {
+        tr(G_TRSLACK, E);
+        tr(G_RELUSLACK, E);
+      } else {
+        tr(G_TRRELU, E);
+      }
     }
     int pairs[32];
     int Lv = pool_levels(N, pairs);
@@ -696,7 +705,12 @@ class Model final : public ModelBase, KeySource {
       TRY(pub_gemm(rX.p, l, BN, t1.p));
       TRY(d.tr(xw_kind(), En, t1.p, t2.p));
       TRY(d.sxs(B, N, N, fo, rN.p, t2.p, t1.p, gt.p));
-      TRY(d.tr(G_TRRELU, En, t1.p, rX.p));
+      if (agg_split()) {
+        TRY(d.tr(G_TRSLACK, En, t1.p, t2.p));
+        TRY(d.tr(G_RELUSLACK, En, t2.p, rX.p));
+      } else {
+        TRY(d.tr(G_TRRELU, En, t1.p, rX.p));
+      }
     }
     // pool
     const int C = d_.gcn[2];
@@ -1202,7 +1216,12 @@ class Model final : public ModelBase, KeySource {
       TRY(pub_gemm(H, l, BN, Z));
       TRY(r.tr(xw_kind(), En, Z, nullptr, 1, XW));
       TRY(r.sxs(B, N, N, fo, An_.p, XW, Z));
-      TRY(r.tr(G_TRRELU, En, Z, bias_[l].p, fo, H));
+      if (agg_split()) {  // truncate with the bias, reveal, then ReLU of the small value
+        TRY(r.tr(G_TRSLACK, En, Z, bias_[l].p, fo, XW));
+        TRY(r.tr(G_RELUSLACK, En, XW, nullptr, 1, H));
+      } else {
+        TRY(r.tr(G_TRRELU, En, Z, bias_[l].p, fo, H));
+      }
     }
     // masked max-pool: V = H + 2^(bw-2-ms) m^ - 2^(bw-2) (the sentinel -2^(bw-2) on
     // padding rows for a mask of 0 or 2^ms), then a tree of max(a,b) = a + ReLU(b-a)
@@ -1330,8 +1349,8 @@ ModelBase *make_model(int bw, int s, const ModelDims &d, const int64_t *W, size_
     *err = "layer widths must be >= 1 (protein width >= 0, lut_nmax in [0, 255])";
     return nullptr;
   }
-  if (d.xw_slack != 0 && d.xw_slack != 1) {
-    *err = "xw_slack must be 0 or 1";
+  if (d.slack < 0 || d.slack > 2) {
+    *err = "slack must be 0, 1 or 2";
     return nullptr;
   }
   if (d.mask_scale < 0 || d.mask_scale > bw - 2 - 1) {

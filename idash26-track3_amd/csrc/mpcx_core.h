@@ -28,6 +28,7 @@ enum GateKind : int {
   G_LUT8 = 6,     // 8-bit DPF lookup table
   G_SXS = 7,      // batched secret x secret ring GEMM
   G_REVEAL = 8,   // additive shares -> masked public
+  G_RELUSLACK = 9,  // ReLU for |x| < 2^(bw-2-s): a (bw-2-s)-bit DCF (after TRSLACK)
   G_OUTPUT = 9    // final unmask (output mask in the clear)
 };
 
@@ -75,19 +76,23 @@ struct TrLayout {
   int ncase = 0;
 };
 
+// Bit of the shifted input that carries the sign: the top bit, or bit bw-2-s
+// for RELUSLACK (inputs |x| < 2^(bw-2-s), e.g. a value truncated by TRSLACK).
+inline int tr_sign_bit(int kind, int bw, int s) { return kind == G_RELUSLACK ? bw - 2 - s : bw - 1; }
+
 inline TrLayout tr_layout(int kind, int bw, int s, size_t N, size_t base) {
   TrLayout t;
   t.kind = kind;
   t.bw = bw;
   t.s = s;
   t.N = N;
-  t.relu = kind == G_TRRELU || kind == G_RELU;
+  t.relu = kind == G_TRRELU || kind == G_RELU || kind == G_RELUSLACK;
   t.use_a = kind != G_TRSLACK;
-  t.use_b = kind != G_RELU;
+  t.use_b = kind != G_RELU && kind != G_RELUSLACK;
   const size_t tb = size_t(bw) / 8;
   size_t o = align_up(base);
   if (t.use_a) {
-    t.a = dcf_layout(bw - 1, N, o, true);
+    t.a = dcf_layout(tr_sign_bit(kind, bw, s), N, o, true);
     o = t.a.end;
   }
   if (t.use_b) {
@@ -98,7 +103,7 @@ inline TrLayout tr_layout(int kind, int bw, int s, size_t N, size_t base) {
     t.off_kappa = o;
     o = align_up(o + N * tb);
   }
-  t.ncase = kind == G_RELU ? 2 : 8;
+  t.ncase = kind == G_RELU || kind == G_RELUSLACK ? 2 : 8;
   t.off_g = o;
   o = align_up(o + size_t(t.ncase) * N * tb);
   t.end = o;

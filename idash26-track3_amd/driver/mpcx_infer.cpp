@@ -12,7 +12,8 @@
 //     role 2  dealer and evaluator in one run (keys stay resident in HBM)
 //   environment: MPCX_WEIGHTS_BIN (default ./weights.bin), MPCX_SEED (dealer
 //   seed, default 12345), MPCX_LANES (concurrent sub-batches, default 1),
-//   MPCX_LUT_NMAX (largest degree with a D^-1/2 table entry, default 138).
+//   MPCX_LUT_NMAX (largest degree with a D^-1/2 table entry, default 138),
+//   MPCX_SLACK (slack truncations of the GCN, 0 / 1 / 2, default 0: exact).
 //
 // Differences from the reference driver: one process evaluates both parties
 // (no peer address), so "Comm (B)" is the bytes both parties would exchange per
@@ -142,7 +143,7 @@ int main(int argc, char **argv) {
   for (int i = 0; i < d.nfus; i++) d.fus[i] = int(layers[size_t(5 + i)].second);
   d.lut_nmax = env_int("MPCX_LUT_NMAX", 138);
   d.mask_scale = scale;  // the mask files hold 2^s for a real atom (reference/share_data.py:135-159)
-  d.xw_slack = 0;
+  d.slack = env_int("MPCX_SLACK", 0);
   if (d.feat != feat || d.prot != prot) die("weights and batch manifest disagree on feature or protein width");
 
   mpcx_ctx *ctx = nullptr;

@@ -12,7 +12,7 @@ import numpy as np
 HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(HERE, "libmpcx.so")
 
-TR, TRRELU, RELU, TRSLACK = 1, 2, 3, 4
+TR, TRRELU, RELU, TRSLACK, RELUSLACK = 1, 2, 3, 4, 9
 
 _lib = None
 
@@ -20,7 +20,7 @@ _lib = None
 class ModelDims(C.Structure):
     _fields_ = [("n_nodes", C.c_int), ("feat", C.c_int), ("gcn", C.c_int * 3), ("dfc", C.c_int * 2),
                 ("prot", C.c_int), ("nfus", C.c_int), ("fus", C.c_int * 4), ("lut_nmax", C.c_int),
-                ("mask_scale", C.c_int), ("xw_slack", C.c_int)]
+                ("mask_scale", C.c_int), ("slack", C.c_int)]
 
 
 _SIGS = {
@@ -405,7 +405,7 @@ def model_dims(d):
     md = ModelDims()
     md.n_nodes, md.feat, md.prot, md.lut_nmax = d.n_nodes, d.feat, d.prot, d.lut_nmax
     md.mask_scale = getattr(d, "mask_scale", 0)
-    md.xw_slack = int(getattr(d, "xw_slack", 0))
+    md.slack = int(getattr(d, "slack", 0))
     for i, v in enumerate(d.gcn):
         md.gcn[i] = v
     for i, v in enumerate(d.dfc):

@@ -39,6 +39,7 @@ typedef struct mpcx_model mpcx_model;
 #define MPCX_TRRELU 2   /* ReLU(floor(x/2^s) + bias), fused                   */
 #define MPCX_RELU 3     /* ReLU(x)                                            */
 #define MPCX_TRSLACK 4  /* exact floor(x/2^s), requires |x| < 2^(bw-2)        */
+#define MPCX_RELUSLACK 9 /* ReLU(x), requires |x| < 2^(bw-2-s): one (bw-2-s)-bit DCF */
 
 /* ---------------- context ----------------
  * Replaces the evaluator/dealer constructors DDGOrcaBase(party, ip, bw, scale)
@@ -212,12 +213,15 @@ typedef struct {
   int lut_nmax; /* largest degree with a D^-1/2 table entry */
   int mask_scale; /* atom mask values are 0 or 2^mask_scale: 0, or s for the reference's
                      mask files (reference/share_data.py:135-159 shares the mask at scale s) */
-  int xw_slack;   /* 0: the GCN products H.W^T are truncated exactly over the signed ring
-                     (DDGOrca::truncateForward TrFloor, gpu_mpc/ddg_orca.h:112-123: two DCFs,
-                     31 AES per element and party at bw=32); 1: with the top-two-bit slack
-                     truncation (the reference's TrWithSlack, ddg_orca.h:50, 60), exact for
-                     |H.W^T| < 2^(bw-2), one 12-bit DCF (6 AES).  Outputs are bit-exact with
-                     the fixed-point forward while every H.W^T lies in that half ring. */
+  int slack;      /* 0: every truncation is exact over the signed ring (DDGOrca::truncateForward
+                     TrFloor, gpu_mpc/ddg_orca.h:112-123: two DCFs, 31 AES per element and party
+                     at bw=32).  1: the GCN products H.W^T use the top-two-bit slack truncation
+                     (the reference's TrWithSlack, ddg_orca.h:50, 60), exact for |H.W^T| <
+                     2^(bw-2), one s-bit DCF (6 AES).  2: also the aggregation A.XW + bias:
+                     slack truncation with the bias, then MPCX_RELUSLACK on the truncated value
+                     (a (bw-2-s)-bit DCF, 12 AES at bw=32; two more exchange rounds), exact for
+                     |A.XW + b 2^s| < 2^(bw-2).  Outputs are bit-exact with the fixed-point
+                     forward while every such value lies in that half ring. */
 } mpcx_model_dims;
 
 mpcx_status mpcx_model_create(mpcx_ctx *ctx, const mpcx_model_dims *dims, const int64_t *h_weights,

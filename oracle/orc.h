@@ -88,7 +88,8 @@ enum {
   ORC_G_MUL = 5,      /* Beaver elementwise product (index maps)        */
   ORC_G_LUT8 = 6,     /* 8-bit DPF lookup table                         */
   ORC_G_SXS = 7,      /* batched secret x secret ring GEMM              */
-  ORC_G_REVEAL = 8    /* additive shares -> masked public               */
+  ORC_G_REVEAL = 8,   /* additive shares -> masked public               */
+  ORC_G_RELUSLACK = 9 /* ReLU for |x| < 2^(bw-2-s) (a (bw-2-s)-bit DCF)  */
 };
 
 /* Dealer randomness fields. */
@@ -110,6 +111,7 @@ typedef struct {
   int ncase;
   size_t end;
 } orc_tr_layout;
+int orc_sign_bit(int kind, int bw, int s);
 orc_tr_layout orc_tr_layout_make(int kind, int bw, int s, size_t N, size_t base);
 
 /* ---------------- gates (keygen + two-party eval) ----------------
@@ -193,8 +195,9 @@ typedef struct {
   int fus[4];     /* fusion widths */
   int lut_nmax;   /* largest degree with a table entry (mpc_config.py NMAX) */
   int mask_scale; /* the atom mask is 0 or 2^mask_scale (0; s for the reference's files) */
-  int xw_slack;   /* 1: the GCN products H.W^T are truncated with TRSLACK, exact for
-                     |H.W^T| < 2^(bw-2) (half the signed ring); 0: exact TR over the ring */
+  int slack;      /* 0: exact truncations over the signed ring; 1: the GCN products
+                     H.W^T are truncated with TRSLACK (exact for |H.W^T| < 2^(bw-2));
+                     2: also A.XW + bias: TRSLACK then RELUSLACK (|A.XW + b 2^s| < 2^(bw-2)) */
 } orc_dims;
 
 /* Weights: for each linear layer in order gcn0..2, dfc0..1, fus0..nfus-1:

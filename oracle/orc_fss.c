@@ -133,6 +133,10 @@ orc_dcf_layout orc_dcf_layout_make(int m, size_t N, size_t base, int with_z) {
   return L;
 }
 
+/* bit of the shifted input that carries the sign: the top bit, or bit bw-2-s for
+ * RELUSLACK (inputs |x| < 2^(bw-2-s), e.g. a value truncated by TRSLACK) */
+int orc_sign_bit(int kind, int bw, int s) { return kind == ORC_G_RELUSLACK ? bw - 2 - s : bw - 1; }
+
 orc_tr_layout orc_tr_layout_make(int kind, int bw, int s, size_t N, size_t base) {
   orc_tr_layout T;
   memset(&T, 0, sizeof(T));
@@ -140,11 +144,11 @@ orc_tr_layout orc_tr_layout_make(int kind, int bw, int s, size_t N, size_t base)
   T.bw = bw;
   T.s = s;
   T.N = N;
-  T.relu = (kind == ORC_G_TRRELU || kind == ORC_G_RELU);
+  T.relu = (kind == ORC_G_TRRELU || kind == ORC_G_RELU || kind == ORC_G_RELUSLACK);
   size_t o = orc_align(base);
   size_t tb = (size_t)bw / 8;
-  if (kind == ORC_G_TR || kind == ORC_G_TRRELU || kind == ORC_G_RELU) {
-    T.a = orc_dcf_layout_make(bw - 1, N, o, 1);
+  if (kind == ORC_G_TR || kind == ORC_G_TRRELU || kind == ORC_G_RELU || kind == ORC_G_RELUSLACK) {
+    T.a = orc_dcf_layout_make(orc_sign_bit(kind, bw, s), N, o, 1);
     o = T.a.end;
   }
   if (kind == ORC_G_TR || kind == ORC_G_TRRELU || kind == ORC_G_TRSLACK) {
@@ -155,7 +159,7 @@ orc_tr_layout orc_tr_layout_make(int kind, int bw, int s, size_t N, size_t base)
     T.off_kappa = o;
     o = orc_align(o + N * tb);
   }
-  T.ncase = (kind == ORC_G_RELU) ? 2 : 8;
+  T.ncase = (kind == ORC_G_RELU || kind == ORC_G_RELUSLACK) ? 2 : 8;
   T.off_g = o;
   o = orc_align(o + (size_t)T.ncase * N * tb);
   T.end = o;
@@ -313,15 +317,16 @@ void orc_tr_keygen(uint64_t seed, uint32_t gate, int kind, int bw, int s, size_t
   orc_prf_init(&P, seed);
   orc_tr_layout T = orc_tr_layout_make(kind, bw, s, N, base);
   const uint64_t M = rmask(bw);
-  const int n = bw;
-  const uint64_t lowmask = (1ull << (n - 1)) - 1ull;
+  const int n = bw, sb = orc_sign_bit(kind, bw, s);
+  const int relu_like = kind == ORC_G_RELU || kind == ORC_G_RELUSLACK;
+  const uint64_t lowmask = (1ull << sb) - 1ull;
   const uint64_t smask = (1ull << s) - 1ull;
   uint8_t *rb = (uint8_t *)calloc(N, 1), *rd = (uint8_t *)calloc(N, 1);
   uint64_t *aa = (uint64_t *)calloc(N, 8), *ab = (uint64_t *)calloc(N, 8);
   OMP_FOR
   for (size_t i = 0; i < N; i++) {
     uint64_t r = in_mask[i] & M;
-    int rho = (int)((r >> (n - 1)) & 1u);
+    int rho = (int)((r >> sb) & 1u);
     uint64_t R = r >> s;
     int rbi = prf_bit(&P, gate, ORC_F_DCFA + 3, i);
     int rdi = prf_bit(&P, gate, ORC_F_DCFB + 3, i);
@@ -344,7 +349,7 @@ void orc_tr_keygen(uint64_t seed, uint32_t gate, int kind, int bw, int s, size_t
         } else {
           G = rout - R - (uint64_t)d + ((uint64_t)w << (n - s));
         }
-      } else if (kind == ORC_G_RELU) {
+      } else if (relu_like) {
         uint64_t cc = (uint64_t)(c ^ kappa);
         G = rout - cc * r;
       } else { /* TRSLACK */
@@ -365,8 +370,8 @@ void orc_tr_keygen(uint64_t seed, uint32_t gate, int kind, int bw, int s, size_t
       put_t(k1, T.off_kappa, i, bw, ((uint64_t)kappa - q0) & M);
     }
   }
-  if (kind != ORC_G_TRSLACK) orc_dcf_keygen(seed, gate, ORC_F_DCFA, n - 1, N, aa, rb, k0, k1, T.a.off_root);
-  if (kind != ORC_G_RELU) orc_dcf_keygen(seed, gate, ORC_F_DCFB, s, N, ab, rd, k0, k1, T.b.off_root);
+  if (kind != ORC_G_TRSLACK) orc_dcf_keygen(seed, gate, ORC_F_DCFA, sb, N, aa, rb, k0, k1, T.a.off_root);
+  if (!relu_like) orc_dcf_keygen(seed, gate, ORC_F_DCFB, s, N, ab, rd, k0, k1, T.b.off_root);
   free(rb);
   free(rd);
   free(aa);
@@ -378,10 +383,11 @@ void orc_tr_eval(int kind, int bw, int s, size_t N, const uint8_t *k0, const uin
                  uint64_t *yhat, uint64_t *bytes) {
   orc_tr_layout T = orc_tr_layout_make(kind, bw, s, N, base);
   const uint64_t M = rmask(bw);
-  const int n = bw;
-  const uint64_t lowmask = (1ull << (n - 1)) - 1ull;
+  const int n = bw, sb = orc_sign_bit(kind, bw, s);
+  const int relu_like = kind == ORC_G_RELU || kind == ORC_G_RELUSLACK;
+  const uint64_t lowmask = (1ull << sb) - 1ull;
   const uint64_t smask = (1ull << s) - 1ull;
-  const int use_a = kind != ORC_G_TRSLACK, use_b = kind != ORC_G_RELU;
+  const int use_a = kind != ORC_G_TRSLACK, use_b = !relu_like;
   uint8_t *bb[2], *dd[2];
   for (int p = 0; p < 2; p++) {
     bb[p] = (uint8_t *)calloc(N, 1);
@@ -392,8 +398,8 @@ void orc_tr_eval(int kind, int bw, int s, size_t N, const uint8_t *k0, const uin
   for (int p = 0; p < 2; p++) {
     OMP_FOR
     for (size_t i = 0; i < N; i++) {
-      uint64_t b = (kind != ORC_G_RELU && bias_elem) ? ((uint64_t)bias_elem[i] << s) : 0;
-      uint64_t xp = (xhat[i] + b + (1ull << (n - 1))) & M;
+      uint64_t b = (!relu_like && bias_elem) ? ((uint64_t)bias_elem[i] << s) : 0;
+      uint64_t xp = (xhat[i] + b + (1ull << sb)) & M;
       if (use_a) bb[p][i] = (uint8_t)orc_dcf_eval1(p, K[p], &T.a, i, xp & lowmask);
       if (use_b) dd[p][i] = (uint8_t)orc_dcf_eval1(p, K[p], &T.b, i, xp & smask);
     }
@@ -405,9 +411,9 @@ void orc_tr_eval(int kind, int bw, int s, size_t N, const uint8_t *k0, const uin
   for (int p = 0; p < 2; p++) {
     OMP_FOR
     for (size_t i = 0; i < N; i++) {
-      uint64_t b = (kind != ORC_G_RELU && bias_elem) ? ((uint64_t)bias_elem[i] << s) : 0;
-      uint64_t xp = (xhat[i] + b + (1ull << (n - 1))) & M;
-      int h = (int)(xp >> (n - 1));
+      uint64_t b = (!relu_like && bias_elem) ? ((uint64_t)bias_elem[i] << s) : 0;
+      uint64_t xp = (xhat[i] + b + (1ull << sb)) & M;
+      int h = (int)((xp >> sb) & 1u);
       int bh = bb[0][i] ^ bb[1][i];
       int dh = dd[0][i] ^ dd[1][i];
       uint64_t A = ((xp >> s) - (1ull << (n - 1 - s))) & M;
@@ -423,7 +429,7 @@ void orc_tr_eval(int kind, int bw, int s, size_t N, const uint8_t *k0, const uin
         } else {
           out = (p == 0 ? A : 0) + G;
         }
-      } else if (kind == ORC_G_RELU) {
+      } else if (relu_like) {
         int z = h ^ bh;
         uint64_t G = get_t(K[p], T.off_g, (size_t)z * N + i, bw);
         uint64_t kap = get_t(K[p], T.off_kappa, i, bw);

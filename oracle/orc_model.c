@@ -35,8 +35,11 @@ static void trace(uint32_t g, size_t n, const uint64_t *v) {
 
 /* ---------------- dims / weights ---------------- */
 static int nlayers(const orc_dims *d) { return 5 + d->nfus; }
-/* gate of the GCN products H.W^T: exact TR, or TRSLACK when d->xw_slack */
-static int xw_kind(const orc_dims *d) { return d->xw_slack ? ORC_G_TRSLACK : ORC_G_TR; }
+/* gate of the GCN products H.W^T: exact TR, or TRSLACK when d->slack >= 1 */
+static int xw_kind(const orc_dims *d) { return d->slack >= 1 ? ORC_G_TRSLACK : ORC_G_TR; }
+/* the GCN aggregation A.XW + bias then ReLU: one TRRELU gate, or (d->slack >= 2)
+ * TRSLACK (with the bias) followed by RELUSLACK on the truncated value */
+static int agg_split(const orc_dims *d) { return d->slack >= 2; }
 static void layer_io(const orc_dims *d, int l, int *in, int *out) {
   if (l < 3) {
     *in = l == 0 ? d->feat : d->gcn[l - 1];
@@ -77,9 +80,10 @@ static const char *DOMAIN_MSG[] = {
     "node degree outside the 8-bit LUT domain",
     "adjacency or mask entry not 0/1",
     "GCN product H.W^T outside the slack truncation's domain (|x| < 2^(bw-2))",
+    "GCN aggregation A.XW + bias*2^s outside the slack truncation's domain (|x| < 2^(bw-2))",
 };
 const char *orc_domain_msg(int code) {
-  if (code < 0 || code > 7) return "unknown";
+  if (code < 0 || code > 8) return "unknown";
   return DOMAIN_MSG[code];
 }
 
@@ -108,14 +112,18 @@ static i128 dot(const int64_t *a, size_t as, const int64_t *b, size_t bs, size_t
   return (i128)acc;
 }
 /* y(MxN) = wrap(tr(X(MxK) . B(KxN))); optional bias check for the fused gate;
- * slack: the product must also lie in [-2^(bw-2), 2^(bw-2)) (TRSLACK) */
+ * slack_code != 0: the truncated value (product, plus bias*2^s when bias_check is
+ * given) must also lie in [-2^(bw-2), 2^(bw-2)) (TRSLACK), else that code */
 static void fixed_mm(fx *f, const int64_t *X, const int64_t *Bm, size_t M, size_t K, size_t N,
-                     const int64_t *bias_check, int slack, int64_t *Y) {
+                     const int64_t *bias_check, int slack_code, int64_t *Y) {
   for (size_t i = 0; i < M; i++)
     for (size_t j = 0; j < N; j++) {
       i128 P = dot(X + i * K, 1, Bm + j, N, K);
       if (!fits(f, P)) seterr(f, 1);
-      if (slack && !(P >= -((i128)1 << (f->bw - 2)) && P < ((i128)1 << (f->bw - 2)))) seterr(f, 7);
+      if (slack_code) {
+        const i128 v = P + (bias_check ? ((i128)bias_check[j] << f->s) : 0);
+        if (!(v >= -((i128)1 << (f->bw - 2)) && v < ((i128)1 << (f->bw - 2)))) seterr(f, slack_code);
+      }
       if (bias_check && !fits(f, P + ((i128)bias_check[j] << f->s))) seterr(f, 2);
       Y[i * N + j] = wrapv(f, P >> f->s);
     }
@@ -187,8 +195,8 @@ int orc_plain_forward(const orc_dims *d, int B, const int64_t *X, const int64_t 
       int fo = d->gcn[l];
       const int64_t *Wt = W + layer_off(d, l);
       const int64_t *bias = Wt + (size_t)fin * fo;
-      fixed_mm(&f, H, Wt, (size_t)N, (size_t)fin, (size_t)fo, NULL, d->xw_slack, XW); /* XW */
-      fixed_mm(&f, Af, XW, (size_t)N, (size_t)N, (size_t)fo, bias, 0, Hn);  /* A . XW */
+      fixed_mm(&f, H, Wt, (size_t)N, (size_t)fin, (size_t)fo, NULL, d->slack >= 1 ? 7 : 0, XW); /* XW */
+      fixed_mm(&f, Af, XW, (size_t)N, (size_t)N, (size_t)fo, bias, d->slack >= 2 ? 8 : 0, Hn); /* A.XW */
       for (int i = 0; i < N; i++)
         for (int j = 0; j < fo; j++) {
           int64_t v = wrapv(&f, (i128)Hn[(size_t)i * fo + j] + bias[j]);
@@ -444,7 +452,12 @@ size_t orc_model_key_bytes(const orc_dims *d, int B) {
     size_t E = (size_t)B * N * d->gcn[l];
     o = orc_tr_layout_make(xw_kind(d), bw, s, E, o).end;
     o = orc_sxs_layout(bw, (size_t)B, (size_t)N, (size_t)N, (size_t)d->gcn[l], o, &r1, &r2, &r3);
-    o = orc_tr_layout_make(ORC_G_TRRELU, bw, s, E, o).end;
+    if (agg_split(d)) {
+      o = orc_tr_layout_make(ORC_G_TRSLACK, bw, s, E, o).end;
+      o = orc_tr_layout_make(ORC_G_RELUSLACK, bw, s, E, o).end;
+    } else {
+      o = orc_tr_layout_make(ORC_G_TRRELU, bw, s, E, o).end;
+    }
   }
   int pairs[32];
   int L = pool_levels(N, pairs);
@@ -499,8 +512,15 @@ int orc_model_keygen(const orc_dims *d, int B, uint64_t seed, const int64_t *W, 
     o = orc_tr_layout_make(xw_kind(d), bw, s, E, o).end;
     orc_sxs_keygen(seed, g++, bw, (size_t)B, (size_t)N, (size_t)N, (size_t)fo, rN, t2, t1, k0, k1, o);
     o = orc_sxs_layout(bw, (size_t)B, (size_t)N, (size_t)N, (size_t)fo, o, &r1, &r2, &r3);
-    orc_tr_keygen(seed, g++, ORC_G_TRRELU, bw, s, E, t1, rX, k0, k1, o);
-    o = orc_tr_layout_make(ORC_G_TRRELU, bw, s, E, o).end;
+    if (agg_split(d)) {
+      orc_tr_keygen(seed, g++, ORC_G_TRSLACK, bw, s, E, t1, t2, k0, k1, o);
+      o = orc_tr_layout_make(ORC_G_TRSLACK, bw, s, E, o).end;
+      orc_tr_keygen(seed, g++, ORC_G_RELUSLACK, bw, s, E, t2, rX, k0, k1, o);
+      o = orc_tr_layout_make(ORC_G_RELUSLACK, bw, s, E, o).end;
+    } else {
+      orc_tr_keygen(seed, g++, ORC_G_TRRELU, bw, s, E, t1, rX, k0, k1, o);
+      o = orc_tr_layout_make(ORC_G_TRRELU, bw, s, E, o).end;
+    }
     fin = fo;
   }
   /* pool: V = H3 + S*m - S, mask rH3 + S*rm */
@@ -627,9 +647,18 @@ int orc_model_eval(const orc_dims *d, int B, const int64_t *W, const uint8_t *k0
     trace(g++, E, t1);
     o = orc_sxs_layout(bw, (size_t)B, (size_t)N, (size_t)N, (size_t)fo, o, &r1, &r2, &r3);
     for (size_t e = 0; e < E; e++) be[e] = bias[e % fo];
-    orc_tr_eval(ORC_G_TRRELU, bw, s, E, k0, k1, o, t1, be, H, &by);
-    trace(g++, E, H);
-    o = orc_tr_layout_make(ORC_G_TRRELU, bw, s, E, o).end;
+    if (agg_split(d)) {
+      orc_tr_eval(ORC_G_TRSLACK, bw, s, E, k0, k1, o, t1, be, t2, &by);
+      trace(g++, E, t2);
+      o = orc_tr_layout_make(ORC_G_TRSLACK, bw, s, E, o).end;
+      orc_tr_eval(ORC_G_RELUSLACK, bw, s, E, k0, k1, o, t2, NULL, H, &by);
+      trace(g++, E, H);
+      o = orc_tr_layout_make(ORC_G_RELUSLACK, bw, s, E, o).end;
+    } else {
+      orc_tr_eval(ORC_G_TRRELU, bw, s, E, k0, k1, o, t1, be, H, &by);
+      trace(g++, E, H);
+      o = orc_tr_layout_make(ORC_G_TRRELU, bw, s, E, o).end;
+    }
     fin = fo;
   }
   const int C = d->gcn[2];

@@ -96,6 +96,10 @@ def _tr_inputs(rng, kind, bw, n=4000):
     if kind == 4:
         x = np.concatenate([np.array([-q, -1, 0, 1, q - 1], np.int64), rng.integers(-q, q, size=n, dtype=np.int64)])
         return x, None
+    if kind == 9:
+        qs = 1 << (bw - 2 - S)
+        x = np.concatenate([np.array([-qs, -1, 0, 1, qs - 1], np.int64), rng.integers(-qs, qs, size=n, dtype=np.int64)])
+        return x, None
     x = np.concatenate([np.array(edge, np.int64), rng.integers(-(h // 4), h // 4, size=n // 2, dtype=np.int64),
                         rng.integers(-8 << S, 8 << S, size=n // 2)])
     bias = None
@@ -111,12 +115,12 @@ def _tr_expected(kind, x, bias):
         bb = np.resize(bias, x.size)
         t = (x + (bb << S)) >> S
         return t if kind == 1 else np.maximum(t, 0)
-    if kind == 3:
+    if kind in (3, 9):
         return np.maximum(x, 0)
     return x >> S
 
 
-@pytest.mark.parametrize("kind", [1, 2, 3, 4])
+@pytest.mark.parametrize("kind", [1, 2, 3, 4, 9])
 def test_tr_family_keys_and_eval(ctx, orc, kind):
     bw = ctx.bw
     rng = np.random.default_rng(kind * 100 + bw)
@@ -250,15 +254,15 @@ def test_reveal_keys_and_eval(ctx, orc):
 def _od(orc, dims):
     return orc.make_dims(bw=dims.bw, s=dims.s, n_nodes=dims.n_nodes, feat=dims.feat, gcn=dims.gcn, dfc=dims.dfc,
                          prot=dims.prot, fus=dims.fus, lut_nmax=dims.lut_nmax, mask_scale=dims.mask_scale,
-                         xw_slack=dims.xw_slack)
+                         slack=dims.slack)
 
 
-@pytest.mark.parametrize("bw,xw_slack", [(32, 0), (64, 0), (32, 1), (64, 1)])
-def test_model_keys_and_forward(mp, orc, synth, bw, xw_slack):
+@pytest.mark.parametrize("bw,slack", [(32, 0), (64, 0), (32, 1), (64, 1), (32, 2), (64, 2)])
+def test_model_keys_and_forward(mp, orc, synth, bw, slack):
     """GPU dealer keys byte-identical to the oracle's, forward bit-exact, same
-    exchange bytes; with exact and with slack truncation of the GCN products."""
+    exchange bytes; exact, and with the slack truncations of the GCN."""
     B = 2
-    wl = synth.workload(B, synth.Dims(bw=bw, xw_slack=xw_slack), seed=21)
+    wl = synth.workload(B, synth.Dims(bw=bw, slack=slack), seed=21)
     d = _od(orc, wl.dims)
     want, code = orc.plain_forward(d, wl.X, wl.A, wl.mask, wl.prot, wl.W)
     assert code == 0

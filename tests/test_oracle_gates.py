@@ -85,6 +85,35 @@ def test_tr_slack(orc, bw):
 
 
 @pytest.mark.parametrize("bw", [32, 64])
+def test_relu_slack(orc, bw):
+    """ReLU for |x| < 2^(bw-2-s) with a (bw-2-s)-bit DCF: the domain edges, small
+    values around 0 and uniform values; its key is smaller than the full ReLU's."""
+    rng = np.random.default_rng(bw + 7)
+    q = 1 << (bw - 2 - S)
+    x = np.concatenate([np.array([-q, -q + 1, -2, -1, 0, 1, 2, q - 2, q - 1], np.int64),
+                        rng.integers(-q, q, size=4000, dtype=np.int64), rng.integers(-40, 40, size=500)])
+    rin = mask_in(rng, x.size, bw)
+    k0, k1, rout = orc.tr_keygen(9, 4, 9, bw, S, rin)
+    xhat = (ring(x, bw) + rin) & np.uint64(mod(bw) if bw < 64 else 0xFFFFFFFFFFFFFFFF)
+    y, by = orc.tr_eval(9, bw, S, k0, k1, xhat)
+    assert np.array_equal(to_signed(y - rout, bw), np.maximum(x, 0))
+    assert by == 2 * (((x.size + 31) // 32) * 4 + x.size * bw // 8)
+    assert orc.tr_layout(9, bw, S, x.size).end < orc.tr_layout(3, bw, S, x.size).end
+
+
+def test_relu_slack_catches_wrong_sign_bit(orc):
+    """A value just outside the domain (x = 2^(bw-2-s)) reads as negative: the
+    gate really uses bit bw-2-s, which the in-domain test alone would not show."""
+    bw = 32
+    q = 1 << (bw - 2 - S)
+    x = np.array([q, -q - 1], np.int64)
+    rin = np.array([12345, 987654321], np.uint64)
+    k0, k1, rout = orc.tr_keygen(9, 5, 9, bw, S, rin)
+    y, _ = orc.tr_eval(9, bw, S, k0, k1, (ring(x, bw) + rin) & np.uint64(mod(bw)))
+    assert np.array_equal(to_signed(y - rout, bw), [0, -q - 1])
+
+
+@pytest.mark.parametrize("bw", [32, 64])
 def test_mul_index_maps(orc, bw):
     rng = np.random.default_rng(3)
     nx, ny, nz = 50, 40, 500

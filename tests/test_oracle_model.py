@@ -92,27 +92,41 @@ def test_slack_domain_violation_is_reported(orc):
     d, W, X, A, mask, prot = _tiny(orc)
     W = W.copy()
     W[0] = 1 << 18  # XW product 4096 * 2^18 = 2^30
-    d.xw_slack = 1
+    d.slack = 1
     _, code = orc.plain_forward(d, X, A, mask, prot, W)
     assert code == 7 and "slack" in orc.domain_msg(code)
-    d.xw_slack = 0
+    d.slack = 0
     _, code = orc.plain_forward(d, X, A, mask, prot, W)
     assert code != 7
     W[0] = (1 << 18) - 1  # just inside the half ring
-    d.xw_slack = 1
+    d.slack = 1
     _, code = orc.plain_forward(d, X, A, mask, prot, W)
     assert code != 7
 
 
-def _wl(synth, B, bw=32, seed=0, n_nodes=140, xw_slack=0):
-    dims = synth.Dims(bw=bw, n_nodes=n_nodes, xw_slack=xw_slack)
+def test_slack2_aggregation_domain_is_reported(orc):
+    """slack = 2 also needs |A.XW + b 2^s| < 2^(bw-2): a bias that pushes the
+    aggregation of the first layer past it gives code 8 (and not under slack 1)."""
+    d, W, X, A, mask, prot = _tiny(orc)
+    W = W.copy()
+    W[1] = (1 << 18)  # gcn0 bias: b*2^s = 2^30
+    d.slack = 2
+    _, code = orc.plain_forward(d, X, A, mask, prot, W)
+    assert code == 8 and "aggregation" in orc.domain_msg(code)
+    d.slack = 1
+    _, code = orc.plain_forward(d, X, A, mask, prot, W)
+    assert code != 8
+
+
+def _wl(synth, B, bw=32, seed=0, n_nodes=140, slack=0):
+    dims = synth.Dims(bw=bw, n_nodes=n_nodes, slack=slack)
     return synth.workload(B, dims, seed=seed)
 
 
 def _od(orc, wl):
     d = wl.dims
     return orc.make_dims(bw=d.bw, s=d.s, n_nodes=d.n_nodes, feat=d.feat, gcn=d.gcn, dfc=d.dfc, prot=d.prot,
-                         fus=d.fus, lut_nmax=d.lut_nmax, mask_scale=d.mask_scale, xw_slack=d.xw_slack)
+                         fus=d.fus, lut_nmax=d.lut_nmax, mask_scale=d.mask_scale, slack=d.slack)
 
 
 def test_permutation_invariance(orc, synth):
@@ -196,11 +210,11 @@ def test_bw32_equals_bw64_in_domain(orc, synth):
     assert c32 == 0 and c64 == 0 and np.array_equal(o32, o64)
 
 
-@pytest.mark.parametrize("bw,xw_slack", [(32, 0), (64, 0), (32, 1), (64, 1)])
-def test_two_party_matches_plaintext(orc, synth, bw, xw_slack):
+@pytest.mark.parametrize("bw,slack", [(32, 0), (64, 0), (32, 1), (64, 1), (32, 2), (64, 2)])
+def test_two_party_matches_plaintext(orc, synth, bw, slack):
     """Two-party evaluation reconstructs the plaintext forward, with exact and
     with slack truncation of the GCN products (in the slack domain)."""
-    wl = _wl(synth, 2, bw=bw, seed=10, xw_slack=xw_slack)
+    wl = _wl(synth, 2, bw=bw, seed=10, slack=slack)
     d = _od(orc, wl)
     out, code = orc.plain_forward(d, wl.X, wl.A, wl.mask, wl.prot, wl.W)
     assert code == 0
