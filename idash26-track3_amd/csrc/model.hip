@@ -664,8 +664,20 @@ class Model final : public ModelBase, KeySource {
   }
 
   // ---------------- dealer ----------------
+  // back from streamed keys to a resident arena (keygen or import after attach)
+  hipError_t leave_stream() {
+    if (!streaming_) return hipSuccess;
+    stop_io();
+    TRY(hipStreamSynchronize(L_.stream));
+    if (cs_) TRY(hipStreamSynchronize(cs_));
+    free_stream();
+    keyed_B_ = -1;
+    return hipSuccess;
+  }
+
   hipError_t keygen(int B, uint64_t seed) override {
-    if (streaming_) return hipErrorInvalidValue;
+    TRY(leave_stream());
+    keyed_B_ = -1;  // until the new keys are complete
     TRY(hipStreamSynchronize(L_.stream));  // a running forward may still read the arena
     drop_graph();
     TRY(ensure_arena(B));
@@ -752,8 +764,10 @@ class Model final : public ModelBase, KeySource {
   }
 
   hipError_t import_keys(int B, const void *k0, const void *k1, size_t bytes) override {
-    if (streaming_ || bytes != key_bytes(B)) return hipErrorInvalidValue;
+    if (bytes != key_bytes(B)) return hipErrorInvalidValue;
+    TRY(leave_stream());
     TRY(hipStreamSynchronize(L_.stream));  // a running forward may still read the arena
+    keyed_B_ = -1;  // until the new keys are complete
     drop_graph();
     TRY(ensure_arena(B));
     TRY(hipMemcpy(arena_[0], k0, bytes, hipMemcpyHostToDevice));
@@ -830,6 +844,7 @@ class Model final : public ModelBase, KeySource {
 
   // plan, chunks, device slots and events of the streamed arena
   hipError_t setup_stream(int B, bool packed, size_t slot_bytes) {
+    keyed_B_ = -1;  // the resident keys go away below; set again once the slots exist
     stop_io();
     TRY(hipStreamSynchronize(L_.stream));
     if (cs_) TRY(hipStreamSynchronize(cs_));

@@ -703,6 +703,11 @@ def test_model_streamed_keys_match_resident(mp, orc, synth, bw):
     m.set_inputs(B, *wl2.shares["x"], *wl2.shares["a"], *wl2.shares["m"], wl2.prot)
     m.forward(B)
     assert np.array_equal(m.output(B), want2)
+    # back to a resident arena: a fresh dealer run replaces the streamed keys
+    m.keygen(B, 556)
+    m.forward(B)
+    assert np.array_equal(m.output(B), want2)
+    assert m.stream_stats()["chunks"] == 0
     m.close()
     c.close()
     for h in (h0, h1, hp):
