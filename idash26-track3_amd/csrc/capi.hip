@@ -505,19 +505,17 @@ static mpcx_status sxs_eval_t(mpcx_ctx *c, int nb, int M, int K, int N, const vo
   g.B2 = reinterpret_cast<const T *>(k0 + lay.off_rb);
   g.Cin = reinterpret_cast<const T *>(k0 + lay.off_c);
   g.C = m0;
-  HIPC(c, launch_gemm<T>(c->L, g), "gemm");
+  // party 1: C1 - [A^ RA1] [RB1; B^]
   GemmArgs<T> h = g;
   h.A2 = nullptr;
   h.B2 = nullptr;
   h.B1 = reinterpret_cast<const T *>(k1 + lay.off_rb);
+  h.A1b = reinterpret_cast<const T *>(k1 + lay.off_ra);
+  h.B1b = static_cast<const T *>(b);
   h.Cin = reinterpret_cast<const T *>(k1 + lay.off_c);
   h.C = m1;
   h.sign = -1;
-  HIPC(c, launch_gemm<T>(c->L, h), "gemm");
-  h.A1 = reinterpret_cast<const T *>(k1 + lay.off_ra);
-  h.B1 = static_cast<const T *>(b);
-  h.Cin = m1;
-  HIPC(c, launch_gemm<T>(c->L, h), "gemm");
+  HIPC(c, launch_gemm_pair<T>(c->L, g, h), "gemm");
   c->counters.msg(nc, c->bw);
   HIPC(c, launch_reconstruct<T>(c->L, nc, m0, m1, static_cast<T *>(out)), "reconstruct");
   HIPC(c, hipStreamSynchronize(c->L.stream), "sync");

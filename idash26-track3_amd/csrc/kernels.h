@@ -137,9 +137,16 @@ struct GemmArgs {
   size_t sA = 0, sB = 0, sC = 0;
   int sign = 1;
   int ksplit = 1;  // set by launch_gemm: K slices accumulated with atomic adds
+  // optional second K segment of the same shapes and strides:
+  // C = Cin + sign * ((A1 - A2)(B1 - B2) + A1b B1b)
+  const T *A1b = nullptr, *B1b = nullptr;
 };
 template <typename T>
 hipError_t launch_gemm(const Launch &L, const GemmArgs<T> &g);
+// Two independent products in one launch where the matrix-core path applies
+// (the Beaver products of both parties of an SxS gate), else one after another.
+template <typename T>
+hipError_t launch_gemm_pair(const Launch &L, const GemmArgs<T> &g0, const GemmArgs<T> &g1);
 
 // ---------------- SxS keys ----------------
 template <typename T>

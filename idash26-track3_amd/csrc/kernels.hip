@@ -1057,18 +1057,24 @@ typedef int v4i_t __attribute__((ext_vector_type(4)));
 
 __device__ __forceinline__ uint32_t ring_digits(uint32_t a) { return (a + 0x80808080u) ^ 0x80808080u; }
 
-__global__ __launch_bounds__(256) void k_gemm_mfma(GemmArgs<uint32_t> g) {
+// One 64 x 64 output tile of problem g; z = batch * ksplit + K slice.  A second
+// K segment (A1b, B1b) starts at the K tile after the first segment's last one,
+// so every 64-wide K tile reads one segment only.
+__device__ __forceinline__ void gemm_mfma_tile(const GemmArgs<uint32_t> &g, int z, uint32_t *As, uint32_t *Bt) {
   constexpr int BM = 64, BN = 64, BK = 64, LD = BK + 4;
-  __shared__ __align__(16) uint32_t As[BM * LD];
-  __shared__ __align__(16) uint32_t Bt[BN * LD];
-  const int bz = blockIdx.z / g.ksplit, kz = blockIdx.z % g.ksplit;
-  const int kchunk = ((g.K + g.ksplit - 1) / g.ksplit + BK - 1) / BK * BK;
-  const int kbeg = kz * kchunk, kend = min(g.K, kbeg + kchunk);
+  const int Kp = (g.K + BK - 1) / BK * BK;
+  const int Kt = g.A1b ? Kp + g.K : g.K;
+  const int bz = z / g.ksplit, kz = z % g.ksplit;
+  const int kchunk = ((Kt + g.ksplit - 1) / g.ksplit + BK - 1) / BK * BK;
+  const int kbeg = kz * kchunk, kend = min(Kt, kbeg + kchunk);
   const uint32_t *A1 = g.A1 + size_t(bz) * g.sA;
   const uint32_t *A2 = g.A2 ? g.A2 + size_t(bz) * g.sA : nullptr;
   const uint32_t *B1 = g.B1 + size_t(bz) * g.sB;
   const uint32_t *B2 = g.B2 ? g.B2 + size_t(bz) * g.sB : nullptr;
+  const uint32_t *A1b = g.A1b ? g.A1b + size_t(bz) * g.sA : nullptr;
+  const uint32_t *B1b = g.B1b ? g.B1b + size_t(bz) * g.sB : nullptr;
   const int m0 = blockIdx.y * BM, n0 = blockIdx.x * BN;
+  if (m0 >= g.M || n0 >= g.N) return;  // the grid spans the larger of two problems
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int li = lane & 15, lg = lane >> 4;
   v4i_t acc[4][4];
@@ -1083,27 +1089,31 @@ __global__ __launch_bounds__(256) void k_gemm_mfma(GemmArgs<uint32_t> g) {
   uint32_t ra[16], rb[16];
   const int lo = tid & 63, hb = tid >> 6;
   auto load = [&](int k0) {
+    const bool seg = k0 >= Kp;  // uniform over the block
+    const uint32_t *a1 = seg ? A1b : A1, *a2 = seg ? nullptr : A2;
+    const uint32_t *b1 = seg ? B1b : B1, *b2 = seg ? nullptr : B2;
+    const int kk = seg ? k0 - Kp : k0, klim = min(g.K, kend - (seg ? Kp : 0));
 #pragma unroll
     for (int r = 0; r < 16; r++) {
       const int hi = hb + 4 * r;
-      const int gm = m0 + hi, gk = k0 + lo;
+      const int gm = m0 + hi, gk = kk + lo;
       uint32_t v = 0;
-      if (gm < g.M && gk < kend) {
+      if (gm < g.M && gk < klim) {
         const size_t idx = size_t(gm) * g.K + gk;
-        v = A1[idx];
-        if (A2) v -= A2[idx];
+        v = a1[idx];
+        if (a2) v -= a2[idx];
       }
       ra[r] = v;
     }
 #pragma unroll
     for (int r = 0; r < 16; r++) {
       const int hi = hb + 4 * r;
-      const int gk = k0 + hi, gn = n0 + lo;
+      const int gk = kk + hi, gn = n0 + lo;
       uint32_t v = 0;
-      if (gk < kend && gn < g.N) {
+      if (gk < klim && gn < g.N) {
         const size_t idx = size_t(gk) * g.N + gn;
-        v = B1[idx];
-        if (B2) v -= B2[idx];
+        v = b1[idx];
+        if (b2) v -= b2[idx];
       }
       rb[r] = v;
     }
@@ -1160,6 +1170,15 @@ __global__ __launch_bounds__(256) void k_gemm_mfma(GemmArgs<uint32_t> g) {
   }
 }
 
+// blockIdx.z < nz0: problem g0, else problem g1 (nz = batch * ksplit of each)
+__global__ __launch_bounds__(256) void k_gemm_mfma(GemmArgs<uint32_t> g0, GemmArgs<uint32_t> g1, int nz0) {
+  __shared__ __align__(16) uint32_t As[64 * 68];
+  __shared__ __align__(16) uint32_t Bt[64 * 68];
+  const int z = int(blockIdx.z);
+  const bool second = z >= nz0;
+  gemm_mfma_tile(second ? g1 : g0, second ? z - nz0 : z, As, Bt);
+}
+
 // C[b] = Cin[b] (or 0) before the split-K slices are added
 template <typename T>
 __global__ void k_gemm_init(int M, int N, int batch, size_t sC, const T *Cin, T *C) {
@@ -1170,34 +1189,82 @@ __global__ void k_gemm_init(int M, int N, int batch, size_t sC, const T *Cin, T 
   }
 }
 
+// split-K factor: enough K slices that the launch has about two tiles per CU
+template <typename T>
+static int gemm_ksplit(const Launch &L, const GemmArgs<T> &g, int tiles, bool mfma) {
+  const int Kt = g.A1b ? (g.K + 63) / 64 * 64 + g.K : g.K;
+  if (tiles >= L.num_cu || Kt < 64) return 1;
+  const int want = (2 * L.num_cu + tiles - 1) / tiles;
+  return std::max(1, std::min(want, mfma ? (Kt + 63) / 64 : Kt / 32));
+}
+template <typename T>
+static int gemm_tiles(const GemmArgs<T> &g) {
+  return ((g.N + 63) / 64) * ((g.M + 63) / 64) * g.batch;
+}
+template <typename T>
+static hipError_t gemm_init(const Launch &L, const GemmArgs<T> &g) {
+  if (g.ksplit <= 1 || g.C == g.Cin) return hipSuccess;
+  const int block = 256;
+  int grid = grid_for(k_gemm_init<T>, block, size_t(g.M) * g.N * g.batch, L.num_cu);
+  hipLaunchKernelGGL((k_gemm_init<T>), dim3(grid), dim3(block), 0, L.stream, g.M, g.N, g.batch, g.sC, g.Cin, g.C);
+  return hipGetLastError();
+}
+
 template <typename T>
 hipError_t launch_gemm(const Launch &L, const GemmArgs<T> &g0) {
   if (g0.M <= 0 || g0.N <= 0 || g0.batch <= 0) return hipSuccess;
-  GemmArgs<T> g = g0;
   constexpr bool kMfma = sizeof(T) == 4;
   const bool mfma = kMfma && L.gemm == 0;
-  const int tiles = ((g.N + 63) / 64) * ((g.M + 63) / 64) * g.batch;
-  g.ksplit = 1;
-  if (tiles < L.num_cu && g.K >= 64) {
-    const int want = (2 * L.num_cu + tiles - 1) / tiles;
-    g.ksplit = std::max(1, std::min(want, mfma ? (g.K + 63) / 64 : g.K / 32));
+  if (g0.A1b && !mfma) {
+    // the VALU kernel takes one K segment: add the second product in a second launch
+    GemmArgs<T> a = g0, b = g0;
+    a.A1b = a.B1b = nullptr;
+    b.A1 = g0.A1b;
+    b.B1 = g0.B1b;
+    b.A2 = b.B2 = b.A1b = b.B1b = nullptr;
+    b.Cin = b.C;
+    hipError_t e = launch_gemm<T>(L, a);
+    return e != hipSuccess ? e : launch_gemm<T>(L, b);
   }
-  if (g.ksplit > 1 && g.C != g.Cin) {
-    const int block = 256;
-    int grid = grid_for(k_gemm_init<T>, block, size_t(g.M) * g.N * g.batch, L.num_cu);
-    hipLaunchKernelGGL((k_gemm_init<T>), dim3(grid), dim3(block), 0, L.stream, g.M, g.N, g.batch, g.sC, g.Cin, g.C);
-    hipError_t e = hipGetLastError();
-    if (e != hipSuccess) return e;
-  }
+  GemmArgs<T> g = g0;
+  g.ksplit = gemm_ksplit(L, g, gemm_tiles(g), mfma);
+  hipError_t e = gemm_init(L, g);
+  if (e != hipSuccess) return e;
   dim3 grid((g.N + 63) / 64, (g.M + 63) / 64, g.batch * g.ksplit);
   if constexpr (kMfma) {
     if (mfma) {
-      hipLaunchKernelGGL(k_gemm_mfma, grid, dim3(256), 0, L.stream, g);
+      hipLaunchKernelGGL(k_gemm_mfma, grid, dim3(256), 0, L.stream, g, g, int(grid.z));
       return hipGetLastError();
     }
   }
   hipLaunchKernelGGL((k_gemm<T>), grid, dim3(256), 0, L.stream, g);
   return hipGetLastError();
+}
+
+template <typename T>
+hipError_t launch_gemm_pair(const Launch &L, const GemmArgs<T> &p0, const GemmArgs<T> &p1) {
+  constexpr bool kMfma = sizeof(T) == 4;
+  const bool mfma = kMfma && L.gemm == 0;
+  const bool empty0 = p0.M <= 0 || p0.N <= 0 || p0.batch <= 0;
+  const bool empty1 = p1.M <= 0 || p1.N <= 0 || p1.batch <= 0;
+  if (!mfma || empty0 || empty1) {
+    hipError_t e = launch_gemm<T>(L, p0);
+    return e != hipSuccess ? e : launch_gemm<T>(L, p1);
+  }
+  if constexpr (kMfma) {
+    GemmArgs<T> g0 = p0, g1 = p1;
+    const int tiles = gemm_tiles(g0) + gemm_tiles(g1);
+    g0.ksplit = gemm_ksplit(L, g0, tiles, true);
+    g1.ksplit = gemm_ksplit(L, g1, tiles, true);
+    hipError_t e = gemm_init(L, g0);
+    if (e == hipSuccess) e = gemm_init(L, g1);
+    if (e != hipSuccess) return e;
+    const int nz0 = g0.batch * g0.ksplit;
+    dim3 grid((std::max(g0.N, g1.N) + 63) / 64, (std::max(g0.M, g1.M) + 63) / 64, nz0 + g1.batch * g1.ksplit);
+    hipLaunchKernelGGL(k_gemm_mfma, grid, dim3(256), 0, L.stream, g0, g1, nz0);
+    return hipGetLastError();
+  }
+  return hipSuccess;
 }
 
 template <typename T, int NT, int REP>
@@ -1402,6 +1469,7 @@ hipError_t launch_rowsum(const Launch &L, size_t rows, int len, const T *a, T *o
   template hipError_t launch_lut8_phase2<T>(const Launch &, const Lut8Layout &, const uint8_t *, const uint8_t *,    \
                                             const T *, T *, T *);                                                    \
   template hipError_t launch_gemm<T>(const Launch &, const GemmArgs<T> &);                                           \
+  template hipError_t launch_gemm_pair<T>(const Launch &, const GemmArgs<T> &, const GemmArgs<T> &);                \
   template hipError_t launch_split<T>(const Launch &, uint64_t, uint32_t, uint32_t, size_t, const T *, T *, T *,     \
                                       T *);                                                                          \
   template hipError_t launch_prf_ring<T>(const Launch &, uint64_t, uint32_t, uint32_t, size_t, T *);                \

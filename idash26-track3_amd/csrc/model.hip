@@ -277,20 +277,17 @@ struct Runner {
     g.B2 = reinterpret_cast<const T *>(K0 + lay.off_rb);
     g.Cin = reinterpret_cast<const T *>(K0 + lay.off_c);
     g.C = ws.m0.p;
-    TRY(launch_gemm<T>(L, g));
-    // party 1: C1 - A^ RB1 - RA1 B^
+    // party 1: C1 - (A^ RB1 + RA1 B^) = C1 - [A^ RA1] [RB1; B^]
     GemmArgs<T> h = g;
     h.A2 = nullptr;
     h.B2 = nullptr;
     h.B1 = reinterpret_cast<const T *>(K1 + lay.off_rb);
+    h.A1b = reinterpret_cast<const T *>(K1 + lay.off_ra);
+    h.B1b = Bm;
     h.Cin = reinterpret_cast<const T *>(K1 + lay.off_c);
     h.C = ws.m1.p;
     h.sign = -1;
-    TRY(launch_gemm<T>(L, h));
-    h.A1 = reinterpret_cast<const T *>(K1 + lay.off_ra);
-    h.B1 = Bm;
-    h.Cin = ws.m1.p;
-    TRY(launch_gemm<T>(L, h));
+    TRY(launch_gemm_pair<T>(L, g, h));
     TRY(span.end());
     const size_t nc = size_t(nb) * M * N;
     ctr.msg(nc, bw);

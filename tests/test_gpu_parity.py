@@ -190,10 +190,16 @@ def test_lut8_keys_and_eval(ctx, orc):
     assert np.array_equal((y.astype(np.uint64) - orout) & M(bw), table[x.astype(np.int64)])
 
 
-def test_sxs_keys_and_eval(ctx, orc):
+SXS_SHAPES = [(3, 70, 66, 37), (1, 3, 1000, 70), (2, 140, 140, 312), (1, 1, 1, 1), (4, 17, 63, 5)]
+
+
+@pytest.mark.parametrize("shape", SXS_SHAPES)
+def test_sxs_keys_and_eval(ctx, orc, shape):
+    """Batched Beaver products: both parties' GEMMs in one launch (party 1 over
+    the concatenated K of its two products), split-K shapes included."""
     bw = ctx.bw
-    rng = np.random.default_rng(12)
-    nb, Mm, K, N = 3, 70, 66, 37
+    nb, Mm, K, N = shape
+    rng = np.random.default_rng(12 + K)
     A = rng.integers(-(1 << 10), 1 << 10, size=(nb, Mm, K))
     B = rng.integers(-(1 << 10), 1 << 10, size=(nb, K, N))
     ra, rb = rmask(rng, A.size, bw), rmask(rng, B.size, bw)
@@ -233,6 +239,25 @@ def test_ring_gemm_valu_path(mp, orc, monkeypatch):
         A = rmask(rng, M * K, 32).reshape(M, K)
         B = rmask(rng, K * N, 32).reshape(K, N)
         assert np.array_equal(c.ring_gemm(A, B).astype(np.uint64), orc.ring_gemm(32, A, B))
+    c.close()
+
+
+def test_sxs_valu_path(mp, orc, monkeypatch):
+    """The same Beaver products on the VALU GEMM path (two launches for party 1)."""
+    monkeypatch.setenv("MPCX_GEMM", "valu")
+    c = mp.Ctx(bw=32)
+    rng = np.random.default_rng(5)
+    for nb, Mm, K, N in [(2, 70, 66, 37), (1, 3, 1000, 70)]:
+        A = rng.integers(-(1 << 10), 1 << 10, size=(nb, Mm, K))
+        B = rng.integers(-(1 << 10), 1 << 10, size=(nb, K, N))
+        ra, rb = rmask(rng, A.size, 32), rmask(rng, B.size, 32)
+        g0, g1, grc = c.sxs_keygen(nb, Mm, K, N, ra, rb, seed=3, gate=2)
+        _, _, orc_ = orc.sxs_keygen(3, 2, 32, nb, Mm, K, N, ra, rb)
+        ah = (A.ravel().astype(np.uint64) + ra) & M(32)
+        bh = (B.ravel().astype(np.uint64) + rb) & M(32)
+        got = c.sxs_eval(nb, Mm, K, N, g0, g1, ah, bh)
+        assert np.array_equal(signed(got.astype(np.uint64) - orc_, 32).reshape(nb, Mm, N),
+                              np.einsum("bmk,bkn->bmn", A, B))
     c.close()
 
 
