@@ -1059,7 +1059,9 @@ __device__ __forceinline__ uint32_t ring_digits(uint32_t a) { return (a + 0x8080
 
 // One 64 x 64 output tile of problem g; z = batch * ksplit + K slice.  A second
 // K segment (A1b, B1b) starts at the K tile after the first segment's last one,
-// so every 64-wide K tile reads one segment only.
+// so every 64-wide K tile reads one segment only.  VA / VB: rows of A / B are
+// read as 16-byte words (K resp. N a multiple of 4, operands 16-byte aligned).
+template <bool VA, bool VB>
 __device__ __forceinline__ void gemm_mfma_tile(const GemmArgs<uint32_t> &g, int z, uint32_t *As, uint32_t *Bt) {
   constexpr int BM = 64, BN = 64, BK = 64, LD = BK + 4;
   const int Kp = (g.K + BK - 1) / BK * BK;
@@ -1082,50 +1084,134 @@ __device__ __forceinline__ void gemm_mfma_tile(const GemmArgs<uint32_t> &g, int 
   for (int t = 0; t < 4; t++)
 #pragma unroll
     for (int q = 0; q < 4; q++) acc[t][q] = v4i_t{0, 0, 0, 0};
-  // Each thread stages 16 words of the A tile (row hi, column lo) and 16 of the
-  // B tile (row hi, column lo; stored at Bt[lo][hi]), hi = (tid >> 6) + 4r,
-  // lo = tid & 63.  The next slice's words are loaded into registers while the
+  // Each thread stages 16 words of the A tile and 16 of the B tile (B stored
+  // transposed, Bt[n][k]).  Scalar layout: word r at row hb + 4r, column lo;
+  // 16-byte layout: words 4r..4r+3 at row (tid >> 4) + 16r, columns 4 (tid & 15) + 0..3.
+  // The next K tile is loaded into registers (addresses clamped in bounds, the
+  // masking and the A1 - A2 difference applied when stored to LDS) while the
   // matrix cores work on the current one.
-  uint32_t ra[16], rb[16];
-  const int lo = tid & 63, hb = tid >> 6;
+  uint32_t ra[16], ra2[16], rb[16], rb2[16];
+  const int lo = tid & 63, hb = tid >> 6, vq = tid & 15, vr = tid >> 4;
+  struct Seg {
+    const uint32_t *a1, *a2, *b1, *b2;
+    int kk, klim;
+  };
+  auto seg_of = [&](int k0) {
+    const bool second = k0 >= Kp;  // uniform over the block
+    Seg sg;
+    sg.a1 = second ? A1b : A1;
+    sg.a2 = second ? nullptr : A2;
+    sg.b1 = second ? B1b : B1;
+    sg.b2 = second ? nullptr : B2;
+    sg.kk = second ? k0 - Kp : k0;
+    sg.klim = min(g.K, kend - (second ? Kp : 0));
+    return sg;
+  };
+  // (row, column) of staged word r of A and of B, relative to the tile origin
+  auto a_rc = [&](int r, int &row, int &col) {
+    if constexpr (VA) {
+      row = vr + 16 * (r >> 2);
+      col = 4 * vq + (r & 3);
+    } else {
+      row = hb + 4 * r;
+      col = lo;
+    }
+  };
+  auto b_rc = [&](int r, int &row, int &col) {  // row = k, col = n
+    if constexpr (VB) {
+      row = vr + 16 * (r >> 2);
+      col = 4 * vq + (r & 3);
+    } else {
+      row = hb + 4 * r;
+      col = lo;
+    }
+  };
   auto load = [&](int k0) {
-    const bool seg = k0 >= Kp;  // uniform over the block
-    const uint32_t *a1 = seg ? A1b : A1, *a2 = seg ? nullptr : A2;
-    const uint32_t *b1 = seg ? B1b : B1, *b2 = seg ? nullptr : B2;
-    const int kk = seg ? k0 - Kp : k0, klim = min(g.K, kend - (seg ? Kp : 0));
+    const Seg sg = seg_of(k0);
+#pragma unroll
+    for (int r = 0; r < 16; r += VA ? 4 : 1) {
+      int row, col;
+      a_rc(r, row, col);
+      const int gm = m0 + row, gk = sg.kk + col;
+      const size_t idx = (gm < g.M && gk < sg.klim) ? size_t(gm) * g.K + gk : 0;
+      if constexpr (VA) {
+        const uint4 v = *reinterpret_cast<const uint4 *>(sg.a1 + idx);
+        ra[r] = v.x, ra[r + 1] = v.y, ra[r + 2] = v.z, ra[r + 3] = v.w;
+      } else {
+        ra[r] = sg.a1[idx];
+      }
+    }
+    if (sg.a2) {
+#pragma unroll
+      for (int r = 0; r < 16; r += VA ? 4 : 1) {
+        int row, col;
+        a_rc(r, row, col);
+        const int gm = m0 + row, gk = sg.kk + col;
+        const size_t idx = (gm < g.M && gk < sg.klim) ? size_t(gm) * g.K + gk : 0;
+        if constexpr (VA) {
+          const uint4 v = *reinterpret_cast<const uint4 *>(sg.a2 + idx);
+          ra2[r] = v.x, ra2[r + 1] = v.y, ra2[r + 2] = v.z, ra2[r + 3] = v.w;
+        } else {
+          ra2[r] = sg.a2[idx];
+        }
+      }
+    } else {
+#pragma unroll
+      for (int r = 0; r < 16; r++) ra2[r] = 0;
+    }
+#pragma unroll
+    for (int r = 0; r < 16; r += VB ? 4 : 1) {
+      int row, col;
+      b_rc(r, row, col);
+      const int gk = sg.kk + row, gn = n0 + col;
+      const size_t idx = (gk < sg.klim && gn < g.N) ? size_t(gk) * g.N + gn : 0;
+      if constexpr (VB) {
+        const uint4 v = *reinterpret_cast<const uint4 *>(sg.b1 + idx);
+        rb[r] = v.x, rb[r + 1] = v.y, rb[r + 2] = v.z, rb[r + 3] = v.w;
+      } else {
+        rb[r] = sg.b1[idx];
+      }
+    }
+    if (sg.b2) {
+#pragma unroll
+      for (int r = 0; r < 16; r += VB ? 4 : 1) {
+        int row, col;
+        b_rc(r, row, col);
+        const int gk = sg.kk + row, gn = n0 + col;
+        const size_t idx = (gk < sg.klim && gn < g.N) ? size_t(gk) * g.N + gn : 0;
+        if constexpr (VB) {
+          const uint4 v = *reinterpret_cast<const uint4 *>(sg.b2 + idx);
+          rb2[r] = v.x, rb2[r + 1] = v.y, rb2[r + 2] = v.z, rb2[r + 3] = v.w;
+        } else {
+          rb2[r] = sg.b2[idx];
+        }
+      }
+    } else {
+#pragma unroll
+      for (int r = 0; r < 16; r++) rb2[r] = 0;
+    }
+  };
+  // K columns past klim and rows past M / N are staged as zeros
+  auto store = [&](int k0) {
+    const Seg sg = seg_of(k0);
 #pragma unroll
     for (int r = 0; r < 16; r++) {
-      const int hi = hb + 4 * r;
-      const int gm = m0 + hi, gk = kk + lo;
-      uint32_t v = 0;
-      if (gm < g.M && gk < klim) {
-        const size_t idx = size_t(gm) * g.K + gk;
-        v = a1[idx];
-        if (a2) v -= a2[idx];
-      }
-      ra[r] = v;
+      int row, col;
+      a_rc(r, row, col);
+      const bool in = m0 + row < g.M && sg.kk + col < sg.klim;
+      As[row * LD + col] = in ? ring_digits(ra[r] - ra2[r]) : 0u;
     }
 #pragma unroll
     for (int r = 0; r < 16; r++) {
-      const int hi = hb + 4 * r;
-      const int gk = kk + hi, gn = n0 + lo;
-      uint32_t v = 0;
-      if (gk < klim && gn < g.N) {
-        const size_t idx = size_t(gk) * g.N + gn;
-        v = b1[idx];
-        if (b2) v -= b2[idx];
-      }
-      rb[r] = v;
+      int row, col;
+      b_rc(r, row, col);
+      const bool in = sg.kk + row < sg.klim && n0 + col < g.N;
+      Bt[col * LD + row] = in ? ring_digits(rb[r] - rb2[r]) : 0u;
     }
   };
   if (kbeg < kend) load(kbeg);
   for (int k0 = kbeg; k0 < kend; k0 += BK) {
-#pragma unroll
-    for (int r = 0; r < 16; r++) {
-      const int hi = hb + 4 * r;
-      As[hi * LD + lo] = ring_digits(ra[r]);
-      Bt[lo * LD + hi] = ring_digits(rb[r]);
-    }
+    store(k0);
     __syncthreads();
     if (k0 + BK < kend) load(k0 + BK);
 #pragma unroll
@@ -1171,12 +1257,13 @@ __device__ __forceinline__ void gemm_mfma_tile(const GemmArgs<uint32_t> &g, int 
 }
 
 // blockIdx.z < nz0: problem g0, else problem g1 (nz = batch * ksplit of each)
+template <bool VA, bool VB>
 __global__ __launch_bounds__(256) void k_gemm_mfma(GemmArgs<uint32_t> g0, GemmArgs<uint32_t> g1, int nz0) {
   __shared__ __align__(16) uint32_t As[64 * 68];
   __shared__ __align__(16) uint32_t Bt[64 * 68];
   const int z = int(blockIdx.z);
   const bool second = z >= nz0;
-  gemm_mfma_tile(second ? g1 : g0, second ? z - nz0 : z, As, Bt);
+  gemm_mfma_tile<VA, VB>(second ? g1 : g0, second ? z - nz0 : z, As, Bt);
 }
 
 // C[b] = Cin[b] (or 0) before the split-K slices are added
@@ -1187,6 +1274,28 @@ __global__ void k_gemm_init(int M, int N, int batch, size_t sC, const T *Cin, T 
     const size_t b = i / per, r = i % per;
     C[b * sC + r] = Cin ? Cin[b * sC + r] : T(0);
   }
+}
+
+static bool aligned16(const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
+// rows of A (resp. B) can be read as 16-byte words
+static bool gemm_vec_a(const GemmArgs<uint32_t> &g) {
+  return g.K % 4 == 0 && (g.batch == 1 || g.sA % 4 == 0) && aligned16(g.A1) && aligned16(g.A2) && aligned16(g.A1b);
+}
+static bool gemm_vec_b(const GemmArgs<uint32_t> &g) {
+  return g.N % 4 == 0 && (g.batch == 1 || g.sB % 4 == 0) && aligned16(g.B1) && aligned16(g.B2) && aligned16(g.B1b);
+}
+static hipError_t launch_mfma(const Launch &L, dim3 grid, const GemmArgs<uint32_t> &g0,
+                              const GemmArgs<uint32_t> &g1, int nz0) {
+  const bool va = gemm_vec_a(g0) && gemm_vec_a(g1), vb = gemm_vec_b(g0) && gemm_vec_b(g1);
+  if (va && vb)
+    hipLaunchKernelGGL((k_gemm_mfma<true, true>), grid, dim3(256), 0, L.stream, g0, g1, nz0);
+  else if (va)
+    hipLaunchKernelGGL((k_gemm_mfma<true, false>), grid, dim3(256), 0, L.stream, g0, g1, nz0);
+  else if (vb)
+    hipLaunchKernelGGL((k_gemm_mfma<false, true>), grid, dim3(256), 0, L.stream, g0, g1, nz0);
+  else
+    hipLaunchKernelGGL((k_gemm_mfma<false, false>), grid, dim3(256), 0, L.stream, g0, g1, nz0);
+  return hipGetLastError();
 }
 
 // split-K factor: enough K slices that the launch has about two tiles per CU
@@ -1233,8 +1342,7 @@ hipError_t launch_gemm(const Launch &L, const GemmArgs<T> &g0) {
   dim3 grid((g.N + 63) / 64, (g.M + 63) / 64, g.batch * g.ksplit);
   if constexpr (kMfma) {
     if (mfma) {
-      hipLaunchKernelGGL(k_gemm_mfma, grid, dim3(256), 0, L.stream, g, g, int(grid.z));
-      return hipGetLastError();
+      return launch_mfma(L, grid, g, g, int(grid.z));
     }
   }
   hipLaunchKernelGGL((k_gemm<T>), grid, dim3(256), 0, L.stream, g);
@@ -1261,8 +1369,7 @@ hipError_t launch_gemm_pair(const Launch &L, const GemmArgs<T> &p0, const GemmAr
     if (e != hipSuccess) return e;
     const int nz0 = g0.batch * g0.ksplit;
     dim3 grid((std::max(g0.N, g1.N) + 63) / 64, (std::max(g0.M, g1.M) + 63) / 64, nz0 + g1.batch * g1.ksplit);
-    hipLaunchKernelGGL(k_gemm_mfma, grid, dim3(256), 0, L.stream, g0, g1, nz0);
-    return hipGetLastError();
+    return launch_mfma(L, grid, g0, g1, nz0);
   }
   return hipSuccess;
 }
