@@ -301,6 +301,21 @@ mpcx_status mpcx_tr_keygen(mpcx_ctx *c, int kind, size_t n, const void *in, void
                      : tr_keygen_t<uint64_t>(c, kind, n, in, out, seed, gate, k0, k1);
 }
 
+// One TR-family gate evaluation of both parties into y (no synchronisation).
+// bits: four bit planes of ((n + 63) / 64) words; m: 2 n ring words.
+template <typename T>
+static hipError_t tr_eval_run(mpcx_ctx *c, const TrLayout &lay, size_t n, const uint8_t *K0, const uint8_t *K1,
+                              const T *X, const T *Bi, int ncol, T *y, uint64_t *bits, T *m) {
+  const size_t ww = (n + 63) / 64;
+  hipError_t e = launch_tr_phase1<T>(c->L, lay, K0, K1, X, Bi, ncol, bits, bits + ww, bits + 2 * ww, bits + 3 * ww);
+  if (e != hipSuccess) return e;
+  c->counters.bitplanes(n, int(lay.use_a) + int(lay.use_b));
+  e = launch_tr_phase2<T>(c->L, lay, K0, K1, X, Bi, ncol, bits, bits + ww, bits + 2 * ww, bits + 3 * ww, m, m + n);
+  if (e != hipSuccess) return e;
+  c->counters.msg(n, c->bw);
+  return launch_reconstruct<T>(c->L, n, m, m + n, y);
+}
+
 template <typename T>
 static mpcx_status tr_eval_t(mpcx_ctx *c, int kind, size_t n, const void *k0, const void *k1, const void *x,
                              const void *bias, int ncol, void *y) {
@@ -309,17 +324,11 @@ static mpcx_status tr_eval_t(mpcx_ctx *c, int kind, size_t n, const void *k0, co
   void *sp = nullptr;
   HIPC(c, ctx_scratch(c, 4 * wb + 2 * n * sizeof(T), &sp), "hipMalloc");
   uint64_t *b = static_cast<uint64_t *>(sp);
-  const size_t ww = wb / 8;
-  T *m0 = reinterpret_cast<T *>(b + 4 * ww);
-  T *m1 = m0 + n;
-  const uint8_t *K0 = static_cast<const uint8_t *>(k0), *K1 = static_cast<const uint8_t *>(k1);
-  const T *X = static_cast<const T *>(x), *Bi = static_cast<const T *>(bias);
-  HIPC(c, launch_tr_phase1<T>(c->L, lay, K0, K1, X, Bi, ncol, b, b + ww, b + 2 * ww, b + 3 * ww), "tr_phase1");
-  c->counters.bitplanes(n, int(lay.use_a) + int(lay.use_b));
-  HIPC(c, launch_tr_phase2<T>(c->L, lay, K0, K1, X, Bi, ncol, b, b + ww, b + 2 * ww, b + 3 * ww, m0, m1),
-       "tr_phase2");
-  c->counters.msg(n, c->bw);
-  HIPC(c, launch_reconstruct<T>(c->L, n, m0, m1, static_cast<T *>(y)), "reconstruct");
+  T *m = reinterpret_cast<T *>(b + 4 * (wb / 8));
+  HIPC(c,
+       tr_eval_run<T>(c, lay, n, static_cast<const uint8_t *>(k0), static_cast<const uint8_t *>(k1),
+                      static_cast<const T *>(x), static_cast<const T *>(bias), ncol, static_cast<T *>(y), b, m),
+       "tr_eval");
   HIPC(c, hipStreamSynchronize(c->L.stream), "sync");
   return MPCX_OK;
 }
@@ -331,6 +340,117 @@ mpcx_status mpcx_tr_eval(mpcx_ctx *c, int kind, size_t n, const void *k0, const 
     return fail(c, MPCX_EINVAL, "tr_eval: bad argument");
   return c->bw == 32 ? tr_eval_t<uint32_t>(c, kind, n, k0, k1, x, bias, ncol, y)
                      : tr_eval_t<uint64_t>(c, kind, n, k0, k1, x, bias, ncol, y);
+}
+
+// ---------------- masked max-pool ----------------
+namespace {
+constexpr int kMaxPoolLevels = 32;
+bool maxpool_dims_ok(int B, int N, int C) { return B >= 1 && N >= 1 && C >= 1; }
+// the key of level l: a RELU gate over B * pairs[l] * C differences, back to back
+int maxpool_plan(const mpcx_ctx *c, int B, int N, int C, TrLayout *lay, int *pairs) {
+  const int Lv = pool_levels(N, pairs);
+  size_t o = 0;
+  for (int l = 0; l < Lv; l++) {
+    lay[l] = tr_layout(MPCX_RELU, c->bw, c->s, size_t(B) * pairs[l] * C, o);
+    o = lay[l].end;
+  }
+  return Lv;
+}
+}  // namespace
+
+int mpcx_maxpool_levels(int N) {
+  int pairs[kMaxPoolLevels];
+  return N >= 1 ? pool_levels(N, pairs) : 0;
+}
+
+size_t mpcx_maxpool_key_bytes(mpcx_ctx *c, int B, int N, int C) {
+  if (!c || !maxpool_dims_ok(B, N, C)) return 0;
+  TrLayout lay[kMaxPoolLevels];
+  int pairs[kMaxPoolLevels];
+  const int Lv = maxpool_plan(c, B, N, C, lay, pairs);
+  return Lv ? lay[Lv - 1].end : 0;
+}
+
+// The dealer runs the evaluator's linear steps on the masks: the difference of a
+// pair has mask r_odd - r_even, the ReLU gate returns a fresh output mask r_y,
+// and the pair's maximum has mask r_even + r_y.
+template <typename T>
+static mpcx_status maxpool_keygen_t(mpcx_ctx *c, int B, int N, int C, const void *in_mask, void *out_mask,
+                                    uint64_t seed, uint32_t gate, void *k0, void *k1) {
+  TrLayout lay[kMaxPoolLevels];
+  int pairs[kMaxPoolLevels];
+  const int Lv = maxpool_plan(c, B, N, C, lay, pairs);
+  const size_t rows = size_t(B) * N * C, P0 = Lv ? size_t(B) * pairs[0] * C : 0;
+  void *sp = nullptr;
+  HIPC(c, ctx_scratch(c, (2 * rows + 2 * P0) * sizeof(T), &sp), "hipMalloc");
+  T *va = static_cast<T *>(sp), *vb = va + rows, *dm = vb + rows, *ym = dm + P0;
+  const T *cur = static_cast<const T *>(in_mask);
+  T *nxt = va;
+  uint8_t *K0 = static_cast<uint8_t *>(k0), *K1 = static_cast<uint8_t *>(k1);
+  int R = N;
+  for (int l = 0; l < Lv; l++) {
+    HIPC(c, launch_pool_diff<T>(c->L, B, R, C, cur, dm), "maxpool_keygen");
+    HIPC(c, launch_tr_keygen<T>(c->L, lay[l], seed, gate + uint32_t(l), dm, ym, K0, K1), "maxpool_keygen");
+    HIPC(c, launch_pool_combine<T>(c->L, B, R, C, cur, ym, nullptr, nxt), "maxpool_keygen");
+    cur = nxt;
+    nxt = nxt == va ? vb : va;
+    R = pairs[l] + (R & 1);
+  }
+  HIPC(c, hipMemcpyAsync(out_mask, cur, size_t(B) * C * sizeof(T), hipMemcpyDeviceToDevice, c->L.stream),
+       "maxpool_keygen");
+  HIPC(c, hipStreamSynchronize(c->L.stream), "sync");
+  return MPCX_OK;
+}
+
+mpcx_status mpcx_maxpool_keygen(mpcx_ctx *c, int B, int N, int C, const void *in_mask, void *out_mask, uint64_t seed,
+                                uint32_t gate, void *k0, void *k1) {
+  CHECK_CTX(c);
+  if (!maxpool_dims_ok(B, N, C) || !in_mask || !out_mask || (N > 1 && (!k0 || !k1)))
+    return fail(c, MPCX_EINVAL, "maxpool_keygen: bad argument");
+  return c->bw == 32 ? maxpool_keygen_t<uint32_t>(c, B, N, C, in_mask, out_mask, seed, gate, k0, k1)
+                     : maxpool_keygen_t<uint64_t>(c, B, N, C, in_mask, out_mask, seed, gate, k0, k1);
+}
+
+// Per level: the pair differences (local), one RELU gate (two exchange rounds),
+// and max(a, b) = a + ReLU(b - a) (local), on planes (B, R, C) that shrink to
+// (B, 1, C).
+template <typename T>
+static mpcx_status maxpool_eval_t(mpcx_ctx *c, int B, int N, int C, const void *k0, const void *k1, const void *in,
+                                  void *out) {
+  TrLayout lay[kMaxPoolLevels];
+  int pairs[kMaxPoolLevels];
+  const int Lv = maxpool_plan(c, B, N, C, lay, pairs);
+  const size_t rows = size_t(B) * N * C, P0 = Lv ? size_t(B) * pairs[0] * C : 0;
+  const size_t ww = (P0 + 63) / 64;
+  void *sp = nullptr;
+  HIPC(c, ctx_scratch(c, 4 * ww * 8 + (2 * rows + 4 * P0) * sizeof(T), &sp), "hipMalloc");
+  uint64_t *bits = static_cast<uint64_t *>(sp);
+  T *va = reinterpret_cast<T *>(bits + 4 * ww), *vb = va + rows, *d = vb + rows, *y = d + P0, *m = y + P0;
+  const T *cur = static_cast<const T *>(in);
+  T *nxt = va;
+  const uint8_t *K0 = static_cast<const uint8_t *>(k0), *K1 = static_cast<const uint8_t *>(k1);
+  int R = N;
+  for (int l = 0; l < Lv; l++) {
+    const size_t n = size_t(B) * pairs[l] * C;
+    HIPC(c, launch_pool_diff<T>(c->L, B, R, C, cur, d), "maxpool_eval");
+    HIPC(c, tr_eval_run<T>(c, lay[l], n, K0, K1, d, nullptr, 1, y, bits, m), "maxpool_eval");
+    HIPC(c, launch_pool_combine<T>(c->L, B, R, C, cur, y, nullptr, nxt), "maxpool_eval");
+    cur = nxt;
+    nxt = nxt == va ? vb : va;
+    R = pairs[l] + (R & 1);
+  }
+  HIPC(c, hipMemcpyAsync(out, cur, size_t(B) * C * sizeof(T), hipMemcpyDeviceToDevice, c->L.stream), "maxpool_eval");
+  HIPC(c, hipStreamSynchronize(c->L.stream), "sync");
+  return MPCX_OK;
+}
+
+mpcx_status mpcx_maxpool_eval(mpcx_ctx *c, int B, int N, int C, const void *k0, const void *k1, const void *in,
+                              void *out) {
+  CHECK_CTX(c);
+  if (!maxpool_dims_ok(B, N, C) || !in || !out || (N > 1 && (!k0 || !k1)))
+    return fail(c, MPCX_EINVAL, "maxpool_eval: bad argument");
+  return c->bw == 32 ? maxpool_eval_t<uint32_t>(c, B, N, C, k0, k1, in, out)
+                     : maxpool_eval_t<uint64_t>(c, B, N, C, k0, k1, in, out);
 }
 
 // ---------------- MUL ----------------

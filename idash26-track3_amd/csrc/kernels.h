@@ -162,6 +162,16 @@ hipError_t launch_axpby(const Launch &L, size_t n, T a, const T *x, T b, const T
 template <typename T>
 hipError_t launch_lincomb(const Launch &L, size_t rows, size_t cols, T a, const T *x, T b, const T *y, const T *v,
                           int shift, T *out);
+// Levels of the pairwise max tree over N rows (pairs (2j, 2j+1), an odd last
+// row carried to the next level); pairs[l] = pairs at level l (31 levels at most).
+inline int pool_levels(int N, int *pairs) {
+  int R = N, L = 0;
+  while (R > 1) {
+    pairs[L++] = R / 2;
+    R = R / 2 + (R & 1);
+  }
+  return L;
+}
 // pool prep: V[r*C+c] = H[r*C+c] + S*m[r] + off
 template <typename T>
 hipError_t launch_pool_prep(const Launch &L, size_t rows, int C, const T *H, const T *m, T S, T off, T *V);

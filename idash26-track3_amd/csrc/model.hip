@@ -72,15 +72,6 @@ struct Cursor {
 
 inline size_t pairs_of(int N) { return size_t(N) * (N + 1) / 2; }
 
-int pool_levels(int N, int *pairs) {
-  int R = N, L = 0;
-  while (R > 1) {
-    pairs[L++] = R / 2;
-    R = R / 2 + (R & 1);
-  }
-  return L;
-}
-
 template <typename T>
 struct DevBuf {
   T *p = nullptr;

@@ -43,6 +43,12 @@ _SIGS = {
                                   C.c_uint32, C.c_void_p, C.c_void_p]),
     "mpcx_dcf_eval": (C.c_int, [C.c_void_p, C.c_int, C.c_int, C.c_size_t, C.c_void_p, C.c_void_p,
                                 C.c_void_p]),
+    "mpcx_maxpool_levels": (C.c_int, [C.c_int]),
+    "mpcx_maxpool_key_bytes": (C.c_size_t, [C.c_void_p, C.c_int, C.c_int, C.c_int]),
+    "mpcx_maxpool_keygen": (C.c_int, [C.c_void_p, C.c_int, C.c_int, C.c_int, C.c_void_p, C.c_void_p, C.c_uint64,
+                                      C.c_uint32, C.c_void_p, C.c_void_p]),
+    "mpcx_maxpool_eval": (C.c_int, [C.c_void_p, C.c_int, C.c_int, C.c_int, C.c_void_p, C.c_void_p, C.c_void_p,
+                                    C.c_void_p]),
     "mpcx_tr_key_bytes": (C.c_size_t, [C.c_void_p, C.c_int, C.c_size_t]),
     "mpcx_tr_keygen": (C.c_int, [C.c_void_p, C.c_int, C.c_size_t, C.c_void_p, C.c_void_p, C.c_uint64,
                                  C.c_uint32, C.c_void_p, C.c_void_p]),
@@ -267,6 +273,24 @@ class Ctx:
         self.check(self.lib.mpcx_tr_eval(self.h, kind, n, dptr(k0), dptr(k1), dptr(dx), dptr(db), ncol, dptr(out)),
                    "tr_eval")
         return from_dev(out, self.T, n)
+
+    def maxpool_keygen(self, B, N, C, in_mask, seed=1, gate=1):
+        in_mask = self.ring(in_mask)
+        nb = self.lib.mpcx_maxpool_key_bytes(self.h, B, N, C)
+        k0, k1 = empty_dev(nb), empty_dev(nb)
+        dm = to_dev(in_mask)
+        out = empty_dev(B * C * in_mask.itemsize)
+        self.check(self.lib.mpcx_maxpool_keygen(self.h, B, N, C, dptr(dm), dptr(out), seed, gate, dptr(k0),
+                                                dptr(k1)), "maxpool_keygen")
+        return k0, k1, from_dev(out, self.T, B * C)
+
+    def maxpool_eval(self, B, N, C, k0, k1, xhat):
+        xhat = self.ring(xhat)
+        dx = to_dev(xhat)
+        out = empty_dev(B * C * xhat.itemsize)
+        self.check(self.lib.mpcx_maxpool_eval(self.h, B, N, C, dptr(k0), dptr(k1), dptr(dx), dptr(out)),
+                   "maxpool_eval")
+        return from_dev(out, self.T, B * C)
 
     def mul_keygen(self, rx, ry, ia, ib, seed=1, gate=1):
         rx, ry = self.ring(rx), self.ring(ry)

@@ -114,6 +114,25 @@ mpcx_status mpcx_tr_eval(mpcx_ctx *ctx, int kind, size_t n, const void *d_key0,
                          const void *d_key1, const void *d_xhat, const void *d_bias, int ncol,
                          void *d_yhat);
 
+/* ---------------- masked global max-pool ----------------
+ * Replaces MaskedMaxPoolLayer<T>(B, Nmax, F)::_forward
+ * (gpu_mpc/masked_maxpool_layer.h:47-165; MaskedGlobalMaxPool for B = 1,
+ * gpu_mpc/masked_maxpool.h:62-84): input (B*N, C) masked-public, sample-major
+ * (the reference's input is already H (.) mask), output (B, C): per sample and
+ * channel the maximum over the N rows, as the reference's tree — pairs of rows
+ * (2j, 2j+1), max(a, b) = a + ReLU(b - a), an odd last row carried to the next
+ * level — over mpcx_maxpool_levels(N) = ceil(log2 N) levels, two exchange
+ * rounds each.  Exact while every pairwise difference lies in the signed ring.
+ * Keygen uses the gate ids gate .. gate + levels - 1; with N = 1 there is no key
+ * (key pointers may be NULL) and the output is the input. */
+int mpcx_maxpool_levels(int N);
+size_t mpcx_maxpool_key_bytes(mpcx_ctx *ctx, int B, int N, int C);
+mpcx_status mpcx_maxpool_keygen(mpcx_ctx *ctx, int B, int N, int C, const void *d_in_mask,
+                                void *d_out_mask, uint64_t seed, uint32_t gate, void *d_key0,
+                                void *d_key1);
+mpcx_status mpcx_maxpool_eval(mpcx_ctx *ctx, int B, int N, int C, const void *d_key0,
+                              const void *d_key1, const void *d_xhat, void *d_yhat);
+
 /* ---------------- Beaver product ----------------
  * z[i] = x[ia[i]] * y[ib[i]] on masked operands (index maps allow the
  * broadcast/outer products of the adjacency normalisation).  Replaces

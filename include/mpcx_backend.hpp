@@ -151,6 +151,24 @@ class SecureBackend {
     gate(MPCX_RELU, in, out, nullptr, 0);
   }
 
+  // ---- masked global max-pool (MaskedMaxPoolLayer<T>(B, Nmax, F)::_forward,
+  // masked_maxpool_layer.h:47-165): in (B*N, C) sample-major -> out (B, C), a
+  // tree of max(a, b) = a + ReLU(b - a), two rounds per level ----
+  template <class TI, class TO>
+  void maxpool(const TI &in, TO &out, int B, int N, int C) {
+    if (in.size() != size_t(B) * N * C) throw std::invalid_argument("maxpool: input is not (B*N, C)");
+    ensure(out, size_t(B) * C);
+    const size_t kb = mpcx_maxpool_key_bytes(ctx_, B, N, C);
+    uint8_t *k0, *k1;
+    take(kb, &k0, &k1);
+    if (dealer()) {
+      check(mpcx_maxpool_keygen(ctx_, B, N, C, in.d_data, out.d_data, seed_, gate_, k0, k1));
+      gate_ += uint32_t(mpcx_maxpool_levels(N));
+    } else {
+      check(mpcx_maxpool_eval(ctx_, B, N, C, k0, k1, in.d_data, out.d_data));
+    }
+  }
+
   // ---- exact truncation by the scale (ddg_orca.h:112-123, TrFloor) ----
   template <class TI>
   void truncateForward(TI &in, uint64_t shift, uint8_t /*mode*/ = 0) {

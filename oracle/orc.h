@@ -237,6 +237,17 @@ int orc_adjnorm_keygen(int bw, int s, int B, int N, uint64_t seed, uint64_t *out
 int orc_adjnorm_eval(int bw, int s, int B, int N, int nmax, const uint8_t *k0, const uint8_t *k1,
                      const uint64_t *a0, const uint64_t *a1, uint64_t *out_masked, uint64_t *bytes);
 
+/* Standalone masked global max-pool (gpu_mpc/masked_maxpool_layer.h:47-165):
+ * masked-public (B*N x C, sample-major) -> (B x C) maximum over the N rows, a
+ * tree of max(a, b) = a + ReLU(b - a) over pairs (2j, 2j+1), the odd last row
+ * carried; keys of the levels back to back from base, gate ids gate, gate+1, ... */
+size_t orc_maxpool_layout(int bw, int s, int B, int N, int C, size_t base);
+void orc_maxpool_keygen(uint64_t seed, uint32_t gate, int bw, int s, int B, int N, int C,
+                        const uint64_t *in_mask, uint64_t *out_mask, uint8_t *k0, uint8_t *k1,
+                        size_t base);
+void orc_maxpool_eval(int bw, int s, int B, int N, int C, const uint8_t *k0, const uint8_t *k1,
+                      size_t base, const uint64_t *xhat, uint64_t *yhat, uint64_t *bytes);
+
 /* Optional trace of reconstructed masked values (for debugging parity):
  * when set, each gate's public output is copied to the callback. */
 typedef void (*orc_trace_fn)(uint32_t gate, size_t n, const uint64_t *vals);

@@ -106,6 +106,9 @@ def lib():
             "orc_adjnorm_key_bytes": (sz, [i, i, i, i]),
             "orc_adjnorm_keygen": (i, [i, i, i, i, u64, P, P, P]),
             "orc_adjnorm_eval": (i, [i, i, i, i, i, P, P, P, P, P, P]),
+            "orc_maxpool_layout": (sz, [i, i, i, i, i, sz]),
+            "orc_maxpool_keygen": (None, [u64, u32, i, i, i, i, i, P, P, P, P, sz]),
+            "orc_maxpool_eval": (None, [i, i, i, i, i, P, P, sz, P, P, P]),
             "orc_set_threads": (None, [i]),
             "orc_get_threads": (i, []),
         }
@@ -371,6 +374,24 @@ def adjnorm_eval(bw, s, B, N, nmax, k0, k1, a0, a1):
     by = np.zeros(1, np.uint64)
     lib().orc_adjnorm_eval(bw, s, B, N, nmax, ptr(k0), ptr(k1), ptr(a0), ptr(a1), ptr(out), ptr(by))
     return out, int(by[0])
+
+
+def maxpool_keygen(seed, gate, bw, s, B, N, C, in_mask):
+    in_mask = _u64(in_mask)
+    n = lib().orc_maxpool_layout(bw, s, B, N, C, 0)
+    k0 = np.zeros(n, np.uint8)
+    k1 = np.zeros(n, np.uint8)
+    out_mask = np.zeros(B * C, np.uint64)
+    lib().orc_maxpool_keygen(seed, gate, bw, s, B, N, C, ptr(in_mask), ptr(out_mask), ptr(k0), ptr(k1), 0)
+    return k0, k1, out_mask
+
+
+def maxpool_eval(bw, s, B, N, C, k0, k1, xhat):
+    xhat = _u64(xhat)
+    y = np.zeros(B * C, np.uint64)
+    by = np.zeros(1, np.uint64)
+    lib().orc_maxpool_eval(bw, s, B, N, C, ptr(k0), ptr(k1), 0, ptr(xhat), ptr(y), ptr(by))
+    return y, int(by[0])
 
 
 def set_threads(n):

@@ -313,6 +313,108 @@ static void build_maps(int B, int N, uint32_t *oa, uint32_t *ob, uint32_t *wa, u
   }
 }
 
+/* Masked global max-pool tree, shared by the model and the standalone entry
+ * points (gpu_mpc/masked_maxpool_layer.h:47-165): planes V (B x R x C,
+ * sample-major, masked-public) shrink to (B x 1 x C).  Per level the pair
+ * differences V[2j+1] - V[2j] (:91-112), one RELU gate (:114-118) and
+ * V[2j] + ReLU(.) (:120-124), the odd last row carried forward (:140-147).
+ * The dealer runs the same linear steps on the masks.  V is overwritten (its
+ * first B*C words hold the result); t1, t2: scratch of B*N*C words. */
+static size_t pool_keygen_blk(uint64_t seed, uint32_t *g, int bw, int s, int B, int N, int C, uint64_t *rV,
+                              uint64_t *t1, uint64_t *t2, uint8_t *k0, uint8_t *k1, size_t o) {
+  const uint64_t M = rmask(bw);
+  int pairs[32];
+  int L = pool_levels(N, pairs), R = N;
+  for (int l = 0; l < L; l++) {
+    int pr = pairs[l];
+    size_t E = (size_t)B * pr * C;
+    for (int b = 0; b < B; b++)
+      for (int j = 0; j < pr; j++)
+        for (int c = 0; c < C; c++)
+          t1[((size_t)b * pr + j) * C + c] =
+              (rV[((size_t)b * R + 2 * j + 1) * C + c] - rV[((size_t)b * R + 2 * j) * C + c]) & M;
+    orc_tr_keygen(seed, (*g)++, ORC_G_RELU, bw, s, E, t1, t2, k0, k1, o);
+    o = orc_tr_layout_make(ORC_G_RELU, bw, s, E, o).end;
+    int Rn = pr + (R & 1);
+    for (int b = 0; b < B; b++) {
+      for (int j = 0; j < pr; j++)
+        for (int c = 0; c < C; c++)
+          t1[((size_t)b * Rn + j) * C + c] =
+              (rV[((size_t)b * R + 2 * j) * C + c] + t2[((size_t)b * pr + j) * C + c]) & M;
+      if (R & 1)
+        for (int c = 0; c < C; c++)
+          t1[((size_t)b * Rn + pr) * C + c] = rV[((size_t)b * R + R - 1) * C + c];
+    }
+    memcpy(rV, t1, 8 * (size_t)B * Rn * C);
+    R = Rn;
+  }
+  return o;
+}
+
+static size_t pool_eval_blk(uint32_t *g, int bw, int s, int B, int N, int C, const uint8_t *k0, const uint8_t *k1,
+                            size_t o, uint64_t *V, uint64_t *t1, uint64_t *t2, uint64_t *bytes) {
+  const uint64_t M = rmask(bw);
+  int pairs[32];
+  int L = pool_levels(N, pairs), R = N;
+  for (int l = 0; l < L; l++) {
+    int pr = pairs[l];
+    size_t E = (size_t)B * pr * C;
+    for (int b = 0; b < B; b++)
+      for (int j = 0; j < pr; j++)
+        for (int c = 0; c < C; c++)
+          t1[((size_t)b * pr + j) * C + c] =
+              (V[((size_t)b * R + 2 * j + 1) * C + c] - V[((size_t)b * R + 2 * j) * C + c]) & M;
+    orc_tr_eval(ORC_G_RELU, bw, s, E, k0, k1, o, t1, NULL, t2, bytes);
+    trace((*g)++, E, t2);
+    o = orc_tr_layout_make(ORC_G_RELU, bw, s, E, o).end;
+    int Rn = pr + (R & 1);
+    for (int b = 0; b < B; b++) {
+      for (int j = 0; j < pr; j++)
+        for (int c = 0; c < C; c++)
+          t1[((size_t)b * Rn + j) * C + c] =
+              (V[((size_t)b * R + 2 * j) * C + c] + t2[((size_t)b * pr + j) * C + c]) & M;
+      if (R & 1)
+        for (int c = 0; c < C; c++)
+          t1[((size_t)b * Rn + pr) * C + c] = V[((size_t)b * R + R - 1) * C + c];
+    }
+    memcpy(V, t1, 8 * (size_t)B * Rn * C);
+    R = Rn;
+  }
+  return o;
+}
+
+size_t orc_maxpool_layout(int bw, int s, int B, int N, int C, size_t base) {
+  int pairs[32];
+  int L = pool_levels(N, pairs);
+  for (int l = 0; l < L; l++) base = orc_tr_layout_make(ORC_G_RELU, bw, s, (size_t)B * pairs[l] * C, base).end;
+  return base;
+}
+
+void orc_maxpool_keygen(uint64_t seed, uint32_t gate, int bw, int s, int B, int N, int C, const uint64_t *in_mask,
+                        uint64_t *out_mask, uint8_t *k0, uint8_t *k1, size_t base) {
+  const size_t n = (size_t)B * N * C;
+  uint64_t *rV = (uint64_t *)malloc(8 * n), *t1 = (uint64_t *)malloc(8 * n), *t2 = (uint64_t *)malloc(8 * n);
+  memcpy(rV, in_mask, 8 * n);
+  pool_keygen_blk(seed, &gate, bw, s, B, N, C, rV, t1, t2, k0, k1, base);
+  memcpy(out_mask, rV, 8 * (size_t)B * C);
+  free(rV);
+  free(t1);
+  free(t2);
+}
+
+void orc_maxpool_eval(int bw, int s, int B, int N, int C, const uint8_t *k0, const uint8_t *k1, size_t base,
+                      const uint64_t *xhat, uint64_t *yhat, uint64_t *bytes) {
+  const size_t n = (size_t)B * N * C;
+  uint64_t *V = (uint64_t *)malloc(8 * n), *t1 = (uint64_t *)malloc(8 * n), *t2 = (uint64_t *)malloc(8 * n);
+  uint32_t g = 0;
+  memcpy(V, xhat, 8 * n);
+  pool_eval_blk(&g, bw, s, B, N, C, k0, k1, base, V, t1, t2, bytes);
+  memcpy(yhat, V, 8 * (size_t)B * C);
+  free(V);
+  free(t1);
+  free(t2);
+}
+
 /* Secure adjacency normalisation block, shared by the model and the standalone
  * entry points (gpu_mpc/secure_adj_norm.h:203-374 keygen, :393-659 eval):
  *   reveal A; reveal the degrees (row sums of the A shares, :421-493);
@@ -530,31 +632,7 @@ int orc_model_keygen(const orc_dims *d, int B, uint64_t seed, const int64_t *W, 
   const uint64_t Sm = 1ull << (bw - 2 - d->mask_scale);
   for (size_t r = 0; r < BN; r++)
     for (int c = 0; c < C; c++) rX[r * C + c] = (rX[r * C + c] + Sm * rm[r]) & M;
-  int pairs[32];
-  int L = pool_levels(N, pairs), R = N;
-  for (int l = 0; l < L; l++) {
-    int pr = pairs[l];
-    size_t E = (size_t)B * pr * C;
-    for (int b = 0; b < B; b++)
-      for (int j = 0; j < pr; j++)
-        for (int c = 0; c < C; c++)
-          t1[((size_t)b * pr + j) * C + c] =
-              (rX[((size_t)b * R + 2 * j + 1) * C + c] - rX[((size_t)b * R + 2 * j) * C + c]) & M;
-    orc_tr_keygen(seed, g++, ORC_G_RELU, bw, s, E, t1, t2, k0, k1, o);
-    o = orc_tr_layout_make(ORC_G_RELU, bw, s, E, o).end;
-    int Rn = pr + (R & 1);
-    for (int b = 0; b < B; b++) {
-      for (int j = 0; j < pr; j++)
-        for (int c = 0; c < C; c++)
-          t1[((size_t)b * Rn + j) * C + c] =
-              (rX[((size_t)b * R + 2 * j) * C + c] + t2[((size_t)b * pr + j) * C + c]) & M;
-      if (R & 1)
-        for (int c = 0; c < C; c++)
-          t1[((size_t)b * Rn + pr) * C + c] = rX[((size_t)b * R + R - 1) * C + c];
-    }
-    memcpy(rX, t1, 8 * (size_t)B * Rn * C);
-    R = Rn;
-  }
+  o = pool_keygen_blk(seed, &g, bw, s, B, N, C, rX, t1, t2, k0, k1, o);
   /* drug FCs on the pooled (B x C) mask in rX */
   pub_gemm(bw, (size_t)B, C, d->dfc[0], rX, W + layer_off(d, 3), t1);
   orc_tr_keygen(seed, g++, ORC_G_TRRELU, bw, s, (size_t)B * d->dfc[0], t1, t2, k0, k1, o);
@@ -665,32 +743,7 @@ int orc_model_eval(const orc_dims *d, int B, const int64_t *W, const uint8_t *k0
   const uint64_t S = 1ull << (bw - 2), Sm = 1ull << (bw - 2 - d->mask_scale);
   for (size_t r = 0; r < BN; r++)
     for (int c = 0; c < C; c++) H[r * C + c] = (H[r * C + c] + Sm * mh[r] - S) & M;
-  int pairs[32];
-  int L = pool_levels(N, pairs), R = N;
-  for (int l = 0; l < L; l++) {
-    int pr = pairs[l];
-    size_t E = (size_t)B * pr * C;
-    for (int b = 0; b < B; b++)
-      for (int j = 0; j < pr; j++)
-        for (int c = 0; c < C; c++)
-          t1[((size_t)b * pr + j) * C + c] =
-              (H[((size_t)b * R + 2 * j + 1) * C + c] - H[((size_t)b * R + 2 * j) * C + c]) & M;
-    orc_tr_eval(ORC_G_RELU, bw, s, E, k0, k1, o, t1, NULL, t2, &by);
-    trace(g++, E, t2);
-    o = orc_tr_layout_make(ORC_G_RELU, bw, s, E, o).end;
-    int Rn = pr + (R & 1);
-    for (int b = 0; b < B; b++) {
-      for (int j = 0; j < pr; j++)
-        for (int c = 0; c < C; c++)
-          t1[((size_t)b * Rn + j) * C + c] =
-              (H[((size_t)b * R + 2 * j) * C + c] + t2[((size_t)b * pr + j) * C + c]) & M;
-      if (R & 1)
-        for (int c = 0; c < C; c++)
-          t1[((size_t)b * Rn + pr) * C + c] = H[((size_t)b * R + R - 1) * C + c];
-    }
-    memcpy(H, t1, 8 * (size_t)B * Rn * C);
-    R = Rn;
-  }
+  o = pool_eval_blk(&g, bw, s, B, N, C, k0, k1, o, H, t1, t2, &by);
   {
     const int64_t *Wt = W + layer_off(d, 3);
     const int64_t *bias = Wt + (size_t)C * d->dfc[0];

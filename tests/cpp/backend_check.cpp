@@ -2,7 +2,8 @@
 // an evaluator pass of a small network and compares the reconstructed outputs
 // with exact integer arithmetic on the host:
 //   h = reveal(x);  z = h . W + b (bias at scale 2s);  truncateForward(z);
-//   y = relu(z);  u = 3y - y (= 2y, local ops);  v = u (.) y;  output(v) -> floor(v / 2^s)
+//   y = relu(z);  u = 3y - y (= 2y, local ops);  v = u (.) y;  output(v) -> floor(v / 2^s);
+//   p = maxpool of y over its M rows (one sample, N channels);  output(p) -> floor(p / 2^s)
 // Usage: backend_check <bw: 32|64>.  Exit status 0 on success.
 #include <cstdio>
 #include <cstdlib>
@@ -28,13 +29,14 @@ static int run(int bw) {
   for (auto &v : W) v = uni(-(1 << s), 1 << s) / 16;
   for (auto &v : b) v = uni(-(1 << s), 1 << s) / 2;
   // plaintext reference
-  std::vector<int64_t> want(size_t(M) * N);
+  std::vector<int64_t> want(size_t(M) * N), ymax(N, 0);
   for (int i = 0; i < M; i++)
     for (int j = 0; j < N; j++) {
       __int128 acc = 0;
       for (int k = 0; k < K; k++) acc += __int128(x[size_t(i) * K + k]) * W[size_t(k) * N + j];
       int64_t z = int64_t((acc + (__int128(b[j]) << s)) >> s);
       int64_t y = z > 0 ? z : 0;
+      ymax[j] = y > ymax[j] ? y : ymax[j];
       int64_t u = 2 * y;
       want[size_t(i) * N + j] = int64_t((__int128(u) * y) >> s);
     }
@@ -60,7 +62,7 @@ static int run(int bw) {
   arena.capacity = size_t(64) << 20;
   for (int p = 0; p < 2; p++) (void)hipMalloc(&arena.d_key[p], arena.capacity);
 
-  std::vector<int64_t> got(size_t(M) * N);
+  std::vector<int64_t> got(size_t(M) * N), gotp(N);
   for (int pass = 0; pass < 2; pass++) {
     const bool dealer = pass == 0;
     arena.offset = 0;
@@ -69,6 +71,7 @@ static int run(int bw) {
                               &arena, 4242);
     Tn h{nullptr, size_t(M), size_t(K)}, z{nullptr, size_t(M), size_t(N)}, y{nullptr, size_t(M), size_t(N)};
     Tn t3{nullptr, size_t(M), size_t(N)}, u{nullptr, size_t(M), size_t(N)}, v{nullptr, size_t(M), size_t(N)};
+    Tn pl{nullptr, 1, size_t(N)};
     be.reveal(X0, X1, h);
     be.matmul(h, Wt, z, true, Bt, true);
     be.truncateForward(z, s);
@@ -77,16 +80,22 @@ static int run(int bw) {
     be.sub(t3, y, u);
     be.mul(u, y, v);
     be.output(v, dealer ? nullptr : got.data());
+    be.maxpool(y, pl, 1, M, N);
+    be.output(pl, dealer ? nullptr : gotp.data());
     std::printf("bw=%d %s pass: %zu key bytes per party\n", bw, dealer ? "dealer" : "evaluator", arena.offset);
   }
   int bad = 0;
   for (size_t i = 0; i < got.size(); i++)
     if (got[i] != want[i] && bad++ < 5)
       std::fprintf(stderr, "mismatch at %zu: got %lld want %lld\n", i, (long long)got[i], (long long)want[i]);
+  for (int j = 0; j < N; j++)
+    if (gotp[j] != (ymax[j] >> s) && bad++ < 5)
+      std::fprintf(stderr, "pool mismatch at %d: got %lld want %lld\n", j, (long long)gotp[j],
+                   (long long)(ymax[j] >> s));
   for (Tn *t : {&X0, &X1, &Wt, &Bt}) (void)hipFree(t->d_data);
   for (int p = 0; p < 2; p++) (void)hipFree(arena.d_key[p]);
   mpcx_destroy(ctx);
-  std::printf("bw=%d: %s (%zu outputs)\n", bw, bad ? "MISMATCH" : "bit-exact", got.size());
+  std::printf("bw=%d: %s (%zu outputs, %d pooled)\n", bw, bad ? "MISMATCH" : "bit-exact", got.size(), N);
   return bad ? 1 : 0;
 }
 

@@ -1,8 +1,8 @@
 """The header-only sytorch-style backend (include/mpcx_backend.hpp), driven
 from C++ (tests/cpp/backend_check.cpp): a dealer pass writes the keys of a
 small network (reveal, matmul with public weights + bias, truncation, ReLU,
-local linear ops, Beaver product, output), an evaluator pass consumes them,
-and the outputs are compared with exact host integer arithmetic."""
+local linear ops, Beaver product, masked max-pool, output), an evaluator pass
+consumes them, and the outputs are compared with exact host integer arithmetic."""
 import os
 import subprocess
 

@@ -542,6 +542,50 @@ def test_model_forward_on_oracle_keys_config0(mp, orc, synth):
     c.close()
 
 
+@pytest.mark.parametrize("B,N,C", [(1, 1, 3), (3, 7, 4), (2, 140, 6), (4, 2, 33)])
+def test_maxpool_keys_and_eval(ctx, orc, B, N, C):
+    """Standalone masked max-pool (MaskedMaxPoolLayer, masked_maxpool_layer.h:47-165):
+    keys byte-identical to the oracle dealer's, outputs and exchanged bytes
+    identical to the oracle's, unmasked output = max over the rows."""
+    bw = ctx.bw
+    rng = np.random.default_rng(bw + N)
+    q = 1 << (bw - 2)
+    v = rng.integers(-q, q, size=(B, N, C), dtype=np.int64)
+    v[:, :, 0] = rng.integers(-2, 2, size=(B, N))
+    rin = rmask(rng, v.size, bw)
+    g0, g1, grout = ctx.maxpool_keygen(B, N, C, rin, seed=3, gate=40)
+    o0, o1, orout = orc.maxpool_keygen(3, 40, bw, S, B, N, C, rin)
+    assert ctx.lib.mpcx_maxpool_key_bytes(ctx.h, B, N, C) == o0.size
+    assert ctx.lib.mpcx_maxpool_levels(N) == (int(np.ceil(np.log2(N))) if N > 1 else 0)
+    assert np.array_equal(grout.astype(np.uint64), orout)
+    assert np.array_equal(host(g0)[:o0.size], o0) and np.array_equal(host(g1)[:o1.size], o1)
+    xhat = (v.reshape(-1).astype(np.uint64) + rin) & M(bw)
+    ctx.reset_counters()
+    y = ctx.maxpool_eval(B, N, C, g0, g1, xhat)
+    by = ctx.bytes_exchanged
+    oy, oby = orc.maxpool_eval(bw, S, B, N, C, o0, o1, xhat)
+    assert np.array_equal(y.astype(np.uint64), oy)
+    assert by == oby
+    assert np.array_equal(signed(y.astype(np.uint64) - orout, bw).reshape(B, C), v.max(axis=1))
+
+
+def test_maxpool_affinity_pool_shape(mp):
+    """The affinity forward's pool at full size (B=64 molecules x 140 atoms x 312
+    channels, bw=32, 8 levels): non-negative activations with zeroed padding rows
+    (the reference's H (.) mask input), against numpy's max."""
+    c = mp.Ctx(bw=32)
+    rng = np.random.default_rng(5)
+    B, N, C = 64, 140, 312
+    v = rng.integers(0, 1 << 24, size=(B, N, C), dtype=np.int64)
+    real = rng.integers(10, 61, size=B)
+    v[np.arange(N)[None, :] >= real[:, None]] = 0
+    rin = rmask(rng, v.size, 32)
+    k0, k1, rout = c.maxpool_keygen(B, N, C, rin, seed=8, gate=1)
+    y = c.maxpool_eval(B, N, C, k0, k1, (v.reshape(-1).astype(np.uint64) + rin) & M(32))
+    assert np.array_equal(signed(y.astype(np.uint64) - rout.astype(np.uint64), 32).reshape(B, C), v.max(axis=1))
+    c.close()
+
+
 def test_relu_microbench_slice(mp):
     """Config 1 shape at 2^20 elements: ReLU of uniform fixed-point values in
     [-8, 8), reconstructed against max(x, 0)."""

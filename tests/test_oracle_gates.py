@@ -180,3 +180,59 @@ def test_gate_keys_deterministic_and_seed_dependent(orc):
     c0, _, rc = orc.tr_keygen(2, 2, 2, 32, S, rin)
     assert np.array_equal(a0, b0) and np.array_equal(a1, b1) and np.array_equal(ra, rb)
     assert not np.array_equal(a0, c0) and not np.array_equal(ra, rc)
+
+
+@pytest.mark.parametrize("bw", [32, 64])
+@pytest.mark.parametrize("B,N,C", [(1, 1, 3), (2, 2, 5), (3, 7, 4), (2, 140, 6), (1, 33, 1)])
+def test_maxpool_tree(orc, bw, B, N, C):
+    """Masked global max-pool (gpu_mpc/masked_maxpool_layer.h:47-165): the
+    reconstructed, unmasked output is the maximum over the N rows of every
+    (sample, channel), for signed values whose pairwise differences stay in the
+    ring (|v| < 2^(bw-2)); ties, one row and odd levels included."""
+    rng = np.random.default_rng(bw + 7 * N + C)
+    q = 1 << (bw - 2)
+    v = rng.integers(-q, q, size=(B, N, C), dtype=np.int64)
+    v[:, :, 0] = rng.integers(-3, 3, size=(B, N))  # many ties
+    if N > 2:
+        v[0, N - 1, :] = q - 1  # the carried odd row holds the maximum
+        v[B - 1, 1, :] = -q     # the ring's lower edge
+    rin = mask_in(rng, v.size, bw)
+    k0, k1, rout = orc.maxpool_keygen(3, 40, bw, S, B, N, C, rin)
+    levels = int(np.ceil(np.log2(N))) if N > 1 else 0
+    assert k0.size == orc.lib().orc_maxpool_layout(bw, S, B, N, C, 0)
+    assert (k0.size == 0) == (levels == 0)
+    xhat = (ring(v.reshape(-1), bw) + rin) & np.uint64(mod(bw) if bw < 64 else 0xFFFFFFFFFFFFFFFF)
+    y, by = orc.maxpool_eval(bw, S, B, N, C, k0, k1, xhat)
+    got = to_signed(y - rout, bw).reshape(B, C)
+    assert np.array_equal(got, v.max(axis=1))
+    # every level is one RELU gate over B * pairs * C differences
+    want_bytes = 0
+    R = N
+    while R > 1:
+        n = B * (R // 2) * C
+        want_bytes += 2 * ((n + 31) // 32) * 4 + 2 * n * (bw // 8)
+        R = R // 2 + (R & 1)
+    assert by == want_bytes
+
+
+def test_maxpool_keys_are_the_relu_gates(orc):
+    """The pool's key is the sequence of the RELU gates of its levels: level l
+    keyed under gate id gate + l on the mask differences r[2j+1] - r[2j]."""
+    bw, B, N, C = 32, 2, 5, 3
+    rng = np.random.default_rng(1)
+    rin = mask_in(rng, B * N * C, bw)
+    k0, k1, rout = orc.maxpool_keygen(9, 100, bw, S, B, N, C, rin)
+    r = rin.reshape(B, N, C).astype(np.uint64)
+    m = np.uint64(mod(bw))
+    off, gate = 0, 100
+    while r.shape[1] > 1:
+        R = r.shape[1]
+        d = ((r[:, 1:R - R % 2:2] - r[:, 0:R - R % 2:2]) & m).reshape(-1)
+        g0, g1, gout = orc.tr_keygen(9, gate, 3, bw, S, d)
+        assert np.array_equal(k0[off:off + g0.size], g0) and np.array_equal(k1[off:off + g1.size], g1)
+        off += g0.size
+        gate += 1
+        nxt = (r[:, 0:R - R % 2:2] + gout.reshape(B, R // 2, C)) & m
+        r = np.concatenate([nxt, r[:, R - 1:R]], axis=1) if R % 2 else nxt
+    assert off == k0.size
+    assert np.array_equal(r.reshape(-1), rout)
