@@ -36,6 +36,9 @@ GEMM_PEAK_TMACS = {"mfma": 5.0e3 / 2 / 16, "valu": VALU_PEAK_TOPS / 2}
 # The summary is profiles/k_tr_phase1_affinity_bw32_B64.md.
 TRAFFIC_BYTES_PER_LAUNCH = {("perm64_b512", 64, 32, 3, 0): 229638822,
                             ("perm64_b512", 64, 32, 1, 0): 689753000}
+SLACK_DESC = {1: ", GCN products H.W^T truncated with the slack gate",
+              2: ", GCN products and aggregations truncated with the slack gate",
+              3: ", every layer truncation local (LocalARS, the reference's default truncation; not bit-exact)"}
 VALU_OPS_PER_AES = {"perm64_b512": 402, "perm64_b1024": 402, "t4_rep32_b1024": 462}
 
 
@@ -56,10 +59,11 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--aes-variant", type=int, default=-1)
     ap.add_argument("--lanes", type=int, default=3, help="concurrent sub-batches, each on its own stream")
-    ap.add_argument("--slack", type=int, default=0, choices=(0, 1, 2),
+    ap.add_argument("--slack", type=int, default=0, choices=(0, 1, 2, 3),
                     help="slack truncations of the GCN (exact while the values lie in half the signed ring): "
                          "0 none (exact truncation over the whole ring), 1 the products H.W^T, 2 also the "
-                         "aggregation A.XW + bias (then a small-domain ReLU)")
+                         "aggregation A.XW + bias (then a small-domain ReLU); 3 every layer truncation local "
+                         "(LocalARS, the reference's default; not bit-exact, bw=64 only in practice)")
     ap.add_argument("--xw-slack", action="store_true", help="same as --slack 1")
     ap.add_argument("--workload", choices=("affinity", "relu", "adjnorm"), default="affinity",
                     help="affinity: the secure forward (default); relu: secure ReLU over --n elements (bw=32); "
@@ -163,9 +167,7 @@ def main():
         "config": {"workload": f"two-party secure affinity forward, bw={args.bw} s=12, B={B} molecules x "
                                f"{dims.n_nodes} atoms, GCN 78-78-156-312, FC 312-1024-128, fusion 256-1024-512-1, "
                                f"FSS keys resident in HBM, {args.lanes} concurrent sub-batches"
-                               + ({1: ", GCN products H.W^T truncated with the slack gate",
-                                   2: ", GCN products and aggregations truncated with the slack gate"}
-                                  .get(args.slack, "")),
+                               + SLACK_DESC.get(args.slack, ""),
                    "B": B, "n_nodes": dims.n_nodes, "bw": args.bw, "scale": dims.s, "lanes": args.lanes,
                    "slack": args.slack},
         "dcf_evals_per_s": round(dcf_evals_per_s, 1),
@@ -229,19 +231,22 @@ def main():
                            slack=d.slack)
         want, code = orc.plain_forward(od, wl.X, wl.A, wl.mask, wl.prot, wl.W)
         result["bit_exact"] = bool(code == 0 and np.array_equal(want, out))
+        if code == 0:  # outputs in units of 2^-s (0 unless the truncation is local)
+            result["max_abs_err_lsb"] = int(np.max(np.abs(out.astype(np.int64) - want)))
         if not args.no_cpu:
             nb = min(args.cpu_samples, B)
             sl = synth.workload(nb, dims, seed=args.seed)  # same generator, first nb molecules
             k0, k1 = orc.model_keygen(od, nb, 99, sl.W)
             sh = sl.shares
             cwant, _ = orc.plain_forward(od, sl.X, sl.A, sl.mask, sl.prot, sl.W)
-            reps, ct, exact = 0, 0.0, True
+            reps, ct, exact, cerr = 0, 0.0, True, 0
             while ct < args.cpu_seconds or reps == 0:
                 t0 = time.perf_counter()
                 cout, _ = orc.model_eval(od, nb, sl.W, k0, k1, *sh["x"], *sh["a"], *sh["m"], sl.prot)
                 ct += time.perf_counter() - t0
                 reps += 1
                 exact = exact and bool(np.array_equal(cout, cwant))
+                cerr = max(cerr, int(np.max(np.abs(cout - cwant))))
             result["cpu_baseline"] = {
                 "value": round(nb * reps / ct, 3),
                 "unit": "samples/s",
@@ -250,6 +255,7 @@ def main():
                 "sample": f"{reps} x {nb} molecules of the same workload: two-party online eval (both parties, "
                           f"same gates and key format) in oracle/ C with AES-NI + OpenMP, {ct:.1f}s",
                 "bit_exact": exact,
+                "max_abs_err_lsb": cerr,
             }
             log(f"[bench] CPU oracle: {reps}x{nb} samples in {ct:.2f}s on {orc.get_threads()} threads")
     except Exception as e:  # the product number stands without the checker
@@ -348,9 +354,12 @@ def run_stream(args):
         if k % 8 == 7:
             log(f"[stream] {k + 1}/{nmb} micro-batches, {time.perf_counter() - t0:.1f}s")
     elapsed = time.perf_counter() - t0
+    err = 0
     for k, out in enumerate(outs):
         w = want[k % len(want)] if want else None
         exact = exact and (w is not None and bool(np.array_equal(out, w)))
+        if w is not None:
+            err = max(err, int(np.max(np.abs(out.astype(np.int64) - w))))
     value = nmb * B / elapsed
     result = {
         "metric": f"online secure samples/s (bw={bw}, B={B} micro-batches, keys streamed from "
@@ -372,7 +381,8 @@ def run_stream(args):
         "config": {"workload": f"two-party secure affinity forward, bw={bw} s=12, {nmb} micro-batches of B={B} "
                                f"molecules x {dims.n_nodes} atoms, keys streamed "
                                + ("from key files through pinned staging buffers and " if args.key_files else "")
-                               + f"through two {args.slot_gb:g} GiB device slots per party",
+                               + f"through two {args.slot_gb:g} GiB device slots per party"
+                               + SLACK_DESC.get(args.slack, ""),
                    "B": B, "total": nmb * B, "bw": bw, "key_source": "files" if args.key_files else "pinned",
                    "slack": args.slack},
         "key_bytes_per_sample_per_party": round(kb / B, 1),
@@ -381,6 +391,7 @@ def run_stream(args):
         "key_h2d_GBps": round(h2d / elapsed / 1e9, 2),
         "bytes_exchanged_per_sample": round(ctx.bytes_exchanged / (nmb * B), 1),
         "bit_exact": exact,
+        "max_abs_err_lsb": err if want else None,
     }
     print(json.dumps(result), flush=True)
     model.close()

@@ -273,7 +273,8 @@ hipError_t ctx_scratch(mpcx_ctx *c, size_t bytes, void **p) {
   return hipSuccess;
 }
 bool valid_kind(int k) {
-  return k == MPCX_TR || k == MPCX_TRRELU || k == MPCX_RELU || k == MPCX_TRSLACK || k == MPCX_RELUSLACK;
+  return k == MPCX_TR || k == MPCX_TRRELU || k == MPCX_RELU || k == MPCX_TRSLACK || k == MPCX_RELUSLACK ||
+         k == MPCX_LOCALARS;
 }
 }  // namespace
 
@@ -285,6 +286,12 @@ size_t mpcx_tr_key_bytes(mpcx_ctx *c, int kind, size_t n) {
 template <typename T>
 static mpcx_status tr_keygen_t(mpcx_ctx *c, int kind, size_t n, const void *in, void *out, uint64_t seed,
                                uint32_t gate, void *k0, void *k1) {
+  if (kind == MPCX_LOCALARS) {  // no key: the output mask is the shifted input mask
+    HIPC(c, launch_local_ars<T>(c->L, n, c->s, static_cast<const T *>(in), nullptr, 1, static_cast<T *>(out)),
+         "tr_keygen");
+    HIPC(c, hipStreamSynchronize(c->L.stream), "sync");
+    return MPCX_OK;
+  }
   TrLayout lay = tr_layout(kind, c->bw, c->s, n, 0);
   HIPC(c,
        launch_tr_keygen<T>(c->L, lay, seed, gate, static_cast<const T *>(in), static_cast<T *>(out),
@@ -296,7 +303,8 @@ static mpcx_status tr_keygen_t(mpcx_ctx *c, int kind, size_t n, const void *in, 
 mpcx_status mpcx_tr_keygen(mpcx_ctx *c, int kind, size_t n, const void *in, void *out, uint64_t seed, uint32_t gate,
                            void *k0, void *k1) {
   CHECK_CTX(c);
-  if (!valid_kind(kind) || !in || !out || !k0 || !k1) return fail(c, MPCX_EINVAL, "tr_keygen: bad argument");
+  if (!valid_kind(kind) || !in || !out || (kind != MPCX_LOCALARS && (!k0 || !k1)))
+    return fail(c, MPCX_EINVAL, "tr_keygen: bad argument");
   return c->bw == 32 ? tr_keygen_t<uint32_t>(c, kind, n, in, out, seed, gate, k0, k1)
                      : tr_keygen_t<uint64_t>(c, kind, n, in, out, seed, gate, k0, k1);
 }
@@ -319,6 +327,14 @@ static hipError_t tr_eval_run(mpcx_ctx *c, const TrLayout &lay, size_t n, const 
 template <typename T>
 static mpcx_status tr_eval_t(mpcx_ctx *c, int kind, size_t n, const void *k0, const void *k1, const void *x,
                              const void *bias, int ncol, void *y) {
+  if (kind == MPCX_LOCALARS) {  // local: no key, no exchange
+    HIPC(c,
+         launch_local_ars<T>(c->L, n, c->s, static_cast<const T *>(x), static_cast<const T *>(bias), ncol,
+                             static_cast<T *>(y)),
+         "tr_eval");
+    HIPC(c, hipStreamSynchronize(c->L.stream), "sync");
+    return MPCX_OK;
+  }
   TrLayout lay = tr_layout(kind, c->bw, c->s, n, 0);
   const size_t wb = ((n + 63) / 64) * 8;
   void *sp = nullptr;
@@ -336,7 +352,7 @@ static mpcx_status tr_eval_t(mpcx_ctx *c, int kind, size_t n, const void *k0, co
 mpcx_status mpcx_tr_eval(mpcx_ctx *c, int kind, size_t n, const void *k0, const void *k1, const void *x,
                          const void *bias, int ncol, void *y) {
   CHECK_CTX(c);
-  if (!valid_kind(kind) || !k0 || !k1 || !x || !y || (bias && ncol < 1))
+  if (!valid_kind(kind) || (kind != MPCX_LOCALARS && (!k0 || !k1)) || !x || !y || (bias && ncol < 1))
     return fail(c, MPCX_EINVAL, "tr_eval: bad argument");
   return c->bw == 32 ? tr_eval_t<uint32_t>(c, kind, n, k0, k1, x, bias, ncol, y)
                      : tr_eval_t<uint64_t>(c, kind, n, k0, k1, x, bias, ncol, y);

@@ -72,6 +72,9 @@ hipError_t launch_tr_phase2(const Launch &L, const TrLayout &lay, const uint8_t 
 // out = m0 + m1 (reconstruction of a revealed value from both parties' messages)
 template <typename T>
 hipError_t launch_reconstruct(const Launch &L, size_t n, const T *m0, const T *m1, T *out);
+// LocalARS: y[i] = (signed x[i]) >> s + (bias ? bias[i % ncol] : 0), mod 2^bw (bw = 8 sizeof(T))
+template <typename T>
+hipError_t launch_local_ars(const Launch &L, size_t n, int s, const T *x, const T *bias, int ncol, T *y);
 
 // ---------------- reveal ----------------
 template <typename T>

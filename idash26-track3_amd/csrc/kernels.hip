@@ -544,6 +544,28 @@ hipError_t launch_reconstruct(const Launch &L, size_t n, const T *m0, const T *m
   return hipGetLastError();
 }
 
+// LocalARS (TruncateType::LocalARS, gpu_mpc/ddg_orca_batched.h:180-199): the
+// masked value and (at keygen) its mask are shifted locally, no key, no exchange.
+template <typename T>
+__global__ void k_local_ars(size_t n, int s, const T *x, const T *bias, uint32_t ncol, T *y) {
+  using S = std::make_signed_t<T>;
+  for (size_t i = size_t(blockIdx.x) * blockDim.x + threadIdx.x; i < n; i += size_t(gridDim.x) * blockDim.x) {
+    T v = T(S(x[i]) >> s);
+    if (bias) v += bias[uint32_t(i % ncol)];
+    y[i] = v;
+  }
+}
+template <typename T>
+hipError_t launch_local_ars(const Launch &L, size_t n, int s, const T *x, const T *bias, int ncol, T *y) {
+  if (n == 0) return hipSuccess;
+  if (bias && ncol < 1) return hipErrorInvalidValue;
+  const int block = 256;
+  int grid = grid_for(k_local_ars<T>, block, n, L.num_cu);
+  hipLaunchKernelGGL((k_local_ars<T>), dim3(grid), dim3(block), 0, L.stream, n, s, x, bias,
+                     uint32_t(bias ? ncol : 1), y);
+  return hipGetLastError();
+}
+
 template <typename T, int NT, int REP>
 __global__ void k_split(AesRK kd, uint32_t gate, uint32_t field, size_t n, const T *v, T *p0, T *p1, T *copy0,
                         T *mask_out) {
@@ -1561,6 +1583,7 @@ hipError_t launch_rowsum(const Launch &L, size_t rows, int len, const T *a, T *o
                                           const T *, const T *, int, const uint64_t *, const uint64_t *,             \
                                           const uint64_t *, const uint64_t *, T *, T *);                             \
   template hipError_t launch_reconstruct<T>(const Launch &, size_t, const T *, const T *, T *);                      \
+  template hipError_t launch_local_ars<T>(const Launch &, size_t, int, const T *, const T *, int, T *);              \
   template hipError_t launch_reveal_keygen<T>(const Launch &, const RevealLayout &, uint64_t, uint32_t, T *,         \
                                               uint8_t *, uint8_t *);                                                 \
   template hipError_t launch_reveal_eval<T>(const Launch &, const RevealLayout &, const uint8_t *, const uint8_t *,  \

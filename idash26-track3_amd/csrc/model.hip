@@ -482,12 +482,30 @@ class Model final : public ModelBase, KeySource {
     timer.reset();
   }
 
-  // gate of the GCN products H.W^T: exact TR, or (slack >= 1) TRSLACK, exact
+  // slack 3: every layer truncation is LocalARS (the reference's default,
+  // gpu_mpc/ddg_orca_batched.h:180-199): a local shift, then a RELU gate where the
+  // layer has a ReLU
+  bool local_trunc() const { return d_.slack == 3; }
+  // gate of the GCN products H.W^T: exact TR, or (slack 1, 2) TRSLACK, exact
   // for |x| < 2^(bw-2)
-  int xw_kind() const { return d_.slack >= 1 ? G_TRSLACK : G_TR; }
-  // the GCN aggregation A.XW + bias, then ReLU: one TRRELU gate, or (slack >= 2)
+  int xw_kind() const { return d_.slack == 1 || d_.slack == 2 ? G_TRSLACK : G_TR; }
+  // the GCN aggregation A.XW + bias, then ReLU: one TRRELU gate, or (slack 2)
   // TRSLACK with the bias followed by RELUSLACK on the truncated value
-  bool agg_split() const { return d_.slack >= 2; }
+  bool agg_split() const { return d_.slack == 2; }
+
+  // A layer truncation by s (+ bias) and, for relu, the ReLU: one TR / TRRELU
+  // gate, or with local truncation the local shift (no key) followed, for relu,
+  // by a RELU gate.  Eval may overwrite x; keygen may overwrite the mask rin.
+  hipError_t trunc_eval(Runner<T> &r, bool relu, size_t n, T *x, const T *bias, int ncol, T *y) {
+    if (!local_trunc()) return r.tr(relu ? G_TRRELU : G_TR, n, x, bias, ncol, y);
+    TRY(launch_local_ars<T>(L_, n, s_, x, bias, ncol, relu ? x : y));
+    return relu ? r.tr(G_RELU, n, x, nullptr, 1, y) : hipSuccess;
+  }
+  hipError_t trunc_keygen(Dealer<T> &d, bool relu, size_t n, T *rin, T *rout) {
+    if (!local_trunc()) return d.tr(relu ? G_TRRELU : G_TR, n, rin, rout);
+    TRY(launch_local_ars<T>(L_, n, s_, rin, nullptr, 1, relu ? rin : rout));
+    return relu ? d.tr(G_RELU, n, rin, rout) : hipSuccess;
+  }
 
   // ---------------- weights ----------------
   int nlayers() const { return 5 + d_.nfus; }
@@ -571,9 +589,11 @@ class Model final : public ModelBase, KeySource {
     }
     for (int l = 0; l < 3; l++) {
       size_t E = BN * d_.gcn[l];
-      tr(xw_kind(), E);
+      if (!local_trunc()) tr(xw_kind(), E);
       push(sxs_layout(bw_, B, N, N, d_.gcn[l], o).end);
-      if (agg_split()) {
+      if (local_trunc()) {
+        tr(G_RELU, E);
+      } else if (agg_split()) {
         tr(G_TRSLACK, E);
         tr(G_RELUSLACK, E);
       } else {
@@ -583,9 +603,10 @@ class Model final : public ModelBase, KeySource {
     int pairs[32];
     int Lv = pool_levels(N, pairs);
     for (int l = 0; l < Lv; l++) tr(G_RELU, size_t(B) * pairs[l] * d_.gcn[2]);
-    tr(G_TRRELU, size_t(B) * d_.dfc[0]);
-    tr(G_TR, size_t(B) * d_.dfc[1]);
-    for (int k = 0; k < d_.nfus - 1; k++) tr(G_TRRELU, size_t(B) * d_.fus[k]);
+    const int relu_kind = local_trunc() ? G_RELU : G_TRRELU;
+    tr(relu_kind, size_t(B) * d_.dfc[0]);
+    if (!local_trunc()) tr(G_TR, size_t(B) * d_.dfc[1]);
+    for (int k = 0; k < d_.nfus - 1; k++) tr(relu_kind, size_t(B) * d_.fus[k]);
     {  // output: the clear output mask, the same for both parties
       RevealLayout lay = reveal_layout(bw_, size_t(B) * d_.fus[d_.nfus - 1], o);
       push(lay.end).share(lay.off_r, lay.end);
@@ -703,9 +724,14 @@ class Model final : public ModelBase, KeySource {
       const int fo = d_.gcn[l];
       const size_t En = BN * fo;
       TRY(pub_gemm(rX.p, l, BN, t1.p));
-      TRY(d.tr(xw_kind(), En, t1.p, t2.p));
+      if (local_trunc())
+        TRY(trunc_keygen(d, false, En, t1.p, t2.p));
+      else
+        TRY(d.tr(xw_kind(), En, t1.p, t2.p));
       TRY(d.sxs(B, N, N, fo, rN.p, t2.p, t1.p, gt.p));
-      if (agg_split()) {
+      if (local_trunc()) {
+        TRY(trunc_keygen(d, true, En, t1.p, rX.p));
+      } else if (agg_split()) {
         TRY(d.tr(G_TRSLACK, En, t1.p, t2.p));
         TRY(d.tr(G_RELUSLACK, En, t2.p, rX.p));
       } else {
@@ -731,15 +757,15 @@ class Model final : public ModelBase, KeySource {
     }
     // drug FCs
     TRY(pub_gemm(cur, 3, B, t1.p));
-    TRY(d.tr(G_TRRELU, size_t(B) * d_.dfc[0], t1.p, gt.p));
+    TRY(trunc_keygen(d, true, size_t(B) * d_.dfc[0], t1.p, gt.p));
     TRY(pub_gemm(gt.p, 4, B, t1.p));
-    TRY(d.tr(G_TR, size_t(B) * d_.dfc[1], t1.p, gt.p));
+    TRY(trunc_keygen(d, false, size_t(B) * d_.dfc[1], t1.p, gt.p));
     TRY(launch_concat<T>(L_, B, d_.dfc[1], d_.prot, gt.p, nullptr, nxt));
     T *h = nxt, *h2 = cur;
     for (int k = 0; k < d_.nfus; k++) {
       TRY(pub_gemm(h, 5 + k, B, t1.p));
       if (k < d_.nfus - 1) {
-        TRY(d.tr(G_TRRELU, size_t(B) * d_.fus[k], t1.p, h2));
+        TRY(trunc_keygen(d, true, size_t(B) * d_.fus[k], t1.p, h2));
         std::swap(h, h2);
       } else {
         TRY(d.output(size_t(B) * d_.fus[k], t1.p));
@@ -1217,9 +1243,14 @@ class Model final : public ModelBase, KeySource {
       const int fo = d_.gcn[l];
       const size_t En = BN * fo;
       TRY(pub_gemm(H, l, BN, Z));
-      TRY(r.tr(xw_kind(), En, Z, nullptr, 1, XW));
+      if (local_trunc())
+        TRY(trunc_eval(r, false, En, Z, nullptr, 1, XW));
+      else
+        TRY(r.tr(xw_kind(), En, Z, nullptr, 1, XW));
       TRY(r.sxs(B, N, N, fo, An_.p, XW, Z));
-      if (agg_split()) {  // truncate with the bias, reveal, then ReLU of the small value
+      if (local_trunc()) {
+        TRY(trunc_eval(r, true, En, Z, bias_[l].p, fo, H));
+      } else if (agg_split()) {  // truncate with the bias, reveal, then ReLU of the small value
         TRY(r.tr(G_TRSLACK, En, Z, bias_[l].p, fo, XW));
         TRY(r.tr(G_RELUSLACK, En, XW, nullptr, 1, H));
       } else {
@@ -1246,9 +1277,9 @@ class Model final : public ModelBase, KeySource {
     }
     // drug FCs
     TRY(pub_gemm(cur, 3, B, Z));
-    TRY(r.tr(G_TRRELU, size_t(B) * d_.dfc[0], Z, bias_[3].p, d_.dfc[0], XW));
+    TRY(trunc_eval(r, true, size_t(B) * d_.dfc[0], Z, bias_[3].p, d_.dfc[0], XW));
     TRY(pub_gemm(XW, 4, B, Z));
-    TRY(r.tr(G_TR, size_t(B) * d_.dfc[1], Z, bias_[4].p, d_.dfc[1], XW));
+    TRY(trunc_eval(r, false, size_t(B) * d_.dfc[1], Z, bias_[4].p, d_.dfc[1], XW));
     // concat [drug, protein]; the protein embedding owner reveals it (one message)
     counters.msg(size_t(B) * d_.prot, bw);
     TRY(launch_concat<T>(L_, B, d_.dfc[1], d_.prot, XW, prot_.p, H));
@@ -1256,7 +1287,7 @@ class Model final : public ModelBase, KeySource {
     for (int k = 0; k < d_.nfus; k++) {
       TRY(pub_gemm(h, 5 + k, B, Z));
       if (k < d_.nfus - 1) {
-        TRY(r.tr(G_TRRELU, size_t(B) * d_.fus[k], Z, bias_[5 + k].p, d_.fus[k], h2));
+        TRY(trunc_eval(r, true, size_t(B) * d_.fus[k], Z, bias_[5 + k].p, d_.fus[k], h2));
         std::swap(h, h2);
       } else {
         TRY(r.output(B, size_t(B) * d_.fus[k], Z, hbias_[5 + k][0], out_.p));
@@ -1352,8 +1383,8 @@ ModelBase *make_model(int bw, int s, const ModelDims &d, const int64_t *W, size_
     *err = "layer widths must be >= 1 (protein width >= 0, lut_nmax in [0, 255])";
     return nullptr;
   }
-  if (d.slack < 0 || d.slack > 2) {
-    *err = "slack must be 0, 1 or 2";
+  if (d.slack < 0 || d.slack > 3) {
+    *err = "slack must be 0, 1, 2 or 3";
     return nullptr;
   }
   if (d.mask_scale < 0 || d.mask_scale > bw - 2 - 1) {

@@ -19,17 +19,14 @@ inline constexpr size_t align_up(size_t x) { return (x + (kAlign - 1)) & ~(kAlig
 // packed-bit plane words (u32), rounded up to whole u64 words
 inline constexpr size_t zwords(size_t n) { return ((n + 63) / 64) * 2; }
 
+// kinds of the truncation / ReLU gate family (the MPCX_* codes of mpcx.h)
 enum GateKind : int {
-  G_TR = 1,       // exact truncation (+bias), full-width sign extension
-  G_TRRELU = 2,   // ReLU(trunc(x) + bias)
-  G_RELU = 3,     // ReLU without truncation
-  G_TRSLACK = 4,  // exact truncation for |x| < 2^(bw-2)
-  G_MUL = 5,      // Beaver elementwise product with index maps
-  G_LUT8 = 6,     // 8-bit DPF lookup table
-  G_SXS = 7,      // batched secret x secret ring GEMM
-  G_REVEAL = 8,   // additive shares -> masked public
-  G_RELUSLACK = 9,  // ReLU for |x| < 2^(bw-2-s): a (bw-2-s)-bit DCF (after TRSLACK)
-  G_OUTPUT = 9    // final unmask (output mask in the clear)
+  G_TR = 1,          // exact truncation (+bias), full-width sign extension
+  G_TRRELU = 2,      // ReLU(trunc(x) + bias)
+  G_RELU = 3,        // ReLU without truncation
+  G_TRSLACK = 4,     // exact truncation for |x| < 2^(bw-2)
+  G_RELUSLACK = 9,   // ReLU for |x| < 2^(bw-2-s): a (bw-2-s)-bit DCF (after TRSLACK)
+  G_LOCALARS = 10    // local arithmetic shift of the masked value and its mask (no key)
 };
 
 enum Field : uint32_t {
@@ -87,6 +84,12 @@ inline TrLayout tr_layout(int kind, int bw, int s, size_t N, size_t base) {
   t.s = s;
   t.N = N;
   t.relu = kind == G_TRRELU || kind == G_RELU || kind == G_RELUSLACK;
+  if (kind == G_LOCALARS) {  // keyless: consumes no key bytes
+    t.use_a = t.use_b = false;
+    t.ncase = 0;
+    t.off_g = t.end = base;
+    return t;
+  }
   t.use_a = kind != G_TRSLACK;
   t.use_b = kind != G_RELU && kind != G_RELUSLACK;
   const size_t tb = size_t(bw) / 8;

@@ -37,7 +37,7 @@ class Dims:
     fus: tuple = (1024, 512, 1)
     lut_nmax: int = 138
     mask_scale: int = 0  # the atom mask is 0 or 2^mask_scale
-    slack: int = 0  # 0 exact; 1 H.W^T slack-truncated; 2 also A.XW + b (|x| < 2^(bw-2))
+    slack: int = 0  # 0 exact; 1 H.W^T slack-truncated; 2 also A.XW + b (|x| < 2^(bw-2)); 3 LocalARS
 
     def layers(self):
         """(in, out) of every linear layer in weight-blob order."""

@@ -40,6 +40,11 @@ typedef struct mpcx_model mpcx_model;
 #define MPCX_RELU 3     /* ReLU(x)                                            */
 #define MPCX_TRSLACK 4  /* exact floor(x/2^s), requires |x| < 2^(bw-2)        */
 #define MPCX_RELUSLACK 9 /* ReLU(x), requires |x| < 2^(bw-2-s): one (bw-2-s)-bit DCF */
+#define MPCX_LOCALARS 10 /* TruncateType::LocalARS, the default of DDGOrcaBatched::truncateForward
+                            (gpu_mpc/ddg_orca_batched.h:180-199, keygen :273-277): the masked
+                            value and its mask are shifted locally (arithmetic shift), no key
+                            bytes, no exchange; floor(x/2^s) + bias + e, e in {0, 1}, or off by
+                            2^(bw-s) when x + r leaves the signed ring (probability ~|x|/2^bw) */
 
 /* ---------------- context ----------------
  * Replaces the evaluator/dealer constructors DDGOrcaBase(party, ip, bw, scale)
@@ -105,7 +110,8 @@ mpcx_status mpcx_dcf_eval(mpcx_ctx *ctx, int party, int bin, size_t n, const voi
  * shift, peer, party, N, d_in, g, s) (gpu_mpc/ddg_orca.h:116-118), for both
  * parties at once: masked input in, masked output out.
  * bias: ncol ring elements at scale s (element i uses bias[i % ncol]) or NULL;
- * ignored by MPCX_RELU. */
+ * ignored by MPCX_RELU.  MPCX_LOCALARS has no key (key bytes 0, key pointers may
+ * be NULL, the gate id is unused). */
 size_t mpcx_tr_key_bytes(mpcx_ctx *ctx, int kind, size_t n);
 mpcx_status mpcx_tr_keygen(mpcx_ctx *ctx, int kind, size_t n, const void *d_in_mask,
                            void *d_out_mask, uint64_t seed, uint32_t gate, void *d_key0,
@@ -240,7 +246,12 @@ typedef struct {
                      slack truncation with the bias, then MPCX_RELUSLACK on the truncated value
                      (a (bw-2-s)-bit DCF, 12 AES at bw=32; two more exchange rounds), exact for
                      |A.XW + b 2^s| < 2^(bw-2).  Outputs are bit-exact with the fixed-point
-                     forward while every such value lies in that half ring. */
+                     forward while every such value lies in that half ring.  3: every layer
+                     truncation (H.W^T, A.XW + b, the FCs) is MPCX_LOCALARS, the reference's
+                     default (gpu_mpc/ddg_orca_batched.h:180-199), followed by a RELU gate on
+                     ReLU layers; the adjacency normalisation stays exact.  Not bit-exact:
+                     +1 per truncation, and a 2^(bw-s) error when x + r wraps (~|x|/2^bw per
+                     element: usable at bw=64 only, as the reference notes). */
 } mpcx_model_dims;
 
 mpcx_status mpcx_model_create(mpcx_ctx *ctx, const mpcx_model_dims *dims, const int64_t *h_weights,

@@ -169,11 +169,21 @@ class SecureBackend {
     }
   }
 
-  // ---- exact truncation by the scale (ddg_orca.h:112-123, TrFloor) ----
+  // ---- truncation by the scale: exact (ddg_orca.h:112-123, TrFloor) by default;
+  // set_truncation(MPCX_LOCALARS) selects the reference batched backend's default
+  // local shift (ddg_orca_batched.h:180-199: no key, no exchange, not exact) and
+  // MPCX_TRSLACK the exact truncation for |x| < 2^(bw-2).  The dealer and the
+  // evaluator must select the same kind (the reference reads DDG_EXACT_TRUNC on
+  // both sides, ddg_orca_batched.h:133-134, 239-240). ----
+  void set_truncation(int kind) {
+    if (kind != MPCX_TR && kind != MPCX_TRSLACK && kind != MPCX_LOCALARS)
+      throw std::invalid_argument("set_truncation: MPCX_TR, MPCX_TRSLACK or MPCX_LOCALARS");
+    trunc_kind_ = kind;
+  }
   template <class TI>
   void truncateForward(TI &in, uint64_t shift, uint8_t /*mode*/ = 0) {
     if (int(shift) != scale()) throw std::invalid_argument("truncateForward: shift must equal the scale");
-    gate(MPCX_TR, in, in, nullptr, 0);
+    gate(trunc_kind_, in, in, nullptr, 0);
   }
 
   // ---- fused truncation + bias + ReLU (one gate, two rounds) ----
@@ -269,6 +279,7 @@ class SecureBackend {
   uint64_t seed_;
   uint32_t gate_ = 1;
   int scale_ = 12;
+  int trunc_kind_ = MPCX_TR;
   std::vector<void *> owned_;
   uint32_t *ident_ = nullptr;
   size_t ident_n_ = 0;

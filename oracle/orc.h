@@ -89,7 +89,9 @@ enum {
   ORC_G_LUT8 = 6,     /* 8-bit DPF lookup table                         */
   ORC_G_SXS = 7,      /* batched secret x secret ring GEMM              */
   ORC_G_REVEAL = 8,   /* additive shares -> masked public               */
-  ORC_G_RELUSLACK = 9 /* ReLU for |x| < 2^(bw-2-s) (a (bw-2-s)-bit DCF)  */
+  ORC_G_RELUSLACK = 9, /* ReLU for |x| < 2^(bw-2-s) (a (bw-2-s)-bit DCF) */
+  ORC_G_LOCALARS = 10  /* local arithmetic shift of the masked value and of
+                          its mask: no key, no exchange, error +1 or a wrap */
 };
 
 /* Dealer randomness fields. */
@@ -197,7 +199,9 @@ typedef struct {
   int mask_scale; /* the atom mask is 0 or 2^mask_scale (0; s for the reference's files) */
   int slack;      /* 0: exact truncations over the signed ring; 1: the GCN products
                      H.W^T are truncated with TRSLACK (exact for |H.W^T| < 2^(bw-2));
-                     2: also A.XW + bias: TRSLACK then RELUSLACK (|A.XW + b 2^s| < 2^(bw-2)) */
+                     2: also A.XW + bias: TRSLACK then RELUSLACK (|A.XW + b 2^s| < 2^(bw-2));
+                     3: every layer truncation is LocalARS (local shift, no key), followed
+                     by a RELU gate on ReLU layers: not bit-exact with orc_plain_forward */
 } orc_dims;
 
 /* Weights: for each linear layer in order gcn0..2, dfc0..1, fus0..nfus-1:

@@ -145,6 +145,10 @@ orc_tr_layout orc_tr_layout_make(int kind, int bw, int s, size_t N, size_t base)
   T.s = s;
   T.N = N;
   T.relu = (kind == ORC_G_TRRELU || kind == ORC_G_RELU || kind == ORC_G_RELUSLACK);
+  if (kind == ORC_G_LOCALARS) { /* keyless: consumes no key bytes */
+    T.off_g = T.end = base;
+    return T;
+  }
   size_t o = orc_align(base);
   size_t tb = (size_t)bw / 8;
   if (kind == ORC_G_TR || kind == ORC_G_TRRELU || kind == ORC_G_RELU || kind == ORC_G_RELUSLACK) {
@@ -310,9 +314,35 @@ void orc_dpf_full_eval(int party, int m, const uint8_t *key, const orc_dcf_layou
 }
 
 /* ---------------- TR / TRRELU / RELU / TRSLACK ---------------- */
+/* Arithmetic right shift by s of a bw-bit ring element (sign-extended from bit
+ * bw-1), reduced mod 2^bw. */
+static uint64_t ars_bw(uint64_t v, int bw, int s) {
+  const int64_t sv = bw >= 64 ? (int64_t)v : (int64_t)(v << (64 - bw)) >> (64 - bw);
+  return (uint64_t)(sv >> s) & rmask(bw);
+}
+
+/* LocalARS (TruncateType::LocalARS, the default of DDGOrcaBatched::truncateForward,
+ * gpu_mpc/ddg_orca_batched.h:180-199 and keygen :273-277): both parties shift the
+ * public masked value, the dealer shifts the mask.  No key bytes, no exchange.
+ * y^ - r_y = floor(x/2^s) + b + e, e in {0, 1} (the carry of the low s bits of
+ * x + r), minus 2^(bw-s) when x + r leaves the signed ring (probability about
+ * |x| / 2^bw for a uniform mask). */
+static void local_ars_keygen(int bw, int s, size_t N, const uint64_t *in_mask, uint64_t *out_mask) {
+  for (size_t i = 0; i < N; i++) out_mask[i] = ars_bw(in_mask[i] & rmask(bw), bw, s);
+}
+static void local_ars_eval(int bw, int s, size_t N, const uint64_t *xhat, const int64_t *bias_elem,
+                           uint64_t *yhat) {
+  for (size_t i = 0; i < N; i++)
+    yhat[i] = (ars_bw(xhat[i] & rmask(bw), bw, s) + (bias_elem ? (uint64_t)bias_elem[i] : 0)) & rmask(bw);
+}
+
 void orc_tr_keygen(uint64_t seed, uint32_t gate, int kind, int bw, int s, size_t N,
                    const uint64_t *in_mask, uint64_t *out_mask, uint8_t *k0, uint8_t *k1,
                    size_t base) {
+  if (kind == ORC_G_LOCALARS) {
+    local_ars_keygen(bw, s, N, in_mask, out_mask);
+    return;
+  }
   orc_prf P;
   orc_prf_init(&P, seed);
   orc_tr_layout T = orc_tr_layout_make(kind, bw, s, N, base);
@@ -381,6 +411,10 @@ void orc_tr_keygen(uint64_t seed, uint32_t gate, int kind, int bw, int s, size_t
 void orc_tr_eval(int kind, int bw, int s, size_t N, const uint8_t *k0, const uint8_t *k1,
                  size_t base, const uint64_t *xhat, const int64_t *bias_elem,
                  uint64_t *yhat, uint64_t *bytes) {
+  if (kind == ORC_G_LOCALARS) {
+    local_ars_eval(bw, s, N, xhat, bias_elem, yhat);
+    return;
+  }
   orc_tr_layout T = orc_tr_layout_make(kind, bw, s, N, base);
   const uint64_t M = rmask(bw);
   const int n = bw, sb = orc_sign_bit(kind, bw, s);

@@ -35,11 +35,15 @@ static void trace(uint32_t g, size_t n, const uint64_t *v) {
 
 /* ---------------- dims / weights ---------------- */
 static int nlayers(const orc_dims *d) { return 5 + d->nfus; }
-/* gate of the GCN products H.W^T: exact TR, or TRSLACK when d->slack >= 1 */
-static int xw_kind(const orc_dims *d) { return d->slack >= 1 ? ORC_G_TRSLACK : ORC_G_TR; }
-/* the GCN aggregation A.XW + bias then ReLU: one TRRELU gate, or (d->slack >= 2)
+/* slack 3: every layer truncation is LocalARS (the reference's default,
+ * gpu_mpc/ddg_orca_batched.h:180-199): a local shift, then a RELU gate where the
+ * layer has a ReLU; not bit-exact with the fixed-point forward */
+static int local_trunc(const orc_dims *d) { return d->slack == 3; }
+/* gate of the GCN products H.W^T: exact TR, or TRSLACK when d->slack is 1 or 2 */
+static int xw_kind(const orc_dims *d) { return d->slack == 1 || d->slack == 2 ? ORC_G_TRSLACK : ORC_G_TR; }
+/* the GCN aggregation A.XW + bias then ReLU: one TRRELU gate, or (d->slack == 2)
  * TRSLACK (with the bias) followed by RELUSLACK on the truncated value */
-static int agg_split(const orc_dims *d) { return d->slack >= 2; }
+static int agg_split(const orc_dims *d) { return d->slack == 2; }
 static void layer_io(const orc_dims *d, int l, int *in, int *out) {
   if (l < 3) {
     *in = l == 0 ? d->feat : d->gcn[l - 1];
@@ -195,8 +199,9 @@ int orc_plain_forward(const orc_dims *d, int B, const int64_t *X, const int64_t 
       int fo = d->gcn[l];
       const int64_t *Wt = W + layer_off(d, l);
       const int64_t *bias = Wt + (size_t)fin * fo;
-      fixed_mm(&f, H, Wt, (size_t)N, (size_t)fin, (size_t)fo, NULL, d->slack >= 1 ? 7 : 0, XW); /* XW */
-      fixed_mm(&f, Af, XW, (size_t)N, (size_t)N, (size_t)fo, bias, d->slack >= 2 ? 8 : 0, Hn); /* A.XW */
+      fixed_mm(&f, H, Wt, (size_t)N, (size_t)fin, (size_t)fo, NULL, xw_kind(d) == ORC_G_TRSLACK ? 7 : 0,
+               XW); /* XW */
+      fixed_mm(&f, Af, XW, (size_t)N, (size_t)N, (size_t)fo, bias, agg_split(d) ? 8 : 0, Hn); /* A.XW */
       for (int i = 0; i < N; i++)
         for (int j = 0; j < fo; j++) {
           int64_t v = wrapv(&f, (i128)Hn[(size_t)i * fo + j] + bias[j]);
@@ -552,9 +557,11 @@ size_t orc_model_key_bytes(const orc_dims *d, int B) {
   o = adjnorm_layout(bw, s, B, N, o);
   for (int l = 0; l < 3; l++) {
     size_t E = (size_t)B * N * d->gcn[l];
-    o = orc_tr_layout_make(xw_kind(d), bw, s, E, o).end;
+    if (!local_trunc(d)) o = orc_tr_layout_make(xw_kind(d), bw, s, E, o).end;
     o = orc_sxs_layout(bw, (size_t)B, (size_t)N, (size_t)N, (size_t)d->gcn[l], o, &r1, &r2, &r3);
-    if (agg_split(d)) {
+    if (local_trunc(d)) {
+      o = orc_tr_layout_make(ORC_G_RELU, bw, s, E, o).end;
+    } else if (agg_split(d)) {
       o = orc_tr_layout_make(ORC_G_TRSLACK, bw, s, E, o).end;
       o = orc_tr_layout_make(ORC_G_RELUSLACK, bw, s, E, o).end;
     } else {
@@ -565,10 +572,11 @@ size_t orc_model_key_bytes(const orc_dims *d, int B) {
   int L = pool_levels(N, pairs);
   for (int l = 0; l < L; l++)
     o = orc_tr_layout_make(ORC_G_RELU, bw, s, (size_t)B * pairs[l] * d->gcn[2], o).end;
-  o = orc_tr_layout_make(ORC_G_TRRELU, bw, s, (size_t)B * d->dfc[0], o).end;
-  o = orc_tr_layout_make(ORC_G_TR, bw, s, (size_t)B * d->dfc[1], o).end;
+  const int relu_kind = local_trunc(d) ? ORC_G_RELU : ORC_G_TRRELU;
+  o = orc_tr_layout_make(relu_kind, bw, s, (size_t)B * d->dfc[0], o).end;
+  if (!local_trunc(d)) o = orc_tr_layout_make(ORC_G_TR, bw, s, (size_t)B * d->dfc[1], o).end;
   for (int k = 0; k < d->nfus - 1; k++)
-    o = orc_tr_layout_make(ORC_G_TRRELU, bw, s, (size_t)B * d->fus[k], o).end;
+    o = orc_tr_layout_make(relu_kind, bw, s, (size_t)B * d->fus[k], o).end;
   o = orc_reveal_layout(bw, (size_t)B * d->fus[d->nfus - 1], o, &r1);
   return o;
 }
@@ -577,6 +585,37 @@ size_t orc_model_key_bytes(const orc_dims *d, int B) {
 static void pub_gemm(int bw, size_t rows, int fi, int fo, const uint64_t *x, const int64_t *Wt,
                      uint64_t *y) {
   orc_ring_gemm(bw, 1, rows, (size_t)fi, (size_t)fo, x, (const uint64_t *)Wt, y, 0);
+}
+
+/* A layer truncation by s (+ bias in eval) and, for relu, the ReLU: one TR or
+ * TRRELU gate; with local truncation the local shift (no key, no gate id) and,
+ * for relu, a RELU gate.  Keygen maps the mask rin to rout (rin may be
+ * overwritten); eval maps x (may be overwritten) to y.  Return the key end. */
+static size_t trunc_keygen(const orc_dims *d, uint64_t seed, uint32_t *g, int relu, size_t n, uint64_t *rin,
+                           uint64_t *rout, uint8_t *k0, uint8_t *k1, size_t o) {
+  const int bw = d->bw, s = d->s;
+  int kind = relu ? ORC_G_TRRELU : ORC_G_TR;
+  if (local_trunc(d)) {
+    orc_tr_keygen(0, 0, ORC_G_LOCALARS, bw, s, n, rin, relu ? rin : rout, NULL, NULL, o);
+    if (!relu) return o;
+    kind = ORC_G_RELU;
+  }
+  orc_tr_keygen(seed, (*g)++, kind, bw, s, n, rin, rout, k0, k1, o);
+  return orc_tr_layout_make(kind, bw, s, n, o).end;
+}
+static size_t trunc_eval(const orc_dims *d, uint32_t *g, int relu, size_t n, const uint8_t *k0, const uint8_t *k1,
+                         size_t o, uint64_t *x, const int64_t *be, uint64_t *y, uint64_t *by) {
+  const int bw = d->bw, s = d->s;
+  int kind = relu ? ORC_G_TRRELU : ORC_G_TR;
+  if (local_trunc(d)) {
+    orc_tr_eval(ORC_G_LOCALARS, bw, s, n, NULL, NULL, o, x, be, relu ? x : y, by);
+    if (!relu) return o;
+    kind = ORC_G_RELU;
+    be = NULL;
+  }
+  orc_tr_eval(kind, bw, s, n, k0, k1, o, x, be, y, by);
+  trace((*g)++, n, y);
+  return orc_tr_layout_make(kind, bw, s, n, o).end;
 }
 
 int orc_model_keygen(const orc_dims *d, int B, uint64_t seed, const int64_t *W, uint8_t *k0,
@@ -610,11 +649,17 @@ int orc_model_keygen(const orc_dims *d, int B, uint64_t seed, const int64_t *W, 
     int fo = d->gcn[l];
     size_t E = BN * fo;
     pub_gemm(bw, BN, fin, fo, rX, W + layer_off(d, l), t1); /* mask of H.Wt */
-    orc_tr_keygen(seed, g++, xw_kind(d), bw, s, E, t1, t2, k0, k1, o);
-    o = orc_tr_layout_make(xw_kind(d), bw, s, E, o).end;
+    if (local_trunc(d)) {
+      o = trunc_keygen(d, seed, &g, 0, E, t1, t2, k0, k1, o);
+    } else {
+      orc_tr_keygen(seed, g++, xw_kind(d), bw, s, E, t1, t2, k0, k1, o);
+      o = orc_tr_layout_make(xw_kind(d), bw, s, E, o).end;
+    }
     orc_sxs_keygen(seed, g++, bw, (size_t)B, (size_t)N, (size_t)N, (size_t)fo, rN, t2, t1, k0, k1, o);
     o = orc_sxs_layout(bw, (size_t)B, (size_t)N, (size_t)N, (size_t)fo, o, &r1, &r2, &r3);
-    if (agg_split(d)) {
+    if (local_trunc(d)) {
+      o = trunc_keygen(d, seed, &g, 1, E, t1, rX, k0, k1, o);
+    } else if (agg_split(d)) {
       orc_tr_keygen(seed, g++, ORC_G_TRSLACK, bw, s, E, t1, t2, k0, k1, o);
       o = orc_tr_layout_make(ORC_G_TRSLACK, bw, s, E, o).end;
       orc_tr_keygen(seed, g++, ORC_G_RELUSLACK, bw, s, E, t2, rX, k0, k1, o);
@@ -635,11 +680,9 @@ int orc_model_keygen(const orc_dims *d, int B, uint64_t seed, const int64_t *W, 
   o = pool_keygen_blk(seed, &g, bw, s, B, N, C, rX, t1, t2, k0, k1, o);
   /* drug FCs on the pooled (B x C) mask in rX */
   pub_gemm(bw, (size_t)B, C, d->dfc[0], rX, W + layer_off(d, 3), t1);
-  orc_tr_keygen(seed, g++, ORC_G_TRRELU, bw, s, (size_t)B * d->dfc[0], t1, t2, k0, k1, o);
-  o = orc_tr_layout_make(ORC_G_TRRELU, bw, s, (size_t)B * d->dfc[0], o).end;
+  o = trunc_keygen(d, seed, &g, 1, (size_t)B * d->dfc[0], t1, t2, k0, k1, o);
   pub_gemm(bw, (size_t)B, d->dfc[0], d->dfc[1], t2, W + layer_off(d, 4), t1);
-  orc_tr_keygen(seed, g++, ORC_G_TR, bw, s, (size_t)B * d->dfc[1], t1, t2, k0, k1, o);
-  o = orc_tr_layout_make(ORC_G_TR, bw, s, (size_t)B * d->dfc[1], o).end;
+  o = trunc_keygen(d, seed, &g, 0, (size_t)B * d->dfc[1], t1, t2, k0, k1, o);
   /* concat [drug (mask t2), protein (public, mask 0)] */
   int width = d->dfc[1] + d->prot;
   for (int b = 0; b < B; b++)
@@ -649,8 +692,7 @@ int orc_model_keygen(const orc_dims *d, int B, uint64_t seed, const int64_t *W, 
     int fo = d->fus[k];
     pub_gemm(bw, (size_t)B, width, fo, rX, W + layer_off(d, 5 + k), t1);
     if (k < d->nfus - 1) {
-      orc_tr_keygen(seed, g++, ORC_G_TRRELU, bw, s, (size_t)B * fo, t1, rX, k0, k1, o);
-      o = orc_tr_layout_make(ORC_G_TRRELU, bw, s, (size_t)B * fo, o).end;
+      o = trunc_keygen(d, seed, &g, 1, (size_t)B * fo, t1, rX, k0, k1, o);
     } else {
       /* output mask given to both evaluators in the clear (ddg_orca_base.h:296-302,511-517) */
       size_t orr;
@@ -718,14 +760,20 @@ int orc_model_eval(const orc_dims *d, int B, const int64_t *W, const uint8_t *k0
     const int64_t *Wt = W + layer_off(d, l);
     const int64_t *bias = Wt + (size_t)fin * fo;
     pub_gemm(bw, BN, fin, fo, H, Wt, t1);
-    orc_tr_eval(xw_kind(d), bw, s, E, k0, k1, o, t1, NULL, t2, &by);
-    trace(g++, E, t2);
-    o = orc_tr_layout_make(xw_kind(d), bw, s, E, o).end;
+    if (local_trunc(d)) {
+      o = trunc_eval(d, &g, 0, E, k0, k1, o, t1, NULL, t2, &by);
+    } else {
+      orc_tr_eval(xw_kind(d), bw, s, E, k0, k1, o, t1, NULL, t2, &by);
+      trace(g++, E, t2);
+      o = orc_tr_layout_make(xw_kind(d), bw, s, E, o).end;
+    }
     orc_sxs_eval(bw, (size_t)B, (size_t)N, (size_t)N, (size_t)fo, k0, k1, o, An, t2, t1, &by);
     trace(g++, E, t1);
     o = orc_sxs_layout(bw, (size_t)B, (size_t)N, (size_t)N, (size_t)fo, o, &r1, &r2, &r3);
     for (size_t e = 0; e < E; e++) be[e] = bias[e % fo];
-    if (agg_split(d)) {
+    if (local_trunc(d)) {
+      o = trunc_eval(d, &g, 1, E, k0, k1, o, t1, be, H, &by);
+    } else if (agg_split(d)) {
       orc_tr_eval(ORC_G_TRSLACK, bw, s, E, k0, k1, o, t1, be, t2, &by);
       trace(g++, E, t2);
       o = orc_tr_layout_make(ORC_G_TRSLACK, bw, s, E, o).end;
@@ -749,16 +797,12 @@ int orc_model_eval(const orc_dims *d, int B, const int64_t *W, const uint8_t *k0
     const int64_t *bias = Wt + (size_t)C * d->dfc[0];
     pub_gemm(bw, (size_t)B, C, d->dfc[0], H, Wt, t1);
     for (size_t e = 0; e < (size_t)B * d->dfc[0]; e++) be[e] = bias[e % d->dfc[0]];
-    orc_tr_eval(ORC_G_TRRELU, bw, s, (size_t)B * d->dfc[0], k0, k1, o, t1, be, t2, &by);
-    trace(g++, (size_t)B * d->dfc[0], t2);
-    o = orc_tr_layout_make(ORC_G_TRRELU, bw, s, (size_t)B * d->dfc[0], o).end;
+    o = trunc_eval(d, &g, 1, (size_t)B * d->dfc[0], k0, k1, o, t1, be, t2, &by);
     Wt = W + layer_off(d, 4);
     bias = Wt + (size_t)d->dfc[0] * d->dfc[1];
     pub_gemm(bw, (size_t)B, d->dfc[0], d->dfc[1], t2, Wt, t1);
     for (size_t e = 0; e < (size_t)B * d->dfc[1]; e++) be[e] = bias[e % d->dfc[1]];
-    orc_tr_eval(ORC_G_TR, bw, s, (size_t)B * d->dfc[1], k0, k1, o, t1, be, t2, &by);
-    trace(g++, (size_t)B * d->dfc[1], t2);
-    o = orc_tr_layout_make(ORC_G_TR, bw, s, (size_t)B * d->dfc[1], o).end;
+    o = trunc_eval(d, &g, 0, (size_t)B * d->dfc[1], k0, k1, o, t1, be, t2, &by);
   }
   int width = d->dfc[1] + d->prot;
   for (int b = 0; b < B; b++)
@@ -775,9 +819,7 @@ int orc_model_eval(const orc_dims *d, int B, const int64_t *W, const uint8_t *k0
     pub_gemm(bw, (size_t)B, width, fo, H, Wt, t1);
     if (k < d->nfus - 1) {
       for (size_t e = 0; e < (size_t)B * fo; e++) be[e] = bias[e % fo];
-      orc_tr_eval(ORC_G_TRRELU, bw, s, (size_t)B * fo, k0, k1, o, t1, be, H, &by);
-      trace(g++, (size_t)B * fo, H);
-      o = orc_tr_layout_make(ORC_G_TRRELU, bw, s, (size_t)B * fo, o).end;
+      o = trunc_eval(d, &g, 1, (size_t)B * fo, k0, k1, o, t1, be, H, &by);
     } else {
       size_t orr;
       orc_reveal_layout(bw, (size_t)B * fo, o, &orr);

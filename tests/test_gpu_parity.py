@@ -141,6 +141,28 @@ def test_tr_family_keys_and_eval(ctx, orc, kind):
     assert np.array_equal(signed(y.astype(np.uint64) - orout, bw), _tr_expected(kind, x, bias))
 
 
+def test_local_ars_matches_oracle(ctx, orc):
+    """LocalARS (TruncateType::LocalARS, ddg_orca_batched.h:180-199): no key and no
+    exchange; output mask and outputs identical to the oracle's, whose closed form
+    (carry of the low bits, wrap of x + r) is pinned on the CPU."""
+    bw = ctx.bw
+    rng = np.random.default_rng(bw + 77)
+    x = rng.integers(-(1 << (bw - 3)), 1 << (bw - 3), size=50000, dtype=np.int64)
+    bias = rng.integers(-(1 << 14), 1 << 14, size=312)
+    rin = rmask(rng, x.size, bw)
+    assert ctx.lib.mpcx_tr_key_bytes(ctx.h, 10, x.size) == 0
+    g0, g1, grout = ctx.tr_keygen(10, rin)
+    _, _, orout = orc.tr_keygen(0, 0, 10, bw, S, rin)
+    assert np.array_equal(grout.astype(np.uint64), orout)
+    xhat = (x.astype(np.uint64) + rin) & M(bw)
+    ctx.reset_counters()
+    y = ctx.tr_eval(10, g0, g1, xhat, bias)
+    assert ctx.bytes_exchanged == 0
+    oy, oby = orc.tr_eval(10, bw, S, np.zeros(0, np.uint8), np.zeros(0, np.uint8), xhat, np.resize(bias, x.size))
+    assert oby == 0
+    assert np.array_equal(y.astype(np.uint64), oy)
+
+
 def test_all_aes_variants_agree(mp, orc):
     c = mp.Ctx(bw=32)
     rng = np.random.default_rng(4)
@@ -307,6 +329,36 @@ def test_model_keys_and_forward(mp, orc, synth, bw, slack):
     got = m.output(B)
     assert np.array_equal(got, want)
     _, oby = orc.model_eval(d, B, wl.W, o0, o1, x0, x1, a0, a1, m0, m1, wl.prot)
+    assert c.bytes_exchanged == oby
+    m.close()
+    c.close()
+
+
+@pytest.mark.parametrize("bw", [32, 64])
+def test_model_local_truncation(mp, orc, synth, bw):
+    """slack 3 (every layer truncation LocalARS, the reference's default): GPU
+    dealer keys byte-identical to the oracle's, outputs and exchange bytes
+    identical to the oracle's two-party evaluation on those keys (not to the
+    fixed-point forward: LocalARS is not exact)."""
+    B = 3
+    wl = synth.workload(B, synth.Dims(bw=bw, slack=3), seed=22)
+    d = _od(orc, wl.dims)
+    c = mp.Ctx(bw=bw)
+    m = mp.Model(c, wl.dims, wl.W)
+    assert m.key_bytes(B) == orc.model_key_bytes(d, B)
+    m.keygen(B, 778)
+    o0, o1 = orc.model_keygen(d, B, 778, wl.W)
+    assert np.array_equal(m.export_keys(0, B), o0)
+    assert np.array_equal(m.export_keys(1, B), o1)
+    x0, x1 = wl.shares["x"]
+    a0, a1 = wl.shares["a"]
+    m0, m1 = wl.shares["m"]
+    m.set_inputs(B, x0, x1, a0, a1, m0, m1, wl.prot)
+    c.reset_counters()
+    m.forward(B)
+    got = m.output(B)
+    want, oby = orc.model_eval(d, B, wl.W, o0, o1, x0, x1, a0, a1, m0, m1, wl.prot)
+    assert np.array_equal(got, want)
     assert c.bytes_exchanged == oby
     m.close()
     c.close()

@@ -236,3 +236,41 @@ def test_maxpool_keys_are_the_relu_gates(orc):
         r = np.concatenate([nxt, r[:, R - 1:R]], axis=1) if R % 2 else nxt
     assert off == k0.size
     assert np.array_equal(r.reshape(-1), rout)
+
+
+def local_ars_expected(x, r, bias, bw, s):
+    """floor(x/2^s) + b + e - k 2^(bw-s) (mod 2^bw): e is the carry out of the low
+    s bits of x + r, k the wrap of x + r (signed mask r) out of the signed ring."""
+    h = 1 << (bw - 1)
+    out = []
+    for xi, ri, bi in zip(x.tolist(), to_signed(r, bw).tolist(), bias.tolist()):
+        tot = xi + ri
+        k = 1 if tot >= h else (-1 if tot < -h else 0)
+        e = 1 if (xi % (1 << s)) + (ri % (1 << s)) >= (1 << s) else 0
+        out.append(((xi >> s) + bi + e - k * (1 << (bw - s))) % (1 << bw))
+    return np.array(out, dtype=np.uint64)
+
+
+@pytest.mark.parametrize("bw", [32, 64])
+def test_local_ars(orc, bw):
+    """LocalARS (TruncateType::LocalARS, gpu_mpc/ddg_orca_batched.h:180-199): no key
+    bytes, no exchange; the unmasked output is floor(x/2^s) + bias up to the carry
+    of the low bits and the wrap of x + r, both counted here from their
+    definitions (wraps included: |x| up to 2^(bw-3))."""
+    rng = np.random.default_rng(bw + 1000)
+    h = 1 << (bw - 1)
+    x = np.concatenate([np.array([-h // 4, -1, 0, 1, (1 << S) - 1, -(1 << S)], np.int64),
+                        rng.integers(-(h // 4), h // 4, size=4000, dtype=np.int64),
+                        rng.integers(-8 << S, 8 << S, size=4000)])
+    r = mask_in(rng, x.size, bw)
+    bias = rng.integers(-(1 << 14), 1 << 14, size=x.size)
+    k0, k1, rout = orc.tr_keygen(1, 1, 10, bw, S, r)
+    assert k0.size == 0 and k1.size == 0
+    full = np.uint64(mod(bw) if bw < 64 else 0xFFFFFFFFFFFFFFFF)
+    xhat = (ring(x, bw) + r) & full
+    y, by = orc.tr_eval(10, bw, S, k0, k1, xhat, bias)
+    assert by == 0
+    got = (y - rout) & full
+    assert np.array_equal(got, local_ars_expected(x, r, bias, bw, S))
+    wrapped = np.abs(x.astype(object) + to_signed(r, bw).astype(object)) >= h
+    assert wrapped.any() and not wrapped.all()

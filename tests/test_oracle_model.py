@@ -242,3 +242,29 @@ def test_adjnorm_two_party_matches_closed_form(orc, synth, bw):
     assert np.array_equal(val.astype(np.int64), want)
     # five exchanges of ring elements + one of DCF bit planes
     assert by > 0
+
+
+@pytest.mark.parametrize("bw", [32, 64])
+def test_local_truncation_model(orc, synth, bw):
+    """slack 3: every layer truncation is LocalARS (the reference's default,
+    gpu_mpc/ddg_orca_batched.h:180-199): no truncation keys (under 60% of the exact
+    key set, a RELU key per ReLU layer remains).  At bw=64
+    the outputs stay within a few units of 2^-12 of the fixed-point forward; at
+    bw=32 masked values wrap (probability ~|x|/2^32 per element) and the outputs
+    are far off, as the reference records for bw=32."""
+    wl = _wl(synth, 4, bw=bw, seed=10, slack=3)
+    d = _od(orc, wl)
+    out, code = orc.plain_forward(d, wl.X, wl.A, wl.mask, wl.prot, wl.W)
+    assert code == 0
+    k0, k1 = orc.model_keygen(d, 4, 2024, wl.W)
+    x0, x1 = wl.shares["x"]
+    a0, a1 = wl.shares["a"]
+    m0, m1 = wl.shares["m"]
+    o2, by = orc.model_eval(d, 4, wl.W, k0, k1, x0, x1, a0, a1, m0, m1, wl.prot)
+    err = np.abs(o2 - out)
+    if bw == 64:
+        assert err.max() <= 16
+    else:
+        assert err.max() > 1 << 12
+    d0 = _od(orc, _wl(synth, 4, bw=bw, seed=10, slack=0))
+    assert k0.size < 0.6 * orc.model_key_bytes(d0, 4) and by > 0
