@@ -108,7 +108,9 @@ class SecureBackend {
                               c.d_data));
   }
 
-  // ---- element-wise product (ddg_orca.h:43-63): Beaver with identity maps ----
+  // ---- element-wise fixed-point product (ddg_orca.h:43-63, keygen :176-193):
+  // Beaver product with identity maps, then truncation by the scale with slack
+  // (the reference's TrWithSlack: MPCX_TRSLACK, exact for |a*b| < 2^(bw-2)) ----
   template <class TA, class TB, class TO>
   void mul(const TA &a, const TB &b, TO &out) {
     const size_t n = a.size();
@@ -122,6 +124,7 @@ class SecureBackend {
       check(mpcx_mul_keygen(ctx_, n, n, n, idx, idx, a.d_data, b.d_data, out.d_data, seed_, gate_++, k0, k1));
     else
       check(mpcx_mul_eval(ctx_, n, n, n, idx, idx, k0, k1, a.d_data, b.d_data, out.d_data));
+    gate(MPCX_TRSLACK, out, out, nullptr, 0);
   }
 
   // ---- local linear ops (no key, no exchange) ----

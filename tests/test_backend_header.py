@@ -22,3 +22,12 @@ def test_backend_dealer_then_evaluator(bw):
     r = subprocess.run([BIN, str(bw)], capture_output=True, text=True, timeout=120)
     assert r.returncode == 0, r.stdout + r.stderr
     assert "bit-exact" in r.stdout
+
+
+@pytest.mark.gpu
+def test_backend_local_truncation():
+    """set_truncation(MPCX_LOCALARS) on the dealer and the evaluator (the reference
+    batched backend's default): keyless truncations, outputs within 1 of exact."""
+    r = subprocess.run([BIN, "64", "local"], capture_output=True, text=True, timeout=120)
+    assert r.returncode == 0, r.stdout + r.stderr
+    assert "within 1" in r.stdout
