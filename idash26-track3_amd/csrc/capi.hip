@@ -274,7 +274,7 @@ hipError_t ctx_scratch(mpcx_ctx *c, size_t bytes, void **p) {
 }
 bool valid_kind(int k) {
   return k == MPCX_TR || k == MPCX_TRRELU || k == MPCX_RELU || k == MPCX_TRSLACK || k == MPCX_RELUSLACK ||
-         k == MPCX_LOCALARS;
+         k == MPCX_LOCALARS || k == MPCX_DRELU;
 }
 }  // namespace
 
@@ -320,7 +320,7 @@ static hipError_t tr_eval_run(mpcx_ctx *c, const TrLayout &lay, size_t n, const 
   c->counters.bitplanes(n, int(lay.use_a) + int(lay.use_b));
   e = launch_tr_phase2<T>(c->L, lay, K0, K1, X, Bi, ncol, bits, bits + ww, bits + 2 * ww, bits + 3 * ww, m, m + n);
   if (e != hipSuccess) return e;
-  c->counters.msg(n, c->bw);
+  if (lay.kind != MPCX_DRELU) c->counters.msg(n, c->bw);  // DRELU: the output bit is already public
   return launch_reconstruct<T>(c->L, n, m, m + n, y);
 }
 

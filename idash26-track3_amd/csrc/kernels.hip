@@ -274,7 +274,7 @@ __device__ __forceinline__ bool relu_like(int kind) { return kind == G_RELU || k
 template <typename T>
 __device__ __forceinline__ T tr_shifted_input(const TrArgs<T> &a, size_t i) {
   T x = a.xhat[i];
-  if (!relu_like(a.kind) && a.bias) x += T(a.bias[uint32_t(i % uint32_t(a.bias_ncol))]) << a.s;
+  if (!relu_like(a.kind) && a.kind != G_DRELU && a.bias) x += T(a.bias[uint32_t(i % uint32_t(a.bias_ncol))]) << a.s;
   return x + (T(1) << a.sb);
 }
 
@@ -343,6 +343,8 @@ __global__ void k_tr_phase2(TrArgs<T> a) {
       const T k = kap[i];
       const T cp = z ? T(one0 - k) : k;
       y = cp * A + G[size_t(c) * a.N + i];
+    } else if (a.kind == G_DRELU) {  // the public masked bit; party 0 carries it
+      y = one0 * T(h ^ bh);
     } else if (relu_like(a.kind)) {
       const uint32_t z = h ^ bh;
       const T k = kap[i];
@@ -368,7 +370,7 @@ __global__ void k_tr_keygen(TrArgs<T> a) {
   const T smask = (T(1) << s) - T(1);
   T *G0 = reinterpret_cast<T *>(a.w0 + a.off_g);
   T *G1 = reinterpret_cast<T *>(a.w1 + a.off_g);
-  const int ncase = relu_like(a.kind) ? 2 : 8;
+  const int ncase = a.kind == G_DRELU ? 0 : relu_like(a.kind) ? 2 : 8;
   for (size_t base = size_t(blockIdx.x) * blockDim.x + (threadIdx.x & ~63u); base < a.N; base += stride) {
     const size_t i = base + lane_id();
     uint32_t za0 = 0, za1 = 0, zb0 = 0, zb1 = 0;
@@ -379,8 +381,8 @@ __global__ void k_tr_keygen(TrArgs<T> a) {
       const uint32_t rbi = aes.prf(a.kd, a.gate, F_DCFA + 3, i).x & 1u;
       const uint32_t rdi = aes.prf(a.kd, a.gate, F_DCFB + 3, i).x & 1u;
       const T rout = ring_of<T>(aes.prf(a.kd, a.gate, F_ROUT, i));
-      a.out_mask[i] = rout;
       const uint32_t kappa = rho ^ rbi;
+      a.out_mask[i] = a.kind == G_DRELU ? T(kappa) : rout;  // DRELU: the mask of the output bit
       for (int c = 0; c < ncase; c++) {
         T Gv;
         if (a.kind == G_TR || a.kind == G_TRRELU) {

@@ -26,7 +26,8 @@ enum GateKind : int {
   G_RELU = 3,        // ReLU without truncation
   G_TRSLACK = 4,     // exact truncation for |x| < 2^(bw-2)
   G_RELUSLACK = 9,   // ReLU for |x| < 2^(bw-2-s): a (bw-2-s)-bit DCF (after TRSLACK)
-  G_LOCALARS = 10    // local arithmetic shift of the masked value and its mask (no key)
+  G_LOCALARS = 10,   // local arithmetic shift of the masked value and its mask (no key)
+  G_DRELU = 11       // [x >= 0] as a masked public bit: one (bw-1)-bit DCF, one round
 };
 
 enum Field : uint32_t {
@@ -91,7 +92,7 @@ inline TrLayout tr_layout(int kind, int bw, int s, size_t N, size_t base) {
     return t;
   }
   t.use_a = kind != G_TRSLACK;
-  t.use_b = kind != G_RELU && kind != G_RELUSLACK;
+  t.use_b = kind != G_RELU && kind != G_RELUSLACK && kind != G_DRELU;
   const size_t tb = size_t(bw) / 8;
   size_t o = align_up(base);
   if (t.use_a) {
@@ -106,7 +107,7 @@ inline TrLayout tr_layout(int kind, int bw, int s, size_t N, size_t base) {
     t.off_kappa = o;
     o = align_up(o + N * tb);
   }
-  t.ncase = kind == G_RELU || kind == G_RELUSLACK ? 2 : 8;
+  t.ncase = kind == G_DRELU ? 0 : kind == G_RELU || kind == G_RELUSLACK ? 2 : 8;
   t.off_g = o;
   o = align_up(o + size_t(t.ncase) * N * tb);
   t.end = o;

@@ -45,6 +45,11 @@ typedef struct mpcx_model mpcx_model;
                             value and its mask are shifted locally (arithmetic shift), no key
                             bytes, no exchange; floor(x/2^s) + bias + e, e in {0, 1}, or off by
                             2^(bw-s) when x + r leaves the signed ring (probability ~|x|/2^bw) */
+#define MPCX_DRELU 11   /* DReLU, [x >= 0] (gpuKeyGenDRelu / the DReLU half of gpuRelu,
+                           gpu_mpc/dpf_dcf_adapter.h:32-36, 97-104, 330): one (bw-1)-bit DCF and
+                           one bit-plane round; the output is a masked public bit held as a ring
+                           element 0/1, keygen's output "mask" is the mask bit (0/1): the
+                           DReLU bit is yhat XOR mask */
 
 /* ---------------- context ----------------
  * Replaces the evaluator/dealer constructors DDGOrcaBase(party, ip, bw, scale)

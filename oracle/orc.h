@@ -90,8 +90,10 @@ enum {
   ORC_G_SXS = 7,      /* batched secret x secret ring GEMM              */
   ORC_G_REVEAL = 8,   /* additive shares -> masked public               */
   ORC_G_RELUSLACK = 9, /* ReLU for |x| < 2^(bw-2-s) (a (bw-2-s)-bit DCF) */
-  ORC_G_LOCALARS = 10  /* local arithmetic shift of the masked value and of
+  ORC_G_LOCALARS = 10, /* local arithmetic shift of the masked value and of
                           its mask: no key, no exchange, error +1 or a wrap */
+  ORC_G_DRELU = 11     /* [x >= 0] as a masked public bit (0/1 ring element),
+                          mask bit returned by keygen: one (bw-1)-bit DCF */
 };
 
 /* Dealer randomness fields. */

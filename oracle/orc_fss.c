@@ -151,7 +151,8 @@ orc_tr_layout orc_tr_layout_make(int kind, int bw, int s, size_t N, size_t base)
   }
   size_t o = orc_align(base);
   size_t tb = (size_t)bw / 8;
-  if (kind == ORC_G_TR || kind == ORC_G_TRRELU || kind == ORC_G_RELU || kind == ORC_G_RELUSLACK) {
+  if (kind == ORC_G_TR || kind == ORC_G_TRRELU || kind == ORC_G_RELU || kind == ORC_G_RELUSLACK ||
+      kind == ORC_G_DRELU) {
     T.a = orc_dcf_layout_make(orc_sign_bit(kind, bw, s), N, o, 1);
     o = T.a.end;
   }
@@ -163,7 +164,7 @@ orc_tr_layout orc_tr_layout_make(int kind, int bw, int s, size_t N, size_t base)
     T.off_kappa = o;
     o = orc_align(o + N * tb);
   }
-  T.ncase = (kind == ORC_G_RELU || kind == ORC_G_RELUSLACK) ? 2 : 8;
+  T.ncase = kind == ORC_G_DRELU ? 0 : (kind == ORC_G_RELU || kind == ORC_G_RELUSLACK) ? 2 : 8;
   T.off_g = o;
   o = orc_align(o + (size_t)T.ncase * N * tb);
   T.end = o;
@@ -349,6 +350,7 @@ void orc_tr_keygen(uint64_t seed, uint32_t gate, int kind, int bw, int s, size_t
   const uint64_t M = rmask(bw);
   const int n = bw, sb = orc_sign_bit(kind, bw, s);
   const int relu_like = kind == ORC_G_RELU || kind == ORC_G_RELUSLACK;
+  const int no_b = relu_like || kind == ORC_G_DRELU; /* no s-bit DCF */
   const uint64_t lowmask = (1ull << sb) - 1ull;
   const uint64_t smask = (1ull << s) - 1ull;
   uint8_t *rb = (uint8_t *)calloc(N, 1), *rd = (uint8_t *)calloc(N, 1);
@@ -365,8 +367,9 @@ void orc_tr_keygen(uint64_t seed, uint32_t gate, int kind, int bw, int s, size_t
     aa[i] = r & lowmask;
     ab[i] = r & smask;
     uint64_t rout = prf_ring(&P, gate, ORC_F_ROUT, i, bw);
-    out_mask[i] = rout;
     int kappa = rho ^ rbi;
+    /* DRELU: the output is the public bit h ^ c^, whose mask is kappa */
+    out_mask[i] = kind == ORC_G_DRELU ? (uint64_t)kappa : rout;
     for (int c = 0; c < T.ncase; c++) {
       uint64_t G = 0;
       if (kind == ORC_G_TR || kind == ORC_G_TRRELU) {
@@ -401,7 +404,7 @@ void orc_tr_keygen(uint64_t seed, uint32_t gate, int kind, int bw, int s, size_t
     }
   }
   if (kind != ORC_G_TRSLACK) orc_dcf_keygen(seed, gate, ORC_F_DCFA, sb, N, aa, rb, k0, k1, T.a.off_root);
-  if (!relu_like) orc_dcf_keygen(seed, gate, ORC_F_DCFB, s, N, ab, rd, k0, k1, T.b.off_root);
+  if (!no_b) orc_dcf_keygen(seed, gate, ORC_F_DCFB, s, N, ab, rd, k0, k1, T.b.off_root);
   free(rb);
   free(rd);
   free(aa);
@@ -421,7 +424,7 @@ void orc_tr_eval(int kind, int bw, int s, size_t N, const uint8_t *k0, const uin
   const int relu_like = kind == ORC_G_RELU || kind == ORC_G_RELUSLACK;
   const uint64_t lowmask = (1ull << sb) - 1ull;
   const uint64_t smask = (1ull << s) - 1ull;
-  const int use_a = kind != ORC_G_TRSLACK, use_b = !relu_like;
+  const int use_a = kind != ORC_G_TRSLACK, use_b = !relu_like && kind != ORC_G_DRELU;
   uint8_t *bb[2], *dd[2];
   for (int p = 0; p < 2; p++) {
     bb[p] = (uint8_t *)calloc(N, 1);
@@ -432,7 +435,7 @@ void orc_tr_eval(int kind, int bw, int s, size_t N, const uint8_t *k0, const uin
   for (int p = 0; p < 2; p++) {
     OMP_FOR
     for (size_t i = 0; i < N; i++) {
-      uint64_t b = (!relu_like && bias_elem) ? ((uint64_t)bias_elem[i] << s) : 0;
+      uint64_t b = (use_b && bias_elem) ? ((uint64_t)bias_elem[i] << s) : 0;
       uint64_t xp = (xhat[i] + b + (1ull << sb)) & M;
       if (use_a) bb[p][i] = (uint8_t)orc_dcf_eval1(p, K[p], &T.a, i, xp & lowmask);
       if (use_b) dd[p][i] = (uint8_t)orc_dcf_eval1(p, K[p], &T.b, i, xp & smask);
@@ -445,7 +448,7 @@ void orc_tr_eval(int kind, int bw, int s, size_t N, const uint8_t *k0, const uin
   for (int p = 0; p < 2; p++) {
     OMP_FOR
     for (size_t i = 0; i < N; i++) {
-      uint64_t b = (!relu_like && bias_elem) ? ((uint64_t)bias_elem[i] << s) : 0;
+      uint64_t b = (use_b && bias_elem) ? ((uint64_t)bias_elem[i] << s) : 0;
       uint64_t xp = (xhat[i] + b + (1ull << sb)) & M;
       int h = (int)((xp >> sb) & 1u);
       int bh = bb[0][i] ^ bb[1][i];
@@ -463,6 +466,8 @@ void orc_tr_eval(int kind, int bw, int s, size_t N, const uint8_t *k0, const uin
         } else {
           out = (p == 0 ? A : 0) + G;
         }
+      } else if (kind == ORC_G_DRELU) { /* public: party 0 carries it, no message */
+        out = p == 0 ? (uint64_t)(h ^ bh) : 0;
       } else if (relu_like) {
         int z = h ^ bh;
         uint64_t G = get_t(K[p], T.off_g, (size_t)z * N + i, bw);
@@ -478,7 +483,7 @@ void orc_tr_eval(int kind, int bw, int s, size_t N, const uint8_t *k0, const uin
       y[p][i] = out & M;
     }
   }
-  if (bytes) *bytes += 2ull * N * (uint64_t)(bw / 8);
+  if (bytes && kind != ORC_G_DRELU) *bytes += 2ull * N * (uint64_t)(bw / 8);
   for (size_t i = 0; i < N; i++) yhat[i] = (y[0][i] + y[1][i]) & M;
   for (int p = 0; p < 2; p++) {
     free(bb[p]);

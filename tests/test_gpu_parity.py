@@ -163,6 +163,29 @@ def test_local_ars_matches_oracle(ctx, orc):
     assert np.array_equal(y.astype(np.uint64), oy)
 
 
+def test_drelu_keys_and_eval(ctx, orc):
+    """DReLU gate: keys byte-identical to the oracle's, masked bits and exchange
+    bytes identical, masked bit XOR mask bit = [x >= 0] (ring edges included)."""
+    bw = ctx.bw
+    rng = np.random.default_rng(bw + 12)
+    h = 1 << (bw - 1)
+    x = np.concatenate([np.array([-h, -h + 1, -1, 0, 1, h - 1], np.int64),
+                        rng.integers(-h, h, size=20000, dtype=np.int64)])
+    rin = rmask(rng, x.size, bw)
+    g0, g1, grbit = ctx.tr_keygen(11, rin, seed=4, gate=9)
+    o0, o1, orbit = orc.tr_keygen(4, 9, 11, bw, S, rin)
+    assert ctx.lib.mpcx_tr_key_bytes(ctx.h, 11, x.size) == o0.size
+    assert np.array_equal(grbit.astype(np.uint64), orbit)
+    assert np.array_equal(host(g0)[:o0.size], o0) and np.array_equal(host(g1)[:o1.size], o1)
+    xhat = (x.astype(np.uint64) + rin) & M(bw)
+    ctx.reset_counters()
+    y = ctx.tr_eval(11, g0, g1, xhat)
+    oy, oby = orc.tr_eval(11, bw, S, o0, o1, xhat)
+    assert ctx.bytes_exchanged == oby
+    assert np.array_equal(y.astype(np.uint64), oy)
+    assert np.array_equal(y.astype(np.uint64) ^ orbit, (x >= 0).astype(np.uint64))
+
+
 def test_all_aes_variants_agree(mp, orc):
     c = mp.Ctx(bw=32)
     rng = np.random.default_rng(4)

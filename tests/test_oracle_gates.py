@@ -274,3 +274,23 @@ def test_local_ars(orc, bw):
     assert np.array_equal(got, local_ars_expected(x, r, bias, bw, S))
     wrapped = np.abs(x.astype(object) + to_signed(r, bw).astype(object)) >= h
     assert wrapped.any() and not wrapped.all()
+
+
+@pytest.mark.parametrize("bw", [32, 64])
+def test_drelu(orc, bw):
+    """DReLU (gpuKeyGenDRelu, gpu_mpc/dpf_dcf_adapter.h:32-36, 330): the masked
+    public bit XOR the dealer's mask bit is [x >= 0] over the signed ring, edges
+    included; one bit plane each way, no ring message."""
+    rng = np.random.default_rng(bw + 11)
+    h = 1 << (bw - 1)
+    x = np.concatenate([np.array([-h, -h + 1, -1, 0, 1, h - 1], np.int64),
+                        rng.integers(-h, h, size=3000, dtype=np.int64),
+                        rng.integers(-4, 4, size=500)])
+    r = mask_in(rng, x.size, bw)
+    k0, k1, rbit = orc.tr_keygen(4, 9, 11, bw, S, r)
+    assert set(np.unique(rbit).tolist()) <= {0, 1}
+    full = np.uint64(mod(bw) if bw < 64 else 0xFFFFFFFFFFFFFFFF)
+    xhat = (ring(x, bw) + r) & full
+    y, by = orc.tr_eval(11, bw, S, k0, k1, xhat)
+    assert np.array_equal(y ^ rbit, (x >= 0).astype(np.uint64))
+    assert by == 2 * ((x.size + 31) // 32) * 4
