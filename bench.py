@@ -289,7 +289,7 @@ def run_stream(args):
     ctx = mpcx.Ctx(bw=bw, scale=dims.s)
     model = mpcx.Model(ctx, dims, W)
     kb = model.key_bytes(B)
-    ku = model.unique_key_bytes(B, 1)
+    ku0, ku = model.unique_key_bytes(B, 0), model.unique_key_bytes(B, 1)
     h0 = h1 = None
     if args.key_files:
         # distinct dealer key sets in two files (party 0's arenas, party 1's
@@ -299,23 +299,24 @@ def run_stream(args):
         t0 = time.time()
         for k in range(args.sets):
             model.keygen(B, 0xBEEF + args.seed + k)
-            model.write_keys(0, f0, append=k > 0)
+            model.write_keys(0, f0, packed=True, append=k > 0)
             model.write_keys(1, f1, packed=True, append=k > 0)
-            log(f"[stream] key set {k + 1}/{args.sets} written ({(kb + ku) / 1e9:.1f} GB), {time.time() - t0:.1f}s")
+            log(f"[stream] key set {k + 1}/{args.sets} written ({(ku0 + ku) / 1e9:.1f} GB), {time.time() - t0:.1f}s")
         model.release_arena()
         model.attach_key_files(B, f0, f1, int(args.slot_gb * 2 ** 30))
-        host_key_bytes = kb + ku
+        host_key_bytes = ku0 + ku
     else:
         t0 = time.time()
         model.keygen(B, 0xBEEF + args.seed)
         log(f"[stream] dealer: {2 * kb / 1e9:.1f} GB of keys for B={B} in {time.time() - t0:.1f}s")
-        # party 0's whole arena and party 1's unique planes (the correction words
-        # both parties hold are stored once): what fits the host's pinned memory
+        # both parties' packed keys: the correction words both parties hold are
+        # stored once (party 0's), and the planes the dealer drew from a party's
+        # own PRF key are expanded on the device after each chunk's copy
         t0 = time.time()
-        h0, h1 = mpcx.PinnedBuffer(kb), mpcx.PinnedBuffer(ku)
+        h0, h1 = mpcx.PinnedBuffer(ku0), mpcx.PinnedBuffer(ku)
         log(f"[stream] pinned host buffers ({(h0.nbytes + h1.nbytes) / 1e9:.1f} GB) in {time.time() - t0:.1f}s")
         t0 = time.time()
-        model.export_keys(0, B, into=h0)
+        model.export_unique_keys(0, B, into=h0)
         model.export_unique_keys(1, B, into=h1)
         model.release_arena()
         log(f"[stream] keys exported to host in {time.time() - t0:.1f}s")

@@ -70,6 +70,48 @@ AesRK dealer_key(uint64_t seed) {
   return aes_expand(k);
 }
 
+// FIPS-197 encryption of one block on the host (columns as little-endian words,
+// the device code's state layout); used only to derive the parties' PRF keys.
+static void aes_encrypt_host(const AesRK &rk, const uint32_t in[4], uint32_t out[4]) {
+  auto xt = [](uint8_t a) { return uint8_t((a << 1) ^ ((a & 0x80) ? 0x1b : 0)); };
+  uint8_t st[16];
+  for (int j = 0; j < 4; j++)
+    for (int b = 0; b < 4; b++) st[4 * j + b] = uint8_t((in[j] ^ rk.w[j]) >> (8 * b));
+  for (int r = 1; r <= 10; r++) {
+    uint8_t u[16];
+    for (int j = 0; j < 4; j++)  // SubBytes + ShiftRows: row b of column j from column j + b
+      for (int b = 0; b < 4; b++) u[4 * j + b] = kSbox[st[4 * ((j + b) & 3) + b]];
+    if (r < 10)
+      for (int j = 0; j < 4; j++) {  // MixColumns
+        const uint8_t a0 = u[4 * j], a1 = u[4 * j + 1], a2 = u[4 * j + 2], a3 = u[4 * j + 3];
+        u[4 * j + 0] = uint8_t(xt(a0) ^ xt(a1) ^ a1 ^ a2 ^ a3);
+        u[4 * j + 1] = uint8_t(a0 ^ xt(a1) ^ xt(a2) ^ a2 ^ a3);
+        u[4 * j + 2] = uint8_t(a0 ^ a1 ^ xt(a2) ^ xt(a3) ^ a3);
+        u[4 * j + 3] = uint8_t(xt(a0) ^ a0 ^ a1 ^ a2 ^ xt(a3));
+      }
+    for (int j = 0; j < 4; j++)
+      for (int b = 0; b < 4; b++) st[4 * j + b] = uint8_t(u[4 * j + b] ^ (rk.w[4 * r + j] >> (8 * b)));
+  }
+  for (int j = 0; j < 4; j++)
+    out[j] = uint32_t(st[4 * j]) | (uint32_t(st[4 * j + 1]) << 8) | (uint32_t(st[4 * j + 2]) << 16) |
+             (uint32_t(st[4 * j + 3]) << 24);
+}
+
+void party_key_bytes(uint64_t seed, int party, uint8_t out[16]) {
+  const AesRK kd = dealer_key(seed);
+  const uint32_t in[4] = {uint32_t(party), 0u, uint32_t(F_PARTY), 0xFFFFFFFFu};
+  uint32_t w[4];
+  aes_encrypt_host(kd, in, w);
+  for (int j = 0; j < 4; j++)
+    for (int b = 0; b < 4; b++) out[4 * j + b] = uint8_t(w[j] >> (8 * b));
+}
+
+AesRK party_key(uint64_t seed, int party) {
+  uint8_t k[16];
+  party_key_bytes(seed, party, k);
+  return aes_expand(k);
+}
+
 }  // namespace mpcx
 
 using namespace mpcx;
@@ -871,7 +913,7 @@ mpcx_status mpcx_model_release_arena(mpcx_model *m) {
 mpcx_status mpcx_model_attach_host_keys(mpcx_model *m, int B, const void *k0, size_t bytes0, const void *k1,
                                         size_t bytes1, size_t slot_bytes) {
   if (!m || !k0 || !k1) return MPCX_EINVAL;
-  if (B < 1 || bytes0 != mpcx_model_key_bytes(m, B) ||
+  if (B < 1 || (bytes0 != mpcx_model_key_bytes(m, B) && bytes0 != mpcx_model_unique_key_bytes(m, B, 0)) ||
       (bytes1 != mpcx_model_key_bytes(m, B) && bytes1 != mpcx_model_unique_key_bytes(m, B, 1)))
     return fail(m->ctx, MPCX_EINVAL, "attach_host_keys: key size mismatch");
   hipError_t e = guard([&] { return m->impl->attach_host_keys(B, k0, bytes0, k1, bytes1, slot_bytes); });
@@ -882,9 +924,11 @@ mpcx_status mpcx_model_attach_host_keys(mpcx_model *m, int B, const void *k0, si
 }
 
 mpcx_status mpcx_model_write_keys(mpcx_model *m, int party, int packed, const char *path, int append) {
-  if (!m || !path || (party != 0 && party != 1) || (packed && party != 1)) return MPCX_EINVAL;
+  if (!m || !path || (party != 0 && party != 1)) return MPCX_EINVAL;
   hipError_t e = guard([&] { return m->impl->write_keys(party, packed != 0, path, append != 0); });
   if (e == hipErrorInvalidValue) return fail(m->ctx, MPCX_ESTATE, "write_keys: no resident keys");
+  if (e == hipErrorNotSupported)
+    return fail(m->ctx, MPCX_ESTATE, "write_keys: packed keys need keys from mpcx_model_keygen (imported keys)");
   if (e == hipErrorFileNotFound) return fail(m->ctx, MPCX_EIO, std::string("write_keys: cannot write ") + path);
   HIPC(m->ctx, e, "model_write_keys");
   return MPCX_OK;
@@ -910,7 +954,10 @@ size_t mpcx_model_unique_key_bytes(const mpcx_model *m, int B, int party) {
 
 mpcx_status mpcx_model_export_unique_keys(mpcx_model *m, int party, void *dst, size_t bytes) {
   if (!m || !dst || (party != 0 && party != 1)) return MPCX_EINVAL;
-  HIPC(m->ctx, guard([&] { return m->impl->export_unique_keys(party, dst, bytes); }), "model_export_unique_keys");
+  hipError_t e = guard([&] { return m->impl->export_unique_keys(party, dst, bytes); });
+  if (e == hipErrorNotSupported)
+    return fail(m->ctx, MPCX_ESTATE, "export_unique_keys: packed keys need keys from mpcx_model_keygen");
+  HIPC(m->ctx, e, "model_export_unique_keys");
   return MPCX_OK;
 }
 

@@ -49,18 +49,14 @@ struct DcfGenOut {
   uint4 leafcw;  // leaf correction word
 };
 
-// Dealer walk for one element.  Writes the root seeds, level correction words
-// (level-major, stride N) and the leaf correction word of both parties.
+// Dealer walk for one element from the parties' root seeds s0 (lsb 0) and s1
+// (lsb 1): writes the roots, the level correction words (level-major, stride N)
+// and the leaf correction word of both parties.
 template <class A>
-__device__ __forceinline__ DcfGenOut dcf_gen_walk(const A &aes, const AesRK &kd, uint32_t gate, uint32_t fb, int m, int L,
-                                                  uint64_t alpha, size_t i, size_t N, uint8_t *k0,
-                                                  uint8_t *k1, size_t off_root, size_t off_cw,
-                                                  size_t off_leaf) {
-  uint4 s0 = aes.prf(kd, gate, fb + 0, i);
-  s0.x &= ~1u;
-  uint4 D = aes.prf(kd, gate, fb + 1, i);
-  D.x |= 1u;
-  uint4 s1 = xor4(s0, D);
+__device__ __forceinline__ DcfGenOut dcf_gen_roots(const A &aes, uint4 s0, uint4 s1, int m, int L, uint64_t alpha,
+                                                   size_t i, size_t N, uint8_t *k0, uint8_t *k1, size_t off_root,
+                                                   size_t off_cw, size_t off_leaf) {
+  const uint4 D = xor4(s0, s1);
   reinterpret_cast<uint4 *>(k0 + off_root)[i] = s0;
   reinterpret_cast<uint4 *>(k1 + off_root)[i] = s1;
   uint32_t t0 = 0, t1 = 1;
@@ -94,6 +90,29 @@ __device__ __forceinline__ DcfGenOut dcf_gen_walk(const A &aes, const AesRK &kd,
   o.t0 = t0;
   o.leafcw = lcw;
   return o;
+}
+
+// The same with the roots drawn from the dealer PRF: s0 = PRF(fb) with lsb 0,
+// s1 = s0 ^ D, D = PRF(fb + 1) with lsb 1.
+template <class A>
+__device__ __forceinline__ DcfGenOut dcf_gen_walk(const A &aes, const AesRK &kd, uint32_t gate, uint32_t fb, int m, int L,
+                                                  uint64_t alpha, size_t i, size_t N, uint8_t *k0,
+                                                  uint8_t *k1, size_t off_root, size_t off_cw,
+                                                  size_t off_leaf) {
+  uint4 s0 = aes.prf(kd, gate, fb + 0, i);
+  s0.x &= ~1u;
+  uint4 D = aes.prf(kd, gate, fb + 1, i);
+  D.x |= 1u;
+  return dcf_gen_roots(aes, s0, xor4(s0, D), m, L, alpha, i, N, k0, k1, off_root, off_cw, off_leaf);
+}
+
+// Root seed of party p for a DCF drawn from the party's own PRF key: lsb = p.
+template <class A>
+__device__ __forceinline__ uint4 party_root(const A &aes, const AesRK &kp, int p, uint32_t gate, uint32_t fb,
+                                            size_t i) {
+  uint4 s = aes.prf(kp, gate, fb + 0, i);
+  s.x = (s.x & ~1u) | uint32_t(p);
+  return s;
 }
 
 }  // namespace mpcx

@@ -57,6 +57,13 @@ struct TrPlan {
 template <typename T>
 hipError_t launch_tr_keygen(const Launch &L, const TrLayout &lay, uint64_t seed, uint32_t gate, const T *in_mask,
                             T *out_mask, uint8_t *k0, uint8_t *k1);
+// Regenerates into key (laid out by lay) the planes of party p's key of a
+// truncation-family gate that keygen drew from the party's own PRF key
+// (party_key): its DCF roots and output-mask bits, and for party 0 its shares
+// of kappa and of the G table.
+template <typename T>
+hipError_t launch_tr_expand(const Launch &L, const TrLayout &lay, const uint8_t party_key16[16], uint32_t gate,
+                            int party, uint8_t *key);
 // phase 1: DCF evaluation, writes bit messages bits_a[p], bits_b[p] (zwords(N) u32 each)
 template <typename T>
 hipError_t launch_tr_phase1(const Launch &L, const TrLayout &lay, const uint8_t *k0, const uint8_t *k1,

@@ -250,6 +250,7 @@ hipError_t launch_dcf_eval(const Launch &L, int party, int m, size_t n, const ui
 template <typename T>
 struct TrArgs {
   AesRK kd;
+  AesRK kp[2];  // the parties' own PRF keys (keygen and seeded-plane expansion)
   int kind, n, s;
   int sb;  // sign bit of the shifted input (tr_sign_bit)
   size_t N;
@@ -378,8 +379,17 @@ __global__ void k_tr_keygen(TrArgs<T> a) {
       const T r = a.in_mask[i];
       const uint32_t rho = uint32_t(r >> a.sb) & 1u;
       const T R = r >> s;
-      const uint32_t rbi = aes.prf(a.kd, a.gate, F_DCFA + 3, i).x & 1u;
-      const uint32_t rdi = aes.prf(a.kd, a.gate, F_DCFB + 3, i).x & 1u;
+      // each party's output-mask bit of a DCF comes from its own PRF key; the
+      // DCF output mask is their XOR
+      if (a.use_a) {
+        za0 = aes.prf(a.kp[0], a.gate, F_DCFA + 2, i).x & 1u;
+        za1 = aes.prf(a.kp[1], a.gate, F_DCFA + 2, i).x & 1u;
+      }
+      if (a.use_b) {
+        zb0 = aes.prf(a.kp[0], a.gate, F_DCFB + 2, i).x & 1u;
+        zb1 = aes.prf(a.kp[1], a.gate, F_DCFB + 2, i).x & 1u;
+      }
+      const uint32_t rbi = za0 ^ za1, rdi = zb0 ^ zb1;
       const T rout = ring_of<T>(aes.prf(a.kd, a.gate, F_ROUT, i));
       const uint32_t kappa = rho ^ rbi;
       a.out_mask[i] = a.kind == G_DRELU ? T(kappa) : rout;  // DRELU: the mask of the output bit
@@ -405,27 +415,23 @@ __global__ void k_tr_keygen(TrArgs<T> a) {
           const uint32_t w = Hh < R2 ? 1u : 0u;
           Gv = rout - R - T(d) + (T(w) << (n - s));
         }
-        const T g0 = ring_of<T>(aes.prf(a.kd, a.gate, F_SPLIT + uint32_t(c), i));
+        const T g0 = ring_of<T>(aes.prf(a.kp[0], a.gate, F_SPLIT + uint32_t(c), i));
         G0[size_t(c) * a.N + i] = g0;
         G1[size_t(c) * a.N + i] = Gv - g0;
       }
       if (a.kind == G_TRRELU || relu_like(a.kind)) {
-        const T q0 = ring_of<T>(aes.prf(a.kd, a.gate, F_SPLIT + 8, i));
+        const T q0 = ring_of<T>(aes.prf(a.kp[0], a.gate, F_SPLIT + 8, i));
         reinterpret_cast<T *>(a.w0 + a.off_kappa)[i] = q0;
         reinterpret_cast<T *>(a.w1 + a.off_kappa)[i] = T(kappa) - q0;
       }
-      if (a.use_a) {
-        dcf_gen_walk(aes, a.kd, a.gate, F_DCFA, a.a.m, a.a.L, uint64_t(r & lowmask), i, a.N, a.w0,
-                     a.w1, a.a.off_root, a.a.off_cw, a.a.off_leaf);
-        za0 = aes.prf(a.kd, a.gate, F_DCFA + 2, i).x & 1u;
-        za1 = za0 ^ rbi;
-      }
-      if (a.use_b) {
-        dcf_gen_walk(aes, a.kd, a.gate, F_DCFB, a.b.m, a.b.L, uint64_t(r & smask), i, a.N, a.w0,
-                     a.w1, a.b.off_root, a.b.off_cw, a.b.off_leaf);
-        zb0 = aes.prf(a.kd, a.gate, F_DCFB + 2, i).x & 1u;
-        zb1 = zb0 ^ rdi;
-      }
+      if (a.use_a)
+        dcf_gen_roots(aes, party_root(aes, a.kp[0], 0, a.gate, F_DCFA, i),
+                      party_root(aes, a.kp[1], 1, a.gate, F_DCFA, i), a.a.m, a.a.L, uint64_t(r & lowmask), i, a.N,
+                      a.w0, a.w1, a.a.off_root, a.a.off_cw, a.a.off_leaf);
+      if (a.use_b)
+        dcf_gen_roots(aes, party_root(aes, a.kp[0], 0, a.gate, F_DCFB, i),
+                      party_root(aes, a.kp[1], 1, a.gate, F_DCFB, i), a.b.m, a.b.L, uint64_t(r & smask), i, a.N,
+                      a.w0, a.w1, a.b.off_root, a.b.off_cw, a.b.off_leaf);
     }
     const uint64_t wa0 = __ballot(za0), wa1 = __ballot(za1), wb0 = __ballot(zb0), wb1 = __ballot(zb1);
     if (lane_id() == 0) {
@@ -465,6 +471,8 @@ hipError_t launch_tr_keygen(const Launch &L, const TrLayout &lay, uint64_t seed,
   if (lay.bw != int(8 * sizeof(T))) return hipErrorInvalidValue;
   TrArgs<T> a = tr_args<T>(lay);
   a.kd = dealer_key(seed);
+  a.kp[0] = party_key(seed, 0);
+  a.kp[1] = party_key(seed, 1);
   a.gate = gate;
   a.w0 = k0;
   a.w1 = k1;
@@ -502,6 +510,61 @@ hipError_t launch_tr_phase1(const Launch &L, const TrLayout &lay, const uint8_t 
       hipLaunchKernelGGL((k_tr_phase1<T, NT, REP, 1>), dim3(grid, 2), dim3(block), 0, L.stream, a);
     else
       hipLaunchKernelGGL((k_tr_phase1<T, NT, REP, 0>), dim3(grid, 2), dim3(block), 0, L.stream, a);
+    return hipGetLastError();
+  });
+}
+
+template <typename T, int NT, int REP>
+__global__ void k_tr_expand(TrArgs<T> a, int p) {
+  __shared__ uint32_t lds[AesLds<NT, REP>::kWords];
+  AesLds<NT, REP>::fill(lds);
+  AesLds<NT, REP> aes(lds);
+  const AesRK &kp = a.kp[0];
+  uint8_t *w = a.w0;
+  const size_t stride = size_t(gridDim.x) * blockDim.x;
+  const int ncase = a.kind == G_DRELU ? 0 : relu_like(a.kind) ? 2 : 8;
+  const bool kappa = a.kind == G_TRRELU || relu_like(a.kind);
+  for (size_t base = size_t(blockIdx.x) * blockDim.x + (threadIdx.x & ~63u); base < a.N; base += stride) {
+    const size_t i = base + lane_id();
+    uint32_t za = 0, zb = 0;
+    if (i < a.N) {
+      if (a.use_a) {
+        reinterpret_cast<uint4 *>(w + a.a.off_root)[i] = party_root(aes, kp, p, a.gate, F_DCFA, i);
+        za = aes.prf(kp, a.gate, F_DCFA + 2, i).x & 1u;
+      }
+      if (a.use_b) {
+        reinterpret_cast<uint4 *>(w + a.b.off_root)[i] = party_root(aes, kp, p, a.gate, F_DCFB, i);
+        zb = aes.prf(kp, a.gate, F_DCFB + 2, i).x & 1u;
+      }
+      if (p == 0) {
+        T *G0 = reinterpret_cast<T *>(w + a.off_g);
+        for (int c = 0; c < ncase; c++)
+          G0[size_t(c) * a.N + i] = ring_of<T>(aes.prf(kp, a.gate, F_SPLIT + uint32_t(c), i));
+        if (kappa) reinterpret_cast<T *>(w + a.off_kappa)[i] = ring_of<T>(aes.prf(kp, a.gate, F_SPLIT + 8, i));
+      }
+    }
+    const uint64_t wa = __ballot(za), wb = __ballot(zb);
+    if (lane_id() == 0) {
+      if (a.use_a) reinterpret_cast<uint64_t *>(w + a.a.off_z)[base >> 6] = wa;
+      if (a.use_b) reinterpret_cast<uint64_t *>(w + a.b.off_z)[base >> 6] = wb;
+    }
+  }
+}
+
+template <typename T>
+hipError_t launch_tr_expand(const Launch &L, const TrLayout &lay, const uint8_t party_key16[16], uint32_t gate,
+                            int party, uint8_t *key) {
+  if (lay.bw != int(8 * sizeof(T)) || (party != 0 && party != 1)) return hipErrorInvalidValue;
+  if (lay.N == 0 || lay.kind == G_LOCALARS) return hipSuccess;
+  TrArgs<T> a = tr_args<T>(lay);
+  a.kp[0] = aes_expand(party_key16);
+  a.gate = gate;
+  a.w0 = key;
+  return with_variant(L, [&](auto v) {
+    constexpr int NT = decltype(v)::nt, REP = decltype(v)::rep;
+    int block = variant_block(L);
+    int grid = grid_for(k_tr_expand<T, NT, REP>, block, lay.N, L.num_cu);
+    hipLaunchKernelGGL((k_tr_expand<T, NT, REP>), dim3(grid), dim3(block), 0, L.stream, a, party);
     return hipGetLastError();
   });
 }
@@ -1578,6 +1641,8 @@ hipError_t launch_rowsum(const Launch &L, size_t rows, int len, const T *a, T *o
 #define INST(T)                                                                                                      \
   template hipError_t launch_tr_keygen<T>(const Launch &, const TrLayout &, uint64_t, uint32_t, const T *, T *,      \
                                           uint8_t *, uint8_t *);                                                     \
+  template hipError_t launch_tr_expand<T>(const Launch &, const TrLayout &, const uint8_t *, uint32_t, int,          \
+                                          uint8_t *);                                                                \
   template hipError_t launch_tr_phase1<T>(const Launch &, const TrLayout &, const uint8_t *, const uint8_t *,        \
                                           const T *, const T *, int, uint64_t *, uint64_t *, uint64_t *,             \
                                           uint64_t *);                                                               \

@@ -90,23 +90,24 @@ class ModelBase {
   virtual hipError_t import_keys(int B, const void *k0, const void *k1, size_t bytes) = 0;
   virtual hipError_t export_keys(int party, void *dst, size_t bytes) = 0;
   virtual hipError_t release_arena() = 0;
-  // Bytes of party 1's key planes that party 0 does not hold identically
-  // (its "unique" part; party 0's unique part is its whole arena).
+  // Bytes of party p's packed key: a 256-byte header holding the party's own PRF
+  // key, then its planes in arena order without those the party reads from
+  // party 0's copy (party 1: the shared DCF planes) and without those the dealer
+  // drew from the party's PRF key (expanded again on the device).
   virtual size_t unique_key_bytes(int B, int party) const = 0;
-  // Party 1's unique planes, packed back to back in arena order.
+  // Party p's packed key (keys from keygen only: imported keys carry no PRF key).
   virtual hipError_t export_unique_keys(int party, void *dst, size_t bytes) = 0;
   // Host-key (streaming) mode: keys of a batch of B in host memory (pinned for
   // asynchronous copies), copied per chunk of consecutive gates into one of two
   // device slots of slot_bytes per party while the previous chunk computes.
-  // Party 0's whole arena; party 1's arena (bytes1 = key_bytes) or its packed
-  // unique planes (bytes1 = unique_key_bytes).
+  // Each party: its arena (bytes = key_bytes) or its packed key (unique_key_bytes).
   virtual hipError_t attach_host_keys(int B, const void *h_k0, size_t bytes0, const void *h_k1, size_t bytes1,
                                       size_t slot_bytes) = 0;
   // File-backed keys: each forward reads the next key set (cycling) chunk by
   // chunk through pinned staging buffers filled by an I/O thread.
-  virtual hipError_t attach_key_files(int B, const KeyFile &f0, const KeyFile &f1, bool packed1,
+  virtual hipError_t attach_key_files(int B, const KeyFile &f0, const KeyFile &f1, bool packed0, bool packed1,
                                       size_t slot_bytes) = 0;
-  // Appends the resident key set of one party (party 1: arena or packed unique planes) to fd.
+  // Appends the resident key set of one party (arena or packed key) to fd.
   virtual hipError_t write_keys(int party, bool packed, int fd) = 0;
   virtual hipError_t set_inputs(int B, const void *x0, const void *x1, const void *a0, const void *a1,
                                 const void *m0, const void *m1, const int64_t *prot) = 0;
@@ -148,8 +149,8 @@ class LaneSet {
   hipError_t release_arena();
   hipError_t attach_host_keys(int B, const void *h_k0, size_t bytes0, const void *h_k1, size_t bytes1,
                               size_t slot_bytes);
-  // Key files of whole-batch key sets back to back (party 0: key_bytes(B) per set;
-  // party 1: key_bytes(B) or unique_key_bytes(B, 1) per set).  Returns
+  // Key files of whole-batch key sets back to back (per party: key_bytes(B) or
+  // unique_key_bytes(B, p) per set).  Returns
   // hipErrorFileNotFound for files that cannot be opened or do not hold whole sets.
   hipError_t attach_key_files(int B, const char *path0, const char *path1, size_t slot_bytes);
   hipError_t write_keys(int party, bool packed, const char *path, bool append);

@@ -102,6 +102,9 @@ struct KeyView {
 // copies those once, from party 0's buffer.
 struct GateKey {
   size_t begin = 0, end = 0;
+  uint32_t gate = 0;   // the dealer's gate id (position in the plan + 1)
+  int tr_kind = 0;     // truncation-family gates: kind and elements (0: another gate)
+  size_t n = 0;
   int nsh = 0;
   size_t sh[2][2] = {{0, 0}, {0, 0}};
   void share(size_t b, size_t e) {
@@ -564,6 +567,7 @@ class Model final : public ModelBase, KeySource {
       GateKey k;
       k.begin = o;
       k.end = end;
+      k.gate = uint32_t(g.size() + 1);
       g.push_back(k);
       o = end;
       return g.back();
@@ -572,6 +576,8 @@ class Model final : public ModelBase, KeySource {
     auto tr = [&](int kind, size_t n) {
       TrLayout lay = tr_layout(kind, bw_, s_, n, o);
       GateKey &k = push(lay.end);
+      k.tr_kind = kind;
+      k.n = n;
       if (lay.use_a) dcf_shared(k, lay.a);
       if (lay.use_b) dcf_shared(k, lay.b);
     };
@@ -771,8 +777,11 @@ class Model final : public ModelBase, KeySource {
         TRY(d.output(size_t(B) * d_.fus[k], t1.p));
       }
     }
-    if (d.c.off != key_bytes(B)) return hipErrorUnknown;  // plan and dealer disagree
+    // plan and dealer disagree (offsets, or gate ids of the seeded-plane expansion)
+    if (d.c.off != key_bytes(B) || d.c.gate != uint32_t(plan(B).size()) + 1) return hipErrorUnknown;
     TRY(hipStreamSynchronize(L_.stream));
+    for (int p = 0; p < 2; p++) party_key_bytes(seed, p, pk_[p]);
+    have_pk_ = true;
     keyed_B_ = B;
     return hipSuccess;
   }
@@ -786,6 +795,7 @@ class Model final : public ModelBase, KeySource {
     TRY(ensure_arena(B));
     TRY(hipMemcpy(arena_[0], k0, bytes, hipMemcpyHostToDevice));
     TRY(hipMemcpy(arena_[1], k1, bytes, hipMemcpyHostToDevice));
+    have_pk_ = false;  // imported keys: the parties' PRF keys are not known here
     keyed_B_ = B;
     return hipSuccess;
   }
@@ -796,42 +806,72 @@ class Model final : public ModelBase, KeySource {
   }
 
   // ---------------- streaming ----------------
-  // Party 1's key planes outside the shared sub-ranges, split at gate
-  // boundaries so that each run lies inside one gate (hence one chunk).
+  // The bytes of party p's key a streamed copy moves, as runs that each lie
+  // inside one gate (hence one chunk): party 1 skips the planes it reads from
+  // party 0's copy (shared); a packed key also leaves out the planes that the
+  // dealer drew from the party's own PRF key (seeded: regenerated in the device
+  // slot after the copy).  src: offset in the party's host buffer, after the
+  // packed format's header (the party's PRF key), or the arena offset.
+  static constexpr size_t kPackedHeader = 256;
   struct Run {
     size_t b, e, src;
   };
-  std::vector<Run> unique_runs(int B, bool packed) const {
+  // planes of a truncation-family gate drawn from party p's own PRF key
+  void seeded_planes(const GateKey &g, int p, std::vector<std::pair<size_t, size_t>> &out) const {
+    if (!g.tr_kind) return;
+    const TrLayout lay = tr_layout(g.tr_kind, bw_, s_, g.n, g.begin);
+    const size_t tb = size_t(bw_ / 8);
+    for (const DcfLayout *dl : {lay.use_a ? &lay.a : nullptr, lay.use_b ? &lay.b : nullptr}) {
+      if (!dl) continue;
+      out.emplace_back(dl->off_root, dl->off_root + g.n * 16);
+      out.emplace_back(dl->off_z, dl->off_z + zwords(g.n) * 4);
+    }
+    if (p == 0) {
+      if (g.tr_kind == G_TRRELU || g.tr_kind == G_RELU || g.tr_kind == G_RELUSLACK)
+        out.emplace_back(lay.off_kappa, lay.off_kappa + g.n * tb);
+      if (lay.ncase > 0) out.emplace_back(lay.off_g, lay.off_g + size_t(lay.ncase) * g.n * tb);
+    }
+  }
+  std::vector<Run> party_runs(int B, int party, bool packed) const {
     std::vector<Run> r;
-    size_t acc = 0;
-    auto add = [&](size_t b, size_t e) {
-      if (e <= b) return;
-      r.push_back(Run{b, e, packed ? acc : b});
-      acc += e - b;
-    };
+    size_t acc = kPackedHeader;
+    std::vector<std::pair<size_t, size_t>> om;
     for (const GateKey &g : plan(B)) {
+      om.clear();
+      if (party == 1)
+        for (int j = 0; j < g.nsh; j++) om.emplace_back(g.sh[j][0], g.sh[j][1]);
+      if (packed) seeded_planes(g, party, om);
+      std::sort(om.begin(), om.end());
       size_t cur = g.begin;
-      for (int j = 0; j < g.nsh; j++) {
-        add(cur, g.sh[j][0]);
-        cur = g.sh[j][1];
+      auto add = [&](size_t b, size_t e) {
+        if (e <= b) return;
+        r.push_back(Run{b, e, packed ? acc : b});
+        acc += e - b;
+      };
+      for (const auto &x : om) {
+        add(cur, x.first);
+        cur = std::max(cur, x.second);
       }
       add(cur, g.end);
     }
     return r;
   }
+  // packed key of party p: the header (its PRF key) and its runs
   size_t unique_key_bytes(int B, int party) const override {
-    if (party == 0) return key_bytes(B);
-    size_t n = 0;
-    for (const Run &u : unique_runs(B, true)) n += u.e - u.b;
+    size_t n = kPackedHeader;
+    for (const Run &u : party_runs(B, party, true)) n += u.e - u.b;
     return n;
   }
   hipError_t export_unique_keys(int party, void *dst, size_t bytes) override {
-    if (party == 0) return export_keys(0, dst, bytes);
-    if (!arena_[1] || keyed_B_ < 1 || bytes != unique_key_bytes(keyed_B_, 1)) return hipErrorInvalidValue;
+    if (party < 0 || party > 1 || !arena_[party] || keyed_B_ < 1 || bytes != unique_key_bytes(keyed_B_, party))
+      return hipErrorInvalidValue;
+    if (!have_pk_) return hipErrorNotSupported;  // imported keys: no PRF key to expand from
     TRY(hipStreamSynchronize(L_.stream));
     uint8_t *d = static_cast<uint8_t *>(dst);
-    for (const Run &u : unique_runs(keyed_B_, true))
-      TRY(hipMemcpy(d + u.src, arena_[1] + u.b, u.e - u.b, hipMemcpyDeviceToHost));
+    std::memset(d, 0, kPackedHeader);
+    std::memcpy(d, pk_[party], 16);
+    for (const Run &u : party_runs(keyed_B_, party, true))
+      TRY(hipMemcpy(d + u.src, arena_[party] + u.b, u.e - u.b, hipMemcpyDeviceToHost));
     return hipSuccess;
   }
 
@@ -857,7 +897,7 @@ class Model final : public ModelBase, KeySource {
   }
 
   // plan, chunks, device slots and events of the streamed arena
-  hipError_t setup_stream(int B, bool packed, size_t slot_bytes) {
+  hipError_t setup_stream(int B, const bool packed[2], size_t slot_bytes) {
     keyed_B_ = -1;  // the resident keys go away below; set again once the slots exist
     stop_io();
     TRY(hipStreamSynchronize(L_.stream));
@@ -883,24 +923,34 @@ class Model final : public ModelBase, KeySource {
       TRY(hipEventCreateWithFlags(&free_[k], hipEventDisableTiming));
     }
     TRY(hipStreamCreateWithFlags(&cs_, hipStreamNonBlocking));
-    runs1_ = unique_runs(B, packed);
+    for (int p = 0; p < 2; p++) {
+      packed_[p] = packed[p];
+      runs_[p] = party_runs(B, p, packed[p]);
+    }
     return hipSuccess;
+  }
+
+  // a party's host key: its arena (key_bytes) or its packed key (unique_key_bytes)
+  bool packed_size(int B, int party, size_t bytes, bool *packed) const {
+    if (bytes == key_bytes(B)) {
+      *packed = false;
+      return true;
+    }
+    *packed = bytes == unique_key_bytes(B, party);
+    return *packed;
   }
 
   hipError_t attach_host_keys(int B, const void *h0, size_t bytes0, const void *h1, size_t bytes1,
                               size_t slot_bytes) override {
-    const size_t full = key_bytes(B);
-    if (!h0 || !h1 || bytes0 != full || slot_bytes == 0) return hipErrorInvalidValue;
-    bool packed;
-    if (bytes1 == full)
-      packed = false;
-    else if (bytes1 == unique_key_bytes(B, 1))
-      packed = true;
-    else
+    bool packed[2];
+    if (!h0 || !h1 || slot_bytes == 0 || !packed_size(B, 0, bytes0, &packed[0]) ||
+        !packed_size(B, 1, bytes1, &packed[1]))
       return hipErrorInvalidValue;
     TRY(setup_stream(B, packed, slot_bytes));
     host_[0] = static_cast<const uint8_t *>(h0);
     host_[1] = static_cast<const uint8_t *>(h1);
+    for (int p = 0; p < 2; p++)
+      if (packed[p]) std::memcpy(spk_[p], host_[p], 16);
     streaming_ = true;
     keyed_B_ = B;
     return hipSuccess;
@@ -909,10 +959,11 @@ class Model final : public ModelBase, KeySource {
   // ---------------- file-backed keys ----------------
   // Key sets in two files, read chunk by chunk by an I/O thread into two pinned
   // staging buffers per party, then copied into the device slots.
-  hipError_t attach_key_files(int B, const KeyFile &f0, const KeyFile &f1, bool packed1,
+  hipError_t attach_key_files(int B, const KeyFile &f0, const KeyFile &f1, bool packed0, bool packed1,
                               size_t slot_bytes) override {
     if (f0.fd < 0 || f1.fd < 0 || f0.nsets == 0 || slot_bytes == 0) return hipErrorInvalidValue;
-    TRY(setup_stream(B, packed1, slot_bytes));
+    const bool packed[2] = {packed0, packed1};
+    TRY(setup_stream(B, packed, slot_bytes));
     for (int p = 0; p < 2; p++)
       for (int k = 0; k < 2; k++) TRY(hipHostMalloc((void **)&stg_[p][k], chunk_max_, hipHostMallocDefault));
     kf_[0] = f0;
@@ -974,11 +1025,19 @@ class Model final : public ModelBase, KeySource {
       auto add = [&](int fd, uint8_t *dst, size_t n, uint64_t off) {
         for (size_t o = 0; o < n; o += kPiece) pieces.push_back(Piece{fd, dst + o, std::min(kPiece, n - o), off + o});
       };
-      add(kf_[0].fd, stg_[0][sl], en - b, kf_[0].base + set * kf_[0].stride + b);
-      for (const Run &u : runs1_)
-        if (u.b >= b && u.b < en)
-          add(kf_[1].fd, stg_[1][sl] + (u.b - b), u.e - u.b, kf_[1].base + set * kf_[1].stride + u.src);
+      for (int p = 0; p < 2; p++) {
+        const uint64_t set_base = kf_[p].base + set * kf_[p].stride;
+        if (!packed_[p] && p == 0) {  // party 0's arena: the chunk in one piece
+          add(kf_[0].fd, stg_[0][sl], en - b, set_base + b);
+          continue;
+        }
+        for (const Run &u : runs_[p])
+          if (u.b >= b && u.b < en) add(kf_[p].fd, stg_[p][sl] + (u.b - b), u.e - u.b, set_base + u.src);
+      }
       bool ok = e == hipSuccess;
+      if (ok && k == 0)  // the set's header: the packed parties' PRF keys
+        for (int p = 0; p < 2; p++)
+          if (packed_[p]) ok = ok && pread_all(kf_[p].fd, spk_[p], 16, kf_[p].base + set * kf_[p].stride);
       if (ok) {
         std::vector<char> good(kReaders, 1);
         std::vector<std::thread> rd;
@@ -1023,15 +1082,28 @@ class Model final : public ModelBase, KeySource {
   hipError_t write_keys(int party, bool packed, int fd) override {
     if (!arena_[party] || keyed_B_ < 1) return hipErrorInvalidValue;
     TRY(hipStreamSynchronize(L_.stream));
+    if (packed && !have_pk_) return hipErrorNotSupported;  // imported keys: no PRF key
     std::vector<Run> runs;
-    if (party == 1 && packed)
-      runs = unique_runs(keyed_B_, true);
+    if (packed)
+      runs = party_runs(keyed_B_, party, true);
     else
       runs.push_back(Run{0, key_bytes(keyed_B_), 0});
     constexpr size_t kBounce = size_t(64) << 20;
     uint8_t *h = nullptr;
     TRY(hipHostMalloc((void **)&h, kBounce, hipHostMallocDefault));
     hipError_t err = hipSuccess;
+    if (packed) {  // header: the party's PRF key
+      uint8_t hdr[kPackedHeader] = {};
+      std::memcpy(hdr, pk_[party], 16);
+      for (size_t w = 0; w < kPackedHeader;) {
+        const ssize_t r = ::write(fd, hdr + w, kPackedHeader - w);
+        if (r <= 0) {
+          (void)hipHostFree(h);
+          return hipErrorFileNotFound;
+        }
+        w += size_t(r);
+      }
+    }
     for (const Run &u : runs) {
       for (size_t o = u.b; o < u.e && err == hipSuccess; o += kBounce) {
         const size_t n = std::min(kBounce, u.e - o);
@@ -1058,15 +1130,47 @@ class Model final : public ModelBase, KeySource {
       cv_.wait(lk, [&] { return loaded_ >= k || io_err_ != hipSuccess; });
       if (io_err_ != hipSuccess) return io_err_;
     }
-    const uint8_t *src0 = files_ ? stg_[0][sl] : host_[0] + b;
     TRY(hipStreamWaitEvent(cs_, free_[sl], 0));
-    TRY(hipMemcpyAsync(slot_[sl][0], src0, e - b, hipMemcpyHostToDevice, cs_));
-    stream_stats.bytes_h2d += e - b;
-    for (const Run &u : runs1_) {
-      if (u.b < b || u.b >= e) continue;
-      const uint8_t *src1 = files_ ? stg_[1][sl] + (u.b - b) : host_[1] + u.src;
-      TRY(hipMemcpyAsync(slot_[sl][1] + (u.b - b), src1, u.e - u.b, hipMemcpyHostToDevice, cs_));
-      stream_stats.bytes_h2d += u.e - u.b;
+    for (int p = 0; p < 2; p++) {
+      if (p == 0 && !packed_[0]) {  // party 0's arena: the chunk in one copy
+        const uint8_t *src0 = files_ ? stg_[0][sl] : host_[0] + b;
+        TRY(hipMemcpyAsync(slot_[sl][0], src0, e - b, hipMemcpyHostToDevice, cs_));
+        stream_stats.bytes_h2d += e - b;
+        continue;
+      }
+      // runs adjacent in the slot and in the source move as one copy
+      size_t cb = 0, ce = 0;
+      const uint8_t *csrc = nullptr;
+      auto flush = [&]() -> hipError_t {
+        if (ce > cb) {
+          TRY(hipMemcpyAsync(slot_[sl][p] + (cb - b), csrc, ce - cb, hipMemcpyHostToDevice, cs_));
+          stream_stats.bytes_h2d += ce - cb;
+        }
+        return hipSuccess;
+      };
+      for (const Run &u : runs_[p]) {
+        if (u.b < b || u.b >= e) continue;
+        const uint8_t *src = files_ ? stg_[p][sl] + (u.b - b) : host_[p] + u.src;
+        if (ce == u.b && csrc + (ce - cb) == src) {
+          ce = u.e;
+          continue;
+        }
+        TRY(flush());
+        cb = u.b;
+        ce = u.e;
+        csrc = src;
+      }
+      TRY(flush());
+      if (!packed_[p]) continue;
+      // the planes the party expands from its PRF key, on the copy stream
+      Launch Lc = L_;
+      Lc.stream = cs_;
+      for (size_t i = 0; i < gates_.size(); i++) {
+        const GateKey &g = gates_[i];
+        if (chunk_of_[i] != k || !g.tr_kind) continue;
+        const TrLayout lay = tr_layout(g.tr_kind, bw_, s_, g.n, g.begin - b);
+        TRY(launch_tr_expand<T>(Lc, lay, spk_[p], g.gate, p, slot_[sl][p]));
+      }
     }
     TRY(hipEventRecord(ready_[sl], cs_));
     if (files_) {
@@ -1342,7 +1446,11 @@ class Model final : public ModelBase, KeySource {
   int loaded_ = -1, issued_ = -1;
   bool abort_ = false;
   hipError_t io_err_ = hipSuccess;
-  std::vector<Run> runs1_;
+  std::vector<Run> runs_[2];       // what a chunk copy moves per party
+  bool packed_[2] = {false, false};  // streamed party p's key is packed (seeded planes expanded)
+  uint8_t spk_[2][16] = {};          // the streamed packed parties' PRF keys
+  uint8_t pk_[2][16] = {};           // the resident keys' PRF keys (from keygen)
+  bool have_pk_ = false;
   uint8_t *slot_[2][2] = {{nullptr, nullptr}, {nullptr, nullptr}};
   hipEvent_t ready_[2] = {nullptr, nullptr}, free_[2] = {nullptr, nullptr};
   hipStream_t cs_ = nullptr;
@@ -1527,18 +1635,22 @@ hipError_t LaneSet::release_arena() {
 
 hipError_t LaneSet::attach_host_keys(int B, const void *h0, size_t bytes0, const void *h1, size_t bytes1,
                                      size_t slot_bytes) {
-  if (bytes0 != key_bytes(B)) return hipErrorInvalidValue;
-  bool packed;
-  if (bytes1 == key_bytes(B))
-    packed = false;
-  else if (bytes1 == unique_key_bytes(B, 1))
-    packed = true;
-  else
-    return hipErrorInvalidValue;
+  // each party's buffer: the lanes' arenas back to back, or their packed keys
+  bool packed[2];
+  const size_t bytes[2] = {bytes0, bytes1};
+  for (int p = 0; p < 2; p++) {
+    if (bytes[p] == key_bytes(B))
+      packed[p] = false;
+    else if (bytes[p] == unique_key_bytes(B, p))
+      packed[p] = true;
+    else
+      return hipErrorInvalidValue;
+  }
   keyed_B_ = -1;
   size_t o0 = 0, o1 = 0;
   TRY(each(B, [&](int i, int Bi, int) {
-    const size_t n0 = lane_[i]->key_bytes(Bi), n1 = packed ? lane_[i]->unique_key_bytes(Bi, 1) : n0;
+    const size_t n0 = packed[0] ? lane_[i]->unique_key_bytes(Bi, 0) : lane_[i]->key_bytes(Bi);
+    const size_t n1 = packed[1] ? lane_[i]->unique_key_bytes(Bi, 1) : lane_[i]->key_bytes(Bi);
     hipError_t r = lane_[i]->attach_host_keys(Bi, static_cast<const uint8_t *>(h0) + o0, n0,
                                               static_cast<const uint8_t *>(h1) + o1, n1, slot_bytes);
     o0 += n0;
@@ -1557,8 +1669,8 @@ void LaneSet::close_files() {
 }
 
 hipError_t LaneSet::attach_key_files(int B, const char *path0, const char *path1, size_t slot_bytes) {
-  const size_t set0 = key_bytes(B), full1 = set0, packed1 = unique_key_bytes(B, 1);
-  if (!path0 || !path1 || set0 == 0 || slot_bytes == 0) return hipErrorInvalidValue;
+  const size_t full = key_bytes(B);
+  if (!path0 || !path1 || full == 0 || slot_bytes == 0) return hipErrorInvalidValue;
   int fd[2] = {::open(path0, O_RDONLY), ::open(path1, O_RDONLY)};
   auto fail = [&](hipError_t e) {
     for (int p = 0; p < 2; p++)
@@ -1566,32 +1678,40 @@ hipError_t LaneSet::attach_key_files(int B, const char *path0, const char *path1
     return e;
   };
   if (fd[0] < 0 || fd[1] < 0) return fail(hipErrorFileNotFound);
-  const off_t size0 = ::lseek(fd[0], 0, SEEK_END), size1 = ::lseek(fd[1], 0, SEEK_END);
-  if (size0 <= 0 || size_t(size0) % set0 != 0) return fail(hipErrorFileNotFound);
-  const uint64_t nsets = uint64_t(size0) / set0;
-  bool packed;
-  if (uint64_t(size1) == nsets * full1)
-    packed = false;
-  else if (uint64_t(size1) == nsets * packed1)
-    packed = true;
-  else
-    return fail(hipErrorFileNotFound);
-  const uint64_t stride1 = packed ? packed1 : full1;
+  // each file holds whole key sets of one format: arenas or packed keys (the
+  // lanes' back to back), told apart by the file size; both files the same count
+  bool packed[2];
+  uint64_t set[2], nsets = 0;
+  for (int p = 0; p < 2; p++) {
+    const off_t size = ::lseek(fd[p], 0, SEEK_END);
+    const size_t pk = unique_key_bytes(B, p);
+    if (size > 0 && uint64_t(size) % full == 0)
+      packed[p] = false, set[p] = full;
+    else if (size > 0 && uint64_t(size) % pk == 0)
+      packed[p] = true, set[p] = pk;
+    else
+      return fail(hipErrorFileNotFound);
+    const uint64_t n = uint64_t(size) / set[p];
+    if (p == 1 && n != nsets) {  // a size that divides both ways: take the matching count
+      if (!packed[1] && uint64_t(size) % pk == 0 && uint64_t(size) / pk == nsets)
+        packed[1] = true, set[1] = pk;
+      else
+        return fail(hipErrorFileNotFound);
+    }
+    if (p == 0) nsets = n;
+  }
   keyed_B_ = -1;
-  uint64_t o0 = 0, o1 = 0;
+  uint64_t o[2] = {0, 0};
   hipError_t e = each(B, [&](int i, int Bi, int) {
-    KeyFile f0, f1;
-    f0.fd = fd[0];
-    f0.base = o0;
-    f0.stride = set0;
-    f0.nsets = nsets;
-    f1.fd = fd[1];
-    f1.base = o1;
-    f1.stride = stride1;
-    f1.nsets = nsets;
-    o0 += lane_[i]->key_bytes(Bi);
-    o1 += packed ? lane_[i]->unique_key_bytes(Bi, 1) : lane_[i]->key_bytes(Bi);
-    return lane_[i]->attach_key_files(Bi, f0, f1, packed, slot_bytes);
+    KeyFile f[2];
+    for (int p = 0; p < 2; p++) {
+      f[p].fd = fd[p];
+      f[p].base = o[p];
+      f[p].stride = set[p];
+      f[p].nsets = nsets;
+      o[p] += packed[p] ? lane_[i]->unique_key_bytes(Bi, p) : lane_[i]->key_bytes(Bi);
+    }
+    return lane_[i]->attach_key_files(Bi, f[0], f[1], packed[0], packed[1], slot_bytes);
   });
   if (e != hipSuccess) return fail(e);
   close_files();  // the lanes no longer read earlier files
@@ -1602,7 +1722,7 @@ hipError_t LaneSet::attach_key_files(int B, const char *path0, const char *path1
 }
 
 hipError_t LaneSet::write_keys(int party, bool packed, const char *path, bool append) {
-  if (!path || keyed_B_ < 1 || (packed && party != 1)) return hipErrorInvalidValue;
+  if (!path || keyed_B_ < 1 || party < 0 || party > 1) return hipErrorInvalidValue;
   const int fd = ::open(path, O_WRONLY | O_CREAT | (append ? O_APPEND : O_TRUNC), 0644);
   if (fd < 0) return hipErrorFileNotFound;
   hipError_t e = each(keyed_B_, [&](int i, int, int) { return lane_[i]->write_keys(party, packed, fd); });

@@ -36,7 +36,8 @@ enum Field : uint32_t {
   F_ROUT = 0x30,   // fresh output mask
   F_SPLIT = 0x40,  // +k: share 0 of plane k
   F_LUTV = 0x58,
-  F_RIN = 0x60     // input masks of reveal gates
+  F_RIN = 0x60,    // input masks of reveal gates
+  F_PARTY = 0x70   // party p's PRF key: dealer PRF block (p, F_PARTY, gate 0xFFFFFFFF)
 };
 
 struct DcfLayout {
@@ -198,6 +199,12 @@ struct AesRK {
 extern const uint8_t kSbox[256];
 AesRK aes_expand(const uint8_t key[16]);
 AesRK dealer_key(uint64_t seed);  // dealer PRF key derived from a 64-bit seed
+// Party p's own PRF key (a dealer PRF output): the dealer draws every purely
+// random plane of party p's truncation-family keys from it (DCF roots and output
+// mask bits; for party 0 also its shares of kappa and of the G table), so that a
+// party holding the 16 key bytes can expand those planes itself.
+void party_key_bytes(uint64_t seed, int party, uint8_t out[16]);
+AesRK party_key(uint64_t seed, int party);
 extern const uint8_t kKeyH[16];   // fixed key of the tree hash H
 extern const uint8_t kKeyL[16];   // fixed key of the leaf hash HL
 

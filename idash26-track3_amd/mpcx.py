@@ -522,8 +522,10 @@ class Model:
         return int(self.lib.mpcx_model_unique_key_bytes(self.h, B, party))
 
     def export_unique_keys(self, party, B, into=None):
-        """Party 1: its key planes that differ from party 0's, packed (party 0:
-        the whole arena)."""
+        """Party p's packed key: a 256-byte header with the party's own PRF key,
+        then its planes without those it reads from party 0's copy (party 1) and
+        without those the dealer drew from its PRF key (expanded on the device
+        when streamed).  Keys from keygen only."""
         n = self.unique_key_bytes(B, party)
         out = np.zeros(n, np.uint8) if into is None else into
         ptr = out.ptr if isinstance(out, PinnedBuffer) else out.ctypes.data_as(C.c_void_p)
@@ -532,8 +534,8 @@ class Model:
 
     def attach_host_keys(self, B, k0, k1, slot_bytes):
         """Stream keys from host buffers (PinnedBuffer for overlap) through two
-        device slots of slot_bytes per party; k1 is party 1's whole arena or its
-        packed unique planes."""
+        device slots of slot_bytes per party; each of k0, k1 is the party's
+        whole arena or its packed key (export_unique_keys)."""
         self._host_keys = (k0, k1)
         p0 = k0.ptr if isinstance(k0, PinnedBuffer) else k0.ctypes.data_as(C.c_void_p)
         p1 = k1.ptr if isinstance(k1, PinnedBuffer) else k1.ctypes.data_as(C.c_void_p)
@@ -544,7 +546,7 @@ class Model:
 
     def write_keys(self, party, path, packed=False, append=False):
         """Append (or write) the key set of the last keygen for one party to a
-        file: party 0's arena, party 1's arena or packed unique planes."""
+        file: the party's arena, or its packed key (packed=True)."""
         self.ctx.check(self.lib.mpcx_model_write_keys(self.h, party, 1 if packed else 0, os.fsencode(path),
                                                       1 if append else 0), "write_keys")
 

@@ -289,20 +289,28 @@ mpcx_status mpcx_model_import_keys(mpcx_model *m, int B, const void *h_key0, con
 mpcx_status mpcx_model_export_keys(mpcx_model *m, int party, void *h_dst, size_t bytes);
 /* Frees the resident key arenas (e.g. after mpcx_model_export_keys). */
 mpcx_status mpcx_model_release_arena(mpcx_model *m);
-/* The DCF correction and leaf words and the clear output mask are the same in
- * both parties' keys; the evaluation reads them from party 0's copy.  Party 1's
- * remaining ("unique") planes, packed back to back in arena order, are
- * mpcx_model_unique_key_bytes(m, B, 1) bytes (about a tenth of its arena at
- * bw=64); party 0's unique part is its whole arena. */
+/* Packed keys.  The DCF correction and leaf words and the clear output mask are
+ * the same in both parties' keys; the evaluation reads them from party 0's copy.
+ * The dealer draws every purely random plane of a party's truncation-family
+ * keys (DCF roots and output-mask bits; for party 0 also its shares of kappa and
+ * of the G tables) from that party's own PRF key, which the party receives
+ * instead of those planes (the seed compression of the reference's key format
+ * notes, README.md:144-157, 319-322).  Party p's packed key: a 256-byte header
+ * (its 16-byte PRF key, then zeros) and its remaining planes back to back in
+ * arena order, mpcx_model_unique_key_bytes(m, B, p) bytes (at bw=64 about 90%
+ * of party 0's arena and 7% of party 1's); with lanes, the lanes' packed keys
+ * back to back.  Exported from keys made by mpcx_model_keygen only (imported
+ * keys carry no PRF keys: MPCX_ESTATE). */
 size_t mpcx_model_unique_key_bytes(const mpcx_model *m, int B, int party);
 mpcx_status mpcx_model_export_unique_keys(mpcx_model *m, int party, void *h_dst, size_t bytes);
 /* Streaming key arena for batches whose keys do not stay resident: both parties'
  * keys in host memory (pinned for overlap) are copied per chunk of consecutive
  * gates into one of two device slots of at most slot_bytes per party, on a copy
  * stream, while the previous chunk computes; party 1's shared planes are not
- * copied.  h_key0: party 0's arena (bytes0 = mpcx_model_key_bytes); h_key1:
- * party 1's arena (bytes1 = mpcx_model_key_bytes) or its packed unique planes
- * (bytes1 = mpcx_model_unique_key_bytes(m, B, 1)).  Replaces the chunked key
+ * copied.  Each of h_key0, h_key1: the party's arena (bytes = mpcx_model_key_bytes)
+ * or its packed key (bytes = mpcx_model_unique_key_bytes(m, B, p)), whose
+ * PRF-drawn planes are expanded in the device slot after each chunk's copy, on
+ * the copy stream.  Replaces the chunked key
  * pipeline of gpu_mpc/deepdtagen_inference.cu:608-859 (pinned double-buffered
  * slots, copy stream, ready/free events) and setGPUKeyArenaSlot
  * (patches/EzPC-GPU-MPC.track3.patch:680-685).  The resident arena is freed;
@@ -311,8 +319,8 @@ mpcx_status mpcx_model_export_unique_keys(mpcx_model *m, int party, void *h_dst,
 mpcx_status mpcx_model_attach_host_keys(mpcx_model *m, int B, const void *h_key0, size_t bytes0,
                                         const void *h_key1, size_t bytes1, size_t slot_bytes);
 /* Key files.  mpcx_model_write_keys appends the key set of the batch keyed
- * last (mpcx_model_keygen / import) for one party to a file: party 0's arena,
- * or party 1's arena (packed = 0) or packed unique planes (packed = 1); append
+ * last (mpcx_model_keygen / import) for one party to a file: the party's arena
+ * (packed = 0) or its packed key (packed = 1, keys from keygen only); append
  * = 0 truncates the file first.  Sets of successive keygens (fresh seeds)
  * appended in order form a key file of whole-batch key sets.
  * mpcx_model_attach_key_files streams such files: each forward reads the next
@@ -323,8 +331,8 @@ mpcx_status mpcx_model_attach_host_keys(mpcx_model *m, int B, const void *h_key0
  * SSD -> pinned -> VRAM pipeline of gpu_mpc/deepdtagen_inference.cu:608-859
  * (I/O thread, pread into pinned slots, evH2D / evFree handshake); the
  * reference's chunks are whole micro-batch key sets, these are gate-aligned
- * pieces of one, so a key set need not fit in memory twice.  Party 1's file
- * holds arenas or packed unique planes, told apart by its size.  MPCX_EIO if a
+ * pieces of one, so a key set need not fit in memory twice.  Each file holds
+ * arenas or packed keys, told apart by its size.  MPCX_EIO if a
  * file is missing, does not hold whole key sets, or a read fails. */
 mpcx_status mpcx_model_write_keys(mpcx_model *m, int party, int packed, const char *path, int append);
 mpcx_status mpcx_model_attach_key_files(mpcx_model *m, int B, const char *path0, const char *path1,

@@ -103,7 +103,8 @@ enum {
   ORC_F_ROUT = 0x30, /* fresh output mask */
   ORC_F_SPLIT = 0x40, /* +k: share-0 of plane k */
   ORC_F_LUTV = 0x58,
-  ORC_F_RIN = 0x60   /* input masks of reveal gates */
+  ORC_F_RIN = 0x60,  /* input masks of reveal gates */
+  ORC_F_PARTY = 0x70 /* +0: the parties' own PRF keys (gate 0xFFFFFFFF, index p) */
 };
 
 typedef struct {
@@ -133,6 +134,10 @@ int orc_dcf_eval1(int party, const uint8_t *key, const orc_dcf_layout *L, size_t
                   uint64_t x);
 void orc_dcf_eval(int party, int m, size_t N, const uint8_t *key, size_t base,
                   const uint64_t *x, uint8_t *out);
+
+/* Party p's own PRF key (16 bytes): the truncation-family keygen draws party p's
+ * DCF roots and output-mask bits (party 0: also its kappa and G shares) from it. */
+void orc_party_key(uint64_t seed, int party, uint8_t key[16]);
 
 /* Truncation / ReLU family.  bias: per element (scale s) or NULL.
  * in_mask: mask of the gate input; out_mask: output mask (written). */

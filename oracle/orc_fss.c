@@ -191,14 +191,11 @@ static int parity_above(orc_blk b, int pos) {
   return __builtin_parity(acc);
 }
 
-static void dcf_gen1(const orc_prf *P, uint32_t gate, uint32_t fb, const orc_dcf_layout *L,
-                     uint64_t alpha, size_t i, uint8_t *k0, uint8_t *k1) {
+/* Dealer walk from the parties' roots s0 (lsb 0) and s1 (lsb 1), D = s0 ^ s1. */
+static void dcf_gen_roots(orc_blk s0, orc_blk s1, const orc_dcf_layout *L, uint64_t alpha, size_t i,
+                          uint8_t *k0, uint8_t *k1) {
   const int m = L->m;
-  orc_blk s0 = orc_prf_blk(P, gate, fb + 0, i);
-  s0.w[0] &= ~1u;
-  orc_blk D = orc_prf_blk(P, gate, fb + 1, i);
-  D.w[0] |= 1u;
-  orc_blk s1 = bxor(s0, D);
+  const orc_blk D = bxor(s0, s1);
   put_blk(k0, L->off_root, i, s0);
   put_blk(k1, L->off_root, i, s1);
   int t0 = 0, t1 = 1;
@@ -225,6 +222,54 @@ static void dcf_gen1(const orc_prf *P, uint32_t gate, uint32_t fb, const orc_dcf
   lcw.w[pos / 32] ^= 1u << (pos % 32);
   put_blk(k0, L->off_leaf, i, lcw);
   put_blk(k1, L->off_leaf, i, lcw);
+}
+
+/* Roots from the dealer PRF: s0 = PRF(fb) with lsb 0, s1 = s0 ^ D, D = PRF(fb+1) | 1. */
+static void dcf_gen1(const orc_prf *P, uint32_t gate, uint32_t fb, const orc_dcf_layout *L,
+                     uint64_t alpha, size_t i, uint8_t *k0, uint8_t *k1) {
+  orc_blk s0 = orc_prf_blk(P, gate, fb + 0, i);
+  s0.w[0] &= ~1u;
+  orc_blk D = orc_prf_blk(P, gate, fb + 1, i);
+  D.w[0] |= 1u;
+  dcf_gen_roots(s0, bxor(s0, D), L, alpha, i, k0, k1);
+}
+
+/* Party p's own PRF key: the dealer PRF block (p, ORC_F_PARTY, gate 0xFFFFFFFF)
+ * as an AES-128 key.  The dealer draws every purely random plane of party p's
+ * truncation-family keys from it (DCF roots and output-mask bits; for party 0
+ * also its shares of kappa and of the G table). */
+void orc_party_key(uint64_t seed, int party, uint8_t key[16]) {
+  orc_prf P;
+  orc_prf_init(&P, seed);
+  orc_blk b = orc_prf_blk(&P, 0xFFFFFFFFu, ORC_F_PARTY, (uint64_t)party);
+  for (int j = 0; j < 4; j++)
+    for (int k = 0; k < 4; k++) key[4 * j + k] = (uint8_t)(b.w[j] >> (8 * k));
+}
+static void party_prf(uint64_t seed, int party, orc_prf *Pp) {
+  uint8_t key[16];
+  orc_party_key(seed, party, key);
+  orc_aes_expand(key, Pp->rk);
+}
+/* root of party p: its PRF block with lsb = p */
+static orc_blk party_root(const orc_prf *Pp, int p, uint32_t gate, uint32_t fb, size_t i) {
+  orc_blk s = orc_prf_blk(Pp, gate, fb + 0, i);
+  s.w[0] = (s.w[0] & ~1u) | (uint32_t)p;
+  return s;
+}
+/* DCF key of a truncation-family gate: roots and output-mask bits from the
+ * parties' own PRF keys (rbit = z0 ^ z1 was computed by the caller the same way) */
+static void dcf_keygen_parties(const orc_prf *P0, const orc_prf *P1, uint32_t gate, uint32_t fb, int m,
+                               size_t N, const uint64_t *alpha, uint8_t *k0, uint8_t *k1, size_t base) {
+  orc_dcf_layout L = orc_dcf_layout_make(m, N, base, 1);
+  OMP_FOR
+  for (size_t i = 0; i < N; i++)
+    dcf_gen_roots(party_root(P0, 0, gate, fb, i), party_root(P1, 1, gate, fb, i), &L, alpha[i], i, k0, k1);
+  memset(k0 + L.off_z, 0, orc_zwords(N) * 4);
+  memset(k1 + L.off_z, 0, orc_zwords(N) * 4);
+  for (size_t i = 0; i < N; i++) {
+    setbit(k0, L.off_z, i, prf_bit(P0, gate, fb + 2, i));
+    setbit(k1, L.off_z, i, prf_bit(P1, gate, fb + 2, i));
+  }
 }
 
 void orc_dcf_keygen(uint64_t seed, uint32_t gate, uint32_t fbase, int m, size_t N,
@@ -344,26 +389,27 @@ void orc_tr_keygen(uint64_t seed, uint32_t gate, int kind, int bw, int s, size_t
     local_ars_keygen(bw, s, N, in_mask, out_mask);
     return;
   }
-  orc_prf P;
+  orc_prf P, P0, P1;
   orc_prf_init(&P, seed);
+  party_prf(seed, 0, &P0);
+  party_prf(seed, 1, &P1);
   orc_tr_layout T = orc_tr_layout_make(kind, bw, s, N, base);
   const uint64_t M = rmask(bw);
   const int n = bw, sb = orc_sign_bit(kind, bw, s);
   const int relu_like = kind == ORC_G_RELU || kind == ORC_G_RELUSLACK;
   const int no_b = relu_like || kind == ORC_G_DRELU; /* no s-bit DCF */
+  const int use_a = kind != ORC_G_TRSLACK;
   const uint64_t lowmask = (1ull << sb) - 1ull;
   const uint64_t smask = (1ull << s) - 1ull;
-  uint8_t *rb = (uint8_t *)calloc(N, 1), *rd = (uint8_t *)calloc(N, 1);
   uint64_t *aa = (uint64_t *)calloc(N, 8), *ab = (uint64_t *)calloc(N, 8);
   OMP_FOR
   for (size_t i = 0; i < N; i++) {
     uint64_t r = in_mask[i] & M;
     int rho = (int)((r >> sb) & 1u);
     uint64_t R = r >> s;
-    int rbi = prf_bit(&P, gate, ORC_F_DCFA + 3, i);
-    int rdi = prf_bit(&P, gate, ORC_F_DCFB + 3, i);
-    rb[i] = (uint8_t)rbi;
-    rd[i] = (uint8_t)rdi;
+    /* the DCF output masks: XOR of the parties' own mask bits */
+    int rbi = use_a ? prf_bit(&P0, gate, ORC_F_DCFA + 2, i) ^ prf_bit(&P1, gate, ORC_F_DCFA + 2, i) : 0;
+    int rdi = !no_b ? prf_bit(&P0, gate, ORC_F_DCFB + 2, i) ^ prf_bit(&P1, gate, ORC_F_DCFB + 2, i) : 0;
     aa[i] = r & lowmask;
     ab[i] = r & smask;
     uint64_t rout = prf_ring(&P, gate, ORC_F_ROUT, i, bw);
@@ -393,20 +439,18 @@ void orc_tr_keygen(uint64_t seed, uint32_t gate, int kind, int bw, int s, size_t
         G = rout - R - (uint64_t)d + ((uint64_t)w << (n - s));
       }
       G &= M;
-      uint64_t g0 = prf_ring(&P, gate, ORC_F_SPLIT + (uint32_t)c, i, bw);
+      uint64_t g0 = prf_ring(&P0, gate, ORC_F_SPLIT + (uint32_t)c, i, bw);
       put_t(k0, T.off_g, (size_t)c * N + i, bw, g0);
       put_t(k1, T.off_g, (size_t)c * N + i, bw, (G - g0) & M);
     }
     if (T.relu) {
-      uint64_t q0 = prf_ring(&P, gate, ORC_F_SPLIT + 8, i, bw);
+      uint64_t q0 = prf_ring(&P0, gate, ORC_F_SPLIT + 8, i, bw);
       put_t(k0, T.off_kappa, i, bw, q0);
       put_t(k1, T.off_kappa, i, bw, ((uint64_t)kappa - q0) & M);
     }
   }
-  if (kind != ORC_G_TRSLACK) orc_dcf_keygen(seed, gate, ORC_F_DCFA, sb, N, aa, rb, k0, k1, T.a.off_root);
-  if (!no_b) orc_dcf_keygen(seed, gate, ORC_F_DCFB, s, N, ab, rd, k0, k1, T.b.off_root);
-  free(rb);
-  free(rd);
+  if (use_a) dcf_keygen_parties(&P0, &P1, gate, ORC_F_DCFA, sb, N, aa, k0, k1, T.a.off_root);
+  if (!no_b) dcf_keygen_parties(&P0, &P1, gate, ORC_F_DCFB, s, N, ab, k0, k1, T.b.off_root);
   free(aa);
   free(ab);
 }

@@ -472,8 +472,9 @@ def test_model_lanes_keys_and_forward(mp, orc, synth, bw, B, lanes):
 
 
 def test_model_lanes_streamed_keys(mp, orc, synth):
-    """Two lanes on host-streamed keys (party 1 packed to its unique planes):
-    each lane streams its part of the host buffers through its own two slots."""
+    """Two lanes on host-streamed packed keys (both parties): each lane streams
+    its part of the host buffers through its own two slots and expands its
+    parties' PRF-drawn planes there."""
     B, bw = 3, 64
     wl = synth.workload(B, synth.Dims(bw=bw), seed=33)
     d = _od(orc, wl.dims)
@@ -483,8 +484,8 @@ def test_model_lanes_streamed_keys(mp, orc, synth):
     m = mp.Model(c, wl.dims, wl.W, lanes=2)
     m.keygen(B, 4321)
     nbytes = m.key_bytes(B)
-    h0, hp = mp.PinnedBuffer(nbytes), mp.PinnedBuffer(m.unique_key_bytes(B, 1))
-    m.export_keys(0, B, into=h0)
+    h0, hp = mp.PinnedBuffer(m.unique_key_bytes(B, 0)), mp.PinnedBuffer(m.unique_key_bytes(B, 1))
+    m.export_unique_keys(0, B, into=h0)
     m.export_unique_keys(1, B, into=hp)
     m.release_arena()
     m.attach_host_keys(B, h0, hp, slot_bytes=nbytes // 6)
@@ -493,7 +494,8 @@ def test_model_lanes_streamed_keys(mp, orc, synth):
         m.forward(B)
         assert np.array_equal(m.output(B), want)
         st = m.stream_stats()
-        assert st["bytes_h2d"] == nbytes + hp.nbytes and st["chunks"] >= 4
+        # each lane's packed keys start with a 256-byte header that is not copied
+        assert st["bytes_h2d"] == h0.nbytes + hp.nbytes - 2 * 2 * 256 and st["chunks"] >= 4
     m.close()
     c.close()
     h0.free()
@@ -826,8 +828,8 @@ def test_model_streamed_keys_match_resident(mp, orc, synth, bw):
         st = m.stream_stats()
         # party 1's copy skips the correction/leaf words both parties hold
         assert st["chunks"] >= 4 and nbytes < st["bytes_h2d"] < 1.6 * nbytes
-    # party 1's keys packed to its unique planes (what a host that cannot pin
-    # two whole arenas holds): same outputs, same traffic
+    # party 1's key packed (without the planes it reads from party 0's copy and
+    # those drawn from its own PRF key, expanded on the device): same outputs
     m.close()
     m = mp.Model(c, wl.dims, wl.W)
     m.keygen(B, 555)
@@ -839,7 +841,8 @@ def test_model_streamed_keys_match_resident(mp, orc, synth, bw):
     m.set_inputs(B, *wl.shares["x"], *wl.shares["a"], *wl.shares["m"], wl.prot)
     m.forward(B)
     assert np.array_equal(m.output(B), want)
-    assert m.stream_stats()["bytes_h2d"] == nbytes + hp.nbytes
+    hdr = 256  # the packed key's header (the party's PRF key) is not copied
+    assert m.stream_stats()["bytes_h2d"] == nbytes + hp.nbytes - hdr
     # a second input batch on the same streamed keys
     wl2 = synth.workload(B, synth.Dims(bw=bw), seed=32)
     want2, code = orc.plain_forward(d, wl2.X, wl2.A, wl2.mask, wl2.prot, wl.W)
@@ -852,9 +855,29 @@ def test_model_streamed_keys_match_resident(mp, orc, synth, bw):
     m.forward(B)
     assert np.array_equal(m.output(B), want2)
     assert m.stream_stats()["chunks"] == 0
+    # both parties packed: the planes the dealer drew from each party's PRF key
+    # are expanded in the device slots after the copies
+    hq = mp.PinnedBuffer(m.unique_key_bytes(B, 0))
+    hq1 = mp.PinnedBuffer(m.unique_key_bytes(B, 1))
+    assert hq.nbytes < 0.95 * nbytes and hq1.nbytes == hp.nbytes
+    m.export_unique_keys(0, B, into=hq)
+    m.export_unique_keys(1, B, into=hq1)
+    m.release_arena()
+    m.attach_host_keys(B, hq, hq1, slot_bytes=nbytes // 4)
+    m.set_inputs(B, *wl2.shares["x"], *wl2.shares["a"], *wl2.shares["m"], wl2.prot)
+    for _ in range(2):
+        m.forward(B)
+        assert np.array_equal(m.output(B), want2)
+        assert m.stream_stats()["bytes_h2d"] == hq.nbytes + hq1.nbytes - 2 * hdr
+    # imported keys carry no PRF keys: no packed export
+    m.keygen(B, 557)
+    k0, k1 = m.export_keys(0, B), m.export_keys(1, B)
+    m.import_keys(B, k0, k1)
+    with pytest.raises(mp.MpcxError):
+        m.export_unique_keys(0, B, into=hq)
     m.close()
     c.close()
-    for h in (h0, h1, hp):
+    for h in (h0, h1, hp, hq, hq1):
         h.free()
 
 
@@ -874,14 +897,14 @@ def test_model_key_files(mp, orc, synth, tmp_path, bw, lanes, packed):
     p0, p1 = tmp_path / "keys0.bin", tmp_path / "keys1.bin"
     for k in range(3):
         m.keygen(B, 1000 + k)
-        m.write_keys(0, p0, append=k > 0)
+        m.write_keys(0, p0, packed=packed, append=k > 0)
         m.write_keys(1, p1, packed=packed, append=k > 0)
     nbytes = m.key_bytes(B)
-    assert p0.stat().st_size == 3 * nbytes
+    assert p0.stat().st_size == 3 * (m.unique_key_bytes(B, 0) if packed else nbytes)
     assert p1.stat().st_size == 3 * (m.unique_key_bytes(B, 1) if packed else nbytes)
     m.release_arena()
     bad = tmp_path / "short.bin"
-    bad.write_bytes(p0.read_bytes()[: nbytes // 2])
+    bad.write_bytes(p0.read_bytes()[: p0.stat().st_size // 3 // 2])
     with pytest.raises(mp.MpcxError):
         m.attach_key_files(B, bad, p1, slot_bytes=nbytes // 4)
     with pytest.raises(mp.MpcxError):
