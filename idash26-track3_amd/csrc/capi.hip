@@ -262,12 +262,14 @@ void mpcx_reset_counters(mpcx_ctx *c) {
 // ---------------- PRG ----------------
 mpcx_status mpcx_prg_hash(mpcx_ctx *c, int leaf, size_t n, const void *in, void *out) {
   CHECK_CTX(c);
+  if (n == 0) return MPCX_OK;
   if (!in || !out) return fail(c, MPCX_EINVAL, "null pointer");
   HIPC(c, launch_hash(c->L, leaf, n, static_cast<const uint4 *>(in), static_cast<uint4 *>(out)), "prg_hash");
   return MPCX_OK;
 }
 mpcx_status mpcx_prf(mpcx_ctx *c, uint64_t seed, uint32_t gate, uint32_t field, size_t n, void *out) {
   CHECK_CTX(c);
+  if (n == 0) return MPCX_OK;
   if (!out) return fail(c, MPCX_EINVAL, "null pointer");
   HIPC(c, launch_prf(c->L, seed, gate, field, n, static_cast<uint4 *>(out)), "prf");
   return MPCX_OK;
@@ -279,7 +281,9 @@ size_t mpcx_dcf_key_bytes(int bin, size_t n) { return dcf_layout(bin, n, 0, true
 mpcx_status mpcx_dcf_keygen(mpcx_ctx *c, int bin, size_t n, const uint64_t *alpha, const uint8_t *rbit,
                             uint64_t seed, uint32_t gate, void *k0, void *k1) {
   CHECK_CTX(c);
-  if (bin < 1 || bin > 64 || !alpha || !k0 || !k1) return fail(c, MPCX_EINVAL, "dcf_keygen: bad argument");
+  if (bin < 1 || bin > 64) return fail(c, MPCX_EINVAL, "dcf_keygen: bad argument");
+  if (n == 0) return MPCX_OK;
+  if (!alpha || !k0 || !k1) return fail(c, MPCX_EINVAL, "dcf_keygen: null pointer");
   HIPC(c,
        launch_dcf_keygen(c->L, seed, gate, F_DCFA, bin, n, alpha, rbit, static_cast<uint8_t *>(k0),
                          static_cast<uint8_t *>(k1), 0),
@@ -290,8 +294,9 @@ mpcx_status mpcx_dcf_keygen(mpcx_ctx *c, int bin, size_t n, const uint64_t *alph
 mpcx_status mpcx_dcf_eval(mpcx_ctx *c, int party, int bin, size_t n, const void *key, const uint64_t *x,
                           uint64_t *out) {
   CHECK_CTX(c);
-  if (bin < 1 || bin > 64 || (party != 0 && party != 1) || !key || !x || !out)
-    return fail(c, MPCX_EINVAL, "dcf_eval: bad argument");
+  if (bin < 1 || bin > 64 || (party != 0 && party != 1)) return fail(c, MPCX_EINVAL, "dcf_eval: bad argument");
+  if (n == 0) return MPCX_OK;
+  if (!key || !x || !out) return fail(c, MPCX_EINVAL, "dcf_eval: null pointer");
   HIPC(c, launch_dcf_eval(c->L, party, bin, n, static_cast<const uint8_t *>(key), 0, x, out), "dcf_eval");
   return MPCX_OK;
 }
@@ -345,8 +350,9 @@ static mpcx_status tr_keygen_t(mpcx_ctx *c, int kind, size_t n, const void *in, 
 mpcx_status mpcx_tr_keygen(mpcx_ctx *c, int kind, size_t n, const void *in, void *out, uint64_t seed, uint32_t gate,
                            void *k0, void *k1) {
   CHECK_CTX(c);
-  if (!valid_kind(kind) || !in || !out || (kind != MPCX_LOCALARS && (!k0 || !k1)))
-    return fail(c, MPCX_EINVAL, "tr_keygen: bad argument");
+  if (!valid_kind(kind)) return fail(c, MPCX_EINVAL, "tr_keygen: bad gate kind");
+  if (n == 0) return MPCX_OK;
+  if (!in || !out || (kind != MPCX_LOCALARS && (!k0 || !k1))) return fail(c, MPCX_EINVAL, "tr_keygen: null pointer");
   return c->bw == 32 ? tr_keygen_t<uint32_t>(c, kind, n, in, out, seed, gate, k0, k1)
                      : tr_keygen_t<uint64_t>(c, kind, n, in, out, seed, gate, k0, k1);
 }
@@ -394,8 +400,9 @@ static mpcx_status tr_eval_t(mpcx_ctx *c, int kind, size_t n, const void *k0, co
 mpcx_status mpcx_tr_eval(mpcx_ctx *c, int kind, size_t n, const void *k0, const void *k1, const void *x,
                          const void *bias, int ncol, void *y) {
   CHECK_CTX(c);
-  if (!valid_kind(kind) || (kind != MPCX_LOCALARS && (!k0 || !k1)) || !x || !y || (bias && ncol < 1))
-    return fail(c, MPCX_EINVAL, "tr_eval: bad argument");
+  if (!valid_kind(kind) || (bias && ncol < 1)) return fail(c, MPCX_EINVAL, "tr_eval: bad argument");
+  if (n == 0) return MPCX_OK;
+  if ((kind != MPCX_LOCALARS && (!k0 || !k1)) || !x || !y) return fail(c, MPCX_EINVAL, "tr_eval: null pointer");
   return c->bw == 32 ? tr_eval_t<uint32_t>(c, kind, n, k0, k1, x, bias, ncol, y)
                      : tr_eval_t<uint64_t>(c, kind, n, k0, k1, x, bias, ncol, y);
 }
@@ -531,6 +538,7 @@ mpcx_status mpcx_mul_keygen(mpcx_ctx *c, size_t nx, size_t ny, size_t nz, const 
                             const void *rx, const void *ry, void *rz, uint64_t seed, uint32_t gate, void *k0,
                             void *k1) {
   CHECK_CTX(c);
+  if (nx == 0 && ny == 0 && nz == 0) return MPCX_OK;
   if (!ia || !ib || !rx || !ry || !rz || !k0 || !k1) return fail(c, MPCX_EINVAL, "mul_keygen: null pointer");
   return c->bw == 32 ? mul_keygen_t<uint32_t>(c, nx, ny, nz, ia, ib, rx, ry, rz, seed, gate, k0, k1)
                      : mul_keygen_t<uint64_t>(c, nx, ny, nz, ia, ib, rx, ry, rz, seed, gate, k0, k1);
@@ -555,6 +563,7 @@ static mpcx_status mul_eval_t(mpcx_ctx *c, size_t nx, size_t ny, size_t nz, cons
 mpcx_status mpcx_mul_eval(mpcx_ctx *c, size_t nx, size_t ny, size_t nz, const uint32_t *ia, const uint32_t *ib,
                           const void *k0, const void *k1, const void *x, const void *y, void *z) {
   CHECK_CTX(c);
+  if (nz == 0) return MPCX_OK;  // no products
   if (!ia || !ib || !k0 || !k1 || !x || !y || !z) return fail(c, MPCX_EINVAL, "mul_eval: null pointer");
   return c->bw == 32 ? mul_eval_t<uint32_t>(c, nx, ny, nz, ia, ib, k0, k1, x, y, z)
                      : mul_eval_t<uint64_t>(c, nx, ny, nz, ia, ib, k0, k1, x, y, z);
@@ -575,6 +584,7 @@ static mpcx_status lut_keygen_t(mpcx_ctx *c, size_t n, const void *in, void *out
 mpcx_status mpcx_lut8_keygen(mpcx_ctx *c, size_t n, const void *in, void *out, uint64_t seed, uint32_t gate, void *k0,
                              void *k1) {
   CHECK_CTX(c);
+  if (n == 0) return MPCX_OK;
   if (!in || !out || !k0 || !k1) return fail(c, MPCX_EINVAL, "lut8_keygen: null pointer");
   return c->bw == 32 ? lut_keygen_t<uint32_t>(c, n, in, out, seed, gate, k0, k1)
                      : lut_keygen_t<uint64_t>(c, n, in, out, seed, gate, k0, k1);
@@ -601,6 +611,7 @@ static mpcx_status lut_eval_t(mpcx_ctx *c, size_t n, const void *k0, const void 
 mpcx_status mpcx_lut8_eval(mpcx_ctx *c, size_t n, const void *k0, const void *k1, const void *table, const void *x,
                            void *y) {
   CHECK_CTX(c);
+  if (n == 0) return MPCX_OK;
   if (!k0 || !k1 || !table || !x || !y) return fail(c, MPCX_EINVAL, "lut8_eval: null pointer");
   return c->bw == 32 ? lut_eval_t<uint32_t>(c, n, k0, k1, table, x, y)
                      : lut_eval_t<uint64_t>(c, n, k0, k1, table, x, y);
@@ -730,7 +741,9 @@ mpcx_status mpcx_ring_gemm(mpcx_ctx *c, int M, int K, int N, const void *a, cons
 mpcx_status mpcx_ring_lincomb(mpcx_ctx *c, size_t rows, size_t cols, uint64_t a, const void *x, uint64_t b,
                               const void *y, const void *v, int shift, void *out) {
   CHECK_CTX(c);
-  if (!out || cols == 0 || shift < 0 || shift >= c->bw) return fail(c, MPCX_EINVAL, "ring_lincomb: bad argument");
+  if (cols == 0 || shift < 0 || shift >= c->bw) return fail(c, MPCX_EINVAL, "ring_lincomb: bad argument");
+  if (rows == 0) return MPCX_OK;
+  if (!out) return fail(c, MPCX_EINVAL, "ring_lincomb: null pointer");
   if (c->bw == 32) {
     HIPC(c,
          launch_lincomb<uint32_t>(c->L, rows, cols, uint32_t(a), static_cast<const uint32_t *>(x), uint32_t(b),
@@ -761,6 +774,7 @@ static mpcx_status reveal_keygen_t(mpcx_ctx *c, size_t n, void *mask, uint64_t s
 }
 mpcx_status mpcx_reveal_keygen(mpcx_ctx *c, size_t n, void *mask, uint64_t seed, uint32_t gate, void *k0, void *k1) {
   CHECK_CTX(c);
+  if (n == 0) return MPCX_OK;
   if (!mask || !k0 || !k1) return fail(c, MPCX_EINVAL, "reveal_keygen: null pointer");
   return c->bw == 32 ? reveal_keygen_t<uint32_t>(c, n, mask, seed, gate, k0, k1)
                      : reveal_keygen_t<uint64_t>(c, n, mask, seed, gate, k0, k1);
@@ -784,6 +798,7 @@ static mpcx_status reveal_eval_t(mpcx_ctx *c, size_t n, const void *k0, const vo
 mpcx_status mpcx_reveal_eval(mpcx_ctx *c, size_t n, const void *k0, const void *k1, const void *v0, const void *v1,
                              void *out) {
   CHECK_CTX(c);
+  if (n == 0) return MPCX_OK;
   if (!k0 || !k1 || !v0 || !v1 || !out) return fail(c, MPCX_EINVAL, "reveal_eval: null pointer");
   return c->bw == 32 ? reveal_eval_t<uint32_t>(c, n, k0, k1, v0, v1, out)
                      : reveal_eval_t<uint64_t>(c, n, k0, k1, v0, v1, out);

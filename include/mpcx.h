@@ -12,7 +12,10 @@
  * (not vendored); their signatures are those used at the cited call sites.
  *
  * Ring elements: uint32_t when bw == 32, uint64_t when bw == 64 ("T" below).
- * Device pointers are marked d_, host pointers h_.
+ * Device pointers are marked d_, host pointers h_.  A gate call over zero
+ * elements (n = 0; nz = 0 for mpcx_mul_eval, rows = 0 for mpcx_ring_lincomb)
+ * returns MPCX_OK without reading its pointers or counting an exchange; matrix
+ * dimensions (B, N, C, nb, M, K) must be at least 1.
  */
 #ifndef MPCX_H
 #define MPCX_H

@@ -186,6 +186,33 @@ def test_drelu_keys_and_eval(ctx, orc):
     assert np.array_equal(y.astype(np.uint64) ^ orbit, (x >= 0).astype(np.uint64))
 
 
+def test_empty_inputs_are_no_ops(ctx):
+    """Every gate entry point over zero elements returns MPCX_OK without reading
+    its (null) pointers or counting an exchange; bad kinds are still refused."""
+    lib, h, N = ctx.lib, ctx.h, None
+    ctx.reset_counters()
+    for kind in (1, 2, 3, 4, 9, 10, 11):
+        assert ctx.lib.mpcx_tr_key_bytes(h, kind, 0) == 0
+        assert lib.mpcx_tr_keygen(h, kind, 0, N, N, 1, 1, N, N) == 0
+        assert lib.mpcx_tr_eval(h, kind, 0, N, N, N, N, 0, N) == 0
+    assert lib.mpcx_tr_eval(h, 99, 0, N, N, N, N, 0, N) != 0
+    assert lib.mpcx_dcf_keygen(h, 31, 0, N, N, 1, 1, N, N) == 0
+    assert lib.mpcx_dcf_eval(h, 0, 31, 0, N, N, N) == 0
+    assert lib.mpcx_mul_keygen(h, 0, 0, 0, N, N, N, N, N, 1, 1, N, N) == 0
+    assert lib.mpcx_mul_eval(h, 0, 0, 0, N, N, N, N, N, N, N) == 0
+    assert lib.mpcx_lut8_keygen(h, 0, N, N, 1, 1, N, N) == 0
+    assert lib.mpcx_lut8_eval(h, 0, N, N, N, N, N) == 0
+    assert lib.mpcx_reveal_keygen(h, 0, N, 1, 1, N, N) == 0
+    assert lib.mpcx_reveal_eval(h, 0, N, N, N, N, N) == 0
+    assert lib.mpcx_prg_hash(h, 0, 0, N, N) == 0
+    assert lib.mpcx_prf(h, 1, 1, 1, 0, N) == 0
+    assert lib.mpcx_ring_lincomb(h, 0, 5, 1, N, 0, N, N, 0, N) == 0
+    assert ctx.bytes_exchanged == 0 and ctx.lib.mpcx_rounds(h) == 0
+    # matrix shapes must be non-empty
+    assert lib.mpcx_maxpool_eval(h, 0, 3, 3, N, N, N, N) != 0
+    assert lib.mpcx_ring_gemm(h, 0, 3, 3, N, N, N) != 0
+
+
 def test_all_aes_variants_agree(mp, orc):
     c = mp.Ctx(bw=32)
     rng = np.random.default_rng(4)
