@@ -72,6 +72,8 @@ _SIGS = {
                                 C.c_void_p, C.c_void_p, C.c_void_p]),
     "mpcx_ring_gemm": (C.c_int, [C.c_void_p, C.c_int, C.c_int, C.c_int, C.c_void_p, C.c_void_p,
                                  C.c_void_p]),
+    "mpcx_ring_lincomb": (C.c_int, [C.c_void_p, C.c_size_t, C.c_size_t, C.c_uint64, C.c_void_p, C.c_uint64,
+                                    C.c_void_p, C.c_void_p, C.c_int, C.c_void_p]),
     "mpcx_reveal_key_bytes": (C.c_size_t, [C.c_void_p, C.c_size_t]),
     "mpcx_reveal_keygen": (C.c_int, [C.c_void_p, C.c_size_t, C.c_void_p, C.c_uint64, C.c_uint32, C.c_void_p,
                                      C.c_void_p]),
