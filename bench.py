@@ -516,6 +516,7 @@ def run_adjnorm(args):
     ctx = mpcx.Ctx(bw=bw)
     if args.aes_variant >= 0:
         ctx.set_aes_variant(args.aes_variant)
+    ctx.set_adjnorm_lanes(args.lanes)  # concurrent graph groups, each on its own stream
     k0, k1, mask = ctx.adjnorm_keygen(B, N, seed=0xADD + args.seed)
     d0, d1 = mpcx.to_dev(ctx.ring(a0)), mpcx.to_dev(ctx.ring(a1))
     out = mpcx.empty_dev(B * N * N * 4)
@@ -553,8 +554,9 @@ def run_adjnorm(args):
         "n_gpus": 1, "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(1e3 * per, 3),
         "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "u32",
         "data": "synthetic molecular graphs (random trees + ring closures, 10-60 atoms, self loops)",
-        "config": {"workload": f"secure adjacency normalisation, B={B} graphs x N={N}, bw=32 s=12, keys resident",
-                   "B": B, "N": N},
+        "config": {"workload": f"secure adjacency normalisation, B={B} graphs x N={N}, bw=32 s=12, keys resident, "
+                               f"{args.lanes} concurrent graph groups",
+                   "B": B, "N": N, "lanes": args.lanes},
         "lut_evals_per_s": round(B * N / per, 1),
         "beaver_products_per_s": round(2 * B * N * N / per, 1),
         "truncations_per_s": round(B * P / per, 1),

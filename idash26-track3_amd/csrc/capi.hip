@@ -128,6 +128,7 @@ struct mpcx_ctx {
   void *scratch = nullptr;
   size_t scratch_bytes = 0;
   AdjNormCache *adj = nullptr;  // prepared state of mpcx_adjnorm_eval
+  int adj_lanes = 1;            // concurrent graph groups of the adjacency normalisation
 };
 
 struct mpcx_model {
@@ -805,14 +806,23 @@ mpcx_status mpcx_reveal_eval(mpcx_ctx *c, size_t n, const void *k0, const void *
 }
 
 // ---------------- adjacency normalisation ----------------
+mpcx_status mpcx_set_adjnorm_lanes(mpcx_ctx *c, int lanes) {
+  CHECK_CTX(c);
+  if (lanes < 1 || lanes > 16) return fail(c, MPCX_EINVAL, "adjnorm lanes must be in [1, 16]");
+  c->adj_lanes = lanes;
+  return MPCX_OK;
+}
+
 size_t mpcx_adjnorm_key_bytes(mpcx_ctx *c, int B, int N) {
-  return (c && B > 0 && N > 0) ? adjnorm_key_bytes(c->bw, c->s, B, N) : 0;
+  return (c && B > 0 && N > 0) ? adjnorm_key_bytes(c->bw, c->s, B, N, c->adj_lanes) : 0;
 }
 
 mpcx_status mpcx_adjnorm_keygen(mpcx_ctx *c, int B, int N, uint64_t seed, void *mask, void *k0, void *k1) {
   CHECK_CTX(c);
   if (B < 1 || N < 1 || N > 255 || !mask || !k0 || !k1) return fail(c, MPCX_EINVAL, "adjnorm_keygen: bad argument");
-  HIPC(c, adjnorm_keygen(c->bw, c->s, B, N, seed, c->L, mask, static_cast<uint8_t *>(k0), static_cast<uint8_t *>(k1)),
+  HIPC(c,
+       adjnorm_keygen(c->bw, c->s, B, N, seed, c->adj_lanes, c->L, mask, static_cast<uint8_t *>(k0),
+                      static_cast<uint8_t *>(k1)),
        "adjnorm_keygen");
   return MPCX_OK;
 }
@@ -823,8 +833,8 @@ mpcx_status mpcx_adjnorm_eval(mpcx_ctx *c, int B, int N, int nmax, const void *k
   if (B < 1 || N < 1 || N > 255 || nmax < 0 || nmax > 255 || !k0 || !k1 || !a0 || !a1 || !out)
     return fail(c, MPCX_EINVAL, "adjnorm_eval: bad argument");
   HIPC(c,
-       adjnorm_eval(c->bw, c->s, B, N, nmax, c->L, static_cast<const uint8_t *>(k0), static_cast<const uint8_t *>(k1),
-                    a0, a1, out, &c->counters, &c->adj),
+       adjnorm_eval(c->bw, c->s, B, N, nmax, c->adj_lanes, c->L, static_cast<const uint8_t *>(k0),
+                    static_cast<const uint8_t *>(k1), a0, a1, out, &c->counters, &c->adj),
        "adjnorm_eval");
   return MPCX_OK;
 }

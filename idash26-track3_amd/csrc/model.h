@@ -195,14 +195,15 @@ LaneSet *make_lane_set(int bw, int s, const ModelDims &d, const int64_t *W, size
 // ddgSecureAdjNormKeygen / ddgSecureAdjNormEval (gpu_mpc/secure_adj_norm.h:203-374,
 // 393-659): A (B x N x N, 0/1 with self loops) as additive shares -> masked
 // A_norm = A (.) floor(T[d_i] T[d_j] / 2^s) + out_mask.
-size_t adjnorm_key_bytes(int bw, int s, int B, int N);
-hipError_t adjnorm_keygen(int bw, int s, int B, int N, uint64_t seed, const Launch &L, void *out_mask,
+size_t adjnorm_key_bytes(int bw, int s, int B, int N, int lanes);
+hipError_t adjnorm_keygen(int bw, int s, int B, int N, uint64_t seed, int lanes, const Launch &L, void *out_mask,
                           uint8_t *k0, uint8_t *k1);
-// *cache keeps the index maps, D^-1/2 table and scratch of the last (bw, B, N,
-// nmax) between calls (created on first use; free with adjnorm_cache_free).
+// *cache keeps, per lane, the index maps, D^-1/2 table, scratch and stream of
+// the last (bw, B, N, nmax) between calls (created on first use; free with
+// adjnorm_cache_free).
 struct AdjNormCache;
 void adjnorm_cache_free(AdjNormCache *cache);
-hipError_t adjnorm_eval(int bw, int s, int B, int N, int nmax, const Launch &L, const uint8_t *k0,
+hipError_t adjnorm_eval(int bw, int s, int B, int N, int nmax, int lanes, const Launch &L, const uint8_t *k0,
                         const uint8_t *k1, const void *a0, const void *a1, void *out_masked, Counters *ctr,
                         AdjNormCache **cache);
 

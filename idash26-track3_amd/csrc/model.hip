@@ -442,12 +442,15 @@ struct AdjNorm {
   }
 
   // a0, a1: A shares (BNN); Ah: revealed A (BNN); An: masked A_norm (BNN)
-  hipError_t eval(Runner<T> &r, const T *a0, const T *a1, T *Ah, T *An) {
+  // pre_done (optional): recorded on the runner's stream once the memory-bound
+  // gates before the truncation are enqueued (a pipelined next group waits on it)
+  hipError_t eval(Runner<T> &r, const T *a0, const T *a1, T *Ah, T *An, hipEvent_t pre_done = nullptr) {
     const size_t BN = size_t(B) * N, BNN = BN * N, BP = size_t(B) * pairs_of(N);
     TRY(r.reveal(BNN, a0, a1, 0, Ah));
     TRY(r.reveal(BN, a0, a1, N, t0.p));  // degree = row sums of the A shares
     TRY(r.lut8(BN, table.p, t0.p, t1.p, t0.p));
     TRY(r.mul(BN, BN, BP, MulMap::of(MulMap::OUTER_TRI, N), t0.p, t0.p, p0.p));
+    if (pre_done) TRY(hipEventRecord(pre_done, r.L.stream));
     TRY(r.tr(G_TRSLACK, BP, p0.p, nullptr, 1, p1.p));
     TRY(r.mul(BNN, BP, BNN, MulMap::of(MulMap::SYM_HADAMARD, N), Ah, p1.p, An));
     return hipSuccess;
@@ -1840,24 +1843,45 @@ LaneSet *make_lane_set(int bw, int s, const ModelDims &d, const int64_t *W, size
 // ===========================================================================
 // standalone secure adjacency normalisation
 // ===========================================================================
-size_t adjnorm_key_bytes(int bw, int s, int B, int N) { return AdjNorm<uint32_t>::layout_end(bw, s, B, N, 0); }
+// With L lanes the B graphs are split into L groups of consecutive graphs (B/L
+// each, the first B % L one larger, as the model's lanes); group i's key set is
+// the one-lane key set of its graphs under the lane seed, the sets back to back.
+namespace {
+int adj_lanes(int B, int lanes) { return std::max(1, std::min(lanes, B)); }
+int adj_lane_B(int B, int L, int i) { return B / L + (i < B % L ? 1 : 0); }
+int adj_lane_off(int B, int L, int i) { return i * (B / L) + std::min(i, B % L); }
+}  // namespace
 
-template <typename T>
-static hipError_t adjnorm_keygen_t(int bw, int s, int B, int N, uint64_t seed, const Launch &L, void *out_mask,
-                                   uint8_t *k0, uint8_t *k1) {
-  AdjNorm<T> adj;
-  TRY(adj.prepare(B, N, s, 0));
-  DevBuf<T> rA;
-  TRY(rA.alloc(size_t(B) * N * N));
-  Dealer<T> d{L, bw, s, seed, k0, k1, Cursor{}};
-  TRY(adj.keygen(d, rA.p, static_cast<T *>(out_mask)));
-  return hipStreamSynchronize(L.stream);
+size_t adjnorm_key_bytes(int bw, int s, int B, int N, int lanes) {
+  const int L = adj_lanes(B, lanes);
+  size_t o = 0;
+  for (int i = 0; i < L; i++) o = AdjNorm<uint32_t>::layout_end(bw, s, adj_lane_B(B, L, i), N, o);
+  return o;
 }
 
-hipError_t adjnorm_keygen(int bw, int s, int B, int N, uint64_t seed, const Launch &L, void *out_mask, uint8_t *k0,
-                          uint8_t *k1) {
-  return bw == 32 ? adjnorm_keygen_t<uint32_t>(bw, s, B, N, seed, L, out_mask, k0, k1)
-                  : adjnorm_keygen_t<uint64_t>(bw, s, B, N, seed, L, out_mask, k0, k1);
+template <typename T>
+static hipError_t adjnorm_keygen_t(int bw, int s, int B, int N, uint64_t seed, int lanes, const Launch &L,
+                                   void *out_mask, uint8_t *k0, uint8_t *k1) {
+  const int nl = adj_lanes(B, lanes);
+  size_t o = 0;
+  for (int i = 0; i < nl; i++) {
+    const int Bi = adj_lane_B(B, nl, i);
+    AdjNorm<T> adj;
+    TRY(adj.prepare(Bi, N, s, 0));
+    DevBuf<T> rA;
+    TRY(rA.alloc(size_t(Bi) * N * N));
+    Dealer<T> d{L, bw, s, LaneSet::lane_seed(seed, i), k0 + o, k1 + o, Cursor{}};
+    TRY(adj.keygen(d, rA.p, static_cast<T *>(out_mask) + size_t(adj_lane_off(B, nl, i)) * N * N));
+    TRY(hipStreamSynchronize(L.stream));  // rA and the lane's scratch are freed below
+    o = AdjNorm<T>::layout_end(bw, s, Bi, N, o);
+  }
+  return hipSuccess;
+}
+
+hipError_t adjnorm_keygen(int bw, int s, int B, int N, uint64_t seed, int lanes, const Launch &L, void *out_mask,
+                          uint8_t *k0, uint8_t *k1) {
+  return bw == 32 ? adjnorm_keygen_t<uint32_t>(bw, s, B, N, seed, lanes, L, out_mask, k0, k1)
+                  : adjnorm_keygen_t<uint64_t>(bw, s, B, N, seed, lanes, L, out_mask, k0, k1);
 }
 
 struct AdjNormCache {
@@ -1868,18 +1892,34 @@ struct AdjNormCache {
 void adjnorm_cache_free(AdjNormCache *cache) { delete cache; }
 
 namespace {
+// per lane: the prepared block (index maps, table, scratch), its workspace and,
+// past lane 0, its own stream and the events that join it to the caller's stream
 template <typename T>
-struct AdjNormCacheT final : AdjNormCache {
+struct AdjLane {
   AdjNorm<T> adj;
   DevBuf<T> Ah;
   Workspace<T> ws;
+  hipStream_t st = nullptr;
+  hipEvent_t pre = nullptr, done = nullptr;
+  ~AdjLane() {
+    if (st) {
+      (void)hipStreamSynchronize(st);
+      (void)hipStreamDestroy(st);
+    }
+    if (pre) (void)hipEventDestroy(pre);
+    if (done) (void)hipEventDestroy(done);
+  }
+};
+template <typename T>
+struct AdjNormCacheT final : AdjNormCache {
+  std::vector<std::unique_ptr<AdjLane<T>>> lanes;
 };
 }  // namespace
 
 template <typename T>
-static hipError_t adjnorm_eval_t(int bw, int s, int B, int N, int nmax, const Launch &L, const uint8_t *k0,
-                                 const uint8_t *k1, const void *a0, const void *a1, void *out, Counters *ctr,
-                                 AdjNormCache **cache) {
+static hipError_t adjnorm_eval_t(int bw, int s, int B, int N, int nmax, int lanes, const Launch &L,
+                                 const uint8_t *k0, const uint8_t *k1, const void *a0, const void *a1, void *out,
+                                 Counters *ctr, AdjNormCache **cache) {
   if (*cache && (*cache)->bw != bw) {
     TRY(hipStreamSynchronize(L.stream));
     delete *cache;
@@ -1891,24 +1931,57 @@ static hipError_t adjnorm_eval_t(int bw, int s, int B, int N, int nmax, const La
     *cache = c;
   }
   auto *st = static_cast<AdjNormCacheT<T> *>(*cache);
-  TRY(st->adj.prepare(B, N, s, nmax));
-  const size_t BNN = size_t(B) * N * N;
-  TRY(st->Ah.alloc(BNN));
-  TRY(st->ws.ensure(std::max(BNN, size_t(B) * pairs_of(N))));
-  ArenaSource src;
-  src.k[0] = k0;
-  src.k[1] = k1;
-  src.bytes = AdjNorm<T>::layout_end(bw, s, B, N, 0);
+  const int nl = adj_lanes(B, lanes);
+  while (int(st->lanes.size()) < nl) {
+    auto ln = std::make_unique<AdjLane<T>>();
+    TRY(hipEventCreateWithFlags(&ln->pre, hipEventDisableTiming));
+    if (!st->lanes.empty()) {  // lane 0 runs on the caller's stream
+      TRY(hipStreamCreateWithFlags(&ln->st, hipStreamNonBlocking));
+      TRY(hipEventCreateWithFlags(&ln->done, hipEventDisableTiming));
+    }
+    st->lanes.push_back(std::move(ln));
+  }
   Counters local;
-  Runner<T> r(L, bw, s, st->ws, ctr ? *ctr : local, nullptr, src);
-  TRY(st->adj.eval(r, static_cast<const T *>(a0), static_cast<const T *>(a1), st->Ah.p, static_cast<T *>(out)));
+  Counters &cnt = ctr ? *ctr : local;
+  const size_t es = sizeof(T), NN = size_t(N) * N;
+  size_t o = 0;
+  for (int i = 0; i < nl; i++) {
+    AdjLane<T> &ln = *st->lanes[size_t(i)];
+    const int Bi = adj_lane_B(B, nl, i);
+    const size_t g0 = size_t(adj_lane_off(B, nl, i));
+    Launch Li = L;
+    if (i > 0) {
+      // Group i starts once group i-1 has enqueued its memory-bound gates before
+      // the truncation (which also orders it after the caller's stream): its
+      // reveals and products then run beside group i-1's DCF work instead of
+      // in step with them.
+      Li.stream = ln.st;
+      TRY(hipStreamWaitEvent(ln.st, st->lanes[size_t(i - 1)]->pre, 0));
+    }
+    TRY(ln.adj.prepare(Bi, N, s, nmax));
+    const size_t BNN = size_t(Bi) * NN;
+    TRY(ln.Ah.alloc(BNN));
+    TRY(ln.ws.ensure(std::max(BNN, size_t(Bi) * pairs_of(N))));
+    ArenaSource src;
+    src.k[0] = k0 + o;
+    src.k[1] = k1 + o;
+    src.bytes = AdjNorm<T>::layout_end(bw, s, Bi, N, 0);
+    Runner<T> r(Li, bw, s, ln.ws, cnt, nullptr, src);
+    auto at = [&](const void *p) { return reinterpret_cast<const T *>(static_cast<const uint8_t *>(p) + g0 * NN * es); };
+    TRY(ln.adj.eval(r, at(a0), at(a1), ln.Ah.p,
+                    reinterpret_cast<T *>(static_cast<uint8_t *>(out) + g0 * NN * es), nl > 1 ? ln.pre : nullptr));
+    if (i > 0) TRY(hipEventRecord(ln.done, ln.st));
+    o = AdjNorm<T>::layout_end(bw, s, Bi, N, o);
+  }
+  for (int i = 1; i < nl; i++) TRY(hipStreamWaitEvent(L.stream, st->lanes[size_t(i)]->done, 0));
   return hipStreamSynchronize(L.stream);
 }
 
-hipError_t adjnorm_eval(int bw, int s, int B, int N, int nmax, const Launch &L, const uint8_t *k0, const uint8_t *k1,
-                        const void *a0, const void *a1, void *out, Counters *ctr, AdjNormCache **cache) {
-  return bw == 32 ? adjnorm_eval_t<uint32_t>(bw, s, B, N, nmax, L, k0, k1, a0, a1, out, ctr, cache)
-                  : adjnorm_eval_t<uint64_t>(bw, s, B, N, nmax, L, k0, k1, a0, a1, out, ctr, cache);
+hipError_t adjnorm_eval(int bw, int s, int B, int N, int nmax, int lanes, const Launch &L, const uint8_t *k0,
+                        const uint8_t *k1, const void *a0, const void *a1, void *out, Counters *ctr,
+                        AdjNormCache **cache) {
+  return bw == 32 ? adjnorm_eval_t<uint32_t>(bw, s, B, N, nmax, lanes, L, k0, k1, a0, a1, out, ctr, cache)
+                  : adjnorm_eval_t<uint64_t>(bw, s, B, N, nmax, lanes, L, k0, k1, a0, a1, out, ctr, cache);
 }
 
 }  // namespace mpcx

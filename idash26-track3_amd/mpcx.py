@@ -74,6 +74,7 @@ _SIGS = {
                                  C.c_void_p]),
     "mpcx_ring_lincomb": (C.c_int, [C.c_void_p, C.c_size_t, C.c_size_t, C.c_uint64, C.c_void_p, C.c_uint64,
                                     C.c_void_p, C.c_void_p, C.c_int, C.c_void_p]),
+    "mpcx_set_adjnorm_lanes": (C.c_int, [C.c_void_p, C.c_int]),
     "mpcx_reveal_key_bytes": (C.c_size_t, [C.c_void_p, C.c_size_t]),
     "mpcx_reveal_keygen": (C.c_int, [C.c_void_p, C.c_size_t, C.c_void_p, C.c_uint64, C.c_uint32, C.c_void_p,
                                      C.c_void_p]),
@@ -383,6 +384,11 @@ class Ctx:
         return from_dev(out, self.T, v0.size)
 
     # ---------------- adjacency normalisation ----------------
+    def set_adjnorm_lanes(self, lanes):
+        """Concurrent graph groups of the adjacency normalisation (keygen and eval
+        must agree: the key set is the groups' key sets back to back)."""
+        self.check(self.lib.mpcx_set_adjnorm_lanes(self.h, int(lanes)), "set_adjnorm_lanes")
+
     def adjnorm_keygen(self, B, N, seed=1):
         nb = self.lib.mpcx_adjnorm_key_bytes(self.h, B, N)
         k0, k1 = empty_dev(nb), empty_dev(nb)

@@ -220,6 +220,14 @@ mpcx_status mpcx_reveal_eval(mpcx_ctx *ctx, size_t n, const void *d_key0, const 
  * one exact truncation, Beaver A (.) W.  a0, a1: both parties' shares of A
  * (B x N x N ring elements, N <= 255); out: A_norm + out_mask. */
 size_t mpcx_adjnorm_key_bytes(mpcx_ctx *ctx, int B, int N);
+/* Concurrent graph groups (1..16, default 1) of the adjacency normalisation
+ * calls of this context: the B graphs are split into that many groups of
+ * consecutive graphs (B/L each, the first B%L one larger), each evaluated on its
+ * own stream so that one group's DCF work overlaps another's memory-bound
+ * gates.  The key set is the groups' one-group key sets back to back, group i
+ * keyed under seed + i * 0x9E3779B97F4A7C15: keygen and eval must use the same
+ * setting (like the model's lanes, mpcx_model_set_lanes). */
+mpcx_status mpcx_set_adjnorm_lanes(mpcx_ctx *ctx, int lanes);
 mpcx_status mpcx_adjnorm_keygen(mpcx_ctx *ctx, int B, int N, uint64_t seed, void *d_out_mask, void *d_key0,
                                 void *d_key1);
 mpcx_status mpcx_adjnorm_eval(mpcx_ctx *ctx, int B, int N, int nmax, const void *d_key0, const void *d_key1,

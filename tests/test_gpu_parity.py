@@ -772,6 +772,41 @@ def test_adjnorm_keys_and_eval(mp, orc, synth, bw):
     c.close()
 
 
+@pytest.mark.parametrize("bw,lanes", [(32, 3), (64, 2)])
+def test_adjnorm_lanes(mp, orc, synth, bw, lanes):
+    """Concurrent graph groups: the key set is the groups' one-group key sets
+    (group i under seed + i * 0x9E3779B97F4A7C15) back to back, byte-identical
+    to the oracle dealer's; the outputs and exchange bytes are the groups'."""
+    B, N, seed = 5, 20, 321
+    _, A, _ = synth.molecules(B, synth.Dims(bw=bw, n_nodes=N), seed=6, min_atoms=3, max_atoms=N)
+    a0, a1 = synth.share(A, bw, 78)
+    c = mp.Ctx(bw=bw)
+    c.set_adjnorm_lanes(lanes)
+    g0, g1, gmask = c.adjnorm_keygen(B, N, seed=seed)
+    sizes = [B // lanes + (1 if i < B % lanes else 0) for i in range(lanes)]
+    ok0, ok1, omask, want, oby, g = [], [], [], [], 0, 0
+    for i, Bi in enumerate(sizes):
+        si = (seed + i * 0x9E3779B97F4A7C15) % (1 << 64)
+        k0, k1, m = orc.adjnorm_keygen(bw, S, Bi, N, si)
+        ok0.append(k0)
+        ok1.append(k1)
+        omask.append(m)
+        y, by = orc.adjnorm_eval(bw, S, Bi, N, 138, k0, k1, a0[g:g + Bi], a1[g:g + Bi])
+        want.append(y)
+        oby += by
+        g += Bi
+    o0, o1 = np.concatenate(ok0), np.concatenate(ok1)
+    assert c.lib.mpcx_adjnorm_key_bytes(c.h, B, N) == o0.size
+    assert np.array_equal(host(g0)[:o0.size], o0) and np.array_equal(host(g1)[:o1.size], o1)
+    assert np.array_equal(mp.from_dev(gmask, c.T, B * N * N).astype(np.uint64), np.concatenate(omask))
+    c.reset_counters()
+    for _ in range(2):  # the second call reuses the prepared groups and streams
+        got = c.adjnorm_eval(B, N, 138, g0, g1, a0, a1)
+        assert np.array_equal(got.astype(np.uint64), np.concatenate(want))
+    assert c.bytes_exchanged == 2 * oby
+    c.close()
+
+
 @pytest.mark.parametrize("bw", [32, 64])
 def test_adjnorm_max_nodes_and_degrees(mp, orc, bw):
     """N = 255 (the 8-bit degree domain's limit): a star whose centre has degree
