@@ -65,9 +65,11 @@ def main():
                          "aggregation A.XW + bias (then a small-domain ReLU); 3 every layer truncation local "
                          "(LocalARS, the reference's default; not bit-exact, bw=64 only in practice)")
     ap.add_argument("--xw-slack", action="store_true", help="same as --slack 1")
-    ap.add_argument("--workload", choices=("affinity", "relu", "adjnorm"), default="affinity",
+    ap.add_argument("--workload", choices=("affinity", "relu", "adjnorm", "copy"), default="affinity",
                     help="affinity: the secure forward (default); relu: secure ReLU over --n elements (bw=32); "
-                         "adjnorm: secure adjacency normalisation of B=1024 graphs (bw=32)")
+                         "adjnorm: secure adjacency normalisation of B=1024 graphs (bw=32); copy: a 1 GiB "
+                         "elementwise kernel (b = a + 1 over 2^28 int32), the HBM reference for the PMC byte "
+                         "counters and the achievable copy bandwidth")
     ap.add_argument("--n", type=int, default=1 << 24, help="elements of the relu workload")
     ap.add_argument("--stream", action="store_true",
                     help="bw=64 streamed-key workload: micro-batches of --batch (default 256) over --total samples, "
@@ -94,6 +96,8 @@ def main():
         return run_relu(args)
     if args.workload == "adjnorm":
         return run_adjnorm(args)
+    if args.workload == "copy":
+        return run_copy(args)
 
     import numpy as np
 
@@ -406,6 +410,36 @@ def _oracle():
     sys.path.insert(0, os.path.join(ROOT, "oracle"))
     import orc
     return orc
+
+
+def run_copy(args):
+    """b = a + 1 over 2^28 int32 on the device (1 GiB read, 1 GiB written per
+    step): the plain copy whose FETCH_SIZE / WRITE_SIZE readings scale those
+    counters to bytes, and the HBM bandwidth an elementwise kernel reaches."""
+    import torch
+
+    n = 1 << 28
+    a = torch.ones(n, dtype=torch.int32, device="cuda")
+    b = torch.empty_like(a)
+    for _ in range(args.warmup):
+        torch.add(a, 1, out=b)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        torch.add(a, 1, out=b)
+    torch.cuda.synchronize()
+    elapsed = time.perf_counter() - t0
+    assert int(b[0].item()) == 2 and int(b[-1].item()) == 2
+    gbs = 2 * 4 * n * args.steps / elapsed / 1e9
+    print(json.dumps({
+        "metric": "elementwise copy bandwidth (read + write, 1 GPU)", "value": round(gbs, 1), "unit": "GB/s",
+        "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+        "ms_per_step": round(1e3 * elapsed / max(args.steps, 1), 3), "higher_is_better": True, "scaling": "weak",
+        "vs_baseline": None, "dtype": "int32", "data": "synthetic",
+        "config": {"workload": "b = a + 1 over 2^28 int32 (1 GiB read, 1 GiB written per step)"},
+        "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(gbs / HBM_PEAK_GBS, 4)},
+    }), flush=True)
 
 
 def run_relu(args):
