@@ -21,10 +21,11 @@ METRIC = "online secure samples/s (bw=32, B=64, 1 GPU); DCF evals/s; % roofline"
 # Peak integer VALU rate of MI355X: 256 CUs x 4 SIMD x 16 lanes x 2.4 GHz.
 VALU_PEAK_TOPS = 256 * 64 * 2.4e9 / 1e12
 HBM_PEAK_GBS = 8000.0
-# Ring multiply-adds per second at the peak of each Z_2^32 GEMM path: the int8
-# matrix cores (5.0 POP/s dense = 2.5 P int8 MAC/s) spend 16 int8 MACs per ring
-# MAC (four digit bytes x four shift MFMAs); the VALU path 2 instructions.
-GEMM_PEAK_TMACS = {"mfma": 5.0e3 / 2 / 16, "valu": VALU_PEAK_TOPS / 2}
+# Ring multiply-adds per second at the peak of each GEMM path: the int8 matrix
+# cores (5.0 POP/s dense = 2.5 P int8 MAC/s) spend 16 int8 MACs per Z_2^32 MAC
+# (four digit bytes x four shift MFMAs) and 64 per Z_2^64 MAC (eight x eight);
+# the VALU path 2 instructions per MAC.
+GEMM_PEAK_TMACS = {"mfma32": 5.0e3 / 2 / 16, "mfma64": 5.0e3 / 2 / 64, "valu": VALU_PEAK_TOPS / 2}
 # VALU instructions per AES call of the DCF walk (one tree level: the unrolled
 # cipher, sigma, feed-forward and the level update), counted in the gfx950 ISA
 # of this build: hipcc --cuda-device-only -S csrc/kernels.hip, level-loop block
@@ -150,7 +151,7 @@ def main():
     key_gbs = prof["hbm_bytes"] / (dcf_ms / 1e3) / 1e9 if dcf_ms > 0 else 0.0
     achieved_tops = aes_per_s * VALU_OPS_PER_AES.get(variant, float("nan")) / 1e12
     step_tops = prof["aes_calls"] * VALU_OPS_PER_AES.get(variant, float("nan")) / (ms_per_step / 1e3) / 1e12
-    gemm_path = "valu" if (args.bw == 64 or os.environ.get("MPCX_GEMM") == "valu") else "mfma"
+    gemm_path = "valu" if os.environ.get("MPCX_GEMM") == "valu" else f"mfma{args.bw}"
     gemm_tmacs = prof["gemm_macs"] / (prof["gemm_ms"] / 1e3) / 1e12 if prof["gemm_ms"] > 0 else 0.0
     log(f"[bench] DCF phase-1: {prof['launches']} launches, {dcf_ms:.2f} ms/forward, "
         f"{dcf_evals_per_s / 1e9:.3f} G evals/s, {aes_per_s / 1e9:.2f} G AES/s")
@@ -207,7 +208,7 @@ def main():
         "roofline_gemm": {
             "kernel": f"ring GEMMs ({gemm_path}: public-weight products and SxS Beaver products, "
                       f"{prof['gemm_sections']} sections of the profiled forward)",
-            "bound": "mfma" if gemm_path == "mfma" else "valu",
+            "bound": "valu" if gemm_path == "valu" else "mfma",
             "achieved": round(gemm_tmacs, 3),
             "peak": round(GEMM_PEAK_TMACS[gemm_path], 2),
             "unit": "T ring MAC/s",

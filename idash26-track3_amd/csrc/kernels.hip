@@ -1353,6 +1353,165 @@ __global__ __launch_bounds__(256) void k_gemm_mfma(GemmArgs<uint32_t> g0, GemmAr
   gemm_mfma_tile<VA, VB>(second ? g1 : g0, second ? z - nz0 : z, As, Bt);
 }
 
+// ---------------------------------------------------------------------------
+// ring GEMM over Z_2^64 on the int8 matrix cores.  Eight balanced base-256
+// digits per word (the bytes of (a + 0x8080..80) ^ 0x8080..80 read as int8):
+// a*b mod 2^64 = sum_{s<8} 2^(8s) sum_{p+q=s} a_p b_q.  One MFMA takes 8
+// operand words per row and column (8 digit bytes each); with each row word's
+// digits permuted to (a_s, .., a_0, 0, ..) it returns the shift-s sum over those
+// 8 words, so eight MFMAs (s = 0..7) cover 8 k.  acc_s enters bits 8s..63 of the
+// result, so for s < 4 it must be exact in int32: |acc_s| <= K * 4 * 2^14, i.e.
+// K < 2^15 per product (launch_gemm keeps larger K on the VALU kernel).
+// Tile 64 x 64 per 256-thread block as in the Z_2^32 kernel; K slices of 32
+// words (64 u32 of LDS per row, B transposed).
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ uint64_t ring_digits64(uint64_t a) {
+  return (a + 0x8080808080808080ull) ^ 0x8080808080808080ull;
+}
+// v_perm_b32 selector of output bytes j0..j0+3 for shift s: digit s - j (bytes
+// 0..3 of the low source word, 4..7 of the high one), 0x0c (zero) when s < j
+constexpr uint32_t digit_sel(int s, int j0) {
+  uint32_t v = 0;
+  for (int j = 0; j < 4; j++) v |= uint32_t(s - (j0 + j) >= 0 ? s - (j0 + j) : 0x0c) << (8 * j);
+  return v;
+}
+
+__device__ __forceinline__ void gemm_mfma64_tile(const GemmArgs<uint64_t> &g, int z, uint32_t *As, uint32_t *Bt) {
+  constexpr int BM = 64, BN = 64, BK = 32, LD = 2 * BK + 4;  // LD in 32-bit words
+  const int Kp = (g.K + BK - 1) / BK * BK;
+  const int Kt = g.A1b ? Kp + g.K : g.K;
+  const int bz = z / g.ksplit, kz = z % g.ksplit;
+  const int kchunk = ((Kt + g.ksplit - 1) / g.ksplit + BK - 1) / BK * BK;
+  const int kbeg = kz * kchunk, kend = min(Kt, kbeg + kchunk);
+  const uint64_t *A1 = g.A1 + size_t(bz) * g.sA;
+  const uint64_t *A2 = g.A2 ? g.A2 + size_t(bz) * g.sA : nullptr;
+  const uint64_t *B1 = g.B1 + size_t(bz) * g.sB;
+  const uint64_t *B2 = g.B2 ? g.B2 + size_t(bz) * g.sB : nullptr;
+  const uint64_t *A1b = g.A1b ? g.A1b + size_t(bz) * g.sA : nullptr;
+  const uint64_t *B1b = g.B1b ? g.B1b + size_t(bz) * g.sB : nullptr;
+  const int m0 = blockIdx.y * BM, n0 = blockIdx.x * BN;
+  if (m0 >= g.M || n0 >= g.N) return;  // the grid spans the larger of two problems
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int li = lane & 15, lg = lane >> 4;
+  v4i_t acc[4][8];
+#pragma unroll
+  for (int t = 0; t < 4; t++)
+#pragma unroll
+    for (int q = 0; q < 8; q++) acc[t][q] = v4i_t{0, 0, 0, 0};
+  // staged word r (r < 8) of A: row (tid >> 5) + 8r, column tid & 31; of B:
+  // k (tid >> 6) + 4r, column tid & 63 (B stored transposed, Bt[n][k]); rows of
+  // 32 consecutive 8-byte words per 32 threads.  The next K slice is loaded into
+  // registers while the matrix cores work on the current one.
+  uint64_t ra[8], ra2[8], rb[8], rb2[8];
+  const int ar = tid >> 5, ac = tid & 31, bk = tid >> 6, bn = tid & 63;
+  struct Seg {
+    const uint64_t *a1, *a2, *b1, *b2;
+    int kk, klim;
+  };
+  auto seg_of = [&](int k0) {
+    const bool second = k0 >= Kp;  // uniform over the block
+    Seg sg;
+    sg.a1 = second ? A1b : A1;
+    sg.a2 = second ? nullptr : A2;
+    sg.b1 = second ? B1b : B1;
+    sg.b2 = second ? nullptr : B2;
+    sg.kk = second ? k0 - Kp : k0;
+    sg.klim = min(g.K, kend - (second ? Kp : 0));
+    return sg;
+  };
+  auto load = [&](int k0) {
+    const Seg sg = seg_of(k0);
+#pragma unroll
+    for (int r = 0; r < 8; r++) {
+      const int gm = m0 + ar + 8 * r, gk = sg.kk + ac;
+      const size_t idx = (gm < g.M && gk < sg.klim) ? size_t(gm) * g.K + gk : 0;
+      ra[r] = sg.a1[idx];
+      ra2[r] = sg.a2 ? sg.a2[idx] : 0ull;
+    }
+#pragma unroll
+    for (int r = 0; r < 8; r++) {
+      const int gk = sg.kk + bk + 4 * r, gn = n0 + bn;
+      const size_t idx = (gk < sg.klim && gn < g.N) ? size_t(gk) * g.N + gn : 0;
+      rb[r] = sg.b1[idx];
+      rb2[r] = sg.b2 ? sg.b2[idx] : 0ull;
+    }
+  };
+  // K columns past klim and rows past M / N are staged as zeros
+  auto store = [&](int k0) {
+    const Seg sg = seg_of(k0);
+#pragma unroll
+    for (int r = 0; r < 8; r++) {
+      const int row = ar + 8 * r;
+      const bool in = m0 + row < g.M && sg.kk + ac < sg.klim;
+      const uint64_t v = in ? ring_digits64(ra[r] - ra2[r]) : 0ull;
+      *reinterpret_cast<uint2 *>(&As[row * LD + 2 * ac]) = make_uint2(uint32_t(v), uint32_t(v >> 32));
+    }
+#pragma unroll
+    for (int r = 0; r < 8; r++) {
+      const int k = bk + 4 * r;
+      const bool in = sg.kk + k < sg.klim && n0 + bn < g.N;
+      const uint64_t v = in ? ring_digits64(rb[r] - rb2[r]) : 0ull;
+      *reinterpret_cast<uint2 *>(&Bt[bn * LD + 2 * k]) = make_uint2(uint32_t(v), uint32_t(v >> 32));
+    }
+  };
+  if (kbeg < kend) load(kbeg);
+  for (int k0 = kbeg; k0 < kend; k0 += BK) {
+    store(k0);
+    __syncthreads();
+    if (k0 + BK < kend) load(k0 + BK);
+#pragma unroll
+    for (int kc = 0; kc < BK / 8; kc++) {
+      // lane (li, lg): words 2 lg, 2 lg + 1 of the 8-word step, as (lo, hi) pairs
+      const uint4 a = *reinterpret_cast<const uint4 *>(&As[(wave * 16 + li) * LD + kc * 16 + lg * 4]);
+      v4i_t as[8];
+#pragma unroll
+      for (int q = 0; q < 8; q++) {
+        const uint32_t lo = digit_sel(q, 0), hi = digit_sel(q, 4);
+        as[q] = v4i_t{int(__builtin_amdgcn_perm(a.y, a.x, lo)), int(__builtin_amdgcn_perm(a.y, a.x, hi)),
+                      int(__builtin_amdgcn_perm(a.w, a.z, lo)), int(__builtin_amdgcn_perm(a.w, a.z, hi))};
+      }
+#pragma unroll
+      for (int t = 0; t < 4; t++) {
+        const uint4 b = *reinterpret_cast<const uint4 *>(&Bt[(t * 16 + li) * LD + kc * 16 + lg * 4]);
+        const v4i_t bv = v4i_t{int(b.x), int(b.y), int(b.z), int(b.w)};
+#pragma unroll
+        for (int q = 0; q < 8; q++) acc[t][q] = __builtin_amdgcn_mfma_i32_16x16x64_i8(as[q], bv, acc[t][q], 0, 0, 0);
+      }
+    }
+    __syncthreads();
+  }
+  uint64_t *C = g.C + size_t(bz) * g.sC;
+  const uint64_t *Cin = g.Cin ? g.Cin + size_t(bz) * g.sC : nullptr;
+#pragma unroll
+  for (int t = 0; t < 4; t++) {
+    const int gn = n0 + t * 16 + li;
+#pragma unroll
+    for (int r = 0; r < 4; r++) {
+      // accumulator register r of lane (li, lg): row 4*lg + r, column li of the tile
+      const int gm = m0 + wave * 16 + lg * 4 + r;
+      if (gm >= g.M || gn >= g.N) continue;
+      uint64_t v = 0;
+#pragma unroll
+      for (int q = 0; q < 8; q++) v += uint64_t(int64_t(acc[t][q][r])) << (8 * q);
+      if (g.sign < 0) v = 0ull - v;
+      const size_t idx = size_t(gm) * g.N + gn;
+      if (g.ksplit > 1)
+        atomicAdd(reinterpret_cast<unsigned long long *>(&C[idx]), static_cast<unsigned long long>(v));
+      else
+        C[idx] = Cin ? v + Cin[idx] : v;
+    }
+  }
+}
+
+// blockIdx.z < nz0: problem g0, else problem g1 (nz = batch * ksplit of each)
+__global__ __launch_bounds__(256) void k_gemm_mfma64(GemmArgs<uint64_t> g0, GemmArgs<uint64_t> g1, int nz0) {
+  __shared__ __align__(16) uint32_t As[64 * 68];
+  __shared__ __align__(16) uint32_t Bt[64 * 68];
+  const int z = int(blockIdx.z);
+  const bool second = z >= nz0;
+  gemm_mfma64_tile(second ? g1 : g0, second ? z - nz0 : z, As, Bt);
+}
+
 // C[b] = Cin[b] (or 0) before the split-K slices are added
 template <typename T>
 __global__ void k_gemm_init(int M, int N, int batch, size_t sC, const T *Cin, T *C) {
@@ -1371,6 +1530,11 @@ static bool gemm_vec_a(const GemmArgs<uint32_t> &g) {
 static bool gemm_vec_b(const GemmArgs<uint32_t> &g) {
   return g.N % 4 == 0 && (g.batch == 1 || g.sB % 4 == 0) && aligned16(g.B1) && aligned16(g.B2) && aligned16(g.B1b);
 }
+static hipError_t launch_mfma(const Launch &L, dim3 grid, const GemmArgs<uint64_t> &g0,
+                              const GemmArgs<uint64_t> &g1, int nz0) {
+  hipLaunchKernelGGL(k_gemm_mfma64, grid, dim3(256), 0, L.stream, g0, g1, nz0);
+  return hipGetLastError();
+}
 static hipError_t launch_mfma(const Launch &L, dim3 grid, const GemmArgs<uint32_t> &g0,
                               const GemmArgs<uint32_t> &g1, int nz0) {
   const bool va = gemm_vec_a(g0) && gemm_vec_a(g1), vb = gemm_vec_b(g0) && gemm_vec_b(g1);
@@ -1385,13 +1549,28 @@ static hipError_t launch_mfma(const Launch &L, dim3 grid, const GemmArgs<uint32_
   return hipGetLastError();
 }
 
+// K slice of the matrix-core kernels: 64 words (Z_2^32), 32 (Z_2^64)
+template <typename T>
+constexpr int mfma_bk() {
+  return sizeof(T) == 4 ? 64 : 32;
+}
+// the matrix-core path: selected (not MPCX_GEMM=valu), and for Z_2^64 a total K
+// below 2^15 (the low shifts' int32 sums stay exact)
+template <typename T>
+static bool use_mfma(const Launch &L, const GemmArgs<T> &g) {
+  if (L.gemm != 0) return false;
+  constexpr int bk = mfma_bk<T>();
+  const int Kt = g.A1b ? (g.K + bk - 1) / bk * bk + g.K : g.K;
+  return sizeof(T) == 4 || Kt < (1 << 15);
+}
 // split-K factor: enough K slices that the launch has about two tiles per CU
 template <typename T>
 static int gemm_ksplit(const Launch &L, const GemmArgs<T> &g, int tiles, bool mfma) {
-  const int Kt = g.A1b ? (g.K + 63) / 64 * 64 + g.K : g.K;
+  constexpr int bk = mfma_bk<T>();
+  const int Kt = g.A1b ? (g.K + bk - 1) / bk * bk + g.K : g.K;
   if (tiles >= L.num_cu || Kt < 64) return 1;
   const int want = (2 * L.num_cu + tiles - 1) / tiles;
-  return std::max(1, std::min(want, mfma ? (Kt + 63) / 64 : Kt / 32));
+  return std::max(1, std::min(want, mfma ? (Kt + bk - 1) / bk : Kt / 32));
 }
 template <typename T>
 static int gemm_tiles(const GemmArgs<T> &g) {
@@ -1409,8 +1588,7 @@ static hipError_t gemm_init(const Launch &L, const GemmArgs<T> &g) {
 template <typename T>
 hipError_t launch_gemm(const Launch &L, const GemmArgs<T> &g0) {
   if (g0.M <= 0 || g0.N <= 0 || g0.batch <= 0) return hipSuccess;
-  constexpr bool kMfma = sizeof(T) == 4;
-  const bool mfma = kMfma && L.gemm == 0;
+  const bool mfma = use_mfma(L, g0);
   if (g0.A1b && !mfma) {
     // the VALU kernel takes one K segment: add the second product in a second launch
     GemmArgs<T> a = g0, b = g0;
@@ -1427,38 +1605,29 @@ hipError_t launch_gemm(const Launch &L, const GemmArgs<T> &g0) {
   hipError_t e = gemm_init(L, g);
   if (e != hipSuccess) return e;
   dim3 grid((g.N + 63) / 64, (g.M + 63) / 64, g.batch * g.ksplit);
-  if constexpr (kMfma) {
-    if (mfma) {
-      return launch_mfma(L, grid, g, g, int(grid.z));
-    }
-  }
+  if (mfma) return launch_mfma(L, grid, g, g, int(grid.z));
   hipLaunchKernelGGL((k_gemm<T>), grid, dim3(256), 0, L.stream, g);
   return hipGetLastError();
 }
 
 template <typename T>
 hipError_t launch_gemm_pair(const Launch &L, const GemmArgs<T> &p0, const GemmArgs<T> &p1) {
-  constexpr bool kMfma = sizeof(T) == 4;
-  const bool mfma = kMfma && L.gemm == 0;
   const bool empty0 = p0.M <= 0 || p0.N <= 0 || p0.batch <= 0;
   const bool empty1 = p1.M <= 0 || p1.N <= 0 || p1.batch <= 0;
-  if (!mfma || empty0 || empty1) {
+  if (empty0 || empty1 || !use_mfma(L, p0) || !use_mfma(L, p1)) {
     hipError_t e = launch_gemm<T>(L, p0);
     return e != hipSuccess ? e : launch_gemm<T>(L, p1);
   }
-  if constexpr (kMfma) {
-    GemmArgs<T> g0 = p0, g1 = p1;
-    const int tiles = gemm_tiles(g0) + gemm_tiles(g1);
-    g0.ksplit = gemm_ksplit(L, g0, tiles, true);
-    g1.ksplit = gemm_ksplit(L, g1, tiles, true);
-    hipError_t e = gemm_init(L, g0);
-    if (e == hipSuccess) e = gemm_init(L, g1);
-    if (e != hipSuccess) return e;
-    const int nz0 = g0.batch * g0.ksplit;
-    dim3 grid((std::max(g0.N, g1.N) + 63) / 64, (std::max(g0.M, g1.M) + 63) / 64, nz0 + g1.batch * g1.ksplit);
-    return launch_mfma(L, grid, g0, g1, nz0);
-  }
-  return hipSuccess;
+  GemmArgs<T> g0 = p0, g1 = p1;
+  const int tiles = gemm_tiles(g0) + gemm_tiles(g1);
+  g0.ksplit = gemm_ksplit(L, g0, tiles, true);
+  g1.ksplit = gemm_ksplit(L, g1, tiles, true);
+  hipError_t e = gemm_init(L, g0);
+  if (e == hipSuccess) e = gemm_init(L, g1);
+  if (e != hipSuccess) return e;
+  const int nz0 = g0.batch * g0.ksplit;
+  dim3 grid((std::max(g0.N, g1.N) + 63) / 64, (std::max(g0.M, g1.M) + 63) / 64, nz0 + g1.batch * g1.ksplit);
+  return launch_mfma(L, grid, g0, g1, nz0);
 }
 
 template <typename T, int NT, int REP>

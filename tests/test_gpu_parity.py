@@ -301,6 +301,26 @@ def test_ring_gemm(ctx, orc, shape):
     assert np.array_equal(ctx.ring_gemm(A, B).astype(np.uint64), orc.ring_gemm(bw, A, B))
 
 
+@pytest.mark.parametrize("K", [32767, 40000])
+def test_ring_gemm64_digit_sum_bound(mp, orc, K):
+    """Z_2^64 on the matrix cores keeps the low shifts' int32 digit sums exact
+    for K < 2^15: a 1024 x 1024 product (256 tiles: no split-K, the whole K in
+    one accumulator) at K = 2^15 - 1 with every digit at -128 (the largest
+    sums) equals K a^2 mod 2^64 everywhere; K = 40000 runs on the VALU kernel.
+    Uniform operands at both K against the oracle."""
+    c = mp.Ctx(bw=64)
+    a = 0x8080808080808080
+    worst = np.full((1024, K), a, np.uint64)
+    got = c.ring_gemm(worst, worst.T.copy()).astype(np.uint64)
+    assert np.all(got == np.uint64((K * a * a) % (1 << 64)))
+    del worst, got
+    rng = np.random.default_rng(K)
+    A = rmask(rng, 3 * K, 64).reshape(3, K)
+    B = rmask(rng, K * 2, 64).reshape(K, 2)
+    assert np.array_equal(c.ring_gemm(A, B).astype(np.uint64), orc.ring_gemm(64, A, B))
+    c.close()
+
+
 def test_ring_gemm_valu_path(mp, orc, monkeypatch):
     """Z_2^32 products on the VALU path (MPCX_GEMM=valu; the default is the
     int8 matrix-core path) agree with the oracle too."""
