@@ -252,7 +252,11 @@ struct TrArgs {
   AesRK kd;
   AesRK kp[2];  // the parties' own PRF keys (keygen and seeded-plane expansion)
   int kind, n, s;
-  int sb;  // sign bit of the shifted input (tr_sign_bit)
+  int sb;        // sign bit of the shifted input (tr_sign_bit)
+  int m, sh;     // input width (tr_in_bits) and the gate's own shift (tr_shift)
+  int ncase;     // cases of the G table
+  int relu;      // the gate carries kappa shares
+  int has_bias;  // the bias is added before the shift
   size_t N;
   const uint8_t *k0, *k1;
   uint8_t *w0, *w1;  // writable keys (keygen)
@@ -272,11 +276,17 @@ struct TrArgs {
 
 __device__ __forceinline__ bool relu_like(int kind) { return kind == G_RELU || kind == G_RELUSLACK; }
 
+// v mod 2^m for 1 <= m <= bits of T
+template <typename T>
+__device__ __forceinline__ T low_bits(T v, int m) {
+  return m >= int(8 * sizeof(T)) ? v : T(v & ((T(1) << m) - T(1)));
+}
+
 template <typename T>
 __device__ __forceinline__ T tr_shifted_input(const TrArgs<T> &a, size_t i) {
   T x = a.xhat[i];
-  if (!relu_like(a.kind) && a.kind != G_DRELU && a.bias) x += T(a.bias[uint32_t(i % uint32_t(a.bias_ncol))]) << a.s;
-  return x + (T(1) << a.sb);
+  if (a.has_bias && a.bias) x += T(a.bias[uint32_t(i % uint32_t(a.bias_ncol))]) << a.s;
+  return low_bits<T>(x + (T(1) << a.sb), a.m);
 }
 
 // TAG = 1 marks the launches of a profiled forward (identical code, its own
@@ -333,9 +343,18 @@ __global__ void k_tr_phase2(TrArgs<T> a) {
     const uint32_t h = uint32_t(xp >> a.sb) & 1u;
     const uint32_t bh = a.use_a ? (get_bit(a.cba[0], i) ^ get_bit(a.cba[1], i)) : 0u;
     const uint32_t dh = a.use_b ? (get_bit(a.cbb[0], i) ^ get_bit(a.cbb[1], i)) : 0u;
-    const T A = (xp >> a.s) - (T(1) << (a.n - 1 - a.s));
+    const T A = (xp >> a.sh) - (T(1) << (a.m - 1 - a.sh));
     T y;
-    if (a.kind == G_TR) {
+    if (a.kind == G_TRMOD) {  // exact modulo 2^(n-s): no wrap term
+      y = one0 * A + G[size_t(dh) * a.N + i];
+    } else if (a.kind == G_EXT) {
+      y = one0 * A + G[size_t(h * 2 + bh) * a.N + i];
+    } else if (a.kind == G_EXTRELU) {
+      const uint32_t z = h ^ bh;
+      const T k = kap[i];
+      const T cp = z ? T(one0 - k) : k;
+      y = cp * A + G[size_t(h * 2 + bh) * a.N + i];
+    } else if (a.kind == G_TR) {
       const uint32_t c = h * 4 + bh * 2 + dh;
       y = one0 * A + G[size_t(c) * a.N + i];
     } else if (a.kind == G_TRRELU) {
@@ -369,16 +388,17 @@ __global__ void k_tr_keygen(TrArgs<T> a) {
   const int n = a.n, s = a.s;
   const T lowmask = (T(1) << a.sb) - T(1);
   const T smask = (T(1) << s) - T(1);
+  const int wsh = a.m - a.sh;  // weight of the wrap bit after the shift
   T *G0 = reinterpret_cast<T *>(a.w0 + a.off_g);
   T *G1 = reinterpret_cast<T *>(a.w1 + a.off_g);
-  const int ncase = a.kind == G_DRELU ? 0 : relu_like(a.kind) ? 2 : 8;
+  const int ncase = a.ncase;
   for (size_t base = size_t(blockIdx.x) * blockDim.x + (threadIdx.x & ~63u); base < a.N; base += stride) {
     const size_t i = base + lane_id();
     uint32_t za0 = 0, za1 = 0, zb0 = 0, zb1 = 0;
     if (i < a.N) {
-      const T r = a.in_mask[i];
+      const T r = low_bits<T>(a.in_mask[i], a.m);
       const uint32_t rho = uint32_t(r >> a.sb) & 1u;
-      const T R = r >> s;
+      const T R = r >> a.sh;
       // each party's output-mask bit of a DCF comes from its own PRF key; the
       // DCF output mask is their XOR
       if (a.use_a) {
@@ -395,7 +415,18 @@ __global__ void k_tr_keygen(TrArgs<T> a) {
       a.out_mask[i] = a.kind == G_DRELU ? T(kappa) : rout;  // DRELU: the mask of the output bit
       for (int c = 0; c < ncase; c++) {
         T Gv;
-        if (a.kind == G_TR || a.kind == G_TRRELU) {
+        if (a.kind == G_TRMOD) {
+          Gv = rout - R - T(uint32_t(c) ^ rdi);
+        } else if (a.kind == G_EXT || a.kind == G_EXTRELU) {
+          const uint32_t h = uint32_t(c) >> 1, b = (uint32_t(c) & 1u) ^ rbi;
+          const uint32_t w = h ? (rho & b) : (rho | b);
+          if (a.kind == G_EXTRELU) {
+            const T cc = T(h ^ rho ^ b);
+            Gv = rout - cc * R + ((cc * T(w)) << wsh);
+          } else {
+            Gv = rout - R + (T(w) << wsh);
+          }
+        } else if (a.kind == G_TR || a.kind == G_TRRELU) {
           const uint32_t h = uint32_t(c) >> 2, bh = (uint32_t(c) >> 1) & 1u, dh = uint32_t(c) & 1u;
           const uint32_t b = bh ^ rbi, d = dh ^ rdi;
           const uint32_t w = h ? (rho & b) : (rho | b);
@@ -419,7 +450,7 @@ __global__ void k_tr_keygen(TrArgs<T> a) {
         G0[size_t(c) * a.N + i] = g0;
         G1[size_t(c) * a.N + i] = Gv - g0;
       }
-      if (a.kind == G_TRRELU || relu_like(a.kind)) {
+      if (a.relu) {
         const T q0 = ring_of<T>(aes.prf(a.kp[0], a.gate, F_SPLIT + 8, i));
         reinterpret_cast<T *>(a.w0 + a.off_kappa)[i] = q0;
         reinterpret_cast<T *>(a.w1 + a.off_kappa)[i] = T(kappa) - q0;
@@ -454,6 +485,11 @@ static TrArgs<T> tr_args(const TrLayout &lay) {
   a.n = lay.bw;
   a.s = lay.s;
   a.sb = tr_sign_bit(lay.kind, lay.bw, lay.s);
+  a.m = tr_in_bits(lay.kind, lay.bw, lay.s);
+  a.sh = tr_shift(lay.kind, lay.s);
+  a.ncase = lay.ncase;
+  a.relu = lay.relu;
+  a.has_bias = tr_has_bias(lay.kind);
   a.N = lay.N;
   a.a = lay.a;
   a.b = lay.b;
@@ -522,8 +558,8 @@ __global__ void k_tr_expand(TrArgs<T> a, int p) {
   const AesRK &kp = a.kp[0];
   uint8_t *w = a.w0;
   const size_t stride = size_t(gridDim.x) * blockDim.x;
-  const int ncase = a.kind == G_DRELU ? 0 : relu_like(a.kind) ? 2 : 8;
-  const bool kappa = a.kind == G_TRRELU || relu_like(a.kind);
+  const int ncase = a.ncase;
+  const bool kappa = a.relu;
   for (size_t base = size_t(blockIdx.x) * blockDim.x + (threadIdx.x & ~63u); base < a.N; base += stride) {
     const size_t i = base + lane_id();
     uint32_t za = 0, zb = 0;

@@ -492,23 +492,35 @@ class Model final : public ModelBase, KeySource {
   // gpu_mpc/ddg_orca_batched.h:180-199): a local shift, then a RELU gate where the
   // layer has a ReLU
   bool local_trunc() const { return d_.slack == 3; }
-  // gate of the GCN products H.W^T: exact TR, or (slack 1, 2) TRSLACK, exact
-  // for |x| < 2^(bw-2)
-  int xw_kind() const { return d_.slack == 1 || d_.slack == 2 ? G_TRSLACK : G_TR; }
-  // the GCN aggregation A.XW + bias, then ReLU: one TRRELU gate, or (slack 2)
-  // TRSLACK with the bias followed by RELUSLACK on the truncated value
+  // the GCN products H.W^T: (slack 1, 2) TRSLACK, exact for |x| < 2^(bw-2), else
+  // the layer truncation
+  bool xw_slack() const { return d_.slack == 1 || d_.slack == 2; }
+  // the GCN aggregation A.XW + bias, then ReLU: the layer truncation with ReLU, or
+  // (slack 2) TRSLACK with the bias followed by RELUSLACK on the truncated value
   bool agg_split() const { return d_.slack == 2; }
 
-  // A layer truncation by s (+ bias) and, for relu, the ReLU: one TR / TRRELU
-  // gate, or with local truncation the local shift (no key) followed, for relu,
-  // by a RELU gate.  Eval may overwrite x; keygen may overwrite the mask rin.
+  // A layer truncation by s (+ bias) and, for relu, the ReLU.  Exact: the
+  // truncate-reduce TRMOD (one s-bit DCF; its output is exact modulo 2^(bw-s)),
+  // revealed, then EXT or EXTRELU (one (bw-s-1)-bit DCF gives the sign and the
+  // wrap) -- the reference's TrFloor as truncate-reduce plus sign extension
+  // (gpu_mpc/dpf_dcf_adapter.h:274-303) with the ReLU fused into the extension as
+  // in gpuReluExtend (:225-234): 6 + 13 AES per element and party at bw=32
+  // instead of 31 for one fused gate over the full width.  With local
+  // truncation: the local shift (no key) followed, for relu, by a RELU gate.
+  // Eval may overwrite x; keygen may overwrite the mask rin.
   hipError_t trunc_eval(Runner<T> &r, bool relu, size_t n, T *x, const T *bias, int ncol, T *y) {
-    if (!local_trunc()) return r.tr(relu ? G_TRRELU : G_TR, n, x, bias, ncol, y);
+    if (!local_trunc()) {
+      TRY(r.tr(G_TRMOD, n, x, bias, ncol, x));
+      return r.tr(relu ? G_EXTRELU : G_EXT, n, x, nullptr, 1, y);
+    }
     TRY(launch_local_ars<T>(L_, n, s_, x, bias, ncol, relu ? x : y));
     return relu ? r.tr(G_RELU, n, x, nullptr, 1, y) : hipSuccess;
   }
   hipError_t trunc_keygen(Dealer<T> &d, bool relu, size_t n, T *rin, T *rout) {
-    if (!local_trunc()) return d.tr(relu ? G_TRRELU : G_TR, n, rin, rout);
+    if (!local_trunc()) {
+      TRY(d.tr(G_TRMOD, n, rin, rin));
+      return d.tr(relu ? G_EXTRELU : G_EXT, n, rin, rout);
+    }
     TRY(launch_local_ars<T>(L_, n, s_, rin, nullptr, 1, relu ? rin : rout));
     return relu ? d.tr(G_RELU, n, rin, rout) : hipSuccess;
   }
@@ -596,26 +608,35 @@ class Model final : public ModelBase, KeySource {
       tr(G_TRSLACK, BP);
       push(mul_layout(bw_, BNN, BP, BNN, o).end);
     }
+    // the gates of trunc_keygen / trunc_eval
+    auto trunc = [&](bool relu, size_t n) {
+      if (local_trunc()) {
+        if (relu) tr(G_RELU, n);
+        return;
+      }
+      tr(G_TRMOD, n);
+      tr(relu ? G_EXTRELU : G_EXT, n);
+    };
     for (int l = 0; l < 3; l++) {
       size_t E = BN * d_.gcn[l];
-      if (!local_trunc()) tr(xw_kind(), E);
+      if (xw_slack())
+        tr(G_TRSLACK, E);
+      else
+        trunc(false, E);
       push(sxs_layout(bw_, B, N, N, d_.gcn[l], o).end);
-      if (local_trunc()) {
-        tr(G_RELU, E);
-      } else if (agg_split()) {
+      if (agg_split()) {
         tr(G_TRSLACK, E);
         tr(G_RELUSLACK, E);
       } else {
-        tr(G_TRRELU, E);
+        trunc(true, E);
       }
     }
     int pairs[32];
     int Lv = pool_levels(N, pairs);
     for (int l = 0; l < Lv; l++) tr(G_RELU, size_t(B) * pairs[l] * d_.gcn[2]);
-    const int relu_kind = local_trunc() ? G_RELU : G_TRRELU;
-    tr(relu_kind, size_t(B) * d_.dfc[0]);
-    if (!local_trunc()) tr(G_TR, size_t(B) * d_.dfc[1]);
-    for (int k = 0; k < d_.nfus - 1; k++) tr(relu_kind, size_t(B) * d_.fus[k]);
+    trunc(true, size_t(B) * d_.dfc[0]);
+    trunc(false, size_t(B) * d_.dfc[1]);
+    for (int k = 0; k < d_.nfus - 1; k++) trunc(true, size_t(B) * d_.fus[k]);
     {  // output: the clear output mask, the same for both parties
       RevealLayout lay = reveal_layout(bw_, size_t(B) * d_.fus[d_.nfus - 1], o);
       push(lay.end).share(lay.off_r, lay.end);
@@ -733,18 +754,16 @@ class Model final : public ModelBase, KeySource {
       const int fo = d_.gcn[l];
       const size_t En = BN * fo;
       TRY(pub_gemm(rX.p, l, BN, t1.p));
-      if (local_trunc())
-        TRY(trunc_keygen(d, false, En, t1.p, t2.p));
+      if (xw_slack())
+        TRY(d.tr(G_TRSLACK, En, t1.p, t2.p));
       else
-        TRY(d.tr(xw_kind(), En, t1.p, t2.p));
+        TRY(trunc_keygen(d, false, En, t1.p, t2.p));
       TRY(d.sxs(B, N, N, fo, rN.p, t2.p, t1.p, gt.p));
-      if (local_trunc()) {
-        TRY(trunc_keygen(d, true, En, t1.p, rX.p));
-      } else if (agg_split()) {
+      if (agg_split()) {
         TRY(d.tr(G_TRSLACK, En, t1.p, t2.p));
         TRY(d.tr(G_RELUSLACK, En, t2.p, rX.p));
       } else {
-        TRY(d.tr(G_TRRELU, En, t1.p, rX.p));
+        TRY(trunc_keygen(d, true, En, t1.p, rX.p));
       }
     }
     // pool
@@ -830,8 +849,7 @@ class Model final : public ModelBase, KeySource {
       out.emplace_back(dl->off_z, dl->off_z + zwords(g.n) * 4);
     }
     if (p == 0) {
-      if (g.tr_kind == G_TRRELU || g.tr_kind == G_RELU || g.tr_kind == G_RELUSLACK)
-        out.emplace_back(lay.off_kappa, lay.off_kappa + g.n * tb);
+      if (lay.relu) out.emplace_back(lay.off_kappa, lay.off_kappa + g.n * tb);
       if (lay.ncase > 0) out.emplace_back(lay.off_g, lay.off_g + size_t(lay.ncase) * g.n * tb);
     }
   }
@@ -1350,18 +1368,16 @@ class Model final : public ModelBase, KeySource {
       const int fo = d_.gcn[l];
       const size_t En = BN * fo;
       TRY(pub_gemm(H, l, BN, Z));
-      if (local_trunc())
-        TRY(trunc_eval(r, false, En, Z, nullptr, 1, XW));
+      if (xw_slack())
+        TRY(r.tr(G_TRSLACK, En, Z, nullptr, 1, XW));
       else
-        TRY(r.tr(xw_kind(), En, Z, nullptr, 1, XW));
+        TRY(trunc_eval(r, false, En, Z, nullptr, 1, XW));
       TRY(r.sxs(B, N, N, fo, An_.p, XW, Z));
-      if (local_trunc()) {
-        TRY(trunc_eval(r, true, En, Z, bias_[l].p, fo, H));
-      } else if (agg_split()) {  // truncate with the bias, reveal, then ReLU of the small value
+      if (agg_split()) {  // truncate with the bias, reveal, then ReLU of the small value
         TRY(r.tr(G_TRSLACK, En, Z, bias_[l].p, fo, XW));
         TRY(r.tr(G_RELUSLACK, En, XW, nullptr, 1, H));
       } else {
-        TRY(r.tr(G_TRRELU, En, Z, bias_[l].p, fo, H));
+        TRY(trunc_eval(r, true, En, Z, bias_[l].p, fo, H));
       }
     }
     // masked max-pool: V = H + 2^(bw-2-ms) m^ - 2^(bw-2) (the sentinel -2^(bw-2) on

@@ -27,8 +27,34 @@ enum GateKind : int {
   G_TRSLACK = 4,     // exact truncation for |x| < 2^(bw-2)
   G_RELUSLACK = 9,   // ReLU for |x| < 2^(bw-2-s): a (bw-2-s)-bit DCF (after TRSLACK)
   G_LOCALARS = 10,   // local arithmetic shift of the masked value and its mask (no key)
-  G_DRELU = 11       // [x >= 0] as a masked public bit: one (bw-1)-bit DCF, one round
+  G_DRELU = 11,      // [x >= 0] as a masked public bit: one (bw-1)-bit DCF, one round
+  G_TRMOD = 12,      // floor(x/2^s) + bias, exact modulo 2^(bw-s) only: one s-bit DCF
+  G_EXT = 13,        // a value known modulo 2^(bw-s) (a TRMOD output) sign-extended to bw bits
+  G_EXTRELU = 14     // ReLU of that value, sign-extended: one (bw-s-1)-bit DCF for both
 };
+
+// Gate-kind properties of the truncation family.  A gate reads its public
+// input modulo 2^tr_in_bits, shifts it right by tr_shift, and takes the sign
+// from bit tr_sign_bit of the input plus 2^tr_sign_bit.
+inline bool tr_ext(int kind) { return kind == G_EXT || kind == G_EXTRELU; }
+inline int tr_in_bits(int kind, int bw, int s) { return tr_ext(kind) ? bw - s : bw; }
+inline int tr_shift(int kind, int s) { return tr_ext(kind) ? 0 : s; }
+inline bool tr_has_bias(int kind) { return kind == G_TR || kind == G_TRRELU || kind == G_TRSLACK || kind == G_TRMOD; }
+inline bool tr_is_relu(int kind) {
+  return kind == G_TRRELU || kind == G_RELU || kind == G_RELUSLACK || kind == G_EXTRELU;
+}
+// the (sign-bit)-bit DCF "a" and the s-bit DCF "b"
+inline bool tr_uses_a(int kind) { return kind != G_TRSLACK && kind != G_TRMOD && kind != G_LOCALARS; }
+inline bool tr_uses_b(int kind) { return tr_has_bias(kind); }
+// public cases of the output correction table G
+inline int tr_ncase(int kind) {
+  switch (kind) {
+    case G_TR: case G_TRRELU: case G_TRSLACK: return 8;
+    case G_EXT: case G_EXTRELU: return 4;
+    case G_RELU: case G_RELUSLACK: case G_TRMOD: return 2;
+    default: return 0;
+  }
+}
 
 enum Field : uint32_t {
   F_DCFA = 0x10,   // +0 root seed, +1 delta, +2 z0 bit, +3 output mask bit
@@ -75,9 +101,12 @@ struct TrLayout {
   int ncase = 0;
 };
 
-// Bit of the shifted input that carries the sign: the top bit, or bit bw-2-s
-// for RELUSLACK (inputs |x| < 2^(bw-2-s), e.g. a value truncated by TRSLACK).
-inline int tr_sign_bit(int kind, int bw, int s) { return kind == G_RELUSLACK ? bw - 2 - s : bw - 1; }
+// Bit of the shifted input that carries the sign: the top bit of the input
+// width, or bit bw-2-s for RELUSLACK (inputs |x| < 2^(bw-2-s), e.g. a value
+// truncated by TRSLACK).
+inline int tr_sign_bit(int kind, int bw, int s) {
+  return kind == G_RELUSLACK ? bw - 2 - s : tr_in_bits(kind, bw, s) - 1;
+}
 
 inline TrLayout tr_layout(int kind, int bw, int s, size_t N, size_t base) {
   TrLayout t;
@@ -85,15 +114,15 @@ inline TrLayout tr_layout(int kind, int bw, int s, size_t N, size_t base) {
   t.bw = bw;
   t.s = s;
   t.N = N;
-  t.relu = kind == G_TRRELU || kind == G_RELU || kind == G_RELUSLACK;
+  t.relu = tr_is_relu(kind);
   if (kind == G_LOCALARS) {  // keyless: consumes no key bytes
     t.use_a = t.use_b = false;
     t.ncase = 0;
     t.off_g = t.end = base;
     return t;
   }
-  t.use_a = kind != G_TRSLACK;
-  t.use_b = kind != G_RELU && kind != G_RELUSLACK && kind != G_DRELU;
+  t.use_a = tr_uses_a(kind);
+  t.use_b = tr_uses_b(kind);
   const size_t tb = size_t(bw) / 8;
   size_t o = align_up(base);
   if (t.use_a) {
@@ -108,7 +137,7 @@ inline TrLayout tr_layout(int kind, int bw, int s, size_t N, size_t base) {
     t.off_kappa = o;
     o = align_up(o + N * tb);
   }
-  t.ncase = kind == G_DRELU ? 0 : kind == G_RELU || kind == G_RELUSLACK ? 2 : 8;
+  t.ncase = tr_ncase(kind);
   t.off_g = o;
   o = align_up(o + size_t(t.ncase) * N * tb);
   t.end = o;

@@ -12,7 +12,7 @@ import numpy as np
 HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(HERE, "libmpcx.so")
 
-TR, TRRELU, RELU, TRSLACK, RELUSLACK = 1, 2, 3, 4, 9
+TR, TRRELU, RELU, TRSLACK, RELUSLACK, LOCALARS, DRELU, TRMOD, EXT, EXTRELU = 1, 2, 3, 4, 9, 10, 11, 12, 13, 14
 
 _lib = None
 

@@ -53,6 +53,16 @@ typedef struct mpcx_model mpcx_model;
                            one bit-plane round; the output is a masked public bit held as a ring
                            element 0/1, keygen's output "mask" is the mask bit (0/1): the
                            DReLU bit is yhat XOR mask */
+/* Exact truncation in two gates, the reference's TrFloor composition (truncate-reduce
+   then sign extension, gpu_mpc/dpf_dcf_adapter.h:274-303) and its ReLU-extend
+   (gpuReluExtend, :225-234; keygen bin = bw - scale, bout = bw, gpu_mpc/ddg_orca.h:222): */
+#define MPCX_TRMOD 12   /* floor(x/2^s) + bias, exact modulo 2^(bw-s) only (the yhat bits
+                           above bw-s are not meaningful): one s-bit DCF */
+#define MPCX_EXT 13     /* y sign-extended from bw-s bits: the input is a TRMOD output
+                           (only its low bw-s bits are read, and of the input mask too);
+                           one (bw-s-1)-bit DCF.  TRMOD then EXT = MPCX_TR */
+#define MPCX_EXTRELU 14 /* ReLU(y) of that value, sign-extended: the same one DCF gives the
+                           sign and the wrap.  TRMOD then EXTRELU = MPCX_TRRELU */
 
 /* ---------------- context ----------------
  * Replaces the evaluator/dealer constructors DDGOrcaBase(party, ip, bw, scale)
@@ -118,8 +128,9 @@ mpcx_status mpcx_dcf_eval(mpcx_ctx *ctx, int party, int bin, size_t n, const voi
  * shift, peer, party, N, d_in, g, s) (gpu_mpc/ddg_orca.h:116-118), for both
  * parties at once: masked input in, masked output out.
  * bias: ncol ring elements at scale s (element i uses bias[i % ncol]) or NULL;
- * ignored by MPCX_RELU.  MPCX_LOCALARS has no key (key bytes 0, key pointers may
- * be NULL, the gate id is unused). */
+ * read only by MPCX_TR, MPCX_TRRELU, MPCX_TRSLACK, MPCX_TRMOD and MPCX_LOCALARS
+ * (the kinds that shift).  MPCX_LOCALARS has no key (key bytes 0, key pointers
+ * may be NULL, the gate id is unused). */
 size_t mpcx_tr_key_bytes(mpcx_ctx *ctx, int kind, size_t n);
 mpcx_status mpcx_tr_keygen(mpcx_ctx *ctx, int kind, size_t n, const void *d_in_mask,
                            void *d_out_mask, uint64_t seed, uint32_t gate, void *d_key0,

@@ -172,7 +172,9 @@ class SecureBackend {
     }
   }
 
-  // ---- truncation by the scale: exact (ddg_orca.h:112-123, TrFloor) by default;
+  // ---- truncation by the scale: exact (ddg_orca.h:112-123, TrFloor) by default,
+  // as TrFloor composes it: the truncate-reduce MPCX_TRMOD then the sign
+  // extension MPCX_EXT (dpf_dcf_adapter.h:274-303);
   // set_truncation(MPCX_LOCALARS) selects the reference batched backend's default
   // local shift (ddg_orca_batched.h:180-199: no key, no exchange, not exact) and
   // MPCX_TRSLACK the exact truncation for |x| < 2^(bw-2).  The dealer and the
@@ -186,13 +188,20 @@ class SecureBackend {
   template <class TI>
   void truncateForward(TI &in, uint64_t shift, uint8_t /*mode*/ = 0) {
     if (int(shift) != scale()) throw std::invalid_argument("truncateForward: shift must equal the scale");
-    gate(trunc_kind_, in, in, nullptr, 0);
+    if (trunc_kind_ == MPCX_TR) {
+      gate(MPCX_TRMOD, in, in, nullptr, 0);
+      gate(MPCX_EXT, in, in, nullptr, 0);
+    } else {
+      gate(trunc_kind_, in, in, nullptr, 0);
+    }
   }
 
-  // ---- fused truncation + bias + ReLU (one gate, two rounds) ----
+  // ---- truncation + bias + ReLU: the truncate-reduce, then the ReLU fused into
+  // the sign extension (gpuReluExtend, dpf_dcf_adapter.h:225-234), four rounds ----
   template <class TI, class TO, class TD>
   void truncate_bias_relu(const TI &in, TO &out, const TD &bias) {
-    gate(MPCX_TRRELU, in, out, bias.d_data, int(bias.size()));
+    gate(MPCX_TRMOD, in, out, bias.d_data, int(bias.size()));
+    gate(MPCX_EXTRELU, out, out, nullptr, 0);
   }
 
   // ---- output (ddg_orca_base.h:296-302 / 511-517) ----

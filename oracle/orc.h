@@ -92,8 +92,12 @@ enum {
   ORC_G_RELUSLACK = 9, /* ReLU for |x| < 2^(bw-2-s) (a (bw-2-s)-bit DCF) */
   ORC_G_LOCALARS = 10, /* local arithmetic shift of the masked value and of
                           its mask: no key, no exchange, error +1 or a wrap */
-  ORC_G_DRELU = 11     /* [x >= 0] as a masked public bit (0/1 ring element),
+  ORC_G_DRELU = 11,    /* [x >= 0] as a masked public bit (0/1 ring element),
                           mask bit returned by keygen: one (bw-1)-bit DCF */
+  ORC_G_TRMOD = 12,    /* floor(x/2^s) + bias modulo 2^(bw-s): one s-bit DCF */
+  ORC_G_EXT = 13,      /* a value known modulo 2^(bw-s) sign-extended to bw bits:
+                          one (bw-s-1)-bit DCF */
+  ORC_G_EXTRELU = 14   /* ReLU of that value, sign-extended: the same one DCF */
 };
 
 /* Dealer randomness fields. */

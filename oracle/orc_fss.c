@@ -133,9 +133,33 @@ orc_dcf_layout orc_dcf_layout_make(int m, size_t N, size_t base, int with_z) {
   return L;
 }
 
-/* bit of the shifted input that carries the sign: the top bit, or bit bw-2-s for
- * RELUSLACK (inputs |x| < 2^(bw-2-s), e.g. a value truncated by TRSLACK) */
-int orc_sign_bit(int kind, int bw, int s) { return kind == ORC_G_RELUSLACK ? bw - 2 - s : bw - 1; }
+/* EXT kinds read their input modulo 2^(bw-s) and do not shift; every other
+ * kind reads all bw bits and shifts by s (the reference's TrFloor is the
+ * truncate-reduce then the sign extension, gpu_mpc/dpf_dcf_adapter.h:274-303;
+ * its ReLU-extend gpuReluExtend, :225-234, takes bin = bw - scale) */
+static int is_ext(int kind) { return kind == ORC_G_EXT || kind == ORC_G_EXTRELU; }
+static int in_bits(int kind, int bw, int s) { return is_ext(kind) ? bw - s : bw; }
+static int own_shift(int kind, int s) { return is_ext(kind) ? 0 : s; }
+static int has_bias(int kind) {
+  return kind == ORC_G_TR || kind == ORC_G_TRRELU || kind == ORC_G_TRSLACK || kind == ORC_G_TRMOD;
+}
+static int uses_a(int kind) { return kind != ORC_G_TRSLACK && kind != ORC_G_TRMOD; }
+static int is_relu(int kind) {
+  return kind == ORC_G_TRRELU || kind == ORC_G_RELU || kind == ORC_G_RELUSLACK || kind == ORC_G_EXTRELU;
+}
+static int ncase_of(int kind) {
+  switch (kind) {
+    case ORC_G_TR: case ORC_G_TRRELU: case ORC_G_TRSLACK: return 8;
+    case ORC_G_EXT: case ORC_G_EXTRELU: return 4;
+    case ORC_G_RELU: case ORC_G_RELUSLACK: case ORC_G_TRMOD: return 2;
+    default: return 0;
+  }
+}
+
+/* bit of the shifted input that carries the sign: the top bit of the input
+ * width, or bit bw-2-s for RELUSLACK (inputs |x| < 2^(bw-2-s), e.g. a value
+ * truncated by TRSLACK) */
+int orc_sign_bit(int kind, int bw, int s) { return kind == ORC_G_RELUSLACK ? bw - 2 - s : in_bits(kind, bw, s) - 1; }
 
 orc_tr_layout orc_tr_layout_make(int kind, int bw, int s, size_t N, size_t base) {
   orc_tr_layout T;
@@ -144,19 +168,18 @@ orc_tr_layout orc_tr_layout_make(int kind, int bw, int s, size_t N, size_t base)
   T.bw = bw;
   T.s = s;
   T.N = N;
-  T.relu = (kind == ORC_G_TRRELU || kind == ORC_G_RELU || kind == ORC_G_RELUSLACK);
+  T.relu = is_relu(kind);
   if (kind == ORC_G_LOCALARS) { /* keyless: consumes no key bytes */
     T.off_g = T.end = base;
     return T;
   }
   size_t o = orc_align(base);
   size_t tb = (size_t)bw / 8;
-  if (kind == ORC_G_TR || kind == ORC_G_TRRELU || kind == ORC_G_RELU || kind == ORC_G_RELUSLACK ||
-      kind == ORC_G_DRELU) {
+  if (uses_a(kind)) {
     T.a = orc_dcf_layout_make(orc_sign_bit(kind, bw, s), N, o, 1);
     o = T.a.end;
   }
-  if (kind == ORC_G_TR || kind == ORC_G_TRRELU || kind == ORC_G_TRSLACK) {
+  if (has_bias(kind)) {
     T.b = orc_dcf_layout_make(s, N, o, 1);
     o = T.b.end;
   }
@@ -164,7 +187,7 @@ orc_tr_layout orc_tr_layout_make(int kind, int bw, int s, size_t N, size_t base)
     T.off_kappa = o;
     o = orc_align(o + N * tb);
   }
-  T.ncase = kind == ORC_G_DRELU ? 0 : (kind == ORC_G_RELU || kind == ORC_G_RELUSLACK) ? 2 : 8;
+  T.ncase = ncase_of(kind);
   T.off_g = o;
   o = orc_align(o + (size_t)T.ncase * N * tb);
   T.end = o;
@@ -396,17 +419,18 @@ void orc_tr_keygen(uint64_t seed, uint32_t gate, int kind, int bw, int s, size_t
   orc_tr_layout T = orc_tr_layout_make(kind, bw, s, N, base);
   const uint64_t M = rmask(bw);
   const int n = bw, sb = orc_sign_bit(kind, bw, s);
+  const int m = in_bits(kind, bw, s), sh = own_shift(kind, s);
   const int relu_like = kind == ORC_G_RELU || kind == ORC_G_RELUSLACK;
-  const int no_b = relu_like || kind == ORC_G_DRELU; /* no s-bit DCF */
-  const int use_a = kind != ORC_G_TRSLACK;
+  const int no_b = !has_bias(kind); /* no s-bit DCF */
+  const int use_a = uses_a(kind);
   const uint64_t lowmask = (1ull << sb) - 1ull;
   const uint64_t smask = (1ull << s) - 1ull;
   uint64_t *aa = (uint64_t *)calloc(N, 8), *ab = (uint64_t *)calloc(N, 8);
   OMP_FOR
   for (size_t i = 0; i < N; i++) {
-    uint64_t r = in_mask[i] & M;
+    uint64_t r = in_mask[i] & rmask(m);
     int rho = (int)((r >> sb) & 1u);
-    uint64_t R = r >> s;
+    uint64_t R = r >> sh;
     /* the DCF output masks: XOR of the parties' own mask bits */
     int rbi = use_a ? prf_bit(&P0, gate, ORC_F_DCFA + 2, i) ^ prf_bit(&P1, gate, ORC_F_DCFA + 2, i) : 0;
     int rdi = !no_b ? prf_bit(&P0, gate, ORC_F_DCFB + 2, i) ^ prf_bit(&P1, gate, ORC_F_DCFB + 2, i) : 0;
@@ -418,7 +442,14 @@ void orc_tr_keygen(uint64_t seed, uint32_t gate, int kind, int bw, int s, size_t
     out_mask[i] = kind == ORC_G_DRELU ? (uint64_t)kappa : rout;
     for (int c = 0; c < T.ncase; c++) {
       uint64_t G = 0;
-      if (kind == ORC_G_TR || kind == ORC_G_TRRELU) {
+      if (kind == ORC_G_TRMOD) { /* no wrap term: exact modulo 2^(n-s) */
+        G = rout - R - (uint64_t)(c ^ rdi);
+      } else if (is_ext(kind)) { /* cases (h, c^); the wrap has weight 2^m */
+        int h = c >> 1, b = (c & 1) ^ rbi;
+        int w = h ? (rho & b) : (rho | b);
+        uint64_t cc = kind == ORC_G_EXTRELU ? (uint64_t)(h ^ rho ^ b) : 1u;
+        G = rout - cc * R + ((cc * (uint64_t)w) << m);
+      } else if (kind == ORC_G_TR || kind == ORC_G_TRRELU) {
         int h = c >> 2, bh = (c >> 1) & 1, dh = c & 1;
         int b = bh ^ rbi, d = dh ^ rdi;
         int w = h ? (rho & b) : (rho | b);
@@ -465,10 +496,11 @@ void orc_tr_eval(int kind, int bw, int s, size_t N, const uint8_t *k0, const uin
   orc_tr_layout T = orc_tr_layout_make(kind, bw, s, N, base);
   const uint64_t M = rmask(bw);
   const int n = bw, sb = orc_sign_bit(kind, bw, s);
+  const int m = in_bits(kind, bw, s), sh = own_shift(kind, s);
   const int relu_like = kind == ORC_G_RELU || kind == ORC_G_RELUSLACK;
   const uint64_t lowmask = (1ull << sb) - 1ull;
   const uint64_t smask = (1ull << s) - 1ull;
-  const int use_a = kind != ORC_G_TRSLACK, use_b = !relu_like && kind != ORC_G_DRELU;
+  const int use_a = uses_a(kind), use_b = has_bias(kind);
   uint8_t *bb[2], *dd[2];
   for (int p = 0; p < 2; p++) {
     bb[p] = (uint8_t *)calloc(N, 1);
@@ -480,7 +512,7 @@ void orc_tr_eval(int kind, int bw, int s, size_t N, const uint8_t *k0, const uin
     OMP_FOR
     for (size_t i = 0; i < N; i++) {
       uint64_t b = (use_b && bias_elem) ? ((uint64_t)bias_elem[i] << s) : 0;
-      uint64_t xp = (xhat[i] + b + (1ull << sb)) & M;
+      uint64_t xp = (xhat[i] + b + (1ull << sb)) & rmask(m);
       if (use_a) bb[p][i] = (uint8_t)orc_dcf_eval1(p, K[p], &T.a, i, xp & lowmask);
       if (use_b) dd[p][i] = (uint8_t)orc_dcf_eval1(p, K[p], &T.b, i, xp & smask);
     }
@@ -493,13 +525,25 @@ void orc_tr_eval(int kind, int bw, int s, size_t N, const uint8_t *k0, const uin
     OMP_FOR
     for (size_t i = 0; i < N; i++) {
       uint64_t b = (use_b && bias_elem) ? ((uint64_t)bias_elem[i] << s) : 0;
-      uint64_t xp = (xhat[i] + b + (1ull << sb)) & M;
+      uint64_t xp = (xhat[i] + b + (1ull << sb)) & rmask(m);
       int h = (int)((xp >> sb) & 1u);
       int bh = bb[0][i] ^ bb[1][i];
       int dh = dd[0][i] ^ dd[1][i];
-      uint64_t A = ((xp >> s) - (1ull << (n - 1 - s))) & M;
+      uint64_t A = ((xp >> sh) - (1ull << (m - 1 - sh))) & M;
       uint64_t out;
-      if (kind == ORC_G_TR || kind == ORC_G_TRRELU) {
+      if (kind == ORC_G_TRMOD) {
+        out = (p == 0 ? A : 0) + get_t(K[p], T.off_g, (size_t)dh * N + i, bw);
+      } else if (is_ext(kind)) {
+        uint64_t G = get_t(K[p], T.off_g, (size_t)(h * 2 + bh) * N + i, bw);
+        if (kind == ORC_G_EXTRELU) {
+          int z = h ^ bh;
+          uint64_t kap = get_t(K[p], T.off_kappa, i, bw);
+          uint64_t cp = z ? ((uint64_t)(p == 0) - kap) : kap;
+          out = cp * A + G;
+        } else {
+          out = (p == 0 ? A : 0) + G;
+        }
+      } else if (kind == ORC_G_TR || kind == ORC_G_TRRELU) {
         int c = h * 4 + bh * 2 + dh;
         uint64_t G = get_t(K[p], T.off_g, (size_t)c * N + i, bw);
         if (kind == ORC_G_TRRELU) {

@@ -39,11 +39,14 @@ static int nlayers(const orc_dims *d) { return 5 + d->nfus; }
  * gpu_mpc/ddg_orca_batched.h:180-199): a local shift, then a RELU gate where the
  * layer has a ReLU; not bit-exact with the fixed-point forward */
 static int local_trunc(const orc_dims *d) { return d->slack == 3; }
-/* gate of the GCN products H.W^T: exact TR, or TRSLACK when d->slack is 1 or 2 */
-static int xw_kind(const orc_dims *d) { return d->slack == 1 || d->slack == 2 ? ORC_G_TRSLACK : ORC_G_TR; }
-/* the GCN aggregation A.XW + bias then ReLU: one TRRELU gate, or (d->slack == 2)
- * TRSLACK (with the bias) followed by RELUSLACK on the truncated value */
+/* the GCN products H.W^T: TRSLACK when d->slack is 1 or 2, else the layer
+ * truncation (exact: TRMOD then EXT) */
+static int xw_slack(const orc_dims *d) { return d->slack == 1 || d->slack == 2; }
+/* the GCN aggregation A.XW + bias then ReLU: the layer truncation with ReLU
+ * (exact: TRMOD then EXTRELU), or (d->slack == 2) TRSLACK (with the bias)
+ * followed by RELUSLACK on the truncated value */
 static int agg_split(const orc_dims *d) { return d->slack == 2; }
+static size_t trunc_layout(const orc_dims *d, int relu, size_t n, size_t o);
 static void layer_io(const orc_dims *d, int l, int *in, int *out) {
   if (l < 3) {
     *in = l == 0 ? d->feat : d->gcn[l - 1];
@@ -199,7 +202,7 @@ int orc_plain_forward(const orc_dims *d, int B, const int64_t *X, const int64_t 
       int fo = d->gcn[l];
       const int64_t *Wt = W + layer_off(d, l);
       const int64_t *bias = Wt + (size_t)fin * fo;
-      fixed_mm(&f, H, Wt, (size_t)N, (size_t)fin, (size_t)fo, NULL, xw_kind(d) == ORC_G_TRSLACK ? 7 : 0,
+      fixed_mm(&f, H, Wt, (size_t)N, (size_t)fin, (size_t)fo, NULL, xw_slack(d) ? 7 : 0,
                XW); /* XW */
       fixed_mm(&f, Af, XW, (size_t)N, (size_t)N, (size_t)fo, bias, agg_split(d) ? 8 : 0, Hn); /* A.XW */
       for (int i = 0; i < N; i++)
@@ -557,26 +560,22 @@ size_t orc_model_key_bytes(const orc_dims *d, int B) {
   o = adjnorm_layout(bw, s, B, N, o);
   for (int l = 0; l < 3; l++) {
     size_t E = (size_t)B * N * d->gcn[l];
-    if (!local_trunc(d)) o = orc_tr_layout_make(xw_kind(d), bw, s, E, o).end;
+    o = xw_slack(d) ? orc_tr_layout_make(ORC_G_TRSLACK, bw, s, E, o).end : trunc_layout(d, 0, E, o);
     o = orc_sxs_layout(bw, (size_t)B, (size_t)N, (size_t)N, (size_t)d->gcn[l], o, &r1, &r2, &r3);
-    if (local_trunc(d)) {
-      o = orc_tr_layout_make(ORC_G_RELU, bw, s, E, o).end;
-    } else if (agg_split(d)) {
+    if (agg_split(d)) {
       o = orc_tr_layout_make(ORC_G_TRSLACK, bw, s, E, o).end;
       o = orc_tr_layout_make(ORC_G_RELUSLACK, bw, s, E, o).end;
     } else {
-      o = orc_tr_layout_make(ORC_G_TRRELU, bw, s, E, o).end;
+      o = trunc_layout(d, 1, E, o);
     }
   }
   int pairs[32];
   int L = pool_levels(N, pairs);
   for (int l = 0; l < L; l++)
     o = orc_tr_layout_make(ORC_G_RELU, bw, s, (size_t)B * pairs[l] * d->gcn[2], o).end;
-  const int relu_kind = local_trunc(d) ? ORC_G_RELU : ORC_G_TRRELU;
-  o = orc_tr_layout_make(relu_kind, bw, s, (size_t)B * d->dfc[0], o).end;
-  if (!local_trunc(d)) o = orc_tr_layout_make(ORC_G_TR, bw, s, (size_t)B * d->dfc[1], o).end;
-  for (int k = 0; k < d->nfus - 1; k++)
-    o = orc_tr_layout_make(relu_kind, bw, s, (size_t)B * d->fus[k], o).end;
+  o = trunc_layout(d, 1, (size_t)B * d->dfc[0], o);
+  o = trunc_layout(d, 0, (size_t)B * d->dfc[1], o);
+  for (int k = 0; k < d->nfus - 1; k++) o = trunc_layout(d, 1, (size_t)B * d->fus[k], o);
   o = orc_reveal_layout(bw, (size_t)B * d->fus[d->nfus - 1], o, &r1);
   return o;
 }
@@ -587,18 +586,31 @@ static void pub_gemm(int bw, size_t rows, int fi, int fo, const uint64_t *x, con
   orc_ring_gemm(bw, 1, rows, (size_t)fi, (size_t)fo, x, (const uint64_t *)Wt, y, 0);
 }
 
-/* A layer truncation by s (+ bias in eval) and, for relu, the ReLU: one TR or
- * TRRELU gate; with local truncation the local shift (no key, no gate id) and,
- * for relu, a RELU gate.  Keygen maps the mask rin to rout (rin may be
- * overwritten); eval maps x (may be overwritten) to y.  Return the key end. */
+/* A layer truncation by s (+ bias in eval) and, for relu, the ReLU.  Exact: the
+ * truncate-reduce TRMOD (one s-bit DCF, output exact modulo 2^(bw-s)), revealed,
+ * then EXT or EXTRELU (one (bw-s-1)-bit DCF for the sign and the wrap) -- the
+ * reference's TrFloor as truncate-reduce plus sign extension
+ * (gpu_mpc/dpf_dcf_adapter.h:274-303) with the ReLU fused into the extension
+ * (gpuReluExtend, :225-234).  With local truncation: the local shift (no key, no
+ * gate id) and, for relu, a RELU gate.  Keygen maps the mask rin to rout (rin
+ * may be overwritten); eval maps x (may be overwritten) to y.  Return the key end. */
+static size_t trunc_layout(const orc_dims *d, int relu, size_t n, size_t o) {
+  const int bw = d->bw, s = d->s;
+  if (local_trunc(d)) return relu ? orc_tr_layout_make(ORC_G_RELU, bw, s, n, o).end : o;
+  o = orc_tr_layout_make(ORC_G_TRMOD, bw, s, n, o).end;
+  return orc_tr_layout_make(relu ? ORC_G_EXTRELU : ORC_G_EXT, bw, s, n, o).end;
+}
 static size_t trunc_keygen(const orc_dims *d, uint64_t seed, uint32_t *g, int relu, size_t n, uint64_t *rin,
                            uint64_t *rout, uint8_t *k0, uint8_t *k1, size_t o) {
   const int bw = d->bw, s = d->s;
-  int kind = relu ? ORC_G_TRRELU : ORC_G_TR;
+  int kind = relu ? ORC_G_EXTRELU : ORC_G_EXT;
   if (local_trunc(d)) {
     orc_tr_keygen(0, 0, ORC_G_LOCALARS, bw, s, n, rin, relu ? rin : rout, NULL, NULL, o);
     if (!relu) return o;
     kind = ORC_G_RELU;
+  } else {
+    orc_tr_keygen(seed, (*g)++, ORC_G_TRMOD, bw, s, n, rin, rin, k0, k1, o);
+    o = orc_tr_layout_make(ORC_G_TRMOD, bw, s, n, o).end;
   }
   orc_tr_keygen(seed, (*g)++, kind, bw, s, n, rin, rout, k0, k1, o);
   return orc_tr_layout_make(kind, bw, s, n, o).end;
@@ -606,14 +618,17 @@ static size_t trunc_keygen(const orc_dims *d, uint64_t seed, uint32_t *g, int re
 static size_t trunc_eval(const orc_dims *d, uint32_t *g, int relu, size_t n, const uint8_t *k0, const uint8_t *k1,
                          size_t o, uint64_t *x, const int64_t *be, uint64_t *y, uint64_t *by) {
   const int bw = d->bw, s = d->s;
-  int kind = relu ? ORC_G_TRRELU : ORC_G_TR;
+  int kind = relu ? ORC_G_EXTRELU : ORC_G_EXT;
   if (local_trunc(d)) {
     orc_tr_eval(ORC_G_LOCALARS, bw, s, n, NULL, NULL, o, x, be, relu ? x : y, by);
     if (!relu) return o;
     kind = ORC_G_RELU;
-    be = NULL;
+  } else {
+    orc_tr_eval(ORC_G_TRMOD, bw, s, n, k0, k1, o, x, be, x, by);
+    trace((*g)++, n, x);
+    o = orc_tr_layout_make(ORC_G_TRMOD, bw, s, n, o).end;
   }
-  orc_tr_eval(kind, bw, s, n, k0, k1, o, x, be, y, by);
+  orc_tr_eval(kind, bw, s, n, k0, k1, o, x, NULL, y, by);
   trace((*g)++, n, y);
   return orc_tr_layout_make(kind, bw, s, n, o).end;
 }
@@ -649,24 +664,21 @@ int orc_model_keygen(const orc_dims *d, int B, uint64_t seed, const int64_t *W, 
     int fo = d->gcn[l];
     size_t E = BN * fo;
     pub_gemm(bw, BN, fin, fo, rX, W + layer_off(d, l), t1); /* mask of H.Wt */
-    if (local_trunc(d)) {
-      o = trunc_keygen(d, seed, &g, 0, E, t1, t2, k0, k1, o);
+    if (xw_slack(d)) {
+      orc_tr_keygen(seed, g++, ORC_G_TRSLACK, bw, s, E, t1, t2, k0, k1, o);
+      o = orc_tr_layout_make(ORC_G_TRSLACK, bw, s, E, o).end;
     } else {
-      orc_tr_keygen(seed, g++, xw_kind(d), bw, s, E, t1, t2, k0, k1, o);
-      o = orc_tr_layout_make(xw_kind(d), bw, s, E, o).end;
+      o = trunc_keygen(d, seed, &g, 0, E, t1, t2, k0, k1, o);
     }
     orc_sxs_keygen(seed, g++, bw, (size_t)B, (size_t)N, (size_t)N, (size_t)fo, rN, t2, t1, k0, k1, o);
     o = orc_sxs_layout(bw, (size_t)B, (size_t)N, (size_t)N, (size_t)fo, o, &r1, &r2, &r3);
-    if (local_trunc(d)) {
-      o = trunc_keygen(d, seed, &g, 1, E, t1, rX, k0, k1, o);
-    } else if (agg_split(d)) {
+    if (agg_split(d)) {
       orc_tr_keygen(seed, g++, ORC_G_TRSLACK, bw, s, E, t1, t2, k0, k1, o);
       o = orc_tr_layout_make(ORC_G_TRSLACK, bw, s, E, o).end;
       orc_tr_keygen(seed, g++, ORC_G_RELUSLACK, bw, s, E, t2, rX, k0, k1, o);
       o = orc_tr_layout_make(ORC_G_RELUSLACK, bw, s, E, o).end;
     } else {
-      orc_tr_keygen(seed, g++, ORC_G_TRRELU, bw, s, E, t1, rX, k0, k1, o);
-      o = orc_tr_layout_make(ORC_G_TRRELU, bw, s, E, o).end;
+      o = trunc_keygen(d, seed, &g, 1, E, t1, rX, k0, k1, o);
     }
     fin = fo;
   }
@@ -760,30 +772,26 @@ int orc_model_eval(const orc_dims *d, int B, const int64_t *W, const uint8_t *k0
     const int64_t *Wt = W + layer_off(d, l);
     const int64_t *bias = Wt + (size_t)fin * fo;
     pub_gemm(bw, BN, fin, fo, H, Wt, t1);
-    if (local_trunc(d)) {
-      o = trunc_eval(d, &g, 0, E, k0, k1, o, t1, NULL, t2, &by);
-    } else {
-      orc_tr_eval(xw_kind(d), bw, s, E, k0, k1, o, t1, NULL, t2, &by);
+    if (xw_slack(d)) {
+      orc_tr_eval(ORC_G_TRSLACK, bw, s, E, k0, k1, o, t1, NULL, t2, &by);
       trace(g++, E, t2);
-      o = orc_tr_layout_make(xw_kind(d), bw, s, E, o).end;
+      o = orc_tr_layout_make(ORC_G_TRSLACK, bw, s, E, o).end;
+    } else {
+      o = trunc_eval(d, &g, 0, E, k0, k1, o, t1, NULL, t2, &by);
     }
     orc_sxs_eval(bw, (size_t)B, (size_t)N, (size_t)N, (size_t)fo, k0, k1, o, An, t2, t1, &by);
     trace(g++, E, t1);
     o = orc_sxs_layout(bw, (size_t)B, (size_t)N, (size_t)N, (size_t)fo, o, &r1, &r2, &r3);
     for (size_t e = 0; e < E; e++) be[e] = bias[e % fo];
-    if (local_trunc(d)) {
+    if (!agg_split(d)) {
       o = trunc_eval(d, &g, 1, E, k0, k1, o, t1, be, H, &by);
-    } else if (agg_split(d)) {
+    } else {
       orc_tr_eval(ORC_G_TRSLACK, bw, s, E, k0, k1, o, t1, be, t2, &by);
       trace(g++, E, t2);
       o = orc_tr_layout_make(ORC_G_TRSLACK, bw, s, E, o).end;
       orc_tr_eval(ORC_G_RELUSLACK, bw, s, E, k0, k1, o, t2, NULL, H, &by);
       trace(g++, E, H);
       o = orc_tr_layout_make(ORC_G_RELUSLACK, bw, s, E, o).end;
-    } else {
-      orc_tr_eval(ORC_G_TRRELU, bw, s, E, k0, k1, o, t1, be, H, &by);
-      trace(g++, E, H);
-      o = orc_tr_layout_make(ORC_G_TRRELU, bw, s, E, o).end;
     }
     fin = fo;
   }

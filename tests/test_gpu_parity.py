@@ -141,6 +141,38 @@ def test_tr_family_keys_and_eval(ctx, orc, kind):
     assert np.array_equal(signed(y.astype(np.uint64) - orout, bw), _tr_expected(kind, x, bias))
 
 
+@pytest.mark.parametrize("relu", [False, True])
+def test_split_truncation_keys_and_eval(ctx, orc, relu):
+    """The exact truncation as two gates, TRMOD (truncate-reduce, s-bit DCF) then
+    EXT / EXTRELU (sign extension, (bw-s-1)-bit DCF; gpu_mpc/dpf_dcf_adapter.h:
+    225-234, 274-303): both gates' keys byte-identical to the oracle's, each
+    revealed value and the exchanged bytes identical, and the unmasked result the
+    signed floor (+ bias), and its ReLU, over the whole ring."""
+    bw = ctx.bw
+    rng = np.random.default_rng(bw * 7 + relu)
+    x, bias = _tr_inputs(rng, 1, bw)
+    rin = rmask(rng, x.size, bw)
+    kind = 14 if relu else 13
+    g0, g1, gr1 = ctx.tr_keygen(12, rin, seed=6, gate=30)
+    q0, q1, gr2 = ctx.tr_keygen(kind, gr1, seed=6, gate=31)
+    o0, o1, or1 = orc.tr_keygen(6, 30, 12, bw, S, rin)
+    p0, p1, or2 = orc.tr_keygen(6, 31, kind, bw, S, or1)
+    assert np.array_equal(gr1.astype(np.uint64), or1) and np.array_equal(gr2.astype(np.uint64), or2)
+    for g, o in ((g0, o0), (g1, o1), (q0, p0), (q1, p1)):
+        assert np.array_equal(host(g)[:o.size], o)
+    xhat = (x.astype(np.uint64) + rin) & M(bw)
+    ctx.reset_counters()
+    y1 = ctx.tr_eval(12, g0, g1, xhat, bias)
+    y2 = ctx.tr_eval(kind, q0, q1, y1)
+    by = ctx.bytes_exchanged
+    be = np.resize(bias, x.size)
+    oy1, b1 = orc.tr_eval(12, bw, S, o0, o1, xhat, be)
+    oy2, b2 = orc.tr_eval(kind, bw, S, p0, p1, oy1)
+    assert np.array_equal(y1.astype(np.uint64), oy1) and np.array_equal(y2.astype(np.uint64), oy2)
+    assert by == b1 + b2
+    assert np.array_equal(signed(y2.astype(np.uint64) - or2, bw), _tr_expected(2 if relu else 1, x, bias))
+
+
 def test_local_ars_matches_oracle(ctx, orc):
     """LocalARS (TruncateType::LocalARS, ddg_orca_batched.h:180-199): no key and no
     exchange; output mask and outputs identical to the oracle's, whose closed form
@@ -191,7 +223,7 @@ def test_empty_inputs_are_no_ops(ctx):
     its (null) pointers or counting an exchange; bad kinds are still refused."""
     lib, h, N = ctx.lib, ctx.h, None
     ctx.reset_counters()
-    for kind in (1, 2, 3, 4, 9, 10, 11):
+    for kind in (1, 2, 3, 4, 9, 10, 11, 12, 13, 14):
         assert ctx.lib.mpcx_tr_key_bytes(h, kind, 0) == 0
         assert lib.mpcx_tr_keygen(h, kind, 0, N, N, 1, 1, N, N) == 0
         assert lib.mpcx_tr_eval(h, kind, 0, N, N, N, N, 0, N) == 0
@@ -435,12 +467,13 @@ def test_model_local_truncation(mp, orc, synth, bw):
 
 
 def _tr_gates(dims):
-    """DCF-evaluation launches of one forward: TRSLACK, 3 x (TR, TRRELU), the
-    pool levels, the two drug FCs and the hidden fusion layers."""
+    """DCF-evaluation launches of one exact forward: the adjacency block's
+    TRSLACK, 3 x (TRMOD, EXT, TRMOD, EXTRELU), the pool levels, then TRMOD and
+    EXT / EXTRELU for the two drug FCs and the hidden fusion layers."""
     R, levels = dims.n_nodes, 0
     while R > 1:
         R, levels = R // 2 + (R & 1), levels + 1
-    return 1 + 6 + levels + 2 + len(dims.fus) - 1
+    return 1 + 12 + levels + 2 * (2 + len(dims.fus) - 1)
 
 
 @pytest.mark.parametrize("bw,B,lanes", [(32, 5, 2), (64, 4, 3), (32, 2, 4)])

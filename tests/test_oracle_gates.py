@@ -72,6 +72,45 @@ def test_tr_relu_family(orc, bw, kind):
 
 
 @pytest.mark.parametrize("bw", [32, 64])
+@pytest.mark.parametrize("relu", [False, True])
+def test_split_truncation(orc, bw, relu):
+    """TRMOD then EXT (EXTRELU) = signed floor((x + bias*2^s)/2^s), and its ReLU,
+    over the whole signed ring (the ring's edges included): the two-gate exact
+    truncation with one s-bit and one (bw-s-1)-bit DCF (gpu_mpc/dpf_dcf_adapter.h:
+    274-303, ReLU-extend :225-234).  TRMOD alone is exact modulo 2^(bw-s) only;
+    EXT reads only the low bw-s bits of its input and of its input mask."""
+    rng = np.random.default_rng(bw * 3 + relu)
+    n = 4000
+    h = 1 << (bw - 1)
+    x = np.concatenate([np.array(edge_values(bw, S), np.int64), rng.integers(-h, h - 1, size=n, dtype=np.int64),
+                        rng.integers(-5 << S, 5 << S, size=n)])
+    N = x.size
+    bias = rng.integers(-(1 << 14), 1 << 14, size=N)
+    lim = h - (1 << (14 + S)) - 1
+    x = np.clip(x, -lim, lim)
+    M = np.uint64(mod(bw) if bw < 64 else 0xFFFFFFFFFFFFFFFF)
+    low = np.uint64((1 << (bw - S)) - 1)
+    rin = mask_in(rng, N, bw)
+    k0, k1, r1 = orc.tr_keygen(5, 20, 12, bw, S, rin)
+    y1, b1 = orc.tr_eval(12, bw, S, k0, k1, (ring(x, bw) + rin) & M, bias)
+    exp = (x + (bias << S)) >> S
+    assert np.array_equal((y1 - r1) & low, ring(exp, bw) & low)
+    # only the low bw-s bits are meaningful: move the high bits of the value and
+    # of its mask independently
+    y1x = (y1 + (rng.integers(0, 1 << S, size=N).astype(np.uint64) << np.uint64(bw - S))) & M
+    r1x = (r1 + (rng.integers(0, 1 << S, size=N).astype(np.uint64) << np.uint64(bw - S))) & M
+    kind = 14 if relu else 13
+    q0, q1, r2 = orc.tr_keygen(5, 21, kind, bw, S, r1x)
+    y2, b2 = orc.tr_eval(kind, bw, S, q0, q1, y1x)
+    got = to_signed(y2 - r2, bw)
+    assert np.array_equal(got, np.maximum(exp, 0) if relu else exp)
+    per = 2 * (((N + 31) // 32) * 4 + N * bw // 8)
+    assert b1 == per and b2 == per
+    split = orc.tr_layout(12, bw, S, N).end + orc.tr_layout(kind, bw, S, N).end
+    assert split < orc.tr_layout(2 if relu else 1, bw, S, N).end
+
+
+@pytest.mark.parametrize("bw", [32, 64])
 def test_tr_slack(orc, bw):
     rng = np.random.default_rng(bw)
     q = 1 << (bw - 2)
