@@ -322,11 +322,13 @@ hipError_t ctx_scratch(mpcx_ctx *c, size_t bytes, void **p) {
 }
 static_assert(MPCX_TR == G_TR && MPCX_TRRELU == G_TRRELU && MPCX_RELU == G_RELU && MPCX_TRSLACK == G_TRSLACK &&
                   MPCX_RELUSLACK == G_RELUSLACK && MPCX_LOCALARS == G_LOCALARS && MPCX_DRELU == G_DRELU &&
-                  MPCX_TRMOD == G_TRMOD && MPCX_EXT == G_EXT && MPCX_EXTRELU == G_EXTRELU,
+                  MPCX_TRMOD == G_TRMOD && MPCX_EXT == G_EXT && MPCX_EXTRELU == G_EXTRELU &&
+                  MPCX_RELUPOOL == G_RELUPOOL,
               "the C API's gate kinds are the library's");
 bool valid_kind(int k) {
   return k == MPCX_TR || k == MPCX_TRRELU || k == MPCX_RELU || k == MPCX_TRSLACK || k == MPCX_RELUSLACK ||
-         k == MPCX_LOCALARS || k == MPCX_DRELU || k == MPCX_TRMOD || k == MPCX_EXT || k == MPCX_EXTRELU;
+         k == MPCX_LOCALARS || k == MPCX_DRELU || k == MPCX_TRMOD || k == MPCX_EXT || k == MPCX_EXTRELU ||
+         k == MPCX_RELUPOOL;
 }
 }  // namespace
 

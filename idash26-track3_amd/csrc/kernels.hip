@@ -274,7 +274,9 @@ struct TrArgs {
   uint32_t gate;
 };
 
-__device__ __forceinline__ bool relu_like(int kind) { return kind == G_RELU || kind == G_RELUSLACK; }
+__device__ __forceinline__ bool relu_like(int kind) {
+  return kind == G_RELU || kind == G_RELUSLACK || kind == G_RELUPOOL;
+}
 
 // v mod 2^m for 1 <= m <= bits of T
 template <typename T>

@@ -498,6 +498,19 @@ class Model final : public ModelBase, KeySource {
   // the GCN aggregation A.XW + bias, then ReLU: the layer truncation with ReLU, or
   // (slack 2) TRSLACK with the bias followed by RELUSLACK on the truncated value
   bool agg_split() const { return d_.slack == 2; }
+  // The max-pool's sentinel and ReLU gate.  Exact and slack layer truncations
+  // leave the GCN activations in [0, 2^(bw-s-1)) (EXTRELU outputs; RELUSLACK's
+  // are smaller), so with the sentinel -2^(bw-s-1) on padding rows every pool
+  // value lies in [-2^(bw-s-1), 2^(bw-s-1)), every pair difference below 2^(bw-s)
+  // in magnitude, and its ReLU takes a (bw-s)-bit DCF (RELUPOOL, 14 AES at bw=32)
+  // instead of a (bw-1)-bit one (25).  The maximum over a sample with a real atom
+  // is the one the reference's sentinel -2^(bw-2) gives (fixed_forward.py:33-36,
+  // 76-80).  Local truncation leaves activations anywhere in [0, 2^(bw-1)), and
+  // a mask scale above bw-s-1 does not fit the smaller sentinel: there the
+  // reference's sentinel and a full RELU gate.
+  bool pool_narrow() const { return !local_trunc() && d_.mask_scale <= bw_ - s_ - 1; }
+  int pool_kind() const { return pool_narrow() ? G_RELUPOOL : G_RELU; }
+  int pool_sentinel_bit() const { return pool_narrow() ? bw_ - s_ - 1 : bw_ - 2; }
 
   // A layer truncation by s (+ bias) and, for relu, the ReLU.  Exact: the
   // truncate-reduce TRMOD (one s-bit DCF; its output is exact modulo 2^(bw-s)),
@@ -633,7 +646,7 @@ class Model final : public ModelBase, KeySource {
     }
     int pairs[32];
     int Lv = pool_levels(N, pairs);
-    for (int l = 0; l < Lv; l++) tr(G_RELU, size_t(B) * pairs[l] * d_.gcn[2]);
+    for (int l = 0; l < Lv; l++) tr(pool_kind(), size_t(B) * pairs[l] * d_.gcn[2]);
     trunc(true, size_t(B) * d_.dfc[0]);
     trunc(false, size_t(B) * d_.dfc[1]);
     for (int k = 0; k < d_.nfus - 1; k++) trunc(true, size_t(B) * d_.fus[k]);
@@ -768,7 +781,7 @@ class Model final : public ModelBase, KeySource {
     }
     // pool
     const int C = d_.gcn[2];
-    const T Sm = T(1) << (bw - 2 - d_.mask_scale);
+    const T Sm = T(1) << (pool_sentinel_bit() - d_.mask_scale);
     TRY(launch_pool_prep<T>(L_, BN, C, rX.p, rm.p, Sm, T(0), t2.p));  // rV in t2
     T *cur = t2.p, *nxt = rX.p;
     int pairs[32];
@@ -778,7 +791,7 @@ class Model final : public ModelBase, KeySource {
       const int pr = pairs[l];
       const size_t En = size_t(B) * pr * C;
       TRY(launch_pool_diff<T>(L_, B, R, C, cur, t1.p));
-      TRY(d.tr(G_RELU, En, t1.p, gt.p));
+      TRY(d.tr(pool_kind(), En, t1.p, gt.p));
       TRY(launch_pool_combine<T>(L_, B, R, C, cur, gt.p, nullptr, nxt));
       std::swap(cur, nxt);
       R = pr + (R & 1);
@@ -1380,10 +1393,11 @@ class Model final : public ModelBase, KeySource {
         TRY(trunc_eval(r, true, En, Z, bias_[l].p, fo, H));
       }
     }
-    // masked max-pool: V = H + 2^(bw-2-ms) m^ - 2^(bw-2) (the sentinel -2^(bw-2) on
-    // padding rows for a mask of 0 or 2^ms), then a tree of max(a,b) = a + ReLU(b-a)
+    // masked max-pool: V = H + 2^(q-ms) m^ - 2^q (the sentinel -2^q on padding rows
+    // for a mask of 0 or 2^ms, q = pool_sentinel_bit()), then a tree of
+    // max(a,b) = a + ReLU(b-a)
     const int C = d_.gcn[2];
-    const T S = T(1) << (bw - 2), Sm = T(1) << (bw - 2 - d_.mask_scale);
+    const T S = T(1) << pool_sentinel_bit(), Sm = T(1) << (pool_sentinel_bit() - d_.mask_scale);
     TRY(launch_pool_prep<T>(L_, BN, C, H, mh_.p, Sm, T(0) - S, V0_.p));
     T *cur = V0_.p, *nxt = V1_.p;
     int pairs[32];
@@ -1393,7 +1407,7 @@ class Model final : public ModelBase, KeySource {
       const int pr = pairs[l];
       const size_t En = size_t(B) * pr * C;
       TRY(launch_pool_diff<T>(L_, B, R, C, cur, Z));
-      TRY(r.tr(G_RELU, En, Z, nullptr, 1, XW));
+      TRY(r.tr(pool_kind(), En, Z, nullptr, 1, XW));
       TRY(launch_pool_combine<T>(L_, B, R, C, cur, XW, nullptr, nxt));
       std::swap(cur, nxt);
       R = pr + (R & 1);

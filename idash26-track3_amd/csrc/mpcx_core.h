@@ -30,7 +30,9 @@ enum GateKind : int {
   G_DRELU = 11,      // [x >= 0] as a masked public bit: one (bw-1)-bit DCF, one round
   G_TRMOD = 12,      // floor(x/2^s) + bias, exact modulo 2^(bw-s) only: one s-bit DCF
   G_EXT = 13,        // a value known modulo 2^(bw-s) (a TRMOD output) sign-extended to bw bits
-  G_EXTRELU = 14     // ReLU of that value, sign-extended: one (bw-s-1)-bit DCF for both
+  G_EXTRELU = 14,    // ReLU of that value, sign-extended: one (bw-s-1)-bit DCF for both
+  G_RELUPOOL = 15    // ReLU for |x| < 2^(bw-s), e.g. the difference of two values in
+                     // [-2^(bw-s-1), 2^(bw-s-1)) (truncated ones): a (bw-s)-bit DCF
 };
 
 // Gate-kind properties of the truncation family.  A gate reads its public
@@ -41,7 +43,7 @@ inline int tr_in_bits(int kind, int bw, int s) { return tr_ext(kind) ? bw - s : 
 inline int tr_shift(int kind, int s) { return tr_ext(kind) ? 0 : s; }
 inline bool tr_has_bias(int kind) { return kind == G_TR || kind == G_TRRELU || kind == G_TRSLACK || kind == G_TRMOD; }
 inline bool tr_is_relu(int kind) {
-  return kind == G_TRRELU || kind == G_RELU || kind == G_RELUSLACK || kind == G_EXTRELU;
+  return kind == G_TRRELU || kind == G_RELU || kind == G_RELUSLACK || kind == G_EXTRELU || kind == G_RELUPOOL;
 }
 // the (sign-bit)-bit DCF "a" and the s-bit DCF "b"
 inline bool tr_uses_a(int kind) { return kind != G_TRSLACK && kind != G_TRMOD && kind != G_LOCALARS; }
@@ -51,7 +53,7 @@ inline int tr_ncase(int kind) {
   switch (kind) {
     case G_TR: case G_TRRELU: case G_TRSLACK: return 8;
     case G_EXT: case G_EXTRELU: return 4;
-    case G_RELU: case G_RELUSLACK: case G_TRMOD: return 2;
+    case G_RELU: case G_RELUSLACK: case G_RELUPOOL: case G_TRMOD: return 2;
     default: return 0;
   }
 }
@@ -102,10 +104,10 @@ struct TrLayout {
 };
 
 // Bit of the shifted input that carries the sign: the top bit of the input
-// width, or bit bw-2-s for RELUSLACK (inputs |x| < 2^(bw-2-s), e.g. a value
-// truncated by TRSLACK).
+// width, bit bw-2-s for RELUSLACK (inputs |x| < 2^(bw-2-s), e.g. a value
+// truncated by TRSLACK) and bit bw-s for RELUPOOL (|x| < 2^(bw-s)).
 inline int tr_sign_bit(int kind, int bw, int s) {
-  return kind == G_RELUSLACK ? bw - 2 - s : tr_in_bits(kind, bw, s) - 1;
+  return kind == G_RELUSLACK ? bw - 2 - s : kind == G_RELUPOOL ? bw - s : tr_in_bits(kind, bw, s) - 1;
 }
 
 inline TrLayout tr_layout(int kind, int bw, int s, size_t N, size_t base) {

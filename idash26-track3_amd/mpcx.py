@@ -12,7 +12,8 @@ import numpy as np
 HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(HERE, "libmpcx.so")
 
-TR, TRRELU, RELU, TRSLACK, RELUSLACK, LOCALARS, DRELU, TRMOD, EXT, EXTRELU = 1, 2, 3, 4, 9, 10, 11, 12, 13, 14
+TR, TRRELU, RELU, TRSLACK, RELUSLACK, LOCALARS, DRELU, TRMOD, EXT, EXTRELU, RELUPOOL = \
+    1, 2, 3, 4, 9, 10, 11, 12, 13, 14, 15
 
 _lib = None
 

@@ -63,6 +63,9 @@ typedef struct mpcx_model mpcx_model;
                            one (bw-s-1)-bit DCF.  TRMOD then EXT = MPCX_TR */
 #define MPCX_EXTRELU 14 /* ReLU(y) of that value, sign-extended: the same one DCF gives the
                            sign and the wrap.  TRMOD then EXTRELU = MPCX_TRRELU */
+#define MPCX_RELUPOOL 15 /* ReLU(x), requires |x| < 2^(bw-s): one (bw-s)-bit DCF (the max-pool
+                            differences of EXT / EXTRELU outputs, which lie in
+                            [-2^(bw-s-1), 2^(bw-s-1))) */
 
 /* ---------------- context ----------------
  * Replaces the evaluator/dealer constructors DDGOrcaBase(party, ip, bw, scale)

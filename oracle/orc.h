@@ -97,7 +97,8 @@ enum {
   ORC_G_TRMOD = 12,    /* floor(x/2^s) + bias modulo 2^(bw-s): one s-bit DCF */
   ORC_G_EXT = 13,      /* a value known modulo 2^(bw-s) sign-extended to bw bits:
                           one (bw-s-1)-bit DCF */
-  ORC_G_EXTRELU = 14   /* ReLU of that value, sign-extended: the same one DCF */
+  ORC_G_EXTRELU = 14,  /* ReLU of that value, sign-extended: the same one DCF */
+  ORC_G_RELUPOOL = 15  /* ReLU for |x| < 2^(bw-s): a (bw-s)-bit DCF */
 };
 
 /* Dealer randomness fields. */

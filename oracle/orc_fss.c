@@ -145,21 +145,24 @@ static int has_bias(int kind) {
 }
 static int uses_a(int kind) { return kind != ORC_G_TRSLACK && kind != ORC_G_TRMOD; }
 static int is_relu(int kind) {
-  return kind == ORC_G_TRRELU || kind == ORC_G_RELU || kind == ORC_G_RELUSLACK || kind == ORC_G_EXTRELU;
+  return kind == ORC_G_TRRELU || kind == ORC_G_RELU || kind == ORC_G_RELUSLACK || kind == ORC_G_EXTRELU ||
+         kind == ORC_G_RELUPOOL;
 }
 static int ncase_of(int kind) {
   switch (kind) {
     case ORC_G_TR: case ORC_G_TRRELU: case ORC_G_TRSLACK: return 8;
     case ORC_G_EXT: case ORC_G_EXTRELU: return 4;
-    case ORC_G_RELU: case ORC_G_RELUSLACK: case ORC_G_TRMOD: return 2;
+    case ORC_G_RELU: case ORC_G_RELUSLACK: case ORC_G_RELUPOOL: case ORC_G_TRMOD: return 2;
     default: return 0;
   }
 }
 
 /* bit of the shifted input that carries the sign: the top bit of the input
- * width, or bit bw-2-s for RELUSLACK (inputs |x| < 2^(bw-2-s), e.g. a value
- * truncated by TRSLACK) */
-int orc_sign_bit(int kind, int bw, int s) { return kind == ORC_G_RELUSLACK ? bw - 2 - s : in_bits(kind, bw, s) - 1; }
+ * width, bit bw-2-s for RELUSLACK (inputs |x| < 2^(bw-2-s), e.g. a value
+ * truncated by TRSLACK) and bit bw-s for RELUPOOL (|x| < 2^(bw-s)) */
+int orc_sign_bit(int kind, int bw, int s) {
+  return kind == ORC_G_RELUSLACK ? bw - 2 - s : kind == ORC_G_RELUPOOL ? bw - s : in_bits(kind, bw, s) - 1;
+}
 
 orc_tr_layout orc_tr_layout_make(int kind, int bw, int s, size_t N, size_t base) {
   orc_tr_layout T;
@@ -420,7 +423,7 @@ void orc_tr_keygen(uint64_t seed, uint32_t gate, int kind, int bw, int s, size_t
   const uint64_t M = rmask(bw);
   const int n = bw, sb = orc_sign_bit(kind, bw, s);
   const int m = in_bits(kind, bw, s), sh = own_shift(kind, s);
-  const int relu_like = kind == ORC_G_RELU || kind == ORC_G_RELUSLACK;
+  const int relu_like = kind == ORC_G_RELU || kind == ORC_G_RELUSLACK || kind == ORC_G_RELUPOOL;
   const int no_b = !has_bias(kind); /* no s-bit DCF */
   const int use_a = uses_a(kind);
   const uint64_t lowmask = (1ull << sb) - 1ull;
@@ -497,7 +500,7 @@ void orc_tr_eval(int kind, int bw, int s, size_t N, const uint8_t *k0, const uin
   const uint64_t M = rmask(bw);
   const int n = bw, sb = orc_sign_bit(kind, bw, s);
   const int m = in_bits(kind, bw, s), sh = own_shift(kind, s);
-  const int relu_like = kind == ORC_G_RELU || kind == ORC_G_RELUSLACK;
+  const int relu_like = kind == ORC_G_RELU || kind == ORC_G_RELUSLACK || kind == ORC_G_RELUPOOL;
   const uint64_t lowmask = (1ull << sb) - 1ull;
   const uint64_t smask = (1ull << s) - 1ull;
   const int use_a = uses_a(kind), use_b = has_bias(kind);

@@ -46,6 +46,15 @@ static int xw_slack(const orc_dims *d) { return d->slack == 1 || d->slack == 2; 
  * (exact: TRMOD then EXTRELU), or (d->slack == 2) TRSLACK (with the bias)
  * followed by RELUSLACK on the truncated value */
 static int agg_split(const orc_dims *d) { return d->slack == 2; }
+/* the max-pool: exact and slack truncations leave activations in
+ * [0, 2^(bw-s-1)), so the sentinel -2^(bw-s-1) keeps every pool value in
+ * [-2^(bw-s-1), 2^(bw-s-1)) and a (bw-s)-bit DCF (RELUPOOL) decides each pair; the
+ * maximum over a sample with a real atom equals the one the reference's sentinel
+ * -2^(bw-2) gives (fixed_forward.py:33-36).  Local truncation (activations up to
+ * 2^(bw-1)) or a mask scale above bw-s-1: the sentinel -2^(bw-2) and RELU. */
+static int pool_narrow(const orc_dims *d) { return !local_trunc(d) && d->mask_scale <= d->bw - d->s - 1; }
+static int pool_kind(const orc_dims *d) { return pool_narrow(d) ? ORC_G_RELUPOOL : ORC_G_RELU; }
+static int pool_sentinel_bit(const orc_dims *d) { return pool_narrow(d) ? d->bw - d->s - 1 : d->bw - 2; }
 static size_t trunc_layout(const orc_dims *d, int relu, size_t n, size_t o);
 static void layer_io(const orc_dims *d, int l, int *in, int *out) {
   if (l < 3) {
@@ -328,8 +337,8 @@ static void build_maps(int B, int N, uint32_t *oa, uint32_t *ob, uint32_t *wa, u
  * V[2j] + ReLU(.) (:120-124), the odd last row carried forward (:140-147).
  * The dealer runs the same linear steps on the masks.  V is overwritten (its
  * first B*C words hold the result); t1, t2: scratch of B*N*C words. */
-static size_t pool_keygen_blk(uint64_t seed, uint32_t *g, int bw, int s, int B, int N, int C, uint64_t *rV,
-                              uint64_t *t1, uint64_t *t2, uint8_t *k0, uint8_t *k1, size_t o) {
+static size_t pool_keygen_blk(uint64_t seed, uint32_t *g, int kind, int bw, int s, int B, int N, int C,
+                              uint64_t *rV, uint64_t *t1, uint64_t *t2, uint8_t *k0, uint8_t *k1, size_t o) {
   const uint64_t M = rmask(bw);
   int pairs[32];
   int L = pool_levels(N, pairs), R = N;
@@ -341,8 +350,8 @@ static size_t pool_keygen_blk(uint64_t seed, uint32_t *g, int bw, int s, int B, 
         for (int c = 0; c < C; c++)
           t1[((size_t)b * pr + j) * C + c] =
               (rV[((size_t)b * R + 2 * j + 1) * C + c] - rV[((size_t)b * R + 2 * j) * C + c]) & M;
-    orc_tr_keygen(seed, (*g)++, ORC_G_RELU, bw, s, E, t1, t2, k0, k1, o);
-    o = orc_tr_layout_make(ORC_G_RELU, bw, s, E, o).end;
+    orc_tr_keygen(seed, (*g)++, kind, bw, s, E, t1, t2, k0, k1, o);
+    o = orc_tr_layout_make(kind, bw, s, E, o).end;
     int Rn = pr + (R & 1);
     for (int b = 0; b < B; b++) {
       for (int j = 0; j < pr; j++)
@@ -359,8 +368,8 @@ static size_t pool_keygen_blk(uint64_t seed, uint32_t *g, int bw, int s, int B, 
   return o;
 }
 
-static size_t pool_eval_blk(uint32_t *g, int bw, int s, int B, int N, int C, const uint8_t *k0, const uint8_t *k1,
-                            size_t o, uint64_t *V, uint64_t *t1, uint64_t *t2, uint64_t *bytes) {
+static size_t pool_eval_blk(uint32_t *g, int kind, int bw, int s, int B, int N, int C, const uint8_t *k0,
+                            const uint8_t *k1, size_t o, uint64_t *V, uint64_t *t1, uint64_t *t2, uint64_t *bytes) {
   const uint64_t M = rmask(bw);
   int pairs[32];
   int L = pool_levels(N, pairs), R = N;
@@ -372,9 +381,9 @@ static size_t pool_eval_blk(uint32_t *g, int bw, int s, int B, int N, int C, con
         for (int c = 0; c < C; c++)
           t1[((size_t)b * pr + j) * C + c] =
               (V[((size_t)b * R + 2 * j + 1) * C + c] - V[((size_t)b * R + 2 * j) * C + c]) & M;
-    orc_tr_eval(ORC_G_RELU, bw, s, E, k0, k1, o, t1, NULL, t2, bytes);
+    orc_tr_eval(kind, bw, s, E, k0, k1, o, t1, NULL, t2, bytes);
     trace((*g)++, E, t2);
-    o = orc_tr_layout_make(ORC_G_RELU, bw, s, E, o).end;
+    o = orc_tr_layout_make(kind, bw, s, E, o).end;
     int Rn = pr + (R & 1);
     for (int b = 0; b < B; b++) {
       for (int j = 0; j < pr; j++)
@@ -403,7 +412,7 @@ void orc_maxpool_keygen(uint64_t seed, uint32_t gate, int bw, int s, int B, int 
   const size_t n = (size_t)B * N * C;
   uint64_t *rV = (uint64_t *)malloc(8 * n), *t1 = (uint64_t *)malloc(8 * n), *t2 = (uint64_t *)malloc(8 * n);
   memcpy(rV, in_mask, 8 * n);
-  pool_keygen_blk(seed, &gate, bw, s, B, N, C, rV, t1, t2, k0, k1, base);
+  pool_keygen_blk(seed, &gate, ORC_G_RELU, bw, s, B, N, C, rV, t1, t2, k0, k1, base);
   memcpy(out_mask, rV, 8 * (size_t)B * C);
   free(rV);
   free(t1);
@@ -416,7 +425,7 @@ void orc_maxpool_eval(int bw, int s, int B, int N, int C, const uint8_t *k0, con
   uint64_t *V = (uint64_t *)malloc(8 * n), *t1 = (uint64_t *)malloc(8 * n), *t2 = (uint64_t *)malloc(8 * n);
   uint32_t g = 0;
   memcpy(V, xhat, 8 * n);
-  pool_eval_blk(&g, bw, s, B, N, C, k0, k1, base, V, t1, t2, bytes);
+  pool_eval_blk(&g, ORC_G_RELU, bw, s, B, N, C, k0, k1, base, V, t1, t2, bytes);
   memcpy(yhat, V, 8 * (size_t)B * C);
   free(V);
   free(t1);
@@ -572,7 +581,7 @@ size_t orc_model_key_bytes(const orc_dims *d, int B) {
   int pairs[32];
   int L = pool_levels(N, pairs);
   for (int l = 0; l < L; l++)
-    o = orc_tr_layout_make(ORC_G_RELU, bw, s, (size_t)B * pairs[l] * d->gcn[2], o).end;
+    o = orc_tr_layout_make(pool_kind(d), bw, s, (size_t)B * pairs[l] * d->gcn[2], o).end;
   o = trunc_layout(d, 1, (size_t)B * d->dfc[0], o);
   o = trunc_layout(d, 0, (size_t)B * d->dfc[1], o);
   for (int k = 0; k < d->nfus - 1; k++) o = trunc_layout(d, 1, (size_t)B * d->fus[k], o);
@@ -684,12 +693,12 @@ int orc_model_keygen(const orc_dims *d, int B, uint64_t seed, const int64_t *W, 
   }
   /* pool: V = H3 + S*m - S, mask rH3 + S*rm */
   const int C = d->gcn[2];
-  /* V = H + 2^(bw-2-ms) m - 2^(bw-2): the sentinel -2^(bw-2) on padding rows for a
-   * mask of 0 or 2^ms (ms = mask_scale) */
-  const uint64_t Sm = 1ull << (bw - 2 - d->mask_scale);
+  /* V = H + 2^(q-ms) m - 2^q: the sentinel -2^q on padding rows for a mask of 0
+   * or 2^ms (ms = mask_scale, q = pool_sentinel_bit) */
+  const uint64_t Sm = 1ull << (pool_sentinel_bit(d) - d->mask_scale);
   for (size_t r = 0; r < BN; r++)
     for (int c = 0; c < C; c++) rX[r * C + c] = (rX[r * C + c] + Sm * rm[r]) & M;
-  o = pool_keygen_blk(seed, &g, bw, s, B, N, C, rX, t1, t2, k0, k1, o);
+  o = pool_keygen_blk(seed, &g, pool_kind(d), bw, s, B, N, C, rX, t1, t2, k0, k1, o);
   /* drug FCs on the pooled (B x C) mask in rX */
   pub_gemm(bw, (size_t)B, C, d->dfc[0], rX, W + layer_off(d, 3), t1);
   o = trunc_keygen(d, seed, &g, 1, (size_t)B * d->dfc[0], t1, t2, k0, k1, o);
@@ -796,10 +805,10 @@ int orc_model_eval(const orc_dims *d, int B, const int64_t *W, const uint8_t *k0
     fin = fo;
   }
   const int C = d->gcn[2];
-  const uint64_t S = 1ull << (bw - 2), Sm = 1ull << (bw - 2 - d->mask_scale);
+  const uint64_t S = 1ull << pool_sentinel_bit(d), Sm = 1ull << (pool_sentinel_bit(d) - d->mask_scale);
   for (size_t r = 0; r < BN; r++)
     for (int c = 0; c < C; c++) H[r * C + c] = (H[r * C + c] + Sm * mh[r] - S) & M;
-  o = pool_eval_blk(&g, bw, s, B, N, C, k0, k1, o, H, t1, t2, &by);
+  o = pool_eval_blk(&g, pool_kind(d), bw, s, B, N, C, k0, k1, o, H, t1, t2, &by);
   {
     const int64_t *Wt = W + layer_off(d, 3);
     const int64_t *bias = Wt + (size_t)C * d->dfc[0];

@@ -96,8 +96,8 @@ def _tr_inputs(rng, kind, bw, n=4000):
     if kind == 4:
         x = np.concatenate([np.array([-q, -1, 0, 1, q - 1], np.int64), rng.integers(-q, q, size=n, dtype=np.int64)])
         return x, None
-    if kind == 9:
-        qs = 1 << (bw - 2 - S)
+    if kind in (9, 15):
+        qs = 1 << (bw - 2 - S if kind == 9 else bw - S)
         x = np.concatenate([np.array([-qs, -1, 0, 1, qs - 1], np.int64), rng.integers(-qs, qs, size=n, dtype=np.int64)])
         return x, None
     x = np.concatenate([np.array(edge, np.int64), rng.integers(-(h // 4), h // 4, size=n // 2, dtype=np.int64),
@@ -115,12 +115,12 @@ def _tr_expected(kind, x, bias):
         bb = np.resize(bias, x.size)
         t = (x + (bb << S)) >> S
         return t if kind == 1 else np.maximum(t, 0)
-    if kind in (3, 9):
+    if kind in (3, 9, 15):
         return np.maximum(x, 0)
     return x >> S
 
 
-@pytest.mark.parametrize("kind", [1, 2, 3, 4, 9])
+@pytest.mark.parametrize("kind", [1, 2, 3, 4, 9, 15])
 def test_tr_family_keys_and_eval(ctx, orc, kind):
     bw = ctx.bw
     rng = np.random.default_rng(kind * 100 + bw)
@@ -223,7 +223,7 @@ def test_empty_inputs_are_no_ops(ctx):
     its (null) pointers or counting an exchange; bad kinds are still refused."""
     lib, h, N = ctx.lib, ctx.h, None
     ctx.reset_counters()
-    for kind in (1, 2, 3, 4, 9, 10, 11, 12, 13, 14):
+    for kind in (1, 2, 3, 4, 9, 10, 11, 12, 13, 14, 15):
         assert ctx.lib.mpcx_tr_key_bytes(h, kind, 0) == 0
         assert lib.mpcx_tr_keygen(h, kind, 0, N, N, 1, 1, N, N) == 0
         assert lib.mpcx_tr_eval(h, kind, 0, N, N, N, N, 0, N) == 0

@@ -140,6 +140,29 @@ def test_relu_slack(orc, bw):
     assert orc.tr_layout(9, bw, S, x.size).end < orc.tr_layout(3, bw, S, x.size).end
 
 
+@pytest.mark.parametrize("bw", [32, 64])
+def test_relu_pool(orc, bw):
+    """ReLU for |x| < 2^(bw-s) with a (bw-s)-bit DCF (the max-pool differences of
+    truncated activations): the domain edges, values around 0, uniform values;
+    a value just outside (2^(bw-s)) reads as negative, so the gate really takes
+    the sign from bit bw-s."""
+    rng = np.random.default_rng(bw + 9)
+    q = 1 << (bw - S)
+    x = np.concatenate([np.array([-q + 1, -q // 2, -2, -1, 0, 1, 2, q // 2, q - 1], np.int64),
+                        rng.integers(-q + 1, q, size=4000, dtype=np.int64), rng.integers(-40, 40, size=500)])
+    rin = mask_in(rng, x.size, bw)
+    k0, k1, rout = orc.tr_keygen(9, 6, 15, bw, S, rin)
+    M = np.uint64(mod(bw) if bw < 64 else 0xFFFFFFFFFFFFFFFF)
+    y, by = orc.tr_eval(15, bw, S, k0, k1, (ring(x, bw) + rin) & M)
+    assert np.array_equal(to_signed(y - rout, bw), np.maximum(x, 0))
+    assert by == 2 * (((x.size + 31) // 32) * 4 + x.size * bw // 8)
+    assert orc.tr_layout(15, bw, S, x.size).end < orc.tr_layout(3, bw, S, x.size).end
+    xo = np.array([q, q + 5], np.int64)
+    ko0, ko1, ro = orc.tr_keygen(9, 7, 15, bw, S, rin[:2])
+    yo, _ = orc.tr_eval(15, bw, S, ko0, ko1, (ring(xo, bw) + rin[:2]) & M)
+    assert np.array_equal(to_signed(yo - ro, bw), [0, 0])
+
+
 def test_relu_slack_catches_wrong_sign_bit(orc):
     """A value just outside the domain (x = 2^(bw-2-s)) reads as negative: the
     gate really uses bit bw-2-s, which the in-domain test alone would not show."""
