@@ -194,8 +194,13 @@ struct AesPerm {
   const char *base;
   uint32_t lane4;  // (lane * 4) mod 256
 
+  // 16-byte stores: 16 per entry (its 64 copies), kWords / 4 in all
   __device__ static void fill(uint32_t *lds) {
-    for (int w = threadIdx.x; w < kWords; w += blockDim.x) lds[w] = c_T0.v[w >> 6];
+    uint4 *l4 = reinterpret_cast<uint4 *>(lds);
+    for (int q = threadIdx.x; q < kWords / 4; q += blockDim.x) {
+      const uint32_t v = c_T0.v[q >> 4];
+      l4[q] = make_uint4(v, v, v, v);
+    }
     __syncthreads();
   }
 
