@@ -29,12 +29,12 @@ GEMM_PEAK_TMACS = {"mfma32": 5.0e3 / 2 / 16, "mfma64": 5.0e3 / 2 / 64, "valu": V
 # VALU instructions per AES call of the DCF walk (one tree level: the unrolled
 # cipher, sigma, feed-forward and the level update), counted in the gfx950 ISA
 # of this build: hipcc --cuda-device-only -S csrc/kernels.hip, level-loop block
-# of k_tr_phase1<uint32_t, NT, REP> for each LDS table variant.
-# HBM bytes per k_tr_phase1 launch measured with rocprofv3 --pmc FETCH_SIZE and
+# of k_tr_eval<uint32_t, NT, REP> for each LDS table variant.
+# HBM bytes per k_tr_eval launch measured with rocprofv3 --pmc FETCH_SIZE and
 # WRITE_SIZE on this bench command (mean over the profiled forward's launches,
 # 19 per lane), each scaled by the same counter's reading for a 1 GiB elementwise
 # copy (FETCH_SIZE x 2.0, WRITE_SIZE x 1.0); keyed by (variant, B, bw, lanes, slack).
-# The summary is profiles/k_tr_phase1_affinity_bw32_B64.md.
+# The summary is profiles/k_tr_eval_affinity_bw32_B64.md.
 TRAFFIC_BYTES_PER_LAUNCH = {("perm64_b512", 64, 32, 3, 0): 229638822,
                             ("perm64_b512", 64, 32, 1, 0): 689753000}
 SLACK_DESC = {1: ", GCN products H.W^T truncated with the slack gate",
@@ -153,7 +153,7 @@ def main():
     step_tops = prof["aes_calls"] * VALU_OPS_PER_AES.get(variant, float("nan")) / (ms_per_step / 1e3) / 1e12
     gemm_path = "valu" if os.environ.get("MPCX_GEMM") == "valu" else f"mfma{args.bw}"
     gemm_tmacs = prof["gemm_macs"] / (prof["gemm_ms"] / 1e3) / 1e12 if prof["gemm_ms"] > 0 else 0.0
-    log(f"[bench] DCF phase-1: {prof['launches']} launches, {dcf_ms:.2f} ms/forward, "
+    log(f"[bench] DCF gate launches: {prof['launches']} launches, {dcf_ms:.2f} ms/forward, "
         f"{dcf_evals_per_s / 1e9:.3f} G evals/s, {aes_per_s / 1e9:.2f} G AES/s")
 
     result = {
@@ -182,8 +182,8 @@ def main():
         "rounds_per_step": rounds_per_fwd,
         "key_bytes_per_sample_per_party": round(key_bytes / B, 1),
         "roofline": {
-            "kernel": f"k_tr_phase1 (DCF evaluation, AES-128 T-tables in LDS, {variant}; the profiled "
-                      f"forward's launches, lanes one after another, traced as k_tr_phase1<..., 1>)",
+            "kernel": f"k_tr_eval (DCF gate evaluation of both parties, AES-128 T-tables in LDS, {variant}; "
+                      f"the profiled forward's launches, lanes one after another, traced as k_tr_eval<..., 1>)",
             "launches": prof["launches"],
             "avg_launch_us": round(1e3 * dcf_ms / max(prof["launches"], 1), 2),
             "bound": "valu",
@@ -198,7 +198,7 @@ def main():
         # the same DCF VALU work over the whole timed step (lanes overlapping):
         # a lower bound on the kernel's rate while it shares the GPU
         "roofline_step": {
-            "kernel": "k_tr_phase1, all launches of a step",
+            "kernel": "k_tr_eval, all launches of a step",
             "bound": "valu",
             "achieved": round(step_tops, 3),
             "peak": round(VALU_PEAK_TOPS, 2),
@@ -217,7 +217,7 @@ def main():
             "ring_macs_per_step": prof["gemm_macs"],
         },
         "roofline_hbm": {
-            "kernel": "k_tr_phase1 key stream",
+            "kernel": "k_tr_eval key stream",
             "bound": "hbm",
             "achieved": round(key_gbs, 1),
             "peak": HBM_PEAK_GBS,
@@ -499,7 +499,7 @@ def run_relu(args):
         "config": {"workload": f"secure ReLU microbench, {n} elements, bw=32, keys resident in HBM", "n": n},
         "aes_blocks_per_s": round(aes_s, 1),
         "key_bytes_per_element_per_party": round(key_bytes / n, 2),
-        "roofline": {"kernel": "RELU gate call (k_tr_phase1, k_tr_phase2, k_reconstruct)", "bound": "valu",
+        "roofline": {"kernel": "RELU gate call (k_tr_eval)", "bound": "valu",
                      "achieved": round(tops, 3), "peak": round(VALU_PEAK_TOPS, 2), "unit": "TOP/s",
                      "frac": round(tops / VALU_PEAK_TOPS, 4)},
         "roofline_hbm": {"kernel": "key stream", "bound": "hbm", "achieved": round(key_gbs, 1),

@@ -365,18 +365,14 @@ mpcx_status mpcx_tr_keygen(mpcx_ctx *c, int kind, size_t n, const void *in, void
 }
 
 // One TR-family gate evaluation of both parties into y (no synchronisation).
-// bits: four bit planes of ((n + 63) / 64) words; m: 2 n ring words.
 template <typename T>
 static hipError_t tr_eval_run(mpcx_ctx *c, const TrLayout &lay, size_t n, const uint8_t *K0, const uint8_t *K1,
-                              const T *X, const T *Bi, int ncol, T *y, uint64_t *bits, T *m) {
-  const size_t ww = (n + 63) / 64;
-  hipError_t e = launch_tr_phase1<T>(c->L, lay, K0, K1, X, Bi, ncol, bits, bits + ww, bits + 2 * ww, bits + 3 * ww);
+                              const T *X, const T *Bi, int ncol, T *y) {
+  hipError_t e = launch_tr_eval<T>(c->L, lay, K0, K1, X, Bi, ncol, y);
   if (e != hipSuccess) return e;
   c->counters.bitplanes(n, int(lay.use_a) + int(lay.use_b));
-  e = launch_tr_phase2<T>(c->L, lay, K0, K1, X, Bi, ncol, bits, bits + ww, bits + 2 * ww, bits + 3 * ww, m, m + n);
-  if (e != hipSuccess) return e;
   if (lay.kind != MPCX_DRELU) c->counters.msg(n, c->bw);  // DRELU: the output bit is already public
-  return launch_reconstruct<T>(c->L, n, m, m + n, y);
+  return hipSuccess;
 }
 
 template <typename T>
@@ -391,14 +387,9 @@ static mpcx_status tr_eval_t(mpcx_ctx *c, int kind, size_t n, const void *k0, co
     return MPCX_OK;
   }
   TrLayout lay = tr_layout(kind, c->bw, c->s, n, 0);
-  const size_t wb = ((n + 63) / 64) * 8;
-  void *sp = nullptr;
-  HIPC(c, ctx_scratch(c, 4 * wb + 2 * n * sizeof(T), &sp), "hipMalloc");
-  uint64_t *b = static_cast<uint64_t *>(sp);
-  T *m = reinterpret_cast<T *>(b + 4 * (wb / 8));
   HIPC(c,
        tr_eval_run<T>(c, lay, n, static_cast<const uint8_t *>(k0), static_cast<const uint8_t *>(k1),
-                      static_cast<const T *>(x), static_cast<const T *>(bias), ncol, static_cast<T *>(y), b, m),
+                      static_cast<const T *>(x), static_cast<const T *>(bias), ncol, static_cast<T *>(y)),
        "tr_eval");
   HIPC(c, hipStreamSynchronize(c->L.stream), "sync");
   return MPCX_OK;
@@ -493,11 +484,9 @@ static mpcx_status maxpool_eval_t(mpcx_ctx *c, int B, int N, int C, const void *
   int pairs[kMaxPoolLevels];
   const int Lv = maxpool_plan(c, B, N, C, lay, pairs);
   const size_t rows = size_t(B) * N * C, P0 = Lv ? size_t(B) * pairs[0] * C : 0;
-  const size_t ww = (P0 + 63) / 64;
   void *sp = nullptr;
-  HIPC(c, ctx_scratch(c, 4 * ww * 8 + (2 * rows + 4 * P0) * sizeof(T), &sp), "hipMalloc");
-  uint64_t *bits = static_cast<uint64_t *>(sp);
-  T *va = reinterpret_cast<T *>(bits + 4 * ww), *vb = va + rows, *d = vb + rows, *y = d + P0, *m = y + P0;
+  HIPC(c, ctx_scratch(c, (2 * rows + 2 * P0) * sizeof(T), &sp), "hipMalloc");
+  T *va = static_cast<T *>(sp), *vb = va + rows, *d = vb + rows, *y = d + P0;
   const T *cur = static_cast<const T *>(in);
   T *nxt = va;
   const uint8_t *K0 = static_cast<const uint8_t *>(k0), *K1 = static_cast<const uint8_t *>(k1);
@@ -505,7 +494,7 @@ static mpcx_status maxpool_eval_t(mpcx_ctx *c, int B, int N, int C, const void *
   for (int l = 0; l < Lv; l++) {
     const size_t n = size_t(B) * pairs[l] * C;
     HIPC(c, launch_pool_diff<T>(c->L, B, R, C, cur, d), "maxpool_eval");
-    HIPC(c, tr_eval_run<T>(c, lay[l], n, K0, K1, d, nullptr, 1, y, bits, m), "maxpool_eval");
+    HIPC(c, tr_eval_run<T>(c, lay[l], n, K0, K1, d, nullptr, 1, y), "maxpool_eval");
     HIPC(c, launch_pool_combine<T>(c->L, B, R, C, cur, y, nullptr, nxt), "maxpool_eval");
     cur = nxt;
     nxt = nxt == va ? vb : va;

@@ -64,17 +64,12 @@ hipError_t launch_tr_keygen(const Launch &L, const TrLayout &lay, uint64_t seed,
 template <typename T>
 hipError_t launch_tr_expand(const Launch &L, const TrLayout &lay, const uint8_t party_key16[16], uint32_t gate,
                             int party, uint8_t *key);
-// phase 1: DCF evaluation, writes bit messages bits_a[p], bits_b[p] (zwords(N) u32 each)
+// Evaluation of a truncation-family gate by both parties in one launch: the DCF
+// walks, the exchange of the masked DCF output bits, the output messages and
+// their sum, the revealed output yhat (N words; may alias xhat).
 template <typename T>
-hipError_t launch_tr_phase1(const Launch &L, const TrLayout &lay, const uint8_t *k0, const uint8_t *k1,
-                            const T *xhat, const T *bias, int bias_ncol, uint64_t *bits_a0, uint64_t *bits_a1,
-                            uint64_t *bits_b0, uint64_t *bits_b1);
-// phase 2: output shares after the bit exchange, writes msg0/msg1 (N each)
-template <typename T>
-hipError_t launch_tr_phase2(const Launch &L, const TrLayout &lay, const uint8_t *k0, const uint8_t *k1,
-                            const T *xhat, const T *bias, int bias_ncol, const uint64_t *bits_a0,
-                            const uint64_t *bits_a1, const uint64_t *bits_b0, const uint64_t *bits_b1, T *msg0,
-                            T *msg1);
+hipError_t launch_tr_eval(const Launch &L, const TrLayout &lay, const uint8_t *k0, const uint8_t *k1,
+                          const T *xhat, const T *bias, int bias_ncol, T *yhat);
 
 // out = m0 + m1 (reconstruction of a revealed value from both parties' messages)
 template <typename T>

@@ -266,9 +266,7 @@ struct TrArgs {
   const T *xhat;
   const T *bias;
   int bias_ncol;
-  uint64_t *ba[2], *bb[2];
-  const uint64_t *cba[2], *cbb[2];
-  T *msg[2];
+  T *out;  // revealed output (eval)
   const T *in_mask;
   T *out_mask;
   uint32_t gate;
@@ -291,27 +289,44 @@ __device__ __forceinline__ T tr_shifted_input(const TrArgs<T> &a, size_t i) {
   return low_bits<T>(x + (T(1) << a.sb), a.m);
 }
 
-// TAG = 1 marks the launches of a profiled forward (identical code, its own
-// name in kernel traces).
+// One launch evaluates a gate for both parties.  A workgroup of 2h threads
+// takes tiles of h elements: its first h threads are party 0, the last h party
+// 1, each evaluating its own keys on the same elements.  The two exchanges of
+// the protocol go through LDS: the masked DCF output bits (one ballot word per
+// wave and DCF), then the output messages, which party 0's threads add into the
+// revealed output.  TAG = 1 marks the launches of a profiled forward (identical
+// code, its own name in kernel traces).
+constexpr int kTrMaxTile = 512;  // elements per tile (workgroups of up to 1024 threads)
+
 template <typename T, int NT, int REP, int TAG>
-__global__ void k_tr_phase1(TrArgs<T> a) {
+__global__ void k_tr_eval(TrArgs<T> a) {
   __shared__ uint32_t lds[AesLds<NT, REP>::kWords];
+  __shared__ uint64_t xa[2][kTrMaxTile / 64], xb[2][kTrMaxTile / 64];
+  __shared__ T xm[2][kTrMaxTile];
   AesLds<NT, REP>::fill(lds);
   AesLds<NT, REP> aes(lds);
-  const int p = blockIdx.y;
+  const int h = int(blockDim.x) / 2;
+  const int p = int(threadIdx.x) >= h ? 1 : 0;
+  const int e = int(threadIdx.x) - p * h;  // element of the tile
+  const int wv = e >> 6;                   // wave of the party's half
   const uint8_t *K = p ? a.k1 : a.k0;
   // The correction words and leaf words of a DCF key are the same for both
   // parties (public to both); both parties read party 0's planes, so one copy
   // serves the two evaluations (and a streamed arena moves it once).
   const uint8_t *KC = a.k0;
-  const size_t stride = size_t(gridDim.x) * blockDim.x;
+  const T *G = reinterpret_cast<const T *>(K + a.off_g);
+  const T *kap = reinterpret_cast<const T *>(K + a.off_kappa);
+  const T one0 = p == 0 ? T(1) : T(0);
   const T lowmask = (T(1) << a.sb) - T(1);
   const T smask = (T(1) << a.s) - T(1);
-  for (size_t base = size_t(blockIdx.x) * blockDim.x + (threadIdx.x & ~63u); base < a.N; base += stride) {
-    const size_t i = base + lane_id();
+  const size_t stride = size_t(gridDim.x) * size_t(h);
+  for (size_t base = size_t(blockIdx.x) * h; base < a.N; base += stride) {
+    const size_t i = base + size_t(e);
+    const bool in = i < a.N;
     uint32_t ra = 0, rb = 0;
-    if (i < a.N) {
-      const T xp = tr_shifted_input(a, i);
+    T xp = 0;
+    if (in) {
+      xp = tr_shifted_input(a, i);
       if (a.use_a) {
         ra = dcf_eval_walk(aes, reinterpret_cast<const uint4 *>(K + a.a.off_root)[i], a.a.m, a.a.L,
                            reinterpret_cast<const uint4 *>(KC + a.a.off_cw) + i, a.N,
@@ -325,59 +340,47 @@ __global__ void k_tr_phase1(TrArgs<T> a) {
         rb ^= get_bit(reinterpret_cast<const uint64_t *>(K + a.b.off_z), i);
       }
     }
+    // exchange 1: the masked DCF output bits
     const uint64_t wa = __ballot(ra), wb = __ballot(rb);
     if (lane_id() == 0) {
-      if (a.use_a) a.ba[p][base >> 6] = wa;
-      if (a.use_b) a.bb[p][base >> 6] = wb;
+      xa[p][wv] = wa;
+      xb[p][wv] = wb;
     }
-  }
-}
-
-template <typename T>
-__global__ void k_tr_phase2(TrArgs<T> a) {
-  const int p = blockIdx.y;
-  const uint8_t *K = p ? a.k1 : a.k0;
-  const T *G = reinterpret_cast<const T *>(K + a.off_g);
-  const T *kap = reinterpret_cast<const T *>(K + a.off_kappa);
-  const T one0 = p == 0 ? T(1) : T(0);
-  for (size_t i = size_t(blockIdx.x) * blockDim.x + threadIdx.x; i < a.N; i += size_t(gridDim.x) * blockDim.x) {
-    const T xp = tr_shifted_input(a, i);
-    const uint32_t h = uint32_t(xp >> a.sb) & 1u;
-    const uint32_t bh = a.use_a ? (get_bit(a.cba[0], i) ^ get_bit(a.cba[1], i)) : 0u;
-    const uint32_t dh = a.use_b ? (get_bit(a.cbb[0], i) ^ get_bit(a.cbb[1], i)) : 0u;
-    const T A = (xp >> a.sh) - (T(1) << (a.m - 1 - a.sh));
-    T y;
-    if (a.kind == G_TRMOD) {  // exact modulo 2^(n-s): no wrap term
-      y = one0 * A + G[size_t(dh) * a.N + i];
-    } else if (a.kind == G_EXT) {
-      y = one0 * A + G[size_t(h * 2 + bh) * a.N + i];
-    } else if (a.kind == G_EXTRELU) {
-      const uint32_t z = h ^ bh;
-      const T k = kap[i];
-      const T cp = z ? T(one0 - k) : k;
-      y = cp * A + G[size_t(h * 2 + bh) * a.N + i];
-    } else if (a.kind == G_TR) {
-      const uint32_t c = h * 4 + bh * 2 + dh;
-      y = one0 * A + G[size_t(c) * a.N + i];
-    } else if (a.kind == G_TRRELU) {
-      const uint32_t c = h * 4 + bh * 2 + dh;
-      const uint32_t z = h ^ bh;
-      const T k = kap[i];
-      const T cp = z ? T(one0 - k) : k;
-      y = cp * A + G[size_t(c) * a.N + i];
-    } else if (a.kind == G_DRELU) {  // the public masked bit; party 0 carries it
-      y = one0 * T(h ^ bh);
-    } else if (relu_like(a.kind)) {
-      const uint32_t z = h ^ bh;
-      const T k = kap[i];
-      const T cp = z ? T(one0 - k) : k;
-      y = cp * a.xhat[i] + G[size_t(z) * a.N + i];
-    } else {  // G_TRSLACK
-      const uint32_t Hh = uint32_t(xp >> (a.n - 2)) & 3u;
-      const uint32_t c = Hh * 2 + dh;
-      y = one0 * A + G[size_t(c) * a.N + i];
+    __syncthreads();
+    if (in) {
+      const uint32_t hb = uint32_t(xp >> a.sb) & 1u;
+      const uint32_t bh = a.use_a ? uint32_t((xa[0][wv] ^ xa[1][wv]) >> lane_id()) & 1u : 0u;
+      const uint32_t dh = a.use_b ? uint32_t((xb[0][wv] ^ xb[1][wv]) >> lane_id()) & 1u : 0u;
+      const T A = (xp >> a.sh) - (T(1) << (a.m - 1 - a.sh));
+      T y;
+      if (a.kind == G_TRMOD) {  // exact modulo 2^(n-s): no wrap term
+        y = one0 * A + G[size_t(dh) * a.N + i];
+      } else if (a.kind == G_EXT) {
+        y = one0 * A + G[size_t(hb * 2 + bh) * a.N + i];
+      } else if (a.kind == G_EXTRELU || a.kind == G_TRRELU) {
+        const uint32_t z = hb ^ bh;
+        const T k = kap[i];
+        const T cp = z ? T(one0 - k) : k;
+        const size_t c = a.kind == G_EXTRELU ? hb * 2 + bh : hb * 4 + bh * 2 + dh;
+        y = cp * A + G[c * a.N + i];
+      } else if (a.kind == G_TR) {
+        y = one0 * A + G[size_t(hb * 4 + bh * 2 + dh) * a.N + i];
+      } else if (a.kind == G_DRELU) {  // the public masked bit; party 0 carries it
+        y = one0 * T(hb ^ bh);
+      } else if (relu_like(a.kind)) {
+        const uint32_t z = hb ^ bh;
+        const T k = kap[i];
+        const T cp = z ? T(one0 - k) : k;
+        y = cp * a.xhat[i] + G[size_t(z) * a.N + i];
+      } else {  // G_TRSLACK
+        const uint32_t Hh = uint32_t(xp >> (a.n - 2)) & 3u;
+        y = one0 * A + G[size_t(Hh * 2 + dh) * a.N + i];
+      }
+      xm[p][e] = y;  // exchange 2: the output messages
     }
-    a.msg[p][i] = y;
+    __syncthreads();
+    if (p == 0 && in) a.out[i] = xm[0][e] + xm[1][e];
+    __syncthreads();  // the next tile reuses the exchange buffers
   }
 }
 
@@ -526,9 +529,8 @@ hipError_t launch_tr_keygen(const Launch &L, const TrLayout &lay, uint64_t seed,
 }
 
 template <typename T>
-hipError_t launch_tr_phase1(const Launch &L, const TrLayout &lay, const uint8_t *k0, const uint8_t *k1,
-                            const T *xhat, const T *bias, int bias_ncol, uint64_t *bits_a0, uint64_t *bits_a1,
-                            uint64_t *bits_b0, uint64_t *bits_b1) {
+hipError_t launch_tr_eval(const Launch &L, const TrLayout &lay, const uint8_t *k0, const uint8_t *k1, const T *xhat,
+                          const T *bias, int bias_ncol, T *out) {
   if (lay.bw != int(8 * sizeof(T))) return hipErrorInvalidValue;
   TrArgs<T> a = tr_args<T>(lay);
   a.k0 = k0;
@@ -536,18 +538,17 @@ hipError_t launch_tr_phase1(const Launch &L, const TrLayout &lay, const uint8_t 
   a.xhat = xhat;
   a.bias = bias;
   a.bias_ncol = bias_ncol > 0 ? bias_ncol : 1;
-  a.ba[0] = bits_a0;
-  a.ba[1] = bits_a1;
-  a.bb[0] = bits_b0;
-  a.bb[1] = bits_b1;
+  a.out = out;
   return with_variant(L, [&](auto v) {
     constexpr int NT = decltype(v)::nt, REP = decltype(v)::rep;
-    int block = variant_block(L);
-    int grid = grid_for(k_tr_phase1<T, NT, REP, 0>, block, lay.N, L.num_cu);
+    const int block = variant_block(L);
+    // a workgroup holds both parties' threads for block/2 elements
+    if (block < 128 || block > 2 * kTrMaxTile || block % 128 != 0) return hipErrorInvalidConfiguration;
+    const int grid = grid_for(k_tr_eval<T, NT, REP, 0>, block, 2 * lay.N, L.num_cu);
     if (L.profiled)
-      hipLaunchKernelGGL((k_tr_phase1<T, NT, REP, 1>), dim3(grid, 2), dim3(block), 0, L.stream, a);
+      hipLaunchKernelGGL((k_tr_eval<T, NT, REP, 1>), dim3(grid), dim3(block), 0, L.stream, a);
     else
-      hipLaunchKernelGGL((k_tr_phase1<T, NT, REP, 0>), dim3(grid, 2), dim3(block), 0, L.stream, a);
+      hipLaunchKernelGGL((k_tr_eval<T, NT, REP, 0>), dim3(grid), dim3(block), 0, L.stream, a);
     return hipGetLastError();
   });
 }
@@ -605,30 +606,6 @@ hipError_t launch_tr_expand(const Launch &L, const TrLayout &lay, const uint8_t 
     hipLaunchKernelGGL((k_tr_expand<T, NT, REP>), dim3(grid), dim3(block), 0, L.stream, a, party);
     return hipGetLastError();
   });
-}
-
-template <typename T>
-hipError_t launch_tr_phase2(const Launch &L, const TrLayout &lay, const uint8_t *k0, const uint8_t *k1,
-                            const T *xhat, const T *bias, int bias_ncol, const uint64_t *bits_a0,
-                            const uint64_t *bits_a1, const uint64_t *bits_b0, const uint64_t *bits_b1, T *msg0,
-                            T *msg1) {
-  if (lay.bw != int(8 * sizeof(T))) return hipErrorInvalidValue;
-  TrArgs<T> a = tr_args<T>(lay);
-  a.k0 = k0;
-  a.k1 = k1;
-  a.xhat = xhat;
-  a.bias = bias;
-  a.bias_ncol = bias_ncol > 0 ? bias_ncol : 1;
-  a.cba[0] = bits_a0;
-  a.cba[1] = bits_a1;
-  a.cbb[0] = bits_b0;
-  a.cbb[1] = bits_b1;
-  a.msg[0] = msg0;
-  a.msg[1] = msg1;
-  const int block = 256;
-  int grid = grid_for(k_tr_phase2<T>, block, lay.N, L.num_cu);
-  hipLaunchKernelGGL((k_tr_phase2<T>), dim3(grid, 2), dim3(block), 0, L.stream, a);
-  return hipGetLastError();
 }
 
 // ---------------------------------------------------------------------------
@@ -1850,12 +1827,8 @@ hipError_t launch_rowsum(const Launch &L, size_t rows, int len, const T *a, T *o
                                           uint8_t *, uint8_t *);                                                     \
   template hipError_t launch_tr_expand<T>(const Launch &, const TrLayout &, const uint8_t *, uint32_t, int,          \
                                           uint8_t *);                                                                \
-  template hipError_t launch_tr_phase1<T>(const Launch &, const TrLayout &, const uint8_t *, const uint8_t *,        \
-                                          const T *, const T *, int, uint64_t *, uint64_t *, uint64_t *,             \
-                                          uint64_t *);                                                               \
-  template hipError_t launch_tr_phase2<T>(const Launch &, const TrLayout &, const uint8_t *, const uint8_t *,        \
-                                          const T *, const T *, int, const uint64_t *, const uint64_t *,             \
-                                          const uint64_t *, const uint64_t *, T *, T *);                             \
+  template hipError_t launch_tr_eval<T>(const Launch &, const TrLayout &, const uint8_t *, const uint8_t *,          \
+                                        const T *, const T *, int, T *);                                             \
   template hipError_t launch_reconstruct<T>(const Launch &, size_t, const T *, const T *, T *);                      \
   template hipError_t launch_local_ars<T>(const Launch &, size_t, int, const T *, const T *, int, T *);              \
   template hipError_t launch_reveal_keygen<T>(const Launch &, const RevealLayout &, uint64_t, uint32_t, T *,         \

@@ -54,7 +54,7 @@ struct Counters {
   }
 };
 
-// Per-kernel timing of the DCF-evaluation (phase-1) launches, HIP events on the
+// Per-kernel timing of the DCF gate launches (k_tr_eval), HIP events on the
 // launch stream.
 struct Phase1Timer {
   bool on = false;

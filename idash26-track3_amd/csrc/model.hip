@@ -121,23 +121,19 @@ struct KeySource {
   virtual ~KeySource() = default;
 };
 
-// Exchange buffers shared by the gates: both parties' messages and the four
-// packed bit planes of the DCF outputs.
+// Exchange buffers shared by the gates: both parties' messages (the
+// truncation-family gates exchange through LDS inside their one launch).
 template <typename T>
 struct Workspace {
   DevBuf<T> m0, m1;
-  DevBuf<uint64_t> bits;
-  size_t cap = 0, wpp = 0;
+  size_t cap = 0;
   hipError_t ensure(size_t n) {
     if (n <= cap) return hipSuccess;
     TRY(m0.alloc(n));
     TRY(m1.alloc(n));
-    wpp = (n + 63) / 64;
-    TRY(bits.alloc(4 * wpp));
     cap = n;
     return hipSuccess;
   }
-  uint64_t *plane(int k) { return bits.p + size_t(k) * wpp; }
 };
 
 // ---------------------------------------------------------------------------
@@ -194,27 +190,26 @@ struct Runner {
       TRY(hipEventRecord(e0, L.stream));
       L1.profiled = true;
     }
-    TRY(launch_tr_phase1<T>(L1, lay, kv.k[0], kv.k[1], x, bias, ncol, ws.plane(0), ws.plane(1), ws.plane(2),
-                            ws.plane(3)));
+    TRY(launch_tr_eval<T>(L1, lay, kv.k[0], kv.k[1], x, bias, ncol, out));
     if (timer && timer->on) {
       TRY(hipEventRecord(e1, L.stream));
       timer->ev.push_back(e0);
       timer->ev.push_back(e1);
       timer->elems.push_back(n);
       timer->levels.push_back((lay.use_a ? lay.a.L + 1 : 0) + (lay.use_b ? lay.b.L + 1 : 0));
-      // per element and party: the masked input, and for every DCF the root,
-      // correction words and leaf (16 B each), the output-mask bit read and the
-      // message bit written (the bias vector is ncol words, cache resident)
-      double per = double(sizeof(T));
-      if (lay.use_a) per += 16.0 * (lay.a.L + 2) + 0.125 + 0.125;
-      if (lay.use_b) per += 16.0 * (lay.b.L + 2) + 0.125 + 0.125;
+      // per element and party: the masked input, for every DCF the root,
+      // correction words and leaf (16 B each) and the output-mask bit, the G
+      // word of the element's case and kappa; half of the revealed output
+      // written (the bias vector is ncol words, cache resident; the exchanges
+      // stay in LDS)
+      double per = double(sizeof(T)) * (lay.ncase > 0 ? 2.5 : 1.5);
+      if (lay.relu) per += double(sizeof(T));
+      if (lay.use_a) per += 16.0 * (lay.a.L + 2) + 0.125;
+      if (lay.use_b) per += 16.0 * (lay.b.L + 2) + 0.125;
       timer->bytes.push_back(2.0 * per * double(n));
     }
     ctr.bitplanes(n, int(lay.use_a) + int(lay.use_b));
-    TRY(launch_tr_phase2<T>(L, lay, kv.k[0], kv.k[1], x, bias, ncol, ws.plane(0), ws.plane(1), ws.plane(2),
-                            ws.plane(3), ws.m0.p, ws.m1.p));
-    ctr.msg(n, bw);
-    TRY(launch_reconstruct<T>(L, n, ws.m0.p, ws.m1.p, out));
+    if (kind != G_DRELU) ctr.msg(n, bw);  // DRELU: the output bit is already public
     leave(end);
     return hipSuccess;
   }
@@ -734,7 +729,7 @@ class Model final : public ModelBase, KeySource {
     drop_graph();
     TRY(ensure_arena(B));
     TRY(ensure_work(B));
-    const int N = d_.n_nodes, bw = bw_;
+    const int N = d_.n_nodes;
     const size_t BN = size_t(B) * N, BNN = BN * N;
     const size_t E = emax(B);
     DevBuf<T> rX, t1, t2, rA, rN, rm, gt;

@@ -374,13 +374,14 @@ mpcx_status mpcx_model_set_inputs(mpcx_model *m, int B, const void *h_x0, const 
 mpcx_status mpcx_model_forward(mpcx_model *m, int B);
 /* Reconstructed outputs (B int64 at scale s); synchronizes the stream. */
 mpcx_status mpcx_model_output(mpcx_model *m, int B, int64_t *h_out);
-/* DCF (phase-1) kernel timing with HIP events on the launch streams.  While
+/* DCF gate kernel (k_tr_eval) timing with HIP events on the launch streams.  While
  * enabled, forwards run their lanes one after another (each launch is timed
- * alone) and launch the separately named k_tr_phase1<..., 1> instantiation. */
+ * alone) and launch the separately named k_tr_eval<..., 1> instantiation. */
 mpcx_status mpcx_model_profile(mpcx_model *m, int enable);
-/* After a synchronized forward: number of phase-1 launches, their summed time
+/* After a synchronized forward: number of DCF gate launches, their summed time
  * (ms), elements (both parties), AES calls (both parties) and algorithmic HBM
- * bytes (keys and inputs read, message bits written; both parties). */
+ * bytes (keys, inputs, G words and kappa read, the revealed output written; both
+ * parties). */
 mpcx_status mpcx_model_profile_read(mpcx_model *m, int *launches, double *ms, double *elements,
                                     double *aes_calls, double *hbm_bytes);
 /* After a synchronized profiled forward: ring-GEMM sections (one per public-
