@@ -487,7 +487,11 @@ def run_relu(args):
     evals = 2.0 * n * args.steps
     aes_s = evals * aes_per_elem / elapsed
     tops = aes_s * VALU_OPS_PER_AES.get(ctx.aes_variant_name(), float("nan")) / 1e12
-    key_gbs = 2.0 * key_bytes * args.steps / elapsed / 1e9
+    # algorithmic HBM bytes per element (both parties): the correction words and
+    # leaf once (both parties' threads read party 0's copy), each party's root,
+    # mask bit, kappa and G word, the masked input and the revealed output
+    per_elem = 16.0 * aes_per_elem + 2.0 * (16.0 + 0.125 + 4.0 + 4.0) + 4.0 + 4.0
+    key_gbs = per_elem * n * args.steps / elapsed / 1e9
     result = {
         "metric": "DCF evals/s (secure ReLU, Z_2^32, both parties' evaluations, 1 GPU)",
         "value": round(evals / elapsed, 1),
@@ -502,7 +506,7 @@ def run_relu(args):
         "roofline": {"kernel": "RELU gate call (k_tr_eval)", "bound": "valu",
                      "achieved": round(tops, 3), "peak": round(VALU_PEAK_TOPS, 2), "unit": "TOP/s",
                      "frac": round(tops / VALU_PEAK_TOPS, 4)},
-        "roofline_hbm": {"kernel": "key stream", "bound": "hbm", "achieved": round(key_gbs, 1),
+        "roofline_hbm": {"kernel": "k_tr_eval key stream and inputs", "bound": "hbm", "achieved": round(key_gbs, 1),
                          "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(key_gbs / HBM_PEAK_GBS, 4)},
         "bit_exact": exact,
     }

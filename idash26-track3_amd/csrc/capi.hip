@@ -247,8 +247,9 @@ int mpcx_aes_variant(const mpcx_ctx *c) { return c ? c->L.aes_variant : -1; }
 mpcx_status mpcx_set_aes_variant(mpcx_ctx *c, int variant, int block) {
   CHECK_CTX(c);
   if (variant < 0 || variant >= mpcx_aes_variant_count()) return fail(c, MPCX_EINVAL, "bad AES variant");
-  if (block != 0 && (block < 64 || block > 1024 || (block % 64) != 0))
-    return fail(c, MPCX_EINVAL, "block must be a multiple of 64 in [64, 1024]");
+  // the gate kernel splits a workgroup into two parties' halves of whole waves
+  if (block != 0 && (block < 128 || block > 1024 || (block % 128) != 0))
+    return fail(c, MPCX_EINVAL, "block must be a multiple of 128 in [128, 1024]");
   c->L.aes_variant = variant;
   c->L.aes_block = block;
   return MPCX_OK;

@@ -197,16 +197,16 @@ struct Runner {
       timer->ev.push_back(e1);
       timer->elems.push_back(n);
       timer->levels.push_back((lay.use_a ? lay.a.L + 1 : 0) + (lay.use_b ? lay.b.L + 1 : 0));
-      // per element and party: the masked input, for every DCF the root,
-      // correction words and leaf (16 B each) and the output-mask bit, the G
-      // word of the element's case and kappa; half of the revealed output
-      // written (the bias vector is ncol words, cache resident; the exchanges
-      // stay in LDS)
-      double per = double(sizeof(T)) * (lay.ncase > 0 ? 2.5 : 1.5);
-      if (lay.relu) per += double(sizeof(T));
-      if (lay.use_a) per += 16.0 * (lay.a.L + 2) + 0.125;
-      if (lay.use_b) per += 16.0 * (lay.b.L + 2) + 0.125;
-      timer->bytes.push_back(2.0 * per * double(n));
+      // per element: the masked input and the revealed output once; per DCF
+      // the correction words and the leaf once (both parties' threads of a
+      // workgroup read party 0's copy) and each party's root (16 B) and mask
+      // bit; each party's G word of the element's case and kappa (the bias
+      // vector is ncol words, cache resident; the exchanges stay in LDS)
+      const double tb = double(sizeof(T));
+      double per = 2.0 * tb + (lay.ncase > 0 ? 2.0 * tb : 0.0) + (lay.relu ? 2.0 * tb : 0.0);
+      if (lay.use_a) per += 16.0 * (lay.a.L + 1) + 2.0 * (16.0 + 0.125);
+      if (lay.use_b) per += 16.0 * (lay.b.L + 1) + 2.0 * (16.0 + 0.125);
+      timer->bytes.push_back(per * double(n));
     }
     ctr.bitplanes(n, int(lay.use_a) + int(lay.use_b));
     if (kind != G_DRELU) ctr.msg(n, bw);  // DRELU: the output bit is already public

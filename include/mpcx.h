@@ -83,7 +83,8 @@ int mpcx_scale(const mpcx_ctx *ctx);
 mpcx_status mpcx_set_stream(mpcx_ctx *ctx, void *hip_stream);
 mpcx_status mpcx_synchronize(mpcx_ctx *ctx);
 /* AES T-table LDS layout used by the DCF kernels (0 = default).  Returns the
- * number of variants; name of variant i via mpcx_aes_variant_name. */
+ * number of variants; name of variant i via mpcx_aes_variant_name.
+ * block_threads: 0 (the variant's own) or a multiple of 128 in [128, 1024]. */
 int mpcx_aes_variant_count(void);
 const char *mpcx_aes_variant_name(int i);
 mpcx_status mpcx_set_aes_variant(mpcx_ctx *ctx, int variant, int block_threads);
