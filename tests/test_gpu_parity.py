@@ -259,6 +259,16 @@ def test_all_aes_variants_agree(mp, orc):
         c.set_aes_variant(v)
         y = c.tr_eval(2, k0, k1, xhat, bias)
         assert np.array_equal(signed(y.astype(np.uint64) - orout, 32), want), v
+    # explicit workgroup sizes: the gate kernel splits a workgroup into the two
+    # parties' halves of whole waves (tiles of block/2 elements, the last one
+    # partial here); other sizes are refused when set
+    for block in (128, 256, 384, 1024):
+        c.set_aes_variant(0, block)
+        y = c.tr_eval(2, k0, k1, xhat, bias)
+        assert np.array_equal(signed(y.astype(np.uint64) - orout, 32), want), block
+    for block in (64, 192, 2048):
+        assert c.lib.mpcx_set_aes_variant(c.h, 0, block) != 0
+    c.set_aes_variant(0)
     c.close()
 
 
