@@ -173,6 +173,27 @@ def test_split_truncation_keys_and_eval(ctx, orc, relu):
     assert np.array_equal(signed(y2.astype(np.uint64) - or2, bw), _tr_expected(2 if relu else 1, x, bias))
 
 
+@pytest.mark.parametrize("n", [1, 63, 64, 65, 255, 256, 257, 511, 513, 1023, 1025])
+def test_gate_tile_edges(ctx, mp, orc, n):
+    """One gate launch takes tiles of (workgroup / 2) elements, both parties' threads
+    per tile: element counts around the wave and tile sizes give the oracle's
+    outputs (EXTRELU after TRMOD, so both DCF widths and both exchanges run)."""
+    bw = ctx.bw
+    rng = np.random.default_rng(n + bw)
+    h = 1 << (bw - 1)
+    x = rng.integers(-(h // 2), h // 2, size=n, dtype=np.int64)
+    rin = rmask(rng, n, bw)
+    o0, o1, r1 = orc.tr_keygen(3, 40, 12, bw, S, rin)
+    p0, p1, r2 = orc.tr_keygen(3, 41, 14, bw, S, r1)
+    xhat = (x.astype(np.uint64) + rin) & M(bw)
+    y1 = ctx.tr_eval(12, mp.to_dev(o0), mp.to_dev(o1), xhat)
+    y2 = ctx.tr_eval(14, mp.to_dev(p0), mp.to_dev(p1), y1)
+    oy1, _ = orc.tr_eval(12, bw, S, o0, o1, xhat)
+    oy2, _ = orc.tr_eval(14, bw, S, p0, p1, oy1)
+    assert np.array_equal(y1.astype(np.uint64), oy1) and np.array_equal(y2.astype(np.uint64), oy2)
+    assert np.array_equal(signed(y2.astype(np.uint64) - r2, bw), np.maximum(x >> S, 0))
+
+
 def test_local_ars_matches_oracle(ctx, orc):
     """LocalARS (TruncateType::LocalARS, ddg_orca_batched.h:180-199): no key and no
     exchange; output mask and outputs identical to the oracle's, whose closed form
