@@ -437,14 +437,19 @@ def _od(orc, dims):
                          slack=dims.slack)
 
 
-@pytest.mark.parametrize("bw,slack", [(32, 0), (64, 0), (32, 1), (64, 1), (32, 2), (64, 2)])
-def test_model_keys_and_forward(mp, orc, synth, bw, slack):
+@pytest.mark.parametrize("bw,slack,ms", [(32, 0, 0), (64, 0, 0), (32, 1, 0), (64, 1, 0), (32, 2, 0), (64, 2, 0),
+                                         (32, 0, 12), (32, 0, 25), (64, 0, 55)])
+def test_model_keys_and_forward(mp, orc, synth, bw, slack, ms):
     """GPU dealer keys byte-identical to the oracle's, forward bit-exact, same
-    exchange bytes; exact, and with the slack truncations of the GCN."""
+    exchange bytes; exact, and with the slack truncations of the GCN.  Atom masks
+    at scale ms: 12 (the reference's share files) keeps the max-pool's narrow
+    sentinel and RELUPOOL gates, 25 (bw=32) and 55 (bw=64) exceed bw-s-1 and take
+    the reference's sentinel with full RELU gates."""
     B = 2
-    wl = synth.workload(B, synth.Dims(bw=bw, slack=slack), seed=21)
+    wl = synth.workload(B, synth.Dims(bw=bw, slack=slack, mask_scale=ms), seed=21)
     d = _od(orc, wl.dims)
-    want, code = orc.plain_forward(d, wl.X, wl.A, wl.mask, wl.prot, wl.W)
+    mask = wl.mask << ms
+    want, code = orc.plain_forward(d, wl.X, wl.A, mask, wl.prot, wl.W)
     assert code == 0
     c = mp.Ctx(bw=bw)
     m = mp.Model(c, wl.dims, wl.W)
@@ -455,7 +460,7 @@ def test_model_keys_and_forward(mp, orc, synth, bw, slack):
     assert np.array_equal(m.export_keys(1, B), o1)
     x0, x1 = wl.shares["x"]
     a0, a1 = wl.shares["a"]
-    m0, m1 = wl.shares["m"]
+    m0, m1 = synth.share(mask, bw, 5) if ms else wl.shares["m"]
     m.set_inputs(B, x0, x1, a0, a1, m0, m1, wl.prot)
     c.reset_counters()
     m.forward(B)

@@ -227,6 +227,29 @@ def test_two_party_matches_plaintext(orc, synth, bw, slack):
     assert by > 0
 
 
+@pytest.mark.parametrize("bw,ms", [(32, 12), (32, 19), (32, 20), (32, 25), (64, 51), (64, 55)])
+def test_two_party_mask_scales(orc, synth, bw, ms):
+    """Atom masks 0 / 2^ms: up to ms = bw-s-1 the max-pool takes the narrow
+    sentinel -2^(bw-s-1) and RELUPOOL gates, above it the reference's sentinel
+    -2^(bw-2) and RELU gates (a larger key); both reconstruct the plaintext forward,
+    whose own sentinel is always -2^(bw-2)."""
+    dims = synth.Dims(bw=bw, n_nodes=140, mask_scale=ms)
+    wl = synth.workload(2, dims, seed=12)
+    d = _od(orc, wl)
+    mask = wl.mask << ms
+    out, code = orc.plain_forward(d, wl.X, wl.A, mask, wl.prot, wl.W)
+    assert code == 0
+    k0, k1 = orc.model_keygen(d, 2, 99, wl.W)
+    x0, x1 = wl.shares["x"]
+    a0, a1 = wl.shares["a"]
+    m0, m1 = synth.share(mask, bw, 5)
+    o2, _ = orc.model_eval(d, 2, wl.W, k0, k1, x0, x1, a0, a1, m0, m1, wl.prot)
+    assert np.array_equal(o2, out)
+    narrow = ms <= bw - 12 - 1
+    d0 = _od(orc, synth.workload(2, synth.Dims(bw=bw, n_nodes=140, mask_scale=0), seed=12))
+    assert (k0.size == orc.model_key_bytes(d0, 2)) == narrow
+
+
 @pytest.mark.parametrize("bw", [32, 64])
 def test_adjnorm_two_party_matches_closed_form(orc, synth, bw):
     """Standalone secure adjacency normalisation (the config-2 pipeline) on
