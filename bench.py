@@ -59,6 +59,8 @@ def main():
     ap.add_argument("--cpu-seconds", type=float, default=10.0, help="minimum timed CPU baseline work")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--aes-variant", type=int, default=-1)
+    ap.add_argument("--aes-block", type=int, default=0,
+                    help="threads per DCF workgroup (0: the variant's own; a multiple of 128 up to 1024)")
     ap.add_argument("--lanes", type=int, default=3, help="concurrent sub-batches, each on its own stream")
     ap.add_argument("--slack", type=int, default=0, choices=(0, 1, 2, 3),
                     help="slack truncations of the GCN (exact while the values lie in half the signed ring): "
@@ -113,7 +115,7 @@ def main():
 
     ctx = mpcx.Ctx(bw=args.bw, scale=dims.s)
     if args.aes_variant >= 0:
-        ctx.set_aes_variant(args.aes_variant)
+        ctx.set_aes_variant(args.aes_variant, args.aes_block)
     model = mpcx.Model(ctx, dims, wl.W, lanes=args.lanes)
     key_bytes = model.key_bytes(B)
     t0 = time.time()
@@ -461,7 +463,7 @@ def run_relu(args):
     rin = rng.integers(0, 1 << 32, size=n, dtype=np.uint64)
     ctx = mpcx.Ctx(bw=bw, scale=s)
     if args.aes_variant >= 0:
-        ctx.set_aes_variant(args.aes_variant)
+        ctx.set_aes_variant(args.aes_variant, args.aes_block)
     k0, k1, rout = ctx.tr_keygen(mpcx.RELU, rin, seed=0xACE + args.seed, gate=1)
     key_bytes = int(ctx.lib.mpcx_tr_key_bytes(ctx.h, mpcx.RELU, n))
     dx = mpcx.to_dev(((x.astype(np.uint64) + rin) & 0xFFFFFFFF).astype(np.uint32))
@@ -554,7 +556,7 @@ def run_adjnorm(args):
     a0, a1 = synth.share(A, bw, args.seed + 3)
     ctx = mpcx.Ctx(bw=bw)
     if args.aes_variant >= 0:
-        ctx.set_aes_variant(args.aes_variant)
+        ctx.set_aes_variant(args.aes_variant, args.aes_block)
     ctx.set_adjnorm_lanes(args.lanes)  # concurrent graph groups, each on its own stream
     k0, k1, mask = ctx.adjnorm_keygen(B, N, seed=0xADD + args.seed)
     d0, d1 = mpcx.to_dev(ctx.ring(a0)), mpcx.to_dev(ctx.ring(a1))
