@@ -8,8 +8,10 @@ molecules (inputs and keys resident in HBM; keygen is the offline dealer and
 is not timed).  Prints one JSON line.
 """
 import argparse
+import hashlib
 import json
 import os
+import platform
 import sys
 import time
 
@@ -30,13 +32,17 @@ GEMM_PEAK_TMACS = {"mfma32": 5.0e3 / 2 / 16, "mfma64": 5.0e3 / 2 / 64, "valu": V
 # cipher, sigma, feed-forward and the level update), counted in the gfx950 ISA
 # of this build: hipcc --cuda-device-only -S csrc/kernels.hip, level-loop block
 # of k_tr_eval<uint32_t, NT, REP> for each LDS table variant.
-# HBM bytes per k_tr_eval launch measured with rocprofv3 --pmc FETCH_SIZE and
-# WRITE_SIZE on this bench command (mean over the profiled forward's launches,
-# 19 per lane), each scaled by the same counter's reading for a 1 GiB elementwise
-# copy (FETCH_SIZE x 2.0, WRITE_SIZE x 1.0); keyed by (variant, B, bw, lanes, slack).
-# The summary is profiles/k_tr_eval_affinity_bw32_B64.md.
-TRAFFIC_BYTES_PER_LAUNCH = {("perm64_b512", 64, 32, 3, 0): 229638822,
-                            ("perm64_b512", 64, 32, 1, 0): 689753000}
+# HBM bytes per k_tr_eval launch, measured with rocprofv3 --pmc FETCH_SIZE and
+# WRITE_SIZE (one run each) on this bench command, mean over the launches of the
+# forward, each counter scaled by its reading on a plain 1 GiB copy
+# (bench.py --workload copy: FETCH_SIZE x 2.0, WRITE_SIZE x 1.0).  A measurement
+# holds only for the kernel sources it was taken on: it is keyed by the digest of
+# those sources (kernel_digest()) and the workload, and the line reports null
+# when the current sources or workload have no measurement.  Each entry names
+# the profile summary under profiles/ that it comes from.
+TRAFFIC_MEASURED = {
+}
+KERNEL_SOURCES = ("csrc/kernels.hip", "csrc/kernels.h", "csrc/dcf_dev.h", "csrc/aes_dev.h", "csrc/mpcx_core.h")
 SLACK_DESC = {1: ", GCN products H.W^T truncated with the slack gate",
               2: ", GCN products and aggregations truncated with the slack gate",
               3: ", every layer truncation local (LocalARS, the reference's default truncation; not bit-exact)"}
@@ -45,6 +51,40 @@ VALU_OPS_PER_AES = {"perm64_b512": 402, "perm64_b1024": 402, "t4_rep32_b1024": 4
 
 def log(msg):
     print(msg, file=sys.stderr, flush=True)
+
+
+def kernel_digest():
+    """First 12 hex digits of the SHA-256 of the DCF kernel's sources."""
+    h = hashlib.sha256()
+    for rel in KERNEL_SOURCES:
+        with open(os.path.join(ROOT, "idash26-track3_amd", rel), "rb") as f:
+            h.update(f.read())
+    return h.hexdigest()[:12]
+
+
+def host_cpu():
+    """The host CPU the baseline runs on: model name and logical CPUs visible."""
+    model = platform.processor() or "unknown"
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    model = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    try:
+        avail = len(os.sched_getaffinity(0))
+    except AttributeError:
+        avail = os.cpu_count()
+    return {"cpu_model": model, "nproc": avail, "cpu_count": os.cpu_count()}
+
+
+def cpu_fields(orc):
+    """cores and host description of a CPU-baseline object."""
+    d = {"cores": orc.get_threads()}
+    d.update(host_cpu())
+    return d
 
 
 def main():
@@ -147,15 +187,23 @@ def main():
     prof = model.profile_read()
     model.profile(False)
     dcf_ms = prof["ms"]
-    dcf_evals_per_s = prof["elements"] / (dcf_ms / 1e3) if dcf_ms > 0 else 0.0
-    aes_per_s = prof["aes_calls"] / (dcf_ms / 1e3) if dcf_ms > 0 else 0.0
     variant = ctx.aes_variant_name()
-    key_gbs = prof["hbm_bytes"] / (dcf_ms / 1e3) / 1e9 if dcf_ms > 0 else 0.0
-    achieved_tops = aes_per_s * VALU_OPS_PER_AES.get(variant, float("nan")) / 1e12
-    step_tops = prof["aes_calls"] * VALU_OPS_PER_AES.get(variant, float("nan")) / (ms_per_step / 1e3) / 1e12
+    # rates over the timed step (the work of one forward, whatever overlaps it)
+    step_s = ms_per_step / 1e3
+    dcf_evals_per_s = prof["elements"] / step_s
+    aes_per_s = prof["aes_calls"] / step_s
+    key_gbs = prof["hbm_bytes"] / step_s / 1e9
+    step_tops = aes_per_s * VALU_OPS_PER_AES.get(variant, float("nan")) / 1e12
+    # rate of the launches alone (profiled forward, lanes one after another)
+    launch_aes_per_s = prof["aes_calls"] / (dcf_ms / 1e3) if dcf_ms > 0 else 0.0
+    achieved_tops = launch_aes_per_s * VALU_OPS_PER_AES.get(variant, float("nan")) / 1e12
     gemm_path = "valu" if os.environ.get("MPCX_GEMM") == "valu" else f"mfma{args.bw}"
     gemm_tmacs = prof["gemm_macs"] / (prof["gemm_ms"] / 1e3) / 1e12 if prof["gemm_ms"] > 0 else 0.0
-    log(f"[bench] DCF gate launches: {prof['launches']} launches, {dcf_ms:.2f} ms/forward, "
+    digest = kernel_digest()
+    tm = TRAFFIC_MEASURED.get((digest, variant, B, args.bw, args.lanes, args.slack))
+    traffic = tm["bytes_per_launch"] if tm else None
+    traffic_src = tm["profile"] if tm else f"no PMC measurement for kernel sources {digest} and this workload"
+    log(f"[bench] DCF gate launches: {prof['launches']} per forward ({dcf_ms:.2f} ms alone); over the step "
         f"{dcf_evals_per_s / 1e9:.3f} G evals/s, {aes_per_s / 1e9:.2f} G AES/s")
 
     result = {
@@ -179,33 +227,44 @@ def main():
                    "slack": args.slack},
         "dcf_evals_per_s": round(dcf_evals_per_s, 1),
         "aes_blocks_per_s": round(aes_per_s, 1),
-        "dcf_ms_per_step": round(dcf_ms, 3),
         "bytes_exchanged_per_sample": round(bytes_per_fwd / B, 1),
         "rounds_per_step": rounds_per_fwd,
         "key_bytes_per_sample_per_party": round(key_bytes / B, 1),
+        # The DCF gate kernel's VALU work of every launch of a timed step over
+        # the timed step itself: the lanes' launches overlap each other and the
+        # GEMM and exchange kernels, so this is the kernel's rate as the timed
+        # configuration runs it (a lower bound on its rate while it runs).
         "roofline": {
-            "kernel": f"k_tr_eval (DCF gate evaluation of both parties, AES-128 T-tables in LDS, {variant}; "
-                      f"the profiled forward's launches, lanes one after another, traced as k_tr_eval<..., 1>)",
-            "launches": prof["launches"],
-            "avg_launch_us": round(1e3 * dcf_ms / max(prof["launches"], 1), 2),
-            "bound": "valu",
-            "achieved": round(achieved_tops, 3),
-            "peak": round(VALU_PEAK_TOPS, 2),
-            "unit": "TOP/s",
-            "frac": round(achieved_tops / VALU_PEAK_TOPS, 4),
-            "traffic": TRAFFIC_BYTES_PER_LAUNCH.get((variant, B, args.bw, args.lanes, args.slack)),
-            "traffic_unit": "bytes per launch (mean over the forward's launches)",
-            "algorithmic_bytes_per_launch": round(prof["hbm_bytes"] / max(prof["launches"], 1)),
-        },
-        # the same DCF VALU work over the whole timed step (lanes overlapping):
-        # a lower bound on the kernel's rate while it shares the GPU
-        "roofline_step": {
-            "kernel": "k_tr_eval, all launches of a step",
+            "kernel": f"k_tr_eval (DCF gate evaluation of both parties, AES-128 T-tables in LDS, {variant}): "
+                      f"VALU work of all {prof['launches']} launches of a step over the timed step",
             "bound": "valu",
             "achieved": round(step_tops, 3),
             "peak": round(VALU_PEAK_TOPS, 2),
             "unit": "TOP/s",
             "frac": round(step_tops / VALU_PEAK_TOPS, 4),
+            "traffic": traffic,
+            "traffic_unit": "HBM bytes per launch (FETCH_SIZE + WRITE_SIZE, mean over a forward's launches)",
+            "traffic_source": traffic_src,
+            "algorithmic_bytes_per_launch": round(prof["hbm_bytes"] / max(prof["launches"], 1)),
+            "launches_per_step": prof["launches"],
+            "aes_calls_per_step": prof["aes_calls"],
+            "valu_ops_per_aes": VALU_OPS_PER_AES.get(variant),
+            "kernel_digest": digest,
+        },
+        # The same launches timed one by one (HIP events on the launch streams)
+        # in a profiled forward whose lanes run one after another: the kernel's
+        # rate alone, per launch.  rocprofv3 --kernel-trace lists these launches
+        # under their own instantiation k_tr_eval<..., 1>.
+        "roofline_launch": {
+            "kernel": "k_tr_eval, profiled forward (lanes one after another, every launch timed alone)",
+            "launches": prof["launches"],
+            "avg_launch_us": round(1e3 * dcf_ms / max(prof["launches"], 1), 2),
+            "ms_per_forward": round(dcf_ms, 3),
+            "bound": "valu",
+            "achieved": round(achieved_tops, 3),
+            "peak": round(VALU_PEAK_TOPS, 2),
+            "unit": "TOP/s",
+            "frac": round(achieved_tops / VALU_PEAK_TOPS, 4),
         },
         "roofline_gemm": {
             "kernel": f"ring GEMMs ({gemm_path}: public-weight products and SxS Beaver products, "
@@ -219,7 +278,7 @@ def main():
             "ring_macs_per_step": prof["gemm_macs"],
         },
         "roofline_hbm": {
-            "kernel": "k_tr_eval key stream",
+            "kernel": "k_tr_eval key stream (algorithmic bytes of a forward over the timed step)",
             "bound": "hbm",
             "achieved": round(key_gbs, 1),
             "peak": HBM_PEAK_GBS,
@@ -257,7 +316,7 @@ def main():
             result["cpu_baseline"] = {
                 "value": round(nb * reps / ct, 3),
                 "unit": "samples/s",
-                "cores": orc.get_threads(),
+                **cpu_fields(orc),
                 "kind": "port",
                 "sample": f"{reps} x {nb} molecules of the same workload: two-party online eval (both parties, "
                           f"same gates and key format) in oracle/ C with AES-NI + OpenMP, {ct:.1f}s",
@@ -528,7 +587,7 @@ def run_relu(args):
             gc = (np.asarray(yc, np.int64) - np.asarray(orout, np.int64)) & 0xFFFFFFFF
             gc = np.where(gc >= 1 << 31, gc - (1 << 32), gc)
             result["cpu_baseline"] = {
-                "value": round(2.0 * m * reps / ct, 1), "unit": "DCF evals/s", "cores": orc.get_threads(),
+                "value": round(2.0 * m * reps / ct, 1), "unit": "DCF evals/s", **cpu_fields(orc),
                 "kind": "port",
                 "sample": f"{reps} x {m} elements of the same workload, both parties, oracle/ C with AES-NI + "
                           f"OpenMP, {ct:.1f}s",
@@ -622,7 +681,7 @@ def run_adjnorm(args):
                 reps += 1
             gc = (np.asarray(oc, np.uint64) - np.asarray(omask, np.uint64)) & 0xFFFFFFFF
             result["cpu_baseline"] = {
-                "value": round(Bs * reps / ct, 2), "unit": "graphs/s", "cores": orc.get_threads(), "kind": "port",
+                "value": round(Bs * reps / ct, 2), "unit": "graphs/s", **cpu_fields(orc), "kind": "port",
                 "sample": f"{reps} x {Bs} graphs of the same workload, both parties, oracle/ C with AES-NI + "
                           f"OpenMP, {ct:.1f}s",
                 "bit_exact": bool(np.array_equal(gc.astype(np.int64), orc.adj_norm_plain(A[:Bs]).reshape(-1))),

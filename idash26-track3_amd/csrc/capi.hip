@@ -2,6 +2,7 @@
 #include <hip/hip_runtime.h>
 
 #include <cstdio>
+#include <cstdlib>
 #include <cstring>
 #include <new>
 #include <string>
@@ -125,8 +126,8 @@ struct mpcx_ctx {
   // Device workspace of the standalone gate evaluations, grown on demand and
   // kept until the context is destroyed (every such call synchronizes its
   // stream before returning, so the next call may reuse it).
-  void *scratch = nullptr;
-  size_t scratch_bytes = 0;
+  void *work = nullptr;
+  size_t work_bytes = 0;
   AdjNormCache *adj = nullptr;  // prepared state of mpcx_adjnorm_eval
   int adj_lanes = 1;            // concurrent graph groups of the adjacency normalisation
 };
@@ -197,8 +198,21 @@ mpcx_status mpcx_create(int bw, int scale, int device, mpcx_ctx **out) {
     return MPCX_EHIP;
   }
   c->L.stream = c->own;
-  if (const char *v = std::getenv("MPCX_AES_VARIANT")) c->L.aes_variant = std::atoi(v);
-  if (const char *v = std::getenv("MPCX_AES_BLOCK")) c->L.aes_block = std::atoi(v);
+  // The environment overrides take the same checks as mpcx_set_aes_variant: a
+  // bad value is ignored with a warning (a block that is not a whole number of
+  // wave pairs would misplace the DCF kernels' ballot words).
+  {
+    int variant = 0, block = 0;
+    if (const char *v = std::getenv("MPCX_AES_VARIANT")) variant = std::atoi(v);
+    if (const char *v = std::getenv("MPCX_AES_BLOCK")) block = std::atoi(v);
+    if (mpcx_set_aes_variant(c, variant, block) != MPCX_OK) {
+      std::fprintf(stderr, "libmpcx: ignoring MPCX_AES_VARIANT=%d / MPCX_AES_BLOCK=%d: %s\n", variant, block,
+                   c->err.c_str());
+      c->err.clear();
+      c->L.aes_variant = 0;
+      c->L.aes_block = 0;
+    }
+  }
   if (const char *v = std::getenv("MPCX_GEMM")) c->L.gemm = std::strcmp(v, "valu") == 0 ? 1 : 0;
   if (const char *v = std::getenv("MPCX_GRAPH")) c->L.graph = std::atoi(v) != 0 ? 1 : 0;
   *out = c;
@@ -211,7 +225,7 @@ void mpcx_destroy(mpcx_ctx *c) {
     (void)hipStreamSynchronize(c->own);
     (void)hipStreamDestroy(c->own);
   }
-  if (c->scratch) (void)hipFree(c->scratch);
+  if (c->work) (void)hipFree(c->work);
   adjnorm_cache_free(c->adj);
   delete c;
 }
@@ -305,20 +319,20 @@ mpcx_status mpcx_dcf_eval(mpcx_ctx *c, int party, int bin, size_t n, const void 
 
 // ---------------- workspace for standalone gate evaluation ----------------
 namespace {
-hipError_t ctx_scratch(mpcx_ctx *c, size_t bytes, void **p) {
-  if (bytes > c->scratch_bytes) {
-    if (c->scratch) {
+hipError_t ctx_work(mpcx_ctx *c, size_t bytes, void **p) {
+  if (bytes > c->work_bytes) {
+    if (c->work) {
       hipError_t e = hipDeviceSynchronize();
       if (e != hipSuccess) return e;
-      (void)hipFree(c->scratch);
-      c->scratch = nullptr;
-      c->scratch_bytes = 0;
+      (void)hipFree(c->work);
+      c->work = nullptr;
+      c->work_bytes = 0;
     }
-    hipError_t e = hipMalloc(&c->scratch, bytes);
+    hipError_t e = hipMalloc(&c->work, bytes);
     if (e != hipSuccess) return e;
-    c->scratch_bytes = bytes;
+    c->work_bytes = bytes;
   }
-  *p = c->scratch;
+  *p = c->work;
   return hipSuccess;
 }
 static_assert(MPCX_TR == G_TR && MPCX_TRRELU == G_TRRELU && MPCX_RELU == G_RELU && MPCX_TRSLACK == G_TRSLACK &&
@@ -446,7 +460,7 @@ static mpcx_status maxpool_keygen_t(mpcx_ctx *c, int B, int N, int C, const void
   const int Lv = maxpool_plan(c, B, N, C, lay, pairs);
   const size_t rows = size_t(B) * N * C, P0 = Lv ? size_t(B) * pairs[0] * C : 0;
   void *sp = nullptr;
-  HIPC(c, ctx_scratch(c, (2 * rows + 2 * P0) * sizeof(T), &sp), "hipMalloc");
+  HIPC(c, ctx_work(c, (2 * rows + 2 * P0) * sizeof(T), &sp), "hipMalloc");
   T *va = static_cast<T *>(sp), *vb = va + rows, *dm = vb + rows, *ym = dm + P0;
   const T *cur = static_cast<const T *>(in_mask);
   T *nxt = va;
@@ -486,7 +500,7 @@ static mpcx_status maxpool_eval_t(mpcx_ctx *c, int B, int N, int C, const void *
   const int Lv = maxpool_plan(c, B, N, C, lay, pairs);
   const size_t rows = size_t(B) * N * C, P0 = Lv ? size_t(B) * pairs[0] * C : 0;
   void *sp = nullptr;
-  HIPC(c, ctx_scratch(c, (2 * rows + 2 * P0) * sizeof(T), &sp), "hipMalloc");
+  HIPC(c, ctx_work(c, (2 * rows + 2 * P0) * sizeof(T), &sp), "hipMalloc");
   T *va = static_cast<T *>(sp), *vb = va + rows, *d = vb + rows, *y = d + P0;
   const T *cur = static_cast<const T *>(in);
   T *nxt = va;
@@ -545,7 +559,7 @@ static mpcx_status mul_eval_t(mpcx_ctx *c, size_t nx, size_t ny, size_t nz, cons
                               const void *k0, const void *k1, const void *x, const void *y, void *z) {
   MulLayout lay = mul_layout(c->bw, nx, ny, nz, 0);
   void *sp = nullptr;
-  HIPC(c, ctx_scratch(c, 2 * nz * sizeof(T), &sp), "hipMalloc");
+  HIPC(c, ctx_work(c, 2 * nz * sizeof(T), &sp), "hipMalloc");
   T *m0 = static_cast<T *>(sp), *m1 = m0 + nz;
   HIPC(c,
        launch_mul_eval<T>(c->L, lay, static_cast<const uint8_t *>(k0), static_cast<const uint8_t *>(k1),
@@ -591,7 +605,7 @@ static mpcx_status lut_eval_t(mpcx_ctx *c, size_t n, const void *k0, const void 
                               void *y) {
   Lut8Layout lay = lut8_layout(c->bw, n, 0);
   void *sp = nullptr;
-  HIPC(c, ctx_scratch(c, 3 * n * sizeof(T), &sp), "hipMalloc");
+  HIPC(c, ctx_work(c, 3 * n * sizeof(T), &sp), "hipMalloc");
   T *m0 = static_cast<T *>(sp), *m1 = m0 + n, *vh = m1 + n;
   const uint8_t *K0 = static_cast<const uint8_t *>(k0), *K1 = static_cast<const uint8_t *>(k1);
   HIPC(c,
@@ -634,7 +648,7 @@ static mpcx_status sxs_keygen_t(mpcx_ctx *c, int nb, int M, int K, int N, const 
        "split");
   HIPC(c, launch_prf_ring<T>(c->L, seed, gate, F_ROUT, nc, static_cast<T *>(rc)), "prf");
   void *sp = nullptr;
-  HIPC(c, ctx_scratch(c, nc * sizeof(T), &sp), "hipMalloc");
+  HIPC(c, ctx_work(c, nc * sizeof(T), &sp), "hipMalloc");
   T *g = static_cast<T *>(sp);
   GemmArgs<T> a;
   a.M = M;
@@ -675,7 +689,7 @@ static mpcx_status sxs_eval_t(mpcx_ctx *c, int nb, int M, int K, int N, const vo
   const uint8_t *k0 = static_cast<const uint8_t *>(k0v), *k1 = static_cast<const uint8_t *>(k1v);
   const size_t nc = size_t(nb) * M * N;
   void *sp = nullptr;
-  HIPC(c, ctx_scratch(c, 2 * nc * sizeof(T), &sp), "hipMalloc");
+  HIPC(c, ctx_work(c, 2 * nc * sizeof(T), &sp), "hipMalloc");
   T *m0 = static_cast<T *>(sp), *m1 = m0 + nc;
   GemmArgs<T> g;
   g.M = M;
@@ -781,7 +795,7 @@ static mpcx_status reveal_eval_t(mpcx_ctx *c, size_t n, const void *k0, const vo
                                  const void *v1, void *out) {
   RevealLayout lay = reveal_layout(c->bw, n, 0);
   void *sp = nullptr;
-  HIPC(c, ctx_scratch(c, 2 * n * sizeof(T), &sp), "hipMalloc");
+  HIPC(c, ctx_work(c, 2 * n * sizeof(T), &sp), "hipMalloc");
   T *m0 = static_cast<T *>(sp), *m1 = m0 + n;
   HIPC(c,
        launch_reveal_eval<T>(c->L, lay, static_cast<const uint8_t *>(k0), static_cast<const uint8_t *>(k1),

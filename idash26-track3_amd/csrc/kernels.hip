@@ -88,7 +88,7 @@ __device__ __forceinline__ uint32_t get_bit(const uint64_t *plane, size_t i) {
 // ---------------------------------------------------------------------------
 template <int NT, int REP>
 __global__ void k_hash(int leaf, size_t n, const uint4 *in, uint4 *out) {
-  __shared__ uint32_t lds[AesLds<NT, REP>::kWords];
+  __shared__ __align__(16) uint32_t lds[AesLds<NT, REP>::kWords];
   AesLds<NT, REP>::fill(lds);
   AesLds<NT, REP> aes(lds);
   for (size_t i = size_t(blockIdx.x) * blockDim.x + threadIdx.x; i < n; i += size_t(gridDim.x) * blockDim.x)
@@ -107,7 +107,7 @@ hipError_t launch_hash(const Launch &L, int leaf, size_t n, const uint4 *in, uin
 
 template <int NT, int REP>
 __global__ void k_prf(AesRK kd, uint32_t gate, uint32_t field, size_t n, uint4 *out) {
-  __shared__ uint32_t lds[AesLds<NT, REP>::kWords];
+  __shared__ __align__(16) uint32_t lds[AesLds<NT, REP>::kWords];
   AesLds<NT, REP>::fill(lds);
   AesLds<NT, REP> aes(lds);
   for (size_t i = size_t(blockIdx.x) * blockDim.x + threadIdx.x; i < n; i += size_t(gridDim.x) * blockDim.x)
@@ -141,7 +141,7 @@ struct DcfGenArgs {
 
 template <int NT, int REP>
 __global__ void k_dcf_keygen(DcfGenArgs a) {
-  __shared__ uint32_t lds[AesLds<NT, REP>::kWords];
+  __shared__ __align__(16) uint32_t lds[AesLds<NT, REP>::kWords];
   AesLds<NT, REP>::fill(lds);
   AesLds<NT, REP> aes(lds);
   const size_t stride = size_t(gridDim.x) * blockDim.x;
@@ -200,7 +200,7 @@ struct DcfEvalArgs {
 
 template <int NT, int REP>
 __global__ void k_dcf_eval(DcfEvalArgs a) {
-  __shared__ uint32_t lds[AesLds<NT, REP>::kWords];
+  __shared__ __align__(16) uint32_t lds[AesLds<NT, REP>::kWords];
   AesLds<NT, REP>::fill(lds);
   AesLds<NT, REP> aes(lds);
   const size_t stride = size_t(gridDim.x) * blockDim.x;
@@ -300,7 +300,7 @@ constexpr int kTrMaxTile = 512;  // elements per tile (workgroups of up to 1024 
 
 template <typename T, int NT, int REP, int TAG>
 __global__ void k_tr_eval(TrArgs<T> a) {
-  __shared__ uint32_t lds[AesLds<NT, REP>::kWords];
+  __shared__ __align__(16) uint32_t lds[AesLds<NT, REP>::kWords];
   __shared__ uint64_t xa[2][kTrMaxTile / 64], xb[2][kTrMaxTile / 64];
   __shared__ T xm[2][kTrMaxTile];
   AesLds<NT, REP>::fill(lds);
@@ -386,7 +386,7 @@ __global__ void k_tr_eval(TrArgs<T> a) {
 
 template <typename T, int NT, int REP>
 __global__ void k_tr_keygen(TrArgs<T> a) {
-  __shared__ uint32_t lds[AesLds<NT, REP>::kWords];
+  __shared__ __align__(16) uint32_t lds[AesLds<NT, REP>::kWords];
   AesLds<NT, REP>::fill(lds);
   AesLds<NT, REP> aes(lds);
   const size_t stride = size_t(gridDim.x) * blockDim.x;
@@ -555,7 +555,7 @@ hipError_t launch_tr_eval(const Launch &L, const TrLayout &lay, const uint8_t *k
 
 template <typename T, int NT, int REP>
 __global__ void k_tr_expand(TrArgs<T> a, int p) {
-  __shared__ uint32_t lds[AesLds<NT, REP>::kWords];
+  __shared__ __align__(16) uint32_t lds[AesLds<NT, REP>::kWords];
   AesLds<NT, REP>::fill(lds);
   AesLds<NT, REP> aes(lds);
   const AesRK &kp = a.kp[0];
@@ -649,7 +649,7 @@ hipError_t launch_local_ars(const Launch &L, size_t n, int s, const T *x, const 
 template <typename T, int NT, int REP>
 __global__ void k_split(AesRK kd, uint32_t gate, uint32_t field, size_t n, const T *v, T *p0, T *p1, T *copy0,
                         T *mask_out) {
-  __shared__ uint32_t lds[AesLds<NT, REP>::kWords];
+  __shared__ __align__(16) uint32_t lds[AesLds<NT, REP>::kWords];
   AesLds<NT, REP>::fill(lds);
   AesLds<NT, REP> aes(lds);
   for (size_t i = size_t(blockIdx.x) * blockDim.x + threadIdx.x; i < n; i += size_t(gridDim.x) * blockDim.x) {
@@ -791,7 +791,7 @@ __device__ __forceinline__ void mul_operands(const MulMap &m, size_t k, uint32_t
 template <typename T, int NT, int REP>
 __global__ void k_mul_keygen_c(AesRK kd, uint32_t gate, size_t nz, MulMap map, const T *rx, const T *ry, T *rz,
                                T *C0, T *C1) {
-  __shared__ uint32_t lds[AesLds<NT, REP>::kWords];
+  __shared__ __align__(16) uint32_t lds[AesLds<NT, REP>::kWords];
   AesLds<NT, REP>::fill(lds);
   AesLds<NT, REP> aes(lds);
   for (size_t i = size_t(blockIdx.x) * blockDim.x + threadIdx.x; i < nz; i += size_t(gridDim.x) * blockDim.x) {
@@ -927,7 +927,7 @@ hipError_t launch_mul_eval(const Launch &L, const MulLayout &lay, const uint8_t 
 template <typename T, int NT, int REP>
 __global__ void k_lut8_keygen(AesRK kd, uint32_t gate, Lut8Layout lay, const T *in_mask,
                               T *out_mask, uint8_t *k0, uint8_t *k1) {
-  __shared__ uint32_t lds[AesLds<NT, REP>::kWords];
+  __shared__ __align__(16) uint32_t lds[AesLds<NT, REP>::kWords];
   AesLds<NT, REP>::fill(lds);
   AesLds<NT, REP> aes(lds);
   const size_t N = lay.dpf.N;
@@ -976,7 +976,7 @@ hipError_t launch_lut8_keygen(const Launch &L, const Lut8Layout &lay, uint64_t s
 template <typename T, int NT, int REP>
 __global__ void k_lut8_phase1(Lut8Layout lay, const uint8_t *k0, const uint8_t *k1,
                               const T *table, const T *xhat, T *msg0, T *msg1) {
-  __shared__ uint32_t lds[AesLds<NT, REP>::kWords];
+  __shared__ __align__(16) uint32_t lds[AesLds<NT, REP>::kWords];
   __shared__ T tab[256];
   for (int k = threadIdx.x; k < 256; k += blockDim.x) tab[k] = table[k];
   AesLds<NT, REP>::fill(lds);
@@ -1647,7 +1647,7 @@ hipError_t launch_gemm_pair(const Launch &L, const GemmArgs<T> &p0, const GemmAr
 
 template <typename T, int NT, int REP>
 __global__ void k_prf_ring(AesRK kd, uint32_t gate, uint32_t field, size_t n, T *out) {
-  __shared__ uint32_t lds[AesLds<NT, REP>::kWords];
+  __shared__ __align__(16) uint32_t lds[AesLds<NT, REP>::kWords];
   AesLds<NT, REP>::fill(lds);
   AesLds<NT, REP> aes(lds);
   for (size_t i = size_t(blockIdx.x) * blockDim.x + threadIdx.x; i < n; i += size_t(gridDim.x) * blockDim.x)
