@@ -4,6 +4,7 @@
 #include <cstdio>
 #include <cstdlib>
 #include <cstring>
+#include <mutex>
 #include <new>
 #include <string>
 
@@ -128,6 +129,9 @@ struct mpcx_ctx {
   // stream before returning, so the next call may reuse it).
   void *work = nullptr;
   size_t work_bytes = 0;
+  // this device's copy of the static scratch array (mpcx_maxpool_eval_noalloc)
+  void *noalloc_scratch = nullptr;
+  hipError_t noalloc_err = hipSuccess;
   AdjNormCache *adj = nullptr;  // prepared state of mpcx_adjnorm_eval
   int adj_lanes = 1;            // concurrent graph groups of the adjacency normalisation
 };
@@ -179,6 +183,41 @@ static size_t guard_size(F &&f) noexcept {
   }
 }
 
+// ---------------- allocation-free max-pool ----------------
+// mpcx_maxpool_eval_noalloc runs the same kernels as mpcx_maxpool_eval on a
+// workspace that is never allocated at call time: the file-scope device array
+// `scratch` below, one copy per GPU, loaded with the library's code object and
+// held until the process ends.  Its per-device address is looked up once per
+// device by mpcx_create (noalloc_scratch_resolve) and kept in g_scratch_addr;
+// host code uses only that address, never the array's name (which names a
+// host-side stand-in).  Every level plane is written before it is read, so
+// nothing in the array has to start at zero.
+static __device__ __align__(256) unsigned char scratch[MPCX_NOALLOC_SCRATCH_BYTES];
+
+namespace {
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void *g_scratch_addr[kMaxDevices];
+hipError_t g_scratch_err[kMaxDevices];
+bool g_scratch_done[kMaxDevices];
+
+// With `device` current: look up the device's copy of `scratch` (once per device).
+hipError_t noalloc_scratch_resolve(int device, void **out) {
+  *out = nullptr;
+  if (device < 0 || device >= kMaxDevices) return hipErrorInvalidDevice;
+  std::lock_guard<std::mutex> lk(g_scratch_mu);
+  if (!g_scratch_done[device]) {
+    void *ptr = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    g_scratch_err[device] = e;
+    g_scratch_addr[device] = e == hipSuccess ? ptr : nullptr;
+    g_scratch_done[device] = true;
+  }
+  *out = g_scratch_addr[device];
+  return g_scratch_err[device];
+}
+}  // namespace
+
 // All entry points below were declared extern "C" in mpcx.h and keep C linkage.
 
 mpcx_status mpcx_create(int bw, int scale, int device, mpcx_ctx **out) {
@@ -198,6 +237,7 @@ mpcx_status mpcx_create(int bw, int scale, int device, mpcx_ctx **out) {
     return MPCX_EHIP;
   }
   c->L.stream = c->own;
+  c->noalloc_err = noalloc_scratch_resolve(device, &c->noalloc_scratch);
   // The environment overrides take the same checks as mpcx_set_aes_variant: a
   // bad value is ignored with a warning (a block that is not a whole number of
   // wave pairs would misplace the DCF kernels' ballot words).
@@ -493,29 +533,45 @@ mpcx_status mpcx_maxpool_keygen(mpcx_ctx *c, int B, int N, int C, const void *in
 // and max(a, b) = a + ReLU(b - a) (local), on planes (B, R, C) that shrink to
 // (B, 1, C).
 template <typename T>
-static mpcx_status maxpool_eval_t(mpcx_ctx *c, int B, int N, int C, const void *k0, const void *k1, const void *in,
-                                  void *out) {
+static hipError_t maxpool_eval_run(mpcx_ctx *c, int B, int N, int C, const void *k0, const void *k1, const void *in,
+                                   void *out, void *work) {
   TrLayout lay[kMaxPoolLevels];
   int pairs[kMaxPoolLevels];
   const int Lv = maxpool_plan(c, B, N, C, lay, pairs);
   const size_t rows = size_t(B) * N * C, P0 = Lv ? size_t(B) * pairs[0] * C : 0;
-  void *sp = nullptr;
-  HIPC(c, ctx_work(c, (2 * rows + 2 * P0) * sizeof(T), &sp), "hipMalloc");
-  T *va = static_cast<T *>(sp), *vb = va + rows, *d = vb + rows, *y = d + P0;
+  T *va = static_cast<T *>(work), *vb = va + rows, *d = vb + rows, *y = d + P0;
   const T *cur = static_cast<const T *>(in);
   T *nxt = va;
   const uint8_t *K0 = static_cast<const uint8_t *>(k0), *K1 = static_cast<const uint8_t *>(k1);
   int R = N;
   for (int l = 0; l < Lv; l++) {
     const size_t n = size_t(B) * pairs[l] * C;
-    HIPC(c, launch_pool_diff<T>(c->L, B, R, C, cur, d), "maxpool_eval");
-    HIPC(c, tr_eval_run<T>(c, lay[l], n, K0, K1, d, nullptr, 1, y), "maxpool_eval");
-    HIPC(c, launch_pool_combine<T>(c->L, B, R, C, cur, y, nullptr, nxt), "maxpool_eval");
+    hipError_t e = launch_pool_diff<T>(c->L, B, R, C, cur, d);
+    if (e == hipSuccess) e = tr_eval_run<T>(c, lay[l], n, K0, K1, d, nullptr, 1, y);
+    if (e == hipSuccess) e = launch_pool_combine<T>(c->L, B, R, C, cur, y, nullptr, nxt);
+    if (e != hipSuccess) return e;
     cur = nxt;
     nxt = nxt == va ? vb : va;
     R = pairs[l] + (R & 1);
   }
-  HIPC(c, hipMemcpyAsync(out, cur, size_t(B) * C * sizeof(T), hipMemcpyDeviceToDevice, c->L.stream), "maxpool_eval");
+  return hipMemcpyAsync(out, cur, size_t(B) * C * sizeof(T), hipMemcpyDeviceToDevice, c->L.stream);
+}
+
+// Device workspace of a max-pool evaluation: the level planes (two of B x N x C,
+// ping-pong) and the first level's pair differences and ReLU outputs.
+static size_t maxpool_work_bytes(const mpcx_ctx *c, int B, int N, int C) {
+  int pairs[kMaxPoolLevels];
+  const int Lv = pool_levels(N, pairs);
+  const size_t rows = size_t(B) * N * C, P0 = Lv ? size_t(B) * pairs[0] * C : 0;
+  return (2 * rows + 2 * P0) * size_t(c->bw / 8);
+}
+
+template <typename T>
+static mpcx_status maxpool_eval_t(mpcx_ctx *c, int B, int N, int C, const void *k0, const void *k1, const void *in,
+                                  void *out) {
+  void *sp = nullptr;
+  HIPC(c, ctx_work(c, maxpool_work_bytes(c, B, N, C), &sp), "hipMalloc");
+  HIPC(c, (maxpool_eval_run<T>(c, B, N, C, k0, k1, in, out, sp)), "maxpool_eval");
   HIPC(c, hipStreamSynchronize(c->L.stream), "sync");
   return MPCX_OK;
 }
@@ -527,6 +583,28 @@ mpcx_status mpcx_maxpool_eval(mpcx_ctx *c, int B, int N, int C, const void *k0, 
     return fail(c, MPCX_EINVAL, "maxpool_eval: bad argument");
   return c->bw == 32 ? maxpool_eval_t<uint32_t>(c, B, N, C, k0, k1, in, out)
                      : maxpool_eval_t<uint64_t>(c, B, N, C, k0, k1, in, out);
+}
+
+// Allocation-free variant of mpcx_maxpool_eval on the static scratch array
+// (defined with its per-device lookup above mpcx_create).
+mpcx_status mpcx_maxpool_eval_noalloc(mpcx_ctx *c, int B, int N, int C, const void *k0, const void *k1,
+                                      const void *in, void *out) {
+  CHECK_CTX(c);
+  if (!maxpool_dims_ok(B, N, C) || !in || !out || (N > 1 && (!k0 || !k1)))
+    return fail(c, MPCX_EINVAL, "maxpool_eval_noalloc: bad argument");
+  const size_t need = maxpool_work_bytes(c, B, N, C);
+  if (need > MPCX_NOALLOC_SCRATCH_BYTES)
+    return fail(c, MPCX_EINVAL,
+                "maxpool_eval_noalloc: workspace of " + std::to_string(need) + " bytes exceeds the " +
+                    std::to_string(size_t(MPCX_NOALLOC_SCRATCH_BYTES)) + "-byte static scratch array");
+  if (!c->noalloc_scratch)
+    return fail(c, MPCX_EHIP, std::string("maxpool_eval_noalloc: no scratch address on this device: ") +
+                                  hipGetErrorString(c->noalloc_err));
+  const hipError_t e = c->bw == 32
+                           ? maxpool_eval_run<uint32_t>(c, B, N, C, k0, k1, in, out, c->noalloc_scratch)
+                           : maxpool_eval_run<uint64_t>(c, B, N, C, k0, k1, in, out, c->noalloc_scratch);
+  HIPC(c, e, "maxpool_eval_noalloc");
+  return MPCX_OK;
 }
 
 // ---------------- MUL ----------------

@@ -50,6 +50,8 @@ _SIGS = {
                                       C.c_uint32, C.c_void_p, C.c_void_p]),
     "mpcx_maxpool_eval": (C.c_int, [C.c_void_p, C.c_int, C.c_int, C.c_int, C.c_void_p, C.c_void_p, C.c_void_p,
                                     C.c_void_p]),
+    "mpcx_maxpool_eval_noalloc": (C.c_int, [C.c_void_p, C.c_int, C.c_int, C.c_int, C.c_void_p, C.c_void_p,
+                                            C.c_void_p, C.c_void_p]),
     "mpcx_tr_key_bytes": (C.c_size_t, [C.c_void_p, C.c_int, C.c_size_t]),
     "mpcx_tr_keygen": (C.c_int, [C.c_void_p, C.c_int, C.c_size_t, C.c_void_p, C.c_void_p, C.c_uint64,
                                  C.c_uint32, C.c_void_p, C.c_void_p]),
@@ -294,6 +296,17 @@ class Ctx:
         out = empty_dev(B * C * xhat.itemsize)
         self.check(self.lib.mpcx_maxpool_eval(self.h, B, N, C, dptr(k0), dptr(k1), dptr(dx), dptr(out)),
                    "maxpool_eval")
+        return from_dev(out, self.T, B * C)
+
+    def maxpool_eval_noalloc(self, B, N, C, k0, k1, xhat):
+        """mpcx_maxpool_eval_noalloc: the same evaluation on the library's static
+        device scratch array (no allocation inside the call, no synchronisation)."""
+        xhat = self.ring(xhat)
+        dx = to_dev(xhat)
+        out = empty_dev(B * C * xhat.itemsize)
+        self.check(self.lib.mpcx_maxpool_eval_noalloc(self.h, B, N, C, dptr(k0), dptr(k1), dptr(dx), dptr(out)),
+                   "maxpool_eval_noalloc")
+        self.sync()
         return from_dev(out, self.T, B * C)
 
     def mul_keygen(self, rx, ry, ia, ib, seed=1, gate=1):

@@ -161,6 +161,21 @@ mpcx_status mpcx_maxpool_keygen(mpcx_ctx *ctx, int B, int N, int C, const void *
                                 void *d_key1);
 mpcx_status mpcx_maxpool_eval(mpcx_ctx *ctx, int B, int N, int C, const void *d_key0,
                               const void *d_key1, const void *d_xhat, void *d_yhat);
+/* Allocation-free variant of mpcx_maxpool_eval.  It has no counterpart in the
+ * reference: it is for callers that cannot allocate device memory (code under
+ * HIP graph capture, tight serving loops, harnesses that forbid hipMalloc).
+ * Same arguments, keys and results.  Its level planes live in a static device
+ * array of MPCX_NOALLOC_SCRATCH_BYTES per GPU (resident from the library's load
+ * until the process ends) instead of the context's workspace: it calls no
+ * hipMalloc, hipFree or allocating routine and does not synchronize (the
+ * output is ready when the context's stream reaches it).  It needs
+ * (2*B*N*C + 2*B*floor(N/2)*C) * bw/8 bytes of that array (64 x 140 x 312 fits
+ * at both widths); larger calls fail with MPCX_EINVAL.  Every call on one GPU
+ * shares that GPU's array: calls on one stream run in order, calls that overlap
+ * (other streams, threads or contexts on the same GPU) race. */
+#define MPCX_NOALLOC_SCRATCH_BYTES ((size_t)64 << 20)
+mpcx_status mpcx_maxpool_eval_noalloc(mpcx_ctx *ctx, int B, int N, int C, const void *d_key0,
+                                      const void *d_key1, const void *d_xhat, void *d_yhat);
 
 /* ---------------- Beaver product ----------------
  * z[i] = x[ia[i]] * y[ib[i]] on masked operands (index maps allow the
