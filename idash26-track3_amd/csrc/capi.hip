@@ -12,6 +12,7 @@
 #include "kernels.h"
 #include "model.h"
 #include "mpcx_core.h"
+#include "peer.h"
 
 // ---------------------------------------------------------------------------
 // AES-128 key schedule (FIPS-197 5.2) and the fixed keys
@@ -132,6 +133,7 @@ struct mpcx_ctx {
   // this device's copy of the static scratch array (mpcx_maxpool_eval_noalloc)
   void *noalloc_scratch = nullptr;
   hipError_t noalloc_err = hipSuccess;
+  PartyWork *party = nullptr;   // workspace of the party-mode gate calls
   AdjNormCache *adj = nullptr;  // prepared state of mpcx_adjnorm_eval
   int adj_lanes = 1;            // concurrent graph groups of the adjacency normalisation
 };
@@ -139,6 +141,10 @@ struct mpcx_ctx {
 struct mpcx_model {
   mpcx_ctx *ctx = nullptr;
   LaneSet *impl = nullptr;
+};
+
+struct mpcx_peer {
+  Peer *impl = nullptr;
 };
 
 static mpcx_status fail(mpcx_ctx *c, mpcx_status st, const std::string &msg) {
@@ -266,6 +272,7 @@ void mpcx_destroy(mpcx_ctx *c) {
     (void)hipStreamDestroy(c->own);
   }
   if (c->work) (void)hipFree(c->work);
+  party_work_free(c->party);
   adjnorm_cache_free(c->adj);
   delete c;
 }
@@ -927,6 +934,157 @@ mpcx_status mpcx_adjnorm_eval(mpcx_ctx *c, int B, int N, int nmax, const void *k
   return MPCX_OK;
 }
 
+// ---------------- party mode ----------------
+constexpr int kPeerIoTimeoutMs = 120000;  // a silent peer fails the exchange after this
+
+mpcx_status mpcx_peer_connect(int party, const char *path, int timeout_ms, mpcx_peer **out) {
+  if (!out || !path || (party != 0 && party != 1) || timeout_ms < 0) return MPCX_EINVAL;
+  *out = nullptr;
+  std::string err;
+  Peer *p = nullptr;
+  const hipError_t e = guard([&] {
+    return peer_connect(party, path, timeout_ms, std::max(timeout_ms, kPeerIoTimeoutMs), &p, &err);
+  });
+  if (e != hipSuccess) {
+    std::fprintf(stderr, "libmpcx: mpcx_peer_connect(party %d): %s\n", party, err.c_str());
+    return e == hipErrorInvalidValue ? MPCX_EINVAL : e == hipErrorOutOfMemory ? MPCX_ENOMEM : MPCX_EIO;
+  }
+  *out = new (std::nothrow) mpcx_peer();
+  if (!*out) {
+    delete p;
+    return MPCX_ENOMEM;
+  }
+  (*out)->impl = p;
+  return MPCX_OK;
+}
+
+mpcx_status mpcx_peer_pair(int timeout_ms, mpcx_peer **p0, mpcx_peer **p1) {
+  if (!p0 || !p1 || timeout_ms < 0) return MPCX_EINVAL;
+  *p0 = *p1 = nullptr;
+  std::string err;
+  Peer *a = nullptr, *b = nullptr;
+  const hipError_t e = guard([&] { return peer_pair(timeout_ms, &a, &b, &err); });
+  if (e != hipSuccess) return e == hipErrorOutOfMemory ? MPCX_ENOMEM : MPCX_EIO;
+  *p0 = new (std::nothrow) mpcx_peer();
+  *p1 = new (std::nothrow) mpcx_peer();
+  if (!*p0 || !*p1) {
+    delete a;
+    delete b;
+    delete *p0;
+    delete *p1;
+    *p0 = *p1 = nullptr;
+    return MPCX_ENOMEM;
+  }
+  (*p0)->impl = a;
+  (*p1)->impl = b;
+  return MPCX_OK;
+}
+
+void mpcx_peer_close(mpcx_peer *p) {
+  if (!p) return;
+  delete p->impl;
+  delete p;
+}
+int mpcx_peer_party(const mpcx_peer *p) { return p ? p->impl->party() : -1; }
+uint64_t mpcx_peer_bytes(const mpcx_peer *p) { return p ? p->impl->bytes_sent() + p->impl->bytes_received() : 0; }
+uint64_t mpcx_peer_rounds(const mpcx_peer *p) { return p ? p->impl->rounds() : 0; }
+const char *mpcx_peer_error(const mpcx_peer *p) { return p ? p->impl->error().c_str() : "null peer"; }
+
+namespace {
+// A party-mode call's status: channel failures are MPCX_EIO with the peer's message.
+mpcx_status party_status(mpcx_ctx *c, mpcx_peer *p, hipError_t e, const char *what) {
+  if (e == hipSuccess) return MPCX_OK;
+  if (e == hipErrorNotReady) return fail(c, MPCX_EIO, std::string(what) + ": " + p->impl->error());
+  return hip_status(c, e, what);
+}
+Launch party_launch(const mpcx_ctx *c, const mpcx_peer *p) {
+  Launch L = c->L;
+  L.party = p->impl->party();
+  return L;
+}
+}  // namespace
+
+mpcx_status mpcx_party_reconstruct(mpcx_ctx *c, mpcx_peer *p, size_t n, void *d) {
+  CHECK_CTX(c);
+  if (!p) return fail(c, MPCX_EINVAL, "party_reconstruct: null peer");
+  if (n == 0) return MPCX_OK;
+  if (!d) return fail(c, MPCX_EINVAL, "party_reconstruct: null pointer");
+  const Launch L = party_launch(c, p);
+  return party_status(c, p, guard([&] { return party_reconstruct(&c->party, L, p->impl, &c->counters, c->bw, c->s, n, d); }),
+                      "party_reconstruct");
+}
+
+mpcx_status mpcx_party_tr_eval(mpcx_ctx *c, mpcx_peer *p, int kind, size_t n, const void *key, const void *x,
+                               const void *bias, int ncol, void *y) {
+  CHECK_CTX(c);
+  if (!p || !valid_kind(kind) || (bias && ncol < 1)) return fail(c, MPCX_EINVAL, "party_tr_eval: bad argument");
+  if (n == 0) return MPCX_OK;
+  if ((kind != MPCX_LOCALARS && !key) || !x || !y) return fail(c, MPCX_EINVAL, "party_tr_eval: null pointer");
+  if (kind == MPCX_LOCALARS)  // local: the same on both parties, no key, no exchange
+    return mpcx_tr_eval(c, kind, n, nullptr, nullptr, x, bias, ncol, y);
+  const Launch L = party_launch(c, p);
+  return party_status(c, p, guard([&] {
+                        return party_tr_eval(&c->party, L, p->impl, &c->counters, c->bw, c->s, kind, n,
+                                             static_cast<const uint8_t *>(key), x, bias, ncol, y);
+                      }),
+                      "party_tr_eval");
+}
+
+mpcx_status mpcx_party_mul_eval(mpcx_ctx *c, mpcx_peer *p, size_t nx, size_t ny, size_t nz, const uint32_t *ia,
+                                const uint32_t *ib, const void *key, const void *x, const void *y, void *z) {
+  CHECK_CTX(c);
+  if (!p) return fail(c, MPCX_EINVAL, "party_mul_eval: null peer");
+  if (nz == 0) return MPCX_OK;
+  if (!ia || !ib || !key || !x || !y || !z) return fail(c, MPCX_EINVAL, "party_mul_eval: null pointer");
+  const Launch L = party_launch(c, p);
+  return party_status(c, p, guard([&] {
+                        return party_mul_eval(&c->party, L, p->impl, &c->counters, c->bw, c->s, nx, ny, nz, ia, ib,
+                                              static_cast<const uint8_t *>(key), x, y, z);
+                      }),
+                      "party_mul_eval");
+}
+
+mpcx_status mpcx_party_lut8_eval(mpcx_ctx *c, mpcx_peer *p, size_t n, const void *key, const void *table,
+                                 const void *x, void *y) {
+  CHECK_CTX(c);
+  if (!p) return fail(c, MPCX_EINVAL, "party_lut8_eval: null peer");
+  if (n == 0) return MPCX_OK;
+  if (!key || !table || !x || !y) return fail(c, MPCX_EINVAL, "party_lut8_eval: null pointer");
+  const Launch L = party_launch(c, p);
+  return party_status(c, p, guard([&] {
+                        return party_lut8_eval(&c->party, L, p->impl, &c->counters, c->bw, c->s, n,
+                                               static_cast<const uint8_t *>(key), table, x, y);
+                      }),
+                      "party_lut8_eval");
+}
+
+mpcx_status mpcx_party_sxs_eval(mpcx_ctx *c, mpcx_peer *p, int nb, int M, int K, int N, const void *key,
+                                const void *a, const void *b, void *out) {
+  CHECK_CTX(c);
+  if (!p || nb < 1 || M < 1 || K < 1 || N < 1 || !key || !a || !b || !out)
+    return fail(c, MPCX_EINVAL, "party_sxs_eval: bad argument");
+  const Launch L = party_launch(c, p);
+  return party_status(c, p, guard([&] {
+                        return party_sxs_eval(&c->party, L, p->impl, &c->counters, c->bw, c->s, nb, M, K, N,
+                                              static_cast<const uint8_t *>(key), a, b, out);
+                      }),
+                      "party_sxs_eval");
+}
+
+mpcx_status mpcx_party_reveal_eval(mpcx_ctx *c, mpcx_peer *p, size_t n, const void *key, const void *v,
+                                   void *out) {
+  CHECK_CTX(c);
+  if (!p) return fail(c, MPCX_EINVAL, "party_reveal_eval: null peer");
+  if (n == 0) return MPCX_OK;
+  if (!key || !v || !out) return fail(c, MPCX_EINVAL, "party_reveal_eval: null pointer");
+  const Launch L = party_launch(c, p);
+  return party_status(c, p, guard([&] {
+                        return party_reveal_eval(&c->party, L, p->impl, &c->counters, c->bw, c->s, n,
+                                                 static_cast<const uint8_t *>(key), v, out);
+                      }),
+                      "party_reveal_eval");
+}
+
 // ---------------- pinned host memory ----------------
 mpcx_status mpcx_host_alloc(size_t bytes, void **out) {
   if (!out || bytes == 0) return MPCX_EINVAL;
@@ -1094,6 +1252,7 @@ mpcx_status mpcx_model_forward(mpcx_model *m, int B) {
   hipError_t e = guard([&] { return m->impl->forward(B); });
   if (e == hipErrorInvalidValue) return fail(m->ctx, MPCX_ESTATE, "forward: keys or inputs not set for this B");
   if (e == hipErrorFileNotFound) return fail(m->ctx, MPCX_EIO, "forward: key file read failed");
+  if (e == hipErrorNotReady) return fail(m->ctx, MPCX_EIO, "forward: the channel to the other party failed");
   HIPC(m->ctx, e, "model_forward");
   m->ctx->counters.bytes += m->impl->counters.bytes;
   m->ctx->counters.rounds += m->impl->counters.rounds;
@@ -1103,6 +1262,32 @@ mpcx_status mpcx_model_forward(mpcx_model *m, int B) {
 mpcx_status mpcx_model_output(mpcx_model *m, int B, int64_t *out) {
   if (!m || !out) return MPCX_EINVAL;
   HIPC(m->ctx, guard([&] { return m->impl->output(out, B); }), "model_output");
+  return MPCX_OK;
+}
+
+mpcx_status mpcx_model_set_party(mpcx_model *m, mpcx_peer *peer) {
+  if (!m) return MPCX_EINVAL;
+  const hipError_t e =
+      guard([&] { return m->impl->set_party(peer ? peer->impl->party() : -1, peer ? peer->impl : nullptr); });
+  if (e == hipErrorInvalidValue) return fail(m->ctx, MPCX_EINVAL, "model_set_party: " + m->impl->err);
+  HIPC(m->ctx, e, "model_set_party");
+  return MPCX_OK;
+}
+
+mpcx_status mpcx_model_import_party_key(mpcx_model *m, int B, const void *key, size_t bytes) {
+  if (!m || !key) return MPCX_EINVAL;
+  if (m->impl->party() < 0) return fail(m->ctx, MPCX_ESTATE, "import_party_key: the model is not in party mode");
+  if (B < 1 || bytes != mpcx_model_key_bytes(m, B)) return fail(m->ctx, MPCX_EINVAL, "import_party_key: key size mismatch");
+  HIPC(m->ctx, guard([&] { return m->impl->import_party_key(B, key, bytes); }), "model_import_party_key");
+  return MPCX_OK;
+}
+
+mpcx_status mpcx_model_set_party_inputs(mpcx_model *m, int B, const void *x, const void *a, const void *mask,
+                                        const int64_t *prot) {
+  if (!m || !x || !a || !mask) return MPCX_EINVAL;
+  if (m->impl->party() < 0) return fail(m->ctx, MPCX_ESTATE, "set_party_inputs: the model is not in party mode");
+  if (B < 1) return fail(m->ctx, MPCX_EINVAL, "B must be >= 1");
+  HIPC(m->ctx, guard([&] { return m->impl->set_party_inputs(B, x, a, mask, prot); }), "model_set_party_inputs");
   return MPCX_OK;
 }
 

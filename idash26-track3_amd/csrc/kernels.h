@@ -29,6 +29,11 @@ struct Launch {
   // model forwards with resident keys are captured once per batch size into a
   // HIP graph and replayed (0 = enqueue every kernel each time)
   int graph = 1;
+  // -1: two-party kernels evaluate both parties (blockIdx.y = party).  0 or 1:
+  // only that party (one process per party): the launchers take the party's own
+  // key (and input share, message buffer) in both party slots and launch one
+  // party row of workgroups.
+  int party = -1;
 };
 
 struct AesVariant {
@@ -70,6 +75,20 @@ hipError_t launch_tr_expand(const Launch &L, const TrLayout &lay, const uint8_t 
 template <typename T>
 hipError_t launch_tr_eval(const Launch &L, const TrLayout &lay, const uint8_t *k0, const uint8_t *k1,
                           const T *xhat, const T *bias, int bias_ncol, T *yhat);
+
+// Party mode (L.party = p), the same gate in two launches around the two
+// exchanges.  Phase 1: party p's masked DCF output bits, one bit per element,
+// packed 64 per word: plane a at bits[0, W), plane b at bits[W, 2W), W = ceil(N/64)
+// (lay.use_a / lay.use_b tell which planes the gate has).
+template <typename T>
+hipError_t launch_tr_party_bits(const Launch &L, const TrLayout &lay, const uint8_t *key, const T *xhat,
+                                const T *bias, int bias_ncol, uint64_t *bits);
+// Phase 2, after the planes are exchanged: party p's output message msg (N
+// words) from its own and the peer's planes.  For G_DRELU the output bit is
+// public after phase 1: msg receives it directly (no second exchange).
+template <typename T>
+hipError_t launch_tr_party_msg(const Launch &L, const TrLayout &lay, const uint8_t *key, const T *xhat,
+                               const T *bias, int bias_ncol, const uint64_t *own, const uint64_t *peer, T *msg);
 
 // out = m0 + m1 (reconstruction of a revealed value from both parties' messages)
 template <typename T>

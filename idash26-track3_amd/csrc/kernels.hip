@@ -51,6 +51,10 @@ static hipError_t with_variant(const Launch &L, Fn &&fn) {
     default: return hipErrorInvalidValue;
   }
 }
+// Rows of workgroups of a two-party kernel (blockIdx.y + party_base = party):
+// both parties, or only L.party in party mode.
+static unsigned party_rows(const Launch &L) { return L.party < 0 ? 2u : 1u; }
+static int party_base(const Launch &L) { return L.party < 0 ? 0 : L.party; }
 static int variant_block(const Launch &L) {
   if (L.aes_block > 0) return L.aes_block;
   int n;
@@ -289,6 +293,62 @@ __device__ __forceinline__ T tr_shifted_input(const TrArgs<T> &a, size_t i) {
   return low_bits<T>(x + (T(1) << a.sb), a.m);
 }
 
+// Party p's masked DCF output bits of element i (the gate's planes a and b):
+// the DCF walks over the shifted input xp with the party's roots and mask bits
+// (K) and the correction and leaf words, which are the same in both parties'
+// keys (KC: any party's copy).
+template <typename T, class Aes>
+__device__ __forceinline__ void tr_dcf_bits(Aes &aes, const TrArgs<T> &a, const uint8_t *K,
+                                            const uint8_t *KC, size_t i, T xp, uint32_t *ra, uint32_t *rb) {
+  const T lowmask = (T(1) << a.sb) - T(1);
+  const T smask = (T(1) << a.s) - T(1);
+  if (a.use_a) {
+    *ra = dcf_eval_walk(aes, reinterpret_cast<const uint4 *>(K + a.a.off_root)[i], a.a.m, a.a.L,
+                        reinterpret_cast<const uint4 *>(KC + a.a.off_cw) + i, a.N,
+                        reinterpret_cast<const uint4 *>(KC + a.a.off_leaf)[i], uint64_t(xp & lowmask));
+    *ra ^= get_bit(reinterpret_cast<const uint64_t *>(K + a.a.off_z), i);
+  }
+  if (a.use_b) {
+    *rb = dcf_eval_walk(aes, reinterpret_cast<const uint4 *>(K + a.b.off_root)[i], a.b.m, a.b.L,
+                        reinterpret_cast<const uint4 *>(KC + a.b.off_cw) + i, a.N,
+                        reinterpret_cast<const uint4 *>(KC + a.b.off_leaf)[i], uint64_t(xp & smask));
+    *rb ^= get_bit(reinterpret_cast<const uint64_t *>(K + a.b.off_z), i);
+  }
+}
+
+// Party p's output message for element i once the masked DCF outputs are
+// public: hb the sign-position bit of the shifted input, bh and dh the
+// reconstructed masked bits of planes a and b.  The two parties' messages add
+// up to the masked output.
+template <typename T>
+__device__ __forceinline__ T tr_out_share(const TrArgs<T> &a, int p, const uint8_t *K, size_t i, T xp, uint32_t hb,
+                                          uint32_t bh, uint32_t dh) {
+  const T *G = reinterpret_cast<const T *>(K + a.off_g);
+  const T *kap = reinterpret_cast<const T *>(K + a.off_kappa);
+  const T one0 = p == 0 ? T(1) : T(0);
+  const T A = (xp >> a.sh) - (T(1) << (a.m - 1 - a.sh));
+  if (a.kind == G_TRMOD) return one0 * A + G[size_t(dh) * a.N + i];  // exact modulo 2^(n-s): no wrap term
+  if (a.kind == G_EXT) return one0 * A + G[size_t(hb * 2 + bh) * a.N + i];
+  if (a.kind == G_EXTRELU || a.kind == G_TRRELU) {
+    const uint32_t z = hb ^ bh;
+    const T k = kap[i];
+    const T cp = z ? T(one0 - k) : k;
+    const size_t c = a.kind == G_EXTRELU ? hb * 2 + bh : hb * 4 + bh * 2 + dh;
+    return cp * A + G[c * a.N + i];
+  }
+  if (a.kind == G_TR) return one0 * A + G[size_t(hb * 4 + bh * 2 + dh) * a.N + i];
+  if (a.kind == G_DRELU) return one0 * T(hb ^ bh);  // the public masked bit; party 0 carries it
+  if (relu_like(a.kind)) {
+    const uint32_t z = hb ^ bh;
+    const T k = kap[i];
+    const T cp = z ? T(one0 - k) : k;
+    return cp * a.xhat[i] + G[size_t(z) * a.N + i];
+  }
+  // G_TRSLACK
+  const uint32_t Hh = uint32_t(xp >> (a.n - 2)) & 3u;
+  return one0 * A + G[size_t(Hh * 2 + dh) * a.N + i];
+}
+
 // One launch evaluates a gate for both parties.  A workgroup of 2h threads
 // takes tiles of h elements: its first h threads are party 0, the last h party
 // 1, each evaluating its own keys on the same elements.  The two exchanges of
@@ -314,11 +374,6 @@ __global__ void k_tr_eval(TrArgs<T> a) {
   // parties (public to both); both parties read party 0's planes, so one copy
   // serves the two evaluations (and a streamed arena moves it once).
   const uint8_t *KC = a.k0;
-  const T *G = reinterpret_cast<const T *>(K + a.off_g);
-  const T *kap = reinterpret_cast<const T *>(K + a.off_kappa);
-  const T one0 = p == 0 ? T(1) : T(0);
-  const T lowmask = (T(1) << a.sb) - T(1);
-  const T smask = (T(1) << a.s) - T(1);
   const size_t stride = size_t(gridDim.x) * size_t(h);
   for (size_t base = size_t(blockIdx.x) * h; base < a.N; base += stride) {
     const size_t i = base + size_t(e);
@@ -327,18 +382,7 @@ __global__ void k_tr_eval(TrArgs<T> a) {
     T xp = 0;
     if (in) {
       xp = tr_shifted_input(a, i);
-      if (a.use_a) {
-        ra = dcf_eval_walk(aes, reinterpret_cast<const uint4 *>(K + a.a.off_root)[i], a.a.m, a.a.L,
-                           reinterpret_cast<const uint4 *>(KC + a.a.off_cw) + i, a.N,
-                           reinterpret_cast<const uint4 *>(KC + a.a.off_leaf)[i], uint64_t(xp & lowmask));
-        ra ^= get_bit(reinterpret_cast<const uint64_t *>(K + a.a.off_z), i);
-      }
-      if (a.use_b) {
-        rb = dcf_eval_walk(aes, reinterpret_cast<const uint4 *>(K + a.b.off_root)[i], a.b.m, a.b.L,
-                           reinterpret_cast<const uint4 *>(KC + a.b.off_cw) + i, a.N,
-                           reinterpret_cast<const uint4 *>(KC + a.b.off_leaf)[i], uint64_t(xp & smask));
-        rb ^= get_bit(reinterpret_cast<const uint64_t *>(K + a.b.off_z), i);
-      }
+      tr_dcf_bits(aes, a, K, KC, i, xp, &ra, &rb);
     }
     // exchange 1: the masked DCF output bits
     const uint64_t wa = __ballot(ra), wb = __ballot(rb);
@@ -351,36 +395,48 @@ __global__ void k_tr_eval(TrArgs<T> a) {
       const uint32_t hb = uint32_t(xp >> a.sb) & 1u;
       const uint32_t bh = a.use_a ? uint32_t((xa[0][wv] ^ xa[1][wv]) >> lane_id()) & 1u : 0u;
       const uint32_t dh = a.use_b ? uint32_t((xb[0][wv] ^ xb[1][wv]) >> lane_id()) & 1u : 0u;
-      const T A = (xp >> a.sh) - (T(1) << (a.m - 1 - a.sh));
-      T y;
-      if (a.kind == G_TRMOD) {  // exact modulo 2^(n-s): no wrap term
-        y = one0 * A + G[size_t(dh) * a.N + i];
-      } else if (a.kind == G_EXT) {
-        y = one0 * A + G[size_t(hb * 2 + bh) * a.N + i];
-      } else if (a.kind == G_EXTRELU || a.kind == G_TRRELU) {
-        const uint32_t z = hb ^ bh;
-        const T k = kap[i];
-        const T cp = z ? T(one0 - k) : k;
-        const size_t c = a.kind == G_EXTRELU ? hb * 2 + bh : hb * 4 + bh * 2 + dh;
-        y = cp * A + G[c * a.N + i];
-      } else if (a.kind == G_TR) {
-        y = one0 * A + G[size_t(hb * 4 + bh * 2 + dh) * a.N + i];
-      } else if (a.kind == G_DRELU) {  // the public masked bit; party 0 carries it
-        y = one0 * T(hb ^ bh);
-      } else if (relu_like(a.kind)) {
-        const uint32_t z = hb ^ bh;
-        const T k = kap[i];
-        const T cp = z ? T(one0 - k) : k;
-        y = cp * a.xhat[i] + G[size_t(z) * a.N + i];
-      } else {  // G_TRSLACK
-        const uint32_t Hh = uint32_t(xp >> (a.n - 2)) & 3u;
-        y = one0 * A + G[size_t(Hh * 2 + dh) * a.N + i];
-      }
-      xm[p][e] = y;  // exchange 2: the output messages
+      xm[p][e] = tr_out_share(a, p, K, i, xp, hb, bh, dh);  // exchange 2: the output messages
     }
     __syncthreads();
     if (p == 0 && in) a.out[i] = xm[0][e] + xm[1][e];
     __syncthreads();  // the next tile reuses the exchange buffers
+  }
+}
+
+// Party mode, phase 1: party p's masked DCF output bits (one ballot word per
+// wave and plane).  a.k0 = a.k1 = the party's own key.
+template <typename T, int NT, int REP>
+__global__ void k_tr_party_bits(TrArgs<T> a, uint64_t *bits) {
+  __shared__ __align__(16) uint32_t lds[AesLds<NT, REP>::kWords];
+  AesLds<NT, REP>::fill(lds);
+  AesLds<NT, REP> aes(lds);
+  const size_t W = (a.N + 63) / 64;
+  const size_t stride = size_t(gridDim.x) * blockDim.x;
+  for (size_t base = size_t(blockIdx.x) * blockDim.x + (threadIdx.x & ~63u); base < a.N; base += stride) {
+    const size_t i = base + lane_id();
+    uint32_t ra = 0, rb = 0;
+    if (i < a.N) tr_dcf_bits(aes, a, a.k0, a.k0, i, tr_shifted_input(a, i), &ra, &rb);
+    const uint64_t wa = __ballot(ra), wb = __ballot(rb);
+    if (lane_id() == 0) {
+      if (a.use_a) bits[base >> 6] = wa;
+      if (a.use_b) bits[W + (base >> 6)] = wb;
+    }
+  }
+}
+
+// Party mode, phase 2: party p's output message from the reconstructed bits
+// (own XOR peer); for G_DRELU the public output bit itself.
+template <typename T>
+__global__ void k_tr_party_msg(TrArgs<T> a, int p, const uint64_t *own, const uint64_t *peer, T *msg) {
+  const size_t W = (a.N + 63) / 64;
+  for (size_t i = size_t(blockIdx.x) * blockDim.x + threadIdx.x; i < a.N; i += size_t(gridDim.x) * blockDim.x) {
+    const T xp = tr_shifted_input(a, i);
+    const size_t w = i >> 6;
+    const uint32_t sh = uint32_t(i & 63u);
+    const uint32_t hb = uint32_t(xp >> a.sb) & 1u;
+    const uint32_t bh = a.use_a ? uint32_t((own[w] ^ peer[w]) >> sh) & 1u : 0u;
+    const uint32_t dh = a.use_b ? uint32_t((own[W + w] ^ peer[W + w]) >> sh) & 1u : 0u;
+    msg[i] = a.kind == G_DRELU ? T(hb ^ bh) : tr_out_share(a, p, a.k0, i, xp, hb, bh, dh);
   }
 }
 
@@ -553,6 +609,45 @@ hipError_t launch_tr_eval(const Launch &L, const TrLayout &lay, const uint8_t *k
   });
 }
 
+template <typename T>
+static TrArgs<T> tr_party_args(const TrLayout &lay, const uint8_t *key, const T *xhat, const T *bias,
+                               int bias_ncol) {
+  TrArgs<T> a = tr_args<T>(lay);
+  a.k0 = key;  // the party's own key in both slots
+  a.k1 = key;
+  a.xhat = xhat;
+  a.bias = bias;
+  a.bias_ncol = bias_ncol > 0 ? bias_ncol : 1;
+  return a;
+}
+
+template <typename T>
+hipError_t launch_tr_party_bits(const Launch &L, const TrLayout &lay, const uint8_t *key, const T *xhat,
+                                const T *bias, int bias_ncol, uint64_t *bits) {
+  if (lay.bw != int(8 * sizeof(T)) || L.party < 0) return hipErrorInvalidValue;
+  if (lay.N == 0) return hipSuccess;
+  const TrArgs<T> a = tr_party_args<T>(lay, key, xhat, bias, bias_ncol);
+  return with_variant(L, [&](auto v) {
+    constexpr int NT = decltype(v)::nt, REP = decltype(v)::rep;
+    const int block = variant_block(L);
+    const int grid = grid_for(k_tr_party_bits<T, NT, REP>, block, lay.N, L.num_cu);
+    hipLaunchKernelGGL((k_tr_party_bits<T, NT, REP>), dim3(grid), dim3(block), 0, L.stream, a, bits);
+    return hipGetLastError();
+  });
+}
+
+template <typename T>
+hipError_t launch_tr_party_msg(const Launch &L, const TrLayout &lay, const uint8_t *key, const T *xhat,
+                               const T *bias, int bias_ncol, const uint64_t *own, const uint64_t *peer, T *msg) {
+  if (lay.bw != int(8 * sizeof(T)) || L.party < 0) return hipErrorInvalidValue;
+  if (lay.N == 0) return hipSuccess;
+  const TrArgs<T> a = tr_party_args<T>(lay, key, xhat, bias, bias_ncol);
+  const int block = 256;
+  const int grid = grid_for(k_tr_party_msg<T>, block, lay.N, L.num_cu);
+  hipLaunchKernelGGL((k_tr_party_msg<T>), dim3(grid), dim3(block), 0, L.stream, a, L.party, own, peer, msg);
+  return hipGetLastError();
+}
+
 template <typename T, int NT, int REP>
 __global__ void k_tr_expand(TrArgs<T> a, int p) {
   __shared__ __align__(16) uint32_t lds[AesLds<NT, REP>::kWords];
@@ -696,8 +791,8 @@ hipError_t launch_reveal_keygen(const Launch &L, const RevealLayout &lay, uint64
 
 template <typename T>
 __global__ void k_reveal_eval(size_t n, const T *R0, const T *R1, const T *v0, const T *v1, int rowlen, T *msg0,
-                              T *msg1) {
-  const int p = blockIdx.y;
+                              T *msg1, int pbase) {
+  const int p = int(blockIdx.y) + pbase;
   const T *R = p ? R1 : R0;
   const T *v = p ? v1 : v0;
   T *msg = p ? msg1 : msg0;
@@ -719,8 +814,8 @@ __global__ void k_reveal_eval(size_t n, const T *R0, const T *R1, const T *v0, c
 // depend on the order).
 template <typename T>
 __global__ void k_reveal_rowsum(size_t n, const T *R0, const T *R1, const T *v0, const T *v1, int rowlen, T *msg0,
-                                T *msg1) {
-  const int p = blockIdx.y;
+                                T *msg1, int pbase) {
+  const int p = int(blockIdx.y) + pbase;
   const T *R = p ? R1 : R0;
   const T *v = p ? v1 : v0;
   T *msg = p ? msg1 : msg0;
@@ -742,15 +837,15 @@ hipError_t launch_reveal_eval(const Launch &L, const RevealLayout &lay, const ui
   const int block = 256;
   if (rowlen > 0) {
     int grid = grid_for(k_reveal_rowsum<T>, block, lay.N * 64, L.num_cu);
-    hipLaunchKernelGGL((k_reveal_rowsum<T>), dim3(grid, 2), dim3(block), 0, L.stream, lay.N,
+    hipLaunchKernelGGL((k_reveal_rowsum<T>), dim3(grid, party_rows(L)), dim3(block), 0, L.stream, lay.N,
                        reinterpret_cast<const T *>(k0 + lay.off_r), reinterpret_cast<const T *>(k1 + lay.off_r), v0,
-                       v1, rowlen, msg0, msg1);
+                       v1, rowlen, msg0, msg1, party_base(L));
     return hipGetLastError();
   }
   int grid = grid_for(k_reveal_eval<T>, block, lay.N, L.num_cu);
-  hipLaunchKernelGGL((k_reveal_eval<T>), dim3(grid, 2), dim3(block), 0, L.stream, lay.N,
+  hipLaunchKernelGGL((k_reveal_eval<T>), dim3(grid, party_rows(L)), dim3(block), 0, L.stream, lay.N,
                      reinterpret_cast<const T *>(k0 + lay.off_r), reinterpret_cast<const T *>(k1 + lay.off_r), v0,
-                     v1, rowlen, msg0, msg1);
+                     v1, rowlen, msg0, msg1, party_base(L));
   return hipGetLastError();
 }
 
@@ -828,8 +923,8 @@ hipError_t launch_mul_keygen(const Launch &L, const MulLayout &lay, uint64_t see
 
 template <typename T>
 __global__ void k_mul_eval(size_t nz, const T *Rx0, const T *Rx1, const T *Ry0, const T *Ry1, const T *C0,
-                           const T *C1, MulMap map, const T *xhat, const T *yhat, T *msg0, T *msg1) {
-  const int p = blockIdx.y;
+                           const T *C1, MulMap map, const T *xhat, const T *yhat, T *msg0, T *msg1, int pbase) {
+  const int p = int(blockIdx.y) + pbase;
   const T *Rx = p ? Rx1 : Rx0;
   const T *Ry = p ? Ry1 : Ry0;
   const T *Cc = p ? C1 : C0;
@@ -852,11 +947,11 @@ __global__ void k_mul_eval(size_t nz, const T *Rx0, const T *Rx1, const T *Ry0, 
 // then consecutive elements of A_norm, read and written coalesced.
 template <typename T, int TI>
 __global__ void k_mul_eval_sym(uint32_t N, const T *Rx0, const T *Rx1, const T *Ry0, const T *Ry1, const T *C0,
-                               const T *C1, const T *xhat, const T *yhat, T *msg0, T *msg1) {
+                               const T *C1, const T *xhat, const T *yhat, T *msg0, T *msg1, int pbase) {
   extern __shared__ unsigned char lds_raw[];
   T *Wy = reinterpret_cast<T *>(lds_raw);
   T *Wr = Wy + TI * N;
-  const int p = blockIdx.y;
+  const int p = int(blockIdx.y) + pbase;
   const T *Rx = p ? Rx1 : Rx0;
   const T *Ry = p ? Ry1 : Ry0;
   const T *Cc = p ? C1 : C0;
@@ -905,19 +1000,19 @@ hipError_t launch_mul_eval(const Launch &L, const MulLayout &lay, const uint8_t 
     const size_t tiles = (N + TI - 1) / TI, blocks = (lay.nz / NN) * tiles;
     if (blocks >= (size_t(1) << 31)) return hipErrorInvalidValue;
     const size_t lds = 2 * TI * N * sizeof(T);
-    hipLaunchKernelGGL((k_mul_eval_sym<T, TI>), dim3(unsigned(blocks), 2), dim3(block), lds, L.stream,
+    hipLaunchKernelGGL((k_mul_eval_sym<T, TI>), dim3(unsigned(blocks), party_rows(L)), dim3(block), lds, L.stream,
                        uint32_t(N), reinterpret_cast<const T *>(k0 + lay.off_rx),
                        reinterpret_cast<const T *>(k1 + lay.off_rx), reinterpret_cast<const T *>(k0 + lay.off_ry),
                        reinterpret_cast<const T *>(k1 + lay.off_ry), reinterpret_cast<const T *>(k0 + lay.off_c),
-                       reinterpret_cast<const T *>(k1 + lay.off_c), xhat, yhat, msg0, msg1);
+                       reinterpret_cast<const T *>(k1 + lay.off_c), xhat, yhat, msg0, msg1, party_base(L));
     return hipGetLastError();
   }
   int grid = grid_for(k_mul_eval<T>, block, lay.nz, L.num_cu);
-  hipLaunchKernelGGL((k_mul_eval<T>), dim3(grid, 2), dim3(block), 0, L.stream, lay.nz,
+  hipLaunchKernelGGL((k_mul_eval<T>), dim3(grid, party_rows(L)), dim3(block), 0, L.stream, lay.nz,
                      reinterpret_cast<const T *>(k0 + lay.off_rx), reinterpret_cast<const T *>(k1 + lay.off_rx),
                      reinterpret_cast<const T *>(k0 + lay.off_ry), reinterpret_cast<const T *>(k1 + lay.off_ry),
                      reinterpret_cast<const T *>(k0 + lay.off_c), reinterpret_cast<const T *>(k1 + lay.off_c), map,
-                     xhat, yhat, msg0, msg1);
+                     xhat, yhat, msg0, msg1, party_base(L));
   return hipGetLastError();
 }
 
@@ -975,13 +1070,13 @@ hipError_t launch_lut8_keygen(const Launch &L, const Lut8Layout &lay, uint64_t s
 // leaves) and the signed inner product with the public table rotated by x^.
 template <typename T, int NT, int REP>
 __global__ void k_lut8_phase1(Lut8Layout lay, const uint8_t *k0, const uint8_t *k1,
-                              const T *table, const T *xhat, T *msg0, T *msg1) {
+                              const T *table, const T *xhat, T *msg0, T *msg1, int pbase) {
   __shared__ __align__(16) uint32_t lds[AesLds<NT, REP>::kWords];
   __shared__ T tab[256];
   for (int k = threadIdx.x; k < 256; k += blockDim.x) tab[k] = table[k];
   AesLds<NT, REP>::fill(lds);
   AesLds<NT, REP> aes(lds);
-  const int p = blockIdx.y;
+  const int p = int(blockIdx.y) + pbase;
   const uint8_t *K = p ? k1 : k0;
   T *msg = p ? msg1 : msg0;
   const size_t N = lay.dpf.N;
@@ -1020,16 +1115,16 @@ hipError_t launch_lut8_phase1(const Launch &L, const Lut8Layout &lay, const uint
     constexpr int NT = decltype(v)::nt, REP = decltype(v)::rep;
     int block = variant_block(L);
     int grid = grid_for(k_lut8_phase1<T, NT, REP>, block, lay.dpf.N, L.num_cu);
-    hipLaunchKernelGGL((k_lut8_phase1<T, NT, REP>), dim3(grid, 2), dim3(block), 0, L.stream, lay, k0,
-                       k1, table, xhat, msg0, msg1);
+    hipLaunchKernelGGL((k_lut8_phase1<T, NT, REP>), dim3(grid, party_rows(L)), dim3(block), 0, L.stream, lay, k0,
+                       k1, table, xhat, msg0, msg1, party_base(L));
     return hipGetLastError();
   });
 }
 
 template <typename T>
 __global__ void k_lut8_phase2(Lut8Layout lay, const uint8_t *k0, const uint8_t *k1, const T *vhat, T *msg0,
-                              T *msg1) {
-  const int p = blockIdx.y;
+                              T *msg1, int pbase) {
+  const int p = int(blockIdx.y) + pbase;
   const uint8_t *K = p ? k1 : k0;
   T *msg = p ? msg1 : msg0;
   const size_t N = lay.dpf.N;
@@ -1042,7 +1137,8 @@ hipError_t launch_lut8_phase2(const Launch &L, const Lut8Layout &lay, const uint
                               const T *vhat, T *msg0, T *msg1) {
   const int block = 256;
   int grid = grid_for(k_lut8_phase2<T>, block, lay.dpf.N, L.num_cu);
-  hipLaunchKernelGGL((k_lut8_phase2<T>), dim3(grid, 2), dim3(block), 0, L.stream, lay, k0, k1, vhat, msg0, msg1);
+  hipLaunchKernelGGL((k_lut8_phase2<T>), dim3(grid, party_rows(L)), dim3(block), 0, L.stream, lay, k0, k1, vhat, msg0,
+                     msg1, party_base(L));
   return hipGetLastError();
 }
 
@@ -1829,6 +1925,10 @@ hipError_t launch_rowsum(const Launch &L, size_t rows, int len, const T *a, T *o
                                           uint8_t *);                                                                \
   template hipError_t launch_tr_eval<T>(const Launch &, const TrLayout &, const uint8_t *, const uint8_t *,          \
                                         const T *, const T *, int, T *);                                             \
+  template hipError_t launch_tr_party_bits<T>(const Launch &, const TrLayout &, const uint8_t *, const T *,         \
+                                              const T *, int, uint64_t *);                                           \
+  template hipError_t launch_tr_party_msg<T>(const Launch &, const TrLayout &, const uint8_t *, const T *,          \
+                                             const T *, int, const uint64_t *, const uint64_t *, T *);               \
   template hipError_t launch_reconstruct<T>(const Launch &, size_t, const T *, const T *, T *);                      \
   template hipError_t launch_local_ars<T>(const Launch &, size_t, int, const T *, const T *, int, T *);              \
   template hipError_t launch_reveal_keygen<T>(const Launch &, const RevealLayout &, uint64_t, uint32_t, T *,         \

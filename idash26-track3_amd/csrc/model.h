@@ -29,6 +29,8 @@
 
 namespace mpcx {
 
+class Peer;
+
 struct ModelDims {
   int n_nodes = 140, feat = 78;
   int gcn[3] = {78, 156, 312};
@@ -114,6 +116,11 @@ class ModelBase {
   virtual hipError_t forward(int B) = 0;
   virtual hipError_t output(int64_t *h_out, int B) = 0;
   virtual uint8_t *arena(int party) = 0;
+  // Party mode (one party per process or thread; party -1: both parties here).
+  virtual hipError_t set_party(int party, Peer *peer) = 0;
+  virtual int party() const = 0;
+  virtual hipError_t import_party_key(int B, const void *key, size_t bytes) = 0;
+  virtual hipError_t set_party_inputs(int B, const void *x, const void *a, const void *m, const int64_t *prot) = 0;
   Counters counters;
   Phase1Timer timer;
   StreamStats stream_stats;
@@ -158,6 +165,11 @@ class LaneSet {
                         const void *m1, const int64_t *prot);
   hipError_t forward(int B);
   hipError_t output(int64_t *h_out, int B);
+  // Party mode: one lane only.
+  hipError_t set_party(int party, Peer *peer);
+  int party() const { return lane_.empty() ? -1 : lane_[0]->party(); }
+  hipError_t import_party_key(int B, const void *key, size_t bytes);
+  hipError_t set_party_inputs(int B, const void *x, const void *a, const void *m, const int64_t *prot);
   // Per-launch timing of the DCF-evaluation kernels.  A profiled forward runs
   // the lanes one after another, so every launch is timed alone.
   void profile(bool on);
@@ -206,5 +218,29 @@ void adjnorm_cache_free(AdjNormCache *cache);
 hipError_t adjnorm_eval(int bw, int s, int B, int N, int nmax, int lanes, const Launch &L, const uint8_t *k0,
                         const uint8_t *k1, const void *a0, const void *a1, void *out_masked, Counters *ctr,
                         AdjNormCache **cache);
+
+// ---------------- standalone gates in party mode ----------------
+// One party's evaluation of one gate (L.party = 0 or 1) with the exchanges
+// through `peer`: the party's key of the gate (laid out from offset 0), its
+// share or the masked public input, the reconstructed masked output (the same
+// on both parties).  *w keeps the device workspace between calls (created on
+// first use; free with party_work_free).  Each call synchronises L.stream.
+struct PartyWork;
+void party_work_free(PartyWork *w);
+hipError_t party_tr_eval(PartyWork **w, const Launch &L, Peer *peer, Counters *ctr, int bw, int s, int kind,
+                         size_t n, const uint8_t *key, const void *x, const void *bias, int ncol, void *y);
+hipError_t party_mul_eval(PartyWork **w, const Launch &L, Peer *peer, Counters *ctr, int bw, int s, size_t nx,
+                          size_t ny, size_t nz, const uint32_t *ia, const uint32_t *ib, const uint8_t *key,
+                          const void *x, const void *y, void *z);
+hipError_t party_lut8_eval(PartyWork **w, const Launch &L, Peer *peer, Counters *ctr, int bw, int s, size_t n,
+                           const uint8_t *key, const void *table, const void *x, void *y);
+hipError_t party_sxs_eval(PartyWork **w, const Launch &L, Peer *peer, Counters *ctr, int bw, int s, int nb, int M,
+                          int K, int N, const uint8_t *key, const void *a, const void *b, void *c);
+// v: this party's additive share; vhat = v0 + v1 + mask
+hipError_t party_reveal_eval(PartyWork **w, const Launch &L, Peer *peer, Counters *ctr, int bw, int s, size_t n,
+                             const uint8_t *key, const void *v, void *vhat);
+// d: this party's additive share in, the sum of both parties' shares out
+hipError_t party_reconstruct(PartyWork **w, const Launch &L, Peer *peer, Counters *ctr, int bw, int s, size_t n,
+                             void *d);
 
 }  // namespace mpcx

@@ -18,6 +18,7 @@
 #include <thread>
 
 #include "model.h"
+#include "peer.h"
 
 namespace mpcx {
 
@@ -123,9 +124,12 @@ struct KeySource {
 
 // Exchange buffers shared by the gates: both parties' messages (the
 // truncation-family gates exchange through LDS inside their one launch).
+// In party mode (one process per party) m0 holds this party's message and m1
+// the peer's, and b0 / b1 the two parties' DCF output-bit planes.
 template <typename T>
 struct Workspace {
   DevBuf<T> m0, m1;
+  DevBuf<uint64_t> b0, b1;
   size_t cap = 0;
   hipError_t ensure(size_t n) {
     if (n <= cap) return hipSuccess;
@@ -133,6 +137,10 @@ struct Workspace {
     TRY(m1.alloc(n));
     cap = n;
     return hipSuccess;
+  }
+  hipError_t ensure_bits(size_t words) {
+    TRY(b0.alloc(words));
+    return b1.alloc(words);
   }
 };
 
@@ -149,9 +157,23 @@ struct Runner {
   KeySource &src;
   KeyView kv;
   Cursor c;
+  // Party mode (L.party = 0 or 1): only this party's kernels run; its key is
+  // kv.k[L.party] and each exchange goes through the peer.
+  Peer *peer = nullptr;
 
-  Runner(const Launch &L_, int bw_, int s_, Workspace<T> &ws_, Counters &ctr_, Phase1Timer *t, KeySource &src_)
-      : L(L_), bw(bw_), s(s_), ws(ws_), ctr(ctr_), timer(t), src(src_) {}
+  Runner(const Launch &L_, int bw_, int s_, Workspace<T> &ws_, Counters &ctr_, Phase1Timer *t, KeySource &src_,
+         Peer *peer_ = nullptr)
+      : L(L_), bw(bw_), s(s_), ws(ws_), ctr(ctr_), timer(t), src(src_), peer(peer_) {}
+
+  bool party_mode() const { return L.party >= 0; }
+  const uint8_t *own_key() const { return kv.k[L.party]; }
+  // party mode: send this party's message (ws.m0), receive the peer's (ws.m1),
+  // and reconstruct out = m0 + m1
+  hipError_t exchange_reconstruct(size_t n, T *out) {
+    const Peer::Seg seg{ws.m0.p, ws.m1.p, n * sizeof(T)};
+    TRY(peer->exchange(L.stream, &seg, 1));
+    return launch_reconstruct<T>(L, n, ws.m0.p, ws.m1.p, out);
+  }
 
   // Make the gate [c.off, end) available; returns the base of the gate
   // relative to the key view.
@@ -170,11 +192,36 @@ struct Runner {
     size_t b;
     TRY(enter(end, &b));
     RevealLayout lay = reveal_layout(bw, n, b);
-    TRY(launch_reveal_eval<T>(L, lay, kv.k[0], kv.k[1], v0, v1, rowlen, ws.m0.p, ws.m1.p));
     ctr.msg(n, bw);
-    TRY(launch_reconstruct<T>(L, n, ws.m0.p, ws.m1.p, out));
+    if (party_mode()) {  // this party's share only (v0 or v1 by party)
+      const T *v = L.party ? v1 : v0;
+      TRY(launch_reveal_eval<T>(L, lay, own_key(), own_key(), v, v, rowlen, ws.m0.p, ws.m0.p));
+      TRY(exchange_reconstruct(n, out));
+    } else {
+      TRY(launch_reveal_eval<T>(L, lay, kv.k[0], kv.k[1], v0, v1, rowlen, ws.m0.p, ws.m1.p));
+      TRY(launch_reconstruct<T>(L, n, ws.m0.p, ws.m1.p, out));
+    }
     leave(end);
     return hipSuccess;
+  }
+
+  // party mode: the truncation-family gate in two launches around the two
+  // exchanges (bit planes, then messages)
+  hipError_t tr_party(const TrLayout &lay, size_t n, const T *x, const T *bias, int ncol, T *out) {
+    const size_t W = (n + 63) / 64;
+    TRY(ws.ensure_bits(2 * W));
+    TRY(launch_tr_party_bits<T>(L, lay, own_key(), x, bias, ncol, ws.b0.p));
+    // each plane goes on the wire as ceil(n/32) 32-bit words
+    const size_t pb = ((n + 31) / 32) * 4;
+    Peer::Seg seg[2];
+    int ns = 0;
+    if (lay.use_a) seg[ns++] = Peer::Seg{ws.b0.p, ws.b1.p, pb};
+    if (lay.use_b) seg[ns++] = Peer::Seg{ws.b0.p + W, ws.b1.p + W, pb};
+    TRY(peer->exchange(L.stream, seg, ns));
+    if (lay.kind == G_DRELU)  // the output bit is public now
+      return launch_tr_party_msg<T>(L, lay, own_key(), x, bias, ncol, ws.b0.p, ws.b1.p, out);
+    TRY(launch_tr_party_msg<T>(L, lay, own_key(), x, bias, ncol, ws.b0.p, ws.b1.p, ws.m0.p));
+    return exchange_reconstruct(n, out);
   }
 
   hipError_t tr(int kind, size_t n, const T *x, const T *bias, int ncol, T *out) {
@@ -190,7 +237,10 @@ struct Runner {
       TRY(hipEventRecord(e0, L.stream));
       L1.profiled = true;
     }
-    TRY(launch_tr_eval<T>(L1, lay, kv.k[0], kv.k[1], x, bias, ncol, out));
+    if (party_mode())
+      TRY(tr_party(lay, n, x, bias, ncol, out));
+    else
+      TRY(launch_tr_eval<T>(L1, lay, kv.k[0], kv.k[1], x, bias, ncol, out));
     if (timer && timer->on) {
       TRY(hipEventRecord(e1, L.stream));
       timer->ev.push_back(e0);
@@ -219,9 +269,14 @@ struct Runner {
     size_t b;
     TRY(enter(end, &b));
     MulLayout lay = mul_layout(bw, nx, ny, nz, b);
-    TRY(launch_mul_eval<T>(L, lay, kv.k[0], kv.k[1], map, x, y, ws.m0.p, ws.m1.p));
     ctr.msg(nz, bw);
-    TRY(launch_reconstruct<T>(L, nz, ws.m0.p, ws.m1.p, out));
+    if (party_mode()) {
+      TRY(launch_mul_eval<T>(L, lay, own_key(), own_key(), map, x, y, ws.m0.p, ws.m0.p));
+      TRY(exchange_reconstruct(nz, out));
+    } else {
+      TRY(launch_mul_eval<T>(L, lay, kv.k[0], kv.k[1], map, x, y, ws.m0.p, ws.m1.p));
+      TRY(launch_reconstruct<T>(L, nz, ws.m0.p, ws.m1.p, out));
+    }
     leave(end);
     return hipSuccess;
   }
@@ -232,6 +287,16 @@ struct Runner {
     size_t b;
     TRY(enter(end, &b));
     Lut8Layout lay = lut8_layout(bw, n, b);
+    if (party_mode()) {
+      ctr.msg(n, bw);
+      ctr.msg(n, bw);
+      TRY(launch_lut8_phase1<T>(L, lay, own_key(), own_key(), table, x, ws.m0.p, ws.m0.p));
+      TRY(exchange_reconstruct(n, vh));
+      TRY(launch_lut8_phase2<T>(L, lay, own_key(), own_key(), vh, ws.m0.p, ws.m0.p));
+      TRY(exchange_reconstruct(n, out));
+      leave(end);
+      return hipSuccess;
+    }
     TRY(launch_lut8_phase1<T>(L, lay, kv.k[0], kv.k[1], table, x, ws.m0.p, ws.m1.p));
     ctr.msg(n, bw);
     TRY(launch_reconstruct<T>(L, n, ws.m0.p, ws.m1.p, vh));
@@ -276,10 +341,19 @@ struct Runner {
     h.Cin = reinterpret_cast<const T *>(K1 + lay.off_c);
     h.C = ws.m1.p;
     h.sign = -1;
-    TRY(launch_gemm_pair<T>(L, g, h));
-    TRY(span.end());
     const size_t nc = size_t(nb) * M * N;
     ctr.msg(nc, bw);
+    if (party_mode()) {  // this party's product only, into m0
+      GemmArgs<T> &mine = L.party ? h : g;
+      mine.C = ws.m0.p;
+      TRY(launch_gemm<T>(L, mine));
+      TRY(span.end());
+      TRY(exchange_reconstruct(nc, out));
+      leave(end);
+      return hipSuccess;
+    }
+    TRY(launch_gemm_pair<T>(L, g, h));
+    TRY(span.end());
     TRY(launch_reconstruct<T>(L, nc, ws.m0.p, ws.m1.p, out));
     leave(end);
     return hipSuccess;
@@ -675,7 +749,8 @@ class Model final : public ModelBase, KeySource {
     size_t need = key_bytes(B);
     if (need <= arena_bytes_) return hipSuccess;
     free_arena();
-    for (int p = 0; p < 2; p++) TRY(hipMalloc((void **)&arena_[p], need));
+    for (int p = 0; p < 2; p++)  // party mode: this party's key only
+      if (party_ < 0 || p == party_) TRY(hipMalloc((void **)&arena_[p], need));
     arena_bytes_ = need;
     return hipSuccess;
   }
@@ -723,6 +798,7 @@ class Model final : public ModelBase, KeySource {
   }
 
   hipError_t keygen(int B, uint64_t seed) override {
+    if (party_ >= 0) return hipErrorNotSupported;  // the dealer holds both parties' keys
     TRY(leave_stream());
     keyed_B_ = -1;  // until the new keys are complete
     TRY(hipStreamSynchronize(L_.stream));  // a running forward may still read the arena
@@ -817,6 +893,7 @@ class Model final : public ModelBase, KeySource {
   }
 
   hipError_t import_keys(int B, const void *k0, const void *k1, size_t bytes) override {
+    if (party_ >= 0) return hipErrorNotSupported;
     if (bytes != key_bytes(B)) return hipErrorInvalidValue;
     TRY(leave_stream());
     TRY(hipStreamSynchronize(L_.stream));  // a running forward may still read the arena
@@ -1216,6 +1293,11 @@ class Model final : public ModelBase, KeySource {
     if (gi_ >= gates_.size() || gates_[gi_].begin != begin || gates_[gi_].end != end)
       return hipErrorUnknown;  // forward walked off the plan
     const int k = chunk_of_[gi_++];
+    if (party_ >= 0) {  // this party's key in both slots
+      kv->k[0] = kv->k[1] = arena_[party_];
+      kv->begin = 0;
+      return hipSuccess;
+    }
     if (!streaming_) {
       kv->k[0] = arena_[0];
       kv->k[1] = arena_[1];
@@ -1237,9 +1319,65 @@ class Model final : public ModelBase, KeySource {
     return hipSuccess;
   }
 
+  // ---------------- party mode ----------------
+  // One party per process (or thread): only this party's key, shares and kernels,
+  // every exchange through the peer.  party = -1 returns to both parties in one
+  // process.  Drops keys and inputs.
+  hipError_t set_party(int party, Peer *peer) override {
+    if (party < -1 || party > 1 || (party >= 0 && !peer)) return hipErrorInvalidValue;
+    if (files_ || streaming_) {
+      stop_io();
+      TRY(leave_stream());
+    }
+    TRY(hipStreamSynchronize(L_.stream));
+    drop_graph();
+    free_arena();
+    keyed_B_ = input_B_ = -1;
+    have_pk_ = false;
+    party_ = party;
+    peer_ = party >= 0 ? peer : nullptr;
+    L_.party = party;
+    return hipSuccess;
+  }
+  int party() const override { return party_; }
+  hipError_t import_party_key(int B, const void *key, size_t bytes) override {
+    if (party_ < 0) return hipErrorNotSupported;
+    if (bytes != key_bytes(B)) return hipErrorInvalidValue;
+    TRY(hipStreamSynchronize(L_.stream));
+    keyed_B_ = -1;
+    TRY(ensure_arena(B));
+    TRY(hipMemcpy(arena_[party_], key, bytes, hipMemcpyHostToDevice));
+    keyed_B_ = B;
+    return hipSuccess;
+  }
+  // This party's shares of x, A and the atom mask; prot: the protein embedding
+  // (the party that owns it, party 1 in the reference's deployment) or null
+  // (zeros: the other party's share of it).
+  hipError_t set_party_inputs(int B, const void *x, const void *a, const void *m, const int64_t *prot) override {
+    if (party_ < 0) return hipErrorNotSupported;
+    const int N = d_.n_nodes;
+    const size_t BN = size_t(B) * N, nx = BN * d_.feat, na = BN * N;
+    TRY(hipStreamSynchronize(L_.stream));
+    DevBuf<T> &xb = party_ ? x1_ : x0_, &ab = party_ ? a1_ : a0_, &mb = party_ ? m1_ : m0_;
+    TRY(xb.alloc(nx));
+    TRY(ab.alloc(na));
+    TRY(mb.alloc(BN));
+    TRY(prot_.alloc(size_t(B) * d_.prot));
+    TRY(hipMemcpy(xb.p, x, nx * sizeof(T), hipMemcpyHostToDevice));
+    TRY(hipMemcpy(ab.p, a, na * sizeof(T), hipMemcpyHostToDevice));
+    TRY(hipMemcpy(mb.p, m, BN * sizeof(T), hipMemcpyHostToDevice));
+    std::vector<T> pr(size_t(B) * d_.prot, T(0));
+    if (prot)
+      for (size_t i = 0; i < pr.size(); i++) pr[i] = T(uint64_t(prot[i]));
+    TRY(hipMemcpy(prot_.p, pr.data(), pr.size() * sizeof(T), hipMemcpyHostToDevice));
+    input_B_ = B;
+    return hipSuccess;
+  }
+
   // ---------------- inputs ----------------
   hipError_t set_inputs(int B, const void *x0, const void *x1, const void *a0, const void *a1, const void *m0,
                         const void *m1, const int64_t *prot) override {
+    if (party_ >= 0) return hipErrorNotSupported;
     const int N = d_.n_nodes;
     const size_t BN = size_t(B) * N, nx = BN * d_.feat, na = BN * N;
     TRY(hipStreamSynchronize(L_.stream));  // earlier forwards read these buffers
@@ -1313,6 +1451,7 @@ class Model final : public ModelBase, KeySource {
   }
 
   hipError_t forward(int B) override {
+    if (party_ >= 0) return forward_body(B);  // host-driven exchanges: no graph
     if (!files_ && !streaming_ && !timer.on && L_.graph) return forward_graph(B);
     if (!files_) return forward_body(B);
     if (keyed_B_ != B || input_B_ != B) return hipErrorInvalidValue;
@@ -1351,7 +1490,7 @@ class Model final : public ModelBase, KeySource {
       TRY(issue_copy(0));
       if (chunks_.size() > 1) TRY(issue_copy(1));
     }
-    Runner<T> r(L_, bw_, s_, ws_, counters, &timer, *this);
+    Runner<T> r(L_, bw_, s_, ws_, counters, &timer, *this, peer_);
     auto pub_gemm = [&](const T *x, int l, size_t rows, T *y) -> hipError_t {
       int in, out;
       layer_io(l, &in, &out);
@@ -1412,9 +1551,18 @@ class Model final : public ModelBase, KeySource {
     TRY(trunc_eval(r, true, size_t(B) * d_.dfc[0], Z, bias_[3].p, d_.dfc[0], XW));
     TRY(pub_gemm(XW, 4, B, Z));
     TRY(trunc_eval(r, false, size_t(B) * d_.dfc[1], Z, bias_[4].p, d_.dfc[1], XW));
-    // concat [drug, protein]; the protein embedding owner reveals it (one message)
+    // concat [drug, protein]; the protein embedding owner reveals it (one message
+    // each way: the other party's share is zero, revealPublicLeaf,
+    // ddg_orca_base.h:84-89)
     counters.msg(size_t(B) * d_.prot, bw);
-    TRY(launch_concat<T>(L_, B, d_.dfc[1], d_.prot, XW, prot_.p, H));
+    const T *prot_pub = prot_.p;
+    if (party_ >= 0) {
+      const size_t np = size_t(B) * d_.prot;
+      TRY(hipMemcpyAsync(ws_.m0.p, prot_.p, np * sizeof(T), hipMemcpyDeviceToDevice, L_.stream));
+      TRY(r.exchange_reconstruct(np, Z));
+      prot_pub = Z;
+    }
+    TRY(launch_concat<T>(L_, B, d_.dfc[1], d_.prot, XW, prot_pub, H));
     T *h = H, *h2 = XW;
     for (int k = 0; k < d_.nfus; k++) {
       TRY(pub_gemm(h, 5 + k, B, Z));
@@ -1440,6 +1588,8 @@ class Model final : public ModelBase, KeySource {
   int bw_, s_;
   ModelDims d_;
   Launch L_;
+  int party_ = -1;       // party mode: this process's party
+  Peer *peer_ = nullptr;  // party mode: the channel to the other party
   std::vector<DevBuf<T>> wt_, bias_;
   std::vector<std::vector<int64_t>> hbias_;
   uint8_t *arena_[2] = {nullptr, nullptr};
@@ -1798,6 +1948,28 @@ hipError_t LaneSet::forward(int B) {
   return hipSuccess;
 }
 
+hipError_t LaneSet::set_party(int party, Peer *peer) {
+  if (party >= 0 && lane_.size() != 1) {
+    err = "party mode runs one lane";
+    return hipErrorInvalidValue;
+  }
+  keyed_B_ = -1;
+  close_files();
+  return lane_[0]->set_party(party, peer);
+}
+
+hipError_t LaneSet::import_party_key(int B, const void *key, size_t bytes) {
+  if (party() < 0) return hipErrorNotSupported;
+  TRY(lane_[0]->import_party_key(B, key, bytes));
+  keyed_B_ = B;
+  return hipSuccess;
+}
+
+hipError_t LaneSet::set_party_inputs(int B, const void *x, const void *a, const void *m, const int64_t *prot) {
+  if (party() < 0) return hipErrorNotSupported;
+  return lane_[0]->set_party_inputs(B, x, a, m, prot);
+}
+
 hipError_t LaneSet::output(int64_t *h_out, int B) {
   return each(B, [&](int i, int Bi, int off) { return lane_[i]->output(h_out + off, Bi); });
 }
@@ -2008,5 +2180,138 @@ hipError_t adjnorm_eval(int bw, int s, int B, int N, int nmax, int lanes, const 
   return bw == 32 ? adjnorm_eval_t<uint32_t>(bw, s, B, N, nmax, lanes, L, k0, k1, a0, a1, out, ctr, cache)
                   : adjnorm_eval_t<uint64_t>(bw, s, B, N, nmax, lanes, L, k0, k1, a0, a1, out, ctr, cache);
 }
+
+// ---------------------------------------------------------------------------
+// standalone gates in party mode (one party per process or thread)
+// ---------------------------------------------------------------------------
+struct PartyWork {
+  Workspace<uint32_t> w32;
+  Workspace<uint64_t> w64;
+  DevBuf<uint32_t> v32;  // the LUT's revealed intermediate
+  DevBuf<uint64_t> v64;
+};
+void party_work_free(PartyWork *w) { delete w; }
+
+namespace {
+template <typename T>
+Workspace<T> &party_ws(PartyWork &w);
+template <>
+Workspace<uint32_t> &party_ws<uint32_t>(PartyWork &w) {
+  return w.w32;
+}
+template <>
+Workspace<uint64_t> &party_ws<uint64_t>(PartyWork &w) {
+  return w.w64;
+}
+template <typename T>
+DevBuf<T> &party_tmp(PartyWork &w);
+template <>
+DevBuf<uint32_t> &party_tmp<uint32_t>(PartyWork &w) {
+  return w.v32;
+}
+template <>
+DevBuf<uint64_t> &party_tmp<uint64_t>(PartyWork &w) {
+  return w.v64;
+}
+
+// One gate of party L.party over its key (laid out from offset 0), messages of
+// nmsg elements; synchronises the stream at the end.
+template <typename T, class Fn>
+hipError_t party_gate(PartyWork **w, const Launch &L, Peer *peer, Counters *ctr, int bw, int s, const uint8_t *key,
+                      size_t key_bytes, size_t nmsg, Fn &&fn) {
+  if (L.party < 0 || L.party > 1 || !peer) return hipErrorInvalidValue;
+  if (!*w) *w = new PartyWork();
+  Workspace<T> &ws = party_ws<T>(**w);
+  TRY(ws.ensure(nmsg));
+  ArenaSource src;
+  src.k[0] = src.k[1] = key;
+  src.bytes = key_bytes;
+  Runner<T> r(L, bw, s, ws, *ctr, nullptr, src, peer);
+  TRY(fn(r, **w));
+  return hipStreamSynchronize(L.stream);
+}
+template <typename T>
+const T *cp(const void *p) {
+  return static_cast<const T *>(p);
+}
+template <typename T>
+T *mp(void *p) {
+  return static_cast<T *>(p);
+}
+}  // namespace
+
+#define PARTY_DISPATCH(bw, CALL) ((bw) == 32 ? CALL(uint32_t) : CALL(uint64_t))
+
+hipError_t party_tr_eval(PartyWork **w, const Launch &L, Peer *peer, Counters *ctr, int bw, int s, int kind,
+                         size_t n, const uint8_t *key, const void *x, const void *bias, int ncol, void *y) {
+  const size_t kb = tr_layout(kind, bw, s, n, 0).end;
+#define CALL(T)                                                                                       \
+  party_gate<T>(w, L, peer, ctr, bw, s, key, kb, n, [&](Runner<T> &r, PartyWork &) {                  \
+    return r.tr(kind, n, cp<T>(x), cp<T>(bias), ncol, mp<T>(y));                                        \
+  })
+  return PARTY_DISPATCH(bw, CALL);
+#undef CALL
+}
+
+hipError_t party_mul_eval(PartyWork **w, const Launch &L, Peer *peer, Counters *ctr, int bw, int s, size_t nx,
+                          size_t ny, size_t nz, const uint32_t *ia, const uint32_t *ib, const uint8_t *key,
+                          const void *x, const void *y, void *z) {
+  const size_t kb = mul_layout(bw, nx, ny, nz, 0).end;
+#define CALL(T)                                                                                       \
+  party_gate<T>(w, L, peer, ctr, bw, s, key, kb, nz, [&](Runner<T> &r, PartyWork &) {                 \
+    return r.mul(nx, ny, nz, MulMap::explicit_maps(ia, ib), cp<T>(x), cp<T>(y), mp<T>(z));              \
+  })
+  return PARTY_DISPATCH(bw, CALL);
+#undef CALL
+}
+
+hipError_t party_lut8_eval(PartyWork **w, const Launch &L, Peer *peer, Counters *ctr, int bw, int s, size_t n,
+                           const uint8_t *key, const void *table, const void *x, void *y) {
+  const size_t kb = lut8_layout(bw, n, 0).end;
+#define CALL(T)                                                                                       \
+  party_gate<T>(w, L, peer, ctr, bw, s, key, kb, n, [&](Runner<T> &r, PartyWork &pw) -> hipError_t {  \
+    DevBuf<T> &vh = party_tmp<T>(pw);                                                                   \
+    TRY(vh.alloc(n));                                                                                   \
+    return r.lut8(n, cp<T>(table), cp<T>(x), vh.p, mp<T>(y));                                           \
+  })
+  return PARTY_DISPATCH(bw, CALL);
+#undef CALL
+}
+
+hipError_t party_sxs_eval(PartyWork **w, const Launch &L, Peer *peer, Counters *ctr, int bw, int s, int nb, int M,
+                          int K, int N, const uint8_t *key, const void *a, const void *b, void *c) {
+  const size_t kb = sxs_layout(bw, nb, M, K, N, 0).end;
+  const size_t nc = size_t(nb) * M * N;
+#define CALL(T)                                                                                       \
+  party_gate<T>(w, L, peer, ctr, bw, s, key, kb, nc, [&](Runner<T> &r, PartyWork &) {                 \
+    return r.sxs(nb, M, K, N, cp<T>(a), cp<T>(b), mp<T>(c));                                            \
+  })
+  return PARTY_DISPATCH(bw, CALL);
+#undef CALL
+}
+
+hipError_t party_reveal_eval(PartyWork **w, const Launch &L, Peer *peer, Counters *ctr, int bw, int s, size_t n,
+                             const uint8_t *key, const void *v, void *vhat) {
+  const size_t kb = reveal_layout(bw, n, 0).end;
+#define CALL(T)                                                                                       \
+  party_gate<T>(w, L, peer, ctr, bw, s, key, kb, n, [&](Runner<T> &r, PartyWork &) {                  \
+    return r.reveal(n, cp<T>(v), cp<T>(v), 0, mp<T>(vhat));                                             \
+  })
+  return PARTY_DISPATCH(bw, CALL);
+#undef CALL
+}
+
+hipError_t party_reconstruct(PartyWork **w, const Launch &L, Peer *peer, Counters *ctr, int bw, int s, size_t n,
+                             void *d) {
+#define CALL(T)                                                                                       \
+  party_gate<T>(w, L, peer, ctr, bw, s, nullptr, 0, n, [&](Runner<T> &r, PartyWork &) -> hipError_t {  \
+    TRY(hipMemcpyAsync(r.ws.m0.p, d, n * sizeof(T), hipMemcpyDeviceToDevice, L.stream));               \
+    ctr->msg(n, bw);                                                                                    \
+    return r.exchange_reconstruct(n, mp<T>(d));                                                         \
+  })
+  return PARTY_DISPATCH(bw, CALL);
+#undef CALL
+}
+#undef PARTY_DISPATCH
 
 }  // namespace mpcx

@@ -1,0 +1,78 @@
+// peer.h -- one party's end of the two-party channel (one process, or one
+// thread, per party).
+//
+// Replaces the reference's GpuPeer / SigmaPeer (gpu_mpc/utils/gpu_comms.h:94-397,
+// gpu_mpc/utils/sigma_comms.cpp:36-150): a connected stream socket between the
+// two parties, a background sender so that both parties can send a large message
+// at the same time, and device <-> pinned-host staging around each exchange.
+// Messages are sent exactly as counted: ring elements at their width, bit planes
+// packed 32 per 32-bit word (the reference's bit-packed wire format for bit
+// outputs, gpu_comms.h:28-73).
+#pragma once
+#include <hip/hip_runtime.h>
+
+#include <condition_variable>
+#include <cstddef>
+#include <cstdint>
+#include <mutex>
+#include <string>
+#include <thread>
+
+namespace mpcx {
+
+class Peer {
+ public:
+  // One region of an exchange: `bytes` of device memory `send` go to the peer,
+  // the peer's matching region lands in device memory `recv`.
+  struct Seg {
+    const void *send;
+    void *recv;
+    size_t bytes;
+  };
+
+  Peer(int fd, int party);
+  ~Peer();
+  Peer(const Peer &) = delete;
+  Peer &operator=(const Peer &) = delete;
+
+  int party() const { return party_; }
+  // Synchronises `stream` (the messages were produced on it), sends the
+  // segments back to back, receives the peer's, and enqueues their copies into
+  // the recv regions on `stream`.  hipErrorNotReady: the channel failed (peer
+  // gone, timeout); the peer is unusable afterwards.
+  hipError_t exchange(hipStream_t stream, const Seg *segs, int nseg);
+  uint64_t bytes_sent() const { return sent_; }
+  uint64_t bytes_received() const { return recv_; }
+  uint64_t rounds() const { return rounds_; }
+  const std::string &error() const { return err_; }
+
+ private:
+  hipError_t ensure(size_t bytes);
+  void sender_loop();
+  bool send_all(const uint8_t *p, size_t n);
+  bool recv_all(uint8_t *p, size_t n);
+
+  int fd_ = -1, party_ = 0;
+  uint8_t *hs_ = nullptr, *hr_ = nullptr;  // pinned staging (send, receive)
+  size_t cap_ = 0;
+  uint64_t sent_ = 0, recv_ = 0, rounds_ = 0;
+  bool broken_ = false;
+  std::string err_;
+  // background sender: one job at a time
+  std::thread th_;
+  std::mutex mu_;
+  std::condition_variable cv_;
+  const uint8_t *job_ = nullptr;
+  size_t job_n_ = 0;
+  bool job_ready_ = false, job_done_ = true, job_ok_ = true, stop_ = false;
+};
+
+// Party 0 listens on the Unix socket `path` and accepts one connection; party 1
+// connects to it (retrying until timeout_ms).  Receives time out after
+// io_timeout_ms of silence.
+hipError_t peer_connect(int party, const std::string &path, int timeout_ms, int io_timeout_ms, Peer **out,
+                        std::string *err);
+// Both ends of a socket pair (two parties as two threads of one process).
+hipError_t peer_pair(int io_timeout_ms, Peer **p0, Peer **p1, std::string *err);
+
+}  // namespace mpcx

@@ -10,14 +10,21 @@
 //     role 1  evaluator: reads those key files and the shares of <shareDir>,
 //             runs the online forward (both parties in this process)
 //     role 2  dealer and evaluator in one run (keys stay resident in HBM)
+//     role 3  one party's evaluator (the reference's deployment: two such
+//             processes, gpu_mpc/run_local_2pc.sh:196-233): reads its own key
+//             file and share files, exchanges with the other party's process over
+//             the Unix socket MPCX_PEER (party 0 listens, party 1 connects);
+//             party MPCX_PARTY (0 or 1); party 1 reads protein_emb.dat
 //   environment: MPCX_WEIGHTS_BIN (default ./weights.bin), MPCX_SEED (dealer
 //   seed, default 12345), MPCX_LANES (concurrent sub-batches, default 1),
 //   MPCX_LUT_NMAX (largest degree with a D^-1/2 table entry, default 138),
 //   MPCX_SLACK (slack truncations of the GCN, 0 / 1 / 2, default 0: exact).
 //
-// Differences from the reference driver: one process evaluates both parties
-// (no peer address), so "Comm (B)" is the bytes both parties would exchange per
-// forward (both directions); the dealer's keys are this library's format.
+// Differences from the reference driver: roles 1 and 2 evaluate both parties in
+// one process (no peer address), and "Comm (B)" is the bytes both parties
+// exchange per forward (both directions), as it is for role 3, which also prints
+// the bytes that crossed its socket ("Peer (B)"); the dealer's keys are this
+// library's format.
 #include <chrono>
 #include <cmath>
 #include <cstdint>
@@ -114,7 +121,9 @@ int main(int argc, char **argv) {
   if (!keyDir.empty() && keyDir.back() != '/') keyDir += '/';
   if (!shareDir.empty() && shareDir.back() != '/') shareDir += '/';
   const int reps = argc > 7 ? std::max(1, std::atoi(argv[7])) : 1;
-  if ((bw != 32 && bw != 64) || role < 0 || role > 2) die("bw must be 32 or 64, role 0, 1 or 2");
+  if ((bw != 32 && bw != 64) || role < 0 || role > 3) die("bw must be 32 or 64, role 0, 1, 2 or 3");
+  const int party = env_int("MPCX_PARTY", -1);
+  if (role == 3 && party != 0 && party != 1) die("role 3 needs MPCX_PARTY=0 or 1");
 
   // weights and the layer shapes of their manifest
   const char *wenv = std::getenv("MPCX_WEIGHTS_BIN");
@@ -168,11 +177,22 @@ int main(int argc, char **argv) {
     if (k0.size() != kbytes || k1.size() != kbytes) die("key files do not hold one key set of this batch");
     check(ctx, mpcx_model_import_keys(m, B, k0.data(), k1.data(), kbytes), "model_import_keys");
   }
-  if (role == 1 || role == 2) {
+  mpcx_peer *peer = nullptr;
+  if (role == 3) {
+    const char *penv = std::getenv("MPCX_PEER");
+    const std::string path = penv && *penv ? penv : "/tmp/mpcx_" + std::to_string(bw) + ".sock";
+    if (mpcx_peer_connect(party, path.c_str(), 60000, &peer) != MPCX_OK) die("no connection to the other party");
+    check(ctx, mpcx_model_set_party(m, peer), "model_set_party");
+    const std::vector<uint8_t> k = read_bytes(kf[party]);
+    if (k.size() != kbytes) die("key file does not hold one key set of this batch");
+    check(ctx, mpcx_model_import_party_key(m, B, k.data(), kbytes), "model_import_party_key");
+  }
+  if (role >= 1) {
     // share files (read by the reference at deepdtagen_inference.cu:426-432)
     const size_t es = size_t(bw / 8), BN = size_t(B) * size_t(N);
     std::vector<uint8_t> x[2], a[2], mk[2];
     for (int p = 0; p < 2; p++) {
+      if (role == 3 && p != party) continue;  // the other party's shares stay with it
       const std::string sfx = "_share" + std::to_string(p) + ".dat";
       x[p] = read_array<uint8_t>(shareDir + "x" + sfx, BN * size_t(feat) * es);
       a[p] = read_array<uint8_t>(shareDir + "adj" + sfx, BN * size_t(N) * es);
@@ -180,7 +200,12 @@ int main(int argc, char **argv) {
       mk[p].resize(BN * es);
       for (size_t r = 0; r < BN; r++) std::memcpy(&mk[p][r * es], &tiled[r * size_t(pool) * es], es);  // column 0
     }
-    const std::vector<uint8_t> pr = read_array<uint8_t>(shareDir + "protein_emb.dat", size_t(B) * size_t(prot) * es);
+    // the protein embedding: public to the evaluator of both parties, party 1's
+    // alone in the two-process deployment (revealed inside the forward)
+    const bool has_prot = role != 3 || party == 1;
+    const std::vector<uint8_t> pr =
+        has_prot ? read_array<uint8_t>(shareDir + "protein_emb.dat", size_t(B) * size_t(prot) * es)
+                 : std::vector<uint8_t>(size_t(B) * size_t(prot) * es, 0);
     std::vector<int64_t> protv(size_t(B) * size_t(prot));
     for (size_t i = 0; i < protv.size(); i++) {
       if (bw == 32) {
@@ -191,22 +216,30 @@ int main(int argc, char **argv) {
         std::memcpy(&protv[i], &pr[i * 8], 8);
       }
     }
-    check(ctx, mpcx_model_set_inputs(m, B, x[0].data(), x[1].data(), a[0].data(), a[1].data(), mk[0].data(),
-                                     mk[1].data(), protv.data()),
-          "model_set_inputs");
+    if (role == 3)
+      check(ctx, mpcx_model_set_party_inputs(m, B, x[party].data(), a[party].data(), mk[party].data(),
+                                             has_prot ? protv.data() : nullptr),
+            "model_set_party_inputs");
+    else
+      check(ctx, mpcx_model_set_inputs(m, B, x[0].data(), x[1].data(), a[0].data(), a[1].data(), mk[0].data(),
+                                       mk[1].data(), protv.data()),
+            "model_set_inputs");
     std::vector<int64_t> out(static_cast<size_t>(B));
     double total_us = 0;
-    uint64_t comm = 0;
+    uint64_t comm = 0, wire = 0;
     for (int r = 0; r < reps; r++) {
       mpcx_reset_counters(ctx);
+      const uint64_t w0 = peer ? mpcx_peer_bytes(peer) : 0;
       const auto t0 = std::chrono::steady_clock::now();
       check(ctx, mpcx_model_forward(m, B), "model_forward");
       check(ctx, mpcx_model_output(m, B, out.data()), "model_output");
       total_us += std::chrono::duration<double, std::micro>(std::chrono::steady_clock::now() - t0).count();
       comm = mpcx_bytes_exchanged(ctx);
+      wire = peer ? mpcx_peer_bytes(peer) - w0 : 0;
     }
     std::printf("Average time taken (microseconds)=%f\n", total_us / reps);
     std::printf("Comm (B)=%llu\n", static_cast<unsigned long long>(comm));
+    if (peer) std::printf("Peer (B)=%llu\n", static_cast<unsigned long long>(wire));
     for (int j = 0; j < B; j++) {
       const double aff = double(out[size_t(j)]) / std::ldexp(1.0, scale);
       if (B == 1)
@@ -216,6 +249,7 @@ int main(int argc, char **argv) {
     }
   }
   mpcx_model_destroy(m);
+  mpcx_peer_close(peer);
   mpcx_destroy(ctx);
   return 0;
 }

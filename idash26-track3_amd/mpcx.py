@@ -110,6 +110,25 @@ _SIGS = {
     "mpcx_host_alloc": (C.c_int, [C.c_size_t, C.c_void_p]),
     "mpcx_host_free": (None, [C.c_void_p]),
     "mpcx_model_profile_read": (C.c_int, [C.c_void_p] + [C.c_void_p] * 5),
+    "mpcx_peer_connect": (C.c_int, [C.c_int, C.c_char_p, C.c_int, C.c_void_p]),
+    "mpcx_peer_pair": (C.c_int, [C.c_int, C.c_void_p, C.c_void_p]),
+    "mpcx_peer_close": (None, [C.c_void_p]),
+    "mpcx_peer_party": (C.c_int, [C.c_void_p]),
+    "mpcx_peer_bytes": (C.c_uint64, [C.c_void_p]),
+    "mpcx_peer_rounds": (C.c_uint64, [C.c_void_p]),
+    "mpcx_peer_error": (C.c_char_p, [C.c_void_p]),
+    "mpcx_party_reconstruct": (C.c_int, [C.c_void_p, C.c_void_p, C.c_size_t, C.c_void_p]),
+    "mpcx_party_tr_eval": (C.c_int, [C.c_void_p, C.c_void_p, C.c_int, C.c_size_t, C.c_void_p, C.c_void_p,
+                                     C.c_void_p, C.c_int, C.c_void_p]),
+    "mpcx_party_mul_eval": (C.c_int, [C.c_void_p, C.c_void_p, C.c_size_t, C.c_size_t, C.c_size_t] +
+                            [C.c_void_p] * 6),
+    "mpcx_party_lut8_eval": (C.c_int, [C.c_void_p, C.c_void_p, C.c_size_t] + [C.c_void_p] * 4),
+    "mpcx_party_sxs_eval": (C.c_int, [C.c_void_p, C.c_void_p, C.c_int, C.c_int, C.c_int, C.c_int] +
+                            [C.c_void_p] * 4),
+    "mpcx_party_reveal_eval": (C.c_int, [C.c_void_p, C.c_void_p, C.c_size_t] + [C.c_void_p] * 3),
+    "mpcx_model_set_party": (C.c_int, [C.c_void_p, C.c_void_p]),
+    "mpcx_model_import_party_key": (C.c_int, [C.c_void_p, C.c_int, C.c_void_p, C.c_size_t]),
+    "mpcx_model_set_party_inputs": (C.c_int, [C.c_void_p, C.c_int] + [C.c_void_p] * 4),
     "mpcx_model_profile_gemm": (C.c_int, [C.c_void_p] + [C.c_void_p] * 3),
 }
 
@@ -397,6 +416,61 @@ class Ctx:
                    "reveal_eval")
         return from_dev(out, self.T, v0.size)
 
+    # ---------------- party mode (one party per process or thread) ----------------
+    def party_tr_eval(self, peer, kind, key, xhat, bias=None):
+        xhat = self.ring(xhat)
+        n = xhat.size
+        dx = to_dev(xhat)
+        db = to_dev(self.ring(bias)) if bias is not None else None
+        ncol = int(np.asarray(bias).size) if bias is not None else 0
+        out = empty_dev(n * xhat.itemsize)
+        self.check(self.lib.mpcx_party_tr_eval(self.h, peer.h, kind, n, dptr(key), dptr(dx), dptr(db), ncol,
+                                               dptr(out)), "party_tr_eval")
+        return from_dev(out, self.T, n)
+
+    def party_mul_eval(self, peer, key, xhat, yhat, ia, ib):
+        xhat, yhat = self.ring(xhat), self.ring(yhat)
+        ia = np.ascontiguousarray(ia, np.uint32)
+        ib = np.ascontiguousarray(ib, np.uint32)
+        nz = ia.size
+        d = [to_dev(v) for v in (ia, ib)]
+        dx, dy = to_dev(xhat), to_dev(yhat)
+        out = empty_dev(nz * xhat.itemsize)
+        self.check(self.lib.mpcx_party_mul_eval(self.h, peer.h, xhat.size, yhat.size, nz, dptr(d[0]), dptr(d[1]),
+                                                dptr(key), dptr(dx), dptr(dy), dptr(out)), "party_mul_eval")
+        return from_dev(out, self.T, nz)
+
+    def party_lut8_eval(self, peer, key, table, xhat):
+        xhat, table = self.ring(xhat), self.ring(table)
+        n = xhat.size
+        dx, dt = to_dev(xhat), to_dev(table)
+        out = empty_dev(n * xhat.itemsize)
+        self.check(self.lib.mpcx_party_lut8_eval(self.h, peer.h, n, dptr(key), dptr(dt), dptr(dx), dptr(out)),
+                   "party_lut8_eval")
+        return from_dev(out, self.T, n)
+
+    def party_sxs_eval(self, peer, nb, M, K, N, key, ahat, bhat):
+        ahat, bhat = self.ring(ahat), self.ring(bhat)
+        da, db = to_dev(ahat), to_dev(bhat)
+        out = empty_dev(nb * M * N * ahat.itemsize)
+        self.check(self.lib.mpcx_party_sxs_eval(self.h, peer.h, nb, M, K, N, dptr(key), dptr(da), dptr(db),
+                                                dptr(out)), "party_sxs_eval")
+        return from_dev(out, self.T, nb * M * N)
+
+    def party_reveal_eval(self, peer, key, v):
+        v = self.ring(v)
+        dv = to_dev(v)
+        out = empty_dev(v.size * v.itemsize)
+        self.check(self.lib.mpcx_party_reveal_eval(self.h, peer.h, v.size, dptr(key), dptr(dv), dptr(out)),
+                   "party_reveal_eval")
+        return from_dev(out, self.T, v.size)
+
+    def party_reconstruct(self, peer, v):
+        v = self.ring(v)
+        dv = to_dev(v)
+        self.check(self.lib.mpcx_party_reconstruct(self.h, peer.h, v.size, dptr(dv)), "party_reconstruct")
+        return from_dev(dv, self.T, v.size)
+
     # ---------------- adjacency normalisation ----------------
     def set_adjnorm_lanes(self, lanes):
         """Concurrent graph groups of the adjacency normalisation (keygen and eval
@@ -418,6 +492,56 @@ class Ctx:
         self.check(self.lib.mpcx_adjnorm_eval(self.h, B, N, nmax, dptr(k0), dptr(k1), dptr(d0), dptr(d1), dptr(out)),
                    "adjnorm_eval")
         return out if as_device else from_dev(out, self.T, B * N * N)
+
+
+class Peer:
+    """One party's end of the channel between the two parties (party mode)."""
+
+    def __init__(self, handle):
+        self.lib = load()
+        self.h = handle
+
+    @staticmethod
+    def connect(party, path, timeout_ms=60000):
+        lib = load()
+        h = C.c_void_p()
+        st = lib.mpcx_peer_connect(int(party), os.fsencode(path), int(timeout_ms), C.byref(h))
+        if st != 0:
+            raise MpcxError(f"mpcx_peer_connect(party {party}, {path}) failed ({st})")
+        return Peer(h)
+
+    @staticmethod
+    def pair(timeout_ms=60000):
+        """Both ends of one channel (two parties as two threads of this process)."""
+        lib = load()
+        a, b = C.c_void_p(), C.c_void_p()
+        st = lib.mpcx_peer_pair(int(timeout_ms), C.byref(a), C.byref(b))
+        if st != 0:
+            raise MpcxError(f"mpcx_peer_pair failed ({st})")
+        return Peer(a), Peer(b)
+
+    @property
+    def party(self):
+        return int(self.lib.mpcx_peer_party(self.h))
+
+    @property
+    def bytes(self):
+        return int(self.lib.mpcx_peer_bytes(self.h))
+
+    @property
+    def rounds(self):
+        return int(self.lib.mpcx_peer_rounds(self.h))
+
+    def close(self):
+        if self.h:
+            self.lib.mpcx_peer_close(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
 
 
 class PinnedBuffer:
@@ -597,6 +721,25 @@ class Model:
         out = np.zeros(B, np.int64)
         self.ctx.check(self.lib.mpcx_model_output(self.h, B, out.ctypes.data_as(C.c_void_p)), "model_output")
         return out
+
+    def set_party(self, peer):
+        """Party mode: evaluate only peer.party's side, exchanging through peer
+        (None: both parties in this process).  Drops keys and inputs."""
+        self._peer = peer
+        self.ctx.check(self.lib.mpcx_model_set_party(self.h, peer.h if peer is not None else None), "set_party")
+
+    def import_party_key(self, B, key):
+        key = np.ascontiguousarray(key, np.uint8)
+        self.ctx.check(self.lib.mpcx_model_import_party_key(self.h, B, key.ctypes.data_as(C.c_void_p), key.size),
+                       "import_party_key")
+
+    def set_party_inputs(self, B, x, a, m, prot=None):
+        arrs = [self.ctx.ring(v) for v in (x, a, m)]
+        pr = np.ascontiguousarray(prot, np.int64) if prot is not None else None
+        self._inputs = arrs + [pr]
+        self.ctx.check(self.lib.mpcx_model_set_party_inputs(
+            self.h, B, *[v.ctypes.data_as(C.c_void_p) for v in arrs],
+            pr.ctypes.data_as(C.c_void_p) if pr is not None else None), "set_party_inputs")
 
     def profile(self, on=True):
         self.ctx.check(self.lib.mpcx_model_profile(self.h, 1 if on else 0), "profile")

@@ -32,7 +32,8 @@ typedef int mpcx_status;
 #define MPCX_EHIP 2    /* a HIP call failed; see mpcx_last_error            */
 #define MPCX_ENOMEM 3  /* device allocation failed                          */
 #define MPCX_ESTATE 4  /* call out of order (e.g. forward before keygen)    */
-#define MPCX_EIO 5     /* a key file could not be opened, read or written  */
+#define MPCX_EIO 5     /* a key file could not be opened, read or written, or
+                          the channel to the other party failed              */
 
 typedef struct mpcx_ctx mpcx_ctx;
 typedef struct mpcx_model mpcx_model;
@@ -263,6 +264,55 @@ mpcx_status mpcx_adjnorm_keygen(mpcx_ctx *ctx, int B, int N, uint64_t seed, void
 mpcx_status mpcx_adjnorm_eval(mpcx_ctx *ctx, int B, int N, int nmax, const void *d_key0, const void *d_key1,
                               const void *d_a0, const void *d_a1, void *d_out);
 
+/* ---------------- party mode: one process (or thread) per party ----------------
+ * The reference deploys the two parties as two processes on one GPU, each with
+ * its own key file, talking over a socket (gpu_mpc/run_local_2pc.sh:196-233;
+ * GpuPeer / SigmaPeer, gpu_mpc/utils/gpu_comms.h:94-397,
+ * gpu_mpc/utils/sigma_comms.cpp:36-150).  In party mode each process creates its
+ * own context on the GPU and one end of a channel; every exchange sends exactly
+ * the bytes mpcx_bytes_exchanged counts (ring elements at their width, DCF output
+ * bits packed 32 per 32-bit word: the bit-packed wire of gpu_comms.h:28-73), and
+ * each party's context counts both directions, as in the one-process mode.  The
+ * gate calls below take this party's key (as written by the keygen calls for
+ * that party) and its share or the masked public input, and return the
+ * reconstructed masked output on both parties; they synchronise the context's
+ * stream. */
+typedef struct mpcx_peer mpcx_peer;
+/* Party 0 listens on the Unix socket `path`, party 1 connects (GpuPeer::connect,
+ * gpu_mpc/ddg_orca_base.h:113-114).  timeout_ms bounds the rendezvous and every
+ * later receive.  MPCX_EIO if no connection is made. */
+mpcx_status mpcx_peer_connect(int party, const char *path, int timeout_ms, mpcx_peer **out);
+/* Both ends of one channel, for two parties run as two threads of one process. */
+mpcx_status mpcx_peer_pair(int timeout_ms, mpcx_peer **p0, mpcx_peer **p1);
+void mpcx_peer_close(mpcx_peer *peer);
+int mpcx_peer_party(const mpcx_peer *peer);
+/* Bytes sent plus bytes received over the channel, and exchanges made. */
+uint64_t mpcx_peer_bytes(const mpcx_peer *peer);
+uint64_t mpcx_peer_rounds(const mpcx_peer *peer);
+const char *mpcx_peer_error(const mpcx_peer *peer);
+/* peer->reconstructInPlace(d, bw, n, s) (gpu_mpc/utils/gpu_comms.h:290-302):
+ * d_inout holds this party's additive share and receives the sum of both. */
+mpcx_status mpcx_party_reconstruct(mpcx_ctx *ctx, mpcx_peer *peer, size_t n, void *d_inout);
+/* gpuRelu / gpuTruncate / gpuReluExtend / the DReLU of gpuRelu for this party
+ * (gpu_mpc/ddg_orca.h:90, 103-104, 116-118; dpf_dcf_adapter.h:225-234):
+ * d_key = this party's key (mpcx_tr_key_bytes); MPCX_DRELU returns the public
+ * masked bit after one round, the other kinds the masked output after two. */
+mpcx_status mpcx_party_tr_eval(mpcx_ctx *ctx, mpcx_peer *peer, int kind, size_t n, const void *d_key,
+                               const void *d_xhat, const void *d_bias, int ncol, void *d_yhat);
+/* gpuMul (gpu_mpc/secure_adj_norm.h:611-624, gpu_mpc/ddg_orca.h:43-63). */
+mpcx_status mpcx_party_mul_eval(mpcx_ctx *ctx, mpcx_peer *peer, size_t nx, size_t ny, size_t nz,
+                                const uint32_t *d_ia, const uint32_t *d_ib, const void *d_key,
+                                const void *d_xhat, const void *d_yhat, void *d_zhat);
+/* gpuDpfLUT (gpu_mpc/secure_adj_norm.h:510-520). */
+mpcx_status mpcx_party_lut8_eval(mpcx_ctx *ctx, mpcx_peer *peer, size_t n, const void *d_key,
+                                 const void *d_table, const void *d_xhat, void *d_yhat);
+/* gpuMatmul, secret x secret (gpu_mpc/ddg_orca_base.h:170-205). */
+mpcx_status mpcx_party_sxs_eval(mpcx_ctx *ctx, mpcx_peer *peer, int nb, int M, int K, int N, const void *d_key,
+                                const void *d_ahat, const void *d_bhat, void *d_chat);
+/* revealIfLeaf (gpu_mpc/ddg_orca_base.h:72-80): d_v this party's share. */
+mpcx_status mpcx_party_reveal_eval(mpcx_ctx *ctx, mpcx_peer *peer, size_t n, const void *d_key,
+                                   const void *d_v, void *d_vhat);
+
 /* ---------------- pinned host memory ----------------
  * Page-locked host buffers for streamed key arenas (hipHostMalloc). */
 mpcx_status mpcx_host_alloc(size_t bytes, void **out);
@@ -390,6 +440,20 @@ mpcx_status mpcx_model_set_inputs(mpcx_model *m, int B, const void *h_x0, const 
 mpcx_status mpcx_model_forward(mpcx_model *m, int B);
 /* Reconstructed outputs (B int64 at scale s); synchronizes the stream. */
 mpcx_status mpcx_model_output(mpcx_model *m, int B, int64_t *h_out);
+/* Party mode of the model (one lane; the reference's evaluator process,
+ * gpu_mpc/deepdtagen_inference.cu:422-607 with run_local_2pc.sh:196-233): the
+ * model evaluates only the peer's party, holding that party's key and shares,
+ * and exchanges through the peer; peer = NULL returns to both parties in one
+ * process.  Drops keys and inputs.  The party imports its own key
+ * (mpcx_model_export_keys / mpcx_model_write_keys of the dealer's run for that
+ * party, mpcx_model_key_bytes bytes) and its input shares; h_prot is the
+ * protein embedding on the party that owns it (party 1 in the reference's
+ * deployment) and NULL on the other.  mpcx_model_forward / _output then work
+ * as in the one-process mode and give the same outputs and exchange bytes. */
+mpcx_status mpcx_model_set_party(mpcx_model *m, mpcx_peer *peer);
+mpcx_status mpcx_model_import_party_key(mpcx_model *m, int B, const void *h_key, size_t bytes);
+mpcx_status mpcx_model_set_party_inputs(mpcx_model *m, int B, const void *h_x, const void *h_a,
+                                        const void *h_m, const int64_t *h_prot);
 /* DCF gate kernel (k_tr_eval) timing with HIP events on the launch streams.  While
  * enabled, forwards run their lanes one after another (each launch is timed
  * alone) and launch the separately named k_tr_eval<..., 1> instantiation. */
