@@ -15,63 +15,9 @@
 #include "peer.h"
 
 // ---------------------------------------------------------------------------
-// AES-128 key schedule (FIPS-197 5.2) and the fixed keys
+// dealer and party keys (the S-box and key schedule are mpcx_core.h's)
 // ---------------------------------------------------------------------------
 namespace mpcx {
-
-const uint8_t kSbox[256] = {
-    0x63, 0x7c, 0x77, 0x7b, 0xf2, 0x6b, 0x6f, 0xc5, 0x30, 0x01, 0x67, 0x2b, 0xfe, 0xd7, 0xab, 0x76,
-    0xca, 0x82, 0xc9, 0x7d, 0xfa, 0x59, 0x47, 0xf0, 0xad, 0xd4, 0xa2, 0xaf, 0x9c, 0xa4, 0x72, 0xc0,
-    0xb7, 0xfd, 0x93, 0x26, 0x36, 0x3f, 0xf7, 0xcc, 0x34, 0xa5, 0xe5, 0xf1, 0x71, 0xd8, 0x31, 0x15,
-    0x04, 0xc7, 0x23, 0xc3, 0x18, 0x96, 0x05, 0x9a, 0x07, 0x12, 0x80, 0xe2, 0xeb, 0x27, 0xb2, 0x75,
-    0x09, 0x83, 0x2c, 0x1a, 0x1b, 0x6e, 0x5a, 0xa0, 0x52, 0x3b, 0xd6, 0xb3, 0x29, 0xe3, 0x2f, 0x84,
-    0x53, 0xd1, 0x00, 0xed, 0x20, 0xfc, 0xb1, 0x5b, 0x6a, 0xcb, 0xbe, 0x39, 0x4a, 0x4c, 0x58, 0xcf,
-    0xd0, 0xef, 0xaa, 0xfb, 0x43, 0x4d, 0x33, 0x85, 0x45, 0xf9, 0x02, 0x7f, 0x50, 0x3c, 0x9f, 0xa8,
-    0x51, 0xa3, 0x40, 0x8f, 0x92, 0x9d, 0x38, 0xf5, 0xbc, 0xb6, 0xda, 0x21, 0x10, 0xff, 0xf3, 0xd2,
-    0xcd, 0x0c, 0x13, 0xec, 0x5f, 0x97, 0x44, 0x17, 0xc4, 0xa7, 0x7e, 0x3d, 0x64, 0x5d, 0x19, 0x73,
-    0x60, 0x81, 0x4f, 0xdc, 0x22, 0x2a, 0x90, 0x88, 0x46, 0xee, 0xb8, 0x14, 0xde, 0x5e, 0x0b, 0xdb,
-    0xe0, 0x32, 0x3a, 0x0a, 0x49, 0x06, 0x24, 0x5c, 0xc2, 0xd3, 0xac, 0x62, 0x91, 0x95, 0xe4, 0x79,
-    0xe7, 0xc8, 0x37, 0x6d, 0x8d, 0xd5, 0x4e, 0xa9, 0x6c, 0x56, 0xf4, 0xea, 0x65, 0x7a, 0xae, 0x08,
-    0xba, 0x78, 0x25, 0x2e, 0x1c, 0xa6, 0xb4, 0xc6, 0xe8, 0xdd, 0x74, 0x1f, 0x4b, 0xbd, 0x8b, 0x8a,
-    0x70, 0x3e, 0xb5, 0x66, 0x48, 0x03, 0xf6, 0x0e, 0x61, 0x35, 0x57, 0xb9, 0x86, 0xc1, 0x1d, 0x9e,
-    0xe1, 0xf8, 0x98, 0x11, 0x69, 0xd9, 0x8e, 0x94, 0x9b, 0x1e, 0x87, 0xe9, 0xce, 0x55, 0x28, 0xdf,
-    0x8c, 0xa1, 0x89, 0x0d, 0xbf, 0xe6, 0x42, 0x68, 0x41, 0x99, 0x2d, 0x0f, 0xb0, 0x54, 0xbb, 0x16};
-
-const uint8_t kKeyH[16] = {'M', 'I', '3', '5', '5', 'X', '-', 'H', 'a', 'l', 'f', 'T', 'r', 'e', 'e', 'H'};
-const uint8_t kKeyL[16] = {'M', 'I', '3', '5', '5', 'X', '-', 'H', 'a', 'l', 'f', 'T', 'r', 'e', 'e', 'L'};
-
-AesRK aes_expand(const uint8_t key[16]) {
-  static const uint8_t rcon[10] = {0x01, 0x02, 0x04, 0x08, 0x10, 0x20, 0x40, 0x80, 0x1b, 0x36};
-  uint8_t b[176];
-  std::memcpy(b, key, 16);
-  for (int i = 4; i < 44; i++) {
-    uint8_t t[4];
-    std::memcpy(t, b + 4 * (i - 1), 4);
-    if (i % 4 == 0) {
-      const uint8_t t0 = t[0];
-      t[0] = uint8_t(kSbox[t[1]] ^ rcon[i / 4 - 1]);
-      t[1] = kSbox[t[2]];
-      t[2] = kSbox[t[3]];
-      t[3] = kSbox[t0];
-    }
-    for (int j = 0; j < 4; j++) b[4 * i + j] = uint8_t(b[4 * (i - 4) + j] ^ t[j]);
-  }
-  AesRK rk;
-  for (int j = 0; j < 44; j++)
-    rk.w[j] = uint32_t(b[4 * j]) | (uint32_t(b[4 * j + 1]) << 8) | (uint32_t(b[4 * j + 2]) << 16) |
-              (uint32_t(b[4 * j + 3]) << 24);
-  return rk;
-}
-
-AesRK dealer_key(uint64_t seed) {
-  uint8_t k[16];
-  const uint64_t a = seed, b = seed ^ 0x9E3779B97F4A7C15ull;
-  for (int i = 0; i < 8; i++) {
-    k[i] = uint8_t(a >> (8 * i));
-    k[8 + i] = uint8_t(b >> (8 * i));
-  }
-  return aes_expand(k);
-}
 
 // FIPS-197 encryption of one block on the host (columns as little-endian words,
 // the device code's state layout); used only to derive the parties' PRF keys.
@@ -83,7 +29,7 @@ static void aes_encrypt_host(const AesRK &rk, const uint32_t in[4], uint32_t out
   for (int r = 1; r <= 10; r++) {
     uint8_t u[16];
     for (int j = 0; j < 4; j++)  // SubBytes + ShiftRows: row b of column j from column j + b
-      for (int b = 0; b < 4; b++) u[4 * j + b] = kSbox[st[4 * ((j + b) & 3) + b]];
+      for (int b = 0; b < 4; b++) u[4 * j + b] = kSboxC[st[4 * ((j + b) & 3) + b]];
     if (r < 10)
       for (int j = 0; j < 4; j++) {  // MixColumns
         const uint8_t a0 = u[4 * j], a1 = u[4 * j + 1], a2 = u[4 * j + 2], a3 = u[4 * j + 3];
@@ -100,18 +46,39 @@ static void aes_encrypt_host(const AesRK &rk, const uint32_t in[4], uint32_t out
              (uint32_t(st[4 * j + 3]) << 24);
 }
 
-void party_key_bytes(uint64_t seed, int party, uint8_t out[16]) {
-  const AesRK kd = dealer_key(seed);
-  const uint32_t in[4] = {uint32_t(party), 0u, uint32_t(F_PARTY), 0xFFFFFFFFu};
-  uint32_t w[4];
-  aes_encrypt_host(kd, in, w);
+static void words_to_bytes(const uint32_t w[4], uint8_t out[16]) {
   for (int j = 0; j < 4; j++)
     for (int b = 0; b < 4; b++) out[4 * j + b] = uint8_t(w[j] >> (8 * b));
 }
 
-AesRK party_key(uint64_t seed, int party) {
+AesRK dealer_key(const Launch &L, uint64_t seed) {
   uint8_t k[16];
-  party_key_bytes(seed, party, k);
+  if (L.has_dealer_key) {
+    const uint32_t in[4] = {uint32_t(seed), uint32_t(seed >> 32), 0x4D415354u, 0xFFFFFFFEu};
+    uint32_t w[4];
+    aes_encrypt_host(aes_expand(L.dealer_key), in, w);
+    words_to_bytes(w, k);
+  } else {
+    const uint64_t a = seed, b = seed ^ 0x9E3779B97F4A7C15ull;
+    for (int i = 0; i < 8; i++) {
+      k[i] = uint8_t(a >> (8 * i));
+      k[8 + i] = uint8_t(b >> (8 * i));
+    }
+  }
+  return aes_expand(k);
+}
+
+void party_key_bytes(const Launch &L, uint64_t seed, int party, uint8_t out[16]) {
+  const AesRK kd = dealer_key(L, seed);
+  const uint32_t in[4] = {uint32_t(party), 0u, uint32_t(F_PARTY), 0xFFFFFFFFu};
+  uint32_t w[4];
+  aes_encrypt_host(kd, in, w);
+  words_to_bytes(w, out);
+}
+
+AesRK party_key(const Launch &L, uint64_t seed, int party) {
+  uint8_t k[16];
+  party_key_bytes(L, seed, party, k);
   return aes_expand(k);
 }
 
@@ -313,6 +280,13 @@ mpcx_status mpcx_set_aes_variant(mpcx_ctx *c, int variant, int block) {
     return fail(c, MPCX_EINVAL, "block must be a multiple of 128 in [128, 1024]");
   c->L.aes_variant = variant;
   c->L.aes_block = block;
+  return MPCX_OK;
+}
+
+mpcx_status mpcx_set_dealer_key(mpcx_ctx *c, const uint8_t *key) {
+  CHECK_CTX(c);
+  c->L.has_dealer_key = key != nullptr;
+  for (int i = 0; i < 16; i++) c->L.dealer_key[i] = key ? key[i] : 0;
   return MPCX_OK;
 }
 
@@ -665,6 +639,16 @@ mpcx_status mpcx_mul_eval(mpcx_ctx *c, size_t nx, size_t ny, size_t nz, const ui
                      : mul_eval_t<uint64_t>(c, nx, ny, nz, ia, ib, k0, k1, x, y, z);
 }
 
+mpcx_status mpcx_mul_key_layout(mpcx_ctx *c, size_t nx, size_t ny, size_t nz, size_t off[3]) {
+  CHECK_CTX(c);
+  if (!off) return fail(c, MPCX_EINVAL, "mul_key_layout: null pointer");
+  const MulLayout l = mul_layout(c->bw, nx, ny, nz, 0);
+  off[0] = l.off_rx;
+  off[1] = l.off_ry;
+  off[2] = l.off_c;
+  return MPCX_OK;
+}
+
 // ---------------- LUT8 ----------------
 size_t mpcx_lut8_key_bytes(mpcx_ctx *c, size_t n) { return c ? lut8_layout(c->bw, n, 0).end : 0; }
 template <typename T>
@@ -813,6 +797,16 @@ mpcx_status mpcx_sxs_eval(mpcx_ctx *c, int nb, int M, int K, int N, const void *
     return fail(c, MPCX_EINVAL, "sxs_eval: bad argument");
   return c->bw == 32 ? sxs_eval_t<uint32_t>(c, nb, M, K, N, k0, k1, a, b, out)
                      : sxs_eval_t<uint64_t>(c, nb, M, K, N, k0, k1, a, b, out);
+}
+
+mpcx_status mpcx_sxs_key_layout(mpcx_ctx *c, int nb, int M, int K, int N, size_t off[3]) {
+  CHECK_CTX(c);
+  if (!off || nb < 1 || M < 1 || K < 1 || N < 1) return fail(c, MPCX_EINVAL, "sxs_key_layout: bad argument");
+  const SxsLayout l = sxs_layout(c->bw, nb, M, K, N, 0);
+  off[0] = l.off_ra;
+  off[1] = l.off_rb;
+  off[2] = l.off_c;
+  return MPCX_OK;
 }
 
 template <typename T>

@@ -29,6 +29,9 @@ struct Launch {
   // model forwards with resident keys are captured once per batch size into a
   // HIP graph and replayed (0 = enqueue every kernel each time)
   int graph = 1;
+  // the dealer's 16-byte key (dealer_key): set, or the seed alone
+  bool has_dealer_key = false;
+  uint8_t dealer_key[16] = {};
   // -1: two-party kernels evaluate both parties (blockIdx.y = party).  0 or 1:
   // only that party (one process per party): the launchers take the party's own
   // key (and input share, message buffer) in both party slots and launch one

@@ -119,7 +119,7 @@ __global__ void k_prf(AesRK kd, uint32_t gate, uint32_t field, size_t n, uint4 *
 }
 
 hipError_t launch_prf(const Launch &L, uint64_t seed, uint32_t gate, uint32_t field, size_t n, uint4 *out) {
-  const AesRK kd = dealer_key(seed);
+  const AesRK kd = dealer_key(L, seed);
   return with_variant(L, [&](auto v) {
     constexpr int NT = decltype(v)::nt, REP = decltype(v)::rep;
     int block = variant_block(L);
@@ -170,7 +170,7 @@ hipError_t launch_dcf_keygen(const Launch &L, uint64_t seed, uint32_t gate, uint
                              const uint64_t *alpha, const uint8_t *rbit, uint8_t *k0, uint8_t *k1, size_t base) {
   DcfLayout lay = dcf_layout(m, n, base, true);
   DcfGenArgs a;
-  a.kd = dealer_key(seed);
+  a.kd = dealer_key(L, seed);
   a.gate = gate;
   a.fb = fbase;
   a.m = m;
@@ -567,9 +567,9 @@ hipError_t launch_tr_keygen(const Launch &L, const TrLayout &lay, uint64_t seed,
                             T *out_mask, uint8_t *k0, uint8_t *k1) {
   if (lay.bw != int(8 * sizeof(T))) return hipErrorInvalidValue;
   TrArgs<T> a = tr_args<T>(lay);
-  a.kd = dealer_key(seed);
-  a.kp[0] = party_key(seed, 0);
-  a.kp[1] = party_key(seed, 1);
+  a.kd = dealer_key(L, seed);
+  a.kp[0] = party_key(L, seed, 0);
+  a.kp[1] = party_key(L, seed, 1);
   a.gate = gate;
   a.w0 = k0;
   a.w1 = k1;
@@ -765,7 +765,7 @@ __global__ void k_split(AesRK kd, uint32_t gate, uint32_t field, size_t n, const
 template <typename T>
 static hipError_t split_impl(const Launch &L, uint64_t seed, uint32_t gate, uint32_t field, size_t n, const T *v,
                              T *p0, T *p1, T *copy0, T *mask_out) {
-  const AesRK kd = dealer_key(seed);
+  const AesRK kd = dealer_key(L, seed);
   return with_variant(L, [&](auto vv) {
     constexpr int NT = decltype(vv)::nt, REP = decltype(vv)::rep;
     int block = variant_block(L);
@@ -910,7 +910,7 @@ hipError_t launch_mul_keygen(const Launch &L, const MulLayout &lay, uint64_t see
   e = launch_split<T>(L, seed, gate, F_SPLIT + 1, lay.ny, ry, reinterpret_cast<T *>(k0 + lay.off_ry),
                       reinterpret_cast<T *>(k1 + lay.off_ry), nullptr);
   if (e != hipSuccess) return e;
-  const AesRK kd = dealer_key(seed);
+  const AesRK kd = dealer_key(L, seed);
   return with_variant(L, [&](auto v) {
     constexpr int NT = decltype(v)::nt, REP = decltype(v)::rep;
     int block = variant_block(L);
@@ -1055,7 +1055,7 @@ __global__ void k_lut8_keygen(AesRK kd, uint32_t gate, Lut8Layout lay, const T *
 template <typename T>
 hipError_t launch_lut8_keygen(const Launch &L, const Lut8Layout &lay, uint64_t seed, uint32_t gate,
                               const T *in_mask, T *out_mask, uint8_t *k0, uint8_t *k1) {
-  const AesRK kd = dealer_key(seed);
+  const AesRK kd = dealer_key(L, seed);
   return with_variant(L, [&](auto v) {
     constexpr int NT = decltype(v)::nt, REP = decltype(v)::rep;
     int block = variant_block(L);
@@ -1751,7 +1751,7 @@ __global__ void k_prf_ring(AesRK kd, uint32_t gate, uint32_t field, size_t n, T 
 }
 template <typename T>
 hipError_t launch_prf_ring(const Launch &L, uint64_t seed, uint32_t gate, uint32_t field, size_t n, T *out) {
-  const AesRK kd = dealer_key(seed);
+  const AesRK kd = dealer_key(L, seed);
   return with_variant(L, [&](auto v) {
     constexpr int NT = decltype(v)::nt, REP = decltype(v)::rep;
     int block = variant_block(L);

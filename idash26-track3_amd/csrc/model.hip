@@ -886,7 +886,7 @@ class Model final : public ModelBase, KeySource {
     // plan and dealer disagree (offsets, or gate ids of the seeded-plane expansion)
     if (d.c.off != key_bytes(B) || d.c.gate != uint32_t(plan(B).size()) + 1) return hipErrorUnknown;
     TRY(hipStreamSynchronize(L_.stream));
-    for (int p = 0; p < 2; p++) party_key_bytes(seed, p, pk_[p]);
+    for (int p = 0; p < 2; p++) party_key_bytes(L_, seed, p, pk_[p]);
     have_pk_ = true;
     keyed_B_ = B;
     return hipSuccess;

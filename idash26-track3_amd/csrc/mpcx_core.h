@@ -227,16 +227,68 @@ struct AesRK {
   uint32_t w[44];
 };
 
-extern const uint8_t kSbox[256];
-AesRK aes_expand(const uint8_t key[16]);
-AesRK dealer_key(uint64_t seed);  // dealer PRF key derived from a 64-bit seed
+// The FIPS-197 S-box: the one copy of the library (host key schedules, device T-tables).
+constexpr uint8_t kSboxC[256] = {
+    0x63, 0x7c, 0x77, 0x7b, 0xf2, 0x6b, 0x6f, 0xc5, 0x30, 0x01, 0x67, 0x2b, 0xfe, 0xd7, 0xab, 0x76,
+    0xca, 0x82, 0xc9, 0x7d, 0xfa, 0x59, 0x47, 0xf0, 0xad, 0xd4, 0xa2, 0xaf, 0x9c, 0xa4, 0x72, 0xc0,
+    0xb7, 0xfd, 0x93, 0x26, 0x36, 0x3f, 0xf7, 0xcc, 0x34, 0xa5, 0xe5, 0xf1, 0x71, 0xd8, 0x31, 0x15,
+    0x04, 0xc7, 0x23, 0xc3, 0x18, 0x96, 0x05, 0x9a, 0x07, 0x12, 0x80, 0xe2, 0xeb, 0x27, 0xb2, 0x75,
+    0x09, 0x83, 0x2c, 0x1a, 0x1b, 0x6e, 0x5a, 0xa0, 0x52, 0x3b, 0xd6, 0xb3, 0x29, 0xe3, 0x2f, 0x84,
+    0x53, 0xd1, 0x00, 0xed, 0x20, 0xfc, 0xb1, 0x5b, 0x6a, 0xcb, 0xbe, 0x39, 0x4a, 0x4c, 0x58, 0xcf,
+    0xd0, 0xef, 0xaa, 0xfb, 0x43, 0x4d, 0x33, 0x85, 0x45, 0xf9, 0x02, 0x7f, 0x50, 0x3c, 0x9f, 0xa8,
+    0x51, 0xa3, 0x40, 0x8f, 0x92, 0x9d, 0x38, 0xf5, 0xbc, 0xb6, 0xda, 0x21, 0x10, 0xff, 0xf3, 0xd2,
+    0xcd, 0x0c, 0x13, 0xec, 0x5f, 0x97, 0x44, 0x17, 0xc4, 0xa7, 0x7e, 0x3d, 0x64, 0x5d, 0x19, 0x73,
+    0x60, 0x81, 0x4f, 0xdc, 0x22, 0x2a, 0x90, 0x88, 0x46, 0xee, 0xb8, 0x14, 0xde, 0x5e, 0x0b, 0xdb,
+    0xe0, 0x32, 0x3a, 0x0a, 0x49, 0x06, 0x24, 0x5c, 0xc2, 0xd3, 0xac, 0x62, 0x91, 0x95, 0xe4, 0x79,
+    0xe7, 0xc8, 0x37, 0x6d, 0x8d, 0xd5, 0x4e, 0xa9, 0x6c, 0x56, 0xf4, 0xea, 0x65, 0x7a, 0xae, 0x08,
+    0xba, 0x78, 0x25, 0x2e, 0x1c, 0xa6, 0xb4, 0xc6, 0xe8, 0xdd, 0x74, 0x1f, 0x4b, 0xbd, 0x8b, 0x8a,
+    0x70, 0x3e, 0xb5, 0x66, 0x48, 0x03, 0xf6, 0x0e, 0x61, 0x35, 0x57, 0xb9, 0x86, 0xc1, 0x1d, 0x9e,
+    0xe1, 0xf8, 0x98, 0x11, 0x69, 0xd9, 0x8e, 0x94, 0x9b, 0x1e, 0x87, 0xe9, 0xce, 0x55, 0x28, 0xdf,
+    0x8c, 0xa1, 0x89, 0x0d, 0xbf, 0xe6, 0x42, 0x68, 0x41, 0x99, 0x2d, 0x0f, 0xb0, 0x54, 0xbb, 0x16};
+
+// FIPS-197 5.2 key expansion: at compile time for the two fixed keys (so that
+// every round-key word folds into an instruction literal), at run time for the
+// dealer and party keys.
+constexpr AesRK aes_expand_c(const uint8_t (&key)[16]) {
+  constexpr uint8_t rcon[10] = {0x01, 0x02, 0x04, 0x08, 0x10, 0x20, 0x40, 0x80, 0x1b, 0x36};
+  uint8_t b[176] = {};
+  for (int i = 0; i < 16; i++) b[i] = key[i];
+  for (int i = 4; i < 44; i++) {
+    uint8_t t[4] = {b[4 * (i - 1)], b[4 * (i - 1) + 1], b[4 * (i - 1) + 2], b[4 * (i - 1) + 3]};
+    if (i % 4 == 0) {
+      const uint8_t t0 = t[0];
+      t[0] = uint8_t(kSboxC[t[1]] ^ rcon[i / 4 - 1]);
+      t[1] = kSboxC[t[2]];
+      t[2] = kSboxC[t[3]];
+      t[3] = kSboxC[t0];
+    }
+    for (int j = 0; j < 4; j++) b[4 * i + j] = uint8_t(b[4 * (i - 4) + j] ^ t[j]);
+  }
+  AesRK rk{};
+  for (int j = 0; j < 44; j++)
+    rk.w[j] = uint32_t(b[4 * j]) | (uint32_t(b[4 * j + 1]) << 8) | (uint32_t(b[4 * j + 2]) << 16) |
+              (uint32_t(b[4 * j + 3]) << 24);
+  return rk;
+}
+constexpr uint8_t kKeyHc[16] = {'M', 'I', '3', '5', '5', 'X', '-', 'H', 'a', 'l', 'f', 'T', 'r', 'e', 'e', 'H'};
+constexpr uint8_t kKeyLc[16] = {'M', 'I', '3', '5', '5', 'X', '-', 'H', 'a', 'l', 'f', 'T', 'r', 'e', 'e', 'L'};
+inline AesRK aes_expand(const uint8_t key[16]) {
+  uint8_t k[16];
+  for (int i = 0; i < 16; i++) k[i] = key[i];
+  return aes_expand_c(k);
+}
+struct Launch;
+// The dealer's PRF key for a key set: from the 64-bit seed alone (seed, then
+// seed XOR 0x9E3779B97F4A7C15, as the key bytes) or, with a 16-byte dealer key
+// set on the launch configuration, the AES encryption under that key of the
+// block (seed low word, seed high word, 0x4D415354, 0xFFFFFFFE): the seed then
+// only names the key set and the keys rest on the 16 secret bytes.
+AesRK dealer_key(const Launch &L, uint64_t seed);
 // Party p's own PRF key (a dealer PRF output): the dealer draws every purely
 // random plane of party p's truncation-family keys from it (DCF roots and output
 // mask bits; for party 0 also its shares of kappa and of the G table), so that a
 // party holding the 16 key bytes can expand those planes itself.
-void party_key_bytes(uint64_t seed, int party, uint8_t out[16]);
-AesRK party_key(uint64_t seed, int party);
-extern const uint8_t kKeyH[16];   // fixed key of the tree hash H
-extern const uint8_t kKeyL[16];   // fixed key of the leaf hash HL
+void party_key_bytes(const Launch &L, uint64_t seed, int party, uint8_t out[16]);
+AesRK party_key(const Launch &L, uint64_t seed, int party);
 
 }  // namespace mpcx

@@ -110,6 +110,9 @@ _SIGS = {
     "mpcx_host_alloc": (C.c_int, [C.c_size_t, C.c_void_p]),
     "mpcx_host_free": (None, [C.c_void_p]),
     "mpcx_model_profile_read": (C.c_int, [C.c_void_p] + [C.c_void_p] * 5),
+    "mpcx_mul_key_layout": (C.c_int, [C.c_void_p, C.c_size_t, C.c_size_t, C.c_size_t, C.c_void_p]),
+    "mpcx_sxs_key_layout": (C.c_int, [C.c_void_p, C.c_int, C.c_int, C.c_int, C.c_int, C.c_void_p]),
+    "mpcx_set_dealer_key": (C.c_int, [C.c_void_p, C.c_void_p]),
     "mpcx_peer_connect": (C.c_int, [C.c_int, C.c_char_p, C.c_int, C.c_void_p]),
     "mpcx_peer_pair": (C.c_int, [C.c_int, C.c_void_p, C.c_void_p]),
     "mpcx_peer_close": (None, [C.c_void_p]),
@@ -224,6 +227,12 @@ class Ctx:
 
     def set_aes_variant(self, v, block=0):
         self.check(self.lib.mpcx_set_aes_variant(self.h, v, block), "set_aes_variant")
+
+    def set_dealer_key(self, key16):
+        """The dealer's 16 secret key bytes (None: keys from the seed alone)."""
+        buf = (C.c_uint8 * 16)(*bytes(key16)) if key16 is not None else None
+        self.check(self.lib.mpcx_set_dealer_key(self.h, C.cast(buf, C.c_void_p) if buf is not None else None),
+                   "set_dealer_key")
 
     def aes_variant_name(self):
         return self.lib.mpcx_aes_variant_name(self.lib.mpcx_aes_variant(self.h)).decode()

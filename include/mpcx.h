@@ -93,6 +93,15 @@ mpcx_status mpcx_set_aes_variant(mpcx_ctx *ctx, int variant, int block_threads);
  * variable at mpcx_create). */
 int mpcx_aes_variant(const mpcx_ctx *ctx);
 
+/* The dealer's 16 secret key bytes (NULL: none).  With a key set, every
+ * keygen of this context (and of models created afterwards) derives its PRF key
+ * from these bytes and the seed (which then only names the key set), so the
+ * keys rest on 128 secret bits; without one the seed alone determines them,
+ * which suits tests and benchmarks.  Both parties' keys come from the one dealer
+ * run, as the reference's dealer (DDGOrcaBaseKeygen, gpu_mpc/ddg_orca_base.h:
+ * 338-355, with initGPURandomness) draws them. */
+mpcx_status mpcx_set_dealer_key(mpcx_ctx *ctx, const uint8_t *key16);
+
 /* Exchange accounting, both directions summed (the reference's "Comm (B)",
  * gpu_mpc/deepdtagen_inference.cu:556-558, and GpuPeer::bytesSent/Received,
  * gpu_mpc/utils/gpu_comms.h:290-397). */
@@ -192,6 +201,12 @@ mpcx_status mpcx_mul_eval(mpcx_ctx *ctx, size_t nx, size_t ny, size_t nz, const 
                           const uint32_t *d_ib, const void *d_key0, const void *d_key1,
                           const void *d_xhat, const void *d_yhat, void *d_zhat);
 
+/* Byte offsets, from the start of a party's Beaver-product key, of its share of
+ * the x mask (nx elements), of the y mask (ny) and of the product term (nz): the
+ * fields a, b, c of the reference's GPUMulKey, which callers read to reveal a
+ * leaf operand (gpu_mpc/ddg_orca.h:50-57, gpu_mpc/secure_adj_norm.h:630-640). */
+mpcx_status mpcx_mul_key_layout(mpcx_ctx *ctx, size_t nx, size_t ny, size_t nz, size_t off[3]);
+
 /* ---------------- 8-bit DPF lookup table ----------------
  * y = table[x] for secret x in [0, 256) (the D^-1/2 degree table).  Replaces
  * gpuKeyGenLUT<T,T>(kb, party, 8, bw, N, d_inMask, g), readGPULUTKey and
@@ -216,6 +231,10 @@ mpcx_status mpcx_sxs_keygen(mpcx_ctx *ctx, int nb, int M, int K, int N, const vo
 mpcx_status mpcx_sxs_eval(mpcx_ctx *ctx, int nb, int M, int K, int N, const void *d_key0,
                           const void *d_key1, const void *d_ahat, const void *d_bhat,
                           void *d_chat);
+/* Byte offsets, from the start of a party's SxS key, of its shares of the A
+ * mask (nb*M*K), of the B mask (nb*K*N) and of its C term (nb*M*N): the fields
+ * A, B, C of the reference's GPUMatmulKey (gpu_mpc/ddg_orca_base.h:181-186). */
+mpcx_status mpcx_sxs_key_layout(mpcx_ctx *ctx, int nb, int M, int K, int N, size_t off[3]);
 /* Public ring GEMM C = A . B mod 2^bw (masked activations x public weights;
  * the 4-argument DDGOrcaBase::matmul, gpu_mpc/ddg_orca_base.h:208-271, needs no
  * key and no exchange when the output mask is r_A . W). */

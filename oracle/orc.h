@@ -59,6 +59,8 @@ extern const uint8_t ORC_KEY_L[16];
 /* Dealer PRF: AES_Kd(idx_lo, idx_hi, field, gate); Kd derived from seed. */
 typedef struct { uint8_t rk[176]; } orc_prf;
 void orc_prf_init(orc_prf *p, uint64_t seed);
+/* The dealer's 16 secret key bytes (NULL: the seed alone derives the PRF key). */
+void orc_set_dealer_key(const uint8_t *key16);
 orc_blk orc_prf_blk(const orc_prf *p, uint32_t gate, uint32_t field, uint64_t idx);
 void orc_prf_batch(uint64_t seed, uint32_t gate, uint32_t field, size_t n, orc_blk *out);
 

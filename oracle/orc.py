@@ -110,6 +110,7 @@ def lib():
             "orc_maxpool_keygen": (None, [u64, u32, i, i, i, i, i, P, P, P, P, sz]),
             "orc_maxpool_eval": (None, [i, i, i, i, i, P, P, sz, P, P, P]),
             "orc_set_threads": (None, [i]),
+            "orc_set_dealer_key": (None, [C.c_void_p]),
             "orc_get_threads": (i, []),
         }
         for name, (res, args) in sigs.items():
@@ -392,6 +393,15 @@ def maxpool_eval(bw, s, B, N, C, k0, k1, xhat):
     by = np.zeros(1, np.uint64)
     lib().orc_maxpool_eval(bw, s, B, N, C, ptr(k0), ptr(k1), 0, ptr(xhat), ptr(y), ptr(by))
     return y, int(by[0])
+
+
+def set_dealer_key(key16):
+    """The dealer's 16 secret key bytes (None: derive keys from the seed alone)."""
+    if key16 is None:
+        lib().orc_set_dealer_key(None)
+        return
+    buf = (C.c_uint8 * 16)(*bytes(key16))
+    lib().orc_set_dealer_key(C.cast(buf, C.c_void_p))
 
 
 def set_threads(n):

@@ -176,12 +176,35 @@ void orc_H_batch(size_t n, const orc_blk *in, orc_blk *out, int leaf) {
 }
 
 /* ---------------- dealer PRF ---------------- */
+/* The dealer's 16 secret key bytes, when set: the PRF key of a key set is then
+ * the AES encryption under them of the block (seed low word, seed high word,
+ * 0x4D415354, 0xFFFFFFFE); without them it is the seed and seed ^
+ * 0x9E3779B97F4A7C15 as the key bytes. */
+static int g_has_dealer_key = 0;
+static uint8_t g_dealer_rk[176];
+
+void orc_set_dealer_key(const uint8_t *key16) {
+  g_has_dealer_key = key16 != NULL;
+  if (key16) orc_aes_expand(key16, g_dealer_rk);
+}
+
 void orc_prf_init(orc_prf *p, uint64_t seed) {
   uint8_t key[16];
-  uint64_t a = seed, b = seed ^ 0x9E3779B97F4A7C15ull;
-  for (int i = 0; i < 8; i++) {
-    key[i] = (uint8_t)(a >> (8 * i));
-    key[8 + i] = (uint8_t)(b >> (8 * i));
+  if (g_has_dealer_key) {
+    orc_blk in;
+    in.w[0] = (uint32_t)seed;
+    in.w[1] = (uint32_t)(seed >> 32);
+    in.w[2] = 0x4D415354u;
+    in.w[3] = 0xFFFFFFFEu;
+    uint8_t b[16];
+    blk_to_bytes(in, b);
+    orc_aes_encrypt(g_dealer_rk, b, key);
+  } else {
+    uint64_t a = seed, b = seed ^ 0x9E3779B97F4A7C15ull;
+    for (int i = 0; i < 8; i++) {
+      key[i] = (uint8_t)(a >> (8 * i));
+      key[8 + i] = (uint8_t)(b >> (8 * i));
+    }
   }
   orc_aes_expand(key, p->rk);
 }

@@ -1,0 +1,71 @@
+"""The EzPC-named entry points (include/mpcx_ezpc.hpp) and the sytorch Backend<T>
+subclasses (include/mpcx_sytorch.hpp), driven from C++ (tests/cpp/ezpc_check.cpp)
+through two of the reference's call sequences, one dealer run per party and
+the two evaluators as two threads on one channel:
+  - ddgSecureAdjNormKeygen / ddgSecureAdjNormEval (gpu_mpc/secure_adj_norm.h:
+    203-374, 393-659), against the oracle's closed form of A_norm;
+  - a GCN layer's backend calls (gcn_layer.h:107-116, layers.h:67-93: the
+    per-graph secret x secret matmul, truncateForward, the public-weight matmul
+    with bias, truncateForward, relu, output), against exact integer arithmetic
+    on the oracle's A_norm.
+"""
+import os
+import subprocess
+
+import numpy as np
+import pytest
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+BIN = os.path.join(ROOT, "tests", "cpp", "ezpc_check")
+S = 12
+
+
+def test_ezpc_check_built():
+    assert os.path.exists(BIN), "tests/cpp/ezpc_check not built (run __graft_entry__.build())"
+
+
+def _ring(v, bw):
+    dt = np.uint32 if bw == 32 else np.uint64
+    m = (1 << bw) - 1
+    return (np.asarray(v, np.int64).astype(np.uint64) & np.uint64(m)).astype(dt)
+
+
+def _signed(v, bw):
+    v = np.asarray(v).astype(np.uint64)
+    if bw == 64:
+        return v.view(np.int64)
+    v = v.astype(np.int64)
+    return np.where(v >= 1 << 31, v - (1 << 32), v)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("bw", [32, 64])
+def test_shim_adjnorm_and_gcn_layer(orc, synth, tmp_path, bw):
+    B, N, F, O, nmax = 3, 24, 8, 6, 138
+    dims = synth.Dims(bw=bw, n_nodes=N)
+    _, A, _ = synth.molecules(B, dims, seed=bw, min_atoms=5, max_atoms=N)
+    rng = np.random.default_rng(bw + 1)
+    X = rng.integers(-(1 << S), 1 << S, size=(B, N, F))
+    W = rng.integers(-256, 257, size=(F, O))
+    b = rng.integers(-(1 << S), 1 << S, size=O)
+    a0, a1 = synth.share(A, bw, 3)
+    x0, x1 = synth.share(X, bw, 4)
+    d = tmp_path
+    (d / "meta.txt").write_text(f"{bw} {B} {N} {F} {O} {S} {nmax}\n")
+    for name, v in (("a0", a0), ("a1", a1), ("x0", x0), ("x1", x1), ("w", W), ("b", b << S)):
+        _ring(v, bw).tofile(str(d / f"{name}.bin"))
+    r = subprocess.run([BIN, str(d)], capture_output=True, text=True, timeout=180)
+    assert r.returncode == 0, r.stdout + r.stderr
+    dt = np.uint32 if bw == 32 else np.uint64
+    An = orc.adj_norm_plain(A)
+    got_an = _signed(np.fromfile(str(d / "adjn.bin"), dt), bw).reshape(B, N, N)
+    assert np.array_equal(got_an, An)
+    AX = np.floor_divide(np.einsum("bij,bjf->bif", An, X), 1 << S).reshape(B * N, F)
+    Z = np.floor_divide(AX @ W + (b << S), 1 << S)
+    act = np.maximum(Z, 0)
+    got_act = _signed(np.fromfile(str(d / "act.bin"), dt), bw).reshape(B * N, O)
+    assert np.array_equal(got_act, act)
+    got_out = _signed(np.fromfile(str(d / "out.bin"), dt), bw).reshape(B * N, O)
+    assert np.array_equal(got_out, act >> S)
+    c0, c1 = (int(v) for v in (d / "comm.txt").read_text().split())
+    assert c0 == c1 > 0

@@ -132,3 +132,72 @@ def test_config4_streamed_b256_bw64(orc, synth):
                            sh["m"][0][sl], sh["m"][1][sl], wl.prot[sl])
     assert np.array_equal(y, wants[0][sl])
     assert byts[0] == (B // Bs) * by
+
+
+@pytest.mark.parametrize("bw", [32, 64])
+def test_reference_model_dims_from_weights_file(orc, synth, tmp_path, bw):
+    """The model at the dimensions the reference deploys (gpu_mpc/deepdtagen.h:
+    12-31: 94 atom features, GCN 94-188-282-376, Nmax = 138, drug FCs 376-1024-128,
+    fusion 256-1024-512-256-1), weights read back from a weights.bin written in
+    the reference layout (reference/export_weights.py:38-75): the GPU dealer's keys
+    reproduce the oracle's, and the forward equals the fixed-point forward."""
+    import mpcx
+    import formats
+    B = 4
+    dims = synth.Dims(bw=bw, n_nodes=138, feat=94, gcn=(188, 282, 376), dfc=(1024, 128), prot=128,
+                      fus=(1024, 512, 256, 1))
+    wl = synth.workload(B, dims, seed=5)
+    wpath = str(tmp_path / "weights.bin")
+    formats.write_weights(wpath, wl.W, dims.layers(), scale=12)
+    W, layers, _ = formats.read_weights(wpath)
+    assert layers == dims.layers() and np.array_equal(W, wl.W)
+    d = _od(orc, dims)
+    want, code = orc.plain_forward(d, wl.X, wl.A, wl.mask, wl.prot, W)
+    assert code == 0, orc.domain_msg(code)
+    c = mpcx.Ctx(bw=bw)
+    m = mpcx.Model(c, dims, W, lanes=2)
+    m.keygen(B, 31)
+    split = mpcx.Model.lane_split(B, 2)
+    k0 = m.export_keys(0, B)
+    o0, _ = orc.model_keygen(d, split[0][1], mpcx.Model.lane_seed(31, 0), W)
+    assert np.array_equal(k0[:o0.size], o0)
+    m.set_inputs(B, *wl.shares["x"], *wl.shares["a"], *wl.shares["m"], wl.prot)
+    m.forward(B)
+    assert np.array_equal(m.output(B), want)
+    m.close()
+    c.close()
+
+
+@pytest.mark.parametrize("bw", [32, 64])
+def test_dealer_key_bytes(orc, synth, bw):
+    """A 16-byte dealer key (mpcx_set_dealer_key): the GPU dealer's keys equal
+    the oracle dealer's under the same key bytes, differ from the seed-only keys
+    of the same seed, and the forward stays bit-exact."""
+    import mpcx
+    B = 2
+    wl = synth.workload(B, synth.Dims(bw=bw), seed=8)
+    d = _od(orc, wl.dims)
+    want, code = orc.plain_forward(d, wl.X, wl.A, wl.mask, wl.prot, wl.W)
+    assert code == 0
+    dk = bytes(range(200, 216))
+    c = mpcx.Ctx(bw=bw)
+    plain = mpcx.Model(c, wl.dims, wl.W)
+    plain.keygen(B, 5)
+    k_plain = plain.export_keys(0, B)
+    plain.close()
+    c.set_dealer_key(dk)
+    m = mpcx.Model(c, wl.dims, wl.W)
+    m.keygen(B, 5)
+    got = [m.export_keys(p, B) for p in (0, 1)]
+    try:
+        orc.set_dealer_key(dk)
+        o0, o1 = orc.model_keygen(d, B, 5, wl.W)
+    finally:
+        orc.set_dealer_key(None)
+    assert np.array_equal(got[0], o0) and np.array_equal(got[1], o1)
+    assert not np.array_equal(got[0], k_plain)
+    m.set_inputs(B, *wl.shares["x"], *wl.shares["a"], *wl.shares["m"], wl.prot)
+    m.forward(B)
+    assert np.array_equal(m.output(B), want)
+    m.close()
+    c.close()

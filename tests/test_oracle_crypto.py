@@ -71,6 +71,28 @@ def test_prf_is_aes_of_counter(orc):
         assert np.array_equal(out[i], np.frombuffer(orc.aes_encrypt(key, _blk_bytes(blk)), "<u4"))
 
 
+def test_prf_under_dealer_key(orc):
+    """With the dealer's 16 secret bytes set, the PRF key of a key set is AES
+    under those bytes of (seed lo, seed hi, 0x4D415354, 0xFFFFFFFE); the PRF
+    blocks change with the key bytes at a fixed seed, and return to the
+    seed-only ones when the key is cleared."""
+    seed, dk = 0x1234, bytes(range(100, 116))
+    plain = orc.prf_blocks(seed, 7, 0x30, 5)
+    try:
+        orc.set_dealer_key(dk)
+        out = orc.prf_blocks(seed, 7, 0x30, 5)
+        kset = orc.aes_encrypt(dk, _blk_bytes(np.array([seed, 0, 0x4D415354, 0xFFFFFFFE], np.uint32)))
+        for i in range(5):
+            blk = np.array([i, 0, 0x30, 7], np.uint32)
+            assert np.array_equal(out[i], np.frombuffer(orc.aes_encrypt(kset, _blk_bytes(blk)), "<u4"))
+        assert not np.array_equal(out, plain)
+        orc.set_dealer_key(bytes(range(101, 117)))
+        assert not np.array_equal(orc.prf_blocks(seed, 7, 0x30, 5), out)
+    finally:
+        orc.set_dealer_key(None)
+    assert np.array_equal(orc.prf_blocks(seed, 7, 0x30, 5), plain)
+
+
 @pytest.mark.parametrize("m", [1, 3, 6, 7, 8, 9, 11])
 def test_dcf_exhaustive_small(orc, m):
     rng = np.random.default_rng(m)
