@@ -226,7 +226,12 @@ mpcx_status mpcx_create(int bw, int scale, int device, mpcx_ctx **out) {
       c->L.aes_block = 0;
     }
   }
-  if (const char *v = std::getenv("MPCX_GEMM")) c->L.gemm = std::strcmp(v, "valu") == 0 ? 1 : 0;
+  if (const char *v = std::getenv("MPCX_GEMM")) {
+    if (std::strcmp(v, "valu") == 0) c->L.gemm = 1;
+    else if (std::strcmp(v, "tiled") == 0) c->L.gemm = 2;
+    else if (std::strcmp(v, "auto") == 0 || !*v) c->L.gemm = 0;
+    else std::fprintf(stderr, "libmpcx: ignoring MPCX_GEMM=%s (auto, tiled or valu)\n", v);
+  }
   if (const char *v = std::getenv("MPCX_GRAPH")) c->L.graph = std::atoi(v) != 0 ? 1 : 0;
   *out = c;
   return MPCX_OK;
@@ -784,9 +789,9 @@ static mpcx_status sxs_eval_t(mpcx_ctx *c, int nb, int M, int K, int N, const vo
   h.Cin = reinterpret_cast<const T *>(k1 + lay.off_c);
   h.C = m1;
   h.sign = -1;
-  HIPC(c, launch_gemm_pair<T>(c->L, g, h), "gemm");
+  // both parties' products and the reconstruction of the exchanged shares
+  HIPC(c, launch_gemm_pair_sum<T>(c->L, g, h, static_cast<T *>(out)), "gemm");
   c->counters.msg(nc, c->bw);
-  HIPC(c, launch_reconstruct<T>(c->L, nc, m0, m1, static_cast<T *>(out)), "reconstruct");
   HIPC(c, hipStreamSynchronize(c->L.stream), "sync");
   return MPCX_OK;
 }

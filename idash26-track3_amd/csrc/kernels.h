@@ -23,8 +23,9 @@ struct Launch {
   // Launches of a profiled forward use a separately named instantiation of the
   // DCF-evaluation kernel (same code), so kernel traces can tell them apart.
   bool profiled = false;
-  // ring GEMM path over Z_2^32: 0 = int8 matrix cores (limb products), 1 = VALU
-  // (Z_2^64 always uses the VALU path)
+  // ring GEMM path: 0 = int8 matrix cores, the wide-K kernel where it applies
+  // (use_wide) and the tiled kernels elsewhere; 1 = VALU; 2 = tiled matrix-core
+  // kernels only.  Z_2^64 products with K >= 2^15 take the VALU path always.
   int gemm = 0;
   // model forwards with resident keys are captured once per batch size into a
   // HIP graph and replayed (0 = enqueue every kernel each time)
@@ -174,6 +175,11 @@ hipError_t launch_gemm(const Launch &L, const GemmArgs<T> &g);
 // (the Beaver products of both parties of an SxS gate), else one after another.
 template <typename T>
 hipError_t launch_gemm_pair(const Launch &L, const GemmArgs<T> &g0, const GemmArgs<T> &g1);
+// Both parties' products of an SxS gate, reconstructed: out = C0 + C1 (batch x
+// M x N, contiguous).  One launch where the wide-K kernel applies; otherwise
+// launch_gemm_pair into g0.C and g1.C, then the sum.
+template <typename T>
+hipError_t launch_gemm_pair_sum(const Launch &L, const GemmArgs<T> &g0, const GemmArgs<T> &g1, T *out);
 
 // ---------------- SxS keys ----------------
 template <typename T>

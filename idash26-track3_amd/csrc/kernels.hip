@@ -1623,6 +1623,269 @@ __global__ __launch_bounds__(256) void k_gemm_mfma64(GemmArgs<uint64_t> g0, Gemm
   gemm_mfma64_tile(second ? g1 : g0, second ? z - nz0 : z, As, Bt);
 }
 
+// ---------------------------------------------------------------------------
+// Wide-K ring GEMM on the int8 matrix cores (both rings, the digit algebra of
+// the two kernels above).  Those walk K in 64-word (Z_2^32) or 32-word (Z_2^64)
+// steps and wait for a round trip to memory at every step, with about one
+// 4-wave block per CU on this path's shapes (K = 78..312 words per segment,
+// 140 x 140 per-graph blocks), so a tile costs a few memory latencies.  Here a
+// 512-thread block stages KW 32-bit words of K per step (kWideK words of
+// Z_2^32, half as many of Z_2^64): every load of a step is in flight at once,
+// and the next step's loads are issued before the current step's MFMAs, so a
+// segment of at most KW words costs one round trip.  LDS as above: A as [m][k],
+// B transposed to [n][k], rows of KW + 4 words (16-byte reads by 8 consecutive
+// lanes of consecutive rows fall in distinct bank groups).  Wave w computes
+// rows 16 (w & 3) .. + 15 and columns 32 (w >> 2) .. + 31 of the 64 x 64 tile
+// (two 16 x 16 MFMA tiles).  One step covers one segment only; a problem's
+// steps run first segment first.
+//
+// FUSED (both parties of an SxS gate on one GPU): the block evaluates party
+// 0's problem g0 and then party 1's problem g1 on the same tile and writes
+// C0 + C1, the reconstruction of the masked product, to g0.C -- what
+// launch_gemm_pair followed by a reconstruction returns, without writing the
+// shares.  Otherwise g1 is unused and g0.C = g0.Cin + g0.sign * (products).
+// ---------------------------------------------------------------------------
+constexpr int kWideK = 288;        // 32-bit words of K per step (LDS: 2 * 64 * 292 * 4 = 149.5 KB)
+constexpr int kWideThreads = 512;  // 8 waves
+
+template <typename T>
+struct WideStep {
+  const T *a, *a2, *b, *b2;  // segment operands of batch entry bz (a2, b2: masks or null)
+  int kb, klen;              // K range [kb, kb + klen) of the segment
+};
+// K words of a step: a segment with masks stages four operands, so its steps
+// are half as wide (the staging registers hold two operand panels of KW words)
+template <typename T, int KW>
+__device__ __forceinline__ int wide_kt(bool masked) {
+  return (masked ? KW / 2 : KW) * 4 / int(sizeof(T));
+}
+template <typename T, int KW>
+__device__ __forceinline__ int wide_steps(const GemmArgs<T> &g) {
+  const int k0 = wide_kt<T, KW>(g.A2 || g.B2), k1 = wide_kt<T, KW>(false);
+  return (g.K + k0 - 1) / k0 + (g.A1b ? (g.K + k1 - 1) / k1 : 0);
+}
+template <typename T, int KW>
+__device__ __forceinline__ WideStep<T> wide_step(const GemmArgs<T> &g, int bz, int i) {
+  const bool masked = g.A2 || g.B2;
+  const int k0 = wide_kt<T, KW>(masked), n0 = (g.K + k0 - 1) / k0;
+  const bool seg = i >= n0;
+  const int kt = seg ? wide_kt<T, KW>(false) : k0;
+  WideStep<T> w;
+  w.kb = (seg ? i - n0 : i) * kt;
+  w.klen = min(kt, g.K - w.kb);
+  w.a = (seg ? g.A1b : g.A1) + size_t(bz) * g.sA;
+  w.b = (seg ? g.B1b : g.B1) + size_t(bz) * g.sB;
+  w.a2 = (!seg && g.A2) ? g.A2 + size_t(bz) * g.sA : nullptr;
+  w.b2 = (!seg && g.B2) ? g.B2 + size_t(bz) * g.sB : nullptr;
+  return w;
+}
+// balanced digits of a 16-byte group (four Z_2^32 words or two Z_2^64 words) of x - y
+template <typename T>
+__device__ __forceinline__ uint4 wide_digits(uint4 x, uint4 y) {
+  if constexpr (sizeof(T) == 4) {
+    return make_uint4(ring_digits(x.x - y.x), ring_digits(x.y - y.y), ring_digits(x.z - y.z), ring_digits(x.w - y.w));
+  } else {
+    const uint64_t lo = ring_digits64(((uint64_t(x.y) << 32) | x.x) - ((uint64_t(y.y) << 32) | y.x));
+    const uint64_t hi = ring_digits64(((uint64_t(x.w) << 32) | x.z) - ((uint64_t(y.w) << 32) | y.z));
+    return make_uint4(uint32_t(lo), uint32_t(lo >> 32), uint32_t(hi), uint32_t(hi >> 32));
+  }
+}
+template <typename T>
+__device__ __forceinline__ uint4 wide_pack(const T (&v)[16 / sizeof(T)]) {
+  if constexpr (sizeof(T) == 4) return make_uint4(v[0], v[1], v[2], v[3]);
+  else return make_uint4(uint32_t(v[0]), uint32_t(v[0] >> 32), uint32_t(v[1]), uint32_t(v[1] >> 32));
+}
+// 16-byte group kv .. kv + WPG - 1 of row `row` of a row-major matrix with
+// `ld` words per row, zero where out of [0, klen) (in = the row exists)
+template <typename T, bool VA>
+__device__ __forceinline__ uint4 wide_row_group(const T *p, size_t row, int ld, int kb, int kv, int klen, bool in) {
+  constexpr int WPG = 16 / int(sizeof(T));
+  uint4 r = make_uint4(0u, 0u, 0u, 0u);
+  if constexpr (VA) {  // ld, kb and klen are multiples of WPG
+    if (in && kv < klen) r = *reinterpret_cast<const uint4 *>(p + row * ld + kb + kv);
+  } else {
+    T x[WPG];
+    const T *q = p + row * ld + kb + kv;
+#pragma unroll
+    for (int e = 0; e < WPG; e++) {
+      x[e] = 0;
+      if (in && kv + e < klen) x[e] = q[e];
+    }
+    r = wide_pack<T>(x);
+  }
+  return r;
+}
+// WPG consecutive k (from kb + kv) of column `col` of a row-major K x ld matrix
+template <typename T>
+__device__ __forceinline__ uint4 wide_col_group(const T *p, int col, int ld, int kb, int kv, int klen, bool in) {
+  constexpr int WPG = 16 / int(sizeof(T));
+  T x[WPG];
+  const T *q = p + size_t(kb + kv) * ld + col;
+#pragma unroll
+  for (int e = 0; e < WPG; e++) {
+    x[e] = 0;
+    if (in && kv + e < klen) x[e] = q[size_t(e) * ld];
+  }
+  return wide_pack<T>(x);
+}
+
+template <typename T, int KW, bool VA, bool FUSED>
+__global__ __launch_bounds__(kWideThreads) void k_gemm_wide(GemmArgs<T> g0, GemmArgs<T> g1) {
+  constexpr int LDK = KW + 4, WPG = 16 / int(sizeof(T)), NQ = int(sizeof(T));
+  // 16-byte groups per thread and operand panel: NJ in a plain step, NJM in a
+  // masked one (then slots NJM.. hold the masks' groups)
+  constexpr int NJ = (KW / 4 + 7) / 8, NJM = (KW / 8 + 7) / 8, NS = NJ > 2 * NJM ? NJ : 2 * NJM;
+  __shared__ __align__(16) uint32_t As[64 * LDK];
+  __shared__ __align__(16) uint32_t Bt[64 * LDK];
+  const int bz = int(blockIdx.z), m0 = int(blockIdx.y) * 64, n0 = int(blockIdx.x) * 64;
+  const int tid = int(threadIdx.x), lane = tid & 63, wave = tid >> 6;
+  const int li = lane & 15, lg = lane >> 4, rg = wave & 3, cg = wave >> 2;
+  const int M = g0.M, N = g0.N, K = g0.K;  // FUSED: both problems have the shape of g0
+  // staging: A group j of thread tid is row tid >> 3, 16-byte group (tid & 7) + 8j
+  // of the step; B group j is column tid & 63, k words WPG ((tid >> 6) + 8j) + e
+  const int arow = tid >> 3, bn = tid & 63, ag = tid & 7, bg = tid >> 6;
+  const bool arow_ok = m0 + arow < M, bn_ok = n0 + bn < N;
+  uint4 ra[NS], rb[NS];
+  bool masked = false;  // the staged step's kind (uniform)
+  auto load = [&](const WideStep<T> &w) {
+    masked = w.a2 || w.b2;
+    const size_t row = size_t(m0 + arow);
+    const T *a2 = w.a2 ? w.a2 : w.a, *b2 = w.b2 ? w.b2 : w.b;  // a missing mask reads as zero below
+    if (masked) {
+#pragma unroll
+      for (int j = 0; j < NJM; j++) {
+        const int gi = ag + 8 * j;
+        const bool in = arow_ok && gi < KW / 8;
+        ra[j] = wide_row_group<T, VA>(w.a, row, K, w.kb, gi * WPG, w.klen, in);
+        ra[NJM + j] = wide_row_group<T, VA>(a2, row, K, w.kb, gi * WPG, w.klen, in && w.a2);
+      }
+#pragma unroll
+      for (int j = 0; j < NJM; j++) {
+        const int gi = bg + 8 * j;
+        const bool in = bn_ok && gi < KW / 8;
+        rb[j] = wide_col_group<T>(w.b, n0 + bn, N, w.kb, gi * WPG, w.klen, in);
+        rb[NJM + j] = wide_col_group<T>(b2, n0 + bn, N, w.kb, gi * WPG, w.klen, in && w.b2);
+      }
+    } else {
+#pragma unroll
+      for (int j = 0; j < NJ; j++) {
+        const int gi = ag + 8 * j;
+        ra[j] = wide_row_group<T, VA>(w.a, row, K, w.kb, gi * WPG, w.klen, arow_ok && gi < KW / 4);
+      }
+#pragma unroll
+      for (int j = 0; j < NJ; j++) {
+        const int gi = bg + 8 * j;
+        rb[j] = wide_col_group<T>(w.b, n0 + bn, N, w.kb, gi * WPG, w.klen, bn_ok && gi < KW / 4);
+      }
+    }
+  };
+  // every word of the step's rows is written (zeros past klen, M and N)
+  auto store = [&]() {
+    const uint4 z = make_uint4(0u, 0u, 0u, 0u);
+    if (masked) {
+#pragma unroll
+      for (int j = 0; j < NJM; j++) {
+        const int ga = ag + 8 * j, gb = bg + 8 * j;
+        if (ga < KW / 8) *reinterpret_cast<uint4 *>(&As[arow * LDK + 4 * ga]) = wide_digits<T>(ra[j], ra[NJM + j]);
+        if (gb < KW / 8) *reinterpret_cast<uint4 *>(&Bt[bn * LDK + 4 * gb]) = wide_digits<T>(rb[j], rb[NJM + j]);
+      }
+    } else {
+#pragma unroll
+      for (int j = 0; j < NJ; j++) {
+        const int ga = ag + 8 * j, gb = bg + 8 * j;
+        if (ga < KW / 4) *reinterpret_cast<uint4 *>(&As[arow * LDK + 4 * ga]) = wide_digits<T>(ra[j], z);
+        if (gb < KW / 4) *reinterpret_cast<uint4 *>(&Bt[bn * LDK + 4 * gb]) = wide_digits<T>(rb[j], z);
+      }
+    }
+  };
+  v4i_t acc[2][NQ];
+#pragma unroll
+  for (int t = 0; t < 2; t++)
+#pragma unroll
+    for (int q = 0; q < NQ; q++) acc[t][q] = v4i_t{0, 0, 0, 0};
+  T vs[2][4];
+#pragma unroll
+  for (int t = 0; t < 2; t++)
+#pragma unroll
+    for (int r = 0; r < 4; r++) vs[t][r] = 0;
+  // adds sign * (this problem's products) to vs and clears the accumulators
+  auto fold = [&](int sign) {
+#pragma unroll
+    for (int t = 0; t < 2; t++)
+#pragma unroll
+      for (int r = 0; r < 4; r++) {
+        T v = 0;
+#pragma unroll
+        for (int q = 0; q < NQ; q++) {
+          if constexpr (sizeof(T) == 4) v += uint32_t(acc[t][q][r]) << (8 * q);
+          else v += uint64_t(int64_t(acc[t][q][r])) << (8 * q);
+        }
+        vs[t][r] += sign < 0 ? T(0) - v : v;
+#pragma unroll
+        for (int q = 0; q < NQ; q++) acc[t][q][r] = 0;
+      }
+  };
+  const int n0steps = wide_steps<T, KW>(g0), nsteps = n0steps + (FUSED ? wide_steps<T, KW>(g1) : 0);
+  auto step_of = [&](int i) { return i < n0steps ? wide_step<T, KW>(g0, bz, i) : wide_step<T, KW>(g1, bz, i - n0steps); };
+  WideStep<T> cur = step_of(0);
+  load(cur);
+  for (int i = 0; i < nsteps; i++) {
+    store();
+    __syncthreads();
+    const int nkc = (cur.klen * int(sizeof(T) / 4) + 15) / 16;
+    if (i + 1 < nsteps) {
+      cur = step_of(i + 1);
+      load(cur);
+    }
+    for (int kc = 0; kc < nkc; kc++) {
+      const uint4 a = *reinterpret_cast<const uint4 *>(&As[(16 * rg + li) * LDK + 16 * kc + 4 * lg]);
+      v4i_t as[NQ];
+      if constexpr (sizeof(T) == 4) {
+        constexpr uint32_t sel[4] = {0x0c0c0c00u, 0x0c0c0001u, 0x0c000102u, 0x00010203u};
+#pragma unroll
+        for (int q = 0; q < 4; q++)
+          as[q] = v4i_t{int(__builtin_amdgcn_perm(0u, a.x, sel[q])), int(__builtin_amdgcn_perm(0u, a.y, sel[q])),
+                        int(__builtin_amdgcn_perm(0u, a.z, sel[q])), int(__builtin_amdgcn_perm(0u, a.w, sel[q]))};
+      } else {
+#pragma unroll
+        for (int q = 0; q < 8; q++) {
+          const uint32_t lo = digit_sel(q, 0), hi = digit_sel(q, 4);
+          as[q] = v4i_t{int(__builtin_amdgcn_perm(a.y, a.x, lo)), int(__builtin_amdgcn_perm(a.y, a.x, hi)),
+                        int(__builtin_amdgcn_perm(a.w, a.z, lo)), int(__builtin_amdgcn_perm(a.w, a.z, hi))};
+        }
+      }
+#pragma unroll
+      for (int t = 0; t < 2; t++) {
+        const uint4 b = *reinterpret_cast<const uint4 *>(&Bt[(32 * cg + 16 * t + li) * LDK + 16 * kc + 4 * lg]);
+        const v4i_t bv = v4i_t{int(b.x), int(b.y), int(b.z), int(b.w)};
+#pragma unroll
+        for (int q = 0; q < NQ; q++) acc[t][q] = __builtin_amdgcn_mfma_i32_16x16x64_i8(as[q], bv, acc[t][q], 0, 0, 0);
+      }
+    }
+    if (i + 1 == n0steps) fold(g0.sign);
+    else if (i + 1 == nsteps) fold(g1.sign);
+    __syncthreads();
+  }
+  T *C = g0.C + size_t(bz) * g0.sC;
+  const T *Cin0 = g0.Cin ? g0.Cin + size_t(bz) * g0.sC : nullptr;
+  const T *Cin1 = FUSED && g1.Cin ? g1.Cin + size_t(bz) * g1.sC : nullptr;
+#pragma unroll
+  for (int t = 0; t < 2; t++) {
+    const int gn = n0 + 32 * cg + 16 * t + li;
+#pragma unroll
+    for (int r = 0; r < 4; r++) {
+      // accumulator register r of lane (li, lg): row 4 lg + r, column li of the MFMA tile
+      const int gm = m0 + 16 * rg + 4 * lg + r;
+      if (gm >= M || gn >= N) continue;
+      const size_t idx = size_t(gm) * N + gn;
+      T v = vs[t][r];
+      if (Cin0) v += Cin0[idx];
+      if (Cin1) v += Cin1[idx];
+      C[idx] = v;
+    }
+  }
+}
+
 // C[b] = Cin[b] (or 0) before the split-K slices are added
 template <typename T>
 __global__ void k_gemm_init(int M, int N, int batch, size_t sC, const T *Cin, T *C) {
@@ -1669,7 +1932,7 @@ constexpr int mfma_bk() {
 // below 2^15 (the low shifts' int32 sums stay exact)
 template <typename T>
 static bool use_mfma(const Launch &L, const GemmArgs<T> &g) {
-  if (L.gemm != 0) return false;
+  if (L.gemm == 1) return false;
   constexpr int bk = mfma_bk<T>();
   const int Kt = g.A1b ? (g.K + bk - 1) / bk * bk + g.K : g.K;
   return sizeof(T) == 4 || Kt < (1 << 15);
@@ -1696,9 +1959,37 @@ static hipError_t gemm_init(const Launch &L, const GemmArgs<T> &g) {
   return hipGetLastError();
 }
 
+// The wide-K kernel: automatic path selection, the matrix-core path, and either
+// enough tiles to occupy a quarter of the CUs or at most one K step per
+// segment.  A long K over few tiles (the fully connected layers: 22 rows,
+// K = 312..1024) is spread over more CUs by the split-K tiled kernel.
+template <typename T>
+static bool use_wide(const Launch &L, const GemmArgs<T> &g) {
+  if (L.gemm != 0 || !use_mfma(L, g)) return false;
+  constexpr int KT = kWideK * 4 / int(sizeof(T));
+  return gemm_tiles(g) >= L.num_cu / 4 || g.K <= KT;
+}
+// rows of A (and of the masks and second segment) read as 16-byte groups
+template <typename T>
+static bool wide_vec_a(const GemmArgs<T> &g) {
+  constexpr int wpg = 16 / int(sizeof(T));
+  return g.K % wpg == 0 && (g.batch == 1 || g.sA % wpg == 0) && aligned16(g.A1) && aligned16(g.A2) &&
+         aligned16(g.A1b);
+}
+template <typename T, bool FUSED>
+static hipError_t launch_wide(const Launch &L, const GemmArgs<T> &g0, const GemmArgs<T> &g1) {
+  const dim3 grid((g0.N + 63) / 64, (g0.M + 63) / 64, g0.batch);
+  if (wide_vec_a(g0) && (!FUSED || wide_vec_a(g1)))
+    hipLaunchKernelGGL((k_gemm_wide<T, kWideK, true, FUSED>), grid, dim3(kWideThreads), 0, L.stream, g0, g1);
+  else
+    hipLaunchKernelGGL((k_gemm_wide<T, kWideK, false, FUSED>), grid, dim3(kWideThreads), 0, L.stream, g0, g1);
+  return hipGetLastError();
+}
+
 template <typename T>
 hipError_t launch_gemm(const Launch &L, const GemmArgs<T> &g0) {
   if (g0.M <= 0 || g0.N <= 0 || g0.batch <= 0) return hipSuccess;
+  if (use_wide(L, g0)) return launch_wide<T, false>(L, g0, g0);
   const bool mfma = use_mfma(L, g0);
   if (g0.A1b && !mfma) {
     // the VALU kernel takes one K segment: add the second product in a second launch
@@ -1739,6 +2030,21 @@ hipError_t launch_gemm_pair(const Launch &L, const GemmArgs<T> &p0, const GemmAr
   const int nz0 = g0.batch * g0.ksplit;
   dim3 grid((std::max(g0.N, g1.N) + 63) / 64, (std::max(g0.M, g1.M) + 63) / 64, nz0 + g1.batch * g1.ksplit);
   return launch_mfma(L, grid, g0, g1, nz0);
+}
+
+template <typename T>
+hipError_t launch_gemm_pair_sum(const Launch &L, const GemmArgs<T> &g0, const GemmArgs<T> &g1, T *out) {
+  if (g0.M <= 0 || g0.N <= 0 || g0.batch <= 0) return hipSuccess;
+  const bool same = g0.M == g1.M && g0.N == g1.N && g0.K == g1.K && g0.batch == g1.batch &&
+                    g0.sC == size_t(g0.M) * g0.N && g1.sC == g0.sC;
+  if (same && use_wide(L, g0) && use_wide(L, g1)) {
+    GemmArgs<T> a = g0;
+    a.C = out;
+    return launch_wide<T, true>(L, a, g1);
+  }
+  hipError_t e = launch_gemm_pair<T>(L, g0, g1);
+  if (e != hipSuccess) return e;
+  return launch_reconstruct<T>(L, size_t(g0.batch) * g0.M * g0.N, g0.C, g1.C, out);
 }
 
 template <typename T, int NT, int REP>
@@ -1947,6 +2253,7 @@ hipError_t launch_rowsum(const Launch &L, size_t rows, int len, const T *a, T *o
                                             const T *, T *, T *);                                                    \
   template hipError_t launch_gemm<T>(const Launch &, const GemmArgs<T> &);                                           \
   template hipError_t launch_gemm_pair<T>(const Launch &, const GemmArgs<T> &, const GemmArgs<T> &);                \
+  template hipError_t launch_gemm_pair_sum<T>(const Launch &, const GemmArgs<T> &, const GemmArgs<T> &, T *);       \
   template hipError_t launch_split<T>(const Launch &, uint64_t, uint32_t, uint32_t, size_t, const T *, T *, T *,     \
                                       T *);                                                                          \
   template hipError_t launch_prf_ring<T>(const Launch &, uint64_t, uint32_t, uint32_t, size_t, T *);                \

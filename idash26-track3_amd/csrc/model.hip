@@ -352,9 +352,9 @@ struct Runner {
       leave(end);
       return hipSuccess;
     }
-    TRY(launch_gemm_pair<T>(L, g, h));
+    // both parties' products and the reconstruction of the exchanged shares
+    TRY(launch_gemm_pair_sum<T>(L, g, h, out));
     TRY(span.end());
-    TRY(launch_reconstruct<T>(L, nc, ws.m0.p, ws.m1.p, out));
     leave(end);
     return hipSuccess;
   }
