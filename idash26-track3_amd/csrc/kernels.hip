@@ -1886,6 +1886,178 @@ __global__ __launch_bounds__(kWideThreads) void k_gemm_wide(GemmArgs<T> g0, Gemm
   }
 }
 
+// MFMA row operands of one 16-byte LDS read (16 Z_2^32 or 8 Z_2^64 words of a
+// row, balanced digits): shift s takes digit s - j of each word at byte j
+template <typename T>
+__device__ __forceinline__ void digit_shifts(uint4 a, v4i_t (&as)[sizeof(T)]) {
+  if constexpr (sizeof(T) == 4) {
+    constexpr uint32_t sel[4] = {0x0c0c0c00u, 0x0c0c0001u, 0x0c000102u, 0x00010203u};
+#pragma unroll
+    for (int q = 0; q < 4; q++)
+      as[q] = v4i_t{int(__builtin_amdgcn_perm(0u, a.x, sel[q])), int(__builtin_amdgcn_perm(0u, a.y, sel[q])),
+                    int(__builtin_amdgcn_perm(0u, a.z, sel[q])), int(__builtin_amdgcn_perm(0u, a.w, sel[q]))};
+  } else {
+#pragma unroll
+    for (int q = 0; q < 8; q++) {
+      const uint32_t lo = digit_sel(q, 0), hi = digit_sel(q, 4);
+      as[q] = v4i_t{int(__builtin_amdgcn_perm(a.y, a.x, lo)), int(__builtin_amdgcn_perm(a.y, a.x, hi)),
+                    int(__builtin_amdgcn_perm(a.w, a.z, lo)), int(__builtin_amdgcn_perm(a.w, a.z, hi))};
+    }
+  }
+}
+// the ring word of accumulator register r (shift sums acc[q][r])
+template <typename T>
+__device__ __forceinline__ T digit_fold(const v4i_t (&acc)[sizeof(T)], int r) {
+  T v = 0;
+#pragma unroll
+  for (int q = 0; q < int(sizeof(T)); q++) {
+    if constexpr (sizeof(T) == 4) v += uint32_t(acc[q][r]) << (8 * q);
+    else v += uint64_t(int64_t(acc[q][r])) << (8 * q);
+  }
+  return v;
+}
+
+// ---------------------------------------------------------------------------
+// Both parties' Beaver products of an SxS gate on one GPU, reconstructed, per
+// 48 x 32 output tile: party 0's C0 + (A^ - RA0)(B^ - RB0) and party 1's
+// C1 - (A^ RB1 + RA1 B^), written as their sum (the masked product both
+// parties reveal).  Each K phase (144 words of Z_2^32, 48 of Z_2^64) stages all
+// six operand panels at once -- A^, RA0, RA1 rows and B^, RB0, RB1 columns, as
+// digits of A^ - RA0, A^, RA1 and of B^ - RB0, RB1, B^ in LDS -- so the
+// per-graph products of the affinity model (140 x 140 by 140 x N) cost one
+// memory round trip (three for Z_2^64); the next phase's loads are issued before
+// the current phase's MFMAs.  Six waves, one 16 x 16 MFMA tile each (rows
+// 16 (w % 3), columns 16 (w / 3)), with party 0's and party 1's accumulators.
+// The 48-row tiles cover 140 rows as 48 + 48 + 44.
+// ---------------------------------------------------------------------------
+constexpr int kSxsTM = 48, kSxsTN = 32, kSxsThreads = 384;
+// 32-bit words of K per phase: the Z_2^64 kernel's staging registers (and
+// wider accumulator sets) leave room for two thirds of the Z_2^32 width
+template <typename T>
+constexpr int sxs_kc() {
+  return sizeof(T) == 4 ? 144 : 96;
+}
+
+template <typename T, bool VA>
+__global__ __launch_bounds__(kSxsThreads) void k_sxs_fused(GemmArgs<T> g0, GemmArgs<T> g1) {
+  constexpr int KC = sxs_kc<T>(), WPG = 16 / int(sizeof(T)), NQ = int(sizeof(T)), LDK = KC + 4, GR = KC / 4;
+  constexpr int KT = KC * 4 / int(sizeof(T));  // words of T per phase
+  constexpr int NA = (kSxsTM * GR + kSxsThreads - 1) / kSxsThreads, NB = kSxsTN * GR / kSxsThreads;
+  static_assert(kSxsTN * GR % kSxsThreads == 0, "B groups split evenly");
+  __shared__ __align__(16) uint32_t As[3 * kSxsTM * LDK];  // digits of A^ - RA0, A^, RA1
+  __shared__ __align__(16) uint32_t Bt[3 * kSxsTN * LDK];  // digits of B^ - RB0, RB1, B^ (as [n][k])
+  const int bz = int(blockIdx.z), m0 = int(blockIdx.y) * kSxsTM, n0 = int(blockIdx.x) * kSxsTN;
+  const int M = g0.M, N = g0.N, K = g0.K;
+  const int tid = int(threadIdx.x), lane = tid & 63, wave = tid >> 6;
+  const int li = lane & 15, lg = lane >> 4, rg = wave % 3, cg = wave / 3;
+  const T *Ah = g0.A1 + size_t(bz) * g0.sA, *RA0 = g0.A2 + size_t(bz) * g0.sA, *RA1 = g1.A1b + size_t(bz) * g1.sA;
+  const T *Bh = g0.B1 + size_t(bz) * g0.sB, *RB0 = g0.B2 + size_t(bz) * g0.sB, *RB1 = g1.B1 + size_t(bz) * g1.sB;
+  // this lane's four outputs: rows 4 lg + r of the wave's MFMA tile, column li
+  const int on = n0 + 16 * cg + li;
+  T cin[4];
+#pragma unroll
+  for (int r = 0; r < 4; r++) {
+    const int om = m0 + 16 * rg + 4 * lg + r;
+    cin[r] = 0;
+    if (om < M && on < N) {
+      const size_t idx = size_t(om) * N + on;
+      if (g0.Cin) cin[r] += g0.Cin[size_t(bz) * g0.sC + idx];
+      if (g1.Cin) cin[r] += g1.Cin[size_t(bz) * g1.sC + idx];
+    }
+  }
+  uint4 xa[NA], xa0[NA], xa1[NA], xb[NB], xb0[NB], xb1[NB];
+  auto load = [&](int kb) {
+    const int klen = min(KT, K - kb);
+#pragma unroll
+    for (int j = 0; j < NA; j++) {
+      const int f = tid + kSxsThreads * j, r = f / GR, gi = f % GR;
+      const bool in = f < kSxsTM * GR && m0 + r < M;
+      const size_t row = size_t(m0 + r);
+      xa[j] = wide_row_group<T, VA>(Ah, row, K, kb, gi * WPG, klen, in);
+      xa0[j] = wide_row_group<T, VA>(RA0, row, K, kb, gi * WPG, klen, in);
+      xa1[j] = wide_row_group<T, VA>(RA1, row, K, kb, gi * WPG, klen, in);
+    }
+#pragma unroll
+    for (int j = 0; j < NB; j++) {
+      const int f = tid + kSxsThreads * j, n = f % kSxsTN, gi = f / kSxsTN;
+      const bool in = n0 + n < N;
+      xb[j] = wide_col_group<T>(Bh, n0 + n, N, kb, gi * WPG, klen, in);
+      xb0[j] = wide_col_group<T>(RB0, n0 + n, N, kb, gi * WPG, klen, in);
+      xb1[j] = wide_col_group<T>(RB1, n0 + n, N, kb, gi * WPG, klen, in);
+    }
+  };
+  // every word of the panels' rows is written (zeros past K, M and N)
+  auto store = [&]() {
+    const uint4 z = make_uint4(0u, 0u, 0u, 0u);
+#pragma unroll
+    for (int j = 0; j < NA; j++) {
+      const int f = tid + kSxsThreads * j, r = f / GR, gi = f % GR;
+      if (f < kSxsTM * GR) {
+        uint32_t *p = &As[r * LDK + 4 * gi];
+        *reinterpret_cast<uint4 *>(p) = wide_digits<T>(xa[j], xa0[j]);
+        *reinterpret_cast<uint4 *>(p + kSxsTM * LDK) = wide_digits<T>(xa[j], z);
+        *reinterpret_cast<uint4 *>(p + 2 * kSxsTM * LDK) = wide_digits<T>(xa1[j], z);
+      }
+    }
+#pragma unroll
+    for (int j = 0; j < NB; j++) {
+      const int f = tid + kSxsThreads * j, n = f % kSxsTN, gi = f / kSxsTN;
+      uint32_t *p = &Bt[n * LDK + 4 * gi];
+      *reinterpret_cast<uint4 *>(p) = wide_digits<T>(xb[j], xb0[j]);
+      *reinterpret_cast<uint4 *>(p + kSxsTN * LDK) = wide_digits<T>(xb1[j], z);
+      *reinterpret_cast<uint4 *>(p + 2 * kSxsTN * LDK) = wide_digits<T>(xb[j], z);
+    }
+  };
+  // one accumulator set, folded into ring words after each party's MFMAs of a
+  // phase (a phase's shift sums are exact, far below 2^15 words of K)
+  v4i_t acc[NQ];
+#pragma unroll
+  for (int q = 0; q < NQ; q++) acc[q] = v4i_t{0, 0, 0, 0};
+  T vs0[4] = {0, 0, 0, 0}, vs1[4] = {0, 0, 0, 0};
+  auto fold = [&](T (&vs)[4]) {
+#pragma unroll
+    for (int r = 0; r < 4; r++) {
+      vs[r] += digit_fold<T>(acc, r);
+#pragma unroll
+      for (int q = 0; q < NQ; q++) acc[q][r] = 0;
+    }
+  };
+  // acc += (row panel pa) . (column panel pb)^T over the phase's nkc 16-word chunks
+  auto mfma_panel = [&](int pa, int pb, int nkc) {
+    const int ar = pa * kSxsTM * LDK + (16 * rg + li) * LDK + 4 * lg;
+    const int br = pb * kSxsTN * LDK + (16 * cg + li) * LDK + 4 * lg;
+    for (int kc = 0; kc < nkc; kc++) {
+      v4i_t as[NQ];
+      const uint4 b = *reinterpret_cast<const uint4 *>(&Bt[br + 16 * kc]);
+      const v4i_t bv = v4i_t{int(b.x), int(b.y), int(b.z), int(b.w)};
+      digit_shifts<T>(*reinterpret_cast<const uint4 *>(&As[ar + 16 * kc]), as);
+#pragma unroll
+      for (int q = 0; q < NQ; q++) acc[q] = __builtin_amdgcn_mfma_i32_16x16x64_i8(as[q], bv, acc[q], 0, 0, 0);
+    }
+  };
+  load(0);
+  for (int kb = 0; kb < K; kb += KT) {
+    store();
+    __syncthreads();
+    const int nkc = (min(KT, K - kb) * int(sizeof(T) / 4) + 15) / 16;
+    if (kb + KT < K) load(kb + KT);
+    mfma_panel(0, 0, nkc);  // party 0: (A^ - RA0)(B^ - RB0)
+    fold(vs0);
+    mfma_panel(1, 1, nkc);  // party 1: A^ RB1 + RA1 B^
+    mfma_panel(2, 2, nkc);
+    fold(vs1);
+    __syncthreads();
+  }
+  T *C = g0.C + size_t(bz) * g0.sC;
+#pragma unroll
+  for (int r = 0; r < 4; r++) {
+    const int om = m0 + 16 * rg + 4 * lg + r;
+    if (om >= M || on >= N) continue;
+    // party 0's share (sign +1) plus party 1's (sign -1)
+    C[size_t(om) * N + on] = cin[r] + vs0[r] - vs1[r];
+  }
+}
+
 // C[b] = Cin[b] (or 0) before the split-K slices are added
 template <typename T>
 __global__ void k_gemm_init(int M, int N, int batch, size_t sC, const T *Cin, T *C) {
@@ -2032,9 +2204,34 @@ hipError_t launch_gemm_pair(const Launch &L, const GemmArgs<T> &p0, const GemmAr
   return launch_mfma(L, grid, g0, g1, nz0);
 }
 
+// k_sxs_fused applies to the Beaver pair as the SxS gates form it: party 0
+// (A1 - A2)(B1 - B2) + Cin with sign +1, party 1 with the same A1 in its first
+// segment, the same B1 in its second, no masks, sign -1; the same shapes and
+// strides; enough tiles for a quarter of the CUs or K within one phase.
+template <typename T>
+static bool use_sxs_fused(const Launch &L, const GemmArgs<T> &g0, const GemmArgs<T> &g1) {
+  if (L.gemm != 0 || !use_mfma(L, g0) || !use_mfma(L, g1)) return false;
+  const bool form = g0.A2 && g0.B2 && !g0.A1b && g0.sign == 1 && g1.A1 == g0.A1 && g1.B1b == g0.B1 && g1.A1b &&
+                    g1.B1 && !g1.A2 && !g1.B2 && g1.sign == -1;
+  const bool shape = g0.M == g1.M && g0.N == g1.N && g0.K == g1.K && g0.batch == g1.batch && g0.sA == g1.sA &&
+                     g0.sB == g1.sB && g0.sC == size_t(g0.M) * g0.N && g1.sC == g0.sC;
+  const int tiles = ((g0.N + kSxsTN - 1) / kSxsTN) * ((g0.M + kSxsTM - 1) / kSxsTM) * g0.batch;
+  return form && shape && (tiles >= L.num_cu / 4 || g0.K <= sxs_kc<T>() * 4 / int(sizeof(T)));
+}
+
 template <typename T>
 hipError_t launch_gemm_pair_sum(const Launch &L, const GemmArgs<T> &g0, const GemmArgs<T> &g1, T *out) {
   if (g0.M <= 0 || g0.N <= 0 || g0.batch <= 0) return hipSuccess;
+  if (use_sxs_fused(L, g0, g1)) {
+    GemmArgs<T> a = g0;
+    a.C = out;
+    const dim3 grid((g0.N + kSxsTN - 1) / kSxsTN, (g0.M + kSxsTM - 1) / kSxsTM, g0.batch);
+    if (wide_vec_a(g0) && wide_vec_a(g1))
+      hipLaunchKernelGGL((k_sxs_fused<T, true>), grid, dim3(kSxsThreads), 0, L.stream, a, g1);
+    else
+      hipLaunchKernelGGL((k_sxs_fused<T, false>), grid, dim3(kSxsThreads), 0, L.stream, a, g1);
+    return hipGetLastError();
+  }
   const bool same = g0.M == g1.M && g0.N == g1.N && g0.K == g1.K && g0.batch == g1.batch &&
                     g0.sC == size_t(g0.M) * g0.N && g1.sC == g0.sC;
   if (same && use_wide(L, g0) && use_wide(L, g1)) {
