@@ -20,6 +20,11 @@ sys.path.insert(0, os.path.join(ROOT, "idash26-track3_amd"))
 
 METRIC = "online secure samples/s (bw=32, B=64, 1 GPU); DCF evals/s; % roofline"
 
+
+def affinity_metric(bw, B):
+    """The headline metric's name for a ring width and batch (METRIC itself at bw=32, B=64)."""
+    return f"online secure samples/s (bw={bw}, B={B}, 1 GPU); DCF evals/s; % roofline"
+
 # Peak integer VALU rate of MI355X: 256 CUs x 4 SIMD x 16 lanes x 2.4 GHz.
 VALU_PEAK_TOPS = 256 * 64 * 2.4e9 / 1e12
 HBM_PEAK_GBS = 8000.0
@@ -209,7 +214,7 @@ def main():
         f"{dcf_evals_per_s / 1e9:.3f} G evals/s, {aes_per_s / 1e9:.2f} G AES/s")
 
     result = {
-        "metric": METRIC,
+        "metric": affinity_metric(args.bw, B),
         "value": round(value, 2),
         "unit": "samples/s",
         "n_gpus": 1,
