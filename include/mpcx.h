@@ -72,6 +72,13 @@ typedef struct mpcx_model mpcx_model;
  * Replaces the evaluator/dealer constructors DDGOrcaBase(party, ip, bw, scale)
  * and DDGOrcaBaseKeygen(party, bw, scale, keyFile)
  * (gpu_mpc/ddg_orca_base.h:93-116, 338-355): one context serves both parties. */
+/* Environment read by mpcx_create: MPCX_AES_VARIANT and MPCX_AES_BLOCK (as
+ * mpcx_set_aes_variant; bad values are ignored with a warning); MPCX_GEMM = auto
+ * (default: the fused SxS and wide-K matrix-core kernels where they apply, the
+ * tiled matrix-core kernels elsewhere), tiled (the tiled matrix-core kernels
+ * only) or valu (the VALU kernels); MPCX_GRAPH = 0 (model forwards enqueue every
+ * kernel instead of replaying a captured HIP graph).  All paths give the same
+ * results bit for bit. */
 mpcx_status mpcx_create(int bw, int scale, int device, mpcx_ctx **out);
 void mpcx_destroy(mpcx_ctx *ctx);
 const char *mpcx_last_error(const mpcx_ctx *ctx);
