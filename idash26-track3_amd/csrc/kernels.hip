@@ -1732,6 +1732,8 @@ __device__ __forceinline__ uint4 wide_col_group(const T *p, int col, int ld, int
 template <typename T, int KW, bool VA, bool FUSED>
 __global__ __launch_bounds__(kWideThreads) void k_gemm_wide(GemmArgs<T> g0, GemmArgs<T> g1) {
   constexpr int LDK = KW + 4, WPG = 16 / int(sizeof(T)), NQ = int(sizeof(T));
+  // plain and masked steps (KW, KW / 2 words) are whole 16-word MFMA chunks
+  static_assert(KW % 32 == 0, "step widths a whole number of MFMA chunks");
   // 16-byte groups per thread and operand panel: NJ in a plain step, NJM in a
   // masked one (then slots NJM.. hold the masks' groups)
   constexpr int NJ = (KW / 4 + 7) / 8, NJM = (KW / 8 + 7) / 8, NS = NJ > 2 * NJM ? NJ : 2 * NJM;
@@ -1931,8 +1933,12 @@ __device__ __forceinline__ T digit_fold(const v4i_t (&acc)[sizeof(T)], int r) {
 // The 48-row tiles cover 140 rows as 48 + 48 + 44.
 // ---------------------------------------------------------------------------
 constexpr int kSxsTM = 48, kSxsTN = 32, kSxsThreads = 384;
-// 32-bit words of K per phase: the Z_2^64 kernel's staging registers (and
-// wider accumulator sets) leave room for two thirds of the Z_2^32 width
+// 32-bit words of K per phase, a multiple of 16 (the MFMA chunk): 144 in
+// Z_2^32 (142 KB of LDS, one workgroup per CU, the affinity model's products in
+// one phase), 96 in Z_2^64 (its staging registers and eight-shift accumulators
+// leave room for two thirds of the width; three phases).  Measured alternative:
+// 80-word phases in Z_2^32 (two workgroups per CU, 168 VGPRs) were slower,
+// 17.7 / 26.6 / 38.5 against 11.8 / 23.5 / 35.7 us for N = 78 / 156 / 312.
 template <typename T>
 constexpr int sxs_kc() {
   return sizeof(T) == 4 ? 144 : 96;
@@ -1942,8 +1948,12 @@ template <typename T, bool VA>
 __global__ __launch_bounds__(kSxsThreads) void k_sxs_fused(GemmArgs<T> g0, GemmArgs<T> g1) {
   constexpr int KC = sxs_kc<T>(), WPG = 16 / int(sizeof(T)), NQ = int(sizeof(T)), LDK = KC + 4, GR = KC / 4;
   constexpr int KT = KC * 4 / int(sizeof(T));  // words of T per phase
-  constexpr int NA = (kSxsTM * GR + kSxsThreads - 1) / kSxsThreads, NB = kSxsTN * GR / kSxsThreads;
-  static_assert(kSxsTN * GR % kSxsThreads == 0, "B groups split evenly");
+  constexpr int NA = (kSxsTM * GR + kSxsThreads - 1) / kSxsThreads;
+  constexpr int NB = (kSxsTN * GR + kSxsThreads - 1) / kSxsThreads;
+  // the MFMA loop reads whole 16-word chunks of a row: KC a multiple of 16 keeps
+  // them inside the staged words (zeros past the phase's K); rows of KC + 4
+  // words put 16-byte reads of consecutive rows in distinct bank groups
+  static_assert(KC % 16 == 0, "phase width a whole number of MFMA chunks");
   __shared__ __align__(16) uint32_t As[3 * kSxsTM * LDK];  // digits of A^ - RA0, A^, RA1
   __shared__ __align__(16) uint32_t Bt[3 * kSxsTN * LDK];  // digits of B^ - RB0, RB1, B^ (as [n][k])
   const int bz = int(blockIdx.z), m0 = int(blockIdx.y) * kSxsTM, n0 = int(blockIdx.x) * kSxsTN;
@@ -1980,7 +1990,7 @@ __global__ __launch_bounds__(kSxsThreads) void k_sxs_fused(GemmArgs<T> g0, GemmA
 #pragma unroll
     for (int j = 0; j < NB; j++) {
       const int f = tid + kSxsThreads * j, n = f % kSxsTN, gi = f / kSxsTN;
-      const bool in = n0 + n < N;
+      const bool in = f < kSxsTN * GR && n0 + n < N;
       xb[j] = wide_col_group<T>(Bh, n0 + n, N, kb, gi * WPG, klen, in);
       xb0[j] = wide_col_group<T>(RB0, n0 + n, N, kb, gi * WPG, klen, in);
       xb1[j] = wide_col_group<T>(RB1, n0 + n, N, kb, gi * WPG, klen, in);
@@ -2002,10 +2012,12 @@ __global__ __launch_bounds__(kSxsThreads) void k_sxs_fused(GemmArgs<T> g0, GemmA
 #pragma unroll
     for (int j = 0; j < NB; j++) {
       const int f = tid + kSxsThreads * j, n = f % kSxsTN, gi = f / kSxsTN;
-      uint32_t *p = &Bt[n * LDK + 4 * gi];
-      *reinterpret_cast<uint4 *>(p) = wide_digits<T>(xb[j], xb0[j]);
-      *reinterpret_cast<uint4 *>(p + kSxsTN * LDK) = wide_digits<T>(xb1[j], z);
-      *reinterpret_cast<uint4 *>(p + 2 * kSxsTN * LDK) = wide_digits<T>(xb[j], z);
+      if (f < kSxsTN * GR) {
+        uint32_t *p = &Bt[n * LDK + 4 * gi];
+        *reinterpret_cast<uint4 *>(p) = wide_digits<T>(xb[j], xb0[j]);
+        *reinterpret_cast<uint4 *>(p + kSxsTN * LDK) = wide_digits<T>(xb1[j], z);
+        *reinterpret_cast<uint4 *>(p + 2 * kSxsTN * LDK) = wide_digits<T>(xb[j], z);
+      }
     }
   };
   // one accumulator set, folded into ring words after each party's MFMAs of a
