@@ -176,8 +176,8 @@ hipError_t launch_gemm(const Launch &L, const GemmArgs<T> &g);
 template <typename T>
 hipError_t launch_gemm_pair(const Launch &L, const GemmArgs<T> &g0, const GemmArgs<T> &g1);
 // Both parties' products of an SxS gate, reconstructed: out = C0 + C1 (batch x
-// M x N, contiguous).  One launch where the wide-K kernel applies; otherwise
-// launch_gemm_pair into g0.C and g1.C, then the sum.
+// M x N, contiguous).  One launch (k_sxs_fused) for the pair as the SxS gates
+// form it; otherwise launch_gemm_pair into g0.C and g1.C, then the sum.
 template <typename T>
 hipError_t launch_gemm_pair_sum(const Launch &L, const GemmArgs<T> &g0, const GemmArgs<T> &g1, T *out);
 

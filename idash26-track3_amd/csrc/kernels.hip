@@ -1623,6 +1623,37 @@ __global__ __launch_bounds__(256) void k_gemm_mfma64(GemmArgs<uint64_t> g0, Gemm
   gemm_mfma64_tile(second ? g1 : g0, second ? z - nz0 : z, As, Bt);
 }
 
+// MFMA row operands of one 16-byte LDS read (16 Z_2^32 or 8 Z_2^64 words of a
+// row, balanced digits): shift s takes digit s - j of each word at byte j
+template <typename T>
+__device__ __forceinline__ void digit_shifts(uint4 a, v4i_t (&as)[sizeof(T)]) {
+  if constexpr (sizeof(T) == 4) {
+    constexpr uint32_t sel[4] = {0x0c0c0c00u, 0x0c0c0001u, 0x0c000102u, 0x00010203u};
+#pragma unroll
+    for (int q = 0; q < 4; q++)
+      as[q] = v4i_t{int(__builtin_amdgcn_perm(0u, a.x, sel[q])), int(__builtin_amdgcn_perm(0u, a.y, sel[q])),
+                    int(__builtin_amdgcn_perm(0u, a.z, sel[q])), int(__builtin_amdgcn_perm(0u, a.w, sel[q]))};
+  } else {
+#pragma unroll
+    for (int q = 0; q < 8; q++) {
+      const uint32_t lo = digit_sel(q, 0), hi = digit_sel(q, 4);
+      as[q] = v4i_t{int(__builtin_amdgcn_perm(a.y, a.x, lo)), int(__builtin_amdgcn_perm(a.y, a.x, hi)),
+                    int(__builtin_amdgcn_perm(a.w, a.z, lo)), int(__builtin_amdgcn_perm(a.w, a.z, hi))};
+    }
+  }
+}
+// the ring word of accumulator register r (shift sums acc[q][r])
+template <typename T>
+__device__ __forceinline__ T digit_fold(const v4i_t (&acc)[sizeof(T)], int r) {
+  T v = 0;
+#pragma unroll
+  for (int q = 0; q < int(sizeof(T)); q++) {
+    if constexpr (sizeof(T) == 4) v += uint32_t(acc[q][r]) << (8 * q);
+    else v += uint64_t(int64_t(acc[q][r])) << (8 * q);
+  }
+  return v;
+}
+
 // ---------------------------------------------------------------------------
 // Wide-K ring GEMM on the int8 matrix cores (both rings, the digit algebra of
 // the two kernels above).  Those walk K in 64-word (Z_2^32) or 32-word (Z_2^64)
@@ -1637,13 +1668,7 @@ __global__ __launch_bounds__(256) void k_gemm_mfma64(GemmArgs<uint64_t> g0, Gemm
 // lanes of consecutive rows fall in distinct bank groups).  Wave w computes
 // rows 16 (w & 3) .. + 15 and columns 32 (w >> 2) .. + 31 of the 64 x 64 tile
 // (two 16 x 16 MFMA tiles).  One step covers one segment only; a problem's
-// steps run first segment first.
-//
-// FUSED (both parties of an SxS gate on one GPU): the block evaluates party
-// 0's problem g0 and then party 1's problem g1 on the same tile and writes
-// C0 + C1, the reconstruction of the masked product, to g0.C -- what
-// launch_gemm_pair followed by a reconstruction returns, without writing the
-// shares.  Otherwise g1 is unused and g0.C = g0.Cin + g0.sign * (products).
+// steps run first segment first.  C = Cin + sign * (products).
 // ---------------------------------------------------------------------------
 constexpr int kWideK = 288;        // 32-bit words of K per step (LDS: 2 * 64 * 292 * 4 = 149.5 KB)
 constexpr int kWideThreads = 512;  // 8 waves
@@ -1729,8 +1754,8 @@ __device__ __forceinline__ uint4 wide_col_group(const T *p, int col, int ld, int
   return wide_pack<T>(x);
 }
 
-template <typename T, int KW, bool VA, bool FUSED>
-__global__ __launch_bounds__(kWideThreads) void k_gemm_wide(GemmArgs<T> g0, GemmArgs<T> g1) {
+template <typename T, int KW, bool VA>
+__global__ __launch_bounds__(kWideThreads) void k_gemm_wide(GemmArgs<T> g) {
   constexpr int LDK = KW + 4, WPG = 16 / int(sizeof(T)), NQ = int(sizeof(T));
   // plain and masked steps (KW, KW / 2 words) are whole 16-word MFMA chunks
   static_assert(KW % 32 == 0, "step widths a whole number of MFMA chunks");
@@ -1742,7 +1767,7 @@ __global__ __launch_bounds__(kWideThreads) void k_gemm_wide(GemmArgs<T> g0, Gemm
   const int bz = int(blockIdx.z), m0 = int(blockIdx.y) * 64, n0 = int(blockIdx.x) * 64;
   const int tid = int(threadIdx.x), lane = tid & 63, wave = tid >> 6;
   const int li = lane & 15, lg = lane >> 4, rg = wave & 3, cg = wave >> 2;
-  const int M = g0.M, N = g0.N, K = g0.K;  // FUSED: both problems have the shape of g0
+  const int M = g.M, N = g.N, K = g.K;
   // staging: A group j of thread tid is row tid >> 3, 16-byte group (tid & 7) + 8j
   // of the step; B group j is column tid & 63, k words WPG ((tid >> 6) + 8j) + e
   const int arow = tid >> 3, bn = tid & 63, ag = tid & 7, bg = tid >> 6;
@@ -1805,57 +1830,20 @@ __global__ __launch_bounds__(kWideThreads) void k_gemm_wide(GemmArgs<T> g0, Gemm
   for (int t = 0; t < 2; t++)
 #pragma unroll
     for (int q = 0; q < NQ; q++) acc[t][q] = v4i_t{0, 0, 0, 0};
-  T vs[2][4];
-#pragma unroll
-  for (int t = 0; t < 2; t++)
-#pragma unroll
-    for (int r = 0; r < 4; r++) vs[t][r] = 0;
-  // adds sign * (this problem's products) to vs and clears the accumulators
-  auto fold = [&](int sign) {
-#pragma unroll
-    for (int t = 0; t < 2; t++)
-#pragma unroll
-      for (int r = 0; r < 4; r++) {
-        T v = 0;
-#pragma unroll
-        for (int q = 0; q < NQ; q++) {
-          if constexpr (sizeof(T) == 4) v += uint32_t(acc[t][q][r]) << (8 * q);
-          else v += uint64_t(int64_t(acc[t][q][r])) << (8 * q);
-        }
-        vs[t][r] += sign < 0 ? T(0) - v : v;
-#pragma unroll
-        for (int q = 0; q < NQ; q++) acc[t][q][r] = 0;
-      }
-  };
-  const int n0steps = wide_steps<T, KW>(g0), nsteps = n0steps + (FUSED ? wide_steps<T, KW>(g1) : 0);
-  auto step_of = [&](int i) { return i < n0steps ? wide_step<T, KW>(g0, bz, i) : wide_step<T, KW>(g1, bz, i - n0steps); };
-  WideStep<T> cur = step_of(0);
+  const int nsteps = wide_steps<T, KW>(g);
+  WideStep<T> cur = wide_step<T, KW>(g, bz, 0);
   load(cur);
   for (int i = 0; i < nsteps; i++) {
     store();
     __syncthreads();
     const int nkc = (cur.klen * int(sizeof(T) / 4) + 15) / 16;
     if (i + 1 < nsteps) {
-      cur = step_of(i + 1);
+      cur = wide_step<T, KW>(g, bz, i + 1);
       load(cur);
     }
     for (int kc = 0; kc < nkc; kc++) {
-      const uint4 a = *reinterpret_cast<const uint4 *>(&As[(16 * rg + li) * LDK + 16 * kc + 4 * lg]);
       v4i_t as[NQ];
-      if constexpr (sizeof(T) == 4) {
-        constexpr uint32_t sel[4] = {0x0c0c0c00u, 0x0c0c0001u, 0x0c000102u, 0x00010203u};
-#pragma unroll
-        for (int q = 0; q < 4; q++)
-          as[q] = v4i_t{int(__builtin_amdgcn_perm(0u, a.x, sel[q])), int(__builtin_amdgcn_perm(0u, a.y, sel[q])),
-                        int(__builtin_amdgcn_perm(0u, a.z, sel[q])), int(__builtin_amdgcn_perm(0u, a.w, sel[q]))};
-      } else {
-#pragma unroll
-        for (int q = 0; q < 8; q++) {
-          const uint32_t lo = digit_sel(q, 0), hi = digit_sel(q, 4);
-          as[q] = v4i_t{int(__builtin_amdgcn_perm(a.y, a.x, lo)), int(__builtin_amdgcn_perm(a.y, a.x, hi)),
-                        int(__builtin_amdgcn_perm(a.w, a.z, lo)), int(__builtin_amdgcn_perm(a.w, a.z, hi))};
-        }
-      }
+      digit_shifts<T>(*reinterpret_cast<const uint4 *>(&As[(16 * rg + li) * LDK + 16 * kc + 4 * lg]), as);
 #pragma unroll
       for (int t = 0; t < 2; t++) {
         const uint4 b = *reinterpret_cast<const uint4 *>(&Bt[(32 * cg + 16 * t + li) * LDK + 16 * kc + 4 * lg]);
@@ -1864,13 +1852,10 @@ __global__ __launch_bounds__(kWideThreads) void k_gemm_wide(GemmArgs<T> g0, Gemm
         for (int q = 0; q < NQ; q++) acc[t][q] = __builtin_amdgcn_mfma_i32_16x16x64_i8(as[q], bv, acc[t][q], 0, 0, 0);
       }
     }
-    if (i + 1 == n0steps) fold(g0.sign);
-    else if (i + 1 == nsteps) fold(g1.sign);
     __syncthreads();
   }
-  T *C = g0.C + size_t(bz) * g0.sC;
-  const T *Cin0 = g0.Cin ? g0.Cin + size_t(bz) * g0.sC : nullptr;
-  const T *Cin1 = FUSED && g1.Cin ? g1.Cin + size_t(bz) * g1.sC : nullptr;
+  T *C = g.C + size_t(bz) * g.sC;
+  const T *Cin = g.Cin ? g.Cin + size_t(bz) * g.sC : nullptr;
 #pragma unroll
   for (int t = 0; t < 2; t++) {
     const int gn = n0 + 32 * cg + 16 * t + li;
@@ -1880,43 +1865,10 @@ __global__ __launch_bounds__(kWideThreads) void k_gemm_wide(GemmArgs<T> g0, Gemm
       const int gm = m0 + 16 * rg + 4 * lg + r;
       if (gm >= M || gn >= N) continue;
       const size_t idx = size_t(gm) * N + gn;
-      T v = vs[t][r];
-      if (Cin0) v += Cin0[idx];
-      if (Cin1) v += Cin1[idx];
-      C[idx] = v;
+      const T v = digit_fold<T>(acc[t], r);
+      C[idx] = (Cin ? Cin[idx] : T(0)) + (g.sign < 0 ? T(0) - v : v);
     }
   }
-}
-
-// MFMA row operands of one 16-byte LDS read (16 Z_2^32 or 8 Z_2^64 words of a
-// row, balanced digits): shift s takes digit s - j of each word at byte j
-template <typename T>
-__device__ __forceinline__ void digit_shifts(uint4 a, v4i_t (&as)[sizeof(T)]) {
-  if constexpr (sizeof(T) == 4) {
-    constexpr uint32_t sel[4] = {0x0c0c0c00u, 0x0c0c0001u, 0x0c000102u, 0x00010203u};
-#pragma unroll
-    for (int q = 0; q < 4; q++)
-      as[q] = v4i_t{int(__builtin_amdgcn_perm(0u, a.x, sel[q])), int(__builtin_amdgcn_perm(0u, a.y, sel[q])),
-                    int(__builtin_amdgcn_perm(0u, a.z, sel[q])), int(__builtin_amdgcn_perm(0u, a.w, sel[q]))};
-  } else {
-#pragma unroll
-    for (int q = 0; q < 8; q++) {
-      const uint32_t lo = digit_sel(q, 0), hi = digit_sel(q, 4);
-      as[q] = v4i_t{int(__builtin_amdgcn_perm(a.y, a.x, lo)), int(__builtin_amdgcn_perm(a.y, a.x, hi)),
-                    int(__builtin_amdgcn_perm(a.w, a.z, lo)), int(__builtin_amdgcn_perm(a.w, a.z, hi))};
-    }
-  }
-}
-// the ring word of accumulator register r (shift sums acc[q][r])
-template <typename T>
-__device__ __forceinline__ T digit_fold(const v4i_t (&acc)[sizeof(T)], int r) {
-  T v = 0;
-#pragma unroll
-  for (int q = 0; q < int(sizeof(T)); q++) {
-    if constexpr (sizeof(T) == 4) v += uint32_t(acc[q][r]) << (8 * q);
-    else v += uint64_t(int64_t(acc[q][r])) << (8 * q);
-  }
-  return v;
 }
 
 // ---------------------------------------------------------------------------
@@ -2160,20 +2112,20 @@ static bool wide_vec_a(const GemmArgs<T> &g) {
   return g.K % wpg == 0 && (g.batch == 1 || g.sA % wpg == 0) && aligned16(g.A1) && aligned16(g.A2) &&
          aligned16(g.A1b);
 }
-template <typename T, bool FUSED>
-static hipError_t launch_wide(const Launch &L, const GemmArgs<T> &g0, const GemmArgs<T> &g1) {
-  const dim3 grid((g0.N + 63) / 64, (g0.M + 63) / 64, g0.batch);
-  if (wide_vec_a(g0) && (!FUSED || wide_vec_a(g1)))
-    hipLaunchKernelGGL((k_gemm_wide<T, kWideK, true, FUSED>), grid, dim3(kWideThreads), 0, L.stream, g0, g1);
+template <typename T>
+static hipError_t launch_wide(const Launch &L, const GemmArgs<T> &g) {
+  const dim3 grid((g.N + 63) / 64, (g.M + 63) / 64, g.batch);
+  if (wide_vec_a(g))
+    hipLaunchKernelGGL((k_gemm_wide<T, kWideK, true>), grid, dim3(kWideThreads), 0, L.stream, g);
   else
-    hipLaunchKernelGGL((k_gemm_wide<T, kWideK, false, FUSED>), grid, dim3(kWideThreads), 0, L.stream, g0, g1);
+    hipLaunchKernelGGL((k_gemm_wide<T, kWideK, false>), grid, dim3(kWideThreads), 0, L.stream, g);
   return hipGetLastError();
 }
 
 template <typename T>
 hipError_t launch_gemm(const Launch &L, const GemmArgs<T> &g0) {
   if (g0.M <= 0 || g0.N <= 0 || g0.batch <= 0) return hipSuccess;
-  if (use_wide(L, g0)) return launch_wide<T, false>(L, g0, g0);
+  if (use_wide(L, g0)) return launch_wide<T>(L, g0);
   const bool mfma = use_mfma(L, g0);
   if (g0.A1b && !mfma) {
     // the VALU kernel takes one K segment: add the second product in a second launch
@@ -2243,13 +2195,6 @@ hipError_t launch_gemm_pair_sum(const Launch &L, const GemmArgs<T> &g0, const Ge
     else
       hipLaunchKernelGGL((k_sxs_fused<T, false>), grid, dim3(kSxsThreads), 0, L.stream, a, g1);
     return hipGetLastError();
-  }
-  const bool same = g0.M == g1.M && g0.N == g1.N && g0.K == g1.K && g0.batch == g1.batch &&
-                    g0.sC == size_t(g0.M) * g0.N && g1.sC == g0.sC;
-  if (same && use_wide(L, g0) && use_wide(L, g1)) {
-    GemmArgs<T> a = g0;
-    a.C = out;
-    return launch_wide<T, true>(L, a, g1);
   }
   hipError_t e = launch_gemm_pair<T>(L, g0, g1);
   if (e != hipSuccess) return e;
