@@ -584,6 +584,17 @@ hipError_t launch_tr_keygen(const Launch &L, const TrLayout &lay, uint64_t seed,
   });
 }
 
+// Workgroup of a gate evaluation: the context's explicit size, else the
+// variant's; a launch of at least 2^22 elements on the default 512-thread
+// variant takes 1024 threads (one T-table per 16 waves).  Measured: 3.28
+// against 3.11 G DCF evals/s on 2^24 ReLUs, while the model's launches (up to
+// 10^6 elements) and the adjacency normalisation's (3.4 * 10^6) lose 6-10% at
+// 1024 and keep 512.
+static int tr_eval_block(const Launch &L, size_t n) {
+  const int b = variant_block(L);
+  return (L.aes_block == 0 && b == 512 && n >= (size_t(1) << 22)) ? 1024 : b;
+}
+
 template <typename T>
 hipError_t launch_tr_eval(const Launch &L, const TrLayout &lay, const uint8_t *k0, const uint8_t *k1, const T *xhat,
                           const T *bias, int bias_ncol, T *out) {
@@ -597,7 +608,7 @@ hipError_t launch_tr_eval(const Launch &L, const TrLayout &lay, const uint8_t *k
   a.out = out;
   return with_variant(L, [&](auto v) {
     constexpr int NT = decltype(v)::nt, REP = decltype(v)::rep;
-    const int block = variant_block(L);
+    const int block = tr_eval_block(L, lay.N);
     // a workgroup holds both parties' threads for block/2 elements
     if (block < 128 || block > 2 * kTrMaxTile || block % 128 != 0) return hipErrorInvalidConfiguration;
     const int grid = grid_for(k_tr_eval<T, NT, REP, 0>, block, 2 * lay.N, L.num_cu);
