@@ -53,7 +53,7 @@ KERNEL_SOURCES = ("csrc/kernels.hip", "csrc/kernels.h", "csrc/dcf_dev.h", "csrc/
 SLACK_DESC = {1: ", GCN products H.W^T truncated with the slack gate",
               2: ", GCN products and aggregations truncated with the slack gate",
               3: ", every layer truncation local (LocalARS, the reference's default truncation; not bit-exact)"}
-VALU_OPS_PER_AES = {"perm64_b512": 402, "perm64_b1024": 402, "t4_rep32_b1024": 462}
+VALU_OPS_PER_AES = {"perm32x2_b512": 318, "perm64_b512": 390, "perm64_b1024": 390, "t4_rep32_b1024": 452}
 
 
 def log(msg):

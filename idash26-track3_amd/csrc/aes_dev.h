@@ -236,7 +236,113 @@ struct AesPerm {
   }
 };
 
-// NT = 0 selects the permute-addressed single table (REP must be 64).
+// T0 and T1 = rotl(T0, 8) in one 64 KiB table, 32 copies each: entry x holds
+// T0[x] at byte address 256*x + 4*j and T1[x] at 256*x + 128 + 4*j, copy j.
+// Lane l reads copy l mod 32, so the two half-waves, which the LDS serves in
+// turn, never have two lanes on one bank.  One v_perm_b32 gives the address of
+// "T0[byte k of c]" (byte 0 = 4 (lane mod 32), byte 1 = byte k of c); T1 is the
+// same address plus the read's immediate offset 128.  A column is then
+// T0[a] ^ T1[b] ^ rotl(T0[c] ^ T1[d] ^ rotl(k, 16), 16): 4 address permutes, one
+// rotation and two three-input XORs (28 VALU per round against 36 with T0 alone).
+struct AesPerm2 {
+  static constexpr int kWords = 256 * 64;
+  static constexpr int kBytes = kWords * 4;
+
+  const char *base;
+  uint32_t lane4;  // (lane * 4) mod 128
+
+  // 16-byte stores: entry x is 8 stores of T0[x], then 8 of T1[x]
+  __device__ static void fill(uint32_t *lds) {
+    uint4 *l4 = reinterpret_cast<uint4 *>(lds);
+    for (int q = threadIdx.x; q < kWords / 4; q += blockDim.x) {
+      const uint32_t t = c_T0.v[q >> 4];
+      const uint32_t v = (q & 8) ? rotl32(t, 8) : t;
+      l4[q] = make_uint4(v, v, v, v);
+    }
+    __syncthreads();
+  }
+
+  __device__ AesPerm2(const uint32_t *lds) : base((const char *)lds) { lane4 = (threadIdx.x & 31u) * 4u; }
+
+  // byte address of entry (byte K of c), copy lane mod 32
+  template <int K>
+  __device__ __forceinline__ uint32_t adr(uint32_t c) const {
+    return __builtin_amdgcn_perm(c, lane4, 0x0c0c0000u | ((4u + K) << 8));
+  }
+  template <int K>
+  __device__ __forceinline__ uint32_t t0(uint32_t c) const {
+    return *(const uint32_t *)(base + adr<K>(c));
+  }
+  template <int K>
+  __device__ __forceinline__ uint32_t t1(uint32_t c) const {
+    return *(const uint32_t *)(base + adr<K>(c) + 128);
+  }
+  // rotl(T0[c] ^ T1[d] ^ rotl(k, 16), 16) = T2[c] ^ T3[d] ^ k; the round key is
+  // uniform, so its rotation is scalar work
+  __device__ __forceinline__ uint32_t col(uint32_t a, uint32_t b, uint32_t c, uint32_t d, uint32_t k) const {
+    const uint32_t h = xor3(t0<2>(c), t1<3>(d), (k << 16) | (k >> 16));
+    return xor3(t0<0>(a), t1<1>(b), __builtin_amdgcn_alignbit(h, h, 16));
+  }
+  // S[byte 0 of a] | S[byte 1 of b] << 8 | S[byte 2 of c] << 16 | S[byte 3 of d] << 24
+  // (S[x] is byte 1 of T0[x])
+  __device__ __forceinline__ uint32_t last(uint32_t a, uint32_t b, uint32_t c, uint32_t d) const {
+    const uint32_t lo = __builtin_amdgcn_perm(t0<1>(b), t0<0>(a), 0x0c0c0501u);
+    const uint32_t hi = __builtin_amdgcn_perm(t0<3>(d), t0<2>(c), 0x0c0c0501u);
+    return (hi << 16) | lo;
+  }
+
+  __device__ __forceinline__ void rounds(uint32_t &c0, uint32_t &c1, uint32_t &c2, uint32_t &c3,
+                                         const AesRK &rk) const {
+#pragma unroll
+    for (int r = 1; r < 10; r++) {
+      const uint32_t n0 = col(c0, c1, c2, c3, rk.w[4 * r + 0]);
+      const uint32_t n1 = col(c1, c2, c3, c0, rk.w[4 * r + 1]);
+      const uint32_t n2 = col(c2, c3, c0, c1, rk.w[4 * r + 2]);
+      const uint32_t n3 = col(c3, c0, c1, c2, rk.w[4 * r + 3]);
+      c0 = n0;
+      c1 = n1;
+      c2 = n2;
+      c3 = n3;
+    }
+  }
+
+  __device__ __forceinline__ uint4 enc(uint4 in, const AesRK &rk) const {
+    uint32_t c0 = in.x ^ rk.w[0], c1 = in.y ^ rk.w[1], c2 = in.z ^ rk.w[2], c3 = in.w ^ rk.w[3];
+    rounds(c0, c1, c2, c3, rk);
+    uint4 o;
+    o.x = last(c0, c1, c2, c3) ^ rk.w[40];
+    o.y = last(c1, c2, c3, c0) ^ rk.w[41];
+    o.z = last(c2, c3, c0, c1) ^ rk.w[42];
+    o.w = last(c3, c0, c1, c2) ^ rk.w[43];
+    return o;
+  }
+
+  // H(s) = AES_k(sigma(s)) ^ sigma(s), sigma(xL||xR) = (xL^xR)||xL, xR = words 0,1
+  __device__ __forceinline__ uint4 hash(uint4 s, const AesRK &rk) const {
+    uint32_t c0 = s.z ^ rk.w[0], c1 = s.w ^ rk.w[1];
+    uint32_t c2 = xor3(s.z, s.x, rk.w[2]), c3 = xor3(s.w, s.y, rk.w[3]);
+    rounds(c0, c1, c2, c3, rk);
+    uint4 o;
+    o.x = xor3(last(c0, c1, c2, c3), rk.w[40], s.z);
+    o.y = xor3(last(c1, c2, c3, c0), rk.w[41], s.w);
+    o.z = xor3(last(c2, c3, c0, c1), rk.w[42], s.z) ^ s.x;
+    o.w = xor3(last(c3, c0, c1, c2), rk.w[43], s.w) ^ s.y;
+    return o;
+  }
+
+  // Dealer PRF block AES_kd(idx_lo, idx_hi, field, gate).
+  __device__ __forceinline__ uint4 prf(const AesRK &kd, uint32_t gate, uint32_t field, uint64_t idx) const {
+    uint4 b;
+    b.x = uint32_t(idx);
+    b.y = uint32_t(idx >> 32);
+    b.z = field;
+    b.w = gate;
+    return enc(b, kd);
+  }
+};
+
+// NT = 0 selects the permute-addressed single table (REP must be 64); NT = 2
+// (REP 32) the interleaved pair.
 template <int NT, int REP>
 struct AesSel {
   using type = AesTab<NT, REP>;
@@ -244,6 +350,11 @@ struct AesSel {
 template <>
 struct AesSel<0, 64> {
   using type = AesPerm;
+};
+// NT = 2, REP = 32: T0 and T1 interleaved in one table (AesPerm2)
+template <>
+struct AesSel<2, 32> {
+  using type = AesPerm2;
 };
 template <int NT, int REP>
 using AesLds = typename AesSel<NT, REP>::type;

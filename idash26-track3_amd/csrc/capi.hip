@@ -9,6 +9,7 @@
 #include <string>
 
 #include "../../include/mpcx.h"
+#include "gemm.h"
 #include "kernels.h"
 #include "model.h"
 #include "mpcx_core.h"

@@ -1,0 +1,1111 @@
+// gemm.hip -- ring GEMMs of the secure-inference online path on the int8 matrix
+// cores of gfx950 (and a VALU fallback), both rings.
+//
+// Reference interface: gpuMatmul / gpuKeygenMatmul behind DDGOrcaBase::matmul
+// (gpu_mpc/ddg_orca_base.h:170-271, 394-469), the per-sample SxS loop of
+// sytorch's _MatMul (layers.h:67-93).  A product C = Cin + sign (A1 - A2)(B1 - B2)
+// (+ A1b B1b) mod 2^bw with optional masks, a second K segment and batches.
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <type_traits>
+
+#include "gemm.h"
+
+namespace mpcx {
+
+template <typename K>
+static int grid_for(K kernel, int block, size_t n, int num_cu) {
+  int occ = 0;
+  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ, kernel, block, 0) != hipSuccess || occ < 1) occ = 1;
+  size_t need = (n + block - 1) / block;
+  size_t cap = size_t(occ) * size_t(num_cu);
+  size_t g = need < cap ? need : cap;
+  return int(g < 1 ? 1 : g);
+}
+// ---------------------------------------------------------------------------
+// ring GEMM: 64x64 tile per 256-thread block, 4x4 outputs per thread,
+// K staged through LDS in slices of 16.  Integer multiply-add on the VALU
+// (v_mul_lo_u32 / v_mad_u64_u32); operand differences are applied on load.
+// Skinny products (the FC layers: M = batch) would leave most CUs idle, so K is
+// split across blocks (gridDim.z = batch * ksplit) and the partial sums are
+// added with atomics into C, which is first set to Cin (or 0): addition mod
+// 2^bw is associative and commutative, so the result does not depend on the
+// order in which the slices land.
+// ---------------------------------------------------------------------------
+template <typename T>
+__global__ __launch_bounds__(256) void k_gemm(GemmArgs<T> g) {
+  constexpr int BM = 64, BN = 64, BK = 16;
+  __shared__ T As[BK][BM + 1];
+  __shared__ T Bs[BK][BN + 1];
+  const int bz = blockIdx.z / g.ksplit, kz = blockIdx.z % g.ksplit;
+  const int kchunk = ((g.K + g.ksplit - 1) / g.ksplit + BK - 1) / BK * BK;
+  const int kbeg = kz * kchunk, kend = min(g.K, kbeg + kchunk);
+  const T *A1 = g.A1 + size_t(bz) * g.sA;
+  const T *A2 = g.A2 ? g.A2 + size_t(bz) * g.sA : nullptr;
+  const T *B1 = g.B1 + size_t(bz) * g.sB;
+  const T *B2 = g.B2 ? g.B2 + size_t(bz) * g.sB : nullptr;
+  const int m0 = blockIdx.y * BM, n0 = blockIdx.x * BN;
+  const int tid = threadIdx.x;
+  const int tr = tid / 16, tc = tid % 16;  // 16 x 16 thread grid, 4 x 4 each
+  T acc[4][4];
+#pragma unroll
+  for (int i = 0; i < 4; i++)
+#pragma unroll
+    for (int j = 0; j < 4; j++) acc[i][j] = 0;
+  for (int k0 = kbeg; k0 < kend; k0 += BK) {
+#pragma unroll
+    for (int r = 0; r < 4; r++) {
+      const int e = tid + r * 256;  // 0..1023
+      // A tile: 64 rows x 16 cols, row-major source
+      const int am = e / BK, ak = e % BK;
+      const int gm = m0 + am, gk = k0 + ak;
+      T av = 0;
+      if (gm < g.M && gk < kend) {
+        const size_t idx = size_t(gm) * g.K + gk;
+        av = A1[idx];
+        if (A2) av -= A2[idx];
+      }
+      As[ak][am] = av;
+      // B tile: 16 rows x 64 cols
+      const int bk = e / BN, bn = e % BN;
+      const int gk2 = k0 + bk, gn = n0 + bn;
+      T bv = 0;
+      if (gk2 < kend && gn < g.N) {
+        const size_t idx = size_t(gk2) * g.N + gn;
+        bv = B1[idx];
+        if (B2) bv -= B2[idx];
+      }
+      Bs[bk][bn] = bv;
+    }
+    __syncthreads();
+#pragma unroll
+    for (int kk = 0; kk < BK; kk++) {
+      T a[4], b[4];
+#pragma unroll
+      for (int i = 0; i < 4; i++) a[i] = As[kk][tr * 4 + i];
+#pragma unroll
+      for (int j = 0; j < 4; j++) b[j] = Bs[kk][tc * 4 + j];
+#pragma unroll
+      for (int i = 0; i < 4; i++)
+#pragma unroll
+        for (int j = 0; j < 4; j++) acc[i][j] += a[i] * b[j];
+    }
+    __syncthreads();
+  }
+  T *C = g.C + size_t(bz) * g.sC;
+  const T *Cin = g.Cin ? g.Cin + size_t(bz) * g.sC : nullptr;
+#pragma unroll
+  for (int i = 0; i < 4; i++) {
+    const int gm = m0 + tr * 4 + i;
+    if (gm >= g.M) continue;
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+      const int gn = n0 + tc * 4 + j;
+      if (gn >= g.N) continue;
+      const size_t idx = size_t(gm) * g.N + gn;
+      const T v = g.sign < 0 ? T(T(0) - acc[i][j]) : acc[i][j];
+      if (g.ksplit > 1) {
+        if constexpr (sizeof(T) == 4)
+          atomicAdd(reinterpret_cast<unsigned int *>(&C[idx]), static_cast<unsigned int>(v));
+        else
+          atomicAdd(reinterpret_cast<unsigned long long *>(&C[idx]), static_cast<unsigned long long>(v));
+      } else {
+        C[idx] = Cin ? T(v + Cin[idx]) : v;
+      }
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// ring GEMM over Z_2^32 on the int8 matrix cores (v_mfma_i32_16x16x64_i8).
+// Balanced base-256 digits: the bytes of y = (a + 0x80808080) ^ 0x80808080,
+// read as signed int8 d_0..d_3 in [-128, 127], satisfy a = sum_p d_p 2^(8p)
+// mod 2^32 (y - 0x80808080 = a, and byte ^ 0x80 read as int8 is byte - 128).
+// Hence a*b mod 2^32 = sum_{s<4} 2^(8s) sum_{p+q=s} a_p b_q.  One MFMA takes 16
+// operand words per row and column (4 digit bytes each); with the row words'
+// digits permuted to (a_s, a_{s-1}, .., a_0, 0, ..) it returns the shift-s sum
+// over those 16 words, so four MFMAs (s = 0..3) cover 16 k.  The int32
+// accumulators wrap, and only acc_s mod 2^(32-8s) enters the result.
+// Tile: 64 x 64 per 256-thread block; wave w owns rows 16w..16w+15 and the four
+// 16-column MFMA tiles; K staged through LDS in slices of 64 words (A as
+// [m][k], B transposed to [n][k], rows padded to 68 words).  Split-K and the
+// epilogue follow k_gemm.
+// ---------------------------------------------------------------------------
+typedef int v4i_t __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ uint32_t ring_digits(uint32_t a) { return (a + 0x80808080u) ^ 0x80808080u; }
+
+// One 64 x 64 output tile of problem g; z = batch * ksplit + K slice.  A second
+// K segment (A1b, B1b) starts at the K tile after the first segment's last one,
+// so every 64-wide K tile reads one segment only.  VA / VB: rows of A / B are
+// read as 16-byte words (K resp. N a multiple of 4, operands 16-byte aligned).
+template <bool VA, bool VB>
+__device__ __forceinline__ void gemm_mfma_tile(const GemmArgs<uint32_t> &g, int z, uint32_t *As, uint32_t *Bt) {
+  constexpr int BM = 64, BN = 64, BK = 64, LD = BK + 4;
+  const int Kp = (g.K + BK - 1) / BK * BK;
+  const int Kt = g.A1b ? Kp + g.K : g.K;
+  const int bz = z / g.ksplit, kz = z % g.ksplit;
+  const int kchunk = ((Kt + g.ksplit - 1) / g.ksplit + BK - 1) / BK * BK;
+  const int kbeg = kz * kchunk, kend = min(Kt, kbeg + kchunk);
+  const uint32_t *A1 = g.A1 + size_t(bz) * g.sA;
+  const uint32_t *A2 = g.A2 ? g.A2 + size_t(bz) * g.sA : nullptr;
+  const uint32_t *B1 = g.B1 + size_t(bz) * g.sB;
+  const uint32_t *B2 = g.B2 ? g.B2 + size_t(bz) * g.sB : nullptr;
+  const uint32_t *A1b = g.A1b ? g.A1b + size_t(bz) * g.sA : nullptr;
+  const uint32_t *B1b = g.B1b ? g.B1b + size_t(bz) * g.sB : nullptr;
+  const int m0 = blockIdx.y * BM, n0 = blockIdx.x * BN;
+  if (m0 >= g.M || n0 >= g.N) return;  // the grid spans the larger of two problems
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int li = lane & 15, lg = lane >> 4;
+  v4i_t acc[4][4];
+#pragma unroll
+  for (int t = 0; t < 4; t++)
+#pragma unroll
+    for (int q = 0; q < 4; q++) acc[t][q] = v4i_t{0, 0, 0, 0};
+  // Each thread stages 16 words of the A tile and 16 of the B tile (B stored
+  // transposed, Bt[n][k]).  Scalar layout: word r at row hb + 4r, column lo;
+  // 16-byte layout: words 4r..4r+3 at row (tid >> 4) + 16r, columns 4 (tid & 15) + 0..3.
+  // The next K tile is loaded into registers (addresses clamped in bounds, the
+  // masking and the A1 - A2 difference applied when stored to LDS) while the
+  // matrix cores work on the current one.
+  uint32_t ra[16], ra2[16], rb[16], rb2[16];
+  const int lo = tid & 63, hb = tid >> 6, vq = tid & 15, vr = tid >> 4;
+  struct Seg {
+    const uint32_t *a1, *a2, *b1, *b2;
+    int kk, klim;
+  };
+  auto seg_of = [&](int k0) {
+    const bool second = k0 >= Kp;  // uniform over the block
+    Seg sg;
+    sg.a1 = second ? A1b : A1;
+    sg.a2 = second ? nullptr : A2;
+    sg.b1 = second ? B1b : B1;
+    sg.b2 = second ? nullptr : B2;
+    sg.kk = second ? k0 - Kp : k0;
+    sg.klim = min(g.K, kend - (second ? Kp : 0));
+    return sg;
+  };
+  // (row, column) of staged word r of A and of B, relative to the tile origin
+  auto a_rc = [&](int r, int &row, int &col) {
+    if constexpr (VA) {
+      row = vr + 16 * (r >> 2);
+      col = 4 * vq + (r & 3);
+    } else {
+      row = hb + 4 * r;
+      col = lo;
+    }
+  };
+  auto b_rc = [&](int r, int &row, int &col) {  // row = k, col = n
+    if constexpr (VB) {
+      row = vr + 16 * (r >> 2);
+      col = 4 * vq + (r & 3);
+    } else {
+      row = hb + 4 * r;
+      col = lo;
+    }
+  };
+  auto load = [&](int k0) {
+    const Seg sg = seg_of(k0);
+#pragma unroll
+    for (int r = 0; r < 16; r += VA ? 4 : 1) {
+      int row, col;
+      a_rc(r, row, col);
+      const int gm = m0 + row, gk = sg.kk + col;
+      const size_t idx = (gm < g.M && gk < sg.klim) ? size_t(gm) * g.K + gk : 0;
+      if constexpr (VA) {
+        const uint4 v = *reinterpret_cast<const uint4 *>(sg.a1 + idx);
+        ra[r] = v.x, ra[r + 1] = v.y, ra[r + 2] = v.z, ra[r + 3] = v.w;
+      } else {
+        ra[r] = sg.a1[idx];
+      }
+    }
+    if (sg.a2) {
+#pragma unroll
+      for (int r = 0; r < 16; r += VA ? 4 : 1) {
+        int row, col;
+        a_rc(r, row, col);
+        const int gm = m0 + row, gk = sg.kk + col;
+        const size_t idx = (gm < g.M && gk < sg.klim) ? size_t(gm) * g.K + gk : 0;
+        if constexpr (VA) {
+          const uint4 v = *reinterpret_cast<const uint4 *>(sg.a2 + idx);
+          ra2[r] = v.x, ra2[r + 1] = v.y, ra2[r + 2] = v.z, ra2[r + 3] = v.w;
+        } else {
+          ra2[r] = sg.a2[idx];
+        }
+      }
+    } else {
+#pragma unroll
+      for (int r = 0; r < 16; r++) ra2[r] = 0;
+    }
+#pragma unroll
+    for (int r = 0; r < 16; r += VB ? 4 : 1) {
+      int row, col;
+      b_rc(r, row, col);
+      const int gk = sg.kk + row, gn = n0 + col;
+      const size_t idx = (gk < sg.klim && gn < g.N) ? size_t(gk) * g.N + gn : 0;
+      if constexpr (VB) {
+        const uint4 v = *reinterpret_cast<const uint4 *>(sg.b1 + idx);
+        rb[r] = v.x, rb[r + 1] = v.y, rb[r + 2] = v.z, rb[r + 3] = v.w;
+      } else {
+        rb[r] = sg.b1[idx];
+      }
+    }
+    if (sg.b2) {
+#pragma unroll
+      for (int r = 0; r < 16; r += VB ? 4 : 1) {
+        int row, col;
+        b_rc(r, row, col);
+        const int gk = sg.kk + row, gn = n0 + col;
+        const size_t idx = (gk < sg.klim && gn < g.N) ? size_t(gk) * g.N + gn : 0;
+        if constexpr (VB) {
+          const uint4 v = *reinterpret_cast<const uint4 *>(sg.b2 + idx);
+          rb2[r] = v.x, rb2[r + 1] = v.y, rb2[r + 2] = v.z, rb2[r + 3] = v.w;
+        } else {
+          rb2[r] = sg.b2[idx];
+        }
+      }
+    } else {
+#pragma unroll
+      for (int r = 0; r < 16; r++) rb2[r] = 0;
+    }
+  };
+  // K columns past klim and rows past M / N are staged as zeros
+  auto store = [&](int k0) {
+    const Seg sg = seg_of(k0);
+#pragma unroll
+    for (int r = 0; r < 16; r++) {
+      int row, col;
+      a_rc(r, row, col);
+      const bool in = m0 + row < g.M && sg.kk + col < sg.klim;
+      As[row * LD + col] = in ? ring_digits(ra[r] - ra2[r]) : 0u;
+    }
+#pragma unroll
+    for (int r = 0; r < 16; r++) {
+      int row, col;
+      b_rc(r, row, col);
+      const bool in = sg.kk + row < sg.klim && n0 + col < g.N;
+      Bt[col * LD + row] = in ? ring_digits(rb[r] - rb2[r]) : 0u;
+    }
+  };
+  if (kbeg < kend) load(kbeg);
+  for (int k0 = kbeg; k0 < kend; k0 += BK) {
+    store(k0);
+    __syncthreads();
+    if (k0 + BK < kend) load(k0 + BK);
+#pragma unroll
+    for (int kc = 0; kc < BK / 16; kc++) {
+      const uint4 a = *reinterpret_cast<const uint4 *>(&As[(wave * 16 + li) * LD + kc * 16 + lg * 4]);
+      v4i_t as[4];
+      // byte p of the shift-s word: digit s-p of the row word (0x0c selects a zero byte)
+      constexpr uint32_t sel[4] = {0x0c0c0c00u, 0x0c0c0001u, 0x0c000102u, 0x00010203u};
+#pragma unroll
+      for (int q = 0; q < 4; q++)
+        as[q] = v4i_t{int(__builtin_amdgcn_perm(0u, a.x, sel[q])), int(__builtin_amdgcn_perm(0u, a.y, sel[q])),
+                      int(__builtin_amdgcn_perm(0u, a.z, sel[q])), int(__builtin_amdgcn_perm(0u, a.w, sel[q]))};
+#pragma unroll
+      for (int t = 0; t < 4; t++) {
+        const uint4 b = *reinterpret_cast<const uint4 *>(&Bt[(t * 16 + li) * LD + kc * 16 + lg * 4]);
+        const v4i_t bv = v4i_t{int(b.x), int(b.y), int(b.z), int(b.w)};
+#pragma unroll
+        for (int q = 0; q < 4; q++) acc[t][q] = __builtin_amdgcn_mfma_i32_16x16x64_i8(as[q], bv, acc[t][q], 0, 0, 0);
+      }
+    }
+    __syncthreads();
+  }
+  uint32_t *C = g.C + size_t(bz) * g.sC;
+  const uint32_t *Cin = g.Cin ? g.Cin + size_t(bz) * g.sC : nullptr;
+#pragma unroll
+  for (int t = 0; t < 4; t++) {
+    const int gn = n0 + t * 16 + li;
+#pragma unroll
+    for (int r = 0; r < 4; r++) {
+      // accumulator register r of lane (li, lg): row 4*lg + r, column li of the tile
+      const int gm = m0 + wave * 16 + lg * 4 + r;
+      if (gm >= g.M || gn >= g.N) continue;
+      uint32_t v = uint32_t(acc[t][0][r]) + (uint32_t(acc[t][1][r]) << 8) + (uint32_t(acc[t][2][r]) << 16) +
+                   (uint32_t(acc[t][3][r]) << 24);
+      if (g.sign < 0) v = 0u - v;
+      const size_t idx = size_t(gm) * g.N + gn;
+      if (g.ksplit > 1)
+        atomicAdd(reinterpret_cast<unsigned int *>(&C[idx]), static_cast<unsigned int>(v));
+      else
+        C[idx] = Cin ? v + Cin[idx] : v;
+    }
+  }
+}
+
+// blockIdx.z < nz0: problem g0, else problem g1 (nz = batch * ksplit of each)
+template <bool VA, bool VB>
+__global__ __launch_bounds__(256) void k_gemm_mfma(GemmArgs<uint32_t> g0, GemmArgs<uint32_t> g1, int nz0) {
+  __shared__ __align__(16) uint32_t As[64 * 68];
+  __shared__ __align__(16) uint32_t Bt[64 * 68];
+  const int z = int(blockIdx.z);
+  const bool second = z >= nz0;
+  gemm_mfma_tile<VA, VB>(second ? g1 : g0, second ? z - nz0 : z, As, Bt);
+}
+
+// ---------------------------------------------------------------------------
+// ring GEMM over Z_2^64 on the int8 matrix cores.  Eight balanced base-256
+// digits per word (the bytes of (a + 0x8080..80) ^ 0x8080..80 read as int8):
+// a*b mod 2^64 = sum_{s<8} 2^(8s) sum_{p+q=s} a_p b_q.  One MFMA takes 8
+// operand words per row and column (8 digit bytes each); with each row word's
+// digits permuted to (a_s, .., a_0, 0, ..) it returns the shift-s sum over those
+// 8 words, so eight MFMAs (s = 0..7) cover 8 k.  acc_s enters bits 8s..63 of the
+// result, so for s < 4 it must be exact in int32: |acc_s| <= K * 4 * 2^14, i.e.
+// K < 2^15 per product (launch_gemm keeps larger K on the VALU kernel).
+// Tile 64 x 64 per 256-thread block as in the Z_2^32 kernel; K slices of 32
+// words (64 u32 of LDS per row, B transposed).
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ uint64_t ring_digits64(uint64_t a) {
+  return (a + 0x8080808080808080ull) ^ 0x8080808080808080ull;
+}
+// v_perm_b32 selector of output bytes j0..j0+3 for shift s: digit s - j (bytes
+// 0..3 of the low source word, 4..7 of the high one), 0x0c (zero) when s < j
+constexpr uint32_t digit_sel(int s, int j0) {
+  uint32_t v = 0;
+  for (int j = 0; j < 4; j++) v |= uint32_t(s - (j0 + j) >= 0 ? s - (j0 + j) : 0x0c) << (8 * j);
+  return v;
+}
+
+__device__ __forceinline__ void gemm_mfma64_tile(const GemmArgs<uint64_t> &g, int z, uint32_t *As, uint32_t *Bt) {
+  constexpr int BM = 64, BN = 64, BK = 32, LD = 2 * BK + 4;  // LD in 32-bit words
+  const int Kp = (g.K + BK - 1) / BK * BK;
+  const int Kt = g.A1b ? Kp + g.K : g.K;
+  const int bz = z / g.ksplit, kz = z % g.ksplit;
+  const int kchunk = ((Kt + g.ksplit - 1) / g.ksplit + BK - 1) / BK * BK;
+  const int kbeg = kz * kchunk, kend = min(Kt, kbeg + kchunk);
+  const uint64_t *A1 = g.A1 + size_t(bz) * g.sA;
+  const uint64_t *A2 = g.A2 ? g.A2 + size_t(bz) * g.sA : nullptr;
+  const uint64_t *B1 = g.B1 + size_t(bz) * g.sB;
+  const uint64_t *B2 = g.B2 ? g.B2 + size_t(bz) * g.sB : nullptr;
+  const uint64_t *A1b = g.A1b ? g.A1b + size_t(bz) * g.sA : nullptr;
+  const uint64_t *B1b = g.B1b ? g.B1b + size_t(bz) * g.sB : nullptr;
+  const int m0 = blockIdx.y * BM, n0 = blockIdx.x * BN;
+  if (m0 >= g.M || n0 >= g.N) return;  // the grid spans the larger of two problems
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int li = lane & 15, lg = lane >> 4;
+  v4i_t acc[4][8];
+#pragma unroll
+  for (int t = 0; t < 4; t++)
+#pragma unroll
+    for (int q = 0; q < 8; q++) acc[t][q] = v4i_t{0, 0, 0, 0};
+  // staged word r (r < 8) of A: row (tid >> 5) + 8r, column tid & 31; of B:
+  // k (tid >> 6) + 4r, column tid & 63 (B stored transposed, Bt[n][k]); rows of
+  // 32 consecutive 8-byte words per 32 threads.  The next K slice is loaded into
+  // registers while the matrix cores work on the current one.
+  uint64_t ra[8], ra2[8], rb[8], rb2[8];
+  const int ar = tid >> 5, ac = tid & 31, bk = tid >> 6, bn = tid & 63;
+  struct Seg {
+    const uint64_t *a1, *a2, *b1, *b2;
+    int kk, klim;
+  };
+  auto seg_of = [&](int k0) {
+    const bool second = k0 >= Kp;  // uniform over the block
+    Seg sg;
+    sg.a1 = second ? A1b : A1;
+    sg.a2 = second ? nullptr : A2;
+    sg.b1 = second ? B1b : B1;
+    sg.b2 = second ? nullptr : B2;
+    sg.kk = second ? k0 - Kp : k0;
+    sg.klim = min(g.K, kend - (second ? Kp : 0));
+    return sg;
+  };
+  auto load = [&](int k0) {
+    const Seg sg = seg_of(k0);
+#pragma unroll
+    for (int r = 0; r < 8; r++) {
+      const int gm = m0 + ar + 8 * r, gk = sg.kk + ac;
+      const size_t idx = (gm < g.M && gk < sg.klim) ? size_t(gm) * g.K + gk : 0;
+      ra[r] = sg.a1[idx];
+      ra2[r] = sg.a2 ? sg.a2[idx] : 0ull;
+    }
+#pragma unroll
+    for (int r = 0; r < 8; r++) {
+      const int gk = sg.kk + bk + 4 * r, gn = n0 + bn;
+      const size_t idx = (gk < sg.klim && gn < g.N) ? size_t(gk) * g.N + gn : 0;
+      rb[r] = sg.b1[idx];
+      rb2[r] = sg.b2 ? sg.b2[idx] : 0ull;
+    }
+  };
+  // K columns past klim and rows past M / N are staged as zeros
+  auto store = [&](int k0) {
+    const Seg sg = seg_of(k0);
+#pragma unroll
+    for (int r = 0; r < 8; r++) {
+      const int row = ar + 8 * r;
+      const bool in = m0 + row < g.M && sg.kk + ac < sg.klim;
+      const uint64_t v = in ? ring_digits64(ra[r] - ra2[r]) : 0ull;
+      *reinterpret_cast<uint2 *>(&As[row * LD + 2 * ac]) = make_uint2(uint32_t(v), uint32_t(v >> 32));
+    }
+#pragma unroll
+    for (int r = 0; r < 8; r++) {
+      const int k = bk + 4 * r;
+      const bool in = sg.kk + k < sg.klim && n0 + bn < g.N;
+      const uint64_t v = in ? ring_digits64(rb[r] - rb2[r]) : 0ull;
+      *reinterpret_cast<uint2 *>(&Bt[bn * LD + 2 * k]) = make_uint2(uint32_t(v), uint32_t(v >> 32));
+    }
+  };
+  if (kbeg < kend) load(kbeg);
+  for (int k0 = kbeg; k0 < kend; k0 += BK) {
+    store(k0);
+    __syncthreads();
+    if (k0 + BK < kend) load(k0 + BK);
+#pragma unroll
+    for (int kc = 0; kc < BK / 8; kc++) {
+      // lane (li, lg): words 2 lg, 2 lg + 1 of the 8-word step, as (lo, hi) pairs
+      const uint4 a = *reinterpret_cast<const uint4 *>(&As[(wave * 16 + li) * LD + kc * 16 + lg * 4]);
+      v4i_t as[8];
+#pragma unroll
+      for (int q = 0; q < 8; q++) {
+        const uint32_t lo = digit_sel(q, 0), hi = digit_sel(q, 4);
+        as[q] = v4i_t{int(__builtin_amdgcn_perm(a.y, a.x, lo)), int(__builtin_amdgcn_perm(a.y, a.x, hi)),
+                      int(__builtin_amdgcn_perm(a.w, a.z, lo)), int(__builtin_amdgcn_perm(a.w, a.z, hi))};
+      }
+#pragma unroll
+      for (int t = 0; t < 4; t++) {
+        const uint4 b = *reinterpret_cast<const uint4 *>(&Bt[(t * 16 + li) * LD + kc * 16 + lg * 4]);
+        const v4i_t bv = v4i_t{int(b.x), int(b.y), int(b.z), int(b.w)};
+#pragma unroll
+        for (int q = 0; q < 8; q++) acc[t][q] = __builtin_amdgcn_mfma_i32_16x16x64_i8(as[q], bv, acc[t][q], 0, 0, 0);
+      }
+    }
+    __syncthreads();
+  }
+  uint64_t *C = g.C + size_t(bz) * g.sC;
+  const uint64_t *Cin = g.Cin ? g.Cin + size_t(bz) * g.sC : nullptr;
+#pragma unroll
+  for (int t = 0; t < 4; t++) {
+    const int gn = n0 + t * 16 + li;
+#pragma unroll
+    for (int r = 0; r < 4; r++) {
+      // accumulator register r of lane (li, lg): row 4*lg + r, column li of the tile
+      const int gm = m0 + wave * 16 + lg * 4 + r;
+      if (gm >= g.M || gn >= g.N) continue;
+      uint64_t v = 0;
+#pragma unroll
+      for (int q = 0; q < 8; q++) v += uint64_t(int64_t(acc[t][q][r])) << (8 * q);
+      if (g.sign < 0) v = 0ull - v;
+      const size_t idx = size_t(gm) * g.N + gn;
+      if (g.ksplit > 1)
+        atomicAdd(reinterpret_cast<unsigned long long *>(&C[idx]), static_cast<unsigned long long>(v));
+      else
+        C[idx] = Cin ? v + Cin[idx] : v;
+    }
+  }
+}
+
+// blockIdx.z < nz0: problem g0, else problem g1 (nz = batch * ksplit of each)
+__global__ __launch_bounds__(256) void k_gemm_mfma64(GemmArgs<uint64_t> g0, GemmArgs<uint64_t> g1, int nz0) {
+  __shared__ __align__(16) uint32_t As[64 * 68];
+  __shared__ __align__(16) uint32_t Bt[64 * 68];
+  const int z = int(blockIdx.z);
+  const bool second = z >= nz0;
+  gemm_mfma64_tile(second ? g1 : g0, second ? z - nz0 : z, As, Bt);
+}
+
+// MFMA row operands of one 16-byte LDS read (16 Z_2^32 or 8 Z_2^64 words of a
+// row, balanced digits): shift s takes digit s - j of each word at byte j
+template <typename T>
+__device__ __forceinline__ void digit_shifts(uint4 a, v4i_t (&as)[sizeof(T)]) {
+  if constexpr (sizeof(T) == 4) {
+    constexpr uint32_t sel[4] = {0x0c0c0c00u, 0x0c0c0001u, 0x0c000102u, 0x00010203u};
+#pragma unroll
+    for (int q = 0; q < 4; q++)
+      as[q] = v4i_t{int(__builtin_amdgcn_perm(0u, a.x, sel[q])), int(__builtin_amdgcn_perm(0u, a.y, sel[q])),
+                    int(__builtin_amdgcn_perm(0u, a.z, sel[q])), int(__builtin_amdgcn_perm(0u, a.w, sel[q]))};
+  } else {
+#pragma unroll
+    for (int q = 0; q < 8; q++) {
+      const uint32_t lo = digit_sel(q, 0), hi = digit_sel(q, 4);
+      as[q] = v4i_t{int(__builtin_amdgcn_perm(a.y, a.x, lo)), int(__builtin_amdgcn_perm(a.y, a.x, hi)),
+                    int(__builtin_amdgcn_perm(a.w, a.z, lo)), int(__builtin_amdgcn_perm(a.w, a.z, hi))};
+    }
+  }
+}
+// the ring word of accumulator register r (shift sums acc[q][r])
+template <typename T>
+__device__ __forceinline__ T digit_fold(const v4i_t (&acc)[sizeof(T)], int r) {
+  T v = 0;
+#pragma unroll
+  for (int q = 0; q < int(sizeof(T)); q++) {
+    if constexpr (sizeof(T) == 4) v += uint32_t(acc[q][r]) << (8 * q);
+    else v += uint64_t(int64_t(acc[q][r])) << (8 * q);
+  }
+  return v;
+}
+
+// Workgroup p of a one-dimensional launch of W runs on XCD p mod 8 (the
+// dispatcher deals workgroups to the eight XCDs in turn); renumbering so that
+// each XCD takes a contiguous range of W / 8 logical workgroups keeps a batch
+// entry's tiles, which share their operands, in one XCD's L2.
+constexpr int kXcds = 8;
+__device__ __forceinline__ int xcd_swizzle(int p, int W) {
+  const int xcd = p % kXcds, q = p / kXcds, base = W / kXcds, rem = W % kXcds;
+  return (xcd < rem ? xcd * (base + 1) : rem * (base + 1) + (xcd - rem) * base) + q;
+}
+// ---------------------------------------------------------------------------
+// Wide-K ring GEMM on the int8 matrix cores (both rings, the digit algebra of
+// the two kernels above).  Those walk K in 64-word (Z_2^32) or 32-word (Z_2^64)
+// steps and wait for a round trip to memory at every step, with about one
+// 4-wave block per CU on this path's shapes (K = 78..312 words per segment,
+// 140 x 140 per-graph blocks), so a tile costs a few memory latencies.  Here a
+// 512-thread block stages KW 32-bit words of K per step (kWideK words of
+// Z_2^32, half as many of Z_2^64): every load of a step is in flight at once,
+// and the next step's loads are issued before the current step's MFMAs, so a
+// segment of at most KW words costs one round trip.  LDS as above: A as [m][k],
+// B transposed to [n][k], rows of KW + 4 words (16-byte reads by 8 consecutive
+// lanes of consecutive rows fall in distinct bank groups).  Wave w computes
+// rows 16 (w & 3) .. + 15 and columns 32 (w >> 2) .. + 31 of the 64 x 64 tile
+// (two 16 x 16 MFMA tiles).  One step covers one segment only; a problem's
+// steps run first segment first.  C = Cin + sign * (products).
+// ---------------------------------------------------------------------------
+constexpr int kWideK = 288;        // 32-bit words of K per step (LDS: 2 * 64 * 292 * 4 = 149.5 KB)
+constexpr int kWideThreads = 512;  // 8 waves
+
+template <typename T>
+struct WideStep {
+  const T *a, *a2, *b, *b2;  // segment operands of batch entry bz (a2, b2: masks or null)
+  int kb, klen;              // K range [kb, kb + klen) of the segment
+};
+// K words of a step: a segment with masks stages four operands, so its steps
+// are half as wide (the staging registers hold two operand panels of KW words)
+template <typename T, int KW>
+__device__ __forceinline__ int wide_kt(bool masked) {
+  return (masked ? KW / 2 : KW) * 4 / int(sizeof(T));
+}
+template <typename T, int KW>
+__device__ __forceinline__ int wide_steps(const GemmArgs<T> &g) {
+  const int k0 = wide_kt<T, KW>(g.A2 || g.B2), k1 = wide_kt<T, KW>(false);
+  return (g.K + k0 - 1) / k0 + (g.A1b ? (g.K + k1 - 1) / k1 : 0);
+}
+template <typename T, int KW>
+__device__ __forceinline__ WideStep<T> wide_step(const GemmArgs<T> &g, int bz, int i) {
+  const bool masked = g.A2 || g.B2;
+  const int k0 = wide_kt<T, KW>(masked), n0 = (g.K + k0 - 1) / k0;
+  const bool seg = i >= n0;
+  const int kt = seg ? wide_kt<T, KW>(false) : k0;
+  WideStep<T> w;
+  w.kb = (seg ? i - n0 : i) * kt;
+  w.klen = min(kt, g.K - w.kb);
+  w.a = (seg ? g.A1b : g.A1) + size_t(bz) * g.sA;
+  w.b = (seg ? g.B1b : g.B1) + size_t(bz) * g.sB;
+  w.a2 = (!seg && g.A2) ? g.A2 + size_t(bz) * g.sA : nullptr;
+  w.b2 = (!seg && g.B2) ? g.B2 + size_t(bz) * g.sB : nullptr;
+  return w;
+}
+// balanced digits of a 16-byte group (four Z_2^32 words or two Z_2^64 words) of x - y
+template <typename T>
+__device__ __forceinline__ uint4 wide_digits(uint4 x, uint4 y) {
+  if constexpr (sizeof(T) == 4) {
+    return make_uint4(ring_digits(x.x - y.x), ring_digits(x.y - y.y), ring_digits(x.z - y.z), ring_digits(x.w - y.w));
+  } else {
+    const uint64_t lo = ring_digits64(((uint64_t(x.y) << 32) | x.x) - ((uint64_t(y.y) << 32) | y.x));
+    const uint64_t hi = ring_digits64(((uint64_t(x.w) << 32) | x.z) - ((uint64_t(y.w) << 32) | y.z));
+    return make_uint4(uint32_t(lo), uint32_t(lo >> 32), uint32_t(hi), uint32_t(hi >> 32));
+  }
+}
+template <typename T>
+__device__ __forceinline__ uint4 wide_pack(const T (&v)[16 / sizeof(T)]) {
+  if constexpr (sizeof(T) == 4) return make_uint4(v[0], v[1], v[2], v[3]);
+  else return make_uint4(uint32_t(v[0]), uint32_t(v[0] >> 32), uint32_t(v[1]), uint32_t(v[1] >> 32));
+}
+// 16-byte group kv .. kv + WPG - 1 of row `row` of a row-major matrix with
+// `ld` words per row, zero where out of [0, klen) (in = the row exists)
+template <typename T, bool VA>
+__device__ __forceinline__ uint4 wide_row_group(const T *p, size_t row, int ld, int kb, int kv, int klen, bool in) {
+  constexpr int WPG = 16 / int(sizeof(T));
+  uint4 r = make_uint4(0u, 0u, 0u, 0u);
+  if constexpr (VA) {  // ld, kb and klen are multiples of WPG
+    if (in && kv < klen) r = *reinterpret_cast<const uint4 *>(p + row * ld + kb + kv);
+  } else {
+    T x[WPG];
+    const T *q = p + row * ld + kb + kv;
+#pragma unroll
+    for (int e = 0; e < WPG; e++) {
+      x[e] = 0;
+      if (in && kv + e < klen) x[e] = q[e];
+    }
+    r = wide_pack<T>(x);
+  }
+  return r;
+}
+// WPG consecutive k (from kb + kv) of column `col` of a row-major K x ld matrix
+template <typename T>
+__device__ __forceinline__ uint4 wide_col_group(const T *p, int col, int ld, int kb, int kv, int klen, bool in) {
+  constexpr int WPG = 16 / int(sizeof(T));
+  T x[WPG];
+  const T *q = p + size_t(kb + kv) * ld + col;
+#pragma unroll
+  for (int e = 0; e < WPG; e++) {
+    x[e] = 0;
+    if (in && kv + e < klen) x[e] = q[size_t(e) * ld];
+  }
+  return wide_pack<T>(x);
+}
+
+template <typename T, int KW, bool VA>
+__global__ __launch_bounds__(kWideThreads) void k_gemm_wide(GemmArgs<T> g) {
+  constexpr int LDK = KW + 4, WPG = 16 / int(sizeof(T)), NQ = int(sizeof(T));
+  // plain and masked steps (KW, KW / 2 words) are whole 16-word MFMA chunks
+  static_assert(KW % 32 == 0, "step widths a whole number of MFMA chunks");
+  // 16-byte groups per thread and operand panel: NJ in a plain step, NJM in a
+  // masked one (then slots NJM.. hold the masks' groups)
+  constexpr int NJ = (KW / 4 + 7) / 8, NJM = (KW / 8 + 7) / 8, NS = NJ > 2 * NJM ? NJ : 2 * NJM;
+  __shared__ __align__(16) uint32_t As[64 * LDK];
+  __shared__ __align__(16) uint32_t Bt[64 * LDK];
+  const int M = g.M, N = g.N, K = g.K;
+  // one-dimensional launch, renumbered per XCD: column tile fastest, batch entry slowest
+  const int gx = (N + 63) / 64, gy = (M + 63) / 64, lw = xcd_swizzle(int(blockIdx.x), int(gridDim.x));
+  const int bz = lw / (gx * gy), m0 = (lw / gx) % gy * 64, n0 = lw % gx * 64;
+  const int tid = int(threadIdx.x), lane = tid & 63, wave = tid >> 6;
+  const int li = lane & 15, lg = lane >> 4, rg = wave & 3, cg = wave >> 2;
+  // staging: A group j of thread tid is row tid >> 3, 16-byte group (tid & 7) + 8j
+  // of the step; B group j is column tid & 63, k words WPG ((tid >> 6) + 8j) + e
+  const int arow = tid >> 3, bn = tid & 63, ag = tid & 7, bg = tid >> 6;
+  const bool arow_ok = m0 + arow < M, bn_ok = n0 + bn < N;
+  uint4 ra[NS], rb[NS];
+  bool masked = false;  // the staged step's kind (uniform)
+  auto load = [&](const WideStep<T> &w) {
+    masked = w.a2 || w.b2;
+    const size_t row = size_t(m0 + arow);
+    const T *a2 = w.a2 ? w.a2 : w.a, *b2 = w.b2 ? w.b2 : w.b;  // a missing mask reads as zero below
+    if (masked) {
+#pragma unroll
+      for (int j = 0; j < NJM; j++) {
+        const int gi = ag + 8 * j;
+        const bool in = arow_ok && gi < KW / 8;
+        ra[j] = wide_row_group<T, VA>(w.a, row, K, w.kb, gi * WPG, w.klen, in);
+        ra[NJM + j] = wide_row_group<T, VA>(a2, row, K, w.kb, gi * WPG, w.klen, in && w.a2);
+      }
+#pragma unroll
+      for (int j = 0; j < NJM; j++) {
+        const int gi = bg + 8 * j;
+        const bool in = bn_ok && gi < KW / 8;
+        rb[j] = wide_col_group<T>(w.b, n0 + bn, N, w.kb, gi * WPG, w.klen, in);
+        rb[NJM + j] = wide_col_group<T>(b2, n0 + bn, N, w.kb, gi * WPG, w.klen, in && w.b2);
+      }
+    } else {
+#pragma unroll
+      for (int j = 0; j < NJ; j++) {
+        const int gi = ag + 8 * j;
+        ra[j] = wide_row_group<T, VA>(w.a, row, K, w.kb, gi * WPG, w.klen, arow_ok && gi < KW / 4);
+      }
+#pragma unroll
+      for (int j = 0; j < NJ; j++) {
+        const int gi = bg + 8 * j;
+        rb[j] = wide_col_group<T>(w.b, n0 + bn, N, w.kb, gi * WPG, w.klen, bn_ok && gi < KW / 4);
+      }
+    }
+  };
+  // every word of the step's rows is written (zeros past klen, M and N)
+  auto store = [&]() {
+    const uint4 z = make_uint4(0u, 0u, 0u, 0u);
+    if (masked) {
+#pragma unroll
+      for (int j = 0; j < NJM; j++) {
+        const int ga = ag + 8 * j, gb = bg + 8 * j;
+        if (ga < KW / 8) *reinterpret_cast<uint4 *>(&As[arow * LDK + 4 * ga]) = wide_digits<T>(ra[j], ra[NJM + j]);
+        if (gb < KW / 8) *reinterpret_cast<uint4 *>(&Bt[bn * LDK + 4 * gb]) = wide_digits<T>(rb[j], rb[NJM + j]);
+      }
+    } else {
+#pragma unroll
+      for (int j = 0; j < NJ; j++) {
+        const int ga = ag + 8 * j, gb = bg + 8 * j;
+        if (ga < KW / 4) *reinterpret_cast<uint4 *>(&As[arow * LDK + 4 * ga]) = wide_digits<T>(ra[j], z);
+        if (gb < KW / 4) *reinterpret_cast<uint4 *>(&Bt[bn * LDK + 4 * gb]) = wide_digits<T>(rb[j], z);
+      }
+    }
+  };
+  v4i_t acc[2][NQ];
+#pragma unroll
+  for (int t = 0; t < 2; t++)
+#pragma unroll
+    for (int q = 0; q < NQ; q++) acc[t][q] = v4i_t{0, 0, 0, 0};
+  const int nsteps = wide_steps<T, KW>(g);
+  WideStep<T> cur = wide_step<T, KW>(g, bz, 0);
+  load(cur);
+  for (int i = 0; i < nsteps; i++) {
+    store();
+    __syncthreads();
+    const int nkc = (cur.klen * int(sizeof(T) / 4) + 15) / 16;
+    if (i + 1 < nsteps) {
+      cur = wide_step<T, KW>(g, bz, i + 1);
+      load(cur);
+    }
+    for (int kc = 0; kc < nkc; kc++) {
+      v4i_t as[NQ];
+      digit_shifts<T>(*reinterpret_cast<const uint4 *>(&As[(16 * rg + li) * LDK + 16 * kc + 4 * lg]), as);
+#pragma unroll
+      for (int t = 0; t < 2; t++) {
+        const uint4 b = *reinterpret_cast<const uint4 *>(&Bt[(32 * cg + 16 * t + li) * LDK + 16 * kc + 4 * lg]);
+        const v4i_t bv = v4i_t{int(b.x), int(b.y), int(b.z), int(b.w)};
+#pragma unroll
+        for (int q = 0; q < NQ; q++) acc[t][q] = __builtin_amdgcn_mfma_i32_16x16x64_i8(as[q], bv, acc[t][q], 0, 0, 0);
+      }
+    }
+    __syncthreads();
+  }
+  T *C = g.C + size_t(bz) * g.sC;
+  const T *Cin = g.Cin ? g.Cin + size_t(bz) * g.sC : nullptr;
+#pragma unroll
+  for (int t = 0; t < 2; t++) {
+    const int gn = n0 + 32 * cg + 16 * t + li;
+#pragma unroll
+    for (int r = 0; r < 4; r++) {
+      // accumulator register r of lane (li, lg): row 4 lg + r, column li of the MFMA tile
+      const int gm = m0 + 16 * rg + 4 * lg + r;
+      if (gm >= M || gn >= N) continue;
+      const size_t idx = size_t(gm) * N + gn;
+      const T v = digit_fold<T>(acc[t], r);
+      C[idx] = (Cin ? Cin[idx] : T(0)) + (g.sign < 0 ? T(0) - v : v);
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Both parties' Beaver products of an SxS gate on one GPU, reconstructed, per
+// 48 x 32 output tile: party 0's C0 + (A^ - RA0)(B^ - RB0) and party 1's
+// C1 - (A^ RB1 + RA1 B^), written as their sum (the masked product both
+// parties reveal).  Each K phase (144 words of Z_2^32, 48 of Z_2^64) stages all
+// six operand panels at once -- A^, RA0, RA1 rows and B^, RB0, RB1 columns, as
+// digits of A^ - RA0, A^, RA1 and of B^ - RB0, RB1, B^ in LDS -- so the
+// per-graph products of the affinity model (140 x 140 by 140 x N) cost one
+// memory round trip (three for Z_2^64); the next phase's loads are issued before
+// the current phase's MFMAs.  Six waves, one 16 x 16 MFMA tile each (rows
+// 16 (w % 3), columns 16 (w / 3)), with party 0's and party 1's accumulators.
+// The 48-row tiles cover 140 rows as 48 + 48 + 44.
+// ---------------------------------------------------------------------------
+constexpr int kSxsTM = 48, kSxsTN = 32, kSxsThreads = 384;
+// 32-bit words of K per phase, a multiple of 16 (the MFMA chunk): 144 in
+// Z_2^32 (142 KB of LDS, one workgroup per CU, the affinity model's products in
+// one phase), 96 in Z_2^64 (its staging registers and eight-shift accumulators
+// leave room for two thirds of the width; three phases).  Measured alternative:
+// 80-word phases in Z_2^32 (two workgroups per CU, 168 VGPRs) were slower,
+// 17.7 / 26.6 / 38.5 against 11.8 / 23.5 / 35.7 us for N = 78 / 156 / 312.
+template <typename T>
+constexpr int sxs_kc() {
+  return sizeof(T) == 4 ? 144 : 96;
+}
+
+template <typename T, bool VA>
+__global__ __launch_bounds__(kSxsThreads) void k_sxs_fused(GemmArgs<T> g0, GemmArgs<T> g1) {
+  constexpr int KC = sxs_kc<T>(), WPG = 16 / int(sizeof(T)), NQ = int(sizeof(T)), LDK = KC + 4, GR = KC / 4;
+  constexpr int KT = KC * 4 / int(sizeof(T));  // words of T per phase
+  constexpr int NA = (kSxsTM * GR + kSxsThreads - 1) / kSxsThreads;
+  constexpr int NB = (kSxsTN * GR + kSxsThreads - 1) / kSxsThreads;
+  // the MFMA loop reads whole 16-word chunks of a row: KC a multiple of 16 keeps
+  // them inside the staged words (zeros past the phase's K); rows of KC + 4
+  // words put 16-byte reads of consecutive rows in distinct bank groups
+  static_assert(KC % 16 == 0, "phase width a whole number of MFMA chunks");
+  __shared__ __align__(16) uint32_t As[3 * kSxsTM * LDK];  // digits of A^ - RA0, A^, RA1
+  __shared__ __align__(16) uint32_t Bt[3 * kSxsTN * LDK];  // digits of B^ - RB0, RB1, B^ (as [n][k])
+  const int M = g0.M, N = g0.N, K = g0.K;
+  // one-dimensional launch, renumbered per XCD: column tile fastest, graph slowest
+  const int gx = (N + kSxsTN - 1) / kSxsTN, gy = (M + kSxsTM - 1) / kSxsTM;
+  const int lw = xcd_swizzle(int(blockIdx.x), int(gridDim.x));
+  const int bz = lw / (gx * gy), m0 = (lw / gx) % gy * kSxsTM, n0 = lw % gx * kSxsTN;
+  const int tid = int(threadIdx.x), lane = tid & 63, wave = tid >> 6;
+  const int li = lane & 15, lg = lane >> 4, rg = wave % 3, cg = wave / 3;
+  const T *Ah = g0.A1 + size_t(bz) * g0.sA, *RA0 = g0.A2 + size_t(bz) * g0.sA, *RA1 = g1.A1b + size_t(bz) * g1.sA;
+  const T *Bh = g0.B1 + size_t(bz) * g0.sB, *RB0 = g0.B2 + size_t(bz) * g0.sB, *RB1 = g1.B1 + size_t(bz) * g1.sB;
+  // this lane's four outputs: rows 4 lg + r of the wave's MFMA tile, column li
+  const int on = n0 + 16 * cg + li;
+  T cin[4];
+#pragma unroll
+  for (int r = 0; r < 4; r++) {
+    const int om = m0 + 16 * rg + 4 * lg + r;
+    cin[r] = 0;
+    if (om < M && on < N) {
+      const size_t idx = size_t(om) * N + on;
+      if (g0.Cin) cin[r] += g0.Cin[size_t(bz) * g0.sC + idx];
+      if (g1.Cin) cin[r] += g1.Cin[size_t(bz) * g1.sC + idx];
+    }
+  }
+  uint4 xa[NA], xa0[NA], xa1[NA], xb[NB], xb0[NB], xb1[NB];
+  auto load = [&](int kb) {
+    const int klen = min(KT, K - kb);
+#pragma unroll
+    for (int j = 0; j < NA; j++) {
+      const int f = tid + kSxsThreads * j, r = f / GR, gi = f % GR;
+      const bool in = f < kSxsTM * GR && m0 + r < M;
+      const size_t row = size_t(m0 + r);
+      xa[j] = wide_row_group<T, VA>(Ah, row, K, kb, gi * WPG, klen, in);
+      xa0[j] = wide_row_group<T, VA>(RA0, row, K, kb, gi * WPG, klen, in);
+      xa1[j] = wide_row_group<T, VA>(RA1, row, K, kb, gi * WPG, klen, in);
+    }
+#pragma unroll
+    for (int j = 0; j < NB; j++) {
+      const int f = tid + kSxsThreads * j, n = f % kSxsTN, gi = f / kSxsTN;
+      const bool in = f < kSxsTN * GR && n0 + n < N;
+      xb[j] = wide_col_group<T>(Bh, n0 + n, N, kb, gi * WPG, klen, in);
+      xb0[j] = wide_col_group<T>(RB0, n0 + n, N, kb, gi * WPG, klen, in);
+      xb1[j] = wide_col_group<T>(RB1, n0 + n, N, kb, gi * WPG, klen, in);
+    }
+  };
+  // every word of the panels' rows is written (zeros past K, M and N)
+  auto store = [&]() {
+    const uint4 z = make_uint4(0u, 0u, 0u, 0u);
+#pragma unroll
+    for (int j = 0; j < NA; j++) {
+      const int f = tid + kSxsThreads * j, r = f / GR, gi = f % GR;
+      if (f < kSxsTM * GR) {
+        uint32_t *p = &As[r * LDK + 4 * gi];
+        *reinterpret_cast<uint4 *>(p) = wide_digits<T>(xa[j], xa0[j]);
+        *reinterpret_cast<uint4 *>(p + kSxsTM * LDK) = wide_digits<T>(xa[j], z);
+        *reinterpret_cast<uint4 *>(p + 2 * kSxsTM * LDK) = wide_digits<T>(xa1[j], z);
+      }
+    }
+#pragma unroll
+    for (int j = 0; j < NB; j++) {
+      const int f = tid + kSxsThreads * j, n = f % kSxsTN, gi = f / kSxsTN;
+      if (f < kSxsTN * GR) {
+        uint32_t *p = &Bt[n * LDK + 4 * gi];
+        *reinterpret_cast<uint4 *>(p) = wide_digits<T>(xb[j], xb0[j]);
+        *reinterpret_cast<uint4 *>(p + kSxsTN * LDK) = wide_digits<T>(xb1[j], z);
+        *reinterpret_cast<uint4 *>(p + 2 * kSxsTN * LDK) = wide_digits<T>(xb[j], z);
+      }
+    }
+  };
+  // one accumulator set, folded into ring words after each party's MFMAs of a
+  // phase (a phase's shift sums are exact, far below 2^15 words of K)
+  v4i_t acc[NQ];
+#pragma unroll
+  for (int q = 0; q < NQ; q++) acc[q] = v4i_t{0, 0, 0, 0};
+  T vs0[4] = {0, 0, 0, 0}, vs1[4] = {0, 0, 0, 0};
+  auto fold = [&](T (&vs)[4]) {
+#pragma unroll
+    for (int r = 0; r < 4; r++) {
+      vs[r] += digit_fold<T>(acc, r);
+#pragma unroll
+      for (int q = 0; q < NQ; q++) acc[q][r] = 0;
+    }
+  };
+  // acc += (row panel pa) . (column panel pb)^T over the phase's nkc 16-word chunks
+  auto mfma_panel = [&](int pa, int pb, int nkc) {
+    const int ar = pa * kSxsTM * LDK + (16 * rg + li) * LDK + 4 * lg;
+    const int br = pb * kSxsTN * LDK + (16 * cg + li) * LDK + 4 * lg;
+    for (int kc = 0; kc < nkc; kc++) {
+      v4i_t as[NQ];
+      const uint4 b = *reinterpret_cast<const uint4 *>(&Bt[br + 16 * kc]);
+      const v4i_t bv = v4i_t{int(b.x), int(b.y), int(b.z), int(b.w)};
+      digit_shifts<T>(*reinterpret_cast<const uint4 *>(&As[ar + 16 * kc]), as);
+#pragma unroll
+      for (int q = 0; q < NQ; q++) acc[q] = __builtin_amdgcn_mfma_i32_16x16x64_i8(as[q], bv, acc[q], 0, 0, 0);
+    }
+  };
+  load(0);
+  for (int kb = 0; kb < K; kb += KT) {
+    store();
+    __syncthreads();
+    const int nkc = (min(KT, K - kb) * int(sizeof(T) / 4) + 15) / 16;
+    if (kb + KT < K) load(kb + KT);
+    mfma_panel(0, 0, nkc);  // party 0: (A^ - RA0)(B^ - RB0)
+    fold(vs0);
+    mfma_panel(1, 1, nkc);  // party 1: A^ RB1 + RA1 B^
+    mfma_panel(2, 2, nkc);
+    fold(vs1);
+    __syncthreads();
+  }
+  T *C = g0.C + size_t(bz) * g0.sC;
+#pragma unroll
+  for (int r = 0; r < 4; r++) {
+    const int om = m0 + 16 * rg + 4 * lg + r;
+    if (om >= M || on >= N) continue;
+    // party 0's share (sign +1) plus party 1's (sign -1)
+    C[size_t(om) * N + on] = cin[r] + vs0[r] - vs1[r];
+  }
+}
+
+// C[b] = Cin[b] (or 0) before the split-K slices are added
+template <typename T>
+__global__ void k_gemm_init(int M, int N, int batch, size_t sC, const T *Cin, T *C) {
+  const size_t per = size_t(M) * N, n = per * batch;
+  for (size_t i = size_t(blockIdx.x) * blockDim.x + threadIdx.x; i < n; i += size_t(gridDim.x) * blockDim.x) {
+    const size_t b = i / per, r = i % per;
+    C[b * sC + r] = Cin ? Cin[b * sC + r] : T(0);
+  }
+}
+
+static bool aligned16(const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
+// rows of A (resp. B) can be read as 16-byte words
+static bool gemm_vec_a(const GemmArgs<uint32_t> &g) {
+  return g.K % 4 == 0 && (g.batch == 1 || g.sA % 4 == 0) && aligned16(g.A1) && aligned16(g.A2) && aligned16(g.A1b);
+}
+static bool gemm_vec_b(const GemmArgs<uint32_t> &g) {
+  return g.N % 4 == 0 && (g.batch == 1 || g.sB % 4 == 0) && aligned16(g.B1) && aligned16(g.B2) && aligned16(g.B1b);
+}
+static hipError_t launch_mfma(const Launch &L, dim3 grid, const GemmArgs<uint64_t> &g0,
+                              const GemmArgs<uint64_t> &g1, int nz0) {
+  hipLaunchKernelGGL(k_gemm_mfma64, grid, dim3(256), 0, L.stream, g0, g1, nz0);
+  return hipGetLastError();
+}
+static hipError_t launch_mfma(const Launch &L, dim3 grid, const GemmArgs<uint32_t> &g0,
+                              const GemmArgs<uint32_t> &g1, int nz0) {
+  const bool va = gemm_vec_a(g0) && gemm_vec_a(g1), vb = gemm_vec_b(g0) && gemm_vec_b(g1);
+  if (va && vb)
+    hipLaunchKernelGGL((k_gemm_mfma<true, true>), grid, dim3(256), 0, L.stream, g0, g1, nz0);
+  else if (va)
+    hipLaunchKernelGGL((k_gemm_mfma<true, false>), grid, dim3(256), 0, L.stream, g0, g1, nz0);
+  else if (vb)
+    hipLaunchKernelGGL((k_gemm_mfma<false, true>), grid, dim3(256), 0, L.stream, g0, g1, nz0);
+  else
+    hipLaunchKernelGGL((k_gemm_mfma<false, false>), grid, dim3(256), 0, L.stream, g0, g1, nz0);
+  return hipGetLastError();
+}
+
+// K slice of the matrix-core kernels: 64 words (Z_2^32), 32 (Z_2^64)
+template <typename T>
+constexpr int mfma_bk() {
+  return sizeof(T) == 4 ? 64 : 32;
+}
+// the matrix-core path: selected (not MPCX_GEMM=valu), and for Z_2^64 a total K
+// below 2^15 (the low shifts' int32 sums stay exact)
+template <typename T>
+static bool use_mfma(const Launch &L, const GemmArgs<T> &g) {
+  if (L.gemm == 1) return false;
+  constexpr int bk = mfma_bk<T>();
+  const int Kt = g.A1b ? (g.K + bk - 1) / bk * bk + g.K : g.K;
+  return sizeof(T) == 4 || Kt < (1 << 15);
+}
+// split-K factor: enough K slices that the launch has about two tiles per CU
+template <typename T>
+static int gemm_ksplit(const Launch &L, const GemmArgs<T> &g, int tiles, bool mfma) {
+  constexpr int bk = mfma_bk<T>();
+  const int Kt = g.A1b ? (g.K + bk - 1) / bk * bk + g.K : g.K;
+  if (tiles >= L.num_cu || Kt < 64) return 1;
+  const int want = (2 * L.num_cu + tiles - 1) / tiles;
+  return std::max(1, std::min(want, mfma ? (Kt + bk - 1) / bk : Kt / 32));
+}
+template <typename T>
+static int gemm_tiles(const GemmArgs<T> &g) {
+  return ((g.N + 63) / 64) * ((g.M + 63) / 64) * g.batch;
+}
+template <typename T>
+static hipError_t gemm_init(const Launch &L, const GemmArgs<T> &g) {
+  if (g.ksplit <= 1 || g.C == g.Cin || (g.c_zero && !g.Cin)) return hipSuccess;
+  const int block = 256;
+  int grid = grid_for(k_gemm_init<T>, block, size_t(g.M) * g.N * g.batch, L.num_cu);
+  hipLaunchKernelGGL((k_gemm_init<T>), dim3(grid), dim3(block), 0, L.stream, g.M, g.N, g.batch, g.sC, g.Cin, g.C);
+  return hipGetLastError();
+}
+
+// The wide-K kernel: automatic path selection, the matrix-core path, and either
+// enough tiles to occupy a quarter of the CUs or at most one K step per
+// segment.  A long K over few tiles (the fully connected layers: 22 rows,
+// K = 312..1024) is spread over more CUs by the split-K tiled kernel.
+template <typename T>
+static bool use_wide(const Launch &L, const GemmArgs<T> &g) {
+  if (L.gemm != 0 || !use_mfma(L, g)) return false;
+  constexpr int KT = kWideK * 4 / int(sizeof(T));
+  return gemm_tiles(g) >= L.num_cu / 4 || g.K <= KT;
+}
+// rows of A (and of the masks and second segment) read as 16-byte groups
+template <typename T>
+static bool wide_vec_a(const GemmArgs<T> &g) {
+  constexpr int wpg = 16 / int(sizeof(T));
+  return g.K % wpg == 0 && (g.batch == 1 || g.sA % wpg == 0) && aligned16(g.A1) && aligned16(g.A2) &&
+         aligned16(g.A1b);
+}
+template <typename T>
+static hipError_t launch_wide(const Launch &L, const GemmArgs<T> &g) {
+  const size_t wgs = size_t((g.N + 63) / 64) * size_t((g.M + 63) / 64) * size_t(g.batch);
+  if (wgs > size_t(INT32_MAX)) return hipErrorInvalidValue;  // one-dimensional, XCD-ordered launch
+  const dim3 grid{unsigned(wgs), 1u, 1u};
+  if (wide_vec_a(g))
+    hipLaunchKernelGGL((k_gemm_wide<T, kWideK, true>), grid, dim3(kWideThreads), 0, L.stream, g);
+  else
+    hipLaunchKernelGGL((k_gemm_wide<T, kWideK, false>), grid, dim3(kWideThreads), 0, L.stream, g);
+  return hipGetLastError();
+}
+
+template <typename T>
+hipError_t launch_gemm(const Launch &L, const GemmArgs<T> &g0) {
+  if (g0.M <= 0 || g0.N <= 0 || g0.batch <= 0) return hipSuccess;
+  if (use_wide(L, g0)) return launch_wide<T>(L, g0);
+  const bool mfma = use_mfma(L, g0);
+  if (g0.A1b && !mfma) {
+    // the VALU kernel takes one K segment: add the second product in a second launch
+    GemmArgs<T> a = g0, b = g0;
+    a.A1b = a.B1b = nullptr;
+    b.A1 = g0.A1b;
+    b.B1 = g0.B1b;
+    b.A2 = b.B2 = b.A1b = b.B1b = nullptr;
+    b.Cin = b.C;
+    hipError_t e = launch_gemm<T>(L, a);
+    return e != hipSuccess ? e : launch_gemm<T>(L, b);
+  }
+  GemmArgs<T> g = g0;
+  g.ksplit = gemm_ksplit(L, g, gemm_tiles(g), mfma);
+  hipError_t e = gemm_init(L, g);
+  if (e != hipSuccess) return e;
+  dim3 grid((g.N + 63) / 64, (g.M + 63) / 64, g.batch * g.ksplit);
+  if (mfma) return launch_mfma(L, grid, g, g, int(grid.z));
+  hipLaunchKernelGGL((k_gemm<T>), grid, dim3(256), 0, L.stream, g);
+  return hipGetLastError();
+}
+
+template <typename T>
+hipError_t launch_gemm_pair(const Launch &L, const GemmArgs<T> &p0, const GemmArgs<T> &p1) {
+  const bool empty0 = p0.M <= 0 || p0.N <= 0 || p0.batch <= 0;
+  const bool empty1 = p1.M <= 0 || p1.N <= 0 || p1.batch <= 0;
+  if (empty0 || empty1 || !use_mfma(L, p0) || !use_mfma(L, p1)) {
+    hipError_t e = launch_gemm<T>(L, p0);
+    return e != hipSuccess ? e : launch_gemm<T>(L, p1);
+  }
+  GemmArgs<T> g0 = p0, g1 = p1;
+  const int tiles = gemm_tiles(g0) + gemm_tiles(g1);
+  g0.ksplit = gemm_ksplit(L, g0, tiles, true);
+  g1.ksplit = gemm_ksplit(L, g1, tiles, true);
+  hipError_t e = gemm_init(L, g0);
+  if (e == hipSuccess) e = gemm_init(L, g1);
+  if (e != hipSuccess) return e;
+  const int nz0 = g0.batch * g0.ksplit;
+  dim3 grid((std::max(g0.N, g1.N) + 63) / 64, (std::max(g0.M, g1.M) + 63) / 64, nz0 + g1.batch * g1.ksplit);
+  return launch_mfma(L, grid, g0, g1, nz0);
+}
+
+// k_sxs_fused applies to the Beaver pair as the SxS gates form it: party 0
+// (A1 - A2)(B1 - B2) + Cin with sign +1, party 1 with the same A1 in its first
+// segment, the same B1 in its second, no masks, sign -1; the same shapes and
+// strides; enough tiles for a quarter of the CUs or K within one phase.
+template <typename T>
+static bool use_sxs_fused(const Launch &L, const GemmArgs<T> &g0, const GemmArgs<T> &g1) {
+  if (L.gemm != 0 || !use_mfma(L, g0) || !use_mfma(L, g1)) return false;
+  const bool form = g0.A2 && g0.B2 && !g0.A1b && g0.sign == 1 && g1.A1 == g0.A1 && g1.B1b == g0.B1 && g1.A1b &&
+                    g1.B1 && !g1.A2 && !g1.B2 && g1.sign == -1;
+  const bool shape = g0.M == g1.M && g0.N == g1.N && g0.K == g1.K && g0.batch == g1.batch && g0.sA == g1.sA &&
+                     g0.sB == g1.sB && g0.sC == size_t(g0.M) * g0.N && g1.sC == g0.sC;
+  const int tiles = ((g0.N + kSxsTN - 1) / kSxsTN) * ((g0.M + kSxsTM - 1) / kSxsTM) * g0.batch;
+  return form && shape && (tiles >= L.num_cu / 4 || g0.K <= sxs_kc<T>() * 4 / int(sizeof(T)));
+}
+
+template <typename T>
+hipError_t launch_gemm_pair_sum(const Launch &L, const GemmArgs<T> &g0, const GemmArgs<T> &g1, T *out) {
+  if (g0.M <= 0 || g0.N <= 0 || g0.batch <= 0) return hipSuccess;
+  if (use_sxs_fused(L, g0, g1)) {
+    GemmArgs<T> a = g0;
+    a.C = out;
+    const size_t wgs = size_t((g0.N + kSxsTN - 1) / kSxsTN) * size_t((g0.M + kSxsTM - 1) / kSxsTM) * size_t(g0.batch);
+    if (wgs > size_t(INT32_MAX)) return hipErrorInvalidValue;  // one-dimensional, XCD-ordered launch
+    const dim3 grid{unsigned(wgs), 1u, 1u};
+    if (wide_vec_a(g0) && wide_vec_a(g1))
+      hipLaunchKernelGGL((k_sxs_fused<T, true>), grid, dim3(kSxsThreads), 0, L.stream, a, g1);
+    else
+      hipLaunchKernelGGL((k_sxs_fused<T, false>), grid, dim3(kSxsThreads), 0, L.stream, a, g1);
+    return hipGetLastError();
+  }
+  hipError_t e = launch_gemm_pair<T>(L, g0, g1);
+  if (e != hipSuccess) return e;
+  return launch_reconstruct<T>(L, size_t(g0.batch) * g0.M * g0.N, g0.C, g1.C, out);
+}
+
+#define INST(T)                                                                                                      \
+  template hipError_t launch_gemm<T>(const Launch &, const GemmArgs<T> &);                                           \
+  template hipError_t launch_gemm_pair<T>(const Launch &, const GemmArgs<T> &, const GemmArgs<T> &);                \
+  template hipError_t launch_gemm_pair_sum<T>(const Launch &, const GemmArgs<T> &, const GemmArgs<T> &, T *);
+
+INST(uint32_t)
+INST(uint64_t)
+
+}  // namespace mpcx

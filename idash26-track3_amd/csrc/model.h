@@ -24,6 +24,7 @@
 #include <utility>
 #include <vector>
 
+#include "gemm.h"
 #include "kernels.h"
 #include "mpcx_core.h"
 

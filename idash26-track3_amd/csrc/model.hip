@@ -609,6 +609,18 @@ class Model final : public ModelBase, KeySource {
 
   // ---------------- weights ----------------
   int nlayers() const { return 5 + d_.nfus; }
+  // The fully connected products' outputs (layers l >= 3) each have their own
+  // range of fc_, cleared by one launch per forward, so that their split-K
+  // slices add into zeros without a clearing launch per product.
+  size_t fc_off(int B, int l) const {
+    size_t o = 0;
+    for (int j = 3; j < l; j++) {
+      int in, out;
+      layer_io(j, &in, &out);
+      o += size_t(B) * out;
+    }
+    return o;
+  }
   void layer_io(int l, int *in, int *out) const {
     if (l < 3) {
       *in = l == 0 ? d_.feat : d_.gcn[l - 1];
@@ -779,6 +791,7 @@ class Model final : public ModelBase, KeySource {
     TRY(mh_.alloc(BN));
     TRY(V0_.alloc(BN * d_.gcn[2]));
     TRY(V1_.alloc(BN * d_.gcn[2]));
+    TRY(fc_.alloc(fc_off(B, 5 + d_.nfus)));
     TRY(out_.alloc(B));
     TRY(adj_.prepare(B, N, s_, d_.lut_nmax));
     work_B_ = B;
@@ -1503,9 +1516,11 @@ class Model final : public ModelBase, KeySource {
       g.A1 = x;
       g.B1 = wt_[l].p;
       g.C = y;
+      g.c_zero = l >= 3;  // y is the layer's range of fc_
       TRY(launch_gemm<T>(L_, g));
       return span.end();
     };
+    auto fc = [&](int l) { return fc_.p + fc_off(B, l); };
     T *H = bA_.p, *Z = bB_.p, *XW = bC_.p;
 
     TRY(r.reveal(BN * d_.feat, x0_.p, x1_.p, 0, H));
@@ -1546,11 +1561,12 @@ class Model final : public ModelBase, KeySource {
       std::swap(cur, nxt);
       R = pr + (R & 1);
     }
-    // drug FCs
-    TRY(pub_gemm(cur, 3, B, Z));
-    TRY(trunc_eval(r, true, size_t(B) * d_.dfc[0], Z, bias_[3].p, d_.dfc[0], XW));
-    TRY(pub_gemm(XW, 4, B, Z));
-    TRY(trunc_eval(r, false, size_t(B) * d_.dfc[1], Z, bias_[4].p, d_.dfc[1], XW));
+    // drug FCs (one clearing launch for every fully connected product's output)
+    TRY(launch_axpby<T>(L_, fc_off(B, 5 + d_.nfus), T(0), nullptr, T(0), nullptr, T(0), fc_.p));
+    TRY(pub_gemm(cur, 3, B, fc(3)));
+    TRY(trunc_eval(r, true, size_t(B) * d_.dfc[0], fc(3), bias_[3].p, d_.dfc[0], XW));
+    TRY(pub_gemm(XW, 4, B, fc(4)));
+    TRY(trunc_eval(r, false, size_t(B) * d_.dfc[1], fc(4), bias_[4].p, d_.dfc[1], XW));
     // concat [drug, protein]; the protein embedding owner reveals it (one message
     // each way: the other party's share is zero, revealPublicLeaf,
     // ddg_orca_base.h:84-89)
@@ -1565,12 +1581,13 @@ class Model final : public ModelBase, KeySource {
     TRY(launch_concat<T>(L_, B, d_.dfc[1], d_.prot, XW, prot_pub, H));
     T *h = H, *h2 = XW;
     for (int k = 0; k < d_.nfus; k++) {
-      TRY(pub_gemm(h, 5 + k, B, Z));
+      T *z = fc(5 + k);
+      TRY(pub_gemm(h, 5 + k, B, z));
       if (k < d_.nfus - 1) {
-        TRY(trunc_eval(r, true, size_t(B) * d_.fus[k], Z, bias_[5 + k].p, d_.fus[k], h2));
+        TRY(trunc_eval(r, true, size_t(B) * d_.fus[k], z, bias_[5 + k].p, d_.fus[k], h2));
         std::swap(h, h2);
       } else {
-        TRY(r.output(B, size_t(B) * d_.fus[k], Z, hbias_[5 + k][0], out_.p));
+        TRY(r.output(B, size_t(B) * d_.fus[k], z, hbias_[5 + k][0], out_.p));
       }
     }
     if (gi_ != gates_.size()) return hipErrorUnknown;
@@ -1600,7 +1617,7 @@ class Model final : public ModelBase, KeySource {
   int graph_B_ = -1;
   Counters graph_ctr_;
   DevBuf<T> x0_, x1_, a0_, a1_, m0_, m1_, prot_;
-  DevBuf<T> bA_, bB_, bC_, Ah_, An_, mh_, V0_, V1_;
+  DevBuf<T> bA_, bB_, bC_, Ah_, An_, mh_, V0_, V1_, fc_;
   DevBuf<int64_t> out_;
   Workspace<T> ws_;
   AdjNorm<T> adj_;
