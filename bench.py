@@ -27,6 +27,9 @@ def affinity_metric(bw, B):
 
 # Peak integer VALU rate of MI355X: 256 CUs x 4 SIMD x 16 lanes x 2.4 GHz.
 VALU_PEAK_TOPS = 256 * 64 * 2.4e9 / 1e12
+# Peak LDS read rate: 128 bytes per clock per CU (a 64-lane ds_read_b32 in two
+# clocks), 256 CUs x 2.4 GHz.
+LDS_PEAK_TBS = 256 * 128 * 2.4e9 / 1e12
 HBM_PEAK_GBS = 8000.0
 # Ring multiply-adds per second at the peak of each GEMM path: the int8 matrix
 # cores (5.0 POP/s dense = 2.5 P int8 MAC/s) spend 16 int8 MACs per Z_2^32 MAC
@@ -54,6 +57,18 @@ SLACK_DESC = {1: ", GCN products H.W^T truncated with the slack gate",
               2: ", GCN products and aggregations truncated with the slack gate",
               3: ", every layer truncation local (LocalARS, the reference's default truncation; not bit-exact)"}
 VALU_OPS_PER_AES = {"perm32x2_b512": 318, "perm64_b512": 390, "perm64_b1024": 390, "t4_rep32_b1024": 452}
+# LDS table bytes read per AES call: 16 four-byte lookups per round, ten rounds
+# (the same level-loop blocks: 160 ds_read_b32 in every variant)
+LDS_BYTES_PER_AES = 160 * 4
+
+
+def lds_colimit(aes_per_s):
+    """The T-table reads of the same AES work against the LDS peak: the second
+    limit of the DCF kernel (its level loop issues about two VALU instructions
+    per table read, and a read takes two LDS clocks)."""
+    tbs = aes_per_s * LDS_BYTES_PER_AES / 1e12
+    return {"resource": "lds", "achieved": round(tbs, 2), "peak": round(LDS_PEAK_TBS, 2), "unit": "TB/s",
+            "frac": round(tbs / LDS_PEAK_TBS, 4)}
 
 
 def log(msg):
@@ -256,6 +271,7 @@ def main():
             "launches_per_step": prof["launches"],
             "aes_calls_per_step": prof["aes_calls"],
             "valu_ops_per_aes": VALU_OPS_PER_AES.get(variant),
+            "co_limit": lds_colimit(aes_per_s),
             "kernel_digest": digest,
         },
         # The same launches timed one by one (HIP events on the launch streams)
@@ -272,6 +288,7 @@ def main():
             "peak": round(VALU_PEAK_TOPS, 2),
             "unit": "TOP/s",
             "frac": round(achieved_tops / VALU_PEAK_TOPS, 4),
+            "co_limit": lds_colimit(launch_aes_per_s),
         },
         "roofline_gemm": {
             "kernel": f"ring GEMMs ({gemm_path}: public-weight products and SxS Beaver products, "
@@ -573,7 +590,7 @@ def run_relu(args):
         "key_bytes_per_element_per_party": round(key_bytes / n, 2),
         "roofline": {"kernel": "RELU gate call (k_tr_eval)", "bound": "valu",
                      "achieved": round(tops, 3), "peak": round(VALU_PEAK_TOPS, 2), "unit": "TOP/s",
-                     "frac": round(tops / VALU_PEAK_TOPS, 4)},
+                     "frac": round(tops / VALU_PEAK_TOPS, 4), "co_limit": lds_colimit(aes_s)},
         "roofline_hbm": {"kernel": "k_tr_eval key stream and inputs", "bound": "hbm", "achieved": round(key_gbs, 1),
                          "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(key_gbs / HBM_PEAK_GBS, 4)},
         "bit_exact": exact,
@@ -670,7 +687,7 @@ def run_adjnorm(args):
         "bytes_exchanged_per_graph": round(ctx.bytes_exchanged / (args.steps * B), 1),
         "roofline": {"kernel": "adjacency normalisation call (DCF/DPF AES work over the call)", "bound": "valu",
                      "achieved": round(tops, 3), "peak": round(VALU_PEAK_TOPS, 2), "unit": "TOP/s",
-                     "frac": round(tops / VALU_PEAK_TOPS, 4)},
+                     "frac": round(tops / VALU_PEAK_TOPS, 4), "co_limit": lds_colimit(aes / per)},
         "bit_exact": exact,
     }
     log(f"[adjnorm] {args.steps} x {B} graphs in {elapsed:.3f}s: {B / per:.0f} graphs/s")

@@ -230,8 +230,9 @@ mpcx_status mpcx_create(int bw, int scale, int device, mpcx_ctx **out) {
   if (const char *v = std::getenv("MPCX_GEMM")) {
     if (std::strcmp(v, "valu") == 0) c->L.gemm = 1;
     else if (std::strcmp(v, "tiled") == 0) c->L.gemm = 2;
+    else if (std::strcmp(v, "wide") == 0) c->L.gemm = 3;
     else if (std::strcmp(v, "auto") == 0 || !*v) c->L.gemm = 0;
-    else std::fprintf(stderr, "libmpcx: ignoring MPCX_GEMM=%s (auto, tiled or valu)\n", v);
+    else std::fprintf(stderr, "libmpcx: ignoring MPCX_GEMM=%s (auto, wide, tiled or valu)\n", v);
   }
   if (const char *v = std::getenv("MPCX_GRAPH")) c->L.graph = std::atoi(v) != 0 ? 1 : 0;
   *out = c;

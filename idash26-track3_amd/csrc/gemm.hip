@@ -917,6 +917,189 @@ __global__ __launch_bounds__(kSxsThreads) void k_sxs_fused(GemmArgs<T> g0, GemmA
   }
 }
 
+// ---------------------------------------------------------------------------
+// Panel products on buffer loads (both rings, the digit algebra above):
+// C[b] = Cin0[b] + Cin1[b] + sum_p sign_p (A_p1 - A_p2)[b] (B_p1 - B_p2)[b] over
+// NP <= 3 panels of one shape (M x K by K x N per batch entry; A_p2, B_p2, Cin
+// may be null).  An SxS gate is three panels -- party 0's (A^ - RA0)(B^ - RB0)
+// + C0 and party 1's C1 - A^ RB1 - RA1 B^ -- whose sum is the masked product
+// both parties reveal.  The kernel is meant to share CUs with the DCF gate
+// kernels of other lanes: 21 KB of LDS, three waves per workgroup, and a raised
+// wave priority (a short product on a lane's critical path).
+// Every operand load is a buffer load: the matrix of the batch entry is a buffer
+// resource in scalar registers, a lane supplies one 32-bit byte offset per step
+// and each MFMA chunk adds an immediate, and an element outside the matrix is
+// read through an offset past the resource's end, which the hardware returns as
+// zero (no address arithmetic in 64 bits, no exec-mask branches).
+// Workgroup: RW waves, 16 NT output columns; wave w owns the 16-row MFMA tile
+// at rows m0 + 16 w and keeps its A operands of a step in registers, in the
+// MFMA layout (row li, 16-byte group lg of each chunk), as balanced digits; the
+// workgroup stages the step's B rows as digits in LDS as [k][n] (LDN words per
+// row: the four k rows one lane reads for a chunk fall in distinct bank groups),
+// one 16-byte group per thread and operand.  A step is KPW 32-bit words of K of
+// one panel; the shift sums are folded into ring words after every step (a
+// step's int32 sums are exact, so Z_2^64 has no bound on K here).
+// Requires rows of A and B readable as 16-byte groups: K and N multiples of the
+// group, 16-byte aligned operands and batch strides (launch_gemm checks).
+// ---------------------------------------------------------------------------
+template <typename T>
+struct PanelArgs {
+  int M = 0, N = 0, K = 0, batch = 1, np = 1;
+  const T *a1[3] = {}, *a2[3] = {}, *b1[3] = {}, *b2[3] = {};
+  int sign[3] = {1, 1, 1};
+  size_t sA = 0, sB = 0, sC = 0;
+  const T *cin0 = nullptr, *cin1 = nullptr;
+  T *C = nullptr;
+};
+constexpr int kPanKPW = 144;           // 32-bit words of K per step: 9 MFMA chunks (K = 140 in one step)
+constexpr uint32_t kPanOob = 0x80000000u;  // a byte offset past every resource (matrices below 2 GiB)
+constexpr int kPanRsrcWord3 = 0x00020000;  // gfx9 buffer resource word 3: 32-bit data format
+
+typedef unsigned v4u_t __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t pan_rsrc(const void *p, size_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(p), short(0), int(bytes), kPanRsrcWord3);
+}
+__device__ __forceinline__ uint4 pan_load(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+  const v4u_t v = __builtin_amdgcn_raw_buffer_load_b128(r, int(off), 0, 0);
+  return make_uint4(v[0], v[1], v[2], v[3]);
+}
+
+// Waves per SIMD the register budget is set for: three in Z_2^32 (measured
+// faster than two even where a few registers spill), two in Z_2^64.
+template <typename T, int RW, int NT>
+constexpr int pan_waves() {
+  return sizeof(T) == 4 ? 3 : 2;
+}
+template <typename T, int NP, int RW, int NT>
+__global__ __launch_bounds__(64 * RW, (pan_waves<T, RW, NT>())) void k_panels(PanelArgs<T> g) {
+  constexpr int KPW = kPanKPW, NTH = 64 * RW, TN = 16 * NT, NQ = int(sizeof(T)), NC = KPW / 16;
+  constexpr int WPG = 16 / int(sizeof(T)), KT = KPW * 4 / int(sizeof(T));
+  constexpr int LDK = KPW + 4;                    // 32-bit words per LDS row (one column of B)
+  constexpr int GPR = TN / WPG;                   // 16-byte groups per B row of the tile
+  constexpr int NB = (KT * GPR + NTH - 1) / NTH;  // B groups per thread and operand
+  static_assert(KPW % 16 == 0, "whole MFMA chunks");
+  __shared__ __align__(16) uint32_t Bt[TN * LDK];  // B of a step as [n][k] digits
+  __builtin_amdgcn_s_setprio(2);
+  const int M = g.M, N = g.N, K = g.K;
+  const int gx = (N + TN - 1) / TN, gy = (M + 16 * RW - 1) / (16 * RW);
+  const int lw = xcd_swizzle(int(blockIdx.x), int(gridDim.x));
+  const int bz = lw / (gx * gy), m0 = (lw / gx) % gy * 16 * RW, n0 = lw % gx * TN;
+  const int tid = int(threadIdx.x), lane = tid & 63, wave = tid >> 6, li = lane & 15, lg = lane >> 4;
+  const int arow = m0 + 16 * wave + li;
+  const bool wave_ok = m0 + 16 * wave < M;
+  const size_t abytes = size_t(M) * K * sizeof(T), bbytes = size_t(K) * N * sizeof(T);
+  // byte offset of this lane's A row (past the resource if the row is past M)
+  const uint32_t arow_off = arow < M ? uint32_t(arow) * uint32_t(K) * uint32_t(sizeof(T)) : kPanOob;
+  const int ksteps = (K + KT - 1) / KT;
+  const uint4 z4 = make_uint4(0u, 0u, 0u, 0u);
+  v4i_t acc[NT][NQ];
+#pragma unroll
+  for (int t = 0; t < NT; t++)
+#pragma unroll
+    for (int q = 0; q < NQ; q++) acc[t][q] = v4i_t{0, 0, 0, 0};
+  T vs[NT][4];
+#pragma unroll
+  for (int t = 0; t < NT; t++)
+#pragma unroll
+    for (int r = 0; r < 4; r++) vs[t][r] = 0;
+#pragma unroll
+  for (int p = 0; p < NP; p++) {
+    // masks (uniform): only panel 0 may have them (party 0's product, or a
+    // product's first K segment), so later panels compile without
+    const bool ma = p == 0 && g.a2[0] != nullptr, mb = p == 0 && g.b2[0] != nullptr;
+    const __amdgpu_buffer_rsrc_t ra1 = pan_rsrc(g.a1[p] + size_t(bz) * g.sA, abytes);
+    const __amdgpu_buffer_rsrc_t rb1 = pan_rsrc(g.b1[p] + size_t(bz) * g.sB, bbytes);
+    const __amdgpu_buffer_rsrc_t ra2 = pan_rsrc(ma ? g.a2[0] + size_t(bz) * g.sA : g.a1[p], abytes);
+    const __amdgpu_buffer_rsrc_t rb2 = pan_rsrc(mb ? g.b2[0] + size_t(bz) * g.sB : g.b1[p], bbytes);
+    for (int ks = 0; ks < ksteps; ks++) {
+      const int kb = ks * KT, klen = min(KT, K - kb);
+      // B groups: k row kr of the step, 16-byte group q of the tile's columns
+      uint4 xb[NB], yb[NB];
+#pragma unroll
+      for (int j = 0; j < NB; j++) {
+        const int f = tid + NTH * j, kr = f / GPR, q = f % GPR, n = n0 + q * WPG;
+        const uint32_t off = (f < KT * GPR && kr < klen && n < N)
+                                 ? (uint32_t(kb + kr) * uint32_t(N) + uint32_t(n)) * uint32_t(sizeof(T))
+                                 : kPanOob;
+        xb[j] = pan_load(rb1, off);
+        yb[j] = mb ? pan_load(rb2, off) : z4;
+      }
+      // A groups of this lane: chunk c covers words (4c + lg) WPG .. of the step
+      uint4 xa[NC], ya[NC];
+      const uint32_t abase = arow_off + uint32_t(kb + lg * WPG) * uint32_t(sizeof(T));
+      const int kfull = klen / (4 * WPG);  // chunks whose 16 words are all inside the step
+#pragma unroll
+      for (int c = 0; c < NC; c++) {
+        uint32_t off = abase + uint32_t(c) * 64u;
+        if (c >= kfull && (4 * c + lg) * WPG >= klen) off = kPanOob;
+        xa[c] = pan_load(ra1, off);
+        ya[c] = ma ? pan_load(ra2, off) : z4;
+      }
+      // the B groups' digits, transposed into the [n][k] rows (one element per write)
+#pragma unroll
+      for (int j = 0; j < NB; j++) {
+        const int f = tid + NTH * j, kr = f / GPR, q = f % GPR;
+        if (f < KT * GPR) {
+          const uint4 d = wide_digits<T>(xb[j], yb[j]);
+          if constexpr (sizeof(T) == 4) {
+            uint32_t *bp = &Bt[(4 * q) * LDK + kr];
+            bp[0] = d.x;
+            bp[LDK] = d.y;
+            bp[2 * LDK] = d.z;
+            bp[3 * LDK] = d.w;
+          } else {
+            uint32_t *bp = &Bt[(2 * q) * LDK + 2 * kr];
+            *reinterpret_cast<uint2 *>(bp) = make_uint2(d.x, d.y);
+            *reinterpret_cast<uint2 *>(bp + LDK) = make_uint2(d.z, d.w);
+          }
+        }
+      }
+      __syncthreads();
+      const int nkc = (klen * NQ / 4 + 15) / 16;
+      if (wave_ok) {
+#pragma unroll
+        for (int c = 0; c < NC; c++) {
+          if (c < nkc) {
+            v4i_t as[NQ];
+            digit_shifts<T>(wide_digits<T>(xa[c], ya[c]), as);
+#pragma unroll
+            for (int t = 0; t < NT; t++) {
+              const uint4 b = *reinterpret_cast<const uint4 *>(&Bt[(16 * t + li) * LDK + 16 * c + 4 * lg]);
+              const v4i_t bv = v4i_t{int(b.x), int(b.y), int(b.z), int(b.w)};
+#pragma unroll
+              for (int q = 0; q < NQ; q++) acc[t][q] = __builtin_amdgcn_mfma_i32_16x16x64_i8(as[q], bv, acc[t][q], 0, 0, 0);
+            }
+          }
+        }
+      }
+#pragma unroll
+      for (int t = 0; t < NT; t++)
+#pragma unroll
+        for (int r = 0; r < 4; r++) {
+          const T v = digit_fold<T>(acc[t], r);
+          vs[t][r] += g.sign[p] < 0 ? T(0) - v : v;
+#pragma unroll
+          for (int q = 0; q < NQ; q++) acc[t][q][r] = 0;
+        }
+      __syncthreads();  // Bt is rewritten by the next step
+    }
+  }
+  T *C = g.C + size_t(bz) * g.sC;
+  const T *c0 = g.cin0 ? g.cin0 + size_t(bz) * g.sC : nullptr, *c1 = g.cin1 ? g.cin1 + size_t(bz) * g.sC : nullptr;
+#pragma unroll
+  for (int t = 0; t < NT; t++) {
+    const int on = n0 + 16 * t + li;
+#pragma unroll
+    for (int r = 0; r < 4; r++) {
+      // accumulator register r of lane (li, lg): row 4 lg + r, column li of the MFMA tile
+      const int om = m0 + 16 * wave + 4 * lg + r;
+      if (om >= M || on >= N) continue;
+      const size_t idx = size_t(om) * N + on;
+      C[idx] = (c0 ? c0[idx] : T(0)) + (c1 ? c1[idx] : T(0)) + vs[t][r];
+    }
+  }
+}
+
 // C[b] = Cin[b] (or 0) before the split-K slices are added
 template <typename T>
 __global__ void k_gemm_init(int M, int N, int batch, size_t sC, const T *Cin, T *C) {
@@ -996,7 +1179,7 @@ static hipError_t gemm_init(const Launch &L, const GemmArgs<T> &g) {
 // K = 312..1024) is spread over more CUs by the split-K tiled kernel.
 template <typename T>
 static bool use_wide(const Launch &L, const GemmArgs<T> &g) {
-  if (L.gemm != 0 || !use_mfma(L, g)) return false;
+  if ((L.gemm != 0 && L.gemm != 3) || !use_mfma(L, g)) return false;
   constexpr int KT = kWideK * 4 / int(sizeof(T));
   return gemm_tiles(g) >= L.num_cu / 4 || g.K <= KT;
 }
@@ -1019,9 +1202,108 @@ static hipError_t launch_wide(const Launch &L, const GemmArgs<T> &g) {
   return hipGetLastError();
 }
 
+// The panel kernel: automatic path selection (MPCX_GEMM=auto), operands whose
+// rows and columns are whole 16-byte groups at 16-byte aligned addresses,
+// matrices below 2 GiB per batch entry, and either K within one step or enough
+// workgroups for half the CUs at 16 columns; a long K over few tiles (the fully
+// connected layers: 22 rows, K = 312..1024) goes to the split-K tiled kernel.
+// Workgroups of 3 waves (48 rows: a 140-row product as 48 + 48 + 44) for short
+// matrices, else 4; in Z_2^32 32 columns per workgroup when that still gives a
+// workgroup per CU, else 16 (Z_2^64: 16).
+template <typename T>
+static bool pan_vec(const T *p, size_t stride, int batch) {
+  constexpr int wpg = 16 / int(sizeof(T));
+  return aligned16(p) && (batch == 1 || stride % wpg == 0);
+}
+template <typename T>
+static int pan_rw(int M) {
+  return M <= 160 ? 3 : 4;
+}
+template <typename T>
+static bool use_panels(const Launch &L, const PanelArgs<T> &r) {
+  // Z_2^32 only: in Z_2^64 the eight-shift products measured slower here than
+  // on the wide-K and fused kernels (GEMM time per bw=64 forward 0.99 against
+  // 0.78 ms)
+  if (sizeof(T) != 4 || L.gemm != 0 || r.M <= 0 || r.N <= 0 || r.K <= 0 || r.batch <= 0) return false;
+  constexpr int wpg = 16 / int(sizeof(T)), KT = kPanKPW * 4 / int(sizeof(T));
+  bool ok = r.K % wpg == 0 && r.N % wpg == 0 && size_t(r.M) * r.K * sizeof(T) < size_t(kPanOob) &&
+            size_t(r.K) * r.N * sizeof(T) < size_t(kPanOob);
+  for (int p = 0; p < r.np; p++)
+    ok = ok && pan_vec(r.a1[p], r.sA, r.batch) && pan_vec(r.a2[p], r.sA, r.batch) &&
+         pan_vec(r.b1[p], r.sB, r.batch) && pan_vec(r.b2[p], r.sB, r.batch) &&
+         (p == 0 || (!r.a2[p] && !r.b2[p]));  // masks on the first panel only
+  const int rw = pan_rw<T>(r.M);
+  const size_t wgs = size_t((r.N + 15) / 16) * ((r.M + 16 * rw - 1) / (16 * rw)) * r.batch;
+  return ok && (r.K <= KT || wgs >= size_t(L.num_cu / 2));
+}
+template <typename T, int NP, int RW, int NT>
+static hipError_t launch_panels_v(const Launch &L, const PanelArgs<T> &r) {
+  const size_t wgs = size_t((r.N + 16 * NT - 1) / (16 * NT)) * size_t((r.M + 16 * RW - 1) / (16 * RW)) * r.batch;
+  if (wgs > size_t(INT32_MAX)) return hipErrorInvalidValue;  // one-dimensional, XCD-ordered launch
+  hipLaunchKernelGGL((k_panels<T, NP, RW, NT>), dim3(unsigned(wgs)), dim3(64 * RW), 0, L.stream, r);
+  return hipGetLastError();
+}
+template <typename T, int NP>
+static hipError_t launch_panels_np(const Launch &L, const PanelArgs<T> &r) {
+  const int rw = pan_rw<T>(r.M);
+  const size_t groups = size_t((r.M + 16 * rw - 1) / (16 * rw)) * r.batch;
+  if constexpr (sizeof(T) == 4) {
+    if (size_t((r.N + 31) / 32) * groups >= size_t(L.num_cu))
+      return rw == 3 ? launch_panels_v<T, NP, 3, 2>(L, r) : launch_panels_v<T, NP, 4, 2>(L, r);
+  }
+  return rw == 3 ? launch_panels_v<T, NP, 3, 1>(L, r) : launch_panels_v<T, NP, 4, 1>(L, r);
+}
+template <typename T>
+static hipError_t launch_panels(const Launch &L, const PanelArgs<T> &r) {
+  if constexpr (sizeof(T) != 4) {
+    return hipErrorInvalidValue;  // use_panels refuses Z_2^64
+  } else {
+    switch (r.np) {
+      case 1: return launch_panels_np<T, 1>(L, r);
+      case 2: return launch_panels_np<T, 2>(L, r);
+      case 3: return launch_panels_np<T, 3>(L, r);
+      default: return hipErrorInvalidValue;
+    }
+  }
+}
+// GemmArgs as panels: (A1 - A2)(B1 - B2), then A1b B1b, both with g.sign
+template <typename T>
+static void panels_add(PanelArgs<T> &r, const GemmArgs<T> &g) {
+  r.a1[r.np] = g.A1;
+  r.a2[r.np] = g.A2;
+  r.b1[r.np] = g.B1;
+  r.b2[r.np] = g.B2;
+  r.sign[r.np++] = g.sign;
+  if (g.A1b) {
+    r.a1[r.np] = g.A1b;
+    r.b1[r.np] = g.B1b;
+    r.sign[r.np++] = g.sign;
+  }
+}
+template <typename T>
+static PanelArgs<T> panels_of(const GemmArgs<T> &g) {
+  PanelArgs<T> r;
+  r.M = g.M;
+  r.N = g.N;
+  r.K = g.K;
+  r.batch = g.batch;
+  r.np = 0;
+  r.sA = g.sA;
+  r.sB = g.sB;
+  r.sC = g.sC;
+  r.cin0 = g.Cin;
+  r.C = g.C;
+  panels_add(r, g);
+  return r;
+}
+
 template <typename T>
 hipError_t launch_gemm(const Launch &L, const GemmArgs<T> &g0) {
   if (g0.M <= 0 || g0.N <= 0 || g0.batch <= 0) return hipSuccess;
+  {
+    const PanelArgs<T> r = panels_of(g0);
+    if (use_panels(L, r)) return launch_panels<T>(L, r);
+  }
   if (use_wide(L, g0)) return launch_wide<T>(L, g0);
   const bool mfma = use_mfma(L, g0);
   if (g0.A1b && !mfma) {
@@ -1071,7 +1353,7 @@ hipError_t launch_gemm_pair(const Launch &L, const GemmArgs<T> &p0, const GemmAr
 // strides; enough tiles for a quarter of the CUs or K within one phase.
 template <typename T>
 static bool use_sxs_fused(const Launch &L, const GemmArgs<T> &g0, const GemmArgs<T> &g1) {
-  if (L.gemm != 0 || !use_mfma(L, g0) || !use_mfma(L, g1)) return false;
+  if ((L.gemm != 0 && L.gemm != 3) || !use_mfma(L, g0) || !use_mfma(L, g1)) return false;
   const bool form = g0.A2 && g0.B2 && !g0.A1b && g0.sign == 1 && g1.A1 == g0.A1 && g1.B1b == g0.B1 && g1.A1b &&
                     g1.B1 && !g1.A2 && !g1.B2 && g1.sign == -1;
   const bool shape = g0.M == g1.M && g0.N == g1.N && g0.K == g1.K && g0.batch == g1.batch && g0.sA == g1.sA &&
@@ -1083,6 +1365,15 @@ static bool use_sxs_fused(const Launch &L, const GemmArgs<T> &g0, const GemmArgs
 template <typename T>
 hipError_t launch_gemm_pair_sum(const Launch &L, const GemmArgs<T> &g0, const GemmArgs<T> &g1, T *out) {
   if (g0.M <= 0 || g0.N <= 0 || g0.batch <= 0) return hipSuccess;
+  const bool same = g0.M == g1.M && g0.N == g1.N && g0.K == g1.K && g0.batch == g1.batch && g0.sA == g1.sA &&
+                    g0.sB == g1.sB && g0.sC == size_t(g0.M) * g0.N && g1.sC == g0.sC;
+  if (same && (g0.A1b ? 2 : 1) + (g1.A1b ? 2 : 1) <= 3) {  // both parties' products and the sum in one launch
+    PanelArgs<T> r = panels_of(g0);
+    panels_add(r, g1);
+    r.cin1 = g1.Cin;
+    r.C = out;
+    if (use_panels(L, r)) return launch_panels<T>(L, r);
+  }
   if (use_sxs_fused(L, g0, g1)) {
     GemmArgs<T> a = g0;
     a.C = out;

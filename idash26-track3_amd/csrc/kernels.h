@@ -23,9 +23,11 @@ struct Launch {
   // Launches of a profiled forward use a separately named instantiation of the
   // DCF-evaluation kernel (same code), so kernel traces can tell them apart.
   bool profiled = false;
-  // ring GEMM path: 0 = int8 matrix cores, the wide-K kernel where it applies
-  // (use_wide) and the tiled kernels elsewhere; 1 = VALU; 2 = tiled matrix-core
-  // kernels only.  Z_2^64 products with K >= 2^15 take the VALU path always.
+  // ring GEMM path: 0 = int8 matrix cores, in Z_2^32 the panel kernel where it
+  // applies (use_panels), else the wide-K / fused SxS kernels where they apply
+  // and the tiled kernels elsewhere; 3 = the same without the panel kernel;
+  // 1 = VALU; 2 = tiled matrix-core kernels only.  Z_2^64 products with
+  // K >= 2^15 take the VALU path always.
   int gemm = 0;
   // model forwards with resident keys are captured once per batch size into a
   // HIP graph and replayed (0 = enqueue every kernel each time)

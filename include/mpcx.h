@@ -74,11 +74,12 @@ typedef struct mpcx_model mpcx_model;
  * (gpu_mpc/ddg_orca_base.h:93-116, 338-355): one context serves both parties. */
 /* Environment read by mpcx_create: MPCX_AES_VARIANT and MPCX_AES_BLOCK (as
  * mpcx_set_aes_variant; bad values are ignored with a warning); MPCX_GEMM = auto
- * (default: the fused SxS and wide-K matrix-core kernels where they apply, the
- * tiled matrix-core kernels elsewhere), tiled (the tiled matrix-core kernels
- * only) or valu (the VALU kernels); MPCX_GRAPH = 0 (model forwards enqueue every
- * kernel instead of replaying a captured HIP graph).  All paths give the same
- * results bit for bit. */
+ * (default: in Z_2^32 the panel kernel where it applies, else the fused SxS and
+ * wide-K matrix-core kernels where they apply, the tiled matrix-core kernels
+ * elsewhere), wide (the same without the panel kernel), tiled (the tiled
+ * matrix-core kernels only) or valu (the VALU kernels); MPCX_GRAPH = 0 (model
+ * forwards enqueue every kernel instead of replaying a captured HIP graph).  All
+ * paths give the same results bit for bit. */
 mpcx_status mpcx_create(int bw, int scale, int device, mpcx_ctx **out);
 void mpcx_destroy(mpcx_ctx *ctx);
 const char *mpcx_last_error(const mpcx_ctx *ctx);
