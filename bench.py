@@ -49,8 +49,8 @@ GEMM_PEAK_TMACS = {"mfma32": 5.0e3 / 2 / 16, "mfma64": 5.0e3 / 2 / 64, "valu": V
 # when the current sources or workload have no measurement.  Each entry names
 # the profile summary under profiles/ that it comes from.
 TRAFFIC_MEASURED = {
-    ("af8a46ee155a", "perm64_b512", 64, 32, 3, 0): {
-        "bytes_per_launch": 61436085, "profile": "profiles/k_tr_eval_affinity_bw32_B64.md"},
+    ("fcb35472d9aa", "perm32x2_b512", 64, 32, 3, 0): {
+        "bytes_per_launch": 61381563, "profile": "profiles/k_tr_eval_affinity_bw32_B64.md"},
 }
 KERNEL_SOURCES = ("csrc/kernels.hip", "csrc/kernels.h", "csrc/dcf_dev.h", "csrc/aes_dev.h", "csrc/mpcx_core.h")
 SLACK_DESC = {1: ", GCN products H.W^T truncated with the slack gate",

@@ -10,6 +10,9 @@
       counter scaled by what it reads for a plain copy of known size (the
       calibration runs: --cal-kernel, default the elementwise add of
       `bench.py --workload copy`, which reads and writes --cal-bytes, default 1 GiB)
+  rocprof_summary.py shapes <prefix>_kernel_trace.csv [--top N]
+      markdown table per kernel and launch shape (grid size in work-items along
+      x): launches and average duration, largest total first
   rocprof_summary.py counters C.csv --kernel SUBSTRING [--per-wave]
       one row per dispatch of those kernels: its duration in the counter run and
       every counter of the run (divided by SQ_WAVES with --per-wave)
@@ -35,6 +38,21 @@ def stats(path, top):
         name = r["Name"] if len(r["Name"]) < 100 else r["Name"][:97] + "..."
         print(f"| `{name}` | {r['Calls']} | {float(r['TotalDurationNs']) / 1e6:.3f} | "
               f"{float(r['AverageNs']) / 1e3:.2f} | {float(r['Percentage']):.2f} |")
+
+
+def shapes(path, top):
+    agg = {}
+    for r in _rows(path):
+        name = r["Kernel_Name"]
+        name = name[5:] if name.startswith("void ") else name
+        name = name.split("(")[0] if "mpcx::" in name else name[:60]
+        key = (name.replace("mpcx::", ""), int(r["Grid_Size_X"]))
+        n, t = agg.get(key, (0, 0.0))
+        agg[key] = (n + 1, t + (int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3)
+    print("| Kernel | grid x | launches | avg us |")
+    print("|---|---|---|---|")
+    for (name, gx), (n, t) in sorted(agg.items(), key=lambda kv: -kv[1][1])[:top]:
+        print(f"| `{name}` | {gx} | {n} | {t / n:.1f} |")
 
 
 def _values(path, counter, sub):
@@ -117,9 +135,14 @@ def main():
     c.add_argument("csv")
     c.add_argument("--kernel", required=True)
     c.add_argument("--per-wave", action="store_true")
+    h = sp.add_parser("shapes")
+    h.add_argument("csv")
+    h.add_argument("--top", type=int, default=15)
     a = ap.parse_args()
     if a.cmd == "stats":
         stats(a.csv, a.top)
+    elif a.cmd == "shapes":
+        shapes(a.csv, a.top)
     elif a.cmd == "counters":
         counters(a)
     else:
