@@ -278,6 +278,7 @@ struct TrArgs {
   const T *in_mask;
   T *out_mask;
   uint32_t gate;
+  int prio;  // eval: the launch's waves raise their issue priority (a small gate)
 };
 
 __device__ __forceinline__ bool relu_like(int kind) {
@@ -364,6 +365,7 @@ constexpr int kTrMaxTile = 512;  // elements per tile (workgroups of up to 1024 
 
 template <typename T, int NT, int REP, int TAG>
 __global__ void k_tr_eval(TrArgs<T> a) {
+  if (a.prio) __builtin_amdgcn_s_setprio(2);
   __shared__ __align__(16) uint32_t lds[AesLds<NT, REP>::kWords];
   __shared__ uint64_t xa[2][kTrMaxTile / 64], xb[2][kTrMaxTile / 64];
   __shared__ T xm[2][kTrMaxTile];
@@ -594,6 +596,11 @@ hipError_t launch_tr_keygen(const Launch &L, const TrLayout &lay, uint64_t seed,
 // against 3.11 G DCF evals/s on 2^24 ReLUs, while the model's launches (up to
 // 10^6 elements) and the adjacency normalisation's (3.4 * 10^6) lose 6-10% at
 // 1024 and keep 512.
+// A gate evaluation of fewer elements than this is latency-bound (a few
+// thousand wavefronts of one dependent AES chain each) and sits on its lane's
+// critical path while other lanes' large gates fill the GPU: its waves take the
+// SIMDs' issue slots first.
+constexpr size_t kTrPrioN = size_t(1) << 17;
 static int tr_eval_block(const Launch &L, size_t n) {
   const int b = variant_block(L);
   return (L.aes_block == 0 && b == 512 && n >= (size_t(1) << 22)) ? 1024 : b;
@@ -610,6 +617,7 @@ hipError_t launch_tr_eval(const Launch &L, const TrLayout &lay, const uint8_t *k
   a.bias = bias;
   a.bias_ncol = bias_ncol > 0 ? bias_ncol : 1;
   a.out = out;
+  a.prio = lay.N < kTrPrioN;
   return with_variant(L, [&](auto v) {
     constexpr int NT = decltype(v)::nt, REP = decltype(v)::rep;
     const int block = tr_eval_block(L, lay.N);
