@@ -38,7 +38,7 @@ HBM_PEAK_GBS = 8000.0
 GEMM_PEAK_TMACS = {"mfma32": 5.0e3 / 2 / 16, "mfma64": 5.0e3 / 2 / 64, "valu": VALU_PEAK_TOPS / 2}
 # VALU instructions per AES call of the DCF walk (one tree level: the unrolled
 # cipher, sigma, feed-forward and the level update), counted in the gfx950 ISA
-# of this build: hipcc --cuda-device-only -S csrc/kernels.hip, level-loop block
+# of this build: hipcc --cuda-device-only -S csrc/gates.hip, level-loop block
 # of k_tr_eval<uint32_t, NT, REP> for each LDS table variant.
 # HBM bytes per k_tr_eval launch, measured with rocprofv3 --pmc FETCH_SIZE and
 # WRITE_SIZE (one run each) on this bench command, mean over the launches of the
@@ -52,7 +52,8 @@ TRAFFIC_MEASURED = {
     ("fcb35472d9aa", "perm32x2_b512", 64, 32, 3, 0): {
         "bytes_per_launch": 61381563, "profile": "profiles/k_tr_eval_affinity_bw32_B64.md"},
 }
-KERNEL_SOURCES = ("csrc/kernels.hip", "csrc/kernels.h", "csrc/dcf_dev.h", "csrc/aes_dev.h", "csrc/mpcx_core.h")
+KERNEL_SOURCES = ("csrc/gates.hip", "csrc/launch_util.h", "csrc/kernels.h", "csrc/dcf_dev.h", "csrc/aes_dev.h",
+                  "csrc/mpcx_core.h")
 SLACK_DESC = {1: ", GCN products H.W^T truncated with the slack gate",
               2: ", GCN products and aggregations truncated with the slack gate",
               3: ", every layer truncation local (LocalARS, the reference's default truncation; not bit-exact)"}

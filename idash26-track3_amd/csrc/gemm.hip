@@ -11,18 +11,10 @@
 #include <type_traits>
 
 #include "gemm.h"
+#include "launch_util.h"
 
 namespace mpcx {
 
-template <typename K>
-static int grid_for(K kernel, int block, size_t n, int num_cu) {
-  int occ = 0;
-  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ, kernel, block, 0) != hipSuccess || occ < 1) occ = 1;
-  size_t need = (n + block - 1) / block;
-  size_t cap = size_t(occ) * size_t(num_cu);
-  size_t g = need < cap ? need : cap;
-  return int(g < 1 ? 1 : g);
-}
 // ---------------------------------------------------------------------------
 // ring GEMM: 64x64 tile per 256-thread block, 4x4 outputs per thread,
 // K staged through LDS in slices of 16.  Integer multiply-add on the VALU

@@ -1,19 +1,12 @@
-// kernels.hip -- HIP kernels of the secure-inference online path for gfx950.
+// kernels.hip -- HIP kernels of the secure-inference online path for gfx950
+// (the truncation / ReLU gate family is in gates.hip, the ring GEMMs in gemm.hip).
 //
 // Reference interfaces these kernels stand behind (EzPC GPU-MPC, called from the
 // reference's backend; signatures reconstructed from the call sites):
 //   DCF eval / keygen ........ gpuDcf / gpuKeyGenDCF    (gpu_mpc/dpf_dcf_adapter.h:266,372)
-//   ReLU ..................... gpuRelu / gpuGenReluKey   (gpu_mpc/ddg_orca.h:103-104,233)
-//   exact truncation ......... gpuTruncate / genGPUTruncateKey (gpu_mpc/ddg_orca.h:116-118,240)
 //   Beaver product ........... gpuMul / gpuKeygenMul    (gpu_mpc/secure_adj_norm.h:611-651,326-365)
 //   8-bit DPF LUT ............ gpuDpfLUT / gpuKeyGenLUT (gpu_mpc/secure_adj_norm.h:510-520,270-279)
-//   ring GEMM ................ gpuMatmul / gpuKeygenMatmul (gpu_mpc/ddg_orca_base.h:170-271,394-469)
 //   reveal ................... reconstructInPlace       (gpu_mpc/utils/gpu_comms.h:290-302)
-// Gate algebra (masked-public x^ = x + r): the truncation family evaluates two DCFs on
-// x' = x^ + bias*2^s + 2^(n-1), c = [x' mod 2^(n-1) < r mod 2^(n-1)] and
-// d = [x' mod 2^s < r mod 2^s], then floor(u/2^s) = floor(x'/2^s) - floor(r/2^s) - d
-// + 2^(n-s)*w with the wrap w = msb(x') ? (msb(r) & c) : (msb(r) | c); the dealer
-// tabulates all but the public floor(x'/2^s) over the 8 public cases.
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
@@ -21,6 +14,7 @@
 
 #include "dcf_dev.h"
 #include "kernels.h"
+#include "launch_util.h"
 
 namespace mpcx {
 
@@ -38,57 +32,6 @@ static const AesVariant kVariants[] = {
 const AesVariant *aes_variants(int *count) {
   *count = int(sizeof(kVariants) / sizeof(kVariants[0]));
   return kVariants;
-}
-
-template <int NT, int REP>
-struct V {
-  static constexpr int nt = NT, rep = REP;
-};
-
-template <class Fn>
-static hipError_t with_variant(const Launch &L, Fn &&fn) {
-  switch (L.aes_variant) {
-    case 0: return fn(V<2, 32>{});
-    case 1: return fn(V<0, 64>{});
-    case 2: return fn(V<0, 64>{});
-    case 3: return fn(V<4, 32>{});
-    default: return hipErrorInvalidValue;
-  }
-}
-// Rows of workgroups of a two-party kernel (blockIdx.y + party_base = party):
-// both parties, or only L.party in party mode.
-static unsigned party_rows(const Launch &L) { return L.party < 0 ? 2u : 1u; }
-static int party_base(const Launch &L) { return L.party < 0 ? 0 : L.party; }
-static int variant_block(const Launch &L) {
-  if (L.aes_block > 0) return L.aes_block;
-  int n;
-  const AesVariant *v = aes_variants(&n);
-  return (L.aes_variant >= 0 && L.aes_variant < n) ? v[L.aes_variant].block : 256;
-}
-
-template <typename K>
-static int grid_for(K kernel, int block, size_t n, int num_cu) {
-  int occ = 0;
-  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ, kernel, block, 0) != hipSuccess || occ < 1) occ = 1;
-  size_t need = (n + block - 1) / block;
-  size_t cap = size_t(occ) * size_t(num_cu);
-  size_t g = need < cap ? need : cap;
-  return int(g < 1 ? 1 : g);
-}
-
-
-__device__ __forceinline__ uint32_t lane_id() { return threadIdx.x & 63u; }
-
-template <typename T>
-__device__ __forceinline__ T ring_of(uint4 b) {
-  if constexpr (sizeof(T) == 4)
-    return T(b.x);
-  else
-    return T(uint64_t(b.x) | (uint64_t(b.y) << 32));
-}
-
-__device__ __forceinline__ uint32_t get_bit(const uint64_t *plane, size_t i) {
-  return uint32_t(plane[i >> 6] >> (i & 63)) & 1u;
 }
 
 // ---------------------------------------------------------------------------
@@ -248,480 +191,6 @@ hipError_t launch_dcf_eval(const Launch &L, int party, int m, size_t n, const ui
     int block = variant_block(L);
     int grid = grid_for(k_dcf_eval<NT, REP>, block, n, L.num_cu);
     hipLaunchKernelGGL((k_dcf_eval<NT, REP>), dim3(grid), dim3(block), 0, L.stream, a);
-    return hipGetLastError();
-  });
-}
-
-// ---------------------------------------------------------------------------
-// truncation / ReLU family
-// ---------------------------------------------------------------------------
-template <typename T>
-struct TrArgs {
-  AesRK kd;
-  AesRK kp[2];  // the parties' own PRF keys (keygen and seeded-plane expansion)
-  int kind, n, s;
-  int sb;        // sign bit of the shifted input (tr_sign_bit)
-  int m, sh;     // input width (tr_in_bits) and the gate's own shift (tr_shift)
-  int ncase;     // cases of the G table
-  int relu;      // the gate carries kappa shares
-  int has_bias;  // the bias is added before the shift
-  size_t N;
-  const uint8_t *k0, *k1;
-  uint8_t *w0, *w1;  // writable keys (keygen)
-  DcfLayout a, b;
-  size_t off_kappa, off_g;
-  int use_a, use_b;
-  const T *xhat;
-  const T *bias;
-  int bias_ncol;
-  T *out;  // revealed output (eval)
-  const T *in_mask;
-  T *out_mask;
-  uint32_t gate;
-  int prio;  // eval: the launch's waves raise their issue priority (a small gate)
-};
-
-__device__ __forceinline__ bool relu_like(int kind) {
-  return kind == G_RELU || kind == G_RELUSLACK || kind == G_RELUPOOL;
-}
-
-// v mod 2^m for 1 <= m <= bits of T
-template <typename T>
-__device__ __forceinline__ T low_bits(T v, int m) {
-  return m >= int(8 * sizeof(T)) ? v : T(v & ((T(1) << m) - T(1)));
-}
-
-template <typename T>
-__device__ __forceinline__ T tr_shifted_input(const TrArgs<T> &a, size_t i) {
-  T x = a.xhat[i];
-  if (a.has_bias && a.bias) x += T(a.bias[uint32_t(i % uint32_t(a.bias_ncol))]) << a.s;
-  return low_bits<T>(x + (T(1) << a.sb), a.m);
-}
-
-// Party p's masked DCF output bits of element i (the gate's planes a and b):
-// the DCF walks over the shifted input xp with the party's roots and mask bits
-// (K) and the correction and leaf words, which are the same in both parties'
-// keys (KC: any party's copy).
-template <typename T, class Aes>
-__device__ __forceinline__ void tr_dcf_bits(Aes &aes, const TrArgs<T> &a, const uint8_t *K,
-                                            const uint8_t *KC, size_t i, T xp, uint32_t *ra, uint32_t *rb) {
-  const T lowmask = (T(1) << a.sb) - T(1);
-  const T smask = (T(1) << a.s) - T(1);
-  if (a.use_a) {
-    *ra = dcf_eval_walk(aes, reinterpret_cast<const uint4 *>(K + a.a.off_root)[i], a.a.m, a.a.L,
-                        reinterpret_cast<const uint4 *>(KC + a.a.off_cw) + i, a.N,
-                        reinterpret_cast<const uint4 *>(KC + a.a.off_leaf)[i], uint64_t(xp & lowmask));
-    *ra ^= get_bit(reinterpret_cast<const uint64_t *>(K + a.a.off_z), i);
-  }
-  if (a.use_b) {
-    *rb = dcf_eval_walk(aes, reinterpret_cast<const uint4 *>(K + a.b.off_root)[i], a.b.m, a.b.L,
-                        reinterpret_cast<const uint4 *>(KC + a.b.off_cw) + i, a.N,
-                        reinterpret_cast<const uint4 *>(KC + a.b.off_leaf)[i], uint64_t(xp & smask));
-    *rb ^= get_bit(reinterpret_cast<const uint64_t *>(K + a.b.off_z), i);
-  }
-}
-
-// Party p's output message for element i once the masked DCF outputs are
-// public: hb the sign-position bit of the shifted input, bh and dh the
-// reconstructed masked bits of planes a and b.  The two parties' messages add
-// up to the masked output.
-template <typename T>
-__device__ __forceinline__ T tr_out_share(const TrArgs<T> &a, int p, const uint8_t *K, size_t i, T xp, uint32_t hb,
-                                          uint32_t bh, uint32_t dh) {
-  const T *G = reinterpret_cast<const T *>(K + a.off_g);
-  const T *kap = reinterpret_cast<const T *>(K + a.off_kappa);
-  const T one0 = p == 0 ? T(1) : T(0);
-  const T A = (xp >> a.sh) - (T(1) << (a.m - 1 - a.sh));
-  if (a.kind == G_TRMOD) return one0 * A + G[size_t(dh) * a.N + i];  // exact modulo 2^(n-s): no wrap term
-  if (a.kind == G_EXT) return one0 * A + G[size_t(hb * 2 + bh) * a.N + i];
-  if (a.kind == G_EXTRELU || a.kind == G_TRRELU) {
-    const uint32_t z = hb ^ bh;
-    const T k = kap[i];
-    const T cp = z ? T(one0 - k) : k;
-    const size_t c = a.kind == G_EXTRELU ? hb * 2 + bh : hb * 4 + bh * 2 + dh;
-    return cp * A + G[c * a.N + i];
-  }
-  if (a.kind == G_TR) return one0 * A + G[size_t(hb * 4 + bh * 2 + dh) * a.N + i];
-  if (a.kind == G_DRELU) return one0 * T(hb ^ bh);  // the public masked bit; party 0 carries it
-  if (relu_like(a.kind)) {
-    const uint32_t z = hb ^ bh;
-    const T k = kap[i];
-    const T cp = z ? T(one0 - k) : k;
-    return cp * a.xhat[i] + G[size_t(z) * a.N + i];
-  }
-  // G_TRSLACK
-  const uint32_t Hh = uint32_t(xp >> (a.n - 2)) & 3u;
-  return one0 * A + G[size_t(Hh * 2 + dh) * a.N + i];
-}
-
-// One launch evaluates a gate for both parties.  A workgroup of 2h threads
-// takes tiles of h elements: its first h threads are party 0, the last h party
-// 1, each evaluating its own keys on the same elements.  The two exchanges of
-// the protocol go through LDS: the masked DCF output bits (one ballot word per
-// wave and DCF), then the output messages, which party 0's threads add into the
-// revealed output.  TAG = 1 marks the launches of a profiled forward (identical
-// code, its own name in kernel traces).
-constexpr int kTrMaxTile = 512;  // elements per tile (workgroups of up to 1024 threads)
-
-template <typename T, int NT, int REP, int TAG>
-__global__ void k_tr_eval(TrArgs<T> a) {
-  if (a.prio) __builtin_amdgcn_s_setprio(2);
-  __shared__ __align__(16) uint32_t lds[AesLds<NT, REP>::kWords];
-  __shared__ uint64_t xa[2][kTrMaxTile / 64], xb[2][kTrMaxTile / 64];
-  __shared__ T xm[2][kTrMaxTile];
-  AesLds<NT, REP>::fill(lds);
-  AesLds<NT, REP> aes(lds);
-  const int h = int(blockDim.x) / 2;
-  const int p = int(threadIdx.x) >= h ? 1 : 0;
-  const int e = int(threadIdx.x) - p * h;  // element of the tile
-  const int wv = e >> 6;                   // wave of the party's half
-  const uint8_t *K = p ? a.k1 : a.k0;
-  // The correction words and leaf words of a DCF key are the same for both
-  // parties (public to both); both parties read party 0's planes, so one copy
-  // serves the two evaluations (and a streamed arena moves it once).
-  const uint8_t *KC = a.k0;
-  const size_t stride = size_t(gridDim.x) * size_t(h);
-  for (size_t base = size_t(blockIdx.x) * h; base < a.N; base += stride) {
-    const size_t i = base + size_t(e);
-    const bool in = i < a.N;
-    uint32_t ra = 0, rb = 0;
-    T xp = 0;
-    if (in) {
-      xp = tr_shifted_input(a, i);
-      tr_dcf_bits(aes, a, K, KC, i, xp, &ra, &rb);
-    }
-    // exchange 1: the masked DCF output bits
-    const uint64_t wa = __ballot(ra), wb = __ballot(rb);
-    if (lane_id() == 0) {
-      xa[p][wv] = wa;
-      xb[p][wv] = wb;
-    }
-    __syncthreads();
-    if (in) {
-      const uint32_t hb = uint32_t(xp >> a.sb) & 1u;
-      const uint32_t bh = a.use_a ? uint32_t((xa[0][wv] ^ xa[1][wv]) >> lane_id()) & 1u : 0u;
-      const uint32_t dh = a.use_b ? uint32_t((xb[0][wv] ^ xb[1][wv]) >> lane_id()) & 1u : 0u;
-      xm[p][e] = tr_out_share(a, p, K, i, xp, hb, bh, dh);  // exchange 2: the output messages
-    }
-    __syncthreads();
-    if (p == 0 && in) a.out[i] = xm[0][e] + xm[1][e];
-    __syncthreads();  // the next tile reuses the exchange buffers
-  }
-}
-
-// Party mode, phase 1: party p's masked DCF output bits (one ballot word per
-// wave and plane).  a.k0 = a.k1 = the party's own key.
-template <typename T, int NT, int REP>
-__global__ void k_tr_party_bits(TrArgs<T> a, uint64_t *bits) {
-  __shared__ __align__(16) uint32_t lds[AesLds<NT, REP>::kWords];
-  AesLds<NT, REP>::fill(lds);
-  AesLds<NT, REP> aes(lds);
-  const size_t W = (a.N + 63) / 64;
-  const size_t stride = size_t(gridDim.x) * blockDim.x;
-  for (size_t base = size_t(blockIdx.x) * blockDim.x + (threadIdx.x & ~63u); base < a.N; base += stride) {
-    const size_t i = base + lane_id();
-    uint32_t ra = 0, rb = 0;
-    if (i < a.N) tr_dcf_bits(aes, a, a.k0, a.k0, i, tr_shifted_input(a, i), &ra, &rb);
-    const uint64_t wa = __ballot(ra), wb = __ballot(rb);
-    if (lane_id() == 0) {
-      if (a.use_a) bits[base >> 6] = wa;
-      if (a.use_b) bits[W + (base >> 6)] = wb;
-    }
-  }
-}
-
-// Party mode, phase 2: party p's output message from the reconstructed bits
-// (own XOR peer); for G_DRELU the public output bit itself.
-template <typename T>
-__global__ void k_tr_party_msg(TrArgs<T> a, int p, const uint64_t *own, const uint64_t *peer, T *msg) {
-  const size_t W = (a.N + 63) / 64;
-  for (size_t i = size_t(blockIdx.x) * blockDim.x + threadIdx.x; i < a.N; i += size_t(gridDim.x) * blockDim.x) {
-    const T xp = tr_shifted_input(a, i);
-    const size_t w = i >> 6;
-    const uint32_t sh = uint32_t(i & 63u);
-    const uint32_t hb = uint32_t(xp >> a.sb) & 1u;
-    const uint32_t bh = a.use_a ? uint32_t((own[w] ^ peer[w]) >> sh) & 1u : 0u;
-    const uint32_t dh = a.use_b ? uint32_t((own[W + w] ^ peer[W + w]) >> sh) & 1u : 0u;
-    msg[i] = a.kind == G_DRELU ? T(hb ^ bh) : tr_out_share(a, p, a.k0, i, xp, hb, bh, dh);
-  }
-}
-
-template <typename T, int NT, int REP>
-__global__ void k_tr_keygen(TrArgs<T> a) {
-  __shared__ __align__(16) uint32_t lds[AesLds<NT, REP>::kWords];
-  AesLds<NT, REP>::fill(lds);
-  AesLds<NT, REP> aes(lds);
-  const size_t stride = size_t(gridDim.x) * blockDim.x;
-  const int n = a.n, s = a.s;
-  const T lowmask = (T(1) << a.sb) - T(1);
-  const T smask = (T(1) << s) - T(1);
-  const int wsh = a.m - a.sh;  // weight of the wrap bit after the shift
-  T *G0 = reinterpret_cast<T *>(a.w0 + a.off_g);
-  T *G1 = reinterpret_cast<T *>(a.w1 + a.off_g);
-  const int ncase = a.ncase;
-  for (size_t base = size_t(blockIdx.x) * blockDim.x + (threadIdx.x & ~63u); base < a.N; base += stride) {
-    const size_t i = base + lane_id();
-    uint32_t za0 = 0, za1 = 0, zb0 = 0, zb1 = 0;
-    if (i < a.N) {
-      const T r = low_bits<T>(a.in_mask[i], a.m);
-      const uint32_t rho = uint32_t(r >> a.sb) & 1u;
-      const T R = r >> a.sh;
-      // each party's output-mask bit of a DCF comes from its own PRF key; the
-      // DCF output mask is their XOR
-      if (a.use_a) {
-        za0 = aes.prf(a.kp[0], a.gate, F_DCFA + 2, i).x & 1u;
-        za1 = aes.prf(a.kp[1], a.gate, F_DCFA + 2, i).x & 1u;
-      }
-      if (a.use_b) {
-        zb0 = aes.prf(a.kp[0], a.gate, F_DCFB + 2, i).x & 1u;
-        zb1 = aes.prf(a.kp[1], a.gate, F_DCFB + 2, i).x & 1u;
-      }
-      const uint32_t rbi = za0 ^ za1, rdi = zb0 ^ zb1;
-      const T rout = ring_of<T>(aes.prf(a.kd, a.gate, F_ROUT, i));
-      const uint32_t kappa = rho ^ rbi;
-      a.out_mask[i] = a.kind == G_DRELU ? T(kappa) : rout;  // DRELU: the mask of the output bit
-      for (int c = 0; c < ncase; c++) {
-        T Gv;
-        if (a.kind == G_TRMOD) {
-          Gv = rout - R - T(uint32_t(c) ^ rdi);
-        } else if (a.kind == G_EXT || a.kind == G_EXTRELU) {
-          const uint32_t h = uint32_t(c) >> 1, b = (uint32_t(c) & 1u) ^ rbi;
-          const uint32_t w = h ? (rho & b) : (rho | b);
-          if (a.kind == G_EXTRELU) {
-            const T cc = T(h ^ rho ^ b);
-            Gv = rout - cc * R + ((cc * T(w)) << wsh);
-          } else {
-            Gv = rout - R + (T(w) << wsh);
-          }
-        } else if (a.kind == G_TR || a.kind == G_TRRELU) {
-          const uint32_t h = uint32_t(c) >> 2, bh = (uint32_t(c) >> 1) & 1u, dh = uint32_t(c) & 1u;
-          const uint32_t b = bh ^ rbi, d = dh ^ rdi;
-          const uint32_t w = h ? (rho & b) : (rho | b);
-          if (a.kind == G_TRRELU) {
-            const T cc = T(h ^ rho ^ b);
-            Gv = rout - cc * R - cc * T(d) + ((cc * T(w)) << (n - s));
-          } else {
-            Gv = rout - R - T(d) + (T(w) << (n - s));
-          }
-        } else if (relu_like(a.kind)) {
-          const T cc = T(uint32_t(c) ^ kappa);
-          Gv = rout - cc * r;
-        } else {
-          const uint32_t Hh = uint32_t(c) >> 1, dh = uint32_t(c) & 1u;
-          const uint32_t d = dh ^ rdi;
-          const uint32_t R2 = uint32_t(r >> (n - 2)) & 3u;
-          const uint32_t w = Hh < R2 ? 1u : 0u;
-          Gv = rout - R - T(d) + (T(w) << (n - s));
-        }
-        const T g0 = ring_of<T>(aes.prf(a.kp[0], a.gate, F_SPLIT + uint32_t(c), i));
-        G0[size_t(c) * a.N + i] = g0;
-        G1[size_t(c) * a.N + i] = Gv - g0;
-      }
-      if (a.relu) {
-        const T q0 = ring_of<T>(aes.prf(a.kp[0], a.gate, F_SPLIT + 8, i));
-        reinterpret_cast<T *>(a.w0 + a.off_kappa)[i] = q0;
-        reinterpret_cast<T *>(a.w1 + a.off_kappa)[i] = T(kappa) - q0;
-      }
-      if (a.use_a)
-        dcf_gen_roots(aes, party_root(aes, a.kp[0], 0, a.gate, F_DCFA, i),
-                      party_root(aes, a.kp[1], 1, a.gate, F_DCFA, i), a.a.m, a.a.L, uint64_t(r & lowmask), i, a.N,
-                      a.w0, a.w1, a.a.off_root, a.a.off_cw, a.a.off_leaf);
-      if (a.use_b)
-        dcf_gen_roots(aes, party_root(aes, a.kp[0], 0, a.gate, F_DCFB, i),
-                      party_root(aes, a.kp[1], 1, a.gate, F_DCFB, i), a.b.m, a.b.L, uint64_t(r & smask), i, a.N,
-                      a.w0, a.w1, a.b.off_root, a.b.off_cw, a.b.off_leaf);
-    }
-    const uint64_t wa0 = __ballot(za0), wa1 = __ballot(za1), wb0 = __ballot(zb0), wb1 = __ballot(zb1);
-    if (lane_id() == 0) {
-      if (a.use_a) {
-        reinterpret_cast<uint64_t *>(a.w0 + a.a.off_z)[base >> 6] = wa0;
-        reinterpret_cast<uint64_t *>(a.w1 + a.a.off_z)[base >> 6] = wa1;
-      }
-      if (a.use_b) {
-        reinterpret_cast<uint64_t *>(a.w0 + a.b.off_z)[base >> 6] = wb0;
-        reinterpret_cast<uint64_t *>(a.w1 + a.b.off_z)[base >> 6] = wb1;
-      }
-    }
-  }
-}
-
-template <typename T>
-static TrArgs<T> tr_args(const TrLayout &lay) {
-  TrArgs<T> a{};
-  a.kind = lay.kind;
-  a.n = lay.bw;
-  a.s = lay.s;
-  a.sb = tr_sign_bit(lay.kind, lay.bw, lay.s);
-  a.m = tr_in_bits(lay.kind, lay.bw, lay.s);
-  a.sh = tr_shift(lay.kind, lay.s);
-  a.ncase = lay.ncase;
-  a.relu = lay.relu;
-  a.has_bias = tr_has_bias(lay.kind);
-  a.N = lay.N;
-  a.a = lay.a;
-  a.b = lay.b;
-  a.off_kappa = lay.off_kappa;
-  a.off_g = lay.off_g;
-  a.use_a = lay.use_a;
-  a.use_b = lay.use_b;
-  a.bias_ncol = 1;
-  return a;
-}
-
-template <typename T>
-hipError_t launch_tr_keygen(const Launch &L, const TrLayout &lay, uint64_t seed, uint32_t gate, const T *in_mask,
-                            T *out_mask, uint8_t *k0, uint8_t *k1) {
-  if (lay.bw != int(8 * sizeof(T))) return hipErrorInvalidValue;
-  TrArgs<T> a = tr_args<T>(lay);
-  a.kd = dealer_key(L, seed);
-  a.kp[0] = party_key(L, seed, 0);
-  a.kp[1] = party_key(L, seed, 1);
-  a.gate = gate;
-  a.w0 = k0;
-  a.w1 = k1;
-  a.in_mask = in_mask;
-  a.out_mask = out_mask;
-  return with_variant(L, [&](auto v) {
-    constexpr int NT = decltype(v)::nt, REP = decltype(v)::rep;
-    int block = variant_block(L);
-    int grid = grid_for(k_tr_keygen<T, NT, REP>, block, lay.N, L.num_cu);
-    hipLaunchKernelGGL((k_tr_keygen<T, NT, REP>), dim3(grid), dim3(block), 0, L.stream, a);
-    return hipGetLastError();
-  });
-}
-
-// Workgroup of a gate evaluation: the context's explicit size, else the
-// variant's; a launch of at least 2^22 elements on the default 512-thread
-// variant takes 1024 threads (one T-table per 16 waves).  Measured: 3.28
-// against 3.11 G DCF evals/s on 2^24 ReLUs, while the model's launches (up to
-// 10^6 elements) and the adjacency normalisation's (3.4 * 10^6) lose 6-10% at
-// 1024 and keep 512.
-// A gate evaluation of fewer elements than this is latency-bound (a few
-// thousand wavefronts of one dependent AES chain each) and sits on its lane's
-// critical path while other lanes' large gates fill the GPU: its waves take the
-// SIMDs' issue slots first.
-constexpr size_t kTrPrioN = size_t(1) << 17;
-static int tr_eval_block(const Launch &L, size_t n) {
-  const int b = variant_block(L);
-  return (L.aes_block == 0 && b == 512 && n >= (size_t(1) << 22)) ? 1024 : b;
-}
-
-template <typename T>
-hipError_t launch_tr_eval(const Launch &L, const TrLayout &lay, const uint8_t *k0, const uint8_t *k1, const T *xhat,
-                          const T *bias, int bias_ncol, T *out) {
-  if (lay.bw != int(8 * sizeof(T))) return hipErrorInvalidValue;
-  TrArgs<T> a = tr_args<T>(lay);
-  a.k0 = k0;
-  a.k1 = k1;
-  a.xhat = xhat;
-  a.bias = bias;
-  a.bias_ncol = bias_ncol > 0 ? bias_ncol : 1;
-  a.out = out;
-  a.prio = lay.N < kTrPrioN;
-  return with_variant(L, [&](auto v) {
-    constexpr int NT = decltype(v)::nt, REP = decltype(v)::rep;
-    const int block = tr_eval_block(L, lay.N);
-    // a workgroup holds both parties' threads for block/2 elements
-    if (block < 128 || block > 2 * kTrMaxTile || block % 128 != 0) return hipErrorInvalidConfiguration;
-    const int grid = grid_for(k_tr_eval<T, NT, REP, 0>, block, 2 * lay.N, L.num_cu);
-    if (L.profiled)
-      hipLaunchKernelGGL((k_tr_eval<T, NT, REP, 1>), dim3(grid), dim3(block), 0, L.stream, a);
-    else
-      hipLaunchKernelGGL((k_tr_eval<T, NT, REP, 0>), dim3(grid), dim3(block), 0, L.stream, a);
-    return hipGetLastError();
-  });
-}
-
-template <typename T>
-static TrArgs<T> tr_party_args(const TrLayout &lay, const uint8_t *key, const T *xhat, const T *bias,
-                               int bias_ncol) {
-  TrArgs<T> a = tr_args<T>(lay);
-  a.k0 = key;  // the party's own key in both slots
-  a.k1 = key;
-  a.xhat = xhat;
-  a.bias = bias;
-  a.bias_ncol = bias_ncol > 0 ? bias_ncol : 1;
-  return a;
-}
-
-template <typename T>
-hipError_t launch_tr_party_bits(const Launch &L, const TrLayout &lay, const uint8_t *key, const T *xhat,
-                                const T *bias, int bias_ncol, uint64_t *bits) {
-  if (lay.bw != int(8 * sizeof(T)) || L.party < 0) return hipErrorInvalidValue;
-  if (lay.N == 0) return hipSuccess;
-  const TrArgs<T> a = tr_party_args<T>(lay, key, xhat, bias, bias_ncol);
-  return with_variant(L, [&](auto v) {
-    constexpr int NT = decltype(v)::nt, REP = decltype(v)::rep;
-    const int block = variant_block(L);
-    const int grid = grid_for(k_tr_party_bits<T, NT, REP>, block, lay.N, L.num_cu);
-    hipLaunchKernelGGL((k_tr_party_bits<T, NT, REP>), dim3(grid), dim3(block), 0, L.stream, a, bits);
-    return hipGetLastError();
-  });
-}
-
-template <typename T>
-hipError_t launch_tr_party_msg(const Launch &L, const TrLayout &lay, const uint8_t *key, const T *xhat,
-                               const T *bias, int bias_ncol, const uint64_t *own, const uint64_t *peer, T *msg) {
-  if (lay.bw != int(8 * sizeof(T)) || L.party < 0) return hipErrorInvalidValue;
-  if (lay.N == 0) return hipSuccess;
-  const TrArgs<T> a = tr_party_args<T>(lay, key, xhat, bias, bias_ncol);
-  const int block = 256;
-  const int grid = grid_for(k_tr_party_msg<T>, block, lay.N, L.num_cu);
-  hipLaunchKernelGGL((k_tr_party_msg<T>), dim3(grid), dim3(block), 0, L.stream, a, L.party, own, peer, msg);
-  return hipGetLastError();
-}
-
-template <typename T, int NT, int REP>
-__global__ void k_tr_expand(TrArgs<T> a, int p) {
-  __shared__ __align__(16) uint32_t lds[AesLds<NT, REP>::kWords];
-  AesLds<NT, REP>::fill(lds);
-  AesLds<NT, REP> aes(lds);
-  const AesRK &kp = a.kp[0];
-  uint8_t *w = a.w0;
-  const size_t stride = size_t(gridDim.x) * blockDim.x;
-  const int ncase = a.ncase;
-  const bool kappa = a.relu;
-  for (size_t base = size_t(blockIdx.x) * blockDim.x + (threadIdx.x & ~63u); base < a.N; base += stride) {
-    const size_t i = base + lane_id();
-    uint32_t za = 0, zb = 0;
-    if (i < a.N) {
-      if (a.use_a) {
-        reinterpret_cast<uint4 *>(w + a.a.off_root)[i] = party_root(aes, kp, p, a.gate, F_DCFA, i);
-        za = aes.prf(kp, a.gate, F_DCFA + 2, i).x & 1u;
-      }
-      if (a.use_b) {
-        reinterpret_cast<uint4 *>(w + a.b.off_root)[i] = party_root(aes, kp, p, a.gate, F_DCFB, i);
-        zb = aes.prf(kp, a.gate, F_DCFB + 2, i).x & 1u;
-      }
-      if (p == 0) {
-        T *G0 = reinterpret_cast<T *>(w + a.off_g);
-        for (int c = 0; c < ncase; c++)
-          G0[size_t(c) * a.N + i] = ring_of<T>(aes.prf(kp, a.gate, F_SPLIT + uint32_t(c), i));
-        if (kappa) reinterpret_cast<T *>(w + a.off_kappa)[i] = ring_of<T>(aes.prf(kp, a.gate, F_SPLIT + 8, i));
-      }
-    }
-    const uint64_t wa = __ballot(za), wb = __ballot(zb);
-    if (lane_id() == 0) {
-      if (a.use_a) reinterpret_cast<uint64_t *>(w + a.a.off_z)[base >> 6] = wa;
-      if (a.use_b) reinterpret_cast<uint64_t *>(w + a.b.off_z)[base >> 6] = wb;
-    }
-  }
-}
-
-template <typename T>
-hipError_t launch_tr_expand(const Launch &L, const TrLayout &lay, const uint8_t party_key16[16], uint32_t gate,
-                            int party, uint8_t *key) {
-  if (lay.bw != int(8 * sizeof(T)) || (party != 0 && party != 1)) return hipErrorInvalidValue;
-  if (lay.N == 0 || lay.kind == G_LOCALARS) return hipSuccess;
-  TrArgs<T> a = tr_args<T>(lay);
-  a.kp[0] = aes_expand(party_key16);
-  a.gate = gate;
-  a.w0 = key;
-  return with_variant(L, [&](auto v) {
-    constexpr int NT = decltype(v)::nt, REP = decltype(v)::rep;
-    int block = variant_block(L);
-    int grid = grid_for(k_tr_expand<T, NT, REP>, block, lay.N, L.num_cu);
-    hipLaunchKernelGGL((k_tr_expand<T, NT, REP>), dim3(grid), dim3(block), 0, L.stream, a, party);
     return hipGetLastError();
   });
 }
@@ -1342,46 +811,35 @@ hipError_t launch_rowsum(const Launch &L, size_t rows, int len, const T *a, T *o
 // ---------------------------------------------------------------------------
 // explicit instantiations
 // ---------------------------------------------------------------------------
-#define INST(T)                                                                                                      \
-  template hipError_t launch_tr_keygen<T>(const Launch &, const TrLayout &, uint64_t, uint32_t, const T *, T *,      \
-                                          uint8_t *, uint8_t *);                                                     \
-  template hipError_t launch_tr_expand<T>(const Launch &, const TrLayout &, const uint8_t *, uint32_t, int,          \
-                                          uint8_t *);                                                                \
-  template hipError_t launch_tr_eval<T>(const Launch &, const TrLayout &, const uint8_t *, const uint8_t *,          \
-                                        const T *, const T *, int, T *);                                             \
-  template hipError_t launch_tr_party_bits<T>(const Launch &, const TrLayout &, const uint8_t *, const T *,         \
-                                              const T *, int, uint64_t *);                                           \
-  template hipError_t launch_tr_party_msg<T>(const Launch &, const TrLayout &, const uint8_t *, const T *,          \
-                                             const T *, int, const uint64_t *, const uint64_t *, T *);               \
-  template hipError_t launch_reconstruct<T>(const Launch &, size_t, const T *, const T *, T *);                      \
-  template hipError_t launch_local_ars<T>(const Launch &, size_t, int, const T *, const T *, int, T *);              \
-  template hipError_t launch_reveal_keygen<T>(const Launch &, const RevealLayout &, uint64_t, uint32_t, T *,         \
-                                              uint8_t *, uint8_t *);                                                 \
-  template hipError_t launch_reveal_eval<T>(const Launch &, const RevealLayout &, const uint8_t *, const uint8_t *,  \
-                                            const T *, const T *, int, T *, T *);                                    \
-  template hipError_t launch_mul_keygen<T>(const Launch &, const MulLayout &, uint64_t, uint32_t, const MulMap &,   \
-                                           const T *, const T *, T *, uint8_t *, uint8_t *);                         \
-  template hipError_t launch_mul_eval<T>(const Launch &, const MulLayout &, const uint8_t *, const uint8_t *,        \
-                                         const MulMap &, const T *, const T *, T *, T *);                            \
-  template hipError_t launch_lut8_keygen<T>(const Launch &, const Lut8Layout &, uint64_t, uint32_t, const T *, T *, \
-                                            uint8_t *, uint8_t *);                                                   \
-  template hipError_t launch_lut8_phase1<T>(const Launch &, const Lut8Layout &, const uint8_t *, const uint8_t *,    \
-                                            const T *, const T *, T *, T *);                                         \
-  template hipError_t launch_lut8_phase2<T>(const Launch &, const Lut8Layout &, const uint8_t *, const uint8_t *,    \
-                                            const T *, T *, T *);                                                    \
-  template hipError_t launch_split<T>(const Launch &, uint64_t, uint32_t, uint32_t, size_t, const T *, T *, T *,     \
-                                      T *);                                                                          \
-  template hipError_t launch_prf_ring<T>(const Launch &, uint64_t, uint32_t, uint32_t, size_t, T *);                \
-  template hipError_t launch_axpby<T>(const Launch &, size_t, T, const T *, T, const T *, T, T *);                   \
+#define INST(T)                                                                                                       \
+  template hipError_t launch_reconstruct<T>(const Launch &, size_t, const T *, const T *, T *);                       \
+  template hipError_t launch_local_ars<T>(const Launch &, size_t, int, const T *, const T *, int, T *);               \
+  template hipError_t launch_reveal_keygen<T>(const Launch &, const RevealLayout &, uint64_t, uint32_t, T *,          \
+                                              uint8_t *, uint8_t *);                                                  \
+  template hipError_t launch_reveal_eval<T>(const Launch &, const RevealLayout &, const uint8_t *, const uint8_t *,   \
+                                            const T *, const T *, int, T *, T *);                                     \
+  template hipError_t launch_mul_keygen<T>(const Launch &, const MulLayout &, uint64_t, uint32_t, const MulMap &,     \
+                                           const T *, const T *, T *, uint8_t *, uint8_t *);                          \
+  template hipError_t launch_mul_eval<T>(const Launch &, const MulLayout &, const uint8_t *, const uint8_t *,         \
+                                         const MulMap &, const T *, const T *, T *, T *);                             \
+  template hipError_t launch_lut8_keygen<T>(const Launch &, const Lut8Layout &, uint64_t, uint32_t, const T *, T *,   \
+                                            uint8_t *, uint8_t *);                                                    \
+  template hipError_t launch_lut8_phase1<T>(const Launch &, const Lut8Layout &, const uint8_t *, const uint8_t *,     \
+                                            const T *, const T *, T *, T *);                                          \
+  template hipError_t launch_lut8_phase2<T>(const Launch &, const Lut8Layout &, const uint8_t *, const uint8_t *,     \
+                                            const T *, T *, T *);                                                     \
+  template hipError_t launch_split<T>(const Launch &, uint64_t, uint32_t, uint32_t, size_t, const T *, T *, T *,      \
+                                      T *);                                                                           \
+  template hipError_t launch_prf_ring<T>(const Launch &, uint64_t, uint32_t, uint32_t, size_t, T *);                  \
+  template hipError_t launch_axpby<T>(const Launch &, size_t, T, const T *, T, const T *, T, T *);                    \
   template hipError_t launch_lincomb<T>(const Launch &, size_t, size_t, T, const T *, T, const T *, const T *, int,   \
-                                        T *);                                                                        \
-  template hipError_t launch_pool_prep<T>(const Launch &, size_t, int, const T *, const T *, T, T, T *);            \
-  template hipError_t launch_pool_diff<T>(const Launch &, int, int, int, const T *, T *);                            \
-  template hipError_t launch_pool_combine<T>(const Launch &, int, int, int, const T *, const T *, const T *, T *);   \
-  template hipError_t launch_concat<T>(const Launch &, int, int, int, const T *, const T *, T *);                    \
-  template hipError_t launch_output<T>(const Launch &, int, int, int, const T *, const T *, int64_t, int64_t *);     \
+                                        T *);                                                                         \
+  template hipError_t launch_pool_prep<T>(const Launch &, size_t, int, const T *, const T *, T, T, T *);              \
+  template hipError_t launch_pool_diff<T>(const Launch &, int, int, int, const T *, T *);                             \
+  template hipError_t launch_pool_combine<T>(const Launch &, int, int, int, const T *, const T *, const T *, T *);    \
+  template hipError_t launch_concat<T>(const Launch &, int, int, int, const T *, const T *, T *);                     \
+  template hipError_t launch_output<T>(const Launch &, int, int, int, const T *, const T *, int64_t, int64_t *);      \
   template hipError_t launch_rowsum<T>(const Launch &, size_t, int, const T *, T *);
-
 INST(uint32_t)
 INST(uint64_t)
 
