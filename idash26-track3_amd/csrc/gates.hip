@@ -370,9 +370,20 @@ hipError_t launch_tr_keygen(const Launch &L, const TrLayout &lay, uint64_t seed,
 // critical path while other lanes' large gates fill the GPU: its waves take the
 // SIMDs' issue slots first.
 constexpr size_t kTrPrioN = size_t(1) << 17;
+// Threads per workgroup of the one-launch gate kernel (both parties' threads for
+// block/2 elements).  A small gate spreads over the CUs: with the variant's block
+// its few workgroups put 8 waves on each CU they land on, and a CU's LDS serves
+// one 64-lane table read per two clocks, so every AES round of those waves waits
+// on one CU's LDS while the other CUs idle; about one workgroup per CU, of at
+// least one wave per party, divides the reads among the CUs (Launch::spread_small).
 static int tr_eval_block(const Launch &L, size_t n) {
   const int b = variant_block(L);
-  return (L.aes_block == 0 && b == 512 && n >= (size_t(1) << 22)) ? 1024 : b;
+  if (L.aes_block != 0) return b;
+  if (b == 512 && n >= (size_t(1) << 22)) return 1024;
+  if (!L.spread_small) return b;
+  const size_t per_cu = (n + size_t(L.num_cu) - 1) / size_t(L.num_cu);
+  const size_t h = std::max<size_t>(64, (per_cu + 63) / 64 * 64);
+  return int(std::min<size_t>(size_t(b), 2 * h));
 }
 
 template <typename T>

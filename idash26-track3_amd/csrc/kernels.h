@@ -20,6 +20,10 @@ struct Launch {
   int num_cu = 256;
   int aes_variant = 0;  // LDS T-table layout, see aes_variants()
   int aes_block = 0;    // threads per block for AES kernels (0 = variant default)
+  // The one-launch gate kernel spreads a small gate over the CUs (smaller
+  // workgroups, about one per CU).  A caller whose other streams keep the GPU
+  // busy clears it: the spread workgroups would take LDS from theirs.
+  bool spread_small = true;
   // Launches of a profiled forward use a separately named instantiation of the
   // DCF-evaluation kernel (same code), so kernel traces can tell them apart.
   bool profiled = false;
