@@ -60,9 +60,10 @@ __device__ __forceinline__ T low_bits(T v, int m) {
   return m >= int(8 * sizeof(T)) ? v : T(v & ((T(1) << m) - T(1)));
 }
 
+// the shifted input of element i from its masked input xh = x^[i]
 template <typename T>
-__device__ __forceinline__ T tr_shifted_input(const TrArgs<T> &a, size_t i) {
-  T x = a.xhat[i];
+__device__ __forceinline__ T tr_shifted_input(const TrArgs<T> &a, size_t i, T xh) {
+  T x = xh;
   if (a.has_bias && a.bias) x += T(a.bias[uint32_t(i % uint32_t(a.bias_ncol))]) << a.s;
   return low_bits<T>(x + (T(1) << a.sb), a.m);
 }
@@ -95,8 +96,8 @@ __device__ __forceinline__ void tr_dcf_bits(Aes &aes, const TrArgs<T> &a, const 
 // reconstructed masked bits of planes a and b.  The two parties' messages add
 // up to the masked output.
 template <typename T>
-__device__ __forceinline__ T tr_out_share(const TrArgs<T> &a, int p, const uint8_t *K, size_t i, T xp, uint32_t hb,
-                                          uint32_t bh, uint32_t dh) {
+__device__ __forceinline__ T tr_out_share(const TrArgs<T> &a, int p, const uint8_t *K, size_t i, T xh, T xp,
+                                          uint32_t hb, uint32_t bh, uint32_t dh) {
   const T *G = reinterpret_cast<const T *>(K + a.off_g);
   const T *kap = reinterpret_cast<const T *>(K + a.off_kappa);
   const T one0 = p == 0 ? T(1) : T(0);
@@ -116,7 +117,7 @@ __device__ __forceinline__ T tr_out_share(const TrArgs<T> &a, int p, const uint8
     const uint32_t z = hb ^ bh;
     const T k = kap[i];
     const T cp = z ? T(one0 - k) : k;
-    return cp * a.xhat[i] + G[size_t(z) * a.N + i];
+    return cp * xh + G[size_t(z) * a.N + i];
   }
   // G_TRSLACK
   const uint32_t Hh = uint32_t(xp >> (a.n - 2)) & 3u;
@@ -132,50 +133,88 @@ __device__ __forceinline__ T tr_out_share(const TrArgs<T> &a, int p, const uint8
 // code, its own name in kernel traces).
 constexpr int kTrMaxTile = 512;  // elements per tile (workgroups of up to 1024 threads)
 
-template <typename T, int NT, int REP, int TAG>
-__global__ void k_tr_eval(TrArgs<T> a) {
-  if (a.prio) __builtin_amdgcn_s_setprio(2);
+// The exchange buffers of a workgroup: per party, the ballot words of the two
+// DCF planes (one per wave) and the output messages.
+template <typename T>
+struct TrXchg {
+  uint64_t xa[2][kTrMaxTile / 64], xb[2][kTrMaxTile / 64];
+  T xm[2][kTrMaxTile];
+};
+
+// Gate a on element i of a tile (element e of the tile, wave wv of its party's
+// half, masked input xh): party p's DCF walks, the exchange of the masked DCF
+// output bits, party p's output message, the exchange of the messages.  Every
+// thread of the workgroup calls it (the exchanges synchronise the workgroup);
+// it returns the revealed output of element i to both parties' threads.
+template <typename T, class Aes>
+__device__ __forceinline__ T tr_tile(Aes &aes, const TrArgs<T> &a, TrXchg<T> &x, int p, int e, int wv,
+                                     const uint8_t *K, const uint8_t *KC, size_t i, bool in, T xh) {
+  uint32_t ra = 0, rb = 0;
+  T xp = 0;
+  if (in) {
+    xp = tr_shifted_input(a, i, xh);
+    tr_dcf_bits(aes, a, K, KC, i, xp, &ra, &rb);
+  }
+  // exchange 1: the masked DCF output bits
+  const uint64_t wa = __ballot(ra), wb = __ballot(rb);
+  if (lane_id() == 0) {
+    x.xa[p][wv] = wa;
+    x.xb[p][wv] = wb;
+  }
+  __syncthreads();
+  if (in) {
+    const uint32_t hb = uint32_t(xp >> a.sb) & 1u;
+    const uint32_t bh = a.use_a ? uint32_t((x.xa[0][wv] ^ x.xa[1][wv]) >> lane_id()) & 1u : 0u;
+    const uint32_t dh = a.use_b ? uint32_t((x.xb[0][wv] ^ x.xb[1][wv]) >> lane_id()) & 1u : 0u;
+    x.xm[p][e] = tr_out_share(a, p, K, i, xh, xp, hb, bh, dh);  // exchange 2: the output messages
+  }
+  __syncthreads();
+  const T y = in ? T(x.xm[0][e] + x.xm[1][e]) : T(0);
+  __syncthreads();  // the next gate or tile reuses the exchange buffers
+  return y;
+}
+
+// The tiles of one launch: gate a on x^, then (TWO) gate a2 on a's revealed
+// output, which both parties hold once it is revealed; party 0's threads write
+// the last gate's revealed output.
+template <typename T, int NT, int REP, bool TWO>
+__device__ __forceinline__ void tr_eval_tiles(const TrArgs<T> &a, const TrArgs<T> &a2) {
   __shared__ __align__(16) uint32_t lds[AesLds<NT, REP>::kWords];
-  __shared__ uint64_t xa[2][kTrMaxTile / 64], xb[2][kTrMaxTile / 64];
-  __shared__ T xm[2][kTrMaxTile];
+  __shared__ TrXchg<T> x;
   AesLds<NT, REP>::fill(lds);
   AesLds<NT, REP> aes(lds);
   const int h = int(blockDim.x) / 2;
   const int p = int(threadIdx.x) >= h ? 1 : 0;
   const int e = int(threadIdx.x) - p * h;  // element of the tile
   const int wv = e >> 6;                   // wave of the party's half
-  const uint8_t *K = p ? a.k1 : a.k0;
   // The correction words and leaf words of a DCF key are the same for both
   // parties (public to both); both parties read party 0's planes, so one copy
   // serves the two evaluations (and a streamed arena moves it once).
-  const uint8_t *KC = a.k0;
+  const uint8_t *K = p ? a.k1 : a.k0, *KC = a.k0;
   const size_t stride = size_t(gridDim.x) * size_t(h);
   for (size_t base = size_t(blockIdx.x) * h; base < a.N; base += stride) {
     const size_t i = base + size_t(e);
     const bool in = i < a.N;
-    uint32_t ra = 0, rb = 0;
-    T xp = 0;
-    if (in) {
-      xp = tr_shifted_input(a, i);
-      tr_dcf_bits(aes, a, K, KC, i, xp, &ra, &rb);
-    }
-    // exchange 1: the masked DCF output bits
-    const uint64_t wa = __ballot(ra), wb = __ballot(rb);
-    if (lane_id() == 0) {
-      xa[p][wv] = wa;
-      xb[p][wv] = wb;
-    }
-    __syncthreads();
-    if (in) {
-      const uint32_t hb = uint32_t(xp >> a.sb) & 1u;
-      const uint32_t bh = a.use_a ? uint32_t((xa[0][wv] ^ xa[1][wv]) >> lane_id()) & 1u : 0u;
-      const uint32_t dh = a.use_b ? uint32_t((xb[0][wv] ^ xb[1][wv]) >> lane_id()) & 1u : 0u;
-      xm[p][e] = tr_out_share(a, p, K, i, xp, hb, bh, dh);  // exchange 2: the output messages
-    }
-    __syncthreads();
-    if (p == 0 && in) a.out[i] = xm[0][e] + xm[1][e];
-    __syncthreads();  // the next tile reuses the exchange buffers
+    T y = tr_tile(aes, a, x, p, e, wv, K, KC, i, in, in ? a.xhat[i] : T(0));
+    if constexpr (TWO) y = tr_tile(aes, a2, x, p, e, wv, K, KC, i, in, y);
+    if (p == 0 && in) a.out[i] = y;
   }
+}
+
+template <typename T, int NT, int REP, int TAG>
+__global__ void k_tr_eval(TrArgs<T> a) {
+  if (a.prio) __builtin_amdgcn_s_setprio(2);
+  tr_eval_tiles<T, NT, REP, false>(a, a);
+}
+
+// Two gates of one element count in one launch (a truncation and its extension):
+// the second gate's masked input is the first's revealed output, element by
+// element, so no workgroup waits on another and the intermediate stays in
+// registers.  Output in a.out.
+template <typename T, int NT, int REP, int TAG>
+__global__ void k_tr_eval2(TrArgs<T> a, TrArgs<T> a2) {
+  if (a.prio) __builtin_amdgcn_s_setprio(2);
+  tr_eval_tiles<T, NT, REP, true>(a, a2);
 }
 
 // Party mode, phase 1: party p's masked DCF output bits (one ballot word per
@@ -190,7 +229,7 @@ __global__ void k_tr_party_bits(TrArgs<T> a, uint64_t *bits) {
   for (size_t base = size_t(blockIdx.x) * blockDim.x + (threadIdx.x & ~63u); base < a.N; base += stride) {
     const size_t i = base + lane_id();
     uint32_t ra = 0, rb = 0;
-    if (i < a.N) tr_dcf_bits(aes, a, a.k0, a.k0, i, tr_shifted_input(a, i), &ra, &rb);
+    if (i < a.N) tr_dcf_bits(aes, a, a.k0, a.k0, i, tr_shifted_input(a, i, a.xhat[i]), &ra, &rb);
     const uint64_t wa = __ballot(ra), wb = __ballot(rb);
     if (lane_id() == 0) {
       if (a.use_a) bits[base >> 6] = wa;
@@ -205,13 +244,14 @@ template <typename T>
 __global__ void k_tr_party_msg(TrArgs<T> a, int p, const uint64_t *own, const uint64_t *peer, T *msg) {
   const size_t W = (a.N + 63) / 64;
   for (size_t i = size_t(blockIdx.x) * blockDim.x + threadIdx.x; i < a.N; i += size_t(gridDim.x) * blockDim.x) {
-    const T xp = tr_shifted_input(a, i);
+    const T xh = a.xhat[i];
+    const T xp = tr_shifted_input(a, i, xh);
     const size_t w = i >> 6;
     const uint32_t sh = uint32_t(i & 63u);
     const uint32_t hb = uint32_t(xp >> a.sb) & 1u;
     const uint32_t bh = a.use_a ? uint32_t((own[w] ^ peer[w]) >> sh) & 1u : 0u;
     const uint32_t dh = a.use_b ? uint32_t((own[W + w] ^ peer[W + w]) >> sh) & 1u : 0u;
-    msg[i] = a.kind == G_DRELU ? T(hb ^ bh) : tr_out_share(a, p, a.k0, i, xp, hb, bh, dh);
+    msg[i] = a.kind == G_DRELU ? T(hb ^ bh) : tr_out_share(a, p, a.k0, i, xh, xp, hb, bh, dh);
   }
 }
 
@@ -413,6 +453,31 @@ hipError_t launch_tr_eval(const Launch &L, const TrLayout &lay, const uint8_t *k
 }
 
 template <typename T>
+hipError_t launch_tr_eval2(const Launch &L, const TrLayout &lay, const TrLayout &lay2, const uint8_t *k0,
+                           const uint8_t *k1, const T *xhat, const T *bias, int bias_ncol, T *out) {
+  if (lay.bw != int(8 * sizeof(T)) || lay2.bw != lay.bw || lay2.N != lay.N) return hipErrorInvalidValue;
+  TrArgs<T> a = tr_args<T>(lay), a2 = tr_args<T>(lay2);
+  a.k0 = a2.k0 = k0;
+  a.k1 = a2.k1 = k1;
+  a.xhat = xhat;
+  a.bias = bias;
+  a.bias_ncol = bias_ncol > 0 ? bias_ncol : 1;
+  a.out = out;
+  a.prio = lay.N < kTrPrioN;
+  return with_variant(L, [&](auto v) {
+    constexpr int NT = decltype(v)::nt, REP = decltype(v)::rep;
+    const int block = tr_eval_block(L, lay.N);
+    if (block < 128 || block > 2 * kTrMaxTile || block % 128 != 0) return hipErrorInvalidConfiguration;
+    const int grid = grid_for(k_tr_eval2<T, NT, REP, 0>, block, 2 * lay.N, L.num_cu);
+    if (L.profiled)
+      hipLaunchKernelGGL((k_tr_eval2<T, NT, REP, 1>), dim3(grid), dim3(block), 0, L.stream, a, a2);
+    else
+      hipLaunchKernelGGL((k_tr_eval2<T, NT, REP, 0>), dim3(grid), dim3(block), 0, L.stream, a, a2);
+    return hipGetLastError();
+  });
+}
+
+template <typename T>
 static TrArgs<T> tr_party_args(const TrLayout &lay, const uint8_t *key, const T *xhat, const T *bias,
                                int bias_ncol) {
   TrArgs<T> a = tr_args<T>(lay);
@@ -514,6 +579,8 @@ hipError_t launch_tr_expand(const Launch &L, const TrLayout &lay, const uint8_t 
                                           uint8_t *);                                                                 \
   template hipError_t launch_tr_eval<T>(const Launch &, const TrLayout &, const uint8_t *, const uint8_t *,           \
                                         const T *, const T *, int, T *);                                              \
+  template hipError_t launch_tr_eval2<T>(const Launch &, const TrLayout &, const TrLayout &, const uint8_t *,         \
+                                         const uint8_t *, const T *, const T *, int, T *);                            \
   template hipError_t launch_tr_party_bits<T>(const Launch &, const TrLayout &, const uint8_t *, const T *,           \
                                               const T *, int, uint64_t *);                                            \
   template hipError_t launch_tr_party_msg<T>(const Launch &, const TrLayout &, const uint8_t *, const T *,            \

@@ -86,6 +86,14 @@ template <typename T>
 hipError_t launch_tr_eval(const Launch &L, const TrLayout &lay, const uint8_t *k0, const uint8_t *k1,
                           const T *xhat, const T *bias, int bias_ncol, T *yhat);
 
+// Two gates of the same element count in one launch: lay on xhat (with the
+// bias), then lay2 on lay's revealed output, which never leaves the launch;
+// lay2's revealed output in out.  The model's truncations (TRMOD, then EXT or
+// EXTRELU) with resident keys.
+template <typename T>
+hipError_t launch_tr_eval2(const Launch &L, const TrLayout &lay, const TrLayout &lay2, const uint8_t *k0,
+                           const uint8_t *k1, const T *xhat, const T *bias, int bias_ncol, T *out);
+
 // Party mode (L.party = p), the same gate in two launches around the two
 // exchanges.  Phase 1: party p's masked DCF output bits, one bit per element,
 // packed 64 per word: plane a at bits[0, W), plane b at bits[W, 2W), W = ceil(N/64)

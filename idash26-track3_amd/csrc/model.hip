@@ -34,8 +34,9 @@ void Phase1Timer::reset() {
 }
 
 namespace {
-// A model lane of at most this many samples spreads its small gates over the CUs.
-constexpr int kSpreadLaneB = 8;
+// A model lane of at most this many samples runs in the latency-bound form
+// (small gates spread over the CUs, truncation pairs in one launch).
+constexpr int kFewLaneB = 8;
 // Events of the profiled forward only time work: they are read after a stream
 // synchronisation, so they skip the system-scope fence (an L2 writeback and
 // invalidation at every record, which would also slow the kernel after it).
@@ -166,6 +167,8 @@ struct Runner {
   // Party mode (L.party = 0 or 1): only this party's kernels run; its key is
   // kv.k[L.party] and each exchange goes through the peer.
   Peer *peer = nullptr;
+  // Consecutive gates may share a launch (tr2): keys resident, both parties here.
+  bool fuse = false;
 
   Runner(const Launch &L_, int bw_, int s_, Workspace<T> &ws_, Counters &ctr_, Phase1Timer *t, KeySource &src_,
          Peer *peer_ = nullptr)
@@ -230,6 +233,44 @@ struct Runner {
     return exchange_reconstruct(n, out);
   }
 
+  // AES calls per element and party of a gate's DCF walks
+  static int tr_levels(const TrLayout &lay) {
+    return (lay.use_a ? lay.a.L + 1 : 0) + (lay.use_b ? lay.b.L + 1 : 0);
+  }
+  // Algorithmic key bytes per element of a gate evaluated by both parties in one
+  // launch: per DCF the correction words and the leaf once (both parties'
+  // threads of a workgroup read party 0's copy) and each party's root (16 B) and
+  // mask bit; each party's G word of the element's case and kappa (the bias
+  // vector is ncol words, cache resident; the exchanges stay in LDS).
+  static double tr_key_bytes(const TrLayout &lay) {
+    const double tb = double(sizeof(T));
+    double per = (lay.ncase > 0 ? 2.0 * tb : 0.0) + (lay.relu ? 2.0 * tb : 0.0);
+    if (lay.use_a) per += 16.0 * (lay.a.L + 1) + 2.0 * (16.0 + 0.125);
+    if (lay.use_b) per += 16.0 * (lay.b.L + 1) + 2.0 * (16.0 + 0.125);
+    return per;
+  }
+  // profiled forward: events around one gate launch and its algorithmic work
+  // (AES calls per element and party, bytes per element: the masked input and the
+  // revealed output once, plus the keys)
+  hipError_t time_begin(hipEvent_t *e0, hipEvent_t *e1, Launch *L1) {
+    if (!timer || !timer->on) return hipSuccess;
+    TRY(hipEventCreateWithFlags(e0, kTimingEvent));
+    TRY(hipEventCreateWithFlags(e1, kTimingEvent));
+    TRY(hipEventRecord(*e0, L.stream));
+    L1->profiled = true;
+    return hipSuccess;
+  }
+  hipError_t time_end(hipEvent_t e0, hipEvent_t e1, size_t n, int levels, double key_bytes) {
+    if (!timer || !timer->on) return hipSuccess;
+    TRY(hipEventRecord(e1, L.stream));
+    timer->ev.push_back(e0);
+    timer->ev.push_back(e1);
+    timer->elems.push_back(n);
+    timer->levels.push_back(levels);
+    timer->bytes.push_back((2.0 * double(sizeof(T)) + key_bytes) * double(n));
+    return hipSuccess;
+  }
+
   hipError_t tr(int kind, size_t n, const T *x, const T *bias, int ncol, T *out) {
     const size_t end = tr_layout(kind, bw, s, n, c.off).end;
     size_t b;
@@ -237,36 +278,41 @@ struct Runner {
     TrLayout lay = tr_layout(kind, bw, s, n, b);
     hipEvent_t e0 = nullptr, e1 = nullptr;
     Launch L1 = L;
-    if (timer && timer->on) {
-      TRY(hipEventCreateWithFlags(&e0, kTimingEvent));
-      TRY(hipEventCreateWithFlags(&e1, kTimingEvent));
-      TRY(hipEventRecord(e0, L.stream));
-      L1.profiled = true;
-    }
+    TRY(time_begin(&e0, &e1, &L1));
     if (party_mode())
       TRY(tr_party(lay, n, x, bias, ncol, out));
     else
       TRY(launch_tr_eval<T>(L1, lay, kv.k[0], kv.k[1], x, bias, ncol, out));
-    if (timer && timer->on) {
-      TRY(hipEventRecord(e1, L.stream));
-      timer->ev.push_back(e0);
-      timer->ev.push_back(e1);
-      timer->elems.push_back(n);
-      timer->levels.push_back((lay.use_a ? lay.a.L + 1 : 0) + (lay.use_b ? lay.b.L + 1 : 0));
-      // per element: the masked input and the revealed output once; per DCF
-      // the correction words and the leaf once (both parties' threads of a
-      // workgroup read party 0's copy) and each party's root (16 B) and mask
-      // bit; each party's G word of the element's case and kappa (the bias
-      // vector is ncol words, cache resident; the exchanges stay in LDS)
-      const double tb = double(sizeof(T));
-      double per = 2.0 * tb + (lay.ncase > 0 ? 2.0 * tb : 0.0) + (lay.relu ? 2.0 * tb : 0.0);
-      if (lay.use_a) per += 16.0 * (lay.a.L + 1) + 2.0 * (16.0 + 0.125);
-      if (lay.use_b) per += 16.0 * (lay.b.L + 1) + 2.0 * (16.0 + 0.125);
-      timer->bytes.push_back(per * double(n));
-    }
+    TRY(time_end(e0, e1, n, tr_levels(lay), tr_key_bytes(lay)));
     ctr.bitplanes(n, int(lay.use_a) + int(lay.use_b));
     if (kind != G_DRELU) ctr.msg(n, bw);  // DRELU: the output bit is already public
     leave(end);
+    return hipSuccess;
+  }
+
+  // Gate kind on x (with the bias), then gate kind2 on its revealed output, in
+  // one launch (both parties here, resident keys: both gates' keys in one view);
+  // the same keys, exchanges and counted bytes as tr(kind) then tr(kind2), and x
+  // is left as it was.
+  hipError_t tr2(int kind, int kind2, size_t n, const T *x, const T *bias, int ncol, T *out) {
+    const size_t end1 = tr_layout(kind, bw, s, n, c.off).end;
+    size_t b1, b2;
+    TRY(enter(end1, &b1));
+    const TrLayout lay = tr_layout(kind, bw, s, n, b1);
+    leave(end1);
+    const size_t end2 = tr_layout(kind2, bw, s, n, c.off).end;
+    TRY(enter(end2, &b2));
+    const TrLayout lay2 = tr_layout(kind2, bw, s, n, b2);
+    hipEvent_t e0 = nullptr, e1 = nullptr;
+    Launch L1 = L;
+    TRY(time_begin(&e0, &e1, &L1));
+    TRY(launch_tr_eval2<T>(L1, lay, lay2, kv.k[0], kv.k[1], x, bias, ncol, out));
+    TRY(time_end(e0, e1, n, tr_levels(lay) + tr_levels(lay2), tr_key_bytes(lay) + tr_key_bytes(lay2)));
+    for (const TrLayout *l : {&lay, &lay2}) {
+      ctr.bitplanes(n, int(l->use_a) + int(l->use_b));
+      ctr.msg(n, bw);
+    }
+    leave(end2);
     return hipSuccess;
   }
 
@@ -598,6 +644,7 @@ class Model final : public ModelBase, KeySource {
   // Eval may overwrite x; keygen may overwrite the mask rin.
   hipError_t trunc_eval(Runner<T> &r, bool relu, size_t n, T *x, const T *bias, int ncol, T *y) {
     if (!local_trunc()) {
+      if (r.fuse) return r.tr2(G_TRMOD, relu ? G_EXTRELU : G_EXT, n, x, bias, ncol, y);
       TRY(r.tr(G_TRMOD, n, x, bias, ncol, x));
       return r.tr(relu ? G_EXTRELU : G_EXT, n, x, nullptr, 1, y);
     }
@@ -1496,11 +1543,13 @@ class Model final : public ModelBase, KeySource {
   hipError_t forward_body(int B) {
     if (keyed_B_ != B || input_B_ != B) return hipErrorInvalidValue;
     TRY(ensure_work(B));
-    // Small gates spread over the CUs only in a lane of a few samples: lanes of
-    // more keep the GPU busy between them, and a spread gate's workgroups would
-    // take LDS from the other lanes' gates (measured at B = 64 in 3 lanes: 0.7%
-    // slower spread; at B = 16 0.9% faster, at B = 1 4.7% lower latency).
-    L_.spread_small = B <= kSpreadLaneB;
+    // A lane of a few samples is latency-bound: its small gates spread over the
+    // CUs and each truncation's two gates run in one launch.  Lanes of more keep
+    // the GPU busy between them, where a spread gate's workgroups take LDS from
+    // the other lanes' gates and the paired launches measured slower (B = 64 in
+    // 3 lanes: 0.7% and 1.5% slower; B = 1: 4.7% and 3.4% lower latency).
+    const bool few = B <= kFewLaneB;
+    L_.spread_small = few;
     const int N = d_.n_nodes, bw = bw_;
     const size_t BN = size_t(B) * N;
     if (!streaming_) {
@@ -1515,6 +1564,7 @@ class Model final : public ModelBase, KeySource {
       if (chunks_.size() > 1) TRY(issue_copy(1));
     }
     Runner<T> r(L_, bw_, s_, ws_, counters, &timer, *this, peer_);
+    r.fuse = few && !streaming_ && party_ < 0;
     auto pub_gemm = [&](const T *x, int l, size_t rows, T *y) -> hipError_t {
       int in, out;
       layer_io(l, &in, &out);

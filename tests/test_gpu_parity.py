@@ -503,23 +503,33 @@ def test_model_local_truncation(mp, orc, synth, bw):
 
 
 def _tr_gates(dims):
-    """DCF-evaluation launches of one exact forward: the adjacency block's
-    TRSLACK, 3 x (TRMOD, EXT, TRMOD, EXTRELU), the pool levels, then TRMOD and
-    EXT / EXTRELU for the two drug FCs and the hidden fusion layers."""
+    """DCF gates of one exact forward: the adjacency block's TRSLACK,
+    3 x (TRMOD, EXT, TRMOD, EXTRELU), the pool levels, then TRMOD and EXT /
+    EXTRELU for the two drug FCs and the hidden fusion layers."""
     R, levels = dims.n_nodes, 0
     while R > 1:
         R, levels = R // 2 + (R & 1), levels + 1
     return 1 + 12 + levels + 2 * (2 + len(dims.fus) - 1)
 
 
-@pytest.mark.parametrize("bw,B,lanes", [(32, 5, 2), (64, 4, 3), (32, 2, 4)])
+def _tr_launches(dims, n):
+    """DCF-evaluation launches of one exact forward of a lane of n samples with
+    resident keys and both parties in one process: a lane of at most 8 samples
+    (latency-bound) runs every truncation (TRMOD with its EXT or EXTRELU) as one
+    launch, one fewer per truncation than there are gates; larger lanes launch
+    every gate on its own."""
+    return _tr_gates(dims) - (6 + 2 + len(dims.fus) - 1 if n <= 8 else 0)
+
+
+@pytest.mark.parametrize("bw,B,lanes", [(32, 5, 2), (64, 4, 3), (32, 2, 4), (32, 10, 1)])
 def test_model_lanes_keys_and_forward(mp, orc, synth, bw, B, lanes):
     """Concurrent sub-batches: the key arena is the lanes' one-lane key sets
     back to back, each byte-identical to the oracle dealer's under its lane
     seed; each lane's key set evaluates correctly in the oracle; the forward
     gives the plaintext outputs and the lanes' summed exchange bytes; a profiled
     forward (lanes one after another) gives the same outputs and times every
-    lane's DCF launches.  B=2 with 4 lanes leaves two lanes empty."""
+    lane's DCF launches.  B=2 with 4 lanes leaves two lanes empty; a lane of 10
+    samples launches every gate on its own, the smaller ones pair truncations."""
     wl = synth.workload(B, synth.Dims(bw=bw), seed=23)
     d = _od(orc, wl.dims)
     want, code = orc.plain_forward(d, wl.X, wl.A, wl.mask, wl.prot, wl.W)
@@ -557,7 +567,7 @@ def test_model_lanes_keys_and_forward(mp, orc, synth, bw, B, lanes):
     prof = m.profile_read()
     m.profile(False)
     assert np.array_equal(m.output(B), want)
-    assert prof["launches"] == _tr_gates(wl.dims) * len(split) and prof["ms"] > 0
+    assert prof["launches"] == sum(_tr_launches(wl.dims, n) for _, n in split) and prof["ms"] > 0
     # ring GEMM sections: per lane 3 public GCN products, 3 SxS gates, 2 drug FCs
     # and the fusion layers, with their ring multiply-adds
     dm = wl.dims
