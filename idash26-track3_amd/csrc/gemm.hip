@@ -1166,14 +1166,14 @@ static hipError_t gemm_init(const Launch &L, const GemmArgs<T> &g) {
 }
 
 // The wide-K kernel: automatic path selection, the matrix-core path, and either
-// enough tiles to occupy a quarter of the CUs or at most one K step per
-// segment.  A long K over few tiles (the fully connected layers: 22 rows,
-// K = 312..1024) is spread over more CUs by the split-K tiled kernel.
+// enough tiles to occupy a quarter of the CUs or K within one tiled K slice.  A
+// longer K over few tiles (the fully connected layers: 22 rows, K = 256..1024)
+// is spread over more CUs by the split-K tiled kernel (K = 256 by 1024 columns:
+// 16 wide workgroups took 8.3 us, the split-K launch's 64 about 6).
 template <typename T>
 static bool use_wide(const Launch &L, const GemmArgs<T> &g) {
   if ((L.gemm != 0 && L.gemm != 3) || !use_mfma(L, g)) return false;
-  constexpr int KT = kWideK * 4 / int(sizeof(T));
-  return gemm_tiles(g) >= L.num_cu / 4 || g.K <= KT;
+  return gemm_tiles(g) >= L.num_cu / 4 || g.K <= mfma_bk<T>();
 }
 // rows of A (and of the masks and second segment) read as 16-byte groups
 template <typename T>
