@@ -123,6 +123,11 @@ hipError_t launch_reveal_keygen(const Launch &L, const RevealLayout &lay, uint64
 template <typename T>
 hipError_t launch_reveal_eval(const Launch &L, const RevealLayout &lay, const uint8_t *k0, const uint8_t *k1,
                               const T *v0, const T *v1, int rowlen, T *msg0, T *msg1);
+// Both parties in this process: out = msg0 + msg1 from one launch (each party's
+// message formed from its own share and key; no message planes in HBM).
+template <typename T>
+hipError_t launch_reveal_sum(const Launch &L, const RevealLayout &lay, const uint8_t *k0, const uint8_t *k1,
+                             const T *v0, const T *v1, int rowlen, T *out);
 
 // ---------------- Beaver product ----------------
 // Operand indices of z[k] = x[a(k)] * y[b(k)]: explicit index arrays, or one of
@@ -156,6 +161,10 @@ hipError_t launch_mul_keygen(const Launch &L, const MulLayout &lay, uint64_t see
 template <typename T>
 hipError_t launch_mul_eval(const Launch &L, const MulLayout &lay, const uint8_t *k0, const uint8_t *k1,
                            const MulMap &map, const T *xhat, const T *yhat, T *msg0, T *msg1);
+// Both parties in this process: the revealed product msg0 + msg1 from one launch.
+template <typename T>
+hipError_t launch_mul_eval_sum(const Launch &L, const MulLayout &lay, const uint8_t *k0, const uint8_t *k1,
+                               const MulMap &map, const T *xhat, const T *yhat, T *out);
 
 // ---------------- LUT8 ----------------
 template <typename T>

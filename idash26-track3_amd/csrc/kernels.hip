@@ -341,6 +341,83 @@ hipError_t launch_reveal_eval(const Launch &L, const RevealLayout &lay, const ui
   return hipGetLastError();
 }
 
+// Both parties in this process: each thread forms party 0's message v0 + R0 and
+// party 1's v1 + R1 from each party's own share and key, and writes their sum,
+// the revealed value; the message planes never reach HBM and no reconstruction
+// launch follows.
+template <typename T>
+__global__ void k_reveal_sum(size_t n, const T *R0, const T *R1, const T *v0, const T *v1, T *out) {
+  for (size_t i = size_t(blockIdx.x) * blockDim.x + threadIdx.x; i < n; i += size_t(gridDim.x) * blockDim.x) {
+    const T m0 = v0[i] + R0[i], m1 = v1[i] + R1[i];
+    out[i] = m0 + m1;
+  }
+}
+// The row-sum reveal (degrees) in the same form: 16 lanes per row of rowlen
+// contiguous words, each lane adding its words of both parties' rows (16-byte
+// loads where rows are whole 16-byte groups), then a 16-lane reduction; lane 0
+// of the group adds both parties' masks.  The two messages are sums, so adding
+// the parties' partial sums before the reduction gives the same revealed value.
+constexpr int kRowLanes = 16;
+template <typename T, bool VEC>
+__global__ void k_reveal_rowsum_sum(size_t n, const T *R0, const T *R1, const T *v0, const T *v1, int rowlen,
+                                    T *out) {
+  const int sub = int(threadIdx.x) % kRowLanes;
+  const size_t grp = (size_t(blockIdx.x) * blockDim.x + threadIdx.x) / kRowLanes;
+  const size_t ngrp = size_t(gridDim.x) * blockDim.x / kRowLanes;
+  const size_t rows = (n + ngrp - 1) / ngrp * ngrp;  // every group runs the same trip count
+  for (size_t r = grp; r < rows; r += ngrp) {
+    T x = 0;
+    if (r < n) {
+      const T *a = v0 + r * size_t(rowlen), *b = v1 + r * size_t(rowlen);
+      if constexpr (VEC) {
+        constexpr int W = 16 / int(sizeof(T));
+        const int ng = rowlen / W;
+        for (int g = sub; g < ng; g += kRowLanes) {
+          const uint4 pa = reinterpret_cast<const uint4 *>(a)[g], pb = reinterpret_cast<const uint4 *>(b)[g];
+          if constexpr (sizeof(T) == 4) {
+            x += (pa.x + pa.y + pa.z + pa.w) + (pb.x + pb.y + pb.z + pb.w);
+          } else {
+            x += ((uint64_t(pa.y) << 32 | pa.x) + (uint64_t(pa.w) << 32 | pa.z)) +
+                 ((uint64_t(pb.y) << 32 | pb.x) + (uint64_t(pb.w) << 32 | pb.z));
+          }
+        }
+      } else {
+        for (int j = sub; j < rowlen; j += kRowLanes) x += a[j] + b[j];
+      }
+    }
+#pragma unroll
+    for (int o = kRowLanes / 2; o > 0; o >>= 1) x += __shfl_xor(x, o, kRowLanes);
+    if (r < n && sub == 0) {
+      const T m0 = R0[r], m1 = R1[r];
+      out[r] = x + m0 + m1;
+    }
+  }
+}
+
+template <typename T>
+hipError_t launch_reveal_sum(const Launch &L, const RevealLayout &lay, const uint8_t *k0, const uint8_t *k1,
+                             const T *v0, const T *v1, int rowlen, T *out) {
+  const int block = 256;
+  const T *R0 = reinterpret_cast<const T *>(k0 + lay.off_r), *R1 = reinterpret_cast<const T *>(k1 + lay.off_r);
+  if (rowlen > 0) {
+    const bool vec = (size_t(rowlen) * sizeof(T)) % 16 == 0 && (reinterpret_cast<uintptr_t>(v0) & 15) == 0 &&
+                     (reinterpret_cast<uintptr_t>(v1) & 15) == 0;
+    if (vec) {
+      const int grid = grid_for(k_reveal_rowsum_sum<T, true>, block, lay.N * kRowLanes, L.num_cu);
+      hipLaunchKernelGGL((k_reveal_rowsum_sum<T, true>), dim3(grid), dim3(block), 0, L.stream, lay.N, R0, R1, v0, v1,
+                         rowlen, out);
+    } else {
+      const int grid = grid_for(k_reveal_rowsum_sum<T, false>, block, lay.N * kRowLanes, L.num_cu);
+      hipLaunchKernelGGL((k_reveal_rowsum_sum<T, false>), dim3(grid), dim3(block), 0, L.stream, lay.N, R0, R1, v0,
+                         v1, rowlen, out);
+    }
+    return hipGetLastError();
+  }
+  const int grid = grid_for(k_reveal_sum<T>, block, lay.N, L.num_cu);
+  hipLaunchKernelGGL((k_reveal_sum<T>), dim3(grid), dim3(block), 0, L.stream, lay.N, R0, R1, v0, v1, out);
+  return hipGetLastError();
+}
+
 // ---------------------------------------------------------------------------
 // Beaver product
 // ---------------------------------------------------------------------------
@@ -505,6 +582,114 @@ hipError_t launch_mul_eval(const Launch &L, const MulLayout &lay, const uint8_t 
                      reinterpret_cast<const T *>(k0 + lay.off_ry), reinterpret_cast<const T *>(k1 + lay.off_ry),
                      reinterpret_cast<const T *>(k0 + lay.off_c), reinterpret_cast<const T *>(k1 + lay.off_c), map,
                      xhat, yhat, msg0, msg1, party_base(L));
+  return hipGetLastError();
+}
+
+// Both parties in this process: each thread forms party 0's message
+// x^y^ - x^ ry0 - y^ rx0 + c0 and party 1's - x^ ry1 - y^ rx1 + c1, each from the
+// party's own key, and writes their sum, the revealed product (the operands are
+// read once, no message planes, no reconstruction launch).
+template <typename T>
+__global__ void k_mul_eval_sum(size_t nz, const T *Rx0, const T *Rx1, const T *Ry0, const T *Ry1, const T *C0,
+                               const T *C1, MulMap map, const T *xhat, const T *yhat, T *out) {
+  for (size_t i = size_t(blockIdx.x) * blockDim.x + threadIdx.x; i < nz; i += size_t(gridDim.x) * blockDim.x) {
+    uint32_t a, b;
+    mul_operands(map, i, &a, &b);
+    const T x = xhat[a], y = yhat[b];
+    const T z0 = C0[i] - x * Ry0[b] - y * Rx0[a] + x * y;
+    const T z1 = C1[i] - x * Ry1[b] - y * Rx1[a];
+    out[i] = z0 + z1;
+  }
+}
+
+// A (.) W with W symmetric (SYM_HADAMARD) in the same form: one workgroup per
+// (graph, tile of TI rows).  The tile's W entries and both parties' masks of W
+// are staged in LDS as dense TI x N blocks (contiguous global runs: row i of the
+// triangle for j >= i, entries (j, i0..i0+TI-1) of triangle row j for j < i), in
+// batches of kStage slots per thread whose loads all go out before any store;
+// then the tile's outputs, consecutive elements of A_norm, are read and written
+// coalesced.
+constexpr int kStage = 8;
+template <typename T, int TI>
+__global__ void k_mul_eval_sym_sum(uint32_t N, const T *Rx0, const T *Rx1, const T *Ry0, const T *Ry1, const T *C0,
+                                   const T *C1, const T *xhat, const T *yhat, T *out) {
+  extern __shared__ unsigned char lds_raw[];
+  T *Wy = reinterpret_cast<T *>(lds_raw);
+  T *W0 = Wy + TI * N, *W1 = W0 + TI * N;
+  const uint32_t tiles = (N + TI - 1) / TI, P = N * (N + 1) / 2;
+  const uint32_t g = blockIdx.x / tiles, i0 = (blockIdx.x - g * tiles) * TI;
+  const uint32_t ni = N - i0 < uint32_t(TI) ? N - i0 : uint32_t(TI);
+  const T *yg = yhat + size_t(g) * P, *r0g = Ry0 + size_t(g) * P, *r1g = Ry1 + size_t(g) * P;
+  // staging slots: [0, ni N) row-major over (ii, j), taken where j >= i; then
+  // [ni N, ni N + nj TI) over (j, ii) with tile rows fastest, taken where j < i
+  const uint32_t n1 = ni * N, nj = i0 + ni - 1, n2 = nj * TI;
+  for (uint32_t t0 = threadIdx.x; t0 < n1 + n2; t0 += kStage * blockDim.x) {
+    T vy[kStage], v0[kStage], v1[kStage];
+    uint32_t dst[kStage];
+#pragma unroll
+    for (int u = 0; u < kStage; u++) {
+      const uint32_t t = t0 + uint32_t(u) * blockDim.x;
+      uint32_t q = 0, d = ~0u;
+      if (t < n1) {
+        const uint32_t ii = t / N, j = t - ii * N, i = i0 + ii;
+        if (j >= i) {
+          q = pair_row_start(N, i) + (j - i);
+          d = ii * N + j;
+        }
+      } else if (t < n1 + n2) {
+        const uint32_t tt = t - n1, j = tt / TI, ii = tt - j * TI, i = i0 + ii;
+        if (ii < ni && j < i) {
+          q = pair_row_start(N, j) + (i - j);
+          d = ii * N + j;
+        }
+      }
+      dst[u] = d;
+      vy[u] = d != ~0u ? yg[q] : T(0);
+      v0[u] = d != ~0u ? r0g[q] : T(0);
+      v1[u] = d != ~0u ? r1g[q] : T(0);
+    }
+#pragma unroll
+    for (int u = 0; u < kStage; u++)
+      if (dst[u] != ~0u) {
+        Wy[dst[u]] = vy[u];
+        W0[dst[u]] = v0[u];
+        W1[dst[u]] = v1[u];
+      }
+  }
+  __syncthreads();
+  const size_t kb = (size_t(g) * N + i0) * N;
+  for (uint32_t t = threadIdx.x; t < ni * N; t += blockDim.x) {
+    const size_t k = kb + t;
+    const T x = xhat[k], y = Wy[t];
+    const T z0 = C0[k] - x * W0[t] - y * Rx0[k] + x * y;
+    const T z1 = C1[k] - x * W1[t] - y * Rx1[k];
+    out[k] = z0 + z1;
+  }
+}
+
+template <typename T>
+hipError_t launch_mul_eval_sum(const Launch &L, const MulLayout &lay, const uint8_t *k0, const uint8_t *k1,
+                               const MulMap &map, const T *xhat, const T *yhat, T *out) {
+  const T *Rx0 = reinterpret_cast<const T *>(k0 + lay.off_rx), *Rx1 = reinterpret_cast<const T *>(k1 + lay.off_rx);
+  const T *Ry0 = reinterpret_cast<const T *>(k0 + lay.off_ry), *Ry1 = reinterpret_cast<const T *>(k1 + lay.off_ry);
+  const T *C0 = reinterpret_cast<const T *>(k0 + lay.off_c), *C1 = reinterpret_cast<const T *>(k1 + lay.off_c);
+  const int block = 256;
+  constexpr int TI = sizeof(T) == 4 ? 16 : 8;
+  // the staged tile fits 64 KiB of LDS up to N = 341; larger graphs gather W in
+  // the generic kernel (the same map, computed per product)
+  if (map.kind == MulMap::SYM_HADAMARD && 3 * TI * size_t(map.N) * sizeof(T) <= 65536) {
+    const size_t N = map.N, NN = N * N, P = N * (N + 1) / 2;
+    if (N == 0 || lay.nz % NN != 0 || lay.nx != lay.nz || lay.ny != (lay.nz / NN) * P) return hipErrorInvalidValue;
+    const size_t tiles = (N + TI - 1) / TI, blocks = (lay.nz / NN) * tiles;
+    if (blocks >= (size_t(1) << 31)) return hipErrorInvalidValue;
+    const size_t lds = 3 * TI * N * sizeof(T);
+    hipLaunchKernelGGL((k_mul_eval_sym_sum<T, TI>), dim3(unsigned(blocks)), dim3(block), lds, L.stream, uint32_t(N),
+                       Rx0, Rx1, Ry0, Ry1, C0, C1, xhat, yhat, out);
+    return hipGetLastError();
+  }
+  const int grid = grid_for(k_mul_eval_sum<T>, block, lay.nz, L.num_cu);
+  hipLaunchKernelGGL((k_mul_eval_sum<T>), dim3(grid), dim3(block), 0, L.stream, lay.nz, Rx0, Rx1, Ry0, Ry1, C0, C1, map,
+                     xhat, yhat, out);
   return hipGetLastError();
 }
 
@@ -822,6 +1007,10 @@ hipError_t launch_rowsum(const Launch &L, size_t rows, int len, const T *a, T *o
                                            const T *, const T *, T *, uint8_t *, uint8_t *);                          \
   template hipError_t launch_mul_eval<T>(const Launch &, const MulLayout &, const uint8_t *, const uint8_t *,         \
                                          const MulMap &, const T *, const T *, T *, T *);                             \
+  template hipError_t launch_mul_eval_sum<T>(const Launch &, const MulLayout &, const uint8_t *, const uint8_t *,     \
+                                             const MulMap &, const T *, const T *, T *);                              \
+  template hipError_t launch_reveal_sum<T>(const Launch &, const RevealLayout &, const uint8_t *, const uint8_t *,    \
+                                           const T *, const T *, int, T *);                                           \
   template hipError_t launch_lut8_keygen<T>(const Launch &, const Lut8Layout &, uint64_t, uint32_t, const T *, T *,   \
                                             uint8_t *, uint8_t *);                                                    \
   template hipError_t launch_lut8_phase1<T>(const Launch &, const Lut8Layout &, const uint8_t *, const uint8_t *,     \

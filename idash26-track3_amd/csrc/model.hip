@@ -175,6 +175,13 @@ struct Runner {
       : L(L_), bw(bw_), s(s_), ws(ws_), ctr(ctr_), timer(t), src(src_), peer(peer_) {}
 
   bool party_mode() const { return L.party >= 0; }
+  // [a, a + na) and [b, b + nb) (elements) share no byte: the one-launch reveal
+  // and Beaver evaluations write their output while other threads still read
+  // their inputs
+  static bool disjoint(const T *a, size_t na, const T *b, size_t nb) {
+    const uintptr_t a0 = reinterpret_cast<uintptr_t>(a), b0 = reinterpret_cast<uintptr_t>(b);
+    return a0 + na * sizeof(T) <= b0 || b0 + nb * sizeof(T) <= a0;
+  }
   const uint8_t *own_key() const { return kv.k[L.party]; }
   // party mode: send this party's message (ws.m0), receive the peer's (ws.m1),
   // and reconstruct out = m0 + m1
@@ -206,7 +213,9 @@ struct Runner {
       const T *v = L.party ? v1 : v0;
       TRY(launch_reveal_eval<T>(L, lay, own_key(), own_key(), v, v, rowlen, ws.m0.p, ws.m0.p));
       TRY(exchange_reconstruct(n, out));
-    } else {
+    } else if (disjoint(out, n, v0, rowlen > 0 ? n * rowlen : n) && disjoint(out, n, v1, rowlen > 0 ? n * rowlen : n)) {
+      TRY(launch_reveal_sum<T>(L, lay, kv.k[0], kv.k[1], v0, v1, rowlen, out));
+    } else {  // out overlaps a share: messages first
       TRY(launch_reveal_eval<T>(L, lay, kv.k[0], kv.k[1], v0, v1, rowlen, ws.m0.p, ws.m1.p));
       TRY(launch_reconstruct<T>(L, n, ws.m0.p, ws.m1.p, out));
     }
@@ -325,7 +334,9 @@ struct Runner {
     if (party_mode()) {
       TRY(launch_mul_eval<T>(L, lay, own_key(), own_key(), map, x, y, ws.m0.p, ws.m0.p));
       TRY(exchange_reconstruct(nz, out));
-    } else {
+    } else if (disjoint(out, nz, x, nx) && disjoint(out, nz, y, ny)) {
+      TRY(launch_mul_eval_sum<T>(L, lay, kv.k[0], kv.k[1], map, x, y, out));
+    } else {  // out overlaps an operand, which other threads gather: messages first
       TRY(launch_mul_eval<T>(L, lay, kv.k[0], kv.k[1], map, x, y, ws.m0.p, ws.m1.p));
       TRY(launch_reconstruct<T>(L, nz, ws.m0.p, ws.m1.p, out));
     }

@@ -312,6 +312,41 @@ def test_mul_keys_and_eval(ctx, orc):
     assert np.array_equal(signed(z.astype(np.uint64) - orz, bw), xv[ia] * yv[ib])
 
 
+def test_mul_and_reveal_in_place(ctx, orc, mp):
+    """Outputs that overlap an input (the product over its own x^ buffer, the
+    reveal over party 0's share) take the message path and give the same values:
+    the one-launch evaluation writes outputs while other threads gather inputs."""
+    bw = ctx.bw
+    rng = np.random.default_rng(bw + 5)
+    nx, ny, nz = 3000, 200, 2500
+    lim = 1 << (14 if bw == 32 else 30)
+    xv = rng.integers(-lim, lim, size=nx)
+    yv = rng.integers(-lim, lim, size=ny)
+    ia = rng.integers(0, nx, size=nz).astype(np.uint32)
+    ib = rng.integers(0, ny, size=nz).astype(np.uint32)
+    rx, ry = rmask(rng, nx, bw), rmask(rng, ny, bw)
+    g0, g1, grz = ctx.mul_keygen(rx, ry, ia, ib, seed=3, gate=5)
+    xh = (xv.astype(np.uint64) + rx) & M(bw)
+    yh = (yv.astype(np.uint64) + ry) & M(bw)
+    want = ctx.mul_eval(g0, g1, xh, yh, ia, ib)
+    d = [mp.to_dev(v) for v in (ia, ib)]
+    dx, dy = mp.to_dev(ctx.ring(xh)), mp.to_dev(ctx.ring(yh))
+    ctx.check(ctx.lib.mpcx_mul_eval(ctx.h, nx, ny, nz, mp.dptr(d[0]), mp.dptr(d[1]), mp.dptr(g0), mp.dptr(g1),
+                                    mp.dptr(dx), mp.dptr(dy), mp.dptr(dx)), "mul_eval")
+    got = mp.from_dev(dx, ctx.T, nz)
+    assert np.array_equal(got, want)
+    assert np.array_equal(signed(got.astype(np.uint64) - grz, bw), xv[ia] * yv[ib])
+    n = 777
+    r0, r1, rm = ctx.reveal_keygen(n, seed=4, gate=6)
+    v = rng.integers(-1000, 1000, size=n)
+    v0 = rmask(rng, n, bw)
+    v1 = (v.astype(np.uint64) - v0) & M(bw)
+    d0, d1 = mp.to_dev(ctx.ring(v0)), mp.to_dev(ctx.ring(v1))
+    ctx.check(ctx.lib.mpcx_reveal_eval(ctx.h, n, mp.dptr(r0), mp.dptr(r1), mp.dptr(d0), mp.dptr(d1), mp.dptr(d0)),
+              "reveal_eval")
+    assert np.array_equal(signed(mp.from_dev(d0, ctx.T, n).astype(np.uint64) - rm, bw), v)
+
+
 def test_lut8_keys_and_eval(ctx, orc):
     bw = ctx.bw
     rng = np.random.default_rng(9)
