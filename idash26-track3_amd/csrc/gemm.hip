@@ -1166,14 +1166,18 @@ static hipError_t gemm_init(const Launch &L, const GemmArgs<T> &g) {
 }
 
 // The wide-K kernel: automatic path selection, the matrix-core path, and either
-// enough tiles to occupy a quarter of the CUs or K within one tiled K slice.  A
-// longer K over few tiles (the fully connected layers: 22 rows, K = 256..1024)
-// is spread over more CUs by the split-K tiled kernel (K = 256 by 1024 columns:
-// 16 wide workgroups took 8.3 us, the split-K launch's 64 about 6).
+// enough tiles to occupy a quarter of the CUs, or K within one tiled K slice, or
+// K within one wide step where a split-K launch would first need a clearing
+// launch (C not known to hold zeros).  A longer K over few tiles (the fully
+// connected layers: 22 rows, K = 256..1024, outputs cleared once per forward) is
+// spread over more CUs by the split-K tiled kernel (K = 256 by 1024 columns: 16
+// wide workgroups took 8.3 us, the split-K launch's 64 about 6).
 template <typename T>
 static bool use_wide(const Launch &L, const GemmArgs<T> &g) {
   if ((L.gemm != 0 && L.gemm != 3) || !use_mfma(L, g)) return false;
-  return gemm_tiles(g) >= L.num_cu / 4 || g.K <= mfma_bk<T>();
+  constexpr int KT = kWideK * 4 / int(sizeof(T));
+  const bool zeroed = g.c_zero && !g.Cin;
+  return gemm_tiles(g) >= L.num_cu / 4 || g.K <= mfma_bk<T>() || (g.K <= KT && !zeroed);
 }
 // rows of A (and of the masks and second segment) read as 16-byte groups
 template <typename T>
