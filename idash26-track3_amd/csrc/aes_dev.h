@@ -341,6 +341,72 @@ struct AesPerm2 {
   }
 };
 
+// Quad-lane AES on the AesPerm2 table, for latency-bound launches: four
+// consecutive lanes (a quad) hold one block, lane j its column c_j.  A round has
+// each lane look up its own column's four bytes -- A = T0[b0], B = T1[b1],
+// C = T0[b2], D = T1[b3] -- and take the other three terms of its new column from
+// the quad's other lanes (DPP quad permutes):
+//   n_j = A_j ^ B_(j+1) ^ rotl(C_(j+2) ^ D_(j+3) ^ rotl(k_j, 16), 16),
+// 10 VALU instructions and 4 table reads per lane and round instead of 28 and 16
+// for one lane per block, so a round's dependent chain is shorter.  Every lane of
+// a quad must run the same code (the permutes read the other three lanes).
+struct AesQuad {
+  const AesPerm2 &t;
+  uint32_t j;  // the lane's column (lane mod 4)
+  __device__ AesQuad(const AesPerm2 &tab) : t(tab), j(threadIdx.x & 3u) {}
+
+  // DPP quad permutes: the value of lane (j + d) mod 4 of the quad
+  __device__ __forceinline__ static uint32_t from1(uint32_t v) { return __builtin_amdgcn_mov_dpp(int(v), 0x39, 0xf, 0xf, false); }
+  __device__ __forceinline__ static uint32_t from2(uint32_t v) { return __builtin_amdgcn_mov_dpp(int(v), 0x4e, 0xf, 0xf, false); }
+  __device__ __forceinline__ static uint32_t from3(uint32_t v) { return __builtin_amdgcn_mov_dpp(int(v), 0x93, 0xf, 0xf, false); }
+  // the value of the quad's lane 0, and the xor over the quad
+  __device__ __forceinline__ static uint32_t lane0(uint32_t v) { return __builtin_amdgcn_mov_dpp(int(v), 0x00, 0xf, 0xf, false); }
+  __device__ __forceinline__ static uint32_t quad_xor(uint32_t v) {
+    v ^= __builtin_amdgcn_mov_dpp(int(v), 0xb1, 0xf, 0xf, false);  // lanes 1,0,3,2
+    return v ^ __builtin_amdgcn_mov_dpp(int(v), 0x4e, 0xf, 0xf, false);
+  }
+
+  // The lane's round-key words of rk: k[0] and k[10] as they are, k[1..9]
+  // rotated by 16 (the rotation the round folds in).
+  struct Keys {
+    uint32_t k[11];
+  };
+  __device__ __forceinline__ Keys keys(const AesRK &rk) const {
+    Keys o;
+#pragma unroll
+    for (int r = 0; r < 11; r++) {
+      const uint32_t w = rk.w[4 * r + int(j)];
+      o.k[r] = (r == 0 || r == 10) ? w : ((w << 16) | (w >> 16));
+    }
+    return o;
+  }
+
+  __device__ __forceinline__ uint32_t enc(uint32_t c, const Keys &k) const {
+    c ^= k.k[0];
+#pragma unroll
+    for (int r = 1; r < 10; r++) {
+      const uint32_t a = t.t0<0>(c), b = t.t1<1>(c), cc = t.t0<2>(c), d = t.t1<3>(c);
+      const uint32_t h = xor3(from2(cc), from3(d), k.k[r]);
+      c = xor3(a, from1(b), __builtin_amdgcn_alignbit(h, h, 16));
+    }
+    // last round: S[x] is byte 1 of T0[x]; the lane packs the S bytes of its own
+    // column, byte i of the new column comes from lane j + i
+    const uint32_t lo = __builtin_amdgcn_perm(t.t0<1>(c), t.t0<0>(c), 0x0c0c0501u);
+    const uint32_t hi = __builtin_amdgcn_perm(t.t0<3>(c), t.t0<2>(c), 0x0c0c0501u);
+    const uint32_t P = (hi << 16) | lo;
+    const uint32_t x01 = __builtin_amdgcn_perm(from1(P), P, 0x0c0c0500u);       // bytes 0 (own), 1 (lane j+1)
+    const uint32_t x23 = __builtin_amdgcn_perm(from3(P), from2(P), 0x07020c0cu);  // bytes 2 (lane j+2), 3 (j+3)
+    return (x01 | x23) ^ k.k[10];
+  }
+
+  // H(s) = AES_k(sigma(s)) ^ sigma(s), sigma(xL||xR) = (xL^xR)||xL, xR = words 0,1:
+  // sigma_j = s_(j^2), and ^ s_j for j >= 2
+  __device__ __forceinline__ uint32_t hash(uint32_t s, const Keys &k) const {
+    const uint32_t sg = from2(s) ^ ((j & 2u) ? s : 0u);
+    return enc(sg, k) ^ sg;
+  }
+};
+
 // NT = 0 selects the permute-addressed single table (REP must be 64); NT = 2
 // (REP 32) the interleaved pair.
 template <int NT, int REP>

@@ -43,6 +43,37 @@ __device__ __forceinline__ uint32_t dcf_eval_walk(const A &aes, uint4 s,
   return out ^ parity_above(lb, pos);
 }
 
+// The same walk on the quad-lane AES (latency-bound launches): lane j of a quad
+// holds word j of the seed, of every correction word (cw: the lane's word of
+// level 0, levels stride_words apart) and of the leaf; the control bits are bit
+// 0 of word 0 (lane 0's), and the leaf's parity above pos is the xor of the four
+// lanes' parities of their 32 bits.  Every lane of the quad returns the bit.
+__device__ __forceinline__ uint32_t dcf_eval_walk_quad(const AesQuad &aes, const AesQuad::Keys &kH,
+                                                       const AesQuad::Keys &kL, uint32_t s, int m, int L,
+                                                       const uint32_t *__restrict__ cw, size_t stride_words,
+                                                       uint32_t leaf, uint64_t x) {
+  uint32_t t = AesQuad::lane0(s) & 1u, out = 0;
+  uint32_t cnext = L > 0 ? cw[0] : 0u;
+  const bool wide = m > 32;
+  const uint32_t xlo = uint32_t(x);
+  for (int l = 0; l < L; l++) {
+    const uint32_t c = cnext;
+    if (l + 1 < L) cnext = cw[size_t(l + 1) * stride_words];
+    const int sh = m - 1 - l;
+    const uint32_t bit = wide ? uint32_t(x >> sh) & 1u : (xlo >> sh) & 1u;
+    const uint32_t sl = xor_and(aes.hash(s, kH), c, 0u - t);
+    const uint32_t tl = AesQuad::lane0(sl) & 1u;
+    out ^= (bit ^ 1u) & (tl ^ t);
+    s = xor_and(sl, s, 0u - bit);
+    t = tl ^ (t & bit);
+  }
+  const uint32_t lb = xor_and(aes.hash(s, kL), leaf, 0u - t);
+  const uint32_t pos = m >= 7 ? uint32_t(x & 127u) : uint32_t(x);
+  const uint32_t lo = 32u * aes.j;
+  const uint32_t msk = pos < lo ? 0xffffffffu : (pos >= lo + 31 ? 0u : 0xffffffffu << (pos - lo + 1));
+  return out ^ (AesQuad::quad_xor(__popc(lb & msk) & 1u) & 1u);
+}
+
 struct DcfGenOut {
   uint4 s0;      // party 0's final on-path seed
   uint32_t t0;   // party 0's final on-path control bit

@@ -201,6 +201,100 @@ __device__ __forceinline__ void tr_eval_tiles(const TrArgs<T> &a, const TrArgs<T
   }
 }
 
+// ---- quad-lane form (latency-bound launches, AesPerm2 table) ----
+// The DCF walks of tr_dcf_bits with four lanes per element and party (lane j of
+// the quad reads word j of the roots, correction words and leaves).
+template <typename T>
+__device__ __forceinline__ void tr_dcf_bits_quad(const AesQuad &aes, const AesQuad::Keys &kH,
+                                                 const AesQuad::Keys &kL, const TrArgs<T> &a, const uint8_t *K,
+                                                 const uint8_t *KC, size_t i, T xp, uint32_t *ra, uint32_t *rb) {
+  const T lowmask = (T(1) << a.sb) - T(1);
+  const T smask = (T(1) << a.s) - T(1);
+  const size_t w = 4 * i + aes.j, sw = 4 * a.N;
+  if (a.use_a) {
+    *ra = dcf_eval_walk_quad(aes, kH, kL, reinterpret_cast<const uint32_t *>(K + a.a.off_root)[w], a.a.m, a.a.L,
+                             reinterpret_cast<const uint32_t *>(KC + a.a.off_cw) + w, sw,
+                             reinterpret_cast<const uint32_t *>(KC + a.a.off_leaf)[w], uint64_t(xp & lowmask));
+    *ra ^= get_bit(reinterpret_cast<const uint64_t *>(K + a.a.off_z), i);
+  }
+  if (a.use_b) {
+    *rb = dcf_eval_walk_quad(aes, kH, kL, reinterpret_cast<const uint32_t *>(K + a.b.off_root)[w], a.b.m, a.b.L,
+                             reinterpret_cast<const uint32_t *>(KC + a.b.off_cw) + w, sw,
+                             reinterpret_cast<const uint32_t *>(KC + a.b.off_leaf)[w], uint64_t(xp & smask));
+    *rb ^= get_bit(reinterpret_cast<const uint64_t *>(K + a.b.off_z), i);
+  }
+}
+
+// tr_tile with a quad of lanes per element and party: the quad's lanes carry the
+// same bits, so an element's bit in a ballot word is at its quad's first lane;
+// every lane of the quad forms the message, the first one writes it.
+template <typename T>
+__device__ __forceinline__ T tr_tile_quad(const AesQuad &aes, const AesQuad::Keys &kH, const AesQuad::Keys &kL,
+                                          const TrArgs<T> &a, TrXchg<T> &x, int p, int e, int wv, const uint8_t *K,
+                                          const uint8_t *KC, size_t i, bool in, T xh) {
+  uint32_t ra = 0, rb = 0;
+  T xp = 0;
+  if (in) {
+    xp = tr_shifted_input(a, i, xh);
+    tr_dcf_bits_quad(aes, kH, kL, a, K, KC, i, xp, &ra, &rb);
+  }
+  const uint64_t wa = __ballot(ra), wb = __ballot(rb);
+  if (lane_id() == 0) {
+    x.xa[p][wv] = wa;
+    x.xb[p][wv] = wb;
+  }
+  __syncthreads();
+  const uint32_t q0 = lane_id() & ~3u;
+  if (in) {
+    const uint32_t hb = uint32_t(xp >> a.sb) & 1u;
+    const uint32_t bh = a.use_a ? uint32_t((x.xa[0][wv] ^ x.xa[1][wv]) >> q0) & 1u : 0u;
+    const uint32_t dh = a.use_b ? uint32_t((x.xb[0][wv] ^ x.xb[1][wv]) >> q0) & 1u : 0u;
+    const T msg = tr_out_share(a, p, K, i, xh, xp, hb, bh, dh);
+    if ((lane_id() & 3u) == 0) x.xm[p][e] = msg;
+  }
+  __syncthreads();
+  const T y = in ? T(x.xm[0][e] + x.xm[1][e]) : T(0);
+  __syncthreads();
+  return y;
+}
+
+// The tiles of a quad-lane launch: a workgroup of 2 * 4h threads takes tiles of
+// h elements, the first 4h threads party 0 (four consecutive lanes per element),
+// the last 4h party 1.
+template <typename T, bool TWO>
+__device__ __forceinline__ void tr_eval_tiles_quad(const TrArgs<T> &a, const TrArgs<T> &a2) {
+  __shared__ __align__(16) uint32_t lds[AesPerm2::kWords];
+  __shared__ TrXchg<T> x;
+  AesPerm2::fill(lds);
+  const AesPerm2 tab(lds);
+  const AesQuad aes(tab);
+  const AesQuad::Keys kH = aes.keys(c_rkH), kL = aes.keys(c_rkL);
+  const int hq = int(blockDim.x) / 2, h = hq / 4;
+  const int p = int(threadIdx.x) >= hq ? 1 : 0;
+  const int lt = int(threadIdx.x) - p * hq;  // thread of the party's half
+  const int e = lt >> 2, wv = lt >> 6;
+  const uint8_t *K = p ? a.k1 : a.k0, *KC = a.k0;
+  const size_t stride = size_t(gridDim.x) * size_t(h);
+  for (size_t base = size_t(blockIdx.x) * h; base < a.N; base += stride) {
+    const size_t i = base + size_t(e);
+    const bool in = i < a.N;
+    T y = tr_tile_quad(aes, kH, kL, a, x, p, e, wv, K, KC, i, in, in ? a.xhat[i] : T(0));
+    if constexpr (TWO) y = tr_tile_quad(aes, kH, kL, a2, x, p, e, wv, K, KC, i, in, y);
+    if (p == 0 && in && (lt & 3) == 0) a.out[i] = y;
+  }
+}
+
+template <typename T, int TAG>
+__global__ void k_tr_eval_q(TrArgs<T> a) {
+  if (a.prio) __builtin_amdgcn_s_setprio(2);
+  tr_eval_tiles_quad<T, false>(a, a);
+}
+template <typename T, int TAG>
+__global__ void k_tr_eval2_q(TrArgs<T> a, TrArgs<T> a2) {
+  if (a.prio) __builtin_amdgcn_s_setprio(2);
+  tr_eval_tiles_quad<T, true>(a, a2);
+}
+
 template <typename T, int NT, int REP, int TAG>
 __global__ void k_tr_eval(TrArgs<T> a) {
   if (a.prio) __builtin_amdgcn_s_setprio(2);
@@ -426,6 +520,19 @@ static int tr_eval_block(const Launch &L, size_t n) {
   return int(std::min<size_t>(size_t(b), 2 * h));
 }
 
+// Quad-lane evaluation: a spread small launch (Launch::spread_small) with the
+// default T0/T1 table whose elements fit one 256-thread workgroup (32 elements)
+// per CU, so that every element's AES rounds run on four lanes.
+constexpr int kQuadBlock = 256, kQuadElems = kQuadBlock / 8;
+static bool use_quad(const Launch &L, size_t n) {
+  if (!L.spread_small || L.aes_block != 0) return false;
+  int nv;
+  const AesVariant *v = aes_variants(&nv);
+  const int vi = L.aes_variant >= 0 && L.aes_variant < nv ? L.aes_variant : 0;
+  return v[vi].nt == 2 && v[vi].rep == 32 && n <= size_t(L.num_cu) * kQuadElems;
+}
+static int quad_grid(size_t n) { return int((n + kQuadElems - 1) / kQuadElems); }
+
 template <typename T>
 hipError_t launch_tr_eval(const Launch &L, const TrLayout &lay, const uint8_t *k0, const uint8_t *k1, const T *xhat,
                           const T *bias, int bias_ncol, T *out) {
@@ -438,6 +545,13 @@ hipError_t launch_tr_eval(const Launch &L, const TrLayout &lay, const uint8_t *k
   a.bias_ncol = bias_ncol > 0 ? bias_ncol : 1;
   a.out = out;
   a.prio = lay.N < kTrPrioN;
+  if (use_quad(L, lay.N)) {
+    if (L.profiled)
+      hipLaunchKernelGGL((k_tr_eval_q<T, 1>), dim3(quad_grid(lay.N)), dim3(kQuadBlock), 0, L.stream, a);
+    else
+      hipLaunchKernelGGL((k_tr_eval_q<T, 0>), dim3(quad_grid(lay.N)), dim3(kQuadBlock), 0, L.stream, a);
+    return hipGetLastError();
+  }
   return with_variant(L, [&](auto v) {
     constexpr int NT = decltype(v)::nt, REP = decltype(v)::rep;
     const int block = tr_eval_block(L, lay.N);
@@ -464,6 +578,13 @@ hipError_t launch_tr_eval2(const Launch &L, const TrLayout &lay, const TrLayout 
   a.bias_ncol = bias_ncol > 0 ? bias_ncol : 1;
   a.out = out;
   a.prio = lay.N < kTrPrioN;
+  if (use_quad(L, lay.N)) {
+    if (L.profiled)
+      hipLaunchKernelGGL((k_tr_eval2_q<T, 1>), dim3(quad_grid(lay.N)), dim3(kQuadBlock), 0, L.stream, a, a2);
+    else
+      hipLaunchKernelGGL((k_tr_eval2_q<T, 0>), dim3(quad_grid(lay.N)), dim3(kQuadBlock), 0, L.stream, a, a2);
+    return hipGetLastError();
+  }
   return with_variant(L, [&](auto v) {
     constexpr int NT = decltype(v)::nt, REP = decltype(v)::rep;
     const int block = tr_eval_block(L, lay.N);
