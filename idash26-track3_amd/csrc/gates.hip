@@ -521,15 +521,17 @@ static int tr_eval_block(const Launch &L, size_t n) {
 }
 
 // Quad-lane evaluation: a spread small launch (Launch::spread_small) with the
-// default T0/T1 table whose elements fit one 256-thread workgroup (32 elements)
-// per CU, so that every element's AES rounds run on four lanes.
+// default T0/T1 table whose elements fit two 256-thread workgroups (32 elements
+// each; both fit a CU's LDS) per CU, so that every element's AES rounds run on
+// four lanes (at B = 1: 0.566 ms per forward against 0.609 with one workgroup
+// per CU and 0.570 with four).
 constexpr int kQuadBlock = 256, kQuadElems = kQuadBlock / 8;
 static bool use_quad(const Launch &L, size_t n) {
   if (!L.spread_small || L.aes_block != 0) return false;
   int nv;
   const AesVariant *v = aes_variants(&nv);
   const int vi = L.aes_variant >= 0 && L.aes_variant < nv ? L.aes_variant : 0;
-  return v[vi].nt == 2 && v[vi].rep == 32 && n <= size_t(L.num_cu) * kQuadElems;
+  return v[vi].nt == 2 && v[vi].rep == 32 && n <= size_t(L.num_cu) * 2 * kQuadElems;
 }
 static int quad_grid(size_t n) { return int((n + kQuadElems - 1) / kQuadElems); }
 
