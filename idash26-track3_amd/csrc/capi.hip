@@ -519,7 +519,7 @@ mpcx_status mpcx_maxpool_keygen(mpcx_ctx *c, int B, int N, int C, const void *in
 
 // Per level: the pair differences (local), one RELU gate (two exchange rounds),
 // and max(a, b) = a + ReLU(b - a) (local), on planes (B, R, C) that shrink to
-// (B, 1, C).
+// (B, 1, C); with both parties here one gate launch per level does all three.
 template <typename T>
 static hipError_t maxpool_eval_run(mpcx_ctx *c, int B, int N, int C, const void *k0, const void *k1, const void *in,
                                    void *out, void *work) {
@@ -534,9 +534,18 @@ static hipError_t maxpool_eval_run(mpcx_ctx *c, int B, int N, int C, const void 
   int R = N;
   for (int l = 0; l < Lv; l++) {
     const size_t n = size_t(B) * pairs[l] * C;
-    hipError_t e = launch_pool_diff<T>(c->L, B, R, C, cur, d);
-    if (e == hipSuccess) e = tr_eval_run<T>(c, lay[l], n, K0, K1, d, nullptr, 1, y);
-    if (e == hipSuccess) e = launch_pool_combine<T>(c->L, B, R, C, cur, y, nullptr, nxt);
+    hipError_t e;
+    if (c->L.party < 0 && rows < (size_t(1) << 32)) {
+      e = launch_tr_eval_pool<T>(c->L, lay[l], K0, K1, B, R, C, cur, nxt);
+      if (e == hipSuccess) {
+        c->counters.bitplanes(n, int(lay[l].use_a) + int(lay[l].use_b));
+        c->counters.msg(n, c->bw);
+      }
+    } else {
+      e = launch_pool_diff<T>(c->L, B, R, C, cur, d);
+      if (e == hipSuccess) e = tr_eval_run<T>(c, lay[l], n, K0, K1, d, nullptr, 1, y);
+      if (e == hipSuccess) e = launch_pool_combine<T>(c->L, B, R, C, cur, y, nullptr, nxt);
+    }
     if (e != hipSuccess) return e;
     cur = nxt;
     nxt = nxt == va ? vb : va;

@@ -48,7 +48,34 @@ struct TrArgs {
   T *out_mask;
   uint32_t gate;
   int prio;  // eval: the launch's waves raise their issue priority (a small gate)
+  // eval in the max-pool form (pv set): element i is pair j of block b, column c
+  // (i = (b pr + j) C + c) of the level's rows pv (R rows of C per block); its
+  // masked input is pv[2j+1] - pv[2j] and party 0 writes pv[2j] + y into row j
+  // of the next level pvn (R / 2 + R % 2 rows per block), the odd last row carried
+  uint32_t pR = 0, pC = 0, ppr = 0, pB = 0;
+  const T *pv = nullptr;
+  T *pvn = nullptr;
 };
+
+// The max-pool form's element i: offset of row 2j of its pair in pv, and of its
+// row j in pvn.
+template <typename T>
+__device__ __forceinline__ uint32_t pool_src(const TrArgs<T> &a, uint32_t i, uint32_t *o) {
+  const uint32_t C = a.pC, pr = a.ppr, Rn = pr + (a.pR & 1u);
+  const uint32_t bj = i / C, c = i - bj * C, b = bj / pr, j = bj - b * pr;
+  *o = (b * Rn + j) * C + c;
+  return (b * a.pR + 2 * j) * C + c;
+}
+// The carried last rows of an odd level (all threads of the launch share them).
+template <typename T>
+__device__ __forceinline__ void pool_carry(const TrArgs<T> &a) {
+  if (!a.pv || !(a.pR & 1u)) return;
+  const uint32_t C = a.pC, pr = a.ppr, Rn = pr + 1, nc = a.pB * C;
+  for (uint32_t k = blockIdx.x * blockDim.x + threadIdx.x; k < nc; k += gridDim.x * blockDim.x) {
+    const uint32_t b = k / C, c = k - b * C;
+    a.pvn[(b * Rn + pr) * C + c] = a.pv[(b * a.pR + a.pR - 1) * C + c];
+  }
+}
 
 __device__ __forceinline__ bool relu_like(int kind) {
   return kind == G_RELU || kind == G_RELUSLACK || kind == G_RELUPOOL;
@@ -195,10 +222,27 @@ __device__ __forceinline__ void tr_eval_tiles(const TrArgs<T> &a, const TrArgs<T
   for (size_t base = size_t(blockIdx.x) * h; base < a.N; base += stride) {
     const size_t i = base + size_t(e);
     const bool in = i < a.N;
-    T y = tr_tile(aes, a, x, p, e, wv, K, KC, i, in, in ? a.xhat[i] : T(0));
+    T xin = 0, v0 = 0;
+    uint32_t o = 0;
+    if (in) {
+      if (a.pv) {
+        const uint32_t s0 = pool_src(a, uint32_t(i), &o);
+        v0 = a.pv[s0];
+        xin = a.pv[s0 + a.pC] - v0;
+      } else {
+        xin = a.xhat[i];
+      }
+    }
+    T y = tr_tile(aes, a, x, p, e, wv, K, KC, i, in, xin);
     if constexpr (TWO) y = tr_tile(aes, a2, x, p, e, wv, K, KC, i, in, y);
-    if (p == 0 && in) a.out[i] = y;
+    if (p == 0 && in) {
+      if (a.pv)
+        a.pvn[o] = v0 + y;
+      else
+        a.out[i] = y;
+    }
   }
+  pool_carry(a);
 }
 
 // ---- quad-lane form (latency-bound launches, AesPerm2 table) ----
@@ -278,10 +322,27 @@ __device__ __forceinline__ void tr_eval_tiles_quad(const TrArgs<T> &a, const TrA
   for (size_t base = size_t(blockIdx.x) * h; base < a.N; base += stride) {
     const size_t i = base + size_t(e);
     const bool in = i < a.N;
-    T y = tr_tile_quad(aes, kH, kL, a, x, p, e, wv, K, KC, i, in, in ? a.xhat[i] : T(0));
+    T xin = 0, v0 = 0;
+    uint32_t o = 0;
+    if (in) {
+      if (a.pv) {
+        const uint32_t s0 = pool_src(a, uint32_t(i), &o);
+        v0 = a.pv[s0];
+        xin = a.pv[s0 + a.pC] - v0;
+      } else {
+        xin = a.xhat[i];
+      }
+    }
+    T y = tr_tile_quad(aes, kH, kL, a, x, p, e, wv, K, KC, i, in, xin);
     if constexpr (TWO) y = tr_tile_quad(aes, kH, kL, a2, x, p, e, wv, K, KC, i, in, y);
-    if (p == 0 && in && (lt & 3) == 0) a.out[i] = y;
+    if (p == 0 && in && (lt & 3) == 0) {
+      if (a.pv)
+        a.pvn[o] = v0 + y;
+      else
+        a.out[i] = y;
+    }
   }
+  pool_carry(a);
 }
 
 template <typename T, int TAG>
@@ -535,6 +596,31 @@ static bool use_quad(const Launch &L, size_t n) {
 }
 static int quad_grid(size_t n) { return int((n + kQuadElems - 1) / kQuadElems); }
 
+// One gate evaluation of both parties with prepared arguments (launch_tr_eval and
+// its max-pool form).
+template <typename T>
+static hipError_t tr_eval_launch(const Launch &L, const TrArgs<T> &a) {
+  if (use_quad(L, a.N)) {
+    if (L.profiled)
+      hipLaunchKernelGGL((k_tr_eval_q<T, 1>), dim3(quad_grid(a.N)), dim3(kQuadBlock), 0, L.stream, a);
+    else
+      hipLaunchKernelGGL((k_tr_eval_q<T, 0>), dim3(quad_grid(a.N)), dim3(kQuadBlock), 0, L.stream, a);
+    return hipGetLastError();
+  }
+  return with_variant(L, [&](auto v) {
+    constexpr int NT = decltype(v)::nt, REP = decltype(v)::rep;
+    const int block = tr_eval_block(L, a.N);
+    // a workgroup holds both parties' threads for block/2 elements
+    if (block < 128 || block > 2 * kTrMaxTile || block % 128 != 0) return hipErrorInvalidConfiguration;
+    const int grid = grid_for(k_tr_eval<T, NT, REP, 0>, block, 2 * a.N, L.num_cu);
+    if (L.profiled)
+      hipLaunchKernelGGL((k_tr_eval<T, NT, REP, 1>), dim3(grid), dim3(block), 0, L.stream, a);
+    else
+      hipLaunchKernelGGL((k_tr_eval<T, NT, REP, 0>), dim3(grid), dim3(block), 0, L.stream, a);
+    return hipGetLastError();
+  });
+}
+
 template <typename T>
 hipError_t launch_tr_eval(const Launch &L, const TrLayout &lay, const uint8_t *k0, const uint8_t *k1, const T *xhat,
                           const T *bias, int bias_ncol, T *out) {
@@ -547,25 +633,27 @@ hipError_t launch_tr_eval(const Launch &L, const TrLayout &lay, const uint8_t *k
   a.bias_ncol = bias_ncol > 0 ? bias_ncol : 1;
   a.out = out;
   a.prio = lay.N < kTrPrioN;
-  if (use_quad(L, lay.N)) {
-    if (L.profiled)
-      hipLaunchKernelGGL((k_tr_eval_q<T, 1>), dim3(quad_grid(lay.N)), dim3(kQuadBlock), 0, L.stream, a);
-    else
-      hipLaunchKernelGGL((k_tr_eval_q<T, 0>), dim3(quad_grid(lay.N)), dim3(kQuadBlock), 0, L.stream, a);
-    return hipGetLastError();
-  }
-  return with_variant(L, [&](auto v) {
-    constexpr int NT = decltype(v)::nt, REP = decltype(v)::rep;
-    const int block = tr_eval_block(L, lay.N);
-    // a workgroup holds both parties' threads for block/2 elements
-    if (block < 128 || block > 2 * kTrMaxTile || block % 128 != 0) return hipErrorInvalidConfiguration;
-    const int grid = grid_for(k_tr_eval<T, NT, REP, 0>, block, 2 * lay.N, L.num_cu);
-    if (L.profiled)
-      hipLaunchKernelGGL((k_tr_eval<T, NT, REP, 1>), dim3(grid), dim3(block), 0, L.stream, a);
-    else
-      hipLaunchKernelGGL((k_tr_eval<T, NT, REP, 0>), dim3(grid), dim3(block), 0, L.stream, a);
-    return hipGetLastError();
-  });
+  return tr_eval_launch(L, a);
+}
+
+template <typename T>
+hipError_t launch_tr_eval_pool(const Launch &L, const TrLayout &lay, const uint8_t *k0, const uint8_t *k1, int B,
+                               int R, int C, const T *V, T *Vn) {
+  if (lay.bw != int(8 * sizeof(T)) || B < 1 || R < 2 || C < 1 || lay.N != size_t(B) * (R / 2) * C ||
+      size_t(B) * R * C >= (size_t(1) << 32))
+    return hipErrorInvalidValue;
+  TrArgs<T> a = tr_args<T>(lay);
+  a.k0 = k0;
+  a.k1 = k1;
+  a.bias_ncol = 1;
+  a.prio = lay.N < kTrPrioN;
+  a.pB = uint32_t(B);
+  a.pR = uint32_t(R);
+  a.pC = uint32_t(C);
+  a.ppr = uint32_t(R / 2);
+  a.pv = V;
+  a.pvn = Vn;
+  return tr_eval_launch(L, a);
 }
 
 template <typename T>
@@ -702,6 +790,8 @@ hipError_t launch_tr_expand(const Launch &L, const TrLayout &lay, const uint8_t 
                                           uint8_t *);                                                                 \
   template hipError_t launch_tr_eval<T>(const Launch &, const TrLayout &, const uint8_t *, const uint8_t *,           \
                                         const T *, const T *, int, T *);                                              \
+  template hipError_t launch_tr_eval_pool<T>(const Launch &, const TrLayout &, const uint8_t *, const uint8_t *, int, \
+                                             int, int, const T *, T *);                                               \
   template hipError_t launch_tr_eval2<T>(const Launch &, const TrLayout &, const TrLayout &, const uint8_t *,         \
                                          const uint8_t *, const T *, const T *, int, T *);                            \
   template hipError_t launch_tr_party_bits<T>(const Launch &, const TrLayout &, const uint8_t *, const T *,           \

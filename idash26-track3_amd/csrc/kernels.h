@@ -86,6 +86,16 @@ template <typename T>
 hipError_t launch_tr_eval(const Launch &L, const TrLayout &lay, const uint8_t *k0, const uint8_t *k1,
                           const T *xhat, const T *bias, int bias_ncol, T *yhat);
 
+// One level of the max-pool tree, max(a, b) = a + ReLU(b - a), as one gate
+// launch of both parties: the gate (lay, N = B (R/2) C elements) evaluates the
+// pair differences V[b][2j+1][c] - V[b][2j][c] of the R rows of C words of each
+// of B blocks, and party 0's threads write V[b][2j][c] + y into row j of Vn
+// (R/2 + R%2 rows per block; an odd level's last row is carried).  Requires
+// B R C < 2^32; V and Vn distinct.
+template <typename T>
+hipError_t launch_tr_eval_pool(const Launch &L, const TrLayout &lay, const uint8_t *k0, const uint8_t *k1, int B,
+                               int R, int C, const T *V, T *Vn);
+
 // Two gates of the same element count in one launch: lay on xhat (with the
 // bias), then lay2 on lay's revealed output, which never leaves the launch;
 // lay2's revealed output in out.  The model's truncations (TRMOD, then EXT or

@@ -325,6 +325,35 @@ struct Runner {
     return hipSuccess;
   }
 
+  // One level of the max-pool tree over B blocks of R rows of C words, V -> Vn
+  // (max(a, b) = a + ReLU(b - a) over the row pairs, an odd last row carried).
+  // In a latency-bound lane (Launch::spread_small) with both parties here the
+  // gate launch forms the pair differences and writes the next level itself;
+  // otherwise the differences (into D), the gate (into Y) and the combination
+  // run apart (in party mode around the gate's exchanges; in lanes of more
+  // samples one launch per level measured up to 1.6% slower at B = 64).
+  hipError_t pool_level(int kind, int B, int R, int C, const T *V, T *D, T *Y, T *Vn) {
+    const size_t n = size_t(B) * (R / 2) * C;
+    if (party_mode() || !L.spread_small || size_t(B) * R * C >= (size_t(1) << 32)) {
+      TRY(launch_pool_diff<T>(L, B, R, C, V, D));
+      TRY(tr(kind, n, D, nullptr, 1, Y));
+      return launch_pool_combine<T>(L, B, R, C, V, Y, nullptr, Vn);
+    }
+    const size_t end = tr_layout(kind, bw, s, n, c.off).end;
+    size_t b;
+    TRY(enter(end, &b));
+    TrLayout lay = tr_layout(kind, bw, s, n, b);
+    hipEvent_t e0 = nullptr, e1 = nullptr;
+    Launch L1 = L;
+    TRY(time_begin(&e0, &e1, &L1));
+    TRY(launch_tr_eval_pool<T>(L1, lay, kv.k[0], kv.k[1], B, R, C, V, Vn));
+    TRY(time_end(e0, e1, n, tr_levels(lay), tr_key_bytes(lay)));
+    ctr.bitplanes(n, int(lay.use_a) + int(lay.use_b));
+    ctr.msg(n, bw);
+    leave(end);
+    return hipSuccess;
+  }
+
   hipError_t mul(size_t nx, size_t ny, size_t nz, const MulMap &map, const T *x, const T *y, T *out) {
     const size_t end = mul_layout(bw, nx, ny, nz, c.off).end;
     size_t b;
@@ -1626,10 +1655,7 @@ class Model final : public ModelBase, KeySource {
     int R = N;
     for (int l = 0; l < Lv; l++) {
       const int pr = pairs[l];
-      const size_t En = size_t(B) * pr * C;
-      TRY(launch_pool_diff<T>(L_, B, R, C, cur, Z));
-      TRY(r.tr(pool_kind(), En, Z, nullptr, 1, XW));
-      TRY(launch_pool_combine<T>(L_, B, R, C, cur, XW, nullptr, nxt));
+      TRY(r.pool_level(pool_kind(), B, R, C, cur, Z, XW, nxt));
       std::swap(cur, nxt);
       R = pr + (R & 1);
     }
