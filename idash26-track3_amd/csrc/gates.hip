@@ -48,32 +48,35 @@ struct TrArgs {
   T *out_mask;
   uint32_t gate;
   int prio;  // eval: the launch's waves raise their issue priority (a small gate)
-  // eval in the max-pool form (pv set): element i is pair j of block b, column c
-  // (i = (b pr + j) C + c) of the level's rows pv (R rows of C per block); its
-  // masked input is pv[2j+1] - pv[2j] and party 0 writes pv[2j] + y into row j
-  // of the next level pvn (R / 2 + R % 2 rows per block), the odd last row carried
-  uint32_t pR = 0, pC = 0, ppr = 0, pB = 0;
-  const T *pv = nullptr;
-  T *pvn = nullptr;
 };
 
-// The max-pool form's element i: offset of row 2j of its pair in pv, and of its
-// row j in pvn.
+// A gate evaluation in the max-pool form: element i is pair j of block b, column
+// c (i = (b pr + j) C + c) of the level's rows v (R rows of C per block); its
+// masked input is v[2j+1] - v[2j] and party 0 writes v[2j] + y into row j of the
+// next level vn (R / 2 + R % 2 rows per block), the odd last row carried.  The
+// regular instances take no such argument and compile without it.
 template <typename T>
-__device__ __forceinline__ uint32_t pool_src(const TrArgs<T> &a, uint32_t i, uint32_t *o) {
-  const uint32_t C = a.pC, pr = a.ppr, Rn = pr + (a.pR & 1u);
+struct TrPool {
+  uint32_t R = 0, C = 0, pr = 0, B = 0;
+  const T *v = nullptr;
+  T *vn = nullptr;
+};
+// offset of row 2j of element i's pair in v, and of its row j in vn
+template <typename T>
+__device__ __forceinline__ uint32_t pool_src(const TrPool<T> &q, uint32_t i, uint32_t *o) {
+  const uint32_t C = q.C, pr = q.pr, Rn = pr + (q.R & 1u);
   const uint32_t bj = i / C, c = i - bj * C, b = bj / pr, j = bj - b * pr;
   *o = (b * Rn + j) * C + c;
-  return (b * a.pR + 2 * j) * C + c;
+  return (b * q.R + 2 * j) * C + c;
 }
 // The carried last rows of an odd level (all threads of the launch share them).
 template <typename T>
-__device__ __forceinline__ void pool_carry(const TrArgs<T> &a) {
-  if (!a.pv || !(a.pR & 1u)) return;
-  const uint32_t C = a.pC, pr = a.ppr, Rn = pr + 1, nc = a.pB * C;
+__device__ __forceinline__ void pool_carry(const TrPool<T> &q) {
+  if (!(q.R & 1u)) return;
+  const uint32_t C = q.C, pr = q.pr, Rn = pr + 1, nc = q.B * C;
   for (uint32_t k = blockIdx.x * blockDim.x + threadIdx.x; k < nc; k += gridDim.x * blockDim.x) {
     const uint32_t b = k / C, c = k - b * C;
-    a.pvn[(b * Rn + pr) * C + c] = a.pv[(b * a.pR + a.pR - 1) * C + c];
+    q.vn[(b * Rn + pr) * C + c] = q.v[(b * q.R + q.R - 1) * C + c];
   }
 }
 
@@ -204,8 +207,8 @@ __device__ __forceinline__ T tr_tile(Aes &aes, const TrArgs<T> &a, TrXchg<T> &x,
 // The tiles of one launch: gate a on x^, then (TWO) gate a2 on a's revealed
 // output, which both parties hold once it is revealed; party 0's threads write
 // the last gate's revealed output.
-template <typename T, int NT, int REP, bool TWO>
-__device__ __forceinline__ void tr_eval_tiles(const TrArgs<T> &a, const TrArgs<T> &a2) {
+template <typename T, int NT, int REP, bool TWO, bool POOL>
+__device__ __forceinline__ void tr_eval_tiles(const TrArgs<T> &a, const TrArgs<T> &a2, const TrPool<T> &q) {
   __shared__ __align__(16) uint32_t lds[AesLds<NT, REP>::kWords];
   __shared__ TrXchg<T> x;
   AesLds<NT, REP>::fill(lds);
@@ -225,10 +228,10 @@ __device__ __forceinline__ void tr_eval_tiles(const TrArgs<T> &a, const TrArgs<T
     T xin = 0, v0 = 0;
     uint32_t o = 0;
     if (in) {
-      if (a.pv) {
-        const uint32_t s0 = pool_src(a, uint32_t(i), &o);
-        v0 = a.pv[s0];
-        xin = a.pv[s0 + a.pC] - v0;
+      if constexpr (POOL) {
+        const uint32_t s0 = pool_src(q, uint32_t(i), &o);
+        v0 = q.v[s0];
+        xin = q.v[s0 + q.C] - v0;
       } else {
         xin = a.xhat[i];
       }
@@ -236,13 +239,13 @@ __device__ __forceinline__ void tr_eval_tiles(const TrArgs<T> &a, const TrArgs<T
     T y = tr_tile(aes, a, x, p, e, wv, K, KC, i, in, xin);
     if constexpr (TWO) y = tr_tile(aes, a2, x, p, e, wv, K, KC, i, in, y);
     if (p == 0 && in) {
-      if (a.pv)
-        a.pvn[o] = v0 + y;
+      if constexpr (POOL)
+        q.vn[o] = v0 + y;
       else
         a.out[i] = y;
     }
   }
-  pool_carry(a);
+  if constexpr (POOL) pool_carry(q);
 }
 
 // ---- quad-lane form (latency-bound launches, AesPerm2 table) ----
@@ -305,8 +308,8 @@ __device__ __forceinline__ T tr_tile_quad(const AesQuad &aes, const AesQuad::Key
 // The tiles of a quad-lane launch: a workgroup of 2 * 4h threads takes tiles of
 // h elements, the first 4h threads party 0 (four consecutive lanes per element),
 // the last 4h party 1.
-template <typename T, bool TWO>
-__device__ __forceinline__ void tr_eval_tiles_quad(const TrArgs<T> &a, const TrArgs<T> &a2) {
+template <typename T, bool TWO, bool POOL>
+__device__ __forceinline__ void tr_eval_tiles_quad(const TrArgs<T> &a, const TrArgs<T> &a2, const TrPool<T> &q) {
   __shared__ __align__(16) uint32_t lds[AesPerm2::kWords];
   __shared__ TrXchg<T> x;
   AesPerm2::fill(lds);
@@ -325,10 +328,10 @@ __device__ __forceinline__ void tr_eval_tiles_quad(const TrArgs<T> &a, const TrA
     T xin = 0, v0 = 0;
     uint32_t o = 0;
     if (in) {
-      if (a.pv) {
-        const uint32_t s0 = pool_src(a, uint32_t(i), &o);
-        v0 = a.pv[s0];
-        xin = a.pv[s0 + a.pC] - v0;
+      if constexpr (POOL) {
+        const uint32_t s0 = pool_src(q, uint32_t(i), &o);
+        v0 = q.v[s0];
+        xin = q.v[s0 + q.C] - v0;
       } else {
         xin = a.xhat[i];
       }
@@ -336,30 +339,42 @@ __device__ __forceinline__ void tr_eval_tiles_quad(const TrArgs<T> &a, const TrA
     T y = tr_tile_quad(aes, kH, kL, a, x, p, e, wv, K, KC, i, in, xin);
     if constexpr (TWO) y = tr_tile_quad(aes, kH, kL, a2, x, p, e, wv, K, KC, i, in, y);
     if (p == 0 && in && (lt & 3) == 0) {
-      if (a.pv)
-        a.pvn[o] = v0 + y;
+      if constexpr (POOL)
+        q.vn[o] = v0 + y;
       else
         a.out[i] = y;
     }
   }
-  pool_carry(a);
+  if constexpr (POOL) pool_carry(q);
 }
 
 template <typename T, int TAG>
 __global__ void k_tr_eval_q(TrArgs<T> a) {
   if (a.prio) __builtin_amdgcn_s_setprio(2);
-  tr_eval_tiles_quad<T, false>(a, a);
+  tr_eval_tiles_quad<T, false, false>(a, a, TrPool<T>{});
 }
 template <typename T, int TAG>
 __global__ void k_tr_eval2_q(TrArgs<T> a, TrArgs<T> a2) {
   if (a.prio) __builtin_amdgcn_s_setprio(2);
-  tr_eval_tiles_quad<T, true>(a, a2);
+  tr_eval_tiles_quad<T, true, false>(a, a2, TrPool<T>{});
+}
+template <typename T, int TAG>
+__global__ void k_tr_eval_pool_q(TrArgs<T> a, TrPool<T> q) {
+  if (a.prio) __builtin_amdgcn_s_setprio(2);
+  tr_eval_tiles_quad<T, false, true>(a, a, q);
 }
 
 template <typename T, int NT, int REP, int TAG>
 __global__ void k_tr_eval(TrArgs<T> a) {
   if (a.prio) __builtin_amdgcn_s_setprio(2);
-  tr_eval_tiles<T, NT, REP, false>(a, a);
+  tr_eval_tiles<T, NT, REP, false, false>(a, a, TrPool<T>{});
+}
+
+// The max-pool form (TrPool) of k_tr_eval.
+template <typename T, int NT, int REP, int TAG>
+__global__ void k_tr_eval_pool(TrArgs<T> a, TrPool<T> q) {
+  if (a.prio) __builtin_amdgcn_s_setprio(2);
+  tr_eval_tiles<T, NT, REP, false, true>(a, a, q);
 }
 
 // Two gates of one element count in one launch (a truncation and its extension):
@@ -369,7 +384,7 @@ __global__ void k_tr_eval(TrArgs<T> a) {
 template <typename T, int NT, int REP, int TAG>
 __global__ void k_tr_eval2(TrArgs<T> a, TrArgs<T> a2) {
   if (a.prio) __builtin_amdgcn_s_setprio(2);
-  tr_eval_tiles<T, NT, REP, true>(a, a2);
+  tr_eval_tiles<T, NT, REP, true, false>(a, a2, TrPool<T>{});
 }
 
 // Party mode, phase 1: party p's masked DCF output bits (one ballot word per
@@ -596,15 +611,18 @@ static bool use_quad(const Launch &L, size_t n) {
 }
 static int quad_grid(size_t n) { return int((n + kQuadElems - 1) / kQuadElems); }
 
-// One gate evaluation of both parties with prepared arguments (launch_tr_eval and
-// its max-pool form).
+// One gate evaluation of both parties with prepared arguments: the regular
+// kernels, or (q set) their max-pool form.
 template <typename T>
-static hipError_t tr_eval_launch(const Launch &L, const TrArgs<T> &a) {
+static hipError_t tr_eval_launch(const Launch &L, const TrArgs<T> &a, const TrPool<T> *q) {
   if (use_quad(L, a.N)) {
-    if (L.profiled)
-      hipLaunchKernelGGL((k_tr_eval_q<T, 1>), dim3(quad_grid(a.N)), dim3(kQuadBlock), 0, L.stream, a);
+    const dim3 grid(quad_grid(a.N)), block(kQuadBlock);
+    if (q)
+      hipLaunchKernelGGL((k_tr_eval_pool_q<T, 0>), grid, block, 0, L.stream, a, *q);
+    else if (L.profiled)
+      hipLaunchKernelGGL((k_tr_eval_q<T, 1>), grid, block, 0, L.stream, a);
     else
-      hipLaunchKernelGGL((k_tr_eval_q<T, 0>), dim3(quad_grid(a.N)), dim3(kQuadBlock), 0, L.stream, a);
+      hipLaunchKernelGGL((k_tr_eval_q<T, 0>), grid, block, 0, L.stream, a);
     return hipGetLastError();
   }
   return with_variant(L, [&](auto v) {
@@ -613,7 +631,9 @@ static hipError_t tr_eval_launch(const Launch &L, const TrArgs<T> &a) {
     // a workgroup holds both parties' threads for block/2 elements
     if (block < 128 || block > 2 * kTrMaxTile || block % 128 != 0) return hipErrorInvalidConfiguration;
     const int grid = grid_for(k_tr_eval<T, NT, REP, 0>, block, 2 * a.N, L.num_cu);
-    if (L.profiled)
+    if (q)
+      hipLaunchKernelGGL((k_tr_eval_pool<T, NT, REP, 0>), dim3(grid), dim3(block), 0, L.stream, a, *q);
+    else if (L.profiled)
       hipLaunchKernelGGL((k_tr_eval<T, NT, REP, 1>), dim3(grid), dim3(block), 0, L.stream, a);
     else
       hipLaunchKernelGGL((k_tr_eval<T, NT, REP, 0>), dim3(grid), dim3(block), 0, L.stream, a);
@@ -633,7 +653,7 @@ hipError_t launch_tr_eval(const Launch &L, const TrLayout &lay, const uint8_t *k
   a.bias_ncol = bias_ncol > 0 ? bias_ncol : 1;
   a.out = out;
   a.prio = lay.N < kTrPrioN;
-  return tr_eval_launch(L, a);
+  return tr_eval_launch<T>(L, a, nullptr);
 }
 
 template <typename T>
@@ -647,13 +667,14 @@ hipError_t launch_tr_eval_pool(const Launch &L, const TrLayout &lay, const uint8
   a.k1 = k1;
   a.bias_ncol = 1;
   a.prio = lay.N < kTrPrioN;
-  a.pB = uint32_t(B);
-  a.pR = uint32_t(R);
-  a.pC = uint32_t(C);
-  a.ppr = uint32_t(R / 2);
-  a.pv = V;
-  a.pvn = Vn;
-  return tr_eval_launch(L, a);
+  TrPool<T> q;
+  q.B = uint32_t(B);
+  q.R = uint32_t(R);
+  q.C = uint32_t(C);
+  q.pr = uint32_t(R / 2);
+  q.v = V;
+  q.vn = Vn;
+  return tr_eval_launch<T>(L, a, &q);
 }
 
 template <typename T>
