@@ -596,14 +596,16 @@ static int tr_eval_block(const Launch &L, size_t n) {
   return int(std::min<size_t>(size_t(b), 2 * h));
 }
 
-// Quad-lane evaluation: a spread small launch (Launch::spread_small) with the
-// default T0/T1 table whose elements fit two 256-thread workgroups (32 elements
-// each; both fit a CU's LDS) per CU, so that every element's AES rounds run on
-// four lanes (at B = 1: 0.566 ms per forward against 0.609 with one workgroup
-// per CU and 0.570 with four).
+// Quad-lane evaluation: a launch with the default T0/T1 table whose elements fit
+// two 256-thread workgroups (32 elements each; both fit a CU's LDS) per CU, so
+// that every element's AES rounds run on four lanes (at B = 1: 0.566 ms per
+// forward against 0.609 with one workgroup per CU and 0.570 with four).  Large
+// lanes take it too: their smallest gates (the last pool levels, two fully
+// connected gates) run at the end of a forward, when the lanes' large gates are
+// done (bw=64, B=64: +1.2-1.7%; bw=32 unchanged).
 constexpr int kQuadBlock = 256, kQuadElems = kQuadBlock / 8;
 static bool use_quad(const Launch &L, size_t n) {
-  if (!L.spread_small || L.aes_block != 0) return false;
+  if (L.aes_block != 0) return false;
   int nv;
   const AesVariant *v = aes_variants(&nv);
   const int vi = L.aes_variant >= 0 && L.aes_variant < nv ? L.aes_variant : 0;

@@ -5,7 +5,8 @@
       markdown table of the kernel-trace statistics (calls, total ms, average us)
   rocprof_summary.py traffic --fetch F.csv --write W.csv --cal-fetch CF.csv --cal-write CW.csv
                              --kernel SUBSTRING [--cal-kernel SUBSTRING] [--cal-bytes N] [--per-dispatch]
-      HBM bytes per dispatch of the kernels whose name contains SUBSTRING, from a
+      HBM bytes per dispatch of the kernels whose name contains SUBSTRING (or one
+      of its alternatives separated by '|'), from a
       FETCH_SIZE run and a WRITE_SIZE run (counter_collection.csv of each), each
       counter scaled by what it reads for a plain copy of known size (the
       calibration runs: --cal-kernel, default the elementwise add of
@@ -55,10 +56,15 @@ def shapes(path, top):
         print(f"| `{name}` | {gx} | {n} | {t / n:.1f} |")
 
 
+def _match(name, sub):
+    """name contains SUB, or one of the alternatives of SUB separated by '|'."""
+    return any(s and s in name for s in sub.split("|"))
+
+
 def _values(path, counter, sub):
     out = []
     for r in _rows(path):
-        if r["Counter_Name"] == counter and sub in r["Kernel_Name"]:
+        if r["Counter_Name"] == counter and _match(r["Kernel_Name"], sub):
             out.append((int(r["Dispatch_Id"]), float(r["Counter_Value"]), r["Kernel_Name"]))
     out.sort()
     return out
@@ -97,7 +103,7 @@ def traffic(a):
 
 
 def counters(a):
-    rows = [r for r in _rows(a.csv) if a.kernel in r["Kernel_Name"]]
+    rows = [r for r in _rows(a.csv) if _match(r["Kernel_Name"], a.kernel)]
     if not rows:
         sys.exit(f"{a.csv}: no dispatch of a kernel containing {a.kernel!r}")
     names = sorted({r["Counter_Name"] for r in rows})
