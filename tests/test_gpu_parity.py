@@ -173,11 +173,19 @@ def test_split_truncation_keys_and_eval(ctx, orc, relu):
     assert np.array_equal(signed(y2.astype(np.uint64) - or2, bw), _tr_expected(2 if relu else 1, x, bias))
 
 
-@pytest.mark.parametrize("n", [1, 63, 64, 65, 255, 256, 257, 511, 513, 1023, 1025])
-def test_gate_tile_edges(ctx, mp, orc, n):
-    """One gate launch takes tiles of (workgroup / 2) elements, both parties' threads
-    per tile: element counts around the wave and tile sizes give the oracle's
-    outputs (EXTRELU after TRMOD, so both DCF widths and both exchanges run)."""
+@pytest.mark.parametrize("form", ["auto", "block512"])
+@pytest.mark.parametrize("n", [1, 63, 64, 65, 255, 256, 257, 511, 513, 1023, 1025, 16384, 16385, 40000])
+def test_gate_tile_edges(ctx, mp, orc, n, form):
+    """One gate launch takes tiles of elements, both parties' threads per tile:
+    element counts around the wave and tile sizes give the oracle's outputs
+    (EXTRELU after TRMOD, so both DCF widths and both exchanges run).  "auto"
+    takes the default forms -- up to 64 elements per CU (16384 on 256 CUs) the
+    quad-lane kernel with 32-element tiles, above it about one workgroup per CU --
+    and "block512" pins the variant's 512-thread workgroups (256-element tiles,
+    one lane per element)."""
+    if form == "block512":
+        ctx = mp.Ctx(bw=ctx.bw)
+        ctx.set_aes_variant(0, 512)
     bw = ctx.bw
     rng = np.random.default_rng(n + bw)
     h = 1 << (bw - 1)
@@ -192,6 +200,8 @@ def test_gate_tile_edges(ctx, mp, orc, n):
     oy2, _ = orc.tr_eval(14, bw, S, p0, p1, oy1)
     assert np.array_equal(y1.astype(np.uint64), oy1) and np.array_equal(y2.astype(np.uint64), oy2)
     assert np.array_equal(signed(y2.astype(np.uint64) - r2, bw), np.maximum(x >> S, 0))
+    if form == "block512":
+        ctx.close()
 
 
 def test_local_ars_matches_oracle(ctx, orc):
