@@ -611,7 +611,7 @@ static bool use_quad(const Launch &L, size_t n) {
   const int vi = L.aes_variant >= 0 && L.aes_variant < nv ? L.aes_variant : 0;
   return v[vi].nt == 2 && v[vi].rep == 32 && n <= size_t(L.num_cu) * 2 * kQuadElems;
 }
-static int quad_grid(size_t n) { return int((n + kQuadElems - 1) / kQuadElems); }
+static int quad_grid(size_t n) { return int(std::max<size_t>(1, (n + kQuadElems - 1) / kQuadElems)); }
 
 // One gate evaluation of both parties with prepared arguments: the regular
 // kernels, or (q set) their max-pool form.
