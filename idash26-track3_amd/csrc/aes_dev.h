@@ -330,6 +330,37 @@ struct AesPerm2 {
     return o;
   }
 
+  // hash of two independent blocks, their rounds side by side: one thread's
+  // two AES chains give the scheduler table reads of one to issue while the
+  // other's XORs wait
+  __device__ __forceinline__ void hash2(uint4 s, uint4 u, const AesRK &rk, uint4 *hs, uint4 *hu) const {
+    uint32_t a0 = s.z ^ rk.w[0], a1 = s.w ^ rk.w[1];
+    uint32_t a2 = xor3(s.z, s.x, rk.w[2]), a3 = xor3(s.w, s.y, rk.w[3]);
+    uint32_t b0 = u.z ^ rk.w[0], b1 = u.w ^ rk.w[1];
+    uint32_t b2 = xor3(u.z, u.x, rk.w[2]), b3 = xor3(u.w, u.y, rk.w[3]);
+#pragma unroll
+    for (int r = 1; r < 10; r++) {
+      const uint32_t n0 = col(a0, a1, a2, a3, rk.w[4 * r + 0]);
+      const uint32_t m0 = col(b0, b1, b2, b3, rk.w[4 * r + 0]);
+      const uint32_t n1 = col(a1, a2, a3, a0, rk.w[4 * r + 1]);
+      const uint32_t m1 = col(b1, b2, b3, b0, rk.w[4 * r + 1]);
+      const uint32_t n2 = col(a2, a3, a0, a1, rk.w[4 * r + 2]);
+      const uint32_t m2 = col(b2, b3, b0, b1, rk.w[4 * r + 2]);
+      const uint32_t n3 = col(a3, a0, a1, a2, rk.w[4 * r + 3]);
+      const uint32_t m3 = col(b3, b0, b1, b2, rk.w[4 * r + 3]);
+      a0 = n0, a1 = n1, a2 = n2, a3 = n3;
+      b0 = m0, b1 = m1, b2 = m2, b3 = m3;
+    }
+    hs->x = xor3(last(a0, a1, a2, a3), rk.w[40], s.z);
+    hu->x = xor3(last(b0, b1, b2, b3), rk.w[40], u.z);
+    hs->y = xor3(last(a1, a2, a3, a0), rk.w[41], s.w);
+    hu->y = xor3(last(b1, b2, b3, b0), rk.w[41], u.w);
+    hs->z = xor3(last(a2, a3, a0, a1), rk.w[42], s.z) ^ s.x;
+    hu->z = xor3(last(b2, b3, b0, b1), rk.w[42], u.z) ^ u.x;
+    hs->w = xor3(last(a3, a0, a1, a2), rk.w[43], s.w) ^ s.y;
+    hu->w = xor3(last(b3, b0, b1, b2), rk.w[43], u.w) ^ u.y;
+  }
+
   // Dealer PRF block AES_kd(idx_lo, idx_hi, field, gate).
   __device__ __forceinline__ uint4 prf(const AesRK &kd, uint32_t gate, uint32_t field, uint64_t idx) const {
     uint4 b;

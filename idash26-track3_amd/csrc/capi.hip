@@ -290,6 +290,13 @@ mpcx_status mpcx_set_aes_variant(mpcx_ctx *c, int variant, int block) {
   return MPCX_OK;
 }
 
+mpcx_status mpcx_set_both_party_aes(mpcx_ctx *c, int max_aes) {
+  CHECK_CTX(c);
+  if (max_aes < 0 || max_aes > 64) return fail(c, MPCX_EINVAL, "max_aes must be in [0, 64]");
+  c->L.both_aes = max_aes;
+  return MPCX_OK;
+}
+
 mpcx_status mpcx_set_dealer_key(mpcx_ctx *c, const uint8_t *key) {
   CHECK_CTX(c);
   c->L.has_dealer_key = key != nullptr;

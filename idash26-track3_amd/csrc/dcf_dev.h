@@ -12,6 +12,8 @@
 // The tree is the half-tree one (Guo et al., EUROCRYPT 2023): one fixed-key AES
 // call per level,  sL = H(s) ^ t*CW,  sR = sL ^ s,  t = lsb(s).
 #pragma once
+#include <type_traits>
+
 #include "aes_dev.h"
 
 namespace mpcx {
@@ -39,6 +41,52 @@ __device__ __forceinline__ uint32_t dcf_eval_walk(const A &aes, uint4 s,
     t = tl ^ (t & bit);
   }
   const uint4 lb = xor_and4(aes.hash(s, c_rkL), leaf, 0u - t);
+  const uint32_t pos = m >= 7 ? uint32_t(x & 127u) : uint32_t(x);
+  return out ^ parity_above(lb, pos);
+}
+
+// Both parties' hashes of a level: side by side on the T0/T1 table, one after
+// the other on the other layouts.
+template <class A>
+__device__ __forceinline__ void hash_pair(const A &aes, uint4 s, uint4 u, const AesRK &rk, uint4 *hs, uint4 *hu) {
+  if constexpr (std::is_same<A, AesPerm2>::value) {
+    aes.hash2(s, u, rk, hs, hu);
+  } else {
+    *hs = aes.hash(s, rk);
+    *hu = aes.hash(u, rk);
+  }
+}
+
+// Both parties' walks of one element in one thread, from their roots s0 and s1
+// (the correction words and the leaf are common to the two keys): the XOR of
+// the two parties' outputs, i.e. the reconstructed bit.  Each level hashes the
+// two seeds side by side and reads its correction word once.
+template <class A>
+__device__ __forceinline__ uint32_t dcf_eval_walk2(const A &aes, uint4 s0, uint4 s1, int m, int L,
+                                                   const uint4 *__restrict__ cw, size_t stride, uint4 leaf,
+                                                   uint64_t x) {
+  uint32_t t0 = s0.x & 1u, t1 = s1.x & 1u, out = 0;
+  uint4 cnext = L > 0 ? cw[0] : make_uint4(0, 0, 0, 0);
+  const bool wide = m > 32;
+  const uint32_t xlo = uint32_t(x);
+  for (int l = 0; l < L; l++) {
+    const uint4 c = cnext;
+    if (l + 1 < L) cnext = cw[size_t(l + 1) * stride];
+    const int sh = m - 1 - l;
+    const uint32_t bit = wide ? uint32_t(x >> sh) & 1u : (xlo >> sh) & 1u;
+    uint4 h0, h1;
+    hash_pair(aes, s0, s1, c_rkH, &h0, &h1);
+    const uint4 sl0 = xor_and4(h0, c, 0u - t0), sl1 = xor_and4(h1, c, 0u - t1);
+    const uint32_t tl0 = sl0.x & 1u, tl1 = sl1.x & 1u;
+    out ^= (bit ^ 1u) & (tl0 ^ t0 ^ tl1 ^ t1);
+    s0 = xor_and4(sl0, s0, 0u - bit);
+    s1 = xor_and4(sl1, s1, 0u - bit);
+    t0 = tl0 ^ (t0 & bit);
+    t1 = tl1 ^ (t1 & bit);
+  }
+  uint4 l0, l1;
+  hash_pair(aes, s0, s1, c_rkL, &l0, &l1);
+  const uint4 lb = xor4(xor_and4(l0, leaf, 0u - t0), xor_and4(l1, leaf, 0u - t1));
   const uint32_t pos = m >= 7 ? uint32_t(x & 127u) : uint32_t(x);
   return out ^ parity_above(lb, pos);
 }

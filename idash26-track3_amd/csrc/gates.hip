@@ -248,6 +248,66 @@ __device__ __forceinline__ void tr_eval_tiles(const TrArgs<T> &a, const TrArgs<T
   if constexpr (POOL) pool_carry(q);
 }
 
+// ---- both-party form (throughput launches) ----
+// Gate a on element i for both parties in one thread: the two parties' DCF
+// walks side by side (dcf_eval_walk2: two independent AES chains, each level's
+// correction word read once), their masked bits combined in registers, and the
+// sum of the two output messages, the revealed output.  The same keys and
+// algebra as tr_tile, with no exchange buffers and no barriers.
+template <typename T, class Aes>
+__device__ __forceinline__ T tr_both(const Aes &aes, const TrArgs<T> &a, size_t i, T xh) {
+  const T xp = tr_shifted_input(a, i, xh);
+  const T lowmask = (T(1) << a.sb) - T(1);
+  const T smask = (T(1) << a.s) - T(1);
+  uint32_t bh = 0, dh = 0;
+  if (a.use_a) {
+    bh = dcf_eval_walk2(aes, reinterpret_cast<const uint4 *>(a.k0 + a.a.off_root)[i],
+                        reinterpret_cast<const uint4 *>(a.k1 + a.a.off_root)[i], a.a.m, a.a.L,
+                        reinterpret_cast<const uint4 *>(a.k0 + a.a.off_cw) + i, a.N,
+                        reinterpret_cast<const uint4 *>(a.k0 + a.a.off_leaf)[i], uint64_t(xp & lowmask));
+    bh ^= get_bit(reinterpret_cast<const uint64_t *>(a.k0 + a.a.off_z), i) ^
+          get_bit(reinterpret_cast<const uint64_t *>(a.k1 + a.a.off_z), i);
+  }
+  if (a.use_b) {
+    dh = dcf_eval_walk2(aes, reinterpret_cast<const uint4 *>(a.k0 + a.b.off_root)[i],
+                        reinterpret_cast<const uint4 *>(a.k1 + a.b.off_root)[i], a.b.m, a.b.L,
+                        reinterpret_cast<const uint4 *>(a.k0 + a.b.off_cw) + i, a.N,
+                        reinterpret_cast<const uint4 *>(a.k0 + a.b.off_leaf)[i], uint64_t(xp & smask));
+    dh ^= get_bit(reinterpret_cast<const uint64_t *>(a.k0 + a.b.off_z), i) ^
+          get_bit(reinterpret_cast<const uint64_t *>(a.k1 + a.b.off_z), i);
+  }
+  const uint32_t hb = uint32_t(xp >> a.sb) & 1u;
+  return T(tr_out_share(a, 0, a.k0, i, xh, xp, hb, bh, dh) + tr_out_share(a, 1, a.k1, i, xh, xp, hb, bh, dh));
+}
+
+// The elements of a both-party launch, one per thread (grid-stride): gate a,
+// then (TWO) gate a2 on its revealed output, or (POOL) a max-pool level.
+template <typename T, int NT, int REP, bool TWO, bool POOL>
+__device__ __forceinline__ void tr_eval_both(const TrArgs<T> &a, const TrArgs<T> &a2, const TrPool<T> &q) {
+  __shared__ __align__(16) uint32_t lds[AesLds<NT, REP>::kWords];
+  AesLds<NT, REP>::fill(lds);
+  const AesLds<NT, REP> aes(lds);
+  const size_t stride = size_t(gridDim.x) * blockDim.x;
+  for (size_t i = size_t(blockIdx.x) * blockDim.x + threadIdx.x; i < a.N; i += stride) {
+    T xin, v0 = 0;
+    uint32_t o = 0;
+    if constexpr (POOL) {
+      const uint32_t s0 = pool_src(q, uint32_t(i), &o);
+      v0 = q.v[s0];
+      xin = q.v[s0 + q.C] - v0;
+    } else {
+      xin = a.xhat[i];
+    }
+    T y = tr_both(aes, a, i, xin);
+    if constexpr (TWO) y = tr_both(aes, a2, i, y);
+    if constexpr (POOL)
+      q.vn[o] = v0 + y;
+    else
+      a.out[i] = y;
+  }
+  if constexpr (POOL) pool_carry(q);
+}
+
 // ---- quad-lane form (latency-bound launches, AesPerm2 table) ----
 // The DCF walks of tr_dcf_bits with four lanes per element and party (lane j of
 // the quad reads word j of the roots, correction words and leaves).
@@ -385,6 +445,13 @@ template <typename T, int NT, int REP, int TAG>
 __global__ void k_tr_eval2(TrArgs<T> a, TrArgs<T> a2) {
   if (a.prio) __builtin_amdgcn_s_setprio(2);
   tr_eval_tiles<T, NT, REP, true, false>(a, a2, TrPool<T>{});
+}
+
+// Both-party forms: one thread per element for both parties.
+template <typename T, int NT, int REP, int TAG>
+__global__ void k_tr_eval_b(TrArgs<T> a) {
+  if (a.prio) __builtin_amdgcn_s_setprio(2);
+  tr_eval_both<T, NT, REP, false, false>(a, a, TrPool<T>{});
 }
 
 // Party mode, phase 1: party p's masked DCF output bits (one ballot word per
@@ -613,6 +680,23 @@ static bool use_quad(const Launch &L, size_t n) {
 }
 static int quad_grid(size_t n) { return int(std::max<size_t>(1, (n + kQuadElems - 1) / kQuadElems)); }
 
+// The both-party form (one thread per element for both parties, 1024-thread
+// workgroups: one per CU at 68 VGPRs, 64 KiB of LDS) for gates of at most
+// L.both_aes AES calls per element and party over Z_2^32 (the launcher's only
+// instance), in launches of at least 1024 elements per CU.  Interleaved on one
+// box against the one-lane kernel: affinity B = 64 in 3 lanes +4.6% (gates up to
+// 14 calls), in 1 lane -3.8% with gates up to 14 calls and unchanged up to 6;
+// adjacency normalisation B = 1024 (6-call gates) +10% in 3 groups, +7.5% in
+// one.  Also measured: every gate launch in this form (smaller launches leave
+// CUs without a workgroup; B = 64 -0.6%), 512 and 768 threads, bw = 64 (2-3%
+// slower), the 25-call RELU of 2^24 elements alone (6% slower).
+template <typename T>
+static int both_block(const Launch &L, const TrArgs<T> &a) {
+  const int aes = (a.use_a ? a.a.L + 1 : 0) + (a.use_b ? a.b.L + 1 : 0);
+  if (L.aes_block != 0 || aes > L.both_aes) return 0;
+  return a.N >= size_t(L.num_cu) * 1024 ? 1024 : 0;
+}
+
 // One gate evaluation of both parties with prepared arguments: the regular
 // kernels, or (q set) their max-pool form.
 template <typename T>
@@ -629,6 +713,17 @@ static hipError_t tr_eval_launch(const Launch &L, const TrArgs<T> &a, const TrPo
   }
   return with_variant(L, [&](auto v) {
     constexpr int NT = decltype(v)::nt, REP = decltype(v)::rep;
+    if constexpr (sizeof(T) == 4) {
+      const int block = q ? 0 : both_block(L, a);
+      if (block) {
+        const int grid = grid_for(k_tr_eval_b<T, NT, REP, 0>, block, a.N, L.num_cu);
+        if (L.profiled)
+          hipLaunchKernelGGL((k_tr_eval_b<T, NT, REP, 1>), dim3(grid), dim3(block), 0, L.stream, a);
+        else
+          hipLaunchKernelGGL((k_tr_eval_b<T, NT, REP, 0>), dim3(grid), dim3(block), 0, L.stream, a);
+        return hipGetLastError();
+      }
+    }
     const int block = tr_eval_block(L, a.N);
     // a workgroup holds both parties' threads for block/2 elements
     if (block < 128 || block > 2 * kTrMaxTile || block % 128 != 0) return hipErrorInvalidConfiguration;

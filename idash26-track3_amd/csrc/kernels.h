@@ -15,6 +15,7 @@
 
 namespace mpcx {
 
+constexpr int kBothAesAlone = 6, kBothAesLanes = 14;
 struct Launch {
   hipStream_t stream = nullptr;
   int num_cu = 256;
@@ -24,6 +25,12 @@ struct Launch {
   // workgroups, about one per CU).  A caller whose other streams keep the GPU
   // busy clears it: the spread workgroups would take LDS from theirs.
   bool spread_small = true;
+  // Longest gate (AES calls per element and party) whose launches of at least
+  // 1024 elements per CU run in the both-party form over Z_2^32: one thread per
+  // element holds both parties' keys (0 = never).  Gates of up to 6 calls gain
+  // alone and beside other streams' work; up to 14 only beside other streams'
+  // work (a model's lanes), and lose alone.
+  int both_aes = kBothAesAlone;
   // Launches of a profiled forward use a separately named instantiation of the
   // DCF-evaluation kernel (same code), so kernel traces can tell them apart.
   bool profiled = false;

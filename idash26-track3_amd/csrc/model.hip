@@ -1836,6 +1836,9 @@ hipError_t LaneSet::set_lanes(int n, std::string *e) {
   for (int i = 0; i < n; i++) {
     Launch Li = L_;
     if (i > 0) TRY(hipStreamCreateWithFlags(&Li.stream, hipStreamNonBlocking));
+    // concurrent lanes keep the GPU busy beside each other's gates: the
+    // both-party form pays for longer gates there
+    if (n > 1 && Li.both_aes > 0) Li.both_aes = std::max(Li.both_aes, kBothAesLanes);
     st_.push_back(Li.stream);
     hipEvent_t ev;
     TRY(hipEventCreateWithFlags(&ev, hipEventDisableTiming));

@@ -33,6 +33,7 @@ _SIGS = {
     "mpcx_aes_variant_count": (C.c_int, []),
     "mpcx_aes_variant_name": (C.c_char_p, [C.c_int]),
     "mpcx_set_aes_variant": (C.c_int, [C.c_void_p, C.c_int, C.c_int]),
+    "mpcx_set_both_party_aes": (C.c_int, [C.c_void_p, C.c_int]),
     "mpcx_aes_variant": (C.c_int, [C.c_void_p]),
     "mpcx_bytes_exchanged": (C.c_uint64, [C.c_void_p]),
     "mpcx_rounds": (C.c_uint64, [C.c_void_p]),
@@ -227,6 +228,11 @@ class Ctx:
 
     def set_aes_variant(self, v, block=0):
         self.check(self.lib.mpcx_set_aes_variant(self.h, v, block), "set_aes_variant")
+
+    def set_both_party_aes(self, max_aes):
+        """Longest gate (AES calls per element and party) evaluated in the
+        both-party form by large Z_2^32 launches (0: never)."""
+        self.check(self.lib.mpcx_set_both_party_aes(self.h, int(max_aes)), "set_both_party_aes")
 
     def set_dealer_key(self, key16):
         """The dealer's 16 secret key bytes (None: keys from the seed alone)."""

@@ -100,6 +100,15 @@ mpcx_status mpcx_set_aes_variant(mpcx_ctx *ctx, int variant, int block_threads);
 /* Variant in use (set by mpcx_set_aes_variant or the MPCX_AES_VARIANT environment
  * variable at mpcx_create). */
 int mpcx_aes_variant(const mpcx_ctx *ctx);
+/* Longest truncation/ReLU gate, in AES calls per element and party, whose
+ * Z_2^32 launches of at least 1024 elements per CU run in the both-party form
+ * (one thread per element holds both parties' keys; same keys and outputs):
+ * 0..64, default 6; 0 keeps every gate on the one-lane-per-party kernel.  A
+ * model with more than one lane takes max(setting, 14) for its own launches
+ * (0 stays 0).  Read by the gate calls of this context and by models created
+ * after it.  No counterpart in the reference: a tuning setting of this
+ * library, as mpcx_set_aes_variant. */
+mpcx_status mpcx_set_both_party_aes(mpcx_ctx *ctx, int max_aes);
 
 /* The dealer's 16 secret key bytes (NULL: none).  With a key set, every
  * keygen of this context (and of models created afterwards) derives its PRF key

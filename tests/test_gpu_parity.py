@@ -204,6 +204,59 @@ def test_gate_tile_edges(ctx, mp, orc, n, form):
         ctx.close()
 
 
+@pytest.mark.parametrize("kind,n", [(4, 300007), (9, 300007), (15, 300007), (13, 300007), (14, 262144),
+                                    (14, 300007)])
+def test_gate_both_party_form(ctx, mp, orc, kind, n):
+    """At bw=32 a launch of at least 1024 elements per CU (262144 on 256 CUs) of a
+    gate of at most mpcx_set_both_party_aes AES calls per element and party (set
+    to 14 here: TRSLACK, RELUSLACK, RELUPOOL, TRMOD, EXT, EXTRELU) runs the
+    both-party form: one thread per element holds both parties' keys, runs the
+    two DCF walks side by side and adds the two messages.  Outputs identical to
+    the oracle's, on one whole grid pass and on a count past it (a ragged second
+    pass), and the unmasked result as the plaintext gate gives it (bw=64 runs the
+    same cases on the one-lane kernel)."""
+    c = mp.Ctx(bw=ctx.bw)
+    try:
+        c.set_both_party_aes(14)
+        _both_party_case(c, mp, orc, kind, n)
+    finally:
+        c.close()
+
+
+def _both_party_case(ctx, mp, orc, kind, n):
+    bw = ctx.bw
+    rng = np.random.default_rng(kind * 31 + n + bw)
+    if kind in (13, 14):  # TRMOD, then EXT or EXTRELU on its output
+        x = rng.integers(-(1 << (bw - 3)), 1 << (bw - 3), size=n, dtype=np.int64)
+        rin = rmask(rng, n, bw)
+        o0, o1, r1 = orc.tr_keygen(7, 50, 12, bw, S, rin)
+        p0, p1, r2 = orc.tr_keygen(7, 51, kind, bw, S, r1)
+        xhat = (x.astype(np.uint64) + rin) & M(bw)
+        y1 = ctx.tr_eval(12, mp.to_dev(o0), mp.to_dev(o1), xhat)
+        y2 = ctx.tr_eval(kind, mp.to_dev(p0), mp.to_dev(p1), y1)
+        oy1, _ = orc.tr_eval(12, bw, S, o0, o1, xhat)
+        oy2, _ = orc.tr_eval(kind, bw, S, p0, p1, oy1)
+        assert np.array_equal(y1.astype(np.uint64), oy1) and np.array_equal(y2.astype(np.uint64), oy2)
+        want = x >> S if kind == 13 else np.maximum(x >> S, 0)
+        assert np.array_equal(signed(y2.astype(np.uint64) - r2, bw), want)
+        return
+    x, bias = _tr_inputs(rng, kind, bw, n=n)
+    rin = rmask(rng, x.size, bw)
+    o0, o1, orout = orc.tr_keygen(7, 52, kind, bw, S, rin)
+    xhat = (x.astype(np.uint64) + rin) & M(bw)
+    y = ctx.tr_eval(kind, mp.to_dev(o0), mp.to_dev(o1), xhat)
+    oy, _ = orc.tr_eval(kind, bw, S, o0, o1, xhat)
+    assert np.array_equal(y.astype(np.uint64), oy)
+    assert np.array_equal(signed(y.astype(np.uint64) - orout, bw), _tr_expected(kind, x, bias))
+
+
+def test_both_party_setting_checked(ctx):
+    """mpcx_set_both_party_aes takes 0..64 and refuses other values."""
+    for bad in (-1, 65):
+        assert ctx.lib.mpcx_set_both_party_aes(ctx.h, bad) != 0
+    assert ctx.lib.mpcx_set_both_party_aes(ctx.h, 6) == 0
+
+
 def test_local_ars_matches_oracle(ctx, orc):
     """LocalARS (TruncateType::LocalARS, ddg_orca_batched.h:180-199): no key and no
     exchange; output mask and outputs identical to the oracle's, whose closed form
