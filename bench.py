@@ -49,8 +49,8 @@ GEMM_PEAK_TMACS = {"mfma32": 5.0e3 / 2 / 16, "mfma64": 5.0e3 / 2 / 64, "valu": V
 # when the current sources or workload have no measurement.  Each entry names
 # the profile summary under profiles/ that it comes from.
 TRAFFIC_MEASURED = {
-    ("7b696a767282", "perm32x2_b512", 64, 32, 3, 0): {
-        "bytes_per_launch": 61308752, "profile": "profiles/k_tr_eval_affinity_bw32_B64.md"},
+    ("6a72048ee9ef", "perm32x2_b512", 64, 32, 3, 0): {
+        "bytes_per_launch": 61115797, "profile": "profiles/k_tr_eval_affinity_bw32_B64.md"},
 }
 KERNEL_SOURCES = ("csrc/gates.hip", "csrc/launch_util.h", "csrc/kernels.h", "csrc/dcf_dev.h", "csrc/aes_dev.h",
                   "csrc/mpcx_core.h")
@@ -58,6 +58,11 @@ SLACK_DESC = {1: ", GCN products H.W^T truncated with the slack gate",
               2: ", GCN products and aggregations truncated with the slack gate",
               3: ", every layer truncation local (LocalARS, the reference's default truncation; not bit-exact)"}
 VALU_OPS_PER_AES = {"perm32x2_b512": 318, "perm64_b512": 390, "perm64_b1024": 390, "t4_rep32_b1024": 452}
+# The both-party form (one thread per element runs both parties' walks) issues
+# 617 VALU instructions per level loop of two AES calls on the T0/T1 table: a
+# forward that mixes the two forms converts its AES calls at the lower count,
+# so its VALU rate is a lower bound.
+VALU_OPS_PER_AES_MIXED = dict(VALU_OPS_PER_AES, perm32x2_b512=308.5)
 # LDS table bytes read per AES call: 16 four-byte lookups per round, ten rounds
 # (the same level-loop blocks: 160 ds_read_b32 in every variant)
 LDS_BYTES_PER_AES = 160 * 4
@@ -216,10 +221,11 @@ def main():
     dcf_evals_per_s = prof["elements"] / step_s
     aes_per_s = prof["aes_calls"] / step_s
     key_gbs = prof["hbm_bytes"] / step_s / 1e9
-    step_tops = aes_per_s * VALU_OPS_PER_AES.get(variant, float("nan")) / 1e12
+    valu_per_aes = (VALU_OPS_PER_AES_MIXED if args.bw == 32 else VALU_OPS_PER_AES).get(variant, float("nan"))
+    step_tops = aes_per_s * valu_per_aes / 1e12
     # rate of the launches alone (profiled forward, lanes one after another)
     launch_aes_per_s = prof["aes_calls"] / (dcf_ms / 1e3) if dcf_ms > 0 else 0.0
-    achieved_tops = launch_aes_per_s * VALU_OPS_PER_AES.get(variant, float("nan")) / 1e12
+    achieved_tops = launch_aes_per_s * valu_per_aes / 1e12
     gemm_path = "valu" if os.environ.get("MPCX_GEMM") == "valu" else f"mfma{args.bw}"
     gemm_tmacs = prof["gemm_macs"] / (prof["gemm_ms"] / 1e3) / 1e12 if prof["gemm_ms"] > 0 else 0.0
     digest = kernel_digest()
@@ -271,7 +277,7 @@ def main():
             "algorithmic_bytes_per_launch": round(prof["hbm_bytes"] / max(prof["launches"], 1)),
             "launches_per_step": prof["launches"],
             "aes_calls_per_step": prof["aes_calls"],
-            "valu_ops_per_aes": VALU_OPS_PER_AES.get(variant),
+            "valu_ops_per_aes": valu_per_aes,
             "co_limit": lds_colimit(aes_per_s),
             "kernel_digest": digest,
         },
@@ -671,7 +677,7 @@ def run_adjnorm(args):
     # AES calls per step: LUT8 (3 per degree and party), TRSLACK (12-bit DCF:
     # 5 levels + leaf per pair and party)
     aes = 2.0 * (3 * B * N + 6 * B * P)
-    tops = aes / per * VALU_OPS_PER_AES.get(ctx.aes_variant_name(), float("nan")) / 1e12
+    tops = aes / per * VALU_OPS_PER_AES_MIXED.get(ctx.aes_variant_name(), float("nan")) / 1e12
     result = {
         "metric": "adjacency-normalisation graphs/s (B=1024, N=140, Z_2^32, 1 GPU)",
         "value": round(B / per, 1),
