@@ -129,6 +129,9 @@ def main():
     ap.add_argument("--aes-variant", type=int, default=-1)
     ap.add_argument("--aes-block", type=int, default=0,
                     help="threads per DCF workgroup (0: the variant's own; a multiple of 128 up to 1024)")
+    ap.add_argument("--both-aes", type=int, default=-1,
+                    help="mpcx_set_both_party_aes: longest gate (AES calls per element and party) in the "
+                         "both-party form (-1: the library's default)")
     ap.add_argument("--lanes", type=int, default=3, help="concurrent sub-batches, each on its own stream")
     ap.add_argument("--slack", type=int, default=0, choices=(0, 1, 2, 3),
                     help="slack truncations of the GCN (exact while the values lie in half the signed ring): "
@@ -184,6 +187,8 @@ def main():
     ctx = mpcx.Ctx(bw=args.bw, scale=dims.s)
     if args.aes_variant >= 0:
         ctx.set_aes_variant(args.aes_variant, args.aes_block)
+    if args.both_aes >= 0:
+        ctx.set_both_party_aes(args.both_aes)
     model = mpcx.Model(ctx, dims, wl.W, lanes=args.lanes)
     key_bytes = model.key_bytes(B)
     t0 = time.time()
@@ -554,6 +559,8 @@ def run_relu(args):
     ctx = mpcx.Ctx(bw=bw, scale=s)
     if args.aes_variant >= 0:
         ctx.set_aes_variant(args.aes_variant, args.aes_block)
+    if args.both_aes >= 0:
+        ctx.set_both_party_aes(args.both_aes)
     k0, k1, rout = ctx.tr_keygen(mpcx.RELU, rin, seed=0xACE + args.seed, gate=1)
     key_bytes = int(ctx.lib.mpcx_tr_key_bytes(ctx.h, mpcx.RELU, n))
     dx = mpcx.to_dev(((x.astype(np.uint64) + rin) & 0xFFFFFFFF).astype(np.uint32))
@@ -647,6 +654,8 @@ def run_adjnorm(args):
     ctx = mpcx.Ctx(bw=bw)
     if args.aes_variant >= 0:
         ctx.set_aes_variant(args.aes_variant, args.aes_block)
+    if args.both_aes >= 0:
+        ctx.set_both_party_aes(args.both_aes)
     ctx.set_adjnorm_lanes(args.lanes)  # concurrent graph groups, each on its own stream
     k0, k1, mask = ctx.adjnorm_keygen(B, N, seed=0xADD + args.seed)
     d0, d1 = mpcx.to_dev(ctx.ring(a0)), mpcx.to_dev(ctx.ring(a1))
