@@ -44,16 +44,17 @@ GEMM_PEAK_TMACS = {"mfma32": 5.0e3 / 2 / 16, "mfma64": 5.0e3 / 2 / 64, "valu": V
 # WRITE_SIZE (one run each) on this bench command, mean over the launches of the
 # forward, each counter scaled by its reading on a plain 1 GiB copy
 # (bench.py --workload copy: FETCH_SIZE x 2.0, WRITE_SIZE x 1.0).  A measurement
-# holds only for the kernel sources it was taken on: it is keyed by the digest of
-# those sources (kernel_digest()) and the workload, and the line reports null
+# holds only for the kernel sources and the model's launch sequence it was taken
+# on: it is keyed by the digest of those sources (kernel_digest(): the gate
+# kernels and csrc/model.hip, which decides the launches) and the workload, and the line reports null
 # when the current sources or workload have no measurement.  Each entry names
 # the profile summary under profiles/ that it comes from.
 TRAFFIC_MEASURED = {
-    ("6a72048ee9ef", "perm32x2_b512", 64, 32, 3, 0): {
-        "bytes_per_launch": 61115797, "profile": "profiles/k_tr_eval_affinity_bw32_B64.md"},
+    ("66912b7ad422", "perm32x2_b512", 64, 32, 3, 0): {
+        "bytes_per_launch": 70918112, "profile": "profiles/k_tr_eval_affinity_bw32_B64.md"},
 }
 KERNEL_SOURCES = ("csrc/gates.hip", "csrc/launch_util.h", "csrc/kernels.h", "csrc/dcf_dev.h", "csrc/aes_dev.h",
-                  "csrc/mpcx_core.h")
+                  "csrc/mpcx_core.h", "csrc/model.hip")
 SLACK_DESC = {1: ", GCN products H.W^T truncated with the slack gate",
               2: ", GCN products and aggregations truncated with the slack gate",
               3: ", every layer truncation local (LocalARS, the reference's default truncation; not bit-exact)"}

@@ -703,7 +703,9 @@ template <typename T>
 static hipError_t tr_eval_launch(const Launch &L, const TrArgs<T> &a, const TrPool<T> *q) {
   if (use_quad(L, a.N)) {
     const dim3 grid(quad_grid(a.N)), block(kQuadBlock);
-    if (q)
+    if (q && L.profiled)
+      hipLaunchKernelGGL((k_tr_eval_pool_q<T, 1>), grid, block, 0, L.stream, a, *q);
+    else if (q)
       hipLaunchKernelGGL((k_tr_eval_pool_q<T, 0>), grid, block, 0, L.stream, a, *q);
     else if (L.profiled)
       hipLaunchKernelGGL((k_tr_eval_q<T, 1>), grid, block, 0, L.stream, a);
@@ -728,7 +730,9 @@ static hipError_t tr_eval_launch(const Launch &L, const TrArgs<T> &a, const TrPo
     // a workgroup holds both parties' threads for block/2 elements
     if (block < 128 || block > 2 * kTrMaxTile || block % 128 != 0) return hipErrorInvalidConfiguration;
     const int grid = grid_for(k_tr_eval<T, NT, REP, 0>, block, 2 * a.N, L.num_cu);
-    if (q)
+    if (q && L.profiled)
+      hipLaunchKernelGGL((k_tr_eval_pool<T, NT, REP, 1>), dim3(grid), dim3(block), 0, L.stream, a, *q);
+    else if (q)
       hipLaunchKernelGGL((k_tr_eval_pool<T, NT, REP, 0>), dim3(grid), dim3(block), 0, L.stream, a, *q);
     else if (L.profiled)
       hipLaunchKernelGGL((k_tr_eval<T, NT, REP, 1>), dim3(grid), dim3(block), 0, L.stream, a);

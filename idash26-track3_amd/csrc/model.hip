@@ -12,6 +12,7 @@
 #include <algorithm>
 #include <cmath>
 #include <condition_variable>
+#include <cstdint>
 #include <cstring>
 #include <memory>
 #include <mutex>
@@ -37,6 +38,7 @@ namespace {
 // A model lane of at most this many samples runs in the latency-bound form
 // (small gates spread over the CUs, truncation pairs in one launch).
 constexpr int kFewLaneB = 8;
+constexpr size_t kFuseSmallN = 65536;
 // Events of the profiled forward only time work: they are read after a stream
 // synchronisation, so they skip the system-scope fence (an L2 writeback and
 // invalidation at every record, which would also slow the kernel after it).
@@ -167,8 +169,10 @@ struct Runner {
   // Party mode (L.party = 0 or 1): only this party's kernels run; its key is
   // kv.k[L.party] and each exchange goes through the peer.
   Peer *peer = nullptr;
-  // Consecutive gates may share a launch (tr2): keys resident, both parties here.
-  bool fuse = false;
+  // Gates of at most pair_max elements share a launch with the next gate of
+  // their truncation (tr2: keys resident, both parties here), and max-pool
+  // levels of at most pool_max pairs run as one launch (pool_level).
+  size_t pair_max = 0, pool_max = 0;
 
   Runner(const Launch &L_, int bw_, int s_, Workspace<T> &ws_, Counters &ctr_, Phase1Timer *t, KeySource &src_,
          Peer *peer_ = nullptr)
@@ -327,14 +331,14 @@ struct Runner {
 
   // One level of the max-pool tree over B blocks of R rows of C words, V -> Vn
   // (max(a, b) = a + ReLU(b - a) over the row pairs, an odd last row carried).
-  // In a latency-bound lane (Launch::spread_small) with both parties here the
-  // gate launch forms the pair differences and writes the next level itself;
+  // A level of at most pool_max pairs with both parties here is one gate launch
+  // that forms the pair differences and writes the next level itself;
   // otherwise the differences (into D), the gate (into Y) and the combination
-  // run apart (in party mode around the gate's exchanges; in lanes of more
-  // samples one launch per level measured up to 1.6% slower at B = 64).
+  // run apart (in party mode around the gate's exchanges; the large levels of
+  // lanes of many samples measured no faster in one launch).
   hipError_t pool_level(int kind, int B, int R, int C, const T *V, T *D, T *Y, T *Vn) {
     const size_t n = size_t(B) * (R / 2) * C;
-    if (party_mode() || !L.spread_small || size_t(B) * R * C >= (size_t(1) << 32)) {
+    if (party_mode() || n > pool_max || size_t(B) * R * C >= (size_t(1) << 32)) {
       TRY(launch_pool_diff<T>(L, B, R, C, V, D));
       TRY(tr(kind, n, D, nullptr, 1, Y));
       return launch_pool_combine<T>(L, B, R, C, V, Y, nullptr, Vn);
@@ -684,7 +688,7 @@ class Model final : public ModelBase, KeySource {
   // Eval may overwrite x; keygen may overwrite the mask rin.
   hipError_t trunc_eval(Runner<T> &r, bool relu, size_t n, T *x, const T *bias, int ncol, T *y) {
     if (!local_trunc()) {
-      if (r.fuse) return r.tr2(G_TRMOD, relu ? G_EXTRELU : G_EXT, n, x, bias, ncol, y);
+      if (n <= r.pair_max) return r.tr2(G_TRMOD, relu ? G_EXTRELU : G_EXT, n, x, bias, ncol, y);
       TRY(r.tr(G_TRMOD, n, x, bias, ncol, x));
       return r.tr(relu ? G_EXTRELU : G_EXT, n, x, nullptr, 1, y);
     }
@@ -1584,10 +1588,13 @@ class Model final : public ModelBase, KeySource {
     if (keyed_B_ != B || input_B_ != B) return hipErrorInvalidValue;
     TRY(ensure_work(B));
     // A lane of a few samples is latency-bound: its small gates spread over the
-    // CUs and each truncation's two gates run in one launch.  Lanes of more keep
-    // the GPU busy between them, where a spread gate's workgroups take LDS from
-    // the other lanes' gates and the paired launches measured slower (B = 64 in
-    // 3 lanes: 0.7% and 1.5% slower; B = 1: 4.7% and 3.4% lower latency).
+    // CUs, each truncation's two gates run in one launch and so does each
+    // max-pool level.  Lanes of more keep the GPU busy between them, where a
+    // spread gate's workgroups take LDS from the other lanes' gates; they pair
+    // only the gates of at most kFuseSmallN elements, the latency-bound end of
+    // a forward (all gates paired: B = 64 in 3 lanes 0.7% and 1.5% slower; B = 1
+    // 4.7% and 3.4% lower latency; up to 65536 elements: B = 32 +1.6%, B = 64
+    // and bw = 64 unchanged, against none).
     const bool few = B <= kFewLaneB;
     L_.spread_small = few;
     const int N = d_.n_nodes, bw = bw_;
@@ -1604,7 +1611,9 @@ class Model final : public ModelBase, KeySource {
       if (chunks_.size() > 1) TRY(issue_copy(1));
     }
     Runner<T> r(L_, bw_, s_, ws_, counters, &timer, *this, peer_);
-    r.fuse = few && !streaming_ && party_ < 0;
+    const size_t small = few ? SIZE_MAX : kFuseSmallN;
+    r.pair_max = !streaming_ && party_ < 0 ? small : 0;
+    r.pool_max = small;
     auto pub_gemm = [&](const T *x, int l, size_t rows, T *y) -> hipError_t {
       int in, out;
       layer_io(l, &in, &out);

@@ -614,9 +614,13 @@ def _tr_launches(dims, n):
     """DCF-evaluation launches of one exact forward of a lane of n samples with
     resident keys and both parties in one process: a lane of at most 8 samples
     (latency-bound) runs every truncation (TRMOD with its EXT or EXTRELU) as one
-    launch, one fewer per truncation than there are gates; larger lanes launch
-    every gate on its own."""
-    return _tr_gates(dims) - (6 + 2 + len(dims.fus) - 1 if n <= 8 else 0)
+    launch, one fewer per truncation than there are gates; larger lanes pair
+    only the truncations of at most 65536 elements (the fully connected layers
+    here)."""
+    sizes = [n * dims.n_nodes * f for f in dims.gcn for _ in range(2)]
+    sizes += [n * w for w in dims.dfc] + [n * w for w in dims.fus[:-1]]
+    assert len(sizes) == 6 + 2 + len(dims.fus) - 1
+    return _tr_gates(dims) - sum(1 for e in sizes if n <= 8 or e <= 65536)
 
 
 @pytest.mark.parametrize("bw,B,lanes", [(32, 5, 2), (64, 4, 3), (32, 2, 4), (32, 10, 1)])
@@ -627,7 +631,7 @@ def test_model_lanes_keys_and_forward(mp, orc, synth, bw, B, lanes):
     gives the plaintext outputs and the lanes' summed exchange bytes; a profiled
     forward (lanes one after another) gives the same outputs and times every
     lane's DCF launches.  B=2 with 4 lanes leaves two lanes empty; a lane of 10
-    samples launches every gate on its own, the smaller ones pair truncations."""
+    samples pairs only its small truncations, the smaller lanes pair all."""
     wl = synth.workload(B, synth.Dims(bw=bw), seed=23)
     d = _od(orc, wl.dims)
     want, code = orc.plain_forward(d, wl.X, wl.A, wl.mask, wl.prot, wl.W)
