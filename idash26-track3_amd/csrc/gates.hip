@@ -683,18 +683,20 @@ static int quad_grid(size_t n) { return int(std::max<size_t>(1, (n + kQuadElems 
 // The both-party form (one thread per element for both parties, 1024-thread
 // workgroups: one per CU at 68 VGPRs, 64 KiB of LDS) for gates of at most
 // L.both_aes AES calls per element and party over Z_2^32 (the launcher's only
-// instance), in launches of at least 1024 elements per CU.  Interleaved on one
-// box against the one-lane kernel: affinity B = 64 in 3 lanes +4.6% (gates up to
-// 14 calls), in 1 lane -3.8% with gates up to 14 calls and unchanged up to 6;
-// adjacency normalisation B = 1024 (6-call gates) +10% in 3 groups, +7.5% in
-// one.  Also measured: every gate launch in this form (smaller launches leave
-// CUs without a workgroup; B = 64 -0.6%), 512 and 768 threads, bw = 64 (2-3%
-// slower), the 25-call RELU of 2^24 elements alone (6% slower).
+// instance), in launches of at least L.both_min elements per CU.  Interleaved
+// on one box against the one-lane kernel: affinity B = 64 in 3 lanes +4.6%
+// (gates up to 14 calls, 1024 elements per CU), in 1 lane -3.8% with gates up
+// to 14 calls and unchanged up to 6; adjacency normalisation B = 1024 (6-call
+// gates) +10% in 3 groups, +7.5% in one.  In lanes 512 elements per CU gains
+// again (B = 64 +1.4%, B = 32 +2.5%; 384 and 256 lose at B = 32).  Also
+// measured: every gate launch in this form (B = 64 -0.6%), 512, 768 and 896
+// threads, bw = 64 (2-3% slower), the 25-call RELU of 2^24 elements alone (6%
+// slower).
 template <typename T>
 static int both_block(const Launch &L, const TrArgs<T> &a) {
   const int aes = (a.use_a ? a.a.L + 1 : 0) + (a.use_b ? a.b.L + 1 : 0);
   if (L.aes_block != 0 || aes > L.both_aes) return 0;
-  return a.N >= size_t(L.num_cu) * 1024 ? 1024 : 0;
+  return a.N >= size_t(L.num_cu) * size_t(L.both_min) ? 1024 : 0;
 }
 
 // One gate evaluation of both parties with prepared arguments: the regular

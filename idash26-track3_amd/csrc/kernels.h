@@ -16,6 +16,7 @@
 namespace mpcx {
 
 constexpr int kBothAesAlone = 6, kBothAesLanes = 14;
+constexpr int kBothMinAlone = 1024, kBothMinLanes = 512;
 struct Launch {
   hipStream_t stream = nullptr;
   int num_cu = 256;
@@ -26,11 +27,14 @@ struct Launch {
   // busy clears it: the spread workgroups would take LDS from theirs.
   bool spread_small = true;
   // Longest gate (AES calls per element and party) whose launches of at least
-  // 1024 elements per CU run in the both-party form over Z_2^32: one thread per
-  // element holds both parties' keys (0 = never).  Gates of up to 6 calls gain
-  // alone and beside other streams' work; up to 14 only beside other streams'
-  // work (a model's lanes), and lose alone.
+  // both_min elements per CU run in the both-party form over Z_2^32: one thread
+  // per element holds both parties' keys (0 = never).  Gates of up to 6 calls
+  // gain alone and beside other streams' work; up to 14 only beside other
+  // streams' work (a model's lanes), and lose alone.  Alone a launch needs 1024
+  // elements per CU to give every CU a 1024-thread workgroup; beside other
+  // lanes' work 512 measured best (they fill the CUs it leaves).
   int both_aes = kBothAesAlone;
+  int both_min = kBothMinAlone;
   // Launches of a profiled forward use a separately named instantiation of the
   // DCF-evaluation kernel (same code), so kernel traces can tell them apart.
   bool profiled = false;

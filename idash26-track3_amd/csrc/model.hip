@@ -1847,7 +1847,10 @@ hipError_t LaneSet::set_lanes(int n, std::string *e) {
     if (i > 0) TRY(hipStreamCreateWithFlags(&Li.stream, hipStreamNonBlocking));
     // concurrent lanes keep the GPU busy beside each other's gates: the
     // both-party form pays for longer gates there
-    if (n > 1 && Li.both_aes > 0) Li.both_aes = std::max(Li.both_aes, kBothAesLanes);
+    if (n > 1 && Li.both_aes > 0) {
+      Li.both_aes = std::max(Li.both_aes, kBothAesLanes);
+      Li.both_min = kBothMinLanes;
+    }
     st_.push_back(Li.stream);
     hipEvent_t ev;
     TRY(hipEventCreateWithFlags(&ev, hipEventDisableTiming));

@@ -105,7 +105,7 @@ int mpcx_aes_variant(const mpcx_ctx *ctx);
  * (one thread per element holds both parties' keys; same keys and outputs):
  * 0..64, default 6; 0 keeps every gate on the one-lane-per-party kernel.  A
  * model with more than one lane takes max(setting, 14) for its own launches
- * (0 stays 0).  Read by the gate calls of this context and by models created
+ * (0 stays 0), from 512 elements per CU.  Read by the gate calls of this context and by models created
  * after it.  No counterpart in the reference: a tuning setting of this
  * library, as mpcx_set_aes_variant. */
 mpcx_status mpcx_set_both_party_aes(mpcx_ctx *ctx, int max_aes);
