@@ -453,6 +453,11 @@ __global__ void k_tr_eval_b(TrArgs<T> a) {
   if (a.prio) __builtin_amdgcn_s_setprio(2);
   tr_eval_both<T, NT, REP, false, false>(a, a, TrPool<T>{});
 }
+template <typename T, int NT, int REP, int TAG>
+__global__ void k_tr_eval2_b(TrArgs<T> a, TrArgs<T> a2) {
+  if (a.prio) __builtin_amdgcn_s_setprio(2);
+  tr_eval_both<T, NT, REP, true, false>(a, a2, TrPool<T>{});
+}
 
 // Party mode, phase 1: party p's masked DCF output bits (one ballot word per
 // wave and plane).  a.k0 = a.k1 = the party's own key.
@@ -691,7 +696,9 @@ static int quad_grid(size_t n) { return int(std::max<size_t>(1, (n + kQuadElems 
 // again (B = 64 +1.4%, B = 32 +2.5%; 384 and 256 lose at B = 32).  Also
 // measured: every gate launch in this form (B = 64 -0.6%), 512, 768 and 896
 // threads, bw = 64 (2-3% slower), the 25-call RELU of 2^24 elements alone (6%
-// slower).
+// slower).  A truncation pair in this form (k_tr_eval2_b, lanes of at most 8
+// samples): B = 16 +4%, B = 24 +2%; a max-pool level in this form measured no
+// gain.
 template <typename T>
 static int both_block(const Launch &L, const TrArgs<T> &a) {
   const int aes = (a.use_a ? a.a.L + 1 : 0) + (a.use_b ? a.b.L + 1 : 0);
@@ -801,6 +808,17 @@ hipError_t launch_tr_eval2(const Launch &L, const TrLayout &lay, const TrLayout 
   }
   return with_variant(L, [&](auto v) {
     constexpr int NT = decltype(v)::nt, REP = decltype(v)::rep;
+    if constexpr (sizeof(T) == 4) {
+      const int bb = both_block(L, a) ? both_block(L, a2) : 0;
+      if (bb) {
+        const int grid = grid_for(k_tr_eval2_b<T, NT, REP, 0>, bb, lay.N, L.num_cu);
+        if (L.profiled)
+          hipLaunchKernelGGL((k_tr_eval2_b<T, NT, REP, 1>), dim3(grid), dim3(bb), 0, L.stream, a, a2);
+        else
+          hipLaunchKernelGGL((k_tr_eval2_b<T, NT, REP, 0>), dim3(grid), dim3(bb), 0, L.stream, a, a2);
+        return hipGetLastError();
+      }
+    }
     const int block = tr_eval_block(L, lay.N);
     if (block < 128 || block > 2 * kTrMaxTile || block % 128 != 0) return hipErrorInvalidConfiguration;
     const int grid = grid_for(k_tr_eval2<T, NT, REP, 0>, block, 2 * lay.N, L.num_cu);

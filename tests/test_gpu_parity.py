@@ -623,7 +623,7 @@ def _tr_launches(dims, n):
     return _tr_gates(dims) - sum(1 for e in sizes if n <= 8 or e <= 65536)
 
 
-@pytest.mark.parametrize("bw,B,lanes", [(32, 5, 2), (64, 4, 3), (32, 2, 4), (32, 10, 1)])
+@pytest.mark.parametrize("bw,B,lanes", [(32, 5, 2), (64, 4, 3), (32, 2, 4), (32, 10, 1), (32, 16, 2)])
 def test_model_lanes_keys_and_forward(mp, orc, synth, bw, B, lanes):
     """Concurrent sub-batches: the key arena is the lanes' one-lane key sets
     back to back, each byte-identical to the oracle dealer's under its lane
@@ -631,7 +631,9 @@ def test_model_lanes_keys_and_forward(mp, orc, synth, bw, B, lanes):
     gives the plaintext outputs and the lanes' summed exchange bytes; a profiled
     forward (lanes one after another) gives the same outputs and times every
     lane's DCF launches.  B=2 with 4 lanes leaves two lanes empty; a lane of 10
-    samples pairs only its small truncations, the smaller lanes pair all."""
+    samples pairs only its small truncations, the smaller lanes pair all (lanes
+    of 8 samples pair their GCN-2 and GCN-3 truncations in the both-party
+    form)."""
     wl = synth.workload(B, synth.Dims(bw=bw), seed=23)
     d = _od(orc, wl.dims)
     want, code = orc.plain_forward(d, wl.X, wl.A, wl.mask, wl.prot, wl.W)
