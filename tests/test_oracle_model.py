@@ -64,6 +64,88 @@ def test_hand_computed_two_node_model(orc):
     assert out.tolist() == [-28164]
 
 
+def _path3(orc):
+    """3-node path graph 0-1-2 with self loops (degrees 2, 3, 2), one feature,
+    every layer one channel wide. GCN-1 W = 6145 (1.500244), every other weight
+    4096 (1.0) or, for the fusion layer, [4096, 8192] on [drug, protein];
+    all biases zero; public protein value 1000."""
+    d = orc.make_dims(bw=32, s=12, n_nodes=3, feat=1, gcn=(1, 1, 1), dfc=(1, 1), prot=1, fus=(1, 1))
+    W = np.array([
+        6145, 0,         # gcn0
+        4096, 0,         # gcn1
+        4096, 0,         # gcn2
+        4096, 0,         # dfc0
+        4096, 0,         # dfc1
+        4096, 8192, 0,   # fus0: W^T = [[1.0], [2.0]] on [drug, protein]
+        4096, 0,         # fus1
+    ], np.int64)
+    assert W.size == orc.weights_len(d)
+    A = np.zeros((1, 3, 3), np.int64)
+    for i, j in ((0, 0), (1, 1), (2, 2), (0, 1), (1, 0), (1, 2), (2, 1)):
+        A[0, i, j] = 1
+    X = np.array([[[4097], [-3], [1]]], np.int64)
+    mask = np.ones((1, 3), np.int64)
+    prot = np.array([[1000]], np.int64)
+    return d, W, X, A, mask, prot
+
+
+def _path3_ints(order):
+    """The same forward in Python integers, GCN layers either transform-first
+    tr(A.tr(H.W)) or aggregate-first tr(tr(A.H).W); returns (pooled, output)."""
+    Af = [[2047, 1672, 0], [1672, 1365, 1672], [0, 1672, 2047]]
+    H = [4097, -3, 1]
+    for w in (6145, 4096, 4096):
+        if order == "transform":
+            XW = [(h * w) >> 12 for h in H]
+            agg = [sum(Af[i][j] * XW[j] for j in range(3)) >> 12 for i in range(3)]
+        else:
+            AH = [sum(Af[i][j] * H[j] for j in range(3)) >> 12 for i in range(3)]
+            agg = [(a * w) >> 12 for a in AH]
+        H = [max(a, 0) for a in agg]
+    pooled = max(H)
+    h = max((pooled * 4096) >> 12, 0)
+    drug = (h * 4096) >> 12
+    fus = max((drug * 4096 + 1000 * 8192) >> 12, 0)
+    return pooled, (fus * 4096) >> 12
+
+
+def test_gcn_order_is_transform_first(orc):
+    """reference/fixed_forward.py:63-67 runs each GCN layer transform-first,
+    H' = ReLU(tr(A_fx . tr(H . W^T)) + b); the C++ path aggregates first
+    (gpu_mpc/gcn_layer.h:113-114). On the path graph the two orders differ
+    by one LSB. By hand, A_fx = [[2047,1672,0],[1672,1365,1672],[0,1672,2047]]
+    (degree pairs (2,2), (2,3), (3,3)), X = [4097, -3, 1], >> is floor:
+      layer 1: H.W = [25176065, -18435, 6145] >> 12 = [6146, -5, 1]
+               (6146.5, -4.5, 1.5 before the floor);
+               A.XW = [12572502, 10270959, -6313] >> 12 = [3069, 2507, -2];
+               ReLU -> [3069, 2507, 0]
+      layer 2 (W = 1.0, so XW = H): A.XW = [10473947, 8553423, 4191704] >> 12
+               = [2557, 2088, 1023]
+      layer 3: A.XW = [8725315, 8835880, 5585217] >> 12 = [2130, 2157, 1363];
+               pooled max = 2157.
+    Aggregate-first: A.X = [8381543, 6847761, -2969] >> 12 = [2046, 1671, -1],
+    times 6145 = [12572670, 10268295, -6145] >> 12 = [3069, 2506, -2]; the
+    next layers give [2556, 2087, 1022] and [2129, 2156, 1362]: pooled 2156.
+    Drug FCs (1.0, no bias) keep 2157; fusion [drug, protein] . [1.0, 2.0]
+    = 2157 + 2000 = 4157 (the swapped concat order would give 5314); the
+    last layer (1.0) outputs 4157."""
+    assert _path3_ints("transform") == (2157, 4157)
+    assert _path3_ints("aggregate") == (2156, 4156)
+    d, W, X, A, mask, prot = _path3(orc)
+    out, code = orc.plain_forward(d, X, A, mask, prot, W)
+    assert code == 0
+    assert out.tolist() == [4157]
+    # the two-party protocol reconstructs the same value
+    k0, k1 = orc.model_keygen(d, 1, 7, W)
+    rng = np.random.default_rng(3)
+    shares = []
+    for v in (X, A, mask):
+        v0 = rng.integers(0, 1 << 32, size=v.size, dtype=np.uint64)
+        shares += [v0, (v.ravel().astype(np.uint64) - v0) & np.uint64(0xFFFFFFFF)]
+    out2, _ = orc.model_eval(d, 1, W, k0, k1, *shares, prot)
+    assert out2.tolist() == [4157]
+
+
 def test_hand_computed_two_party(orc):
     d, W, X, A, mask, prot = _tiny(orc)
     k0, k1 = orc.model_keygen(d, 1, 99, W)
