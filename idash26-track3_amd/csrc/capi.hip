@@ -421,7 +421,8 @@ static hipError_t tr_eval_run(mpcx_ctx *c, const TrLayout &lay, size_t n, const 
   hipError_t e = launch_tr_eval<T>(c->L, lay, K0, K1, X, Bi, ncol, y);
   if (e != hipSuccess) return e;
   c->counters.bitplanes(n, int(lay.use_a) + int(lay.use_b));
-  if (lay.kind != MPCX_DRELU) c->counters.msg(n, c->bw);  // DRELU: the output bit is already public
+  if (lay.kind != MPCX_DRELU)  // DRELU: the output bit is already public
+    c->counters.msg_bits(n, tr_out_bits(lay.kind, c->bw, c->s), c->bw);
   return hipSuccess;
 }
 

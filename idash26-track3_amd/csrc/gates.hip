@@ -154,6 +154,15 @@ __device__ __forceinline__ T tr_out_share(const TrArgs<T> &a, int p, const uint8
   return one0 * A + G[size_t(Hh * 2 + dh) * a.N + i];
 }
 
+// The revealed output from the two parties' messages: their sum, reduced to
+// bw - s bits for TRMOD (tr_out_bits), whose output is known only modulo
+// 2^(bw-s) and is revealed at that width.
+template <typename T>
+__device__ __forceinline__ T tr_reveal_sum(const TrArgs<T> &a, T m0, T m1) {
+  const T y = m0 + m1;
+  return a.kind == G_TRMOD ? low_bits<T>(y, a.n - a.s) : y;
+}
+
 // One launch evaluates a gate for both parties.  A workgroup of 2h threads
 // takes tiles of h elements: its first h threads are party 0, the last h party
 // 1, each evaluating its own keys on the same elements.  The two exchanges of
@@ -199,7 +208,7 @@ __device__ __forceinline__ T tr_tile(Aes &aes, const TrArgs<T> &a, TrXchg<T> &x,
     x.xm[p][e] = tr_out_share(a, p, K, i, xh, xp, hb, bh, dh);  // exchange 2: the output messages
   }
   __syncthreads();
-  const T y = in ? T(x.xm[0][e] + x.xm[1][e]) : T(0);
+  const T y = in ? tr_reveal_sum<T>(a, x.xm[0][e], x.xm[1][e]) : T(0);
   __syncthreads();  // the next gate or tile reuses the exchange buffers
   return y;
 }
@@ -277,7 +286,8 @@ __device__ __forceinline__ T tr_both(const Aes &aes, const TrArgs<T> &a, size_t 
           get_bit(reinterpret_cast<const uint64_t *>(a.k1 + a.b.off_z), i);
   }
   const uint32_t hb = uint32_t(xp >> a.sb) & 1u;
-  return T(tr_out_share(a, 0, a.k0, i, xh, xp, hb, bh, dh) + tr_out_share(a, 1, a.k1, i, xh, xp, hb, bh, dh));
+  return tr_reveal_sum<T>(a, tr_out_share(a, 0, a.k0, i, xh, xp, hb, bh, dh),
+                          tr_out_share(a, 1, a.k1, i, xh, xp, hb, bh, dh));
 }
 
 // The elements of a both-party launch, one per thread (grid-stride): gate a,
@@ -360,7 +370,7 @@ __device__ __forceinline__ T tr_tile_quad(const AesQuad &aes, const AesQuad::Key
     if ((lane_id() & 3u) == 0) x.xm[p][e] = msg;
   }
   __syncthreads();
-  const T y = in ? T(x.xm[0][e] + x.xm[1][e]) : T(0);
+  const T y = in ? tr_reveal_sum<T>(a, x.xm[0][e], x.xm[1][e]) : T(0);
   __syncthreads();
   return y;
 }

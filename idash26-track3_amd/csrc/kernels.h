@@ -132,6 +132,13 @@ hipError_t launch_tr_party_msg(const Launch &L, const TrLayout &lay, const uint8
 // out = m0 + m1 (reconstruction of a revealed value from both parties' messages)
 template <typename T>
 hipError_t launch_reconstruct(const Launch &L, size_t n, const T *m0, const T *m1, T *out);
+// Reduced-width wire form (party mode) of a message known modulo 2^m, 1 <= m <
+// bits of T: element i at bits [i m, i m + m) of packed_words(n, m) 64-bit words.
+template <typename T>
+hipError_t launch_pack_bits(const Launch &L, size_t n, int m, const T *v, uint64_t *words);
+// out[i] = (own[i] + element i of the peer's packed message) mod 2^m
+template <typename T>
+hipError_t launch_unpack_reconstruct(const Launch &L, size_t n, int m, const T *own, const uint64_t *peer, T *out);
 // LocalARS: y[i] = (signed x[i]) >> s + (bias ? bias[i % ncol] : 0), mod 2^bw (bw = 8 sizeof(T))
 template <typename T>
 hipError_t launch_local_ars(const Launch &L, size_t n, int s, const T *x, const T *bias, int ncol, T *y);

@@ -211,6 +211,58 @@ hipError_t launch_reconstruct(const Launch &L, size_t n, const T *m0, const T *m
   return hipGetLastError();
 }
 
+// Reduced-width wire form of a revealed value known modulo 2^m (m < bits of T):
+// element i occupies bits [i m, i m + m) of a little-endian stream of 64-bit
+// words, ceil(n m / 64) words in all (the reference sends truncate-reduce
+// outputs at bout bits the same way, gpu_mpc/utils/gpu_comms.h:143-168).
+// One thread per word: the word's first element may start in the previous
+// word, the others follow every m bits.
+template <typename T>
+__global__ void k_pack_bits(size_t n, int m, const T *v, uint64_t *words, size_t nw) {
+  const uint64_t vm = (m >= 64) ? ~0ull : ((1ull << m) - 1ull);
+  for (size_t w = size_t(blockIdx.x) * blockDim.x + threadIdx.x; w < nw; w += size_t(gridDim.x) * blockDim.x) {
+    const uint64_t bit0 = uint64_t(w) * 64u;
+    size_t e = size_t(bit0 / uint64_t(m));
+    const int off = int(bit0 - uint64_t(e) * uint64_t(m));  // bits of element e already in word w - 1
+    uint64_t acc = (uint64_t(v[e]) & vm) >> off;
+    int pos = m - off;
+    for (++e; pos < 64 && e < n; ++e, pos += m) acc |= (uint64_t(v[e]) & vm) << pos;
+    words[w] = acc;
+  }
+}
+// out[i] = (own[i] + the peer's packed element i) mod 2^m
+template <typename T>
+__global__ void k_unpack_reconstruct(size_t n, int m, const T *own, const uint64_t *peer, T *out) {
+  const uint64_t vm = (1ull << m) - 1ull;
+  for (size_t i = size_t(blockIdx.x) * blockDim.x + threadIdx.x; i < n; i += size_t(gridDim.x) * blockDim.x) {
+    const uint64_t bit = uint64_t(i) * uint64_t(m);
+    const size_t w = size_t(bit >> 6);
+    const int off = int(bit & 63u);
+    uint64_t v = peer[w] >> off;
+    if (off + m > 64) v |= peer[w + 1] << (64 - off);  // the element runs into the next word
+    out[i] = T((uint64_t(own[i]) + v) & vm);
+  }
+}
+template <typename T>
+hipError_t launch_pack_bits(const Launch &L, size_t n, int m, const T *v, uint64_t *words) {
+  if (m < 1 || m >= int(8 * sizeof(T))) return hipErrorInvalidValue;
+  const size_t nw = packed_words(n, m);
+  if (nw == 0) return hipSuccess;
+  const int block = 256;
+  int grid = grid_for(k_pack_bits<T>, block, nw, L.num_cu);
+  hipLaunchKernelGGL((k_pack_bits<T>), dim3(grid), dim3(block), 0, L.stream, n, m, v, words, nw);
+  return hipGetLastError();
+}
+template <typename T>
+hipError_t launch_unpack_reconstruct(const Launch &L, size_t n, int m, const T *own, const uint64_t *peer, T *out) {
+  if (m < 1 || m >= int(8 * sizeof(T))) return hipErrorInvalidValue;
+  if (n == 0) return hipSuccess;
+  const int block = 256;
+  int grid = grid_for(k_unpack_reconstruct<T>, block, n, L.num_cu);
+  hipLaunchKernelGGL((k_unpack_reconstruct<T>), dim3(grid), dim3(block), 0, L.stream, n, m, own, peer, out);
+  return hipGetLastError();
+}
+
 // LocalARS (TruncateType::LocalARS, gpu_mpc/ddg_orca_batched.h:180-199): the
 // masked value and (at keygen) its mask are shifted locally, no key, no exchange.
 template <typename T>
@@ -998,6 +1050,8 @@ hipError_t launch_rowsum(const Launch &L, size_t rows, int len, const T *a, T *o
 // ---------------------------------------------------------------------------
 #define INST(T)                                                                                                       \
   template hipError_t launch_reconstruct<T>(const Launch &, size_t, const T *, const T *, T *);                       \
+  template hipError_t launch_pack_bits<T>(const Launch &, size_t, int, const T *, uint64_t *);                        \
+  template hipError_t launch_unpack_reconstruct<T>(const Launch &, size_t, int, const T *, const uint64_t *, T *);    \
   template hipError_t launch_local_ars<T>(const Launch &, size_t, int, const T *, const T *, int, T *);               \
   template hipError_t launch_reveal_keygen<T>(const Launch &, const RevealLayout &, uint64_t, uint32_t, T *,          \
                                               uint8_t *, uint8_t *);                                                  \

@@ -51,6 +51,12 @@ struct Counters {
     bytes += 2ull * n_elems * uint64_t(bw / 8);
     rounds++;
   }
+  // a message known modulo 2^m, m < bw: packed at m bits into 64-bit words
+  void msg_bits(size_t n_elems, int m, int bw) {
+    if (m >= bw) return msg(n_elems, bw);
+    bytes += 2ull * 8ull * packed_words(n_elems, m);
+    rounds++;
+  }
   void bitplanes(size_t n, int planes) {
     bytes += 2ull * uint64_t(planes) * (((n + 31) / 32) * 4);
     rounds++;

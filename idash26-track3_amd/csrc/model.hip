@@ -194,6 +194,18 @@ struct Runner {
     TRY(peer->exchange(L.stream, &seg, 1));
     return launch_reconstruct<T>(L, n, ws.m0.p, ws.m1.p, out);
   }
+  // the same for a message known modulo 2^m: on the wire at m bits per element
+  // (packed into the bit-plane buffers, free once the gate's planes are used),
+  // out = (m0 + m1) mod 2^m
+  hipError_t exchange_reconstruct_bits(size_t n, int m, T *out) {
+    if (m >= bw) return exchange_reconstruct(n, out);
+    const size_t nw = packed_words(n, m);
+    TRY(ws.ensure_bits(nw));
+    TRY(launch_pack_bits<T>(L, n, m, ws.m0.p, ws.b0.p));
+    const Peer::Seg seg{ws.b0.p, ws.b1.p, nw * 8};
+    TRY(peer->exchange(L.stream, &seg, 1));
+    return launch_unpack_reconstruct<T>(L, n, m, ws.m0.p, ws.b1.p, out);
+  }
 
   // Make the gate [c.off, end) available; returns the base of the gate
   // relative to the key view.
@@ -243,7 +255,7 @@ struct Runner {
     if (lay.kind == G_DRELU)  // the output bit is public now
       return launch_tr_party_msg<T>(L, lay, own_key(), x, bias, ncol, ws.b0.p, ws.b1.p, out);
     TRY(launch_tr_party_msg<T>(L, lay, own_key(), x, bias, ncol, ws.b0.p, ws.b1.p, ws.m0.p));
-    return exchange_reconstruct(n, out);
+    return exchange_reconstruct_bits(n, tr_out_bits(lay.kind, bw, s), out);
   }
 
   // AES calls per element and party of a gate's DCF walks
@@ -298,7 +310,7 @@ struct Runner {
       TRY(launch_tr_eval<T>(L1, lay, kv.k[0], kv.k[1], x, bias, ncol, out));
     TRY(time_end(e0, e1, n, tr_levels(lay), tr_key_bytes(lay)));
     ctr.bitplanes(n, int(lay.use_a) + int(lay.use_b));
-    if (kind != G_DRELU) ctr.msg(n, bw);  // DRELU: the output bit is already public
+    if (kind != G_DRELU) ctr.msg_bits(n, tr_out_bits(kind, bw, s), bw);  // DRELU: the output bit is already public
     leave(end);
     return hipSuccess;
   }
@@ -323,7 +335,7 @@ struct Runner {
     TRY(time_end(e0, e1, n, tr_levels(lay) + tr_levels(lay2), tr_key_bytes(lay) + tr_key_bytes(lay2)));
     for (const TrLayout *l : {&lay, &lay2}) {
       ctr.bitplanes(n, int(l->use_a) + int(l->use_b));
-      ctr.msg(n, bw);
+      ctr.msg_bits(n, tr_out_bits(l->kind, bw, s), bw);
     }
     leave(end2);
     return hipSuccess;

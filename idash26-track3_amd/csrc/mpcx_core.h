@@ -45,6 +45,11 @@ inline bool tr_has_bias(int kind) { return kind == G_TR || kind == G_TRRELU || k
 inline bool tr_is_relu(int kind) {
   return kind == G_TRRELU || kind == G_RELU || kind == G_RELUSLACK || kind == G_EXTRELU || kind == G_RELUPOOL;
 }
+// Bits of a gate's revealed output: a TRMOD output is known modulo 2^(bw-s)
+// only, so it is revealed (and sent) reduced to bw - s bits; the others at bw.
+inline int tr_out_bits(int kind, int bw, int s) { return kind == G_TRMOD ? bw - s : bw; }
+// 64-bit words of n elements packed at m bits each
+inline constexpr size_t packed_words(size_t n, int m) { return (n * size_t(m) + 63) / 64; }
 // the (sign-bit)-bit DCF "a" and the s-bit DCF "b"
 inline bool tr_uses_a(int kind) { return kind != G_TRSLACK && kind != G_TRMOD && kind != G_LOCALARS; }
 inline bool tr_uses_b(int kind) { return tr_has_bias(kind); }

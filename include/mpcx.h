@@ -57,8 +57,11 @@ typedef struct mpcx_model mpcx_model;
 /* Exact truncation in two gates, the reference's TrFloor composition (truncate-reduce
    then sign extension, gpu_mpc/dpf_dcf_adapter.h:274-303) and its ReLU-extend
    (gpuReluExtend, :225-234; keygen bin = bw - scale, bout = bw, gpu_mpc/ddg_orca.h:222): */
-#define MPCX_TRMOD 12   /* floor(x/2^s) + bias, exact modulo 2^(bw-s) only (the yhat bits
-                           above bw-s are not meaningful): one s-bit DCF */
+#define MPCX_TRMOD 12   /* floor(x/2^s) + bias, exact modulo 2^(bw-s) only: one s-bit DCF;
+                           yhat is revealed reduced to bw-s bits (in [0, 2^(bw-s))) and
+                           counted (and sent, in party mode) packed at bw-s bits per
+                           element, as the reference's truncate-reduce reveal at bout bits
+                           (gpu_mpc/dpf_dcf_adapter.h:297, gpu_comms.h:143-168) */
 #define MPCX_EXT 13     /* y sign-extended from bw-s bits: the input is a TRMOD output
                            (only its low bw-s bits are read, and of the input mask too);
                            one (bw-s-1)-bit DCF.  TRMOD then EXT = MPCX_TR */

@@ -95,6 +95,13 @@ static inline uint64_t prf_ring(const orc_prf *P, uint32_t g, uint32_t f, uint64
   return ring_of(orc_prf_blk(P, g, f, i), bw);
 }
 static size_t bitplane_bytes(size_t N) { return ((N + 31) / 32) * 4; }
+/* a message of N elements known modulo 2^m (m < bw) goes out packed at m bits
+ * per element in 64-bit words (gpu_mpc/utils/gpu_comms.h:143-168: compressMem's
+ * ((N m - 1) / 64 + 1) * 8 bytes for a truncate-reduce output revealed at
+ * bout = bin - shift bits, gpu_mpc/dpf_dcf_adapter.h:297) */
+static uint64_t msg_bytes(size_t N, int m, int bw) {
+  return m < bw ? (((uint64_t)N * (uint64_t)m + 63) / 64) * 8 : (uint64_t)N * (uint64_t)(bw / 8);
+}
 
 static int g_threads = 0;
 void orc_set_threads(int n) { g_threads = n; }
@@ -574,8 +581,10 @@ void orc_tr_eval(int kind, int bw, int s, size_t N, const uint8_t *k0, const uin
       y[p][i] = out & M;
     }
   }
-  if (bytes && kind != ORC_G_DRELU) *bytes += 2ull * N * (uint64_t)(bw / 8);
-  for (size_t i = 0; i < N; i++) yhat[i] = (y[0][i] + y[1][i]) & M;
+  /* TRMOD's output is known modulo 2^(n-s) only: revealed (and sent) at n - s bits */
+  const int ob = kind == ORC_G_TRMOD ? n - s : n;
+  if (bytes && kind != ORC_G_DRELU) *bytes += 2ull * msg_bytes(N, ob, bw);
+  for (size_t i = 0; i < N; i++) yhat[i] = (y[0][i] + y[1][i]) & rmask(ob);
   for (int p = 0; p < 2; p++) {
     free(bb[p]);
     free(dd[p]);

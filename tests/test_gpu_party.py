@@ -92,6 +92,15 @@ def test_party_tr_gates(bw, kind, name):
     assert np.array_equal(r0[0], want) and np.array_equal(r1[0], want)
     assert r0[1] == r1[1] == want_bytes
     assert wire[0] == wire[1] == want_bytes
+    if kind == 12:
+        # TRMOD's output is known modulo 2^(bw-s): revealed, and sent, at bw-s
+        # bits per element packed in 64-bit words (gpu_mpc/utils/gpu_comms.h:143-168)
+        assert want_bytes == 2 * (((n + 31) // 32) * 4 + ((n * (bw - S) + 63) // 64) * 8)
+        assert np.all(want.astype(np.uint64) < np.uint64(1 << (bw - S)))
+        exp = (x + (np.resize(bias, n) << S)) >> S
+        low = np.uint64((1 << (bw - S)) - 1)
+        assert np.array_equal((want.astype(np.uint64) - rout.astype(np.uint64)) & low,
+                              exp.astype(np.uint64) & low)
     if kind == 11:  # DRELU: the masked public bit
         assert np.array_equal((want.astype(np.uint64) ^ rout.astype(np.uint64)) & np.uint64(1),
                               (x >= 0).astype(np.uint64))

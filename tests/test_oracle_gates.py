@@ -95,6 +95,7 @@ def test_split_truncation(orc, bw, relu):
     y1, b1 = orc.tr_eval(12, bw, S, k0, k1, (ring(x, bw) + rin) & M, bias)
     exp = (x + (bias << S)) >> S
     assert np.array_equal((y1 - r1) & low, ring(exp, bw) & low)
+    assert np.all(y1 <= low)  # revealed reduced to bw-s bits, as the reference's bout = bin - shift
     # only the low bw-s bits are meaningful: move the high bits of the value and
     # of its mask independently
     y1x = (y1 + (rng.integers(0, 1 << S, size=N).astype(np.uint64) << np.uint64(bw - S))) & M
@@ -105,7 +106,10 @@ def test_split_truncation(orc, bw, relu):
     got = to_signed(y2 - r2, bw)
     assert np.array_equal(got, np.maximum(exp, 0) if relu else exp)
     per = 2 * (((N + 31) // 32) * 4 + N * bw // 8)
-    assert b1 == per and b2 == per
+    # TRMOD's message goes out packed at bw-s bits per element in 64-bit words
+    # (gpu_mpc/utils/gpu_comms.h:143-168): at bw=32, 20 bits instead of 32
+    packed = 2 * (((N + 31) // 32) * 4 + ((N * (bw - S) + 63) // 64) * 8)
+    assert b1 == packed and b2 == per
     split = orc.tr_layout(12, bw, S, N).end + orc.tr_layout(kind, bw, S, N).end
     assert split < orc.tr_layout(2 if relu else 1, bw, S, N).end
 
