@@ -101,6 +101,7 @@ struct mpcx_ctx {
   // this device's copy of the static scratch array (mpcx_maxpool_eval_noalloc)
   void *noalloc_scratch = nullptr;
   hipError_t noalloc_err = hipSuccess;
+  hipEvent_t noalloc_done = nullptr;  // recorded after each of this context's calls on the array
   PartyWork *party = nullptr;   // workspace of the party-mode gate calls
   AdjNormCache *adj = nullptr;  // prepared state of mpcx_adjnorm_eval
   int adj_lanes = 1;            // concurrent graph groups of the adjacency normalisation
@@ -165,7 +166,10 @@ static size_t guard_size(F &&f) noexcept {
 // device by mpcx_create (noalloc_scratch_resolve) and kept in g_scratch_addr;
 // host code uses only that address, never the array's name (which names a
 // host-side stand-in).  Every level plane is written before it is read, so
-// nothing in the array has to start at zero.
+// nothing in the array has to start at zero.  The array's last user on each
+// device (its stream and the event its context recorded after the call) is
+// kept in g_scratch_stream / g_scratch_event: a call from another stream while
+// that event is pending is refused (MPCX_EBUSY) instead of racing on the array.
 static __device__ __align__(256) unsigned char scratch[MPCX_NOALLOC_SCRATCH_BYTES];
 
 namespace {
@@ -174,6 +178,8 @@ std::mutex g_scratch_mu;
 void *g_scratch_addr[kMaxDevices];
 hipError_t g_scratch_err[kMaxDevices];
 bool g_scratch_done[kMaxDevices];
+hipStream_t g_scratch_stream[kMaxDevices];
+hipEvent_t g_scratch_event[kMaxDevices];  // the owner context's noalloc_done (null: none)
 
 // With `device` current: look up the device's copy of `scratch` (once per device).
 hipError_t noalloc_scratch_resolve(int device, void **out) {
@@ -212,6 +218,11 @@ mpcx_status mpcx_create(int bw, int scale, int device, mpcx_ctx **out) {
   }
   c->L.stream = c->own;
   c->noalloc_err = noalloc_scratch_resolve(device, &c->noalloc_scratch);
+  if (hipEventCreateWithFlags(&c->noalloc_done, hipEventDisableTiming) != hipSuccess) {
+    (void)hipStreamDestroy(c->own);
+    delete c;
+    return MPCX_EHIP;
+  }
   // The environment overrides take the same checks as mpcx_set_aes_variant: a
   // bad value is ignored with a warning (a block that is not a whole number of
   // wave pairs would misplace the DCF kernels' ballot words).
@@ -241,6 +252,15 @@ mpcx_status mpcx_create(int bw, int scale, int device, mpcx_ctx **out) {
 
 void mpcx_destroy(mpcx_ctx *c) {
   if (!c) return;
+  if (c->noalloc_done) {  // no longer the scratch array's owner once its last call is done
+    std::lock_guard<std::mutex> lk(g_scratch_mu);
+    (void)hipEventSynchronize(c->noalloc_done);
+    if (c->device >= 0 && c->device < kMaxDevices && g_scratch_event[c->device] == c->noalloc_done) {
+      g_scratch_event[c->device] = nullptr;
+      g_scratch_stream[c->device] = nullptr;
+    }
+    (void)hipEventDestroy(c->noalloc_done);
+  }
   if (c->own) {
     (void)hipStreamSynchronize(c->own);
     (void)hipStreamDestroy(c->own);
@@ -605,10 +625,26 @@ mpcx_status mpcx_maxpool_eval_noalloc(mpcx_ctx *c, int B, int N, int C, const vo
   if (!c->noalloc_scratch)
     return fail(c, MPCX_EHIP, std::string("maxpool_eval_noalloc: no scratch address on this device: ") +
                                   hipGetErrorString(c->noalloc_err));
+  const int dv = c->device;
+  std::lock_guard<std::mutex> lk(g_scratch_mu);  // held until this call's work and event are enqueued
+  if (g_scratch_event[dv] && g_scratch_stream[dv] != c->L.stream) {
+    const hipError_t q = hipEventQuery(g_scratch_event[dv]);
+    if (q == hipErrorNotReady)
+      return fail(c, MPCX_EBUSY,
+                  "maxpool_eval_noalloc: the static scratch array is in use by a call still pending on another stream");
+    HIPC(c, q, "maxpool_eval_noalloc: hipEventQuery");
+  }
+  hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+  HIPC(c, hipStreamIsCapturing(c->L.stream, &cs), "maxpool_eval_noalloc: hipStreamIsCapturing");
   const hipError_t e = c->bw == 32
                            ? maxpool_eval_run<uint32_t>(c, B, N, C, k0, k1, in, out, c->noalloc_scratch)
                            : maxpool_eval_run<uint64_t>(c, B, N, C, k0, k1, in, out, c->noalloc_scratch);
   HIPC(c, e, "maxpool_eval_noalloc");
+  if (cs == hipStreamCaptureStatusNone) {  // captured calls run at replay: not tracked
+    HIPC(c, hipEventRecord(c->noalloc_done, c->L.stream), "maxpool_eval_noalloc: hipEventRecord");
+    g_scratch_stream[dv] = c->L.stream;
+    g_scratch_event[dv] = c->noalloc_done;
+  }
   return MPCX_OK;
 }
 

@@ -15,8 +15,11 @@
 //             file and share files, exchanges with the other party's process over
 //             the Unix socket MPCX_PEER (party 0 listens, party 1 connects);
 //             party MPCX_PARTY (0 or 1); party 1 reads protein_emb.dat
-//   environment: MPCX_WEIGHTS_BIN (default ./weights.bin), MPCX_SEED (dealer
-//   seed, default 12345), MPCX_LANES (concurrent sub-batches, default 1),
+//   environment: MPCX_WEIGHTS_BIN (default ./weights.bin), MPCX_DEALER_KEY (a
+//   file of the dealer's 16 secret key bytes: roles 0 and 2 derive every key
+//   set from them; without it the keys rest on the seed alone, which is said on
+//   stderr), MPCX_SEED (dealer seed, names the key set, default 12345),
+//   MPCX_LANES (concurrent sub-batches, default 1),
 //   MPCX_LUT_NMAX (largest degree with a D^-1/2 table entry, default 138),
 //   MPCX_SLACK (slack truncations of the GCN, 0 / 1 / 2, default 0: exact).
 //
@@ -72,6 +75,16 @@ std::vector<uint8_t> read_bytes(const std::string &path) {
   std::ifstream f(path, std::ios::binary);
   if (!f) die("cannot open " + path);
   return std::vector<uint8_t>(std::istreambuf_iterator<char>(f), std::istreambuf_iterator<char>());
+}
+
+// The dealer's secret key: 16 bytes from the file MPCX_DEALER_KEY, if set.
+bool dealer_key(uint8_t key[16]) {
+  const char *p = std::getenv("MPCX_DEALER_KEY");
+  if (!p || !*p) return false;
+  const std::vector<uint8_t> k = read_bytes(p);
+  if (k.size() != 16) die(std::string("MPCX_DEALER_KEY (") + p + ") must hold exactly 16 bytes");
+  std::memcpy(key, k.data(), 16);
+  return true;
 }
 
 // "key": integer, from a flat manifest
@@ -157,6 +170,18 @@ int main(int argc, char **argv) {
 
   mpcx_ctx *ctx = nullptr;
   if (mpcx_create(bw, scale, 0, &ctx) != MPCX_OK) die("mpcx_create failed (no GPU?)");
+  if (role == 0 || role == 2) {  // the dealer: its secret key, read by models created afterwards
+    uint8_t dk[16];
+    if (dealer_key(dk)) {
+      check(ctx, mpcx_set_dealer_key(ctx, dk), "set_dealer_key");
+      volatile uint8_t *v = dk;
+      for (int i = 0; i < 16; i++) v[i] = 0;
+    } else {
+      std::fprintf(stderr,
+                   "mpcx_infer: warning: no MPCX_DEALER_KEY: the key sets derive from the seed MPCX_SEED alone, "
+                   "so anyone who knows the seed can regenerate every mask\n");
+    }
+  }
   mpcx_model *m = nullptr;
   check(ctx, mpcx_model_create(ctx, &d, W.data(), W.size(), &m), "model_create");
   check(ctx, mpcx_model_set_lanes(m, env_int("MPCX_LANES", 1)), "model_set_lanes");

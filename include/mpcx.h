@@ -34,6 +34,8 @@ typedef int mpcx_status;
 #define MPCX_ESTATE 4  /* call out of order (e.g. forward before keygen)    */
 #define MPCX_EIO 5     /* a key file could not be opened, read or written, or
                           the channel to the other party failed              */
+#define MPCX_EBUSY 6   /* a shared resource is in use by work still pending on
+                          another stream (mpcx_maxpool_eval_noalloc)         */
 
 typedef struct mpcx_ctx mpcx_ctx;
 typedef struct mpcx_model mpcx_model;
@@ -201,8 +203,12 @@ mpcx_status mpcx_maxpool_eval(mpcx_ctx *ctx, int B, int N, int C, const void *d_
  * output is ready when the context's stream reaches it).  It needs
  * (2*B*N*C + 2*B*floor(N/2)*C) * bw/8 bytes of that array (64 x 140 x 312 fits
  * at both widths); larger calls fail with MPCX_EINVAL.  Every call on one GPU
- * shares that GPU's array: calls on one stream run in order, calls that overlap
- * (other streams, threads or contexts on the same GPU) race. */
+ * shares that GPU's array: calls on one stream run in order; a call on another
+ * stream (another context, thread or mpcx_set_stream) while the last call's
+ * work is still pending fails with MPCX_EBUSY before any launch (the library
+ * tracks the last caller's stream and an event it records after the call;
+ * calls captured into a HIP graph are not tracked, so replays of such a graph
+ * must not overlap other calls on the same GPU). */
 #define MPCX_NOALLOC_SCRATCH_BYTES ((size_t)64 << 20)
 mpcx_status mpcx_maxpool_eval_noalloc(mpcx_ctx *ctx, int B, int N, int C, const void *d_key0,
                                       const void *d_key1, const void *d_xhat, void *d_yhat);

@@ -17,8 +17,10 @@
 //     GpuPeer (GpuPeer(compress) + connect(party, addr), reconstructInPlace).
 // Differences, by design:
 //   - the two keygen runs (one per party) draw the dealer's randomness from the
-//     same seed (MPCX_DEALER_SEED, default 0x5EED, reset by initGPURandomness),
-//     so both write consistent keys, as the reference's seeded GPU RNG does;
+//     same secret key and seed (the 16-byte file MPCX_DEALER_KEY and
+//     MPCX_DEALER_SEED, default 0x5EED, read by initGPURandomness), so both
+//     write consistent keys, as the reference's seeded GPU RNG does; without a
+//     key file the seed alone determines the keys (a warning on stderr);
 //   - the key bytes are libmpcx's format: a 256-byte record header (type and
 //     sizes) before each key, checked by the read functions; writeShares writes
 //     raw ring elements, as the reference's readers expect;
@@ -87,6 +89,10 @@ inline void hip_check(hipError_t e, const char *what) {
   if (e != hipSuccess) die(std::string(what) + ": " + hipGetErrorString(e));
 }
 
+// The scale of the context that serves a gate which does not read it (the
+// full-width DReLU and ReLU): any valid one; 12 is the reference's.
+constexpr int kFullWidthScale = 12;
+
 // Process-wide state: the dealer's seed and gate counter, identity index maps,
 // the registered device key arena.
 struct Runtime {
@@ -94,6 +100,11 @@ struct Runtime {
   int device = 0;
   uint64_t seed = 0x5EED;
   uint32_t gate = 1;
+  // the dealer's secret key (initGPURandomness, from the file MPCX_DEALER_KEY);
+  // key_epoch counts its changes so that every thread's contexts take it up
+  uint8_t dealer_key[16] = {};
+  bool has_key = false;
+  uint32_t key_epoch = 0;
   std::map<size_t, uint32_t *> iota;
   const u8 *host_base = nullptr;  // initGPUKeyArena: [host_base, +arena_bytes) mirrored at arena
   u8 *arena = nullptr;
@@ -108,20 +119,32 @@ struct Runtime {
 // workspaces serve one caller at a time; two parties may run as two threads),
 // destroyed when the thread ends.
 struct ThreadContexts {
-  std::map<std::pair<int, int>, mpcx_ctx *> ctx;
+  struct Entry {
+    mpcx_ctx *c = nullptr;
+    uint32_t key_epoch = 0;  // the dealer key this context holds (Runtime::key_epoch)
+  };
+  std::map<std::pair<int, int>, Entry> ctx;
   ~ThreadContexts() {
-    for (auto &kv : ctx) mpcx_destroy(kv.second);
+    for (auto &kv : ctx) mpcx_destroy(kv.second.c);
   }
 };
 inline mpcx_ctx *ctx(int bw, int scale = 12) {
   thread_local ThreadContexts tc;
+  Runtime &R = Runtime::get();
   auto it = tc.ctx.find({bw, scale});
-  if (it != tc.ctx.end()) return it->second;
-  mpcx_ctx *c = nullptr;
-  if (mpcx_create(bw, scale, Runtime::get().device, &c) != MPCX_OK)
-    die("mpcx_create(bw " + std::to_string(bw) + ", scale " + std::to_string(scale) + ") failed");
-  tc.ctx[{bw, scale}] = c;
-  return c;
+  if (it == tc.ctx.end()) {
+    mpcx_ctx *c = nullptr;
+    if (mpcx_create(bw, scale, R.device, &c) != MPCX_OK)
+      die("mpcx_create(bw " + std::to_string(bw) + ", scale " + std::to_string(scale) + ") failed");
+    it = tc.ctx.emplace(std::make_pair(bw, scale), ThreadContexts::Entry{c, 0}).first;
+  }
+  std::lock_guard<std::mutex> lk(R.mu);
+  if (it->second.key_epoch != R.key_epoch) {  // a new dealer key (or none) since this context last dealt
+    if (mpcx_set_dealer_key(it->second.c, R.has_key ? R.dealer_key : nullptr) != MPCX_OK)
+      die("mpcx_set_dealer_key failed");
+    it->second.key_epoch = R.key_epoch;
+  }
+  return it->second.c;
 }
 // Every library call is followed by a synchronisation of the context's stream:
 // the contexts' streams do not order with the null stream that the callers'
@@ -331,12 +354,39 @@ inline void initAESContext(AESGlobalContext *g) {
   if (g) g->device = mpcx_ezpc::Runtime::get().device;
 }
 // Resets the dealer's randomness: both parties' keygen runs then draw the same
-// sequence and write consistent keys.
+// sequence and write consistent keys.  The dealer's secret key comes from the
+// file named by MPCX_DEALER_KEY (16 bytes), and the seed (MPCX_DEALER_SEED)
+// then only names the key set; without a key file the keys rest on the seed
+// alone, which is said once on stderr.
 inline void initGPURandomness() {
   mpcx_ezpc::Runtime &R = mpcx_ezpc::Runtime::get();
   const char *s = std::getenv("MPCX_DEALER_SEED");
+  const char *kf = std::getenv("MPCX_DEALER_KEY");
+  uint8_t key[16] = {};
+  bool has = false;
+  if (kf && *kf) {
+    FILE *f = std::fopen(kf, "rb");
+    if (!f) mpcx_ezpc::die(std::string("cannot open MPCX_DEALER_KEY file ") + kf);
+    const size_t got = std::fread(key, 1, 16, f);
+    const int extra = std::fgetc(f);
+    std::fclose(f);
+    if (got != 16 || extra != EOF) mpcx_ezpc::die(std::string("MPCX_DEALER_KEY (") + kf + ") must hold exactly 16 bytes");
+    has = true;
+  }
+  std::lock_guard<std::mutex> lk(R.mu);
   R.seed = s && *s ? std::strtoull(s, nullptr, 0) : 0x5EEDull;
   R.gate = 1;
+  if (has != R.has_key || std::memcmp(key, R.dealer_key, 16) != 0) {
+    std::memcpy(R.dealer_key, key, 16);
+    R.has_key = has;
+    R.key_epoch++;
+  }
+  static bool warned = false;
+  if (!has && !warned) {
+    warned = true;
+    std::fprintf(stderr, "mpcx_ezpc: warning: no MPCX_DEALER_KEY: the dealer's keys derive from the seed "
+                         "MPCX_DEALER_SEED alone, so anyone who knows the seed can regenerate every mask\n");
+  }
 }
 inline void destroyGPURandomness() {}
 inline void initCPURandomness() {}
@@ -479,7 +529,19 @@ struct KeyPair {
     (void)hipFree(k[1]);
   }
 };
-inline int relu_kind(int bw, int bin, int scale) { return bin == bw - scale ? MPCX_RELUPOOL : MPCX_RELU; }
+// The ReLU gate for inputs of bin significant bits: the full-width RELU at
+// bin = bw; for bin < bw (the reference's mode-3 ReLU, bin = bw - scale,
+// gpu_mpc/ddg_orca.h:229-233) the narrow RELUPOOL gate, exact for a full-width
+// input with |x| < 2^bin, i.e. at the context scale bw - bin, which a context
+// supports for 1 <= bw - bin <= bw/2 - 2.  Other widths cannot be served.
+inline int relu_scale(int bw, int bin, int bout) {
+  if (bout != bin && bout != bw) die("gpuGenReluKey: bout must be bin or the ring width");
+  if (bin == bw) return kFullWidthScale;
+  if (bw - bin < 1 || bw - bin > bw / 2 - 2)
+    die("gpuGenReluKey: no ReLU gate for " + std::to_string(bin) + "-bit inputs in a " + std::to_string(bw) +
+        "-bit ring (bin must be bw, or bw - scale with 1 <= scale <= bw/2 - 2)");
+  return bw - bin;
+}
 }  // namespace mpcx_ezpc
 
 // ===========================================================================
@@ -608,7 +670,9 @@ inline T *tr_eval(SigmaPeer *peer, int party, const GPUReluKey<T> &k, const T *d
 // gpuDRelu gives the masked public bit, [x >= 0] = bit XOR mask.
 template <typename T>
 inline T *gpuKeyGenDRelu(u8 **kb, int party, int bin, int N, T *d_mask, AESGlobalContext *) {
-  return mpcx_ezpc::tr_keygen<T>(kb, party, mpcx_ezpc::R_DRELU, MPCX_DRELU, 12, bin, 1, N, d_mask);
+  if (bin != 8 * int(sizeof(T))) mpcx_ezpc::die("gpuKeyGenDRelu: only full-width inputs (bin = the ring width)");
+  return mpcx_ezpc::tr_keygen<T>(kb, party, mpcx_ezpc::R_DRELU, MPCX_DRELU, mpcx_ezpc::kFullWidthScale, bin, 1, N,
+                                 d_mask);
 }
 inline GPUDReluKey readGPUDReluKey(u8 **kb) {
   return mpcx_ezpc::tr_read<u64>(kb, mpcx_ezpc::R_DRELU, "readGPUDReluKey");
@@ -623,8 +687,9 @@ template <typename TIn, typename TOut, int E1, int E2, bool B>
 inline TOut *gpuGenReluKey(u8 **kb, int party, int bin, int bout, int N, TIn *d_inMask, AESGlobalContext *) {
   static_assert(std::is_same<TIn, TOut>::value, "one ring type in and out");
   const int bw = 8 * int(sizeof(TIn));
-  // an input known to fit bw - 12 bits (the reference's mode-3 ReLU) takes the narrow gate
-  return mpcx_ezpc::tr_keygen<TIn>(kb, party, mpcx_ezpc::R_RELU, mpcx_ezpc::relu_kind(bw, bin, 12), 12, bin, bout,
+  // an input known to fit bin < bw bits (the reference's mode-3 ReLU) takes the narrow gate
+  const int sc = mpcx_ezpc::relu_scale(bw, bin, bout);
+  return mpcx_ezpc::tr_keygen<TIn>(kb, party, mpcx_ezpc::R_RELU, bin == bw ? MPCX_RELU : MPCX_RELUPOOL, sc, bin, bout,
                                    N, d_inMask);
 }
 template <typename T>

@@ -278,9 +278,31 @@ int run(const std::string &dir, const Dims &d) {
 
 }  // namespace
 
+// `ezpc_check width <bw> <bin> <bout> [drelu]`: a ReLU (or DReLU) keygen for
+// bin-bit inputs; widths the gates cannot serve abort with a message before
+// any device call (no GPU needed), the others print "width ok".
+template <typename T>
+int width_check(int bin, int bout, bool drelu) {
+  if (drelu) {
+    if (bin != 8 * int(sizeof(T))) gpuKeyGenDRelu<T>(nullptr, 0, bin, 0, nullptr, nullptr);
+  } else {
+    const int bw = 8 * int(sizeof(T));
+    const int sc = mpcx_ezpc::relu_scale(bw, bin, bout);
+    std::printf("width ok: scale %d\n", sc);
+    return 0;
+  }
+  std::printf("width ok\n");
+  return 0;
+}
+
 int main(int argc, char **argv) {
+  if (argc >= 5 && std::string(argv[1]) == "width") {
+    const int bw = std::atoi(argv[2]), bin = std::atoi(argv[3]), bout = std::atoi(argv[4]);
+    const bool drelu = argc >= 6 && std::string(argv[5]) == "drelu";
+    return bw == 32 ? width_check<uint32_t>(bin, bout, drelu) : width_check<uint64_t>(bin, bout, drelu);
+  }
   if (argc < 2) {
-    std::fprintf(stderr, "usage: %s <dir>\n", argv[0]);
+    std::fprintf(stderr, "usage: %s <dir> | width <bw> <bin> <bout> [drelu]\n", argv[0]);
     return 2;
   }
   const std::string dir = argv[1];

@@ -24,6 +24,26 @@ def test_ezpc_check_built():
     assert os.path.exists(BIN), "tests/cpp/ezpc_check not built (run __graft_entry__.build())"
 
 
+@pytest.mark.parametrize("bw,bin_,bout,drelu,ok", [
+    (32, 32, 32, False, True), (32, 20, 20, False, True), (32, 20, 32, False, True), (64, 52, 52, False, True),
+    (32, 21, 21, False, True), (32, 16, 16, False, False), (32, 20, 24, False, False), (64, 31, 31, False, False),
+    (32, 32, 1, True, True), (32, 20, 1, True, False)])
+def test_shim_relu_widths(bw, bin_, bout, drelu, ok):
+    """gpuGenReluKey serves bin = bw (full-width RELU) and bin = bw - scale for
+    a context scale 1..bw/2-2 (the narrow gate, the reference's mode-3 ReLU with
+    tmpBw = bw - scale, gpu_mpc/ddg_orca.h:229-233); gpuKeyGenDRelu only full
+    width. Any other width aborts with a message instead of evaluating a gate
+    of another width (checked before any device call: no GPU needed)."""
+    args = [BIN, "width", str(bw), str(bin_), str(bout)] + (["drelu"] if drelu else [])
+    r = subprocess.run(args, capture_output=True, text=True, timeout=60)
+    if ok:
+        assert r.returncode == 0 and "width ok" in r.stdout, r.stderr
+        if not drelu and bin_ < bw:
+            assert f"scale {bw - bin_}" in r.stdout
+    else:
+        assert r.returncode != 0 and "mpcx_ezpc:" in r.stderr
+
+
 def _ring(v, bw):
     dt = np.uint32 if bw == 32 else np.uint64
     m = (1 << bw) - 1
@@ -54,8 +74,12 @@ def test_shim_adjnorm_and_gcn_layer(orc, synth, tmp_path, bw):
     (d / "meta.txt").write_text(f"{bw} {B} {N} {F} {O} {S} {nmax}\n")
     for name, v in (("a0", a0), ("a1", a1), ("x0", x0), ("x1", x1), ("w", W), ("b", b << S)):
         _ring(v, bw).tofile(str(d / f"{name}.bin"))
-    r = subprocess.run([BIN, str(d)], capture_output=True, text=True, timeout=180)
+    kfile = d / "dealer.key"  # the dealers draw every key set under this secret key
+    kfile.write_bytes(bytes(range(40, 56)))
+    r = subprocess.run([BIN, str(d)], capture_output=True, text=True, timeout=180,
+                       env=dict(os.environ, MPCX_DEALER_KEY=str(kfile)))
     assert r.returncode == 0, r.stdout + r.stderr
+    assert "MPCX_DEALER_KEY" not in r.stderr
     dt = np.uint32 if bw == 32 else np.uint64
     An = orc.adj_norm_plain(A)
     got_an = _signed(np.fromfile(str(d / "adjn.bin"), dt), bw).reshape(B, N, N)

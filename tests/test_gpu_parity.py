@@ -1238,7 +1238,10 @@ def test_driver_dealer_then_evaluator(mp, orc, synth, tmp_path, bw):
     """mpcx_infer: the dealer run writes both parties' key files, the evaluator
     run reads them with the reference-format batch and weights and prints one
     AFFINITY line per molecule, equal to the fixed-point forward; the combined
-    run (role 2, two lanes) prints the same lines."""
+    run (role 2, two lanes) prints the same lines.  The dealer draws its keys
+    under the 16-byte secret key of MPCX_DEALER_KEY (other key files than the
+    seed alone gives, which it warns about); a key file of another size is
+    refused."""
     import os
     import re
     import subprocess
@@ -1257,19 +1260,35 @@ def test_driver_dealer_then_evaluator(mp, orc, synth, tmp_path, bw):
     lines = [f"AFFINITY[{j}]={v / 4096.0:.6f}" for j, v in enumerate(want)]
     env = dict(os.environ, MPCX_WEIGHTS_BIN=wpath)
 
-    def run(role, extra_env=None):
+    def run(role, extra_env=None, full=False):
         r = subprocess.run([exe, str(bw), "12", str(role), str(kdir), str(bdir)], env=dict(env, **(extra_env or {})),
                            capture_output=True, text=True, timeout=120)
         assert r.returncode == 0, r.stderr
-        return r.stdout
+        return r if full else r.stdout
 
-    run(0)
-    assert (kdir / f"DeepDTAGen_{bw}_12_party0").stat().st_size > 0
+    # the dealer with its secret key file (MPCX_DEALER_KEY), then without one
+    kfile = tmp_path / "dealer.key"
+    kfile.write_bytes(bytes(range(7, 23)))
+    kenv = {"MPCX_DEALER_KEY": str(kfile)}
+    r0 = run(0, kenv, full=True)
+    assert "MPCX_DEALER_KEY" not in r0.stderr
+    k_keyed = (kdir / f"DeepDTAGen_{bw}_12_party0").read_bytes()
+    assert len(k_keyed) > 0
     out = run(1)
     assert re.findall(r"AFFINITY\[\d+\]=\S+", out) == lines
     assert int(re.search(r"Comm \(B\)=(\d+)", out).group(1)) > 0
-    out2 = run(2, {"MPCX_LANES": "2"})
+    r0 = run(0, full=True)
+    assert "warning: no MPCX_DEALER_KEY" in r0.stderr
+    k_seed = (kdir / f"DeepDTAGen_{bw}_12_party0").read_bytes()
+    assert len(k_seed) == len(k_keyed) and k_seed != k_keyed  # the key, not the seed alone, drew the masks
+    out = run(1)
+    assert re.findall(r"AFFINITY\[\d+\]=\S+", out) == lines
+    out2 = run(2, dict(kenv, MPCX_LANES="2"))
     assert re.findall(r"AFFINITY\[\d+\]=\S+", out2) == lines
+    kfile.write_bytes(bytes(15))  # not 16 bytes: refused
+    bad = subprocess.run([exe, str(bw), "12", "0", str(kdir), str(bdir)], env=dict(env, **kenv),
+                         capture_output=True, text=True, timeout=120)
+    assert bad.returncode != 0 and "16 bytes" in bad.stderr
     # a batch that does not match the key files is refused
     bad = subprocess.run([exe, str(bw), "12", "1", str(kdir), str(bdir), "2"], env=env, capture_output=True,
                          text=True, timeout=120)
