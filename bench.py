@@ -156,6 +156,11 @@ def main():
                     help="streamed workload from key files in this directory: --sets distinct dealer key sets are "
                          "appended to two files and every micro-batch reads the next set (cycling)")
     ap.add_argument("--sets", type=int, default=4, help="key sets in the key files")
+    ap.add_argument("--party", action="store_true",
+                    help="party mode: the two parties as two processes on the one GPU, exchanging over a Unix "
+                         "socket (the reference's deployment); one lane per party")
+    ap.add_argument("--party-child", type=int, default=-1, help=argparse.SUPPRESS)
+    ap.add_argument("--party-sock", default="", help=argparse.SUPPRESS)
     args = ap.parse_args()
     if args.xw_slack:
         args.slack = max(args.slack, 1)
@@ -165,6 +170,10 @@ def main():
               file=sys.stderr)
         sys.exit(2)
 
+    if args.party_child >= 0:
+        return run_party_child(args)
+    if args.party:
+        return run_party(args)
     if args.stream:
         return run_stream(args)
     if args.workload == "relu":
@@ -503,6 +512,169 @@ def run_stream(args):
     for h in (h0, h1):
         if h is not None:
             h.free()
+
+
+def run_party_child(args):
+    """One party of the party-mode bench (a child of run_party): the dealer's
+    keys (the GPU dealer run here, this party's key kept), the channel, W
+    untimed forwards, a one-element exchange as a barrier, then K timed
+    forwards; prints one JSON line."""
+    import numpy as np
+
+    import mpcx
+    import synth
+
+    party, B = args.party_child, args.batch
+    dims = synth.Dims(bw=args.bw, slack=args.slack)
+    wl = synth.workload(B, dims, seed=args.seed)
+    ctx = mpcx.Ctx(bw=args.bw, scale=dims.s)
+    dealer = mpcx.Model(ctx, dims, wl.W)
+    dealer.keygen(B, 0xC0FFEE + args.seed)
+    key = dealer.export_keys(party, B)
+    prof = None
+    if party == 0:  # the gates' work per forward, from one profiled one-process forward on the same keys
+        dealer.set_inputs(B, *wl.shares["x"], *wl.shares["a"], *wl.shares["m"], wl.prot)
+        dealer.profile(True)
+        dealer.forward(B)
+        prof = dealer.profile_read()
+        dealer.profile(False)
+    dealer.close()
+    peer = mpcx.Peer.connect(party, args.party_sock, timeout_ms=120000)
+    m = mpcx.Model(ctx, dims, wl.W)
+    m.set_party(peer)
+    m.import_party_key(B, key)
+    sh = wl.shares
+    m.set_party_inputs(B, sh["x"][party], sh["a"][party], sh["m"][party], wl.prot if party == 1 else None)
+    for _ in range(args.warmup):
+        m.forward(B)
+    ctx.sync()
+    bar = np.zeros(1, ctx.T)
+    ctx.party_reconstruct(peer, bar)  # both parties leave this exchange together
+    ctx.reset_counters()
+    b0 = peer.bytes
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        m.forward(B)
+    ctx.sync()
+    elapsed = time.perf_counter() - t0
+    res = {"party": party, "elapsed": elapsed, "bytes": ctx.bytes_exchanged, "socket_bytes": peer.bytes - b0,
+           "out": [int(v) for v in m.output(B)], "key_bytes": len(key) if hasattr(key, "__len__") else None}
+    if prof:
+        res["prof"] = {k: prof[k] for k in ("aes_calls", "elements", "launches", "hbm_bytes")}
+    m.close()
+    peer.close()
+    ctx.close()
+    print(json.dumps(res), flush=True)
+
+
+def run_party(args):
+    """Party mode: the reference's deployment, the two parties as two processes
+    on one GPU with their own key and shares, exchanging over a Unix socket
+    (gpu_mpc/run_local_2pc.sh:196-233, README.md:99-101).  The two processes are
+    started before this process touches the GPU; samples/s = B K / the slower
+    party's time for K forwards.  Prints one JSON line."""
+    import subprocess
+    import tempfile
+
+    import numpy as np
+
+    import synth
+
+    B = args.batch
+    dims = synth.Dims(bw=args.bw, slack=args.slack)
+    wl = synth.workload(B, dims, seed=args.seed)
+    sock = os.path.join(tempfile.mkdtemp(prefix="mpcx_bench_"), "peer.sock")
+    base = [sys.executable, os.path.abspath(__file__), "--batch", str(B), "--bw", str(args.bw), "--seed",
+            str(args.seed), "--slack", str(args.slack), "--steps", str(args.steps), "--warmup", str(args.warmup),
+            "--party-sock", sock]
+    log(f"[bench] party mode: starting party 0 and party 1 (B={B}, bw={args.bw}) on {sock}")
+    procs = [subprocess.Popen(base + ["--party-child", str(p)], stdout=subprocess.PIPE, text=True) for p in (0, 1)]
+    res = []
+    try:
+        for p in procs:
+            o, _ = p.communicate(timeout=900)
+            if p.returncode != 0:
+                raise RuntimeError(f"party process exited with {p.returncode}")
+            res.append(json.loads(o.strip().splitlines()[-1]))
+    finally:
+        for p in procs:
+            if p.poll() is None:
+                p.kill()
+    elapsed = max(r["elapsed"] for r in res)
+    value = B * args.steps / elapsed
+    ms_per_step = 1e3 * elapsed / args.steps
+    out = np.array(res[0]["out"], np.int64)
+    agree = res[0]["out"] == res[1]["out"]
+    log(f"[bench] party mode: {args.steps} steps in {elapsed:.3f}s -> {ms_per_step:.2f} ms/step, {value:.1f} samples/s")
+    prof = res[0]["prof"]
+    step_s = ms_per_step / 1e3
+    aes_per_s = prof["aes_calls"] / step_s
+    valu_per_aes = (VALU_OPS_PER_AES_MIXED if args.bw == 32 else VALU_OPS_PER_AES)["perm32x2_b512"]
+    tops = aes_per_s * valu_per_aes / 1e12
+    result = {
+        "metric": f"online secure samples/s, party mode (bw={args.bw}, B={B}, 1 GPU, two processes)",
+        "value": round(value, 2),
+        "unit": "samples/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 3),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "u32" if args.bw == 32 else "u64",
+        "data": "synthetic molecules (random trees + ring closures, 10-60 atoms), Kaiming-normal weights",
+        "config": {"workload": f"two-party secure affinity forward in party mode: party 0 and party 1 as two "
+                               f"processes on one GPU, each with its own key and shares in HBM, exchanging over a "
+                               f"Unix socket; bw={args.bw} s=12, B={B} molecules x {dims.n_nodes} atoms, "
+                               f"GCN 78-78-156-312, FC 312-1024-128, fusion 256-1024-512-1"
+                               + SLACK_DESC.get(args.slack, ""),
+                   "B": B, "n_nodes": dims.n_nodes, "bw": args.bw, "scale": dims.s, "lanes": 1,
+                   "slack": args.slack, "parties": "two processes"},
+        "bytes_exchanged_per_sample": round(res[0]["bytes"] / args.steps / B, 1),
+        "socket_bytes_per_sample": round(res[0]["socket_bytes"] / args.steps / B, 1),
+        "socket_equals_counted": all(r["socket_bytes"] == r["bytes"] for r in res),
+        "parties_agree": agree,
+        "roofline": {
+            "kernel": "DCF gate kernels of both parties (k_tr_party_bits / k_tr_party_msg and the one-party "
+                      "forms): VALU work of a forward's AES calls over the timed step",
+            "bound": "valu",
+            "achieved": round(tops, 3),
+            "peak": round(VALU_PEAK_TOPS, 2),
+            "unit": "TOP/s",
+            "frac": round(tops / VALU_PEAK_TOPS, 4),
+            "traffic": None,
+            "aes_calls_per_step": prof["aes_calls"],
+            "valu_ops_per_aes": valu_per_aes,
+        },
+    }
+    try:
+        sys.path.insert(0, os.path.join(ROOT, "oracle"))
+        import orc
+        d = dims
+        od = orc.make_dims(bw=d.bw, s=d.s, n_nodes=d.n_nodes, feat=d.feat, gcn=d.gcn, dfc=d.dfc, prot=d.prot,
+                           fus=d.fus, lut_nmax=d.lut_nmax, mask_scale=d.mask_scale, slack=d.slack)
+        want, code = orc.plain_forward(od, wl.X, wl.A, wl.mask, wl.prot, wl.W)
+        result["bit_exact"] = bool(code == 0 and agree and np.array_equal(want, out))
+        if not args.no_cpu:
+            nb = min(args.cpu_samples, B)
+            sl = synth.workload(nb, dims, seed=args.seed)
+            k0, k1 = orc.model_keygen(od, nb, 99, sl.W)
+            sh = sl.shares
+            reps, ct = 0, 0.0
+            while ct < args.cpu_seconds or reps == 0:
+                t0 = time.perf_counter()
+                orc.model_eval(od, nb, sl.W, k0, k1, *sh["x"], *sh["a"], *sh["m"], sl.prot)
+                ct += time.perf_counter() - t0
+                reps += 1
+            result["cpu_baseline"] = {
+                "value": round(nb * reps / ct, 3), "unit": "samples/s", **cpu_fields(orc), "kind": "port",
+                "sample": f"{reps} x {nb} molecules of the same workload: two-party online eval (both parties in "
+                          f"one process, same gates and key format) in oracle/ C with AES-NI + OpenMP, {ct:.1f}s"}
+    except Exception as e:
+        log(f"[bench] oracle unavailable: {e}")
+        result.setdefault("bit_exact", None)
+    print(json.dumps(result), flush=True)
 
 
 def _oracle():
