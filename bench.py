@@ -140,7 +140,7 @@ def main():
                          "aggregation A.XW + bias (then a small-domain ReLU); 3 every layer truncation local "
                          "(LocalARS, the reference's default; not bit-exact, bw=64 only in practice)")
     ap.add_argument("--xw-slack", action="store_true", help="same as --slack 1")
-    ap.add_argument("--workload", choices=("affinity", "relu", "adjnorm", "copy"), default="affinity",
+    ap.add_argument("--workload", choices=("affinity", "relu", "adjnorm", "copy", "shim"), default="affinity",
                     help="affinity: the secure forward (default); relu: secure ReLU over --n elements (bw=32); "
                          "adjnorm: secure adjacency normalisation of B=1024 graphs (bw=32); copy: a 1 GiB "
                          "elementwise kernel (b = a + 1 over 2^28 int32), the HBM reference for the PMC byte "
@@ -182,6 +182,8 @@ def main():
         return run_adjnorm(args)
     if args.workload == "copy":
         return run_copy(args)
+    if args.workload == "shim":
+        return run_shim(args)
 
     import numpy as np
 
@@ -671,6 +673,137 @@ def run_party(args):
                 "value": round(nb * reps / ct, 3), "unit": "samples/s", **cpu_fields(orc), "kind": "port",
                 "sample": f"{reps} x {nb} molecules of the same workload: two-party online eval (both parties in "
                           f"one process, same gates and key format) in oracle/ C with AES-NI + OpenMP, {ct:.1f}s"}
+    except Exception as e:
+        log(f"[bench] oracle unavailable: {e}")
+        result.setdefault("bit_exact", None)
+    print(json.dumps(result), flush=True)
+
+
+def run_shim(args):
+    """The reference's whole online path through the drop-in boundary: the
+    EzPC-named shim and the sytorch Backend<T> subclasses (include/mpcx_ezpc.hpp,
+    include/mpcx_sytorch.hpp) driven by tests/cpp/ezpc_check in the call order of
+    ddgSecureAdjNormEval and DeepDTAGenAffinity::_forward (per-sample secret x
+    secret matmuls, TrFloor truncations, full-width ReLUs, the mask product, the
+    MaskedMaxPoolLayer fold, GPUConcat, FCs, output), the two parties as two
+    threads on one channel, both key sets resident in HBM (initGPUKeyArena).
+    A step is one forward of both parties (adjacency normalisation included);
+    the W + K forwards reuse one key set.  Prints one JSON line."""
+    import subprocess
+    import tempfile
+
+    import numpy as np
+
+    import synth
+
+    B, bw, S = args.batch, args.bw, 12
+    exe = os.path.join(ROOT, "tests", "cpp", "ezpc_check")
+    if not os.path.exists(exe):
+        raise SystemExit("tests/cpp/ezpc_check is not built (run __graft_entry__.build())")
+    dims = synth.Dims(bw=bw)
+    wl = synth.workload(B, dims, seed=args.seed)
+    N, C = dims.n_nodes, dims.gcn[2]
+    T = np.uint32 if bw == 32 else np.uint64
+    mod = (1 << bw) - 1
+
+    def ring(v):
+        return (np.asarray(v, np.int64).astype(np.uint64) & np.uint64(mod)).astype(T)
+
+    d = tempfile.mkdtemp(prefix="mpcx_shim_")
+    maskT = np.repeat((wl.mask << S)[:, :, None], C, axis=2)  # the reference's pre-tiled mask at scale s
+    blob, o = [], 0
+    for fin, fout in dims.layers():
+        blob += [wl.W[o:o + fin * fout], wl.W[o + fin * fout:o + fin * fout + fout] << S]  # bias at scale 2s
+        o += fin * fout + fout
+    reps = args.warmup + args.steps
+    with open(os.path.join(d, "meta.txt"), "w") as f:
+        f.write(" ".join(str(v) for v in (bw, B, N, dims.feat, *dims.gcn, *dims.dfc, dims.prot, len(dims.fus),
+                                          *dims.fus, S, dims.lut_nmax, reps)) + "\n")
+    sh = {"a": wl.shares["a"], "x": wl.shares["x"], "m": synth.share(maskT, bw, args.seed + 50)}
+    for k, (s0, s1) in sh.items():
+        ring(s0).tofile(os.path.join(d, f"{k}0.bin"))
+        ring(s1).tofile(os.path.join(d, f"{k}1.bin"))
+    ring(wl.prot).tofile(os.path.join(d, "prot.bin"))
+    ring(np.concatenate(blob)).tofile(os.path.join(d, "w.bin"))
+    log(f"[bench] shim forward: B={B} bw={bw}, {reps} forwards through ezpc_check")
+    r = subprocess.run([exe, "forward", d], capture_output=True, text=True, timeout=1500)
+    if r.returncode != 0:
+        raise SystemExit(f"ezpc_check forward failed ({r.returncode}): {r.stderr[-2000:]}")
+    ms = [float(v) for v in open(os.path.join(d, "time.txt")).read().split()]
+    timed = ms[args.warmup:]
+    ms_per_step = sum(timed) / len(timed)
+    value = B * 1e3 / ms_per_step
+    comm = [int(v) for v in open(os.path.join(d, "comm.txt")).read().split()]
+    aes = sum(int(v) for v in open(os.path.join(d, "aes.txt")).read().split())
+    kb = [int(v) for v in open(os.path.join(d, "keys.txt")).read().split()]
+    out = np.fromfile(os.path.join(d, "out.bin"), T).astype(np.int64)
+    if bw == 32:
+        out = np.where(out >= 1 << 31, out - (1 << 32), out)
+    log(f"[bench] shim forward: {ms_per_step:.2f} ms per forward (timed {len(timed)}), {value:.1f} samples/s")
+    stats = dict(ln.split() for ln in open(os.path.join(d, "stats.txt")).read().splitlines() if ln.strip())
+    log(f"[bench] shim forward, party 0: {stats['rounds']} exchange rounds; backend timers (ms): matmul "
+        f"{int(stats['matmul_us']) / 1e3:.2f}, relu {int(stats['relu_us']) / 1e3:.2f}, truncate "
+        f"{int(stats['truncate_us']) / 1e3:.2f}")
+    valu = VALU_OPS_PER_AES["perm32x2_b512"]
+    tops = aes / (ms_per_step / 1e3) * valu / 1e12
+    result = {
+        "metric": f"online secure samples/s through the EzPC/sytorch drop-in (bw={bw}, B={B}, 1 GPU)",
+        "value": round(value, 2),
+        "unit": "samples/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 3),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "u32" if bw == 32 else "u64",
+        "data": "synthetic molecules (random trees + ring closures, 10-60 atoms), Kaiming-normal weights",
+        "config": {"workload": f"the reference's online path through the drop-in headers: ddgSecureAdjNormEval and "
+                               f"DeepDTAGenAffinity::_forward's backend calls (aggregate-first GCN, TrFloor "
+                               f"truncations, full-width ReLUs, MaskedMaxPoolLayer), two parties as two threads on "
+                               f"one channel, keys resident (initGPUKeyArena); bw={bw} s=12, B={B} molecules x {N} "
+                               f"atoms, GCN 78-78-156-312, FC 312-1024-128, fusion 256-1024-512-1",
+                   "B": B, "n_nodes": N, "bw": bw, "scale": S},
+        "bytes_exchanged_per_sample": round(comm[0] / B, 1),
+        "rounds_per_step": int(stats["rounds"]),
+        "key_bytes_per_sample_per_party": round(kb[0] / B, 1),
+        "roofline": {
+            "kernel": "DCF gate evaluation of the shim's gates (both parties): VALU work of a forward's AES calls "
+                      "over the timed step",
+            "bound": "valu",
+            "achieved": round(tops, 3),
+            "peak": round(VALU_PEAK_TOPS, 2),
+            "unit": "TOP/s",
+            "frac": round(tops / VALU_PEAK_TOPS, 4),
+            "traffic": None,
+            "aes_calls_per_step": aes,
+            "valu_ops_per_aes": valu,
+        },
+    }
+    try:
+        sys.path.insert(0, os.path.join(ROOT, "oracle"))
+        import orc
+        od = orc.make_dims(bw=bw, s=S, n_nodes=N, feat=dims.feat, gcn=dims.gcn, dfc=dims.dfc, prot=dims.prot,
+                           fus=dims.fus, lut_nmax=dims.lut_nmax, gcn_order=1)
+        want, code = orc.plain_forward(od, wl.X, wl.A, wl.mask, wl.prot, wl.W)  # the C++ layers' op order
+        result["bit_exact"] = bool(code == 0 and np.array_equal(want, out))
+        if not args.no_cpu:
+            od.gcn_order = 0
+            nb = min(args.cpu_samples, B)
+            sl = synth.workload(nb, dims, seed=args.seed)
+            k0, k1 = orc.model_keygen(od, nb, 99, sl.W)
+            shs = sl.shares
+            reps_c, ct = 0, 0.0
+            while ct < args.cpu_seconds or reps_c == 0:
+                t0 = time.perf_counter()
+                orc.model_eval(od, nb, sl.W, k0, k1, *shs["x"], *shs["a"], *shs["m"], sl.prot)
+                ct += time.perf_counter() - t0
+                reps_c += 1
+            result["cpu_baseline"] = {
+                "value": round(nb * reps_c / ct, 3), "unit": "samples/s", **cpu_fields(orc), "kind": "port",
+                "sample": f"{reps_c} x {nb} molecules of the same workload: the oracle's two-party online eval (both "
+                          f"parties, the model's gates and key format) in oracle/ C with AES-NI + OpenMP, {ct:.1f}s"}
     except Exception as e:
         log(f"[bench] oracle unavailable: {e}")
         result.setdefault("bit_exact", None)

@@ -372,6 +372,20 @@ mpcx_status mpcx_dcf_eval(mpcx_ctx *c, int party, int bin, size_t n, const void 
   return MPCX_OK;
 }
 
+mpcx_status mpcx_dcf_eval_ring(mpcx_ctx *c, int party, int bin, size_t n, const void *key, const void *x,
+                               const uint32_t *mask, uint64_t *out) {
+  CHECK_CTX(c);
+  if (bin < 1 || bin > c->bw || (party != 0 && party != 1)) return fail(c, MPCX_EINVAL, "dcf_eval_ring: bad argument");
+  if (n == 0) return MPCX_OK;
+  if (!key || !x || !out) return fail(c, MPCX_EINVAL, "dcf_eval_ring: null pointer");
+  const uint8_t *k = static_cast<const uint8_t *>(key);
+  HIPC(c,
+       c->bw == 32 ? launch_dcf_eval_ring<uint32_t>(c->L, bin, n, k, static_cast<const uint32_t *>(x), mask, out)
+                   : launch_dcf_eval_ring<uint64_t>(c->L, bin, n, k, static_cast<const uint64_t *>(x), mask, out),
+       "dcf_eval_ring");
+  return MPCX_OK;
+}
+
 // ---------------- workspace for standalone gate evaluation ----------------
 namespace {
 hipError_t ctx_work(mpcx_ctx *c, size_t bytes, void **p) {
@@ -405,6 +419,12 @@ bool valid_kind(int k) {
 size_t mpcx_tr_key_bytes(mpcx_ctx *c, int kind, size_t n) {
   if (!c || !valid_kind(kind)) return 0;
   return tr_layout(kind, c->bw, c->s, n, 0).end;
+}
+
+int mpcx_tr_aes_calls(const mpcx_ctx *c, int kind) {
+  if (!c || !valid_kind(kind)) return -1;
+  const TrLayout lay = tr_layout(kind, c->bw, c->s, 1, 0);
+  return (lay.use_a ? lay.a.L + 1 : 0) + (lay.use_b ? lay.b.L + 1 : 0);
 }
 
 template <typename T>

@@ -72,6 +72,12 @@ hipError_t launch_dcf_keygen(const Launch &L, uint64_t seed, uint32_t gate, uint
                              const uint64_t *alpha, const uint8_t *rbit, uint8_t *k0, uint8_t *k1, size_t base);
 hipError_t launch_dcf_eval(const Launch &L, int party, int m, size_t n, const uint8_t *key, size_t base,
                            const uint64_t *x, uint64_t *out_bits);
+// The same on ring elements x (reduced to the m-bit domain in the kernel), the
+// output bits XORed with mask (32-bit words, bit i of word i/32) when mask is
+// not null: the reference's gpuDcf<T, 1, idPrologue, maskEpilogue>.
+template <typename T>
+hipError_t launch_dcf_eval_ring(const Launch &L, int m, size_t n, const uint8_t *key, const T *x,
+                                const uint32_t *mask, uint64_t *out_bits);
 
 // ---------------- truncation / ReLU family ----------------
 template <typename T>

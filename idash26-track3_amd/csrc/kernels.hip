@@ -140,17 +140,23 @@ hipError_t launch_dcf_keygen(const Launch &L, uint64_t seed, uint32_t gate, uint
   });
 }
 
+// Inputs of type X (uint64_t, or the ring's element type) reduced to the m-bit
+// domain; mask: optional 32-bit words of bits XORed into the output (the
+// reference's maskEpilogue, bit i of word i/32), or null.
+template <typename X>
 struct DcfEvalArgs {
   int m, L;
   size_t n;
   const uint8_t *key;
   size_t off_root, off_cw, off_leaf, off_z;
-  const uint64_t *x;
+  const X *x;
+  uint64_t xmask;
+  const uint32_t *mask;
   uint64_t *out;
 };
 
-template <int NT, int REP>
-__global__ void k_dcf_eval(DcfEvalArgs a) {
+template <int NT, int REP, typename X>
+__global__ void k_dcf_eval(DcfEvalArgs<X> a) {
   __shared__ __align__(16) uint32_t lds[AesLds<NT, REP>::kWords];
   AesLds<NT, REP>::fill(lds);
   AesLds<NT, REP> aes(lds);
@@ -163,19 +169,20 @@ __global__ void k_dcf_eval(DcfEvalArgs a) {
     const size_t i = base + lane_id();
     uint32_t b = 0;
     if (i < a.n) {
-      b = dcf_eval_walk(aes, root[i], a.m, a.L, cw + i, a.n, leaf[i], a.x[i]);
+      b = dcf_eval_walk(aes, root[i], a.m, a.L, cw + i, a.n, leaf[i], uint64_t(a.x[i]) & a.xmask);
       b ^= get_bit(zp, i);
+      if (a.mask) b ^= (a.mask[i >> 5] >> (i & 31)) & 1u;
     }
     const uint64_t w = __ballot(b);
     if (lane_id() == 0) a.out[base >> 6] = w;
   }
 }
 
-hipError_t launch_dcf_eval(const Launch &L, int party, int m, size_t n, const uint8_t *key, size_t base,
-                           const uint64_t *x, uint64_t *out_bits) {
-  (void)party;
+template <typename X>
+hipError_t launch_dcf_eval_x(const Launch &L, int m, size_t n, const uint8_t *key, size_t base, const X *x,
+                             const uint32_t *mask, uint64_t *out_bits) {
   DcfLayout lay = dcf_layout(m, n, base, true);
-  DcfEvalArgs a;
+  DcfEvalArgs<X> a;
   a.m = m;
   a.L = lay.L;
   a.n = n;
@@ -185,14 +192,27 @@ hipError_t launch_dcf_eval(const Launch &L, int party, int m, size_t n, const ui
   a.off_leaf = lay.off_leaf;
   a.off_z = lay.off_z;
   a.x = x;
+  a.xmask = m >= 64 ? ~0ull : ((1ull << m) - 1ull);
+  a.mask = mask;
   a.out = out_bits;
   return with_variant(L, [&](auto v) {
     constexpr int NT = decltype(v)::nt, REP = decltype(v)::rep;
     int block = variant_block(L);
-    int grid = grid_for(k_dcf_eval<NT, REP>, block, n, L.num_cu);
-    hipLaunchKernelGGL((k_dcf_eval<NT, REP>), dim3(grid), dim3(block), 0, L.stream, a);
+    int grid = grid_for(k_dcf_eval<NT, REP, X>, block, n, L.num_cu);
+    hipLaunchKernelGGL((k_dcf_eval<NT, REP, X>), dim3(grid), dim3(block), 0, L.stream, a);
     return hipGetLastError();
   });
+}
+
+hipError_t launch_dcf_eval(const Launch &L, int party, int m, size_t n, const uint8_t *key, size_t base,
+                           const uint64_t *x, uint64_t *out_bits) {
+  (void)party;
+  return launch_dcf_eval_x<uint64_t>(L, m, n, key, base, x, nullptr, out_bits);
+}
+template <typename T>
+hipError_t launch_dcf_eval_ring(const Launch &L, int m, size_t n, const uint8_t *key, const T *x,
+                                const uint32_t *mask, uint64_t *out_bits) {
+  return launch_dcf_eval_x<T>(L, m, n, key, 0, x, mask, out_bits);
 }
 
 // ---------------------------------------------------------------------------
@@ -1050,6 +1070,8 @@ hipError_t launch_rowsum(const Launch &L, size_t rows, int len, const T *a, T *o
 // ---------------------------------------------------------------------------
 #define INST(T)                                                                                                       \
   template hipError_t launch_reconstruct<T>(const Launch &, size_t, const T *, const T *, T *);                       \
+  template hipError_t launch_dcf_eval_ring<T>(const Launch &, int, size_t, const uint8_t *, const T *,              \
+                                              const uint32_t *, uint64_t *);                                          \
   template hipError_t launch_pack_bits<T>(const Launch &, size_t, int, const T *, uint64_t *);                        \
   template hipError_t launch_unpack_reconstruct<T>(const Launch &, size_t, int, const T *, const uint64_t *, T *);    \
   template hipError_t launch_local_ars<T>(const Launch &, size_t, int, const T *, const T *, int, T *);               \

@@ -17,6 +17,7 @@
 #include <mutex>
 #include <string>
 #include <thread>
+#include <vector>
 
 namespace mpcx {
 
@@ -36,11 +37,14 @@ class Peer {
   Peer &operator=(const Peer &) = delete;
 
   int party() const { return party_; }
-  // Synchronises `stream` (the messages were produced on it), sends the
-  // segments back to back, receives the peer's, and enqueues their copies into
+  // Stages the segments (produced on `stream`) back to back, sends them while
+  // receiving the peer's, and enqueues the copies of the peer's segments into
   // the recv regions on `stream`.  hipErrorNotReady: the channel failed (peer
   // gone, timeout); the peer is unusable afterwards.
   hipError_t exchange(hipStream_t stream, const Seg *segs, int nseg);
+  // chunk of the pipelined staging, and the largest message sent inline (the
+  // per-sample products of a GCN layer are 44-88 KB)
+  static constexpr size_t kChunk = size_t(4) << 20, kInline = size_t(128) << 10;
   uint64_t bytes_sent() const { return sent_; }
   uint64_t bytes_received() const { return recv_; }
   uint64_t rounds() const { return rounds_; }
@@ -48,12 +52,15 @@ class Peer {
 
  private:
   hipError_t ensure(size_t bytes);
+  hipError_t ensure_events(size_t n);
   void sender_loop();
   bool send_all(const uint8_t *p, size_t n);
   bool recv_all(uint8_t *p, size_t n);
 
   int fd_ = -1, party_ = 0;
   uint8_t *hs_ = nullptr, *hr_ = nullptr;  // pinned staging (send, receive)
+  std::vector<hipEvent_t> ev_;              // one per staged chunk of the current message
+  size_t inline_max_ = size_t(16) << 10;    // set from the socket's send buffer
   size_t cap_ = 0;
   uint64_t sent_ = 0, recv_ = 0, rounds_ = 0;
   bool broken_ = false;

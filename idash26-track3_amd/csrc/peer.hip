@@ -7,13 +7,23 @@
 #include <sys/un.h>
 #include <unistd.h>
 
+#include <algorithm>
 #include <cerrno>
 #include <chrono>
 #include <cstring>
 
 namespace mpcx {
 
-Peer::Peer(int fd, int party) : fd_(fd), party_(party) { th_ = std::thread([this] { sender_loop(); }); }
+Peer::Peer(int fd, int party) : fd_(fd), party_(party) {
+  // Messages sent inline must fit the socket's send buffer in both directions
+  // at once: take a quarter of what the kernel grants (at most kInline).
+  int want = int(4 * kInline), got = 0;
+  socklen_t len = sizeof got;
+  (void)setsockopt(fd_, SOL_SOCKET, SO_SNDBUF, &want, sizeof want);
+  if (getsockopt(fd_, SOL_SOCKET, SO_SNDBUF, &got, &len) == 0 && got > 0)
+    inline_max_ = std::min(kInline, size_t(got) / 4);
+  th_ = std::thread([this] { sender_loop(); });
+}
 
 Peer::~Peer() {
   {
@@ -22,6 +32,7 @@ Peer::~Peer() {
   }
   cv_.notify_all();
   if (th_.joinable()) th_.join();
+  for (hipEvent_t e : ev_) (void)hipEventDestroy(e);
   if (fd_ >= 0) ::close(fd_);
   if (hs_) (void)hipHostFree(hs_);
   if (hr_) (void)hipHostFree(hr_);
@@ -68,6 +79,8 @@ bool Peer::recv_all(uint8_t *p, size_t n) {
   return true;
 }
 
+// The sender thread: the chunks of the current message, each once its staging
+// copy (the event recorded after it) is done.
 void Peer::sender_loop() {
   std::unique_lock<std::mutex> lk(mu_);
   for (;;) {
@@ -77,7 +90,9 @@ void Peer::sender_loop() {
     const size_t n = job_n_;
     job_ready_ = false;
     lk.unlock();
-    const bool ok = send_all(p, n);
+    bool ok = true;
+    for (size_t c = 0, lo = 0; ok && lo < n; c++, lo += kChunk)
+      ok = hipEventSynchronize(ev_[c]) == hipSuccess && send_all(p + lo, std::min(kChunk, n - lo));
     lk.lock();
     job_ok_ = ok;
     job_done_ = true;
@@ -85,6 +100,43 @@ void Peer::sender_loop() {
   }
 }
 
+hipError_t Peer::ensure_events(size_t n) {
+  while (ev_.size() < n) {
+    hipEvent_t e = nullptr;
+    const hipError_t r = hipEventCreateWithFlags(&e, hipEventDisableTiming);
+    if (r != hipSuccess) return r;
+    ev_.push_back(e);
+  }
+  return hipSuccess;
+}
+
+// The parts of the segments that fall in [lo, hi) of the message (the
+// segments back to back), copied device -> staging (to_host) or staging ->
+// device on `stream`.
+static hipError_t copy_part(hipStream_t stream, const Peer::Seg *segs, int nseg, size_t lo, size_t hi,
+                            uint8_t *stage, bool to_host) {
+  size_t o = 0;
+  for (int k = 0; k < nseg; k++) {
+    const size_t b = o, e = o + segs[k].bytes;
+    o = e;
+    const size_t a0 = std::max(b, lo), a1 = std::min(e, hi);
+    if (a0 >= a1) continue;
+    const hipError_t r =
+        to_host ? hipMemcpyAsync(stage + a0, static_cast<const uint8_t *>(segs[k].send) + (a0 - b), a1 - a0,
+                                 hipMemcpyDeviceToHost, stream)
+                : hipMemcpyAsync(static_cast<uint8_t *>(segs[k].recv) + (a0 - b), stage + a0, a1 - a0,
+                                 hipMemcpyHostToDevice, stream);
+    if (r != hipSuccess) return r;
+  }
+  return hipSuccess;
+}
+
+// One exchange.  The message is staged to pinned memory in chunks of kChunk
+// bytes, an event after each: the sender thread sends a chunk once it is
+// staged, while the next ones are still being copied, and each received chunk
+// goes back to the device at once, so the copies overlap the socket.  A
+// message of at most inline_max_ bytes is sent from this thread (both
+// directions fit the socket buffers, so neither send can block on the other).
 hipError_t Peer::exchange(hipStream_t stream, const Seg *segs, int nseg) {
   if (broken_) return hipErrorNotReady;
   size_t total = 0;
@@ -93,28 +145,39 @@ hipError_t Peer::exchange(hipStream_t stream, const Seg *segs, int nseg) {
   if (total == 0) return hipSuccess;
   hipError_t e = ensure(total);
   if (e != hipSuccess) return e;
-  size_t o = 0;
-  for (int k = 0; k < nseg; k++) {
-    if (segs[k].bytes) {
-      e = hipMemcpyAsync(hs_ + o, segs[k].send, segs[k].bytes, hipMemcpyDeviceToHost, stream);
-      if (e != hipSuccess) return e;
-    }
-    o += segs[k].bytes;
-  }
-  // the messages are complete, and the previous exchange's copies out of hr_ done
-  e = hipStreamSynchronize(stream);
+  const size_t nch = (total + kChunk - 1) / kChunk;
+  e = ensure_events(nch);
   if (e != hipSuccess) return e;
-  {
-    std::lock_guard<std::mutex> lk(mu_);
-    job_ = hs_;
-    job_n_ = total;
-    job_ready_ = true;
-    job_done_ = false;
+  for (size_t c = 0; c < nch; c++) {
+    e = copy_part(stream, segs, nseg, c * kChunk, std::min(total, (c + 1) * kChunk), hs_, true);
+    if (e == hipSuccess) e = hipEventRecord(ev_[c], stream);
+    if (e != hipSuccess) return e;
   }
-  cv_.notify_all();
-  const bool rok = recv_all(hr_, total);
-  bool sok;
-  {
+  bool rok = true, sok = true;
+  if (total <= inline_max_) {
+    // staged, and (stream order) the previous exchange's copies out of hr_ done
+    e = hipEventSynchronize(ev_[nch - 1]);
+    if (e != hipSuccess) return e;
+    sok = send_all(hs_, total);
+    rok = sok && recv_all(hr_, total);
+    if (rok) e = copy_part(stream, segs, nseg, 0, total, hr_, false);
+  } else {
+    // the previous exchange's copies out of hr_ are done once chunk 0 is staged
+    e = hipEventSynchronize(ev_[0]);
+    if (e != hipSuccess) return e;
+    {
+      std::lock_guard<std::mutex> lk(mu_);
+      job_ = hs_;
+      job_n_ = total;
+      job_ready_ = true;
+      job_done_ = false;
+    }
+    cv_.notify_all();
+    for (size_t lo = 0; rok && lo < total; lo += kChunk) {
+      const size_t hi = std::min(total, lo + kChunk);
+      rok = recv_all(hr_ + lo, hi - lo);
+      if (rok && e == hipSuccess) e = copy_part(stream, segs, nseg, lo, hi, hr_, false);
+    }
     std::unique_lock<std::mutex> lk(mu_);
     if (!rok) ::shutdown(fd_, SHUT_RDWR);  // unblock a sender stuck on a full socket
     cv_.wait(lk, [this] { return job_done_; });
@@ -125,16 +188,9 @@ hipError_t Peer::exchange(hipStream_t stream, const Seg *segs, int nseg) {
     err_ = !rok ? "receive from the peer failed (closed or timed out)" : "send to the peer failed";
     return hipErrorNotReady;
   }
+  if (e != hipSuccess) return e;
   sent_ += total;
   recv_ += total;
-  o = 0;
-  for (int k = 0; k < nseg; k++) {
-    if (segs[k].bytes) {
-      e = hipMemcpyAsync(segs[k].recv, hr_ + o, segs[k].bytes, hipMemcpyHostToDevice, stream);
-      if (e != hipSuccess) return e;
-    }
-    o += segs[k].bytes;
-  }
   return hipSuccess;
 }
 

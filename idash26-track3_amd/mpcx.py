@@ -45,6 +45,7 @@ _SIGS = {
                                   C.c_uint32, C.c_void_p, C.c_void_p]),
     "mpcx_dcf_eval": (C.c_int, [C.c_void_p, C.c_int, C.c_int, C.c_size_t, C.c_void_p, C.c_void_p,
                                 C.c_void_p]),
+    "mpcx_dcf_eval_ring": (C.c_int, [C.c_void_p, C.c_int, C.c_int, C.c_size_t] + [C.c_void_p] * 4),
     "mpcx_maxpool_levels": (C.c_int, [C.c_int]),
     "mpcx_maxpool_key_bytes": (C.c_size_t, [C.c_void_p, C.c_int, C.c_int, C.c_int]),
     "mpcx_maxpool_keygen": (C.c_int, [C.c_void_p, C.c_int, C.c_int, C.c_int, C.c_void_p, C.c_void_p, C.c_uint64,
@@ -54,6 +55,7 @@ _SIGS = {
     "mpcx_maxpool_eval_noalloc": (C.c_int, [C.c_void_p, C.c_int, C.c_int, C.c_int, C.c_void_p, C.c_void_p,
                                             C.c_void_p, C.c_void_p]),
     "mpcx_tr_key_bytes": (C.c_size_t, [C.c_void_p, C.c_int, C.c_size_t]),
+    "mpcx_tr_aes_calls": (C.c_int, [C.c_void_p, C.c_int]),
     "mpcx_tr_keygen": (C.c_int, [C.c_void_p, C.c_int, C.c_size_t, C.c_void_p, C.c_void_p, C.c_uint64,
                                  C.c_uint32, C.c_void_p, C.c_void_p]),
     "mpcx_tr_eval": (C.c_int, [C.c_void_p, C.c_int, C.c_size_t, C.c_void_p, C.c_void_p, C.c_void_p,
@@ -290,6 +292,20 @@ class Ctx:
         words = from_dev(out, np.uint64)
         bits = np.unpackbits(words.view(np.uint8), bitorder="little")[:n]
         return bits
+
+    def dcf_eval_ring(self, party, m, key, x, mask_words=None):
+        """mpcx_dcf_eval_ring: x as ring elements of the context's width (read
+        modulo 2^m), the output bits XORed with mask_words (uint32, bit i of
+        word i/32) if given; returns the n output bits."""
+        x = self.ring(x)
+        n = x.size
+        dx = to_dev(x)
+        dm = to_dev(np.ascontiguousarray(mask_words, np.uint32)) if mask_words is not None else None
+        out = empty_dev(((n + 63) // 64) * 8)
+        self.check(self.lib.mpcx_dcf_eval_ring(self.h, party, m, n, dptr(key), dptr(dx), dptr(dm), dptr(out)),
+                   "dcf_eval_ring")
+        words = from_dev(out, np.uint64)
+        return np.unpackbits(words.view(np.uint8), bitorder="little")[:n]
 
     # ---------------- gates ----------------
     def tr_keygen(self, kind, in_mask, seed=1, gate=1):

@@ -153,6 +153,13 @@ mpcx_status mpcx_dcf_keygen(mpcx_ctx *ctx, int bin, size_t n, const uint64_t *d_
                             void *d_key1);
 mpcx_status mpcx_dcf_eval(mpcx_ctx *ctx, int party, int bin, size_t n, const void *d_key,
                           const uint64_t *d_x, uint64_t *d_out_bits);
+/* The same on ring elements of the context's width (d_x: n uint32_t at bw=32,
+ * uint64_t at bw=64; each read modulo 2^bin), with the output bits XORed with
+ * d_mask (device, (n+31)/32 words, bit i of word i/32) when it is not NULL: the
+ * reference's gpuDcf<T, 1, idPrologue, maskEpilogue>(key, party, d_in, g, s,
+ * &h_mask) (gpu_mpc/dpf_dcf_adapter.h:266, 293) with no host round trip. */
+mpcx_status mpcx_dcf_eval_ring(mpcx_ctx *ctx, int party, int bin, size_t n, const void *d_key,
+                               const void *d_x, const uint32_t *d_mask, uint64_t *d_out_bits);
 
 /* ---------------- truncation / ReLU ----------------
  * Keygen replaces gpuGenReluKey<T,T,0,0,false>(kb, party, bin, bout, N,
@@ -168,6 +175,11 @@ mpcx_status mpcx_dcf_eval(mpcx_ctx *ctx, int party, int bin, size_t n, const voi
  * (the kinds that shift).  MPCX_LOCALARS has no key (key bytes 0, key pointers
  * may be NULL, the gate id is unused). */
 size_t mpcx_tr_key_bytes(mpcx_ctx *ctx, int kind, size_t n);
+/* AES calls per element and party of a gate kind's evaluation (its DCF walks:
+ * tree levels plus the leaf), for the caller's own accounting of the DCF work
+ * (the reference's Stats counts time only); 0 for MPCX_LOCALARS, -1 for a bad
+ * kind. */
+int mpcx_tr_aes_calls(const mpcx_ctx *ctx, int kind);
 mpcx_status mpcx_tr_keygen(mpcx_ctx *ctx, int kind, size_t n, const void *d_in_mask,
                            void *d_out_mask, uint64_t seed, uint32_t gate, void *d_key0,
                            void *d_key1);

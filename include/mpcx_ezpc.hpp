@@ -34,12 +34,14 @@
 #pragma once
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <cstdint>
 #include <cstdio>
 #include <cstdlib>
 #include <cstring>
 #include <map>
 #include <mutex>
+#include <set>
 #include <string>
 #include <utility>
 #include <vector>
@@ -118,14 +120,27 @@ struct Runtime {
 // Contexts by (bw, scale), one set per thread (a context's stream and
 // workspaces serve one caller at a time; two parties may run as two threads),
 // destroyed when the thread ends.
+// Each context runs on a stream of its own, a blocking one (default flags and
+// priority): the legacy null stream, on which the callers' copies run
+// (hipMemcpy, hipMemcpy2D, whose device-to-device and pageable forms may return
+// before the copy is done) and the shim's own key and weight copies, orders
+// with it both ways, as the reference's code, all on the default stream,
+// expects.  So no shim call has to wait for its kernels: a later copy or
+// gpuFree of the caller waits for them, and the party-mode exchanges wait for
+// what they send.
 struct ThreadContexts {
   struct Entry {
     mpcx_ctx *c = nullptr;
     uint32_t key_epoch = 0;  // the dealer key this context holds (Runtime::key_epoch)
+    hipStream_t stream = nullptr;
   };
   std::map<std::pair<int, int>, Entry> ctx;
   ~ThreadContexts() {
-    for (auto &kv : ctx) mpcx_destroy(kv.second.c);
+    for (auto &kv : ctx) {
+      (void)hipStreamSynchronize(kv.second.stream);
+      mpcx_destroy(kv.second.c);
+      (void)hipStreamDestroy(kv.second.stream);
+    }
   }
 };
 inline mpcx_ctx *ctx(int bw, int scale = 12) {
@@ -133,10 +148,12 @@ inline mpcx_ctx *ctx(int bw, int scale = 12) {
   Runtime &R = Runtime::get();
   auto it = tc.ctx.find({bw, scale});
   if (it == tc.ctx.end()) {
-    mpcx_ctx *c = nullptr;
-    if (mpcx_create(bw, scale, R.device, &c) != MPCX_OK)
+    ThreadContexts::Entry e;
+    if (mpcx_create(bw, scale, R.device, &e.c) != MPCX_OK)
       die("mpcx_create(bw " + std::to_string(bw) + ", scale " + std::to_string(scale) + ") failed");
-    it = tc.ctx.emplace(std::make_pair(bw, scale), ThreadContexts::Entry{c, 0}).first;
+    hip_check(hipStreamCreateWithFlags(&e.stream, hipStreamDefault), "context stream");
+    if (mpcx_set_stream(e.c, e.stream) != MPCX_OK) die("mpcx_set_stream failed");
+    it = tc.ctx.emplace(std::make_pair(bw, scale), e).first;
   }
   std::lock_guard<std::mutex> lk(R.mu);
   if (it->second.key_epoch != R.key_epoch) {  // a new dealer key (or none) since this context last dealt
@@ -146,12 +163,8 @@ inline mpcx_ctx *ctx(int bw, int scale = 12) {
   }
   return it->second.c;
 }
-// Every library call is followed by a synchronisation of the context's stream:
-// the contexts' streams do not order with the null stream that the callers'
-// copies (key bytes to the cursor, shares, gpuMalloc'd outputs) run on, and the
-// reference's functions return with their results complete.
+// A library call's status (its kernels run on; see ctx()).
 inline void check(mpcx_ctx *c, mpcx_status st, const char *what) {
-  if (st == MPCX_OK && c) st = mpcx_synchronize(c);
   if (st != MPCX_OK) die(std::string(what) + ": " + (c ? mpcx_last_error(c) : "status " + std::to_string(st)));
 }
 template <typename T>
@@ -166,10 +179,53 @@ inline uint32_t next_gate() {
 }
 inline uint64_t seed() { return Runtime::get().seed; }
 
+// Device memory of the shim: the device's stream-ordered pool on the null
+// stream, its release threshold at the maximum so that freed blocks stay
+// cached (the reference's initGPUMemPool with cudaMallocAsync / cudaFreeAsync):
+// no allocation or free waits for the device, as a hipFree would.  A free is
+// ordered after the kernels that use the block because the contexts' streams
+// are blocking streams (ctx()); pointers from elsewhere go to hipFree.
+struct Pool {
+  std::mutex mu;
+  std::set<void *> live;
+  bool ready = false;
+  static Pool &get() {
+    static Pool p;
+    return p;
+  }
+};
 inline void *dmalloc(size_t bytes) {
+  Pool &P = Pool::get();
+  {
+    std::lock_guard<std::mutex> lk(P.mu);
+    if (!P.ready) {
+      int dev = 0;
+      hipMemPool_t pool;
+      hip_check(hipGetDevice(&dev), "memory pool");
+      hip_check(hipDeviceGetDefaultMemPool(&pool, dev), "memory pool");
+      uint64_t keep = ~uint64_t(0);
+      hip_check(hipMemPoolSetAttribute(pool, hipMemPoolAttrReleaseThreshold, &keep), "memory pool");
+      P.ready = true;
+    }
+  }
   void *p = nullptr;
-  hip_check(hipMalloc(&p, bytes ? bytes : 1), "gpuMalloc");
+  hip_check(hipMallocAsync(&p, bytes ? bytes : 1, nullptr), "gpuMalloc");
+  std::lock_guard<std::mutex> lk(P.mu);
+  P.live.insert(p);
   return p;
+}
+inline void dfree(void *p) {
+  if (!p) return;
+  Pool &P = Pool::get();
+  bool pooled;
+  {
+    std::lock_guard<std::mutex> lk(P.mu);
+    pooled = P.live.erase(p) > 0;
+  }
+  if (pooled)
+    hip_check(hipFreeAsync(p, nullptr), "gpuFree");
+  else
+    (void)hipFree(p);
 }
 // Identity index map 0..n-1 (element-wise Beaver products).
 inline const uint32_t *iota(size_t n) {
@@ -246,6 +302,7 @@ struct DevKey {
 inline DevKey key_on_device(const u8 *h, size_t bytes) {
   Runtime &R = Runtime::get();
   DevKey k;
+  if (!h || bytes == 0) return k;  // nothing to stage: a null device pointer
   if (R.arena && h >= R.host_base && h + bytes <= R.host_base + R.arena_bytes) {
     u8 *d = R.arena + (h - R.host_base);
     if ((reinterpret_cast<uintptr_t>(d) & 255u) == 0) {
@@ -270,7 +327,7 @@ inline DevKey on_device(const void *p, size_t bytes) {
   return key_on_device(static_cast<const u8 *>(p), bytes);
 }
 inline void key_release(DevKey &k) {
-  if (k.owned && k.d) (void)hipFree(k.d);
+  if (k.owned && k.d) dfree(k.d);
   k.d = nullptr;
 }
 
@@ -281,7 +338,7 @@ inline void split(mpcx_ctx *c, size_t n, const T *d_v, T *d_s0, T *d_s1) {
   void *tmp = dmalloc(blocks * 16);
   check(c, mpcx_prf(c, seed(), next_gate(), 0x51u, blocks, tmp), "share PRF");
   hip_check(hipMemcpy(d_s0, tmp, n * sizeof(T), hipMemcpyDeviceToDevice), "share");
-  (void)hipFree(tmp);
+  dfree(tmp);
   check(c, mpcx_ring_lincomb(c, n, 1, 1, d_v, uint64_t(0) - 1, d_s0, nullptr, 0, d_s1), "share");
 }
 
@@ -291,11 +348,11 @@ inline void split(mpcx_ctx *c, size_t n, const T *d_v, T *d_s0, T *d_s1) {
 // memory (extern "C" in the reference: gpuMalloc, gpuFree, moveToGPU,
 // moveIntoCPUMem, initGPUKeyArena, freeGPUKeyArena; patch:632-768)
 // ===========================================================================
-inline void initGPUMemPool() {}
+inline void initGPUMemPool() { mpcx_ezpc::dfree(mpcx_ezpc::dmalloc(1)); }
 inline u8 *gpuMalloc(size_t bytes) { return static_cast<u8 *>(mpcx_ezpc::dmalloc(bytes)); }
 // No-op for addresses inside the key arena (patch:692-697).
 inline void gpuFree(void *d) {
-  if (d && !mpcx_ezpc::in_arena(d)) (void)hipFree(d);
+  if (d && !mpcx_ezpc::in_arena(d)) mpcx_ezpc::dfree(d);
 }
 inline u8 *cpuMalloc(size_t bytes, bool pin = true) {
   void *p = nullptr;
@@ -331,7 +388,7 @@ inline void moveIntoCPUMem(u8 *h, u8 *d, size_t bytes, Stats *) {
 // reads in that range use the device copy (initGPUKeyArena, patch:632-661).
 inline void initGPUKeyArena(u8 *h, size_t bytes) {
   mpcx_ezpc::Runtime &R = mpcx_ezpc::Runtime::get();
-  if (R.arena) (void)hipFree(R.arena);
+  if (R.arena) mpcx_ezpc::dfree(R.arena);
   R.arena = static_cast<u8 *>(mpcx_ezpc::dmalloc(bytes));
   mpcx_ezpc::hip_check(hipMemcpy(R.arena, h, bytes, hipMemcpyHostToDevice), "initGPUKeyArena");
   R.host_base = h;
@@ -339,7 +396,7 @@ inline void initGPUKeyArena(u8 *h, size_t bytes) {
 }
 inline void freeGPUKeyArena() {
   mpcx_ezpc::Runtime &R = mpcx_ezpc::Runtime::get();
-  if (R.arena) (void)hipFree(R.arena);
+  if (R.arena) mpcx_ezpc::dfree(R.arena);
   R.arena = nullptr;
   R.host_base = nullptr;
   R.arena_bytes = 0;
@@ -525,8 +582,8 @@ struct KeyPair {
     k[1] = dmalloc(n);
   }
   ~KeyPair() {
-    (void)hipFree(k[0]);
-    (void)hipFree(k[1]);
+    dfree(k[0]);
+    dfree(k[1]);
   }
 };
 // The ReLU gate for inputs of bin significant bits: the full-width RELU at
@@ -581,28 +638,23 @@ inline GPUDPFKey readGPUDcfKey(u8 **kb) {
 }
 // Party p's share of the packed output bits (32 per u32 word), XORed with
 // (*h_mask)[0] when given (maskEpilogue: the masked DCF of DReLU / truncation).
+// The inputs stay on the device (read modulo 2^bin by the kernel) and the mask
+// words go to the device with the key (the arena's copy when the key buffer is
+// resident), so nothing returns to the host.
 template <typename T, int E, typename Pro, typename Epi>
 inline u32 *gpuDcf(GPUDPFKey k, int party, T *d_in, AESGlobalContext *, Stats *, std::vector<u32 *> *h_mask = nullptr) {
   static_assert(E == 1, "one output bit per element");
   mpcx_ctx *c = mpcx_ezpc::ctx(8 * int(sizeof(T)));
   const size_t N = size_t(k.M), words = (N + 63) / 64;
-  std::vector<T> h(N);
-  std::vector<uint64_t> x(N);
-  mpcx_ezpc::hip_check(hipMemcpy(h.data(), d_in, N * sizeof(T), hipMemcpyDeviceToHost), "gpuDcf");
-  for (size_t i = 0; i < N; i++) x[i] = uint64_t(h[i]);
-  auto *d_x = reinterpret_cast<uint64_t *>(gpuMalloc(N * 8));
-  mpcx_ezpc::hip_check(hipMemcpy(d_x, x.data(), N * 8, hipMemcpyHostToDevice), "gpuDcf");
   auto *d_out = reinterpret_cast<uint64_t *>(gpuMalloc(words * 8));
   mpcx_ezpc::ScopedKey key(k.key, k.bytes);
-  mpcx_ezpc::check(c, mpcx_dcf_eval(c, party, k.bin, N, key.get(), d_x, d_out), "gpuDcf");
-  gpuFree(d_x);
-  if (h_mask && !h_mask->empty() && (*h_mask)[0]) {
-    std::vector<u32> bits(2 * words), m((N + 31) / 32);
-    mpcx_ezpc::hip_check(hipMemcpy(bits.data(), d_out, words * 8, hipMemcpyDeviceToHost), "gpuDcf");
-    std::memcpy(m.data(), (*h_mask)[0], m.size() * 4);
-    for (size_t w = 0; w < m.size(); w++) bits[w] ^= m[w];
-    mpcx_ezpc::hip_check(hipMemcpy(d_out, bits.data(), words * 8, hipMemcpyHostToDevice), "gpuDcf");
-  }
+  const bool masked = h_mask && !h_mask->empty() && (*h_mask)[0];
+  mpcx_ezpc::ScopedKey mask(masked ? reinterpret_cast<const u8 *>((*h_mask)[0]) : nullptr,
+                            masked ? ((N + 31) / 32) * 4 : 0);
+  mpcx_ezpc::check(c,
+                   mpcx_dcf_eval_ring(c, party, k.bin, N, key.get(), d_in,
+                                      reinterpret_cast<const uint32_t *>(mask.get()), d_out),
+                   "gpuDcf");
   return reinterpret_cast<u32 *>(d_out);
 }
 
@@ -650,10 +702,17 @@ inline GPUReluKey<T> tr_read(u8 **kb, uint32_t type, const char *what) {
   k.bytes = k.kind == MPCX_LOCALARS ? 0 : mpcx_tr_key_bytes(ctx(8 * int(sizeof(T)), k.scale), k.kind, size_t(k.N));
   return k;
 }
+// AES calls of this thread's gate evaluations (one thread per party), for the
+// caller's accounting of the DCF work.
+inline uint64_t &aes_calls() {
+  thread_local uint64_t n = 0;
+  return n;
+}
 template <typename T>
 inline T *tr_eval(SigmaPeer *peer, int party, const GPUReluKey<T> &k, const T *d_in, const T *d_bias = nullptr,
                   int ncol = 0) {
   mpcx_ctx *c = ctx(8 * int(sizeof(T)), k.scale);
+  aes_calls() += uint64_t(k.N) * uint64_t(std::max(0, mpcx_tr_aes_calls(c, k.kind)));
   T *out = reinterpret_cast<T *>(gpuMalloc(size_t(k.N) * sizeof(T)));
   if (k.kind == MPCX_LOCALARS) {
     check(c, mpcx_tr_eval(c, k.kind, size_t(k.N), nullptr, nullptr, d_in, d_bias, ncol, out), "eval");

@@ -22,8 +22,10 @@
 //   - errors abort with a message (the reference's checkCudaErrors / assert).
 #pragma once
 #include <chrono>
+#include <cstring>
 #include <filesystem>
 #include <fstream>
+#include <map>
 #include <set>
 #include <string>
 #include <vector>
@@ -37,14 +39,38 @@ template <typename T>
 inline T *dev_alloc(u64 n) {
   return reinterpret_cast<T *>(gpuMalloc(n * sizeof(T)));
 }
-// Public weights (host, the layer's data) on the device.
-template <typename T>
-inline T *upload(const T *h, u64 n) {
-  T *d = dev_alloc<T>(n);
-  mpcx_ezpc::hip_check(hipMemcpy(d, h, n * sizeof(T), hipMemcpyHostToDevice), "weights to device");
-  return d;
-}
 enum : uint32_t { R_SXP_PUBLIC = 100 };
+
+// Public weights and biases kept on the device across calls (a layer's weights
+// do not change between forwards): keyed by the host array and its size, and
+// checked against a host copy on every call, so weights changed in place are
+// uploaded again.  Saves the upload and, above all, the hipMalloc / hipFree
+// pair per call (hipFree waits for the whole device).
+template <typename T>
+class Resident {
+ public:
+  Resident() = default;
+  Resident(const Resident &) = delete;
+  Resident &operator=(const Resident &) = delete;
+  ~Resident() {
+    for (auto &kv : m_) gpuFree(kv.second.d);
+  }
+  const T *get(const T *h, u64 n) {
+    Entry &e = m_[{h, n}];
+    if (e.d && std::memcmp(e.host.data(), h, n * sizeof(T)) == 0) return e.d;
+    if (!e.d) e.d = dev_alloc<T>(n);
+    e.host.assign(h, h + n);
+    mpcx_ezpc::hip_check(hipMemcpy(e.d, h, n * sizeof(T), hipMemcpyHostToDevice), "weights to device");
+    return e.d;
+  }
+
+ private:
+  struct Entry {
+    std::vector<T> host;
+    T *d = nullptr;
+  };
+  std::map<std::pair<const T *, u64>, Entry> m_;
+};
 }  // namespace mpcx_sytorch
 
 // ===========================================================================
@@ -153,15 +179,12 @@ class MpcxOrca : public Backend<T> {
       gpuFree(d_mask_A);
     }
     mpcx_ctx *cx = mpcx_ezpc::ctx(bw);
-    T *d_W = mpcx_sytorch::upload(b.data, K * N);
+    const T *d_W = weights_.get(b.data, K * N);
     T *out = mpcx_sytorch::dev_alloc<T>(M * N);
     mpcx_ezpc::check(cx, mpcx_ring_gemm(cx, int(M), int(K), int(N), a.d_data, d_W, out), "matmul");
-    if (useBias) {
-      T *d_b = mpcx_sytorch::upload(d.data, N);
-      mpcx_ezpc::check(cx, mpcx_ring_lincomb(cx, M, N, 1, out, 0, nullptr, d_b, 0, out), "matmul bias");
-      gpuFree(d_b);
-    }
-    gpuFree(d_W);
+    if (useBias)
+      mpcx_ezpc::check(cx, mpcx_ring_lincomb(cx, M, N, 1, out, 0, nullptr, weights_.get(d.data, N), 0, out),
+                       "matmul bias");
     c.d_data = out;
     s.matmul_time += elapsed_us(t0);
   }
@@ -246,6 +269,7 @@ class MpcxOrca : public Backend<T> {
 
  private:
   bool owns_channel_ = false;
+  mpcx_sytorch::Resident<T> weights_;  // the public weights and biases on the device
   static u64 elapsed_us(std::chrono::high_resolution_clock::time_point t0) {
     return u64(std::chrono::duration_cast<std::chrono::microseconds>(std::chrono::high_resolution_clock::now() - t0)
                    .count());
@@ -316,10 +340,9 @@ class MpcxOrcaKeygen : public Backend<T> {
                       {{party == SERVER0 ? s0 : s1, M * K * sizeof(T)}});
     gpuFree(s0);
     gpuFree(s1);
-    T *d_W = mpcx_sytorch::upload(b.data, K * N);
     T *out = mpcx_sytorch::dev_alloc<T>(M * N);
-    mpcx_ezpc::check(cx, mpcx_ring_gemm(cx, int(M), int(K), int(N), a.d_data, d_W, out), "matmul keygen");
-    gpuFree(d_W);
+    mpcx_ezpc::check(cx, mpcx_ring_gemm(cx, int(M), int(K), int(N), a.d_data, weights_.get(b.data, K * N), out),
+                     "matmul keygen");
     c.d_data = out;
   }
 
@@ -369,4 +392,7 @@ class MpcxOrcaKeygen : public Backend<T> {
     keyBuf += n;
   }
   void optimize(LayerGraphNode<T> *root) override { (void)root; }
+
+ private:
+  mpcx_sytorch::Resident<T> weights_;  // the public weights on the device
 };

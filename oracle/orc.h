@@ -216,6 +216,9 @@ typedef struct {
                      2: also A.XW + bias: TRSLACK then RELUSLACK (|A.XW + b 2^s| < 2^(bw-2));
                      3: every layer truncation is LocalARS (local shift, no key), followed
                      by a RELU gate on ReLU layers: not bit-exact with orc_plain_forward */
+  int gcn_order;  /* orc_plain_forward only: 0 transform-first, H' = ReLU(tr(A.tr(H.W^T)) + b)
+                     (reference/fixed_forward.py:63-67); 1 aggregate-first, the order of the
+                     C++ layers, H' = ReLU(tr(tr(A.H).W^T + b 2^s)) (gpu_mpc/gcn_layer.h:113-114) */
 } orc_dims;
 
 /* Weights: for each linear layer in order gcn0..2, dfc0..1, fus0..nfus-1:

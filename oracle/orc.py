@@ -22,7 +22,7 @@ class Dims(C.Structure):
     _fields_ = [("bw", C.c_int), ("s", C.c_int), ("n_nodes", C.c_int), ("feat", C.c_int),
                 ("gcn", C.c_int * 3), ("dfc", C.c_int * 2), ("prot", C.c_int),
                 ("nfus", C.c_int), ("fus", C.c_int * 4), ("lut_nmax", C.c_int),
-                ("mask_scale", C.c_int), ("slack", C.c_int)]
+                ("mask_scale", C.c_int), ("slack", C.c_int), ("gcn_order", C.c_int)]
 
 
 class DcfLayout(C.Structure):
@@ -39,7 +39,7 @@ class TrLayout(C.Structure):
 
 
 def make_dims(bw=32, s=12, n_nodes=140, feat=78, gcn=(78, 156, 312), dfc=(1024, 128), prot=128,
-              fus=(1024, 512, 1), lut_nmax=138, mask_scale=0, slack=0):
+              fus=(1024, 512, 1), lut_nmax=138, mask_scale=0, slack=0, gcn_order=0):
     d = Dims()
     d.bw, d.s, d.n_nodes, d.feat = bw, s, n_nodes, feat
     for i, v in enumerate(gcn):
@@ -53,6 +53,7 @@ def make_dims(bw=32, s=12, n_nodes=140, feat=78, gcn=(78, 156, 312), dfc=(1024, 
     d.lut_nmax = lut_nmax
     d.mask_scale = mask_scale
     d.slack = int(slack)
+    d.gcn_order = int(gcn_order)  # plain_forward: 0 transform-first, 1 aggregate-first
     return d
 
 

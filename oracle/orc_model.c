@@ -211,9 +211,14 @@ int orc_plain_forward(const orc_dims *d, int B, const int64_t *X, const int64_t 
       int fo = d->gcn[l];
       const int64_t *Wt = W + layer_off(d, l);
       const int64_t *bias = Wt + (size_t)fin * fo;
-      fixed_mm(&f, H, Wt, (size_t)N, (size_t)fin, (size_t)fo, NULL, xw_slack(d) ? 7 : 0,
-               XW); /* XW */
-      fixed_mm(&f, Af, XW, (size_t)N, (size_t)N, (size_t)fo, bias, agg_split(d) ? 8 : 0, Hn); /* A.XW */
+      if (d->gcn_order == 1) { /* aggregate first: tr(A.H), then tr(AH.W^T) (+ b below) */
+        fixed_mm(&f, Af, H, (size_t)N, (size_t)N, (size_t)fin, NULL, 0, XW);
+        fixed_mm(&f, XW, Wt, (size_t)N, (size_t)fin, (size_t)fo, bias, 0, Hn);
+      } else {
+        fixed_mm(&f, H, Wt, (size_t)N, (size_t)fin, (size_t)fo, NULL, xw_slack(d) ? 7 : 0,
+                 XW); /* XW */
+        fixed_mm(&f, Af, XW, (size_t)N, (size_t)N, (size_t)fo, bias, agg_split(d) ? 8 : 0, Hn); /* A.XW */
+      }
       for (int i = 0; i < N; i++)
         for (int j = 0; j < fo; j++) {
           int64_t v = wrapv(&f, (i128)Hn[(size_t)i * fo + j] + bias[j]);

@@ -18,8 +18,11 @@
 // at scale 2s); writes adjn.bin (A_norm, unmasked), act.bin (the layer's output,
 // unmasked), out.bin (output(): act >> s), comm.txt (bytes on each party's
 // channel).  Exit status 0 when both parties agree.
+#include <atomic>
+#include <chrono>
 #include <cmath>
 #include <cstdio>
+#include <deque>
 #include <fstream>
 #include <iterator>
 #include <string>
@@ -276,6 +279,320 @@ int run(const std::string &dir, const Dims &d) {
   return 0;
 }
 
+// ---------------- 3. the whole affinity forward through a backend ----------------
+// DeepDTAGenAffinity::_forward (gpu_mpc/deepdtagen.h:183-222) as its layers
+// call the backend: per GCN layer _MatMul's per-sample secret x secret loop
+// (layers.h:67-93) and its truncation, the FC with public weights and bias and
+// its truncation, ReLU (mode 0: every layer full width, ddg_orca_opt.h:47-77);
+// the mask product (_Mul, backend mul with TrWithSlack, layers.h:318-346);
+// MaskedMaxPoolLayer::_forward (masked_maxpool_layer.h:47-165); the drug FCs;
+// GPUConcat (deepdtagen.h:45-101: the protein leaf revealed, rows interleaved);
+// the fusion FCs, the last one untruncated; output() (ddg_orca_base.h:296-302).
+struct FDims {
+  int bw, B, N, F, gcn[3], dfc[2], prot, nfus, fus[4], s, nmax, reps, stop = 0;
+  std::vector<std::pair<u64, u64>> layers() const {
+    std::vector<std::pair<u64, u64>> io;
+    u64 fin = u64(F);
+    for (int g : gcn) io.push_back({fin, u64(g)}), fin = u64(g);
+    io.push_back({u64(gcn[2]), u64(dfc[0])});
+    io.push_back({u64(dfc[0]), u64(dfc[1])});
+    fin = u64(dfc[1] + prot);
+    for (int i = 0; i < nfus; i++) io.push_back({fin, u64(fus[i])}), fin = u64(fus[i]);
+    return io;
+  }
+};
+
+// A linear layer's public weights (in x out) and bias (at scale 2s), held the
+// way FC<T> holds them: host arrays that live as long as the model.
+template <typename T>
+struct Lin {
+  Tensor<T> W;
+  Tensor1D<T> b;
+  Lin(u64 in, u64 out, const T *w, const T *bias) : W({in, out}), b(out) {
+    std::memcpy(W.data, w, in * out * sizeof(T));
+    std::memcpy(b.data, bias, out * sizeof(T));
+  }
+};
+
+// FC<T>::_forward: x . W + b, then the layer truncation (all but the last layer)
+template <typename T, class BE>
+Tensor<T> *fc(BE &be, Tensor<T> &x, Lin<T> &L, int s, bool trunc) {
+  const u64 out = L.W.shape[1], M = x.size() / L.W.shape[0];
+  auto *z = new Tensor<T>({M, out});
+  Tensor2D<T> x2(x.data, x.d_data, M, L.W.shape[0]), z2 = z->as_2d();
+  Tensor2D<T> w2 = L.W.as_2d();
+  be.matmul(x2, w2, z2, true, L.b, false);
+  z->d_data = z2.d_data;
+  if (trunc) be.truncateForward(*z, u64(s));
+  return z;
+}
+// ReLU<T>::_forward in mode 0 (full width)
+template <typename T, class BE>
+Tensor<T> *relu(BE &be, Tensor<T> *x, int s) {
+  auto *y = new Tensor<T>(x->shape);
+  Tensor<T> drelu(x->shape);
+  be.relu(*x, *y, drelu, u64(s), 0);
+  gpuFree(x->d_data);
+  delete x;
+  return y;
+}
+// GCNLayer::_forward (gcn_layer.h:107-116): aggregate first, then the FC, ReLU
+template <typename T, class BE>
+Tensor<T> *gcn(BE &be, int B, int N, Tensor<T> &A, Tensor<T> &H, Lin<T> &L, int s) {
+  const u64 K = L.W.shape[0], Nn = u64(N), BN = u64(B) * Nn;
+  auto *AX = new Tensor<T>({BN, K});
+  AX->d_data = reinterpret_cast<T *>(gpuMalloc(BN * K * sizeof(T)));
+  for (int b = 0; b < B; b++) {  // _MatMul's per-sample loop
+    Tensor2D<T> A_slice(A.data + b * Nn * Nn, A.d_data + b * Nn * Nn, Nn, Nn);
+    Tensor2D<T> X_slice(H.data + b * Nn * K, H.d_data + b * Nn * K, Nn, K);
+    Tensor2D<T> out_slice(AX->data + b * Nn * K, nullptr, Nn, K);
+    be.matmul(A_slice, X_slice, out_slice);
+    mpcx_ezpc::hip_check(hipMemcpy(AX->d_data + b * Nn * K, out_slice.d_data, Nn * K * sizeof(T),
+                                   hipMemcpyDeviceToDevice), "fold");
+    gpuFree(out_slice.d_data);
+  }
+  be.truncateForward(*AX, u64(s));
+  Tensor<T> *Z = fc(be, *AX, L, s, true);
+  gpuFree(AX->d_data);
+  delete AX;
+  return relu(be, Z, s);
+}
+// MaskedMaxPoolLayer::_forward: node-major planes, then per level
+// scalarmul(even, -1), add(., odd), relu, add(even, .), the odd plane carried
+template <typename T, class BE>
+Tensor<T> *maxpool(BE &be, Tensor<T> &masked, int B, int N, int F, int s) {
+  const u64 plane = u64(B) * u64(F);
+  T *d_buf = reinterpret_cast<T *>(gpuMalloc(u64(N) * plane * sizeof(T)));
+  for (int b = 0; b < B; b++)
+    mpcx_ezpc::hip_check(hipMemcpy2D(d_buf + u64(b) * F, plane * sizeof(T), masked.d_data + u64(b) * N * F,
+                                     u64(F) * sizeof(T), u64(F) * sizeof(T), u64(N), hipMemcpyDeviceToDevice),
+                         "pool planes");
+  u64 cur = u64(N);
+  T *d_cur = d_buf;
+  while (cur > 1) {
+    const u64 pairs = cur / 2, rem = cur % 2, n = pairs * plane;
+    T *d_even = reinterpret_cast<T *>(gpuMalloc(n * sizeof(T)));
+    T *d_odd = reinterpret_cast<T *>(gpuMalloc(n * sizeof(T)));
+    for (u64 p = 0; p < pairs; p++) {
+      mpcx_ezpc::hip_check(hipMemcpy(d_even + p * plane, d_cur + 2 * p * plane, plane * sizeof(T),
+                                     hipMemcpyDeviceToDevice), "even plane");
+      mpcx_ezpc::hip_check(hipMemcpy(d_odd + p * plane, d_cur + (2 * p + 1) * plane, plane * sizeof(T),
+                                     hipMemcpyDeviceToDevice), "odd plane");
+    }
+    Tensor<T> t_even(nullptr, d_even, {n}), t_odd(nullptr, d_odd, {n});
+    Tensor<T> t_neg({n}), t_diff({n}), t_drelu({n}), t_relu({n}), t_res({n});
+    be.scalarmul(t_even, T(0) - T(1), t_neg);  // ring negation, no truncation
+    std::vector<Tensor<T> *> in1 = {&t_neg, &t_odd};
+    be.add(in1, t_diff);
+    be.relu(t_diff, t_relu, t_drelu, u64(s), 0);
+    std::vector<Tensor<T> *> in2 = {&t_even, &t_relu};
+    be.add(in2, t_res);
+    T *d_next = reinterpret_cast<T *>(gpuMalloc((pairs + rem) * plane * sizeof(T)));
+    mpcx_ezpc::hip_check(hipMemcpy(d_next, t_res.d_data, n * sizeof(T), hipMemcpyDeviceToDevice), "level");
+    if (rem)
+      mpcx_ezpc::hip_check(hipMemcpy(d_next + n, d_cur + (cur - 1) * plane, plane * sizeof(T),
+                                     hipMemcpyDeviceToDevice), "carry");
+    for (T *q : {d_even, d_odd, t_neg.d_data, t_diff.d_data, t_relu.d_data, t_res.d_data, d_cur}) gpuFree(q);
+    d_cur = d_next;
+    cur = pairs + rem;
+  }
+  auto *out = new Tensor<T>({u64(B), u64(F)});
+  out->d_data = d_cur;
+  return out;
+}
+// GPUConcat::_forward: reveal the public leaves, then rows [t0[b] | t1[b]]
+template <typename T>
+void reveal_public(MpcxOrca<T> &be, Tensor<T> &t) {
+  be.revealPublicLeaf(t.d_data, be.bw, t.size());
+}
+template <typename T>
+void reveal_public(MpcxOrcaKeygen<T> &, Tensor<T> &) {}
+template <typename T, class BE>
+Tensor<T> *concat(BE &be, Tensor<T> &a, Tensor<T> &b) {
+  reveal_public(be, a);
+  reveal_public(be, b);
+  const u64 wa = a.shape.back(), wb = b.shape.back(), rows = a.size() / wa, w = wa + wb;
+  auto *o = new Tensor<T>({rows, w});
+  o->d_data = reinterpret_cast<T *>(gpuMalloc(rows * w * sizeof(T)));
+  for (u64 r = 0; r < rows; r++) {
+    mpcx_ezpc::hip_check(hipMemcpy(o->d_data + r * w, a.d_data + r * wa, wa * sizeof(T), hipMemcpyDeviceToDevice),
+                         "concat");
+    mpcx_ezpc::hip_check(hipMemcpy(o->d_data + r * w + wa, b.d_data + r * wb, wb * sizeof(T),
+                                   hipMemcpyDeviceToDevice), "concat");
+  }
+  return o;
+}
+// The model's forward on masked-public A_norm (B*N x N), X (B*N x F), the
+// tiled mask leaf (B*N x gcn[2]) and the protein leaf (B x prot); returns the
+// last layer's output (B x 1), not yet output().
+// stop > 0 returns the tensor after that stage instead (1-3 the GCN layers, 4
+// the mask product, 5 the pool, 6 and 7 the drug FCs, 8 the concat): a
+// diagnostic cut that the dealer and the evaluators make alike.
+template <typename T, class BE>
+Tensor<T> *affinity_forward(BE &be, const FDims &d, std::deque<Lin<T>> &L, Tensor<T> &A, Tensor<T> &X,
+                            Tensor<T> &maskT, Tensor<T> &prot, int stop = 0) {
+  Tensor<T> *h = gcn(be, d.B, d.N, A, X, L[0], d.s);
+  for (int l = 1; l < 3; l++) {
+    if (stop == l) return h;
+    Tensor<T> *h2 = gcn(be, d.B, d.N, A, *h, L[size_t(l)], d.s);
+    gpuFree(h->d_data);
+    delete h;
+    h = h2;
+  }
+  if (stop == 3) return h;
+  auto *masked = new Tensor<T>(h->shape);
+  be.mul(*h, maskT, *masked);
+  gpuFree(h->d_data);
+  delete h;
+  if (stop == 4) return masked;
+  Tensor<T> *pooled = maxpool(be, *masked, d.B, d.N, d.gcn[2], d.s);
+  gpuFree(masked->d_data);
+  delete masked;
+  if (stop == 5) return pooled;
+  Tensor<T> *d1 = relu(be, fc(be, *pooled, L[3], d.s, true), d.s);
+  gpuFree(pooled->d_data);
+  delete pooled;
+  if (stop == 6) return d1;
+  Tensor<T> *d2 = fc(be, *d1, L[4], d.s, true);
+  gpuFree(d1->d_data);
+  delete d1;
+  if (stop == 7) return d2;
+  Tensor<T> *f = concat(be, *d2, prot);
+  gpuFree(d2->d_data);
+  delete d2;
+  if (stop == 8) return f;
+  for (int i = 0; i < d.nfus; i++) {
+    const bool last = i + 1 == d.nfus;
+    Tensor<T> *e = fc(be, *f, L[size_t(5 + i)], d.s, !last);
+    if (!last) e = relu(be, e, d.s);
+    gpuFree(f->d_data);
+    delete f;
+    f = e;
+  }
+  return f;
+}
+
+template <typename T>
+int run_forward(const std::string &dir, const FDims &d) {
+  const u64 N = u64(d.N), NN = N * N, BN = u64(d.B) * N, adjN = u64(d.B) * NN;
+  const u64 C = u64(d.gcn[2]);
+  std::vector<T> a[2] = {load<T>(dir + "/a0.bin", adjN), load<T>(dir + "/a1.bin", adjN)};
+  std::vector<T> x[2] = {load<T>(dir + "/x0.bin", BN * d.F), load<T>(dir + "/x1.bin", BN * d.F)};
+  std::vector<T> m[2] = {load<T>(dir + "/m0.bin", BN * C), load<T>(dir + "/m1.bin", BN * C)};
+  const std::vector<T> prot = load<T>(dir + "/prot.bin", u64(d.B) * d.prot);
+  size_t wlen = 0;
+  for (auto &io : d.layers()) wlen += io.first * io.second + io.second;
+  const std::vector<T> w = load<T>(dir + "/w.bin", wlen);
+  auto make_layers = [&]() {
+    std::deque<Lin<T>> L;  // FC<T> holds its weights in place: no copies
+    size_t o = 0;
+    for (auto &io : d.layers()) {
+      L.emplace_back(io.first, io.second, w.data() + o, w.data() + o + io.first * io.second);
+      o += io.first * io.second + io.second;
+    }
+    return L;
+  };
+  Dims ad{d.bw, d.B, d.N, d.F, 0, d.s, d.nmax};
+
+  // ---- dealer: one run per party; both keys go into one host buffer, which
+  // becomes the device key arena (initGPUKeyArena) for the evaluators
+  const size_t cap = size_t(d.B) * (size_t(d.bw) << 22) + (size_t(256) << 20);
+  std::vector<std::vector<u8>> kh(2);
+  std::vector<T> out_mask(size_t(d.B));
+  for (int party = 0; party < 2; party++) {
+    MpcxOrcaKeygen<T> kg(party, d.bw, d.s, "", cap);
+    std::deque<Lin<T>> L = make_layers();
+    T *d_A_mask = randomGEOnGpu<T>(adjN, d.bw);
+    T *d_X_mask = randomGEOnGpu<T>(BN * d.F, d.bw);
+    T *d_M_mask = randomGEOnGpu<T>(BN * C, d.bw);
+    T *nm = adjnorm_keygen<T>(&kg.keyBuf, party, ad, d_A_mask, &kg.g);
+    Tensor<T> A({BN, N}), X({BN, u64(d.F)}), MT({BN, C}), P({u64(d.B), u64(d.prot)});
+    A.d_data = nm;
+    X.d_data = d_X_mask;
+    MT.d_data = d_M_mask;
+    P.d_data = to_dev(std::vector<T>(P.size(), T(0)));  // the protein leaf: mask 0 (public)
+    Tensor<T> *out = affinity_forward<T>(kg, d, L, A, X, MT, P, d.stop);
+    kg.output(*out);
+    kh[size_t(party)].assign(kg.startPtr, kg.keyBuf);
+    for (T *q : {d_A_mask, d_X_mask, d_M_mask, nm, P.d_data, out->d_data}) gpuFree(q);
+    delete out;
+  }
+  const size_t k0 = kh[0].size(), k1 = kh[1].size(), off1 = (k0 + 4095) / 4096 * 4096;
+  u8 *keys = cpuMalloc(off1 + k1, false);
+  std::memcpy(keys, kh[0].data(), k0);
+  std::memcpy(keys + off1, kh[1].data(), k1);
+  kh[0].clear(), kh[0].shrink_to_fit(), kh[1].clear(), kh[1].shrink_to_fit();
+  initGPUKeyArena(keys, off1 + k1);
+
+  // ---- the two evaluators, concurrently, reps forwards on the same keys
+  mpcx_peer *ends[2];
+  if (mpcx_peer_pair(120000, &ends[0], &ends[1]) != MPCX_OK) mpcx_ezpc::die("mpcx_peer_pair");
+  std::vector<T> out_host[2];
+  std::vector<double> ms[2];
+  u64 comm[2] = {0, 0}, aes[2] = {0, 0}, rounds[2] = {0, 0};
+  Stats st[2];
+  std::atomic<int> ready{0};
+  auto party_main = [&](int party) {
+    u8 *mine = party ? keys + off1 : keys;
+    MpcxOrca<T> be(party, ends[party], d.bw, d.s, mine, party ? k1 : k0);
+    std::deque<Lin<T>> L = make_layers();
+    for (int r = 0; r < d.reps; r++) {
+      be.keyBuf = be.startPtr;  // the same key set for every forward (timing only)
+      be.resetLeaves();
+      T *d_A = to_dev(a[party]);
+      Tensor<T> X({BN, u64(d.F)}), MT({BN, C}), P({u64(d.B), u64(d.prot)});
+      X.d_data = to_dev(x[party]);
+      MT.d_data = to_dev(m[party]);
+      P.d_data = to_dev(party ? prot : std::vector<T>(P.size(), T(0)));  // party 1 holds the protein embedding
+      // start together: each forward is timed from here to its output
+      const int gen = 2 * (r + 1);
+      ready.fetch_add(1);
+      while (ready.load() < gen) std::this_thread::yield();
+      const u64 b0 = mpcx_peer_bytes(ends[party]), aes0 = mpcx_ezpc::aes_calls(), r0 = mpcx_peer_rounds(ends[party]);
+      be.s = Stats();
+      const auto t0 = std::chrono::steady_clock::now();
+      T *d_norm = adjnorm_eval<T>(&be.keyBuf, be.peer, party, ad, &be.g, &be.s, d_A);
+      Tensor<T> A({BN, N});
+      A.d_data = d_norm;
+      for (int g = 0; g < d.B; g++) be.registerLeaf(X.d_data + size_t(g) * N * d.F);  // _MatMul's slices
+      be.registerLeaf(MT.d_data);
+      be.registerLeaf(P.d_data);
+      Tensor<T> *out = affinity_forward<T>(be, d, L, A, X, MT, P, d.stop);
+      be.output(*out);
+      ms[party].push_back(std::chrono::duration<double, std::milli>(std::chrono::steady_clock::now() - t0).count());
+      comm[party] = mpcx_peer_bytes(ends[party]) - b0;
+      aes[party] = mpcx_ezpc::aes_calls() - aes0;
+      rounds[party] = mpcx_peer_rounds(ends[party]) - r0;
+      st[party] = be.s;
+      out_host[party].assign(out->data, out->data + out->size());
+      for (T *q : {d_A, d_norm, X.d_data, MT.d_data, P.d_data, out->d_data}) gpuFree(q);
+      delete out;
+    }
+  };
+  std::thread t0(party_main, 0), t1(party_main, 1);
+  t0.join();
+  t1.join();
+  if (out_host[0] != out_host[1]) mpcx_ezpc::die("the two parties' outputs differ");
+  store(dir + "/out.bin", out_host[0].data(), out_host[0].size(), false);
+  std::ofstream(dir + "/comm.txt") << comm[0] << " " << comm[1] << "\n";
+  std::ofstream tf(dir + "/time.txt");
+  for (int r = 0; r < d.reps; r++) tf << std::max(ms[0][size_t(r)], ms[1][size_t(r)]) << "\n";
+  std::ofstream(dir + "/keys.txt") << k0 << " " << k1 << "\n";
+  std::ofstream(dir + "/aes.txt") << aes[0] << " " << aes[1] << "\n";
+  {  // party 0's backend timers of the last forward (us) and its exchange rounds
+    std::ofstream f(dir + "/stats.txt");
+    f << "rounds " << rounds[0] << "\nmatmul_us " << st[0].matmul_time << "\nrelu_us " << st[0].relu_time
+      << "\ntruncate_us " << st[0].truncate_time << "\n";
+  }
+  mpcx_peer_close(ends[0]);
+  mpcx_peer_close(ends[1]);
+  freeGPUKeyArena();
+  cpuFree(keys, false);
+  std::printf("ezpc_check forward: both parties agree (%zu key bytes per party), %.2f ms last forward\n", k0,
+              std::max(ms[0].back(), ms[1].back()));
+  return 0;
+}
+
 }  // namespace
 
 // `ezpc_check width <bw> <bin> <bout> [drelu]`: a ReLU (or DReLU) keygen for
@@ -301,8 +618,21 @@ int main(int argc, char **argv) {
     const bool drelu = argc >= 6 && std::string(argv[5]) == "drelu";
     return bw == 32 ? width_check<uint32_t>(bin, bout, drelu) : width_check<uint64_t>(bin, bout, drelu);
   }
+  if (argc >= 3 && std::string(argv[1]) == "forward") {
+    const std::string dir = argv[2];
+    FDims d{};
+    std::ifstream meta(dir + "/meta.txt");
+    if (!(meta >> d.bw >> d.B >> d.N >> d.F >> d.gcn[0] >> d.gcn[1] >> d.gcn[2] >> d.dfc[0] >> d.dfc[1] >> d.prot >>
+          d.nfus))
+      mpcx_ezpc::die("bad meta.txt");
+    if (d.nfus < 1 || d.nfus > 4) mpcx_ezpc::die("meta.txt: 1 to 4 fusion layers");
+    for (int i = 0; i < d.nfus; i++) meta >> d.fus[i];
+    if (!(meta >> d.s >> d.nmax >> d.reps) || d.reps < 1) mpcx_ezpc::die("bad meta.txt");
+    if (!(meta >> d.stop)) d.stop = 0;  // optional: the diagnostic stage cut
+    return d.bw == 32 ? run_forward<uint32_t>(dir, d) : run_forward<uint64_t>(dir, d);
+  }
   if (argc < 2) {
-    std::fprintf(stderr, "usage: %s <dir> | width <bw> <bin> <bout> [drelu]\n", argv[0]);
+    std::fprintf(stderr, "usage: %s <dir> | forward <dir> | width <bw> <bin> <bout> [drelu]\n", argv[0]);
     return 2;
   }
   const std::string dir = argv[1];

@@ -59,7 +59,11 @@ class Tensor {
   T *d_data = nullptr;  // device
   std::vector<u64> shape;
   explicit Tensor(const std::vector<u64> &s) : shape(s) { data = new T[size()](); }
-  ~Tensor() { delete[] data; }
+  // a view of existing host and device arrays (masked_maxpool_layer.h:96, 109)
+  Tensor(T *data_, T *d_data_, const std::vector<u64> &s) : data(data_), d_data(d_data_), shape(s), owns_(false) {}
+  ~Tensor() {
+    if (owns_) delete[] data;
+  }
   Tensor(const Tensor &) = delete;
   Tensor &operator=(const Tensor &) = delete;
   u64 size() const {
@@ -72,6 +76,9 @@ class Tensor {
     const u64 d2 = shape.empty() ? 1 : shape.back();
     return Tensor2D<T>(data, d_data, size() / d2, d2);
   }
+
+ private:
+  bool owns_ = true;
 };
 
 template <typename T>

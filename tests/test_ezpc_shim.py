@@ -93,3 +93,76 @@ def test_shim_adjnorm_and_gcn_layer(orc, synth, tmp_path, bw):
     assert np.array_equal(got_out, act >> S)
     c0, c1 = (int(v) for v in (d / "comm.txt").read_text().split())
     assert c0 == c1 > 0
+
+
+def _fwd_expected(A_fx, X, maskT, prot, layers, bw, s=S):
+    """The forward in the backend's op order, in exact integers: GCN aggregate
+    first (gcn_layer.h:113-114: tr(A.H), then the FC + bias and its
+    truncation, ReLU); the mask product truncated once (TrWithSlack); the pool
+    a maximum over all node rows (padding rows are 0 after the mask); the drug
+    FCs; [drug | protein]; the fusion FCs, the last one truncated by output().
+    Checks that every value a ring protocol truncates lies in the signed ring."""
+    half = 1 << (bw - 1)
+
+    def tr(v, lim=half):
+        assert np.abs(v).max() < lim, "outside the bit-exact domain"
+        return np.floor_divide(v, 1 << s)
+
+    H = X
+    for W, b in layers[:3]:
+        AX = tr(np.matmul(A_fx, H))
+        H = np.maximum(tr(np.matmul(AX, W) + (b << s)), 0)
+    pooled = tr(H * maskT, 1 << (bw - 2)).max(axis=1)
+    (W3, b3), (W4, b4) = layers[3], layers[4]
+    d1 = np.maximum(tr(pooled @ W3 + (b3 << s)), 0)
+    f = np.concatenate([tr(d1 @ W4 + (b4 << s)), prot], axis=1)
+    for i, (W, b) in enumerate(layers[5:]):
+        e = tr(f @ W + (b << s))
+        f = e if i + 1 == len(layers) - 5 else np.maximum(e, 0)
+    return f.reshape(-1)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("bw", [32, 64])
+def test_shim_whole_forward(orc, synth, tmp_path, bw):
+    """The reference's whole online path through the shim and Backend<T>
+    (ezpc_check forward): ddgSecureAdjNormEval, then DeepDTAGenAffinity::
+    _forward's backend calls, one dealer run per party, the two evaluators as
+    two threads on one channel with both key sets resident (initGPUKeyArena);
+    both parties' outputs equal the integer forward in that op order."""
+    B = 2
+    dims = synth.Dims(bw=bw)
+    wl = synth.workload(B, dims, seed=23)
+    N, C = dims.n_nodes, dims.gcn[2]
+    maskT = np.repeat((wl.mask << S)[:, :, None], C, axis=2)  # the pre-tiled mask at scale s
+    layers, o = [], 0
+    for fin, fout in dims.layers():
+        W = wl.W[o:o + fin * fout].reshape(fin, fout)
+        b = wl.W[o + fin * fout:o + fin * fout + fout]
+        layers.append((W, b))
+        o += fin * fout + fout
+    want = _fwd_expected(orc.adj_norm_plain(wl.A), wl.X, maskT, wl.prot, layers, bw)
+    od = orc.make_dims(bw=bw, s=S, n_nodes=N, feat=dims.feat, gcn=dims.gcn, dfc=dims.dfc, prot=dims.prot,
+                       fus=dims.fus, lut_nmax=dims.lut_nmax, gcn_order=1)
+    ow, code = orc.plain_forward(od, wl.X, wl.A, wl.mask, wl.prot, wl.W)
+    assert code == 0 and np.array_equal(ow, want)  # the oracle's aggregate-first forward agrees
+    d = tmp_path
+    (d / "meta.txt").write_text(" ".join(str(v) for v in (
+        bw, B, N, dims.feat, *dims.gcn, *dims.dfc, dims.prot, len(dims.fus), *dims.fus, S, dims.lut_nmax, 1)) + "\n")
+    a0, a1 = synth.share(wl.A, bw, 3)
+    x0, x1 = synth.share(wl.X, bw, 4)
+    m0, m1 = synth.share(maskT, bw, 5)
+    blob = np.concatenate([np.concatenate([W.reshape(-1), b << S]) for W, b in layers])
+    for name, v in (("a0", a0), ("a1", a1), ("x0", x0), ("x1", x1), ("m0", m0), ("m1", m1), ("prot", wl.prot),
+                    ("w", blob)):
+        _ring(v, bw).tofile(str(d / f"{name}.bin"))
+    kfile = d / "dealer.key"
+    kfile.write_bytes(bytes(range(90, 106)))
+    r = subprocess.run([BIN, "forward", str(d)], capture_output=True, text=True, timeout=300,
+                       env=dict(os.environ, MPCX_DEALER_KEY=str(kfile)))
+    assert r.returncode == 0, r.stdout + r.stderr
+    dt = np.uint32 if bw == 32 else np.uint64
+    got = _signed(np.fromfile(str(d / "out.bin"), dt), bw)
+    assert np.array_equal(got, want), (got, want)
+    c0, c1 = (int(v) for v in (d / "comm.txt").read_text().split())
+    assert c0 == c1 > 0

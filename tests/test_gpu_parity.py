@@ -78,6 +78,31 @@ def test_dcf_keys_and_eval(mp, orc, m):
     c.close()
 
 
+@pytest.mark.parametrize("bw,m", [(32, 5), (32, 12), (32, 31), (64, 20), (64, 63)])
+def test_dcf_eval_ring_inputs_and_mask(mp, orc, bw, m):
+    """mpcx_dcf_eval_ring (the reference's gpuDcf with maskEpilogue,
+    gpu_mpc/dpf_dcf_adapter.h:266, 293): ring elements read modulo 2^m (their
+    upper bits set at random change nothing), the output bits XORed with a mask
+    of 32-bit words; equal to mpcx_dcf_eval on the reduced inputs."""
+    c = mp.Ctx(bw=bw)
+    rng = np.random.default_rng(bw + m)
+    n = 3001  # odd number of 32-bit mask words: the last one partly used
+    top = (1 << m) - 1
+    alpha = rng.integers(0, top, size=n, dtype=np.uint64, endpoint=True)
+    g0, g1 = c.dcf_keygen(m, alpha, None, seed=5, gate=2)
+    x = rng.integers(0, top, size=n, dtype=np.uint64, endpoint=True)
+    x_ring = x | (rng.integers(0, 1 << (bw - m), size=n, dtype=np.uint64) << np.uint64(m))  # garbage above bit m
+    mask = rng.integers(0, 1 << 32, size=(n + 31) // 32, dtype=np.uint64).astype(np.uint32)
+    mbits = np.unpackbits(mask.view(np.uint8), bitorder="little")[:n]
+    for p, g in ((0, g0), (1, g1)):
+        want = c.dcf_eval(p, m, g, x)
+        assert np.array_equal(c.dcf_eval_ring(p, m, g, x_ring), want)
+        assert np.array_equal(c.dcf_eval_ring(p, m, g, x_ring, mask), want ^ mbits)
+    b = c.dcf_eval_ring(0, m, g0, x_ring, mask) ^ c.dcf_eval_ring(1, m, g1, x_ring)
+    assert np.array_equal(b, (x < alpha).astype(np.uint8) ^ mbits)
+    c.close()
+
+
 def test_dcf_exhaustive_small_domain(mp):
     c = mp.Ctx(bw=32)
     m, N = 10, 1024

@@ -135,6 +135,11 @@ def test_gcn_order_is_transform_first(orc):
     out, code = orc.plain_forward(d, X, A, mask, prot, W)
     assert code == 0
     assert out.tolist() == [4157]
+    # the C++ layers' order (orc_dims.gcn_order = 1) gives the aggregate-first 4156
+    d.gcn_order = 1
+    out, code = orc.plain_forward(d, X, A, mask, prot, W)
+    assert code == 0 and out.tolist() == [4156]
+    d.gcn_order = 0
     # the two-party protocol reconstructs the same value
     k0, k1 = orc.model_keygen(d, 1, 7, W)
     rng = np.random.default_rng(3)
