@@ -246,6 +246,7 @@ mpcx_status mpcx_create(int bw, int scale, int device, mpcx_ctx **out) {
     else std::fprintf(stderr, "libmpcx: ignoring MPCX_GEMM=%s (auto, wide, tiled or valu)\n", v);
   }
   if (const char *v = std::getenv("MPCX_GRAPH")) c->L.graph = std::atoi(v) != 0 ? 1 : 0;
+  if (const char *v = std::getenv("MPCX_POOL_TAIL")) c->L.pool_tail = std::max(-1, std::atoi(v));
   *out = c;
   return MPCX_OK;
 }

@@ -434,6 +434,89 @@ __global__ void k_tr_eval_pool_q(TrArgs<T> a, TrPool<T> q) {
   tr_eval_tiles_quad<T, false, true>(a, a, q);
 }
 
+// ---- the last levels of a max-pool tree in one launch (latency-bound lanes) ----
+// Levels 0..nlev-1 of the tail, each a gate of one RELU kind over the pairs of
+// the level (element i = (b pr + j) C + c, the layout of a level launched
+// alone; N, the sign DCF and the G / kappa planes per level, the rest shared).
+constexpr int kTailMaxLevels = 8;
+template <typename T>
+struct TrTail {
+  TrArgs<T> a;
+  int nlev = 0;
+  size_t N[kTailMaxLevels] = {};
+  DcfLayout dcf[kTailMaxLevels];
+  size_t off_kappa[kTailMaxLevels] = {}, off_g[kTailMaxLevels] = {};
+  int B = 0, R0 = 0, C = 0, ncol = 0;  // ncol: columns (b, c) per workgroup
+  const T *v = nullptr;                // R0 rows of C words per block b
+  T *out = nullptr;                    // one row of C words per block b
+};
+
+// A workgroup owns columns g0 .. g0 + ncol - 1 (g = b C + c) for the whole tail:
+// their R0 values sit in LDS, and every level evaluates the columns' pairs in
+// tiles of h elements with the quad-lane gate (both parties, the exchanges in
+// LDS), party 0 writing V[2j] + y into row j of the other LDS buffer (an odd
+// level's last row carried).  No level waits for another workgroup, so the
+// levels run back to back in one launch.
+template <typename T, int TAG>
+__global__ void k_tr_eval_pool_tail_q(TrTail<T> t) {
+  if (t.a.prio) __builtin_amdgcn_s_setprio(2);
+  __shared__ __align__(16) uint32_t lds[AesPerm2::kWords];
+  __shared__ TrXchg<T> x;
+  extern __shared__ __align__(16) unsigned char tail_lds[];
+  AesPerm2::fill(lds);
+  const AesPerm2 tab(lds);
+  const AesQuad aes(tab);
+  const AesQuad::Keys kH = aes.keys(c_rkH), kL = aes.keys(c_rkL);
+  const int hq = int(blockDim.x) / 2, h = hq / 4;
+  const int p = int(threadIdx.x) >= hq ? 1 : 0;
+  const int lt = int(threadIdx.x) - p * hq;
+  const int e = lt >> 2, wv = lt >> 6;
+  const uint8_t *K = p ? t.a.k1 : t.a.k0, *KC = t.a.k0;
+  const int R0 = t.R0, C = t.C;
+  const int g0 = int(blockIdx.x) * t.ncol;
+  const int nc = min(t.ncol, t.B * C - g0);
+  T *vin = reinterpret_cast<T *>(tail_lds), *vout = vin + t.ncol * R0;
+  for (int k = int(threadIdx.x); k < nc * R0; k += int(blockDim.x)) {
+    const int cc = k / R0, r = k - cc * R0, g = g0 + cc, b = g / C, c = g - b * C;
+    vin[k] = t.v[(size_t(b) * R0 + r) * C + c];
+  }
+  __syncthreads();
+  int R = R0;
+  for (int l = 0; l < t.nlev; l++) {
+    TrArgs<T> a = t.a;
+    a.N = t.N[l];
+    a.a = t.dcf[l];
+    a.off_kappa = t.off_kappa[l];
+    a.off_g = t.off_g[l];
+    const int pr = R / 2, tot = nc * pr;
+    for (int base = 0; base < tot; base += h) {  // uniform over the workgroup
+      const int idx = base + e;
+      const bool in = idx < tot;
+      T v0 = 0, xin = 0;
+      size_t i = 0;
+      int cc = 0, j = 0;
+      if (in) {
+        cc = idx / pr;
+        j = idx - cc * pr;
+        const int g = g0 + cc, b = g / C, c = g - b * C;
+        i = (size_t(b) * pr + j) * C + c;
+        v0 = vin[cc * R0 + 2 * j];
+        xin = vin[cc * R0 + 2 * j + 1] - v0;
+      }
+      const T y = tr_tile_quad(aes, kH, kL, a, x, p, e, wv, K, KC, i, in, xin);
+      if (p == 0 && in && (lt & 3) == 0) vout[cc * R0 + j] = v0 + y;
+    }
+    if (R & 1)
+      for (int k = int(threadIdx.x); k < nc; k += int(blockDim.x)) vout[k * R0 + pr] = vin[k * R0 + R - 1];
+    __syncthreads();
+    T *tmp = vin;
+    vin = vout;
+    vout = tmp;
+    R = pr + (R & 1);
+  }
+  for (int k = int(threadIdx.x); k < nc; k += int(blockDim.x)) t.out[g0 + k] = vin[k * R0];
+}
+
 template <typename T, int NT, int REP, int TAG>
 __global__ void k_tr_eval(TrArgs<T> a) {
   if (a.prio) __builtin_amdgcn_s_setprio(2);
@@ -798,6 +881,51 @@ hipError_t launch_tr_eval_pool(const Launch &L, const TrLayout &lay, const uint8
 }
 
 template <typename T>
+hipError_t launch_tr_eval_pool_tail(const Launch &L, const TrLayout *lay, int nlev, const uint8_t *k0,
+                                   const uint8_t *k1, int B, int R0, int C, const T *V, T *out) {
+  if (nlev < 1 || nlev > kTailMaxLevels || B < 1 || R0 < 2 || C < 1 || size_t(B) * R0 * C >= (size_t(1) << 31))
+    return hipErrorInvalidValue;
+  TrTail<T> t;
+  t.a = tr_args<T>(lay[0]);
+  t.a.k0 = k0;
+  t.a.k1 = k1;
+  t.a.bias_ncol = 1;
+  t.a.prio = 1;
+  int R = R0;
+  for (int l = 0; l < nlev; l++) {  // one RELU kind, sign DCF only, the pairs of level l
+    const TrLayout &y = lay[l];
+    if (y.bw != int(8 * sizeof(T)) || y.kind != lay[0].kind || y.s != lay[0].s || !y.use_a || y.use_b ||
+        !tr_is_relu(y.kind) || R < 2 || y.N != size_t(B) * (R / 2) * C)
+      return hipErrorInvalidValue;
+    t.N[l] = y.N;
+    t.dcf[l] = y.a;
+    t.off_kappa[l] = y.off_kappa;
+    t.off_g[l] = y.off_g;
+    R = R / 2 + (R & 1);
+  }
+  if (R != 1) return hipErrorInvalidValue;  // the tail ends with one row
+  t.nlev = nlev;
+  t.B = B;
+  t.R0 = R0;
+  t.C = C;
+  t.v = V;
+  t.out = out;
+  // about one workgroup per CU; per workgroup h elements per tile (a multiple
+  // of 16, so that each party's 4h threads are whole waves)
+  const int cols = B * C;
+  t.ncol = std::max(1, (cols + L.num_cu - 1) / L.num_cu);
+  const int grid = (cols + t.ncol - 1) / t.ncol;
+  const int h = std::min(64, std::max(16, (t.ncol * (R0 / 2) + 15) / 16 * 16));
+  const size_t shm = 2 * size_t(t.ncol) * size_t(R0) * sizeof(T);
+  if (shm > (size_t(64) << 10)) return hipErrorInvalidValue;  // beside the 64 KiB table and the exchange buffers
+  if (L.profiled)
+    hipLaunchKernelGGL((k_tr_eval_pool_tail_q<T, 1>), dim3(grid), dim3(8 * h), shm, L.stream, t);
+  else
+    hipLaunchKernelGGL((k_tr_eval_pool_tail_q<T, 0>), dim3(grid), dim3(8 * h), shm, L.stream, t);
+  return hipGetLastError();
+}
+
+template <typename T>
 hipError_t launch_tr_eval2(const Launch &L, const TrLayout &lay, const TrLayout &lay2, const uint8_t *k0,
                            const uint8_t *k1, const T *xhat, const T *bias, int bias_ncol, T *out) {
   if (lay.bw != int(8 * sizeof(T)) || lay2.bw != lay.bw || lay2.N != lay.N) return hipErrorInvalidValue;
@@ -944,6 +1072,8 @@ hipError_t launch_tr_expand(const Launch &L, const TrLayout &lay, const uint8_t 
                                         const T *, const T *, int, T *);                                              \
   template hipError_t launch_tr_eval_pool<T>(const Launch &, const TrLayout &, const uint8_t *, const uint8_t *, int, \
                                              int, int, const T *, T *);                                               \
+  template hipError_t launch_tr_eval_pool_tail<T>(const Launch &, const TrLayout *, int, const uint8_t *,           \
+                                                  const uint8_t *, int, int, int, const T *, T *);                    \
   template hipError_t launch_tr_eval2<T>(const Launch &, const TrLayout &, const TrLayout &, const uint8_t *,         \
                                          const uint8_t *, const T *, const T *, int, T *);                            \
   template hipError_t launch_tr_party_bits<T>(const Launch &, const TrLayout &, const uint8_t *, const T *,           \

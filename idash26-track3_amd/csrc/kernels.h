@@ -50,6 +50,10 @@ struct Launch {
   // the dealer's 16-byte key (dealer_key): set, or the seed alone
   bool has_dealer_key = false;
   uint8_t dealer_key[16] = {};
+  // Model lanes of a few samples run the max-pool levels from this index on
+  // (0 = the first level) in one launch (launch_tr_eval_pool_tail); -1: every
+  // level alone.
+  int pool_tail = 2;
   // -1: two-party kernels evaluate both parties (blockIdx.y = party).  0 or 1:
   // only that party (one process per party): the launchers take the party's own
   // key (and input share, message buffer) in both party slots and launch one
@@ -112,6 +116,16 @@ hipError_t launch_tr_eval(const Launch &L, const TrLayout &lay, const uint8_t *k
 template <typename T>
 hipError_t launch_tr_eval_pool(const Launch &L, const TrLayout &lay, const uint8_t *k0, const uint8_t *k1, int B,
                                int R, int C, const T *V, T *Vn);
+
+// The last nlev levels of the max-pool tree in one launch: lay[l] is level l's
+// gate (one RELU kind, N = B (R_l/2) C with R_0 = R0 and R_{l+1} = R_l/2 +
+// R_l%2, ending at one row), the keys of every level relative to k0 / k1; V
+// holds B blocks of R0 rows of C words, out receives B rows of C words (each
+// column's maximum).  Each workgroup takes whole columns and keeps them in LDS
+// across the levels (quad-lane gates, both parties).  B R0 C < 2^31.
+template <typename T>
+hipError_t launch_tr_eval_pool_tail(const Launch &L, const TrLayout *lay, int nlev, const uint8_t *k0,
+                                   const uint8_t *k1, int B, int R0, int C, const T *V, T *out);
 
 // Two gates of the same element count in one launch: lay on xhat (with the
 // bias), then lay2 on lay's revealed output, which never leaves the launch;

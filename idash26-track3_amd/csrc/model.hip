@@ -171,8 +171,10 @@ struct Runner {
   Peer *peer = nullptr;
   // Gates of at most pair_max elements share a launch with the next gate of
   // their truncation (tr2: keys resident, both parties here), and max-pool
-  // levels of at most pool_max pairs run as one launch (pool_level).
+  // levels of at most pool_max pairs run as one launch (pool_level); with
+  // pool_tail, the levels from the third on run in one launch together.
   size_t pair_max = 0, pool_max = 0;
+  bool pool_tail_on = false;
 
   Runner(const Launch &L_, int bw_, int s_, Workspace<T> &ws_, Counters &ctr_, Phase1Timer *t, KeySource &src_,
          Peer *peer_ = nullptr)
@@ -367,6 +369,40 @@ struct Runner {
     ctr.bitplanes(n, int(lay.use_a) + int(lay.use_b));
     ctr.msg(n, bw);
     leave(end);
+    return hipSuccess;
+  }
+
+  // The last nlev levels of the max-pool tree (pairs[l] pairs per block at
+  // level l, R0 rows at the first) in one launch: every workgroup takes whole
+  // columns through all of them (resident keys, both parties here); the same
+  // keys, exchanges and counted bytes as nlev pool_level calls.
+  hipError_t pool_tail(int kind, int B, int R0, int C, const T *V, int nlev, const int *pairs, T *out) {
+    if (nlev < 1 || nlev > 8) return hipErrorInvalidValue;
+    TrLayout lay[8];
+    KeyView kv0;
+    size_t n_all = 0;
+    for (int l = 0; l < nlev; l++) {
+      const size_t n = size_t(B) * pairs[l] * C;
+      const size_t end = tr_layout(kind, bw, s, n, c.off).end;
+      size_t b;
+      TRY(enter(end, &b));
+      if (l == 0)
+        kv0 = kv;
+      else if (kv.k[0] != kv0.k[0] || kv.k[1] != kv0.k[1] || kv.begin != kv0.begin)
+        return hipErrorInvalidValue;  // the levels' keys must sit in one view
+      lay[l] = tr_layout(kind, bw, s, n, b);
+      leave(end);
+      n_all += n;
+    }
+    hipEvent_t e0 = nullptr, e1 = nullptr;
+    Launch L1 = L;
+    TRY(time_begin(&e0, &e1, &L1));
+    TRY(launch_tr_eval_pool_tail<T>(L1, lay, nlev, kv0.k[0], kv0.k[1], B, R0, C, V, out));
+    TRY(time_end(e0, e1, n_all, tr_levels(lay[0]), tr_key_bytes(lay[0])));
+    for (int l = 0; l < nlev; l++) {
+      ctr.bitplanes(lay[l].N, int(lay[l].use_a) + int(lay[l].use_b));
+      ctr.msg(lay[l].N, bw);
+    }
     return hipSuccess;
   }
 
@@ -1626,6 +1662,7 @@ class Model final : public ModelBase, KeySource {
     const size_t small = few ? SIZE_MAX : kFuseSmallN;
     r.pair_max = !streaming_ && party_ < 0 ? small : 0;
     r.pool_max = small;
+    r.pool_tail_on = few && !streaming_ && party_ < 0 && L_.pool_tail >= 0;
     auto pub_gemm = [&](const T *x, int l, size_t rows, T *y) -> hipError_t {
       int in, out;
       layer_io(l, &in, &out);
@@ -1676,6 +1713,12 @@ class Model final : public ModelBase, KeySource {
     int R = N;
     for (int l = 0; l < Lv; l++) {
       const int pr = pairs[l];
+      if (r.pool_tail_on && l == L_.pool_tail && Lv - l >= 2) {  // the latency-bound levels: one launch
+        TRY(r.pool_tail(pool_kind(), B, R, C, cur, Lv - l, pairs + l, nxt));
+        std::swap(cur, nxt);
+        R = 1;
+        break;
+      }
       TRY(r.pool_level(pool_kind(), B, R, C, cur, Z, XW, nxt));
       std::swap(cur, nxt);
       R = pr + (R & 1);

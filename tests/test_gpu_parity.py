@@ -639,13 +639,17 @@ def _tr_launches(dims, n):
     """DCF-evaluation launches of one exact forward of a lane of n samples with
     resident keys and both parties in one process: a lane of at most 8 samples
     (latency-bound) runs every truncation (TRMOD with its EXT or EXTRELU) as one
-    launch, one fewer per truncation than there are gates; larger lanes pair
-    only the truncations of at most 65536 elements (the fully connected layers
-    here)."""
+    launch, one fewer per truncation than there are gates, and its max-pool
+    levels from the third on in one launch; larger lanes pair only the
+    truncations of at most 65536 elements (the fully connected layers here)."""
     sizes = [n * dims.n_nodes * f for f in dims.gcn for _ in range(2)]
     sizes += [n * w for w in dims.dfc] + [n * w for w in dims.fus[:-1]]
     assert len(sizes) == 6 + 2 + len(dims.fus) - 1
-    return _tr_gates(dims) - sum(1 for e in sizes if n <= 8 or e <= 65536)
+    R, levels = dims.n_nodes, 0
+    while R > 1:
+        R, levels = R // 2 + (R & 1), levels + 1
+    tail = levels - 2 if n <= 8 and levels - 2 >= 2 else 0  # levels 3.. in one launch
+    return _tr_gates(dims) - sum(1 for e in sizes if n <= 8 or e <= 65536) - max(tail - 1, 0)
 
 
 @pytest.mark.parametrize("bw,B,lanes", [(32, 5, 2), (64, 4, 3), (32, 2, 4), (32, 10, 1), (32, 16, 2)])
