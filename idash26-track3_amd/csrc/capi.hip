@@ -422,6 +422,13 @@ size_t mpcx_tr_key_bytes(mpcx_ctx *c, int kind, size_t n) {
   return tr_layout(kind, c->bw, c->s, n, 0).end;
 }
 
+int mpcx_tr_eval_form(const mpcx_ctx *c, int kind, size_t n) {
+  if (!c || !valid_kind(kind) || kind == MPCX_LOCALARS) return -1;
+  static_assert(MPCX_FORM_ONE_LANE == kFormOneLane && MPCX_FORM_BOTH == kFormBoth && MPCX_FORM_QUAD == kFormQuad,
+                "form codes");
+  return tr_eval_form(c->L, tr_layout(kind, c->bw, c->s, n, 0));
+}
+
 int mpcx_tr_aes_calls(const mpcx_ctx *c, int kind) {
   if (!c || !valid_kind(kind)) return -1;
   const TrLayout lay = tr_layout(kind, c->bw, c->s, 1, 0);

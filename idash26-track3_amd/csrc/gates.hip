@@ -799,11 +799,24 @@ static int both_block(const Launch &L, const TrArgs<T> &a) {
   return a.N >= size_t(L.num_cu) * size_t(L.both_min) ? 1024 : 0;
 }
 
+// The kernel form of a gate evaluation outside the max-pool form: the
+// quad-lane form, the both-party form, or the one-lane kernel.
+template <typename T>
+static int tr_form(const Launch &L, const TrArgs<T> &a) {
+  if (use_quad(L, a.N)) return kFormQuad;
+  if constexpr (sizeof(T) == 4)
+    if (both_block(L, a)) return kFormBoth;
+  return kFormOneLane;
+}
+int tr_eval_form(const Launch &L, const TrLayout &lay) {
+  return lay.bw == 32 ? tr_form<uint32_t>(L, tr_args<uint32_t>(lay)) : tr_form<uint64_t>(L, tr_args<uint64_t>(lay));
+}
+
 // One gate evaluation of both parties with prepared arguments: the regular
 // kernels, or (q set) their max-pool form.
 template <typename T>
 static hipError_t tr_eval_launch(const Launch &L, const TrArgs<T> &a, const TrPool<T> *q) {
-  if (use_quad(L, a.N)) {
+  if (tr_form(L, a) == kFormQuad) {
     const dim3 grid(quad_grid(a.N)), block(kQuadBlock);
     if (q && L.profiled)
       hipLaunchKernelGGL((k_tr_eval_pool_q<T, 1>), grid, block, 0, L.stream, a, *q);
@@ -818,7 +831,7 @@ static hipError_t tr_eval_launch(const Launch &L, const TrArgs<T> &a, const TrPo
   return with_variant(L, [&](auto v) {
     constexpr int NT = decltype(v)::nt, REP = decltype(v)::rep;
     if constexpr (sizeof(T) == 4) {
-      const int block = q ? 0 : both_block(L, a);
+      const int block = !q && tr_form(L, a) == kFormBoth ? both_block(L, a) : 0;
       if (block) {
         const int grid = grid_for(k_tr_eval_b<T, NT, REP, 0>, block, a.N, L.num_cu);
         if (L.profiled)

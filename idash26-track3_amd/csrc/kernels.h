@@ -100,6 +100,10 @@ hipError_t launch_tr_keygen(const Launch &L, const TrLayout &lay, uint64_t seed,
 template <typename T>
 hipError_t launch_tr_expand(const Launch &L, const TrLayout &lay, const uint8_t party_key16[16], uint32_t gate,
                             int party, uint8_t *key);
+// The kernel form launch_tr_eval takes for a gate on this launch configuration
+// (the same decision the launcher makes).
+constexpr int kFormOneLane = 0, kFormBoth = 1, kFormQuad = 2;
+int tr_eval_form(const Launch &L, const TrLayout &lay);
 // Evaluation of a truncation-family gate by both parties in one launch: the DCF
 // walks, the exchange of the masked DCF output bits, the output messages and
 // their sum, the revealed output yhat (N words; may alias xhat).

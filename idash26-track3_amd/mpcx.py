@@ -56,6 +56,7 @@ _SIGS = {
                                             C.c_void_p, C.c_void_p]),
     "mpcx_tr_key_bytes": (C.c_size_t, [C.c_void_p, C.c_int, C.c_size_t]),
     "mpcx_tr_aes_calls": (C.c_int, [C.c_void_p, C.c_int]),
+    "mpcx_tr_eval_form": (C.c_int, [C.c_void_p, C.c_int, C.c_size_t]),
     "mpcx_tr_keygen": (C.c_int, [C.c_void_p, C.c_int, C.c_size_t, C.c_void_p, C.c_void_p, C.c_uint64,
                                  C.c_uint32, C.c_void_p, C.c_void_p]),
     "mpcx_tr_eval": (C.c_int, [C.c_void_p, C.c_int, C.c_size_t, C.c_void_p, C.c_void_p, C.c_void_p,
@@ -230,6 +231,10 @@ class Ctx:
 
     def set_aes_variant(self, v, block=0):
         self.check(self.lib.mpcx_set_aes_variant(self.h, v, block), "set_aes_variant")
+
+    def tr_eval_form(self, kind, n):
+        """Kernel form of tr_eval on n elements: 0 one-lane, 1 both-party, 2 quad-lane."""
+        return int(self.lib.mpcx_tr_eval_form(self.h, kind, n))
 
     def set_both_party_aes(self, max_aes):
         """Longest gate (AES calls per element and party) evaluated in the

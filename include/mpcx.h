@@ -180,6 +180,16 @@ size_t mpcx_tr_key_bytes(mpcx_ctx *ctx, int kind, size_t n);
  * (the reference's Stats counts time only); 0 for MPCX_LOCALARS, -1 for a bad
  * kind. */
 int mpcx_tr_aes_calls(const mpcx_ctx *ctx, int kind);
+/* The kernel form mpcx_tr_eval takes for n elements of a gate kind on this
+ * context and its settings (mpcx_set_both_party_aes, mpcx_set_aes_variant):
+ * the one-lane kernel, the both-party form (one thread per element runs both
+ * parties' DCF walks) or the quad-lane form (four lanes per element and party);
+ * -1 for a bad kind or MPCX_LOCALARS.  No counterpart in the reference: a query
+ * for tests and tuning. */
+#define MPCX_FORM_ONE_LANE 0
+#define MPCX_FORM_BOTH 1
+#define MPCX_FORM_QUAD 2
+int mpcx_tr_eval_form(const mpcx_ctx *ctx, int kind, size_t n);
 mpcx_status mpcx_tr_keygen(mpcx_ctx *ctx, int kind, size_t n, const void *d_in_mask,
                            void *d_out_mask, uint64_t seed, uint32_t gate, void *d_key0,
                            void *d_key1);

@@ -198,19 +198,33 @@ def test_split_truncation_keys_and_eval(ctx, orc, relu):
     assert np.array_equal(signed(y2.astype(np.uint64) - or2, bw), _tr_expected(2 if relu else 1, x, bias))
 
 
+def _num_cu():
+    import torch
+    return torch.cuda.get_device_properties(0).multi_processor_count
+
+
 @pytest.mark.parametrize("form", ["auto", "block512"])
-@pytest.mark.parametrize("n", [1, 63, 64, 65, 255, 256, 257, 511, 513, 1023, 1025, 16384, 16385, 40000])
+@pytest.mark.parametrize("n", [1, 63, 64, 65, 255, 256, 257, 511, 513, 1023, 1025, "quad", "quad+1", 40000])
 def test_gate_tile_edges(ctx, mp, orc, n, form):
     """One gate launch takes tiles of elements, both parties' threads per tile:
     element counts around the wave and tile sizes give the oracle's outputs
     (EXTRELU after TRMOD, so both DCF widths and both exchanges run).  "auto"
-    takes the default forms -- up to 64 elements per CU (16384 on 256 CUs) the
-    quad-lane kernel with 32-element tiles, above it about one workgroup per CU --
-    and "block512" pins the variant's 512-thread workgroups (256-element tiles,
-    one lane per element)."""
+    takes the default forms -- up to 64 elements per CU ("quad": 64 times the
+    device's CU count) the quad-lane kernel with 32-element tiles, above it
+    ("quad+1") about one workgroup per CU -- and "block512" pins the variant's
+    512-thread workgroups (256-element tiles, one lane per element); the form
+    each case runs is asserted."""
     if form == "block512":
         ctx = mp.Ctx(bw=ctx.bw)
         ctx.set_aes_variant(0, 512)
+    quad_max = 64 * _num_cu()
+    n = quad_max if n == "quad" else quad_max + 1 if n == "quad+1" else n
+    if form == "block512":
+        assert ctx.tr_eval_form(12, n) == ctx.tr_eval_form(14, n) == 0
+    elif n <= quad_max:
+        assert ctx.tr_eval_form(12, n) == ctx.tr_eval_form(14, n) == 2
+    else:
+        assert ctx.tr_eval_form(14, n) == 0
     bw = ctx.bw
     rng = np.random.default_rng(n + bw)
     h = 1 << (bw - 1)
@@ -229,21 +243,59 @@ def test_gate_tile_edges(ctx, mp, orc, n, form):
         ctx.close()
 
 
-@pytest.mark.parametrize("kind,n", [(4, 300007), (9, 300007), (15, 300007), (13, 300007), (14, 262144),
-                                    (14, 300007)])
-def test_gate_both_party_form(ctx, mp, orc, kind, n):
-    """At bw=32 a launch of at least 1024 elements per CU (262144 on 256 CUs) of a
-    gate of at most mpcx_set_both_party_aes AES calls per element and party (set
-    to 14 here: TRSLACK, RELUSLACK, RELUPOOL, TRMOD, EXT, EXTRELU) runs the
-    both-party form: one thread per element holds both parties' keys, runs the
-    two DCF walks side by side and adds the two messages.  Outputs identical to
-    the oracle's, on one whole grid pass and on a count past it (a ragged second
-    pass), and the unmasked result as the plaintext gate gives it (bw=64 runs the
-    same cases on the one-lane kernel)."""
+@pytest.mark.parametrize("kind,size", [(4, "ragged"), (9, "ragged"), (15, "ragged"), (13, "ragged"), (14, "whole"),
+                                       (14, "ragged")])
+def test_gate_both_party_form(ctx, mp, orc, kind, size):
+    """At bw=32 a launch of at least 1024 elements per CU ("whole": 1024 times the
+    device's CU count) of a gate of at most mpcx_set_both_party_aes AES calls per
+    element and party (set to 14 here: TRSLACK, RELUSLACK, RELUPOOL, TRMOD, EXT,
+    EXTRELU) runs the both-party form: one thread per element holds both
+    parties' keys, runs the two DCF walks side by side and adds the two
+    messages.  Outputs identical to the oracle's, on one whole grid pass and on
+    a count past it ("ragged": a partial second pass), and the unmasked result
+    as the plaintext gate gives it (bw=64 runs the same cases on the one-lane
+    kernel); the form is asserted."""
+    n = 1024 * _num_cu() + (37751 if size == "ragged" else 0)
     c = mp.Ctx(bw=ctx.bw)
     try:
         c.set_both_party_aes(14)
+        for k in ((12, kind) if kind in (13, 14) else (kind,)):
+            assert c.tr_eval_form(k, n) == (1 if ctx.bw == 32 else 0), k
         _both_party_case(c, mp, orc, kind, n)
+    finally:
+        c.close()
+
+
+@pytest.mark.parametrize("kind,variant", [(1, 0), (2, 0), (3, 0), (11, 0), (3, 1), (2, 3)])
+def test_gate_both_party_every_kind(ctx, mp, orc, kind, variant):
+    """The both-party form for the longest gates, with mpcx_set_both_party_aes(64)
+    (every gate qualifies): TR and TRRELU (both DCF planes in one thread), the
+    full-width RELU, DRELU (party 0's message carries the public bit), on the
+    default T0/T1 table and on the other AES table layouts (variants 1 and 3,
+    whose both-party walks hash the two parties' seeds one after the other);
+    bit-exact against the oracle at bw=32 (bw=64 runs the one-lane kernel)."""
+    n = 1024 * _num_cu() + 4099
+    c = mp.Ctx(bw=ctx.bw)
+    try:
+        c.set_aes_variant(variant)
+        c.set_both_party_aes(64)
+        assert c.tr_eval_form(kind, n) == (1 if ctx.bw == 32 else 0)
+        if kind == 11:
+            bw = c.bw
+            rng = np.random.default_rng(bw + 11)
+            h = 1 << (bw - 1)
+            x = np.concatenate([np.array([-h, -1, 0, 1, h - 1], np.int64),
+                                rng.integers(-h, h, size=n - 5, dtype=np.int64)])
+            rin = rmask(rng, n, bw)
+            o0, o1, kap = orc.tr_keygen(7, 53, 11, bw, S, rin)
+            xhat = (x.astype(np.uint64) + rin) & M(bw)
+            y = c.tr_eval(11, mp.to_dev(o0), mp.to_dev(o1), xhat)
+            oy, _ = orc.tr_eval(11, bw, S, o0, o1, xhat)
+            assert np.array_equal(y.astype(np.uint64), oy)
+            assert np.array_equal((y.astype(np.uint64) ^ kap.astype(np.uint64)) & np.uint64(1),
+                                  (x >= 0).astype(np.uint64))
+        else:
+            _both_party_case(c, mp, orc, kind, n)
     finally:
         c.close()
 
@@ -269,8 +321,8 @@ def _both_party_case(ctx, mp, orc, kind, n):
     rin = rmask(rng, x.size, bw)
     o0, o1, orout = orc.tr_keygen(7, 52, kind, bw, S, rin)
     xhat = (x.astype(np.uint64) + rin) & M(bw)
-    y = ctx.tr_eval(kind, mp.to_dev(o0), mp.to_dev(o1), xhat)
-    oy, _ = orc.tr_eval(kind, bw, S, o0, o1, xhat)
+    y = ctx.tr_eval(kind, mp.to_dev(o0), mp.to_dev(o1), xhat, bias)
+    oy, _ = orc.tr_eval(kind, bw, S, o0, o1, xhat, None if bias is None else np.resize(bias, x.size))
     assert np.array_equal(y.astype(np.uint64), oy)
     assert np.array_equal(signed(y.astype(np.uint64) - orout, bw), _tr_expected(kind, x, bias))
 
@@ -401,9 +453,13 @@ def test_mul_keys_and_eval(ctx, orc):
 
 
 def test_mul_and_reveal_in_place(ctx, orc, mp):
-    """Outputs that overlap an input (the product over its own x^ buffer, the
-    reveal over party 0's share) take the message path and give the same values:
-    the one-launch evaluation writes outputs while other threads gather inputs."""
+    """Through the C ABI, outputs that overlap an input (the product over its own
+    x^ buffer, the reveal over party 0's share) give the same values: the C-ABI
+    calls always take the message path (messages, then the reconstruction), so
+    no thread writes an output while others still gather inputs.  The model's
+    own choice between that path and the one-launch evaluation (by whether the
+    output overlaps an input) is covered by the model parity tests, whose
+    products and reveals write disjoint buffers."""
     bw = ctx.bw
     rng = np.random.default_rng(bw + 5)
     nx, ny, nz = 3000, 200, 2500
