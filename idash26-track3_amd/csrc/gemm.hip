@@ -1092,6 +1092,161 @@ __global__ __launch_bounds__(64 * RW, (pan_waves<T, RW, NT>())) void k_panels(Pa
   }
 }
 
+// k_panels for Z_2^32 with K within one step (K <= kPanKPW words) and at
+// least two panels, software-pipelined across the panels: panel p + 1's B
+// groups are loaded as soon as panel p's B is in LDS, its A groups as soon as
+// panel p's MFMAs have read theirs (under the fold, the barrier and the next
+// B staging), and the epilogue's Cin words before the last panel's products.
+// A wave's chain (its products and the digit work beside them issue in turn)
+// sets a workgroup's time whatever the load on its SIMD, so a launch costs
+// about one chain per round of resident workgroups: two waves per SIMD hold
+// two workgroups of three or four waves per CU, and the launcher picks the
+// columns per workgroup (16, 32 or 48) that give the fewest rounds times chain
+// length (22 graphs of 140 x 140 x 312: 462 workgroups of 48 columns, one
+// round, against 660 of 32 in two).
+template <int NP, int RW, int NT>
+__global__ __launch_bounds__(64 * RW, 2) void k_panels_pf(PanelArgs<uint32_t> g) {
+  using T = uint32_t;
+  constexpr int KT = kPanKPW, NTH = 64 * RW, TN = 16 * NT, NQ = 4, NC = KT / 16, WPG = 4;
+  constexpr int LDK = KT + 4;                     // 32-bit words per LDS row (one column of B)
+  constexpr int GPR = TN / WPG;                   // 16-byte groups per B row of the tile
+  constexpr int NB = (KT * GPR + NTH - 1) / NTH;  // B groups per thread
+  static_assert(NP >= 2 && NP <= 3, "pipelined across two or three panels");
+  __shared__ __align__(16) uint32_t Bt[TN * LDK];  // B of a panel as [n][k] digits
+  __builtin_amdgcn_s_setprio(2);
+  const int M = g.M, N = g.N, K = g.K;
+  const int gx = (N + TN - 1) / TN, gy = (M + 16 * RW - 1) / (16 * RW);
+  const int lw = xcd_swizzle(int(blockIdx.x), int(gridDim.x));
+  const int bz = lw / (gx * gy), m0 = (lw / gx) % gy * 16 * RW, n0 = lw % gx * TN;
+  const int tid = int(threadIdx.x), lane = tid & 63, wave = tid >> 6, li = lane & 15, lg = lane >> 4;
+  const int arow = m0 + 16 * wave + li;
+  const bool wave_ok = m0 + 16 * wave < M;
+  const size_t abytes = size_t(M) * K * sizeof(T), bbytes = size_t(K) * N * sizeof(T);
+  const uint32_t arow_off = arow < M ? uint32_t(arow) * uint32_t(K) * uint32_t(sizeof(T)) : kPanOob;
+  const int kfull = K / (4 * WPG);  // chunks whose 16 words are all inside K
+  const int nkc = (K + 15) / 16;    // chunks holding any word of K
+  const bool ma = g.a2[0] != nullptr, mb = g.b2[0] != nullptr;  // masks: panel 0 only
+  const uint4 z4 = make_uint4(0u, 0u, 0u, 0u);
+
+  // operands of panel p (p and the mask flags fold after unrolling)
+  auto load_b = [&](int p, uint4(&xb)[NB], uint4(&yb)[NB]) {
+    const __amdgpu_buffer_rsrc_t rb1 = pan_rsrc(g.b1[p] + size_t(bz) * g.sB, bbytes);
+    const __amdgpu_buffer_rsrc_t rb2 = pan_rsrc(p == 0 && mb ? g.b2[0] + size_t(bz) * g.sB : g.b1[p], bbytes);
+#pragma unroll
+    for (int j = 0; j < NB; j++) {
+      const int f = tid + NTH * j, kr = f / GPR, q = f % GPR, n = n0 + q * WPG;
+      const uint32_t off = (f < KT * GPR && kr < K && n < N) ? (uint32_t(kr) * uint32_t(N) + uint32_t(n)) * 4u : kPanOob;
+      xb[j] = pan_load(rb1, off);
+      if (p == 0 && mb) yb[j] = pan_load(rb2, off);
+    }
+  };
+  auto load_a = [&](int p, uint4(&xa)[NC], uint4(&ya)[NC]) {
+    const __amdgpu_buffer_rsrc_t ra1 = pan_rsrc(g.a1[p] + size_t(bz) * g.sA, abytes);
+    const __amdgpu_buffer_rsrc_t ra2 = pan_rsrc(p == 0 && ma ? g.a2[0] + size_t(bz) * g.sA : g.a1[p], abytes);
+    const uint32_t abase = arow_off + uint32_t(lg * WPG) * 4u;
+#pragma unroll
+    for (int c = 0; c < NC; c++) {
+      uint32_t off = abase + uint32_t(c) * 64u;
+      if (c >= kfull && (4 * c + lg) * WPG >= K) off = kPanOob;
+      xa[c] = pan_load(ra1, off);
+      if (p == 0 && ma) ya[c] = pan_load(ra2, off);
+    }
+  };
+
+  v4i_t acc[NT][NQ];
+  T vs[NT][4];
+#pragma unroll
+  for (int t = 0; t < NT; t++)
+#pragma unroll
+    for (int r = 0; r < 4; r++) vs[t][r] = 0;
+  uint4 xa[NC], ya[NC], xb[NB], yb[NB];
+#pragma unroll
+  for (int c = 0; c < NC; c++) ya[c] = z4;
+#pragma unroll
+  for (int j = 0; j < NB; j++) yb[j] = z4;
+  load_a(0, xa, ya);
+  load_b(0, xb, yb);
+  T cin[NT][4];
+  T *C = g.C + size_t(bz) * g.sC;
+  const T *c0 = g.cin0 ? g.cin0 + size_t(bz) * g.sC : nullptr, *c1 = g.cin1 ? g.cin1 + size_t(bz) * g.sC : nullptr;
+#pragma unroll
+  for (int p = 0; p < NP; p++) {
+    // panel p's B digits, transposed into the [n][k] rows (one element per write)
+#pragma unroll
+    for (int j = 0; j < NB; j++) {
+      const int f = tid + NTH * j, kr = f / GPR, q = f % GPR;
+      if (f < KT * GPR) {
+        const uint4 d = wide_digits<T>(xb[j], p == 0 ? yb[j] : z4);
+        uint32_t *bp = &Bt[(4 * q) * LDK + kr];
+        bp[0] = d.x;
+        bp[LDK] = d.y;
+        bp[2 * LDK] = d.z;
+        bp[3 * LDK] = d.w;
+      }
+    }
+    if (p + 1 < NP) load_b(p + 1, xb, yb);
+    __syncthreads();
+    if (p == NP - 1) {
+#pragma unroll
+      for (int t = 0; t < NT; t++)
+#pragma unroll
+        for (int r = 0; r < 4; r++) {
+          const int on = n0 + 16 * t + li, om = m0 + 16 * wave + 4 * lg + r;
+          const size_t idx = size_t(om) * N + on;
+          const bool in = om < M && on < N;
+          cin[t][r] = (in && c0 ? c0[idx] : T(0)) + (in && c1 ? c1[idx] : T(0));
+        }
+    }
+#pragma unroll
+    for (int t = 0; t < NT; t++)
+#pragma unroll
+      for (int q = 0; q < NQ; q++) acc[t][q] = v4i_t{0, 0, 0, 0};
+    // one chunk's products: A digits shifted per shift sum, B from LDS
+    auto chunk = [&](int c) {
+      v4i_t as[NQ];
+      digit_shifts<T>(wide_digits<T>(xa[c], p == 0 ? ya[c] : z4), as);
+#pragma unroll
+      for (int t = 0; t < NT; t++) {
+        const uint4 b = *reinterpret_cast<const uint4 *>(&Bt[(16 * t + li) * LDK + 16 * c + 4 * lg]);
+        const v4i_t bv = v4i_t{int(b.x), int(b.y), int(b.z), int(b.w)};
+#pragma unroll
+        for (int q = 0; q < NQ; q++) acc[t][q] = __builtin_amdgcn_mfma_i32_16x16x64_i8(as[q], bv, acc[t][q], 0, 0, 0);
+      }
+    };
+    if (wave_ok) {
+      if (nkc == NC) {
+        // every chunk holds words of K: one basic block, so the scheduler can
+        // put a chunk's digit work beside the previous chunk's MFMAs
+#pragma unroll
+        for (int c = 0; c < NC; c++) chunk(c);
+      } else {
+#pragma unroll
+        for (int c = 0; c < NC; c++)
+          if (c < nkc) chunk(c);
+      }
+    }
+    if (p + 1 < NP) load_a(p + 1, xa, ya);  // the next panel's A into the same registers
+#pragma unroll
+    for (int t = 0; t < NT; t++)
+#pragma unroll
+      for (int r = 0; r < 4; r++) {
+        const T v = digit_fold<T>(acc[t], r);
+        vs[t][r] += g.sign[p] < 0 ? T(0) - v : v;
+      }
+    if (p + 1 < NP) __syncthreads();  // Bt is rewritten by the next panel
+  }
+#pragma unroll
+  for (int t = 0; t < NT; t++) {
+    const int on = n0 + 16 * t + li;
+#pragma unroll
+    for (int r = 0; r < 4; r++) {
+      const int om = m0 + 16 * wave + 4 * lg + r;
+      if (om >= M || on >= N) continue;
+      C[size_t(om) * N + on] = cin[t][r] + vs[t][r];
+    }
+  }
+}
+
 // C[b] = Cin[b] (or 0) before the split-K slices are added
 template <typename T>
 __global__ void k_gemm_init(int M, int N, int batch, size_t sC, const T *Cin, T *C) {
@@ -1239,10 +1394,38 @@ static hipError_t launch_panels_v(const Launch &L, const PanelArgs<T> &r) {
   hipLaunchKernelGGL((k_panels<T, NP, RW, NT>), dim3(unsigned(wgs)), dim3(64 * RW), 0, L.stream, r);
   return hipGetLastError();
 }
+template <int NP, int RW, int NT>
+static hipError_t launch_panels_pf(const Launch &L, const PanelArgs<uint32_t> &r) {
+  const size_t wgs = size_t((r.N + 16 * NT - 1) / (16 * NT)) * size_t((r.M + 16 * RW - 1) / (16 * RW)) * r.batch;
+  if (wgs > size_t(INT32_MAX)) return hipErrorInvalidValue;  // one-dimensional, XCD-ordered launch
+  hipLaunchKernelGGL((k_panels_pf<NP, RW, NT>), dim3(unsigned(wgs)), dim3(64 * RW), 0, L.stream, r);
+  return hipGetLastError();
+}
 template <typename T, int NP>
 static hipError_t launch_panels_np(const Launch &L, const PanelArgs<T> &r) {
   const int rw = pan_rw<T>(r.M);
   const size_t groups = size_t((r.M + 16 * rw - 1) / (16 * rw)) * r.batch;
+  if constexpr (sizeof(T) == 4 && NP >= 2) {
+    if (L.panel_pf && r.K <= kPanKPW) {
+      // 16, 32 or 48 columns per workgroup: the fewest rounds of resident
+      // workgroups (two per CU) times the chain, which grows with the columns
+      // (one step per column tile plus about one for the loads and stagings)
+      int nt = L.panel_nt;
+      if (nt < 1 || nt > 3) {
+        size_t best = SIZE_MAX;
+        for (int t = 1; t <= 3; t++) {
+          const size_t wgs = size_t((r.N + 16 * t - 1) / (16 * t)) * groups, slots = size_t(2) * L.num_cu;
+          const size_t cost = (wgs + slots - 1) / slots * size_t(1 + t);
+          if (cost < best) best = cost, nt = t;
+        }
+      }
+      if (rw == 3)
+        return nt == 1 ? launch_panels_pf<NP, 3, 1>(L, r) : nt == 2 ? launch_panels_pf<NP, 3, 2>(L, r)
+                                                                    : launch_panels_pf<NP, 3, 3>(L, r);
+      return nt == 1 ? launch_panels_pf<NP, 4, 1>(L, r) : nt == 2 ? launch_panels_pf<NP, 4, 2>(L, r)
+                                                                  : launch_panels_pf<NP, 4, 3>(L, r);
+    }
+  }
   if constexpr (sizeof(T) == 4) {
     if (size_t((r.N + 31) / 32) * groups >= size_t(L.num_cu))
       return rw == 3 ? launch_panels_v<T, NP, 3, 2>(L, r) : launch_panels_v<T, NP, 4, 2>(L, r);

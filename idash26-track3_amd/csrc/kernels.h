@@ -44,6 +44,11 @@ struct Launch {
   // 1 = VALU; 2 = tiled matrix-core kernels only.  Z_2^64 products with
   // K >= 2^15 take the VALU path always.
   int gemm = 0;
+  // two- and three-panel Z_2^32 products with K in one step run on the
+  // panel kernel pipelined across panels (k_panels_pf); 0: k_panels
+  int panel_pf = 1;
+  // columns per k_panels_pf workgroup in 16-column tiles (1..3); 0: by rounds
+  int panel_nt = 0;
   // model forwards with resident keys are captured once per batch size into a
   // HIP graph and replayed (0 = enqueue every kernel each time)
   int graph = 1;

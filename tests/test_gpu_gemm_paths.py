@@ -24,9 +24,26 @@ pytestmark = pytest.mark.gpu
 GEMM_SHAPES = [(3080, 78, 78), (3080, 156, 312), (140, 140, 312), (130, 77, 65), (600, 700, 300), (64, 63, 1),
                (1, 1, 1), (22, 256, 1024), (64, 144, 64), (48, 148, 36), (200, 288, 32)]
 # (nb, M, K, N): the affinity model's per-graph products, several masked and
-# unmasked steps over 64 tiles, K not a multiple of the group, tiny
+# unmasked steps over 64 tiles, K not a multiple of the group, tiny; the
+# panel-pipelined kernel (K within one step; 48-column workgroups at
+# 140 x 140 x 312) with 64-row workgroups, K of exactly one step and ragged N
+# on 16-column tiles, with rows past M in a partly used workgroup and K inside
+# one MFMA chunk, and with 64-row workgroups on 32- and 48-column tiles
 SXS_SHAPES = [(22, 140, 140, 78), (22, 140, 140, 312), (22, 140, 140, 156), (64, 33, 300, 40), (3, 70, 66, 37),
-              (5, 100, 148, 64), (2, 5, 63, 3), (1, 1, 1, 1)]
+              (5, 100, 148, 64), (2, 5, 63, 3), (1, 1, 1, 1), (2, 200, 144, 68), (3, 37, 20, 100),
+              (22, 200, 100, 96), (40, 200, 64, 140)]
+
+
+PATHS = ("default", "wide", "tiled")  # the contexts of the ctxs fixture, in order
+
+
+def _check(got, want, path):
+    """Bit-exact, naming the GEMM path and the first differing elements."""
+    got, want = np.asarray(got), np.asarray(want)
+    assert got.shape == want.shape, (path, got.shape, want.shape)
+    bad = np.flatnonzero(got.ravel() != want.ravel())
+    assert bad.size == 0, (f"{path}: {bad.size} of {got.size} differ, first at flat index "
+                           f"{bad[:8].tolist()}: got {got.ravel()[bad[:4]].tolist()} want {want.ravel()[bad[:4]].tolist()}")
 
 
 def _mask(bw):
@@ -76,8 +93,8 @@ def test_ring_gemm_paths(ctxs, orc, shape):
     A = _uniform(rng, M * K, bw).reshape(M, K)
     B = _uniform(rng, K * N, bw).reshape(K, N)
     want = orc.ring_gemm(bw, A, B)
-    for c in cs:
-        assert np.array_equal(c.ring_gemm(A, B).astype(np.uint64), want)
+    for path, c in zip(PATHS, cs):
+        _check(c.ring_gemm(A, B).astype(np.uint64), want, path)
 
 
 @pytest.mark.parametrize("shape", SXS_SHAPES)
@@ -96,8 +113,44 @@ def test_sxs_paths(ctxs, orc, shape):
     ah = (A.ravel().astype(np.uint64) + ra) & _mask(bw)
     bh = (B.ravel().astype(np.uint64) + rb) & _mask(bw)
     _, _, orc_rc = orc.sxs_keygen(4, 2, bw, nb, Mm, K, N, ra, rb)
-    for c in cs:
+    for path, c in zip(PATHS, cs):
         g0, g1, grc = c.sxs_keygen(nb, Mm, K, N, ra, rb, seed=4, gate=2)
-        assert np.array_equal(grc.astype(np.uint64), orc_rc)
+        _check(grc.astype(np.uint64), orc_rc, path + " keygen")
         got = c.sxs_eval(nb, Mm, K, N, g0, g1, ah, bh)
-        assert np.array_equal(_signed(got.astype(np.uint64) - orc_rc, bw).reshape(nb, Mm, N), want)
+        _check(_signed(got.astype(np.uint64) - orc_rc, bw).reshape(nb, Mm, N), want, path)
+
+
+@pytest.mark.parametrize("shape", [(5, 140, 140, 312), (3, 200, 100, 100), (2, 37, 20, 52)])
+def test_sxs_panel_forms(orc, shape):
+    """The three-panel SxS launch (both parties' Beaver products and their sum)
+    in every form, on the same products: the unpipelined panel kernel
+    (MPCX_PANEL_PF=0) and the pipelined one on 16-, 32- and 48-column
+    workgroups (MPCX_PANEL_NT=1..3), each bit-exact against the oracle."""
+    import os
+    import mpcx
+    nb, Mm, K, N = shape
+    rng = np.random.default_rng(nb * Mm + K + N)
+    A = rng.integers(-(1 << 10), 1 << 10, size=(nb, Mm, K))
+    B = rng.integers(-(1 << 10), 1 << 10, size=(nb, K, N))
+    ra, rb = _uniform(rng, A.size, 32), _uniform(rng, B.size, 32)
+    want = np.einsum("bmk,bkn->bmn", A, B)
+    ah = (A.ravel().astype(np.uint64) + ra) & _mask(32)
+    bh = (B.ravel().astype(np.uint64) + rb) & _mask(32)
+    _, _, orc_rc = orc.sxs_keygen(4, 2, 32, nb, Mm, K, N, ra, rb)
+    forms = [("MPCX_PANEL_PF", "0")] + [("MPCX_PANEL_NT", str(t)) for t in (1, 2, 3)]
+    for var, val in forms:
+        old = os.environ.get(var)
+        os.environ[var] = val
+        try:
+            c = mpcx.Ctx(bw=32)
+        finally:
+            if old is None:
+                del os.environ[var]
+            else:
+                os.environ[var] = old
+        try:
+            g0, g1, _ = c.sxs_keygen(nb, Mm, K, N, ra, rb, seed=4, gate=2)
+            got = c.sxs_eval(nb, Mm, K, N, g0, g1, ah, bh)
+            _check(_signed(got.astype(np.uint64) - orc_rc, 32).reshape(nb, Mm, N), want, f"{var}={val}")
+        finally:
+            c.close()
