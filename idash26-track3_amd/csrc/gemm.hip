@@ -515,6 +515,26 @@ __device__ __forceinline__ void digit_shifts(uint4 a, v4i_t (&as)[sizeof(T)]) {
     }
   }
 }
+// digit_shifts for Z_2^32 with the byte selectors in scalar registers (set
+// once per kernel by pan_shift_selectors): VOP3 takes no literal operand, so
+// constant selectors are otherwise rematerialised in vector registers
+struct ShiftSel {
+  uint32_t s[4];
+};
+__device__ __forceinline__ ShiftSel pan_shift_selectors() {
+  ShiftSel r;
+  asm("s_mov_b32 %0, 0x0c0c0c00" : "=s"(r.s[0]));
+  asm("s_mov_b32 %0, 0x0c0c0001" : "=s"(r.s[1]));
+  asm("s_mov_b32 %0, 0x0c000102" : "=s"(r.s[2]));
+  asm("s_mov_b32 %0, 0x00010203" : "=s"(r.s[3]));
+  return r;
+}
+__device__ __forceinline__ void digit_shifts_s(uint4 a, const ShiftSel &sel, v4i_t (&as)[4]) {
+#pragma unroll
+  for (int q = 0; q < 4; q++)
+    as[q] = v4i_t{int(__builtin_amdgcn_perm(0u, a.x, sel.s[q])), int(__builtin_amdgcn_perm(0u, a.y, sel.s[q])),
+                  int(__builtin_amdgcn_perm(0u, a.z, sel.s[q])), int(__builtin_amdgcn_perm(0u, a.w, sel.s[q]))};
+}
 // the ring word of accumulator register r (shift sums acc[q][r])
 template <typename T>
 __device__ __forceinline__ T digit_fold(const v4i_t (&acc)[sizeof(T)], int r) {
@@ -1092,6 +1112,12 @@ __global__ __launch_bounds__(64 * RW, (pan_waves<T, RW, NT>())) void k_panels(Pa
   }
 }
 
+// XOR applied to the word index k of B's LDS row n in k_panels_pf: it flips
+// bits 2-3 only (k stays in its 16-word chunk, 16-byte groups stay whole).
+// With 148-word rows, a wave's one-word column writes (lanes: 4-column groups
+// of a K row, then the next rows) fall on three times fewer bank conflicts,
+// and its 16-byte reads (16 rows, 4 groups) stay conflict-free.
+__device__ __forceinline__ int pf_swz(int n) { return 4 * ((n >> 3) & 3); }
 // k_panels for Z_2^32 with K within one step (K <= kPanKPW words) and at
 // least two panels, software-pipelined across the panels: panel p + 1's B
 // groups are loaded as soon as panel p's B is in LDS, its A groups as soon as
@@ -1127,6 +1153,7 @@ __global__ __launch_bounds__(64 * RW, 2) void k_panels_pf(PanelArgs<uint32_t> g)
   const int nkc = (K + 15) / 16;    // chunks holding any word of K
   const bool ma = g.a2[0] != nullptr, mb = g.b2[0] != nullptr;  // masks: panel 0 only
   const uint4 z4 = make_uint4(0u, 0u, 0u, 0u);
+  const ShiftSel sel = pan_shift_selectors();
 
   // operands of panel p (p and the mask flags fold after unrolling)
   auto load_b = [&](int p, uint4(&xb)[NB], uint4(&yb)[NB]) {
@@ -1171,13 +1198,15 @@ __global__ __launch_bounds__(64 * RW, 2) void k_panels_pf(PanelArgs<uint32_t> g)
   const T *c0 = g.cin0 ? g.cin0 + size_t(bz) * g.sC : nullptr, *c1 = g.cin1 ? g.cin1 + size_t(bz) * g.sC : nullptr;
 #pragma unroll
   for (int p = 0; p < NP; p++) {
-    // panel p's B digits, transposed into the [n][k] rows (one element per write)
+    // panel p's B digits, transposed into the [n][k] rows (one element per
+    // write); word k of row n sits at k ^ pf_swz(n), which spreads a wave's
+    // column writes over the banks and keeps the 16-byte reads contiguous
 #pragma unroll
     for (int j = 0; j < NB; j++) {
       const int f = tid + NTH * j, kr = f / GPR, q = f % GPR;
       if (f < KT * GPR) {
         const uint4 d = wide_digits<T>(xb[j], p == 0 ? yb[j] : z4);
-        uint32_t *bp = &Bt[(4 * q) * LDK + kr];
+        uint32_t *bp = &Bt[(4 * q) * LDK + (kr ^ pf_swz(4 * q))];  // pf_swz is the same for rows 4q .. 4q + 3
         bp[0] = d.x;
         bp[LDK] = d.y;
         bp[2 * LDK] = d.z;
@@ -1204,10 +1233,11 @@ __global__ __launch_bounds__(64 * RW, 2) void k_panels_pf(PanelArgs<uint32_t> g)
     // one chunk's products: A digits shifted per shift sum, B from LDS
     auto chunk = [&](int c) {
       v4i_t as[NQ];
-      digit_shifts<T>(wide_digits<T>(xa[c], p == 0 ? ya[c] : z4), as);
+      digit_shifts_s(wide_digits<T>(xa[c], p == 0 ? ya[c] : z4), sel, as);
 #pragma unroll
       for (int t = 0; t < NT; t++) {
-        const uint4 b = *reinterpret_cast<const uint4 *>(&Bt[(16 * t + li) * LDK + 16 * c + 4 * lg]);
+        const int n = 16 * t + li;
+        const uint4 b = *reinterpret_cast<const uint4 *>(&Bt[n * LDK + ((16 * c + 4 * lg) ^ pf_swz(n))]);
         const v4i_t bv = v4i_t{int(b.x), int(b.y), int(b.z), int(b.w)};
 #pragma unroll
         for (int q = 0; q < NQ; q++) acc[t][q] = __builtin_amdgcn_mfma_i32_16x16x64_i8(as[q], bv, acc[t][q], 0, 0, 0);
