@@ -1047,7 +1047,10 @@ mpcx_status mpcx_peer_pair(int timeout_ms, mpcx_peer **p0, mpcx_peer **p1) {
   *p0 = *p1 = nullptr;
   std::string err;
   Peer *a = nullptr, *b = nullptr;
-  const hipError_t e = guard([&] { return peer_pair(timeout_ms, &a, &b, &err); });
+  // MPCX_PEER_SOCKETPAIR=1: a socket pair, staged as between two processes
+  const char *sp = std::getenv("MPCX_PEER_SOCKETPAIR");
+  const bool sock = sp && std::atoi(sp) != 0;
+  const hipError_t e = guard([&] { return peer_pair(timeout_ms, &a, &b, &err, sock); });
   if (e != hipSuccess) return e == hipErrorOutOfMemory ? MPCX_ENOMEM : MPCX_EIO;
   *p0 = new (std::nothrow) mpcx_peer();
   *p1 = new (std::nothrow) mpcx_peer();

@@ -14,12 +14,15 @@
 #include <condition_variable>
 #include <cstddef>
 #include <cstdint>
+#include <memory>
 #include <mutex>
 #include <string>
 #include <thread>
 #include <vector>
 
 namespace mpcx {
+
+struct LocalLink;  // the shared state of two ends in one process (peer.hip)
 
 class Peer {
  public:
@@ -32,6 +35,9 @@ class Peer {
   };
 
   Peer(int fd, int party);
+  // An end of an in-process pair: messages go device to device (no staging,
+  // no socket), ordered by events on the two parties' streams.
+  Peer(std::shared_ptr<LocalLink> link, int party, int io_timeout_ms);
   ~Peer();
   Peer(const Peer &) = delete;
   Peer &operator=(const Peer &) = delete;
@@ -53,6 +59,7 @@ class Peer {
  private:
   hipError_t ensure(size_t bytes);
   hipError_t ensure_events(size_t n);
+  hipError_t exchange_local(hipStream_t stream, const Seg *segs, int nseg, size_t total);
   void sender_loop();
   bool send_all(const uint8_t *p, size_t n);
   bool recv_all(uint8_t *p, size_t n);
@@ -72,6 +79,10 @@ class Peer {
   const uint8_t *job_ = nullptr;
   size_t job_n_ = 0;
   bool job_ready_ = false, job_done_ = true, job_ok_ = true, stop_ = false;
+  // in-process pair
+  std::shared_ptr<LocalLink> link_;
+  hipEvent_t lev_[2] = {nullptr, nullptr};  // this end's message ready, the peer's message consumed
+  int io_timeout_ms_ = 0;
 };
 
 // Party 0 listens on the Unix socket `path` and accepts one connection; party 1
@@ -79,7 +90,9 @@ class Peer {
 // io_timeout_ms of silence.
 hipError_t peer_connect(int party, const std::string &path, int timeout_ms, int io_timeout_ms, Peer **out,
                         std::string *err);
-// Both ends of a socket pair (two parties as two threads of one process).
-hipError_t peer_pair(int io_timeout_ms, Peer **p0, Peer **p1, std::string *err);
+// Both ends of one channel, for two parties as two threads of one process:
+// linked in memory, each exchange a pair of device-to-device copies ordered by
+// events (socket = true: a socket pair, staged as between processes).
+hipError_t peer_pair(int io_timeout_ms, Peer **p0, Peer **p1, std::string *err, bool socket = false);
 
 }  // namespace mpcx

@@ -14,6 +14,33 @@
 
 namespace mpcx {
 
+// Two ends of one process: each exchange, an end posts its segments and the
+// event recorded after its message on its stream, waits for the peer's post,
+// makes its stream wait for the peer's event and copies the peer's segments
+// into its own receive regions (device to device), then posts an event after
+// those copies and makes its stream wait for the peer's: a party's send
+// regions are not rewritten before the peer has read them.  Both ends pass the
+// second post of a round before either starts the next, so each event is
+// waited on before it is recorded again.
+struct LocalLink {
+  struct End {
+    uint64_t ready = 0, consumed = 0;  // rounds posted
+    const Peer::Seg *segs = nullptr;
+    int nseg = 0;
+    size_t total = 0;
+    hipEvent_t ev_ready = nullptr, ev_consumed = nullptr;
+    bool closed = false;
+  };
+  std::mutex mu;
+  std::condition_variable cv;
+  End end[2];
+};
+
+// (no HIP call here: the pair may be made before the process's first context;
+// the events are created at the first exchange)
+Peer::Peer(std::shared_ptr<LocalLink> link, int party, int io_timeout_ms)
+    : party_(party), link_(std::move(link)), io_timeout_ms_(io_timeout_ms) {}
+
 Peer::Peer(int fd, int party) : fd_(fd), party_(party) {
   // Messages sent inline must fit the socket's send buffer in both directions
   // at once: take a quarter of what the kernel grants (at most kInline).
@@ -26,12 +53,21 @@ Peer::Peer(int fd, int party) : fd_(fd), party_(party) {
 }
 
 Peer::~Peer() {
+  if (link_) {
+    {
+      std::lock_guard<std::mutex> lk(link_->mu);
+      link_->end[party_].closed = true;
+    }
+    link_->cv.notify_all();
+  }
   {
     std::lock_guard<std::mutex> lk(mu_);
     stop_ = true;
   }
   cv_.notify_all();
   if (th_.joinable()) th_.join();
+  for (hipEvent_t e : lev_)
+    if (e) (void)hipEventDestroy(e);
   for (hipEvent_t e : ev_) (void)hipEventDestroy(e);
   if (fd_ >= 0) ::close(fd_);
   if (hs_) (void)hipHostFree(hs_);
@@ -143,6 +179,7 @@ hipError_t Peer::exchange(hipStream_t stream, const Seg *segs, int nseg) {
   for (int k = 0; k < nseg; k++) total += segs[k].bytes;
   rounds_++;
   if (total == 0) return hipSuccess;
+  if (link_) return exchange_local(stream, segs, nseg, total);
   hipError_t e = ensure(total);
   if (e != hipSuccess) return e;
   const size_t nch = (total + kChunk - 1) / kChunk;
@@ -188,6 +225,83 @@ hipError_t Peer::exchange(hipStream_t stream, const Seg *segs, int nseg) {
     err_ = !rok ? "receive from the peer failed (closed or timed out)" : "send to the peer failed";
     return hipErrorNotReady;
   }
+  if (e != hipSuccess) return e;
+  sent_ += total;
+  recv_ += total;
+  return hipSuccess;
+}
+
+hipError_t Peer::exchange_local(hipStream_t stream, const Seg *segs, int nseg, size_t total) {
+  LocalLink &L = *link_;
+  LocalLink::End &me = L.end[party_], &pe = L.end[1 - party_];
+  const uint64_t r = rounds_;
+  for (hipEvent_t &ev : lev_)
+    if (!ev) {
+      const hipError_t ce = hipEventCreateWithFlags(&ev, hipEventDisableTiming);
+      if (ce != hipSuccess) return ce;
+    }
+  auto wait_peer = [&](std::unique_lock<std::mutex> &lk, uint64_t LocalLink::End::*field) {
+    auto ok = [&] { return pe.*field >= r || pe.closed; };
+    if (io_timeout_ms_ > 0) return L.cv.wait_for(lk, std::chrono::milliseconds(io_timeout_ms_), ok) && !pe.closed;
+    L.cv.wait(lk, ok);
+    return !pe.closed;
+  };
+  hipError_t e = hipEventRecord(lev_[0], stream);
+  if (e != hipSuccess) return e;
+  std::vector<Seg> from;
+  hipEvent_t peer_ready = nullptr;
+  {
+    std::unique_lock<std::mutex> lk(L.mu);
+    me.segs = segs;
+    me.nseg = nseg;
+    me.total = total;
+    me.ev_ready = lev_[0];
+    me.ready = r;
+    L.cv.notify_all();
+    // on failure this end closes, so that a late peer does not read `segs`
+    if (!wait_peer(lk, &LocalLink::End::ready)) {
+      broken_ = me.closed = true;
+      err_ = "the peer closed or did not reach the exchange in time";
+      L.cv.notify_all();
+      return hipErrorNotReady;
+    }
+    if (pe.total != total) {
+      broken_ = me.closed = true;
+      err_ = "the peer's message has another length";
+      L.cv.notify_all();
+      return hipErrorNotReady;
+    }
+    from.assign(pe.segs, pe.segs + pe.nseg);  // the peer's array lives until it sees our second post
+    peer_ready = pe.ev_ready;
+  }
+  e = hipStreamWaitEvent(stream, peer_ready, 0);
+  // the peer's send regions into ours, by offset in the message (segments back to back)
+  size_t i = 0, j = 0, oi = 0, oj = 0;
+  while (e == hipSuccess && i < size_t(nseg) && j < from.size()) {
+    const size_t n = std::min(segs[i].bytes - oi, from[j].bytes - oj);
+    if (n) e = hipMemcpyAsync(static_cast<uint8_t *>(segs[i].recv) + oi,
+                              static_cast<const uint8_t *>(from[j].send) + oj, n, hipMemcpyDeviceToDevice, stream);
+    oi += n;
+    oj += n;
+    if (oi == segs[i].bytes) i++, oi = 0;
+    if (oj == from[j].bytes) j++, oj = 0;
+  }
+  if (e == hipSuccess) e = hipEventRecord(lev_[1], stream);
+  hipEvent_t peer_consumed = nullptr;
+  {
+    std::unique_lock<std::mutex> lk(L.mu);
+    me.ev_consumed = lev_[1];
+    me.consumed = r;  // posted even after a failed copy, so that the peer does not wait out its timeout
+    L.cv.notify_all();
+    if (!wait_peer(lk, &LocalLink::End::consumed)) {
+      broken_ = me.closed = true;
+      err_ = "the peer closed or did not finish the exchange in time";
+      L.cv.notify_all();
+      return hipErrorNotReady;
+    }
+    peer_consumed = pe.ev_consumed;
+  }
+  if (e == hipSuccess) e = hipStreamWaitEvent(stream, peer_consumed, 0);
   if (e != hipSuccess) return e;
   sent_ += total;
   recv_ += total;
@@ -272,8 +386,21 @@ hipError_t peer_connect(int party, const std::string &path, int timeout_ms, int 
   return hipSuccess;
 }
 
-hipError_t peer_pair(int io_timeout_ms, Peer **p0, Peer **p1, std::string *err) {
+hipError_t peer_pair(int io_timeout_ms, Peer **p0, Peer **p1, std::string *err, bool socket) {
   *p0 = *p1 = nullptr;
+  if (!socket) {
+    try {
+      auto link = std::make_shared<LocalLink>();
+      *p0 = new Peer(link, 0, io_timeout_ms);
+      *p1 = new Peer(link, 1, io_timeout_ms);
+    } catch (...) {
+      delete *p0;
+      *p0 = nullptr;
+      *err = "out of memory";
+      return hipErrorOutOfMemory;
+    }
+    return hipSuccess;
+  }
   int sv[2];
   if (::socketpair(AF_UNIX, SOCK_STREAM, 0, sv) != 0) {
     *err = std::string("socketpair: ") + std::strerror(errno);

@@ -539,6 +539,7 @@ class Peer:
 
     @staticmethod
     def connect(party, path, timeout_ms=60000):
+        _torch()  # torch's HIP runtime first, as for a context
         lib = load()
         h = C.c_void_p()
         st = lib.mpcx_peer_connect(int(party), os.fsencode(path), int(timeout_ms), C.byref(h))
@@ -549,6 +550,7 @@ class Peer:
     @staticmethod
     def pair(timeout_ms=60000):
         """Both ends of one channel (two parties as two threads of this process)."""
+        _torch()  # torch's HIP runtime first, as for a context
         lib = load()
         a, b = C.c_void_p(), C.c_void_p()
         st = lib.mpcx_peer_pair(int(timeout_ms), C.byref(a), C.byref(b))

@@ -349,7 +349,13 @@ typedef struct mpcx_peer mpcx_peer;
  * gpu_mpc/ddg_orca_base.h:113-114).  timeout_ms bounds the rendezvous and every
  * later receive.  MPCX_EIO if no connection is made. */
 mpcx_status mpcx_peer_connect(int party, const char *path, int timeout_ms, mpcx_peer **out);
-/* Both ends of one channel, for two parties run as two threads of one process. */
+/* Both ends of one channel, for two parties run as two threads of one process.
+ * The ends are linked in memory: an exchange is a device-to-device copy of each
+ * party's message into the other's receive regions, ordered by events on the
+ * two parties' streams (no host staging, no socket); bytes and rounds are
+ * counted as on a socket.  With MPCX_PEER_SOCKETPAIR=1 in the environment the
+ * ends are a socket pair, staged through pinned host memory as between two
+ * processes.  timeout_ms bounds the wait for the peer at each exchange. */
 mpcx_status mpcx_peer_pair(int timeout_ms, mpcx_peer **p0, mpcx_peer **p1);
 void mpcx_peer_close(mpcx_peer *peer);
 int mpcx_peer_party(const mpcx_peer *peer);

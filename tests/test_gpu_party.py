@@ -1,4 +1,5 @@
-"""Party mode: one party per thread or per process, exchanging over a socket,
+"""Party mode: one party per thread or per process, exchanging over a socket
+(or, for two threads, an in-process pair linked in memory),
 as the reference deploys the two parties (gpu_mpc/run_local_2pc.sh:196-233,
 GpuPeer / SigmaPeer in gpu_mpc/utils/gpu_comms.h and sigma_comms.cpp).
 
@@ -37,12 +38,25 @@ def rmask(rng, n, bw):
     return rng.integers(0, np.iinfo(np.uint64).max, size=n, dtype=np.uint64, endpoint=True) & M(bw)
 
 
-def two_parties(bw, fn):
+TRANSPORTS = ["local", "socket"]
+
+
+def two_parties(bw, fn, transport="local"):
     """Runs fn(ctx, peer, party) for both parties on two threads, each with its
-    own context and one end of a socket pair; returns both results and the
-    parties' counted and channel bytes."""
+    own context and one end of an in-process pair: linked in memory (device to
+    device copies, "local") or a socket pair staged through pinned host memory
+    as between processes ("socket", MPCX_PEER_SOCKETPAIR=1); returns both
+    results and the parties' counted and channel bytes."""
     import mpcx
-    p0, p1 = mpcx.Peer.pair(timeout_ms=30000)
+    old = os.environ.get("MPCX_PEER_SOCKETPAIR")
+    os.environ["MPCX_PEER_SOCKETPAIR"] = "1" if transport == "socket" else "0"
+    try:
+        p0, p1 = mpcx.Peer.pair(timeout_ms=30000)
+    finally:
+        if old is None:
+            del os.environ["MPCX_PEER_SOCKETPAIR"]
+        else:
+            os.environ["MPCX_PEER_SOCKETPAIR"] = old
     ctxs = [mpcx.Ctx(bw=bw, scale=S) for _ in range(2)]
 
     def run(party):
@@ -62,12 +76,50 @@ def two_parties(bw, fn):
     return res, wire
 
 
+@pytest.mark.parametrize("transport", TRANSPORTS)
+def test_peer_gone_or_silent(transport):
+    """An exchange with a closed peer fails at once, and with a live peer that
+    never exchanges fails after the pair's timeout; the channel reports why.
+    Both are host-side conditions: the failing end enqueues no wait on the
+    peer's events, so the context stays usable."""
+    import time
+    import mpcx
+    old = os.environ.get("MPCX_PEER_SOCKETPAIR")
+    os.environ["MPCX_PEER_SOCKETPAIR"] = "1" if transport == "socket" else "0"
+    try:
+        a0, a1 = mpcx.Peer.pair(timeout_ms=500)
+        b0, b1 = mpcx.Peer.pair(timeout_ms=500)
+    finally:
+        if old is None:
+            del os.environ["MPCX_PEER_SOCKETPAIR"]
+        else:
+            os.environ["MPCX_PEER_SOCKETPAIR"] = old
+    c = mpcx.Ctx(bw=32, scale=S)
+    v = np.arange(1000, dtype=np.uint32)
+    try:
+        a1.close()
+        t0 = time.perf_counter()
+        with pytest.raises(mpcx.MpcxError):
+            c.party_reconstruct(a0, v)
+        assert time.perf_counter() - t0 < 5
+        t0 = time.perf_counter()
+        with pytest.raises(mpcx.MpcxError):
+            c.party_reconstruct(b0, v)  # b1 is open but never exchanges
+        assert 0.3 < time.perf_counter() - t0 < 10
+        c.sync()  # nothing left waiting on the stream
+    finally:
+        for p_ in (a0, b0, b1):
+            p_.close()
+        c.close()
+
+
 TR_KINDS = [(3, "RELU"), (12, "TRMOD"), (1, "TR"), (2, "TRRELU"), (4, "TRSLACK"), (15, "RELUPOOL"), (11, "DRELU")]
 
 
+@pytest.mark.parametrize("transport", TRANSPORTS)
 @pytest.mark.parametrize("bw", [32, 64])
 @pytest.mark.parametrize("kind,name", TR_KINDS)
-def test_party_tr_gates(bw, kind, name):
+def test_party_tr_gates(bw, kind, name, transport):
     """Every truncation / ReLU kind: the two parties' outputs are identical,
     equal to the one-process evaluation on the same keys, and the channel
     carried exactly the counted bytes."""
@@ -88,7 +140,7 @@ def test_party_tr_gates(bw, kind, name):
     d.reset_counters()
     want = d.tr_eval(kind, k0, k1, xhat, bias)
     want_bytes = d.bytes_exchanged
-    (r0, r1), wire = two_parties(bw, lambda c, pe, p: c.party_tr_eval(pe, kind, (k0, k1)[p], xhat, bias))
+    (r0, r1), wire = two_parties(bw, lambda c, pe, p: c.party_tr_eval(pe, kind, (k0, k1)[p], xhat, bias), transport)
     assert np.array_equal(r0[0], want) and np.array_equal(r1[0], want)
     assert r0[1] == r1[1] == want_bytes
     assert wire[0] == wire[1] == want_bytes
@@ -109,8 +161,9 @@ def test_party_tr_gates(bw, kind, name):
     d.close()
 
 
+@pytest.mark.parametrize("transport", TRANSPORTS)
 @pytest.mark.parametrize("bw", [32, 64])
-def test_party_split_truncation_chain(bw):
+def test_party_split_truncation_chain(bw, transport):
     """TRMOD (with a bias) then EXTRELU, party by party: the exact ReLU of the
     floor, as the one-process chain."""
     import mpcx
@@ -128,7 +181,7 @@ def test_party_split_truncation_chain(bw):
         y = c.party_tr_eval(pe, 12, (g0, g1)[p], xhat, bias)
         return c.party_tr_eval(pe, 14, (q0, q1)[p], y)
 
-    (a, b), wire = two_parties(bw, fn)
+    (a, b), wire = two_parties(bw, fn, transport)
     assert np.array_equal(a[0], b[0])
     want = np.maximum((x + (np.resize(bias, n) << S)) >> S, 0)
     assert np.array_equal(signed(a[0].astype(np.uint64) - r2.astype(np.uint64), bw), want)
@@ -136,8 +189,9 @@ def test_party_split_truncation_chain(bw):
     d.close()
 
 
+@pytest.mark.parametrize("transport", TRANSPORTS)
 @pytest.mark.parametrize("bw", [32, 64])
-def test_party_mul_lut_sxs_reveal(bw):
+def test_party_mul_lut_sxs_reveal(bw, transport):
     """Beaver product, 8-bit DPF table, batched secret x secret GEMM, reveal and
     reconstructInPlace, party by party, against the one-process calls."""
     import mpcx
@@ -181,7 +235,7 @@ def test_party_mul_lut_sxs_reveal(bw):
                 c.party_reveal_eval(pe, (e0, e1)[p], (v0, v1)[p]),
                 c.party_reconstruct(pe, (v0, v1)[p]))
 
-    (a, b), wire = two_parties(bw, fn)
+    (a, b), wire = two_parties(bw, fn, transport)
     for u, w in zip(a[0], b[0]):
         assert np.array_equal(u, w)
     z, ly, cc, vh, vs = a[0]
@@ -203,8 +257,9 @@ def _od(orc, dims):
                          slack=dims.slack)
 
 
+@pytest.mark.parametrize("transport", TRANSPORTS)
 @pytest.mark.parametrize("bw", [32, 64])
-def test_model_party_threads(orc, synth, bw):
+def test_model_party_threads(orc, synth, bw, transport):
     """The affinity forward with the two parties as two threads: each holds its
     key (exported from the dealer's run) and its input shares, party 1 the
     protein embedding; both get the plaintext outputs, and each party counts,
@@ -239,7 +294,7 @@ def test_model_party_threads(orc, synth, bw):
         m.close()
         return outs
 
-    (a, b), wire = two_parties(bw, fn)
+    (a, b), wire = two_parties(bw, fn, transport)
     for outs in (a[0], b[0]):
         for o in outs:
             assert np.array_equal(o, want)
