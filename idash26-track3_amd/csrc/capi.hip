@@ -284,6 +284,12 @@ mpcx_status mpcx_set_stream(mpcx_ctx *c, void *s) {
   return MPCX_OK;
 }
 
+mpcx_status mpcx_set_party_sync(mpcx_ctx *c, int sync) {
+  CHECK_CTX(c);
+  c->L.party_sync = sync != 0 ? 1 : 0;
+  return MPCX_OK;
+}
+
 mpcx_status mpcx_synchronize(mpcx_ctx *c) {
   CHECK_CTX(c);
   HIPC(c, hipStreamSynchronize(c->L.stream), "hipStreamSynchronize");

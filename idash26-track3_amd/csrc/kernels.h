@@ -49,6 +49,9 @@ struct Launch {
   int panel_pf = 1;
   // columns per k_panels_pf workgroup in 16-column tiles (1..3); 0: by rounds
   int panel_nt = 0;
+  // party-mode gate calls synchronise the stream before returning (0: they
+  // return with their work enqueued, for callers that order by stream)
+  int party_sync = 1;
   // model forwards with resident keys are captured once per batch size into a
   // HIP graph and replayed (0 = enqueue every kernel each time)
   int graph = 1;

@@ -2400,7 +2400,8 @@ DevBuf<uint64_t> &party_tmp<uint64_t>(PartyWork &w) {
 }
 
 // One gate of party L.party over its key (laid out from offset 0), messages of
-// nmsg elements; synchronises the stream at the end.
+// nmsg elements; synchronises the stream at the end unless L.party_sync is 0
+// (the output is then ready in the stream's order).
 template <typename T, class Fn>
 hipError_t party_gate(PartyWork **w, const Launch &L, Peer *peer, Counters *ctr, int bw, int s, const uint8_t *key,
                       size_t key_bytes, size_t nmsg, Fn &&fn) {
@@ -2413,7 +2414,7 @@ hipError_t party_gate(PartyWork **w, const Launch &L, Peer *peer, Counters *ctr,
   src.bytes = key_bytes;
   Runner<T> r(L, bw, s, ws, *ctr, nullptr, src, peer);
   TRY(fn(r, **w));
-  return hipStreamSynchronize(L.stream);
+  return L.party_sync ? hipStreamSynchronize(L.stream) : hipSuccess;
 }
 template <typename T>
 const T *cp(const void *p) {

@@ -33,6 +33,7 @@ _SIGS = {
     "mpcx_aes_variant_count": (C.c_int, []),
     "mpcx_aes_variant_name": (C.c_char_p, [C.c_int]),
     "mpcx_set_aes_variant": (C.c_int, [C.c_void_p, C.c_int, C.c_int]),
+    "mpcx_set_party_sync": (C.c_int, [C.c_void_p, C.c_int]),
     "mpcx_set_both_party_aes": (C.c_int, [C.c_void_p, C.c_int]),
     "mpcx_aes_variant": (C.c_int, [C.c_void_p]),
     "mpcx_bytes_exchanged": (C.c_uint64, [C.c_void_p]),
@@ -228,6 +229,18 @@ class Ctx:
 
     def sync(self):
         self.check(self.lib.mpcx_synchronize(self.h), "synchronize")
+
+    def set_party_sync(self, sync):
+        """Party-mode calls synchronise the stream (True, the default) or return
+        with their work enqueued (False: the methods below then synchronise the
+        context themselves before reading their outputs)."""
+        self.check(self.lib.mpcx_set_party_sync(self.h, 1 if sync else 0), "set_party_sync")
+        self._party_async = not sync
+
+    def _party_out(self, t, n):
+        if getattr(self, "_party_async", False):
+            self.sync()
+        return from_dev(t, self.T, n)
 
     def set_aes_variant(self, v, block=0):
         self.check(self.lib.mpcx_set_aes_variant(self.h, v, block), "set_aes_variant")
@@ -462,7 +475,7 @@ class Ctx:
         out = empty_dev(n * xhat.itemsize)
         self.check(self.lib.mpcx_party_tr_eval(self.h, peer.h, kind, n, dptr(key), dptr(dx), dptr(db), ncol,
                                                dptr(out)), "party_tr_eval")
-        return from_dev(out, self.T, n)
+        return self._party_out(out, n)
 
     def party_mul_eval(self, peer, key, xhat, yhat, ia, ib):
         xhat, yhat = self.ring(xhat), self.ring(yhat)
@@ -474,7 +487,7 @@ class Ctx:
         out = empty_dev(nz * xhat.itemsize)
         self.check(self.lib.mpcx_party_mul_eval(self.h, peer.h, xhat.size, yhat.size, nz, dptr(d[0]), dptr(d[1]),
                                                 dptr(key), dptr(dx), dptr(dy), dptr(out)), "party_mul_eval")
-        return from_dev(out, self.T, nz)
+        return self._party_out(out, nz)
 
     def party_lut8_eval(self, peer, key, table, xhat):
         xhat, table = self.ring(xhat), self.ring(table)
@@ -483,7 +496,7 @@ class Ctx:
         out = empty_dev(n * xhat.itemsize)
         self.check(self.lib.mpcx_party_lut8_eval(self.h, peer.h, n, dptr(key), dptr(dt), dptr(dx), dptr(out)),
                    "party_lut8_eval")
-        return from_dev(out, self.T, n)
+        return self._party_out(out, n)
 
     def party_sxs_eval(self, peer, nb, M, K, N, key, ahat, bhat):
         ahat, bhat = self.ring(ahat), self.ring(bhat)
@@ -491,7 +504,7 @@ class Ctx:
         out = empty_dev(nb * M * N * ahat.itemsize)
         self.check(self.lib.mpcx_party_sxs_eval(self.h, peer.h, nb, M, K, N, dptr(key), dptr(da), dptr(db),
                                                 dptr(out)), "party_sxs_eval")
-        return from_dev(out, self.T, nb * M * N)
+        return self._party_out(out, nb * M * N)
 
     def party_reveal_eval(self, peer, key, v):
         v = self.ring(v)
@@ -499,13 +512,13 @@ class Ctx:
         out = empty_dev(v.size * v.itemsize)
         self.check(self.lib.mpcx_party_reveal_eval(self.h, peer.h, v.size, dptr(key), dptr(dv), dptr(out)),
                    "party_reveal_eval")
-        return from_dev(out, self.T, v.size)
+        return self._party_out(out, v.size)
 
     def party_reconstruct(self, peer, v):
         v = self.ring(v)
         dv = to_dev(v)
         self.check(self.lib.mpcx_party_reconstruct(self.h, peer.h, v.size, dptr(dv)), "party_reconstruct")
-        return from_dev(dv, self.T, v.size)
+        return self._party_out(dv, v.size)
 
     # ---------------- adjacency normalisation ----------------
     def set_adjnorm_lanes(self, lanes):

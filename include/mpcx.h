@@ -96,6 +96,14 @@ int mpcx_scale(const mpcx_ctx *ctx);
  * mpcx_model_create; mpcx_synchronize waits for the context's current stream. */
 mpcx_status mpcx_set_stream(mpcx_ctx *ctx, void *hip_stream);
 mpcx_status mpcx_synchronize(mpcx_ctx *ctx);
+/* sync = 0: the party-mode gate calls (mpcx_party_*) return with their work
+ * enqueued on the context's stream instead of synchronising it, for callers
+ * that order by stream (the drop-in headers: the reference's per-call
+ * semantics, gpu_comms.h's synchronous exchanges, are kept by a blocking
+ * stream, on which a later null-stream copy or free waits).  Outputs are then
+ * ready in the stream's order; read them on the host after mpcx_synchronize or
+ * a copy ordered after the stream.  Default 1 (synchronise). */
+mpcx_status mpcx_set_party_sync(mpcx_ctx *ctx, int sync);
 /* AES T-table LDS layout used by the DCF kernels (0 = default).  Returns the
  * number of variants; name of variant i via mpcx_aes_variant_name.
  * block_threads: 0 (the variant's own) or a multiple of 128 in [128, 1024]. */
@@ -343,7 +351,7 @@ mpcx_status mpcx_adjnorm_eval(mpcx_ctx *ctx, int B, int N, int nmax, const void 
  * gate calls below take this party's key (as written by the keygen calls for
  * that party) and its share or the masked public input, and return the
  * reconstructed masked output on both parties; they synchronise the context's
- * stream. */
+ * stream (unless mpcx_set_party_sync(ctx, 0)). */
 typedef struct mpcx_peer mpcx_peer;
 /* Party 0 listens on the Unix socket `path`, party 1 connects (GpuPeer::connect,
  * gpu_mpc/ddg_orca_base.h:113-114).  timeout_ms bounds the rendezvous and every

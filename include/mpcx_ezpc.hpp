@@ -41,8 +41,9 @@
 #include <cstring>
 #include <map>
 #include <mutex>
-#include <set>
 #include <string>
+#include <thread>
+#include <unordered_map>
 #include <utility>
 #include <vector>
 
@@ -128,19 +129,20 @@ struct Runtime {
 // expects.  So no shim call has to wait for its kernels: a later copy or
 // gpuFree of the caller waits for them, and the party-mode exchanges wait for
 // what they send.
+// A thread's contexts share its one stream, so that all of the thread's GPU
+// work (that stream and the null stream) is ordered, which the thread's block
+// cache (dmalloc) relies on.
 struct ThreadContexts {
   struct Entry {
     mpcx_ctx *c = nullptr;
     uint32_t key_epoch = 0;  // the dealer key this context holds (Runtime::key_epoch)
-    hipStream_t stream = nullptr;
   };
   std::map<std::pair<int, int>, Entry> ctx;
+  hipStream_t stream = nullptr;
   ~ThreadContexts() {
-    for (auto &kv : ctx) {
-      (void)hipStreamSynchronize(kv.second.stream);
-      mpcx_destroy(kv.second.c);
-      (void)hipStreamDestroy(kv.second.stream);
-    }
+    if (stream) (void)hipStreamSynchronize(stream);
+    for (auto &kv : ctx) mpcx_destroy(kv.second.c);
+    if (stream) (void)hipStreamDestroy(stream);
   }
 };
 inline mpcx_ctx *ctx(int bw, int scale = 12) {
@@ -151,8 +153,11 @@ inline mpcx_ctx *ctx(int bw, int scale = 12) {
     ThreadContexts::Entry e;
     if (mpcx_create(bw, scale, R.device, &e.c) != MPCX_OK)
       die("mpcx_create(bw " + std::to_string(bw) + ", scale " + std::to_string(scale) + ") failed");
-    hip_check(hipStreamCreateWithFlags(&e.stream, hipStreamDefault), "context stream");
-    if (mpcx_set_stream(e.c, e.stream) != MPCX_OK) die("mpcx_set_stream failed");
+    if (!tc.stream) hip_check(hipStreamCreateWithFlags(&tc.stream, hipStreamDefault), "context stream");
+    if (mpcx_set_stream(e.c, tc.stream) != MPCX_OK) die("mpcx_set_stream failed");
+    // the stream is blocking: the caller's null-stream copies and frees wait
+    // for the party calls' work, so those calls need not synchronise it
+    if (mpcx_set_party_sync(e.c, 0) != MPCX_OK) die("mpcx_set_party_sync failed");
     it = tc.ctx.emplace(std::make_pair(bw, scale), e).first;
   }
   std::lock_guard<std::mutex> lk(R.mu);
@@ -185,16 +190,58 @@ inline uint64_t seed() { return Runtime::get().seed; }
 // no allocation or free waits for the device, as a hipFree would.  A free is
 // ordered after the kernels that use the block because the contexts' streams
 // are blocking streams (ctx()); pointers from elsewhere go to hipFree.
+// Blocks come in size classes (four per power of two from 256 bytes); a block
+// freed by the thread that allocated it stays on that thread's free list and
+// is handed out again with no HIP call: the thread's GPU work is ordered (its
+// contexts' one blocking stream and the null stream), so the block's next work
+// follows its last.  A block freed by another thread goes back to the pool in
+// null-stream order.
 struct Pool {
+  struct Blk {
+    size_t cls;
+    std::thread::id owner;
+  };
   std::mutex mu;
-  std::set<void *> live;
+  std::unordered_map<void *, Blk> live;
   bool ready = false;
   static Pool &get() {
     static Pool p;
     return p;
   }
 };
+inline size_t size_class(size_t b) {
+  if (b <= 256) return 256;
+  size_t p = 256;
+  while (p * 2 <= b) p *= 2;  // p <= b < 2p
+  const size_t step = p / 4;
+  return (b + step - 1) / step * step;
+}
+struct ThreadBlocks {
+  std::unordered_map<size_t, std::vector<void *>> free;  // size class -> blocks
+  ~ThreadBlocks() {
+    Pool &P = Pool::get();
+    for (auto &kv : free)
+      for (void *p : kv.second) {
+        {
+          std::lock_guard<std::mutex> lk(P.mu);
+          P.live.erase(p);
+        }
+        (void)hipFreeAsync(p, nullptr);
+      }
+  }
+};
+inline ThreadBlocks &thread_blocks() {
+  thread_local ThreadBlocks t;
+  return t;
+}
 inline void *dmalloc(size_t bytes) {
+  const size_t cls = size_class(bytes);
+  auto &fl = thread_blocks().free[cls];
+  if (!fl.empty()) {
+    void *p = fl.back();
+    fl.pop_back();
+    return p;
+  }
   Pool &P = Pool::get();
   {
     std::lock_guard<std::mutex> lk(P.mu);
@@ -209,20 +256,29 @@ inline void *dmalloc(size_t bytes) {
     }
   }
   void *p = nullptr;
-  hip_check(hipMallocAsync(&p, bytes ? bytes : 1, nullptr), "gpuMalloc");
+  hip_check(hipMallocAsync(&p, cls, nullptr), "gpuMalloc");
   std::lock_guard<std::mutex> lk(P.mu);
-  P.live.insert(p);
+  P.live[p] = Pool::Blk{cls, std::this_thread::get_id()};
   return p;
 }
 inline void dfree(void *p) {
   if (!p) return;
   Pool &P = Pool::get();
-  bool pooled;
+  bool pooled = false, mine = false;
+  size_t cls = 0;
   {
     std::lock_guard<std::mutex> lk(P.mu);
-    pooled = P.live.erase(p) > 0;
+    auto it = P.live.find(p);
+    if (it != P.live.end()) {
+      pooled = true;
+      cls = it->second.cls;
+      mine = it->second.owner == std::this_thread::get_id();
+      if (!mine) P.live.erase(it);
+    }
   }
-  if (pooled)
+  if (mine)
+    thread_blocks().free[cls].push_back(p);
+  else if (pooled)
     hip_check(hipFreeAsync(p, nullptr), "gpuFree");
   else
     (void)hipFree(p);

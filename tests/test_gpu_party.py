@@ -38,15 +38,17 @@ def rmask(rng, n, bw):
     return rng.integers(0, np.iinfo(np.uint64).max, size=n, dtype=np.uint64, endpoint=True) & M(bw)
 
 
-TRANSPORTS = ["local", "socket"]
+TRANSPORTS = ["local", "socket", "local-async"]
 
 
 def two_parties(bw, fn, transport="local"):
     """Runs fn(ctx, peer, party) for both parties on two threads, each with its
     own context and one end of an in-process pair: linked in memory (device to
-    device copies, "local") or a socket pair staged through pinned host memory
-    as between processes ("socket", MPCX_PEER_SOCKETPAIR=1); returns both
-    results and the parties' counted and channel bytes."""
+    device copies, "local"; "local-async": the party calls also return without
+    synchronising the stream, mpcx_set_party_sync(ctx, 0)) or a socket pair
+    staged through pinned host memory as between processes ("socket",
+    MPCX_PEER_SOCKETPAIR=1); returns both results and the parties' counted and
+    channel bytes."""
     import mpcx
     old = os.environ.get("MPCX_PEER_SOCKETPAIR")
     os.environ["MPCX_PEER_SOCKETPAIR"] = "1" if transport == "socket" else "0"
@@ -58,6 +60,9 @@ def two_parties(bw, fn, transport="local"):
         else:
             os.environ["MPCX_PEER_SOCKETPAIR"] = old
     ctxs = [mpcx.Ctx(bw=bw, scale=S) for _ in range(2)]
+    if transport == "local-async":
+        for c in ctxs:
+            c.set_party_sync(False)
 
     def run(party):
         c = ctxs[party]
@@ -76,7 +81,7 @@ def two_parties(bw, fn, transport="local"):
     return res, wire
 
 
-@pytest.mark.parametrize("transport", TRANSPORTS)
+@pytest.mark.parametrize("transport", ["local", "socket"])
 def test_peer_gone_or_silent(transport):
     """An exchange with a closed peer fails at once, and with a live peer that
     never exchanges fails after the pair's timeout; the channel reports why.
