@@ -248,6 +248,8 @@ mpcx_status mpcx_create(int bw, int scale, int device, mpcx_ctx **out) {
   if (const char *v = std::getenv("MPCX_GRAPH")) c->L.graph = std::atoi(v) != 0 ? 1 : 0;
   if (const char *v = std::getenv("MPCX_POOL_TAIL")) c->L.pool_tail = std::max(-1, std::atoi(v));
   if (const char *v = std::getenv("MPCX_PANEL_PF")) c->L.panel_pf = std::atoi(v) != 0 ? 1 : 0;
+  if (const char *v = std::getenv("MPCX_QUAD_PER_CU")) c->L.quad_per_cu = std::max(64, std::min(256, std::atoi(v)));
+  if (const char *v = std::getenv("MPCX_QUAD_ALONE")) c->L.quad_alone = std::max(64, std::min(256, std::atoi(v)));
   if (const char *v = std::getenv("MPCX_PANEL_NT")) c->L.panel_nt = std::max(0, std::min(3, std::atoi(v)));
   *out = c;
   return MPCX_OK;

@@ -768,15 +768,23 @@ static int tr_eval_block(const Launch &L, size_t n) {
 // lanes take it too: their smallest gates (the last pool levels, two fully
 // connected gates) run at the end of a forward, when the lanes' large gates are
 // done (bw=64, B=64: +1.2-1.7%; bw=32 unchanged).
+// Above 64 elements per CU (up to L.quad_per_cu) the workgroups are of 512
+// threads (64 elements): two still fit a CU (LDS 2 x 68 KiB, 96 VGPRs).
 constexpr int kQuadBlock = 256, kQuadElems = kQuadBlock / 8;
 static bool use_quad(const Launch &L, size_t n) {
   if (L.aes_block != 0) return false;
   int nv;
   const AesVariant *v = aes_variants(&nv);
   const int vi = L.aes_variant >= 0 && L.aes_variant < nv ? L.aes_variant : 0;
-  return v[vi].nt == 2 && v[vi].rep == 32 && n <= size_t(L.num_cu) * 2 * kQuadElems;
+  return v[vi].nt == 2 && v[vi].rep == 32 && n <= size_t(L.num_cu) * size_t(std::max(2 * kQuadElems, L.quad_per_cu));
 }
-static int quad_grid(size_t n) { return int(std::max<size_t>(1, (n + kQuadElems - 1) / kQuadElems)); }
+static int quad_block(const Launch &L, size_t n) {
+  return n <= size_t(L.num_cu) * 2 * kQuadElems ? kQuadBlock : 2 * kQuadBlock;
+}
+static int quad_grid(const Launch &L, size_t n) {
+  const size_t h = size_t(quad_block(L, n) / 8);
+  return int(std::max<size_t>(1, (n + h - 1) / h));
+}
 
 // The both-party form (one thread per element for both parties, 1024-thread
 // workgroups: one per CU at 68 VGPRs, 64 KiB of LDS) for gates of at most
@@ -817,7 +825,7 @@ int tr_eval_form(const Launch &L, const TrLayout &lay) {
 template <typename T>
 static hipError_t tr_eval_launch(const Launch &L, const TrArgs<T> &a, const TrPool<T> *q) {
   if (tr_form(L, a) == kFormQuad) {
-    const dim3 grid(quad_grid(a.N)), block(kQuadBlock);
+    const dim3 grid(quad_grid(L, a.N)), block(quad_block(L, a.N));
     if (q && L.profiled)
       hipLaunchKernelGGL((k_tr_eval_pool_q<T, 1>), grid, block, 0, L.stream, a, *q);
     else if (q)
@@ -952,9 +960,11 @@ hipError_t launch_tr_eval2(const Launch &L, const TrLayout &lay, const TrLayout 
   a.prio = lay.N < kTrPrioN;
   if (use_quad(L, lay.N)) {
     if (L.profiled)
-      hipLaunchKernelGGL((k_tr_eval2_q<T, 1>), dim3(quad_grid(lay.N)), dim3(kQuadBlock), 0, L.stream, a, a2);
+      hipLaunchKernelGGL((k_tr_eval2_q<T, 1>), dim3(quad_grid(L, lay.N)), dim3(quad_block(L, lay.N)), 0, L.stream, a,
+                         a2);
     else
-      hipLaunchKernelGGL((k_tr_eval2_q<T, 0>), dim3(quad_grid(lay.N)), dim3(kQuadBlock), 0, L.stream, a, a2);
+      hipLaunchKernelGGL((k_tr_eval2_q<T, 0>), dim3(quad_grid(L, lay.N)), dim3(quad_block(L, lay.N)), 0, L.stream, a,
+                         a2);
     return hipGetLastError();
   }
   return with_variant(L, [&](auto v) {

@@ -62,6 +62,15 @@ struct Launch {
   // (0 = the first level) in one launch (launch_tr_eval_pool_tail); -1: every
   // level alone.
   int pool_tail = 2;
+  // gates of at most this many elements per CU take the quad-lane form
+  // (at least 64: two 256-thread workgroups per CU; above, 512-thread ones)
+  int quad_per_cu = 64;
+  // the same in a model lane that runs alone (ModelBase::set_alone): gates of
+  // up to 192 elements per CU, in two rounds of two 512-thread workgroups, are
+  // shorter chains than the one-lane kernel's (B = 1: 0.496-0.497 against
+  // 0.522-0.525 ms at 64); beside other lanes the larger workgroups keep those
+  // lanes' gates off the CUs (B = 8 in 3 lanes: 4% slower at 128)
+  int quad_alone = 192;
   // -1: two-party kernels evaluate both parties (blockIdx.y = party).  0 or 1:
   // only that party (one process per party): the launchers take the party's own
   // key (and input share, message buffer) in both party slots and launch one

@@ -120,6 +120,10 @@ class ModelBase {
   virtual hipError_t write_keys(int party, bool packed, int fd) = 0;
   virtual hipError_t set_inputs(int B, const void *x0, const void *x1, const void *a0, const void *a1,
                                 const void *m0, const void *m1, const int64_t *prot) = 0;
+  // The lane runs alone (no other lane's forward beside it): its mid-size gates
+  // may take the quad-lane form (Launch::quad_alone) without keeping another
+  // lane's workgroups off the CUs.
+  virtual void set_alone(bool) {}
   virtual hipError_t forward(int B) = 0;
   virtual hipError_t output(int64_t *h_out, int B) = 0;
   virtual uint8_t *arena(int party) = 0;

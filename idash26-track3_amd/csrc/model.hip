@@ -691,7 +691,7 @@ struct ArenaSource final : KeySource {
 template <typename T>
 class Model final : public ModelBase, KeySource {
  public:
-  Model(int bw, int s, const ModelDims &d, const Launch &L) : bw_(bw), s_(s), d_(d), L_(L) {}
+  Model(int bw, int s, const ModelDims &d, const Launch &L) : bw_(bw), s_(s), d_(d), L_(L), quad_base_(L.quad_per_cu) {}
   ~Model() override {
     drop_graph();
     stop_io();
@@ -1562,6 +1562,10 @@ class Model final : public ModelBase, KeySource {
 
   // ---------------- online ----------------
   // ---------------- graph capture ----------------
+  void set_alone(bool a) override {
+    if (a != alone_) drop_graph();  // the captured forward's launches depend on it
+    alone_ = a;
+  }
   void drop_graph() {
     if (gexec_) (void)hipGraphExecDestroy(gexec_);
     if (graph_) (void)hipGraphDestroy(graph_);
@@ -1645,6 +1649,7 @@ class Model final : public ModelBase, KeySource {
     // and bw = 64 unchanged, against none).
     const bool few = B <= kFewLaneB;
     L_.spread_small = few;
+    L_.quad_per_cu = alone_ ? std::max(quad_base_, L_.quad_alone) : quad_base_;
     const int N = d_.n_nodes, bw = bw_;
     const size_t BN = size_t(B) * N;
     if (!streaming_) {
@@ -1767,6 +1772,8 @@ class Model final : public ModelBase, KeySource {
   int bw_, s_;
   ModelDims d_;
   Launch L_;
+  int quad_base_ = 64;  // L_.quad_per_cu as created (the lane beside others)
+  bool alone_ = false;
   int party_ = -1;       // party mode: this process's party
   Peer *peer_ = nullptr;  // party mode: the channel to the other party
   std::vector<DevBuf<T>> wt_, bias_;
@@ -2117,6 +2124,7 @@ hipError_t LaneSet::forward(int B) {
     // forward runs lane i after lane i-1 so that launches do not overlap.
     if (i > 0 && serial_) TRY(hipStreamWaitEvent(st_[i], done_[i - 1], 0));
     lane_[i]->counters = Counters();
+    lane_[i]->set_alone(n == 1);
     hipError_t r = lane_[i]->forward(lane_B(B, i));
     if (r != hipSuccess) {  // the caller's stream still waits for the lanes already enqueued
       for (int j = 1; j < i; j++) (void)hipStreamWaitEvent(st_[0], done_[j], 0);

@@ -864,6 +864,48 @@ def test_model_extreme_molecule_sizes(mp, orc, synth, bw, lanes):
     c.close()
 
 
+@pytest.mark.parametrize("bw", [32, 64])
+def test_model_alone_lane_quad_gates(mp, orc, synth, monkeypatch, bw):
+    """A lane that runs alone (one active lane) evaluates its mid-size gates
+    (up to 192 elements per CU: on 256 CUs the GCN-2 and GCN-3 gates of one
+    molecule, 85 and 171) in the quad-lane form, on 512-thread workgroups; a
+    lane beside another does not.  On one two-lane model: B = 1 (alone), B = 2
+    (two lanes), B = 1 again (the captured forward is dropped when the lane's
+    setting changes); and B = 1 with the wider form off (MPCX_QUAD_ALONE=64).
+    Every forward matches the oracle."""
+    dims = synth.Dims(bw=bw)
+    W = synth.weights(dims, seed=31)
+    d = _od(orc, dims)
+
+    def batch(B, seed):
+        X, A, mask = synth.molecules(B, dims, seed=seed, min_atoms=100, max_atoms=140)
+        prot = synth.protein(B, dims, seed=seed + 1)
+        want, code = orc.plain_forward(d, X, A, mask, prot, W)
+        assert code == 0
+        sh = [synth.share(v, bw, seed + 2 + k) for k, v in enumerate((X, A, mask))]
+        return sh, prot, want
+
+    def run(m, B, seed):
+        sh, prot, want = batch(B, seed)
+        m.keygen(B, 500 + seed)
+        m.set_inputs(B, *sh[0], *sh[1], *sh[2], prot)
+        m.forward(B)
+        assert np.array_equal(m.output(B), want), (B, seed)
+
+    c = mp.Ctx(bw=bw)
+    m = mp.Model(c, dims, W, lanes=2)
+    for B, seed in ((1, 40), (2, 41), (1, 42)):
+        run(m, B, seed)
+    m.close()
+    c.close()
+    monkeypatch.setenv("MPCX_QUAD_ALONE", "64")
+    c = mp.Ctx(bw=bw)
+    m = mp.Model(c, dims, W)
+    run(m, 1, 43)
+    m.close()
+    c.close()
+
+
 @pytest.mark.parametrize("lanes", [1, 2])
 def test_model_graph_replays(mp, orc, synth, monkeypatch, lanes):
     """Resident-key forwards are captured into a HIP graph once per batch size
