@@ -560,6 +560,7 @@ def run_party_child(args):
     ctx.sync()
     elapsed = time.perf_counter() - t0
     res = {"party": party, "elapsed": elapsed, "bytes": ctx.bytes_exchanged, "socket_bytes": peer.bytes - b0,
+           "transport": {1: "ipc", 0: "socket"}.get(peer.transport, "none"),
            "out": [int(v) for v in m.output(B)], "key_bytes": len(key) if hasattr(key, "__len__") else None}
     if prof:
         res["prof"] = {k: prof[k] for k in ("aes_calls", "elements", "launches", "hbm_bytes")}
@@ -627,15 +628,17 @@ def run_party(args):
         "dtype": "u32" if args.bw == 32 else "u64",
         "data": "synthetic molecules (random trees + ring closures, 10-60 atoms), Kaiming-normal weights",
         "config": {"workload": f"two-party secure affinity forward in party mode: party 0 and party 1 as two "
-                               f"processes on one GPU, each with its own key and shares in HBM, exchanging over a "
-                               f"Unix socket; bw={args.bw} s=12, B={B} molecules x {dims.n_nodes} atoms, "
+                               f"processes on one GPU, each with its own key and shares in HBM, exchanging "
+                               + ("through device inboxes shared by IPC handles (tokens on a Unix socket)"
+                                  if res[0]["transport"] == "ipc" else "over a Unix socket")
+                               + f"; bw={args.bw} s=12, B={B} molecules x {dims.n_nodes} atoms, "
                                f"GCN 78-78-156-312, FC 312-1024-128, fusion 256-1024-512-1"
                                + SLACK_DESC.get(args.slack, ""),
                    "B": B, "n_nodes": dims.n_nodes, "bw": args.bw, "scale": dims.s, "lanes": 1,
-                   "slack": args.slack, "parties": "two processes"},
+                   "slack": args.slack, "parties": "two processes", "transport": res[0]["transport"]},
         "bytes_exchanged_per_sample": round(res[0]["bytes"] / args.steps / B, 1),
-        "socket_bytes_per_sample": round(res[0]["socket_bytes"] / args.steps / B, 1),
-        "socket_equals_counted": all(r["socket_bytes"] == r["bytes"] for r in res),
+        "channel_bytes_per_sample": round(res[0]["socket_bytes"] / args.steps / B, 1),
+        "channel_equals_counted": all(r["socket_bytes"] == r["bytes"] for r in res),
         "parties_agree": agree,
         "roofline": {
             "kernel": "DCF gate kernels of both parties (k_tr_party_bits / k_tr_party_msg and the one-party "

@@ -1083,6 +1083,7 @@ void mpcx_peer_close(mpcx_peer *p) {
 int mpcx_peer_party(const mpcx_peer *p) { return p ? p->impl->party() : -1; }
 uint64_t mpcx_peer_bytes(const mpcx_peer *p) { return p ? p->impl->bytes_sent() + p->impl->bytes_received() : 0; }
 uint64_t mpcx_peer_rounds(const mpcx_peer *p) { return p ? p->impl->rounds() : 0; }
+int mpcx_peer_transport(const mpcx_peer *p) { return p ? p->impl->transport() : -1; }
 const char *mpcx_peer_error(const mpcx_peer *p) { return p ? p->impl->error().c_str() : "null peer"; }
 
 namespace {

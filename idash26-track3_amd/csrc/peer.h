@@ -54,12 +54,20 @@ class Peer {
   uint64_t bytes_sent() const { return sent_; }
   uint64_t bytes_received() const { return recv_; }
   uint64_t rounds() const { return rounds_; }
+  // 2 linked in memory (in-process pair), 1 IPC inboxes, 0 staged through the
+  // socket, -1 not yet decided (a cross-process channel before its first exchange)
+  int transport() const { return link_ ? 2 : ipc_state_ == 1 ? 1 : (cross_process_ && ipc_state_ < 0) ? -1 : 0; }
   const std::string &error() const { return err_; }
 
  private:
   hipError_t ensure(size_t bytes);
   hipError_t ensure_events(size_t n);
   hipError_t exchange_local(hipStream_t stream, const Seg *segs, int nseg, size_t total);
+  hipError_t exchange_socket(hipStream_t stream, const Seg *segs, int nseg, size_t total);
+  hipError_t exchange_ipc(hipStream_t stream, const Seg *segs, int nseg, size_t total);
+  hipError_t ipc_negotiate();
+  hipError_t ipc_grow(size_t bytes);
+  bool token(char t);  // sends t, receives the peer's token, checks it is t
   void sender_loop();
   bool send_all(const uint8_t *p, size_t n);
   bool recv_all(uint8_t *p, size_t n);
@@ -79,6 +87,20 @@ class Peer {
   const uint8_t *job_ = nullptr;
   size_t job_n_ = 0;
   bool job_ready_ = false, job_done_ = true, job_ok_ = true, stop_ = false;
+  // two processes on one GPU (peer_connect): device inboxes mapped into the
+  // peer process (IPC), negotiated at the first exchange
+ public:
+  static constexpr size_t kIpcMin = size_t(16) << 20, kIpcMax = size_t(1) << 30;
+  bool ipc() const { return ipc_state_ == 1; }
+
+ private:
+  bool cross_process_ = false;
+  int ipc_state_ = -1;  // -1 not negotiated, 0 staged socket, 1 IPC
+  void *inbox_ = nullptr, *peer_inbox_ = nullptr;
+  size_t inbox_cap_ = 0;
+  hipEvent_t ipc_ev_[2] = {nullptr, nullptr};  // message written into the peer's inbox; own inbox read
+  bool read_pending_ = false;
+  friend hipError_t peer_connect(int, const std::string &, int, int, Peer **, std::string *);
   // in-process pair
   std::shared_ptr<LocalLink> link_;
   hipEvent_t lev_[2] = {nullptr, nullptr};  // this end's message ready, the peer's message consumed
@@ -87,7 +109,12 @@ class Peer {
 
 // Party 0 listens on the Unix socket `path` and accepts one connection; party 1
 // connects to it (retrying until timeout_ms).  Receives time out after
-// io_timeout_ms of silence.
+// io_timeout_ms of silence.  When both processes run on the same GPU (and
+// neither sets MPCX_PEER_IPC=0), each exchange writes this party's message
+// straight into the peer's device inbox, mapped into this process by an IPC
+// memory handle, with one-byte tokens on the socket for the ordering; messages
+// over kIpcMax bytes, and every exchange otherwise, are staged through pinned
+// host memory and the socket.
 hipError_t peer_connect(int party, const std::string &path, int timeout_ms, int io_timeout_ms, Peer **out,
                         std::string *err);
 // Both ends of one channel, for two parties as two threads of one process:

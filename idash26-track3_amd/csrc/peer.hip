@@ -10,6 +10,7 @@
 #include <algorithm>
 #include <cerrno>
 #include <chrono>
+#include <cstdlib>
 #include <cstring>
 
 namespace mpcx {
@@ -67,6 +68,11 @@ Peer::~Peer() {
   cv_.notify_all();
   if (th_.joinable()) th_.join();
   for (hipEvent_t e : lev_)
+    if (e) (void)hipEventDestroy(e);
+  if (read_pending_) (void)hipEventSynchronize(ipc_ev_[1]);
+  if (peer_inbox_) (void)hipIpcCloseMemHandle(peer_inbox_);
+  if (inbox_) (void)hipFree(inbox_);
+  for (hipEvent_t e : ipc_ev_)
     if (e) (void)hipEventDestroy(e);
   for (hipEvent_t e : ev_) (void)hipEventDestroy(e);
   if (fd_ >= 0) ::close(fd_);
@@ -180,6 +186,15 @@ hipError_t Peer::exchange(hipStream_t stream, const Seg *segs, int nseg) {
   rounds_++;
   if (total == 0) return hipSuccess;
   if (link_) return exchange_local(stream, segs, nseg, total);
+  if (cross_process_ && ipc_state_ < 0) {
+    const hipError_t ne = ipc_negotiate();
+    if (ne != hipSuccess) return ne;
+  }
+  if (ipc_state_ == 1 && total <= kIpcMax) return exchange_ipc(stream, segs, nseg, total);
+  return exchange_socket(stream, segs, nseg, total);
+}
+
+hipError_t Peer::exchange_socket(hipStream_t stream, const Seg *segs, int nseg, size_t total) {
   hipError_t e = ensure(total);
   if (e != hipSuccess) return e;
   const size_t nch = (total + kChunk - 1) / kChunk;
@@ -308,6 +323,142 @@ hipError_t Peer::exchange_local(hipStream_t stream, const Seg *segs, int nseg, s
   return hipSuccess;
 }
 
+// ---- two processes on one GPU ----
+bool Peer::token(char t) {
+  uint8_t in = 0;
+  const uint8_t out = uint8_t(t);
+  if (!send_all(&out, 1) || !recv_all(&in, 1) || in != out) {
+    broken_ = true;
+    err_ = "the peer closed, timed out or left the exchange order";
+    return false;
+  }
+  return true;
+}
+
+// Both ends send the same hello (whether they want IPC, the process, the GPU's
+// PCI bus id) and take the same decision: IPC when both want it, in two
+// processes on the same GPU.
+hipError_t Peer::ipc_negotiate() {
+  struct Hello {
+    uint32_t magic, want;
+    int64_t pid;  // two ends of one process (threads): no IPC (a process cannot open its own handle)
+    char bus[64];
+  } h{}, q{};
+  h.magic = 0x4d504358u;  // "MPCX"
+  h.pid = int64_t(::getpid());
+  const char *v = std::getenv("MPCX_PEER_IPC");
+  h.want = v && std::atoi(v) == 0 ? 0u : 1u;
+  int dev = 0;
+  if (h.want && (hipGetDevice(&dev) != hipSuccess || hipDeviceGetPCIBusId(h.bus, int(sizeof h.bus), dev) != hipSuccess))
+    h.want = 0;
+  h.bus[sizeof h.bus - 1] = 0;
+  if (!send_all(reinterpret_cast<const uint8_t *>(&h), sizeof h) || !recv_all(reinterpret_cast<uint8_t *>(&q), sizeof q)) {
+    broken_ = true;
+    err_ = "the peer closed or timed out before the first exchange";
+    return hipErrorNotReady;
+  }
+  q.bus[sizeof q.bus - 1] = 0;
+  ipc_state_ = h.want && q.want && q.magic == h.magic && q.pid != h.pid && std::strcmp(h.bus, q.bus) == 0 ? 1 : 0;
+  if (ipc_state_ == 1) {
+    for (hipEvent_t &e : ipc_ev_) {
+      const hipError_t ce = hipEventCreateWithFlags(&e, hipEventDisableTiming);
+      if (ce != hipSuccess) return ce;
+    }
+    return ipc_grow(kIpcMin);
+  }
+  return hipSuccess;
+}
+
+// New inboxes of at least `bytes` on both ends (both call it at the same
+// exchange: the messages have one length); the old ones are released once
+// both ends have closed their mappings.
+hipError_t Peer::ipc_grow(size_t bytes) {
+  size_t cap = kIpcMin;
+  while (cap < bytes) cap *= 2;
+  if (read_pending_) {
+    const hipError_t se = hipEventSynchronize(ipc_ev_[1]);
+    if (se != hipSuccess) return se;
+    read_pending_ = false;
+  }
+  if (peer_inbox_) {
+    (void)hipIpcCloseMemHandle(peer_inbox_);
+    peer_inbox_ = nullptr;
+    if (!token('C')) return hipErrorNotReady;
+  }
+  if (inbox_) (void)hipFree(inbox_);
+  inbox_ = nullptr;
+  inbox_cap_ = 0;
+  hipError_t e = hipMalloc(&inbox_, cap);
+  hipIpcMemHandle_t mine{}, theirs{};
+  if (e == hipSuccess) e = hipIpcGetMemHandle(&mine, inbox_);
+  // the handle goes across even after a failure (zeroed), so that the peer
+  // does not wait out its timeout; a failure then ends IPC on both sides
+  const uint8_t ok = e == hipSuccess ? 1 : 0;
+  uint8_t pok = 0;
+  if (!send_all(&ok, 1) || !send_all(reinterpret_cast<const uint8_t *>(&mine), sizeof mine) ||
+      !recv_all(&pok, 1) || !recv_all(reinterpret_cast<uint8_t *>(&theirs), sizeof theirs)) {
+    broken_ = true;
+    err_ = "the peer closed or timed out while mapping the inboxes";
+    return hipErrorNotReady;
+  }
+  if (!ok || !pok) {
+    broken_ = true;
+    err_ = "an inbox could not be shared with the peer process";
+    return e != hipSuccess ? e : hipErrorNotReady;
+  }
+  e = hipIpcOpenMemHandle(&peer_inbox_, theirs, hipIpcMemLazyEnablePeerAccess);
+  if (e != hipSuccess) {
+    peer_inbox_ = nullptr;
+    broken_ = true;
+    err_ = "the peer's inbox could not be mapped";
+    return e;
+  }
+  inbox_cap_ = cap;
+  return hipSuccess;
+}
+
+// One exchange through the inboxes: this end's inbox is free (its last read
+// done) -> 'R' both ways -> the message into the peer's inbox, waited for ->
+// 'D' both ways -> the peer's message from this end's inbox into the receive
+// regions, on the stream (waited for at the next exchange).
+hipError_t Peer::exchange_ipc(hipStream_t stream, const Seg *segs, int nseg, size_t total) {
+  hipError_t e = hipSuccess;
+  if (total > inbox_cap_) {
+    e = ipc_grow(total);
+    if (e != hipSuccess) return e;
+  }
+  if (read_pending_) {
+    e = hipEventSynchronize(ipc_ev_[1]);
+    if (e != hipSuccess) return e;
+    read_pending_ = false;
+  }
+  if (!token('R')) return hipErrorNotReady;
+  size_t o = 0;
+  for (int k = 0; k < nseg && e == hipSuccess; k++) {
+    if (segs[k].bytes)
+      e = hipMemcpyAsync(static_cast<uint8_t *>(peer_inbox_) + o, segs[k].send, segs[k].bytes,
+                         hipMemcpyDeviceToDevice, stream);
+    o += segs[k].bytes;
+  }
+  if (e == hipSuccess) e = hipEventRecord(ipc_ev_[0], stream);
+  if (e == hipSuccess) e = hipEventSynchronize(ipc_ev_[0]);
+  if (e != hipSuccess) return e;
+  if (!token('D')) return hipErrorNotReady;
+  o = 0;
+  for (int k = 0; k < nseg && e == hipSuccess; k++) {
+    if (segs[k].bytes)
+      e = hipMemcpyAsync(segs[k].recv, static_cast<const uint8_t *>(inbox_) + o, segs[k].bytes,
+                         hipMemcpyDeviceToDevice, stream);
+    o += segs[k].bytes;
+  }
+  if (e == hipSuccess) e = hipEventRecord(ipc_ev_[1], stream);
+  if (e != hipSuccess) return e;
+  read_pending_ = true;
+  sent_ += total;
+  recv_ += total;
+  return hipSuccess;
+}
+
 static void set_io_timeout(int fd, int ms) {
   if (ms <= 0) return;
   timeval tv;
@@ -383,6 +534,7 @@ hipError_t peer_connect(int party, const std::string &path, int timeout_ms, int 
     ::close(fd);
     return hipErrorOutOfMemory;
   }
+  (*out)->cross_process_ = true;
   return hipSuccess;
 }
 

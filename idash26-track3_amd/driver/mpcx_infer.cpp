@@ -264,7 +264,11 @@ int main(int argc, char **argv) {
     }
     std::printf("Average time taken (microseconds)=%f\n", total_us / reps);
     std::printf("Comm (B)=%llu\n", static_cast<unsigned long long>(comm));
-    if (peer) std::printf("Peer (B)=%llu\n", static_cast<unsigned long long>(wire));
+    if (peer) {
+    std::printf("Peer (B)=%llu\n", static_cast<unsigned long long>(wire));
+    const int tr = mpcx_peer_transport(peer);
+    std::printf("Peer transport=%s\n", tr == 1 ? "ipc" : tr == 2 ? "local" : tr == 0 ? "socket" : "none");
+  }
     for (int j = 0; j < B; j++) {
       const double aff = double(out[size_t(j)]) / std::ldexp(1.0, scale);
       if (B == 1)

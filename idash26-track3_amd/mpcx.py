@@ -124,6 +124,7 @@ _SIGS = {
     "mpcx_peer_party": (C.c_int, [C.c_void_p]),
     "mpcx_peer_bytes": (C.c_uint64, [C.c_void_p]),
     "mpcx_peer_rounds": (C.c_uint64, [C.c_void_p]),
+    "mpcx_peer_transport": (C.c_int, [C.c_void_p]),
     "mpcx_peer_error": (C.c_char_p, [C.c_void_p]),
     "mpcx_party_reconstruct": (C.c_int, [C.c_void_p, C.c_void_p, C.c_size_t, C.c_void_p]),
     "mpcx_party_tr_eval": (C.c_int, [C.c_void_p, C.c_void_p, C.c_int, C.c_size_t, C.c_void_p, C.c_void_p,
@@ -582,6 +583,11 @@ class Peer:
     @property
     def rounds(self):
         return int(self.lib.mpcx_peer_rounds(self.h))
+
+    @property
+    def transport(self):
+        """2 linked in memory, 1 IPC inboxes, 0 staged through the socket, -1 undecided."""
+        return int(self.lib.mpcx_peer_transport(self.h))
 
     def close(self):
         if self.h:

@@ -370,6 +370,15 @@ int mpcx_peer_party(const mpcx_peer *peer);
 /* Bytes sent plus bytes received over the channel, and exchanges made. */
 uint64_t mpcx_peer_bytes(const mpcx_peer *peer);
 uint64_t mpcx_peer_rounds(const mpcx_peer *peer);
+/* How the channel moves messages: 2 device to device within one process
+ * (mpcx_peer_pair), 1 through device inboxes shared by IPC memory handles (two
+ * processes on one GPU: each exchange writes this party's message straight into
+ * the peer's inbox, one-byte tokens on the socket order the writes and reads),
+ * 0 staged through pinned host memory and the socket (other setups, messages
+ * over 1 GiB, MPCX_PEER_IPC=0 in either process), -1 not yet decided (a
+ * connected channel before its first exchange).  No counterpart in the
+ * reference, whose GpuPeer always stages through the host. */
+int mpcx_peer_transport(const mpcx_peer *peer);
 const char *mpcx_peer_error(const mpcx_peer *peer);
 /* peer->reconstructInPlace(d, bw, n, s) (gpu_mpc/utils/gpu_comms.h:290-302):
  * d_inout holds this party's additive share and receives the sum of both. */

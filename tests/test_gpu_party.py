@@ -74,6 +74,7 @@ def two_parties(bw, fn, transport="local"):
         f = [ex.submit(run, p) for p in (0, 1)]
         res = [x.result(timeout=120) for x in f]
     wire = (p0.bytes, p1.bytes)
+    assert p0.transport == p1.transport == (0 if transport == "socket" else 2)
     for c in ctxs:
         c.close()
     p0.close()
@@ -307,13 +308,16 @@ def test_model_party_threads(orc, synth, bw, transport):
     assert wire[0] == wire[1] == 2 * one_bytes
 
 
+@pytest.mark.parametrize("transport", ["ipc", "socket"])
 @pytest.mark.parametrize("bw", [32, 64])
-def test_driver_two_processes(orc, synth, tmp_path, bw):
+def test_driver_two_processes(orc, synth, tmp_path, bw, transport):
     """The reference's deployment: the dealer run writes both parties' key
     files, then two evaluator processes (mpcx_infer role 3, party 0 and party 1)
     each read their own key file and share files and exchange over a Unix
     socket; both print the plaintext affinities, and the same Comm (B) as the
-    one-process evaluator, which is also what crossed each party's socket."""
+    one-process evaluator, which is also what crossed each party's channel:
+    through device inboxes shared by IPC handles (the default for two
+    processes on one GPU) or staged through the socket (MPCX_PEER_IPC=0)."""
     import mpcx
     import formats
     exe = os.path.join(os.path.dirname(mpcx.__file__), "mpcx_infer")
@@ -337,7 +341,8 @@ def test_driver_two_processes(orc, synth, tmp_path, bw):
     one_comm = int(re.search(r"Comm \(B\)=(\d+)", r.stdout).group(1))
     sock = str(tmp_path / "peer.sock")
     print(f"[two-process] bw={bw}: starting party 0 and party 1 on {sock}", file=sys.stderr, flush=True)
-    procs = [subprocess.Popen(args + ["3", str(kdir), str(bdir)], env=dict(env, MPCX_PARTY=str(p), MPCX_PEER=sock),
+    penv = dict(env, MPCX_PEER_IPC="1" if transport == "ipc" else "0")
+    procs = [subprocess.Popen(args + ["3", str(kdir), str(bdir)], env=dict(penv, MPCX_PARTY=str(p), MPCX_PEER=sock),
                               stdout=subprocess.PIPE, stderr=subprocess.PIPE, text=True) for p in (0, 1)]
     outs = []
     for p in procs:
@@ -353,3 +358,4 @@ def test_driver_two_processes(orc, synth, tmp_path, bw):
         assert re.findall(r"AFFINITY\[\d+\]=\S+", o) == lines
         assert int(re.search(r"Comm \(B\)=(\d+)", o).group(1)) == one_comm
         assert int(re.search(r"Peer \(B\)=(\d+)", o).group(1)) == one_comm
+        assert re.search(r"Peer transport=(\w+)", o).group(1) == transport
