@@ -1600,6 +1600,268 @@ hipError_t launch_gemm_pair_sum(const Launch &L, const GemmArgs<T> &g0, const Ge
   return launch_reconstruct<T>(L, size_t(g0.batch) * g0.M * g0.N, g0.C, g1.C, out);
 }
 
+// ---------------------------------------------------------------------------
+// Z_2^32 SxS gates on balanced-digit planes (gemm.h, SxsDigitArgs).  The key
+// operands are digit planes formed once per key set; A^ and B^ are the gate's
+// ring words, turned into digits as they are loaded (two VALU operations a
+// word).  Per 16-word chunk and 16-column tile: A^ against B^, -RB0 and -RB1,
+// and -RA0, -RA1 against B^, four shift MFMAs each (shift s pairs digit i of
+// one operand with digit s - i of the other: A^ and B^ are the operands
+// shifted, by byte permutes, so that no mask plane is), into one set of shift
+// sums (Z_2^32: the int32 sums wrap, only acc_s mod 2^(32-8s) enters the
+// result).  Lane (i, g) of a wave holds words 16c + 4g .. +3 of row i and of
+// column i: one 16-byte load from a [row][k] plane (A^, the A-side masks, the
+// transposed B-side masks) and four 4-byte loads down B^'s column, 16 lanes of
+// one row of B^ reading 64 contiguous bytes.  No LDS staging: every load goes
+// to the L2 (about three times the requests of the panel kernel on the same
+// shape, which bounds the launch with the memory latency).
+// ---------------------------------------------------------------------------
+__global__ void k_ring_digits(size_t n, const uint32_t *src, int neg, uint32_t *dst) {
+  for (size_t i = size_t(blockIdx.x) * blockDim.x + threadIdx.x; i < n; i += size_t(gridDim.x) * blockDim.x) {
+    const uint32_t v = src[i];
+    dst[i] = ring_digits(neg ? 0u - v : v);
+  }
+}
+// batch matrices of R x Cc words, transposed through 32 x 32 LDS tiles
+__global__ __launch_bounds__(256) void k_ring_digits_t(int R, int Cc, const uint32_t *src, int neg, uint32_t *dst) {
+  __shared__ uint32_t t[32][33];
+  const size_t plane = size_t(R) * size_t(Cc);
+  const uint32_t *sp = src + size_t(blockIdx.z) * plane;
+  uint32_t *dp = dst + size_t(blockIdx.z) * plane;
+  const int r0 = int(blockIdx.y) * 32, c0 = int(blockIdx.x) * 32;
+  const int tx = int(threadIdx.x) & 31, ty = int(threadIdx.x) >> 5;
+  for (int k = ty; k < 32; k += 8) {
+    const int r = r0 + k, c = c0 + tx;
+    uint32_t v = 0;
+    if (r < R && c < Cc) {
+      v = sp[size_t(r) * Cc + c];
+      v = ring_digits(neg ? 0u - v : v);
+    }
+    t[k][tx] = v;
+  }
+  __syncthreads();
+  for (int k = ty; k < 32; k += 8) {
+    const int c = c0 + k, r = r0 + tx;  // row c of the transposed matrix, column r
+    if (c < Cc && r < R) dp[size_t(c) * R + r] = t[tx][k];
+  }
+}
+
+__device__ __forceinline__ uint32_t pan_load1(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+  return __builtin_amdgcn_raw_buffer_load_b32(r, int(off), 0, 0);
+}
+__device__ __forceinline__ uint4 digits4(uint4 v) {
+  return make_uint4(ring_digits(v.x), ring_digits(v.y), ring_digits(v.z), ring_digits(v.w));
+}
+
+// one chunk's operands of a wave: A^, -RA0, -RA1 of its row; per column tile
+// B^ (ring words) and -RB0, -RB1 (digits)
+template <int NT>
+struct SxsChunk {
+  uint4 a[3];
+  uint4 b[NT][3];
+};
+
+// Workgroup = KS waves on the same 16 x 16 NT output block, wave w taking
+// chunks [CPW w, CPW (w + 1)) of each KS * CPW: its CPW chunks' loads are
+// issued at once (straight-line code: the compiler counts them exactly), so a
+// wave's share of K costs one memory round trip; the waves' shift sums (int32,
+// wrapping: the sum of the parts is the whole) meet in LDS and wave 0 adds K0
+// + C1 (loaded before the products) and stores.
+constexpr int kSxsCpw = 3;  // chunks of 16 words per wave and pass
+template <int NT, int KS, int WPE>
+__global__ __launch_bounds__(64 * KS, WPE) void k_sxs_digits(SxsDigitArgs g) {
+  constexpr int NQ = 4, CPW = kSxsCpw;
+  __shared__ v4i_t red[KS > 1 ? KS - 1 : 1][NT][NQ][64];
+  const int M = g.M, N = g.N, K = g.K;
+  const int gx = (N + 16 * NT - 1) / (16 * NT), gy = (M + 15) / 16;
+  const int lw = xcd_swizzle(int(blockIdx.x), int(gridDim.x));
+  const int bz = lw / (gx * gy), wm = (lw / gx) % gy * 16, n0 = lw % gx * 16 * NT;
+  const int lane = int(threadIdx.x) & 63, wave = int(threadIdx.x) >> 6, li = lane & 15, lg = lane >> 4;
+  const size_t mk = size_t(M) * K, nk = size_t(N) * K, mn = size_t(M) * N;
+  const __amdgpu_buffer_rsrc_t rah = pan_rsrc(g.ahat + size_t(bz) * mk, mk * 4);
+  const __amdgpu_buffer_rsrc_t rbh = pan_rsrc(g.bhat + size_t(bz) * nk, nk * 4);
+  __amdgpu_buffer_rsrc_t ra[2], rb[2];
+#pragma unroll
+  for (int i = 0; i < 2; i++) {
+    ra[i] = pan_rsrc(g.na[i] + size_t(bz) * mk, mk * 4);
+    rb[i] = pan_rsrc(g.nb[i] + size_t(bz) * nk, nk * 4);
+  }
+  // Byte offsets of this lane's row in the [row][k] planes, of its columns in
+  // the transposed planes and in B^'s rows.  An operand outside the matrix
+  // (row or column past its end, word past K) has kPanOob ORed into its
+  // offset, which the buffer's range check turns into zeros: no branch and no
+  // condition around any load.
+  const int row = wm + li;
+  const uint32_t aoob = row < M ? 0u : kPanOob;
+  const uint32_t abase = uint32_t(row < M ? row : 0) * uint32_t(K) * 4u;
+  uint32_t boob[NT], bbase[NT], bcol[NT];
+#pragma unroll
+  for (int t = 0; t < NT; t++) {
+    const int col = n0 + 16 * t + li;
+    boob[t] = col < N ? 0u : kPanOob;
+    bbase[t] = uint32_t(col < N ? col : 0) * uint32_t(K) * 4u;
+    bcol[t] = uint32_t(col < N ? col : 0) * 4u;
+  }
+  const uint32_t nrow = uint32_t(N) * 4u;
+  // this lane's outputs (rows wm + 4lg + r, columns n0 + 16t + li), and
+  // wave 0's K0 and C1 of them, loaded first so that they arrive during the
+  // products (the wave index made scalar: a uniform branch, not a divergent
+  // one, whose end the compiler would make wait for the loads)
+  const int wv = __builtin_amdgcn_readfirstlane(wave);
+  uint32_t coff[NT][4], k0[NT][4], c1[NT][4];
+  const __amdgpu_buffer_rsrc_t rk0 = pan_rsrc(g.k0 + size_t(bz) * mn, mn * 4);
+  const __amdgpu_buffer_rsrc_t rc1 = pan_rsrc(g.c1 + size_t(bz) * mn, mn * 4);
+#pragma unroll
+  for (int t = 0; t < NT; t++)
+#pragma unroll
+    for (int r = 0; r < 4; r++) {
+      const int om = wm + 4 * lg + r;
+      coff[t][r] = (uint32_t(om < M ? om : 0) * uint32_t(N) * 4u + bcol[t]) | boob[t] | (om < M ? 0u : kPanOob);
+      k0[t][r] = c1[t][r] = 0;
+    }
+  if (wv == 0) {
+#pragma unroll
+    for (int t = 0; t < NT; t++)
+#pragma unroll
+      for (int r = 0; r < 4; r++) {
+        k0[t][r] = pan_load1(rk0, coff[t][r]);
+        c1[t][r] = pan_load1(rc1, coff[t][r]);
+      }
+  }
+  // words 16c + 4lg .. +3 (K % 4 == 0: all four inside K, or none)
+  auto load = [&](SxsChunk<NT> &x, int c) {
+    const uint32_t w = uint32_t(16 * c + 4 * lg);
+    const uint32_t koob = w < uint32_t(K) ? 0u : kPanOob;
+    const uint32_t ao = (abase + w * 4u) | aoob | koob;
+    x.a[0] = pan_load(rah, ao);
+    x.a[1] = pan_load(ra[0], ao);
+    x.a[2] = pan_load(ra[1], ao);
+#pragma unroll
+    for (int t = 0; t < NT; t++) {
+      const uint32_t m = boob[t] | koob;
+      const uint32_t bo = (bbase[t] + w * 4u) | m, ho = w * nrow + bcol[t];
+      x.b[t][0].x = pan_load1(rbh, ho | m);
+      x.b[t][0].y = pan_load1(rbh, (ho + nrow) | m);
+      x.b[t][0].z = pan_load1(rbh, (ho + 2u * nrow) | m);
+      x.b[t][0].w = pan_load1(rbh, (ho + 3u * nrow) | m);
+      x.b[t][1] = pan_load(rb[0], bo);
+      x.b[t][2] = pan_load(rb[1], bo);
+    }
+  };
+  const ShiftSel sel = pan_shift_selectors();
+  v4i_t acc[NT][NQ];
+#pragma unroll
+  for (int t = 0; t < NT; t++)
+#pragma unroll
+    for (int q = 0; q < NQ; q++) acc[t][q] = v4i_t{0, 0, 0, 0};
+  auto vec = [](uint4 v) { return v4i_t{int(v.x), int(v.y), int(v.z), int(v.w)}; };
+  const int nc = (K + 15) / 16;
+  for (int c0 = CPW * wv; c0 < nc; c0 += CPW * KS) {
+    SxsChunk<NT> x[CPW];
+#pragma unroll
+    for (int j = 0; j < CPW; j++) load(x[j], c0 + j);  // past K: zeros
+    // every load of the pass ahead of its first product (the scheduler would
+    // otherwise move the later chunks' loads between the MFMAs, each then a
+    // round trip of its own)
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int j = 0; j < CPW; j++) {
+      // shift s pairs digit i of one operand with digit s - i of the other:
+      // A^ shifted against B^ and the B-side masks, the A-side masks against
+      // B^ shifted (no mask plane needs shifting)
+      v4i_t as[NQ];
+      digit_shifts_s(digits4(x[j].a[0]), sel, as);
+      const v4i_t ra0 = vec(x[j].a[1]), ra1 = vec(x[j].a[2]);
+#pragma unroll
+      for (int t = 0; t < NT; t++) {
+        const uint4 bd = digits4(x[j].b[t][0]);
+        v4i_t bs[NQ];
+        digit_shifts_s(bd, sel, bs);
+        const v4i_t bh = vec(bd), b0 = vec(x[j].b[t][1]), b1 = vec(x[j].b[t][2]);
+#pragma unroll
+        for (int q = 0; q < NQ; q++) {
+          v4i_t a = acc[t][q];
+          a = __builtin_amdgcn_mfma_i32_16x16x64_i8(as[q], bh, a, 0, 0, 0);   // A^ B^
+          a = __builtin_amdgcn_mfma_i32_16x16x64_i8(as[q], b0, a, 0, 0, 0);   // A^ (-RB0)
+          a = __builtin_amdgcn_mfma_i32_16x16x64_i8(as[q], b1, a, 0, 0, 0);   // A^ (-RB1)
+          a = __builtin_amdgcn_mfma_i32_16x16x64_i8(ra0, bs[q], a, 0, 0, 0);  // (-RA0) B^
+          a = __builtin_amdgcn_mfma_i32_16x16x64_i8(ra1, bs[q], a, 0, 0, 0);  // (-RA1) B^
+          acc[t][q] = a;
+        }
+      }
+    }
+  }
+  if constexpr (KS > 1) {
+    if (wv > 0) {
+#pragma unroll
+      for (int t = 0; t < NT; t++)
+#pragma unroll
+        for (int q = 0; q < NQ; q++) red[wv - 1][t][q][lane] = acc[t][q];
+    }
+    __syncthreads();
+    if (wv > 0) return;
+#pragma unroll
+    for (int w = 0; w < KS - 1; w++)
+#pragma unroll
+      for (int t = 0; t < NT; t++)
+#pragma unroll
+        for (int q = 0; q < NQ; q++) {
+          const v4i_t v = red[w][t][q][lane];
+          acc[t][q] = v4i_t{acc[t][q][0] + v[0], acc[t][q][1] + v[1], acc[t][q][2] + v[2], acc[t][q][3] + v[3]};
+        }
+  }
+  const __amdgpu_buffer_rsrc_t rc = pan_rsrc(g.C + size_t(bz) * mn, mn * 4);
+#pragma unroll
+  for (int t = 0; t < NT; t++)
+#pragma unroll
+    for (int r = 0; r < 4; r++)  // outputs outside the matrix: dropped by the range check
+      __builtin_amdgcn_raw_buffer_store_b32(k0[t][r] + c1[t][r] + digit_fold<uint32_t>(acc[t], r), rc,
+                                            int(coff[t][r]), 0, 0);
+}
+
+template <int NT, int KS>
+static hipError_t launch_sxs_digits_at(const Launch &L, const SxsDigitArgs &g) {
+  const size_t wgs = size_t((g.N + 16 * NT - 1) / (16 * NT)) * size_t((g.M + 15) / 16) * g.batch;
+  if (wgs > size_t(INT32_MAX)) return hipErrorInvalidValue;
+  constexpr int wpe = NT == 1 ? 3 : 2;  // CPW register sets of 12 + 12 NT words
+  hipLaunchKernelGGL((k_sxs_digits<NT, KS, wpe>), dim3(unsigned(wgs)), dim3(64 * KS), 0, L.stream, g);
+  return hipGetLastError();
+}
+template <int NT>
+static hipError_t launch_sxs_digits_nt(const Launch &L, const SxsDigitArgs &g, int ks) {
+  return ks == 1 ? launch_sxs_digits_at<NT, 1>(L, g)
+                 : ks == 2 ? launch_sxs_digits_at<NT, 2>(L, g)
+                           : ks == 3 ? launch_sxs_digits_at<NT, 3>(L, g) : launch_sxs_digits_at<NT, 4>(L, g);
+}
+hipError_t launch_sxs_digits(const Launch &L, const SxsDigitArgs &g) {
+  if (g.M <= 0 || g.N <= 0 || g.batch <= 0) return hipSuccess;
+  if (g.K <= 0 || g.K % 4 != 0 || !g.C || !g.k0 || !g.c1 || !g.ahat || !g.bhat ||
+      size_t(g.M) * g.K * 4 >= size_t(kPanOob) || size_t(g.N) * g.K * 4 >= size_t(kPanOob) ||
+      size_t(g.M) * g.N * 4 >= size_t(kPanOob))
+    return hipErrorInvalidValue;
+  for (int i = 0; i < 2; i++)
+    if (!g.na[i] || !g.nb[i]) return hipErrorInvalidValue;
+  // waves per workgroup: K split in shares of kSxsCpw chunks (up to four)
+  int ks = L.sxs_digits_ks, nt = L.sxs_digits_nt;
+  if (ks < 1 || ks > 4) ks = std::min(4, (g.K + 16 * kSxsCpw - 1) / (16 * kSxsCpw));
+  if (nt < 1 || nt > 2) nt = 1;
+  return nt == 1 ? launch_sxs_digits_nt<1>(L, g, ks) : launch_sxs_digits_nt<2>(L, g, ks);
+}
+hipError_t launch_ring_digits(const Launch &L, size_t n, const uint32_t *src, bool neg, uint32_t *dst) {
+  if (n == 0) return hipSuccess;
+  const size_t blocks = std::min<size_t>((n + 255) / 256, size_t(L.num_cu) * 8);
+  hipLaunchKernelGGL(k_ring_digits, dim3(unsigned(blocks)), dim3(256), 0, L.stream, n, src, neg ? 1 : 0, dst);
+  return hipGetLastError();
+}
+hipError_t launch_ring_digits_t(const Launch &L, int batch, int R, int Cc, const uint32_t *src, bool neg,
+                                uint32_t *dst) {
+  if (batch <= 0 || R <= 0 || Cc <= 0) return hipSuccess;
+  if (batch > 65535) return hipErrorInvalidValue;
+  const dim3 grid(unsigned((Cc + 31) / 32), unsigned((R + 31) / 32), unsigned(batch));
+  hipLaunchKernelGGL(k_ring_digits_t, grid, dim3(256), 0, L.stream, R, Cc, src, neg ? 1 : 0, dst);
+  return hipGetLastError();
+}
+
 #define INST(T)                                                                                                      \
   template hipError_t launch_gemm<T>(const Launch &, const GemmArgs<T> &);                                           \
   template hipError_t launch_gemm_pair<T>(const Launch &, const GemmArgs<T> &, const GemmArgs<T> &);                \
