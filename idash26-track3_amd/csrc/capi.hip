@@ -251,9 +251,7 @@ mpcx_status mpcx_create(int bw, int scale, int device, mpcx_ctx **out) {
   if (const char *v = std::getenv("MPCX_QUAD_PER_CU")) c->L.quad_per_cu = std::max(64, std::min(256, std::atoi(v)));
   if (const char *v = std::getenv("MPCX_QUAD_ALONE")) c->L.quad_alone = std::max(64, std::min(256, std::atoi(v)));
   if (const char *v = std::getenv("MPCX_PANEL_NT")) c->L.panel_nt = std::max(0, std::min(3, std::atoi(v)));
-  if (const char *v = std::getenv("MPCX_SXS_DIGITS")) c->L.sxs_digits = std::atoi(v) != 0 ? 1 : 0;
-  if (const char *v = std::getenv("MPCX_SXS_DIGITS_KS")) c->L.sxs_digits_ks = std::max(0, std::min(4, std::atoi(v)));
-  if (const char *v = std::getenv("MPCX_SXS_DIGITS_NT")) c->L.sxs_digits_nt = std::max(0, std::min(2, std::atoi(v)));
+  if (const char *v = std::getenv("MPCX_SXS_STAGED")) c->L.sxs_staged = std::atoi(v) != 0 ? 1 : 0;
   *out = c;
   return MPCX_OK;
 }

@@ -34,31 +34,4 @@ hipError_t launch_gemm_pair(const Launch &L, const GemmArgs<T> &g0, const GemmAr
 template <typename T>
 hipError_t launch_gemm_pair_sum(const Launch &L, const GemmArgs<T> &g0, const GemmArgs<T> &g1, T *out);
 
-// ---------------- Z_2^32 SxS gate on balanced-digit planes ----------------
-// Both parties' Beaver products of an SxS gate and their sum, with party 0's
-// product expanded ((A^ - RA0)(B^ - RB0) = A^ B^ - A^ RB0 - RA0 B^ + RA0 RB0):
-//   party 0:  A^ B^ - A^ RB0 - RA0 B^ + K0,   K0 = RA0 RB0 + C0
-//   party 1:  C1 - A^ RB1 - RA1 B^
-// as five products summed in the same accumulators, C = party 0 + party 1.
-// A^ ([batch][M][K]) and B^ ([batch][K][N]) are the gate's ring words; the key
-// operands are planes of balanced base-256 digits (ring_digits) formed from
-// each party's key once per key set: na = digits of -RA0, -RA1 ([batch][M][K]),
-// nb = digits of -RB0, -RB1 transposed ([batch][N][K]); k0 = K0 and c1 = C1
-// ([batch][M][N]).  K a multiple of 4.
-struct SxsDigitArgs {
-  int M = 0, N = 0, K = 0, batch = 0;
-  const uint32_t *ahat = nullptr, *bhat = nullptr;
-  const uint32_t *na[2] = {nullptr, nullptr};
-  const uint32_t *nb[2] = {nullptr, nullptr};
-  const uint32_t *k0 = nullptr, *c1 = nullptr;
-  uint32_t *C = nullptr;
-};
-hipError_t launch_sxs_digits(const Launch &L, const SxsDigitArgs &g);
-// dst[i] = digits of src[i] (of -src[i] when neg), n words
-hipError_t launch_ring_digits(const Launch &L, size_t n, const uint32_t *src, bool neg, uint32_t *dst);
-// dst[b][j][i] = digits of src[b][i][j] (of its negation when neg): batch
-// matrices of R x Ccols words, transposed
-hipError_t launch_ring_digits_t(const Launch &L, int batch, int R, int Ccols, const uint32_t *src, bool neg,
-                                uint32_t *dst);
-
 }  // namespace mpcx

@@ -975,6 +975,9 @@ __device__ __forceinline__ uint4 pan_load(__amdgpu_buffer_rsrc_t r, uint32_t off
   const v4u_t v = __builtin_amdgcn_raw_buffer_load_b128(r, int(off), 0, 0);
   return make_uint4(v[0], v[1], v[2], v[3]);
 }
+__device__ __forceinline__ uint32_t pan_load1(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+  return __builtin_amdgcn_raw_buffer_load_b32(r, int(off), 0, 0);
+}
 
 // Waves per SIMD the register budget is set for: three in Z_2^32 (measured
 // faster than two even where a few registers spill), two in Z_2^64.
@@ -1571,9 +1574,243 @@ static bool use_sxs_fused(const Launch &L, const GemmArgs<T> &g0, const GemmArgs
   return form && shape && (tiles >= L.num_cu / 4 || g0.K <= sxs_kc<T>() * 4 / int(sizeof(T)));
 }
 
+// ---------------------------------------------------------------------------
+// Z_2^32 SxS gate, both parties' products and their sum, staged through LDS in
+// steps of K (the oracle's three products, one set of shift sums):
+//   C = C0 + (A^ - RA0)(B^ - RB0)  +  C1 + A^ (-RB1) + (-RA1) B^
+// Workgroup: three waves on a 48-row x 16 CT-column tile, wave w owning rows
+// 16 w.. of it and all its columns (CT 16-column MFMA tiles), so a wave's
+// A-side operands (three planes, four byte-shifted copies each) serve CT
+// tiles.  A step stages 48 words of K: A^, RA0, RA1 rows as the digits of
+// A^ - RA0, A^ and -RA1 ([m][k]); B^, RB0, RB1 rows as the digits of B^ - RB0,
+// -RB1 and B^, as [k / 4][n][k % 4] (a lane's four k words of a column are one
+// 16-byte cell: one LDS read per MFMA operand).  The digits, differences and
+// negations are formed once per workgroup as the words go to LDS; a staging
+// thread loads four k rows of VW columns (VW divides N), coalesced along the
+// rows.  The next step's loads are in flight while this step's MFMAs run,
+// C0 + C1 are loaded before the first step, and three workgroups share a CU
+// (48 KB of LDS each at CT = 2).  Rows of 52 words put the 16-byte A reads of
+// consecutive rows in distinct bank groups.  Outside the matrices every load
+// reads zero (offsets past the buffer resource) and every store is dropped.
+// ---------------------------------------------------------------------------
+constexpr int kStgRows = 48, kStgKW = 48, kStgLDK = kStgKW + 4, kStgThreads = 192;
+
+template <int VW>
+__device__ __forceinline__ void stg_load(__amdgpu_buffer_rsrc_t r, uint32_t off, uint32_t (&v)[VW]) {
+  if constexpr (VW == 4) {
+    const v4u_t x = __builtin_amdgcn_raw_buffer_load_b128(r, int(off), 0, 0);
+    v[0] = x[0], v[1] = x[1], v[2] = x[2], v[3] = x[3];
+  } else if constexpr (VW == 2) {
+    typedef unsigned v2u_t __attribute__((ext_vector_type(2)));
+    const v2u_t x = __builtin_amdgcn_raw_buffer_load_b64(r, int(off), 0, 0);
+    v[0] = x[0], v[1] = x[1];
+  } else {
+    v[0] = __builtin_amdgcn_raw_buffer_load_b32(r, int(off), 0, 0);
+  }
+}
+
+template <int CT, int VW>
+__global__ __launch_bounds__(kStgThreads, 2) void k_sxs_staged(GemmArgs<uint32_t> g0, GemmArgs<uint32_t> g1) {
+  constexpr int NQ = 4, TN = 16 * CT, GR = kStgKW / 4, NG = TN / VW;
+  constexpr int SA = kStgRows * GR / kStgThreads;  // A groups (row, 4 words) per thread and plane
+  constexpr int SB = GR * NG / kStgThreads;        // B blocks (4 k rows, VW columns) per thread and plane
+  static_assert(kStgRows * GR % kStgThreads == 0 && GR * NG % kStgThreads == 0, "whole slots");
+  static_assert(kStgKW % 16 == 0, "steps of whole MFMA chunks");
+  constexpr int APL = kStgRows * kStgLDK, BPL = GR * TN * 4;  // words per A and B plane
+  __shared__ __align__(16) uint32_t As[3 * APL];  // A^ - RA0, A^, -RA1 as [m][k]
+  __shared__ __align__(16) uint32_t Bs[3 * BPL];  // B^ - RB0, -RB1, B^ as [k / 4][n][k % 4]
+  const int M = g0.M, N = g0.N, K = g0.K;
+  const int gx = (N + TN - 1) / TN, gy = (M + kStgRows - 1) / kStgRows;
+  const int lw = xcd_swizzle(int(blockIdx.x), int(gridDim.x));
+  const int bz = lw / (gx * gy), m0 = (lw / gx) % gy * kStgRows, n0 = lw % gx * TN;
+  const int tid = int(threadIdx.x), lane = tid & 63, wave = tid >> 6, li = lane & 15, lg = lane >> 4;
+  const size_t mk = size_t(M) * K, kn = size_t(K) * N, mn = size_t(M) * N;
+  const __amdgpu_buffer_rsrc_t rah = pan_rsrc(g0.A1 + size_t(bz) * g0.sA, mk * 4);
+  const __amdgpu_buffer_rsrc_t ra0 = pan_rsrc(g0.A2 + size_t(bz) * g0.sA, mk * 4);
+  const __amdgpu_buffer_rsrc_t ra1 = pan_rsrc(g1.A1b + size_t(bz) * g1.sA, mk * 4);
+  const __amdgpu_buffer_rsrc_t rbh = pan_rsrc(g0.B1 + size_t(bz) * g0.sB, kn * 4);
+  const __amdgpu_buffer_rsrc_t rb0 = pan_rsrc(g0.B2 + size_t(bz) * g0.sB, kn * 4);
+  const __amdgpu_buffer_rsrc_t rb1 = pan_rsrc(g1.B1 + size_t(bz) * g1.sB, kn * 4);
+  // this lane's outputs (rows m0 + 16 wave + 4 lg + r, columns n0 + 16 t + li)
+  // and their C0 + C1, loaded first so that they arrive during the products
+  const __amdgpu_buffer_rsrc_t rc0 = pan_rsrc(g0.Cin + size_t(bz) * g0.sC, mn * 4);
+  const __amdgpu_buffer_rsrc_t rc1 = pan_rsrc(g1.Cin + size_t(bz) * g1.sC, mn * 4);
+  uint32_t co[CT][4], c0v[CT][4], c1v[CT][4];
+#pragma unroll
+  for (int t = 0; t < CT; t++) {
+    const int on = n0 + 16 * t + li;
+#pragma unroll
+    for (int r = 0; r < 4; r++) {
+      const int om = m0 + 16 * wave + 4 * lg + r;
+      co[t][r] = (uint32_t(om < M ? om : 0) * uint32_t(N) + uint32_t(on < N ? on : 0)) * 4u |
+                 (om < M && on < N ? 0u : kPanOob);
+      c0v[t][r] = pan_load1(rc0, co[t][r]);
+      c1v[t][r] = pan_load1(rc1, co[t][r]);
+    }
+  }
+  // staging slots: A group (row f / GR, words 4 (f % GR)..) and B block (k rows
+  // 4 (f / NG).. + 3, columns VW (f % NG)..)
+  uint32_t aoff[SA], aoob[SA], boff[SB], boob[SB];
+#pragma unroll
+  for (int j = 0; j < SA; j++) {
+    const int f = tid + kStgThreads * j, r = f / GR;
+    aoob[j] = m0 + r < M ? 0u : kPanOob;
+    aoff[j] = (uint32_t(m0 + r < M ? m0 + r : 0) * uint32_t(K) + uint32_t(4 * (f % GR))) * 4u;
+  }
+#pragma unroll
+  for (int j = 0; j < SB; j++) {
+    const int f = tid + kStgThreads * j, n = n0 + VW * (f % NG);
+    boob[j] = n < N ? 0u : kPanOob;
+    boff[j] = (uint32_t(4 * (f / NG)) * uint32_t(N) + uint32_t(n < N ? n : 0)) * 4u;
+  }
+  uint32_t xa[SA][3][4], xb[SB][3][4][VW];
+  auto load = [&](int kb) {
+#pragma unroll
+    for (int j = 0; j < SA; j++) {
+      const int f = tid + kStgThreads * j;
+      const uint32_t o = (aoff[j] + uint32_t(kb) * 4u) | aoob[j] | (kb + 4 * (f % GR) < K ? 0u : kPanOob);
+      stg_load<4>(rah, o, xa[j][0]);
+      stg_load<4>(ra0, o, xa[j][1]);
+      stg_load<4>(ra1, o, xa[j][2]);
+    }
+#pragma unroll
+    for (int j = 0; j < SB; j++) {
+      const int f = tid + kStgThreads * j, k = kb + 4 * (f / NG);  // K % 4 == 0: all four rows inside K, or none
+      const uint32_t o = (boff[j] + uint32_t(kb) * uint32_t(N) * 4u) | boob[j] | (k < K ? 0u : kPanOob);
+#pragma unroll
+      for (int i = 0; i < 4; i++) {
+        const uint32_t oi = o + uint32_t(i) * uint32_t(N) * 4u;
+        stg_load<VW>(rbh, oi, xb[j][0][i]);
+        stg_load<VW>(rb0, oi, xb[j][1][i]);
+        stg_load<VW>(rb1, oi, xb[j][2][i]);
+      }
+    }
+  };
+  auto store = [&]() {
+#pragma unroll
+    for (int j = 0; j < SA; j++) {
+      const int f = tid + kStgThreads * j;
+      uint32_t *p = &As[(f / GR) * kStgLDK + 4 * (f % GR)];
+      uint4 d0, d1, d2;
+      uint32_t *e0 = &d0.x, *e1 = &d1.x, *e2 = &d2.x;
+#pragma unroll
+      for (int e = 0; e < 4; e++) {
+        e0[e] = ring_digits(xa[j][0][e] - xa[j][1][e]);
+        e1[e] = ring_digits(xa[j][0][e]);
+        e2[e] = ring_digits(0u - xa[j][2][e]);
+      }
+      *reinterpret_cast<uint4 *>(p) = d0;
+      *reinterpret_cast<uint4 *>(p + APL) = d1;
+      *reinterpret_cast<uint4 *>(p + 2 * APL) = d2;
+    }
+#pragma unroll
+    for (int j = 0; j < SB; j++) {
+      const int f = tid + kStgThreads * j;
+#pragma unroll
+      for (int e = 0; e < VW; e++) {  // column VW (f % NG) + e: its four k rows as one 16-byte cell
+        uint32_t *p = &Bs[((f / NG) * TN + VW * (f % NG) + e) * 4];
+        uint4 d0, d1, d2;
+        uint32_t *e0 = &d0.x, *e1 = &d1.x, *e2 = &d2.x;
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+          e0[i] = ring_digits(xb[j][0][i][e] - xb[j][1][i][e]);
+          e1[i] = ring_digits(0u - xb[j][2][i][e]);
+          e2[i] = ring_digits(xb[j][0][i][e]);
+        }
+        *reinterpret_cast<uint4 *>(p) = d0;
+        *reinterpret_cast<uint4 *>(p + BPL) = d1;
+        *reinterpret_cast<uint4 *>(p + 2 * BPL) = d2;
+      }
+    }
+  };
+  const ShiftSel sel = pan_shift_selectors();
+  v4i_t acc[CT][NQ];
+#pragma unroll
+  for (int t = 0; t < CT; t++)
+#pragma unroll
+    for (int q = 0; q < NQ; q++) acc[t][q] = v4i_t{0, 0, 0, 0};
+  // a step's three chunks: A plane p against B plane p (p = 0, 1, 2)
+  auto compute = [&]() {
+    const int ar = (16 * wave + li) * kStgLDK + 4 * lg;
+#pragma unroll
+    for (int c = 0; c < kStgKW / 16; c++)
+#pragma unroll
+      for (int p = 0; p < 3; p++) {  // (A^ - RA0)(B^ - RB0), A^ (-RB1), (-RA1) B^
+        v4i_t as[NQ];
+        digit_shifts_s(*reinterpret_cast<const uint4 *>(&As[p * APL + ar + 16 * c]), sel, as);
+#pragma unroll
+        for (int t = 0; t < CT; t++) {
+          const uint4 b = *reinterpret_cast<const uint4 *>(&Bs[p * BPL + ((4 * c + lg) * TN + 16 * t + li) * 4]);
+          const v4i_t bv = v4i_t{int(b.x), int(b.y), int(b.z), int(b.w)};
+#pragma unroll
+          for (int q = 0; q < NQ; q++) acc[t][q] = __builtin_amdgcn_mfma_i32_16x16x64_i8(as[q], bv, acc[t][q], 0, 0, 0);
+        }
+      }
+  };
+  load(0);
+  for (int kb = 0; kb < K; kb += kStgKW) {
+    store();
+    __syncthreads();
+    if (kb + kStgKW < K) load(kb + kStgKW);  // in flight during this step's MFMAs
+    compute();
+    __syncthreads();
+  }
+  const __amdgpu_buffer_rsrc_t rc = pan_rsrc(g0.C + size_t(bz) * mn, mn * 4);
+#pragma unroll
+  for (int t = 0; t < CT; t++)
+#pragma unroll
+    for (int r = 0; r < 4; r++)  // outside the matrix: dropped by the range check
+      __builtin_amdgcn_raw_buffer_store_b32(c0v[t][r] + c1v[t][r] + digit_fold<uint32_t>(acc[t], r), rc,
+                                            int(co[t][r]), 0, 0);
+}
+
+// The Z_2^32 SxS pair in the staged kernel's form: party 0's (A^ - RA0)(B^ -
+// RB0) + C0 and party 1's C1 - (A^ RB1 + RA1 B^) on one shape, K a multiple of
+// 4, 16-byte aligned operands, every matrix of a batch entry below 2 GiB.
+template <typename T>
+static bool use_sxs_staged(const Launch &L, const GemmArgs<T> &g0, const GemmArgs<T> &g1) {
+  if constexpr (sizeof(T) != 4) {
+    return false;
+  } else {
+    if (!L.sxs_staged || (L.gemm != 0 && L.gemm != 3)) return false;
+    const bool form = g0.A2 && g0.B2 && !g0.A1b && g0.sign == 1 && g1.A1 == g0.A1 && g1.B1b == g0.B1 && g1.A1b &&
+                      g1.B1 && !g1.A2 && !g1.B2 && g1.sign == -1 && g0.Cin && g1.Cin && g0.C;
+    const bool shape = g0.M == g1.M && g0.N == g1.N && g0.K == g1.K && g0.batch == g1.batch && g0.sA == g1.sA &&
+                       g0.sB == g1.sB && g0.sC == size_t(g0.M) * g0.N && g1.sC == g0.sC;
+    if (!form || !shape || g0.K % 4 != 0 || g0.sA % 4 != 0 || g0.sB % 4 != 0 || g0.sC % 4 != 0) return false;
+    const size_t lim = size_t(kPanOob);
+    if (size_t(g0.M) * g0.K * 4 >= lim || size_t(g0.K) * g0.N * 4 >= lim || size_t(g0.M) * g0.N * 4 >= lim)
+      return false;
+    for (const void *q : {(const void *)g0.A1, (const void *)g0.A2, (const void *)g1.A1b, (const void *)g0.B1,
+                          (const void *)g0.B2, (const void *)g1.B1})
+      if (reinterpret_cast<uintptr_t>(q) % 16 != 0) return false;
+    return true;
+  }
+}
+template <int CT, int VW>
+static hipError_t launch_sxs_staged_at(const Launch &L, const GemmArgs<uint32_t> &g0, const GemmArgs<uint32_t> &g1,
+                                       uint32_t *out) {
+  const size_t wgs = size_t((g0.N + 16 * CT - 1) / (16 * CT)) * size_t((g0.M + kStgRows - 1) / kStgRows) * g0.batch;
+  if (wgs > size_t(INT32_MAX)) return hipErrorInvalidValue;
+  GemmArgs<uint32_t> a = g0;
+  a.C = out;
+  hipLaunchKernelGGL((k_sxs_staged<CT, VW>), dim3(unsigned(wgs)), dim3(kStgThreads), 0, L.stream, a, g1);
+  return hipGetLastError();
+}
+// 32 columns per workgroup (64 do not fit the register budget with the
+// staging registers and the prefetched C0 + C1); groups of 2 or 1 words along
+// B's rows, whichever divides N
+static hipError_t launch_sxs_staged(const Launch &L, const GemmArgs<uint32_t> &g0, const GemmArgs<uint32_t> &g1,
+                                    uint32_t *out) {
+  return g0.N % 2 == 0 ? launch_sxs_staged_at<2, 2>(L, g0, g1, out) : launch_sxs_staged_at<2, 1>(L, g0, g1, out);
+}
+
 template <typename T>
 hipError_t launch_gemm_pair_sum(const Launch &L, const GemmArgs<T> &g0, const GemmArgs<T> &g1, T *out) {
   if (g0.M <= 0 || g0.N <= 0 || g0.batch <= 0) return hipSuccess;
+  if constexpr (sizeof(T) == 4) {
+    if (use_sxs_staged(L, g0, g1)) return launch_sxs_staged(L, g0, g1, out);
+  }
   const bool same = g0.M == g1.M && g0.N == g1.N && g0.K == g1.K && g0.batch == g1.batch && g0.sA == g1.sA &&
                     g0.sB == g1.sB && g0.sC == size_t(g0.M) * g0.N && g1.sC == g0.sC;
   if (same && (g0.A1b ? 2 : 1) + (g1.A1b ? 2 : 1) <= 3) {  // both parties' products and the sum in one launch
@@ -1600,267 +1837,6 @@ hipError_t launch_gemm_pair_sum(const Launch &L, const GemmArgs<T> &g0, const Ge
   return launch_reconstruct<T>(L, size_t(g0.batch) * g0.M * g0.N, g0.C, g1.C, out);
 }
 
-// ---------------------------------------------------------------------------
-// Z_2^32 SxS gates on balanced-digit planes (gemm.h, SxsDigitArgs).  The key
-// operands are digit planes formed once per key set; A^ and B^ are the gate's
-// ring words, turned into digits as they are loaded (two VALU operations a
-// word).  Per 16-word chunk and 16-column tile: A^ against B^, -RB0 and -RB1,
-// and -RA0, -RA1 against B^, four shift MFMAs each (shift s pairs digit i of
-// one operand with digit s - i of the other: A^ and B^ are the operands
-// shifted, by byte permutes, so that no mask plane is), into one set of shift
-// sums (Z_2^32: the int32 sums wrap, only acc_s mod 2^(32-8s) enters the
-// result).  Lane (i, g) of a wave holds words 16c + 4g .. +3 of row i and of
-// column i: one 16-byte load from a [row][k] plane (A^, the A-side masks, the
-// transposed B-side masks) and four 4-byte loads down B^'s column, 16 lanes of
-// one row of B^ reading 64 contiguous bytes.  No LDS staging: every load goes
-// to the L2 (about three times the requests of the panel kernel on the same
-// shape, which bounds the launch with the memory latency).
-// ---------------------------------------------------------------------------
-__global__ void k_ring_digits(size_t n, const uint32_t *src, int neg, uint32_t *dst) {
-  for (size_t i = size_t(blockIdx.x) * blockDim.x + threadIdx.x; i < n; i += size_t(gridDim.x) * blockDim.x) {
-    const uint32_t v = src[i];
-    dst[i] = ring_digits(neg ? 0u - v : v);
-  }
-}
-// batch matrices of R x Cc words, transposed through 32 x 32 LDS tiles
-__global__ __launch_bounds__(256) void k_ring_digits_t(int R, int Cc, const uint32_t *src, int neg, uint32_t *dst) {
-  __shared__ uint32_t t[32][33];
-  const size_t plane = size_t(R) * size_t(Cc);
-  const uint32_t *sp = src + size_t(blockIdx.z) * plane;
-  uint32_t *dp = dst + size_t(blockIdx.z) * plane;
-  const int r0 = int(blockIdx.y) * 32, c0 = int(blockIdx.x) * 32;
-  const int tx = int(threadIdx.x) & 31, ty = int(threadIdx.x) >> 5;
-  for (int k = ty; k < 32; k += 8) {
-    const int r = r0 + k, c = c0 + tx;
-    uint32_t v = 0;
-    if (r < R && c < Cc) {
-      v = sp[size_t(r) * Cc + c];
-      v = ring_digits(neg ? 0u - v : v);
-    }
-    t[k][tx] = v;
-  }
-  __syncthreads();
-  for (int k = ty; k < 32; k += 8) {
-    const int c = c0 + k, r = r0 + tx;  // row c of the transposed matrix, column r
-    if (c < Cc && r < R) dp[size_t(c) * R + r] = t[tx][k];
-  }
-}
-
-__device__ __forceinline__ uint32_t pan_load1(__amdgpu_buffer_rsrc_t r, uint32_t off) {
-  return __builtin_amdgcn_raw_buffer_load_b32(r, int(off), 0, 0);
-}
-__device__ __forceinline__ uint4 digits4(uint4 v) {
-  return make_uint4(ring_digits(v.x), ring_digits(v.y), ring_digits(v.z), ring_digits(v.w));
-}
-
-// one chunk's operands of a wave: A^, -RA0, -RA1 of its row; per column tile
-// B^ (ring words) and -RB0, -RB1 (digits)
-template <int NT>
-struct SxsChunk {
-  uint4 a[3];
-  uint4 b[NT][3];
-};
-
-// Workgroup = KS waves on the same 16 x 16 NT output block, wave w taking
-// chunks [CPW w, CPW (w + 1)) of each KS * CPW: its CPW chunks' loads are
-// issued at once (straight-line code: the compiler counts them exactly), so a
-// wave's share of K costs one memory round trip; the waves' shift sums (int32,
-// wrapping: the sum of the parts is the whole) meet in LDS and wave 0 adds K0
-// + C1 (loaded before the products) and stores.
-constexpr int kSxsCpw = 3;  // chunks of 16 words per wave and pass
-template <int NT, int KS, int WPE>
-__global__ __launch_bounds__(64 * KS, WPE) void k_sxs_digits(SxsDigitArgs g) {
-  constexpr int NQ = 4, CPW = kSxsCpw;
-  __shared__ v4i_t red[KS > 1 ? KS - 1 : 1][NT][NQ][64];
-  const int M = g.M, N = g.N, K = g.K;
-  const int gx = (N + 16 * NT - 1) / (16 * NT), gy = (M + 15) / 16;
-  const int lw = xcd_swizzle(int(blockIdx.x), int(gridDim.x));
-  const int bz = lw / (gx * gy), wm = (lw / gx) % gy * 16, n0 = lw % gx * 16 * NT;
-  const int lane = int(threadIdx.x) & 63, wave = int(threadIdx.x) >> 6, li = lane & 15, lg = lane >> 4;
-  const size_t mk = size_t(M) * K, nk = size_t(N) * K, mn = size_t(M) * N;
-  const __amdgpu_buffer_rsrc_t rah = pan_rsrc(g.ahat + size_t(bz) * mk, mk * 4);
-  const __amdgpu_buffer_rsrc_t rbh = pan_rsrc(g.bhat + size_t(bz) * nk, nk * 4);
-  __amdgpu_buffer_rsrc_t ra[2], rb[2];
-#pragma unroll
-  for (int i = 0; i < 2; i++) {
-    ra[i] = pan_rsrc(g.na[i] + size_t(bz) * mk, mk * 4);
-    rb[i] = pan_rsrc(g.nb[i] + size_t(bz) * nk, nk * 4);
-  }
-  // Byte offsets of this lane's row in the [row][k] planes, of its columns in
-  // the transposed planes and in B^'s rows.  An operand outside the matrix
-  // (row or column past its end, word past K) has kPanOob ORed into its
-  // offset, which the buffer's range check turns into zeros: no branch and no
-  // condition around any load.
-  const int row = wm + li;
-  const uint32_t aoob = row < M ? 0u : kPanOob;
-  const uint32_t abase = uint32_t(row < M ? row : 0) * uint32_t(K) * 4u;
-  uint32_t boob[NT], bbase[NT], bcol[NT];
-#pragma unroll
-  for (int t = 0; t < NT; t++) {
-    const int col = n0 + 16 * t + li;
-    boob[t] = col < N ? 0u : kPanOob;
-    bbase[t] = uint32_t(col < N ? col : 0) * uint32_t(K) * 4u;
-    bcol[t] = uint32_t(col < N ? col : 0) * 4u;
-  }
-  const uint32_t nrow = uint32_t(N) * 4u;
-  // this lane's outputs (rows wm + 4lg + r, columns n0 + 16t + li), and
-  // wave 0's K0 and C1 of them, loaded first so that they arrive during the
-  // products (the wave index made scalar: a uniform branch, not a divergent
-  // one, whose end the compiler would make wait for the loads)
-  const int wv = __builtin_amdgcn_readfirstlane(wave);
-  uint32_t coff[NT][4], k0[NT][4], c1[NT][4];
-  const __amdgpu_buffer_rsrc_t rk0 = pan_rsrc(g.k0 + size_t(bz) * mn, mn * 4);
-  const __amdgpu_buffer_rsrc_t rc1 = pan_rsrc(g.c1 + size_t(bz) * mn, mn * 4);
-#pragma unroll
-  for (int t = 0; t < NT; t++)
-#pragma unroll
-    for (int r = 0; r < 4; r++) {
-      const int om = wm + 4 * lg + r;
-      coff[t][r] = (uint32_t(om < M ? om : 0) * uint32_t(N) * 4u + bcol[t]) | boob[t] | (om < M ? 0u : kPanOob);
-      k0[t][r] = c1[t][r] = 0;
-    }
-  if (wv == 0) {
-#pragma unroll
-    for (int t = 0; t < NT; t++)
-#pragma unroll
-      for (int r = 0; r < 4; r++) {
-        k0[t][r] = pan_load1(rk0, coff[t][r]);
-        c1[t][r] = pan_load1(rc1, coff[t][r]);
-      }
-  }
-  // words 16c + 4lg .. +3 (K % 4 == 0: all four inside K, or none)
-  auto load = [&](SxsChunk<NT> &x, int c) {
-    const uint32_t w = uint32_t(16 * c + 4 * lg);
-    const uint32_t koob = w < uint32_t(K) ? 0u : kPanOob;
-    const uint32_t ao = (abase + w * 4u) | aoob | koob;
-    x.a[0] = pan_load(rah, ao);
-    x.a[1] = pan_load(ra[0], ao);
-    x.a[2] = pan_load(ra[1], ao);
-#pragma unroll
-    for (int t = 0; t < NT; t++) {
-      const uint32_t m = boob[t] | koob;
-      const uint32_t bo = (bbase[t] + w * 4u) | m, ho = w * nrow + bcol[t];
-      x.b[t][0].x = pan_load1(rbh, ho | m);
-      x.b[t][0].y = pan_load1(rbh, (ho + nrow) | m);
-      x.b[t][0].z = pan_load1(rbh, (ho + 2u * nrow) | m);
-      x.b[t][0].w = pan_load1(rbh, (ho + 3u * nrow) | m);
-      x.b[t][1] = pan_load(rb[0], bo);
-      x.b[t][2] = pan_load(rb[1], bo);
-    }
-  };
-  const ShiftSel sel = pan_shift_selectors();
-  v4i_t acc[NT][NQ];
-#pragma unroll
-  for (int t = 0; t < NT; t++)
-#pragma unroll
-    for (int q = 0; q < NQ; q++) acc[t][q] = v4i_t{0, 0, 0, 0};
-  auto vec = [](uint4 v) { return v4i_t{int(v.x), int(v.y), int(v.z), int(v.w)}; };
-  const int nc = (K + 15) / 16;
-  for (int c0 = CPW * wv; c0 < nc; c0 += CPW * KS) {
-    SxsChunk<NT> x[CPW];
-#pragma unroll
-    for (int j = 0; j < CPW; j++) load(x[j], c0 + j);  // past K: zeros
-    // every load of the pass ahead of its first product (the scheduler would
-    // otherwise move the later chunks' loads between the MFMAs, each then a
-    // round trip of its own)
-    __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-    for (int j = 0; j < CPW; j++) {
-      // shift s pairs digit i of one operand with digit s - i of the other:
-      // A^ shifted against B^ and the B-side masks, the A-side masks against
-      // B^ shifted (no mask plane needs shifting)
-      v4i_t as[NQ];
-      digit_shifts_s(digits4(x[j].a[0]), sel, as);
-      const v4i_t ra0 = vec(x[j].a[1]), ra1 = vec(x[j].a[2]);
-#pragma unroll
-      for (int t = 0; t < NT; t++) {
-        const uint4 bd = digits4(x[j].b[t][0]);
-        v4i_t bs[NQ];
-        digit_shifts_s(bd, sel, bs);
-        const v4i_t bh = vec(bd), b0 = vec(x[j].b[t][1]), b1 = vec(x[j].b[t][2]);
-#pragma unroll
-        for (int q = 0; q < NQ; q++) {
-          v4i_t a = acc[t][q];
-          a = __builtin_amdgcn_mfma_i32_16x16x64_i8(as[q], bh, a, 0, 0, 0);   // A^ B^
-          a = __builtin_amdgcn_mfma_i32_16x16x64_i8(as[q], b0, a, 0, 0, 0);   // A^ (-RB0)
-          a = __builtin_amdgcn_mfma_i32_16x16x64_i8(as[q], b1, a, 0, 0, 0);   // A^ (-RB1)
-          a = __builtin_amdgcn_mfma_i32_16x16x64_i8(ra0, bs[q], a, 0, 0, 0);  // (-RA0) B^
-          a = __builtin_amdgcn_mfma_i32_16x16x64_i8(ra1, bs[q], a, 0, 0, 0);  // (-RA1) B^
-          acc[t][q] = a;
-        }
-      }
-    }
-  }
-  if constexpr (KS > 1) {
-    if (wv > 0) {
-#pragma unroll
-      for (int t = 0; t < NT; t++)
-#pragma unroll
-        for (int q = 0; q < NQ; q++) red[wv - 1][t][q][lane] = acc[t][q];
-    }
-    __syncthreads();
-    if (wv > 0) return;
-#pragma unroll
-    for (int w = 0; w < KS - 1; w++)
-#pragma unroll
-      for (int t = 0; t < NT; t++)
-#pragma unroll
-        for (int q = 0; q < NQ; q++) {
-          const v4i_t v = red[w][t][q][lane];
-          acc[t][q] = v4i_t{acc[t][q][0] + v[0], acc[t][q][1] + v[1], acc[t][q][2] + v[2], acc[t][q][3] + v[3]};
-        }
-  }
-  const __amdgpu_buffer_rsrc_t rc = pan_rsrc(g.C + size_t(bz) * mn, mn * 4);
-#pragma unroll
-  for (int t = 0; t < NT; t++)
-#pragma unroll
-    for (int r = 0; r < 4; r++)  // outputs outside the matrix: dropped by the range check
-      __builtin_amdgcn_raw_buffer_store_b32(k0[t][r] + c1[t][r] + digit_fold<uint32_t>(acc[t], r), rc,
-                                            int(coff[t][r]), 0, 0);
-}
-
-template <int NT, int KS>
-static hipError_t launch_sxs_digits_at(const Launch &L, const SxsDigitArgs &g) {
-  const size_t wgs = size_t((g.N + 16 * NT - 1) / (16 * NT)) * size_t((g.M + 15) / 16) * g.batch;
-  if (wgs > size_t(INT32_MAX)) return hipErrorInvalidValue;
-  constexpr int wpe = NT == 1 ? 3 : 2;  // CPW register sets of 12 + 12 NT words
-  hipLaunchKernelGGL((k_sxs_digits<NT, KS, wpe>), dim3(unsigned(wgs)), dim3(64 * KS), 0, L.stream, g);
-  return hipGetLastError();
-}
-template <int NT>
-static hipError_t launch_sxs_digits_nt(const Launch &L, const SxsDigitArgs &g, int ks) {
-  return ks == 1 ? launch_sxs_digits_at<NT, 1>(L, g)
-                 : ks == 2 ? launch_sxs_digits_at<NT, 2>(L, g)
-                           : ks == 3 ? launch_sxs_digits_at<NT, 3>(L, g) : launch_sxs_digits_at<NT, 4>(L, g);
-}
-hipError_t launch_sxs_digits(const Launch &L, const SxsDigitArgs &g) {
-  if (g.M <= 0 || g.N <= 0 || g.batch <= 0) return hipSuccess;
-  if (g.K <= 0 || g.K % 4 != 0 || !g.C || !g.k0 || !g.c1 || !g.ahat || !g.bhat ||
-      size_t(g.M) * g.K * 4 >= size_t(kPanOob) || size_t(g.N) * g.K * 4 >= size_t(kPanOob) ||
-      size_t(g.M) * g.N * 4 >= size_t(kPanOob))
-    return hipErrorInvalidValue;
-  for (int i = 0; i < 2; i++)
-    if (!g.na[i] || !g.nb[i]) return hipErrorInvalidValue;
-  // waves per workgroup: K split in shares of kSxsCpw chunks (up to four)
-  int ks = L.sxs_digits_ks, nt = L.sxs_digits_nt;
-  if (ks < 1 || ks > 4) ks = std::min(4, (g.K + 16 * kSxsCpw - 1) / (16 * kSxsCpw));
-  if (nt < 1 || nt > 2) nt = 1;
-  return nt == 1 ? launch_sxs_digits_nt<1>(L, g, ks) : launch_sxs_digits_nt<2>(L, g, ks);
-}
-hipError_t launch_ring_digits(const Launch &L, size_t n, const uint32_t *src, bool neg, uint32_t *dst) {
-  if (n == 0) return hipSuccess;
-  const size_t blocks = std::min<size_t>((n + 255) / 256, size_t(L.num_cu) * 8);
-  hipLaunchKernelGGL(k_ring_digits, dim3(unsigned(blocks)), dim3(256), 0, L.stream, n, src, neg ? 1 : 0, dst);
-  return hipGetLastError();
-}
-hipError_t launch_ring_digits_t(const Launch &L, int batch, int R, int Cc, const uint32_t *src, bool neg,
-                                uint32_t *dst) {
-  if (batch <= 0 || R <= 0 || Cc <= 0) return hipSuccess;
-  if (batch > 65535) return hipErrorInvalidValue;
-  const dim3 grid(unsigned((Cc + 31) / 32), unsigned((R + 31) / 32), unsigned(batch));
-  hipLaunchKernelGGL(k_ring_digits_t, grid, dim3(256), 0, L.stream, R, Cc, src, neg ? 1 : 0, dst);
-  return hipGetLastError();
-}
 
 #define INST(T)                                                                                                      \
   template hipError_t launch_gemm<T>(const Launch &, const GemmArgs<T> &);                                           \

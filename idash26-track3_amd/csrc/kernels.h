@@ -49,11 +49,8 @@ struct Launch {
   int panel_pf = 1;
   // columns per k_panels_pf workgroup in 16-column tiles (1..3); 0: by rounds
   int panel_nt = 0;
-  // Z_2^32 SxS gates of a model with resident keys on balanced-digit planes
-  // (launch_sxs_digits; the masks' planes formed once per key set); 0: the
-  // panel / fused kernels.  sxs_digits_ks / _nt: its waves per workgroup
-  // (shares of K, 1..4) and 16-column tiles per wave (1..2); 0: the defaults
-  int sxs_digits = 1, sxs_digits_ks = 0, sxs_digits_nt = 0;
+  // Z_2^32 SxS pairs (both parties) in the LDS-staged kernel (k_sxs_staged)
+  int sxs_staged = 1;
   // party-mode gate calls synchronise the stream before returning (0: they
   // return with their work enqueued, for callers that order by stream)
   int party_sync = 1;

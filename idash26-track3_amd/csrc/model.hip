@@ -10,7 +10,6 @@
 #include <unistd.h>
 
 #include <algorithm>
-#include <map>
 #include <cmath>
 #include <condition_variable>
 #include <cstdint>
@@ -118,7 +117,6 @@ struct GateKey {
   size_t n = 0;
   int nsh = 0;
   size_t sh[2][2] = {{0, 0}, {0, 0}};
-  int sxs_n = 0;  // SxS gates: N of the product (0: another gate)
   void share(size_t b, size_t e) {
     sh[nsh][0] = b;
     sh[nsh][1] = e;
@@ -128,19 +126,8 @@ struct GateKey {
 
 // Supplies the key bytes [begin, end) of the next gate (resident arena or a
 // streamed slot) before the gate's kernels are enqueued.
-// One SxS gate's Beaver masks as balanced-digit planes (launch_sxs_digits),
-// formed once per resident key set: -RA0, -RA1 [nb][M][K], -RB0, -RB1
-// transposed [nb][N][K], and party 0's K0 = RA0 RB0 + C0 [nb][M][N].
-struct SxsDigitSet {
-  const uint32_t *na0 = nullptr, *na1 = nullptr, *nb0 = nullptr, *nb1 = nullptr, *k0 = nullptr;
-};
 struct KeySource {
   virtual hipError_t acquire(size_t begin, size_t end, KeyView *kv) = 0;
-  // the digit planes of the SxS gate whose key starts at `begin`, if formed
-  virtual const SxsDigitSet *sxs_digits(size_t begin) const {
-    (void)begin;
-    return nullptr;
-  }
   virtual ~KeySource() = default;
 };
 
@@ -466,10 +453,6 @@ struct Runner {
 
   // batched C_b = A_b (M x K) . B_b (K x N), Beaver
   hipError_t sxs(int nb, int M, int K, int N, const T *A, const T *Bm, T *out) {
-    if constexpr (sizeof(T) == 4) {
-      if (!party_mode() && L.sxs_digits)
-        if (const SxsDigitSet *d = src.sxs_digits(c.off)) return sxs_digits(nb, M, K, N, A, Bm, out, *d);
-    }
     const size_t end = sxs_layout(bw, nb, M, K, N, c.off).end;
     size_t b;
     TRY(enter(end, &b));
@@ -515,38 +498,6 @@ struct Runner {
     }
     // both parties' products and the reconstruction of the exchanged shares
     TRY(launch_gemm_pair_sum<T>(L, g, h, out));
-    TRY(span.end());
-    leave(end);
-    return hipSuccess;
-  }
-
-  // The same gate with the masks as digit planes formed once per key set
-  // (Z_2^32): both parties' products and their sum in one launch, which forms
-  // A^'s and B^'s digits as it loads them and reads C1 from party 1's key.
-  hipError_t sxs_digits(int nb, int M, int K, int N, const T *A, const T *Bm, T *out, const SxsDigitSet &d) {
-    const size_t end = sxs_layout(bw, nb, M, K, N, c.off).end;
-    size_t b;
-    TRY(enter(end, &b));
-    const SxsLayout lay = sxs_layout(bw, nb, M, K, N, b);
-    GemmSpan span{timer, L.stream};
-    TRY(span.begin(3.0 * nb * double(M) * K * N));
-    const size_t nc = size_t(nb) * M * N;
-    SxsDigitArgs g;
-    g.M = M;
-    g.N = N;
-    g.K = K;
-    g.batch = nb;
-    g.ahat = reinterpret_cast<const uint32_t *>(A);
-    g.bhat = reinterpret_cast<const uint32_t *>(Bm);
-    g.na[0] = d.na0;
-    g.na[1] = d.na1;
-    g.nb[0] = d.nb0;
-    g.nb[1] = d.nb1;
-    g.k0 = d.k0;
-    g.c1 = reinterpret_cast<const uint32_t *>(kv.k[1] + lay.off_c);
-    g.C = reinterpret_cast<uint32_t *>(out);
-    TRY(launch_sxs_digits(L, g));
-    ctr.msg(nc, bw);
     TRY(span.end());
     leave(end);
     return hipSuccess;
@@ -911,7 +862,7 @@ class Model final : public ModelBase, KeySource {
         tr(G_TRSLACK, E);
       else
         trunc(false, E);
-      push(sxs_layout(bw_, B, N, N, d_.gcn[l], o).end).sxs_n = d_.gcn[l];
+      push(sxs_layout(bw_, B, N, N, d_.gcn[l], o).end);
       if (agg_split()) {
         tr(G_TRSLACK, E);
         tr(G_RELUSLACK, E);
@@ -936,65 +887,8 @@ class Model final : public ModelBase, KeySource {
 
   uint8_t *arena(int party) override { return arena_[party]; }
 
-  // ---------------- SxS digit planes of the resident key set ----------------
-  struct DigitBufs {
-    DevBuf<uint32_t> na0, na1, nb0, nb1, k0;
-    SxsDigitSet set;
-  };
-  std::map<size_t, DigitBufs> digits_;  // by the SxS gate's key offset
-  const SxsDigitSet *sxs_digits(size_t begin) const override {
-    const auto it = digits_.find(begin);
-    return it == digits_.end() ? nullptr : &it->second.set;
-  }
-  // The Beaver masks of every SxS gate of a resident key set (both parties'
-  // keys in this process) as the digit planes launch_sxs_digits reads, and
-  // party 0's K0 = RA0 RB0 + C0: once per key set, on the model's stream,
-  // outside any forward.  Z_2^32 with K = n_nodes a multiple of 4 only.
-  hipError_t install_digits(int B) {
-    digits_.clear();
-    if constexpr (sizeof(T) != 4) {
-      return hipSuccess;
-    } else {
-      const int N = d_.n_nodes;
-      if (!L_.sxs_digits || streaming_ || party_ >= 0 || !arena_[0] || !arena_[1] || N % 4 != 0) return hipSuccess;
-      for (const GateKey &k : plan(B)) {
-        if (k.sxs_n <= 0) continue;
-        const int F = k.sxs_n;
-        const SxsLayout lay = sxs_layout(bw_, B, N, N, F, k.begin);
-        auto at = [&](int p, size_t off) { return reinterpret_cast<const uint32_t *>(arena_[p] + off); };
-        const size_t na = size_t(B) * N * N, nb = size_t(B) * N * F;
-        DigitBufs &d = digits_[k.begin];
-        TRY(d.na0.alloc(na));
-        TRY(d.na1.alloc(na));
-        TRY(d.nb0.alloc(nb));
-        TRY(d.nb1.alloc(nb));
-        TRY(d.k0.alloc(nb));
-        TRY(launch_ring_digits(L_, na, at(0, lay.off_ra), true, d.na0.p));
-        TRY(launch_ring_digits(L_, na, at(1, lay.off_ra), true, d.na1.p));
-        TRY(launch_ring_digits_t(L_, B, N, F, at(0, lay.off_rb), true, d.nb0.p));
-        TRY(launch_ring_digits_t(L_, B, N, F, at(1, lay.off_rb), true, d.nb1.p));
-        GemmArgs<uint32_t> g;  // K0 = C0 + RA0 RB0
-        g.M = N;
-        g.K = N;
-        g.N = F;
-        g.batch = B;
-        g.sA = size_t(N) * N;
-        g.sB = size_t(N) * F;
-        g.sC = size_t(N) * F;
-        g.A1 = at(0, lay.off_ra);
-        g.B1 = at(0, lay.off_rb);
-        g.Cin = at(0, lay.off_c);
-        g.C = d.k0.p;
-        TRY(launch_gemm<uint32_t>(L_, g));
-        d.set = SxsDigitSet{d.na0.p, d.na1.p, d.nb0.p, d.nb1.p, d.k0.p};
-      }
-      return hipStreamSynchronize(L_.stream);
-    }
-  }
-
   void free_arena() {
     drop_graph();
-    digits_.clear();
     for (int p = 0; p < 2; p++) {
       if (arena_[p]) (void)hipFree(arena_[p]);
       arena_[p] = nullptr;
@@ -1152,7 +1046,6 @@ class Model final : public ModelBase, KeySource {
     TRY(hipStreamSynchronize(L_.stream));
     for (int p = 0; p < 2; p++) party_key_bytes(L_, seed, p, pk_[p]);
     have_pk_ = true;
-    TRY(install_digits(B));
     keyed_B_ = B;
     return hipSuccess;
   }
@@ -1168,7 +1061,6 @@ class Model final : public ModelBase, KeySource {
     TRY(hipMemcpy(arena_[0], k0, bytes, hipMemcpyHostToDevice));
     TRY(hipMemcpy(arena_[1], k1, bytes, hipMemcpyHostToDevice));
     have_pk_ = false;  // imported keys: the parties' PRF keys are not known here
-    TRY(install_digits(B));
     keyed_B_ = B;
     return hipSuccess;
   }

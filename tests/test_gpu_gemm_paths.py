@@ -5,7 +5,10 @@ and columns whole 16-byte groups, K within one step or enough workgroups),
 the wide-K matrix-core kernel wherever that applies (enough tiles for a
 quarter of the CUs, or K within one step) and the tiled matrix-core kernels
 elsewhere (long K over few tiles, split-K); MPCX_GEMM=wide skips the panel
-kernel and MPCX_GEMM=tiled forces the tiled kernels everywhere.  The shapes
+kernel and MPCX_GEMM=tiled forces the tiled kernels everywhere.  Z_2^32 SxS
+products of both parties take the LDS-staged kernel (k_sxs_staged) where K is
+a multiple of 4, on the default and wide paths; MPCX_SXS_STAGED=0 gives them
+to the panel and fused kernels as before (the "nostaged" context).  The shapes
 below make the panel and wide kernels take every branch: one and several K
 steps (a last step of one 16-byte group), steps with masks, party 1's two K
 segments, rows read as 16-byte groups or word by word (K not a multiple of
@@ -28,13 +31,15 @@ GEMM_SHAPES = [(3080, 78, 78), (3080, 156, 312), (140, 140, 312), (130, 77, 65),
 # panel-pipelined kernel (K within one step; 48-column workgroups at
 # 140 x 140 x 312) with 64-row workgroups, K of exactly one step and ragged N
 # on 16-column tiles, with rows past M in a partly used workgroup and K inside
-# one MFMA chunk, and with 64-row workgroups on 32- and 48-column tiles
+# one MFMA chunk, and with 64-row workgroups on 32- and 48-column tiles; the
+# staged kernel with odd N (single-word groups along B's rows), K of several
+# 48-word steps and a last partial one, rows past M in a 48-row tile
 SXS_SHAPES = [(22, 140, 140, 78), (22, 140, 140, 312), (22, 140, 140, 156), (64, 33, 300, 40), (3, 70, 66, 37),
               (5, 100, 148, 64), (2, 5, 63, 3), (1, 1, 1, 1), (2, 200, 144, 68), (3, 37, 20, 100),
-              (22, 200, 100, 96), (40, 200, 64, 140)]
+              (22, 200, 100, 96), (40, 200, 64, 140), (3, 50, 52, 37), (4, 97, 196, 33)]
 
 
-PATHS = ("default", "wide", "tiled")  # the contexts of the ctxs fixture, in order
+PATHS = ("default", "wide", "tiled", "nostaged")  # the contexts of the ctxs fixture, in order
 
 
 def _check(got, want, path):
@@ -62,26 +67,30 @@ def _signed(v, bw):
     return np.where(v >= 1 << (bw - 1), v - (1 << bw), v)
 
 
-@pytest.fixture(scope="module", params=[32, 64])
-def ctxs(request):
-    """(ring width, contexts on the default, wide and tiled-only paths)."""
+def _ctx_with(bw, var, val):
+    """A context created with the environment variable var set to val."""
     import os
     import mpcx
-    bw = request.param
-    old = os.environ.get("MPCX_GEMM")
-    auto = mpcx.Ctx(bw=bw)
+    old = os.environ.get(var)
+    os.environ[var] = val
     try:
-        os.environ["MPCX_GEMM"] = "wide"
-        wide = mpcx.Ctx(bw=bw)
-        os.environ["MPCX_GEMM"] = "tiled"
-        tiled = mpcx.Ctx(bw=bw)
+        return mpcx.Ctx(bw=bw)
     finally:
         if old is None:
-            del os.environ["MPCX_GEMM"]
+            del os.environ[var]
         else:
-            os.environ["MPCX_GEMM"] = old
-    yield bw, (auto, wide, tiled)
-    for c in (auto, wide, tiled):
+            os.environ[var] = old
+
+
+@pytest.fixture(scope="module", params=[32, 64])
+def ctxs(request):
+    """(ring width, contexts on the default, wide, tiled-only and unstaged paths)."""
+    import mpcx
+    bw = request.param
+    cs = (mpcx.Ctx(bw=bw), _ctx_with(bw, "MPCX_GEMM", "wide"), _ctx_with(bw, "MPCX_GEMM", "tiled"),
+          _ctx_with(bw, "MPCX_SXS_STAGED", "0"))
+    yield bw, cs
+    for c in cs:
         c.close()
 
 
@@ -125,7 +134,8 @@ def test_sxs_panel_forms(orc, shape):
     """The three-panel SxS launch (both parties' Beaver products and their sum)
     in every form, on the same products: the unpipelined panel kernel
     (MPCX_PANEL_PF=0) and the pipelined one on 16-, 32- and 48-column
-    workgroups (MPCX_PANEL_NT=1..3), each bit-exact against the oracle."""
+    workgroups (MPCX_PANEL_NT=1..3), each bit-exact against the oracle (the
+    staged kernel, which would take these products, switched off)."""
     import os
     import mpcx
     nb, Mm, K, N = shape
@@ -139,15 +149,17 @@ def test_sxs_panel_forms(orc, shape):
     _, _, orc_rc = orc.sxs_keygen(4, 2, 32, nb, Mm, K, N, ra, rb)
     forms = [("MPCX_PANEL_PF", "0")] + [("MPCX_PANEL_NT", str(t)) for t in (1, 2, 3)]
     for var, val in forms:
-        old = os.environ.get(var)
+        saved = {v: os.environ.get(v) for v in (var, "MPCX_SXS_STAGED")}
         os.environ[var] = val
+        os.environ["MPCX_SXS_STAGED"] = "0"
         try:
             c = mpcx.Ctx(bw=32)
         finally:
-            if old is None:
-                del os.environ[var]
-            else:
-                os.environ[var] = old
+            for v, o in saved.items():
+                if o is None:
+                    del os.environ[v]
+                else:
+                    os.environ[v] = o
         try:
             g0, g1, _ = c.sxs_keygen(nb, Mm, K, N, ra, rb, seed=4, gate=2)
             got = c.sxs_eval(nb, Mm, K, N, g0, g1, ah, bh)
