@@ -1575,32 +1575,33 @@ static bool use_sxs_fused(const Launch &L, const GemmArgs<T> &g0, const GemmArgs
 }
 
 // ---------------------------------------------------------------------------
-// Z_2^32 SxS gate, both parties' products and their sum, staged through LDS in
-// steps of K (the oracle's three products, one set of shift sums):
+// SxS gate (Z_2^32 or Z_2^64), both parties' products and their sum, staged
+// through LDS in steps of K (the oracle's three products, one set of shift sums):
 //   C = C0 + (A^ - RA0)(B^ - RB0)  +  C1 + A^ (-RB1) + (-RA1) B^
 // Workgroup: three waves on a 48-row x 16 CT-column tile, wave w owning rows
 // 16 w.. of it and all its columns (CT 16-column MFMA tiles), so a wave's
-// A-side operands (three planes, four byte-shifted copies each) serve CT
-// tiles.  A step stages 48 words of K: A^, RA0, RA1 rows as the digits of
-// A^ - RA0, A^ and -RA1 ([m][k]); B^, RB0, RB1 rows as the digits of B^ - RB0,
-// -RB1 and B^, as [k / 4][n][k % 4] (a lane's four k words of a column are one
-// 16-byte cell: one LDS read per MFMA operand).  The digits, differences and
-// negations are formed once per workgroup as the words go to LDS; a staging
-// thread loads four k rows of VW columns (VW divides N), coalesced along the
-// rows.  The next step's loads are in flight while this step's MFMAs run,
-// C0 + C1 are loaded before the first step, and three workgroups share a CU
-// (48 KB of LDS each at CT = 2).  Rows of 52 words put the 16-byte A reads of
-// consecutive rows in distinct bank groups.  Outside the matrices every load
-// reads zero (offsets past the buffer resource) and every store is dropped.
+// A-side operands (three planes, one byte-shifted copy per digit shift) serve
+// CT tiles.  A step stages 192 bytes of K (48 words of Z_2^32, 24 of Z_2^64):
+// A^, RA0, RA1 rows as the digits of A^ - RA0, A^ and -RA1 ([m][k]); B^, RB0,
+// RB1 rows as the digits of B^ - RB0, -RB1 and B^, as [k / KPC][n][k % KPC]
+// (a lane's KPC = 16 / sizeof(T) k words of a column are one 16-byte cell: one
+// LDS read per MFMA operand).  The digits, differences and negations are
+// formed once per workgroup as the words go to LDS; a staging thread loads KPC
+// k rows of VW columns (VW divides N), coalesced along the rows.  The next
+// step's loads are in flight while this step's MFMAs run, C0 + C1 are loaded
+// before the first step; 48 KB of LDS.  Rows of 52 32-bit words put the
+// 16-byte A reads of consecutive rows in distinct bank groups.  Outside the
+// matrices every load reads zero (offsets past the buffer resource) and every
+// store is dropped.
 // ---------------------------------------------------------------------------
 constexpr int kStgRows = 48, kStgKW = 48, kStgLDK = kStgKW + 4, kStgThreads = 192;
 
-template <int VW>
-__device__ __forceinline__ void stg_load(__amdgpu_buffer_rsrc_t r, uint32_t off, uint32_t (&v)[VW]) {
-  if constexpr (VW == 4) {
+template <int NW>
+__device__ __forceinline__ void stg_load(__amdgpu_buffer_rsrc_t r, uint32_t off, uint32_t (&v)[NW]) {
+  if constexpr (NW == 4) {
     const v4u_t x = __builtin_amdgcn_raw_buffer_load_b128(r, int(off), 0, 0);
     v[0] = x[0], v[1] = x[1], v[2] = x[2], v[3] = x[3];
-  } else if constexpr (VW == 2) {
+  } else if constexpr (NW == 2) {
     typedef unsigned v2u_t __attribute__((ext_vector_type(2)));
     const v2u_t x = __builtin_amdgcn_raw_buffer_load_b64(r, int(off), 0, 0);
     v[0] = x[0], v[1] = x[1];
@@ -1608,118 +1609,139 @@ __device__ __forceinline__ void stg_load(__amdgpu_buffer_rsrc_t r, uint32_t off,
     v[0] = __builtin_amdgcn_raw_buffer_load_b32(r, int(off), 0, 0);
   }
 }
+// one ring word (T) at a byte offset: zero past the resource
+template <typename T>
+__device__ __forceinline__ T stg_word(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+  uint32_t v[sizeof(T) / 4];
+  stg_load<sizeof(T) / 4>(r, off, v);
+  if constexpr (sizeof(T) == 4) return v[0];
+  else return (uint64_t(v[1]) << 32) | v[0];
+}
+template <typename T>
+__device__ __forceinline__ void stg_store_word(__amdgpu_buffer_rsrc_t r, uint32_t off, T x) {
+  if constexpr (sizeof(T) == 4) {
+    __builtin_amdgcn_raw_buffer_store_b32(x, r, int(off), 0, 0);
+  } else {
+    typedef unsigned v2u_t __attribute__((ext_vector_type(2)));
+    __builtin_amdgcn_raw_buffer_store_b64(v2u_t{uint32_t(x), uint32_t(x >> 32)}, r, int(off), 0, 0);
+  }
+}
 
-template <int CT, int VW>
-__global__ __launch_bounds__(kStgThreads, 2) void k_sxs_staged(GemmArgs<uint32_t> g0, GemmArgs<uint32_t> g1) {
-  constexpr int NQ = 4, TN = 16 * CT, GR = kStgKW / 4, NG = TN / VW;
-  constexpr int SA = kStgRows * GR / kStgThreads;  // A groups (row, 4 words) per thread and plane
-  constexpr int SB = GR * NG / kStgThreads;        // B blocks (4 k rows, VW columns) per thread and plane
+// T: the ring (Z_2^32 or Z_2^64); CT: 16-column MFMA tiles per wave; VW: ring
+// words per B load along a row (VW divides N).  A 16-byte group holds KPC =
+// 16 / sizeof(T) words; a step is 192 bytes of K (48 or 24 words, three 64-byte
+// MFMA chunks); shift s of the sizeof(T) digit shifts pairs digit j of an A word
+// with digit s - j of the B word.
+template <typename T, int CT, int VW>
+__global__ __launch_bounds__(kStgThreads, 2) void k_sxs_staged(GemmArgs<T> g0, GemmArgs<T> g1) {
+  constexpr int WB = int(sizeof(T)), NQ = WB, KPC = 16 / WB, KW = 192 / WB, TN = 16 * CT, GR = 12;
+  constexpr int NG = TN / VW, NV = VW * WB / 4;  // B groups per k row, 32-bit words per B load
+  constexpr int SA = kStgRows * GR / kStgThreads;  // A groups (row, 16 bytes) per thread and plane
+  constexpr int SB = GR * NG / kStgThreads;        // B blocks (KPC k rows, VW columns) per thread and plane
   static_assert(kStgRows * GR % kStgThreads == 0 && GR * NG % kStgThreads == 0, "whole slots");
-  static_assert(kStgKW % 16 == 0, "steps of whole MFMA chunks");
-  constexpr int APL = kStgRows * kStgLDK, BPL = GR * TN * 4;  // words per A and B plane
-  __shared__ __align__(16) uint32_t As[3 * APL];  // A^ - RA0, A^, -RA1 as [m][k]
-  __shared__ __align__(16) uint32_t Bs[3 * BPL];  // B^ - RB0, -RB1, B^ as [k / 4][n][k % 4]
+  static_assert(NV >= 1 && NV <= 4, "B loads of 4, 8 or 16 bytes");
+  constexpr int APL = kStgRows * kStgLDK, BPL = GR * TN * 4;  // 32-bit words per A and B plane
+  __shared__ __align__(16) uint32_t As[3 * APL];  // A^ - RA0, A^, -RA1 as [m][k] (52 words a row)
+  __shared__ __align__(16) uint32_t Bs[3 * BPL];  // B^ - RB0, -RB1, B^ as [k / KPC][n][k % KPC]
   const int M = g0.M, N = g0.N, K = g0.K;
   const int gx = (N + TN - 1) / TN, gy = (M + kStgRows - 1) / kStgRows;
   const int lw = xcd_swizzle(int(blockIdx.x), int(gridDim.x));
   const int bz = lw / (gx * gy), m0 = (lw / gx) % gy * kStgRows, n0 = lw % gx * TN;
   const int tid = int(threadIdx.x), lane = tid & 63, wave = tid >> 6, li = lane & 15, lg = lane >> 4;
   const size_t mk = size_t(M) * K, kn = size_t(K) * N, mn = size_t(M) * N;
-  const __amdgpu_buffer_rsrc_t rah = pan_rsrc(g0.A1 + size_t(bz) * g0.sA, mk * 4);
-  const __amdgpu_buffer_rsrc_t ra0 = pan_rsrc(g0.A2 + size_t(bz) * g0.sA, mk * 4);
-  const __amdgpu_buffer_rsrc_t ra1 = pan_rsrc(g1.A1b + size_t(bz) * g1.sA, mk * 4);
-  const __amdgpu_buffer_rsrc_t rbh = pan_rsrc(g0.B1 + size_t(bz) * g0.sB, kn * 4);
-  const __amdgpu_buffer_rsrc_t rb0 = pan_rsrc(g0.B2 + size_t(bz) * g0.sB, kn * 4);
-  const __amdgpu_buffer_rsrc_t rb1 = pan_rsrc(g1.B1 + size_t(bz) * g1.sB, kn * 4);
+  const __amdgpu_buffer_rsrc_t rah = pan_rsrc(g0.A1 + size_t(bz) * g0.sA, mk * WB);
+  const __amdgpu_buffer_rsrc_t ra0 = pan_rsrc(g0.A2 + size_t(bz) * g0.sA, mk * WB);
+  const __amdgpu_buffer_rsrc_t ra1 = pan_rsrc(g1.A1b + size_t(bz) * g1.sA, mk * WB);
+  const __amdgpu_buffer_rsrc_t rbh = pan_rsrc(g0.B1 + size_t(bz) * g0.sB, kn * WB);
+  const __amdgpu_buffer_rsrc_t rb0 = pan_rsrc(g0.B2 + size_t(bz) * g0.sB, kn * WB);
+  const __amdgpu_buffer_rsrc_t rb1 = pan_rsrc(g1.B1 + size_t(bz) * g1.sB, kn * WB);
   // this lane's outputs (rows m0 + 16 wave + 4 lg + r, columns n0 + 16 t + li)
   // and their C0 + C1, loaded first so that they arrive during the products
-  const __amdgpu_buffer_rsrc_t rc0 = pan_rsrc(g0.Cin + size_t(bz) * g0.sC, mn * 4);
-  const __amdgpu_buffer_rsrc_t rc1 = pan_rsrc(g1.Cin + size_t(bz) * g1.sC, mn * 4);
-  uint32_t co[CT][4], c0v[CT][4], c1v[CT][4];
+  const __amdgpu_buffer_rsrc_t rc0 = pan_rsrc(g0.Cin + size_t(bz) * g0.sC, mn * WB);
+  const __amdgpu_buffer_rsrc_t rc1 = pan_rsrc(g1.Cin + size_t(bz) * g1.sC, mn * WB);
+  uint32_t co[CT][4];
+  T c0v[CT][4], c1v[CT][4];
 #pragma unroll
   for (int t = 0; t < CT; t++) {
     const int on = n0 + 16 * t + li;
 #pragma unroll
     for (int r = 0; r < 4; r++) {
       const int om = m0 + 16 * wave + 4 * lg + r;
-      co[t][r] = (uint32_t(om < M ? om : 0) * uint32_t(N) + uint32_t(on < N ? on : 0)) * 4u |
+      co[t][r] = (uint32_t(om < M ? om : 0) * uint32_t(N) + uint32_t(on < N ? on : 0)) * uint32_t(WB) |
                  (om < M && on < N ? 0u : kPanOob);
-      c0v[t][r] = pan_load1(rc0, co[t][r]);
-      c1v[t][r] = pan_load1(rc1, co[t][r]);
+      c0v[t][r] = stg_word<T>(rc0, co[t][r]);
+      c1v[t][r] = stg_word<T>(rc1, co[t][r]);
     }
   }
-  // staging slots: A group (row f / GR, words 4 (f % GR)..) and B block (k rows
-  // 4 (f / NG).. + 3, columns VW (f % NG)..)
+  // staging slots: A group (row f / GR, bytes 16 (f % GR)..) and B block (k rows
+  // KPC (f / NG).. + KPC - 1, columns VW (f % NG)..)
   uint32_t aoff[SA], aoob[SA], boff[SB], boob[SB];
 #pragma unroll
   for (int j = 0; j < SA; j++) {
     const int f = tid + kStgThreads * j, r = f / GR;
     aoob[j] = m0 + r < M ? 0u : kPanOob;
-    aoff[j] = (uint32_t(m0 + r < M ? m0 + r : 0) * uint32_t(K) + uint32_t(4 * (f % GR))) * 4u;
+    aoff[j] = (uint32_t(m0 + r < M ? m0 + r : 0) * uint32_t(K) + uint32_t(KPC * (f % GR))) * uint32_t(WB);
   }
 #pragma unroll
   for (int j = 0; j < SB; j++) {
     const int f = tid + kStgThreads * j, n = n0 + VW * (f % NG);
     boob[j] = n < N ? 0u : kPanOob;
-    boff[j] = (uint32_t(4 * (f / NG)) * uint32_t(N) + uint32_t(n < N ? n : 0)) * 4u;
+    boff[j] = (uint32_t(KPC * (f / NG)) * uint32_t(N) + uint32_t(n < N ? n : 0)) * uint32_t(WB);
   }
-  uint32_t xa[SA][3][4], xb[SB][3][4][VW];
+  uint32_t xa[SA][3][4], xb[SB][3][KPC][NV];
   auto load = [&](int kb) {
 #pragma unroll
     for (int j = 0; j < SA; j++) {
       const int f = tid + kStgThreads * j;
-      const uint32_t o = (aoff[j] + uint32_t(kb) * 4u) | aoob[j] | (kb + 4 * (f % GR) < K ? 0u : kPanOob);
+      const uint32_t o =
+          (aoff[j] + uint32_t(kb) * uint32_t(WB)) | aoob[j] | (kb + KPC * (f % GR) < K ? 0u : kPanOob);
       stg_load<4>(rah, o, xa[j][0]);
       stg_load<4>(ra0, o, xa[j][1]);
       stg_load<4>(ra1, o, xa[j][2]);
     }
 #pragma unroll
     for (int j = 0; j < SB; j++) {
-      const int f = tid + kStgThreads * j, k = kb + 4 * (f / NG);  // K % 4 == 0: all four rows inside K, or none
-      const uint32_t o = (boff[j] + uint32_t(kb) * uint32_t(N) * 4u) | boob[j] | (k < K ? 0u : kPanOob);
+      const int f = tid + kStgThreads * j, k = kb + KPC * (f / NG);  // K % KPC == 0: all rows inside K, or none
+      const uint32_t o =
+          (boff[j] + uint32_t(kb) * uint32_t(N) * uint32_t(WB)) | boob[j] | (k < K ? 0u : kPanOob);
 #pragma unroll
-      for (int i = 0; i < 4; i++) {
-        const uint32_t oi = o + uint32_t(i) * uint32_t(N) * 4u;
-        stg_load<VW>(rbh, oi, xb[j][0][i]);
-        stg_load<VW>(rb0, oi, xb[j][1][i]);
-        stg_load<VW>(rb1, oi, xb[j][2][i]);
+      for (int i = 0; i < KPC; i++) {
+        const uint32_t oi = o + uint32_t(i) * uint32_t(N) * uint32_t(WB);
+        stg_load<NV>(rbh, oi, xb[j][0][i]);
+        stg_load<NV>(rb0, oi, xb[j][1][i]);
+        stg_load<NV>(rb1, oi, xb[j][2][i]);
       }
     }
   };
+  const uint4 z4 = make_uint4(0u, 0u, 0u, 0u);
+  auto u4 = [](const uint32_t (&v)[4]) { return make_uint4(v[0], v[1], v[2], v[3]); };
   auto store = [&]() {
 #pragma unroll
     for (int j = 0; j < SA; j++) {
       const int f = tid + kStgThreads * j;
       uint32_t *p = &As[(f / GR) * kStgLDK + 4 * (f % GR)];
-      uint4 d0, d1, d2;
-      uint32_t *e0 = &d0.x, *e1 = &d1.x, *e2 = &d2.x;
-#pragma unroll
-      for (int e = 0; e < 4; e++) {
-        e0[e] = ring_digits(xa[j][0][e] - xa[j][1][e]);
-        e1[e] = ring_digits(xa[j][0][e]);
-        e2[e] = ring_digits(0u - xa[j][2][e]);
-      }
-      *reinterpret_cast<uint4 *>(p) = d0;
-      *reinterpret_cast<uint4 *>(p + APL) = d1;
-      *reinterpret_cast<uint4 *>(p + 2 * APL) = d2;
+      const uint4 ah = u4(xa[j][0]);
+      *reinterpret_cast<uint4 *>(p) = wide_digits<T>(ah, u4(xa[j][1]));
+      *reinterpret_cast<uint4 *>(p + APL) = wide_digits<T>(ah, z4);
+      *reinterpret_cast<uint4 *>(p + 2 * APL) = wide_digits<T>(z4, u4(xa[j][2]));
     }
 #pragma unroll
     for (int j = 0; j < SB; j++) {
       const int f = tid + kStgThreads * j;
 #pragma unroll
-      for (int e = 0; e < VW; e++) {  // column VW (f % NG) + e: its four k rows as one 16-byte cell
+      for (int e = 0; e < VW; e++) {  // column VW (f % NG) + e: its KPC k words as one 16-byte cell
         uint32_t *p = &Bs[((f / NG) * TN + VW * (f % NG) + e) * 4];
-        uint4 d0, d1, d2;
-        uint32_t *e0 = &d0.x, *e1 = &d1.x, *e2 = &d2.x;
+        uint32_t c[3][4];
 #pragma unroll
-        for (int i = 0; i < 4; i++) {
-          e0[i] = ring_digits(xb[j][0][i][e] - xb[j][1][i][e]);
-          e1[i] = ring_digits(0u - xb[j][2][i][e]);
-          e2[i] = ring_digits(xb[j][0][i][e]);
-        }
-        *reinterpret_cast<uint4 *>(p) = d0;
-        *reinterpret_cast<uint4 *>(p + BPL) = d1;
-        *reinterpret_cast<uint4 *>(p + 2 * BPL) = d2;
+        for (int q = 0; q < 3; q++)
+#pragma unroll
+          for (int i = 0; i < KPC; i++)
+#pragma unroll
+            for (int h = 0; h < WB / 4; h++) c[q][i * (WB / 4) + h] = xb[j][q][i][e * (WB / 4) + h];
+        const uint4 bh = u4(c[0]);
+        *reinterpret_cast<uint4 *>(p) = wide_digits<T>(bh, u4(c[1]));
+        *reinterpret_cast<uint4 *>(p + BPL) = wide_digits<T>(z4, u4(c[2]));
+        *reinterpret_cast<uint4 *>(p + 2 * BPL) = wide_digits<T>(bh, z4);
       }
     }
   };
@@ -1733,11 +1755,15 @@ __global__ __launch_bounds__(kStgThreads, 2) void k_sxs_staged(GemmArgs<uint32_t
   auto compute = [&]() {
     const int ar = (16 * wave + li) * kStgLDK + 4 * lg;
 #pragma unroll
-    for (int c = 0; c < kStgKW / 16; c++)
+    for (int c = 0; c < 3; c++)
 #pragma unroll
       for (int p = 0; p < 3; p++) {  // (A^ - RA0)(B^ - RB0), A^ (-RB1), (-RA1) B^
         v4i_t as[NQ];
-        digit_shifts_s(*reinterpret_cast<const uint4 *>(&As[p * APL + ar + 16 * c]), sel, as);
+        const uint4 a = *reinterpret_cast<const uint4 *>(&As[p * APL + ar + 16 * c]);
+        if constexpr (sizeof(T) == 4)
+          digit_shifts_s(a, sel, as);
+        else
+          digit_shifts<T>(a, as);
 #pragma unroll
         for (int t = 0; t < CT; t++) {
           const uint4 b = *reinterpret_cast<const uint4 *>(&Bs[p * BPL + ((4 * c + lg) * TN + 16 * t + li) * 4]);
@@ -1748,69 +1774,63 @@ __global__ __launch_bounds__(kStgThreads, 2) void k_sxs_staged(GemmArgs<uint32_t
       }
   };
   load(0);
-  for (int kb = 0; kb < K; kb += kStgKW) {
+  for (int kb = 0; kb < K; kb += KW) {
     store();
     __syncthreads();
-    if (kb + kStgKW < K) load(kb + kStgKW);  // in flight during this step's MFMAs
+    if (kb + KW < K) load(kb + KW);  // in flight during this step's MFMAs
     compute();
     __syncthreads();
   }
-  const __amdgpu_buffer_rsrc_t rc = pan_rsrc(g0.C + size_t(bz) * mn, mn * 4);
+  const __amdgpu_buffer_rsrc_t rc = pan_rsrc(g0.C + size_t(bz) * mn, mn * WB);
 #pragma unroll
   for (int t = 0; t < CT; t++)
 #pragma unroll
     for (int r = 0; r < 4; r++)  // outside the matrix: dropped by the range check
-      __builtin_amdgcn_raw_buffer_store_b32(c0v[t][r] + c1v[t][r] + digit_fold<uint32_t>(acc[t], r), rc,
-                                            int(co[t][r]), 0, 0);
+      stg_store_word<T>(rc, co[t][r], T(c0v[t][r] + c1v[t][r] + digit_fold<T>(acc[t], r)));
 }
 
-// The Z_2^32 SxS pair in the staged kernel's form: party 0's (A^ - RA0)(B^ -
-// RB0) + C0 and party 1's C1 - (A^ RB1 + RA1 B^) on one shape, K a multiple of
-// 4, 16-byte aligned operands, every matrix of a batch entry below 2 GiB.
+// An SxS pair in the staged kernel's form: party 0's (A^ - RA0)(B^ - RB0) + C0
+// and party 1's C1 - (A^ RB1 + RA1 B^) on one shape, K a whole number of
+// 16-byte groups, 16-byte aligned operands, every matrix of a batch entry below
+// 2 GiB; in Z_2^64 K below 2^15 (the shift sums' int32 range).
 template <typename T>
 static bool use_sxs_staged(const Launch &L, const GemmArgs<T> &g0, const GemmArgs<T> &g1) {
-  if constexpr (sizeof(T) != 4) {
+  constexpr size_t KPC = 16 / sizeof(T), WB = sizeof(T);
+  if (!L.sxs_staged || (L.gemm != 0 && L.gemm != 3)) return false;
+  const bool form = g0.A2 && g0.B2 && !g0.A1b && g0.sign == 1 && g1.A1 == g0.A1 && g1.B1b == g0.B1 && g1.A1b &&
+                    g1.B1 && !g1.A2 && !g1.B2 && g1.sign == -1 && g0.Cin && g1.Cin && g0.C;
+  const bool shape = g0.M == g1.M && g0.N == g1.N && g0.K == g1.K && g0.batch == g1.batch && g0.sA == g1.sA &&
+                     g0.sB == g1.sB && g0.sC == size_t(g0.M) * g0.N && g1.sC == g0.sC;
+  if (!form || !shape || g0.K % KPC != 0 || g0.sA % KPC != 0 || g0.sB % KPC != 0) return false;
+  if (sizeof(T) == 8 && g0.K >= (1 << 15)) return false;
+  const size_t lim = size_t(kPanOob);
+  if (size_t(g0.M) * g0.K * WB >= lim || size_t(g0.K) * g0.N * WB >= lim || size_t(g0.M) * g0.N * WB >= lim)
     return false;
-  } else {
-    if (!L.sxs_staged || (L.gemm != 0 && L.gemm != 3)) return false;
-    const bool form = g0.A2 && g0.B2 && !g0.A1b && g0.sign == 1 && g1.A1 == g0.A1 && g1.B1b == g0.B1 && g1.A1b &&
-                      g1.B1 && !g1.A2 && !g1.B2 && g1.sign == -1 && g0.Cin && g1.Cin && g0.C;
-    const bool shape = g0.M == g1.M && g0.N == g1.N && g0.K == g1.K && g0.batch == g1.batch && g0.sA == g1.sA &&
-                       g0.sB == g1.sB && g0.sC == size_t(g0.M) * g0.N && g1.sC == g0.sC;
-    if (!form || !shape || g0.K % 4 != 0 || g0.sA % 4 != 0 || g0.sB % 4 != 0 || g0.sC % 4 != 0) return false;
-    const size_t lim = size_t(kPanOob);
-    if (size_t(g0.M) * g0.K * 4 >= lim || size_t(g0.K) * g0.N * 4 >= lim || size_t(g0.M) * g0.N * 4 >= lim)
-      return false;
-    for (const void *q : {(const void *)g0.A1, (const void *)g0.A2, (const void *)g1.A1b, (const void *)g0.B1,
-                          (const void *)g0.B2, (const void *)g1.B1})
-      if (reinterpret_cast<uintptr_t>(q) % 16 != 0) return false;
-    return true;
-  }
+  for (const void *q : {(const void *)g0.A1, (const void *)g0.A2, (const void *)g1.A1b, (const void *)g0.B1,
+                        (const void *)g0.B2, (const void *)g1.B1})
+    if (reinterpret_cast<uintptr_t>(q) % 16 != 0) return false;
+  return true;
 }
-template <int CT, int VW>
-static hipError_t launch_sxs_staged_at(const Launch &L, const GemmArgs<uint32_t> &g0, const GemmArgs<uint32_t> &g1,
-                                       uint32_t *out) {
+template <typename T, int CT, int VW>
+static hipError_t launch_sxs_staged_at(const Launch &L, const GemmArgs<T> &g0, const GemmArgs<T> &g1, T *out) {
   const size_t wgs = size_t((g0.N + 16 * CT - 1) / (16 * CT)) * size_t((g0.M + kStgRows - 1) / kStgRows) * g0.batch;
   if (wgs > size_t(INT32_MAX)) return hipErrorInvalidValue;
-  GemmArgs<uint32_t> a = g0;
+  GemmArgs<T> a = g0;
   a.C = out;
-  hipLaunchKernelGGL((k_sxs_staged<CT, VW>), dim3(unsigned(wgs)), dim3(kStgThreads), 0, L.stream, a, g1);
+  hipLaunchKernelGGL((k_sxs_staged<T, CT, VW>), dim3(unsigned(wgs)), dim3(kStgThreads), 0, L.stream, a, g1);
   return hipGetLastError();
 }
-// 32 columns per workgroup (64 do not fit the register budget with the
-// staging registers and the prefetched C0 + C1); groups of 2 or 1 words along
-// B's rows, whichever divides N
-static hipError_t launch_sxs_staged(const Launch &L, const GemmArgs<uint32_t> &g0, const GemmArgs<uint32_t> &g1,
-                                    uint32_t *out) {
-  return g0.N % 2 == 0 ? launch_sxs_staged_at<2, 2>(L, g0, g1, out) : launch_sxs_staged_at<2, 1>(L, g0, g1, out);
+// 32 columns per workgroup; groups of 2 or 1 words along B's rows, whichever
+// divides N
+template <typename T>
+static hipError_t launch_sxs_staged(const Launch &L, const GemmArgs<T> &g0, const GemmArgs<T> &g1, T *out) {
+  return g0.N % 2 == 0 ? launch_sxs_staged_at<T, 2, 2>(L, g0, g1, out) : launch_sxs_staged_at<T, 2, 1>(L, g0, g1, out);
 }
 
 template <typename T>
 hipError_t launch_gemm_pair_sum(const Launch &L, const GemmArgs<T> &g0, const GemmArgs<T> &g1, T *out) {
   if (g0.M <= 0 || g0.N <= 0 || g0.batch <= 0) return hipSuccess;
-  if constexpr (sizeof(T) == 4) {
-    if (use_sxs_staged(L, g0, g1)) return launch_sxs_staged(L, g0, g1, out);
-  }
+  if (use_sxs_staged(L, g0, g1)) return launch_sxs_staged<T>(L, g0, g1, out);
   const bool same = g0.M == g1.M && g0.N == g1.N && g0.K == g1.K && g0.batch == g1.batch && g0.sA == g1.sA &&
                     g0.sB == g1.sB && g0.sC == size_t(g0.M) * g0.N && g1.sC == g0.sC;
   if (same && (g0.A1b ? 2 : 1) + (g1.A1b ? 2 : 1) <= 3) {  // both parties' products and the sum in one launch
