@@ -573,6 +573,11 @@ __device__ __forceinline__ int xcd_swizzle(int p, int W) {
 // steps run first segment first.  C = Cin + sign * (products).
 // ---------------------------------------------------------------------------
 constexpr int kWideK = 288;        // 32-bit words of K per step (LDS: 2 * 64 * 292 * 4 = 149.5 KB)
+// The same kernel with 96- and 160-word steps (LDS 50 and 82 KB) for problems
+// whose K takes as many steps of them as of kWideK (the public-weight products
+// with K = 78 and 156): a thread stages, converts and stores 3 or 5 groups per
+// operand instead of 9
+constexpr int kWideKShort = 96, kWideKMid = 160;
 constexpr int kWideThreads = 512;  // 8 waves
 
 template <typename T>
@@ -583,11 +588,11 @@ struct WideStep {
 // K words of a step: a segment with masks stages four operands, so its steps
 // are half as wide (the staging registers hold two operand panels of KW words)
 template <typename T, int KW>
-__device__ __forceinline__ int wide_kt(bool masked) {
+__host__ __device__ __forceinline__ int wide_kt(bool masked) {
   return (masked ? KW / 2 : KW) * 4 / int(sizeof(T));
 }
 template <typename T, int KW>
-__device__ __forceinline__ int wide_steps(const GemmArgs<T> &g) {
+__host__ __device__ __forceinline__ int wide_steps(const GemmArgs<T> &g) {
   const int k0 = wide_kt<T, KW>(g.A2 || g.B2), k1 = wide_kt<T, KW>(false);
   return (g.K + k0 - 1) / k0 + (g.A1b ? (g.K + k1 - 1) / k1 : 0);
 }
@@ -1374,15 +1379,25 @@ static bool wide_vec_a(const GemmArgs<T> &g) {
   return g.K % wpg == 0 && (g.batch == 1 || g.sA % wpg == 0) && aligned16(g.A1) && aligned16(g.A2) &&
          aligned16(g.A1b);
 }
+template <typename T, int KW>
+static void launch_wide_kw(const Launch &L, dim3 grid, const GemmArgs<T> &g) {
+  if (wide_vec_a(g))
+    hipLaunchKernelGGL((k_gemm_wide<T, KW, true>), grid, dim3(kWideThreads), 0, L.stream, g);
+  else
+    hipLaunchKernelGGL((k_gemm_wide<T, KW, false>), grid, dim3(kWideThreads), 0, L.stream, g);
+}
 template <typename T>
 static hipError_t launch_wide(const Launch &L, const GemmArgs<T> &g) {
   const size_t wgs = size_t((g.N + 63) / 64) * size_t((g.M + 63) / 64) * size_t(g.batch);
   if (wgs > size_t(INT32_MAX)) return hipErrorInvalidValue;  // one-dimensional, XCD-ordered launch
   const dim3 grid{unsigned(wgs), 1u, 1u};
-  if (wide_vec_a(g))
-    hipLaunchKernelGGL((k_gemm_wide<T, kWideK, true>), grid, dim3(kWideThreads), 0, L.stream, g);
+  const int steps = wide_steps<T, kWideK>(g);  // the narrowest step width that takes no more steps
+  if (wide_steps<T, kWideKShort>(g) == steps)
+    launch_wide_kw<T, kWideKShort>(L, grid, g);
+  else if (wide_steps<T, kWideKMid>(g) == steps)
+    launch_wide_kw<T, kWideKMid>(L, grid, g);
   else
-    hipLaunchKernelGGL((k_gemm_wide<T, kWideK, false>), grid, dim3(kWideThreads), 0, L.stream, g);
+    launch_wide_kw<T, kWideK>(L, grid, g);
   return hipGetLastError();
 }
 
