@@ -1295,6 +1295,70 @@ __global__ void k_gemm_init(int M, int N, int batch, size_t sC, const T *Cin, T 
   }
 }
 
+// ---------------------------------------------------------------------------
+// Products of at most kDotMaxN columns (the last fully connected layer of the
+// affinity model: 22 x 512 x 1 per lane): a 64 x 64 matrix tile would compute
+// mostly padding, and the tiled kernel splits K over a few workgroups that add
+// with atomics.  Here one wave per output element: lane l multiplies k = l,
+// l + 64, .. on the VALU (ring arithmetic wraps mod 2^bw), a butterfly over the
+// wave adds the partial sums, lane 0 writes C = Cin + sign * sum.  A lane loads
+// kDotUnroll of its k at once, so K up to 64 kDotUnroll costs one memory round
+// trip.
+// ---------------------------------------------------------------------------
+constexpr int kDotMaxN = 4, kDotMaxK = 8192, kDotUnroll = 8;
+template <typename T>
+__device__ __forceinline__ T wave_sum(T v) {
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) {
+    if constexpr (sizeof(T) == 4) {
+      v += T(__shfl_xor(int(v), off, 64));
+    } else {
+      const uint32_t lo = uint32_t(__shfl_xor(int(uint32_t(v)), off, 64));
+      const uint32_t hi = uint32_t(__shfl_xor(int(uint32_t(v >> 32)), off, 64));
+      v += (uint64_t(hi) << 32) | lo;
+    }
+  }
+  return v;
+}
+template <typename T>
+__global__ __launch_bounds__(256) void k_gemm_dot(GemmArgs<T> g) {
+  const size_t per = size_t(g.M) * g.N, e = size_t(blockIdx.x) * 4 + (threadIdx.x >> 6);
+  if (e >= per * size_t(g.batch)) return;  // uniform over the wave
+  const int lane = int(threadIdx.x & 63);
+  const size_t bz = e / per, mn = e % per, m = mn / size_t(g.N), n = mn % size_t(g.N);
+  const size_t ao = bz * g.sA + m * size_t(g.K), bo = bz * g.sB + n, ld = size_t(g.N);
+  T s = 0;
+  for (int k0 = lane; k0 < g.K; k0 += 64 * kDotUnroll) {
+    T a[kDotUnroll], b[kDotUnroll];
+#pragma unroll
+    for (int u = 0; u < kDotUnroll; u++) {  // k past K reads k = 0 (loads without branches) and adds 0
+      const int k = k0 + 64 * u < g.K ? k0 + 64 * u : 0;
+      a[u] = g.A1[ao + k];
+      b[u] = g.B1[bo + size_t(k) * ld];
+    }
+#pragma unroll
+    for (int u = 0; u < kDotUnroll; u++) s += k0 + 64 * u < g.K ? a[u] * b[u] : T(0);
+  }
+  s = wave_sum(s);
+  if (lane == 0) {
+    const size_t ci = bz * g.sC + mn;
+    g.C[ci] = (g.Cin ? g.Cin[ci] : T(0)) + (g.sign < 0 ? T(0) - s : s);
+  }
+}
+// the dot kernel: automatic path selection, a plain product (no masks, one K
+// segment), at most kDotMaxN columns, K within kDotMaxK (16 rounds of loads)
+template <typename T>
+static bool use_dot(const Launch &L, const GemmArgs<T> &g) {
+  return L.gemm == 0 && !g.A2 && !g.B2 && !g.A1b && g.N <= kDotMaxN && g.K <= kDotMaxK &&
+         (size_t(g.M) * g.N * g.batch + 3) / 4 <= size_t(INT32_MAX);
+}
+template <typename T>
+static hipError_t launch_dot(const Launch &L, const GemmArgs<T> &g) {
+  const unsigned blocks = unsigned((size_t(g.M) * g.N * g.batch + 3) / 4);
+  hipLaunchKernelGGL((k_gemm_dot<T>), dim3(blocks), dim3(256), 0, L.stream, g);
+  return hipGetLastError();
+}
+
 static bool aligned16(const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
 // rows of A (resp. B) can be read as 16-byte words
 static bool gemm_vec_a(const GemmArgs<uint32_t> &g) {
@@ -1524,12 +1588,23 @@ static PanelArgs<T> panels_of(const GemmArgs<T> &g) {
   return r;
 }
 
+// A single product whose K fits one wide step of at most kWideKMid words and
+// whose 64 x 64 tiles occupy at least half the CUs runs faster on the wide
+// kernel than on the panel kernel (3080 x 156 x 312, the GCN-3 public-weight
+// product of 22 graphs: 8.3 against 10.0 us); smaller launches keep the panel
+// kernel's smaller workgroups (140 x 156 x 312: 5.6 against 7.6 us).
+template <typename T>
+static bool prefer_wide(const Launch &L, const GemmArgs<T> &g) {
+  return !g.A2 && !g.B2 && !g.A1b && use_wide(L, g) && wide_steps<T, kWideKMid>(g) == 1 &&
+         gemm_tiles(g) >= L.num_cu / 2;
+}
 template <typename T>
 hipError_t launch_gemm(const Launch &L, const GemmArgs<T> &g0) {
   if (g0.M <= 0 || g0.N <= 0 || g0.batch <= 0) return hipSuccess;
+  if (use_dot(L, g0)) return launch_dot<T>(L, g0);
   {
     const PanelArgs<T> r = panels_of(g0);
-    if (use_panels(L, r)) return launch_panels<T>(L, r);
+    if (use_panels(L, r) && !prefer_wide(L, g0)) return launch_panels<T>(L, r);
   }
   if (use_wide(L, g0)) return launch_wide<T>(L, g0);
   const bool mfma = use_mfma(L, g0);
