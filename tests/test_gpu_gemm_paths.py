@@ -23,9 +23,13 @@ import pytest
 pytestmark = pytest.mark.gpu
 
 # (M, K, N): single step (K <= 288 words of Z_2^32, 144 of Z_2^64), several
-# steps with 64+ tiles, K not a multiple of the 16-byte group, tiny
+# steps with 64+ tiles, K not a multiple of the 16-byte group, tiny; few-row
+# products (split-K with K ending inside an MFMA chunk and ragged N, one chunk,
+# 128 rows of a long K, K not a whole number of groups); the dot kernel (N <= 4)
+# with two rounds of loads
 GEMM_SHAPES = [(3080, 78, 78), (3080, 156, 312), (140, 140, 312), (130, 77, 65), (600, 700, 300), (64, 63, 1),
-               (1, 1, 1), (22, 256, 1024), (64, 144, 64), (48, 148, 36), (200, 288, 32)]
+               (1, 1, 1), (22, 256, 1024), (64, 144, 64), (48, 148, 36), (200, 288, 32), (100, 340, 70),
+               (33, 12, 17), (128, 1024, 20), (20, 77, 40), (5, 700, 3)]
 # (nb, M, K, N): the affinity model's per-graph products, several masked and
 # unmasked steps over 64 tiles, K not a multiple of the group, tiny; the
 # panel-pipelined kernel (K within one step; 48-column workgroups at
