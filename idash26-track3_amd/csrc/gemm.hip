@@ -1302,8 +1302,8 @@ __global__ void k_gemm_init(int M, int N, int batch, size_t sC, const T *Cin, T 
 // with atomics.  Here one wave per output element: lane l multiplies k = l,
 // l + 64, .. on the VALU (ring arithmetic wraps mod 2^bw), a butterfly over the
 // wave adds the partial sums, lane 0 writes C = Cin + sign * sum.  A lane loads
-// kDotUnroll of its k at once, so K up to 64 kDotUnroll costs one memory round
-// trip.
+// kDotUnroll of its k at once, so K up to 64 * kDotUnroll = 512 costs one
+// memory round trip.
 // ---------------------------------------------------------------------------
 constexpr int kDotMaxN = 4, kDotMaxK = 8192, kDotUnroll = 8;
 template <typename T>
