@@ -316,7 +316,8 @@ def main():
         },
         "roofline_gemm": {
             "kernel": f"ring GEMMs ({gemm_path}: public-weight products and SxS Beaver products, "
-                      f"{prof['gemm_sections']} sections of the profiled forward)",
+                      f"{prof['gemm_sections']} sections of the profiled forward"
+                      + ("; products of at most 4 columns on the VALU dot kernel)" if gemm_path != "valu" else ")"),
             "bound": "valu" if gemm_path == "valu" else "mfma",
             "achieved": round(gemm_tmacs, 3),
             "peak": round(GEMM_PEAK_TMACS[gemm_path], 2),
